@@ -1,0 +1,121 @@
+/* kdn.h -- C ABI of the MI355X (gfx950) Kernel-DeltaNet prefill path.
+ *
+ * The path: spherical-normalise + structured-FWHT feature lift (d_k = 64 -> D = 512), then the exact
+ * chunked gated delta-rule scan  y_t = S_{t-1} phi(q_t),
+ *                                S_t = lambda_t S_{t-1} (I - beta_t phi(k_t) phi(k_t)^T) + beta_t v_t phi(k_t)^T.
+ *
+ * Conventions (every entry point):
+ *   - All tensor pointers are device pointers; the caller allocates every buffer (inputs, outputs,
+ *     workspace).  Nothing in the library allocates device memory.
+ *   - Work is enqueued on `stream` (a hipStream_t passed as void*; NULL = the null stream) and is
+ *     stream-ordered; entry points return without synchronising.
+ *   - Return 0 (KDN_OK) or a negative kdn_status.  No exception or abort crosses the ABI.  Argument
+ *     errors are detected on the host before anything is enqueued.
+ *   - Stateless and reentrant: no global caches, safe to call from several host threads.
+ *   - Strides are in elements; the innermost (feature) dimension of every tensor must be contiguous.
+ *
+ * Reference interfaces replaced (paths relative to jatin-yadav-acad/kernel-deltanet):
+ *   kdn_build_omega     <- FastWalshHadamardProjection.__init__ Omega build, kernels/fwht.py:94-111
+ *   kdn_fwht            <- fast_walsh_hadamard_transform, kernels/fwht.py:25-45
+ *   kdn_fwht_lift       <- pybind fwht_forward(input, rademacher_bits, D_lifted, tau_star_inv),
+ *                          kernels/fwht_cuda.cpp:29-32, with the semantics of the torch branch of
+ *                          FastWalshHadamardProjection.forward, kernels/fwht.py:122-131
+ *   kdn_delta_scan_fwd  <- fused_chunked_deltanet_forward, kernels/fused_kernel_deltanet.py:31-155
+ */
+#ifndef KDN_H
+#define KDN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum kdn_status {
+  KDN_OK = 0,
+  KDN_ERR_INVALID_ARGUMENT = -1,  /* null pointer, non-positive size, bad stride, bad dtype tag */
+  KDN_ERR_UNSUPPORTED = -2,       /* valid request outside what the kernels implement (d_k, D, d_v) */
+  KDN_ERR_WORKSPACE_TOO_SMALL = -3,
+  KDN_ERR_MISALIGNED = -4,        /* a pointer or row stride breaks the 16-byte vector-access rule */
+  KDN_ERR_DEVICE = -5             /* a HIP launch reported an error */
+} kdn_status;
+
+typedef enum kdn_dtype {
+  KDN_DTYPE_F32 = 0,
+  KDN_DTYPE_BF16 = 1
+} kdn_dtype;
+
+/* Human-readable text for a kdn_status value (static storage, never NULL). */
+const char* kdn_strerror(int status);
+
+/* ABI version: (major << 16) | minor. */
+int kdn_abi_version(void);
+
+/* Build the explicit structured projection Omega[D][d_k] = concat_m (H D3_m H D2_m H D1_m) / sqrt(d_k)
+ * from the packed Rademacher table sign_bits[M][3] (M = D / d_k; column s = stage d1,d2,d3; bit i set
+ * <=> entry i is -1), with H the natural-order (Sylvester) Hadamard matrix.  Computed with wave64
+ * butterflies; every entry is an integer / 8 for d_k = 64 and is stored exactly in either dtype.
+ * Replaces kernels/fwht.py:94-111 (and the bit table of :74-83 is its input).
+ * d_k must be 64; D a multiple of 64 up to 1024. */
+int kdn_build_omega(const int64_t* sign_bits, int d_k, int D, void* omega, int omega_dtype, void* stream);
+
+/* Unnormalised natural-order Walsh-Hadamard transform of each row (length n, a power of two <= 64).
+ * out may alias x.  Replaces fast_walsh_hadamard_transform, kernels/fwht.py:25-45. */
+int kdn_fwht(const void* x, int64_t rows, int64_t x_row_stride, int n, int dtype,
+             void* out, int64_t out_row_stride, void* stream);
+
+/* Feature lift of `rows` vectors x[r][0:d_k] -> out[r][0:D]:
+ *   xh  = normalize_input ? x / max(||x||_2, 1e-6) (rounded to x's dtype) : x
+ *   phi = sqrt(2/D) cos(xh Omega^T * inv_tau + phase),   out = phi / (||phi||_2 + 1e-8)
+ * omega is the bf16 [D][d_k] table from kdn_build_omega (exact in bf16); phase is fp32 [D].
+ * Products are exact (bf16 operands; fp32 inputs are split into three bf16 parts), sums in fp32.
+ * Replaces kernels/fwht_cuda.cpp:29-32 with the semantics of kernels/fwht.py:122-131.
+ * d_k must be 64; D in {128, 256, 512}. */
+int kdn_fwht_lift(const void* x, int64_t rows, int64_t x_row_stride, int x_dtype, int normalize_input,
+                  const void* omega_bf16, const float* phase, int d_k, int D, float inv_tau,
+                  void* out, int64_t out_row_stride, int out_dtype, void* stream);
+
+/* Arguments of the chunked delta-rule prefill scan.  Tensors are addressed as
+ *   q[b][t][h][0:d_k], k[b][t][h][0:d_k], v[b][t][h][0:d_v], beta[b][t][h], decay[b][t][h],
+ *   y[b][t][h][0:d_v], state[b][h][0:D][0:d_v]   (state element (d, j) = S[j][d] of the recurrence)
+ * through the given element strides, so (B*H, T, d), (B, T, H, d) and (B, H, T, d) layouts all work
+ * without copies (fold heads into batch with H = 1).  The reference state layout (B, d_v, D) is
+ * state stride {d_v*D, 0, 1, D}. */
+typedef struct kdn_scan_args {
+  int64_t B, T, H;
+  int d_k, D, d_v;             /* d_k = 64, D = 512, d_v a multiple of 16 up to 128 */
+  int in_dtype;                /* dtype of q, k, v */
+  int out_dtype;               /* dtype of y */
+  int normalize_input;         /* L2-normalise q, k rows (F.normalize, eps 1e-6) before the lift */
+  float inv_tau;               /* 1 / tau*, tau* = d_k^(1/4) in the reference */
+  const void* q;   int64_t q_stride[3];
+  const void* k;   int64_t k_stride[3];
+  const void* v;   int64_t v_stride[3];
+  const float* beta;  int64_t beta_stride[3];
+  const float* decay; int64_t decay_stride[3];   /* NULL means lambda = 1 */
+  const void* omega_bf16;      /* [D][d_k] from kdn_build_omega */
+  const float* phase;          /* [D] */
+  const float* initial_state; int64_t init_stride[4];   /* NULL means S_0 = 0 */
+  float* final_state;         int64_t final_stride[4];  /* required; may alias initial_state */
+  void* y;         int64_t y_stride[3];
+  void* workspace; size_t workspace_bytes;
+  int64_t segment_chunks;      /* 64-token chunks per segment; 0 lets the library choose */
+} kdn_scan_args;
+
+/* Workspace bytes kdn_delta_scan_fwd needs for these arguments (0 if the arguments are invalid).
+ * Only the shape, dtype and segment_chunks fields are read. */
+size_t kdn_scan_workspace_bytes(const kdn_scan_args* a);
+
+/* The exact chunked gated delta rule with readout before update (see top of file), carried in fp32,
+ * continuing from initial_state and writing the state after the last token to final_state.  Tokens
+ * past T inside the last chunk are treated as beta = 0, lambda = 1 (exact no-ops), as the reference
+ * pads them (kernels/fused_kernel_deltanet.py:55-62).  log(lambda) is clamped to [log 1e-5, 0]
+ * (kernels/fused_kernel_deltanet.py:74).  Replaces kernels/fused_kernel_deltanet.py:31-155. */
+int kdn_delta_scan_fwd(const kdn_scan_args* a, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KDN_H */

@@ -1,0 +1,23 @@
+// Internal helpers shared by the C-ABI entry points (status codes, dtype tags, launch checks).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stddef.h>
+#include "../../include/kdn.h"
+
+namespace kdn {
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+inline int launch_status() {
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? KDN_OK : KDN_ERR_DEVICE;
+}
+
+inline bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+inline bool valid_dtype(int dt) { return dt == KDN_DTYPE_F32 || dt == KDN_DTYPE_BF16; }
+
+inline size_t dtype_size(int dt) { return dt == KDN_DTYPE_F32 ? 4 : 2; }
+
+}  // namespace kdn

@@ -1,0 +1,263 @@
+// Feature-lift kernels of the Kernel-DeltaNet prefill path (gfx950).
+//
+//  * kdn_build_omega : Omega[D][64] from the packed Rademacher table with wave64 butterflies
+//                      (DPP / ds_swizzle / ds_bpermute cross-lane exchanges), exact integer/8 values.
+//                      Follows the construction of kernels/fwht.py:94-111.
+//  * kdn_fwht        : plain natural-order FWHT of rows of length n <= 64 (kernels/fwht.py:25-45).
+//  * kdn_fwht_lift   : phi_hat = normalise(sqrt(2/D) cos(x Omega^T / tau + b)) (kernels/fwht.py:122-131)
+//                      with the projection on MFMA.  Omega is exact in bf16, so with bf16 inputs the
+//                      products are exact; fp32 inputs are split into three bf16 parts (exact products).
+//                      A dense 64 x D MFMA projection costs ~4 MFMA issues per row versus ~430 VALU
+//                      issues for the 8-block x 3-stage butterfly, so the lift's hot path uses MFMA and
+//                      the butterfly builds Omega once.
+#include "kdn_frag.hpp"
+#include "kdn_internal.hpp"
+#include "kdn_io.hpp"
+
+namespace kdn {
+
+// ------------------------------------------------------------------------------------------------
+// Wave64 natural-order Walsh-Hadamard transform: lane i holds element i.
+// Butterfly at stride h: lanes with bit h clear get u + v, lanes with bit h set get u - v, where u is
+// the element with the bit clear (the ordering of kernels/fwht.py:35-44).
+template <int H>
+__device__ __forceinline__ float fwht_stage(float v, int lane) {
+  float p = xor_shuffle<H>(v);
+  return (lane & H) ? (p - v) : (v + p);
+}
+
+template <int N>
+__device__ __forceinline__ float fwht_wave(float v, int lane) {
+  if constexpr (N > 1) v = fwht_stage<1>(v, lane);
+  if constexpr (N > 2) v = fwht_stage<2>(v, lane);
+  if constexpr (N > 4) v = fwht_stage<4>(v, lane);
+  if constexpr (N > 8) v = fwht_stage<8>(v, lane);
+  if constexpr (N > 16) v = fwht_stage<16>(v, lane);
+  if constexpr (N > 32) v = fwht_stage<32>(v, lane);
+  return v;
+}
+
+__device__ __forceinline__ float sign_of(int64_t bits, int i) { return ((bits >> i) & 1) ? -1.f : 1.f; }
+
+// One wave per (block m, column j): column j of W_m = H d3 o (H d2 o (H (d1 o e_j))) / 8.
+template <typename OutT>
+__global__ void __launch_bounds__(256) build_omega_kernel(const int64_t* __restrict__ bits, int M, OutT* __restrict__ omega) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int m = blockIdx.x;
+  const int64_t b1 = bits[m * 3 + 0], b2 = bits[m * 3 + 1], b3 = bits[m * 3 + 2];
+  for (int j = wave; j < 64; j += 4) {
+    float v = (lane == j) ? sign_of(b1, j) : 0.f;
+    v = fwht_wave<64>(v, lane);
+    v *= sign_of(b2, lane);
+    v = fwht_wave<64>(v, lane);
+    v *= sign_of(b3, lane);
+    v = fwht_wave<64>(v, lane);
+    omega[(int64_t)(m * 64 + lane) * 64 + j] = (OutT)(v * 0.125f);
+  }
+}
+
+// Plain FWHT of rows of length N (one wave per row, lanes >= N idle), fp32 arithmetic.
+template <typename T, int N>
+__global__ void __launch_bounds__(256) fwht_rows_kernel(const T* __restrict__ x, int64_t rows, int64_t xs,
+                                                        T* __restrict__ out, int64_t os) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  float v = (lane < N) ? (float)x[row * xs + lane] : 0.f;
+  // Butterflies at strides >= N never mix valid lanes with each other because N is a power of two
+  // and only strides < N are applied.
+  v = fwht_wave<N>(v, lane);
+  if (lane < N) out[row * os + lane] = (T)v;
+}
+
+// ------------------------------------------------------------------------------------------------
+// Lift: one wave per 16-row tile, four tiles per workgroup, persistent over tiles.
+// Projection in the transposed orientation  Phi^T[f][r] = sum_k Omega[f][k] x[r][k]:
+//   A = Omega fragments (f rows, k depth)   read from LDS (staged once per workgroup)
+//   B = x fragments      (k depth, r column) read from global, 16/32 bytes per lane
+// Accumulator tile (f-tile t): lane l holds Phi^T[16t + 4(l>>4) + i][row (l & 15)].
+template <typename InT, typename OutT, int D>
+__global__ void __launch_bounds__(256) lift_kernel(const InT* __restrict__ x, int64_t rows, int64_t xs, int normalize,
+                                                   const __bf16* __restrict__ omega, const float* __restrict__ phase,
+                                                   float inv_tau, OutT* __restrict__ out, int64_t os) {
+  constexpr int NT = D / 16;                 // feature tiles
+  constexpr int NSPLIT = XFrag<InT>::NSPLIT;
+  __shared__ bf16x8 s_omega[NT * 2 * 64];    // [t][kb][lane] A fragments, D*64*2 bytes
+  __shared__ __attribute__((aligned(16))) float s_phase_rev[D];           // phase / (2 pi)
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+
+  // Stage Omega as A fragments: lane l of fragment (t, kb) holds Omega[16t + (l&15)][32kb + 8(l>>4) .. +8].
+  for (int idx = threadIdx.x; idx < NT * 2 * 64; idx += 256) {
+    const int l = idx & 63, tk = idx >> 6, t = tk >> 1, kb = tk & 1;
+    s_omega[idx] = *reinterpret_cast<const bf16x8*>(omega + (int64_t)(16 * t + (l & 15)) * 64 + 32 * kb + 8 * (l >> 4));
+  }
+  for (int f = threadIdx.x; f < D; f += 256) s_phase_rev[f] = phase[f] * 0.15915494309189535f;
+  __syncthreads();
+
+  const float ang_scale = inv_tau * 0.15915494309189535f;  // radians -> revolutions folded in
+  const float amp = sqrtf(2.0f / (float)D);
+  const int64_t ntiles = (rows + 15) / 16;
+
+  for (int64_t tile = (int64_t)blockIdx.x * 4 + wave; tile < ntiles; tile += (int64_t)gridDim.x * 4) {
+    const int64_t row = tile * 16 + (lane & 15);
+    const bool valid = row < rows;
+    // x fragments for depth blocks kb = 0, 1: slots k = 32kb + 8(l>>4) + s.
+    float xv[2][8];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      if (valid) load8<InT>(x + row * xs + 32 * kb + 8 * (lane >> 4), xv[kb]);
+      else {
+#pragma unroll
+        for (int s = 0; s < 8; ++s) xv[kb][s] = 0.f;
+      }
+    }
+    if (normalize) {
+      float ss = 0.f;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int s = 0; s < 8; ++s) ss += xv[kb][s] * xv[kb][s];
+      ss = sum_over_lane_groups(ss);
+      const float inv = 1.0f / fmaxf(sqrtf(ss), 1e-6f);
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+          float y = xv[kb][s] * inv;
+          xv[kb][s] = (NSPLIT == 1) ? (float)(__bf16)y : y;  // F.normalize output keeps x's dtype
+        }
+    }
+    bf16x8 xb[2][NSPLIT];
+    split_frag<NSPLIT>(xv[0], xb[0]);
+    split_frag<NSPLIT>(xv[1], xb[1]);
+
+    float c[NT][4];
+    float ss = 0.f;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      f32x4 acc = zero4();
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        const bf16x8 a = s_omega[(t * 2 + kb) * 64 + lane];
+#pragma unroll
+        for (int p = 0; p < NSPLIT; ++p) acc = PrecBF16::mma(acc, a, xb[kb][p]);
+      }
+      const f32x4 ph = *reinterpret_cast<const f32x4*>(&s_phase_rev[16 * t + 4 * (lane >> 4)]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float r = acc[i] * ang_scale + ph[i];
+        r = r - __builtin_rintf(r);
+        const float cv = __builtin_amdgcn_cosf(r);
+        c[t][i] = cv;
+        ss += cv * cv;
+      }
+    }
+    ss = sum_over_lane_groups(ss);
+    // phi = amp * c ; out = phi / (||phi|| + 1e-8)
+    const float scale = amp / (amp * sqrtf(ss) + 1e-8f);
+    if (valid) {
+      OutT* o = out + row * os + 4 * (lane >> 4);
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        float v[4] = {c[t][0] * scale, c[t][1] * scale, c[t][2] * scale, c[t][3] * scale};
+        store4<OutT>(o + 16 * t, v);
+      }
+    }
+  }
+}
+
+template <typename InT, typename OutT, int D>
+static void launch_lift(const void* x, int64_t rows, int64_t xs, int normalize, const void* omega, const float* phase,
+                        float inv_tau, void* out, int64_t os, hipStream_t st) {
+  const int64_t ntiles = (rows + 15) / 16;
+  int64_t wgs = (ntiles + 3) / 4;
+  const int64_t cap = 256 * 4;  // a few resident workgroups per CU; the kernel loops over tiles
+  if (wgs > cap) wgs = cap;
+  hipLaunchKernelGGL((lift_kernel<InT, OutT, D>), dim3((unsigned)wgs), dim3(256), 0, st, (const InT*)x, rows, xs, normalize,
+                     (const __bf16*)omega, phase, inv_tau, (OutT*)out, os);
+}
+
+template <typename InT, typename OutT>
+static int dispatch_lift_D(int D, const void* x, int64_t rows, int64_t xs, int normalize, const void* omega,
+                           const float* phase, float inv_tau, void* out, int64_t os, hipStream_t st) {
+  switch (D) {
+    case 128: launch_lift<InT, OutT, 128>(x, rows, xs, normalize, omega, phase, inv_tau, out, os, st); break;
+    case 256: launch_lift<InT, OutT, 256>(x, rows, xs, normalize, omega, phase, inv_tau, out, os, st); break;
+    case 512: launch_lift<InT, OutT, 512>(x, rows, xs, normalize, omega, phase, inv_tau, out, os, st); break;
+    default: return KDN_ERR_UNSUPPORTED;
+  }
+  return launch_status();
+}
+
+}  // namespace kdn
+
+using namespace kdn;
+
+extern "C" int kdn_build_omega(const int64_t* sign_bits, int d_k, int D, void* omega, int omega_dtype, void* stream) {
+  if (!sign_bits || !omega) return KDN_ERR_INVALID_ARGUMENT;
+  if (!valid_dtype(omega_dtype)) return KDN_ERR_INVALID_ARGUMENT;
+  if (d_k != 64) return KDN_ERR_UNSUPPORTED;
+  if (D <= 0 || D % 64 != 0 || D > 1024) return KDN_ERR_UNSUPPORTED;
+  const int M = D / 64;
+  hipStream_t st = as_stream(stream);
+  if (omega_dtype == KDN_DTYPE_BF16)
+    hipLaunchKernelGGL((build_omega_kernel<__bf16>), dim3(M), dim3(256), 0, st, sign_bits, M, (__bf16*)omega);
+  else
+    hipLaunchKernelGGL((build_omega_kernel<float>), dim3(M), dim3(256), 0, st, sign_bits, M, (float*)omega);
+  return launch_status();
+}
+
+extern "C" int kdn_fwht(const void* x, int64_t rows, int64_t x_row_stride, int n, int dtype, void* out,
+                        int64_t out_row_stride, void* stream) {
+  if (!x || !out || rows < 0) return KDN_ERR_INVALID_ARGUMENT;
+  if (!valid_dtype(dtype)) return KDN_ERR_INVALID_ARGUMENT;
+  if (n < 1 || n > 64 || (n & (n - 1)) != 0) return KDN_ERR_UNSUPPORTED;
+  if (x_row_stride < n || out_row_stride < n) return KDN_ERR_INVALID_ARGUMENT;
+  if (rows == 0) return KDN_OK;
+  hipStream_t st = as_stream(stream);
+  const int64_t wgs = (rows + 3) / 4;
+  if (wgs > 0x7fffffff) return KDN_ERR_UNSUPPORTED;
+#define KDN_FWHT_CASE(T, N)                                                                                   \
+  case N:                                                                                                     \
+    hipLaunchKernelGGL((fwht_rows_kernel<T, N>), dim3((unsigned)wgs), dim3(256), 0, st, (const T*)x, rows, \
+                       x_row_stride, (T*)out, out_row_stride);                                                \
+    break;
+  if (dtype == KDN_DTYPE_F32) {
+    switch (n) { KDN_FWHT_CASE(float, 1) KDN_FWHT_CASE(float, 2) KDN_FWHT_CASE(float, 4) KDN_FWHT_CASE(float, 8)
+                 KDN_FWHT_CASE(float, 16) KDN_FWHT_CASE(float, 32) KDN_FWHT_CASE(float, 64) }
+  } else {
+    switch (n) { KDN_FWHT_CASE(__bf16, 1) KDN_FWHT_CASE(__bf16, 2) KDN_FWHT_CASE(__bf16, 4) KDN_FWHT_CASE(__bf16, 8)
+                 KDN_FWHT_CASE(__bf16, 16) KDN_FWHT_CASE(__bf16, 32) KDN_FWHT_CASE(__bf16, 64) }
+  }
+#undef KDN_FWHT_CASE
+  return launch_status();
+}
+
+extern "C" int kdn_fwht_lift(const void* x, int64_t rows, int64_t x_row_stride, int x_dtype, int normalize_input,
+                             const void* omega_bf16, const float* phase, int d_k, int D, float inv_tau, void* out,
+                             int64_t out_row_stride, int out_dtype, void* stream) {
+  if (!x || !omega_bf16 || !phase || !out || rows < 0) return KDN_ERR_INVALID_ARGUMENT;
+  if (!valid_dtype(x_dtype) || !valid_dtype(out_dtype)) return KDN_ERR_INVALID_ARGUMENT;
+  if (d_k != 64) return KDN_ERR_UNSUPPORTED;
+  if (D != 128 && D != 256 && D != 512) return KDN_ERR_UNSUPPORTED;
+  if (x_row_stride < d_k || out_row_stride < D) return KDN_ERR_INVALID_ARGUMENT;
+  if (!(inv_tau == inv_tau)) return KDN_ERR_INVALID_ARGUMENT;
+  // 16-byte vector accesses: row starts of x and out, omega rows, phase.
+  if (!aligned(x, 16) || !aligned(out, 16) || !aligned(omega_bf16, 16) || !aligned(phase, 16)) return KDN_ERR_MISALIGNED;
+  if ((x_row_stride * (int64_t)dtype_size(x_dtype)) % 16 != 0) return KDN_ERR_MISALIGNED;
+  if ((out_row_stride * (int64_t)dtype_size(out_dtype)) % 8 != 0) return KDN_ERR_MISALIGNED;
+  if (rows == 0) return KDN_OK;
+  hipStream_t st = as_stream(stream);
+  const int nz = normalize_input ? 1 : 0;
+  if (x_dtype == KDN_DTYPE_BF16) {
+    if (out_dtype == KDN_DTYPE_BF16)
+      return dispatch_lift_D<__bf16, __bf16>(D, x, rows, x_row_stride, nz, omega_bf16, phase, inv_tau, out, out_row_stride, st);
+    return dispatch_lift_D<__bf16, float>(D, x, rows, x_row_stride, nz, omega_bf16, phase, inv_tau, out, out_row_stride, st);
+  }
+  if (out_dtype == KDN_DTYPE_BF16)
+    return dispatch_lift_D<float, __bf16>(D, x, rows, x_row_stride, nz, omega_bf16, phase, inv_tau, out, out_row_stride, st);
+  return dispatch_lift_D<float, float>(D, x, rows, x_row_stride, nz, omega_bf16, phase, inv_tau, out, out_row_stride, st);
+}

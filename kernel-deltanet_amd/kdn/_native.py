@@ -1,0 +1,100 @@
+"""ctypes binding of libkdn.so, the C ABI declared in include/kdn.h.
+
+The shared library is built in-tree (kdn.build.build_native) and loaded from this directory.  There
+is no fallback: if the library is missing or fails to load, every entry point raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libkdn.so")
+
+KDN_OK = 0
+KDN_DTYPE_F32 = 0
+KDN_DTYPE_BF16 = 1
+
+# Exported symbols of include/kdn.h (checked by tests/test_abi.py).
+EXPORTED = (
+    "kdn_strerror",
+    "kdn_abi_version",
+    "kdn_build_omega",
+    "kdn_fwht",
+    "kdn_fwht_lift",
+    "kdn_scan_workspace_bytes",
+    "kdn_delta_scan_fwd",
+)
+
+_i64 = ctypes.c_int64
+_i64x3 = ctypes.c_int64 * 3
+_i64x4 = ctypes.c_int64 * 4
+
+
+class ScanArgs(ctypes.Structure):
+    """Mirror of struct kdn_scan_args (include/kdn.h); field order and types must match exactly."""
+
+    _fields_ = [
+        ("B", _i64), ("T", _i64), ("H", _i64),
+        ("d_k", ctypes.c_int), ("D", ctypes.c_int), ("d_v", ctypes.c_int),
+        ("in_dtype", ctypes.c_int), ("out_dtype", ctypes.c_int), ("normalize_input", ctypes.c_int),
+        ("inv_tau", ctypes.c_float),
+        ("q", ctypes.c_void_p), ("q_stride", _i64x3),
+        ("k", ctypes.c_void_p), ("k_stride", _i64x3),
+        ("v", ctypes.c_void_p), ("v_stride", _i64x3),
+        ("beta", ctypes.c_void_p), ("beta_stride", _i64x3),
+        ("decay", ctypes.c_void_p), ("decay_stride", _i64x3),
+        ("omega_bf16", ctypes.c_void_p),
+        ("phase", ctypes.c_void_p),
+        ("initial_state", ctypes.c_void_p), ("init_stride", _i64x4),
+        ("final_state", ctypes.c_void_p), ("final_stride", _i64x4),
+        ("y", ctypes.c_void_p), ("y_stride", _i64x3),
+        ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_size_t),
+        ("segment_chunks", _i64),
+    ]
+
+
+_lib = None
+_lock = threading.Lock()
+
+
+class NativeLibraryMissing(RuntimeError):
+    pass
+
+
+def lib() -> ctypes.CDLL:
+    """The loaded library (raises NativeLibraryMissing if it has not been built)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not os.path.exists(LIB_PATH):
+                raise NativeLibraryMissing(
+                    f"kernel-deltanet_amd: native library not built ({LIB_PATH} missing); "
+                    "run __graft_entry__.build() (hipcc --offload-arch=gfx950)")
+            L = ctypes.CDLL(LIB_PATH)
+            vp, i64, ci, cf, sz = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_float, ctypes.c_size_t
+            L.kdn_strerror.argtypes = [ci]
+            L.kdn_strerror.restype = ctypes.c_char_p
+            L.kdn_abi_version.argtypes = []
+            L.kdn_abi_version.restype = ci
+            L.kdn_build_omega.argtypes = [vp, ci, ci, vp, ci, vp]
+            L.kdn_build_omega.restype = ci
+            L.kdn_fwht.argtypes = [vp, i64, i64, ci, ci, vp, i64, vp]
+            L.kdn_fwht.restype = ci
+            L.kdn_fwht_lift.argtypes = [vp, i64, i64, ci, ci, vp, vp, ci, ci, cf, vp, i64, ci, vp]
+            L.kdn_fwht_lift.restype = ci
+            L.kdn_scan_workspace_bytes.argtypes = [ctypes.POINTER(ScanArgs)]
+            L.kdn_scan_workspace_bytes.restype = sz
+            L.kdn_delta_scan_fwd.argtypes = [ctypes.POINTER(ScanArgs), vp]
+            L.kdn_delta_scan_fwd.restype = ci
+            _lib = L
+    return _lib
+
+
+def check(status: int, what: str) -> None:
+    if status != KDN_OK:
+        msg = lib().kdn_strerror(int(status)).decode()
+        raise RuntimeError(f"{what} failed: status {status} ({msg})")

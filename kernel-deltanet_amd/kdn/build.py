@@ -1,0 +1,45 @@
+"""Build libkdn.so (all HIP kernels + the C ABI) in-tree with hipcc for gfx950.
+
+Every HIP translation unit is compiled with packed fp32 arithmetic disabled (the compiler would
+otherwise form v_pk_* fp32 ops from ordinary float code).
+"""
+from __future__ import annotations
+
+import os
+import subprocess
+import sys
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+PKG_ROOT = os.path.dirname(_HERE)
+CSRC = os.path.join(PKG_ROOT, "csrc")
+SOURCES = ["kdn_api.hip", "kdn_lift.hip", "kdn_scan.hip"]
+OUT = os.path.join(_HERE, "libkdn.so")
+ARCH = "gfx950"
+
+
+def hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc"):
+        if cand and os.path.exists(cand):
+            return cand
+    return "hipcc"
+
+
+def build_native(verbose: bool = False) -> str:
+    """Compile every source into kdn/libkdn.so; returns the library path.  Always recompiles."""
+    srcs = [os.path.join(CSRC, s) for s in SOURCES]
+    tmp = OUT + ".tmp"
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-shared",
+           "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+           "-o", tmp] + srcs
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        sys.stderr.write(res.stdout + res.stderr)
+        raise RuntimeError(f"hipcc failed ({res.returncode}) building {OUT}")
+    os.replace(tmp, OUT)
+    return OUT
+
+
+if __name__ == "__main__":
+    print(build_native(verbose=True))

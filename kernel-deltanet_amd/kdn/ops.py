@@ -1,0 +1,191 @@
+"""Tensor-level entry points over the C ABI (include/kdn.h).
+
+torch supplies device memory and the current HIP stream; every computation is a HIP kernel in
+libkdn.so.  Inputs must be gfx950 device tensors -- there is no CPU path.
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import Optional, Tuple
+
+import torch
+
+from . import _native as N
+
+_DTYPE_TAG = {torch.float32: N.KDN_DTYPE_F32, torch.bfloat16: N.KDN_DTYPE_BF16}
+
+
+def _tag(dt: torch.dtype, what: str) -> int:
+    try:
+        return _DTYPE_TAG[dt]
+    except KeyError:
+        raise TypeError(f"{what}: dtype {dt} is not supported (bfloat16 or float32)") from None
+
+
+def require_device(t: torch.Tensor, what: str) -> None:
+    """Raise unless `t` lives on a GPU: there is no CPU implementation of any entry point."""
+    if not t.is_cuda:
+        raise RuntimeError(f"{what}: kernel-deltanet_amd runs on gfx950 device tensors only (got {t.device})")
+
+
+def _stream(dev: torch.device) -> int:
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+def _rows(x: torch.Tensor, n: int) -> torch.Tensor:
+    """(..., n) -> a (rows, n) view with contiguous rows (copies only if no such view exists)."""
+    if x.dim() == 1:
+        x = x.unsqueeze(0)
+    x2 = x.reshape(-1, n)
+    if x2.stride(-1) != 1:
+        x2 = x2.contiguous()
+    return x2
+
+
+def build_omega(sign_bits: torch.Tensor, d_k: int, D: int, device, dtype=torch.bfloat16) -> torch.Tensor:
+    """Omega[D][d_k] built on `device` from the packed [M][3] Rademacher table (kdn_build_omega)."""
+    device = torch.device(device)
+    bits = sign_bits.to(device=device, dtype=torch.int64).contiguous()
+    require_device(bits, "build_omega")
+    out = torch.empty(D, d_k, dtype=dtype, device=device)
+    with torch.cuda.device(device):
+        N.check(N.lib().kdn_build_omega(ctypes.c_void_p(bits.data_ptr()), d_k, D, ctypes.c_void_p(out.data_ptr()),
+                                        _tag(dtype, "build_omega"), ctypes.c_void_p(_stream(device))),
+                "kdn_build_omega")
+    return out
+
+
+def fwht(x: torch.Tensor) -> torch.Tensor:
+    """Unnormalised natural-order FWHT along the last dimension (kdn_fwht)."""
+    require_device(x, "fwht")
+    n = x.shape[-1]
+    x2 = _rows(x, n)
+    out = torch.empty_like(x2)
+    with torch.cuda.device(x.device):
+        N.check(N.lib().kdn_fwht(ctypes.c_void_p(x2.data_ptr()), x2.shape[0], x2.stride(0), n,
+                                 _tag(x.dtype, "fwht"), ctypes.c_void_p(out.data_ptr()), out.stride(0),
+                                 ctypes.c_void_p(_stream(x.device))), "kdn_fwht")
+    return out.view(x.shape)
+
+
+def lift(x: torch.Tensor, omega_bf16: torch.Tensor, phase: torch.Tensor, inv_tau: float,
+         normalize: bool = False, out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+    """(..., d_k) -> (..., D) feature lift (kdn_fwht_lift)."""
+    require_device(x, "lift")
+    D, d_k = omega_bf16.shape
+    if x.shape[-1] != d_k:
+        raise ValueError(f"lift: last dimension {x.shape[-1]} != d_k {d_k}")
+    out_dtype = x.dtype if out_dtype is None else out_dtype
+    x2 = _rows(x, d_k)
+    if (x2.stride(0) * x2.element_size()) % 16 or x2.data_ptr() % 16:
+        x2 = x2.contiguous()
+    ph = phase.to(device=x.device, dtype=torch.float32).contiguous()
+    om = omega_bf16.to(device=x.device).contiguous()
+    out = torch.empty(x2.shape[0], D, dtype=out_dtype, device=x.device)
+    with torch.cuda.device(x.device):
+        N.check(N.lib().kdn_fwht_lift(ctypes.c_void_p(x2.data_ptr()), x2.shape[0], x2.stride(0),
+                                      _tag(x.dtype, "lift"), 1 if normalize else 0,
+                                      ctypes.c_void_p(om.data_ptr()), ctypes.c_void_p(ph.data_ptr()),
+                                      d_k, D, float(inv_tau), ctypes.c_void_p(out.data_ptr()), out.stride(0),
+                                      _tag(out_dtype, "lift output"), ctypes.c_void_p(_stream(x.device))),
+                "kdn_fwht_lift")
+    return out.view(*x.shape[:-1], D)
+
+
+def _last_contig(t: torch.Tensor) -> torch.Tensor:
+    return t if t.stride(-1) == 1 else t.contiguous()
+
+
+def scan_args(q, k, v, beta, decay, omega_bf16, phase, inv_tau, normalize, initial_state, final_state, y,
+              workspace=None, segment_chunks: int = 0) -> N.ScanArgs:
+    """Fill struct kdn_scan_args from (B, T, H, .) views."""
+    B, T, H, d_k = q.shape
+    d_v = v.shape[-1]
+    a = N.ScanArgs()
+    a.B, a.T, a.H = B, T, H
+    a.d_k, a.D, a.d_v = d_k, omega_bf16.shape[0], d_v
+    a.in_dtype = _tag(q.dtype, "scan inputs")
+    a.out_dtype = _tag(y.dtype, "scan output")
+    a.normalize_input = 1 if normalize else 0
+    a.inv_tau = float(inv_tau)
+    a.q, a.q_stride = q.data_ptr(), N._i64x3(*q.stride()[:3])
+    a.k, a.k_stride = k.data_ptr(), N._i64x3(*k.stride()[:3])
+    a.v, a.v_stride = v.data_ptr(), N._i64x3(*v.stride()[:3])
+    a.beta, a.beta_stride = beta.data_ptr(), N._i64x3(*beta.stride())
+    if decay is not None:
+        a.decay, a.decay_stride = decay.data_ptr(), N._i64x3(*decay.stride())
+    else:
+        a.decay, a.decay_stride = None, N._i64x3(0, 0, 0)
+    a.omega_bf16, a.phase = omega_bf16.data_ptr(), phase.data_ptr()
+    if initial_state is not None:
+        a.initial_state, a.init_stride = initial_state.data_ptr(), N._i64x4(*initial_state.stride())
+    else:
+        a.initial_state, a.init_stride = None, N._i64x4(0, 0, 0, 0)
+    a.final_state, a.final_stride = final_state.data_ptr(), N._i64x4(*final_state.stride())
+    a.y, a.y_stride = y.data_ptr(), N._i64x3(*y.stride()[:3])
+    a.segment_chunks = int(segment_chunks)
+    if workspace is not None:
+        a.workspace, a.workspace_bytes = workspace.data_ptr(), workspace.numel() * workspace.element_size()
+    else:
+        a.workspace, a.workspace_bytes = None, 0
+    return a
+
+
+def scan_workspace_bytes(q, v, omega_bf16, segment_chunks: int = 0) -> int:
+    B, T, H, d_k = q.shape
+    a = N.ScanArgs()
+    a.B, a.T, a.H, a.d_k, a.D, a.d_v = B, T, H, d_k, omega_bf16.shape[0], v.shape[-1]
+    a.in_dtype = _tag(q.dtype, "scan inputs")
+    a.out_dtype = a.in_dtype
+    a.inv_tau = 1.0
+    a.segment_chunks = int(segment_chunks)
+    return int(N.lib().kdn_scan_workspace_bytes(ctypes.byref(a)))
+
+
+def scan(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, beta: torch.Tensor, decay: Optional[torch.Tensor],
+         omega_bf16: torch.Tensor, phase: torch.Tensor, inv_tau: float, normalize: bool = False,
+         initial_state: Optional[torch.Tensor] = None, final_state: Optional[torch.Tensor] = None,
+         y: Optional[torch.Tensor] = None, out_dtype: Optional[torch.dtype] = None,
+         workspace: Optional[torch.Tensor] = None, segment_chunks: int = 0) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Chunked delta-rule prefill over (B, T, H, d) views (kdn_delta_scan_fwd).
+
+    q, k (B, T, H, d_k) and v (B, T, H, d_v) share a dtype; beta, decay (B, T, H) are float32 (decay may
+    be None for lambda = 1); initial_state/final_state are (B, H, D, d_v) float32 views with any strides.
+    Returns (y (B, T, H, d_v), final_state).
+    """
+    for t, nm in ((q, "q"), (k, "k"), (v, "v"), (beta, "beta")):
+        require_device(t, nm)
+    dev = q.device
+    if q.dim() != 4 or k.shape != q.shape or v.shape[:3] != q.shape[:3] or beta.shape != q.shape[:3]:
+        raise ValueError(f"scan: shapes q{tuple(q.shape)} k{tuple(k.shape)} v{tuple(v.shape)} beta{tuple(beta.shape)}")
+    if k.dtype != q.dtype or v.dtype != q.dtype:
+        raise TypeError("scan: q, k and v must share a dtype")
+    q, k, v = _last_contig(q), _last_contig(k), _last_contig(v)
+    beta = beta.to(torch.float32)
+    if decay is not None:
+        if decay.shape != beta.shape:
+            raise ValueError("scan: decay must have the shape of beta")
+        decay = decay.to(device=dev, dtype=torch.float32)
+    B, T, H, _ = q.shape
+    D = omega_bf16.shape[0]
+    d_v = v.shape[-1]
+    if initial_state is not None:
+        if tuple(initial_state.shape) != (B, H, D, d_v):
+            raise ValueError(f"scan: initial_state must be (B, H, D, d_v) = {(B, H, D, d_v)}")
+        initial_state = initial_state.to(device=dev, dtype=torch.float32)
+    if final_state is None:
+        final_state = torch.empty(B, H, D, d_v, device=dev, dtype=torch.float32)
+    if y is None:
+        y = torch.empty(B, T, H, d_v, device=dev, dtype=q.dtype if out_dtype is None else out_dtype)
+    om = omega_bf16.to(dev).contiguous()
+    ph = phase.to(device=dev, dtype=torch.float32).contiguous()
+    if workspace is None:
+        nbytes = scan_workspace_bytes(q, v, om, segment_chunks)
+        if nbytes == 0:
+            raise ValueError("scan: unsupported shape (kdn_scan_workspace_bytes returned 0)")
+        workspace = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    a = scan_args(q, k, v, beta, decay, om, ph, inv_tau, normalize, initial_state, final_state, y,
+                  workspace, segment_chunks)
+    with torch.cuda.device(dev):
+        N.check(N.lib().kdn_delta_scan_fwd(ctypes.byref(a), ctypes.c_void_p(_stream(dev))), "kdn_delta_scan_fwd")
+    return y, final_state

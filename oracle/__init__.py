@@ -1,0 +1,26 @@
+"""CPU oracle for the Kernel-DeltaNet prefill path -- TEST INFRASTRUCTURE ONLY.
+
+This package restates the reference algorithm (jatin-yadav-acad/kernel-deltanet) on the CPU so that
+the HIP kernels can be checked against it.  Only ``tests/``, ``__graft_entry__.smoke()`` and the
+``cpu_baseline`` leg of ``bench.py`` may import it, and only as the checker or the timed CPU
+baseline -- never as the thing measured or shipped.  The product package (``kernel-deltanet_amd``)
+never imports it and has no CPU fallback.
+
+Modules
+  lift  -- seeded Rademacher tables, the explicit projection Omega, the plain FWHT and the cosine
+           feature lift (reference kernels/fwht.py:25-131).
+  scan  -- the float64 token recurrence that defines the delta rule (reference
+           tests/test_fused_kernel.py:33-67, kernels/kernel_deltanet_fused.py:288-300) and an op-for-op
+           torch CPU restatement of the chunked WY scan (reference kernels/fused_kernel_deltanet.py:47-155).
+
+How each function is pinned (see tests/test_oracle_*.py):
+  make_projection   torch.manual_seed(42) uniform stream (known values), Sylvester H vs scipy.linalg.hadamard,
+                    Omega_m^T Omega_m = 4096 I, Omega columns vs butterfly construction, bit table vs signs.
+  fwht_rows         explicit H products, involution H(Hx) = n x, brute force on tiny inputs.
+  lift              ||phi_hat|| = 1, closed form on basis vectors (x = 0 -> cos(b)), Omega-vs-butterfly
+                    projection, float32/float64 agreement.
+  token_recurrence  brute-force dense-matrix products on tiny inputs, beta = 0 / orthonormal-key
+                    overwrite closed forms, contractivity.
+  chunked_forward   equals token_recurrence to 1e-12 in float64 for every chunk size, with and without
+                    decay and initial state; reference carry-algebra pin (tests/test_inter_woodbury.py:14-84).
+"""

@@ -1,0 +1,138 @@
+"""Oracle restatement of the chunked delta-rule scan -- TEST INFRASTRUCTURE ONLY.
+
+  token_recurrence  <- the defining recurrence, readout before update:
+                       reference tests/test_fused_kernel.py:53-65 and kernels/kernel_deltanet_fused.py:288-300
+  chunked_forward   <- fused_chunked_deltanet_forward, kernels/fused_kernel_deltanet.py:47-155, op for op
+                       (torch on the CPU, compute dtype selectable, state carried in the compute dtype)
+  delta_rule        <- lift (oracle.lift) followed by token_recurrence, float64: the parity definition.
+"""
+from __future__ import annotations
+
+import math
+from typing import Optional, Tuple
+
+import numpy as np
+import torch
+import torch.nn.functional as F
+
+from . import lift as olift
+
+
+def token_recurrence(phi_q, phi_k, v, beta, decay=None, S0=None) -> Tuple[np.ndarray, np.ndarray]:
+    """y_t = S_{t-1} phi_q(t);  S_t = lambda_t (S_{t-1} - beta_t (S_{t-1} phi_k(t)) phi_k(t)^T) + beta_t v_t phi_k(t)^T.
+
+    Shapes: phi_q, phi_k (B, T, D); v (B, T, d_v); beta, decay (B, T); S0 (B, d_v, D).  Float64.
+    Follows tests/test_fused_kernel.py:53-65 line for line (batched over B).
+    """
+    pq = np.asarray(phi_q, dtype=np.float64)
+    pk = np.asarray(phi_k, dtype=np.float64)
+    vv = np.asarray(v, dtype=np.float64)
+    bb = np.asarray(beta, dtype=np.float64)
+    B, T, D = pk.shape
+    dv = vv.shape[-1]
+    ll = np.ones((B, T)) if decay is None else np.asarray(decay, dtype=np.float64)
+    S = np.zeros((B, dv, D)) if S0 is None else np.array(S0, dtype=np.float64, copy=True)
+    Y = np.zeros((B, T, dv))
+    for t in range(T):
+        Y[:, t] = np.einsum("bvd,bd->bv", S, pq[:, t])
+        s_phi = np.einsum("bvd,bd->bv", S, pk[:, t])
+        S = ll[:, t, None, None] * (S - bb[:, t, None, None] * s_phi[:, :, None] * pk[:, t, None, :]) \
+            + bb[:, t, None, None] * vv[:, t, :, None] * pk[:, t, None, :]
+    return Y, S
+
+
+def delta_rule(q, k, v, beta, decay, proj: dict, initial_state=None, normalize: bool = False):
+    """Float64 definition of the whole path: lift q and k, then the token recurrence."""
+    return token_recurrence(olift.lift(q, proj, normalize), olift.lift(k, proj, normalize), v, beta, decay,
+                            initial_state)
+
+
+def _torch_lift(x: torch.Tensor, proj: dict, normalize: bool) -> torch.Tensor:
+    """kernels/fwht.py:122-131 in the tensor's dtype (CPU)."""
+    if normalize:
+        x = F.normalize(x, p=2, dim=-1, eps=1e-6)
+    omega = torch.as_tensor(proj["omega"], dtype=x.dtype)
+    b = torch.as_tensor(proj["b"]).to(x.dtype)
+    p = torch.matmul(x, omega.T)
+    s = p / proj["tau_star"] + b
+    phi = math.sqrt(2.0 / proj["D"]) * torch.cos(s)
+    return phi / (torch.norm(phi, dim=-1, keepdim=True) + 1e-8)
+
+
+def chunked_forward(q, k, v, beta, decay, proj: dict, chunk_size: int = 64,
+                    initial_state: Optional[torch.Tensor] = None, dtype=torch.float64,
+                    normalize: bool = False) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Op-for-op CPU restatement of kernels/fused_kernel_deltanet.py:47-155.
+
+    q, k (B, T, d_k); v (B, T, d_v); beta, decay (B, T); initial_state (B, d_v, D).  All arithmetic in
+    `dtype` (the reference uses the input dtype for the lift and the state and fp32 for the solves);
+    the lift of each chunk is streamed as in :95-96.  Returns Y (B, T, d_v) and S (B, d_v, D).
+    """
+    q = torch.as_tensor(q).to(dtype)
+    k = torch.as_tensor(k).to(dtype)
+    v = torch.as_tensor(v).to(dtype)
+    beta = torch.as_tensor(beta).to(dtype)
+    decay = torch.ones_like(beta) if decay is None else torch.as_tensor(decay).to(dtype)
+    B, T, d_k = k.shape
+    d_v = v.shape[-1]
+    D = proj["D"]
+    C = chunk_size
+    remainder = T % C                                                       # :55-62
+    pad_len = (C - remainder) if remainder != 0 else 0
+    if pad_len > 0:
+        q = F.pad(q, (0, 0, 0, pad_len))
+        k = F.pad(k, (0, 0, 0, pad_len))
+        v = F.pad(v, (0, 0, 0, pad_len))
+        beta = F.pad(beta, (0, pad_len), value=0.0)
+        decay = F.pad(decay, (0, pad_len), value=1.0)
+    T_pad = T + pad_len
+    nc = T_pad // C
+    k_c = k.view(B, nc, C, d_k)                                             # :67-71
+    q_c = q.view(B, nc, C, d_k)
+    v_c = v.view(B, nc, C, d_v)
+    beta_c = beta.view(B, nc, C)
+    decay_c = decay.view(B, nc, C)
+    log_d = torch.log(torch.clamp(decay_c, min=1e-5, max=1.0))            # :74-77
+    cum_log_d = torch.cumsum(log_d, dim=-1)
+    log_d_diff = cum_log_d.unsqueeze(-1) - cum_log_d.unsqueeze(-2)
+    gamma_pairwise = torch.exp(torch.clamp(log_d_diff, max=0.0))
+    upper_mask = torch.triu(torch.ones(C, C, dtype=dtype), 1).view(1, 1, C, C)   # :79-81
+    lower_mask = torch.tril(torch.ones(C, C, dtype=dtype), -1).view(1, 1, C, C)
+    eye_C = torch.eye(C, dtype=dtype).view(1, 1, C, C)
+    if initial_state is not None:                                           # :83-86
+        S = torch.as_tensor(initial_state).to(dtype).clone()
+    else:
+        S = torch.zeros(B, d_v, D, dtype=dtype)
+    Y = torch.empty(B, nc, C, d_v, dtype=dtype)
+    for c in range(nc):                                                     # :93
+        pk = _torch_lift(k_c[:, c], proj, normalize)                        # :95-96
+        pq = _torch_lift(q_c[:, c], proj, normalize)
+        G_kk = torch.matmul(pk, pk.transpose(-1, -2)).unsqueeze(1)          # :99-100
+        G_qk = torch.matmul(pq, pk.transpose(-1, -2)).unsqueeze(1)
+        bc = beta_c[:, c:c + 1]                                             # :102-105
+        U_bar = -(bc.unsqueeze(-2) * G_kk) * upper_mask
+        inv_U = torch.linalg.solve_triangular(eye_C - U_bar, eye_C.expand(B, 1, C, C), upper=True)
+        W_tilde = (bc.unsqueeze(-1) * inv_U).squeeze(1)                     # :107
+        cum = cum_log_d[:, c:c + 1]                                         # :109-111
+        g_i_to_C = torch.exp(cum[:, :, -1:] - cum)
+        W_c = ((bc * g_i_to_C).unsqueeze(-1) * inv_U).squeeze(1)
+        L_c = -(bc.unsqueeze(-1) * gamma_pairwise[:, c:c + 1] * G_kk) * lower_mask   # :113-116
+        V_tilde = torch.linalg.solve_triangular(eye_C - L_c, bc.unsqueeze(-1) * v_c[:, c:c + 1],
+                                                upper=False).squeeze(1)
+        cum_shift = F.pad(cum[:, :, :-1], (1, 0), value=0.0)               # :119-122
+        P_decay = torch.exp(torch.clamp(cum_shift.unsqueeze(-1) - cum.unsqueeze(-2), max=0.0))
+        A_intra = (G_qk * P_decay * lower_mask).squeeze(1)
+        Y_intra = torch.matmul(A_intra, V_tilde)
+        S_K = torch.matmul(S, pk.transpose(-1, -2))                         # :128-141
+        S_K_W = torch.matmul(S_K, W_tilde)
+        A_corr = (G_qk.squeeze(1) * lower_mask.squeeze(1))
+        inter_corr = torch.matmul(A_corr, S_K_W.transpose(-1, -2))
+        Q_S = torch.matmul(pq, S.transpose(-1, -2))
+        gamma_inter = torch.cat([torch.ones(B, 1, dtype=dtype), torch.exp(cum[:, 0, :-1])], dim=-1).unsqueeze(-1)
+        Y[:, c] = Y_intra + gamma_inter * (Q_S - inter_corr)
+        V_W = torch.matmul(v_c[:, c].transpose(-1, -2), W_c)               # :144-149
+        delta_S = torch.matmul(V_W, pk)
+        g0C = torch.exp(cum[:, :, -1:, None]).squeeze(1)
+        S = g0C * (S - torch.matmul(S_K_W, pk)) + delta_S
+    Yo = Y.view(B, T_pad, d_v)[:, :T]
+    return Yo, S

@@ -1,0 +1,126 @@
+"""C ABI checks that need no GPU: the library loads, exports exactly what include/kdn.h declares, the
+ctypes mirror of kdn_scan_args matches the C layout, and argument errors come back as status codes
+before anything is launched."""
+import ctypes
+import os
+import re
+import subprocess
+import tempfile
+
+import pytest
+
+from kdn import _native as N
+from kdn.build import build_native
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(REPO, "include", "kdn.h")
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(N.LIB_PATH):
+        build_native()
+    return N.lib()
+
+
+def _declared():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:int|size_t|const char\*)\s+(kdn_\w+)\s*\(", text, re.M)))
+
+
+def test_header_declares_exported_set():
+    assert _declared() == sorted(N.EXPORTED)
+
+
+def test_library_exports_every_declared_symbol(lib):
+    out = subprocess.run(["nm", "-D", "--defined-only", N.LIB_PATH], capture_output=True, text=True, check=True).stdout
+    exported = set(re.findall(r"\sT\s+(kdn_\w+)$", out, re.M))
+    for name in _declared():
+        assert name in exported, name
+        assert hasattr(lib, name)
+
+
+def test_scan_args_layout_matches_c():
+    fields = [f[0] for f in N.ScanArgs._fields_]
+    src = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', "int main(void){",
+           'printf("%zu\\n", sizeof(kdn_scan_args));']
+    src += [f'printf("%zu\\n", offsetof(kdn_scan_args, {f}));' for f in fields]
+    src += ["return 0;}"]
+    with tempfile.TemporaryDirectory() as d:
+        c = os.path.join(d, "layout.c")
+        exe = os.path.join(d, "layout")
+        open(c, "w").write("\n".join(src))
+        subprocess.run(["gcc", "-std=c99", "-o", exe, c], check=True)
+        vals = [int(x) for x in subprocess.run([exe], capture_output=True, text=True, check=True).stdout.split()]
+    assert vals[0] == ctypes.sizeof(N.ScanArgs)
+    for f, off in zip(fields, vals[1:]):
+        assert getattr(N.ScanArgs, f).offset == off, f
+
+
+def test_strerror_and_version(lib):
+    for code in (0, -1, -2, -3, -4, -5, -99):
+        assert len(lib.kdn_strerror(code)) > 0
+    assert lib.kdn_abi_version() == (1 << 16)
+
+
+def _args(**kw):
+    a = N.ScanArgs()
+    a.B, a.T, a.H, a.d_k, a.D, a.d_v = 1, 65536, 16, 64, 512, 64
+    a.in_dtype = a.out_dtype = N.KDN_DTYPE_BF16
+    a.inv_tau = 0.35355339
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+def test_workspace_bytes(lib):
+    # one 64-token chunk of one head = 230144 bytes for bf16 inputs, D = 512, d_v = 64
+    a = _args(segment_chunks=1)
+    assert lib.kdn_scan_workspace_bytes(ctypes.byref(a)) == 16 * 230144
+    assert lib.kdn_scan_workspace_bytes(ctypes.byref(_args(d_k=32))) == 0
+    assert lib.kdn_scan_workspace_bytes(ctypes.byref(_args(d_v=48))) == 0
+    a = _args(segment_chunks=100000)  # clamped to the number of chunks
+    assert lib.kdn_scan_workspace_bytes(ctypes.byref(a)) == 16 * 1024 * 230144
+
+
+def _fake_ptrs(a, base=0x7F0000000000):
+    for i, f in enumerate(("q", "k", "v", "beta", "omega_bf16", "phase", "final_state", "y", "workspace")):
+        setattr(a, f, base + 0x100000 * i)
+    a.q_stride = N._i64x3(64 * 65536 * 16, 64 * 16, 64)
+    a.k_stride = N._i64x3(64 * 65536 * 16, 64 * 16, 64)
+    a.v_stride = N._i64x3(64 * 65536 * 16, 64 * 16, 64)
+    return a
+
+
+def test_scan_argument_errors_need_no_device(lib):
+    run = lambda a: lib.kdn_delta_scan_fwd(ctypes.byref(a), None)
+    assert lib.kdn_delta_scan_fwd(None, None) == -1
+    assert run(_fake_ptrs(_args(d_k=32))) == -2
+    assert run(_fake_ptrs(_args(D=256))) == -2
+    assert run(_fake_ptrs(_args(T=0))) == -1
+    assert run(_fake_ptrs(_args(in_dtype=7))) == -1
+    a = _fake_ptrs(_args())
+    a.q = None
+    assert run(a) == -1
+    a = _fake_ptrs(_args())
+    a.q = a.q + 2
+    assert run(a) == -4
+    a = _fake_ptrs(_args())
+    a.v_stride = N._i64x3(1, 3, 1)
+    assert run(a) == -4
+    a = _fake_ptrs(_args())
+    a.workspace_bytes = 1024
+    assert run(a) == -3
+
+
+def test_lift_fwht_omega_argument_errors_need_no_device(lib):
+    p = 0x7F0000000000
+    assert lib.kdn_fwht_lift(p, 10, 64, 1, 0, p, p, 32, 512, 0.35, p, 512, 1, None) == -2
+    assert lib.kdn_fwht_lift(p, 10, 64, 1, 0, p, p, 64, 384, 0.35, p, 512, 1, None) == -2
+    assert lib.kdn_fwht_lift(p + 2, 10, 64, 1, 0, p, p, 64, 512, 0.35, p, 512, 1, None) == -4
+    assert lib.kdn_fwht_lift(None, 10, 64, 1, 0, p, p, 64, 512, 0.35, p, 512, 1, None) == -1
+    assert lib.kdn_fwht_lift(p, 0, 64, 1, 0, p, p, 64, 512, 0.35, p, 512, 1, None) == 0
+    assert lib.kdn_fwht(p, 4, 3, 3, 0, p, 3, None) == -2
+    assert lib.kdn_fwht(p, 0, 64, 64, 0, p, 64, None) == 0
+    assert lib.kdn_build_omega(p, 32, 512, p, 1, None) == -2
+    assert lib.kdn_build_omega(None, 64, 512, p, 1, None) == -1

@@ -1,0 +1,108 @@
+"""GPU parity of the lift kernels (kdn_build_omega, kdn_fwht, kdn_fwht_lift) against the CPU oracle."""
+import numpy as np
+import pytest
+import torch
+
+from kdn import ops
+from kernels import FastWalshHadamardProjection, fast_walsh_hadamard_transform
+from oracle import lift as ol
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+def rel_l2(a, b):
+    a, b = np.asarray(a, np.float64), np.asarray(b, np.float64)
+    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-300))
+
+
+@pytest.fixture(scope="module")
+def proj():
+    return FastWalshHadamardProjection(64, 512, 42)
+
+
+@pytest.fixture(scope="module")
+def oproj():
+    return ol.make_projection(64, 512, 42)
+
+
+@pytest.mark.parametrize("D", [128, 256, 512, 1024])
+@pytest.mark.parametrize("seed", [42, 3])
+def test_build_omega_bit_exact(D, seed):
+    o = ol.make_projection(64, D, seed)
+    bits = torch.tensor(o["bits"])
+    for dt in (torch.float32, torch.bfloat16):
+        om = ops.build_omega(bits, 64, D, DEV, dt).float().cpu().numpy()
+        np.testing.assert_array_equal(om, o["omega"].astype(np.float32))
+
+
+@pytest.mark.parametrize("n", [1, 2, 4, 8, 16, 32, 64])
+def test_fwht_rows(n):
+    g = torch.Generator().manual_seed(n)
+    x = torch.randn(37, n, generator=g)
+    ref = ol.fwht_rows(x.numpy())
+    out = fast_walsh_hadamard_transform(x.to(DEV)).cpu().numpy()
+    np.testing.assert_allclose(out, ref, rtol=1e-5, atol=1e-5)
+    xb = x.to(torch.bfloat16)
+    outb = fast_walsh_hadamard_transform(xb.to(DEV)).float().cpu().numpy()
+    refb = ol.fwht_rows(xb.float().numpy())
+    assert rel_l2(outb, refb) < 1e-2
+
+
+@pytest.mark.parametrize("rows", [1, 15, 16, 17, 1000, 4099])
+@pytest.mark.parametrize("normalize", [False, True])
+def test_lift_fp32(proj, oproj, rows, normalize):
+    g = torch.Generator().manual_seed(rows)
+    x = torch.randn(rows, 64, generator=g) * 1.5
+    out = ops.lift(x.to(DEV), proj.device_omega(DEV), proj.device_phase(DEV), proj.tau_star_inv, normalize)
+    ref = ol.lift(x.numpy(), oproj, normalize)
+    assert out.dtype == torch.float32 and out.shape == (rows, 512)
+    assert rel_l2(out.cpu().numpy(), ref) < 1e-5
+    assert np.abs(out.cpu().numpy() - ref).max() < 2e-5
+
+
+def test_lift_module_forward_shapes(proj, oproj):
+    x = torch.randn(2, 3, 5, 64)
+    out = proj.to(DEV)(x.to(DEV))
+    assert out.shape == (2, 3, 5, 512)
+    ref = ol.lift(x.numpy().reshape(-1, 64), oproj).reshape(2, 3, 5, 512)
+    assert rel_l2(out.cpu().numpy(), ref) < 1e-5
+
+
+def test_lift_strided_rows(proj, oproj):
+    big = torch.randn(50, 128)
+    x = big[:, 32:96]  # row stride 128, 16-byte aligned start
+    out = ops.lift(x.to(DEV), proj.device_omega(DEV), proj.device_phase(DEV), proj.tau_star_inv)
+    assert rel_l2(out.cpu().numpy(), ol.lift(x.numpy(), oproj)) < 1e-5
+
+
+@pytest.mark.parametrize("normalize", [False, True])
+def test_lift_bf16(proj, oproj, normalize):
+    g = torch.Generator().manual_seed(1234)
+    x = torch.randn(3000, 64, generator=g).to(torch.bfloat16)
+    out = ops.lift(x.to(DEV), proj.device_omega(DEV), proj.device_phase(DEV), proj.tau_star_inv, normalize)
+    assert out.dtype == torch.bfloat16
+    xr = x.float().numpy()
+    if normalize:  # F.normalize on a bf16 tensor returns bf16
+        xr = torch.nn.functional.normalize(x.float(), dim=-1, eps=1e-6).to(torch.bfloat16).float().numpy()
+    ref = ol.lift(xr, oproj)
+    o = out.float().cpu().numpy()
+    assert rel_l2(o, ref) < 1e-2
+    assert np.abs(o - ref).max() <= 1e-2 * np.abs(ref).max()
+
+
+def test_lift_config2_properties(proj, oproj):
+    """Standalone lift at the BASELINE config-2 size: 2,097,152 rows (B=8, T=16384, H=16), bf16,
+    L2-normalised rows.  Size-independent checks on all rows (unit norm) and oracle parity on a sample."""
+    rows = 8 * 16384 * 16
+    g = torch.Generator().manual_seed(1234)
+    x = torch.randn(rows, 64, generator=g).to(torch.bfloat16)
+    xd = x.to(DEV)
+    out = ops.lift(xd, proj.device_omega(DEV), proj.device_phase(DEV), proj.tau_star_inv, normalize=True)
+    norms = out.float().norm(dim=-1)
+    assert torch.isfinite(out.float()).all()
+    assert float((norms - 1).abs().max()) < 1e-2
+    idx = torch.randint(0, rows, (2048,), generator=g)
+    xs = torch.nn.functional.normalize(x[idx].float(), dim=-1, eps=1e-6).to(torch.bfloat16).float().numpy()
+    ref = ol.lift(xs, oproj)
+    assert rel_l2(out[idx.to(DEV)].float().cpu().numpy(), ref) < 1e-2
