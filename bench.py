@@ -1,0 +1,212 @@
+#!/usr/bin/env python
+"""Benchmark of the Kernel-DeltaNet prefill hot path on one MI355X.
+
+Workload (the one the headline metric is quoted on): one Kernel-DeltaNet layer
+prefill, B=1, H=16, T=65536, d_k=64 lifted to D=512, d_v=64, 64-token chunks, bf16 q/k/v ~ N(0,1),
+beta = sigmoid(N(0,1)) fp32, lambda = 1, fp32 state [16, 512, 64].  A step = the whole path over that
+batch: lift + chunk prep + state scan (one prep and one state launch; the workspace holds all chunks).
+
+Prints one JSON line.  `value` is prefill tokens/s (B*T tokens per step) with inputs resident in HBM.
+`roofline` is for the dominant kernel, its average duration measured here with HIP events on the
+launch stream; `traffic` comes from the committed rocprofv3 PMC summary when present.
+`cpu_baseline` times the oracle's fp32 chunked restatement of the reference (torch on the host
+cores) on the first tokens of the same inputs.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(REPO, "kernel-deltanet_amd")
+for _p in (REPO, PKG):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+import torch  # noqa: E402
+
+C = 64
+HBM_PEAK = 8.0e12          # B/s, MI355X HBM3E
+MFMA_BF16_PEAK = 2.5e15    # FLOP/s, MI355X dense bf16
+
+
+def flops_per_chunk(D: int, dv: int) -> dict:
+    """Algorithmic FLOPs per (head, 64-token chunk), split by kernel (terms of the reference algebra,
+    kernels/fused_kernel_deltanet.py:99-149; total 4C^2D + 6CDdv + 9C^2dv + (2/3)C^3)."""
+    prep = 4 * C * C * D + 5 * C * C * dv + (2.0 / 3.0) * C ** 3     # Grams, resolvents, U~, W~ factor
+    state = 6 * C * D * dv + 4 * C * C * dv                           # K S^T, Q S^T, update; E and Y
+    return {"prep": prep, "state": state, "total": prep + state}
+
+
+def path_bytes(B: int, T: int, H: int, D: int, dv: int, in_bytes: int = 2, out_bytes: int = 2) -> float:
+    """Minimal HBM I/O of the path: q, k, v, beta, y per head-token plus the final fp32 state."""
+    per_ht = 2 * 64 * in_bytes + dv * in_bytes + 4 + dv * out_bytes
+    return B * T * H * per_ht + B * H * D * dv * 4
+
+
+def read_pmc(path: str) -> dict:
+    """key = value lines of a committed PMC summary (profiles/*.txt)."""
+    out = {}
+    if not os.path.exists(path):
+        return out
+    for line in open(path):
+        line = line.strip()
+        if line and not line.startswith("#") and "=" in line:
+            k, v = line.split("=", 1)
+            try:
+                out[k.strip()] = float(v.strip())
+            except ValueError:
+                pass
+    return out
+
+
+def cpu_baseline(q, k, v, beta, T_sample: int) -> dict:
+    """Oracle fp32 chunked restatement (heads folded into batch) on the first T_sample tokens."""
+    from oracle import lift as ol
+    from oracle import scan as osc
+
+    torch.set_num_threads(len(os.sched_getaffinity(0)))
+    B, T, H, _ = q.shape
+    f = lambda t: t[:, :T_sample].float().permute(0, 2, 1, 3).reshape(B * H, T_sample, -1).contiguous()
+    fb = lambda t: t[:, :T_sample].float().permute(0, 2, 1).reshape(B * H, T_sample).contiguous()
+    proj = ol.make_projection(64, 512, 42)
+    args = (f(q), f(k), f(v), fb(beta), None, proj, C, None, torch.float32)
+    osc.chunked_forward(*[a[:, :C] if isinstance(a, torch.Tensor) else a for a in args])  # warm-up
+    t0 = time.perf_counter()
+    osc.chunked_forward(*args)
+    dt = time.perf_counter() - t0
+    return {"value": B * T_sample / dt, "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"oracle fp32 chunked restatement (torch CPU, heads folded into batch) on the first "
+                      f"{T_sample} tokens of the same B={B}, H={H} inputs; {dt:.2f} s"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--B", type=int, default=1)
+    ap.add_argument("--H", type=int, default=16)
+    ap.add_argument("--T", type=int, default=65536)
+    ap.add_argument("--dv", type=int, default=64)
+    ap.add_argument("--segment-chunks", type=int, default=0,
+                    help="64-token chunks per prep/state segment (0 = all chunks in one segment)")
+    ap.add_argument("--cpu-tokens", type=int, default=65536, help="tokens in the CPU-baseline sample (0 = skip)")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a plain device copy of known size (for PMC byte-counter calibration)")
+    ap.add_argument("--pmc", default=os.path.join(REPO, "profiles", "pmc_config3.txt"))
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py: this build measures one GPU only; --gpus above 1 is not supported "
+              "(the path shards over independent heads with no communication inside the scan)", file=sys.stderr)
+        sys.exit(2)
+
+    dev = torch.device("cuda:0")
+    if args.copy_calibration:
+        n = 256 << 20
+        src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(10):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes_per_dispatch_each_way": n}), flush=True)
+        return
+
+    from kdn import ops
+    from kernels import FastWalshHadamardProjection
+
+    B, H, T, dv, D = args.B, args.H, args.T, args.dv, 512
+    g = torch.Generator().manual_seed(1234)
+    q = torch.randn(B, T, H, 64, generator=g).to(torch.bfloat16)
+    k = torch.randn(B, T, H, 64, generator=g).to(torch.bfloat16)
+    v = torch.randn(B, T, H, dv, generator=g).to(torch.bfloat16)
+    beta = torch.sigmoid(torch.randn(B, T, H, generator=g))
+    proj = FastWalshHadamardProjection(64, D, 42)
+    qd, kd, vd, bd = q.to(dev), k.to(dev), v.to(dev), beta.to(dev)
+    plan = ops.ScanPlan(qd, kd, vd, bd, None, proj.device_omega(dev), proj.device_phase(dev), proj.tau_star_inv,
+                        segment_chunks=args.segment_chunks)
+    nchunks, seg = plan.nchunks, plan.segment_chunks
+    stream = torch.cuda.current_stream(dev)
+
+    for _ in range(args.warmup):
+        plan.run()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(args.steps):
+        plan.run()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms_per_step = e0.elapsed_time(e1) / args.steps
+
+    # Per-kernel durations: the same step issued as its launches (per segment: prep, then state) with
+    # events in between.
+    segs = [(c0, min(seg, nchunks - c0)) for c0 in range(0, nchunks, seg)]
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps * len(segs))]
+    i = 0
+    for _ in range(args.steps):
+        for c0, nc in segs:
+            ev[i][0].record(stream)
+            plan.prep(c0, nc)
+            ev[i][1].record(stream)
+            plan.state(c0, nc)
+            ev[i][2].record(stream)
+            i += 1
+    torch.cuda.synchronize()
+    ms_prep = sum(e[0].elapsed_time(e[1]) for e in ev) / args.steps
+    ms_state = sum(e[1].elapsed_time(e[2]) for e in ev) / args.steps
+
+    fl = flops_per_chunk(D, dv)
+    units = B * H * nchunks
+    tokens = B * T
+    phases = {
+        "prep": {"ms": ms_prep, "alg_flops": fl["prep"] * units, "tflops": fl["prep"] * units / ms_prep / 1e9},
+        "state": {"ms": ms_state, "alg_flops": fl["state"] * units, "tflops": fl["state"] * units / ms_state / 1e9},
+    }
+    dom = max(phases, key=lambda p: phases[p]["ms"])
+    achieved = phases[dom]["tflops"]
+    pmc = read_pmc(args.pmc)
+    traffic = None
+    if f"{dom}_fetch_kib" in pmc and f"{dom}_write_kib" in pmc and "copy_fetch_kib" in pmc and "copy_write_kib" in pmc:
+        copy_bytes = pmc.get("copy_bytes", 256 << 20)
+        f_fac = copy_bytes / (pmc["copy_fetch_kib"] * 1024.0)
+        w_fac = copy_bytes / (pmc["copy_write_kib"] * 1024.0)
+        traffic = pmc[f"{dom}_fetch_kib"] * 1024.0 * f_fac + pmc[f"{dom}_write_kib"] * 1024.0 * w_fac
+    path_flops = fl["total"] * units
+    out = {
+        "metric": "prefill tokens/s + ms/layer at T=64k, D=512 on 1 GPU; % of MFMA/HBM roofline",
+        "value": tokens / (ms_per_step / 1e3),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) q/k/v, sigmoid(N(0,1)) beta; projection seed 42)",
+        "config": {"workload": f"config3: one Kernel-DeltaNet layer prefill, B={B}, H={H}, T={T}, d_k=64->D={D}, "
+                               f"d_v={dv}, chunk 64, bf16 q/k/v, fp32 beta and state, lambda=1",
+                   "B": B, "H": H, "T": T, "D": D, "d_v": dv, "chunk": C, "segment_chunks": seg,
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "mfma", "achieved": achieved, "peak": MFMA_BF16_PEAK / 1e12, "unit": "TFLOP/s",
+                     "frac": achieved / (MFMA_BF16_PEAK / 1e12), "traffic": traffic, "kernel": dom},
+        "phases": phases,
+        "path": {"alg_flops": path_flops, "alg_bytes": path_bytes(B, T, H, D, dv),
+                 "tflops": path_flops / ms_per_step / 1e9,
+                 "mfma_frac": path_flops / (ms_per_step / 1e3) / MFMA_BF16_PEAK},
+    }
+    if args.cpu_tokens > 0:
+        out["cpu_baseline"] = cpu_baseline(q, k, v, beta, min(args.cpu_tokens, T))
+    else:
+        out["cpu_baseline"] = None
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

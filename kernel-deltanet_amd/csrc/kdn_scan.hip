@@ -350,9 +350,18 @@ __global__ void __launch_bounds__(256) prep_kernel(ScanParams p) {
 }
 
 // ------------------------------------------------------------------------------------------------
-// scan: grid (DV/16, H, B), 256 threads.  Workgroup = 16 state rows (value components) of one head;
-// wave w owns features [D/4 * w, D/4 * (w+1)) of those rows: S^T tiles (feature tile, row tile) in
-// accumulator layout, lane l: S^T[16tt + 4(l>>4) + i][r0 + (l&15)].
+// scan: one workgroup of 4 waves per (head, 16 value components = 16 state rows).  Wave w owns features
+// [128w, 128w + 128) of those rows: S^T tiles (feature tile, row tile) in accumulator layout, lane l holds
+// S^T[16tt + 4(l>>4) + i][r0 + (l&15)].  Per chunk:
+//   all waves   X partial over their features  X[m] = sum_j frag(m, j) S^T(j), m: 4 K-row tiles, 4 Q-row tiles
+//   barrier     wave w reduces tile w over the 8 partials
+//   wave w      E tile w  = U~ - Tp X_K,  then (after all E tiles are in LDS)  Y tile w = qscale X_Q + P E
+//   all waves   S^T <- gammaC S^T + K^T (kscale o E) on their feature tiles
+// The next chunk's operand fragments are loaded while the current chunk is computed (about 192 KB
+// in flight per workgroup), since this kernel's only parallelism is B*H*d_v/16 workgroups.
+//
+// Workgroups are dispatched round-robin over the 8 XCDs (linear id % 8); the value tiles of one head
+// get ids with equal residue so that they share one XCD's L2 for the chunk operands they all read.
 template <typename T>
 __device__ __forceinline__ void store_y(T* p, float v);
 template <>
@@ -360,119 +369,197 @@ __device__ __forceinline__ void store_y<float>(float* p, float v) { *p = v; }
 template <>
 __device__ __forceinline__ void store_y<__bf16>(__bf16* p, float v) { *p = (__bf16)v; }
 
-template <class P, typename OutT, int D, int DV>
-__global__ void __launch_bounds__(256) scan_kernel(ScanParams p) {
+constexpr int SCAN_WAVES = 4;
+
+template <class P, int D, int DV>
+struct ScanOps {
   using L = WsLayout<P, D, DV>;
   using frag = typename P::frag;
-  constexpr int NJ = D / 32;
-  constexpr int TPW = D / 64;   // feature tiles per wave
-  constexpr int JPW = D / 128;  // 32-deep feature blocks per wave
-  constexpr int NV = DV / 16;
-  __shared__ f32x4 s_xp[4][8][64];  // per-wave partial X tiles
-  __shared__ f32x4 s_x[8][64];      // reduced X (tiles 0-3: K rows, 4-7: Q rows)
-  __shared__ f32x4 s_e[4][64];      // E tiles
-
-  const int lane = threadIdx.x & 63;
-  const int w = threadIdx.x >> 6;
-  const int n = blockIdx.x;  // value tile
-  const int64_t h = blockIdx.y, b = blockIdx.z;
-  const int r = 16 * n + (lane & 15);
-
-  f32x4 S[TPW];
-#pragma unroll
-  for (int tl = 0; tl < TPW; ++tl) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int64_t d = 16 * (TPW * w + tl) + 4 * (lane >> 4) + i;
-      S[tl][i] = p.state_in ? p.state_in[b * p.is0 + h * p.is1 + d * p.is2 + r * p.is3] : 0.f;
-    }
-  }
-
-  const unsigned char* wsh = p.ws + (b * p.H + h) * p.nseg * L::bytes;
-  for (int64_t cl = 0; cl < p.nseg; ++cl) {
-    const unsigned char* ws = wsh + cl * L::bytes;
-    // X partial over this wave's features: X[m] = sum_j frag(m, j) S^T(j)
-    frag sf[JPW];
-#pragma unroll
-    for (int jj = 0; jj < JPW; ++jj) sf[jj] = P::from_f32(pair_to8(S[2 * jj], S[2 * jj + 1]));
-    f32x4 xp[8];
-#pragma unroll
-    for (int m = 0; m < 8; ++m) xp[m] = zero4();
+  static constexpr int NJ = D / 32;
+  static constexpr int TPW = D / 16 / SCAN_WAVES;  // feature tiles per wave
+  static constexpr int JPW = D / 32 / SCAN_WAVES;  // 32-deep feature blocks per wave
+  static constexpr int NV = DV / 16;
+  struct Small {
+    frag tp[2], pm[2];  // Tp and P fragments of row tile w
+    f32x4 u;            // U~ tile (w, n)
+    f32x4 qs;           // qscale of the rows of tile w
+    f32x4 ks[4];        // kscale of the 64 chunk rows in kappa order (jb, half)
+    float gC;
+  };
+  __device__ static void load_x(const unsigned char* ws, int w, int lane, frag (&ax)[8][JPW]) {
 #pragma unroll
     for (int jj = 0; jj < JPW; ++jj) {
       const int j = JPW * w + jj;
 #pragma unroll
       for (int m = 0; m < 4; ++m) {
-        const frag ak = load_frag<P>(ws + L::phiKX + (size_t)(m * NJ + j) * 64 * L::FB, lane);
-        const frag aq = load_frag<P>(ws + L::phiQX + (size_t)(m * NJ + j) * 64 * L::FB, lane);
-        xp[m] = P::mma(xp[m], ak, sf[jj]);
-        xp[4 + m] = P::mma(xp[4 + m], aq, sf[jj]);
+        ax[m][jj] = load_frag<P>(ws + L::phiKX + (size_t)(m * NJ + j) * 64 * L::FB, lane);
+        ax[4 + m][jj] = load_frag<P>(ws + L::phiQX + (size_t)(m * NJ + j) * 64 * L::FB, lane);
+      }
+    }
+  }
+  __device__ static frag load_x1(const unsigned char* ws, int w, int lane, int m, int jj) {
+    const int j = JPW * w + jj;
+    return m < 4 ? load_frag<P>(ws + L::phiKX + (size_t)(m * NJ + j) * 64 * L::FB, lane)
+                 : load_frag<P>(ws + L::phiQX + (size_t)((m - 4) * NJ + j) * 64 * L::FB, lane);
+  }
+  __device__ static frag load_u1(const unsigned char* ws, int w, int lane, int tl, int jb) {
+    return load_frag<P>(ws + L::phiKU + (size_t)((TPW * w + tl) * 2 + jb) * 64 * L::FB, lane);
+  }
+  __device__ static void load_u(const unsigned char* ws, int w, int lane, frag (&au)[TPW][2]) {
+#pragma unroll
+    for (int tl = 0; tl < TPW; ++tl)
+#pragma unroll
+      for (int jb = 0; jb < 2; ++jb)
+        au[tl][jb] = load_frag<P>(ws + L::phiKU + (size_t)((TPW * w + tl) * 2 + jb) * 64 * L::FB, lane);
+  }
+  __device__ static void load_small(const unsigned char* ws, int w, int lane, int n, Small& sm) {
+    const float* vec = reinterpret_cast<const float*>(ws + L::VEC);
+#pragma unroll
+    for (int jb = 0; jb < 2; ++jb) {
+      sm.tp[jb] = load_frag<P>(ws + L::Tp + (size_t)(w * 2 + jb) * 64 * L::FB, lane);
+      sm.pm[jb] = load_frag<P>(ws + L::Pm + (size_t)(w * 2 + jb) * 64 * L::FB, lane);
+    }
+    sm.u = *reinterpret_cast<const f32x4*>(ws + L::U + ((size_t)(w * NV + n) * 64 + lane) * 16);
+    sm.qs = *reinterpret_cast<const f32x4*>(vec + 16 * w + 4 * (lane >> 4));
+#pragma unroll
+    for (int jb = 0; jb < 2; ++jb)
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf)
+        sm.ks[jb * 2 + hf] = *reinterpret_cast<const f32x4*>(vec + 64 + 32 * jb + 16 * hf + 4 * (lane >> 4));
+    sm.gC = vec[128];
+  }
+};
+
+template <class P, typename OutT, int D, int DV>
+__global__ void __launch_bounds__(64 * SCAN_WAVES) scan_kernel(ScanParams p) {
+  using O = ScanOps<P, D, DV>;
+  using L = typename O::L;
+  using frag = typename P::frag;
+  constexpr int TPW = O::TPW, JPW = O::JPW, NV = O::NV;
+  __shared__ f32x4 s_xp[SCAN_WAVES][8][64];  // per-wave partial X tiles
+  __shared__ f32x4 s_x[8][64];               // reduced X (tiles 0-3: K rows, 4-7: Q rows)
+  __shared__ f32x4 s_e[4][64];               // E tiles
+
+  // XCD-aware decomposition of the 1-D grid: id = xcd + 8 * (rank * NV + n), head-batch pair
+  // hb = rank * 8 + xcd.  Ids that land past B*H exit at once.
+  const int64_t id = blockIdx.x;
+  const int64_t xcd = id & 7, jdx = id >> 3;
+  const int n = (int)(jdx % NV);
+  const int64_t hb = (jdx / NV) * 8 + xcd;
+  if (hb >= p.B * p.H) return;
+  const int64_t b = hb / p.H, h = hb % p.H;
+
+  const int lane = threadIdx.x & 63;
+  const int w = threadIdx.x >> 6;
+  const int r = 16 * n + (lane & 15);
+
+  f32x4 S[TPW];
+  if (p.state_in) {
+    const float* si = p.state_in + b * p.is0 + h * p.is1 + r * p.is3;
+#pragma unroll
+    for (int tl = 0; tl < TPW; ++tl)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) S[tl][i] = si[(int64_t)(16 * (TPW * w + tl) + 4 * (lane >> 4) + i) * p.is2];
+  } else {
+#pragma unroll
+    for (int tl = 0; tl < TPW; ++tl) S[tl] = zero4();
+  }
+
+  // bf16 operands: the whole next chunk is prefetched into registers (fits the 512-register budget);
+  // fp32 operands are twice as wide, so they are loaded where they are used.
+  constexpr bool PF = std::is_same<P, PrecBF16>::value;
+  const unsigned char* wsh = p.ws + hb * p.nseg * L::bytes;
+  frag ax[8][JPW];
+  frag au[TPW][2], au_n[TPW][2];
+  typename O::Small sm, sm_n;
+  if constexpr (PF) {
+    O::load_x(wsh, w, lane, ax);
+    O::load_u(wsh, w, lane, au);
+    O::load_small(wsh, w, lane, n, sm);
+  }
+
+  for (int64_t cl = 0; cl < p.nseg; ++cl) {
+    const bool more = cl + 1 < p.nseg;
+    const unsigned char* wsc = wsh + cl * L::bytes;
+    const unsigned char* wsn = wsh + (cl + 1) * L::bytes;
+    if constexpr (!PF) O::load_small(wsc, w, lane, n, sm);
+    // ---- X partial over this wave's features
+    frag sf[JPW];
+#pragma unroll
+    for (int jj = 0; jj < JPW; ++jj) sf[jj] = P::from_f32(pair_to8(S[2 * jj], S[2 * jj + 1]));
+    f32x4 xp[8];
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+      xp[m] = zero4();
+#pragma unroll
+      for (int jj = 0; jj < JPW; ++jj) {
+        if constexpr (PF) xp[m] = P::mma(xp[m], ax[m][jj], sf[jj]);
+        else xp[m] = P::mma(xp[m], O::load_x1(wsc, w, lane, m, jj), sf[jj]);
+      }
+    }
+    // ---- prefetch the next chunk's operands (the X fragments were just consumed)
+    if constexpr (PF) {
+      if (more) {
+        O::load_x(wsn, w, lane, ax);
+        O::load_u(wsn, w, lane, au_n);
+        O::load_small(wsn, w, lane, n, sm_n);
       }
     }
 #pragma unroll
     for (int m = 0; m < 8; ++m) s_xp[w][m][lane] = xp[m];
     __syncthreads();
 #pragma unroll
-    for (int mm = 0; mm < 2; ++mm) {
-      const int m = 2 * w + mm;
-      s_x[m][lane] = s_xp[0][m][lane] + s_xp[1][m][lane] + s_xp[2][m][lane] + s_xp[3][m][lane];
+    for (int mm = 0; mm < 8 / SCAN_WAVES; ++mm) {
+      const int m = SCAN_WAVES * mm + w;
+      f32x4 acc = s_xp[0][m][lane];
+#pragma unroll
+      for (int v = 1; v < SCAN_WAVES; ++v) acc += s_xp[v][m][lane];
+      s_x[m][lane] = acc;
     }
     __syncthreads();
-
-    // E tile m = w:  E = U~ - W~ S^T = U~ - Tp X_K
-    const float* vec = reinterpret_cast<const float*>(ws + L::VEC);
+    // ---- E tile w:  E = U~ - Tp X_K
     {
       f32x4 ek = zero4();
 #pragma unroll
-      for (int jb = 0; jb < 2; ++jb) {
-        const frag a = load_frag<P>(ws + L::Tp + (size_t)(w * 2 + jb) * 64 * L::FB, lane);
-        const frag bx = P::from_f32(pair_to8(s_x[2 * jb][lane], s_x[2 * jb + 1][lane]));
-        ek = P::mma(ek, a, bx);
-      }
-      const f32x4 u = *reinterpret_cast<const f32x4*>(ws + L::U + ((size_t)(w * NV + n) * 64 + lane) * 16);
-      s_e[w][lane] = u - ek;
+      for (int jb = 0; jb < 2; ++jb)
+        ek = P::mma(ek, sm.tp[jb], P::from_f32(pair_to8(s_x[2 * jb][lane], s_x[2 * jb + 1][lane])));
+      s_e[w][lane] = sm.u - ek;
     }
     __syncthreads();
-
-    // Y tile m = w:  Y = qscale * X_Q + P E
+    // ---- Y tile w:  Y = qscale X_Q + P E
     {
       f32x4 y = zero4();
 #pragma unroll
-      for (int jb = 0; jb < 2; ++jb) {
-        const frag a = load_frag<P>(ws + L::Pm + (size_t)(w * 2 + jb) * 64 * L::FB, lane);
-        const frag be = P::from_f32(pair_to8(s_e[2 * jb][lane], s_e[2 * jb + 1][lane]));
-        y = P::mma(y, a, be);
-      }
+      for (int jb = 0; jb < 2; ++jb)
+        y = P::mma(y, sm.pm[jb], P::from_f32(pair_to8(s_e[2 * jb][lane], s_e[2 * jb + 1][lane])));
       const f32x4 xq = s_x[4 + w][lane];
-      const f32x4 qs = *reinterpret_cast<const f32x4*>(vec + 16 * w + 4 * (lane >> 4));
       const int64_t tb = (p.chunk0 + cl) * CH + 16 * w + 4 * (lane >> 4);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int64_t t = tb + i;
-        if (t < p.T) store_y<OutT>((OutT*)p.y + b * p.ys0 + t * p.ys1 + h * p.ys2 + r, y[i] + qs[i] * xq[i]);
+        if (t < p.T) store_y<OutT>((OutT*)p.y + b * p.ys0 + t * p.ys1 + h * p.ys2 + r, y[i] + sm.qs[i] * xq[i]);
       }
     }
-
-    // state update:  S^T = gammaC S^T + K^T (kscale o E)
-    {
-      const float gC = vec[128];
-      frag eb[2];
+    // ---- state update on this wave's feature tiles:  S^T = gammaC S^T + K^T (kscale o E)
+    frag eb[2];
+#pragma unroll
+    for (int jb = 0; jb < 2; ++jb)
+      eb[jb] = P::from_f32(pair_to8(s_e[2 * jb][lane] * sm.ks[2 * jb], s_e[2 * jb + 1][lane] * sm.ks[2 * jb + 1]));
+#pragma unroll
+    for (int tl = 0; tl < TPW; ++tl) {
+      f32x4 acc = S[tl] * sm.gC;
 #pragma unroll
       for (int jb = 0; jb < 2; ++jb) {
-        const f32x4 k0 = *reinterpret_cast<const f32x4*>(vec + 64 + 32 * jb + 4 * (lane >> 4));
-        const f32x4 k1 = *reinterpret_cast<const f32x4*>(vec + 64 + 32 * jb + 16 + 4 * (lane >> 4));
-        eb[jb] = P::from_f32(pair_to8(s_e[2 * jb][lane] * k0, s_e[2 * jb + 1][lane] * k1));
+        if constexpr (PF) acc = P::mma(acc, au[tl][jb], eb[jb]);
+        else acc = P::mma(acc, O::load_u1(wsc, w, lane, tl, jb), eb[jb]);
       }
+      S[tl] = acc;
+    }
+    if constexpr (PF) {
+      if (more) {
 #pragma unroll
-      for (int tl = 0; tl < TPW; ++tl) {
-        const int tt = TPW * w + tl;
-        f32x4 acc = S[tl] * gC;
-#pragma unroll
-        for (int jb = 0; jb < 2; ++jb) {
-          const frag a = load_frag<P>(ws + L::phiKU + (size_t)(tt * 2 + jb) * 64 * L::FB, lane);
-          acc = P::mma(acc, a, eb[jb]);
-        }
-        S[tl] = acc;
+        for (int tl = 0; tl < TPW; ++tl) { au[tl][0] = au_n[tl][0]; au[tl][1] = au_n[tl][1]; }
+        sm = sm_n;
       }
     }
   }
@@ -487,11 +574,12 @@ __global__ void __launch_bounds__(256) scan_kernel(ScanParams p) {
   }
 }
 
+static inline unsigned scan_grid(int64_t B, int64_t H, int nv) { return (unsigned)(8 * ((B * H + 7) / 8) * nv); }
+
 // ------------------------------------------------------------------------------------------------
-template <class P, typename InT, typename OutT, int D, int DV>
-static int run_scan(const kdn_scan_args* a, int64_t seg, hipStream_t st) {
-  using L = WsLayout<P, D, DV>;
-  const int64_t nchunks = (a->T + CH - 1) / CH;
+enum Phase { PHASE_PREP = 1, PHASE_STATE = 2, PHASE_BOTH = 3 };
+
+static ScanParams fill_params(const kdn_scan_args* a) {
   ScanParams p;
   p.B = a->B; p.T = a->T; p.H = a->H;
   p.q = a->q; p.qs0 = a->q_stride[0]; p.qs1 = a->q_stride[1]; p.qs2 = a->q_stride[2];
@@ -505,9 +593,18 @@ static int run_scan(const kdn_scan_args* a, int64_t seg, hipStream_t st) {
   p.os0 = a->final_stride[0]; p.os1 = a->final_stride[1]; p.os2 = a->final_stride[2]; p.os3 = a->final_stride[3];
   p.y = a->y; p.ys0 = a->y_stride[0]; p.ys1 = a->y_stride[1]; p.ys2 = a->y_stride[2];
   p.ws = (unsigned char*)a->workspace;
-  for (int64_t c0 = 0; c0 < nchunks; c0 += seg) {
+  return p;
+}
+
+// Runs chunks [c_begin, c_end) in segments of `seg` chunks: per segment the prep and/or state kernel.
+// The state kernel of the segment starting at chunk 0 reads initial_state (zeros if NULL); later
+// segments continue from final_state.
+template <class P, typename InT, typename OutT, int D, int DV>
+static int run_scan(const kdn_scan_args* a, int64_t c_begin, int64_t c_end, int64_t seg, int phases, hipStream_t st) {
+  ScanParams p = fill_params(a);
+  for (int64_t c0 = c_begin; c0 < c_end; c0 += seg) {
     p.chunk0 = c0;
-    p.nseg = (nchunks - c0 < seg) ? (nchunks - c0) : seg;
+    p.nseg = (c_end - c0 < seg) ? (c_end - c0) : seg;
     if (c0 == 0) {
       p.state_in = a->initial_state;
       p.is0 = a->init_stride[0]; p.is1 = a->init_stride[1]; p.is2 = a->init_stride[2]; p.is3 = a->init_stride[3];
@@ -515,24 +612,36 @@ static int run_scan(const kdn_scan_args* a, int64_t seg, hipStream_t st) {
       p.state_in = a->final_state;
       p.is0 = p.os0; p.is1 = p.os1; p.is2 = p.os2; p.is3 = p.os3;
     }
-    hipLaunchKernelGGL((prep_kernel<P, InT, D, DV>), dim3((unsigned)p.nseg, (unsigned)p.H, (unsigned)p.B), dim3(256), 0, st, p);
-    if (hipGetLastError() != hipSuccess) return KDN_ERR_DEVICE;
-    hipLaunchKernelGGL((scan_kernel<P, OutT, D, DV>), dim3(DV / 16, (unsigned)p.H, (unsigned)p.B), dim3(256), 0, st, p);
-    if (hipGetLastError() != hipSuccess) return KDN_ERR_DEVICE;
+    if (phases & PHASE_PREP) {
+      hipLaunchKernelGGL((prep_kernel<P, InT, D, DV>), dim3((unsigned)p.nseg, (unsigned)p.H, (unsigned)p.B), dim3(256), 0, st, p);
+      if (hipGetLastError() != hipSuccess) return KDN_ERR_DEVICE;
+    }
+    if (phases & PHASE_STATE) {
+      hipLaunchKernelGGL((scan_kernel<P, OutT, D, DV>), dim3(scan_grid(p.B, p.H, DV / 16)), dim3(64 * SCAN_WAVES), 0, st, p);
+      if (hipGetLastError() != hipSuccess) return KDN_ERR_DEVICE;
+    }
   }
-  (void)sizeof(L);
   return KDN_OK;
 }
 
 template <class P, typename InT, typename OutT, int D>
-static int dispatch_dv(const kdn_scan_args* a, int64_t seg, hipStream_t st) {
+static int dispatch_dv(const kdn_scan_args* a, int64_t c_begin, int64_t c_end, int64_t seg, int phases, hipStream_t st) {
   switch (a->d_v) {
-    case 16: return run_scan<P, InT, OutT, D, 16>(a, seg, st);
-    case 32: return run_scan<P, InT, OutT, D, 32>(a, seg, st);
-    case 64: return run_scan<P, InT, OutT, D, 64>(a, seg, st);
-    case 128: return run_scan<P, InT, OutT, D, 128>(a, seg, st);
+    case 16: return run_scan<P, InT, OutT, D, 16>(a, c_begin, c_end, seg, phases, st);
+    case 32: return run_scan<P, InT, OutT, D, 32>(a, c_begin, c_end, seg, phases, st);
+    case 64: return run_scan<P, InT, OutT, D, 64>(a, c_begin, c_end, seg, phases, st);
+    case 128: return run_scan<P, InT, OutT, D, 128>(a, c_begin, c_end, seg, phases, st);
     default: return KDN_ERR_UNSUPPORTED;
   }
+}
+
+static int dispatch(const kdn_scan_args* a, int64_t c_begin, int64_t c_end, int64_t seg, int phases, hipStream_t st) {
+  if (a->in_dtype == KDN_DTYPE_BF16) {
+    if (a->out_dtype == KDN_DTYPE_BF16) return dispatch_dv<PrecBF16, __bf16, __bf16, 512>(a, c_begin, c_end, seg, phases, st);
+    return dispatch_dv<PrecBF16, __bf16, float, 512>(a, c_begin, c_end, seg, phases, st);
+  }
+  if (a->out_dtype == KDN_DTYPE_BF16) return dispatch_dv<PrecF32, float, __bf16, 512>(a, c_begin, c_end, seg, phases, st);
+  return dispatch_dv<PrecF32, float, float, 512>(a, c_begin, c_end, seg, phases, st);
 }
 
 static size_t chunk_bytes(const kdn_scan_args* a) {
@@ -578,7 +687,8 @@ extern "C" size_t kdn_scan_workspace_bytes(const kdn_scan_args* a) {
   return chunk_bytes(a) * (size_t)a->B * (size_t)a->H * (size_t)seg;
 }
 
-extern "C" int kdn_delta_scan_fwd(const kdn_scan_args* a, void* stream) {
+// Pointer, stride and alignment checks shared by the launching entry points.
+static int validate_launch(const kdn_scan_args* a) {
   int rc = validate(a);
   if (rc != KDN_OK) return rc;
   if (!a->q || !a->k || !a->v || !a->beta || !a->omega_bf16 || !a->phase || !a->final_state || !a->y || !a->workspace)
@@ -593,14 +703,33 @@ extern "C" int kdn_delta_scan_fwd(const kdn_scan_args* a, void* stream) {
         ((a->v_stride[i] * (int64_t)isz) % 16) != 0)
       return KDN_ERR_MISALIGNED;
   }
+  return KDN_OK;
+}
+
+extern "C" int kdn_delta_scan_fwd(const kdn_scan_args* a, void* stream) {
+  int rc = validate_launch(a);
+  if (rc != KDN_OK) return rc;
   const int64_t seg = choose_segment(a);
   const size_t need = chunk_bytes(a) * (size_t)a->B * (size_t)a->H * (size_t)seg;
   if (a->workspace_bytes < need) return KDN_ERR_WORKSPACE_TOO_SMALL;
-  hipStream_t st = as_stream(stream);
-  if (a->in_dtype == KDN_DTYPE_BF16) {
-    if (a->out_dtype == KDN_DTYPE_BF16) return dispatch_dv<PrecBF16, __bf16, __bf16, 512>(a, seg, st);
-    return dispatch_dv<PrecBF16, __bf16, float, 512>(a, seg, st);
-  }
-  if (a->out_dtype == KDN_DTYPE_BF16) return dispatch_dv<PrecF32, float, __bf16, 512>(a, seg, st);
-  return dispatch_dv<PrecF32, float, float, 512>(a, seg, st);
+  const int64_t nchunks = (a->T + CH - 1) / CH;
+  return dispatch(a, 0, nchunks, seg, PHASE_BOTH, as_stream(stream));
+}
+
+static int run_phase(const kdn_scan_args* a, int64_t chunk0, int64_t nchunks, int phase, void* stream) {
+  int rc = validate_launch(a);
+  if (rc != KDN_OK) return rc;
+  const int64_t total = (a->T + CH - 1) / CH;
+  if (chunk0 < 0 || nchunks < 1 || chunk0 + nchunks > total) return KDN_ERR_INVALID_ARGUMENT;
+  const size_t need = chunk_bytes(a) * (size_t)a->B * (size_t)a->H * (size_t)nchunks;
+  if (a->workspace_bytes < need) return KDN_ERR_WORKSPACE_TOO_SMALL;
+  return dispatch(a, chunk0, chunk0 + nchunks, nchunks, phase, as_stream(stream));
+}
+
+extern "C" int kdn_scan_prep(const kdn_scan_args* a, int64_t chunk0, int64_t nchunks, void* stream) {
+  return run_phase(a, chunk0, nchunks, PHASE_PREP, stream);
+}
+
+extern "C" int kdn_scan_state(const kdn_scan_args* a, int64_t chunk0, int64_t nchunks, void* stream) {
+  return run_phase(a, chunk0, nchunks, PHASE_STATE, stream);
 }

@@ -25,6 +25,8 @@ EXPORTED = (
     "kdn_fwht_lift",
     "kdn_scan_workspace_bytes",
     "kdn_delta_scan_fwd",
+    "kdn_scan_prep",
+    "kdn_scan_state",
 )
 
 _i64 = ctypes.c_int64
@@ -90,6 +92,10 @@ def lib() -> ctypes.CDLL:
             L.kdn_scan_workspace_bytes.restype = sz
             L.kdn_delta_scan_fwd.argtypes = [ctypes.POINTER(ScanArgs), vp]
             L.kdn_delta_scan_fwd.restype = ci
+            for nm in ("kdn_scan_prep", "kdn_scan_state"):
+                fn = getattr(L, nm)
+                fn.argtypes = [ctypes.POINTER(ScanArgs), i64, i64, vp]
+                fn.restype = ci
             _lib = L
     return _lib
 

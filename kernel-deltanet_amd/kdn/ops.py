@@ -189,3 +189,48 @@ def scan(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, beta: torch.Tensor, 
     with torch.cuda.device(dev):
         N.check(N.lib().kdn_delta_scan_fwd(ctypes.byref(a), ctypes.c_void_p(_stream(dev))), "kdn_delta_scan_fwd")
     return y, final_state
+
+
+class ScanPlan:
+    """Reusable launch description for repeated prefills of one shape (benchmarks, serving loops).
+
+    Holds the filled kdn_scan_args, the workspace for one segment of `segment_chunks` chunks and the
+    tensors the arguments point into, so each run is only the native calls.  `run()` is
+    kdn_delta_scan_fwd; `prep()` / `state()` launch the two phases of one segment.
+    """
+
+    def __init__(self, q, k, v, beta, decay, omega_bf16, phase, inv_tau, normalize=False, initial_state=None,
+                 out_dtype=None, segment_chunks: int = 0):
+        dev = q.device
+        B, T, H, _ = q.shape
+        D, d_v = omega_bf16.shape[0], v.shape[-1]
+        self.nchunks = (T + 63) // 64
+        self.segment_chunks = self.nchunks if segment_chunks <= 0 else min(segment_chunks, self.nchunks)
+        self.q, self.k, self.v = _last_contig(q), _last_contig(k), _last_contig(v)
+        self.beta = beta.to(torch.float32)
+        self.decay = None if decay is None else decay.to(torch.float32)
+        self.omega = omega_bf16.to(dev).contiguous()
+        self.phase = phase.to(device=dev, dtype=torch.float32).contiguous()
+        self.initial_state = initial_state
+        self.final_state = torch.empty(B, H, D, d_v, device=dev, dtype=torch.float32)
+        self.y = torch.empty(B, T, H, d_v, device=dev, dtype=q.dtype if out_dtype is None else out_dtype)
+        nbytes = scan_workspace_bytes(self.q, self.v, self.omega, self.segment_chunks)
+        if nbytes == 0:
+            raise ValueError("ScanPlan: unsupported shape")
+        self.workspace = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+        self.args = scan_args(self.q, self.k, self.v, self.beta, self.decay, self.omega, self.phase, inv_tau,
+                              normalize, initial_state, self.final_state, self.y, self.workspace, self.segment_chunks)
+        self.device = dev
+
+    def _stream(self):
+        return ctypes.c_void_p(_stream(self.device))
+
+    def run(self):
+        N.check(N.lib().kdn_delta_scan_fwd(ctypes.byref(self.args), self._stream()), "kdn_delta_scan_fwd")
+        return self.y, self.final_state
+
+    def prep(self, chunk0: int, nchunks: int):
+        N.check(N.lib().kdn_scan_prep(ctypes.byref(self.args), chunk0, nchunks, self._stream()), "kdn_scan_prep")
+
+    def state(self, chunk0: int, nchunks: int):
+        N.check(N.lib().kdn_scan_state(ctypes.byref(self.args), chunk0, nchunks, self._stream()), "kdn_scan_state")
