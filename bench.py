@@ -4,7 +4,7 @@
 Workload (the one the headline metric is quoted on): one Kernel-DeltaNet layer
 prefill, B=1, H=16, T=65536, d_k=64 lifted to D=512, d_v=64, 64-token chunks, bf16 q/k/v ~ N(0,1),
 beta = sigmoid(N(0,1)) fp32, lambda = 1, fp32 state [16, 512, 64].  A step = the whole path over that
-batch: lift + chunk prep + state scan (one prep and one state launch; the workspace holds all chunks).
+batch: per segment of chunks, the prep, state and output kernels.
 
 Prints one JSON line.  `value` is prefill tokens/s (B*T tokens per step) with inputs resident in HBM.
 `roofline` is for the dominant kernel, its average duration measured here with HIP events on the
@@ -37,8 +37,9 @@ def flops_per_chunk(D: int, dv: int) -> dict:
     """Algorithmic FLOPs per (head, 64-token chunk), split by kernel (terms of the reference algebra,
     kernels/fused_kernel_deltanet.py:99-149; total 4C^2D + 6CDdv + 9C^2dv + (2/3)C^3)."""
     prep = 4 * C * C * D + 5 * C * C * dv + (2.0 / 3.0) * C ** 3     # Grams, resolvents, U~, W~ factor
-    state = 6 * C * D * dv + 4 * C * C * dv                           # K S^T, Q S^T, update; E and Y
-    return {"prep": prep, "state": state, "total": prep + state}
+    state = 4 * C * D * dv + 2 * C * C * dv                           # K S^T, the update; E
+    output = 2 * C * D * dv + 2 * C * C * dv                          # Q S^T; P E
+    return {"prep": prep, "state": state, "output": output, "total": prep + state + output}
 
 
 def path_bytes(B: int, T: int, H: int, D: int, dv: int, in_bytes: int = 2, out_bytes: int = 2) -> float:
@@ -146,7 +147,7 @@ def main():
     # Per-kernel durations: the same step issued as its launches (per segment: prep, then state) with
     # events in between.
     segs = [(c0, min(seg, nchunks - c0)) for c0 in range(0, nchunks, seg)]
-    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps * len(segs))]
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(args.steps * len(segs))]
     i = 0
     for _ in range(args.steps):
         for c0, nc in segs:
@@ -155,10 +156,13 @@ def main():
             ev[i][1].record(stream)
             plan.state(c0, nc)
             ev[i][2].record(stream)
+            plan.output(c0, nc)
+            ev[i][3].record(stream)
             i += 1
     torch.cuda.synchronize()
     ms_prep = sum(e[0].elapsed_time(e[1]) for e in ev) / args.steps
     ms_state = sum(e[1].elapsed_time(e[2]) for e in ev) / args.steps
+    ms_out = sum(e[2].elapsed_time(e[3]) for e in ev) / args.steps
 
     fl = flops_per_chunk(D, dv)
     units = B * H * nchunks
@@ -166,6 +170,7 @@ def main():
     phases = {
         "prep": {"ms": ms_prep, "alg_flops": fl["prep"] * units, "tflops": fl["prep"] * units / ms_prep / 1e9},
         "state": {"ms": ms_state, "alg_flops": fl["state"] * units, "tflops": fl["state"] * units / ms_state / 1e9},
+        "output": {"ms": ms_out, "alg_flops": fl["output"] * units, "tflops": fl["output"] * units / ms_out / 1e9},
     }
     dom = max(phases, key=lambda p: phases[p]["ms"])
     achieved = phases[dom]["tflops"]

@@ -22,7 +22,8 @@
  *                          FastWalshHadamardProjection.forward, kernels/fwht.py:122-131
  *   kdn_delta_scan_fwd  <- fused_chunked_deltanet_forward, kernels/fused_kernel_deltanet.py:31-155
  *   kdn_scan_prep       <- the S-independent part of its chunk loop, kernels/fused_kernel_deltanet.py:95-122
- *   kdn_scan_state      <- the S-dependent part and the carry, kernels/fused_kernel_deltanet.py:124-149
+ *   kdn_scan_state      <- the state carry, kernels/fused_kernel_deltanet.py:128-129,144-149
+ *   kdn_scan_output     <- the chunk readout, kernels/fused_kernel_deltanet.py:118-141
  */
 #ifndef KDN_H
 #define KDN_H
@@ -116,19 +117,24 @@ size_t kdn_scan_workspace_bytes(const kdn_scan_args* a);
  * (kernels/fused_kernel_deltanet.py:74).  Replaces kernels/fused_kernel_deltanet.py:31-155. */
 int kdn_delta_scan_fwd(const kdn_scan_args* a, void* stream);
 
-/* The two phases kdn_delta_scan_fwd runs per segment, for callers that schedule them themselves (per-
- * phase timing, overlapping the prep of one segment with the state scan of the previous one on two
- * streams).  Both act on chunks [chunk0, chunk0 + nchunks) (64 tokens each) and use workspace slots
- * 0 .. nchunks-1, so a->workspace_bytes must be at least kdn_scan_workspace_bytes() of the same
- * arguments with segment_chunks = nchunks.  segment_chunks itself is ignored.
- *   kdn_scan_prep  : lift, Gram matrices, triangular inverse and every state-independent factor of
- *                    each chunk, written to the workspace.  Replaces kernels/fused_kernel_deltanet.py:95-122.
- *   kdn_scan_state : reads the prepared chunks in order, writes y and carries the state; reads
- *                    initial_state when chunk0 == 0 (zeros if NULL) and final_state otherwise, and
- *                    writes final_state.  Replaces kernels/fused_kernel_deltanet.py:124-149.
- * kdn_scan_state on a slot must follow kdn_scan_prep on that slot in stream order. */
+/* The three phases kdn_delta_scan_fwd runs per segment, for callers that schedule them themselves
+ * (per-phase timing, overlapping phases of different segments on several streams).  Each acts on
+ * chunks [chunk0, chunk0 + nchunks) (64 tokens each) using workspace slots 0 .. nchunks-1, so
+ * a->workspace_bytes must be at least kdn_scan_workspace_bytes() of the same arguments with
+ * segment_chunks = nchunks (segment_chunks itself is ignored).  On a given slot they must run in the
+ * order prep, state, output (stream order or events).
+ *   kdn_scan_prep   : lift of q and k, Gram matrices, triangular inverse and every state-independent
+ *                     factor of each chunk, written to the slot.  Replaces
+ *                     kernels/fused_kernel_deltanet.py:95-122.
+ *   kdn_scan_state  : the sequential carry: reads the prepared chunks in order, checkpoints each
+ *                     chunk's starting state and its error terms E into the slot, reads initial_state
+ *                     when chunk0 == 0 (zeros if NULL) and final_state otherwise, writes final_state.
+ *                     Replaces kernels/fused_kernel_deltanet.py:128-129,144-149.
+ *   kdn_scan_output : y of each chunk from its slot (re-lifting q).  Replaces
+ *                     kernels/fused_kernel_deltanet.py:118-141. */
 int kdn_scan_prep(const kdn_scan_args* a, int64_t chunk0, int64_t nchunks, void* stream);
 int kdn_scan_state(const kdn_scan_args* a, int64_t chunk0, int64_t nchunks, void* stream);
+int kdn_scan_output(const kdn_scan_args* a, int64_t chunk0, int64_t nchunks, void* stream);
 
 #ifdef __cplusplus
 }

@@ -7,20 +7,22 @@
 //   A[t][j]  = beta_t e^{g_t - g_j} (K K^T)[t][j]                       (j < t)
 //   T        = (I + A)^{-1}                                              (unit lower triangular)
 //   U~       = T diag(beta) V,       W~ = T diag(beta e^{g}) K
-//   E        = U~ - W~ S^T           (the per-token "errors" beta_t (v_t - lambda_t S_{t-1} k_t))
+//   E        = U~ - W~ S^T           (the per-token errors beta_t (v_t - lambda_t S_{t-1} k_t))
 //   Y        = diag(e^{g_{t-1}}) Q S^T + P E,   P[t][j] = e^{g_{t-1} - g_j} (Q K^T)[t][j]   (j < t)
 //   S_next   = e^{g_63} S + E^T diag(e^{g_63 - g}) K
 // which is algebraically the scan of kernels/fused_kernel_deltanet.py:93-149 (that code factors the
 // decay-free homogeneous part through an upper-triangular resolvent; both equal the token recurrence).
 //
-// Two kernels per segment of chunks:
-//   prep (one workgroup per chunk and head, fully parallel): lift q/k on MFMA, Gram matrices, the
-//        triangular inverse, and every S-independent factor, written to a workspace in MFMA-fragment
-//        order so that the scan reads 16 contiguous bytes per lane.
-//   scan (one workgroup per 16 state rows of a head, sequential over chunks): the S-dependent
-//        products X = [K; Q] S^T, E, Y and the state update, state resident in accumulators.
+// Three kernels per segment of chunks, so that the only sequential kernel streams as few bytes per
+// chunk as possible (64 KB of K per chunk and head):
+//   prep   (one workgroup per chunk and head): lift q and k on MFMA, Gram matrices, the triangular
+//          inverse and every S-independent factor; writes K, Tp = T diag(beta e^g |phi_k|), P, U~ and
+//          per-token scale vectors to the workspace in MFMA-fragment order.
+//   state  (one workgroup per head and 16 value components, sequential over chunks): X_K = K S^T,
+//          E = U~ - Tp X_K and the state update; checkpoints each chunk's starting S^T and E.
+//   output (one workgroup per chunk and head): re-lifts q, Y = diag(qscale) Q S^T + P E.
 // The lifted features are stored unnormalised (cos values); per-row norms are folded into the small
-// per-token scale vectors, so the lift never has to hold a whole row before writing it.
+// per-token scale vectors, so a lift never has to hold a whole row before using it.
 #include <type_traits>
 #include "kdn_frag.hpp"
 #include "kdn_internal.hpp"
@@ -30,20 +32,20 @@ namespace kdn {
 
 constexpr int CH = 64;  // tokens per chunk (internal; the WY form is exact for any chunk length)
 
+// Per (chunk, head) workspace record.
 template <class P, int D, int DV>
 struct WsLayout {
   static constexpr size_t FB = P::frag_bytes;
   static constexpr int NJ = D / 32;   // 32-deep blocks over features
-  static constexpr int NTD = D / 16;  // 16-wide feature tiles
   static constexpr int NV = DV / 16;  // 16-wide value tiles
-  static constexpr size_t phiKX = 0;                                // [m 4][j NJ][lane] K row frags
-  static constexpr size_t phiQX = phiKX + (size_t)4 * NJ * 64 * FB; // [m 4][j NJ][lane] Q row frags
-  static constexpr size_t phiKU = phiQX + (size_t)4 * NJ * 64 * FB; // [t NTD][jb 2][lane] K^T frags
-  static constexpr size_t Tp = phiKU + (size_t)NTD * 2 * 64 * FB;   // [m 4][jb 2][lane]  W~ factor
+  static constexpr size_t phiK = 0;                                 // [m 4][j NJ][lane] K row frags (cos)
+  static constexpr size_t Tp = phiK + (size_t)4 * NJ * 64 * FB;     // [m 4][jb 2][lane]  T diag(beta e^g s_k)
   static constexpr size_t Pm = Tp + (size_t)4 * 2 * 64 * FB;        // [m 4][jb 2][lane]  P
   static constexpr size_t U = Pm + (size_t)4 * 2 * 64 * FB;         // [m 4][n NV][lane] f32x4  U~
   static constexpr size_t VEC = U + (size_t)4 * NV * 64 * 16;       // qscale[64] kscale[64] gammaC
-  static constexpr size_t bytes = ((VEC + (64 + 64 + 4) * 4) + 255) / 256 * 256;
+  static constexpr size_t Sfr = VEC + 1024;                         // [j NJ][n NV][lane] chunk-start S^T frags
+  static constexpr size_t Eck = Sfr + (size_t)NJ * NV * 64 * FB;    // [m 4][n NV][lane] f32x4  E
+  static constexpr size_t bytes = (Eck + (size_t)4 * NV * 64 * 16 + 255) / 256 * 256;
 };
 
 struct ScanParams {
@@ -63,7 +65,100 @@ struct ScanParams {
 };
 
 template <class P>
-struct PrepOmegaInLds : std::integral_constant<bool, std::is_same<P, PrecBF16>::value> {};
+struct IsBF16 : std::integral_constant<bool, std::is_same<P, PrecBF16>::value> {};
+
+// ------------------------------------------------------------------------------------------------
+// Lift of one 16-row tile per wave, for NX inputs at once (each Omega fragment feeds NX MFMAs).
+// Projection in the transposed orientation Phi^T = Omega X^T: accumulator tile t holds, in lane l,
+// feature 16t + 4(l>>4) + i of row (l & 15), which is slot (t & 1) * 4 + i of X fragment t / 2.
+// Output: unnormalised cos values as X fragments, and each row's sum of squares (all lanes).
+template <class P, typename InT, int D, bool OMEGA_LDS, int NX>
+__device__ __forceinline__ void lift_tile(const InT* const (&rows)[NX], bool valid, int normalize,
+                                          const bf16x8* s_omega, const __bf16* omega, const float* s_phrev,
+                                          float ang, int lane, typename P::frag (&out)[NX][D / 32],
+                                          float (&ss)[NX]) {
+  constexpr int NT = D / 16;
+  constexpr int NSPLIT = XFrag<InT>::NSPLIT;
+  float xv[NX][2][8];
+#pragma unroll
+  for (int x = 0; x < NX; ++x)
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      if (valid) load8<InT>(rows[x] + 32 * kb + 8 * (lane >> 4), xv[x][kb]);
+      else {
+#pragma unroll
+        for (int s = 0; s < 8; ++s) xv[x][kb][s] = 0.f;
+      }
+    }
+  if (normalize) {
+#pragma unroll
+    for (int x = 0; x < NX; ++x) {
+      float sq = 0.f;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int s = 0; s < 8; ++s) sq += xv[x][kb][s] * xv[x][kb][s];
+      sq = sum_over_lane_groups(sq);
+      const float inv = 1.0f / fmaxf(sqrtf(sq), 1e-6f);
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+          const float a = xv[x][kb][s] * inv;
+          xv[x][kb][s] = (NSPLIT == 1) ? (float)(__bf16)a : a;  // F.normalize output keeps x's dtype
+        }
+    }
+  }
+  bf16x8 xb[NX][2][NSPLIT];
+#pragma unroll
+  for (int x = 0; x < NX; ++x) {
+    split_frag<NSPLIT>(xv[x][0], xb[x][0]);
+    split_frag<NSPLIT>(xv[x][1], xb[x][1]);
+    ss[x] = 0.f;
+  }
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    f32x4 acc[NX];
+#pragma unroll
+    for (int x = 0; x < NX; ++x) acc[x] = zero4();
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      bf16x8 a;
+      if constexpr (OMEGA_LDS) a = s_omega[(t * 2 + kb) * 64 + lane];
+      else a = *reinterpret_cast<const bf16x8*>(omega + (int64_t)(16 * t + (lane & 15)) * 64 + 32 * kb + 8 * (lane >> 4));
+#pragma unroll
+      for (int s = 0; s < NSPLIT; ++s)
+#pragma unroll
+        for (int x = 0; x < NX; ++x) acc[x] = PrecBF16::mma(acc[x], a, xb[x][kb][s]);
+    }
+    const f32x4 ph = *reinterpret_cast<const f32x4*>(&s_phrev[16 * t + 4 * (lane >> 4)]);
+#pragma unroll
+    for (int x = 0; x < NX; ++x)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float r = acc[x][i] * ang + ph[i];
+        r -= __builtin_rintf(r);
+        const float c = __builtin_amdgcn_cosf(r);
+        ss[x] += c * c;
+        P::set(out[x][t >> 1], (t & 1) * 4 + i, c);
+      }
+  }
+#pragma unroll
+  for (int x = 0; x < NX; ++x) ss[x] = sum_over_lane_groups(ss[x]);
+}
+
+// Omega as A fragments in LDS (lane l of fragment (t, kb): Omega[16t + (l&15)][32kb + 8(l>>4) .. +8])
+// and phase / (2 pi).
+template <int D, bool OMEGA_LDS>
+__device__ __forceinline__ void stage_omega(const __bf16* omega, const float* phase, bf16x8* s_omega, float* s_phrev) {
+  if constexpr (OMEGA_LDS) {
+    for (int idx = threadIdx.x; idx < (D / 16) * 2 * 64; idx += blockDim.x) {
+      const int l = idx & 63, tk = idx >> 6, t = tk >> 1, kb = tk & 1;
+      s_omega[idx] = *reinterpret_cast<const bf16x8*>(omega + (int64_t)(16 * t + (l & 15)) * 64 + 32 * kb + 8 * (l >> 4));
+    }
+  }
+  for (int f = threadIdx.x; f < D; f += blockDim.x) s_phrev[f] = phase[f] * 0.15915494309189535f;
+}
 
 // ------------------------------------------------------------------------------------------------
 // prep: grid (nseg, H, B), 256 threads.  Wave w owns token rows [16w, 16w+16) of the chunk.
@@ -71,10 +166,8 @@ template <class P, typename InT, int D, int DV>
 __global__ void __launch_bounds__(256) prep_kernel(ScanParams p) {
   using L = WsLayout<P, D, DV>;
   using frag = typename P::frag;
-  typedef typename std::conditional<std::is_same<P, PrecBF16>::value, __bf16, float>::type FE;  // frag element
   constexpr int NT = D / 16, NJ = D / 32, NV = DV / 16;
-  constexpr int NSPLIT = XFrag<InT>::NSPLIT;
-  constexpr bool OMEGA_LDS = PrepOmegaInLds<P>::value;
+  constexpr bool OMEGA_LDS = IsBF16<P>::value;
   constexpr size_t OMEGA_BYTES = OMEGA_LDS ? (size_t)NT * 2 * 64 * 16 : 0;
   constexpr size_t PHIK_BYTES = (size_t)4 * NJ * 64 * sizeof(frag);
   // After the Gram the K-fragment area is reused for A (16 KB), T (17 KB) and V.
@@ -95,13 +188,7 @@ __global__ void __launch_bounds__(256) prep_kernel(ScanParams p) {
   unsigned char* ws = p.ws + ((b * p.H + h) * p.nseg + cl) * L::bytes;
 
   // ---- stage Omega fragments and phases; beta and the in-chunk log-decay prefix (wave 0)
-  if constexpr (OMEGA_LDS) {
-    for (int idx = threadIdx.x; idx < NT * 2 * 64; idx += 256) {
-      const int l = idx & 63, tk = idx >> 6, t = tk >> 1, kb = tk & 1;
-      s_omega[idx] = *reinterpret_cast<const bf16x8*>(p.omega + (int64_t)(16 * t + (l & 15)) * 64 + 32 * kb + 8 * (l >> 4));
-    }
-  }
-  for (int f = threadIdx.x; f < D; f += 256) s_phrev[f] = p.phase[f] * 0.15915494309189535f;
+  stage_omega<D, OMEGA_LDS>(p.omega, p.phase, s_omega, s_phrev);
   if (w == 0) {
     const int64_t t = t0 + lane;
     const bool valid = t < p.T;
@@ -118,90 +205,26 @@ __global__ void __launch_bounds__(256) prep_kernel(ScanParams p) {
   }
   __syncthreads();
 
-  // ---- lift q and k rows of this wave: Phi^T = Omega X^T, cos, row sums of squares
+  // ---- lift q and k rows of this wave
   const int64_t trow = t0 + 16 * w + (lane & 15);
   const bool rvalid = trow < p.T;
-  float xq[2][8], xk[2][8];
-#pragma unroll
-  for (int kb = 0; kb < 2; ++kb) {
-    if (rvalid) {
-      load8<InT>((const InT*)p.q + b * p.qs0 + trow * p.qs1 + h * p.qs2 + 32 * kb + 8 * (lane >> 4), xq[kb]);
-      load8<InT>((const InT*)p.k + b * p.ks0 + trow * p.ks1 + h * p.ks2 + 32 * kb + 8 * (lane >> 4), xk[kb]);
-    } else {
-#pragma unroll
-      for (int s = 0; s < 8; ++s) { xq[kb][s] = 0.f; xk[kb][s] = 0.f; }
-    }
-  }
-  if (p.normalize) {
-    float sq = 0.f, sk = 0.f;
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int s = 0; s < 8; ++s) { sq += xq[kb][s] * xq[kb][s]; sk += xk[kb][s] * xk[kb][s]; }
-    sq = sum_over_lane_groups(sq);
-    sk = sum_over_lane_groups(sk);
-    const float iq = 1.0f / fmaxf(sqrtf(sq), 1e-6f), ik = 1.0f / fmaxf(sqrtf(sk), 1e-6f);
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int s = 0; s < 8; ++s) {
-        const float a = xq[kb][s] * iq, c = xk[kb][s] * ik;
-        xq[kb][s] = (NSPLIT == 1) ? (float)(__bf16)a : a;
-        xk[kb][s] = (NSPLIT == 1) ? (float)(__bf16)c : c;
-      }
-  }
-  bf16x8 xqb[2][NSPLIT], xkb[2][NSPLIT];
-  split_frag<NSPLIT>(xq[0], xqb[0]);
-  split_frag<NSPLIT>(xq[1], xqb[1]);
-  split_frag<NSPLIT>(xk[0], xkb[0]);
-  split_frag<NSPLIT>(xk[1], xkb[1]);
-
-  const float ang = p.inv_tau * 0.15915494309189535f;
-  frag cq[NJ], ck[NJ];  // X fragments (m = w, j): row 16w + (l&15), feature 32j + kappa(l, s)
-  float ssq = 0.f, ssk = 0.f;
-#pragma unroll
-  for (int t = 0; t < NT; ++t) {
-    f32x4 aq = zero4(), ak = zero4();
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      bf16x8 a;
-      if constexpr (OMEGA_LDS) a = s_omega[(t * 2 + kb) * 64 + lane];
-      else a = *reinterpret_cast<const bf16x8*>(p.omega + (int64_t)(16 * t + (lane & 15)) * 64 + 32 * kb + 8 * (lane >> 4));
-#pragma unroll
-      for (int s = 0; s < NSPLIT; ++s) {
-        aq = PrecBF16::mma(aq, a, xqb[kb][s]);
-        ak = PrecBF16::mma(ak, a, xkb[kb][s]);
-      }
-    }
-    // accumulator lane l: feature 16t + 4(l>>4) + i of row (l & 15)  ->  slot (t & 1) * 4 + i of frag t/2
-    const f32x4 ph = *reinterpret_cast<const f32x4*>(&s_phrev[16 * t + 4 * (lane >> 4)]);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      float rq = aq[i] * ang + ph[i];
-      float rk = ak[i] * ang + ph[i];
-      rq -= __builtin_rintf(rq);
-      rk -= __builtin_rintf(rk);
-      const float cqv = __builtin_amdgcn_cosf(rq), ckv = __builtin_amdgcn_cosf(rk);
-      ssq += cqv * cqv;
-      ssk += ckv * ckv;
-      P::set(cq[t >> 1], (t & 1) * 4 + i, cqv);
-      P::set(ck[t >> 1], (t & 1) * 4 + i, ckv);
-    }
-  }
-  ssq = sum_over_lane_groups(ssq);
-  ssk = sum_over_lane_groups(ssk);
+  const InT* rows[2] = {(const InT*)p.q + b * p.qs0 + trow * p.qs1 + h * p.qs2,
+                        (const InT*)p.k + b * p.ks0 + trow * p.ks1 + h * p.ks2};
+  frag cqk[2][NJ];  // [0] = q, [1] = k; X fragments (m = w, j): row 16w + (l&15), feature 32j + kappa(l, s)
+  float ss[2];
+  lift_tile<P, InT, D, OMEGA_LDS, 2>(rows, rvalid, p.normalize, s_omega, p.omega, s_phrev,
+                                     p.inv_tau * 0.15915494309189535f, lane, cqk, ss);
   {
     const float amp = sqrtf(2.0f / (float)D);
     if (lane < 16) {
-      s_sq[16 * w + lane] = amp / (amp * sqrtf(ssq) + 1e-8f);
-      s_sk[16 * w + lane] = amp / (amp * sqrtf(ssk) + 1e-8f);
+      s_sq[16 * w + lane] = amp / (amp * sqrtf(ss[0]) + 1e-8f);
+      s_sk[16 * w + lane] = amp / (amp * sqrtf(ss[1]) + 1e-8f);
     }
   }
 #pragma unroll
   for (int j = 0; j < NJ; ++j) {
-    store_frag<P>(ws + L::phiQX + (size_t)(w * NJ + j) * 64 * L::FB, lane, cq[j]);
-    store_frag<P>(ws + L::phiKX + (size_t)(w * NJ + j) * 64 * L::FB, lane, ck[j]);
-    s_phik[(w * NJ + j) * 64 + lane] = ck[j];
+    store_frag<P>(ws + L::phiK + (size_t)(w * NJ + j) * 64 * L::FB, lane, cqk[1][j]);
+    s_phik[(w * NJ + j) * 64 + lane] = cqk[1][j];
   }
   __syncthreads();
 
@@ -214,29 +237,8 @@ __global__ void __launch_bounds__(256) prep_kernel(ScanParams p) {
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
       const frag a = s_phik[(m * NJ + j) * 64 + lane];
-      gkk[m] = P::mma(gkk[m], a, ck[j]);
-      gqk[m] = P::mma(gqk[m], a, cq[j]);
-    }
-  }
-
-  // ---- K^T fragments for the state update: (tile tt, jb) lane l slot s = K[32jb + kappa][16tt + (l&15)]
-  {
-    const FE* e = reinterpret_cast<const FE*>(s_phik);
-    for (int tt = 8 * (NT / 32) * w; tt < 8 * (NT / 32) * (w + 1); ++tt) {
-#pragma unroll
-      for (int jb = 0; jb < 2; ++jb) {
-        frag f;
-        const int d = 16 * tt + (lane & 15);
-#pragma unroll
-        for (int s = 0; s < 8; ++s) {
-          const int c = 32 * jb + kappa(lane, s);
-          const int fi = (c >> 4) * NJ + (d >> 5);
-          const int sl = (c & 15) + 16 * ((d >> 2) & 3);
-          const int ss = 4 * ((d >> 4) & 1) + (d & 3);
-          f[s] = e[((size_t)fi * 64 + sl) * 8 + ss];
-        }
-        store_frag<P>(ws + L::phiKU + (size_t)(tt * 2 + jb) * 64 * L::FB, lane, f);
-      }
+      gkk[m] = P::mma(gkk[m], a, cqk[1][j]);
+      gqk[m] = P::mma(gqk[m], a, cqk[0][j]);
     }
   }
   __syncthreads();  // K fragments in LDS are dead from here on
@@ -329,7 +331,7 @@ __global__ void __launch_bounds__(256) prep_kernel(ScanParams p) {
         f32x8 vv;
 #pragma unroll
         for (int s = 0; s < 8; ++s) vv[s] = (float)s_V[(32 * jb + kappa(lane, s)) * DV + 16 * n + (lane & 15)];
-        if constexpr (std::is_same<P, PrecBF16>::value) {
+        if constexpr (IsBF16<P>::value) {
           // hi + lo split of T diag(beta): V is exact in bf16, so U~ keeps ~16 bits.
           bf16x8 hi, lo, vb;
 #pragma unroll
@@ -350,77 +352,44 @@ __global__ void __launch_bounds__(256) prep_kernel(ScanParams p) {
 }
 
 // ------------------------------------------------------------------------------------------------
-// scan: one workgroup of 4 waves per (head, 16 value components = 16 state rows).  Wave w owns features
-// [128w, 128w + 128) of those rows: S^T tiles (feature tile, row tile) in accumulator layout, lane l holds
-// S^T[16tt + 4(l>>4) + i][r0 + (l&15)].  Per chunk:
-//   all waves   X partial over their features  X[m] = sum_j frag(m, j) S^T(j), m: 4 K-row tiles, 4 Q-row tiles
-//   barrier     wave w reduces tile w over the 8 partials
-//   wave w      E tile w  = U~ - Tp X_K,  then (after all E tiles are in LDS)  Y tile w = qscale X_Q + P E
-//   all waves   S^T <- gammaC S^T + K^T (kscale o E) on their feature tiles
-// The next chunk's operand fragments are loaded while the current chunk is computed (about 192 KB
-// in flight per workgroup), since this kernel's only parallelism is B*H*d_v/16 workgroups.
+// state: one workgroup of 4 waves per (head, 16 value components = 16 state rows), sequential over the
+// chunks of the segment.  Wave w owns features [128w, 128w + 128) of those rows: S^T tiles (feature
+// tile, row tile) in accumulator layout, lane l holds S^T[16tt + 4(l>>4) + i][r0 + (l&15)].  Per chunk:
+//   checkpoint the chunk-start S^T (B fragments in the operand precision) for the output kernel
+//   X_K partial over the wave's features -> LDS -> wave w reduces tile w
+//   E tile w = U~ - Tp X_K  (checkpointed)
+//   S^T <- gammaC S^T + K^T (kscale o E) on the wave's feature tiles, with the K^T operand read back
+//   transposed (ds_read_b64_tr_b16) from a wave-private LDS copy of the wave's K fragments.
+// bf16: the K fragments and small operands of chunk c+2 are loaded while chunk c is computed (a
+// three-slot register ring, ~128 KB in flight per workgroup).
 //
 // Workgroups are dispatched round-robin over the 8 XCDs (linear id % 8); the value tiles of one head
-// get ids with equal residue so that they share one XCD's L2 for the chunk operands they all read.
-template <typename T>
-__device__ __forceinline__ void store_y(T* p, float v);
-template <>
-__device__ __forceinline__ void store_y<float>(float* p, float v) { *p = v; }
-template <>
-__device__ __forceinline__ void store_y<__bf16>(__bf16* p, float v) { *p = (__bf16)v; }
-
-constexpr int SCAN_WAVES = 4;
-
+// get ids with equal residue so that they share one XCD's L2 for the K fragments they all read.
 template <class P, int D, int DV>
-struct ScanOps {
+struct StateOps {
   using L = WsLayout<P, D, DV>;
   using frag = typename P::frag;
   static constexpr int NJ = D / 32;
-  static constexpr int TPW = D / 16 / SCAN_WAVES;  // feature tiles per wave
-  static constexpr int JPW = D / 32 / SCAN_WAVES;  // 32-deep feature blocks per wave
+  static constexpr int TPW = D / 64;   // feature tiles per wave
+  static constexpr int JPW = D / 128;  // 32-deep feature blocks per wave
   static constexpr int NV = DV / 16;
   struct Small {
-    frag tp[2], pm[2];  // Tp and P fragments of row tile w
-    f32x4 u;            // U~ tile (w, n)
-    f32x4 qs;           // qscale of the rows of tile w
-    f32x4 ks[4];        // kscale of the 64 chunk rows in kappa order (jb, half)
+    frag tp[2];   // Tp fragments of row tile w
+    f32x4 u;      // U~ tile (w, n)
+    f32x4 ks[4];  // kscale of the 64 chunk rows in kappa order (jb, half)
     float gC;
   };
-  __device__ static void load_x(const unsigned char* ws, int w, int lane, frag (&ax)[8][JPW]) {
+  __device__ static void load_k(const unsigned char* ws, int w, int lane, frag (&ak)[4][JPW]) {
 #pragma unroll
-    for (int jj = 0; jj < JPW; ++jj) {
-      const int j = JPW * w + jj;
+    for (int jj = 0; jj < JPW; ++jj)
 #pragma unroll
-      for (int m = 0; m < 4; ++m) {
-        ax[m][jj] = load_frag<P>(ws + L::phiKX + (size_t)(m * NJ + j) * 64 * L::FB, lane);
-        ax[4 + m][jj] = load_frag<P>(ws + L::phiQX + (size_t)(m * NJ + j) * 64 * L::FB, lane);
-      }
-    }
-  }
-  __device__ static frag load_x1(const unsigned char* ws, int w, int lane, int m, int jj) {
-    const int j = JPW * w + jj;
-    return m < 4 ? load_frag<P>(ws + L::phiKX + (size_t)(m * NJ + j) * 64 * L::FB, lane)
-                 : load_frag<P>(ws + L::phiQX + (size_t)((m - 4) * NJ + j) * 64 * L::FB, lane);
-  }
-  __device__ static frag load_u1(const unsigned char* ws, int w, int lane, int tl, int jb) {
-    return load_frag<P>(ws + L::phiKU + (size_t)((TPW * w + tl) * 2 + jb) * 64 * L::FB, lane);
-  }
-  __device__ static void load_u(const unsigned char* ws, int w, int lane, frag (&au)[TPW][2]) {
-#pragma unroll
-    for (int tl = 0; tl < TPW; ++tl)
-#pragma unroll
-      for (int jb = 0; jb < 2; ++jb)
-        au[tl][jb] = load_frag<P>(ws + L::phiKU + (size_t)((TPW * w + tl) * 2 + jb) * 64 * L::FB, lane);
+      for (int m = 0; m < 4; ++m) ak[m][jj] = load_frag<P>(ws + L::phiK + (size_t)(m * NJ + JPW * w + jj) * 64 * L::FB, lane);
   }
   __device__ static void load_small(const unsigned char* ws, int w, int lane, int n, Small& sm) {
     const float* vec = reinterpret_cast<const float*>(ws + L::VEC);
 #pragma unroll
-    for (int jb = 0; jb < 2; ++jb) {
-      sm.tp[jb] = load_frag<P>(ws + L::Tp + (size_t)(w * 2 + jb) * 64 * L::FB, lane);
-      sm.pm[jb] = load_frag<P>(ws + L::Pm + (size_t)(w * 2 + jb) * 64 * L::FB, lane);
-    }
+    for (int jb = 0; jb < 2; ++jb) sm.tp[jb] = load_frag<P>(ws + L::Tp + (size_t)(w * 2 + jb) * 64 * L::FB, lane);
     sm.u = *reinterpret_cast<const f32x4*>(ws + L::U + ((size_t)(w * NV + n) * 64 + lane) * 16);
-    sm.qs = *reinterpret_cast<const f32x4*>(vec + 16 * w + 4 * (lane >> 4));
 #pragma unroll
     for (int jb = 0; jb < 2; ++jb)
 #pragma unroll
@@ -430,15 +399,134 @@ struct ScanOps {
   }
 };
 
-template <class P, typename OutT, int D, int DV>
-__global__ void __launch_bounds__(64 * SCAN_WAVES) scan_kernel(ScanParams p) {
-  using O = ScanOps<P, D, DV>;
+struct StateShared {
+  f32x4 xp[4][4][64];  // per-wave partial X_K tiles
+  f32x4 x[4][64];      // reduced X_K
+  f32x4 e[4][64];      // E tiles
+};
+
+// K^T operand (wave-local feature tile tl, chunk block jb) from the wave's X fragments staged in LDS
+// (local fragment (m, jj) at kl[(m * 4 + jj) * 64 + lane]): lane l slot s = K[32jb + kappa(l,s)][16tl + (l&15)].
+template <class P>
+__device__ __forceinline__ typename P::frag kt_frag(const typename P::frag* kl, int lane, int tl, int jb);
+
+template <>
+__device__ __forceinline__ PrecBF16::frag kt_frag<PrecBF16>(const PrecBF16::frag* kl, int lane, int tl, int jb) {
+  // ds_read_b64_tr_b16: in each 16-lane group, output lane i slot v = element (i & 3) of the 8-byte run
+  // addressed by lane 4v + (i >> 2).  Source lane (group g, j = l & 15) addresses the 4 features
+  // 16tl + 4(j & 3) .. +3 of chunk row c = 32jb + 16 half + 4g + (j >> 2); in X-fragment order that run
+  // sits at fragment (c >> 4, tl >> 1), lane (c & 15) + 16 (j & 3), byte offset 8 (tl & 1).
+  // The two 4-element halves are combined as whole vectors: building the fragment element by element
+  // through scalar bf16 bit casts was miscompiled (every slot took element 0).
+  typedef __attribute__((ext_vector_type(4))) short s16x4;
+  typedef __attribute__((ext_vector_type(4))) __bf16 bf16x4;
+  const int g = lane >> 4, j = lane & 15;
+  bf16x4 part[2];
+#pragma unroll
+  for (int half = 0; half < 2; ++half) {
+    const int c = 32 * jb + 16 * half + 4 * g + (j >> 2);
+    const unsigned char* a = reinterpret_cast<const unsigned char*>(kl) +
+                             ((size_t)(((c >> 4) * 4 + (tl >> 1)) * 64 + (c & 15) + 16 * (j & 3)) * 16) + 8 * (tl & 1);
+    part[half] = __builtin_bit_cast(bf16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(a)));
+  }
+  return __builtin_shufflevector(part[0], part[1], 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+template <>
+__device__ __forceinline__ PrecF32::frag kt_frag<PrecF32>(const PrecF32::frag* kl, int lane, int tl, int jb) {
+  const float* e = reinterpret_cast<const float*>(kl);
+  PrecF32::frag f;
+  const int d = 16 * tl + (lane & 15);  // wave-local feature
+#pragma unroll
+  for (int s = 0; s < 8; ++s) {
+    const int c = 32 * jb + kappa(lane, s);
+    const int fi = (c >> 4) * 4 + (d >> 5);
+    f[s] = e[((size_t)fi * 64 + (c & 15) + 16 * ((d >> 2) & 3)) * 8 + 4 * ((d >> 4) & 1) + (d & 3)];
+  }
+  return f;
+}
+
+template <class P, int D, int DV, bool PF>
+__device__ __forceinline__ void state_step(const ScanParams& p, StateShared& sh, typename P::frag* kl,
+                                           unsigned char* wsh, int64_t cl, int w, int lane, int n,
+                                           f32x4 (&S)[D / 64],
+                                           typename P::frag (&ak)[4][D / 128], typename StateOps<P, D, DV>::Small& sm,
+                                           typename P::frag (&ak_pf)[4][D / 128], typename StateOps<P, D, DV>::Small& sm_pf) {
+  using O = StateOps<P, D, DV>;
   using L = typename O::L;
   using frag = typename P::frag;
   constexpr int TPW = O::TPW, JPW = O::JPW, NV = O::NV;
-  __shared__ f32x4 s_xp[SCAN_WAVES][8][64];  // per-wave partial X tiles
-  __shared__ f32x4 s_x[8][64];               // reduced X (tiles 0-3: K rows, 4-7: Q rows)
-  __shared__ f32x4 s_e[4][64];               // E tiles
+  static_assert(JPW == 4, "the transposed K read assumes four 32-deep feature blocks per wave");
+  unsigned char* cur = wsh + cl * L::bytes;
+  if constexpr (!PF) {
+    O::load_k(cur, w, lane, ak);
+    O::load_small(cur, w, lane, n, sm);
+  }
+  // ---- checkpoint the chunk-start S^T as B fragments and form the X_K partial over this wave's features
+  frag sf[JPW];
+#pragma unroll
+  for (int jj = 0; jj < JPW; ++jj) {
+    sf[jj] = P::from_f32(pair_to8(S[2 * jj], S[2 * jj + 1]));
+    store_frag<P>(cur + L::Sfr + (size_t)((JPW * w + jj) * NV + n) * 64 * L::FB, lane, sf[jj]);
+  }
+  f32x4 xp[4];
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    xp[m] = zero4();
+#pragma unroll
+    for (int jj = 0; jj < JPW; ++jj) xp[m] = P::mma(xp[m], ak[m][jj], sf[jj]);
+  }
+  // ---- stage this wave's K fragments for the transposed read-back (wave-private LDS)
+#pragma unroll
+  for (int m = 0; m < 4; ++m)
+#pragma unroll
+    for (int jj = 0; jj < JPW; ++jj) kl[(m * JPW + jj) * 64 + lane] = ak[m][jj];
+  // ---- prefetch chunk cl + 2 into the slot consumed one step ago
+  if constexpr (PF) {
+    if (cl + 2 < p.nseg) {
+      const unsigned char* nx = wsh + (cl + 2) * L::bytes;
+      O::load_k(nx, w, lane, ak_pf);
+      O::load_small(nx, w, lane, n, sm_pf);
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < 4; ++m) sh.xp[w][m][lane] = xp[m];
+  __syncthreads();
+  sh.x[w][lane] = sh.xp[0][w][lane] + sh.xp[1][w][lane] + sh.xp[2][w][lane] + sh.xp[3][w][lane];
+  __syncthreads();
+  // ---- E tile w:  E = U~ - Tp X_K
+  {
+    f32x4 ek = zero4();
+#pragma unroll
+    for (int jb = 0; jb < 2; ++jb) ek = P::mma(ek, sm.tp[jb], P::from_f32(pair_to8(sh.x[2 * jb][lane], sh.x[2 * jb + 1][lane])));
+    const f32x4 e = sm.u - ek;
+    sh.e[w][lane] = e;
+    *reinterpret_cast<f32x4*>(cur + L::Eck + ((size_t)(w * NV + n) * 64 + lane) * 16) = e;
+  }
+  __syncthreads();
+  // ---- state update on this wave's feature tiles:  S^T = gammaC S^T + K^T (kscale o E)
+  frag eb[2];
+#pragma unroll
+  for (int jb = 0; jb < 2; ++jb)
+    eb[jb] = P::from_f32(pair_to8(sh.e[2 * jb][lane] * sm.ks[2 * jb], sh.e[2 * jb + 1][lane] * sm.ks[2 * jb + 1]));
+#pragma unroll
+  for (int tl = 0; tl < TPW; ++tl) {
+    f32x4 acc = S[tl] * sm.gC;
+#pragma unroll
+    for (int jb = 0; jb < 2; ++jb) acc = P::mma(acc, kt_frag<P>(kl, lane, tl, jb), eb[jb]);
+    S[tl] = acc;
+  }
+}
+
+template <class P, int D, int DV>
+__global__ void __launch_bounds__(256) state_kernel(ScanParams p) {
+  using O = StateOps<P, D, DV>;
+  using L = typename O::L;
+  using frag = typename P::frag;
+  constexpr int TPW = O::TPW, JPW = O::JPW, NV = O::NV;
+  constexpr bool PF = IsBF16<P>::value;  // fp32 fragments are twice as wide; they are loaded per chunk
+  __shared__ StateShared sh;
+  __shared__ frag s_kl[4][4 * JPW * 64];  // wave-private K fragments
 
   // XCD-aware decomposition of the 1-D grid: id = xcd + 8 * (rank * NV + n), head-batch pair
   // hb = rank * 8 + xcd.  Ids that land past B*H exit at once.
@@ -452,6 +540,7 @@ __global__ void __launch_bounds__(64 * SCAN_WAVES) scan_kernel(ScanParams p) {
   const int lane = threadIdx.x & 63;
   const int w = threadIdx.x >> 6;
   const int r = 16 * n + (lane & 15);
+  frag* kl = s_kl[w];
 
   f32x4 S[TPW];
   if (p.state_in) {
@@ -465,119 +554,111 @@ __global__ void __launch_bounds__(64 * SCAN_WAVES) scan_kernel(ScanParams p) {
     for (int tl = 0; tl < TPW; ++tl) S[tl] = zero4();
   }
 
-  // bf16 operands: the whole next chunk is prefetched into registers (fits the 512-register budget);
-  // fp32 operands are twice as wide, so they are loaded where they are used.
-  constexpr bool PF = std::is_same<P, PrecBF16>::value;
-  const unsigned char* wsh = p.ws + hb * p.nseg * L::bytes;
-  frag ax[8][JPW];
-  frag au[TPW][2], au_n[TPW][2];
-  typename O::Small sm, sm_n;
+  unsigned char* wsh = p.ws + hb * p.nseg * L::bytes;
+  frag k0[4][JPW], k1[4][JPW], k2[4][JPW];
+  typename O::Small s0, s1, s2;
   if constexpr (PF) {
-    O::load_x(wsh, w, lane, ax);
-    O::load_u(wsh, w, lane, au);
-    O::load_small(wsh, w, lane, n, sm);
+    O::load_k(wsh, w, lane, k0);
+    O::load_small(wsh, w, lane, n, s0);
+    if (p.nseg > 1) {
+      O::load_k(wsh + L::bytes, w, lane, k1);
+      O::load_small(wsh + L::bytes, w, lane, n, s1);
+    }
+  }
+  for (int64_t cl = 0; cl < p.nseg; cl += 3) {
+    state_step<P, D, DV, PF>(p, sh, kl, wsh, cl, w, lane, n, S, k0, s0, k2, s2);
+    if (cl + 1 < p.nseg) state_step<P, D, DV, PF>(p, sh, kl, wsh, cl + 1, w, lane, n, S, k1, s1, k0, s0);
+    if (cl + 2 < p.nseg) state_step<P, D, DV, PF>(p, sh, kl, wsh, cl + 2, w, lane, n, S, k2, s2, k1, s1);
   }
 
-  for (int64_t cl = 0; cl < p.nseg; ++cl) {
-    const bool more = cl + 1 < p.nseg;
-    const unsigned char* wsc = wsh + cl * L::bytes;
-    const unsigned char* wsn = wsh + (cl + 1) * L::bytes;
-    if constexpr (!PF) O::load_small(wsc, w, lane, n, sm);
-    // ---- X partial over this wave's features
-    frag sf[JPW];
+  float* so = p.state_out + b * p.os0 + h * p.os1 + r * p.os3;
 #pragma unroll
-    for (int jj = 0; jj < JPW; ++jj) sf[jj] = P::from_f32(pair_to8(S[2 * jj], S[2 * jj + 1]));
-    f32x4 xp[8];
+  for (int tl = 0; tl < TPW; ++tl)
 #pragma unroll
-    for (int m = 0; m < 8; ++m) {
-      xp[m] = zero4();
+    for (int i = 0; i < 4; ++i) so[(int64_t)(16 * (TPW * w + tl) + 4 * (lane >> 4) + i) * p.os2] = S[tl][i];
+}
+
+// ------------------------------------------------------------------------------------------------
+// output: grid (nseg, H, B), 256 threads.  Wave w re-lifts query rows [16w, 16w+16) of the chunk into
+// LDS; then wave w computes the value tiles n = w, w+4, ...:  Y[:, n] = diag(qscale) Q S_c^T[:, n] + P E[:, n].
+template <typename T>
+__device__ __forceinline__ void store_y(T* p, float v);
+template <>
+__device__ __forceinline__ void store_y<float>(float* p, float v) { *p = v; }
+template <>
+__device__ __forceinline__ void store_y<__bf16>(__bf16* p, float v) { *p = (__bf16)v; }
+
+template <class P, typename InT, typename OutT, int D, int DV>
+__global__ void __launch_bounds__(256) output_kernel(ScanParams p) {
+  using L = WsLayout<P, D, DV>;
+  using frag = typename P::frag;
+  constexpr int NT = D / 16, NJ = D / 32, NV = DV / 16;
+  constexpr bool OMEGA_LDS = IsBF16<P>::value;
+  constexpr size_t OMEGA_BYTES = OMEGA_LDS ? (size_t)NT * 2 * 64 * 16 : 0;
+  __shared__ __attribute__((aligned(16))) unsigned char smem[OMEGA_BYTES + (size_t)4 * NJ * 64 * sizeof(frag)];
+  __shared__ __attribute__((aligned(16))) float s_phrev[D];
+  bf16x8* s_omega = reinterpret_cast<bf16x8*>(smem);
+  frag* s_q = reinterpret_cast<frag*>(smem + OMEGA_BYTES);
+
+  const int lane = threadIdx.x & 63;
+  const int w = threadIdx.x >> 6;
+  const int64_t cl = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int64_t t0 = (p.chunk0 + cl) * CH;
+  const unsigned char* ws = p.ws + ((b * p.H + h) * p.nseg + cl) * L::bytes;
+  const float* vec = reinterpret_cast<const float*>(ws + L::VEC);
+
+  stage_omega<D, OMEGA_LDS>(p.omega, p.phase, s_omega, s_phrev);
+  __syncthreads();
+  {
+    const int64_t trow = t0 + 16 * w + (lane & 15);
+    const InT* rows[1] = {(const InT*)p.q + b * p.qs0 + trow * p.qs1 + h * p.qs2};
+    frag cq[1][NJ];
+    float ss[1];
+    lift_tile<P, InT, D, OMEGA_LDS, 1>(rows, trow < p.T, p.normalize, s_omega, p.omega, s_phrev,
+                                       p.inv_tau * 0.15915494309189535f, lane, cq, ss);
 #pragma unroll
-      for (int jj = 0; jj < JPW; ++jj) {
-        if constexpr (PF) xp[m] = P::mma(xp[m], ax[m][jj], sf[jj]);
-        else xp[m] = P::mma(xp[m], O::load_x1(wsc, w, lane, m, jj), sf[jj]);
-      }
+    for (int j = 0; j < NJ; ++j) s_q[(w * NJ + j) * 64 + lane] = cq[0][j];
+  }
+  __syncthreads();
+
+  for (int n = w; n < NV; n += 4) {
+    f32x4 xq[4];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) xq[m] = zero4();
+#pragma unroll 4
+    for (int j = 0; j < NJ; ++j) {
+      const frag sfr = load_frag<P>(ws + L::Sfr + (size_t)(j * NV + n) * 64 * L::FB, lane);
+#pragma unroll
+      for (int m = 0; m < 4; ++m) xq[m] = P::mma(xq[m], s_q[(m * NJ + j) * 64 + lane], sfr);
     }
-    // ---- prefetch the next chunk's operands (the X fragments were just consumed)
-    if constexpr (PF) {
-      if (more) {
-        O::load_x(wsn, w, lane, ax);
-        O::load_u(wsn, w, lane, au_n);
-        O::load_small(wsn, w, lane, n, sm_n);
-      }
+    frag eb[2];
+#pragma unroll
+    for (int jb = 0; jb < 2; ++jb) {
+      const f32x4 e0 = *reinterpret_cast<const f32x4*>(ws + L::Eck + ((size_t)((2 * jb) * NV + n) * 64 + lane) * 16);
+      const f32x4 e1 = *reinterpret_cast<const f32x4*>(ws + L::Eck + ((size_t)((2 * jb + 1) * NV + n) * 64 + lane) * 16);
+      eb[jb] = P::from_f32(pair_to8(e0, e1));
     }
+    const int r = 16 * n + (lane & 15);
 #pragma unroll
-    for (int m = 0; m < 8; ++m) s_xp[w][m][lane] = xp[m];
-    __syncthreads();
-#pragma unroll
-    for (int mm = 0; mm < 8 / SCAN_WAVES; ++mm) {
-      const int m = SCAN_WAVES * mm + w;
-      f32x4 acc = s_xp[0][m][lane];
-#pragma unroll
-      for (int v = 1; v < SCAN_WAVES; ++v) acc += s_xp[v][m][lane];
-      s_x[m][lane] = acc;
-    }
-    __syncthreads();
-    // ---- E tile w:  E = U~ - Tp X_K
-    {
-      f32x4 ek = zero4();
-#pragma unroll
-      for (int jb = 0; jb < 2; ++jb)
-        ek = P::mma(ek, sm.tp[jb], P::from_f32(pair_to8(s_x[2 * jb][lane], s_x[2 * jb + 1][lane])));
-      s_e[w][lane] = sm.u - ek;
-    }
-    __syncthreads();
-    // ---- Y tile w:  Y = qscale X_Q + P E
-    {
+    for (int m = 0; m < 4; ++m) {
       f32x4 y = zero4();
 #pragma unroll
-      for (int jb = 0; jb < 2; ++jb)
-        y = P::mma(y, sm.pm[jb], P::from_f32(pair_to8(s_e[2 * jb][lane], s_e[2 * jb + 1][lane])));
-      const f32x4 xq = s_x[4 + w][lane];
-      const int64_t tb = (p.chunk0 + cl) * CH + 16 * w + 4 * (lane >> 4);
+      for (int jb = 0; jb < 2; ++jb) y = P::mma(y, load_frag<P>(ws + L::Pm + (size_t)(m * 2 + jb) * 64 * L::FB, lane), eb[jb]);
+      const f32x4 qs = *reinterpret_cast<const f32x4*>(vec + 16 * m + 4 * (lane >> 4));
+      const int64_t tb = t0 + 16 * m + 4 * (lane >> 4);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int64_t t = tb + i;
-        if (t < p.T) store_y<OutT>((OutT*)p.y + b * p.ys0 + t * p.ys1 + h * p.ys2 + r, y[i] + sm.qs[i] * xq[i]);
+        if (t < p.T) store_y<OutT>((OutT*)p.y + b * p.ys0 + t * p.ys1 + h * p.ys2 + r, y[i] + qs[i] * xq[m][i]);
       }
-    }
-    // ---- state update on this wave's feature tiles:  S^T = gammaC S^T + K^T (kscale o E)
-    frag eb[2];
-#pragma unroll
-    for (int jb = 0; jb < 2; ++jb)
-      eb[jb] = P::from_f32(pair_to8(s_e[2 * jb][lane] * sm.ks[2 * jb], s_e[2 * jb + 1][lane] * sm.ks[2 * jb + 1]));
-#pragma unroll
-    for (int tl = 0; tl < TPW; ++tl) {
-      f32x4 acc = S[tl] * sm.gC;
-#pragma unroll
-      for (int jb = 0; jb < 2; ++jb) {
-        if constexpr (PF) acc = P::mma(acc, au[tl][jb], eb[jb]);
-        else acc = P::mma(acc, O::load_u1(wsc, w, lane, tl, jb), eb[jb]);
-      }
-      S[tl] = acc;
-    }
-    if constexpr (PF) {
-      if (more) {
-#pragma unroll
-        for (int tl = 0; tl < TPW; ++tl) { au[tl][0] = au_n[tl][0]; au[tl][1] = au_n[tl][1]; }
-        sm = sm_n;
-      }
-    }
-  }
-
-#pragma unroll
-  for (int tl = 0; tl < TPW; ++tl) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int64_t d = 16 * (TPW * w + tl) + 4 * (lane >> 4) + i;
-      p.state_out[b * p.os0 + h * p.os1 + d * p.os2 + r * p.os3] = S[tl][i];
     }
   }
 }
 
-static inline unsigned scan_grid(int64_t B, int64_t H, int nv) { return (unsigned)(8 * ((B * H + 7) / 8) * nv); }
+static inline unsigned state_grid(int64_t B, int64_t H, int nv) { return (unsigned)(8 * ((B * H + 7) / 8) * nv); }
 
 // ------------------------------------------------------------------------------------------------
-enum Phase { PHASE_PREP = 1, PHASE_STATE = 2, PHASE_BOTH = 3 };
+enum Phase { PHASE_PREP = 1, PHASE_STATE = 2, PHASE_OUTPUT = 4, PHASE_ALL = 7 };
 
 static ScanParams fill_params(const kdn_scan_args* a) {
   ScanParams p;
@@ -596,9 +677,9 @@ static ScanParams fill_params(const kdn_scan_args* a) {
   return p;
 }
 
-// Runs chunks [c_begin, c_end) in segments of `seg` chunks: per segment the prep and/or state kernel.
-// The state kernel of the segment starting at chunk 0 reads initial_state (zeros if NULL); later
-// segments continue from final_state.
+// Runs chunks [c_begin, c_end) in segments of `seg` chunks: per segment the selected kernels, in the
+// order prep, state, output.  The state kernel of the segment starting at chunk 0 reads initial_state
+// (zeros if NULL); later segments continue from final_state.
 template <class P, typename InT, typename OutT, int D, int DV>
 static int run_scan(const kdn_scan_args* a, int64_t c_begin, int64_t c_end, int64_t seg, int phases, hipStream_t st) {
   ScanParams p = fill_params(a);
@@ -612,12 +693,17 @@ static int run_scan(const kdn_scan_args* a, int64_t c_begin, int64_t c_end, int6
       p.state_in = a->final_state;
       p.is0 = p.os0; p.is1 = p.os1; p.is2 = p.os2; p.is3 = p.os3;
     }
+    const dim3 chunk_grid((unsigned)p.nseg, (unsigned)p.H, (unsigned)p.B);
     if (phases & PHASE_PREP) {
-      hipLaunchKernelGGL((prep_kernel<P, InT, D, DV>), dim3((unsigned)p.nseg, (unsigned)p.H, (unsigned)p.B), dim3(256), 0, st, p);
+      hipLaunchKernelGGL((prep_kernel<P, InT, D, DV>), chunk_grid, dim3(256), 0, st, p);
       if (hipGetLastError() != hipSuccess) return KDN_ERR_DEVICE;
     }
     if (phases & PHASE_STATE) {
-      hipLaunchKernelGGL((scan_kernel<P, OutT, D, DV>), dim3(scan_grid(p.B, p.H, DV / 16)), dim3(64 * SCAN_WAVES), 0, st, p);
+      hipLaunchKernelGGL((state_kernel<P, D, DV>), dim3(state_grid(p.B, p.H, DV / 16)), dim3(256), 0, st, p);
+      if (hipGetLastError() != hipSuccess) return KDN_ERR_DEVICE;
+    }
+    if (phases & PHASE_OUTPUT) {
+      hipLaunchKernelGGL((output_kernel<P, InT, OutT, D, DV>), chunk_grid, dim3(256), 0, st, p);
       if (hipGetLastError() != hipSuccess) return KDN_ERR_DEVICE;
     }
   }
@@ -655,13 +741,14 @@ static size_t chunk_bytes(const kdn_scan_args* a) {
   }
 }
 
-// Default segment: enough chunks that the workspace stays near 1 GiB.
+// Default segment: the workspace of one segment stays near 64 MiB (so that the state and output
+// kernels mostly re-read what prep just wrote from the 256 MB last-level cache), at least 8 chunks.
 static int64_t choose_segment(const kdn_scan_args* a) {
   const int64_t nchunks = (a->T + CH - 1) / CH;
   if (a->segment_chunks > 0) return a->segment_chunks < nchunks ? a->segment_chunks : nchunks;
   const size_t per_step = chunk_bytes(a) * (size_t)a->B * (size_t)a->H;
-  int64_t seg = (int64_t)(((size_t)1 << 30) / (per_step ? per_step : 1));
-  if (seg < 1) seg = 1;
+  int64_t seg = (int64_t)(((size_t)64 << 20) / (per_step ? per_step : 1));
+  if (seg < 8) seg = 8;
   return seg < nchunks ? seg : nchunks;
 }
 
@@ -675,16 +762,6 @@ static int validate(const kdn_scan_args* a) {
   if (a->segment_chunks < 0) return KDN_ERR_INVALID_ARGUMENT;
   if (!(a->inv_tau == a->inv_tau)) return KDN_ERR_INVALID_ARGUMENT;
   return KDN_OK;
-}
-
-}  // namespace kdn
-
-using namespace kdn;
-
-extern "C" size_t kdn_scan_workspace_bytes(const kdn_scan_args* a) {
-  if (validate(a) != KDN_OK) return 0;
-  const int64_t seg = choose_segment(a);
-  return chunk_bytes(a) * (size_t)a->B * (size_t)a->H * (size_t)seg;
 }
 
 // Pointer, stride and alignment checks shared by the launching entry points.
@@ -706,16 +783,6 @@ static int validate_launch(const kdn_scan_args* a) {
   return KDN_OK;
 }
 
-extern "C" int kdn_delta_scan_fwd(const kdn_scan_args* a, void* stream) {
-  int rc = validate_launch(a);
-  if (rc != KDN_OK) return rc;
-  const int64_t seg = choose_segment(a);
-  const size_t need = chunk_bytes(a) * (size_t)a->B * (size_t)a->H * (size_t)seg;
-  if (a->workspace_bytes < need) return KDN_ERR_WORKSPACE_TOO_SMALL;
-  const int64_t nchunks = (a->T + CH - 1) / CH;
-  return dispatch(a, 0, nchunks, seg, PHASE_BOTH, as_stream(stream));
-}
-
 static int run_phase(const kdn_scan_args* a, int64_t chunk0, int64_t nchunks, int phase, void* stream) {
   int rc = validate_launch(a);
   if (rc != KDN_OK) return rc;
@@ -726,10 +793,34 @@ static int run_phase(const kdn_scan_args* a, int64_t chunk0, int64_t nchunks, in
   return dispatch(a, chunk0, chunk0 + nchunks, nchunks, phase, as_stream(stream));
 }
 
+}  // namespace kdn
+
+using namespace kdn;
+
+extern "C" size_t kdn_scan_workspace_bytes(const kdn_scan_args* a) {
+  if (validate(a) != KDN_OK) return 0;
+  const int64_t seg = choose_segment(a);
+  return chunk_bytes(a) * (size_t)a->B * (size_t)a->H * (size_t)seg;
+}
+
+extern "C" int kdn_delta_scan_fwd(const kdn_scan_args* a, void* stream) {
+  int rc = validate_launch(a);
+  if (rc != KDN_OK) return rc;
+  const int64_t seg = choose_segment(a);
+  const size_t need = chunk_bytes(a) * (size_t)a->B * (size_t)a->H * (size_t)seg;
+  if (a->workspace_bytes < need) return KDN_ERR_WORKSPACE_TOO_SMALL;
+  const int64_t nchunks = (a->T + CH - 1) / CH;
+  return dispatch(a, 0, nchunks, seg, PHASE_ALL, as_stream(stream));
+}
+
 extern "C" int kdn_scan_prep(const kdn_scan_args* a, int64_t chunk0, int64_t nchunks, void* stream) {
   return run_phase(a, chunk0, nchunks, PHASE_PREP, stream);
 }
 
 extern "C" int kdn_scan_state(const kdn_scan_args* a, int64_t chunk0, int64_t nchunks, void* stream) {
   return run_phase(a, chunk0, nchunks, PHASE_STATE, stream);
+}
+
+extern "C" int kdn_scan_output(const kdn_scan_args* a, int64_t chunk0, int64_t nchunks, void* stream) {
+  return run_phase(a, chunk0, nchunks, PHASE_OUTPUT, stream);
 }

@@ -27,6 +27,7 @@ EXPORTED = (
     "kdn_delta_scan_fwd",
     "kdn_scan_prep",
     "kdn_scan_state",
+    "kdn_scan_output",
 )
 
 _i64 = ctypes.c_int64
@@ -92,7 +93,7 @@ def lib() -> ctypes.CDLL:
             L.kdn_scan_workspace_bytes.restype = sz
             L.kdn_delta_scan_fwd.argtypes = [ctypes.POINTER(ScanArgs), vp]
             L.kdn_delta_scan_fwd.restype = ci
-            for nm in ("kdn_scan_prep", "kdn_scan_state"):
+            for nm in ("kdn_scan_prep", "kdn_scan_state", "kdn_scan_output"):
                 fn = getattr(L, nm)
                 fn.argtypes = [ctypes.POINTER(ScanArgs), i64, i64, vp]
                 fn.restype = ci

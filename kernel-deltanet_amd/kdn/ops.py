@@ -234,3 +234,6 @@ class ScanPlan:
 
     def state(self, chunk0: int, nchunks: int):
         N.check(N.lib().kdn_scan_state(ctypes.byref(self.args), chunk0, nchunks, self._stream()), "kdn_scan_state")
+
+    def output(self, chunk0: int, nchunks: int):
+        N.check(N.lib().kdn_scan_output(ctypes.byref(self.args), chunk0, nchunks, self._stream()), "kdn_scan_output")
