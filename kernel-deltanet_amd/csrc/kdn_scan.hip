@@ -32,7 +32,8 @@ namespace kdn {
 
 constexpr int CH = 64;  // tokens per chunk (internal; the WY form is exact for any chunk length)
 
-// Per (chunk, head) workspace record.
+// Per (chunk, head) workspace record.  A segment of nseg chunks uses nseg + 1 records per head: the
+// last one is scratch for the state kernel's writes past the final chunk.
 template <class P, int D, int DV>
 struct WsLayout {
   static constexpr size_t FB = P::frag_bytes;
@@ -185,7 +186,7 @@ __global__ void __launch_bounds__(256) prep_kernel(ScanParams p) {
   const int w = threadIdx.x >> 6;
   const int64_t cl = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
   const int64_t t0 = (p.chunk0 + cl) * CH;
-  unsigned char* ws = p.ws + ((b * p.H + h) * p.nseg + cl) * L::bytes;
+  unsigned char* ws = p.ws + ((b * p.H + h) * (p.nseg + 1) + cl) * L::bytes;
 
   // ---- stage Omega fragments and phases; beta and the in-chunk log-decay prefix (wave 0)
   stage_omega<D, OMEGA_LDS>(p.omega, p.phase, s_omega, s_phrev);
@@ -356,12 +357,14 @@ __global__ void __launch_bounds__(256) prep_kernel(ScanParams p) {
 // chunks of the segment.  Wave w owns features [128w, 128w + 128) of those rows: S^T tiles (feature
 // tile, row tile) in accumulator layout, lane l holds S^T[16tt + 4(l>>4) + i][r0 + (l&15)].  Per chunk:
 //   checkpoint the chunk-start S^T (B fragments in the operand precision) for the output kernel
-//   X_K partial over the wave's features -> LDS -> wave w reduces tile w
-//   E tile w = U~ - Tp X_K  (checkpointed)
+//   X_K partial over the wave's features -> LDS -> barrier -> wave w reduces token tile w -> LDS -> barrier
+//   E tile w = U~ - Tp X_K (checkpointed) -> LDS -> barrier
 //   S^T <- gammaC S^T + K^T (kscale o E) on the wave's feature tiles, with the K^T operand read back
 //   transposed (ds_read_b64_tr_b16) from a wave-private LDS copy of the wave's K fragments.
-// bf16: the K fragments and small operands of chunk c+2 are loaded while chunk c is computed (a
-// three-slot register ring, ~128 KB in flight per workgroup).
+// Three workgroup barriers per chunk.  bf16: the K fragments and small operands of chunk c+1 are loaded
+// at the start of chunk c (a two-slot register ring) while an L2 prefetch runs L2_AHEAD chunks ahead;
+// the refill is unconditional (its chunk index is clamped to the segment) so that the compiler's
+// memory-counter waits stay static and only wait for the slot that is about to be used.
 //
 // Workgroups are dispatched round-robin over the 8 XCDs (linear id % 8); the value tiles of one head
 // get ids with equal residue so that they share one XCD's L2 for the K fragments they all read.
@@ -373,40 +376,81 @@ struct StateOps {
   static constexpr int TPW = D / 64;   // feature tiles per wave
   static constexpr int JPW = D / 128;  // 32-deep feature blocks per wave
   static constexpr int NV = DV / 16;
+  static constexpr int L2_AHEAD = 6;  // chunks ahead of the current one that the L2 prefetch touches
+  // dword loads per wave that cover the operand area [0, Sfr) of one chunk record at one per line
+  static constexpr int L2_LOADS = (int)((L::Sfr / 128 + 4 * NV * 64 - 1) / (4 * NV * 64));
   struct Small {
-    frag tp[2];   // Tp fragments of row tile w
-    f32x4 u;      // U~ tile (w, n)
-    f32x4 ks[4];  // kscale of the 64 chunk rows in kappa order (jb, half)
+    frag tp[2];  // Tp fragments of row tile w
+    f32x4 u;     // U~ tile (w, n)
+    f32x4 ks;    // kscale of the rows of token tile w, accumulator order
     float gC;
   };
-  __device__ static void load_k(const unsigned char* ws, int w, int lane, frag (&ak)[4][JPW]) {
+  // The operands of one chunk in four parts (token tile m of K plus one small operand each), so that
+  // the refill of a slot can be spread over the four barrier-separated phases of a step instead of
+  // queueing ~20 KB of loads per wave at once behind the texture unit.
+  template <int PART>
+  __device__ static void load_part(const unsigned char* ws, int w, int lane, int n, frag (&ak)[4][JPW], Small& sm) {
 #pragma unroll
-    for (int jj = 0; jj < JPW; ++jj)
+    for (int jj = 0; jj < JPW; ++jj) ak[PART][jj] = load_frag<P>(ws + L::phiK + (size_t)(PART * NJ + JPW * w + jj) * 64 * L::FB, lane);
+    if constexpr (PART == 0) {
 #pragma unroll
-      for (int m = 0; m < 4; ++m) ak[m][jj] = load_frag<P>(ws + L::phiK + (size_t)(m * NJ + JPW * w + jj) * 64 * L::FB, lane);
+      for (int jb = 0; jb < 2; ++jb) sm.tp[jb] = load_frag<P>(ws + L::Tp + (size_t)(w * 2 + jb) * 64 * L::FB, lane);
+    } else if constexpr (PART == 1) {
+      sm.u = *reinterpret_cast<const f32x4*>(ws + L::U + ((size_t)(w * NV + n) * 64 + lane) * 16);
+    } else if constexpr (PART == 2) {
+      sm.ks = *reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(ws + L::VEC) + 64 + 16 * w + 4 * (lane >> 4));
+    } else {
+      sm.gC = reinterpret_cast<const float*>(ws + L::VEC)[128];
+    }
   }
-  __device__ static void load_small(const unsigned char* ws, int w, int lane, int n, Small& sm) {
-    const float* vec = reinterpret_cast<const float*>(ws + L::VEC);
-#pragma unroll
-    for (int jb = 0; jb < 2; ++jb) sm.tp[jb] = load_frag<P>(ws + L::Tp + (size_t)(w * 2 + jb) * 64 * L::FB, lane);
-    sm.u = *reinterpret_cast<const f32x4*>(ws + L::U + ((size_t)(w * NV + n) * 64 + lane) * 16);
-#pragma unroll
-    for (int jb = 0; jb < 2; ++jb)
-#pragma unroll
-      for (int hf = 0; hf < 2; ++hf)
-        sm.ks[jb * 2 + hf] = *reinterpret_cast<const f32x4*>(vec + 64 + 32 * jb + 16 * hf + 4 * (lane >> 4));
-    sm.gC = vec[128];
+  __device__ static void load_all(const unsigned char* ws, int w, int lane, int n, frag (&ak)[4][JPW], Small& sm) {
+    load_part<0>(ws, w, lane, n, ak, sm);
+    load_part<1>(ws, w, lane, n, ak, sm);
+    load_part<2>(ws, w, lane, n, ak, sm);
+    load_part<3>(ws, w, lane, n, ak, sm);
   }
 };
 
 struct StateShared {
-  f32x4 xp[4][4][64];  // per-wave partial X_K tiles
-  f32x4 x[4][64];      // reduced X_K
-  f32x4 e[4][64];      // E tiles
+  f32x4 xp[4][4][64];  // per-wave partial X_K tiles [wave][token tile][lane]
+  f32x4 x[4][64];      // reduced X_K [token tile][lane]
+  f32x4 e[4][64];      // E tiles [token tile][lane]
 };
 
-// K^T operand (wave-local feature tile tl, chunk block jb) from the wave's X fragments staged in LDS
-// (local fragment (m, jj) at kl[(m * 4 + jj) * 64 + lane]): lane l slot s = K[32jb + kappa(l,s)][16tl + (l&15)].
+// Wave-private LDS copy of the wave's 16 K fragments (token tile m, local 32-feature block jj), from
+// which the K^T operand of the state update is read back transposed.
+//   bf16: two planes of 8 KB; plane h holds bytes [8h, 8h+8) of every lane's 16-byte fragment slot
+//         (features 16h .. 16h+15 of the 32-block) at (fragment * 64 + lane) * 8, so that each
+//         transposed read below covers 512 contiguous bytes (no bank conflicts).
+//   fp32: fragments in lane order, 32 bytes per lane.
+template <class P>
+__device__ __forceinline__ void stage_k(typename P::frag* kl, int lane, const typename P::frag (&ak)[4][4]);
+
+template <>
+__device__ __forceinline__ void stage_k<PrecBF16>(PrecBF16::frag* kl, int lane, const PrecBF16::frag (&ak)[4][4]) {
+  typedef __attribute__((ext_vector_type(4))) __bf16 bf16x4;
+  unsigned char* base = reinterpret_cast<unsigned char*>(kl);
+#pragma unroll
+  for (int m = 0; m < 4; ++m)
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      const int fi = m * 4 + jj;
+      *reinterpret_cast<bf16x4*>(base + (size_t)(fi * 64 + lane) * 8) = __builtin_shufflevector(ak[m][jj], ak[m][jj], 0, 1, 2, 3);
+      *reinterpret_cast<bf16x4*>(base + 8192 + (size_t)(fi * 64 + lane) * 8) =
+          __builtin_shufflevector(ak[m][jj], ak[m][jj], 4, 5, 6, 7);
+    }
+}
+
+template <>
+__device__ __forceinline__ void stage_k<PrecF32>(PrecF32::frag* kl, int lane, const PrecF32::frag (&ak)[4][4]) {
+#pragma unroll
+  for (int m = 0; m < 4; ++m)
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) kl[(m * 4 + jj) * 64 + lane] = ak[m][jj];
+}
+
+// K^T operand (wave-local feature tile tl, chunk block jb) from the staged copy:
+// lane l slot s = K[32jb + kappa(l,s)][16tl + (l&15)].
 template <class P>
 __device__ __forceinline__ typename P::frag kt_frag(const typename P::frag* kl, int lane, int tl, int jb);
 
@@ -415,18 +459,18 @@ __device__ __forceinline__ PrecBF16::frag kt_frag<PrecBF16>(const PrecBF16::frag
   // ds_read_b64_tr_b16: in each 16-lane group, output lane i slot v = element (i & 3) of the 8-byte run
   // addressed by lane 4v + (i >> 2).  Source lane (group g, j = l & 15) addresses the 4 features
   // 16tl + 4(j & 3) .. +3 of chunk row c = 32jb + 16 half + 4g + (j >> 2); in X-fragment order that run
-  // sits at fragment (c >> 4, tl >> 1), lane (c & 15) + 16 (j & 3), byte offset 8 (tl & 1).
+  // is half (tl & 1) of fragment (c >> 4, tl >> 1), lane (c & 15) + 16 (j & 3), i.e. plane (tl & 1).
   // The two 4-element halves are combined as whole vectors: building the fragment element by element
   // through scalar bf16 bit casts was miscompiled (every slot took element 0).
   typedef __attribute__((ext_vector_type(4))) short s16x4;
   typedef __attribute__((ext_vector_type(4))) __bf16 bf16x4;
   const int g = lane >> 4, j = lane & 15;
+  const unsigned char* plane = reinterpret_cast<const unsigned char*>(kl) + 8192 * (tl & 1);
   bf16x4 part[2];
 #pragma unroll
   for (int half = 0; half < 2; ++half) {
     const int c = 32 * jb + 16 * half + 4 * g + (j >> 2);
-    const unsigned char* a = reinterpret_cast<const unsigned char*>(kl) +
-                             ((size_t)(((c >> 4) * 4 + (tl >> 1)) * 64 + (c & 15) + 16 * (j & 3)) * 16) + 8 * (tl & 1);
+    const unsigned char* a = plane + (size_t)(((c >> 4) * 4 + (tl >> 1)) * 64 + (c & 15) + 16 * (j & 3)) * 8;
     part[half] = __builtin_bit_cast(bf16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(a)));
   }
   return __builtin_shufflevector(part[0], part[1], 0, 1, 2, 3, 4, 5, 6, 7);
@@ -446,23 +490,22 @@ __device__ __forceinline__ PrecF32::frag kt_frag<PrecF32>(const PrecF32::frag* k
   return f;
 }
 
-template <class P, int D, int DV, bool PF>
-__device__ __forceinline__ void state_step(const ScanParams& p, StateShared& sh, typename P::frag* kl,
-                                           unsigned char* wsh, int64_t cl, int w, int lane, int n,
-                                           f32x4 (&S)[D / 64],
-                                           typename P::frag (&ak)[4][D / 128], typename StateOps<P, D, DV>::Small& sm,
-                                           typename P::frag (&ak_pf)[4][D / 128], typename StateOps<P, D, DV>::Small& sm_pf) {
+// The sequential loop is rotated so that one scheduling region (between the third barrier of chunk c
+// and the first barrier of chunk c+1) holds the state update of chunk c, the refill loads, the
+// checkpoint stores and the X_K product of chunk c+1.  Per CU each chunk moves ~100 KB through the
+// texture unit (64 KB of K, the checkpoint and the small operands) at ~64 B/clk, so these memory
+// instructions are interleaved one-for-one with the MFMAs of the region (sched_group_barrier) instead
+// of being issued in a burst that would block the in-order wave for ~1500 cycles.
+
+// Phase 1 of chunk cl (region ending at barrier A): checkpoint S^T, X_K partial from the K fragments
+// in `ak`, stage `ak` for the transposed read, publish the partial.
+template <class P, int D, int DV>
+__device__ __forceinline__ void state_phase1(StateShared& sh, typename P::frag* kl, unsigned char* cur, int w, int lane,
+                                             int n, const f32x4 (&S)[D / 64], const typename P::frag (&ak)[4][D / 128]) {
   using O = StateOps<P, D, DV>;
   using L = typename O::L;
   using frag = typename P::frag;
-  constexpr int TPW = O::TPW, JPW = O::JPW, NV = O::NV;
-  static_assert(JPW == 4, "the transposed K read assumes four 32-deep feature blocks per wave");
-  unsigned char* cur = wsh + cl * L::bytes;
-  if constexpr (!PF) {
-    O::load_k(cur, w, lane, ak);
-    O::load_small(cur, w, lane, n, sm);
-  }
-  // ---- checkpoint the chunk-start S^T as B fragments and form the X_K partial over this wave's features
+  constexpr int JPW = O::JPW, NV = O::NV;
   frag sf[JPW];
 #pragma unroll
   for (int jj = 0; jj < JPW; ++jj) {
@@ -476,55 +519,105 @@ __device__ __forceinline__ void state_step(const ScanParams& p, StateShared& sh,
 #pragma unroll
     for (int jj = 0; jj < JPW; ++jj) xp[m] = P::mma(xp[m], ak[m][jj], sf[jj]);
   }
-  // ---- stage this wave's K fragments for the transposed read-back (wave-private LDS)
-#pragma unroll
-  for (int m = 0; m < 4; ++m)
-#pragma unroll
-    for (int jj = 0; jj < JPW; ++jj) kl[(m * JPW + jj) * 64 + lane] = ak[m][jj];
-  // ---- prefetch chunk cl + 2 into the slot consumed one step ago
-  if constexpr (PF) {
-    if (cl + 2 < p.nseg) {
-      const unsigned char* nx = wsh + (cl + 2) * L::bytes;
-      O::load_k(nx, w, lane, ak_pf);
-      O::load_small(nx, w, lane, n, sm_pf);
-    }
-  }
+  stage_k<P>(kl, lane, ak);
 #pragma unroll
   for (int m = 0; m < 4; ++m) sh.xp[w][m][lane] = xp[m];
-  __syncthreads();
+}
+
+// Phase 2 of chunk cl (after barrier A, through barrier C): reduce X_K tile w, E tile w = U~ - Tp X_K
+// (checkpointed; shared scaled by kscale).
+template <class P, int D, int DV>
+__device__ __forceinline__ void state_phase2(StateShared& sh, unsigned char* cur, int w, int lane, int n,
+                                             const typename StateOps<P, D, DV>::Small& sm) {
+  using O = StateOps<P, D, DV>;
+  using L = typename O::L;
+  constexpr int NV = O::NV;
   sh.x[w][lane] = sh.xp[0][w][lane] + sh.xp[1][w][lane] + sh.xp[2][w][lane] + sh.xp[3][w][lane];
   __syncthreads();
-  // ---- E tile w:  E = U~ - Tp X_K
-  {
-    f32x4 ek = zero4();
+  f32x4 ek = zero4();
 #pragma unroll
-    for (int jb = 0; jb < 2; ++jb) ek = P::mma(ek, sm.tp[jb], P::from_f32(pair_to8(sh.x[2 * jb][lane], sh.x[2 * jb + 1][lane])));
-    const f32x4 e = sm.u - ek;
-    sh.e[w][lane] = e;
-    *reinterpret_cast<f32x4*>(cur + L::Eck + ((size_t)(w * NV + n) * 64 + lane) * 16) = e;
-  }
+  for (int jb = 0; jb < 2; ++jb) ek = P::mma(ek, sm.tp[jb], P::from_f32(pair_to8(sh.x[2 * jb][lane], sh.x[2 * jb + 1][lane])));
+  const f32x4 e = sm.u - ek;
+  sh.e[w][lane] = e * sm.ks;
+  *reinterpret_cast<f32x4*>(cur + L::Eck + ((size_t)(w * NV + n) * 64 + lane) * 16) = e;
   __syncthreads();
-  // ---- state update on this wave's feature tiles:  S^T = gammaC S^T + K^T (kscale o E)
+}
+
+// Phase 3 of chunk cl: S^T = gammaC S^T + K^T (kscale o E) on the wave's feature tiles.
+template <class P, int D, int DV, bool DECAY>
+__device__ __forceinline__ void state_phase3(StateShared& sh, const typename P::frag* kl, int lane, f32x4 (&S)[D / 64],
+                                             float gC) {
+  using frag = typename P::frag;
+  constexpr int TPW = D / 64;
   frag eb[2];
 #pragma unroll
-  for (int jb = 0; jb < 2; ++jb)
-    eb[jb] = P::from_f32(pair_to8(sh.e[2 * jb][lane] * sm.ks[2 * jb], sh.e[2 * jb + 1][lane] * sm.ks[2 * jb + 1]));
+  for (int jb = 0; jb < 2; ++jb) eb[jb] = P::from_f32(pair_to8(sh.e[2 * jb][lane], sh.e[2 * jb + 1][lane]));
 #pragma unroll
   for (int tl = 0; tl < TPW; ++tl) {
-    f32x4 acc = S[tl] * sm.gC;
+    f32x4 acc = S[tl];
+    if constexpr (DECAY) acc = acc * gC;  // without decay gammaC is exactly 1
 #pragma unroll
     for (int jb = 0; jb < 2; ++jb) acc = P::mma(acc, kt_frag<P>(kl, lane, tl, jb), eb[jb]);
     S[tl] = acc;
   }
 }
 
+// L2 prefetch of the operands of chunk cp: the 4 NV waves of a head touch one dword per 128-byte line
+// of its K / Tp / P / U~ / scale area.  The dword loaded one iteration earlier is folded into l2acc so
+// that the load is kept; it has long completed by then.
 template <class P, int D, int DV>
+__device__ __forceinline__ void l2_prefetch(const unsigned char* base, int w, int lane, int n, unsigned& slot, unsigned& acc) {
+  using O = StateOps<P, D, DV>;
+  using L = typename O::L;
+  acc += slot;
+  unsigned v = 0;
+#pragma unroll
+  for (int i = 0; i < O::L2_LOADS; ++i) {
+    const size_t off = ((size_t)((i * 4 * O::NV + n * 4 + w) * 64 + lane)) * 128;
+    if (off < L::Sfr) v += *reinterpret_cast<const unsigned*>(base + off);
+  }
+  slot = v;
+}
+
+// One iteration of the rotated loop for chunk cl, whose operands are in (ak_c, sm_c) and whose K is
+// staged in LDS; (ak_n, sm_n) hold chunk cl+1.  Phase 2 and 3 of chunk cl, then -- if cl+1 exists --
+// the refill of (ak_c, sm_c) with chunk min(cl+2, last) and phase 1 of chunk cl+1, then barrier A.
+template <class P, int D, int DV, bool DECAY>
+__device__ __forceinline__ bool state_iter(const ScanParams& p, StateShared& sh, typename P::frag* kl, unsigned char* wsh,
+                                           int64_t cl, int w, int lane, int n, f32x4 (&S)[D / 64],
+                                           typename P::frag (&ak_c)[4][D / 128], typename StateOps<P, D, DV>::Small& sm_c,
+                                           typename P::frag (&ak_n)[4][D / 128], typename StateOps<P, D, DV>::Small& sm_n,
+                                           unsigned& l2slot, unsigned& l2acc) {
+  using O = StateOps<P, D, DV>;
+  using L = typename O::L;
+  unsigned char* cur = wsh + cl * L::bytes;
+  state_phase2<P, D, DV>(sh, cur, w, lane, n, sm_c);
+  const float gC = sm_c.gC;
+  state_phase3<P, D, DV, DECAY>(sh, kl, lane, S, gC);
+  // Unconditional (no branch splits the region): after the last chunk, phase 1 runs on the clamped
+  // operands of the last chunk and writes its checkpoint into the spare record nseg of the head.
+  const int64_t cr = (cl + 2 < p.nseg) ? cl + 2 : p.nseg - 1;
+  O::load_all(wsh + cr * L::bytes, w, lane, n, ak_c, sm_c);
+  const int64_t cp = (cl + 1 + O::L2_AHEAD < p.nseg) ? cl + 1 + O::L2_AHEAD : p.nseg - 1;
+  l2_prefetch<P, D, DV>(wsh + cp * L::bytes, w, lane, n, l2slot, l2acc);
+  state_phase1<P, D, DV>(sh, kl, cur + L::bytes, w, lane, n, S, ak_n);
+  // 32 MFMAs (16 update, 16 X_K) and ~26 memory instructions: alternate them.
+#pragma unroll
+  for (int i = 0; i < 26; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+    __builtin_amdgcn_sched_group_barrier(0x010, 1, 0);  // one vector-memory instruction
+  }
+  __builtin_amdgcn_sched_group_barrier(0x008, 6, 0);
+  __syncthreads();
+  return cl + 1 < p.nseg;
+}
+
+template <class P, int D, int DV, bool DECAY>
 __global__ void __launch_bounds__(256) state_kernel(ScanParams p) {
   using O = StateOps<P, D, DV>;
   using L = typename O::L;
   using frag = typename P::frag;
   constexpr int TPW = O::TPW, JPW = O::JPW, NV = O::NV;
-  constexpr bool PF = IsBF16<P>::value;  // fp32 fragments are twice as wide; they are loaded per chunk
   __shared__ StateShared sh;
   __shared__ frag s_kl[4][4 * JPW * 64];  // wave-private K fragments
 
@@ -538,7 +631,9 @@ __global__ void __launch_bounds__(256) state_kernel(ScanParams p) {
   const int64_t b = hb / p.H, h = hb % p.H;
 
   const int lane = threadIdx.x & 63;
-  const int w = threadIdx.x >> 6;
+  // The wave index is uniform across the wave; reading it into a scalar register lets every
+  // fragment address be a scalar base plus the per-lane offset.
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r = 16 * n + (lane & 15);
   frag* kl = s_kl[w];
 
@@ -554,28 +649,28 @@ __global__ void __launch_bounds__(256) state_kernel(ScanParams p) {
     for (int tl = 0; tl < TPW; ++tl) S[tl] = zero4();
   }
 
-  unsigned char* wsh = p.ws + hb * p.nseg * L::bytes;
-  frag k0[4][JPW], k1[4][JPW], k2[4][JPW];
-  typename O::Small s0, s1, s2;
-  if constexpr (PF) {
-    O::load_k(wsh, w, lane, k0);
-    O::load_small(wsh, w, lane, n, s0);
-    if (p.nseg > 1) {
-      O::load_k(wsh + L::bytes, w, lane, k1);
-      O::load_small(wsh + L::bytes, w, lane, n, s1);
-    }
+  unsigned char* wsh = p.ws + hb * (p.nseg + 1) * L::bytes;
+  frag k0[4][JPW], k1[4][JPW];
+  typename O::Small s0, s1;
+  unsigned l2acc = 0, l2s0 = 0, l2s1 = 0;  // sink of the L2-prefetch loads (never stored; see below)
+  // Prologue: chunk 0 in slot 0, chunk min(1, last) in slot 1, phase 1 of chunk 0.
+  O::load_all(wsh, w, lane, n, k0, s0);
+  O::load_all(wsh + (p.nseg > 1 ? L::bytes : 0), w, lane, n, k1, s1);
+  state_phase1<P, D, DV>(sh, kl, wsh, w, lane, n, S, k0);
+  __syncthreads();
+  for (int64_t cl = 0;; cl += 2) {
+    if (!state_iter<P, D, DV, DECAY>(p, sh, kl, wsh, cl, w, lane, n, S, k0, s0, k1, s1, l2s0, l2acc)) break;
+    if (!state_iter<P, D, DV, DECAY>(p, sh, kl, wsh, cl + 1, w, lane, n, S, k1, s1, k0, s0, l2s1, l2acc)) break;
   }
-  for (int64_t cl = 0; cl < p.nseg; cl += 3) {
-    state_step<P, D, DV, PF>(p, sh, kl, wsh, cl, w, lane, n, S, k0, s0, k2, s2);
-    if (cl + 1 < p.nseg) state_step<P, D, DV, PF>(p, sh, kl, wsh, cl + 1, w, lane, n, S, k1, s1, k0, s0);
-    if (cl + 2 < p.nseg) state_step<P, D, DV, PF>(p, sh, kl, wsh, cl + 2, w, lane, n, S, k2, s2, k1, s1);
-  }
+  l2acc += l2s0 + l2s1;
 
   float* so = p.state_out + b * p.os0 + h * p.os1 + r * p.os3;
 #pragma unroll
   for (int tl = 0; tl < TPW; ++tl)
 #pragma unroll
     for (int i = 0; i < 4; ++i) so[(int64_t)(16 * (TPW * w + tl) + 4 * (lane >> 4) + i) * p.os2] = S[tl][i];
+  // Keeps the prefetch loads alive: nseg is at least 1, so this branch never runs.
+  if (p.nseg < 0) so[0] = (float)l2acc;
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -604,7 +699,7 @@ __global__ void __launch_bounds__(256) output_kernel(ScanParams p) {
   const int w = threadIdx.x >> 6;
   const int64_t cl = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
   const int64_t t0 = (p.chunk0 + cl) * CH;
-  const unsigned char* ws = p.ws + ((b * p.H + h) * p.nseg + cl) * L::bytes;
+  const unsigned char* ws = p.ws + ((b * p.H + h) * (p.nseg + 1) + cl) * L::bytes;
   const float* vec = reinterpret_cast<const float*>(ws + L::VEC);
 
   stage_omega<D, OMEGA_LDS>(p.omega, p.phase, s_omega, s_phrev);
@@ -699,7 +794,8 @@ static int run_scan(const kdn_scan_args* a, int64_t c_begin, int64_t c_end, int6
       if (hipGetLastError() != hipSuccess) return KDN_ERR_DEVICE;
     }
     if (phases & PHASE_STATE) {
-      hipLaunchKernelGGL((state_kernel<P, D, DV>), dim3(state_grid(p.B, p.H, DV / 16)), dim3(256), 0, st, p);
+      if (p.decay) hipLaunchKernelGGL((state_kernel<P, D, DV, true>), dim3(state_grid(p.B, p.H, DV / 16)), dim3(256), 0, st, p);
+      else hipLaunchKernelGGL((state_kernel<P, D, DV, false>), dim3(state_grid(p.B, p.H, DV / 16)), dim3(256), 0, st, p);
       if (hipGetLastError() != hipSuccess) return KDN_ERR_DEVICE;
     }
     if (phases & PHASE_OUTPUT) {
@@ -788,7 +884,7 @@ static int run_phase(const kdn_scan_args* a, int64_t chunk0, int64_t nchunks, in
   if (rc != KDN_OK) return rc;
   const int64_t total = (a->T + CH - 1) / CH;
   if (chunk0 < 0 || nchunks < 1 || chunk0 + nchunks > total) return KDN_ERR_INVALID_ARGUMENT;
-  const size_t need = chunk_bytes(a) * (size_t)a->B * (size_t)a->H * (size_t)nchunks;
+  const size_t need = chunk_bytes(a) * (size_t)a->B * (size_t)a->H * (size_t)(nchunks + 1);
   if (a->workspace_bytes < need) return KDN_ERR_WORKSPACE_TOO_SMALL;
   return dispatch(a, chunk0, chunk0 + nchunks, nchunks, phase, as_stream(stream));
 }
@@ -800,14 +896,14 @@ using namespace kdn;
 extern "C" size_t kdn_scan_workspace_bytes(const kdn_scan_args* a) {
   if (validate(a) != KDN_OK) return 0;
   const int64_t seg = choose_segment(a);
-  return chunk_bytes(a) * (size_t)a->B * (size_t)a->H * (size_t)seg;
+  return chunk_bytes(a) * (size_t)a->B * (size_t)a->H * (size_t)(seg + 1);
 }
 
 extern "C" int kdn_delta_scan_fwd(const kdn_scan_args* a, void* stream) {
   int rc = validate_launch(a);
   if (rc != KDN_OK) return rc;
   const int64_t seg = choose_segment(a);
-  const size_t need = chunk_bytes(a) * (size_t)a->B * (size_t)a->H * (size_t)seg;
+  const size_t need = chunk_bytes(a) * (size_t)a->B * (size_t)a->H * (size_t)(seg + 1);
   if (a->workspace_bytes < need) return KDN_ERR_WORKSPACE_TOO_SMALL;
   const int64_t nchunks = (a->T + CH - 1) / CH;
   return dispatch(a, 0, nchunks, seg, PHASE_ALL, as_stream(stream));

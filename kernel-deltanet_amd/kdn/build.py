@@ -1,20 +1,25 @@
 """Build libkdn.so (all HIP kernels + the C ABI) in-tree with hipcc for gfx950.
 
 Every HIP translation unit is compiled with packed fp32 arithmetic disabled (the compiler would
-otherwise form v_pk_* fp32 ops from ordinary float code).
+otherwise form v_pk_* fp32 ops from ordinary float code).  Translation units are compiled to objects
+in parallel, then linked into the shared library.
 """
 from __future__ import annotations
 
 import os
 import subprocess
 import sys
+from concurrent.futures import ThreadPoolExecutor
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 PKG_ROOT = os.path.dirname(_HERE)
 CSRC = os.path.join(PKG_ROOT, "csrc")
 SOURCES = ["kdn_api.hip", "kdn_lift.hip", "kdn_scan.hip"]
 OUT = os.path.join(_HERE, "libkdn.so")
+OBJDIR = os.path.join(_HERE, "_build")
 ARCH = "gfx950"
+HIP_FLAGS = [f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
+             "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 
 
 def hipcc() -> str:
@@ -24,19 +29,24 @@ def hipcc() -> str:
     return "hipcc"
 
 
-def build_native(verbose: bool = False) -> str:
-    """Compile every source into kdn/libkdn.so; returns the library path.  Always recompiles."""
-    srcs = [os.path.join(CSRC, s) for s in SOURCES]
-    tmp = OUT + ".tmp"
-    cmd = [hipcc(), f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-shared",
-           "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-           "-o", tmp] + srcs
+def _run(cmd, verbose):
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         sys.stderr.write(res.stdout + res.stderr)
-        raise RuntimeError(f"hipcc failed ({res.returncode}) building {OUT}")
+        raise RuntimeError(f"hipcc failed ({res.returncode}): {' '.join(cmd)}")
+
+
+def build_native(verbose: bool = False) -> str:
+    """Compile every source into kdn/libkdn.so; returns the library path.  Always recompiles."""
+    os.makedirs(OBJDIR, exist_ok=True)
+    objs = [os.path.join(OBJDIR, os.path.splitext(s)[0] + ".o") for s in SOURCES]
+    cmds = [[hipcc()] + HIP_FLAGS + ["-c", "-o", o, os.path.join(CSRC, s)] for s, o in zip(SOURCES, objs)]
+    with ThreadPoolExecutor(max_workers=len(cmds)) as ex:
+        list(ex.map(lambda c: _run(c, verbose), cmds))
+    tmp = OUT + ".tmp"
+    _run([hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp] + objs, verbose)
     os.replace(tmp, OUT)
     return OUT
 
