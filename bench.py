@@ -94,7 +94,9 @@ def main():
     ap.add_argument("--T", type=int, default=65536)
     ap.add_argument("--dv", type=int, default=64)
     ap.add_argument("--segment-chunks", type=int, default=0,
-                    help="64-token chunks per prep/state segment (0 = all chunks in one segment)")
+                    help="64-token chunks per segment (0 = 64 when pipelined, all chunks when --serial)")
+    ap.add_argument("--serial", action="store_true",
+                    help="run prep, state and output of each segment back to back on one stream")
     ap.add_argument("--cpu-tokens", type=int, default=65536, help="tokens in the CPU-baseline sample (0 = skip)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain device copy of known size (for PMC byte-counter calibration)")
@@ -129,7 +131,7 @@ def main():
     proj = FastWalshHadamardProjection(64, D, 42)
     qd, kd, vd, bd = q.to(dev), k.to(dev), v.to(dev), beta.to(dev)
     plan = ops.ScanPlan(qd, kd, vd, bd, None, proj.device_omega(dev), proj.device_phase(dev), proj.tau_star_inv,
-                        segment_chunks=args.segment_chunks)
+                        segment_chunks=args.segment_chunks, pipelined=not args.serial)
     nchunks, seg = plan.nchunks, plan.segment_chunks
     stream = torch.cuda.current_stream(dev)
 
@@ -144,34 +146,56 @@ def main():
     torch.cuda.synchronize()
     ms_per_step = e0.elapsed_time(e1) / args.steps
 
-    # Per-kernel durations: the same step issued as its launches (per segment: prep, then state) with
-    # events in between.
+    # Per-kernel durations: the same step issued phase by phase from here, in the order of the library's
+    # schedule, with HIP events around each launch on the stream it is launched on.
     segs = [(c0, min(seg, nchunks - c0)) for c0 in range(0, nchunks, seg)]
-    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(args.steps * len(segs))]
-    i = 0
+    timed = {"prep": [], "state": [], "output": []}
+
+    def launch(kind, s, st):
+        c0, nc = segs[s]
+        a0, a1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a0.record(st)
+        getattr(plan, kind)(c0, nc, args=plan.segment_args(s), stream=st)
+        a1.record(st)
+        timed[kind].append((a0, a1))
+
     for _ in range(args.steps):
-        for c0, nc in segs:
-            ev[i][0].record(stream)
-            plan.prep(c0, nc)
-            ev[i][1].record(stream)
-            plan.state(c0, nc)
-            ev[i][2].record(stream)
-            plan.output(c0, nc)
-            ev[i][3].record(stream)
-            i += 1
+        if plan.pipelined:
+            aux = ops.aux_stream(dev)
+            ev_in = torch.cuda.Event()
+            ev_in.record(stream)
+            aux.wait_event(ev_in)
+            ev_p = [torch.cuda.Event() for _ in segs]
+            ev_s = [torch.cuda.Event() for _ in segs]
+            launch("prep", 0, aux)
+            ev_p[0].record(aux)
+            for s_ in range(len(segs)):
+                stream.wait_event(ev_p[s_])
+                launch("state", s_, stream)
+                ev_s[s_].record(stream)
+                if s_ + 1 < len(segs):
+                    launch("prep", s_ + 1, aux)
+                    ev_p[s_ + 1].record(aux)
+                aux.wait_event(ev_s[s_])
+                launch("output", s_, aux)
+            ev_out = torch.cuda.Event()
+            ev_out.record(aux)
+            stream.wait_event(ev_out)
+        else:
+            for s_ in range(len(segs)):
+                for kind in ("prep", "state", "output"):
+                    launch(kind, s_, stream)
     torch.cuda.synchronize()
-    ms_prep = sum(e[0].elapsed_time(e[1]) for e in ev) / args.steps
-    ms_state = sum(e[1].elapsed_time(e[2]) for e in ev) / args.steps
-    ms_out = sum(e[2].elapsed_time(e[3]) for e in ev) / args.steps
+    ms_kernel = {k: sum(x.elapsed_time(y) for x, y in v) / args.steps for k, v in timed.items()}
+    launches = {k: len(v) / args.steps for k, v in timed.items()}
+    ms_prep, ms_state, ms_out = ms_kernel["prep"], ms_kernel["state"], ms_kernel["output"]
 
     fl = flops_per_chunk(D, dv)
     units = B * H * nchunks
     tokens = B * T
-    phases = {
-        "prep": {"ms": ms_prep, "alg_flops": fl["prep"] * units, "tflops": fl["prep"] * units / ms_prep / 1e9},
-        "state": {"ms": ms_state, "alg_flops": fl["state"] * units, "tflops": fl["state"] * units / ms_state / 1e9},
-        "output": {"ms": ms_out, "alg_flops": fl["output"] * units, "tflops": fl["output"] * units / ms_out / 1e9},
-    }
+    phases = {k: {"ms": ms_kernel[k], "launches": launches[k], "avg_launch_ms": ms_kernel[k] / launches[k],
+                  "alg_flops": fl[k] * units, "tflops": fl[k] * units / ms_kernel[k] / 1e9}
+              for k in ("prep", "state", "output")}
     dom = max(phases, key=lambda p: phases[p]["ms"])
     achieved = phases[dom]["tflops"]
     pmc = read_pmc(args.pmc)
@@ -198,7 +222,8 @@ def main():
         "config": {"workload": f"config3: one Kernel-DeltaNet layer prefill, B={B}, H={H}, T={T}, d_k=64->D={D}, "
                                f"d_v={dv}, chunk 64, bf16 q/k/v, fp32 beta and state, lambda=1",
                    "B": B, "H": H, "T": T, "D": D, "d_v": dv, "chunk": C, "segment_chunks": seg,
-                   "parallelism": "single GPU"},
+                   "schedule": "pipelined (state chain on the launch stream, prep/output on an auxiliary stream)"
+                   if plan.pipelined else "serial", "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "achieved": achieved, "peak": MFMA_BF16_PEAK / 1e12, "unit": "TFLOP/s",
                      "frac": achieved / (MFMA_BF16_PEAK / 1e12), "traffic": traffic, "kernel": dom},
         "phases": phases,

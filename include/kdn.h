@@ -132,6 +132,23 @@ int kdn_delta_scan_fwd(const kdn_scan_args* a, void* stream);
  *                     Replaces kernels/fused_kernel_deltanet.py:128-129,144-149.
  *   kdn_scan_output : y of each chunk from its slot (re-lifting q).  Replaces
  *                     kernels/fused_kernel_deltanet.py:118-141. */
+/* kdn_delta_scan_fwd scheduled over two streams.  The sequence is cut into segments of
+ * a->segment_chunks chunks (0 = 64).  The segments rotate through as many workspace buffers of
+ * kdn_scan_workspace_bytes() (for that segment size) as a->workspace_bytes holds, up to three.
+ *   - The sequential state kernel of segment s runs on `stream`.
+ *   - The prep of segment s+1 and the output of segment s-1 run on `aux_stream`, concurrently, on
+ *     the CUs the state kernel leaves free.
+ * aux_stream first waits for the work already queued on `stream`; `stream` finally waits for
+ * aux_stream.  To the caller this is one stream-ordered operation on `stream`, with the same results
+ * as kdn_delta_scan_fwd, bit for bit.  With fewer than two buffers, a single segment, or a NULL
+ * aux_stream (or aux_stream == stream) it runs serially on `stream`.  Both streams should have default
+ * priority.  Replaces kernels/fused_kernel_deltanet.py:31-155, like kdn_delta_scan_fwd. */
+int kdn_delta_scan_fwd_pipelined(const kdn_scan_args* a, void* stream, void* aux_stream);
+
+/* Workspace bytes for three segment buffers of kdn_delta_scan_fwd_pipelined (fewer when the sequence
+ * has fewer segments); 0 if the arguments are invalid. */
+size_t kdn_scan_workspace_bytes_pipelined(const kdn_scan_args* a);
+
 int kdn_scan_prep(const kdn_scan_args* a, int64_t chunk0, int64_t nchunks, void* stream);
 int kdn_scan_state(const kdn_scan_args* a, int64_t chunk0, int64_t nchunks, void* stream);
 int kdn_scan_output(const kdn_scan_args* a, int64_t chunk0, int64_t nchunks, void* stream);

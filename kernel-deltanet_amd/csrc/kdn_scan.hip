@@ -46,7 +46,8 @@ struct WsLayout {
   static constexpr size_t VEC = U + (size_t)4 * NV * 64 * 16;       // qscale[64] kscale[64] gammaC
   static constexpr size_t Sfr = VEC + 1024;                         // [j NJ][n NV][lane] chunk-start S^T frags
   static constexpr size_t Eck = Sfr + (size_t)NJ * NV * 64 * FB;    // [m 4][n NV][lane] f32x4  E
-  static constexpr size_t bytes = (Eck + (size_t)4 * NV * 64 * 16 + 255) / 256 * 256;
+  static constexpr size_t phiQ = Eck + (size_t)4 * NV * 64 * 16;    // [m 4][j NJ][lane] Q row frags (cos)
+  static constexpr size_t bytes = (phiQ + (size_t)4 * NJ * 64 * FB + 255) / 256 * 256;
 };
 
 struct ScanParams {
@@ -225,6 +226,7 @@ __global__ void __launch_bounds__(256) prep_kernel(ScanParams p) {
 #pragma unroll
   for (int j = 0; j < NJ; ++j) {
     store_frag<P>(ws + L::phiK + (size_t)(w * NJ + j) * 64 * L::FB, lane, cqk[1][j]);
+    store_frag<P>(ws + L::phiQ + (size_t)(w * NJ + j) * 64 * L::FB, lane, cqk[0][j]);
     s_phik[(w * NJ + j) * 64 + lane] = cqk[1][j];
   }
   __syncthreads();
@@ -674,77 +676,95 @@ __global__ void __launch_bounds__(256) state_kernel(ScanParams p) {
 }
 
 // ------------------------------------------------------------------------------------------------
-// output: grid (nseg, H, B), 256 threads.  Wave w re-lifts query rows [16w, 16w+16) of the chunk into
-// LDS; then wave w computes the value tiles n = w, w+4, ...:  Y[:, n] = diag(qscale) Q S_c^T[:, n] + P E[:, n].
+// output: grid (nseg, H, B), 256 threads.  Y = diag(qscale) Q S_c^T + P E for one (chunk, head).
+// Wave w keeps the lifted query fragments of token tile w (written by prep) in registers; the
+// chunk-start S^T fragments are staged in LDS, NG value tiles per pass, and read by all four waves.
+// Each wave assembles its 16 x d_v block of Y in a wave-private LDS tile and writes whole rows with
+// 16-byte stores.
 template <typename T>
-__device__ __forceinline__ void store_y(T* p, float v);
+__device__ __forceinline__ void store_row8(T* p, const float* v);
 template <>
-__device__ __forceinline__ void store_y<float>(float* p, float v) { *p = v; }
+__device__ __forceinline__ void store_row8<__bf16>(__bf16* p, const float* v) {
+  bf16x8 r;
+#pragma unroll
+  for (int s = 0; s < 8; ++s) r[s] = (__bf16)v[s];
+  *reinterpret_cast<bf16x8*>(p) = r;
+}
 template <>
-__device__ __forceinline__ void store_y<__bf16>(__bf16* p, float v) { *p = (__bf16)v; }
+__device__ __forceinline__ void store_row8<float>(float* p, const float* v) {
+  f32x4 a = {v[0], v[1], v[2], v[3]}, c = {v[4], v[5], v[6], v[7]};
+  reinterpret_cast<f32x4*>(p)[0] = a;
+  reinterpret_cast<f32x4*>(p)[1] = c;
+}
 
-template <class P, typename InT, typename OutT, int D, int DV>
+template <class P, typename OutT, int D, int DV>
 __global__ void __launch_bounds__(256) output_kernel(ScanParams p) {
   using L = WsLayout<P, D, DV>;
   using frag = typename P::frag;
-  constexpr int NT = D / 16, NJ = D / 32, NV = DV / 16;
-  constexpr bool OMEGA_LDS = IsBF16<P>::value;
-  constexpr size_t OMEGA_BYTES = OMEGA_LDS ? (size_t)NT * 2 * 64 * 16 : 0;
-  __shared__ __attribute__((aligned(16))) unsigned char smem[OMEGA_BYTES + (size_t)4 * NJ * 64 * sizeof(frag)];
-  __shared__ __attribute__((aligned(16))) float s_phrev[D];
-  bf16x8* s_omega = reinterpret_cast<bf16x8*>(smem);
-  frag* s_q = reinterpret_cast<frag*>(smem + OMEGA_BYTES);
+  constexpr int NJ = D / 32, NV = DV / 16;
+  constexpr int NG0 = IsBF16<P>::value ? 2 : 1;  // value tiles per LDS pass (32 KB of S fragments)
+  constexpr int NG = NV < NG0 ? NV : NG0;
+  constexpr int YS = DV + 4;                     // padded row of the Y tile
+  __shared__ frag s_s[NJ * NG * 64];
+  __shared__ __attribute__((aligned(16))) float s_y[4][16 * YS];
 
   const int lane = threadIdx.x & 63;
-  const int w = threadIdx.x >> 6;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int64_t cl = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
   const int64_t t0 = (p.chunk0 + cl) * CH;
   const unsigned char* ws = p.ws + ((b * p.H + h) * (p.nseg + 1) + cl) * L::bytes;
   const float* vec = reinterpret_cast<const float*>(ws + L::VEC);
 
-  stage_omega<D, OMEGA_LDS>(p.omega, p.phase, s_omega, s_phrev);
-  __syncthreads();
-  {
-    const int64_t trow = t0 + 16 * w + (lane & 15);
-    const InT* rows[1] = {(const InT*)p.q + b * p.qs0 + trow * p.qs1 + h * p.qs2};
-    frag cq[1][NJ];
-    float ss[1];
-    lift_tile<P, InT, D, OMEGA_LDS, 1>(rows, trow < p.T, p.normalize, s_omega, p.omega, s_phrev,
-                                       p.inv_tau * 0.15915494309189535f, lane, cq, ss);
+  frag aq[NJ];
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) s_q[(w * NJ + j) * 64 + lane] = cq[0][j];
-  }
-  __syncthreads();
+  for (int j = 0; j < NJ; ++j) aq[j] = load_frag<P>(ws + L::phiQ + (size_t)(w * NJ + j) * 64 * L::FB, lane);
+  frag pf[2];
+#pragma unroll
+  for (int jb = 0; jb < 2; ++jb) pf[jb] = load_frag<P>(ws + L::Pm + (size_t)(w * 2 + jb) * 64 * L::FB, lane);
+  const f32x4 qs = *reinterpret_cast<const f32x4*>(vec + 16 * w + 4 * (lane >> 4));
+  float* yt = s_y[w];
 
-  for (int n = w; n < NV; n += 4) {
-    f32x4 xq[4];
-#pragma unroll
-    for (int m = 0; m < 4; ++m) xq[m] = zero4();
-#pragma unroll 4
-    for (int j = 0; j < NJ; ++j) {
-      const frag sfr = load_frag<P>(ws + L::Sfr + (size_t)(j * NV + n) * 64 * L::FB, lane);
-#pragma unroll
-      for (int m = 0; m < 4; ++m) xq[m] = P::mma(xq[m], s_q[(m * NJ + j) * 64 + lane], sfr);
+  for (int n0 = 0; n0 < NV; n0 += NG) {
+    if (n0 > 0) __syncthreads();  // the previous pass's fragments have been read
+    for (int idx = threadIdx.x; idx < NJ * NG * 64; idx += 256) {
+      const int l = idx & 63, g = (idx >> 6) % NG, j = idx / (64 * NG);
+      s_s[idx] = load_frag<P>(ws + L::Sfr + (size_t)(j * NV + n0 + g) * 64 * L::FB, l);
     }
-    frag eb[2];
+    __syncthreads();
 #pragma unroll
-    for (int jb = 0; jb < 2; ++jb) {
-      const f32x4 e0 = *reinterpret_cast<const f32x4*>(ws + L::Eck + ((size_t)((2 * jb) * NV + n) * 64 + lane) * 16);
-      const f32x4 e1 = *reinterpret_cast<const f32x4*>(ws + L::Eck + ((size_t)((2 * jb + 1) * NV + n) * 64 + lane) * 16);
-      eb[jb] = P::from_f32(pair_to8(e0, e1));
-    }
-    const int r = 16 * n + (lane & 15);
+    for (int g = 0; g < NG; ++g) {
+      const int n = n0 + g;
+      f32x4 xq = zero4();
 #pragma unroll
-    for (int m = 0; m < 4; ++m) {
+      for (int j = 0; j < NJ; ++j) xq = P::mma(xq, aq[j], s_s[(j * NG + g) * 64 + lane]);
+      frag eb[2];
+#pragma unroll
+      for (int jb = 0; jb < 2; ++jb) {
+        const f32x4 e0 = *reinterpret_cast<const f32x4*>(ws + L::Eck + ((size_t)((2 * jb) * NV + n) * 64 + lane) * 16);
+        const f32x4 e1 = *reinterpret_cast<const f32x4*>(ws + L::Eck + ((size_t)((2 * jb + 1) * NV + n) * 64 + lane) * 16);
+        eb[jb] = P::from_f32(pair_to8(e0, e1));
+      }
       f32x4 y = zero4();
 #pragma unroll
-      for (int jb = 0; jb < 2; ++jb) y = P::mma(y, load_frag<P>(ws + L::Pm + (size_t)(m * 2 + jb) * 64 * L::FB, lane), eb[jb]);
-      const f32x4 qs = *reinterpret_cast<const f32x4*>(vec + 16 * m + 4 * (lane >> 4));
-      const int64_t tb = t0 + 16 * m + 4 * (lane >> 4);
+      for (int jb = 0; jb < 2; ++jb) y = P::mma(y, pf[jb], eb[jb]);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int64_t t = tb + i;
-        if (t < p.T) store_y<OutT>((OutT*)p.y + b * p.ys0 + t * p.ys1 + h * p.ys2 + r, y[i] + qs[i] * xq[m][i]);
+      for (int i = 0; i < 4; ++i) yt[(4 * (lane >> 4) + i) * YS + 16 * n + (lane & 15)] = y[i] + qs[i] * xq[i];
+    }
+  }
+  // Rows of the wave's tile: (16 rows) x (DV / 8 pieces of 8 elements); the tile was written by this
+  // wave only, and a wave's LDS accesses are performed in order.
+  constexpr int PIECES = 16 * (DV / 8);
+#pragma unroll
+  for (int base = 0; base < PIECES; base += 64) {
+    const int idx = base + lane;
+    if (idx < PIECES) {
+      const int row = idx / (DV / 8), pc = idx % (DV / 8);
+      const int64_t t = t0 + 16 * w + row;
+      if (t < p.T) {
+        const f32x4 v0 = *reinterpret_cast<const f32x4*>(yt + row * YS + 8 * pc);
+        const f32x4 v1 = *reinterpret_cast<const f32x4*>(yt + row * YS + 8 * pc + 4);
+        const float v[8] = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+        store_row8<OutT>((OutT*)p.y + b * p.ys0 + t * p.ys1 + h * p.ys2 + 8 * pc, v);
       }
     }
   }
@@ -772,58 +792,154 @@ static ScanParams fill_params(const kdn_scan_args* a) {
   return p;
 }
 
-// Runs chunks [c_begin, c_end) in segments of `seg` chunks: per segment the selected kernels, in the
-// order prep, state, output.  The state kernel of the segment starting at chunk 0 reads initial_state
-// (zeros if NULL); later segments continue from final_state.
+// Parameters of one segment: chunks [c0, c0 + nseg) with its records at `ws`.  The state kernel of the
+// segment starting at chunk 0 reads initial_state (zeros if NULL); later segments continue from
+// final_state.
+static ScanParams segment_params(const kdn_scan_args* a, int64_t c0, int64_t nseg, void* ws) {
+  ScanParams p = fill_params(a);
+  p.chunk0 = c0;
+  p.nseg = nseg;
+  p.ws = (unsigned char*)ws;
+  if (c0 == 0) {
+    p.state_in = a->initial_state;
+    p.is0 = a->init_stride[0]; p.is1 = a->init_stride[1]; p.is2 = a->init_stride[2]; p.is3 = a->init_stride[3];
+  } else {
+    p.state_in = a->final_state;
+    p.is0 = p.os0; p.is1 = p.os1; p.is2 = p.os2; p.is3 = p.os3;
+  }
+  return p;
+}
+
+template <class P, typename InT, typename OutT, int D, int DV>
+static int launch_phase(const ScanParams& p, int phase, hipStream_t st) {
+  const dim3 chunk_grid((unsigned)p.nseg, (unsigned)p.H, (unsigned)p.B);
+  if (phase == PHASE_PREP) {
+    hipLaunchKernelGGL((prep_kernel<P, InT, D, DV>), chunk_grid, dim3(256), 0, st, p);
+  } else if (phase == PHASE_STATE) {
+    if (p.decay) hipLaunchKernelGGL((state_kernel<P, D, DV, true>), dim3(state_grid(p.B, p.H, DV / 16)), dim3(256), 0, st, p);
+    else hipLaunchKernelGGL((state_kernel<P, D, DV, false>), dim3(state_grid(p.B, p.H, DV / 16)), dim3(256), 0, st, p);
+  } else {
+    hipLaunchKernelGGL((output_kernel<P, OutT, D, DV>), chunk_grid, dim3(256), 0, st, p);
+  }
+  return hipGetLastError() == hipSuccess ? KDN_OK : KDN_ERR_DEVICE;
+}
+
+// Runs chunks [c_begin, c_end) in segments of `seg` chunks, all in one workspace buffer: per segment the
+// selected kernels, in the order prep, state, output.
 template <class P, typename InT, typename OutT, int D, int DV>
 static int run_scan(const kdn_scan_args* a, int64_t c_begin, int64_t c_end, int64_t seg, int phases, hipStream_t st) {
-  ScanParams p = fill_params(a);
   for (int64_t c0 = c_begin; c0 < c_end; c0 += seg) {
-    p.chunk0 = c0;
-    p.nseg = (c_end - c0 < seg) ? (c_end - c0) : seg;
-    if (c0 == 0) {
-      p.state_in = a->initial_state;
-      p.is0 = a->init_stride[0]; p.is1 = a->init_stride[1]; p.is2 = a->init_stride[2]; p.is3 = a->init_stride[3];
-    } else {
-      p.state_in = a->final_state;
-      p.is0 = p.os0; p.is1 = p.os1; p.is2 = p.os2; p.is3 = p.os3;
-    }
-    const dim3 chunk_grid((unsigned)p.nseg, (unsigned)p.H, (unsigned)p.B);
-    if (phases & PHASE_PREP) {
-      hipLaunchKernelGGL((prep_kernel<P, InT, D, DV>), chunk_grid, dim3(256), 0, st, p);
-      if (hipGetLastError() != hipSuccess) return KDN_ERR_DEVICE;
-    }
-    if (phases & PHASE_STATE) {
-      if (p.decay) hipLaunchKernelGGL((state_kernel<P, D, DV, true>), dim3(state_grid(p.B, p.H, DV / 16)), dim3(256), 0, st, p);
-      else hipLaunchKernelGGL((state_kernel<P, D, DV, false>), dim3(state_grid(p.B, p.H, DV / 16)), dim3(256), 0, st, p);
-      if (hipGetLastError() != hipSuccess) return KDN_ERR_DEVICE;
-    }
-    if (phases & PHASE_OUTPUT) {
-      hipLaunchKernelGGL((output_kernel<P, InT, OutT, D, DV>), chunk_grid, dim3(256), 0, st, p);
-      if (hipGetLastError() != hipSuccess) return KDN_ERR_DEVICE;
+    const ScanParams p = segment_params(a, c0, (c_end - c0 < seg) ? (c_end - c0) : seg, a->workspace);
+    for (int ph : {PHASE_PREP, PHASE_STATE, PHASE_OUTPUT}) {
+      if (!(phases & ph)) continue;
+      const int rc = launch_phase<P, InT, OutT, D, DV>(p, ph, st);
+      if (rc != KDN_OK) return rc;
     }
   }
   return KDN_OK;
 }
 
+// Events of the pipelined scan, released when the call returns (destroying an event whose record is
+// still pending is allowed; its resources are freed once it completes).
+struct EventSet {
+  hipEvent_t ev[16];
+  int n = 0;
+  int create(int count) {
+    for (; n < count; ++n)
+      if (hipEventCreateWithFlags(&ev[n], hipEventDisableTiming) != hipSuccess) return KDN_ERR_DEVICE;
+    return KDN_OK;
+  }
+  ~EventSet() {
+    for (int i = 0; i < n; ++i) hipEventDestroy(ev[i]);
+  }
+};
+
+// Segments rotate through `nbuf` workspace buffers.  The state chain runs on `st` (the caller's stream);
+// prep and output run on `aux`, in the order prep(s+1), output(s), so that while state(s) occupies its
+// B*H*d_v/16 workgroups the other CUs prepare the next segment and finish the previous one.
+//   state(s)  waits for prep(s)        (event P[s % nbuf])
+//   output(s) waits for state(s)       (event S[s % nbuf])
+//   prep(s)   reuses the buffer of segment s - nbuf, whose output ran earlier on aux
+// aux first waits for the work already queued on st, and st finally waits for the last output.
+template <class P, typename InT, typename OutT, int D, int DV>
+static int run_pipelined(const kdn_scan_args* a, int64_t seg, int nbuf, size_t buf_bytes, hipStream_t st, hipStream_t aux) {
+  const int64_t nchunks = (a->T + CH - 1) / CH;
+  const int64_t nsegs = (nchunks + seg - 1) / seg;
+  EventSet evs;
+  int rc = evs.create(2 * nbuf + 2);
+  if (rc != KDN_OK) return rc;
+  hipEvent_t* evP = evs.ev;
+  hipEvent_t* evS = evs.ev + nbuf;
+  hipEvent_t evIn = evs.ev[2 * nbuf], evOut = evs.ev[2 * nbuf + 1];
+  auto seg_p = [&](int64_t s) {
+    const int64_t c0 = s * seg;
+    return segment_params(a, c0, (nchunks - c0 < seg) ? (nchunks - c0) : seg,
+                          (unsigned char*)a->workspace + (size_t)(s % nbuf) * buf_bytes);
+  };
+#define KDN_TRY(x) do { if ((x) != hipSuccess) return KDN_ERR_DEVICE; } while (0)
+#define KDN_TRYK(x) do { const int _rc = (x); if (_rc != KDN_OK) return _rc; } while (0)
+  KDN_TRY(hipEventRecord(evIn, st));
+  KDN_TRY(hipStreamWaitEvent(aux, evIn, 0));
+  KDN_TRYK((launch_phase<P, InT, OutT, D, DV>(seg_p(0), PHASE_PREP, aux)));
+  KDN_TRY(hipEventRecord(evP[0], aux));
+  for (int64_t s = 0; s < nsegs; ++s) {
+    const ScanParams ps = seg_p(s);
+    KDN_TRY(hipStreamWaitEvent(st, evP[s % nbuf], 0));
+    KDN_TRYK((launch_phase<P, InT, OutT, D, DV>(ps, PHASE_STATE, st)));
+    KDN_TRY(hipEventRecord(evS[s % nbuf], st));
+    if (s + 1 < nsegs) {
+      KDN_TRYK((launch_phase<P, InT, OutT, D, DV>(seg_p(s + 1), PHASE_PREP, aux)));
+      KDN_TRY(hipEventRecord(evP[(s + 1) % nbuf], aux));
+    }
+    KDN_TRY(hipStreamWaitEvent(aux, evS[s % nbuf], 0));
+    KDN_TRYK((launch_phase<P, InT, OutT, D, DV>(ps, PHASE_OUTPUT, aux)));
+  }
+  KDN_TRY(hipEventRecord(evOut, aux));
+  KDN_TRY(hipStreamWaitEvent(st, evOut, 0));
+#undef KDN_TRY
+#undef KDN_TRYK
+  return KDN_OK;
+}
+
+// How the launches of one call are scheduled.
+struct RunSpec {
+  int64_t c_begin, c_end, seg;
+  int phases;
+  hipStream_t st;
+  hipStream_t aux;   // non-null: pipelined over `nbuf` buffers of `buf_bytes`
+  int nbuf;
+  size_t buf_bytes;
+};
+
+template <class P, typename InT, typename OutT, int D, int DV>
+static int run(const kdn_scan_args* a, const RunSpec& r) {
+  if (r.aux) return run_pipelined<P, InT, OutT, D, DV>(a, r.seg, r.nbuf, r.buf_bytes, r.st, r.aux);
+  return run_scan<P, InT, OutT, D, DV>(a, r.c_begin, r.c_end, r.seg, r.phases, r.st);
+}
+
 template <class P, typename InT, typename OutT, int D>
-static int dispatch_dv(const kdn_scan_args* a, int64_t c_begin, int64_t c_end, int64_t seg, int phases, hipStream_t st) {
+static int dispatch_dv(const kdn_scan_args* a, const RunSpec& r) {
   switch (a->d_v) {
-    case 16: return run_scan<P, InT, OutT, D, 16>(a, c_begin, c_end, seg, phases, st);
-    case 32: return run_scan<P, InT, OutT, D, 32>(a, c_begin, c_end, seg, phases, st);
-    case 64: return run_scan<P, InT, OutT, D, 64>(a, c_begin, c_end, seg, phases, st);
-    case 128: return run_scan<P, InT, OutT, D, 128>(a, c_begin, c_end, seg, phases, st);
+    case 16: return run<P, InT, OutT, D, 16>(a, r);
+    case 32: return run<P, InT, OutT, D, 32>(a, r);
+    case 64: return run<P, InT, OutT, D, 64>(a, r);
+    case 128: return run<P, InT, OutT, D, 128>(a, r);
     default: return KDN_ERR_UNSUPPORTED;
   }
 }
 
-static int dispatch(const kdn_scan_args* a, int64_t c_begin, int64_t c_end, int64_t seg, int phases, hipStream_t st) {
+static int dispatch(const kdn_scan_args* a, const RunSpec& r) {
   if (a->in_dtype == KDN_DTYPE_BF16) {
-    if (a->out_dtype == KDN_DTYPE_BF16) return dispatch_dv<PrecBF16, __bf16, __bf16, 512>(a, c_begin, c_end, seg, phases, st);
-    return dispatch_dv<PrecBF16, __bf16, float, 512>(a, c_begin, c_end, seg, phases, st);
+    if (a->out_dtype == KDN_DTYPE_BF16) return dispatch_dv<PrecBF16, __bf16, __bf16, 512>(a, r);
+    return dispatch_dv<PrecBF16, __bf16, float, 512>(a, r);
   }
-  if (a->out_dtype == KDN_DTYPE_BF16) return dispatch_dv<PrecF32, float, __bf16, 512>(a, c_begin, c_end, seg, phases, st);
-  return dispatch_dv<PrecF32, float, float, 512>(a, c_begin, c_end, seg, phases, st);
+  if (a->out_dtype == KDN_DTYPE_BF16) return dispatch_dv<PrecF32, float, __bf16, 512>(a, r);
+  return dispatch_dv<PrecF32, float, float, 512>(a, r);
+}
+
+static int dispatch(const kdn_scan_args* a, int64_t c_begin, int64_t c_end, int64_t seg, int phases, hipStream_t st) {
+  const RunSpec r = {c_begin, c_end, seg, phases, st, nullptr, 0, 0};
+  return dispatch(a, r);
 }
 
 static size_t chunk_bytes(const kdn_scan_args* a) {
@@ -871,9 +987,11 @@ static int validate_launch(const kdn_scan_args* a) {
   if (!aligned(a->q, 16) || !aligned(a->k, 16) || !aligned(a->v, 16) || !aligned(a->omega_bf16, 16) ||
       !aligned(a->phase, 16) || !aligned(a->workspace, 256))
     return KDN_ERR_MISALIGNED;
+  const size_t osz = dtype_size(a->out_dtype);
+  if (!aligned(a->y, 16)) return KDN_ERR_MISALIGNED;
   for (int i = 0; i < 3; ++i) {
     if (((a->q_stride[i] * (int64_t)isz) % 16) != 0 || ((a->k_stride[i] * (int64_t)isz) % 16) != 0 ||
-        ((a->v_stride[i] * (int64_t)isz) % 16) != 0)
+        ((a->v_stride[i] * (int64_t)isz) % 16) != 0 || ((a->y_stride[i] * (int64_t)osz) % 16) != 0)
       return KDN_ERR_MISALIGNED;
   }
   return KDN_OK;
@@ -907,6 +1025,37 @@ extern "C" int kdn_delta_scan_fwd(const kdn_scan_args* a, void* stream) {
   if (a->workspace_bytes < need) return KDN_ERR_WORKSPACE_TOO_SMALL;
   const int64_t nchunks = (a->T + CH - 1) / CH;
   return dispatch(a, 0, nchunks, seg, PHASE_ALL, as_stream(stream));
+}
+
+// Default segment of the pipelined scan: 64 chunks (4096 tokens), fewer for short sequences.
+static int64_t pipeline_segment(const kdn_scan_args* a) {
+  const int64_t nchunks = (a->T + CH - 1) / CH;
+  const int64_t seg = a->segment_chunks > 0 ? a->segment_chunks : 64;
+  return seg < nchunks ? seg : nchunks;
+}
+
+extern "C" size_t kdn_scan_workspace_bytes_pipelined(const kdn_scan_args* a) {
+  if (validate(a) != KDN_OK) return 0;
+  const int64_t seg = pipeline_segment(a);
+  const int64_t nsegs = ((a->T + CH - 1) / CH + seg - 1) / seg;
+  const int64_t nbuf = nsegs < 3 ? nsegs : 3;
+  return chunk_bytes(a) * (size_t)a->B * (size_t)a->H * (size_t)(seg + 1) * (size_t)nbuf;
+}
+
+extern "C" int kdn_delta_scan_fwd_pipelined(const kdn_scan_args* a, void* stream, void* aux_stream) {
+  int rc = validate_launch(a);
+  if (rc != KDN_OK) return rc;
+  const int64_t seg = pipeline_segment(a);
+  const size_t buf = chunk_bytes(a) * (size_t)a->B * (size_t)a->H * (size_t)(seg + 1);
+  if (a->workspace_bytes < buf) return KDN_ERR_WORKSPACE_TOO_SMALL;
+  const int64_t nchunks = (a->T + CH - 1) / CH;
+  const int64_t nsegs = (nchunks + seg - 1) / seg;
+  size_t fit = a->workspace_bytes / buf;
+  const int nbuf = (int)(fit < 3 ? fit : 3);
+  if (!aux_stream || aux_stream == stream || nbuf < 2 || nsegs < 2)
+    return dispatch(a, 0, nchunks, seg, PHASE_ALL, as_stream(stream));
+  const RunSpec r = {0, nchunks, seg, PHASE_ALL, as_stream(stream), as_stream(aux_stream), nbuf, buf};
+  return dispatch(a, r);
 }
 
 extern "C" int kdn_scan_prep(const kdn_scan_args* a, int64_t chunk0, int64_t nchunks, void* stream) {

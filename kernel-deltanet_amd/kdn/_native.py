@@ -28,6 +28,8 @@ EXPORTED = (
     "kdn_scan_prep",
     "kdn_scan_state",
     "kdn_scan_output",
+    "kdn_scan_workspace_bytes_pipelined",
+    "kdn_delta_scan_fwd_pipelined",
 )
 
 _i64 = ctypes.c_int64
@@ -93,6 +95,10 @@ def lib() -> ctypes.CDLL:
             L.kdn_scan_workspace_bytes.restype = sz
             L.kdn_delta_scan_fwd.argtypes = [ctypes.POINTER(ScanArgs), vp]
             L.kdn_delta_scan_fwd.restype = ci
+            L.kdn_scan_workspace_bytes_pipelined.argtypes = [ctypes.POINTER(ScanArgs)]
+            L.kdn_scan_workspace_bytes_pipelined.restype = sz
+            L.kdn_delta_scan_fwd_pipelined.argtypes = [ctypes.POINTER(ScanArgs), vp, vp]
+            L.kdn_delta_scan_fwd_pipelined.restype = ci
             for nm in ("kdn_scan_prep", "kdn_scan_state", "kdn_scan_output"):
                 fn = getattr(L, nm)
                 fn.argtypes = [ctypes.POINTER(ScanArgs), i64, i64, vp]

@@ -131,7 +131,7 @@ def scan_args(q, k, v, beta, decay, omega_bf16, phase, inv_tau, normalize, initi
     return a
 
 
-def scan_workspace_bytes(q, v, omega_bf16, segment_chunks: int = 0) -> int:
+def scan_workspace_bytes(q, v, omega_bf16, segment_chunks: int = 0, pipelined: bool = False) -> int:
     B, T, H, d_k = q.shape
     a = N.ScanArgs()
     a.B, a.T, a.H, a.d_k, a.D, a.d_v = B, T, H, d_k, omega_bf16.shape[0], v.shape[-1]
@@ -139,15 +139,47 @@ def scan_workspace_bytes(q, v, omega_bf16, segment_chunks: int = 0) -> int:
     a.out_dtype = a.in_dtype
     a.inv_tau = 1.0
     a.segment_chunks = int(segment_chunks)
-    return int(N.lib().kdn_scan_workspace_bytes(ctypes.byref(a)))
+    fn = N.lib().kdn_scan_workspace_bytes_pipelined if pipelined else N.lib().kdn_scan_workspace_bytes
+    return int(fn(ctypes.byref(a)))
+
+
+_AUX_STREAMS = {}
+
+
+def aux_stream(dev: torch.device) -> torch.cuda.Stream:
+    """The per-device auxiliary stream of the pipelined scan (default priority), created once."""
+    idx = dev.index if dev.index is not None else torch.cuda.current_device()
+    st = _AUX_STREAMS.get(idx)
+    if st is None:
+        st = torch.cuda.Stream(device=idx)
+        _AUX_STREAMS[idx] = st
+    return st
+
+
+def _launch_scan(a, dev: torch.device, pipelined: bool, keep=()):
+    """kdn_delta_scan_fwd, or the pipelined variant with prep/output on the auxiliary stream.  Tensors
+    the auxiliary stream reads or writes are marked with record_stream so the caching allocator does not
+    hand their memory out again before that work has finished."""
+    st = torch.cuda.current_stream(dev)
+    if pipelined:
+        aux = aux_stream(dev)
+        for t in keep:
+            if t is not None:
+                t.record_stream(aux)
+        N.check(N.lib().kdn_delta_scan_fwd_pipelined(ctypes.byref(a), ctypes.c_void_p(st.cuda_stream),
+                                                     ctypes.c_void_p(aux.cuda_stream)), "kdn_delta_scan_fwd_pipelined")
+    else:
+        N.check(N.lib().kdn_delta_scan_fwd(ctypes.byref(a), ctypes.c_void_p(st.cuda_stream)), "kdn_delta_scan_fwd")
 
 
 def scan(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, beta: torch.Tensor, decay: Optional[torch.Tensor],
          omega_bf16: torch.Tensor, phase: torch.Tensor, inv_tau: float, normalize: bool = False,
          initial_state: Optional[torch.Tensor] = None, final_state: Optional[torch.Tensor] = None,
          y: Optional[torch.Tensor] = None, out_dtype: Optional[torch.dtype] = None,
-         workspace: Optional[torch.Tensor] = None, segment_chunks: int = 0) -> Tuple[torch.Tensor, torch.Tensor]:
-    """Chunked delta-rule prefill over (B, T, H, d) views (kdn_delta_scan_fwd).
+         workspace: Optional[torch.Tensor] = None, segment_chunks: int = 0,
+         pipelined: bool = True) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Chunked delta-rule prefill over (B, T, H, d) views (kdn_delta_scan_fwd_pipelined, or
+    kdn_delta_scan_fwd with pipelined=False).
 
     q, k (B, T, H, d_k) and v (B, T, H, d_v) share a dtype; beta, decay (B, T, H) are float32 (decay may
     be None for lambda = 1); initial_state/final_state are (B, H, D, d_v) float32 views with any strides.
@@ -180,14 +212,14 @@ def scan(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, beta: torch.Tensor, 
     om = omega_bf16.to(dev).contiguous()
     ph = phase.to(device=dev, dtype=torch.float32).contiguous()
     if workspace is None:
-        nbytes = scan_workspace_bytes(q, v, om, segment_chunks)
+        nbytes = scan_workspace_bytes(q, v, om, segment_chunks, pipelined)
         if nbytes == 0:
             raise ValueError("scan: unsupported shape (kdn_scan_workspace_bytes returned 0)")
         workspace = torch.empty(nbytes, dtype=torch.uint8, device=dev)
     a = scan_args(q, k, v, beta, decay, om, ph, inv_tau, normalize, initial_state, final_state, y,
                   workspace, segment_chunks)
     with torch.cuda.device(dev):
-        N.check(N.lib().kdn_delta_scan_fwd(ctypes.byref(a), ctypes.c_void_p(_stream(dev))), "kdn_delta_scan_fwd")
+        _launch_scan(a, dev, pipelined, (q, k, v, beta, decay, om, ph, initial_state, final_state, y, workspace))
     return y, final_state
 
 
@@ -200,12 +232,16 @@ class ScanPlan:
     """
 
     def __init__(self, q, k, v, beta, decay, omega_bf16, phase, inv_tau, normalize=False, initial_state=None,
-                 out_dtype=None, segment_chunks: int = 0):
+                 out_dtype=None, segment_chunks: int = 0, pipelined: bool = False):
         dev = q.device
         B, T, H, _ = q.shape
         D, d_v = omega_bf16.shape[0], v.shape[-1]
         self.nchunks = (T + 63) // 64
-        self.segment_chunks = self.nchunks if segment_chunks <= 0 else min(segment_chunks, self.nchunks)
+        self.pipelined = pipelined
+        if pipelined:
+            self.segment_chunks = min(segment_chunks if segment_chunks > 0 else 64, self.nchunks)
+        else:
+            self.segment_chunks = self.nchunks if segment_chunks <= 0 else min(segment_chunks, self.nchunks)
         self.q, self.k, self.v = _last_contig(q), _last_contig(k), _last_contig(v)
         self.beta = beta.to(torch.float32)
         self.decay = None if decay is None else decay.to(torch.float32)
@@ -214,9 +250,10 @@ class ScanPlan:
         self.initial_state = initial_state
         self.final_state = torch.empty(B, H, D, d_v, device=dev, dtype=torch.float32)
         self.y = torch.empty(B, T, H, d_v, device=dev, dtype=q.dtype if out_dtype is None else out_dtype)
-        nbytes = scan_workspace_bytes(self.q, self.v, self.omega, self.segment_chunks)
+        nbytes = scan_workspace_bytes(self.q, self.v, self.omega, self.segment_chunks, pipelined)
         if nbytes == 0:
             raise ValueError("ScanPlan: unsupported shape")
+        self.seg_bytes = scan_workspace_bytes(self.q, self.v, self.omega, self.segment_chunks, False)
         self.workspace = torch.empty(nbytes, dtype=torch.uint8, device=dev)
         self.args = scan_args(self.q, self.k, self.v, self.beta, self.decay, self.omega, self.phase, inv_tau,
                               normalize, initial_state, self.final_state, self.y, self.workspace, self.segment_chunks)
@@ -226,14 +263,28 @@ class ScanPlan:
         return ctypes.c_void_p(_stream(self.device))
 
     def run(self):
-        N.check(N.lib().kdn_delta_scan_fwd(ctypes.byref(self.args), self._stream()), "kdn_delta_scan_fwd")
+        _launch_scan(self.args, self.device, self.pipelined)
         return self.y, self.final_state
 
-    def prep(self, chunk0: int, nchunks: int):
-        N.check(N.lib().kdn_scan_prep(ctypes.byref(self.args), chunk0, nchunks, self._stream()), "kdn_scan_prep")
+    def segment_args(self, s: int) -> N.ScanArgs:
+        """Arguments whose workspace is buffer (s mod nbuf) of the pipelined layout (for phase-by-phase
+        scheduling of segment s)."""
+        a = N.ScanArgs.from_buffer_copy(self.args)
+        nbuf = max(1, self.workspace.numel() // self.seg_bytes)
+        a.workspace = self.workspace.data_ptr() + (s % nbuf) * self.seg_bytes
+        a.workspace_bytes = self.seg_bytes
+        return a
 
-    def state(self, chunk0: int, nchunks: int):
-        N.check(N.lib().kdn_scan_state(ctypes.byref(self.args), chunk0, nchunks, self._stream()), "kdn_scan_state")
+    def prep(self, chunk0: int, nchunks: int, args: Optional[N.ScanArgs] = None, stream=None):
+        self._phase("kdn_scan_prep", chunk0, nchunks, args, stream)
 
-    def output(self, chunk0: int, nchunks: int):
-        N.check(N.lib().kdn_scan_output(ctypes.byref(self.args), chunk0, nchunks, self._stream()), "kdn_scan_output")
+    def state(self, chunk0: int, nchunks: int, args: Optional[N.ScanArgs] = None, stream=None):
+        self._phase("kdn_scan_state", chunk0, nchunks, args, stream)
+
+    def output(self, chunk0: int, nchunks: int, args: Optional[N.ScanArgs] = None, stream=None):
+        self._phase("kdn_scan_output", chunk0, nchunks, args, stream)
+
+    def _phase(self, name, chunk0, nchunks, args, stream):
+        a = self.args if args is None else args
+        st = self._stream() if stream is None else ctypes.c_void_p(stream.cuda_stream)
+        N.check(getattr(N.lib(), name)(ctypes.byref(a), chunk0, nchunks, st), name)

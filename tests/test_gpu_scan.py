@@ -197,3 +197,29 @@ def test_config3_full_length(proj, oproj):
     yb, Sb = run(proj, q[:, half:], k[:, half:], v[:, half:], beta[:, half:], None, initial_state=Sa)
     assert torch.equal(torch.cat([ya, yb], 1), y)
     assert torch.equal(Sb, S)
+
+
+@pytest.mark.parametrize("seg,decay_kind", [(4, "none"), (16, "sigmoid"), (7, "narrow")])
+def test_pipelined_equals_serial(proj, seg, decay_kind):
+    """kdn_delta_scan_fwd_pipelined (prep/output on an auxiliary stream, segments rotating through up to
+    three workspace buffers) runs the same kernels as the serial schedule: results are bit-identical."""
+    q, k, v, beta, decay = make_inputs(1, 64 * 40 + 17, 3, 64, torch.bfloat16, decay_kind, seed=seg)
+    S0 = 0.1 * torch.randn(1, 3, 512, 64, generator=torch.Generator().manual_seed(7))
+    y1, S1 = run(proj, q, k, v, beta, decay, initial_state=S0, segment_chunks=seg, pipelined=True)
+    y2, S2 = run(proj, q, k, v, beta, decay, initial_state=S0, segment_chunks=seg, pipelined=False)
+    torch.cuda.synchronize()
+    assert torch.equal(y1, y2)
+    assert torch.equal(S1, S2)
+
+
+def test_pipelined_two_buffers_parity(proj, oproj):
+    """Workspace for two segment buffers only; checked against the float64 oracle."""
+    q, k, v, beta, decay = make_inputs(2, 64 * 12 + 5, 2, 32, torch.float32, "sigmoid", seed=11)
+    qd, kd, vd, bd, dd = (t.to(DEV) for t in (q, k, v, beta, decay))
+    om, ph = proj.device_omega(DEV), proj.device_phase(DEV)
+    one = ops.scan_workspace_bytes(qd, vd, om, 3, pipelined=False)
+    ws = torch.empty(2 * one, dtype=torch.uint8, device=DEV)
+    y, S = ops.scan(qd, kd, vd, bd, dd, om, ph, proj.tau_star_inv, workspace=ws, segment_chunks=3, pipelined=True)
+    yr, Sr = oracle_bthd(q, k, v, beta, decay, oproj)
+    assert rel_l2(y.cpu().numpy(), yr) < TOL_F32
+    assert rel_l2(S.cpu().numpy(), Sr) < TOL_F32
