@@ -148,9 +148,7 @@ __global__ void __launch_bounds__(256) lift_kernel(const InT* __restrict__ x, in
       const f32x4 ph = *reinterpret_cast<const f32x4*>(&s_phase_rev[16 * t + 4 * (lane >> 4)]);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        float r = acc[i] * ang_scale + ph[i];
-        r = r - __builtin_rintf(r);
-        const float cv = __builtin_amdgcn_cosf(r);
+        const float cv = __builtin_amdgcn_cosf(__builtin_amdgcn_fractf(acc[i] * ang_scale + ph[i]));
         c[t][i] = cv;
         ss += cv * cv;
       }

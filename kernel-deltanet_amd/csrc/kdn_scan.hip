@@ -64,18 +64,49 @@ struct ScanParams {
   void* y; int64_t ys0, ys1, ys2;
   unsigned char* ws;
   int64_t chunk0, nseg;  // first global chunk of the segment, chunks in the segment
+  int prep_run;          // chunks per prep workgroup (bf16)
 };
 
 template <class P>
 struct IsBF16 : std::integral_constant<bool, std::is_same<P, PrecBF16>::value> {};
 
 // ------------------------------------------------------------------------------------------------
+// Raw 16-byte pieces of one lane's part of an input row (8 elements per 32-deep block kb): 1 piece per
+// block for bf16, 2 for fp32.
+template <typename InT>
+struct RawRow {
+  static constexpr int R = (int)(8 * sizeof(InT) / 16);
+  u32x4 piece[2 * R];
+  __device__ __forceinline__ void load(const InT* row, bool valid, int lane) {
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        u32x4 z = {0u, 0u, 0u, 0u};
+        piece[kb * R + r] = valid ? reinterpret_cast<const u32x4*>(row + 32 * kb + 8 * (lane >> 4))[r] : z;
+      }
+  }
+  __device__ __forceinline__ void to_f32(int kb, float* o) const {
+    if constexpr (R == 1) {
+      const bf16x8 v = __builtin_bit_cast(bf16x8, piece[kb]);
+#pragma unroll
+      for (int s = 0; s < 8; ++s) o[s] = (float)v[s];
+    } else {
+      const f32x4 a = __builtin_bit_cast(f32x4, piece[kb * 2]), c = __builtin_bit_cast(f32x4, piece[kb * 2 + 1]);
+      o[0] = a[0]; o[1] = a[1]; o[2] = a[2]; o[3] = a[3];
+      o[4] = c[0]; o[5] = c[1]; o[6] = c[2]; o[7] = c[3];
+    }
+  }
+};
+
 // Lift of one 16-row tile per wave, for NX inputs at once (each Omega fragment feeds NX MFMAs).
 // Projection in the transposed orientation Phi^T = Omega X^T: accumulator tile t holds, in lane l,
 // feature 16t + 4(l>>4) + i of row (l & 15), which is slot (t & 1) * 4 + i of X fragment t / 2.
+// The angle in revolutions is reduced with v_fract before v_cos (which takes revolutions), so any
+// finite angle stays inside the instruction's domain.
 // Output: unnormalised cos values as X fragments, and each row's sum of squares (all lanes).
 template <class P, typename InT, int D, bool OMEGA_LDS, int NX>
-__device__ __forceinline__ void lift_tile(const InT* const (&rows)[NX], bool valid, int normalize,
+__device__ __forceinline__ void lift_tile(const RawRow<InT> (&raw)[NX], int normalize,
                                           const bf16x8* s_omega, const __bf16* omega, const float* s_phrev,
                                           float ang, int lane, typename P::frag (&out)[NX][D / 32],
                                           float (&ss)[NX]) {
@@ -85,13 +116,7 @@ __device__ __forceinline__ void lift_tile(const InT* const (&rows)[NX], bool val
 #pragma unroll
   for (int x = 0; x < NX; ++x)
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      if (valid) load8<InT>(rows[x] + 32 * kb + 8 * (lane >> 4), xv[x][kb]);
-      else {
-#pragma unroll
-        for (int s = 0; s < 8; ++s) xv[x][kb][s] = 0.f;
-      }
-    }
+    for (int kb = 0; kb < 2; ++kb) raw[x].to_f32(kb, xv[x][kb]);
   if (normalize) {
 #pragma unroll
     for (int x = 0; x < NX; ++x) {
@@ -138,9 +163,7 @@ __device__ __forceinline__ void lift_tile(const InT* const (&rows)[NX], bool val
     for (int x = 0; x < NX; ++x)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        float r = acc[x][i] * ang + ph[i];
-        r -= __builtin_rintf(r);
-        const float c = __builtin_amdgcn_cosf(r);
+        const float c = __builtin_amdgcn_cosf(__builtin_amdgcn_fractf(acc[x][i] * ang + ph[i]));
         ss[x] += c * c;
         P::set(out[x][t >> 1], (t & 1) * 4 + i, c);
       }
@@ -163,11 +186,53 @@ __device__ __forceinline__ void stage_omega(const __bf16* omega, const float* ph
 }
 
 // ------------------------------------------------------------------------------------------------
-// prep: grid (nseg, H, B), 256 threads.  Wave w owns token rows [16w, 16w+16) of the chunk.
+// prep: grid (ceil(nseg / run), H, B), 256 threads.  A workgroup prepares `run` consecutive chunks
+// of one head: Omega and the phases are staged in LDS once, and the raw q / k / v / beta / decay of the
+// next chunk are loaded into registers while the current chunk is processed.  Wave w owns token rows
+// [16w, 16w+16) of a chunk.
+// Chunks per prep workgroup: chosen at launch for bf16 (ScanParams::prep_run); 1 for fp32, whose
+// fragments (twice as wide) leave no registers for the prefetch.
+template <class P>
+struct PrepRun : std::integral_constant<int, IsBF16<P>::value ? 0 : 1> {};
+
+// Raw inputs of one chunk for one thread of the prep workgroup: the q / k row pieces of the lane's row
+// and beta / decay of token `lane` (prefetched one chunk ahead), and the V pieces of the thread
+// (loaded at the start of the chunk; they are first needed after the Gram).
+template <typename InT, int DV>
+struct PrepInputs {
+  static constexpr int VPR = DV * (int)sizeof(InT) / 16;        // 16-byte pieces per V row
+  static constexpr int VPT = (64 * VPR + 255) / 256;             // pieces per thread
+  RawRow<InT> qk[2];
+  float be, la;
+  __device__ __forceinline__ void load_qk(const ScanParams& p, int64_t b, int64_t h, int64_t t0, int w, int lane) {
+    const int64_t trow = t0 + 16 * w + (lane & 15);
+    const bool rvalid = trow < p.T;
+    qk[0].load((const InT*)p.q + b * p.qs0 + trow * p.qs1 + h * p.qs2, rvalid, lane);
+    qk[1].load((const InT*)p.k + b * p.ks0 + trow * p.ks1 + h * p.ks2, rvalid, lane);
+    const int64_t t = t0 + lane;
+    const bool valid = t < p.T;
+    be = valid ? p.beta[b * p.bs0 + t * p.bs1 + h * p.bs2] : 0.f;
+    la = (valid && p.decay) ? p.decay[b * p.ds0 + t * p.ds1 + h * p.ds2] : 1.f;
+  }
+  __device__ __forceinline__ static void load_v(const ScanParams& p, int64_t b, int64_t h, int64_t t0, u32x4 (&v)[VPT]) {
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+      const int idx = (int)threadIdx.x + 256 * i;
+      const int r = idx / VPR, pc = idx % VPR;
+      const int64_t t = t0 + r;
+      u32x4 val = {0u, 0u, 0u, 0u};
+      if (idx < 64 * VPR && t < p.T)
+        val = *reinterpret_cast<const u32x4*>((const InT*)p.v + b * p.vs0 + t * p.vs1 + h * p.vs2 + pc * (16 / (int)sizeof(InT)));
+      v[i] = val;
+    }
+  }
+};
+
 template <class P, typename InT, int D, int DV>
 __global__ void __launch_bounds__(256) prep_kernel(ScanParams p) {
   using L = WsLayout<P, D, DV>;
   using frag = typename P::frag;
+  using In = PrepInputs<InT, DV>;
   constexpr int NT = D / 16, NJ = D / 32, NV = DV / 16;
   constexpr bool OMEGA_LDS = IsBF16<P>::value;
   constexpr size_t OMEGA_BYTES = OMEGA_LDS ? (size_t)NT * 2 * 64 * 16 : 0;
@@ -184,173 +249,181 @@ __global__ void __launch_bounds__(256) prep_kernel(ScanParams p) {
   InT* s_V = reinterpret_cast<InT*>(s_T + 64 * 68);                    // [t][DV]
 
   const int lane = threadIdx.x & 63;
-  const int w = threadIdx.x >> 6;
-  const int64_t cl = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
-  const int64_t t0 = (p.chunk0 + cl) * CH;
-  unsigned char* ws = p.ws + ((b * p.H + h) * (p.nseg + 1) + cl) * L::bytes;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t h = blockIdx.y, b = blockIdx.z;
+  constexpr int RUN = PrepRun<P>::value;  // 0: runtime run length with prefetch
+  const int run = RUN ? RUN : p.prep_run;
+  const int64_t cl0 = (int64_t)blockIdx.x * run;
+  const int64_t cl_end = (cl0 + run < p.nseg) ? cl0 + run : p.nseg;
 
-  // ---- stage Omega fragments and phases; beta and the in-chunk log-decay prefix (wave 0)
+  In in;
   stage_omega<D, OMEGA_LDS>(p.omega, p.phase, s_omega, s_phrev);
-  if (w == 0) {
-    const int64_t t = t0 + lane;
-    const bool valid = t < p.T;
-    const float be = valid ? p.beta[b * p.bs0 + t * p.bs1 + h * p.bs2] : 0.f;
-    const float la = (valid && p.decay) ? p.decay[b * p.ds0 + t * p.ds1 + h * p.ds2] : 1.f;
-    float g = logf(fminf(fmaxf(la, 1e-5f), 1.f));
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const float o = __shfl_up(g, off);
-      if (lane >= off) g += o;
-    }
-    s_beta[lane] = be;
-    s_g[lane] = g;
-  }
-  __syncthreads();
+  in.load_qk(p, b, h, (p.chunk0 + cl0) * CH, w, lane);
 
-  // ---- lift q and k rows of this wave
-  const int64_t trow = t0 + 16 * w + (lane & 15);
-  const bool rvalid = trow < p.T;
-  const InT* rows[2] = {(const InT*)p.q + b * p.qs0 + trow * p.qs1 + h * p.qs2,
-                        (const InT*)p.k + b * p.ks0 + trow * p.ks1 + h * p.ks2};
-  frag cqk[2][NJ];  // [0] = q, [1] = k; X fragments (m = w, j): row 16w + (l&15), feature 32j + kappa(l, s)
-  float ss[2];
-  lift_tile<P, InT, D, OMEGA_LDS, 2>(rows, rvalid, p.normalize, s_omega, p.omega, s_phrev,
-                                     p.inv_tau * 0.15915494309189535f, lane, cqk, ss);
-  {
-    const float amp = sqrtf(2.0f / (float)D);
-    if (lane < 16) {
-      s_sq[16 * w + lane] = amp / (amp * sqrtf(ss[0]) + 1e-8f);
-      s_sk[16 * w + lane] = amp / (amp * sqrtf(ss[1]) + 1e-8f);
-    }
-  }
-#pragma unroll
-  for (int j = 0; j < NJ; ++j) {
-    store_frag<P>(ws + L::phiK + (size_t)(w * NJ + j) * 64 * L::FB, lane, cqk[1][j]);
-    store_frag<P>(ws + L::phiQ + (size_t)(w * NJ + j) * 64 * L::FB, lane, cqk[0][j]);
-    s_phik[(w * NJ + j) * 64 + lane] = cqk[1][j];
-  }
-  __syncthreads();
+  auto process = [&](int64_t cl) {
+    const int64_t t0 = (p.chunk0 + cl) * CH;
+    unsigned char* ws = p.ws + ((b * p.H + h) * (p.nseg + 1) + cl) * L::bytes;
+    u32x4 vraw[In::VPT];
+    if constexpr (RUN != 1) In::load_v(p, b, h, t0, vraw);  // early: first needed after the Gram
+    __syncthreads();  // Omega staged (first chunk); the previous chunk's LDS reads are done
 
-  // ---- Gram tiles (m, n = w):  Gkk[m][w] = K_m K_w^T,  GqkT[m][w] = K_m Q_w^T  (unnormalised)
-  f32x4 gkk[4], gqk[4];
+    // ---- beta and the in-chunk log-decay prefix (wave 0)
+    if (w == 0) {
+      float g = logf(fminf(fmaxf(in.la, 1e-5f), 1.f));
 #pragma unroll
-  for (int m = 0; m < 4; ++m) { gkk[m] = zero4(); gqk[m] = zero4(); }
-#pragma unroll
-  for (int j = 0; j < NJ; ++j) {
-#pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      const frag a = s_phik[(m * NJ + j) * 64 + lane];
-      gkk[m] = P::mma(gkk[m], a, cqk[1][j]);
-      gqk[m] = P::mma(gqk[m], a, cqk[0][j]);
+      for (int off = 1; off < 64; off <<= 1) {
+        const float o = __shfl_up(g, off);
+        if (lane >= off) g += o;
+      }
+      s_beta[lane] = in.be;
+      s_g[lane] = g;
     }
-  }
-  __syncthreads();  // K fragments in LDS are dead from here on
 
-  // ---- A (for the inverse), P fragments, V staging, scale vectors
-  {
-    const int t = 16 * w + (lane & 15);
-    const float bt = s_beta[t], gt = s_g[t], gtm1 = t > 0 ? s_g[t - 1] : 0.f;
-    const float skt = s_sk[t], sqt = s_sq[t];
-    f32x4 pt[4];
-#pragma unroll
-    for (int m = 0; m < 4; ++m) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int j = 16 * m + 4 * (lane >> 4) + i;
-        const float gj = s_g[j], skj = s_sk[j];
-        const float a = (j < t) ? bt * __expf(fminf(gt - gj, 0.f)) * gkk[m][i] * skt * skj : 0.f;
-        s_A[(t * 4 + i) * 16 + 4 * m + (lane >> 4)] = a;  // j = 4(4m + (l>>4)) + i
-        pt[m][i] = (j < t) ? __expf(fminf(gtm1 - gj, 0.f)) * gqk[m][i] * sqt * skj : 0.f;
+    // ---- lift q and k rows of this wave
+    frag cqk[2][NJ];  // [0] = q, [1] = k; X fragments (m = w, j): row 16w + (l&15), feature 32j + kappa(l, s)
+    float ss[2];
+    lift_tile<P, InT, D, OMEGA_LDS, 2>(in.qk, p.normalize, s_omega, p.omega, s_phrev,
+                                       p.inv_tau * 0.15915494309189535f, lane, cqk, ss);
+    // the next chunk's rows travel while this one is processed (clamped: the last chunk reloads itself)
+    if constexpr (RUN != 1) in.load_qk(p, b, h, (p.chunk0 + ((cl + 1 < cl_end) ? cl + 1 : cl)) * CH, w, lane);
+    {
+      const float amp = sqrtf(2.0f / (float)D);
+      if (lane < 16) {
+        s_sq[16 * w + lane] = amp / (amp * sqrtf(ss[0]) + 1e-8f);
+        s_sk[16 * w + lane] = amp / (amp * sqrtf(ss[1]) + 1e-8f);
       }
     }
 #pragma unroll
-    for (int jb = 0; jb < 2; ++jb)
-      store_frag<P>(ws + L::Pm + (size_t)(w * 2 + jb) * 64 * L::FB, lane, P::from_f32(pair_to8(pt[2 * jb], pt[2 * jb + 1])));
-  }
-  {
-    // V rows of the chunk (zero past T), 16-byte loads
-    constexpr int VPR = DV * sizeof(InT) / 16;  // 16-byte pieces per row
-    for (int idx = threadIdx.x; idx < 64 * VPR; idx += 256) {
-      const int r = idx / VPR, pc = idx % VPR;
-      const int64_t t = t0 + r;
-      u32x4 val = {0u, 0u, 0u, 0u};
-      if (t < p.T) val = *reinterpret_cast<const u32x4*>((const InT*)p.v + b * p.vs0 + t * p.vs1 + h * p.vs2 + pc * (16 / sizeof(InT)));
-      *reinterpret_cast<u32x4*>(s_V + r * DV + pc * (16 / sizeof(InT))) = val;
+    for (int j = 0; j < NJ; ++j) {
+      store_frag<P>(ws + L::phiK + (size_t)(w * NJ + j) * 64 * L::FB, lane, cqk[1][j]);
+      store_frag<P>(ws + L::phiQ + (size_t)(w * NJ + j) * 64 * L::FB, lane, cqk[0][j]);
+      s_phik[(w * NJ + j) * 64 + lane] = cqk[1][j];
     }
-  }
-  if (w == 1) {
-    float* vec = reinterpret_cast<float*>(ws + L::VEC);
-    const float g63 = s_g[63];
-    const float gtm1 = lane > 0 ? s_g[lane - 1] : 0.f;
-    vec[lane] = __expf(fminf(gtm1, 0.f)) * s_sq[lane];                 // e^{g_{t-1}} * |phi_q| scale
-    vec[64 + lane] = __expf(fminf(g63 - s_g[lane], 0.f)) * s_sk[lane]; // e^{g_63 - g_t} * |phi_k| scale
-    if (lane == 0) vec[128] = __expf(fminf(g63, 0.f));
-  }
-  __syncthreads();
+    __syncthreads();
 
-  // ---- T = (I + A)^{-1}: column col = 16w + (l>>2) per lane quad; lane p = l&3 keeps rows 4k'+p
-  {
-    const int col = 16 * w + (lane >> 2), pq = lane & 3;
-    float Tr[16];
+    // ---- Gram tiles (m, n = w):  Gkk[m][w] = K_m K_w^T,  GqkT[m][w] = K_m Q_w^T  (unnormalised)
+    f32x4 gkk[4], gqk[4];
 #pragma unroll
-    for (int k = 0; k < 16; ++k) Tr[k] = 0.f;
+    for (int m = 0; m < 4; ++m) { gkk[m] = zero4(); gqk[m] = zero4(); }
 #pragma unroll
-    for (int i = 0; i < 64; ++i) {
-      const float* arow = s_A + (i * 4 + pq) * 16;
-      float part = 0.f;
+    for (int j = 0; j < NJ; ++j) {
 #pragma unroll
-      for (int k = 0; k < (i + 3) / 4; ++k) part += arow[k] * Tr[k];
-      part += xor_shuffle<1>(part);
-      part += xor_shuffle<2>(part);
-      const float val = (i == col ? 1.f : 0.f) - part;
-      if (pq == (i & 3)) Tr[i >> 2] = val;
-    }
-#pragma unroll
-    for (int k = 0; k < 16; ++k) s_T[(4 * k + pq) * 68 + col] = Tr[k];
-  }
-  __syncthreads();
-
-  // ---- W~ factor T diag(beta e^g |phi_k|) fragments, and U~ = T diag(beta) V   (wave w: rows m = w)
-  {
-    const int t = 16 * w + (lane & 15);
-    f32x8 tb[2];
-#pragma unroll
-    for (int jb = 0; jb < 2; ++jb) {
-      f32x8 tw;
-#pragma unroll
-      for (int s = 0; s < 8; ++s) {
-        const int j = 32 * jb + kappa(lane, s);
-        const float tv = s_T[t * 68 + j];
-        tw[s] = tv * s_beta[j] * __expf(s_g[j]) * s_sk[j];
-        tb[jb][s] = tv * s_beta[j];
+      for (int m = 0; m < 4; ++m) {
+        const frag a = s_phik[(m * NJ + j) * 64 + lane];
+        gkk[m] = P::mma(gkk[m], a, cqk[1][j]);
+        gqk[m] = P::mma(gqk[m], a, cqk[0][j]);
       }
-      store_frag<P>(ws + L::Tp + (size_t)(w * 2 + jb) * 64 * L::FB, lane, P::from_f32(tw));
     }
+    __syncthreads();  // K fragments in LDS are dead from here on
+
+    // ---- A (for the inverse), P fragments, V staging, scale vectors
+    {
+      const int t = 16 * w + (lane & 15);
+      const float bt = s_beta[t], gt = s_g[t], gtm1 = t > 0 ? s_g[t - 1] : 0.f;
+      const float skt = s_sk[t], sqt = s_sq[t];
+      f32x4 pt[4];
 #pragma unroll
-    for (int n = 0; n < NV; ++n) {
-      f32x4 acc = zero4();
+      for (int m = 0; m < 4; ++m) {
 #pragma unroll
-      for (int jb = 0; jb < 2; ++jb) {
-        f32x8 vv;
-#pragma unroll
-        for (int s = 0; s < 8; ++s) vv[s] = (float)s_V[(32 * jb + kappa(lane, s)) * DV + 16 * n + (lane & 15)];
-        if constexpr (IsBF16<P>::value) {
-          // hi + lo split of T diag(beta): V is exact in bf16, so U~ keeps ~16 bits.
-          bf16x8 hi, lo, vb;
-#pragma unroll
-          for (int s = 0; s < 8; ++s) {
-            hi[s] = (__bf16)tb[jb][s];
-            lo[s] = (__bf16)(tb[jb][s] - (float)hi[s]);
-            vb[s] = (__bf16)vv[s];
-          }
-          acc = PrecBF16::mma(acc, hi, vb);
-          acc = PrecBF16::mma(acc, lo, vb);
-        } else {
-          acc = P::mma(acc, P::from_f32(tb[jb]), P::from_f32(vv));
+        for (int i = 0; i < 4; ++i) {
+          const int j = 16 * m + 4 * (lane >> 4) + i;
+          const float gj = s_g[j], skj = s_sk[j];
+          const float a = (j < t) ? bt * __expf(fminf(gt - gj, 0.f)) * gkk[m][i] * skt * skj : 0.f;
+          s_A[(t * 4 + i) * 16 + 4 * m + (lane >> 4)] = a;  // j = 4(4m + (l>>4)) + i
+          pt[m][i] = (j < t) ? __expf(fminf(gtm1 - gj, 0.f)) * gqk[m][i] * sqt * skj : 0.f;
         }
       }
-      *reinterpret_cast<f32x4*>(ws + L::U + ((size_t)(w * NV + n) * 64 + lane) * 16) = acc;
+#pragma unroll
+      for (int jb = 0; jb < 2; ++jb)
+        store_frag<P>(ws + L::Pm + (size_t)(w * 2 + jb) * 64 * L::FB, lane, P::from_f32(pair_to8(pt[2 * jb], pt[2 * jb + 1])));
     }
+    if constexpr (RUN == 1) In::load_v(p, b, h, t0, vraw);
+#pragma unroll
+    for (int i = 0; i < In::VPT; ++i) {
+      const int idx = (int)threadIdx.x + 256 * i;
+      if (idx < 64 * In::VPR) *reinterpret_cast<u32x4*>(s_V + (idx / In::VPR) * DV + (idx % In::VPR) * (16 / (int)sizeof(InT))) = vraw[i];
+    }
+    if (w == 1) {
+      float* vec = reinterpret_cast<float*>(ws + L::VEC);
+      const float g63 = s_g[63];
+      const float gtm1 = lane > 0 ? s_g[lane - 1] : 0.f;
+      vec[lane] = __expf(fminf(gtm1, 0.f)) * s_sq[lane];                 // e^{g_{t-1}} * |phi_q| scale
+      vec[64 + lane] = __expf(fminf(g63 - s_g[lane], 0.f)) * s_sk[lane]; // e^{g_63 - g_t} * |phi_k| scale
+      if (lane == 0) vec[128] = __expf(fminf(g63, 0.f));
+    }
+    __syncthreads();
+
+    // ---- T = (I + A)^{-1}: column col = 16w + (l>>2) per lane quad; lane p = l&3 keeps rows 4k'+p.
+    // Forward substitution; each row's dot product is summed as four independent partial sums.
+    {
+      const int col = 16 * w + (lane >> 2), pq = lane & 3;
+      float Tr[16];
+#pragma unroll
+      for (int k = 0; k < 16; ++k) Tr[k] = 0.f;
+#pragma unroll
+      for (int i = 0; i < 64; ++i) {
+        const float* arow = s_A + (i * 4 + pq) * 16;
+        float part4[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int k = 0; k < (i + 3) / 4; ++k) part4[k & 3] += arow[k] * Tr[k];
+        float part = (part4[0] + part4[1]) + (part4[2] + part4[3]);
+        part += xor_shuffle<1>(part);
+        part += xor_shuffle<2>(part);
+        const float val = (i == col ? 1.f : 0.f) - part;
+        if (pq == (i & 3)) Tr[i >> 2] = val;
+      }
+#pragma unroll
+      for (int k = 0; k < 16; ++k) s_T[(4 * k + pq) * 68 + col] = Tr[k];
+    }
+    __syncthreads();
+
+    // ---- W~ factor T diag(beta e^g |phi_k|) fragments, and U~ = T diag(beta) V   (wave w: rows m = w)
+    {
+      const int t = 16 * w + (lane & 15);
+      f32x8 tb[2];
+#pragma unroll
+      for (int jb = 0; jb < 2; ++jb) {
+        f32x8 tw;
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+          const int j = 32 * jb + kappa(lane, s);
+          const float tv = s_T[t * 68 + j];
+          tw[s] = tv * s_beta[j] * __expf(s_g[j]) * s_sk[j];
+          tb[jb][s] = tv * s_beta[j];
+        }
+        store_frag<P>(ws + L::Tp + (size_t)(w * 2 + jb) * 64 * L::FB, lane, P::from_f32(tw));
+      }
+#pragma unroll
+      for (int n = 0; n < NV; ++n) {
+        f32x4 acc = zero4();
+#pragma unroll
+        for (int jb = 0; jb < 2; ++jb) {
+          f32x8 vv;
+#pragma unroll
+          for (int s = 0; s < 8; ++s) vv[s] = (float)s_V[(32 * jb + kappa(lane, s)) * DV + 16 * n + (lane & 15)];
+          if constexpr (IsBF16<P>::value) {
+            // hi + lo split of T diag(beta): V is exact in bf16, so U~ keeps ~16 bits.
+            bf16x8 hi, lo, vb;
+#pragma unroll
+            for (int s = 0; s < 8; ++s) {
+              hi[s] = (__bf16)tb[jb][s];
+              lo[s] = (__bf16)(tb[jb][s] - (float)hi[s]);
+              vb[s] = (__bf16)vv[s];
+            }
+            acc = PrecBF16::mma(acc, hi, vb);
+            acc = PrecBF16::mma(acc, lo, vb);
+          } else {
+            acc = P::mma(acc, P::from_f32(tb[jb]), P::from_f32(vv));
+          }
+        }
+        *reinterpret_cast<f32x4*>(ws + L::U + ((size_t)(w * NV + n) * 64 + lane) * 16) = acc;
+      }
+    }
+  };
+  if constexpr (RUN == 1) {
+    process(cl0);
+  } else {
+    for (int64_t cl = cl0; cl < cl_end; ++cl) process(cl);
   }
 }
 
@@ -795,11 +868,36 @@ static ScanParams fill_params(const kdn_scan_args* a) {
 // Parameters of one segment: chunks [c0, c0 + nseg) with its records at `ws`.  The state kernel of the
 // segment starting at chunk 0 reads initial_state (zeros if NULL); later segments continue from
 // final_state.
-static ScanParams segment_params(const kdn_scan_args* a, int64_t c0, int64_t nseg, void* ws) {
+// Number of compute units of the current device (0 if the query fails).
+static int device_cus() {
+  int dev = 0, n = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+  return n;
+}
+
+// Chunks per prep workgroup: each workgroup of the prep kernel holds a CU alone (its LDS), so the
+// kernel runs in ceil(workgroups / CUs) rounds, each costing the staging of Omega (about 0.3 of a
+// chunk, measured) plus `run` chunks.  Pick the run length (1..8) with the least total for the CUs
+// left free (all of them, or those the concurrent state kernel does not occupy).
+static int choose_prep_run(int64_t nseg, int64_t heads, int cus) {
+  if (cus <= 0) return 4;
+  int best = 1;
+  int64_t best_cost = INT64_MAX;
+  for (int run = 1; run <= 8; ++run) {
+    const int64_t wgs = (nseg + run - 1) / run * heads;
+    const int64_t cost = (wgs + cus - 1) / cus * (10 * run + 3);
+    if (cost < best_cost) { best_cost = cost; best = run; }
+  }
+  return best;
+}
+
+static ScanParams segment_params(const kdn_scan_args* a, int64_t c0, int64_t nseg, void* ws, int prep_cus) {
   ScanParams p = fill_params(a);
   p.chunk0 = c0;
   p.nseg = nseg;
   p.ws = (unsigned char*)ws;
+  p.prep_run = choose_prep_run(nseg, a->B * a->H, prep_cus);
   if (c0 == 0) {
     p.state_in = a->initial_state;
     p.is0 = a->init_stride[0]; p.is1 = a->init_stride[1]; p.is2 = a->init_stride[2]; p.is3 = a->init_stride[3];
@@ -810,14 +908,25 @@ static ScanParams segment_params(const kdn_scan_args* a, int64_t c0, int64_t nse
   return p;
 }
 
+#ifndef STATE_SHARE_CU
+#define STATE_SHARE_CU 0
+#endif
+constexpr int STATE_EXCLUSIVE_LDS = 40 * 1024;  // dynamic LDS: 88 + 40 = 128 KB > 160 - 49 (output WG)
+
 template <class P, typename InT, typename OutT, int D, int DV>
 static int launch_phase(const ScanParams& p, int phase, hipStream_t st) {
   const dim3 chunk_grid((unsigned)p.nseg, (unsigned)p.H, (unsigned)p.B);
   if (phase == PHASE_PREP) {
-    hipLaunchKernelGGL((prep_kernel<P, InT, D, DV>), chunk_grid, dim3(256), 0, st, p);
+    constexpr int RUN = PrepRun<P>::value;
+    const int run = RUN ? RUN : p.prep_run;
+    const dim3 prep_grid((unsigned)((p.nseg + run - 1) / run), (unsigned)p.H, (unsigned)p.B);
+    hipLaunchKernelGGL((prep_kernel<P, InT, D, DV>), prep_grid, dim3(256), 0, st, p);
   } else if (phase == PHASE_STATE) {
-    if (p.decay) hipLaunchKernelGGL((state_kernel<P, D, DV, true>), dim3(state_grid(p.B, p.H, DV / 16)), dim3(256), 0, st, p);
-    else hipLaunchKernelGGL((state_kernel<P, D, DV, false>), dim3(state_grid(p.B, p.H, DV / 16)), dim3(256), 0, st, p);
+    // The state workgroups are the sequential critical path: reserve enough LDS that no prep or output
+    // workgroup can share their CU (a CU has 160 KB; the bf16 state kernel uses 88 KB statically).
+    const size_t excl = (IsBF16<P>::value && !STATE_SHARE_CU) ? (size_t)STATE_EXCLUSIVE_LDS : 0;
+    if (p.decay) hipLaunchKernelGGL((state_kernel<P, D, DV, true>), dim3(state_grid(p.B, p.H, DV / 16)), dim3(256), excl, st, p);
+    else hipLaunchKernelGGL((state_kernel<P, D, DV, false>), dim3(state_grid(p.B, p.H, DV / 16)), dim3(256), excl, st, p);
   } else {
     hipLaunchKernelGGL((output_kernel<P, OutT, D, DV>), chunk_grid, dim3(256), 0, st, p);
   }
@@ -828,8 +937,9 @@ static int launch_phase(const ScanParams& p, int phase, hipStream_t st) {
 // selected kernels, in the order prep, state, output.
 template <class P, typename InT, typename OutT, int D, int DV>
 static int run_scan(const kdn_scan_args* a, int64_t c_begin, int64_t c_end, int64_t seg, int phases, hipStream_t st) {
+  const int cus = device_cus();
   for (int64_t c0 = c_begin; c0 < c_end; c0 += seg) {
-    const ScanParams p = segment_params(a, c0, (c_end - c0 < seg) ? (c_end - c0) : seg, a->workspace);
+    const ScanParams p = segment_params(a, c0, (c_end - c0 < seg) ? (c_end - c0) : seg, a->workspace, cus);
     for (int ph : {PHASE_PREP, PHASE_STATE, PHASE_OUTPUT}) {
       if (!(phases & ph)) continue;
       const int rc = launch_phase<P, InT, OutT, D, DV>(p, ph, st);
@@ -871,10 +981,12 @@ static int run_pipelined(const kdn_scan_args* a, int64_t seg, int nbuf, size_t b
   hipEvent_t* evP = evs.ev;
   hipEvent_t* evS = evs.ev + nbuf;
   hipEvent_t evIn = evs.ev[2 * nbuf], evOut = evs.ev[2 * nbuf + 1];
+  // prep shares the device with the state kernel's workgroups (one per CU)
+  const int prep_cus = device_cus() - (int)state_grid(a->B, a->H, DV / 16);
   auto seg_p = [&](int64_t s) {
     const int64_t c0 = s * seg;
     return segment_params(a, c0, (nchunks - c0 < seg) ? (nchunks - c0) : seg,
-                          (unsigned char*)a->workspace + (size_t)(s % nbuf) * buf_bytes);
+                          (unsigned char*)a->workspace + (size_t)(s % nbuf) * buf_bytes, prep_cus);
   };
 #define KDN_TRY(x) do { if ((x) != hipSuccess) return KDN_ERR_DEVICE; } while (0)
 #define KDN_TRYK(x) do { const int _rc = (x); if (_rc != KDN_OK) return _rc; } while (0)
