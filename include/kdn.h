@@ -104,6 +104,20 @@ typedef struct kdn_scan_args {
   void* y;         int64_t y_stride[3];
   void* workspace; size_t workspace_bytes;
   int64_t segment_chunks;      /* 64-token chunks per segment; 0 lets the library choose */
+  /* Feature map (ABI 1.1).  All-zero values select the structured-FWHT lift above (kernels/fwht.py):
+   *   phi = cos(xh Omega_h^T inv_tau_h + phase_h) * sqrt(2/D), divided by (||.|| + 1e-8) unless
+   *   no_renorm is set.  General projections (kernels/kernel_deltanet_fused.py:238-251 and
+   *   core/rkhs_features.py:107-131 of the reference) pass Omega as hi + lo bf16 parts. */
+  const void* omega_lo;        /* bf16 [D][d_k] low part of Omega (Omega = hi + lo); NULL when hi is exact */
+  int64_t omega_head_stride;   /* elements between heads' Omega (hi and lo); 0 = one Omega for all heads */
+  int64_t phase_head_stride;   /* elements between heads' phases; 0 = shared */
+  const float* inv_tau_head;   /* [H] per-head 1/tau; NULL = inv_tau for every head */
+  int no_renorm;               /* 1: phi = sqrt(2/D) cos(.), no division by its norm */
+  int feature_mode;            /* 0: lift q, k (d_k -> D); 1: q and k are already lifted features (d_k = D) */
+  /* Update rule.  0: the gated delta rule above.  1: gated linear attention without the erasure term,
+   *   S_t = lambda_t S_{t-1} + beta_t v_t phi(k_t)^T, readout y_t = S_{t-1} phi(q_t) as before
+   *   (the recurrence of core/chunked_scan.py:145-186, with beta = eta and lambda per head). */
+  int rule;
 } kdn_scan_args;
 
 /* Workspace bytes kdn_delta_scan_fwd needs for these arguments (0 if the arguments are invalid).

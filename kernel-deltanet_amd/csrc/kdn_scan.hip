@@ -65,7 +65,16 @@ struct ScanParams {
   unsigned char* ws;
   int64_t chunk0, nseg;  // first global chunk of the segment, chunks in the segment
   int prep_run;          // chunks per prep workgroup (bf16)
+  // feature map: per-head Omega (hi [+ lo]) / phases / 1/tau, renormalisation, pre-lifted inputs
+  const __bf16* omega_lo; int64_t oms, phs;
+  const float* inv_tau_head;
+  int no_renorm, prelifted;
+  int linear;  // update rule without the erasure term: T = I, Tp = 0
 };
+
+// Feature modes of the prep kernel: Omega exact in bf16 (the structured projection), Omega as hi + lo
+// bf16 parts (general projections), or q / k already lifted (d_k = D).
+enum FeatureMode { FM_EXACT = 0, FM_HILO = 1, FM_PRELIFTED = 2 };
 
 template <class P>
 struct IsBF16 : std::integral_constant<bool, std::is_same<P, PrecBF16>::value> {};
@@ -105,11 +114,11 @@ struct RawRow {
 // The angle in revolutions is reduced with v_fract before v_cos (which takes revolutions), so any
 // finite angle stays inside the instruction's domain.
 // Output: unnormalised cos values as X fragments, and each row's sum of squares (all lanes).
-template <class P, typename InT, int D, bool OMEGA_LDS, int NX>
+template <class P, typename InT, int D, bool OMEGA_LDS, int NX, bool LO = false>
 __device__ __forceinline__ void lift_tile(const RawRow<InT> (&raw)[NX], int normalize,
                                           const bf16x8* s_omega, const __bf16* omega, const float* s_phrev,
                                           float ang, int lane, typename P::frag (&out)[NX][D / 32],
-                                          float (&ss)[NX]) {
+                                          float (&ss)[NX], const __bf16* omega_lo = nullptr) {
   constexpr int NT = D / 16;
   constexpr int NSPLIT = XFrag<InT>::NSPLIT;
   float xv[NX][2][8];
@@ -157,6 +166,13 @@ __device__ __forceinline__ void lift_tile(const RawRow<InT> (&raw)[NX], int norm
       for (int s = 0; s < NSPLIT; ++s)
 #pragma unroll
         for (int x = 0; x < NX; ++x) acc[x] = PrecBF16::mma(acc[x], a, xb[x][kb][s]);
+      if constexpr (LO) {
+        const bf16x8 alo = *reinterpret_cast<const bf16x8*>(omega_lo + (int64_t)(16 * t + (lane & 15)) * 64 + 32 * kb + 8 * (lane >> 4));
+#pragma unroll
+        for (int s = 0; s < NSPLIT; ++s)
+#pragma unroll
+          for (int x = 0; x < NX; ++x) acc[x] = PrecBF16::mma(acc[x], alo, xb[x][kb][s]);
+      }
     }
     const f32x4 ph = *reinterpret_cast<const f32x4*>(&s_phrev[16 * t + 4 * (lane >> 4)]);
 #pragma unroll
@@ -190,10 +206,11 @@ __device__ __forceinline__ void stage_omega(const __bf16* omega, const float* ph
 // of one head: Omega and the phases are staged in LDS once, and the raw q / k / v / beta / decay of the
 // next chunk are loaded into registers while the current chunk is processed.  Wave w owns token rows
 // [16w, 16w+16) of a chunk.
-// Chunks per prep workgroup: chosen at launch for bf16 (ScanParams::prep_run); 1 for fp32, whose
-// fragments (twice as wide) leave no registers for the prefetch.
-template <class P>
-struct PrepRun : std::integral_constant<int, IsBF16<P>::value ? 0 : 1> {};
+// Chunks per prep workgroup: chosen at launch for bf16 with the exact or given features
+// (ScanParams::prep_run); 1 for fp32, whose fragments (twice as wide) leave no registers for the
+// prefetch, and for the hi + lo projection, whose second operand stream does the same.
+template <class P, int FM>
+struct PrepRun : std::integral_constant<int, (IsBF16<P>::value && FM != FM_HILO) ? 0 : 1> {};
 
 // Raw inputs of one chunk for one thread of the prep workgroup: the q / k row pieces of the lane's row
 // and beta / decay of token `lane` (prefetched one chunk ahead), and the V pieces of the thread
@@ -228,13 +245,28 @@ struct PrepInputs {
   }
 };
 
-template <class P, typename InT, int D, int DV>
+// Lifted features given as input (FM_PRELIFTED): X fragment j of the lane's row, features 32j + kappa(l, s)
+// (two runs of four: 32j + 4(l>>4) .. +3 and 32j + 16 + 4(l>>4) .. +3).
+template <class P, typename InT, int D>
+__device__ __forceinline__ void load_lifted(const InT* row, bool valid, int lane, typename P::frag (&out)[D / 32]) {
+#pragma unroll
+  for (int j = 0; j < D / 32; ++j) {
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      const InT* src = row + 32 * j + 16 * half + 4 * (lane >> 4);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) P::set(out[j], 4 * half + i, valid ? (float)src[i] : 0.f);
+    }
+  }
+}
+
+template <class P, typename InT, int D, int DV, int FM>
 __global__ void __launch_bounds__(256) prep_kernel(ScanParams p) {
   using L = WsLayout<P, D, DV>;
   using frag = typename P::frag;
   using In = PrepInputs<InT, DV>;
   constexpr int NT = D / 16, NJ = D / 32, NV = DV / 16;
-  constexpr bool OMEGA_LDS = IsBF16<P>::value;
+  constexpr bool OMEGA_LDS = IsBF16<P>::value && FM != FM_PRELIFTED;
   constexpr size_t OMEGA_BYTES = OMEGA_LDS ? (size_t)NT * 2 * 64 * 16 : 0;
   constexpr size_t PHIK_BYTES = (size_t)4 * NJ * 64 * sizeof(frag);
   // After the Gram the K-fragment area is reused for A (16 KB), T (17 KB) and V.
@@ -251,14 +283,25 @@ __global__ void __launch_bounds__(256) prep_kernel(ScanParams p) {
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int64_t h = blockIdx.y, b = blockIdx.z;
-  constexpr int RUN = PrepRun<P>::value;  // 0: runtime run length with prefetch
+  constexpr int RUN = PrepRun<P, FM>::value;  // 0: runtime run length with prefetch
   const int run = RUN ? RUN : p.prep_run;
   const int64_t cl0 = (int64_t)blockIdx.x * run;
   const int64_t cl_end = (cl0 + run < p.nseg) ? cl0 + run : p.nseg;
 
+  const __bf16* omega_h = p.omega + h * p.oms;
+  const __bf16* omega_lo_h = (FM == FM_HILO) ? p.omega_lo + h * p.oms : nullptr;
+  const float ang = (p.inv_tau_head ? p.inv_tau_head[h] : p.inv_tau) * 0.15915494309189535f;
   In in;
-  stage_omega<D, OMEGA_LDS>(p.omega, p.phase, s_omega, s_phrev);
-  in.load_qk(p, b, h, (p.chunk0 + cl0) * CH, w, lane);
+  if constexpr (FM != FM_PRELIFTED) {
+    stage_omega<D, OMEGA_LDS>(omega_h, p.phase + h * p.phs, s_omega, s_phrev);
+    in.load_qk(p, b, h, (p.chunk0 + cl0) * CH, w, lane);
+  } else {
+    // no lift: only beta / decay come through the prefetch
+    const int64_t t = (p.chunk0 + cl0) * CH + lane;
+    const bool valid = t < p.T;
+    in.be = valid ? p.beta[b * p.bs0 + t * p.bs1 + h * p.bs2] : 0.f;
+    in.la = (valid && p.decay) ? p.decay[b * p.ds0 + t * p.ds1 + h * p.ds2] : 1.f;
+  }
 
   auto process = [&](int64_t cl) {
     const int64_t t0 = (p.chunk0 + cl) * CH;
@@ -279,18 +322,38 @@ __global__ void __launch_bounds__(256) prep_kernel(ScanParams p) {
       s_g[lane] = g;
     }
 
-    // ---- lift q and k rows of this wave
+    // ---- lift q and k rows of this wave (or load the given features)
     frag cqk[2][NJ];  // [0] = q, [1] = k; X fragments (m = w, j): row 16w + (l&15), feature 32j + kappa(l, s)
-    float ss[2];
-    lift_tile<P, InT, D, OMEGA_LDS, 2>(in.qk, p.normalize, s_omega, p.omega, s_phrev,
-                                       p.inv_tau * 0.15915494309189535f, lane, cqk, ss);
-    // the next chunk's rows travel while this one is processed (clamped: the last chunk reloads itself)
-    if constexpr (RUN != 1) in.load_qk(p, b, h, (p.chunk0 + ((cl + 1 < cl_end) ? cl + 1 : cl)) * CH, w, lane);
+    float ss[2] = {0.f, 0.f};
+    if constexpr (FM == FM_PRELIFTED) {
+      const int64_t trow = t0 + 16 * w + (lane & 15);
+      load_lifted<P, InT, D>((const InT*)p.q + b * p.qs0 + trow * p.qs1 + h * p.qs2, trow < p.T, lane, cqk[0]);
+      load_lifted<P, InT, D>((const InT*)p.k + b * p.ks0 + trow * p.ks1 + h * p.ks2, trow < p.T, lane, cqk[1]);
+      const int64_t tn = (p.chunk0 + ((cl + 1 < cl_end) ? cl + 1 : cl)) * CH + lane;
+      in.be = (tn < p.T) ? p.beta[b * p.bs0 + tn * p.bs1 + h * p.bs2] : 0.f;
+      in.la = (tn < p.T && p.decay) ? p.decay[b * p.ds0 + tn * p.ds1 + h * p.ds2] : 1.f;
+    } else {
+      lift_tile<P, InT, D, OMEGA_LDS, 2, FM == FM_HILO>(in.qk, p.normalize, s_omega, omega_h, s_phrev, ang, lane,
+                                                         cqk, ss, omega_lo_h);
+      // the next chunk's rows travel while this one is processed (clamped: the last chunk reloads itself)
+      if constexpr (RUN != 1) in.load_qk(p, b, h, (p.chunk0 + ((cl + 1 < cl_end) ? cl + 1 : cl)) * CH, w, lane);
+    }
     {
+      // per-row scale of the stored (unnormalised) features: 1 for given features, sqrt(2/D) without
+      // renormalisation, sqrt(2/D) / (||sqrt(2/D) c|| + 1e-8) with it
       const float amp = sqrtf(2.0f / (float)D);
       if (lane < 16) {
-        s_sq[16 * w + lane] = amp / (amp * sqrtf(ss[0]) + 1e-8f);
-        s_sk[16 * w + lane] = amp / (amp * sqrtf(ss[1]) + 1e-8f);
+        float sq_, sk_;
+        if constexpr (FM == FM_PRELIFTED) {
+          sq_ = 1.f; sk_ = 1.f;
+        } else if (p.no_renorm) {
+          sq_ = amp; sk_ = amp;
+        } else {
+          sq_ = amp / (amp * sqrtf(ss[0]) + 1e-8f);
+          sk_ = amp / (amp * sqrtf(ss[1]) + 1e-8f);
+        }
+        s_sq[16 * w + lane] = sq_;
+        s_sk[16 * w + lane] = sk_;
       }
     }
 #pragma unroll
@@ -319,7 +382,8 @@ __global__ void __launch_bounds__(256) prep_kernel(ScanParams p) {
     // ---- A (for the inverse), P fragments, V staging, scale vectors
     {
       const int t = 16 * w + (lane & 15);
-      const float bt = s_beta[t], gt = s_g[t], gtm1 = t > 0 ? s_g[t - 1] : 0.f;
+      // the linear rule has no erasure coupling: A = 0, so T = I below
+      const float bt = p.linear ? 0.f : s_beta[t], gt = s_g[t], gtm1 = t > 0 ? s_g[t - 1] : 0.f;
       const float skt = s_sk[t], sqt = s_sq[t];
       f32x4 pt[4];
 #pragma unroll
@@ -388,7 +452,7 @@ __global__ void __launch_bounds__(256) prep_kernel(ScanParams p) {
         for (int s = 0; s < 8; ++s) {
           const int j = 32 * jb + kappa(lane, s);
           const float tv = s_T[t * 68 + j];
-          tw[s] = tv * s_beta[j] * __expf(s_g[j]) * s_sk[j];
+          tw[s] = p.linear ? 0.f : tv * s_beta[j] * __expf(s_g[j]) * s_sk[j];  // linear: E = U~
           tb[jb][s] = tv * s_beta[j];
         }
         store_frag<P>(ws + L::Tp + (size_t)(w * 2 + jb) * 64 * L::FB, lane, P::from_f32(tw));
@@ -862,6 +926,13 @@ static ScanParams fill_params(const kdn_scan_args* a) {
   p.os0 = a->final_stride[0]; p.os1 = a->final_stride[1]; p.os2 = a->final_stride[2]; p.os3 = a->final_stride[3];
   p.y = a->y; p.ys0 = a->y_stride[0]; p.ys1 = a->y_stride[1]; p.ys2 = a->y_stride[2];
   p.ws = (unsigned char*)a->workspace;
+  p.omega_lo = (const __bf16*)a->omega_lo;
+  p.oms = a->omega_head_stride;
+  p.phs = a->phase_head_stride;
+  p.inv_tau_head = a->inv_tau_head;
+  p.no_renorm = a->no_renorm ? 1 : 0;
+  p.prelifted = a->feature_mode == 1 ? 1 : 0;
+  p.linear = a->rule == 1 ? 1 : 0;
   return p;
 }
 
@@ -917,10 +988,14 @@ template <class P, typename InT, typename OutT, int D, int DV>
 static int launch_phase(const ScanParams& p, int phase, hipStream_t st) {
   const dim3 chunk_grid((unsigned)p.nseg, (unsigned)p.H, (unsigned)p.B);
   if (phase == PHASE_PREP) {
-    constexpr int RUN = PrepRun<P>::value;
-    const int run = RUN ? RUN : p.prep_run;
+    const int fm = p.prelifted ? FM_PRELIFTED : (p.omega_lo ? FM_HILO : FM_EXACT);
+    const int run_t = fm == FM_PRELIFTED ? PrepRun<P, FM_PRELIFTED>::value
+                    : fm == FM_HILO ? PrepRun<P, FM_HILO>::value : PrepRun<P, FM_EXACT>::value;
+    const int run = run_t ? run_t : p.prep_run;
     const dim3 prep_grid((unsigned)((p.nseg + run - 1) / run), (unsigned)p.H, (unsigned)p.B);
-    hipLaunchKernelGGL((prep_kernel<P, InT, D, DV>), prep_grid, dim3(256), 0, st, p);
+    if (fm == FM_PRELIFTED) hipLaunchKernelGGL((prep_kernel<P, InT, D, DV, FM_PRELIFTED>), prep_grid, dim3(256), 0, st, p);
+    else if (fm == FM_HILO) hipLaunchKernelGGL((prep_kernel<P, InT, D, DV, FM_HILO>), prep_grid, dim3(256), 0, st, p);
+    else hipLaunchKernelGGL((prep_kernel<P, InT, D, DV, FM_EXACT>), prep_grid, dim3(256), 0, st, p);
   } else if (phase == PHASE_STATE) {
     // The state workgroups are the sequential critical path: reserve enough LDS that no prep or output
     // workgroup can share their CU (a CU has 160 KB; the bf16 state kernel uses 88 KB statically).
@@ -1081,7 +1156,11 @@ static int validate(const kdn_scan_args* a) {
   if (a->B <= 0 || a->T <= 0 || a->H <= 0) return KDN_ERR_INVALID_ARGUMENT;
   if (a->B > 65535 || a->H > 65535) return KDN_ERR_UNSUPPORTED;
   if (!valid_dtype(a->in_dtype) || !valid_dtype(a->out_dtype)) return KDN_ERR_INVALID_ARGUMENT;
-  if (a->d_k != 64 || a->D != 512) return KDN_ERR_UNSUPPORTED;
+  if (a->feature_mode != 0 && a->feature_mode != 1) return KDN_ERR_INVALID_ARGUMENT;
+  if (a->rule != 0 && a->rule != 1) return KDN_ERR_INVALID_ARGUMENT;
+  if (a->D != 512) return KDN_ERR_UNSUPPORTED;
+  if (a->feature_mode == 0 ? a->d_k != 64 : a->d_k != a->D) return KDN_ERR_UNSUPPORTED;
+  if (a->omega_head_stride < 0 || a->phase_head_stride < 0) return KDN_ERR_INVALID_ARGUMENT;
   if (a->d_v != 16 && a->d_v != 32 && a->d_v != 64 && a->d_v != 128) return KDN_ERR_UNSUPPORTED;
   if (a->segment_chunks < 0) return KDN_ERR_INVALID_ARGUMENT;
   if (!(a->inv_tau == a->inv_tau)) return KDN_ERR_INVALID_ARGUMENT;
@@ -1092,13 +1171,16 @@ static int validate(const kdn_scan_args* a) {
 static int validate_launch(const kdn_scan_args* a) {
   int rc = validate(a);
   if (rc != KDN_OK) return rc;
-  if (!a->q || !a->k || !a->v || !a->beta || !a->omega_bf16 || !a->phase || !a->final_state || !a->y || !a->workspace)
-    return KDN_ERR_INVALID_ARGUMENT;
+  if (!a->q || !a->k || !a->v || !a->beta || !a->final_state || !a->y || !a->workspace) return KDN_ERR_INVALID_ARGUMENT;
+  if (a->feature_mode == 0 && (!a->omega_bf16 || !a->phase)) return KDN_ERR_INVALID_ARGUMENT;
+  if (a->feature_mode == 0 && ((a->omega_lo && !aligned(a->omega_lo, 16)) || (a->omega_head_stride % 8) != 0 ||
+                               (a->phase_head_stride % 4) != 0))
+    return KDN_ERR_MISALIGNED;
   // 16-byte row loads of q, k, v; 16-byte fragment traffic in the workspace.
   const size_t isz = dtype_size(a->in_dtype);
-  if (!aligned(a->q, 16) || !aligned(a->k, 16) || !aligned(a->v, 16) || !aligned(a->omega_bf16, 16) ||
-      !aligned(a->phase, 16) || !aligned(a->workspace, 256))
+  if (!aligned(a->q, 16) || !aligned(a->k, 16) || !aligned(a->v, 16) || !aligned(a->workspace, 256))
     return KDN_ERR_MISALIGNED;
+  if (a->feature_mode == 0 && (!aligned(a->omega_bf16, 16) || !aligned(a->phase, 16))) return KDN_ERR_MISALIGNED;
   const size_t osz = dtype_size(a->out_dtype);
   if (!aligned(a->y, 16)) return KDN_ERR_MISALIGNED;
   for (int i = 0; i < 3; ++i) {

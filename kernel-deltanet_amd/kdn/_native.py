@@ -57,6 +57,13 @@ class ScanArgs(ctypes.Structure):
         ("y", ctypes.c_void_p), ("y_stride", _i64x3),
         ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_size_t),
         ("segment_chunks", _i64),
+        ("omega_lo", ctypes.c_void_p),
+        ("omega_head_stride", _i64),
+        ("phase_head_stride", _i64),
+        ("inv_tau_head", ctypes.c_void_p),
+        ("no_renorm", ctypes.c_int),
+        ("feature_mode", ctypes.c_int),
+        ("rule", ctypes.c_int),
     ]
 
 

@@ -96,14 +96,61 @@ def _last_contig(t: torch.Tensor) -> torch.Tensor:
     return t if t.stride(-1) == 1 else t.contiguous()
 
 
+# Update rules (kdn_scan_args.rule): the gated delta rule, and gated linear attention (no erasure term).
+RULE_DELTA, RULE_LINEAR = 0, 1
+
+
+class FeatureMap:
+    """How the scan maps q, k to features (the feature-map fields of kdn_scan_args).
+
+    - lifted=False (default): phi = sqrt(2/D) cos(x Omega_h^T inv_tau_h + phase_h), renormalised unless
+      no_renorm.  Omega is `omega` (+ `omega_lo` when a bf16 Omega is not exact), either (D, d_k) shared
+      by every head or (H, D, d_k) per head; phase is (D,) or (H, D); inv_tau_head is an optional (H,)
+      float32 tensor overriding the scalar inv_tau.
+    - lifted=True: q and k already are the (B, T, H, D) features; Omega and the phases are unused.
+    """
+
+    def __init__(self, omega=None, phase=None, omega_lo=None, inv_tau_head=None, no_renorm=False,
+                 lifted=False):
+        self.omega, self.phase, self.omega_lo = omega, phase, omega_lo
+        self.inv_tau_head, self.no_renorm, self.lifted = inv_tau_head, bool(no_renorm), bool(lifted)
+
+    def dim(self, q: torch.Tensor) -> int:
+        return q.shape[-1] if self.lifted else self.omega.shape[-2]
+
+    def keep(self):
+        return (self.omega, self.phase, self.omega_lo, self.inv_tau_head)
+
+
+def _head_stride(t: Optional[torch.Tensor], ndim_shared: int) -> int:
+    return 0 if t is None or t.dim() == ndim_shared else t.stride(0)
+
+
+def _fill_features(a: N.ScanArgs, fm: FeatureMap) -> None:
+    a.feature_mode = 1 if fm.lifted else 0
+    a.no_renorm = 1 if fm.no_renorm else 0
+    if fm.lifted:
+        a.omega_bf16, a.phase, a.omega_lo = None, None, None
+        a.omega_head_stride = a.phase_head_stride = 0
+    else:
+        a.omega_bf16, a.phase = fm.omega.data_ptr(), fm.phase.data_ptr()
+        a.omega_lo = fm.omega_lo.data_ptr() if fm.omega_lo is not None else None
+        a.omega_head_stride = _head_stride(fm.omega, 2)
+        a.phase_head_stride = _head_stride(fm.phase, 1)
+    a.inv_tau_head = fm.inv_tau_head.data_ptr() if fm.inv_tau_head is not None else None
+
+
 def scan_args(q, k, v, beta, decay, omega_bf16, phase, inv_tau, normalize, initial_state, final_state, y,
-              workspace=None, segment_chunks: int = 0) -> N.ScanArgs:
-    """Fill struct kdn_scan_args from (B, T, H, .) views."""
+              workspace=None, segment_chunks: int = 0, features: Optional[FeatureMap] = None,
+              rule: int = RULE_DELTA) -> N.ScanArgs:
+    """Fill struct kdn_scan_args from (B, T, H, .) views.  `features` (if given) replaces
+    omega_bf16/phase; `rule` is RULE_DELTA or RULE_LINEAR."""
+    fm = features if features is not None else FeatureMap(omega_bf16, phase)
     B, T, H, d_k = q.shape
     d_v = v.shape[-1]
     a = N.ScanArgs()
     a.B, a.T, a.H = B, T, H
-    a.d_k, a.D, a.d_v = d_k, omega_bf16.shape[0], d_v
+    a.d_k, a.D, a.d_v = d_k, fm.dim(q), d_v
     a.in_dtype = _tag(q.dtype, "scan inputs")
     a.out_dtype = _tag(y.dtype, "scan output")
     a.normalize_input = 1 if normalize else 0
@@ -116,7 +163,7 @@ def scan_args(q, k, v, beta, decay, omega_bf16, phase, inv_tau, normalize, initi
         a.decay, a.decay_stride = decay.data_ptr(), N._i64x3(*decay.stride())
     else:
         a.decay, a.decay_stride = None, N._i64x3(0, 0, 0)
-    a.omega_bf16, a.phase = omega_bf16.data_ptr(), phase.data_ptr()
+    _fill_features(a, fm)
     if initial_state is not None:
         a.initial_state, a.init_stride = initial_state.data_ptr(), N._i64x4(*initial_state.stride())
     else:
@@ -124,6 +171,7 @@ def scan_args(q, k, v, beta, decay, omega_bf16, phase, inv_tau, normalize, initi
     a.final_state, a.final_stride = final_state.data_ptr(), N._i64x4(*final_state.stride())
     a.y, a.y_stride = y.data_ptr(), N._i64x3(*y.stride()[:3])
     a.segment_chunks = int(segment_chunks)
+    a.rule = int(rule)
     if workspace is not None:
         a.workspace, a.workspace_bytes = workspace.data_ptr(), workspace.numel() * workspace.element_size()
     else:
@@ -131,10 +179,13 @@ def scan_args(q, k, v, beta, decay, omega_bf16, phase, inv_tau, normalize, initi
     return a
 
 
-def scan_workspace_bytes(q, v, omega_bf16, segment_chunks: int = 0, pipelined: bool = False) -> int:
+def scan_workspace_bytes(q, v, omega_bf16, segment_chunks: int = 0, pipelined: bool = False,
+                         features: Optional[FeatureMap] = None) -> int:
     B, T, H, d_k = q.shape
     a = N.ScanArgs()
-    a.B, a.T, a.H, a.d_k, a.D, a.d_v = B, T, H, d_k, omega_bf16.shape[0], v.shape[-1]
+    D = features.dim(q) if features is not None else omega_bf16.shape[-2]
+    a.B, a.T, a.H, a.d_k, a.D, a.d_v = B, T, H, d_k, D, v.shape[-1]
+    a.feature_mode = 1 if (features is not None and features.lifted) else 0
     a.in_dtype = _tag(q.dtype, "scan inputs")
     a.out_dtype = a.in_dtype
     a.inv_tau = 1.0
@@ -177,13 +228,16 @@ def scan(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, beta: torch.Tensor, 
          initial_state: Optional[torch.Tensor] = None, final_state: Optional[torch.Tensor] = None,
          y: Optional[torch.Tensor] = None, out_dtype: Optional[torch.dtype] = None,
          workspace: Optional[torch.Tensor] = None, segment_chunks: int = 0,
-         pipelined: bool = True) -> Tuple[torch.Tensor, torch.Tensor]:
+         pipelined: bool = True, features: Optional[FeatureMap] = None,
+         rule: int = RULE_DELTA) -> Tuple[torch.Tensor, torch.Tensor]:
     """Chunked delta-rule prefill over (B, T, H, d) views (kdn_delta_scan_fwd_pipelined, or
     kdn_delta_scan_fwd with pipelined=False).
 
     q, k (B, T, H, d_k) and v (B, T, H, d_v) share a dtype; beta, decay (B, T, H) are float32 (decay may
     be None for lambda = 1); initial_state/final_state are (B, H, D, d_v) float32 views with any strides.
-    Returns (y (B, T, H, d_v), final_state).
+    `features` selects another feature map (per-head or hi + lo Omega, no renormalisation, pre-lifted
+    q, k); omega_bf16/phase are then ignored.  rule=RULE_LINEAR drops the erasure term
+    (S_t = lambda_t S_{t-1} + beta_t v_t phi_k^T).  Returns (y (B, T, H, d_v), final_state).
     """
     for t, nm in ((q, "q"), (k, "k"), (v, "v"), (beta, "beta")):
         require_device(t, nm)
@@ -199,7 +253,10 @@ def scan(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, beta: torch.Tensor, 
             raise ValueError("scan: decay must have the shape of beta")
         decay = decay.to(device=dev, dtype=torch.float32)
     B, T, H, _ = q.shape
-    D = omega_bf16.shape[0]
+    if features is None:
+        features = FeatureMap(omega_bf16, phase)
+    features = _features_on(features, dev, H)
+    D = features.dim(q)
     d_v = v.shape[-1]
     if initial_state is not None:
         if tuple(initial_state.shape) != (B, H, D, d_v):
@@ -209,18 +266,46 @@ def scan(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, beta: torch.Tensor, 
         final_state = torch.empty(B, H, D, d_v, device=dev, dtype=torch.float32)
     if y is None:
         y = torch.empty(B, T, H, d_v, device=dev, dtype=q.dtype if out_dtype is None else out_dtype)
-    om = omega_bf16.to(dev).contiguous()
-    ph = phase.to(device=dev, dtype=torch.float32).contiguous()
     if workspace is None:
-        nbytes = scan_workspace_bytes(q, v, om, segment_chunks, pipelined)
+        nbytes = scan_workspace_bytes(q, v, None, segment_chunks, pipelined, features)
         if nbytes == 0:
             raise ValueError("scan: unsupported shape (kdn_scan_workspace_bytes returned 0)")
         workspace = torch.empty(nbytes, dtype=torch.uint8, device=dev)
-    a = scan_args(q, k, v, beta, decay, om, ph, inv_tau, normalize, initial_state, final_state, y,
-                  workspace, segment_chunks)
+    a = scan_args(q, k, v, beta, decay, None, None, inv_tau, normalize, initial_state, final_state, y,
+                  workspace, segment_chunks, features, rule)
     with torch.cuda.device(dev):
-        _launch_scan(a, dev, pipelined, (q, k, v, beta, decay, om, ph, initial_state, final_state, y, workspace))
+        _launch_scan(a, dev, pipelined, (q, k, v, beta, decay, initial_state, final_state, y, workspace)
+                     + features.keep())
     return y, final_state
+
+
+def _features_on(fm: FeatureMap, dev: torch.device, H: int) -> FeatureMap:
+    """The feature map with its tensors on `dev` in the layouts the library reads (bf16 Omega rows
+    and float32 phases / 1/tau, innermost dimension contiguous), shapes checked."""
+    if fm.lifted:
+        return FeatureMap(inv_tau_head=None, lifted=True)
+
+    def per_head(t, ndim, what):
+        if t.dim() == ndim + 1 and t.shape[0] != H:
+            raise ValueError(f"scan: per-head {what} must have H = {H} rows, got {tuple(t.shape)}")
+        if t.dim() not in (ndim, ndim + 1):
+            raise ValueError(f"scan: {what} has shape {tuple(t.shape)}")
+
+    for t, nm in ((fm.omega, "omega"), (fm.omega_lo, "omega_lo")):
+        if t is not None:
+            per_head(t, 2, nm)
+            if t.dtype != torch.bfloat16:
+                raise TypeError(f"scan: {nm} must be bfloat16")
+    per_head(fm.phase, 1, "phase")
+    if fm.omega_lo is not None and fm.omega_lo.shape != fm.omega.shape:
+        raise ValueError("scan: omega_lo must have the shape of omega")
+    itau = fm.inv_tau_head
+    if itau is not None and tuple(itau.shape) != (H,):
+        raise ValueError(f"scan: inv_tau_head must be ({H},)")
+    return FeatureMap(fm.omega.to(dev).contiguous(), fm.phase.to(device=dev, dtype=torch.float32).contiguous(),
+                      None if fm.omega_lo is None else fm.omega_lo.to(dev).contiguous(),
+                      None if itau is None else itau.to(device=dev, dtype=torch.float32).contiguous(),
+                      fm.no_renorm, False)
 
 
 class ScanPlan:
@@ -288,3 +373,27 @@ class ScanPlan:
         a = self.args if args is None else args
         st = self._stream() if stream is None else ctypes.c_void_p(stream.cuda_stream)
         N.check(getattr(N.lib(), name)(ctypes.byref(a), chunk0, nchunks, st), name)
+
+
+
+class _ForwardOnly(torch.autograd.Function):
+    """Identity on the scan outputs that ties them to the inputs' autograd graph; its backward raises,
+    so a training step fails loudly instead of computing gradients that skip the scan."""
+
+    @staticmethod
+    def forward(ctx, what, n_out, *tensors):
+        ctx.what = what
+        return tuple(t.view_as(t) for t in tensors[:n_out])
+
+    @staticmethod
+    def backward(ctx, *grads):
+        raise NotImplementedError(f"{ctx.what}: the backward pass of the scan is not implemented on MI355X "
+                                  "(forward/prefill only)")
+
+
+def forward_only(what: str, outputs, inputs):
+    """`outputs` unchanged when no input needs a gradient; otherwise views of them whose backward raises."""
+    if not torch.is_grad_enabled() or not any(isinstance(t, torch.Tensor) and t.requires_grad for t in inputs):
+        return tuple(outputs)
+    grads = [t for t in inputs if isinstance(t, torch.Tensor) and t.requires_grad]
+    return _ForwardOnly.apply(what, len(outputs), *outputs, *grads)

@@ -5,6 +5,8 @@ names on the prefill path; every call runs HIP kernels from libkdn.so.
 """
 from .fwht import FastWalshHadamardProjection, fast_walsh_hadamard_transform
 from .fused_kernel_deltanet import FusedKernelDeltaNet, FusedKernelDeltaNetFunction, fused_chunked_deltanet_forward
+from .fused_triton_engine import fused_triton_chunk_scan
+from .tiled_triton_engine import streaming_triton_chunk_scan, tiled_triton_chunk_scan
 
 __all__ = [
     "FastWalshHadamardProjection",
@@ -12,4 +14,7 @@ __all__ = [
     "fused_chunked_deltanet_forward",
     "FusedKernelDeltaNet",
     "FusedKernelDeltaNetFunction",
+    "fused_triton_chunk_scan",
+    "tiled_triton_chunk_scan",
+    "streaming_triton_chunk_scan",
 ]

@@ -23,4 +23,12 @@ How each function is pinned (see tests/test_oracle_*.py):
                     overwrite closed forms, contractivity.
   chunked_forward   equals token_recurrence to 1e-12 in float64 for every chunk size, with and without
                     decay and initial state; reference carry-algebra pin (tests/test_inter_woodbury.py:14-84).
+  rff_features      with renorm and the seed-42 projection equals lift (pinned above); closed form at x = 0.
+  rkhs_features     ||phi|| = 1 exactly; phi(x).phi(y) = mean cos(sqrt(2 gamma) Omega (x - y)) (the
+                    cos/sin pairing); gamma scaling at x and sqrt(gamma) x.
+  linear_recurrence explicit double sum y_t = sum_{j<t} beta_j (prod lambda) (phi_q(t).phi_k(j)) v_j;
+                    equals token_recurrence when the keys are mutually orthogonal (the erasure term
+                    S_{t-1} phi_k(t) then vanishes), and differs from it otherwise.
+  linear_chunked    equals linear_recurrence to 1e-12 for several chunk sizes and ragged T (the reference's
+                    own acceptance check, tests/test_parallel_vs_recurrent.py:19-51).
 """

@@ -4,6 +4,9 @@ Follows the reference file kernels/fwht.py (jatin-yadav-acad/kernel-deltanet):
   make_projection  <- FastWalshHadamardProjection.__init__, kernels/fwht.py:54-111
   fwht_rows        <- fast_walsh_hadamard_transform,       kernels/fwht.py:25-45
   lift             <- FastWalshHadamardProjection.forward,  kernels/fwht.py:122-131 (torch branch)
+  rff_features     <- the per-head random-feature lift of the P2 module, kernels/kernel_deltanet_fused.py:85-92,
+                      113-117 and 286-287 (spherical normalisation, Omega (H, D, d_k), phases (H, D), tau (H,))
+  rkhs_features    <- MultiHeadRKHSKernel.forward, core/rkhs_features.py:107-131 ([cos, sin] / sqrt(m))
 """
 from __future__ import annotations
 
@@ -127,3 +130,39 @@ def lift(x: np.ndarray, proj: dict, normalize: bool = False) -> np.ndarray:
     scaled = proj_ / proj["tau_star"] + proj["b"].astype(np.float64)
     phi = math.sqrt(2.0 / proj["D"]) * np.cos(scaled)
     return phi / (np.linalg.norm(phi, axis=-1, keepdims=True) + 1e-8)
+
+
+def rff_features(x: np.ndarray, omega: np.ndarray, phase: np.ndarray, tau, normalize: bool = True,
+                 renorm: bool = False) -> np.ndarray:
+    """phi = sqrt(2/D) cos(x_hat Omega_h^T / tau_h + b_h), per head; float64.
+
+    x (B, H, T, d_k); omega (H, D, d_k); phase (H, D); tau (H,) or a scalar.  `normalize` applies
+    F.normalize (eps 1e-6) to x (kernels/kernel_deltanet_fused.py:90-91, 286-287); the P2 module does not
+    renormalise phi (`renorm` adds the division by ||phi|| + 1e-8 of kernels/fwht.py:131).
+    """
+    xx = np.asarray(x, dtype=np.float64)
+    if normalize:
+        xx = normalize_rows(xx)
+    om = np.asarray(omega, dtype=np.float64)
+    H, D, _ = om.shape
+    tt = np.broadcast_to(np.asarray(tau, dtype=np.float64).reshape(-1), (H,))
+    ang = np.einsum("bhtd,hfd->bhtf", xx, om) / tt[None, :, None, None] \
+        + np.asarray(phase, dtype=np.float64)[None, :, None, :]
+    phi = math.sqrt(2.0 / D) * np.cos(ang)
+    if renorm:
+        phi = phi / (np.linalg.norm(phi, axis=-1, keepdims=True) + 1e-8)
+    return phi
+
+
+def rkhs_features(x: np.ndarray, omega: np.ndarray, log_gamma: np.ndarray) -> np.ndarray:
+    """MultiHeadRKHSKernel.forward (core/rkhs_features.py:107-131) in float64.
+
+    x (B, H, T, d_head); omega (H, m, d_head); log_gamma (H,).  Returns (B, H, T, 2m):
+    [cos(sqrt(2 gamma_h) x Omega_h^T), sin(same)] / sqrt(m).
+    """
+    xx = np.asarray(x, dtype=np.float64)
+    om = np.asarray(omega, dtype=np.float64)
+    m = om.shape[1]
+    gamma = np.exp(np.asarray(log_gamma, dtype=np.float64))
+    ang = np.einsum("bhtd,hmd->bhtm", xx, om) * np.sqrt(2.0 * gamma)[None, :, None, None]
+    return np.concatenate([np.cos(ang), np.sin(ang)], axis=-1) / math.sqrt(m)

@@ -5,6 +5,9 @@
   chunked_forward   <- fused_chunked_deltanet_forward, kernels/fused_kernel_deltanet.py:47-155, op for op
                        (torch on the CPU, compute dtype selectable, state carried in the compute dtype)
   delta_rule        <- lift (oracle.lift) followed by token_recurrence, float64: the parity definition.
+  linear_recurrence <- recurrent_step of the P4 layer, core/chunked_scan.py:145-186 (no erasure term):
+                       y_t = S_{t-1} phi_q(t);  S_t = lambda_t S_{t-1} + beta_t v_t phi_k(t)^T
+  linear_chunked    <- chunked_affine_scan, core/chunked_scan.py:48-143 (per-head constant lambda, eta)
 """
 from __future__ import annotations
 
@@ -136,3 +139,60 @@ def chunked_forward(q, k, v, beta, decay, proj: dict, chunk_size: int = 64,
         S = g0C * (S - torch.matmul(S_K_W, pk)) + delta_S
     Yo = Y.view(B, T_pad, d_v)[:, :T]
     return Yo, S
+
+
+def linear_recurrence(phi_q, phi_k, v, beta, decay=None, S0=None) -> Tuple[np.ndarray, np.ndarray]:
+    """y_t = S_{t-1} phi_q(t);  S_t = lambda_t S_{t-1} + beta_t v_t phi_k(t)^T  (float64).
+
+    The recurrent step of core/chunked_scan.py:145-186 with eta -> beta_t and decay -> lambda_t, batched
+    over B.  Shapes as token_recurrence.
+    """
+    pq = np.asarray(phi_q, dtype=np.float64)
+    pk = np.asarray(phi_k, dtype=np.float64)
+    vv = np.asarray(v, dtype=np.float64)
+    bb = np.asarray(beta, dtype=np.float64)
+    B, T, D = pk.shape
+    dv = vv.shape[-1]
+    ll = np.ones((B, T)) if decay is None else np.asarray(decay, dtype=np.float64)
+    S = np.zeros((B, dv, D)) if S0 is None else np.array(S0, dtype=np.float64, copy=True)
+    Y = np.zeros((B, T, dv))
+    for t in range(T):
+        Y[:, t] = np.einsum("bvd,bd->bv", S, pq[:, t])
+        S = ll[:, t, None, None] * S + bb[:, t, None, None] * vv[:, t, :, None] * pk[:, t, None, :]
+    return Y, S
+
+
+def linear_chunked(phi_q, phi_k, v, decay, eta, chunk_size: int = 64) -> np.ndarray:
+    """chunked_affine_scan (core/chunked_scan.py:48-143) in float64: per-head constant lambda and eta.
+
+    phi_q, phi_k (B, H, T, D); v (B, H, T, d_v); decay, eta (H,).  Returns y (B, H, T, d_v).  Intra-chunk
+    weights eta lambda^{i-1-j} [i > j] on the q-k Gram, chunk states sum_j lambda^{C-1-j} v_j phi_j^T,
+    carried as S <- lambda^C S + eta dS, inter-chunk readout lambda^i (S phi_q).
+    """
+    pq = np.asarray(phi_q, dtype=np.float64)
+    pk = np.asarray(phi_k, dtype=np.float64)
+    vv = np.asarray(v, dtype=np.float64)
+    B, H, T, D = pk.shape
+    dv = vv.shape[-1]
+    lam = np.asarray(decay, dtype=np.float64).reshape(H)
+    eta = np.asarray(eta, dtype=np.float64).reshape(H)
+    C = chunk_size
+    pad = (-T) % C
+    if pad:
+        z = lambda a: np.concatenate([a, np.zeros(a.shape[:2] + (pad, a.shape[-1]))], axis=2)
+        pq, pk, vv = z(pq), z(pk), z(vv)
+    n = (T + pad) // C
+    pqc, pkc, vc = (a.reshape(B, H, n, C, a.shape[-1]) for a in (pq, pk, vv))
+    i = np.arange(C)[:, None]
+    j = np.arange(C)[None, :]
+    powd = np.clip(i - 1 - j, 0, None)
+    w = eta[:, None, None] * lam[:, None, None] ** powd[None] * (i > j)[None]   # (H, C, C)
+    y_intra = np.einsum("bhnij,hij,bhnjv->bhniv", np.einsum("bhnid,bhnjd->bhnij", pqc, pkc), w, vc)
+    tok = lam[:, None] ** (C - 1 - np.arange(C))[None]                           # (H, C)
+    dS = np.einsum("bhnjv,hj,bhnjd->bhnvd", vc, tok, pkc)
+    S = np.zeros((B, H, dv, D))
+    y = np.zeros((B, H, n, C, dv))
+    for c in range(n):
+        y[:, :, c] = np.einsum("bhid,bhvd->bhiv", pqc[:, :, c], S) * (lam[:, None] ** np.arange(C))[None, :, :, None]
+        S = lam[None, :, None, None] ** C * S + eta[None, :, None, None] * dS[:, :, c]
+    return (y + y_intra).reshape(B, H, n * C, dv)[:, :, :T]

@@ -60,7 +60,7 @@ def test_scan_args_layout_matches_c():
 def test_strerror_and_version(lib):
     for code in (0, -1, -2, -3, -4, -5, -99):
         assert len(lib.kdn_strerror(code)) > 0
-    assert lib.kdn_abi_version() == (1 << 16)
+    assert lib.kdn_abi_version() == (1 << 16) | 1
 
 
 def _args(**kw):
