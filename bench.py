@@ -84,23 +84,39 @@ def cpu_baseline(q, k, v, beta, T_sample: int) -> dict:
                       f"{T_sample} tokens of the same B={B}, H={H} inputs; {dt:.2f} s"}
 
 
+def synthetic_inputs(B: int, T: int, H: int, dv: int, dev) -> tuple:
+    """q, k, v ~ N(0,1) (bf16) and beta = sigmoid(N(0,1)) (fp32) from one generator seeded 1234, drawn in
+    that order; on the host for up to 2^24 head-tokens, on the device beyond (config 4)."""
+    big = B * T * H > (1 << 24)
+    where = dev if big else "cpu"
+    g = torch.Generator(device=where).manual_seed(1234)
+    q = torch.randn(B, T, H, 64, generator=g, device=where).to(torch.bfloat16)
+    k = torch.randn(B, T, H, 64, generator=g, device=where).to(torch.bfloat16)
+    v = torch.randn(B, T, H, dv, generator=g, device=where).to(torch.bfloat16)
+    beta = torch.sigmoid(torch.randn(B, T, H, generator=g, device=where))
+    return q, k, v, beta
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--B", type=int, default=1)
+    ap.add_argument("--config", type=int, default=3, choices=(2, 3, 4),
+                    help="3: one layer B=1 H=16 T=64k (default, the headline); 4: B=32 streams (use --T for "
+                         "the sweep 4096/16384/65536); 2: the standalone lift of 2,097,152 rows")
+    ap.add_argument("--B", type=int, default=None)
     ap.add_argument("--H", type=int, default=16)
-    ap.add_argument("--T", type=int, default=65536)
+    ap.add_argument("--T", type=int, default=None)
     ap.add_argument("--dv", type=int, default=64)
     ap.add_argument("--segment-chunks", type=int, default=0,
-                    help="64-token chunks per segment (0 = 64 when pipelined, all chunks when --serial)")
+                    help="chunks per segment (0 = the library default)")
     ap.add_argument("--serial", action="store_true",
-                    help="run prep, state and output of each segment back to back on one stream")
+                    help="serial schedule (kdn_delta_scan_fwd) instead of the pipelined one")
     ap.add_argument("--cpu-tokens", type=int, default=65536, help="tokens in the CPU-baseline sample (0 = skip)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain device copy of known size (for PMC byte-counter calibration)")
-    ap.add_argument("--pmc", default=os.path.join(REPO, "profiles", "pmc_config3.txt"))
+    ap.add_argument("--pmc", default=None)
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -118,16 +134,20 @@ def main():
         torch.cuda.synchronize()
         print(json.dumps({"copy_calibration_bytes_per_dispatch_each_way": n}), flush=True)
         return
+    if args.config == 2:
+        return bench_lift(args, dev)
+    return bench_scan(args, dev)
 
+
+def bench_scan(args, dev):
     from kdn import ops
     from kernels import FastWalshHadamardProjection
 
-    B, H, T, dv, D = args.B, args.H, args.T, args.dv, 512
-    g = torch.Generator().manual_seed(1234)
-    q = torch.randn(B, T, H, 64, generator=g).to(torch.bfloat16)
-    k = torch.randn(B, T, H, 64, generator=g).to(torch.bfloat16)
-    v = torch.randn(B, T, H, dv, generator=g).to(torch.bfloat16)
-    beta = torch.sigmoid(torch.randn(B, T, H, generator=g))
+    cfg = args.config
+    B = args.B if args.B is not None else (32 if cfg == 4 else 1)
+    T = args.T if args.T is not None else 65536
+    H, dv, D = args.H, args.dv, 512
+    q, k, v, beta = synthetic_inputs(B, T, H, dv, dev)
     proj = FastWalshHadamardProjection(64, D, 42)
     qd, kd, vd, bd = q.to(dev), k.to(dev), v.to(dev), beta.to(dev)
     plan = ops.ScanPlan(qd, kd, vd, bd, None, proj.device_omega(dev), proj.device_phase(dev), proj.tau_star_inv,
@@ -188,7 +208,6 @@ def main():
     torch.cuda.synchronize()
     ms_kernel = {k: sum(x.elapsed_time(y) for x, y in v) / args.steps for k, v in timed.items()}
     launches = {k: len(v) / args.steps for k, v in timed.items()}
-    ms_prep, ms_state, ms_out = ms_kernel["prep"], ms_kernel["state"], ms_kernel["output"]
 
     fl = flops_per_chunk(D, dv)
     units = B * H * nchunks
@@ -198,7 +217,8 @@ def main():
               for k in ("prep", "state", "output")}
     dom = max(phases, key=lambda p: phases[p]["ms"])
     achieved = phases[dom]["tflops"]
-    pmc = read_pmc(args.pmc)
+    pmc_path = args.pmc or os.path.join(REPO, "profiles", f"pmc_config{cfg}.txt")
+    pmc = read_pmc(pmc_path) if (cfg == 3 and B == 1 and T == 65536 and H == 16 and dv == 64) or args.pmc else {}
     traffic = None
     if f"{dom}_fetch_kib" in pmc and f"{dom}_write_kib" in pmc and "copy_fetch_kib" in pmc and "copy_write_kib" in pmc:
         copy_bytes = pmc.get("copy_bytes", 256 << 20)
@@ -206,6 +226,8 @@ def main():
         w_fac = copy_bytes / (pmc["copy_write_kib"] * 1024.0)
         traffic = pmc[f"{dom}_fetch_kib"] * 1024.0 * f_fac + pmc[f"{dom}_write_kib"] * 1024.0 * w_fac
     path_flops = fl["total"] * units
+    name = ("config3: one Kernel-DeltaNet layer prefill" if cfg == 3 else
+            "config4: batched long-context prefill (concurrent streams)")
     out = {
         "metric": "prefill tokens/s + ms/layer at T=64k, D=512 on 1 GPU; % of MFMA/HBM roofline",
         "value": tokens / (ms_per_step / 1e3),
@@ -219,7 +241,7 @@ def main():
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic (seeded N(0,1) q/k/v, sigmoid(N(0,1)) beta; projection seed 42)",
-        "config": {"workload": f"config3: one Kernel-DeltaNet layer prefill, B={B}, H={H}, T={T}, d_k=64->D={D}, "
+        "config": {"workload": f"{name}, B={B}, H={H}, T={T}, d_k=64->D={D}, "
                                f"d_v={dv}, chunk 64, bf16 q/k/v, fp32 beta and state, lambda=1",
                    "B": B, "H": H, "T": T, "D": D, "d_v": dv, "chunk": C, "segment_chunks": seg,
                    "schedule": "pipelined (state chain on the launch stream, prep/output on an auxiliary stream)"
@@ -232,7 +254,63 @@ def main():
                  "mfma_frac": path_flops / (ms_per_step / 1e3) / MFMA_BF16_PEAK},
     }
     if args.cpu_tokens > 0:
-        out["cpu_baseline"] = cpu_baseline(q, k, v, beta, min(args.cpu_tokens, T))
+        Ts = min(args.cpu_tokens, T)
+        Bs = 1 if cfg == 4 else B
+        out["cpu_baseline"] = cpu_baseline(q[:Bs, :Ts].cpu(), k[:Bs, :Ts].cpu(), v[:Bs, :Ts].cpu(),
+                                           beta[:Bs, :Ts].cpu(), Ts)
+    else:
+        out["cpu_baseline"] = None
+    print(json.dumps(out), flush=True)
+
+
+def bench_lift(args, dev):
+    """Config 2: the standalone lift (kdn_fwht_lift) of x [B*T*H, 64] bf16 ~ N(0,1), B=8, T=16384, H=16,
+    L2-normalised per row, to D=512 bf16.  HBM-bound: algorithmic bytes = rows * (64 + 512) * 2."""
+    from kdn import ops
+    from kernels import FastWalshHadamardProjection
+
+    B = args.B if args.B is not None else 8
+    T = args.T if args.T is not None else 16384
+    rows, D = B * T * args.H, 512
+    g = torch.Generator(device=dev).manual_seed(1234)
+    x = torch.randn(rows, 64, generator=g, device=dev).to(torch.bfloat16)
+    proj = FastWalshHadamardProjection(64, D, 42)
+    om, ph = proj.device_omega(dev), proj.device_phase(dev)
+    stream = torch.cuda.current_stream(dev)
+    for _ in range(args.warmup):
+        y = ops.lift(x, om, ph, proj.tau_star_inv, normalize=True)
+    torch.cuda.synchronize()
+    evs = []
+    for _ in range(args.steps):
+        a0, a1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a0.record(stream)
+        y = ops.lift(x, om, ph, proj.tau_star_inv, normalize=True)
+        a1.record(stream)
+        evs.append((a0, a1))
+    torch.cuda.synchronize()
+    ms = sorted(a.elapsed_time(b) for a, b in evs)[len(evs) // 2]
+    alg_bytes = rows * (64 + D) * 2
+    achieved = alg_bytes / (ms / 1e3) / 1e9
+    out = {
+        "metric": "standalone lift rows/s (config 2); % of HBM roofline",
+        "value": rows / (ms / 1e3), "unit": "rows/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) x; projection seed 42)",
+        "config": {"workload": f"config2: standalone lift, x [{rows}, 64] bf16 L2-normalised -> [{rows}, 512] bf16 "
+                               f"(B={B}, T={T}, H={args.H})", "rows": rows, "D": D, "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+                     "frac": achieved * 1e9 / HBM_PEAK, "traffic": None, "kernel": "lift"},
+    }
+    if args.cpu_tokens > 0:
+        from oracle import lift as ol
+        n = min(args.cpu_tokens * 4, rows)
+        xs = x[:n].float().cpu().numpy()
+        op = ol.make_projection(64, D, 42)
+        t0 = time.perf_counter()
+        ol.lift(xs, op, normalize=True)
+        dt = time.perf_counter() - t0
+        out["cpu_baseline"] = {"value": n / dt, "unit": "rows/s", "cores": 1, "kind": "port",
+                               "sample": f"oracle float64 lift (numpy) of the first {n} rows; {dt:.2f} s"}
     else:
         out["cpu_baseline"] = None
     print(json.dumps(out), flush=True)

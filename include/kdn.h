@@ -74,7 +74,8 @@ int kdn_fwht(const void* x, int64_t rows, int64_t x_row_stride, int n, int dtype
  * omega is the bf16 [D][d_k] table from kdn_build_omega (exact in bf16); phase is fp32 [D].
  * Products are exact (bf16 operands; fp32 inputs are split into three bf16 parts), sums in fp32.
  * Replaces kernels/fwht_cuda.cpp:29-32 with the semantics of kernels/fwht.py:122-131.
- * d_k must be 64; D in {128, 256, 512}. */
+ * d_k must be 64; D in {128, 256, 512}.  x, out, omega and phase 16-byte aligned; row strides in bytes
+ * multiples of 16. */
 int kdn_fwht_lift(const void* x, int64_t rows, int64_t x_row_stride, int x_dtype, int normalize_input,
                   const void* omega_bf16, const float* phase, int d_k, int D, float inv_tau,
                   void* out, int64_t out_row_stride, int out_dtype, void* stream);

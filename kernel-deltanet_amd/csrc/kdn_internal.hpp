@@ -20,4 +20,14 @@ inline bool valid_dtype(int dt) { return dt == KDN_DTYPE_F32 || dt == KDN_DTYPE_
 
 inline size_t dtype_size(int dt) { return dt == KDN_DTYPE_F32 ? 4 : 2; }
 
+// Compute units of the current device (0 if it cannot be queried).
+inline int device_cus() {
+  int dev = 0, n = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+  return n;
+}
+
+constexpr size_t CU_LDS_BYTES = 160 * 1024;  // LDS per CU on gfx950
+
 }  // namespace kdn

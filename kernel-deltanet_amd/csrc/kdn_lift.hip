@@ -85,6 +85,10 @@ __global__ void __launch_bounds__(256) lift_kernel(const InT* __restrict__ x, in
   constexpr int NSPLIT = XFrag<InT>::NSPLIT;
   __shared__ bf16x8 s_omega[NT * 2 * 64];    // [t][kb][lane] A fragments, D*64*2 bytes
   __shared__ __attribute__((aligned(16))) float s_phase_rev[D];           // phase / (2 pi)
+  // Per-wave staging of 16 rows x 64 features of output, rows padded by 16 bytes.
+  constexpr int SRS = 64 * (int)sizeof(OutT) + 16;  // row stride in bytes
+  constexpr int SCPR = 64 * (int)sizeof(OutT) / 16;  // 16-byte chunks per staged row
+  __shared__ __attribute__((aligned(16))) unsigned char s_stage[4][16 * SRS];
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -101,18 +105,38 @@ __global__ void __launch_bounds__(256) lift_kernel(const InT* __restrict__ x, in
   const float amp = sqrtf(2.0f / (float)D);
   const int64_t ntiles = (rows + 15) / 16;
 
-  for (int64_t tile = (int64_t)blockIdx.x * 4 + wave; tile < ntiles; tile += (int64_t)gridDim.x * 4) {
+  // The x fragments of the wave's next tile are loaded while the current one is processed.  The row
+  // index is clamped to the last row, so every load is unconditional and in bounds; rows past the end
+  // are zeroed after the load and never stored.
+  constexpr int PIECES = 2 * (int)sizeof(InT) / 2;  // 16-byte pieces per lane: 8 elements per depth block
+  const int64_t stride = (int64_t)gridDim.x * 4;
+  auto load_tile = [&](int64_t t, u32x4 (&raw)[PIECES]) {
+    int64_t row = t * 16 + (lane & 15);
+    row = row < rows ? row : rows - 1;
+    const unsigned char* src = reinterpret_cast<const unsigned char*>(x + row * xs) + 8 * (lane >> 4) * sizeof(InT);
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int pc = 0; pc < PIECES / 2; ++pc)
+        raw[kb * (PIECES / 2) + pc] = *reinterpret_cast<const u32x4*>(src + 32 * kb * sizeof(InT) + 16 * pc);
+  };
+  u32x4 nraw[PIECES];
+  int64_t tile = (int64_t)blockIdx.x * 4 + wave;
+  if (tile < ntiles) load_tile(tile, nraw);
+  for (; tile < ntiles; tile += stride) {
     const int64_t row = tile * 16 + (lane & 15);
     const bool valid = row < rows;
+    u32x4 raw[PIECES];
+#pragma unroll
+    for (int i = 0; i < PIECES; ++i) raw[i] = nraw[i];
+    load_tile(tile + stride < ntiles ? tile + stride : tile, nraw);
     // x fragments for depth blocks kb = 0, 1: slots k = 32kb + 8(l>>4) + s.
     float xv[2][8];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
-      if (valid) load8<InT>(x + row * xs + 32 * kb + 8 * (lane >> 4), xv[kb]);
-      else {
+      load8<InT>(reinterpret_cast<const InT*>(&raw[kb * (PIECES / 2)]), xv[kb]);
 #pragma unroll
-        for (int s = 0; s < 8; ++s) xv[kb][s] = 0.f;
-      }
+      for (int s = 0; s < 8; ++s) xv[kb][s] = valid ? xv[kb][s] : 0.f;
     }
     if (normalize) {
       float ss = 0.f;
@@ -134,10 +158,9 @@ __global__ void __launch_bounds__(256) lift_kernel(const InT* __restrict__ x, in
     split_frag<NSPLIT>(xv[0], xb[0]);
     split_frag<NSPLIT>(xv[1], xb[1]);
 
-    float c[NT][4];
-    float ss = 0.f;
-#pragma unroll
-    for (int t = 0; t < NT; ++t) {
+    // Feature tile t: acc = x . Omega[16t .. 16t+16)^T.  Software-pipelined: the MFMAs of tile t+1 are
+    // issued in the same scheduling region as the cosines of tile t.
+    auto project = [&](int t) {
       f32x4 acc = zero4();
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
@@ -145,6 +168,17 @@ __global__ void __launch_bounds__(256) lift_kernel(const InT* __restrict__ x, in
 #pragma unroll
         for (int p = 0; p < NSPLIT; ++p) acc = PrecBF16::mma(acc, a, xb[kb][p]);
       }
+      return acc;
+    };
+    float c[NT][4];
+    float ss = 0.f;
+    f32x4 acc = project(0);
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      // one feature tile per scheduling region: hoisting the Omega reads of every tile to the top
+      // would need 256 registers for them alone
+      __builtin_amdgcn_sched_barrier(0);
+      const f32x4 next = (t + 1 < NT) ? project(t + 1) : zero4();
       const f32x4 ph = *reinterpret_cast<const f32x4*>(&s_phase_rev[16 * t + 4 * (lane >> 4)]);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -152,16 +186,28 @@ __global__ void __launch_bounds__(256) lift_kernel(const InT* __restrict__ x, in
         c[t][i] = cv;
         ss += cv * cv;
       }
+      acc = next;
     }
     ss = sum_over_lane_groups(ss);
     // phi = amp * c ; out = phi / (||phi|| + 1e-8)
     const float scale = amp / (amp * sqrtf(ss) + 1e-8f);
-    if (valid) {
-      OutT* o = out + row * os + 4 * (lane >> 4);
+    // Store 64 features of the 16 rows at a time through the wave's staging tile, so that every lane
+    // writes 16 contiguous bytes and each store instruction covers whole 128-byte lines of rows.
+    unsigned char* stg = s_stage[wave];
 #pragma unroll
-      for (int t = 0; t < NT; ++t) {
+    for (int g = 0; g < NT / 4; ++g) {
+#pragma unroll
+      for (int tp = 0; tp < 4; ++tp) {
+        const int t = 4 * g + tp;
         float v[4] = {c[t][0] * scale, c[t][1] * scale, c[t][2] * scale, c[t][3] * scale};
-        store4<OutT>(o + 16 * t, v);
+        store4<OutT>(reinterpret_cast<OutT*>(stg + (lane & 15) * SRS) + 16 * tp + 4 * (lane >> 4), v);
+      }
+#pragma unroll
+      for (int j = 0; j < 16 * SCPR / 64; ++j) {
+        const int q = 64 * j + lane, r = q / SCPR, ch = q % SCPR;
+        const u32x4 val = *reinterpret_cast<const u32x4*>(stg + r * SRS + 16 * ch);
+        const int64_t grow = tile * 16 + r;
+        if (grow < rows) *reinterpret_cast<u32x4*>(reinterpret_cast<unsigned char*>(out + grow * os + 64 * g) + 16 * ch) = val;
       }
     }
   }
@@ -172,7 +218,11 @@ static void launch_lift(const void* x, int64_t rows, int64_t xs, int normalize, 
                         float inv_tau, void* out, int64_t os, hipStream_t st) {
   const int64_t ntiles = (rows + 15) / 16;
   int64_t wgs = (ntiles + 3) / 4;
-  const int64_t cap = 256 * 4;  // a few resident workgroups per CU; the kernel loops over tiles
+  // one round of resident workgroups (as many per CU as the LDS allows); the kernel loops over tiles
+  constexpr size_t lds = (size_t)D * 64 * 2 + (size_t)D * 4 + 4 * 16 * (64 * sizeof(OutT) + 16);
+  const int per_cu = (int)(CU_LDS_BYTES / lds) > 0 ? (int)(CU_LDS_BYTES / lds) : 1;
+  const int cus = device_cus() > 0 ? device_cus() : 256;
+  const int64_t cap = (int64_t)cus * per_cu;
   if (wgs > cap) wgs = cap;
   hipLaunchKernelGGL((lift_kernel<InT, OutT, D>), dim3((unsigned)wgs), dim3(256), 0, st, (const InT*)x, rows, xs, normalize,
                      (const __bf16*)omega, phase, inv_tau, (OutT*)out, os);
@@ -246,7 +296,7 @@ extern "C" int kdn_fwht_lift(const void* x, int64_t rows, int64_t x_row_stride, 
   // 16-byte vector accesses: row starts of x and out, omega rows, phase.
   if (!aligned(x, 16) || !aligned(out, 16) || !aligned(omega_bf16, 16) || !aligned(phase, 16)) return KDN_ERR_MISALIGNED;
   if ((x_row_stride * (int64_t)dtype_size(x_dtype)) % 16 != 0) return KDN_ERR_MISALIGNED;
-  if ((out_row_stride * (int64_t)dtype_size(out_dtype)) % 8 != 0) return KDN_ERR_MISALIGNED;
+  if ((out_row_stride * (int64_t)dtype_size(out_dtype)) % 16 != 0) return KDN_ERR_MISALIGNED;
   if (rows == 0) return KDN_OK;
   hipStream_t st = as_stream(stream);
   const int nz = normalize_input ? 1 : 0;

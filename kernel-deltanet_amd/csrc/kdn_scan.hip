@@ -940,13 +940,6 @@ static ScanParams fill_params(const kdn_scan_args* a) {
 // segment starting at chunk 0 reads initial_state (zeros if NULL); later segments continue from
 // final_state.
 // Number of compute units of the current device (0 if the query fails).
-static int device_cus() {
-  int dev = 0, n = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return 0;
-  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-  return n;
-}
-
 // Chunks per prep workgroup: each workgroup of the prep kernel holds a CU alone (its LDS), so the
 // kernel runs in ceil(workgroups / CUs) rounds, each costing the staging of Omega (about 0.3 of a
 // chunk, measured) plus `run` chunks.  Pick the run length (1..8) with the least total for the CUs

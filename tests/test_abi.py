@@ -121,6 +121,8 @@ def test_lift_fwht_omega_argument_errors_need_no_device(lib):
     assert lib.kdn_fwht_lift(p + 2, 10, 64, 1, 0, p, p, 64, 512, 0.35, p, 512, 1, None) == -4
     assert lib.kdn_fwht_lift(None, 10, 64, 1, 0, p, p, 64, 512, 0.35, p, 512, 1, None) == -1
     assert lib.kdn_fwht_lift(p, 0, 64, 1, 0, p, p, 64, 512, 0.35, p, 512, 1, None) == 0
+    # bf16 output rows must be 16-byte multiples (the kernel stores whole 16-byte pieces of rows)
+    assert lib.kdn_fwht_lift(p, 10, 64, 1, 0, p, p, 64, 512, 0.35, p, 516, 1, None) == -4
     assert lib.kdn_fwht(p, 4, 3, 3, 0, p, 3, None) == -2
     assert lib.kdn_fwht(p, 0, 64, 64, 0, p, 64, None) == 0
     assert lib.kdn_build_omega(p, 32, 512, p, 1, None) == -2

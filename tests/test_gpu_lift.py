@@ -3,6 +3,9 @@ import numpy as np
 import pytest
 import torch
 
+import ctypes
+
+from kdn import _native as N
 from kdn import ops
 from kernels import FastWalshHadamardProjection, fast_walsh_hadamard_transform
 from oracle import lift as ol
@@ -74,6 +77,27 @@ def test_lift_strided_rows(proj, oproj):
     x = big[:, 32:96]  # row stride 128, 16-byte aligned start
     out = ops.lift(x.to(DEV), proj.device_omega(DEV), proj.device_phase(DEV), proj.tau_star_inv)
     assert rel_l2(out.cpu().numpy(), ol.lift(x.numpy(), oproj)) < 1e-5
+
+
+@pytest.mark.parametrize("D", [128, 256, 512])
+def test_lift_padded_output_rows_and_ragged_tile(proj, D):
+    # output rows wider than D (the kernel writes only the first D of each) and a row count that
+    # leaves the last 16-row tile partial
+    from kernels import FastWalshHadamardProjection
+    p = FastWalshHadamardProjection(64, D, 42)
+    op = ol.make_projection(64, D, 42)
+    x = torch.randn(37, 64)
+    om, ph = p.device_omega(DEV), p.device_phase(DEV)
+    out = torch.full((37, D + 64), 7.0, dtype=torch.bfloat16, device=DEV)
+    xd = x.to(DEV).to(torch.bfloat16)
+    N.check(N.lib().kdn_fwht_lift(ctypes.c_void_p(xd.data_ptr()), 37, 64, 1, 0, ctypes.c_void_p(om.data_ptr()),
+                                  ctypes.c_void_p(ph.data_ptr()), 64, D, p.tau_star_inv,
+                                  ctypes.c_void_p(out.data_ptr()), D + 64, 1,
+                                  ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)), "kdn_fwht_lift")
+    torch.cuda.synchronize()
+    o = out.float().cpu().numpy()
+    assert (o[:, D:] == 7.0).all()
+    assert rel_l2(o[:, :D], ol.lift(xd.float().cpu().numpy(), op)) < 1e-2
 
 
 @pytest.mark.parametrize("normalize", [False, True])
