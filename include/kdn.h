@@ -41,7 +41,8 @@ typedef enum kdn_status {
   KDN_ERR_UNSUPPORTED = -2,       /* valid request outside what the kernels implement (d_k, D, d_v) */
   KDN_ERR_WORKSPACE_TOO_SMALL = -3,
   KDN_ERR_MISALIGNED = -4,        /* a pointer or row stride breaks the 16-byte vector-access rule */
-  KDN_ERR_DEVICE = -5             /* a HIP launch reported an error */
+  KDN_ERR_DEVICE = -5,            /* a HIP launch reported an error */
+  KDN_ERR_CAPACITY = -6           /* the state pool has no free slot */
 } kdn_status;
 
 typedef enum kdn_dtype {
@@ -119,6 +120,14 @@ typedef struct kdn_scan_args {
    *   S_t = lambda_t S_{t-1} + beta_t v_t phi(k_t)^T, readout y_t = S_{t-1} phi(q_t) as before
    *   (the recurrence of core/chunked_scan.py:145-186, with beta = eta and lambda per head). */
   int rule;
+  /* Ragged batches (ABI 1.2).  With cu_seqlens (device int64 [B+1]) sequence b is the token rows
+   * cu_seqlens[b] .. cu_seqlens[b+1]-1 of a packed token dimension: q, k, v, beta, decay and y are
+   * addressed with stride[1] only (stride[0] is ignored) and T must be at least the longest sequence.
+   * A sequence without tokens gets final = initial state.  With state_slots (device int32 [B])
+   * sequence b reads and writes state slot state_slots[b] (stride[0] of the state tensors); slots must
+   * be distinct.  NULL keeps the uniform layout above. */
+  const int64_t* cu_seqlens;
+  const int32_t* state_slots;
 } kdn_scan_args;
 
 /* Workspace bytes kdn_delta_scan_fwd needs for these arguments (0 if the arguments are invalid).
@@ -167,6 +176,61 @@ size_t kdn_scan_workspace_bytes_pipelined(const kdn_scan_args* a);
 int kdn_scan_prep(const kdn_scan_args* a, int64_t chunk0, int64_t nchunks, void* stream);
 int kdn_scan_state(const kdn_scan_args* a, int64_t chunk0, int64_t nchunks, void* stream);
 int kdn_scan_output(const kdn_scan_args* a, int64_t chunk0, int64_t nchunks, void* stream);
+
+/* ---- Serving: ragged mixed prefill + decode step over resident states -------------------------
+ * One step of a batch of sequences that continue from states resident in a slab (the reference's
+ * serving op vllm_hybrid_recurrent_forward, serving/vllm_kernel_deltanet_op.cpp:11-34, whose body is a
+ * stub; its packing follows serving/vllm_ragged_batching.py:56-66).  Sequence i is the token rows
+ * cu_seqlens[i] .. cu_seqlens[i+1]-1 of q / k / v / beta / decay / y ([token][head][...]) and continues
+ * from state slot slots[i] of `states` ([slot][head][0:D][0:d_v] fp32, updated in place).  Sequences of
+ * one token run the decode kernel (lift of q and k, readout y = S phi(q), rank-1 update of S; one pass
+ * over the state); longer ones run the ragged chunked scan; sequences without tokens are left alone.
+ * The recurrence, feature map (the structured lift: omega_bf16, phase, inv_tau, normalize_input) and
+ * tolerances are those of kdn_delta_scan_fwd; rule 1 selects the linear rule as there. */
+typedef struct kdn_ragged_args {
+  int64_t num_seqs, H;
+  int d_k, D, d_v;             /* d_k = 64, D = 512, d_v in {16, 32, 64, 128} */
+  int in_dtype, out_dtype, normalize_input, rule;
+  float inv_tau;
+  const int64_t* cu_seqlens;       /* device [num_seqs + 1] */
+  const int64_t* cu_seqlens_host;  /* the same offsets in host memory (scheduling: counts, longest) */
+  const int32_t* slots;            /* device [num_seqs]: distinct state slots */
+  const void* q;   int64_t q_stride[2];   /* [token][head] element strides; innermost contiguous */
+  const void* k;   int64_t k_stride[2];
+  const void* v;   int64_t v_stride[2];
+  const float* beta;  int64_t beta_stride[2];
+  const float* decay; int64_t decay_stride[2];   /* NULL means lambda = 1 */
+  const void* omega_bf16; const float* phase;
+  float* states;   int64_t state_stride[4];       /* [slot][head][feature][value] */
+  void* y;         int64_t y_stride[2];
+  void* workspace; size_t workspace_bytes;
+} kdn_ragged_args;
+
+/* Workspace bytes kdn_ragged_step needs (0 if the arguments are invalid); reads the shape fields and
+ * cu_seqlens_host. */
+size_t kdn_ragged_workspace_bytes(const kdn_ragged_args* a);
+
+/* Runs the step on `stream`; the prefill part uses the pipelined scan when aux_stream is not NULL. */
+int kdn_ragged_step(const kdn_ragged_args* a, void* stream, void* aux_stream);
+
+/* ---- Slab state pool --------------------------------------------------------------------------
+ * Slot bookkeeping over a caller-allocated slab of `max_slots` equal fp32 state slots of slot_bytes
+ * each (for example [slot][layer][head][D][d_v]); the reference's HybridMemoryPool recurrent slab,
+ * serving/hybrid_memory_pool.{h,cpp} (the softmax anchor pages of that class are not part of this path).
+ * Host-side and single-threaded per pool; functions that take a slab pointer also enqueue device work
+ * on `stream` (zeroing a new slot, copying a forked one), and skip it when slab is NULL. */
+typedef struct kdn_pool kdn_pool;
+int kdn_pool_create(int64_t max_slots, int64_t slot_bytes, kdn_pool** out);
+void kdn_pool_destroy(kdn_pool* pool);
+/* A free slot (>= 0), zeroed on the device when slab is not NULL; KDN_ERR_CAPACITY when none is free. */
+int kdn_pool_allocate(kdn_pool* pool, void* slab, void* stream);
+/* A new slot holding a copy of active slot `parent` (hybrid_memory_pool.cpp:86-116); negative on error. */
+int kdn_pool_fork(kdn_pool* pool, int parent, void* slab, void* stream);
+/* Returns an active slot to the pool (hybrid_memory_pool.cpp:118-135); negative if it is not active. */
+int kdn_pool_release(kdn_pool* pool, int slot);
+int64_t kdn_pool_active(const kdn_pool* pool);
+int64_t kdn_pool_allocated_bytes(const kdn_pool* pool);
+int64_t kdn_pool_free_bytes(const kdn_pool* pool);
 
 #ifdef __cplusplus
 }

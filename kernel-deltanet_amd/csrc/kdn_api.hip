@@ -9,8 +9,9 @@ extern "C" const char* kdn_strerror(int status) {
     case KDN_ERR_WORKSPACE_TOO_SMALL: return "workspace smaller than kdn_scan_workspace_bytes()";
     case KDN_ERR_MISALIGNED: return "pointer or row stride not aligned for 16-byte vector access";
     case KDN_ERR_DEVICE: return "HIP launch error";
+    case KDN_ERR_CAPACITY: return "state pool has no free slot";
     default: return "unknown kdn status";
   }
 }
 
-extern "C" int kdn_abi_version(void) { return (1 << 16) | 1; }
+extern "C" int kdn_abi_version(void) { return (1 << 16) | 2; }

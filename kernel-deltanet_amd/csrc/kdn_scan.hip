@@ -70,7 +70,38 @@ struct ScanParams {
   const float* inv_tau_head;
   int no_renorm, prelifted;
   int linear;  // update rule without the erasure term: T = I, Tp = 0
+  // ragged batches: sequence b is token rows seq_lo[b] .. seq_hi[b] (stride 1 of each token tensor; for
+  // cu_seqlens, seq_hi = cu_seqlens + 1); its state is slot slots[b] (stride 0 of the state tensors)
+  const int64_t* seq_lo;
+  const int64_t* seq_hi;
+  const int* slots;
 };
+
+// Sequence b of the batch: element offsets of its first token in each token-indexed tensor, and its
+// length.  A uniform batch addresses b * stride0 and has T tokens per sequence; a ragged batch
+// addresses rows seq_lo[b] .. seq_hi[b] of one packed token dimension.
+struct Seq {
+  int64_t q, k, v, be, de, y, len;
+};
+__device__ __forceinline__ Seq seq_of(const ScanParams& p, int64_t b) {
+  Seq s;
+  if (p.seq_lo) {
+    const int64_t r0 = p.seq_lo[b];
+    s.q = r0 * p.qs1; s.k = r0 * p.ks1; s.v = r0 * p.vs1;
+    s.be = r0 * p.bs1; s.de = r0 * p.ds1; s.y = r0 * p.ys1;
+    s.len = p.seq_hi[b] - r0;
+  } else {
+    s.q = b * p.qs0; s.k = b * p.ks0; s.v = b * p.vs0;
+    s.be = b * p.bs0; s.de = b * p.ds0; s.y = b * p.ys0;
+    s.len = p.T;
+  }
+  return s;
+}
+// Chunks of the current segment that hold tokens of the sequence (0 once it has ended).
+__device__ __forceinline__ int64_t seg_chunks(const ScanParams& p, const Seq& s) {
+  const int64_t n = (s.len + CH - 1) / CH - p.chunk0;
+  return n <= 0 ? 0 : (n < p.nseg ? n : p.nseg);
+}
 
 // Feature modes of the prep kernel: Omega exact in bf16 (the structured projection), Omega as hi + lo
 // bf16 parts (general projections), or q / k already lifted (d_k = D).
@@ -221,25 +252,25 @@ struct PrepInputs {
   static constexpr int VPT = (64 * VPR + 255) / 256;             // pieces per thread
   RawRow<InT> qk[2];
   float be, la;
-  __device__ __forceinline__ void load_qk(const ScanParams& p, int64_t b, int64_t h, int64_t t0, int w, int lane) {
+  __device__ __forceinline__ void load_qk(const ScanParams& p, const Seq& sq, int64_t h, int64_t t0, int w, int lane) {
     const int64_t trow = t0 + 16 * w + (lane & 15);
-    const bool rvalid = trow < p.T;
-    qk[0].load((const InT*)p.q + b * p.qs0 + trow * p.qs1 + h * p.qs2, rvalid, lane);
-    qk[1].load((const InT*)p.k + b * p.ks0 + trow * p.ks1 + h * p.ks2, rvalid, lane);
+    const bool rvalid = trow < sq.len;
+    qk[0].load((const InT*)p.q + sq.q + trow * p.qs1 + h * p.qs2, rvalid, lane);
+    qk[1].load((const InT*)p.k + sq.k + trow * p.ks1 + h * p.ks2, rvalid, lane);
     const int64_t t = t0 + lane;
-    const bool valid = t < p.T;
-    be = valid ? p.beta[b * p.bs0 + t * p.bs1 + h * p.bs2] : 0.f;
-    la = (valid && p.decay) ? p.decay[b * p.ds0 + t * p.ds1 + h * p.ds2] : 1.f;
+    const bool valid = t < sq.len;
+    be = valid ? p.beta[sq.be + t * p.bs1 + h * p.bs2] : 0.f;
+    la = (valid && p.decay) ? p.decay[sq.de + t * p.ds1 + h * p.ds2] : 1.f;
   }
-  __device__ __forceinline__ static void load_v(const ScanParams& p, int64_t b, int64_t h, int64_t t0, u32x4 (&v)[VPT]) {
+  __device__ __forceinline__ static void load_v(const ScanParams& p, const Seq& sq, int64_t h, int64_t t0, u32x4 (&v)[VPT]) {
 #pragma unroll
     for (int i = 0; i < VPT; ++i) {
       const int idx = (int)threadIdx.x + 256 * i;
       const int r = idx / VPR, pc = idx % VPR;
       const int64_t t = t0 + r;
       u32x4 val = {0u, 0u, 0u, 0u};
-      if (idx < 64 * VPR && t < p.T)
-        val = *reinterpret_cast<const u32x4*>((const InT*)p.v + b * p.vs0 + t * p.vs1 + h * p.vs2 + pc * (16 / (int)sizeof(InT)));
+      if (idx < 64 * VPR && t < sq.len)
+        val = *reinterpret_cast<const u32x4*>((const InT*)p.v + sq.v + t * p.vs1 + h * p.vs2 + pc * (16 / (int)sizeof(InT)));
       v[i] = val;
     }
   }
@@ -286,7 +317,10 @@ __global__ void __launch_bounds__(256) prep_kernel(ScanParams p) {
   constexpr int RUN = PrepRun<P, FM>::value;  // 0: runtime run length with prefetch
   const int run = RUN ? RUN : p.prep_run;
   const int64_t cl0 = (int64_t)blockIdx.x * run;
-  const int64_t cl_end = (cl0 + run < p.nseg) ? cl0 + run : p.nseg;
+  const Seq sq = seq_of(p, b);
+  const int64_t nloc = seg_chunks(p, sq);
+  if (cl0 >= nloc) return;  // past the end of this sequence (ragged batches): nothing to prepare
+  const int64_t cl_end = (cl0 + run < nloc) ? cl0 + run : nloc;
 
   const __bf16* omega_h = p.omega + h * p.oms;
   const __bf16* omega_lo_h = (FM == FM_HILO) ? p.omega_lo + h * p.oms : nullptr;
@@ -294,20 +328,20 @@ __global__ void __launch_bounds__(256) prep_kernel(ScanParams p) {
   In in;
   if constexpr (FM != FM_PRELIFTED) {
     stage_omega<D, OMEGA_LDS>(omega_h, p.phase + h * p.phs, s_omega, s_phrev);
-    in.load_qk(p, b, h, (p.chunk0 + cl0) * CH, w, lane);
+    in.load_qk(p, sq, h, (p.chunk0 + cl0) * CH, w, lane);
   } else {
     // no lift: only beta / decay come through the prefetch
     const int64_t t = (p.chunk0 + cl0) * CH + lane;
-    const bool valid = t < p.T;
-    in.be = valid ? p.beta[b * p.bs0 + t * p.bs1 + h * p.bs2] : 0.f;
-    in.la = (valid && p.decay) ? p.decay[b * p.ds0 + t * p.ds1 + h * p.ds2] : 1.f;
+    const bool valid = t < sq.len;
+    in.be = valid ? p.beta[sq.be + t * p.bs1 + h * p.bs2] : 0.f;
+    in.la = (valid && p.decay) ? p.decay[sq.de + t * p.ds1 + h * p.ds2] : 1.f;
   }
 
   auto process = [&](int64_t cl) {
     const int64_t t0 = (p.chunk0 + cl) * CH;
     unsigned char* ws = p.ws + ((b * p.H + h) * (p.nseg + 1) + cl) * L::bytes;
     u32x4 vraw[In::VPT];
-    if constexpr (RUN != 1) In::load_v(p, b, h, t0, vraw);  // early: first needed after the Gram
+    if constexpr (RUN != 1) In::load_v(p, sq, h, t0, vraw);  // early: first needed after the Gram
     __syncthreads();  // Omega staged (first chunk); the previous chunk's LDS reads are done
 
     // ---- beta and the in-chunk log-decay prefix (wave 0)
@@ -327,16 +361,16 @@ __global__ void __launch_bounds__(256) prep_kernel(ScanParams p) {
     float ss[2] = {0.f, 0.f};
     if constexpr (FM == FM_PRELIFTED) {
       const int64_t trow = t0 + 16 * w + (lane & 15);
-      load_lifted<P, InT, D>((const InT*)p.q + b * p.qs0 + trow * p.qs1 + h * p.qs2, trow < p.T, lane, cqk[0]);
-      load_lifted<P, InT, D>((const InT*)p.k + b * p.ks0 + trow * p.ks1 + h * p.ks2, trow < p.T, lane, cqk[1]);
+      load_lifted<P, InT, D>((const InT*)p.q + sq.q + trow * p.qs1 + h * p.qs2, trow < sq.len, lane, cqk[0]);
+      load_lifted<P, InT, D>((const InT*)p.k + sq.k + trow * p.ks1 + h * p.ks2, trow < sq.len, lane, cqk[1]);
       const int64_t tn = (p.chunk0 + ((cl + 1 < cl_end) ? cl + 1 : cl)) * CH + lane;
-      in.be = (tn < p.T) ? p.beta[b * p.bs0 + tn * p.bs1 + h * p.bs2] : 0.f;
-      in.la = (tn < p.T && p.decay) ? p.decay[b * p.ds0 + tn * p.ds1 + h * p.ds2] : 1.f;
+      in.be = (tn < sq.len) ? p.beta[sq.be + tn * p.bs1 + h * p.bs2] : 0.f;
+      in.la = (tn < sq.len && p.decay) ? p.decay[sq.de + tn * p.ds1 + h * p.ds2] : 1.f;
     } else {
       lift_tile<P, InT, D, OMEGA_LDS, 2, FM == FM_HILO>(in.qk, p.normalize, s_omega, omega_h, s_phrev, ang, lane,
                                                          cqk, ss, omega_lo_h);
       // the next chunk's rows travel while this one is processed (clamped: the last chunk reloads itself)
-      if constexpr (RUN != 1) in.load_qk(p, b, h, (p.chunk0 + ((cl + 1 < cl_end) ? cl + 1 : cl)) * CH, w, lane);
+      if constexpr (RUN != 1) in.load_qk(p, sq, h, (p.chunk0 + ((cl + 1 < cl_end) ? cl + 1 : cl)) * CH, w, lane);
     }
     {
       // per-row scale of the stored (unnormalised) features: 1 for given features, sqrt(2/D) without
@@ -401,7 +435,7 @@ __global__ void __launch_bounds__(256) prep_kernel(ScanParams p) {
       for (int jb = 0; jb < 2; ++jb)
         store_frag<P>(ws + L::Pm + (size_t)(w * 2 + jb) * 64 * L::FB, lane, P::from_f32(pair_to8(pt[2 * jb], pt[2 * jb + 1])));
     }
-    if constexpr (RUN == 1) In::load_v(p, b, h, t0, vraw);
+    if constexpr (RUN == 1) In::load_v(p, sq, h, t0, vraw);
 #pragma unroll
     for (int i = 0; i < In::VPT; ++i) {
       const int idx = (int)threadIdx.x + 256 * i;
@@ -726,7 +760,7 @@ __device__ __forceinline__ bool state_iter(const ScanParams& p, StateShared& sh,
                                            int64_t cl, int w, int lane, int n, f32x4 (&S)[D / 64],
                                            typename P::frag (&ak_c)[4][D / 128], typename StateOps<P, D, DV>::Small& sm_c,
                                            typename P::frag (&ak_n)[4][D / 128], typename StateOps<P, D, DV>::Small& sm_n,
-                                           unsigned& l2slot, unsigned& l2acc) {
+                                           unsigned& l2slot, unsigned& l2acc, int64_t nloc) {
   using O = StateOps<P, D, DV>;
   using L = typename O::L;
   unsigned char* cur = wsh + cl * L::bytes;
@@ -734,10 +768,11 @@ __device__ __forceinline__ bool state_iter(const ScanParams& p, StateShared& sh,
   const float gC = sm_c.gC;
   state_phase3<P, D, DV, DECAY>(sh, kl, lane, S, gC);
   // Unconditional (no branch splits the region): after the last chunk, phase 1 runs on the clamped
-  // operands of the last chunk and writes its checkpoint into the spare record nseg of the head.
-  const int64_t cr = (cl + 2 < p.nseg) ? cl + 2 : p.nseg - 1;
+  // operands of the last chunk and writes its checkpoint into the record after the last chunk (the
+  // spare record nseg of the head, or an unused record of a ragged sequence that ends earlier).
+  const int64_t cr = (cl + 2 < nloc) ? cl + 2 : nloc - 1;
   O::load_all(wsh + cr * L::bytes, w, lane, n, ak_c, sm_c);
-  const int64_t cp = (cl + 1 + O::L2_AHEAD < p.nseg) ? cl + 1 + O::L2_AHEAD : p.nseg - 1;
+  const int64_t cp = (cl + 1 + O::L2_AHEAD < nloc) ? cl + 1 + O::L2_AHEAD : nloc - 1;
   l2_prefetch<P, D, DV>(wsh + cp * L::bytes, w, lane, n, l2slot, l2acc);
   state_phase1<P, D, DV>(sh, kl, cur + L::bytes, w, lane, n, S, ak_n);
   // 32 MFMAs (16 update, 16 X_K) and ~26 memory instructions: alternate them.
@@ -748,7 +783,7 @@ __device__ __forceinline__ bool state_iter(const ScanParams& p, StateShared& sh,
   }
   __builtin_amdgcn_sched_group_barrier(0x008, 6, 0);
   __syncthreads();
-  return cl + 1 < p.nseg;
+  return cl + 1 < nloc;
 }
 
 template <class P, int D, int DV, bool DECAY>
@@ -768,6 +803,12 @@ __global__ void __launch_bounds__(256) state_kernel(ScanParams p) {
   const int64_t hb = (jdx / NV) * 8 + xcd;
   if (hb >= p.B * p.H) return;
   const int64_t b = hb / p.H, h = hb % p.H;
+  const Seq sq = seq_of(p, b);
+  const int64_t nloc = seg_chunks(p, sq);
+  // A sequence that ended in an earlier segment has its final state already; one without tokens gets
+  // its initial state copied through (below, no chunk is run).
+  if (nloc == 0 && !(sq.len <= 0 && p.chunk0 == 0)) return;
+  const int64_t sl = p.slots ? (int64_t)p.slots[b] : b;
 
   const int lane = threadIdx.x & 63;
   // The wave index is uniform across the wave; reading it into a scalar register lets every
@@ -778,7 +819,7 @@ __global__ void __launch_bounds__(256) state_kernel(ScanParams p) {
 
   f32x4 S[TPW];
   if (p.state_in) {
-    const float* si = p.state_in + b * p.is0 + h * p.is1 + r * p.is3;
+    const float* si = p.state_in + sl * p.is0 + h * p.is1 + r * p.is3;
 #pragma unroll
     for (int tl = 0; tl < TPW; ++tl)
 #pragma unroll
@@ -792,18 +833,20 @@ __global__ void __launch_bounds__(256) state_kernel(ScanParams p) {
   frag k0[4][JPW], k1[4][JPW];
   typename O::Small s0, s1;
   unsigned l2acc = 0, l2s0 = 0, l2s1 = 0;  // sink of the L2-prefetch loads (never stored; see below)
-  // Prologue: chunk 0 in slot 0, chunk min(1, last) in slot 1, phase 1 of chunk 0.
-  O::load_all(wsh, w, lane, n, k0, s0);
-  O::load_all(wsh + (p.nseg > 1 ? L::bytes : 0), w, lane, n, k1, s1);
-  state_phase1<P, D, DV>(sh, kl, wsh, w, lane, n, S, k0);
-  __syncthreads();
-  for (int64_t cl = 0;; cl += 2) {
-    if (!state_iter<P, D, DV, DECAY>(p, sh, kl, wsh, cl, w, lane, n, S, k0, s0, k1, s1, l2s0, l2acc)) break;
-    if (!state_iter<P, D, DV, DECAY>(p, sh, kl, wsh, cl + 1, w, lane, n, S, k1, s1, k0, s0, l2s1, l2acc)) break;
+  if (nloc > 0) {  // an empty sequence (uniform across the workgroup) runs no chunk
+    // Prologue: chunk 0 in slot 0, chunk min(1, last) in slot 1, phase 1 of chunk 0.
+    O::load_all(wsh, w, lane, n, k0, s0);
+    O::load_all(wsh + (nloc > 1 ? L::bytes : 0), w, lane, n, k1, s1);
+    state_phase1<P, D, DV>(sh, kl, wsh, w, lane, n, S, k0);
+    __syncthreads();
+    for (int64_t cl = 0;; cl += 2) {
+      if (!state_iter<P, D, DV, DECAY>(p, sh, kl, wsh, cl, w, lane, n, S, k0, s0, k1, s1, l2s0, l2acc, nloc)) break;
+      if (!state_iter<P, D, DV, DECAY>(p, sh, kl, wsh, cl + 1, w, lane, n, S, k1, s1, k0, s0, l2s1, l2acc, nloc)) break;
+    }
+    l2acc += l2s0 + l2s1;
   }
-  l2acc += l2s0 + l2s1;
 
-  float* so = p.state_out + b * p.os0 + h * p.os1 + r * p.os3;
+  float* so = p.state_out + sl * p.os0 + h * p.os1 + r * p.os3;
 #pragma unroll
   for (int tl = 0; tl < TPW; ++tl)
 #pragma unroll
@@ -848,6 +891,8 @@ __global__ void __launch_bounds__(256) output_kernel(ScanParams p) {
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int64_t cl = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const Seq sq = seq_of(p, b);
+  if (cl >= seg_chunks(p, sq)) return;  // past the end of this sequence (ragged batches)
   const int64_t t0 = (p.chunk0 + cl) * CH;
   const unsigned char* ws = p.ws + ((b * p.H + h) * (p.nseg + 1) + cl) * L::bytes;
   const float* vec = reinterpret_cast<const float*>(ws + L::VEC);
@@ -897,11 +942,11 @@ __global__ void __launch_bounds__(256) output_kernel(ScanParams p) {
     if (idx < PIECES) {
       const int row = idx / (DV / 8), pc = idx % (DV / 8);
       const int64_t t = t0 + 16 * w + row;
-      if (t < p.T) {
+      if (t < sq.len) {
         const f32x4 v0 = *reinterpret_cast<const f32x4*>(yt + row * YS + 8 * pc);
         const f32x4 v1 = *reinterpret_cast<const f32x4*>(yt + row * YS + 8 * pc + 4);
         const float v[8] = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
-        store_row8<OutT>((OutT*)p.y + b * p.ys0 + t * p.ys1 + h * p.ys2 + 8 * pc, v);
+        store_row8<OutT>((OutT*)p.y + sq.y + t * p.ys1 + h * p.ys2 + 8 * pc, v);
       }
     }
   }
@@ -933,13 +978,12 @@ static ScanParams fill_params(const kdn_scan_args* a) {
   p.no_renorm = a->no_renorm ? 1 : 0;
   p.prelifted = a->feature_mode == 1 ? 1 : 0;
   p.linear = a->rule == 1 ? 1 : 0;
+  p.seq_lo = a->cu_seqlens;
+  p.seq_hi = a->cu_seqlens ? a->cu_seqlens + 1 : nullptr;
+  p.slots = a->state_slots;
   return p;
 }
 
-// Parameters of one segment: chunks [c0, c0 + nseg) with its records at `ws`.  The state kernel of the
-// segment starting at chunk 0 reads initial_state (zeros if NULL); later segments continue from
-// final_state.
-// Number of compute units of the current device (0 if the query fails).
 // Chunks per prep workgroup: each workgroup of the prep kernel holds a CU alone (its LDS), so the
 // kernel runs in ceil(workgroups / CUs) rounds, each costing the staging of Omega (about 0.3 of a
 // chunk, measured) plus `run` chunks.  Pick the run length (1..8) with the least total for the CUs
@@ -956,8 +1000,29 @@ static int choose_prep_run(int64_t nseg, int64_t heads, int cus) {
   return best;
 }
 
-static ScanParams segment_params(const kdn_scan_args* a, int64_t c0, int64_t nseg, void* ws, int prep_cus) {
+// How the launches of one call are scheduled.
+struct RunSpec {
+  int64_t c_begin, c_end, seg;
+  int phases;
+  hipStream_t st;
+  hipStream_t aux;   // non-null: pipelined over `nbuf` buffers of `buf_bytes`
+  int nbuf;
+  size_t buf_bytes;
+  // ragged sequences given as separate start / end arrays (device), overriding cu_seqlens
+  const int64_t* seq_lo = nullptr;
+  const int64_t* seq_hi = nullptr;
+};
+
+// Parameters of one segment: chunks [c0, c0 + nseg) with its records at `ws`.  The state kernel of the
+// segment starting at chunk 0 reads initial_state (zeros if NULL); later segments continue from
+// final_state.
+static ScanParams segment_params(const kdn_scan_args* a, const RunSpec& r, int64_t c0, int64_t nseg, void* ws,
+                                 int prep_cus) {
   ScanParams p = fill_params(a);
+  if (r.seq_lo) {
+    p.seq_lo = r.seq_lo;
+    p.seq_hi = r.seq_hi;
+  }
   p.chunk0 = c0;
   p.nseg = nseg;
   p.ws = (unsigned char*)ws;
@@ -972,10 +1037,10 @@ static ScanParams segment_params(const kdn_scan_args* a, int64_t c0, int64_t nse
   return p;
 }
 
-#ifndef STATE_SHARE_CU
-#define STATE_SHARE_CU 0
-#endif
-constexpr int STATE_EXCLUSIVE_LDS = 40 * 1024;  // dynamic LDS: 88 + 40 = 128 KB > 160 - 49 (output WG)
+// The state kernel keeps its CU to itself: 40 KB of unused dynamic LDS raise its request to 128 KB, so
+// that neither a prep workgroup (~131 KB) nor an output workgroup (~49 KB) fits beside it in the CU's
+// 160 KB and takes issue slots from the sequential chain.
+constexpr int STATE_EXCLUSIVE_LDS = 40 * 1024;
 
 template <class P, typename InT, typename OutT, int D, int DV>
 static int launch_phase(const ScanParams& p, int phase, hipStream_t st) {
@@ -992,7 +1057,7 @@ static int launch_phase(const ScanParams& p, int phase, hipStream_t st) {
   } else if (phase == PHASE_STATE) {
     // The state workgroups are the sequential critical path: reserve enough LDS that no prep or output
     // workgroup can share their CU (a CU has 160 KB; the bf16 state kernel uses 88 KB statically).
-    const size_t excl = (IsBF16<P>::value && !STATE_SHARE_CU) ? (size_t)STATE_EXCLUSIVE_LDS : 0;
+    const size_t excl = IsBF16<P>::value ? (size_t)STATE_EXCLUSIVE_LDS : 0;
     if (p.decay) hipLaunchKernelGGL((state_kernel<P, D, DV, true>), dim3(state_grid(p.B, p.H, DV / 16)), dim3(256), excl, st, p);
     else hipLaunchKernelGGL((state_kernel<P, D, DV, false>), dim3(state_grid(p.B, p.H, DV / 16)), dim3(256), excl, st, p);
   } else {
@@ -1004,13 +1069,13 @@ static int launch_phase(const ScanParams& p, int phase, hipStream_t st) {
 // Runs chunks [c_begin, c_end) in segments of `seg` chunks, all in one workspace buffer: per segment the
 // selected kernels, in the order prep, state, output.
 template <class P, typename InT, typename OutT, int D, int DV>
-static int run_scan(const kdn_scan_args* a, int64_t c_begin, int64_t c_end, int64_t seg, int phases, hipStream_t st) {
+static int run_scan(const kdn_scan_args* a, const RunSpec& r) {
   const int cus = device_cus();
-  for (int64_t c0 = c_begin; c0 < c_end; c0 += seg) {
-    const ScanParams p = segment_params(a, c0, (c_end - c0 < seg) ? (c_end - c0) : seg, a->workspace, cus);
+  for (int64_t c0 = r.c_begin; c0 < r.c_end; c0 += r.seg) {
+    const ScanParams p = segment_params(a, r, c0, (r.c_end - c0 < r.seg) ? (r.c_end - c0) : r.seg, a->workspace, cus);
     for (int ph : {PHASE_PREP, PHASE_STATE, PHASE_OUTPUT}) {
-      if (!(phases & ph)) continue;
-      const int rc = launch_phase<P, InT, OutT, D, DV>(p, ph, st);
+      if (!(r.phases & ph)) continue;
+      const int rc = launch_phase<P, InT, OutT, D, DV>(p, ph, r.st);
       if (rc != KDN_OK) return rc;
     }
   }
@@ -1040,7 +1105,11 @@ struct EventSet {
 //   prep(s)   reuses the buffer of segment s - nbuf, whose output ran earlier on aux
 // aux first waits for the work already queued on st, and st finally waits for the last output.
 template <class P, typename InT, typename OutT, int D, int DV>
-static int run_pipelined(const kdn_scan_args* a, int64_t seg, int nbuf, size_t buf_bytes, hipStream_t st, hipStream_t aux) {
+static int run_pipelined(const kdn_scan_args* a, const RunSpec& r) {
+  const int64_t seg = r.seg;
+  const int nbuf = r.nbuf;
+  const size_t buf_bytes = r.buf_bytes;
+  const hipStream_t st = r.st, aux = r.aux;
   const int64_t nchunks = (a->T + CH - 1) / CH;
   const int64_t nsegs = (nchunks + seg - 1) / seg;
   EventSet evs;
@@ -1053,7 +1122,7 @@ static int run_pipelined(const kdn_scan_args* a, int64_t seg, int nbuf, size_t b
   const int prep_cus = device_cus() - (int)state_grid(a->B, a->H, DV / 16);
   auto seg_p = [&](int64_t s) {
     const int64_t c0 = s * seg;
-    return segment_params(a, c0, (nchunks - c0 < seg) ? (nchunks - c0) : seg,
+    return segment_params(a, r, c0, (nchunks - c0 < seg) ? (nchunks - c0) : seg,
                           (unsigned char*)a->workspace + (size_t)(s % nbuf) * buf_bytes, prep_cus);
   };
 #define KDN_TRY(x) do { if ((x) != hipSuccess) return KDN_ERR_DEVICE; } while (0)
@@ -1081,20 +1150,10 @@ static int run_pipelined(const kdn_scan_args* a, int64_t seg, int nbuf, size_t b
   return KDN_OK;
 }
 
-// How the launches of one call are scheduled.
-struct RunSpec {
-  int64_t c_begin, c_end, seg;
-  int phases;
-  hipStream_t st;
-  hipStream_t aux;   // non-null: pipelined over `nbuf` buffers of `buf_bytes`
-  int nbuf;
-  size_t buf_bytes;
-};
-
 template <class P, typename InT, typename OutT, int D, int DV>
 static int run(const kdn_scan_args* a, const RunSpec& r) {
-  if (r.aux) return run_pipelined<P, InT, OutT, D, DV>(a, r.seg, r.nbuf, r.buf_bytes, r.st, r.aux);
-  return run_scan<P, InT, OutT, D, DV>(a, r.c_begin, r.c_end, r.seg, r.phases, r.st);
+  if (r.aux) return run_pipelined<P, InT, OutT, D, DV>(a, r);
+  return run_scan<P, InT, OutT, D, DV>(a, r);
 }
 
 template <class P, typename InT, typename OutT, int D>
@@ -1222,14 +1281,14 @@ static int64_t pipeline_segment(const kdn_scan_args* a) {
 }
 
 extern "C" size_t kdn_scan_workspace_bytes_pipelined(const kdn_scan_args* a) {
-  if (validate(a) != KDN_OK) return 0;
-  const int64_t seg = pipeline_segment(a);
-  const int64_t nsegs = ((a->T + CH - 1) / CH + seg - 1) / seg;
-  const int64_t nbuf = nsegs < 3 ? nsegs : 3;
-  return chunk_bytes(a) * (size_t)a->B * (size_t)a->H * (size_t)(seg + 1) * (size_t)nbuf;
+  return scan_workspace_bytes_pipelined(a);
 }
 
-extern "C" int kdn_delta_scan_fwd_pipelined(const kdn_scan_args* a, void* stream, void* aux_stream) {
+namespace kdn {
+// The pipelined scan (serial when aux_stream is NULL or the workspace holds one segment buffer), with
+// ragged sequences optionally given as device start / end arrays.
+int scan_pipelined(const kdn_scan_args* a, const int64_t* seq_lo, const int64_t* seq_hi, void* stream,
+                   void* aux_stream) {
   int rc = validate_launch(a);
   if (rc != KDN_OK) return rc;
   const int64_t seg = pipeline_segment(a);
@@ -1239,10 +1298,24 @@ extern "C" int kdn_delta_scan_fwd_pipelined(const kdn_scan_args* a, void* stream
   const int64_t nsegs = (nchunks + seg - 1) / seg;
   size_t fit = a->workspace_bytes / buf;
   const int nbuf = (int)(fit < 3 ? fit : 3);
-  if (!aux_stream || aux_stream == stream || nbuf < 2 || nsegs < 2)
-    return dispatch(a, 0, nchunks, seg, PHASE_ALL, as_stream(stream));
-  const RunSpec r = {0, nchunks, seg, PHASE_ALL, as_stream(stream), as_stream(aux_stream), nbuf, buf};
+  RunSpec r = {0, nchunks, seg, PHASE_ALL, as_stream(stream), as_stream(aux_stream), nbuf, buf};
+  r.seq_lo = seq_lo;
+  r.seq_hi = seq_hi;
+  if (!aux_stream || aux_stream == stream || nbuf < 2 || nsegs < 2) r.aux = nullptr;
   return dispatch(a, r);
+}
+
+size_t scan_workspace_bytes_pipelined(const kdn_scan_args* a) {
+  if (validate(a) != KDN_OK) return 0;
+  const int64_t seg = pipeline_segment(a);
+  const int64_t nsegs = ((a->T + CH - 1) / CH + seg - 1) / seg;
+  const int64_t nbuf = nsegs < 3 ? nsegs : 3;
+  return chunk_bytes(a) * (size_t)a->B * (size_t)a->H * (size_t)(seg + 1) * (size_t)nbuf;
+}
+}  // namespace kdn
+
+extern "C" int kdn_delta_scan_fwd_pipelined(const kdn_scan_args* a, void* stream, void* aux_stream) {
+  return scan_pipelined(a, nullptr, nullptr, stream, aux_stream);
 }
 
 extern "C" int kdn_scan_prep(const kdn_scan_args* a, int64_t chunk0, int64_t nchunks, void* stream) {

@@ -30,7 +30,19 @@ EXPORTED = (
     "kdn_scan_output",
     "kdn_scan_workspace_bytes_pipelined",
     "kdn_delta_scan_fwd_pipelined",
+    "kdn_ragged_workspace_bytes",
+    "kdn_ragged_step",
+    "kdn_pool_create",
+    "kdn_pool_destroy",
+    "kdn_pool_allocate",
+    "kdn_pool_fork",
+    "kdn_pool_release",
+    "kdn_pool_active",
+    "kdn_pool_allocated_bytes",
+    "kdn_pool_free_bytes",
 )
+
+KDN_ERR_CAPACITY = -6
 
 _i64 = ctypes.c_int64
 _i64x3 = ctypes.c_int64 * 3
@@ -64,6 +76,35 @@ class ScanArgs(ctypes.Structure):
         ("no_renorm", ctypes.c_int),
         ("feature_mode", ctypes.c_int),
         ("rule", ctypes.c_int),
+        ("cu_seqlens", ctypes.c_void_p),
+        ("state_slots", ctypes.c_void_p),
+    ]
+
+
+_i64x2 = ctypes.c_int64 * 2
+
+
+class RaggedArgs(ctypes.Structure):
+    """Mirror of struct kdn_ragged_args (include/kdn.h)."""
+
+    _fields_ = [
+        ("num_seqs", _i64), ("H", _i64),
+        ("d_k", ctypes.c_int), ("D", ctypes.c_int), ("d_v", ctypes.c_int),
+        ("in_dtype", ctypes.c_int), ("out_dtype", ctypes.c_int), ("normalize_input", ctypes.c_int),
+        ("rule", ctypes.c_int),
+        ("inv_tau", ctypes.c_float),
+        ("cu_seqlens", ctypes.c_void_p),
+        ("cu_seqlens_host", ctypes.c_void_p),
+        ("slots", ctypes.c_void_p),
+        ("q", ctypes.c_void_p), ("q_stride", _i64x2),
+        ("k", ctypes.c_void_p), ("k_stride", _i64x2),
+        ("v", ctypes.c_void_p), ("v_stride", _i64x2),
+        ("beta", ctypes.c_void_p), ("beta_stride", _i64x2),
+        ("decay", ctypes.c_void_p), ("decay_stride", _i64x2),
+        ("omega_bf16", ctypes.c_void_p), ("phase", ctypes.c_void_p),
+        ("states", ctypes.c_void_p), ("state_stride", _i64x4),
+        ("y", ctypes.c_void_p), ("y_stride", _i64x2),
+        ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_size_t),
     ]
 
 
@@ -110,6 +151,24 @@ def lib() -> ctypes.CDLL:
                 fn = getattr(L, nm)
                 fn.argtypes = [ctypes.POINTER(ScanArgs), i64, i64, vp]
                 fn.restype = ci
+            L.kdn_ragged_workspace_bytes.argtypes = [ctypes.POINTER(RaggedArgs)]
+            L.kdn_ragged_workspace_bytes.restype = sz
+            L.kdn_ragged_step.argtypes = [ctypes.POINTER(RaggedArgs), vp, vp]
+            L.kdn_ragged_step.restype = ci
+            L.kdn_pool_create.argtypes = [i64, i64, ctypes.POINTER(vp)]
+            L.kdn_pool_create.restype = ci
+            L.kdn_pool_destroy.argtypes = [vp]
+            L.kdn_pool_destroy.restype = None
+            L.kdn_pool_allocate.argtypes = [vp, vp, vp]
+            L.kdn_pool_allocate.restype = ci
+            L.kdn_pool_fork.argtypes = [vp, ci, vp, vp]
+            L.kdn_pool_fork.restype = ci
+            L.kdn_pool_release.argtypes = [vp, ci]
+            L.kdn_pool_release.restype = ci
+            for nm in ("kdn_pool_active", "kdn_pool_allocated_bytes", "kdn_pool_free_bytes"):
+                fn = getattr(L, nm)
+                fn.argtypes = [vp]
+                fn.restype = i64
             _lib = L
     return _lib
 

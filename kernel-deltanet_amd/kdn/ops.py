@@ -397,3 +397,143 @@ def forward_only(what: str, outputs, inputs):
         return tuple(outputs)
     grads = [t for t in inputs if isinstance(t, torch.Tensor) and t.requires_grad]
     return _ForwardOnly.apply(what, len(outputs), *outputs, *grads)
+
+
+# ------------------------------------------------------------------------------------------------ serving
+
+
+def ragged_step(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, beta: torch.Tensor, decay: Optional[torch.Tensor],
+                cu_seqlens, slots: torch.Tensor, states: torch.Tensor, omega_bf16: torch.Tensor, phase: torch.Tensor,
+                inv_tau: float, normalize: bool = False, rule: int = RULE_DELTA, y: Optional[torch.Tensor] = None,
+                out_dtype: Optional[torch.dtype] = None, workspace: Optional[torch.Tensor] = None,
+                pipelined: bool = True) -> torch.Tensor:
+    """One ragged mixed prefill + decode step (kdn_ragged_step).
+
+    q, k (tokens, H, d_k) and v (tokens, H, d_v) share a dtype; beta, decay (tokens, H) float32 (decay may
+    be None); cu_seqlens: num_seqs + 1 token offsets (host list/array or tensor); slots (num_seqs,) the
+    distinct state slots; states (slots_total, H, D, d_v) float32, any strides, updated in place.
+    Returns y (tokens, H, d_v).
+    """
+    for t, nm in ((q, "q"), (k, "k"), (v, "v"), (beta, "beta"), (states, "states")):
+        require_device(t, f"ragged_step: {nm}")
+    dev = q.device
+    if q.dim() != 3 or k.shape != q.shape or v.dim() != 3 or v.shape[:2] != q.shape[:2] or beta.shape != q.shape[:2]:
+        raise ValueError(f"ragged_step: shapes q{tuple(q.shape)} k{tuple(k.shape)} v{tuple(v.shape)} beta{tuple(beta.shape)}")
+    if k.dtype != q.dtype or v.dtype != q.dtype:
+        raise TypeError("ragged_step: q, k and v must share a dtype")
+    if states.dtype != torch.float32 or states.dim() != 4:
+        raise TypeError("ragged_step: states must be a float32 (slots, H, D, d_v) tensor")
+    cu_host = torch.as_tensor(cu_seqlens, dtype=torch.int64).cpu().contiguous()
+    n = cu_host.numel() - 1
+    if n < 0 or int(cu_host[-1]) > q.shape[0]:
+        raise ValueError("ragged_step: cu_seqlens must hold num_seqs + 1 offsets within the token count")
+    slots_d = torch.as_tensor(slots).to(device=dev, dtype=torch.int32).contiguous()
+    if slots_d.numel() != n:
+        raise ValueError("ragged_step: one slot per sequence")
+    cu_d = cu_host.to(dev)
+    q, k, v = _last_contig(q), _last_contig(k), _last_contig(v)
+    beta = beta.to(torch.float32)
+    if decay is not None:
+        decay = decay.to(device=dev, dtype=torch.float32)
+    T, H = q.shape[:2]
+    d_v = v.shape[-1]
+    if y is None:
+        y = torch.empty(T, H, d_v, device=dev, dtype=q.dtype if out_dtype is None else out_dtype)
+    om = omega_bf16.to(dev).contiguous()
+    ph = phase.to(device=dev, dtype=torch.float32).contiguous()
+    a = N.RaggedArgs()
+    a.num_seqs, a.H = n, H
+    a.d_k, a.D, a.d_v = q.shape[-1], om.shape[0], d_v
+    a.in_dtype, a.out_dtype = _tag(q.dtype, "ragged inputs"), _tag(y.dtype, "ragged output")
+    a.normalize_input, a.rule, a.inv_tau = 1 if normalize else 0, int(rule), float(inv_tau)
+    a.cu_seqlens, a.cu_seqlens_host, a.slots = cu_d.data_ptr(), cu_host.data_ptr(), slots_d.data_ptr()
+    a.q, a.q_stride = q.data_ptr(), N._i64x2(*q.stride()[:2])
+    a.k, a.k_stride = k.data_ptr(), N._i64x2(*k.stride()[:2])
+    a.v, a.v_stride = v.data_ptr(), N._i64x2(*v.stride()[:2])
+    a.beta, a.beta_stride = beta.data_ptr(), N._i64x2(*beta.stride())
+    if decay is not None:
+        a.decay, a.decay_stride = decay.data_ptr(), N._i64x2(*decay.stride())
+    a.omega_bf16, a.phase = om.data_ptr(), ph.data_ptr()
+    a.states, a.state_stride = states.data_ptr(), N._i64x4(*states.stride())
+    a.y, a.y_stride = y.data_ptr(), N._i64x2(*y.stride()[:2])
+    need = int(N.lib().kdn_ragged_workspace_bytes(ctypes.byref(a)))
+    if need == 0:
+        raise ValueError("ragged_step: unsupported shape (kdn_ragged_workspace_bytes returned 0)")
+    if workspace is None or workspace.numel() * workspace.element_size() < need:
+        workspace = torch.empty(need, dtype=torch.uint8, device=dev)
+    a.workspace, a.workspace_bytes = workspace.data_ptr(), workspace.numel() * workspace.element_size()
+    st = torch.cuda.current_stream(dev)
+    with torch.cuda.device(dev):
+        aux = None
+        if pipelined:
+            aux = aux_stream(dev)
+            for t in (q, k, v, beta, decay, om, ph, states, y, workspace, cu_d, slots_d):
+                if t is not None:
+                    t.record_stream(aux)
+        N.check(N.lib().kdn_ragged_step(ctypes.byref(a), ctypes.c_void_p(st.cuda_stream),
+                                        ctypes.c_void_p(aux.cuda_stream) if aux is not None else None),
+                "kdn_ragged_step")
+    return y
+
+
+class StatePool:
+    """Slab state pool (kdn_pool_*): `max_slots` fp32 slots of shape (layers, H, D, d_v) in one device
+    tensor, with slot bookkeeping in the native library.  New slots are zeroed; fork copies a slot."""
+
+    def __init__(self, max_slots: int, layers: int, heads: int, D: int = 512, d_v: int = 64, device="cuda:0",
+                 slab: Optional[torch.Tensor] = None):
+        self.shape = (max_slots, layers, heads, D, d_v)
+        self.device = torch.device(device)
+        self.slab = slab if slab is not None else torch.empty(self.shape, dtype=torch.float32, device=self.device)
+        if tuple(self.slab.shape) != self.shape or not self.slab.is_contiguous() or self.slab.dtype != torch.float32:
+            raise ValueError("StatePool: slab must be a contiguous float32 tensor of shape (slots, layers, H, D, d_v)")
+        self.slot_bytes = layers * heads * D * d_v * 4
+        h = ctypes.c_void_p()
+        N.check(N.lib().kdn_pool_create(max_slots, self.slot_bytes, ctypes.byref(h)), "kdn_pool_create")
+        self._h = h
+
+    def _slab_ptr(self):
+        return ctypes.c_void_p(self.slab.data_ptr()) if self.slab.is_cuda else None
+
+    def _stream(self):
+        return ctypes.c_void_p(torch.cuda.current_stream(self.device).cuda_stream) if self.slab.is_cuda else None
+
+    def allocate(self) -> int:
+        rc = N.lib().kdn_pool_allocate(self._h, self._slab_ptr(), self._stream())
+        if rc == N.KDN_ERR_CAPACITY:
+            return -1
+        N.check(rc if rc < 0 else 0, "kdn_pool_allocate")
+        return rc
+
+    def fork(self, parent: int) -> int:
+        rc = N.lib().kdn_pool_fork(self._h, int(parent), self._slab_ptr(), self._stream())
+        if rc == N.KDN_ERR_CAPACITY:
+            return -1
+        N.check(rc if rc < 0 else 0, "kdn_pool_fork")
+        return rc
+
+    def release(self, slot: int) -> None:
+        N.check(N.lib().kdn_pool_release(self._h, int(slot)), "kdn_pool_release")
+
+    @property
+    def active(self) -> int:
+        return int(N.lib().kdn_pool_active(self._h))
+
+    def allocated_bytes(self) -> int:
+        return int(N.lib().kdn_pool_allocated_bytes(self._h))
+
+    def free_bytes(self) -> int:
+        return int(N.lib().kdn_pool_free_bytes(self._h))
+
+    def layer_states(self, layer: int) -> torch.Tensor:
+        """(slots, H, D, d_v) view of one layer's states, the `states` argument of ragged_step."""
+        return self.slab[:, layer]
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h is not None and h.value:
+            try:
+                N.lib().kdn_pool_destroy(h)
+            except Exception:
+                pass
+            self._h = None

@@ -25,7 +25,7 @@ def lib():
 
 def _declared():
     text = open(HEADER).read()
-    return sorted(set(re.findall(r"^\s*(?:int|size_t|const char\*)\s+(kdn_\w+)\s*\(", text, re.M)))
+    return sorted(set(re.findall(r"^\s*(?:int|int64_t|size_t|void|const char\*)\s+(kdn_\w+)\s*\(", text, re.M)))
 
 
 def test_header_declares_exported_set():
@@ -40,11 +40,12 @@ def test_library_exports_every_declared_symbol(lib):
         assert hasattr(lib, name)
 
 
-def test_scan_args_layout_matches_c():
-    fields = [f[0] for f in N.ScanArgs._fields_]
+@pytest.mark.parametrize("cname,pystruct", [("kdn_scan_args", N.ScanArgs), ("kdn_ragged_args", N.RaggedArgs)])
+def test_args_layout_matches_c(cname, pystruct):
+    fields = [f[0] for f in pystruct._fields_]
     src = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', "int main(void){",
-           'printf("%zu\\n", sizeof(kdn_scan_args));']
-    src += [f'printf("%zu\\n", offsetof(kdn_scan_args, {f}));' for f in fields]
+           f'printf("%zu\\n", sizeof({cname}));']
+    src += [f'printf("%zu\\n", offsetof({cname}, {f}));' for f in fields]
     src += ["return 0;}"]
     with tempfile.TemporaryDirectory() as d:
         c = os.path.join(d, "layout.c")
@@ -52,15 +53,15 @@ def test_scan_args_layout_matches_c():
         open(c, "w").write("\n".join(src))
         subprocess.run(["gcc", "-std=c99", "-o", exe, c], check=True)
         vals = [int(x) for x in subprocess.run([exe], capture_output=True, text=True, check=True).stdout.split()]
-    assert vals[0] == ctypes.sizeof(N.ScanArgs)
+    assert vals[0] == ctypes.sizeof(pystruct)
     for f, off in zip(fields, vals[1:]):
-        assert getattr(N.ScanArgs, f).offset == off, f
+        assert getattr(pystruct, f).offset == off, f
 
 
 def test_strerror_and_version(lib):
     for code in (0, -1, -2, -3, -4, -5, -99):
         assert len(lib.kdn_strerror(code)) > 0
-    assert lib.kdn_abi_version() == (1 << 16) | 1
+    assert lib.kdn_abi_version() == (1 << 16) | 2
 
 
 def _args(**kw):
