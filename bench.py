@@ -102,9 +102,10 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", type=int, default=3, choices=(2, 3, 4),
+    ap.add_argument("--config", type=int, default=3, choices=(2, 3, 4, 5),
                     help="3: one layer B=1 H=16 T=64k (default, the headline); 4: B=32 streams (use --T for "
-                         "the sweep 4096/16384/65536); 2: the standalone lift of 2,097,152 rows")
+                         "the sweep 4096/16384/65536); 2: the standalone lift of 2,097,152 rows; 5: the ragged "
+                         "mixed step, 224 decode + 32 prefill sequences over resident states")
     ap.add_argument("--B", type=int, default=None)
     ap.add_argument("--H", type=int, default=16)
     ap.add_argument("--T", type=int, default=None)
@@ -136,6 +137,8 @@ def main():
         return
     if args.config == 2:
         return bench_lift(args, dev)
+    if args.config == 5:
+        return bench_serving(args, dev)
     return bench_scan(args, dev)
 
 
@@ -263,6 +266,82 @@ def bench_scan(args, dev):
     print(json.dumps(out), flush=True)
 
 
+def bench_serving(args, dev):
+    """Config 5: one ragged mixed step over 256 sequences, 224 single-token decodes (rank-1 update of a
+    resident [16, 512, 64] fp32 state in a slab pool) and 32 prefills with lengths uniform in
+    [512, 8192]; H=16, D=512, d_v=64, bf16 q/k/v ~ N(0,1), beta = sigmoid(N(0,1)), lambda = 1."""
+    from kdn import ops
+    from kernels import FastWalshHadamardProjection
+
+    H, D, dv, n_dec, n_pre = args.H, 512, args.dv, 224, 32
+    g = torch.Generator().manual_seed(1234)
+    pre_lens = torch.randint(512, 8193, (n_pre,), generator=g)
+    lens = torch.cat([torch.ones(n_dec, dtype=torch.int64), pre_lens])
+    T = int(lens.sum())
+    cu = torch.cat([torch.zeros(1, dtype=torch.int64), torch.cumsum(lens, 0)])
+    gd = torch.Generator(device=dev).manual_seed(1234)
+    q = torch.randn(T, H, 64, generator=gd, device=dev).to(torch.bfloat16)
+    k = torch.randn(T, H, 64, generator=gd, device=dev).to(torch.bfloat16)
+    v = torch.randn(T, H, dv, generator=gd, device=dev).to(torch.bfloat16)
+    beta = torch.sigmoid(torch.randn(T, H, generator=gd, device=dev))
+    pool = ops.StatePool(n_dec + n_pre, 1, H, D, dv, device=dev)
+    slots = torch.tensor([pool.allocate() for _ in range(n_dec + n_pre)], dtype=torch.int32)
+    pool.slab.normal_(generator=gd).mul_(0.01)
+    states = pool.layer_states(0)
+    proj = FastWalshHadamardProjection(64, D, 42)
+    om, ph = proj.device_omega(dev), proj.device_phase(dev)
+    y = torch.empty(T, H, dv, device=dev, dtype=torch.bfloat16)
+    stream = torch.cuda.current_stream(dev)
+
+    def timed(cu_, slots_, q_, k_, v_, b_, y_, steps):
+        # batch metadata staged on the device once, as a serving loop keeps it
+        cu_d, slots_d = cu_.to(dev), slots_.to(dev)
+        call = lambda: ops.ragged_step(q_, k_, v_, b_, None, cu_, slots_d, states, om, ph, proj.tau_star_inv, y=y_,
+                                       cu_seqlens_device=cu_d)
+        for _ in range(args.warmup):
+            call()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(steps):
+            call()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / steps
+
+    ms = timed(cu, slots, q, k, v, beta, y, args.steps)
+    # the two parts alone: the decode tokens (rows 0..223) and the prefill tokens (rows 224..)
+    ms_dec = timed(cu[: n_dec + 1], slots[:n_dec], q, k, v, beta, y, args.steps)
+    cu_pre = cu[n_dec:] - n_dec
+    ms_pre = timed(cu_pre, slots[n_dec:], q[n_dec:], k[n_dec:], v[n_dec:], beta[n_dec:], y[n_dec:], args.steps)
+    dec_bytes = n_dec * H * (2 * D * dv * 4 + (2 * 64 + 2 * dv) * 2 + 4)
+    dec_gbs = dec_bytes / (ms_dec / 1e3) / 1e9
+    pre_tokens = int(pre_lens.sum())
+    fl = flops_per_chunk(D, dv)
+    pre_flops = sum(((int(L) + C - 1) // C) for L in pre_lens) * H * fl["total"]
+    pre_tflops = pre_flops / (ms_pre / 1e3) / 1e12
+    out = {
+        "metric": "ragged mixed prefill+decode step tokens/s (config 5); % of HBM (decode) / MFMA (prefill) roofline",
+        "value": T / (ms / 1e3), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": f"synthetic (seeded N(0,1) q/k/v, sigmoid(N(0,1)) beta, N(0,1)*0.01 resident states; prefill "
+                f"lengths U[512, 8192], {pre_tokens} prefill tokens)",
+        "config": {"workload": f"config5: ragged mixed step, {n_dec} decode + {n_pre} prefill sequences, H={H}, D={D}, "
+                               f"d_v={dv}, fp32 states in a slab pool, lambda=1", "tokens": T, "parallelism": "single GPU"},
+        "roofline": ({"bound": "mfma", "achieved": pre_tflops, "peak": MFMA_BF16_PEAK / 1e12, "unit": "TFLOP/s",
+                      "frac": pre_tflops * 1e12 / MFMA_BF16_PEAK, "traffic": None, "kernel": "prefill (scan)"}
+                     if ms_pre >= ms_dec else
+                     {"bound": "hbm", "achieved": dec_gbs, "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+                      "frac": dec_gbs * 1e9 / HBM_PEAK, "traffic": None, "kernel": "decode"}),
+        "parts": {"decode": {"ms": ms_dec, "sequences": n_dec, "alg_bytes": dec_bytes, "GBps": dec_gbs,
+                             "hbm_frac": dec_gbs * 1e9 / HBM_PEAK},
+                  "prefill": {"ms": ms_pre, "sequences": n_pre, "tokens": pre_tokens, "alg_flops": pre_flops,
+                              "tflops": pre_tflops, "mfma_frac": pre_tflops * 1e12 / MFMA_BF16_PEAK}},
+        "cpu_baseline": None,
+    }
+    print(json.dumps(out), flush=True)
+
+
 def bench_lift(args, dev):
     """Config 2: the standalone lift (kdn_fwht_lift) of x [B*T*H, 64] bf16 ~ N(0,1), B=8, T=16384, H=16,
     L2-normalised per row, to D=512 bf16.  HBM-bound: algorithmic bytes = rows * (64 + 512) * 2."""
@@ -291,6 +370,12 @@ def bench_lift(args, dev):
     ms = sorted(a.elapsed_time(b) for a, b in evs)[len(evs) // 2]
     alg_bytes = rows * (64 + D) * 2
     achieved = alg_bytes / (ms / 1e3) / 1e9
+    pmc = read_pmc(args.pmc or os.path.join(REPO, "profiles", "pmc_config2.txt")) if rows == 2097152 else {}
+    traffic = None
+    if all(k in pmc for k in ("lift_fetch_kib", "lift_write_kib", "copy_fetch_kib", "copy_write_kib")):
+        copy_bytes = pmc.get("copy_bytes", 256 << 20)
+        traffic = (pmc["lift_fetch_kib"] * copy_bytes / pmc["copy_fetch_kib"]
+                   + pmc["lift_write_kib"] * copy_bytes / pmc["copy_write_kib"])
     out = {
         "metric": "standalone lift rows/s (config 2); % of HBM roofline",
         "value": rows / (ms / 1e3), "unit": "rows/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
@@ -299,7 +384,7 @@ def bench_lift(args, dev):
         "config": {"workload": f"config2: standalone lift, x [{rows}, 64] bf16 L2-normalised -> [{rows}, 512] bf16 "
                                f"(B={B}, T={T}, H={args.H})", "rows": rows, "D": D, "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK / 1e9, "unit": "GB/s",
-                     "frac": achieved * 1e9 / HBM_PEAK, "traffic": None, "kernel": "lift"},
+                     "frac": achieved * 1e9 / HBM_PEAK, "traffic": traffic, "kernel": "lift"},
     }
     if args.cpu_tokens > 0:
         from oracle import lift as ol

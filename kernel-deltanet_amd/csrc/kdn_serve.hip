@@ -100,7 +100,8 @@ __device__ __forceinline__ float wave_sum(float v) {
 //   2. the lift, thread t computing features t, t + NT, ...: fp32 dot products with the bf16 Omega rows,
 //      c = cos(2 pi frac(x.Omega_f inv_tau / 2 pi + phase_f / 2 pi)), and the renormalisation of
 //      sqrt(2/D) c from the block's sum of squares;
-//   3. thread (g, j) holds state elements S[f][j] for its feature group g (FPT features): partial
+//   3. thread (g, j) holds state elements S[f][j] for its feature group g (FPT features, loaded before
+//      step 1 so that their latency overlaps the lift): partial
 //      S^T phi(k) and S^T phi(q) per group, summed in LDS in group order; y = S^T phi(q) (before the
 //      update); S[f][j] <- lambda S[f][j] + beta phi_k[f] (v_j - lambda u_j)  (delta rule), or
 //      lambda S[f][j] + beta phi_k[f] v_j (linear rule); written back in place.
@@ -120,6 +121,17 @@ __global__ void __launch_bounds__(DecodeThreads<DV>::value) decode_kernel(Decode
   const int64_t i = blockIdx.x, h = blockIdx.y, c0 = (int64_t)blockIdx.z * DV;
   const int64_t row = p.rows[i];
   const int64_t sl = p.slots[i];
+
+  // The state elements of thread (g, j) and its scalar inputs are loaded first: they do not depend on
+  // the lift, so their memory latency overlaps it.
+  const int j = t % DV, g = t / DV;
+  float* sp = p.states + sl * p.ss0 + h * p.ss1 + (int64_t)(g * FPT) * p.ss2 + (c0 + j) * p.ss3;
+  float S[FPT];
+#pragma unroll
+  for (int l = 0; l < FPT; ++l) S[l] = sp[l * p.ss2];
+  const float be = p.beta[row * p.bs0 + h * p.bs1];
+  const float la = p.decay ? fminf(fmaxf(p.decay[row * p.ds0 + h * p.ds1], 1e-5f), 1.f) : 1.f;
+  const float vin = (float)((const InT*)p.v)[row * p.vs0 + h * p.vs1 + c0 + j];
 
   // 1. inputs (waves 0 and 1: q and k)
   if (t < 2 * SRV_DK) {
@@ -178,13 +190,9 @@ __global__ void __launch_bounds__(DecodeThreads<DV>::value) decode_kernel(Decode
   const float sck = amp / (amp * sqrtf(tot[1]) + 1e-8f);
 
   // 3. state pass
-  const int j = t % DV, g = t / DV;
-  float* sp = p.states + sl * p.ss0 + h * p.ss1 + (int64_t)(g * FPT) * p.ss2 + (c0 + j) * p.ss3;
-  float S[FPT];
   float pu = 0.f, py = 0.f;
 #pragma unroll
   for (int l = 0; l < FPT; ++l) {
-    S[l] = sp[l * p.ss2];
     pu += S[l] * s_c[1][g * FPT + l];
     py += S[l] * s_c[0][g * FPT + l];
   }
@@ -200,9 +208,6 @@ __global__ void __launch_bounds__(DecodeThreads<DV>::value) decode_kernel(Decode
   u *= sck;
   yv *= scq;
   if (g == 0) ((OutT*)p.y)[row * p.ys0 + h * p.ys1 + c0 + j] = (OutT)yv;
-  const float be = p.beta[row * p.bs0 + h * p.bs1];
-  const float la = p.decay ? fminf(fmaxf(p.decay[row * p.ds0 + h * p.ds1], 1e-5f), 1.f) : 1.f;
-  const float vin = (float)((const InT*)p.v)[row * p.vs0 + h * p.vs1 + c0 + j];
   const float coef = be * sck * (p.linear ? vin : vin - la * u);  // times c_k[f]
 #pragma unroll
   for (int l = 0; l < FPT; ++l) sp[l * p.ss2] = la * S[l] + coef * s_c[1][g * FPT + l];

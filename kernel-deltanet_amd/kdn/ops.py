@@ -406,12 +406,14 @@ def ragged_step(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, beta: torch.T
                 cu_seqlens, slots: torch.Tensor, states: torch.Tensor, omega_bf16: torch.Tensor, phase: torch.Tensor,
                 inv_tau: float, normalize: bool = False, rule: int = RULE_DELTA, y: Optional[torch.Tensor] = None,
                 out_dtype: Optional[torch.dtype] = None, workspace: Optional[torch.Tensor] = None,
-                pipelined: bool = True) -> torch.Tensor:
+                pipelined: bool = True, cu_seqlens_device: Optional[torch.Tensor] = None) -> torch.Tensor:
     """One ragged mixed prefill + decode step (kdn_ragged_step).
 
     q, k (tokens, H, d_k) and v (tokens, H, d_v) share a dtype; beta, decay (tokens, H) float32 (decay may
     be None); cu_seqlens: num_seqs + 1 token offsets (host list/array or tensor); slots (num_seqs,) the
     distinct state slots; states (slots_total, H, D, d_v) float32, any strides, updated in place.
+    A serving loop that keeps its batch metadata on the device passes slots as a device int32 tensor and
+    cu_seqlens_device (the same offsets, device int64); nothing is then copied to the device per call.
     Returns y (tokens, H, d_v).
     """
     for t, nm in ((q, "q"), (k, "k"), (v, "v"), (beta, "beta"), (states, "states")):
@@ -430,7 +432,12 @@ def ragged_step(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, beta: torch.T
     slots_d = torch.as_tensor(slots).to(device=dev, dtype=torch.int32).contiguous()
     if slots_d.numel() != n:
         raise ValueError("ragged_step: one slot per sequence")
-    cu_d = cu_host.to(dev)
+    if cu_seqlens_device is not None:
+        if cu_seqlens_device.device != dev or cu_seqlens_device.dtype != torch.int64 or cu_seqlens_device.numel() != n + 1:
+            raise ValueError("ragged_step: cu_seqlens_device must be the int64 offsets on the inputs' device")
+        cu_d = cu_seqlens_device.contiguous()
+    else:
+        cu_d = cu_host.to(dev)
     q, k, v = _last_contig(q), _last_contig(k), _last_contig(v)
     beta = beta.to(torch.float32)
     if decay is not None:
