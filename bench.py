@@ -182,14 +182,19 @@ def bench_scan(args, dev):
         a1.record(st)
         timed[kind].append((a0, a1))
 
+    nbuf = max(1, plan.workspace.numel() // plan.seg_bytes)
     for _ in range(args.steps):
         if plan.pipelined:
-            aux = ops.aux_stream(dev)
+            # the library's three-stream schedule: state on the launch stream, prep and output on two
+            # auxiliary streams; prep into a reused buffer waits for that buffer's last output
+            aux, aux_o = ops.aux_stream(dev, 0), ops.aux_stream(dev, 1)
             ev_in = torch.cuda.Event()
             ev_in.record(stream)
             aux.wait_event(ev_in)
+            aux_o.wait_event(ev_in)
             ev_p = [torch.cuda.Event() for _ in segs]
             ev_s = [torch.cuda.Event() for _ in segs]
+            ev_o = [torch.cuda.Event() for _ in segs]
             launch("prep", 0, aux)
             ev_p[0].record(aux)
             for s_ in range(len(segs)):
@@ -197,12 +202,15 @@ def bench_scan(args, dev):
                 launch("state", s_, stream)
                 ev_s[s_].record(stream)
                 if s_ + 1 < len(segs):
+                    if s_ + 1 >= nbuf:
+                        aux.wait_event(ev_o[s_ + 1 - nbuf])
                     launch("prep", s_ + 1, aux)
                     ev_p[s_ + 1].record(aux)
-                aux.wait_event(ev_s[s_])
-                launch("output", s_, aux)
+                aux_o.wait_event(ev_s[s_])
+                launch("output", s_, aux_o)
+                ev_o[s_].record(aux_o)
             ev_out = torch.cuda.Event()
-            ev_out.record(aux)
+            ev_out.record(aux_o)
             stream.wait_event(ev_out)
         else:
             for s_ in range(len(segs)):
@@ -247,8 +255,8 @@ def bench_scan(args, dev):
         "config": {"workload": f"{name}, B={B}, H={H}, T={T}, d_k=64->D={D}, "
                                f"d_v={dv}, chunk 64, bf16 q/k/v, fp32 beta and state, lambda=1",
                    "B": B, "H": H, "T": T, "D": D, "d_v": dv, "chunk": C, "segment_chunks": seg,
-                   "schedule": "pipelined (state chain on the launch stream, prep/output on an auxiliary stream)"
-                   if plan.pipelined else "serial", "parallelism": "single GPU"},
+                   "schedule": "pipelined (state chain on the launch stream, prep and output on two auxiliary "
+                               "streams)" if plan.pipelined else "serial", "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "achieved": achieved, "peak": MFMA_BF16_PEAK / 1e12, "unit": "TFLOP/s",
                      "frac": achieved / (MFMA_BF16_PEAK / 1e12), "traffic": traffic, "kernel": dom},
         "phases": phases,

@@ -173,6 +173,11 @@ int kdn_delta_scan_fwd_pipelined(const kdn_scan_args* a, void* stream, void* aux
  * has fewer segments); 0 if the arguments are invalid. */
 size_t kdn_scan_workspace_bytes_pipelined(const kdn_scan_args* a);
 
+/* kdn_delta_scan_fwd_pipelined with the prep kernels on prep_stream and the output kernels on their own
+ * output_stream (three streams), so that neither waits behind the other; same workspace and results.
+ * output_stream NULL (or equal to another stream) falls back to kdn_delta_scan_fwd_pipelined. */
+int kdn_delta_scan_fwd_streams(const kdn_scan_args* a, void* stream, void* prep_stream, void* output_stream);
+
 int kdn_scan_prep(const kdn_scan_args* a, int64_t chunk0, int64_t nchunks, void* stream);
 int kdn_scan_state(const kdn_scan_args* a, int64_t chunk0, int64_t nchunks, void* stream);
 int kdn_scan_output(const kdn_scan_args* a, int64_t chunk0, int64_t nchunks, void* stream);

@@ -30,10 +30,11 @@ inline int device_cus() {
 
 constexpr size_t CU_LDS_BYTES = 160 * 1024;  // LDS per CU on gfx950
 
-// The pipelined scan of kdn_delta_scan_fwd_pipelined, with ragged sequences optionally given as
-// device start / end arrays (sequence b = token rows seq_lo[b] .. seq_hi[b]-1) instead of cu_seqlens.
+// The pipelined scan of kdn_delta_scan_fwd_pipelined / _streams (out_stream NULL: output kernels on
+// aux_stream), with ragged sequences optionally given as device start / end arrays (sequence b = token
+// rows seq_lo[b] .. seq_hi[b]-1) instead of cu_seqlens.
 int scan_pipelined(const kdn_scan_args* a, const int64_t* seq_lo, const int64_t* seq_hi, void* stream,
-                   void* aux_stream);
+                   void* aux_stream, void* out_stream);
 size_t scan_workspace_bytes_pipelined(const kdn_scan_args* a);
 
 }  // namespace kdn

@@ -183,9 +183,9 @@ __device__ __forceinline__ void lift_tile(const RawRow<InT> (&raw)[NX], int norm
     split_frag<NSPLIT>(xv[x][1], xb[x][1]);
     ss[x] = 0.f;
   }
-#pragma unroll
-  for (int t = 0; t < NT; ++t) {
-    f32x4 acc[NX];
+  // Feature tile t: acc[x] = x . Omega[16t .. 16t+16)^T.  Software-pipelined: the MFMAs of tile t+1 are
+  // issued in the scheduling region of the cosines of tile t.
+  auto project = [&](int t, f32x4 (&acc)[NX]) {
 #pragma unroll
     for (int x = 0; x < NX; ++x) acc[x] = zero4();
 #pragma unroll
@@ -205,6 +205,16 @@ __device__ __forceinline__ void lift_tile(const RawRow<InT> (&raw)[NX], int norm
           for (int x = 0; x < NX; ++x) acc[x] = PrecBF16::mma(acc[x], alo, xb[x][kb][s]);
       }
     }
+  };
+  f32x4 acc[NX];
+  project(0, acc);
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    // one feature tile per scheduling region: hoisting the Omega reads of every tile to the top
+    // would hold them all in registers at once
+    __builtin_amdgcn_sched_barrier(0);
+    f32x4 next[NX];
+    if (t + 1 < NT) project(t + 1, next);
     const f32x4 ph = *reinterpret_cast<const f32x4*>(&s_phrev[16 * t + 4 * (lane >> 4)]);
 #pragma unroll
     for (int x = 0; x < NX; ++x)
@@ -214,6 +224,10 @@ __device__ __forceinline__ void lift_tile(const RawRow<InT> (&raw)[NX], int norm
         ss[x] += c * c;
         P::set(out[x][t >> 1], (t & 1) * 4 + i, c);
       }
+    if (t + 1 < NT) {
+#pragma unroll
+      for (int x = 0; x < NX; ++x) acc[x] = next[x];
+    }
   }
 #pragma unroll
   for (int x = 0; x < NX; ++x) ss[x] = sum_over_lane_groups(ss[x]);
@@ -549,7 +563,7 @@ struct StateOps {
   static constexpr int TPW = D / 64;   // feature tiles per wave
   static constexpr int JPW = D / 128;  // 32-deep feature blocks per wave
   static constexpr int NV = DV / 16;
-  static constexpr int L2_AHEAD = 6;  // chunks ahead of the current one that the L2 prefetch touches
+  static constexpr int L2_AHEAD = 3;  // chunks ahead of the current one that the L2 prefetch touches (3 measured best of 1, 3, 6)
   // dword loads per wave that cover the operand area [0, Sfr) of one chunk record at one per line
   static constexpr int L2_LOADS = (int)((L::Sfr / 128 + 4 * NV * 64 - 1) / (4 * NV * 64));
   struct Small {
@@ -1008,6 +1022,7 @@ struct RunSpec {
   hipStream_t aux;   // non-null: pipelined over `nbuf` buffers of `buf_bytes`
   int nbuf;
   size_t buf_bytes;
+  hipStream_t aux_out = nullptr;  // non-null and not aux: output kernels on their own stream
   // ragged sequences given as separate start / end arrays (device), overriding cu_seqlens
   const int64_t* seq_lo = nullptr;
   const int64_t* seq_hi = nullptr;
@@ -1093,31 +1108,37 @@ struct EventSet {
     return KDN_OK;
   }
   ~EventSet() {
-    for (int i = 0; i < n; ++i) hipEventDestroy(ev[i]);
+    for (int i = 0; i < n; ++i) (void)hipEventDestroy(ev[i]);
   }
 };
 
 // Segments rotate through `nbuf` workspace buffers.  The state chain runs on `st` (the caller's stream);
-// prep and output run on `aux`, in the order prep(s+1), output(s), so that while state(s) occupies its
-// B*H*d_v/16 workgroups the other CUs prepare the next segment and finish the previous one.
-//   state(s)  waits for prep(s)        (event P[s % nbuf])
-//   output(s) waits for state(s)       (event S[s % nbuf])
-//   prep(s)   reuses the buffer of segment s - nbuf, whose output ran earlier on aux
-// aux first waits for the work already queued on st, and st finally waits for the last output.
+// prep runs on `aux` and output on `aux_out` (the same stream as prep when only one auxiliary stream is
+// given, in the order prep(s+1), output(s)), so that while state(s) occupies its B*H*d_v/16 workgroups the
+// other CUs prepare the next segment and finish the previous one.
+//   state(s)  waits for prep(s)          (event P[s % nbuf])
+//   output(s) waits for state(s)         (event S[s % nbuf])
+//   prep(s)   reuses the buffer of segment s - nbuf: on a separate output stream it waits for that
+//             segment's output (event O[s % nbuf]); on one auxiliary stream the order ensures it
+// the auxiliary streams first wait for the work already queued on st, and st finally waits for the last
+// output.
 template <class P, typename InT, typename OutT, int D, int DV>
 static int run_pipelined(const kdn_scan_args* a, const RunSpec& r) {
   const int64_t seg = r.seg;
   const int nbuf = r.nbuf;
   const size_t buf_bytes = r.buf_bytes;
   const hipStream_t st = r.st, aux = r.aux;
+  const hipStream_t aux_out = r.aux_out ? r.aux_out : r.aux;
+  const bool split = aux_out != aux;
   const int64_t nchunks = (a->T + CH - 1) / CH;
   const int64_t nsegs = (nchunks + seg - 1) / seg;
   EventSet evs;
-  int rc = evs.create(2 * nbuf + 2);
+  int rc = evs.create(3 * nbuf + 2);
   if (rc != KDN_OK) return rc;
   hipEvent_t* evP = evs.ev;
   hipEvent_t* evS = evs.ev + nbuf;
-  hipEvent_t evIn = evs.ev[2 * nbuf], evOut = evs.ev[2 * nbuf + 1];
+  hipEvent_t* evO = evs.ev + 2 * nbuf;
+  hipEvent_t evIn = evs.ev[3 * nbuf], evOut = evs.ev[3 * nbuf + 1];
   // prep shares the device with the state kernel's workgroups (one per CU)
   const int prep_cus = device_cus() - (int)state_grid(a->B, a->H, DV / 16);
   auto seg_p = [&](int64_t s) {
@@ -1129,6 +1150,7 @@ static int run_pipelined(const kdn_scan_args* a, const RunSpec& r) {
 #define KDN_TRYK(x) do { const int _rc = (x); if (_rc != KDN_OK) return _rc; } while (0)
   KDN_TRY(hipEventRecord(evIn, st));
   KDN_TRY(hipStreamWaitEvent(aux, evIn, 0));
+  if (split) KDN_TRY(hipStreamWaitEvent(aux_out, evIn, 0));
   KDN_TRYK((launch_phase<P, InT, OutT, D, DV>(seg_p(0), PHASE_PREP, aux)));
   KDN_TRY(hipEventRecord(evP[0], aux));
   for (int64_t s = 0; s < nsegs; ++s) {
@@ -1137,13 +1159,15 @@ static int run_pipelined(const kdn_scan_args* a, const RunSpec& r) {
     KDN_TRYK((launch_phase<P, InT, OutT, D, DV>(ps, PHASE_STATE, st)));
     KDN_TRY(hipEventRecord(evS[s % nbuf], st));
     if (s + 1 < nsegs) {
+      if (split && s + 1 >= nbuf) KDN_TRY(hipStreamWaitEvent(aux, evO[(s + 1) % nbuf], 0));
       KDN_TRYK((launch_phase<P, InT, OutT, D, DV>(seg_p(s + 1), PHASE_PREP, aux)));
       KDN_TRY(hipEventRecord(evP[(s + 1) % nbuf], aux));
     }
-    KDN_TRY(hipStreamWaitEvent(aux, evS[s % nbuf], 0));
-    KDN_TRYK((launch_phase<P, InT, OutT, D, DV>(ps, PHASE_OUTPUT, aux)));
+    KDN_TRY(hipStreamWaitEvent(aux_out, evS[s % nbuf], 0));
+    KDN_TRYK((launch_phase<P, InT, OutT, D, DV>(ps, PHASE_OUTPUT, aux_out)));
+    if (split) KDN_TRY(hipEventRecord(evO[s % nbuf], aux_out));
   }
-  KDN_TRY(hipEventRecord(evOut, aux));
+  KDN_TRY(hipEventRecord(evOut, aux_out));
   KDN_TRY(hipStreamWaitEvent(st, evOut, 0));
 #undef KDN_TRY
 #undef KDN_TRYK
@@ -1288,7 +1312,7 @@ namespace kdn {
 // The pipelined scan (serial when aux_stream is NULL or the workspace holds one segment buffer), with
 // ragged sequences optionally given as device start / end arrays.
 int scan_pipelined(const kdn_scan_args* a, const int64_t* seq_lo, const int64_t* seq_hi, void* stream,
-                   void* aux_stream) {
+                   void* aux_stream, void* out_stream) {
   int rc = validate_launch(a);
   if (rc != KDN_OK) return rc;
   const int64_t seg = pipeline_segment(a);
@@ -1301,7 +1325,11 @@ int scan_pipelined(const kdn_scan_args* a, const int64_t* seq_lo, const int64_t*
   RunSpec r = {0, nchunks, seg, PHASE_ALL, as_stream(stream), as_stream(aux_stream), nbuf, buf};
   r.seq_lo = seq_lo;
   r.seq_hi = seq_hi;
-  if (!aux_stream || aux_stream == stream || nbuf < 2 || nsegs < 2) r.aux = nullptr;
+  if (out_stream && out_stream != stream && out_stream != aux_stream) r.aux_out = as_stream(out_stream);
+  if (!aux_stream || aux_stream == stream || nbuf < 2 || nsegs < 2) {
+    r.aux = nullptr;
+    r.aux_out = nullptr;
+  }
   return dispatch(a, r);
 }
 
@@ -1315,7 +1343,11 @@ size_t scan_workspace_bytes_pipelined(const kdn_scan_args* a) {
 }  // namespace kdn
 
 extern "C" int kdn_delta_scan_fwd_pipelined(const kdn_scan_args* a, void* stream, void* aux_stream) {
-  return scan_pipelined(a, nullptr, nullptr, stream, aux_stream);
+  return scan_pipelined(a, nullptr, nullptr, stream, aux_stream, nullptr);
+}
+
+extern "C" int kdn_delta_scan_fwd_streams(const kdn_scan_args* a, void* stream, void* prep_stream, void* output_stream) {
+  return scan_pipelined(a, nullptr, nullptr, stream, prep_stream, output_stream);
 }
 
 extern "C" int kdn_scan_prep(const kdn_scan_args* a, int64_t chunk0, int64_t nchunks, void* stream) {

@@ -344,7 +344,7 @@ extern "C" int kdn_ragged_step(const kdn_ragged_args* a, void* stream, void* aux
     s.state_slots = pre_slot;
     s.workspace = w;
     s.workspace_bytes = a->workspace_bytes - (size_t)(w - (unsigned char*)a->workspace);
-    rc = scan_pipelined(&s, pre_lo, pre_hi, stream, aux_stream);
+    rc = scan_pipelined(&s, pre_lo, pre_hi, stream, aux_stream, nullptr);
     if (rc != KDN_OK) return rc;
   }
   return KDN_OK;

@@ -30,6 +30,7 @@ EXPORTED = (
     "kdn_scan_output",
     "kdn_scan_workspace_bytes_pipelined",
     "kdn_delta_scan_fwd_pipelined",
+    "kdn_delta_scan_fwd_streams",
     "kdn_ragged_workspace_bytes",
     "kdn_ragged_step",
     "kdn_pool_create",
@@ -147,6 +148,8 @@ def lib() -> ctypes.CDLL:
             L.kdn_scan_workspace_bytes_pipelined.restype = sz
             L.kdn_delta_scan_fwd_pipelined.argtypes = [ctypes.POINTER(ScanArgs), vp, vp]
             L.kdn_delta_scan_fwd_pipelined.restype = ci
+            L.kdn_delta_scan_fwd_streams.argtypes = [ctypes.POINTER(ScanArgs), vp, vp, vp]
+            L.kdn_delta_scan_fwd_streams.restype = ci
             for nm in ("kdn_scan_prep", "kdn_scan_state", "kdn_scan_output"):
                 fn = getattr(L, nm)
                 fn.argtypes = [ctypes.POINTER(ScanArgs), i64, i64, vp]

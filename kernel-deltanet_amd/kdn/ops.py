@@ -197,28 +197,31 @@ def scan_workspace_bytes(q, v, omega_bf16, segment_chunks: int = 0, pipelined: b
 _AUX_STREAMS = {}
 
 
-def aux_stream(dev: torch.device) -> torch.cuda.Stream:
-    """The per-device auxiliary stream of the pipelined scan (default priority), created once."""
+def aux_stream(dev: torch.device, which: int = 0) -> torch.cuda.Stream:
+    """Auxiliary stream `which` of a device (0: prep kernels, 1: output kernels of the pipelined scan),
+    created once, default priority."""
     idx = dev.index if dev.index is not None else torch.cuda.current_device()
-    st = _AUX_STREAMS.get(idx)
+    st = _AUX_STREAMS.get((idx, which))
     if st is None:
         st = torch.cuda.Stream(device=idx)
-        _AUX_STREAMS[idx] = st
+        _AUX_STREAMS[(idx, which)] = st
     return st
 
 
 def _launch_scan(a, dev: torch.device, pipelined: bool, keep=()):
-    """kdn_delta_scan_fwd, or the pipelined variant with prep/output on the auxiliary stream.  Tensors
-    the auxiliary stream reads or writes are marked with record_stream so the caching allocator does not
-    hand their memory out again before that work has finished."""
+    """kdn_delta_scan_fwd, or the pipelined three-stream variant (kdn_delta_scan_fwd_streams: prep and
+    output on two auxiliary streams).  Tensors the auxiliary streams read or write are marked with
+    record_stream so the caching allocator does not hand their memory out again before that work ends."""
     st = torch.cuda.current_stream(dev)
     if pipelined:
-        aux = aux_stream(dev)
+        aux_p, aux_o = aux_stream(dev, 0), aux_stream(dev, 1)
         for t in keep:
             if t is not None:
-                t.record_stream(aux)
-        N.check(N.lib().kdn_delta_scan_fwd_pipelined(ctypes.byref(a), ctypes.c_void_p(st.cuda_stream),
-                                                     ctypes.c_void_p(aux.cuda_stream)), "kdn_delta_scan_fwd_pipelined")
+                t.record_stream(aux_p)
+                t.record_stream(aux_o)
+        N.check(N.lib().kdn_delta_scan_fwd_streams(ctypes.byref(a), ctypes.c_void_p(st.cuda_stream),
+                                                   ctypes.c_void_p(aux_p.cuda_stream),
+                                                   ctypes.c_void_p(aux_o.cuda_stream)), "kdn_delta_scan_fwd_streams")
     else:
         N.check(N.lib().kdn_delta_scan_fwd(ctypes.byref(a), ctypes.c_void_p(st.cuda_stream)), "kdn_delta_scan_fwd")
 
@@ -230,8 +233,8 @@ def scan(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, beta: torch.Tensor, 
          workspace: Optional[torch.Tensor] = None, segment_chunks: int = 0,
          pipelined: bool = True, features: Optional[FeatureMap] = None,
          rule: int = RULE_DELTA) -> Tuple[torch.Tensor, torch.Tensor]:
-    """Chunked delta-rule prefill over (B, T, H, d) views (kdn_delta_scan_fwd_pipelined, or
-    kdn_delta_scan_fwd with pipelined=False).
+    """Chunked delta-rule prefill over (B, T, H, d) views (kdn_delta_scan_fwd_streams: the state chain on
+    the current stream, prep and output on two auxiliary streams; kdn_delta_scan_fwd with pipelined=False).
 
     q, k (B, T, H, d_k) and v (B, T, H, d_v) share a dtype; beta, decay (B, T, H) are float32 (decay may
     be None for lambda = 1); initial_state/final_state are (B, H, D, d_v) float32 views with any strides.

@@ -201,8 +201,8 @@ def test_config3_full_length(proj, oproj):
 
 @pytest.mark.parametrize("seg,decay_kind", [(4, "none"), (16, "sigmoid"), (7, "narrow")])
 def test_pipelined_equals_serial(proj, seg, decay_kind):
-    """kdn_delta_scan_fwd_pipelined (prep/output on an auxiliary stream, segments rotating through up to
-    three workspace buffers) runs the same kernels as the serial schedule: results are bit-identical."""
+    """kdn_delta_scan_fwd_streams (prep and output on two auxiliary streams, segments rotating through up
+    to three workspace buffers) runs the same kernels as the serial schedule: results are bit-identical."""
     q, k, v, beta, decay = make_inputs(1, 64 * 40 + 17, 3, 64, torch.bfloat16, decay_kind, seed=seg)
     S0 = 0.1 * torch.randn(1, 3, 512, 64, generator=torch.Generator().manual_seed(7))
     y1, S1 = run(proj, q, k, v, beta, decay, initial_state=S0, segment_chunks=seg, pipelined=True)
@@ -210,6 +210,27 @@ def test_pipelined_equals_serial(proj, seg, decay_kind):
     torch.cuda.synchronize()
     assert torch.equal(y1, y2)
     assert torch.equal(S1, S2)
+
+
+def test_two_stream_pipeline_equals_serial(proj):
+    """kdn_delta_scan_fwd_pipelined (prep and output sharing one auxiliary stream) is bit-identical too."""
+    import ctypes
+    from kdn import _native as N
+    q, k, v, beta, decay = make_inputs(1, 64 * 23 + 9, 2, 64, torch.bfloat16, "sigmoid", seed=21)
+    qd, kd, vd, bd, dd = (t.to(DEV) for t in (q, k, v, beta, decay))
+    om, ph = proj.device_omega(DEV), proj.device_phase(DEV)
+    ws = torch.empty(ops.scan_workspace_bytes(qd, vd, om, 5, pipelined=True), dtype=torch.uint8, device=DEV)
+    y = torch.empty(1, qd.shape[1], 2, 64, device=DEV, dtype=torch.bfloat16)
+    S = torch.empty(1, 2, 512, 64, device=DEV)
+    a = ops.scan_args(qd, kd, vd, bd, dd, om, ph, proj.tau_star_inv, False, None, S, y, ws, 5)
+    aux = torch.cuda.Stream()
+    st = torch.cuda.current_stream()
+    N.check(N.lib().kdn_delta_scan_fwd_pipelined(ctypes.byref(a), ctypes.c_void_p(st.cuda_stream),
+                                                 ctypes.c_void_p(aux.cuda_stream)), "pipelined")
+    y2, S2 = ops.scan(qd, kd, vd, bd, dd, om, ph, proj.tau_star_inv, segment_chunks=5, pipelined=False)
+    torch.cuda.synchronize()
+    assert torch.equal(y, y2)
+    assert torch.equal(S, S2)
 
 
 def test_pipelined_two_buffers_parity(proj, oproj):
