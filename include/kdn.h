@@ -182,6 +182,41 @@ int kdn_scan_prep(const kdn_scan_args* a, int64_t chunk0, int64_t nchunks, void*
 int kdn_scan_state(const kdn_scan_args* a, int64_t chunk0, int64_t nchunks, void* stream);
 int kdn_scan_output(const kdn_scan_args* a, int64_t chunk0, int64_t nchunks, void* stream);
 
+/* ---- Backward of the scan (ABI 1.3) -------------------------------------------------------------
+ * Gradients of a loss L through kdn_delta_scan_fwd, given dL/dy and optionally dL/d(final state).
+ * Replaces the autograd recompute of FusedKernelDeltaNetFunction.backward,
+ * kernels/fused_kernel_deltanet.py:168-179.  `fwd` holds the forward's arguments (shapes, q, k, v, beta,
+ * decay, omega_bf16, phase, inv_tau, normalize_input, initial_state; its y, final_state, workspace and
+ * segment_chunks are ignored).  Supported: d_k = 64, D = 512, d_v = 64, the delta rule (rule 0) with the
+ * structured lift of one shared Omega (no hi + lo, per-head or pre-lifted features, no_renorm 0), uniform
+ * batches (no cu_seqlens / state_slots); other requests return KDN_ERR_UNSUPPORTED.  dy and
+ * d_final_state are fp32; every gradient is written in fp32 with the layout of its input: dq, dk
+ * (B, T, H, d_k), dv (B, T, H, d_v), dbeta, ddecay (B, T, H), d_initial_state (B, H, D, d_v).
+ * d_final_state NULL means dL/dS_T = 0; ddecay (allowed only with decay) and d_initial_state may be
+ * NULL.  The gradient of lambda is zero where the forward's clamp to [1e-5, 1] is active.  The
+ * workspace holds one fp32 record per (batch, head, 64-token chunk) (854,016 bytes each; 256-byte
+ * aligned). */
+typedef struct kdn_scan_bwd_args {
+  const kdn_scan_args* fwd;
+  const float* dy;            int64_t dy_stride[3];
+  const float* d_final_state; int64_t dfinal_stride[4];
+  float* dq;                  int64_t dq_stride[3];
+  float* dk;                  int64_t dk_stride[3];
+  float* dv;                  int64_t dv_stride[3];
+  float* dbeta;               int64_t dbeta_stride[3];
+  float* ddecay;              int64_t ddecay_stride[3];
+  float* d_initial_state;     int64_t dinit_stride[4];
+  void* workspace;            size_t workspace_bytes;
+} kdn_scan_bwd_args;
+
+/* Workspace bytes kdn_delta_scan_bwd needs (0 if the arguments are invalid or unsupported). */
+size_t kdn_scan_bwd_workspace_bytes(const kdn_scan_bwd_args* a);
+
+/* Enqueues the backward on `stream`: per-chunk recompute of the lift and the chunk matrices, the
+ * forward state carry (state at every chunk start), the reverse carry of dL/dS, and the per-chunk
+ * gradients with the lift's backward. */
+int kdn_delta_scan_bwd(const kdn_scan_bwd_args* a, void* stream);
+
 /* ---- Serving: ragged mixed prefill + decode step over resident states -------------------------
  * One step of a batch of sequences that continue from states resident in a slab (the reference's
  * serving op vllm_hybrid_recurrent_forward, serving/vllm_kernel_deltanet_op.cpp:11-34, whose body is a

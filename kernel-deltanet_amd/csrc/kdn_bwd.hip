@@ -1,0 +1,989 @@
+// Backward pass of the chunked gated delta rule and of the feature lift (gfx950).
+//
+// The reference differentiates its chunked torch forward with autograd (FusedKernelDeltaNetFunction,
+// kernels/fused_kernel_deltanet.py:158-179: the backward recomputes the forward under autograd).  Here
+// the gradient of the same function is computed directly, in closed form per 64-token chunk, by four
+// launches that recompute what they need from the inputs:
+//
+//   prep  (parallel over chunks x heads)  lift q, k; Gram matrices K K^T, Q K^T; A, T = (I + A)^-1,
+//                                         Tp = T diag(beta g), U~ = T (beta o V), P; R = P^T dY and
+//                                         H = Q^T (a o dY) (a_i = g_{i-1})
+//   chain (sequential over chunks)        forward:  S_c^T at every chunk start, X_K = K S_c^T,
+//                                                   W = U~ - Tp X_K, S_{c+1}^T = g_C S_c^T + K^T (kappa o W)
+//         (same kernel, reversed)         backward: Gamma = dL/dS^T at every chunk end, X = K Gamma,
+//                                                   dW = R + kappa o X,
+//                                                   Gamma <- g_C Gamma + H - K^T Tp^T dW
+//   grad  (parallel over chunks x heads)  dv, dbeta, dlambda and dphi_q, dphi_k in closed form, then
+//                                         the lift backward (cos -> -sin, renormalisation, input
+//                                         normalisation) to dq, dk
+//
+// Notation per chunk (tokens i, j in 0..63): l_i = sum_{t <= i} log clamp(lambda_t, 1e-5, 1), g = e^l,
+// g_C = g_63, a_i = g_{i-1} (a_0 = 1), kappa_j = g_C / g_j; A_ij = beta_i (g_i/g_j) k_i.k_j and
+// P_ij = (g_{i-1}/g_j) q_i.k_j for j < i; Y = diag(a) Q S^T + P W; S_C^T = g_C S^T + K^T diag(kappa) W.
+// Every matrix is fp32 and row-major in a per-(head, chunk) record of the workspace; products use the
+// fp32 16x16x4 MFMA through the fragment conventions of kdn_frag.hpp.
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+#include "kdn_frag.hpp"
+#include "kdn_internal.hpp"
+
+namespace kdn {
+namespace bwd {
+
+constexpr int C = 64, D = 512, DK = 64, DV = 64;
+constexpr int LD = 68;  // LDS row stride (floats) of a 64-wide tile: rows stay 16-byte aligned
+
+// Per (head, chunk) record, offsets in floats.
+struct Rec {
+  static constexpr size_t Q = 0;                // [64][512] lifted, normalised q rows (0 past T)
+  static constexpr size_t K = Q + C * D;        // [64][512] lifted, normalised k rows (0 past T)
+  static constexpr size_t H1 = K + C * D;       // [512][64] Q^T (a o dY)
+  static constexpr size_t S = H1 + D * DV;      // [512][64] S^T at the chunk start
+  static constexpr size_t G = S + D * DV;       // [512][64] dL/dS^T at the chunk end
+  static constexpr size_t T = G + D * DV;       // [64][64] (I + A)^-1
+  static constexpr size_t TP = T + C * C;       // [64][64] T diag(beta g)
+  static constexpr size_t TPT = TP + C * C;     // [64][64] Tp^T
+  static constexpr size_t P = TPT + C * C;      // [64][64]
+  static constexpr size_t GKK = P + C * C;      // [64][64] K K^T
+  static constexpr size_t GQK = GKK + C * C;    // [64][64] Q K^T
+  static constexpr size_t U = GQK + C * C;      // [64][64] U~ = T (beta o V)
+  static constexpr size_t R = U + C * DV;       // [64][64] P^T dY
+  static constexpr size_t W = R + C * DV;       // [64][64] W = U~ - Tp X_K
+  static constexpr size_t XK = W + C * DV;      // [64][64] K S^T
+  static constexpr size_t DW = XK + C * DV;     // [64][64] dL/dW
+  static constexpr size_t X = DW + C * DV;      // [64][64] K Gamma
+  static constexpr size_t VEC = X + C * DV;     // l[64], beta[64], |phi~_q|[64], |phi~_k|[64]
+  static constexpr size_t floats = VEC + 512;
+};
+static_assert((Rec::floats * 4) % 256 == 0, "records stay 256-byte aligned");
+
+struct Params {
+  int64_t B, T, H, nch;
+  const void* q; int64_t qs0, qs1, qs2;
+  const void* k; int64_t ks0, ks1, ks2;
+  const void* v; int64_t vs0, vs1, vs2;
+  const float* beta; int64_t bs0, bs1, bs2;
+  const float* decay; int64_t ds0, ds1, ds2;
+  const __bf16* omega; const float* phase;
+  float inv_tau; int normalize;
+  const float* init; int64_t is0, is1, is2, is3;
+  const float* dy; int64_t ys0, ys1, ys2;
+  const float* dfin; int64_t fs0, fs1, fs2, fs3;
+  float* dq; int64_t dqs0, dqs1, dqs2;
+  float* dk; int64_t dks0, dks1, dks2;
+  float* dv; int64_t dvs0, dvs1, dvs2;
+  float* dbeta; int64_t dbs0, dbs1, dbs2;
+  float* ddecay; int64_t dds0, dds1, dds2;
+  float* dinit; int64_t dis0, dis1, dis2, dis3;
+  float* ws;
+};
+
+__device__ __forceinline__ float* record(const Params& p, int64_t b, int64_t h, int64_t c) {
+  return p.ws + ((b * p.H + h) * p.nch + c) * (int64_t)Rec::floats;
+}
+
+template <typename T>
+__device__ __forceinline__ float ldx(const T* p) { return (float)*p; }
+
+// Fragment loads (kappa order, see kdn_frag.hpp).  rows: element (r0 + l%16, k0 + kappa) = base[row * ld + depth]
+// (two 16-byte loads); cols: element (c0 + l%16, k0 + kappa) = base[depth * ld + c0 + l%16] (eight loads).
+__device__ __forceinline__ f32x8 frag_rows(const float* base, int ld, int r0, int k0, int lane) {
+  const float* p = base + (size_t)(r0 + (lane & 15)) * ld + k0 + 4 * (lane >> 4);
+  const f32x4 lo = *reinterpret_cast<const f32x4*>(p);
+  const f32x4 hi = *reinterpret_cast<const f32x4*>(p + 16);
+  return pair_to8(lo, hi);
+}
+__device__ __forceinline__ f32x8 frag_cols(const float* base, int ld, int c0, int k0, int lane) {
+  f32x8 r;
+#pragma unroll
+  for (int s = 0; s < 8; ++s) r[s] = base[(size_t)(k0 + kappa(lane, s)) * ld + c0 + (lane & 15)];
+  return r;
+}
+__device__ __forceinline__ f32x8 frag_rows_bf16(const __bf16* base, int ld, int r0, int k0, int lane) {
+  typedef __attribute__((ext_vector_type(4))) __bf16 bf16x4;
+  const __bf16* p = base + (size_t)(r0 + (lane & 15)) * ld + k0 + 4 * (lane >> 4);
+  const bf16x4 lo = *reinterpret_cast<const bf16x4*>(p);
+  const bf16x4 hi = *reinterpret_cast<const bf16x4*>(p + 16);
+  f32x8 r;
+#pragma unroll
+  for (int s = 0; s < 4; ++s) { r[s] = (float)lo[s]; r[4 + s] = (float)hi[s]; }
+  return r;
+}
+__device__ __forceinline__ f32x8 frag_cols_bf16(const __bf16* base, int ld, int c0, int k0, int lane) {
+  f32x8 r;
+#pragma unroll
+  for (int s = 0; s < 8; ++s) r[s] = (float)base[(size_t)(k0 + kappa(lane, s)) * ld + c0 + (lane & 15)];
+  return r;
+}
+
+template <class P>
+__device__ __forceinline__ f32x4 mm(f32x4 acc, const f32x8& a, const f32x8& b) {
+  return P::mma(acc, P::from_f32(a), P::from_f32(b));
+}
+
+// Sum over the 16 lanes sharing (lane >> 4) (one tile row) / over the 4 lane groups (one tile column).
+__device__ __forceinline__ float sum_row16(float v) {
+  v += __shfl_xor(v, 1);
+  v += __shfl_xor(v, 2);
+  v += __shfl_xor(v, 4);
+  v += __shfl_xor(v, 8);
+  return v;
+}
+__device__ __forceinline__ float sum_col4(float v) {
+  v += __shfl_xor(v, 16);
+  v += __shfl_xor(v, 32);
+  return v;
+}
+
+// Thread `tid` of 256 holds 16 consecutive features (tid & 3) * 16 .. of token row tid >> 2: loads the
+// raw row part of x (zero past T), its L2 norm over the 64 features (shared by the four threads of the
+// row), and the normalised part (x / max(|x|, 1e-6), or x itself without normalisation).
+template <typename InT>
+__device__ __forceinline__ float load_x_part(const InT* x, int64_t base, bool valid, int normalize, float* part) {
+  float ss = 0.f;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) {
+    part[e] = valid ? ldx(x + base + e) : 0.f;
+    ss += part[e] * part[e];
+  }
+  ss += __shfl_xor(ss, 1);
+  ss += __shfl_xor(ss, 2);
+  const float nrm = sqrtf(ss);
+  if (normalize) {
+    const float inv = 1.f / fmaxf(nrm, 1e-6f);
+#pragma unroll
+    for (int e = 0; e < 16; ++e) part[e] *= inv;
+  }
+  return nrm;
+}
+
+// ---------------------------------------------------------------------------------------------- prep
+// grid (nch, H, B), 256 threads.
+template <class P, typename InT>
+__global__ void __launch_bounds__(256) bwd_prep_kernel(Params p) {
+  __shared__ __attribute__((aligned(16))) float xs[C * LD];   // normalised x rows; later beta o V
+  __shared__ __attribute__((aligned(16))) float bA[C * LD];   // a o dY; later A
+  __shared__ __attribute__((aligned(16))) float bT[C * LD];   // T
+  __shared__ __attribute__((aligned(16))) float bP[C * LD];   // P
+  __shared__ __attribute__((aligned(16))) float bY[C * LD];   // dY
+  __shared__ float s_ell[C], s_beta[C], s_n[C], s_red[4][C];
+
+  const int64_t c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int64_t t0 = c * C;
+  float* rec = record(p, b, h, c);
+  const int r = tid >> 2, c0 = (tid & 3) * 16;
+  const bool rvalid = t0 + r < p.T;
+
+  if (w == 0) {
+    const int64_t t = t0 + lane;
+    const bool valid = t < p.T;
+    const float be = valid ? p.beta[b * p.bs0 + t * p.bs1 + h * p.bs2] : 0.f;
+    const float la = (valid && p.decay) ? p.decay[b * p.ds0 + t * p.ds1 + h * p.ds2] : 1.f;
+    float l = logf(fminf(fmaxf(la, 1e-5f), 1.f));
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const float u = __shfl_up(l, o);
+      if (lane >= o) l += u;
+    }
+    s_ell[lane] = l;
+    s_beta[lane] = be;
+    rec[Rec::VEC + lane] = l;
+    rec[Rec::VEC + 64 + lane] = be;
+  }
+#pragma unroll
+  for (int e = 0; e < 16; ++e)
+    bY[r * LD + c0 + e] = rvalid ? p.dy[b * p.ys0 + (t0 + r) * p.ys1 + h * p.ys2 + c0 + e] : 0.f;
+  __syncthreads();
+  {
+    const float a = r == 0 ? 1.f : expf(s_ell[r - 1]);
+#pragma unroll
+    for (int e = 0; e < 16; ++e) bA[r * LD + c0 + e] = a * bY[r * LD + c0 + e];
+  }
+
+  const float amp = sqrtf(2.f / D);
+  for (int which = 0; which < 2; ++which) {  // 0: q, 1: k
+    const InT* x = reinterpret_cast<const InT*>(which == 0 ? p.q : p.k);
+    const int64_t xb = which == 0 ? b * p.qs0 + (t0 + r) * p.qs1 + h * p.qs2 : b * p.ks0 + (t0 + r) * p.ks1 + h * p.ks2;
+    float part[16];
+    load_x_part<InT>(x, xb + c0, rvalid, p.normalize, part);
+#pragma unroll
+    for (int e = 0; e < 16; ++e) xs[r * LD + c0 + e] = part[e];
+    __syncthreads();
+
+    // phi~ (tokens x this wave's 128 features): tile [ft][m] rows token 16m + .., column feature.
+    f32x4 acc[8][4];
+    f32x8 xa[4][2];
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+#pragma unroll
+      for (int jb = 0; jb < 2; ++jb) xa[m][jb] = frag_rows(xs, LD, 16 * m, 32 * jb, lane);
+    float ss[4][4];
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) ss[m][i] = 0.f;
+#pragma unroll
+    for (int ft = 0; ft < 8; ++ft) {
+      const int f0 = 128 * w + 16 * ft;
+      const f32x8 o0 = frag_rows_bf16(p.omega, DK, f0, 0, lane), o1 = frag_rows_bf16(p.omega, DK, f0, 32, lane);
+      const float ph = p.phase[f0 + (lane & 15)];
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        f32x4 s = mm<P>(mm<P>(zero4(), xa[m][0], o0), xa[m][1], o1);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float v = amp * cosf(s[i] * p.inv_tau + ph);
+          s[i] = v;
+          ss[m][i] += v * v;
+        }
+        acc[ft][m] = s;
+      }
+    }
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float v = sum_row16(ss[m][i]);
+        if ((lane & 15) == 0) s_red[w][16 * m + 4 * (lane >> 4) + i] = v;
+      }
+    __syncthreads();
+    if (tid < 64) {
+      const float n = sqrtf(s_red[0][tid] + s_red[1][tid] + s_red[2][tid] + s_red[3][tid]);
+      s_n[tid] = n;
+      rec[Rec::VEC + 128 + 64 * which + tid] = n;
+    }
+    __syncthreads();
+    float* phi = rec + (which == 0 ? Rec::Q : Rec::K);
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int row = 16 * m + 4 * (lane >> 4) + i;
+        const float sc = (t0 + row < p.T) ? 1.f / (s_n[row] + 1e-8f) : 0.f;
+#pragma unroll
+        for (int ft = 0; ft < 8; ++ft) {
+          acc[ft][m][i] *= sc;
+          phi[(size_t)row * D + 128 * w + 16 * ft + (lane & 15)] = acc[ft][m][i];
+        }
+      }
+    if (which == 0) {
+      // H = Q^T (a o dY): A = phi_q^T fragments straight from the accumulators.
+      f32x8 yb[4][2];
+#pragma unroll
+      for (int n = 0; n < 4; ++n)
+#pragma unroll
+        for (int jb = 0; jb < 2; ++jb) yb[n][jb] = frag_cols(bA, LD, 16 * n, 32 * jb, lane);
+#pragma unroll
+      for (int ft = 0; ft < 8; ++ft) {
+        const f32x8 qa0 = pair_to8(acc[ft][0], acc[ft][1]), qa1 = pair_to8(acc[ft][2], acc[ft][3]);
+#pragma unroll
+        for (int n = 0; n < 4; ++n) {
+          const f32x4 hv = mm<P>(mm<P>(zero4(), qa0, yb[n][0]), qa1, yb[n][1]);
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            rec[Rec::H1 + (size_t)(128 * w + 16 * ft + 4 * (lane >> 4) + i) * DV + 16 * n + (lane & 15)] = hv[i];
+        }
+      }
+    }
+    __syncthreads();
+  }
+  __threadfence();
+  __syncthreads();
+
+  // Gram matrices (row tile w) from the rows just written; A and P into LDS.
+  {
+    const float* K = rec + Rec::K;
+    const float* Q = rec + Rec::Q;
+    f32x4 gkk[4], gqk[4];
+#pragma unroll
+    for (int n = 0; n < 4; ++n) gkk[n] = gqk[n] = zero4();
+    for (int jb = 0; jb < D / 32; ++jb) {
+      const f32x8 kw = frag_rows(K, D, 16 * w, 32 * jb, lane);
+      const f32x8 qw = frag_rows(Q, D, 16 * w, 32 * jb, lane);
+#pragma unroll
+      for (int n = 0; n < 4; ++n) {
+        const f32x8 kn = frag_rows(K, D, 16 * n, 32 * jb, lane);
+        gkk[n] = mm<P>(gkk[n], kw, kn);
+        gqk[n] = mm<P>(gqk[n], qw, kn);
+      }
+    }
+#pragma unroll
+    for (int n = 0; n < 4; ++n)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int ri = 16 * w + 4 * (lane >> 4) + i, cj = 16 * n + (lane & 15);
+        rec[Rec::GKK + ri * C + cj] = gkk[n][i];
+        rec[Rec::GQK + ri * C + cj] = gqk[n][i];
+        const float li = s_ell[ri], lj = s_ell[cj], lim1 = ri > 0 ? s_ell[ri - 1] : 0.f;
+        bA[ri * LD + cj] = cj < ri ? s_beta[ri] * expf(fminf(li - lj, 0.f)) * gkk[n][i] : 0.f;
+        bP[ri * LD + cj] = cj < ri ? expf(fminf(lim1 - lj, 0.f)) * gqk[n][i] : 0.f;
+      }
+  }
+  __syncthreads();
+  // T = (I + A)^-1 by forward substitution, one column per thread.
+  if (tid < C) {
+    const int col = tid;
+    for (int i = 0; i < C; ++i) {
+      float acc = (i == col) ? 1.f : 0.f;
+      for (int j = col; j < i; ++j) acc -= bA[i * LD + j] * bT[j * LD + col];
+      bT[i * LD + col] = (i >= col) ? acc : 0.f;
+    }
+  }
+  __syncthreads();
+  for (int idx = tid; idx < C * C; idx += 256) {
+    const int i = idx >> 6, j = idx & 63;
+    const float tij = bT[i * LD + j];
+    const float tp = tij * s_beta[j] * expf(s_ell[j]);
+    rec[Rec::T + idx] = tij;
+    rec[Rec::TP + idx] = tp;
+    rec[Rec::TPT + j * C + i] = tp;
+    rec[Rec::P + idx] = bP[i * LD + j];
+  }
+  {
+    const InT* v = reinterpret_cast<const InT*>(p.v);
+    const int64_t vb = b * p.vs0 + (t0 + r) * p.vs1 + h * p.vs2 + c0;
+    const float be = s_beta[r];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) xs[r * LD + c0 + e] = rvalid ? be * ldx(v + vb + e) : 0.f;
+  }
+  __syncthreads();
+  // U~ = T (beta o V), R = P^T dY (row tile w).
+  {
+    const f32x8 ta0 = frag_rows(bT, LD, 16 * w, 0, lane), ta1 = frag_rows(bT, LD, 16 * w, 32, lane);
+    const f32x8 pa0 = frag_cols(bP, LD, 16 * w, 0, lane), pa1 = frag_cols(bP, LD, 16 * w, 32, lane);
+#pragma unroll
+    for (int n = 0; n < 4; ++n) {
+      const f32x4 u = mm<P>(mm<P>(zero4(), ta0, frag_cols(xs, LD, 16 * n, 0, lane)), ta1, frag_cols(xs, LD, 16 * n, 32, lane));
+      const f32x4 rr = mm<P>(mm<P>(zero4(), pa0, frag_cols(bY, LD, 16 * n, 0, lane)), pa1, frag_cols(bY, LD, 16 * n, 32, lane));
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int ri = 16 * w + 4 * (lane >> 4) + i, cj = 16 * n + (lane & 15);
+        rec[Rec::U + ri * DV + cj] = u[i];
+        rec[Rec::R + ri * DV + cj] = rr[i];
+      }
+    }
+  }
+}
+
+// --------------------------------------------------------------------------------------------- chain
+// grid: 8 * ceil(B*H / 8) * 4 workgroups of 256 threads; workgroup (head-batch hb, value tile n) with
+// the four value tiles of a head on one XCD.  Wave w keeps rows 128w .. 128w+127 of its 512 x 16 slice
+// of the carried matrix (S^T forward, Gamma backward) in registers.
+template <class P, bool REV>
+__global__ void __launch_bounds__(256) bwd_chain_kernel(Params p) {
+  __shared__ f32x4 sh_xp[4][4][64];
+  __shared__ f32x4 sh_x[4][64];
+  __shared__ f32x4 sh_z[4][64];
+  const int64_t id = blockIdx.x;
+  const int64_t xcd = id & 7, jdx = id >> 3;
+  const int n = (int)(jdx & 3);
+  const int64_t hb = (jdx >> 2) * 8 + xcd;
+  if (hb >= p.B * p.H) return;
+  const int64_t b = hb / p.H, h = hb % p.H;
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int vc = 16 * n + (lane & 15);  // this lane's value column
+
+  f32x4 Sg[8];
+  {
+    const float* src = REV ? p.dfin : p.init;
+    const int64_t s0 = REV ? p.fs0 : p.is0, s1 = REV ? p.fs1 : p.is1, s2 = REV ? p.fs2 : p.is2, s3 = REV ? p.fs3 : p.is3;
+#pragma unroll
+    for (int t = 0; t < 8; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int f = 128 * w + 16 * t + 4 * (lane >> 4) + i;
+        Sg[t][i] = src ? src[b * s0 + h * s1 + f * s2 + vc * s3] : 0.f;
+      }
+  }
+  for (int64_t step = 0; step < p.nch; ++step) {
+    const int64_t c = REV ? p.nch - 1 - step : step;
+    float* rec = record(p, b, h, c);
+    float* dst = rec + (REV ? Rec::G : Rec::S);
+#pragma unroll
+    for (int t = 0; t < 8; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) dst[(size_t)(128 * w + 16 * t + 4 * (lane >> 4) + i) * DV + vc] = Sg[t][i];
+
+    // K times the carried slice, partial over this wave's features.
+    f32x4 xp[4];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) xp[m] = zero4();
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      const f32x8 sb = pair_to8(Sg[2 * jj], Sg[2 * jj + 1]);
+#pragma unroll
+      for (int m = 0; m < 4; ++m) xp[m] = mm<P>(xp[m], frag_rows(rec + Rec::K, D, 16 * m, 128 * w + 32 * jj, lane), sb);
+    }
+#pragma unroll
+    for (int m = 0; m < 4; ++m) sh_xp[w][m][lane] = xp[m];
+    __syncthreads();
+    const f32x4 X = sh_xp[0][w][lane] + sh_xp[1][w][lane] + sh_xp[2][w][lane] + sh_xp[3][w][lane];
+    const float l63 = rec[Rec::VEC + 63];
+    const float gC = expf(l63);
+    f32x4 kap;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) kap[i] = expf(l63 - rec[Rec::VEC + 16 * w + 4 * (lane >> 4) + i]);
+    if constexpr (!REV) {
+      sh_x[w][lane] = X;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) rec[Rec::XK + (16 * w + 4 * (lane >> 4) + i) * DV + vc] = X[i];
+      __syncthreads();
+      f32x4 Wt;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) Wt[i] = rec[Rec::U + (16 * w + 4 * (lane >> 4) + i) * DV + vc];
+      f32x4 tx = zero4();
+#pragma unroll
+      for (int jb = 0; jb < 2; ++jb)
+        tx = mm<P>(tx, frag_rows(rec + Rec::TP, C, 16 * w, 32 * jb, lane), pair_to8(sh_x[2 * jb][lane], sh_x[2 * jb + 1][lane]));
+      Wt = Wt - tx;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) rec[Rec::W + (16 * w + 4 * (lane >> 4) + i) * DV + vc] = Wt[i];
+      sh_z[w][lane] = kap * Wt;
+    } else {
+      f32x4 dW;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int ri = 16 * w + 4 * (lane >> 4) + i;
+        dW[i] = rec[Rec::R + ri * DV + vc] + kap[i] * X[i];
+        rec[Rec::X + ri * DV + vc] = X[i];
+        rec[Rec::DW + ri * DV + vc] = dW[i];
+      }
+      sh_x[w][lane] = dW;
+      __syncthreads();
+      f32x4 zt = zero4();
+#pragma unroll
+      for (int jb = 0; jb < 2; ++jb)
+        zt = mm<P>(zt, frag_rows(rec + Rec::TPT, C, 16 * w, 32 * jb, lane), pair_to8(sh_x[2 * jb][lane], sh_x[2 * jb + 1][lane]));
+      sh_z[w][lane] = -zt;
+    }
+    __syncthreads();
+    const f32x8 zb0 = pair_to8(sh_z[0][lane], sh_z[1][lane]), zb1 = pair_to8(sh_z[2][lane], sh_z[3][lane]);
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      f32x4 acc = Sg[t] * gC;
+      if constexpr (REV) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[i] += rec[Rec::H1 + (size_t)(128 * w + 16 * t + 4 * (lane >> 4) + i) * DV + vc];
+      }
+      acc = mm<P>(acc, frag_cols(rec + Rec::K, D, 128 * w + 16 * t, 0, lane), zb0);
+      acc = mm<P>(acc, frag_cols(rec + Rec::K, D, 128 * w + 16 * t, 32, lane), zb1);
+      Sg[t] = acc;
+    }
+  }
+  if constexpr (REV) {
+    if (p.dinit) {
+#pragma unroll
+      for (int t = 0; t < 8; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int f = 128 * w + 16 * t + 4 * (lane >> 4) + i;
+          p.dinit[b * p.dis0 + h * p.dis1 + f * p.dis2 + vc * p.dis3] = Sg[t][i];
+        }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------- grad
+// The lift backward of one of q (which = 0) / k (which = 1) for this wave's 128 features, given
+// dPhi^T in acc[ft][m] (rows feature 128w + 16ft + .., column token 16m + ..): ds = -sqrt(2/D) sin(s)
+// (dphi / (n + 1e-8) - phi (phi . dphi) / n), then dx^ = inv_tau ds Omega reduced over the waves into
+// `dx` (LDS [64][LD], zeroed by the caller).  `xh` holds the normalised input rows.
+template <class P>
+__device__ __forceinline__ void lift_backward(const Params& p, const float* phi, const float* nrm, float* s_rd,
+                                              const float* xh, float* dx, f32x4 (&acc)[8][4], int w, int lane) {
+  // phi . dphi per token
+  float rd[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int ft = 0; ft < 8; ++ft)
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      const f32x4 ph = *reinterpret_cast<const f32x4*>(phi + (size_t)(16 * m + (lane & 15)) * D + 128 * w + 16 * ft + 4 * (lane >> 4));
+      rd[m] += ph[0] * acc[ft][m][0] + ph[1] * acc[ft][m][1] + ph[2] * acc[ft][m][2] + ph[3] * acc[ft][m][3];
+    }
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    const float v = sum_col4(rd[m]);
+    if (lane < 16) atomicAdd(&s_rd[16 * m + lane], v);
+  }
+  __syncthreads();
+  const float amp = sqrtf(2.f / D);
+  f32x8 xb[4][2];
+#pragma unroll
+  for (int m = 0; m < 4; ++m)
+#pragma unroll
+    for (int jb = 0; jb < 2; ++jb) xb[m][jb] = frag_rows(xh, LD, 16 * m, 32 * jb, lane);
+#pragma unroll
+  for (int ft = 0; ft < 8; ++ft) {
+    const int f0 = 128 * w + 16 * ft;
+    const f32x8 o0 = frag_rows_bf16(p.omega, DK, f0, 0, lane), o1 = frag_rows_bf16(p.omega, DK, f0, 32, lane);
+    f32x4 ph4;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ph4[i] = p.phase[f0 + 4 * (lane >> 4) + i];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      const f32x4 s = mm<P>(mm<P>(zero4(), o0, xb[m][0]), o1, xb[m][1]);
+      const int tok = 16 * m + (lane & 15);
+      const float n = nrm[tok], rdt = s_rd[tok];
+      const f32x4 ph = *reinterpret_cast<const f32x4*>(phi + (size_t)tok * D + f0 + 4 * (lane >> 4));
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float dphit = acc[ft][m][i] / (n + 1e-8f) - ph[i] * rdt / n;
+        acc[ft][m][i] = -amp * sinf(s[i] * p.inv_tau + ph4[i]) * dphit;
+      }
+    }
+  }
+  f32x4 d[4][4];
+#pragma unroll
+  for (int a = 0; a < 4; ++a)
+#pragma unroll
+    for (int m = 0; m < 4; ++m) d[a][m] = zero4();
+#pragma unroll
+  for (int jj = 0; jj < 4; ++jj) {
+    f32x8 ob[4];
+#pragma unroll
+    for (int a = 0; a < 4; ++a) ob[a] = frag_cols_bf16(p.omega, DK, 16 * a, 128 * w + 32 * jj, lane);
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      const f32x8 bs = pair_to8(acc[2 * jj][m], acc[2 * jj + 1][m]);
+#pragma unroll
+      for (int a = 0; a < 4; ++a) d[a][m] = mm<P>(d[a][m], ob[a], bs);
+    }
+  }
+#pragma unroll
+  for (int a = 0; a < 4; ++a)
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) atomicAdd(&dx[(16 * m + (lane & 15)) * LD + 16 * a + 4 * (lane >> 4) + i], d[a][m][i]);
+}
+
+// Thread (row tid >> 2, features (tid & 3) * 16 ..): dx = inv_tau * dx^ through the input normalisation,
+// written for tokens before T.
+template <typename InT>
+__device__ __forceinline__ void write_dx(const Params& p, const InT* x, int64_t xbase, float* out, int64_t obase,
+                                         const float* dx, int r, int c0, bool valid) {
+  float part[16];
+  const float nrm = load_x_part<InT>(x, xbase, valid, p.normalize, part);
+  float g[16];
+#pragma unroll
+  for (int e = 0; e < 16; ++e) g[e] = p.inv_tau * dx[r * LD + c0 + e];
+  if (p.normalize) {
+    float dot = 0.f;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) dot += part[e] * g[e];
+    dot += __shfl_xor(dot, 1);
+    dot += __shfl_xor(dot, 2);
+    if (nrm > 1e-6f) {
+      const float inv = 1.f / nrm;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) g[e] = (g[e] - part[e] * dot) * inv;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) g[e] *= 1e6f;
+    }
+  }
+  if (valid) {
+#pragma unroll
+    for (int e = 0; e < 16; ++e) out[obase + e] = g[e];
+  }
+}
+
+// grid (nch, H, B), 256 threads.
+template <class P, typename InT>
+__global__ void __launch_bounds__(256) bwd_grad_kernel(Params p) {
+  __shared__ __attribute__((aligned(16))) float bY[C * LD];   // dY, then a o dY
+  __shared__ __attribute__((aligned(16))) float bW[C * LD];   // W, then kappa o W, then dx^ of k / q
+  __shared__ __attribute__((aligned(16))) float bdW[C * LD];  // dW, then Zn = -Tp^T dW
+  __shared__ __attribute__((aligned(16))) float bXK[C * LD];  // X_K, then N
+  __shared__ __attribute__((aligned(16))) float bX[C * LD];   // X, then dT, then M + M^T
+  __shared__ __attribute__((aligned(16))) float bV[C * LD];   // V, then Y1 = dT T^T
+  __shared__ __attribute__((aligned(16))) float bT[C * LD];   // T, then normalised k / q rows
+  __shared__ float s_ell[C], s_beta[C], s_dl[C], s_db[C], s_ts[C], s_rd[C], s_n[C], s_g[1];
+
+  const int64_t c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int64_t t0 = c * C;
+  const float* rec = record(p, b, h, c);
+  const int r = tid >> 2, c0 = (tid & 3) * 16;
+  const bool rvalid = t0 + r < p.T;
+
+  if (tid < C) {
+    s_ell[tid] = rec[Rec::VEC + tid];
+    s_beta[tid] = rec[Rec::VEC + 64 + tid];
+    s_dl[tid] = s_db[tid] = s_ts[tid] = s_rd[tid] = 0.f;
+  }
+  if (tid == 0) s_g[0] = 0.f;
+  {
+    const InT* v = reinterpret_cast<const InT*>(p.v);
+    const int64_t vb = b * p.vs0 + (t0 + r) * p.vs1 + h * p.vs2 + c0;
+    const int64_t yb = b * p.ys0 + (t0 + r) * p.ys1 + h * p.ys2 + c0;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int o = r * LD + c0 + e, q = r * DV + c0 + e;
+      bY[o] = rvalid ? p.dy[yb + e] : 0.f;
+      bW[o] = rec[Rec::W + q];
+      bdW[o] = rvalid ? rec[Rec::DW + q] : 0.f;
+      bXK[o] = rec[Rec::XK + q];
+      bX[o] = rec[Rec::X + q];
+      bV[o] = rvalid ? ldx(v + vb + e) : 0.f;
+      bT[o] = rec[Rec::T + r * C + c0 + e];
+    }
+  }
+  __syncthreads();
+  const float l63 = s_ell[63], gC = expf(l63);
+
+  // ---- phase 1: dkappa; T^T dW -> dv, dbeta; dTp, dT; dP -> N
+  {
+    float dkp = 0.f;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) dkp += bW[r * LD + c0 + e] * bX[r * LD + c0 + e];
+    dkp += __shfl_xor(dkp, 1);
+    dkp += __shfl_xor(dkp, 2);
+    if ((tid & 3) == 0) {
+      const float t = dkp * expf(l63 - s_ell[r]);
+      atomicAdd(&s_dl[63], t);
+      atomicAdd(&s_dl[r], -t);
+    }
+  }
+  f32x4 dT[4], nN[4];
+  {
+    const f32x8 ta0 = frag_cols(bT, LD, 16 * w, 0, lane), ta1 = frag_cols(bT, LD, 16 * w, 32, lane);
+    const f32x8 da0 = frag_rows(bdW, LD, 16 * w, 0, lane), da1 = frag_rows(bdW, LD, 16 * w, 32, lane);
+    const f32x8 ya0 = frag_rows(bY, LD, 16 * w, 0, lane), ya1 = frag_rows(bY, LD, 16 * w, 32, lane);
+    float dbp[4] = {0.f, 0.f, 0.f, 0.f}, rowp[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int n = 0; n < 4; ++n) {
+      const int cj = 16 * n + (lane & 15);
+      // T^T dW
+      const f32x4 td = mm<P>(mm<P>(zero4(), ta0, frag_cols(bdW, LD, 16 * n, 0, lane)), ta1, frag_cols(bdW, LD, 16 * n, 32, lane));
+      // -dW X_K^T and dW V^T
+      const f32x4 dtp = -mm<P>(mm<P>(zero4(), da0, frag_rows(bXK, LD, 16 * n, 0, lane)), da1, frag_rows(bXK, LD, 16 * n, 32, lane));
+      const f32x4 e1 = mm<P>(mm<P>(zero4(), da0, frag_rows(bV, LD, 16 * n, 0, lane)), da1, frag_rows(bV, LD, 16 * n, 32, lane));
+      // dY W^T
+      const f32x4 dp = mm<P>(mm<P>(zero4(), ya0, frag_rows(bW, LD, 16 * n, 0, lane)), ya1, frag_rows(bW, LD, 16 * n, 32, lane));
+      const float bj = s_beta[cj], lj = s_ell[cj], gj = expf(lj);
+      float ts = 0.f, colp = 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int ri = 16 * w + 4 * (lane >> 4) + i;
+        const bool valid = t0 + ri < p.T;
+        if (valid) p.dv[b * p.dvs0 + (t0 + ri) * p.dvs1 + h * p.dvs2 + cj] = s_beta[ri] * td[i];
+        dbp[i] += bV[ri * LD + cj] * td[i];
+        ts += bT[ri * LD + cj] * dtp[i];
+        dT[n][i] = bj * (e1[i] + gj * dtp[i]);
+        if (cj < ri) {
+          const float pb = dp[i] * rec[Rec::P + ri * C + cj];
+          rowp[i] += pb;
+          colp += pb;
+          const float lim1 = s_ell[ri - 1];
+          nN[n][i] = dp[i] * expf(fminf(lim1 - lj, 0.f));
+        } else {
+          nN[n][i] = 0.f;
+        }
+      }
+      ts = sum_col4(ts);
+      colp = sum_col4(colp);
+      if (lane < 16) {
+        atomicAdd(&s_ts[cj], ts);
+        atomicAdd(&s_dl[cj], -colp);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int ri = 16 * w + 4 * (lane >> 4) + i;
+      const float db = sum_row16(dbp[i]), rp = sum_row16(rowp[i]);
+      if ((lane & 15) == 0) {
+        atomicAdd(&s_db[ri], db);
+        if (ri > 0) atomicAdd(&s_dl[ri - 1], rp);
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- phase 2: dT and N to LDS; Tp sums; Q S^T -> da; a o dY, kappa o W; <Gamma, S>
+#pragma unroll
+  for (int n = 0; n < 4; ++n)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int ri = 16 * w + 4 * (lane >> 4) + i, cj = 16 * n + (lane & 15);
+      bX[ri * LD + cj] = dT[n][i];
+      bXK[ri * LD + cj] = nN[n][i];
+    }
+  if (tid < C) {
+    const float g = expf(s_ell[tid]), ts = s_ts[tid];
+    atomicAdd(&s_db[tid], g * ts);
+    atomicAdd(&s_dl[tid], s_beta[tid] * g * ts);
+  }
+  {
+    f32x4 qs[4];
+#pragma unroll
+    for (int n = 0; n < 4; ++n) qs[n] = zero4();
+    for (int jb = 0; jb < D / 32; ++jb) {
+      const f32x8 qa = frag_rows(rec + Rec::Q, D, 16 * w, 32 * jb, lane);
+#pragma unroll
+      for (int n = 0; n < 4; ++n) qs[n] = mm<P>(qs[n], qa, frag_cols(rec + Rec::S, DV, 16 * n, 32 * jb, lane));
+    }
+    float dap[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int n = 0; n < 4; ++n)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) dap[i] += bY[(16 * w + 4 * (lane >> 4) + i) * LD + 16 * n + (lane & 15)] * qs[n][i];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int ri = 16 * w + 4 * (lane >> 4) + i;
+      const float da = sum_row16(dap[i]);
+      if ((lane & 15) == 0 && ri > 0) atomicAdd(&s_dl[ri - 1], da * expf(s_ell[ri - 1]));
+    }
+    // scale this wave's rows only (no other wave reads them in this phase)
+    for (int e = lane; e < 16 * DV; e += 64) {
+      const int ri = 16 * w + (e >> 6), cv = e & 63;
+      bY[ri * LD + cv] *= ri > 0 ? expf(s_ell[ri - 1]) : 1.f;
+      bW[ri * LD + cv] *= expf(l63 - s_ell[ri]);
+    }
+  }
+  {
+    float gs = 0.f;
+    const f32x4* G4 = reinterpret_cast<const f32x4*>(rec + Rec::G);
+    const f32x4* S4 = reinterpret_cast<const f32x4*>(rec + Rec::S);
+    for (int e = tid; e < D * DV / 4; e += 256) {
+      const f32x4 g = G4[e], s = S4[e];
+      gs += g[0] * s[0] + g[1] * s[1] + g[2] * s[2] + g[3] * s[3];
+    }
+    gs = sum_col4(sum_row16(gs));
+    if (lane == 0) atomicAdd(&s_g[0], gs);
+  }
+  __syncthreads();
+  if (tid == 0) atomicAdd(&s_dl[63], s_g[0] * gC);
+
+  // ---- phase 3: Y1 = dT T^T; Zn = -Tp^T dW
+  f32x4 y1[4], zn[4];
+  {
+    const f32x8 a0 = frag_rows(bX, LD, 16 * w, 0, lane), a1 = frag_rows(bX, LD, 16 * w, 32, lane);
+    const f32x8 p0 = frag_rows(rec + Rec::TPT, C, 16 * w, 0, lane), p1 = frag_rows(rec + Rec::TPT, C, 16 * w, 32, lane);
+#pragma unroll
+    for (int n = 0; n < 4; ++n) {
+      y1[n] = mm<P>(mm<P>(zero4(), a0, frag_rows(bT, LD, 16 * n, 0, lane)), a1, frag_rows(bT, LD, 16 * n, 32, lane));
+      zn[n] = -mm<P>(mm<P>(zero4(), p0, frag_cols(bdW, LD, 16 * n, 0, lane)), p1, frag_cols(bdW, LD, 16 * n, 32, lane));
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int n = 0; n < 4; ++n)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int ri = 16 * w + 4 * (lane >> 4) + i, cj = 16 * n + (lane & 15);
+      bV[ri * LD + cj] = y1[n][i];
+      bdW[ri * LD + cj] = zn[n][i];
+    }
+  __syncthreads();
+
+  // ---- phase 4: dA = -T^T Y1 (strictly lower); M + M^T into bX; dbeta, dl from A
+  {
+    const f32x8 ta0 = frag_cols(bT, LD, 16 * w, 0, lane), ta1 = frag_cols(bT, LD, 16 * w, 32, lane);
+    float dbr[4] = {0.f, 0.f, 0.f, 0.f}, dlr[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int n = 0; n < 4; ++n) {
+      const f32x4 dA = -mm<P>(mm<P>(zero4(), ta0, frag_cols(bV, LD, 16 * n, 0, lane)), ta1, frag_cols(bV, LD, 16 * n, 32, lane));
+      const int cj = 16 * n + (lane & 15);
+      float dlc = 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int ri = 16 * w + 4 * (lane >> 4) + i;
+        if (cj < ri) {
+          const float ex = expf(fminf(s_ell[ri] - s_ell[cj], 0.f));
+          const float e = dA[i] * ex * rec[Rec::GKK + ri * C + cj];
+          const float ab = s_beta[ri] * e;
+          dbr[i] += e;
+          dlr[i] += ab;
+          dlc += ab;
+          const float mv = dA[i] * s_beta[ri] * ex;
+          bX[ri * LD + cj] = mv;
+          bX[cj * LD + ri] = mv;
+        } else if (cj == ri) {
+          bX[ri * LD + cj] = 0.f;
+        }
+      }
+      dlc = sum_col4(dlc);
+      if (lane < 16) atomicAdd(&s_dl[cj], -dlc);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int ri = 16 * w + 4 * (lane >> 4) + i;
+      const float a = sum_row16(dbr[i]), d = sum_row16(dlr[i]);
+      if ((lane & 15) == 0) {
+        atomicAdd(&s_db[ri], a);
+        atomicAdd(&s_dl[ri], d);
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- phase 5: dbeta and dlambda (dlog lambda_t = sum_{i >= t} dl_i)
+  if (w == 0) {
+    float dl = s_dl[lane];
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const float u = __shfl_down(dl, o);
+      if (lane + o < 64) dl += u;
+    }
+    const int64_t t = t0 + lane;
+    if (t < p.T) {
+      p.dbeta[b * p.dbs0 + t * p.dbs1 + h * p.dbs2] = s_db[lane];
+      if (p.ddecay) {
+        const float la = p.decay ? p.decay[b * p.ds0 + t * p.ds1 + h * p.ds2] : 1.f;
+        p.ddecay[b * p.dds0 + t * p.dds1 + h * p.dds2] = (la >= 1e-5f && la <= 1.f) ? dl / la : 0.f;
+      }
+    }
+  }
+
+  // ---- phase 6: dk, then dq
+  for (int which = 1; which >= 0; --which) {
+    const InT* x = reinterpret_cast<const InT*>(which == 0 ? p.q : p.k);
+    const int64_t xb = which == 0 ? b * p.qs0 + (t0 + r) * p.qs1 + h * p.qs2 + c0 : b * p.ks0 + (t0 + r) * p.ks1 + h * p.ks2 + c0;
+    {
+      float part[16];
+      load_x_part<InT>(x, xb, rvalid, p.normalize, part);
+#pragma unroll
+      for (int e = 0; e < 16; ++e) bT[r * LD + c0 + e] = part[e];
+    }
+    if (tid < C) {
+      s_rd[tid] = 0.f;
+      s_n[tid] = rec[Rec::VEC + 128 + 64 * which + tid];
+    }
+    __syncthreads();
+    f32x4 acc[8][4];
+#pragma unroll
+    for (int ft = 0; ft < 8; ++ft) {
+      const int f0 = 128 * w + 16 * ft;
+      if (which == 1) {
+        // dK^T = Gamma (kappa o W)^T + S^T Zn^T + Q^T N + K^T (M + M^T)
+        const f32x8 g0 = frag_rows(rec + Rec::G, DV, f0, 0, lane), g1 = frag_rows(rec + Rec::G, DV, f0, 32, lane);
+        const f32x8 s0 = frag_rows(rec + Rec::S, DV, f0, 0, lane), s1 = frag_rows(rec + Rec::S, DV, f0, 32, lane);
+        const f32x8 q0 = frag_cols(rec + Rec::Q, D, f0, 0, lane), q1 = frag_cols(rec + Rec::Q, D, f0, 32, lane);
+        const f32x8 k0 = frag_cols(rec + Rec::K, D, f0, 0, lane), k1 = frag_cols(rec + Rec::K, D, f0, 32, lane);
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+          f32x4 t = zero4();
+          t = mm<P>(t, g0, frag_rows(bW, LD, 16 * m, 0, lane));
+          t = mm<P>(t, g1, frag_rows(bW, LD, 16 * m, 32, lane));
+          t = mm<P>(t, s0, frag_rows(bdW, LD, 16 * m, 0, lane));
+          t = mm<P>(t, s1, frag_rows(bdW, LD, 16 * m, 32, lane));
+          t = mm<P>(t, q0, frag_cols(bXK, LD, 16 * m, 0, lane));
+          t = mm<P>(t, q1, frag_cols(bXK, LD, 16 * m, 32, lane));
+          t = mm<P>(t, k0, frag_rows(bX, LD, 16 * m, 0, lane));
+          t = mm<P>(t, k1, frag_rows(bX, LD, 16 * m, 32, lane));
+          acc[ft][m] = t;
+        }
+      } else {
+        // dQ^T = S^T (a o dY)^T + K^T N^T
+        const f32x8 s0 = frag_rows(rec + Rec::S, DV, f0, 0, lane), s1 = frag_rows(rec + Rec::S, DV, f0, 32, lane);
+        const f32x8 k0 = frag_cols(rec + Rec::K, D, f0, 0, lane), k1 = frag_cols(rec + Rec::K, D, f0, 32, lane);
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+          f32x4 t = zero4();
+          t = mm<P>(t, s0, frag_rows(bY, LD, 16 * m, 0, lane));
+          t = mm<P>(t, s1, frag_rows(bY, LD, 16 * m, 32, lane));
+          t = mm<P>(t, k0, frag_rows(bXK, LD, 16 * m, 0, lane));
+          t = mm<P>(t, k1, frag_rows(bXK, LD, 16 * m, 32, lane));
+          acc[ft][m] = t;
+        }
+      }
+    }
+    __syncthreads();  // every wave has read bW (kappa o W) before it becomes the dx^ accumulator
+#pragma unroll
+    for (int e = 0; e < 16; ++e) bW[r * LD + c0 + e] = 0.f;
+    __syncthreads();
+    lift_backward<P>(p, rec + (which == 0 ? Rec::Q : Rec::K), s_n, s_rd, bT, bW, acc, w, lane);
+    __syncthreads();
+    if (which == 0) {
+      write_dx<InT>(p, x, xb, p.dq, b * p.dqs0 + (t0 + r) * p.dqs1 + h * p.dqs2 + c0, bW, r, c0, rvalid);
+    } else {
+      write_dx<InT>(p, x, xb, p.dk, b * p.dks0 + (t0 + r) * p.dks1 + h * p.dks2 + c0, bW, r, c0, rvalid);
+    }
+    __syncthreads();
+  }
+}
+
+}  // namespace bwd
+
+using namespace bwd;
+
+static bool bwd_supported(const kdn_scan_args* f) {
+  return f->d_k == DK && f->D == D && f->d_v == DV && f->rule == 0 && f->feature_mode == 0 && !f->omega_lo &&
+         f->omega_head_stride == 0 && f->phase_head_stride == 0 && !f->inv_tau_head && !f->no_renorm &&
+         !f->cu_seqlens && !f->state_slots;
+}
+
+static int bwd_check(const kdn_scan_bwd_args* a) {
+  if (!a || !a->fwd) return KDN_ERR_INVALID_ARGUMENT;
+  const kdn_scan_args* f = a->fwd;
+  if (f->B <= 0 || f->T <= 0 || f->H <= 0 || !valid_dtype(f->in_dtype)) return KDN_ERR_INVALID_ARGUMENT;
+  if (!bwd_supported(f)) return KDN_ERR_UNSUPPORTED;
+  if (!f->q || !f->k || !f->v || !f->beta || !f->omega_bf16 || !f->phase) return KDN_ERR_INVALID_ARGUMENT;
+  if (!a->dy || !a->dq || !a->dk || !a->dv || !a->dbeta) return KDN_ERR_INVALID_ARGUMENT;
+  if (a->ddecay && !f->decay) return KDN_ERR_INVALID_ARGUMENT;
+  if (f->q_stride[2] < 0 || f->k_stride[2] < 0 || f->v_stride[2] < 0) return KDN_ERR_INVALID_ARGUMENT;
+  if (!aligned(f->omega_bf16, 8)) return KDN_ERR_MISALIGNED;
+  return KDN_OK;
+}
+
+static int64_t bwd_chunks(const kdn_scan_args* f) { return (f->T + C - 1) / C; }
+
+extern "C" size_t kdn_scan_bwd_workspace_bytes(const kdn_scan_bwd_args* a) {
+  if (bwd_check(a) != KDN_OK) return 0;
+  const kdn_scan_args* f = a->fwd;
+  return (size_t)(f->B * f->H * bwd_chunks(f)) * Rec::floats * sizeof(float);
+}
+
+template <class P, typename InT>
+static int bwd_launch(const Params& p, hipStream_t st) {
+  const dim3 chunk_grid((unsigned)p.nch, (unsigned)p.H, (unsigned)p.B);
+  const unsigned chain_wgs = (unsigned)(((p.B * p.H + 7) / 8) * 8 * 4);
+  hipLaunchKernelGGL((bwd_prep_kernel<P, InT>), chunk_grid, dim3(256), 0, st, p);
+  hipLaunchKernelGGL((bwd_chain_kernel<P, false>), dim3(chain_wgs), dim3(256), 0, st, p);
+  hipLaunchKernelGGL((bwd_chain_kernel<P, true>), dim3(chain_wgs), dim3(256), 0, st, p);
+  hipLaunchKernelGGL((bwd_grad_kernel<P, InT>), chunk_grid, dim3(256), 0, st, p);
+  return launch_status();
+}
+
+extern "C" int kdn_delta_scan_bwd(const kdn_scan_bwd_args* a, void* stream) {
+  const int rc = bwd_check(a);
+  if (rc != KDN_OK) return rc;
+  const kdn_scan_args* f = a->fwd;
+  const size_t need = kdn_scan_bwd_workspace_bytes(a);
+  if (!a->workspace || a->workspace_bytes < need) return KDN_ERR_WORKSPACE_TOO_SMALL;
+  if (!aligned(a->workspace, 256)) return KDN_ERR_MISALIGNED;
+  if (f->B > 65535 || f->H > 65535 || bwd_chunks(f) > 0x7fffffff) return KDN_ERR_UNSUPPORTED;
+  Params p = {};
+  p.B = f->B; p.T = f->T; p.H = f->H; p.nch = bwd_chunks(f);
+  p.q = f->q; p.qs0 = f->q_stride[0]; p.qs1 = f->q_stride[1]; p.qs2 = f->q_stride[2];
+  p.k = f->k; p.ks0 = f->k_stride[0]; p.ks1 = f->k_stride[1]; p.ks2 = f->k_stride[2];
+  p.v = f->v; p.vs0 = f->v_stride[0]; p.vs1 = f->v_stride[1]; p.vs2 = f->v_stride[2];
+  p.beta = f->beta; p.bs0 = f->beta_stride[0]; p.bs1 = f->beta_stride[1]; p.bs2 = f->beta_stride[2];
+  p.decay = f->decay; p.ds0 = f->decay_stride[0]; p.ds1 = f->decay_stride[1]; p.ds2 = f->decay_stride[2];
+  p.omega = reinterpret_cast<const __bf16*>(f->omega_bf16); p.phase = f->phase;
+  p.inv_tau = f->inv_tau; p.normalize = f->normalize_input;
+  p.init = f->initial_state;
+  p.is0 = f->init_stride[0]; p.is1 = f->init_stride[1]; p.is2 = f->init_stride[2]; p.is3 = f->init_stride[3];
+  p.dy = a->dy; p.ys0 = a->dy_stride[0]; p.ys1 = a->dy_stride[1]; p.ys2 = a->dy_stride[2];
+  p.dfin = a->d_final_state;
+  p.fs0 = a->dfinal_stride[0]; p.fs1 = a->dfinal_stride[1]; p.fs2 = a->dfinal_stride[2]; p.fs3 = a->dfinal_stride[3];
+  p.dq = a->dq; p.dqs0 = a->dq_stride[0]; p.dqs1 = a->dq_stride[1]; p.dqs2 = a->dq_stride[2];
+  p.dk = a->dk; p.dks0 = a->dk_stride[0]; p.dks1 = a->dk_stride[1]; p.dks2 = a->dk_stride[2];
+  p.dv = a->dv; p.dvs0 = a->dv_stride[0]; p.dvs1 = a->dv_stride[1]; p.dvs2 = a->dv_stride[2];
+  p.dbeta = a->dbeta; p.dbs0 = a->dbeta_stride[0]; p.dbs1 = a->dbeta_stride[1]; p.dbs2 = a->dbeta_stride[2];
+  p.ddecay = a->ddecay; p.dds0 = a->ddecay_stride[0]; p.dds1 = a->ddecay_stride[1]; p.dds2 = a->ddecay_stride[2];
+  p.dinit = a->d_initial_state;
+  p.dis0 = a->dinit_stride[0]; p.dis1 = a->dinit_stride[1]; p.dis2 = a->dinit_stride[2]; p.dis3 = a->dinit_stride[3];
+  p.ws = reinterpret_cast<float*>(a->workspace);
+  const hipStream_t st = as_stream(stream);
+  if (f->in_dtype == KDN_DTYPE_BF16) return bwd_launch<PrecF32, __bf16>(p, st);
+  return bwd_launch<PrecF32, float>(p, st);
+}
+
+}  // namespace kdn

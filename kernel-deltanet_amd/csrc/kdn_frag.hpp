@@ -80,6 +80,12 @@ template <class P>
 __device__ __forceinline__ void store_frag(void* base, int lane, const typename P::frag& f) {
   reinterpret_cast<typename P::frag*>(base)[lane] = f;
 }
+// Streaming store (nt): for data no kernel reads back while it could still be in L2, so that it does
+// not evict lines other kernels running at the same time are about to read.
+template <class P>
+__device__ __forceinline__ void store_frag_nt(void* base, int lane, const typename P::frag& f) {
+  __builtin_nontemporal_store(f, reinterpret_cast<typename P::frag*>(base) + lane);
+}
 
 // Read-only streaming loads that bypass nothing: plain global loads (the workspace is re-read once).
 __device__ __forceinline__ f32x4 ld4(const float* p) { return *reinterpret_cast<const f32x4*>(p); }

@@ -406,8 +406,10 @@ __global__ void __launch_bounds__(256) prep_kernel(ScanParams p) {
     }
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
-      store_frag<P>(ws + L::phiK + (size_t)(w * NJ + j) * 64 * L::FB, lane, cqk[1][j]);
-      store_frag<P>(ws + L::phiQ + (size_t)(w * NJ + j) * 64 * L::FB, lane, cqk[0][j]);
+      // The records are read back by the state and output kernels a segment or more later, long after
+      // they could still sit in L2: streaming stores keep them from evicting the state kernel's lines.
+      store_frag_nt<P>(ws + L::phiK + (size_t)(w * NJ + j) * 64 * L::FB, lane, cqk[1][j]);
+      store_frag_nt<P>(ws + L::phiQ + (size_t)(w * NJ + j) * 64 * L::FB, lane, cqk[0][j]);
       s_phik[(w * NJ + j) * 64 + lane] = cqk[1][j];
     }
     __syncthreads();
@@ -447,7 +449,7 @@ __global__ void __launch_bounds__(256) prep_kernel(ScanParams p) {
       }
 #pragma unroll
       for (int jb = 0; jb < 2; ++jb)
-        store_frag<P>(ws + L::Pm + (size_t)(w * 2 + jb) * 64 * L::FB, lane, P::from_f32(pair_to8(pt[2 * jb], pt[2 * jb + 1])));
+        store_frag_nt<P>(ws + L::Pm + (size_t)(w * 2 + jb) * 64 * L::FB, lane, P::from_f32(pair_to8(pt[2 * jb], pt[2 * jb + 1])));
     }
     if constexpr (RUN == 1) In::load_v(p, sq, h, t0, vraw);
 #pragma unroll
@@ -503,7 +505,7 @@ __global__ void __launch_bounds__(256) prep_kernel(ScanParams p) {
           tw[s] = p.linear ? 0.f : tv * s_beta[j] * __expf(s_g[j]) * s_sk[j];  // linear: E = U~
           tb[jb][s] = tv * s_beta[j];
         }
-        store_frag<P>(ws + L::Tp + (size_t)(w * 2 + jb) * 64 * L::FB, lane, P::from_f32(tw));
+        store_frag_nt<P>(ws + L::Tp + (size_t)(w * 2 + jb) * 64 * L::FB, lane, P::from_f32(tw));
       }
 #pragma unroll
       for (int n = 0; n < NV; ++n) {
@@ -528,7 +530,7 @@ __global__ void __launch_bounds__(256) prep_kernel(ScanParams p) {
             acc = P::mma(acc, P::from_f32(tb[jb]), P::from_f32(vv));
           }
         }
-        *reinterpret_cast<f32x4*>(ws + L::U + ((size_t)(w * NV + n) * 64 + lane) * 16) = acc;
+        __builtin_nontemporal_store(acc, reinterpret_cast<f32x4*>(ws + L::U + ((size_t)(w * NV + n) * 64 + lane) * 16));
       }
     }
   };

@@ -41,6 +41,8 @@ EXPORTED = (
     "kdn_pool_active",
     "kdn_pool_allocated_bytes",
     "kdn_pool_free_bytes",
+    "kdn_scan_bwd_workspace_bytes",
+    "kdn_delta_scan_bwd",
 )
 
 KDN_ERR_CAPACITY = -6
@@ -109,6 +111,23 @@ class RaggedArgs(ctypes.Structure):
     ]
 
 
+class ScanBwdArgs(ctypes.Structure):
+    """Mirror of struct kdn_scan_bwd_args (include/kdn.h)."""
+
+    _fields_ = [
+        ("fwd", ctypes.c_void_p),
+        ("dy", ctypes.c_void_p), ("dy_stride", _i64x3),
+        ("d_final_state", ctypes.c_void_p), ("dfinal_stride", _i64x4),
+        ("dq", ctypes.c_void_p), ("dq_stride", _i64x3),
+        ("dk", ctypes.c_void_p), ("dk_stride", _i64x3),
+        ("dv", ctypes.c_void_p), ("dv_stride", _i64x3),
+        ("dbeta", ctypes.c_void_p), ("dbeta_stride", _i64x3),
+        ("ddecay", ctypes.c_void_p), ("ddecay_stride", _i64x3),
+        ("d_initial_state", ctypes.c_void_p), ("dinit_stride", _i64x4),
+        ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_size_t),
+    ]
+
+
 _lib = None
 _lock = threading.Lock()
 
@@ -172,6 +191,10 @@ def lib() -> ctypes.CDLL:
                 fn = getattr(L, nm)
                 fn.argtypes = [vp]
                 fn.restype = i64
+            L.kdn_scan_bwd_workspace_bytes.argtypes = [ctypes.POINTER(ScanBwdArgs)]
+            L.kdn_scan_bwd_workspace_bytes.restype = sz
+            L.kdn_delta_scan_bwd.argtypes = [ctypes.POINTER(ScanBwdArgs), vp]
+            L.kdn_delta_scan_bwd.restype = ci
             _lib = L
     return _lib
 

@@ -282,6 +282,102 @@ def scan(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, beta: torch.Tensor, 
     return y, final_state
 
 
+def scan_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, beta: torch.Tensor,
+                  decay: Optional[torch.Tensor], omega_bf16: torch.Tensor, phase: torch.Tensor, inv_tau: float,
+                  dy: torch.Tensor, d_final_state: Optional[torch.Tensor] = None, normalize: bool = False,
+                  initial_state: Optional[torch.Tensor] = None, need_ddecay: bool = True,
+                  need_dinit: bool = True, workspace: Optional[torch.Tensor] = None):
+    """Gradients of `scan` (kdn_delta_scan_bwd) for the loss with dL/dy = dy and dL/d(final state) =
+    d_final_state (None: zero).  Same layouts as `scan`: q, k (B, T, H, 64), v and dy (B, T, H, 64),
+    beta and decay (B, T, H), states (B, H, 512, 64).  Returns float32
+    (dq, dk, dv, dbeta, ddecay or None, d_initial_state or None).  The structured lift with one shared
+    Omega and the delta rule only (the C entry point returns KDN_ERR_UNSUPPORTED otherwise)."""
+    for t, nm in ((q, "q"), (k, "k"), (v, "v"), (beta, "beta"), (dy, "dy")):
+        require_device(t, f"scan_backward: {nm}")
+    dev = q.device
+    if q.dim() != 4 or k.shape != q.shape or v.shape[:3] != q.shape[:3] or beta.shape != q.shape[:3] \
+            or dy.shape != v.shape:
+        raise ValueError(f"scan_backward: shapes q{tuple(q.shape)} k{tuple(k.shape)} v{tuple(v.shape)} "
+                         f"beta{tuple(beta.shape)} dy{tuple(dy.shape)}")
+    if k.dtype != q.dtype or v.dtype != q.dtype:
+        raise TypeError("scan_backward: q, k and v must share a dtype")
+    q, k, v = _last_contig(q), _last_contig(k), _last_contig(v)
+    beta = beta.to(torch.float32)
+    if decay is not None:
+        decay = decay.to(device=dev, dtype=torch.float32)
+    dy = _last_contig(dy.to(torch.float32))
+    B, T, H, d_k = q.shape
+    d_v = v.shape[-1]
+    fm = _features_on(FeatureMap(omega_bf16, phase), dev, H)
+    D = fm.dim(q)
+    if initial_state is not None:
+        initial_state = initial_state.to(device=dev, dtype=torch.float32)
+    if d_final_state is not None:
+        d_final_state = d_final_state.to(device=dev, dtype=torch.float32)
+        if tuple(d_final_state.shape) != (B, H, D, d_v):
+            raise ValueError(f"scan_backward: d_final_state must be (B, H, D, d_v) = {(B, H, D, d_v)}")
+    unused = torch.empty(1, device=dev, dtype=torch.float32).expand(B, H, D, d_v)  # fwd.final_state (ignored)
+    fa = scan_args(q, k, v, beta, decay, None, None, inv_tau, normalize, initial_state, unused, dy, None, 0, fm)
+    f32 = dict(device=dev, dtype=torch.float32)
+    dq, dk = torch.empty(B, T, H, d_k, **f32), torch.empty(B, T, H, d_k, **f32)
+    dv, dbeta = torch.empty(B, T, H, d_v, **f32), torch.empty(B, T, H, **f32)
+    ddecay = torch.empty(B, T, H, **f32) if (decay is not None and need_ddecay) else None
+    dinit = torch.empty(B, H, D, d_v, **f32) if need_dinit else None
+    a = N.ScanBwdArgs()
+    a.fwd = ctypes.addressof(fa)
+    a.dy, a.dy_stride = dy.data_ptr(), N._i64x3(*dy.stride()[:3])
+    if d_final_state is not None:
+        a.d_final_state, a.dfinal_stride = d_final_state.data_ptr(), N._i64x4(*d_final_state.stride())
+    for nm, t in (("dq", dq), ("dk", dk), ("dv", dv)):
+        setattr(a, nm, t.data_ptr())
+        setattr(a, nm + "_stride", N._i64x3(*t.stride()[:3]))
+    a.dbeta, a.dbeta_stride = dbeta.data_ptr(), N._i64x3(*dbeta.stride())
+    if ddecay is not None:
+        a.ddecay, a.ddecay_stride = ddecay.data_ptr(), N._i64x3(*ddecay.stride())
+    if dinit is not None:
+        a.d_initial_state, a.dinit_stride = dinit.data_ptr(), N._i64x4(*dinit.stride())
+    nbytes = N.lib().kdn_scan_bwd_workspace_bytes(ctypes.byref(a))
+    if nbytes == 0:
+        raise ValueError("scan_backward: unsupported request (kdn_scan_bwd_workspace_bytes returned 0; the "
+                         "backward covers d_k = 64, D = 512, d_v = 64 with the shared structured lift)")
+    if workspace is None or workspace.numel() * workspace.element_size() < nbytes:
+        workspace = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    a.workspace, a.workspace_bytes = workspace.data_ptr(), workspace.numel() * workspace.element_size()
+    with torch.cuda.device(dev):
+        N.check(N.lib().kdn_delta_scan_bwd(ctypes.byref(a), ctypes.c_void_p(_stream(dev))), "kdn_delta_scan_bwd")
+    return dq, dk, dv, dbeta, ddecay, dinit
+
+
+class _Scan(torch.autograd.Function):
+    """`scan` with its backward (kdn_delta_scan_bwd); the autograd node of the differentiable surfaces."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, beta, decay, initial_state, omega_bf16, phase, inv_tau, normalize):
+        y, final = scan(q, k, v, beta, decay, omega_bf16, phase, inv_tau, normalize=normalize,
+                        initial_state=initial_state)
+        ctx.save_for_backward(q, k, v, beta, decay, initial_state, omega_bf16, phase)
+        ctx.inv_tau, ctx.normalize = inv_tau, normalize
+        return y, final
+
+    @staticmethod
+    def backward(ctx, dy, dfinal):
+        q, k, v, beta, decay, init, omega_bf16, phase = ctx.saved_tensors
+        need = ctx.needs_input_grad
+        dq, dk, dv, dbeta, ddecay, dinit = scan_backward(
+            q, k, v, beta, decay, omega_bf16, phase, ctx.inv_tau, dy, dfinal, normalize=ctx.normalize,
+            initial_state=init, need_ddecay=bool(need[4]), need_dinit=bool(need[5]))
+        return (dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), dbeta.to(beta.dtype),
+                None if ddecay is None else ddecay.to(decay.dtype),
+                None if dinit is None or init is None else dinit.to(init.dtype), None, None, None, None)
+
+
+def scan_autograd(q, k, v, beta, decay, omega_bf16, phase, inv_tau, normalize: bool = False,
+                  initial_state: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor]:
+    """`scan` (default schedule) recorded for autograd: gradients flow to q, k, v, beta, decay and
+    initial_state through kdn_delta_scan_bwd.  Returns (y (B, T, H, d_v), final_state (B, H, D, d_v))."""
+    return _Scan.apply(q, k, v, beta, decay, initial_state, omega_bf16, phase, inv_tau, normalize)
+
+
 def _features_on(fm: FeatureMap, dev: torch.device, H: int) -> FeatureMap:
     """The feature map with its tensors on `dev` in the layouts the library reads (bf16 Omega rows
     and float32 phases / 1/tau, innermost dimension contiguous), shapes checked."""

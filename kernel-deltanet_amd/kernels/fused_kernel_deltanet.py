@@ -50,6 +50,20 @@ def fused_chunked_deltanet_forward(
     for t, nm in ((q, "q"), (k, "k"), (v, "v"), (beta, "beta")):
         ops.require_device(t, f"fused_chunked_deltanet_forward: {nm}")
     dev = k.device
+    inputs = (q, k, v, beta, decay, initial_state)
+    if torch.is_grad_enabled() and any(isinstance(t, torch.Tensor) and t.requires_grad for t in inputs):
+        # differentiable path: the scan's autograd node runs kdn_delta_scan_bwd in the backward
+        init4 = None
+        if initial_state is not None:
+            if tuple(initial_state.shape) != (B, d_v, D):
+                raise ValueError(f"initial_state must be (B, d_v, D) = {(B, d_v, D)}")
+            init4 = initial_state.to(device=dev, dtype=torch.float32).unsqueeze(1).transpose(2, 3)
+        y4, f4 = ops.scan_autograd(q.unsqueeze(2), k.unsqueeze(2), v.unsqueeze(2), beta.unsqueeze(-1),
+                                   None if decay is None else decay.unsqueeze(-1), fwht_proj.device_omega(dev),
+                                   fwht_proj.device_phase(dev), fwht_proj.tau_star_inv, initial_state=init4)
+        final = f4.squeeze(1).transpose(1, 2)
+        s_dtype = initial_state.dtype if initial_state is not None else k.dtype
+        return y4.squeeze(2), (final if s_dtype == torch.float32 else final.to(s_dtype))
     y = torch.empty(B, T, d_v, device=dev, dtype=q.dtype)
     final = torch.empty(B, d_v, D, device=dev, dtype=torch.float32)
     init4 = None
@@ -67,17 +81,30 @@ def fused_chunked_deltanet_forward(
 
 
 class FusedKernelDeltaNetFunction(torch.autograd.Function):
-    """Reference: kernels/fused_kernel_deltanet.py:158-179 (forward returns Y only)."""
+    """Reference: kernels/fused_kernel_deltanet.py:158-179 (forward returns Y only).  The reference's
+    backward re-runs its forward under autograd; here it is kdn_delta_scan_bwd (gradients for q, k, v,
+    beta and decay; none for the projection or chunk_size)."""
 
     @staticmethod
     def forward(ctx, q, k, v, beta, decay, fwht_proj, chunk_size=64):
-        Y, _ = fused_chunked_deltanet_forward(q, k, v, beta, decay, fwht_proj, chunk_size)
+        with torch.no_grad():
+            Y, _ = fused_chunked_deltanet_forward(q, k, v, beta, decay, fwht_proj, chunk_size)
+        ctx.save_for_backward(q, k, v, beta, decay)
+        ctx.fwht_proj = fwht_proj
         return Y
 
     @staticmethod
     def backward(ctx, grad_output):
-        raise NotImplementedError("the backward pass of the delta-rule scan is not implemented on MI355X "
-                                  "(forward/prefill only)")
+        q, k, v, beta, decay = ctx.saved_tensors
+        p = ctx.fwht_proj
+        dev = q.device
+        need = ctx.needs_input_grad
+        dq, dk, dv, db, dd, _ = ops.scan_backward(
+            q.unsqueeze(2), k.unsqueeze(2), v.unsqueeze(2), beta.unsqueeze(-1),
+            None if decay is None else decay.unsqueeze(-1), p.device_omega(dev), p.device_phase(dev),
+            p.tau_star_inv, grad_output.unsqueeze(2), need_ddecay=bool(need[4]), need_dinit=False)
+        return (dq.squeeze(2).to(q.dtype), dk.squeeze(2).to(k.dtype), dv.squeeze(2).to(v.dtype),
+                db.squeeze(-1).to(beta.dtype), None if dd is None else dd.squeeze(-1).to(decay.dtype), None, None)
 
 
 class FusedKernelDeltaNet(nn.Module):

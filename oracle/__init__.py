@@ -31,4 +31,8 @@ How each function is pinned (see tests/test_oracle_*.py):
                     S_{t-1} phi_k(t) then vanishes), and differs from it otherwise.
   linear_chunked    equals linear_recurrence to 1e-12 for several chunk sizes and ragged T (the reference's
                     own acceptance check, tests/test_parallel_vs_recurrent.py:19-51).
+  token_recurrence_torch / delta_rule_torch (the gradient oracle of the backward pass)
+                    forward equals token_recurrence / delta_rule to 1e-12; torch.autograd.gradcheck
+                    (central finite differences, float64) of every input -- q, k, v, beta, lambda, S_0 --
+                    through the lift and the recurrence (pattern tests/test_fused_chunk_kernel.py:54-72).
 """

@@ -44,6 +44,36 @@ def token_recurrence(phi_q, phi_k, v, beta, decay=None, S0=None) -> Tuple[np.nda
     return Y, S
 
 
+def token_recurrence_torch(phi_q: torch.Tensor, phi_k: torch.Tensor, v: torch.Tensor, beta: torch.Tensor,
+                           decay: Optional[torch.Tensor] = None, S0: Optional[torch.Tensor] = None
+                           ) -> Tuple[torch.Tensor, torch.Tensor]:
+    """token_recurrence on torch tensors, so that autograd differentiates the defining rule: the same
+    loop (tests/test_fused_kernel.py:53-65), with lambda clamped to [1e-5, 1] as the forward clamps
+    log lambda (kernels/fused_kernel_deltanet.py:74).  The gradient oracle of the backward pass, the
+    role the reference gives torch autograd over its forward (kernels/fused_kernel_deltanet.py:168-179).
+    Shapes as token_recurrence; returns (Y (B, T, d_v), S (B, d_v, D))."""
+    B, T, D = phi_k.shape
+    dv = v.shape[-1]
+    S = torch.zeros(B, dv, D, dtype=phi_k.dtype) if S0 is None else S0
+    ys = []
+    for t in range(T):
+        ys.append(torch.einsum("bvd,bd->bv", S, phi_q[:, t]))
+        s_phi = torch.einsum("bvd,bd->bv", S, phi_k[:, t])
+        lam = 1.0 if decay is None else decay[:, t].clamp(1e-5, 1.0)[:, None, None]
+        b = beta[:, t, None, None]
+        S = lam * (S - b * s_phi[:, :, None] * phi_k[:, t, None, :]) + b * v[:, t, :, None] * phi_k[:, t, None, :]
+    return torch.stack(ys, 1), S
+
+
+def delta_rule_torch(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, beta: torch.Tensor,
+                     decay: Optional[torch.Tensor], proj: dict, initial_state: Optional[torch.Tensor] = None,
+                     normalize: bool = False) -> Tuple[torch.Tensor, torch.Tensor]:
+    """delta_rule on torch tensors (lift by _torch_lift, then token_recurrence_torch): differentiable
+    end to end, in the inputs' dtype (float64 for the gradient oracle)."""
+    return token_recurrence_torch(_torch_lift(q, proj, normalize), _torch_lift(k, proj, normalize), v, beta, decay,
+                                  initial_state)
+
+
 def delta_rule(q, k, v, beta, decay, proj: dict, initial_state=None, normalize: bool = False):
     """Float64 definition of the whole path: lift q and k, then the token recurrence."""
     return token_recurrence(olift.lift(q, proj, normalize), olift.lift(k, proj, normalize), v, beta, decay,
