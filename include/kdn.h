@@ -194,7 +194,7 @@ int kdn_scan_output(const kdn_scan_args* a, int64_t chunk0, int64_t nchunks, voi
  * (B, T, H, d_k), dv (B, T, H, d_v), dbeta, ddecay (B, T, H), d_initial_state (B, H, D, d_v).
  * d_final_state NULL means dL/dS_T = 0; ddecay (allowed only with decay) and d_initial_state may be
  * NULL.  The gradient of lambda is zero where the forward's clamp to [1e-5, 1] is active.  The
- * workspace holds one fp32 record per (batch, head, 64-token chunk) (854,016 bytes each; 256-byte
+ * workspace holds one fp32 record per (batch, head, 64-token chunk) (1,116,160 bytes each; 256-byte
  * aligned). */
 typedef struct kdn_scan_bwd_args {
   const kdn_scan_args* fwd;

@@ -20,11 +20,14 @@
 // Notation per chunk (tokens i, j in 0..63): l_i = sum_{t <= i} log clamp(lambda_t, 1e-5, 1), g = e^l,
 // g_C = g_63, a_i = g_{i-1} (a_0 = 1), kappa_j = g_C / g_j; A_ij = beta_i (g_i/g_j) k_i.k_j and
 // P_ij = (g_{i-1}/g_j) q_i.k_j for j < i; Y = diag(a) Q S^T + P W; S_C^T = g_C S^T + K^T diag(kappa) W.
-// Every matrix is fp32 and row-major in a per-(head, chunk) record of the workspace; products use the
-// fp32 16x16x4 MFMA through the fragment conventions of kdn_frag.hpp.
+// Every matrix is fp32 and row-major in a per-(head, chunk) record of the workspace.  Products use the
+// MFMA fragment conventions of kdn_frag.hpp: the lift and the 64 x 64 chunk algebra in fp32
+// (16x16x4 f32), the contractions over the 512 features in the precision policy P (fp32 for fp32
+// inputs, bf16 operands with fp32 accumulation for bf16 inputs).
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdint.h>
+#include <type_traits>
 #include "kdn_frag.hpp"
 #include "kdn_internal.hpp"
 
@@ -38,7 +41,7 @@ constexpr int LD = 68;  // LDS row stride (floats) of a 64-wide tile: rows stay 
 struct Rec {
   static constexpr size_t Q = 0;                // [64][512] lifted, normalised q rows (0 past T)
   static constexpr size_t K = Q + C * D;        // [64][512] lifted, normalised k rows (0 past T)
-  static constexpr size_t H1 = K + C * D;       // [512][64] Q^T (a o dY)
+  static constexpr size_t H1 = K + C * D;       // Q^T (a o dY) as 16x16 tiles [ft 32][n 4][lane] f32x4
   static constexpr size_t S = H1 + D * DV;      // [512][64] S^T at the chunk start
   static constexpr size_t G = S + D * DV;       // [512][64] dL/dS^T at the chunk end
   static constexpr size_t T = G + D * DV;       // [64][64] (I + A)^-1
@@ -47,14 +50,18 @@ struct Rec {
   static constexpr size_t P = TPT + C * C;      // [64][64]
   static constexpr size_t GKK = P + C * C;      // [64][64] K K^T
   static constexpr size_t GQK = GKK + C * C;    // [64][64] Q K^T
-  static constexpr size_t U = GQK + C * C;      // [64][64] U~ = T (beta o V)
-  static constexpr size_t R = U + C * DV;       // [64][64] P^T dY
+  static constexpr size_t U = GQK + C * C;      // U~ = T (beta o V) as tiles [m 4][n 4][lane] f32x4
+  static constexpr size_t R = U + C * DV;       // P^T dY, tiles as U~
   static constexpr size_t W = R + C * DV;       // [64][64] W = U~ - Tp X_K
   static constexpr size_t XK = W + C * DV;      // [64][64] K S^T
   static constexpr size_t DW = XK + C * DV;     // [64][64] dL/dW
   static constexpr size_t X = DW + C * DV;      // [64][64] K Gamma
   static constexpr size_t VEC = X + C * DV;     // l[64], beta[64], |phi~_q|[64], |phi~_k|[64]
-  static constexpr size_t floats = VEC + 512;
+  // K in MFMA fragment order for the chains (one 16- or 32-byte load per lane and fragment), in the
+  // precision policy's fragment type (bf16x8 or f32x8; the area is sized for f32x8):
+  static constexpr size_t KXF = VEC + 512;      // [m 4][jb 16][lane]: rows 16m.., features 32jb..
+  static constexpr size_t KTF = KXF + C * D;    // [ft 32][jb 2][lane]: K^T rows 16ft.., tokens 32jb..
+  static constexpr size_t floats = KTF + C * D;
 };
 static_assert((Rec::floats * 4) % 256 == 0, "records stay 256-byte aligned");
 
@@ -115,6 +122,16 @@ __device__ __forceinline__ f32x8 frag_cols_bf16(const __bf16* base, int ld, int 
 #pragma unroll
   for (int s = 0; s < 8; ++s) r[s] = (float)base[(size_t)(k0 + kappa(lane, s)) * ld + c0 + (lane & 15)];
   return r;
+}
+
+// cos / sin of an angle in radians, branch-free: the angle in revolutions reduced to [0, 1) (v_fract),
+// then the hardware v_cos_f32 / v_sin_f32 (which take revolutions).  Absolute error ~1e-6 at the
+// angles of the lift (|s| up to ~100 rad).
+__device__ __forceinline__ float cos_rad(float s) {
+  return __builtin_amdgcn_cosf(__builtin_amdgcn_fractf(s * 0.15915494309189535f));
+}
+__device__ __forceinline__ float sin_rad(float s) {
+  return __builtin_amdgcn_sinf(__builtin_amdgcn_fractf(s * 0.15915494309189535f));
 }
 
 template <class P>
@@ -213,85 +230,109 @@ __global__ void __launch_bounds__(256) bwd_prep_kernel(Params p) {
     for (int e = 0; e < 16; ++e) xs[r * LD + c0 + e] = part[e];
     __syncthreads();
 
-    // phi~ (tokens x this wave's 128 features): tile [ft][m] rows token 16m + .., column feature.
-    f32x4 acc[8][4];
-    f32x8 xa[4][2];
-#pragma unroll
-    for (int m = 0; m < 4; ++m)
-#pragma unroll
-      for (int jb = 0; jb < 2; ++jb) xa[m][jb] = frag_rows(xs, LD, 16 * m, 32 * jb, lane);
-    float ss[4][4];
-#pragma unroll
-    for (int m = 0; m < 4; ++m)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) ss[m][i] = 0.f;
-#pragma unroll
-    for (int ft = 0; ft < 8; ++ft) {
-      const int f0 = 128 * w + 16 * ft;
-      const f32x8 o0 = frag_rows_bf16(p.omega, DK, f0, 0, lane), o1 = frag_rows_bf16(p.omega, DK, f0, 32, lane);
-      const float ph = p.phase[f0 + (lane & 15)];
-#pragma unroll
-      for (int m = 0; m < 4; ++m) {
-        f32x4 s = mm<P>(mm<P>(zero4(), xa[m][0], o0), xa[m][1], o1);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float v = amp * cosf(s[i] * p.inv_tau + ph);
-          s[i] = v;
-          ss[m][i] += v * v;
-        }
-        acc[ft][m] = s;
-      }
-    }
-#pragma unroll
-    for (int m = 0; m < 4; ++m)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float v = sum_row16(ss[m][i]);
-        if ((lane & 15) == 0) s_red[w][16 * m + 4 * (lane >> 4) + i] = v;
-      }
-    __syncthreads();
-    if (tid < 64) {
-      const float n = sqrtf(s_red[0][tid] + s_red[1][tid] + s_red[2][tid] + s_red[3][tid]);
-      s_n[tid] = n;
-      rec[Rec::VEC + 128 + 64 * which + tid] = n;
-    }
-    __syncthreads();
+    // phi~ (tokens x this wave's 128 features), in two halves of 32 tokens: tile [ft][u] holds rows
+    // token 16 (2 hm + u) + .., column feature.  Normalised rows go straight to the record.
     float* phi = rec + (which == 0 ? Rec::Q : Rec::K);
+    for (int hm = 0; hm < 2; ++hm) {
+      f32x4 acc[8][2];
+      f32x8 xa[2][2];
 #pragma unroll
-    for (int m = 0; m < 4; ++m)
+      for (int u = 0; u < 2; ++u)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int row = 16 * m + 4 * (lane >> 4) + i;
-        const float sc = (t0 + row < p.T) ? 1.f / (s_n[row] + 1e-8f) : 0.f;
+        for (int jb = 0; jb < 2; ++jb) xa[u][jb] = frag_rows(xs, LD, 16 * (2 * hm + u), 32 * jb, lane);
+      float ss[2][4];
 #pragma unroll
-        for (int ft = 0; ft < 8; ++ft) {
-          acc[ft][m][i] *= sc;
-          phi[(size_t)row * D + 128 * w + 16 * ft + (lane & 15)] = acc[ft][m][i];
-        }
-      }
-    if (which == 0) {
-      // H = Q^T (a o dY): A = phi_q^T fragments straight from the accumulators.
-      f32x8 yb[4][2];
+      for (int u = 0; u < 2; ++u)
 #pragma unroll
-      for (int n = 0; n < 4; ++n)
-#pragma unroll
-        for (int jb = 0; jb < 2; ++jb) yb[n][jb] = frag_cols(bA, LD, 16 * n, 32 * jb, lane);
+        for (int i = 0; i < 4; ++i) ss[u][i] = 0.f;
 #pragma unroll
       for (int ft = 0; ft < 8; ++ft) {
-        const f32x8 qa0 = pair_to8(acc[ft][0], acc[ft][1]), qa1 = pair_to8(acc[ft][2], acc[ft][3]);
+        const int f0 = 128 * w + 16 * ft;
+        const f32x8 o0 = frag_rows_bf16(p.omega, DK, f0, 0, lane), o1 = frag_rows_bf16(p.omega, DK, f0, 32, lane);
+        const float ph = p.phase[f0 + (lane & 15)];
 #pragma unroll
-        for (int n = 0; n < 4; ++n) {
-          const f32x4 hv = mm<P>(mm<P>(zero4(), qa0, yb[n][0]), qa1, yb[n][1]);
+        for (int u = 0; u < 2; ++u) {
+          f32x4 sv = mm<PrecF32>(mm<PrecF32>(zero4(), xa[u][0], o0), xa[u][1], o1);
 #pragma unroll
-          for (int i = 0; i < 4; ++i)
-            rec[Rec::H1 + (size_t)(128 * w + 16 * ft + 4 * (lane >> 4) + i) * DV + 16 * n + (lane & 15)] = hv[i];
+          for (int i = 0; i < 4; ++i) {
+            const float v = amp * cos_rad(sv[i] * p.inv_tau + ph);
+            sv[i] = v;
+            ss[u][i] += v * v;
+          }
+          acc[ft][u] = sv;
         }
+        __builtin_amdgcn_sched_barrier(0);  // one feature tile per scheduling region (no operand hoisting)
       }
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float v = sum_row16(ss[u][i]);
+          if ((lane & 15) == 0) s_red[w][32 * hm + 16 * u + 4 * (lane >> 4) + i] = v;
+        }
+      __syncthreads();
+      if (tid < 32) {
+        const int row = 32 * hm + tid;
+        const float n = sqrtf(s_red[0][row] + s_red[1][row] + s_red[2][row] + s_red[3][row]);
+        s_n[row] = n;
+        rec[Rec::VEC + 128 + 64 * which + row] = n;
+      }
+      __syncthreads();
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int row = 32 * hm + 16 * u + 4 * (lane >> 4) + i;
+          const float sc = (t0 + row < p.T) ? 1.f / (s_n[row] + 1e-8f) : 0.f;
+#pragma unroll
+          for (int ft = 0; ft < 8; ++ft) phi[(size_t)row * D + 128 * w + 16 * ft + (lane & 15)] = acc[ft][u][i] * sc;
+        }
     }
     __syncthreads();
   }
   __threadfence();
   __syncthreads();
+
+  // K packed in fragment order for the chains: wave w the K-row fragments of feature blocks 4w .. 4w+3
+  // and the K^T-row fragments of feature tiles 8w .. 8w+7.
+  {
+    using frag = typename P::frag;
+    const float* K = rec + Rec::K;
+    frag* kxf = reinterpret_cast<frag*>(rec + Rec::KXF);
+    frag* ktf = reinterpret_cast<frag*>(rec + Rec::KTF);
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj)
+        kxf[(m * 16 + 4 * w + jj) * 64 + lane] = P::from_f32(frag_rows(K, D, 16 * m, 32 * (4 * w + jj), lane));
+#pragma unroll
+    for (int t = 0; t < 8; ++t)
+#pragma unroll
+      for (int jb = 0; jb < 2; ++jb)
+        ktf[((8 * w + t) * 2 + jb) * 64 + lane] = P::from_f32(frag_cols(K, D, 16 * (8 * w + t), 32 * jb, lane));
+  }
+
+  // H = Q^T (a o dY) from the Q rows just written (A = Q^T fragments, B = a o dY from LDS).
+  {
+    const float* Q = rec + Rec::Q;
+    f32x8 yb[4][2];
+#pragma unroll
+    for (int n = 0; n < 4; ++n)
+#pragma unroll
+      for (int jb = 0; jb < 2; ++jb) yb[n][jb] = frag_cols(bA, LD, 16 * n, 32 * jb, lane);
+#pragma unroll
+    for (int ft = 0; ft < 8; ++ft) {
+      const int f0 = 128 * w + 16 * ft;
+      const f32x8 qa0 = frag_cols(Q, D, f0, 0, lane), qa1 = frag_cols(Q, D, f0, 32, lane);
+#pragma unroll
+      for (int n = 0; n < 4; ++n) {
+        const f32x4 hv = mm<P>(mm<P>(zero4(), qa0, yb[n][0]), qa1, yb[n][1]);
+        reinterpret_cast<f32x4*>(rec + Rec::H1)[((8 * w + ft) * 4 + n) * 64 + lane] = hv;
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  __syncthreads();  // a o dY in bA is dead from here on (bA becomes A below)
 
   // Gram matrices (row tile w) from the rows just written; A and P into LDS.
   {
@@ -323,14 +364,25 @@ __global__ void __launch_bounds__(256) bwd_prep_kernel(Params p) {
       }
   }
   __syncthreads();
-  // T = (I + A)^-1 by forward substitution, one column per thread.
-  if (tid < C) {
-    const int col = tid;
+  // T = (I + A)^-1 by forward substitution: column 16w + (lane >> 2) per lane quad, lane pq = lane & 3
+  // keeping rows 4k + pq in registers; each row's dot product is split over the quad.
+  {
+    const int col = 16 * w + (lane >> 2), pq = lane & 3;
+    float Tr[16];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) Tr[k] = 0.f;
+#pragma unroll
     for (int i = 0; i < C; ++i) {
-      float acc = (i == col) ? 1.f : 0.f;
-      for (int j = col; j < i; ++j) acc -= bA[i * LD + j] * bT[j * LD + col];
-      bT[i * LD + col] = (i >= col) ? acc : 0.f;
+      float part = 0.f;
+#pragma unroll
+      for (int k = 0; k < (i + 3) / 4; ++k) part += bA[i * LD + 4 * k + pq] * Tr[k];
+      part += __shfl_xor(part, 1);
+      part += __shfl_xor(part, 2);
+      const float val = (i == col ? 1.f : 0.f) - part;
+      if (pq == (i & 3)) Tr[i >> 2] = val;
     }
+#pragma unroll
+    for (int k = 0; k < 16; ++k) bT[(4 * k + pq) * LD + col] = Tr[k];
   }
   __syncthreads();
   for (int idx = tid; idx < C * C; idx += 256) {
@@ -356,14 +408,10 @@ __global__ void __launch_bounds__(256) bwd_prep_kernel(Params p) {
     const f32x8 pa0 = frag_cols(bP, LD, 16 * w, 0, lane), pa1 = frag_cols(bP, LD, 16 * w, 32, lane);
 #pragma unroll
     for (int n = 0; n < 4; ++n) {
-      const f32x4 u = mm<P>(mm<P>(zero4(), ta0, frag_cols(xs, LD, 16 * n, 0, lane)), ta1, frag_cols(xs, LD, 16 * n, 32, lane));
-      const f32x4 rr = mm<P>(mm<P>(zero4(), pa0, frag_cols(bY, LD, 16 * n, 0, lane)), pa1, frag_cols(bY, LD, 16 * n, 32, lane));
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int ri = 16 * w + 4 * (lane >> 4) + i, cj = 16 * n + (lane & 15);
-        rec[Rec::U + ri * DV + cj] = u[i];
-        rec[Rec::R + ri * DV + cj] = rr[i];
-      }
+      const f32x4 u = mm<PrecF32>(mm<PrecF32>(zero4(), ta0, frag_cols(xs, LD, 16 * n, 0, lane)), ta1, frag_cols(xs, LD, 16 * n, 32, lane));
+      const f32x4 rr = mm<PrecF32>(mm<PrecF32>(zero4(), pa0, frag_cols(bY, LD, 16 * n, 0, lane)), pa1, frag_cols(bY, LD, 16 * n, 32, lane));
+      reinterpret_cast<f32x4*>(rec + Rec::U)[(w * 4 + n) * 64 + lane] = u;
+      reinterpret_cast<f32x4*>(rec + Rec::R)[(w * 4 + n) * 64 + lane] = rr;
     }
   }
 }
@@ -372,11 +420,146 @@ __global__ void __launch_bounds__(256) bwd_prep_kernel(Params p) {
 // grid: 8 * ceil(B*H / 8) * 4 workgroups of 256 threads; workgroup (head-batch hb, value tile n) with
 // the four value tiles of a head on one XCD.  Wave w keeps rows 128w .. 128w+127 of its 512 x 16 slice
 // of the carried matrix (S^T forward, Gamma backward) in registers.
+//
+// Per chunk: store the slice (chunk start S^T / chunk end Gamma); X = K Sigma (partial over the wave's
+// features, reduced through LDS); forward W = U~ - Tp X_K and Z = kappa o W, reverse dW = R + kappa o X
+// and Z = -Tp^T dW; Sigma <- g_C Sigma (+ H) + K^T Z.  With bf16 fragments the K-row fragments of the
+// next chunk are loaded one iteration ahead (two register sets); every other operand is issued at the
+// top of its own iteration, ahead of the first barrier, and the next chunk's lines are prefetched to L2.
+template <class P>
+struct ChainK {
+  typename P::frag kx[4][4];  // K rows 16m .., features 128w + 32jj ..
+};
+
+template <class P>
+__device__ __forceinline__ void chain_load_kx(ChainK<P>& o, const float* rec, int w, int lane) {
+  const typename P::frag* kx = reinterpret_cast<const typename P::frag*>(rec + Rec::KXF);
+#pragma unroll
+  for (int m = 0; m < 4; ++m)
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) o.kx[m][jj] = kx[(m * 16 + 4 * w + jj) * 64 + lane];
+}
+
+struct ChainShared {
+  f32x4 xp[4][4][64];
+  f32x4 x[4][64];
+  f32x4 z[4][64];
+};
+
+template <class P, bool REV, bool PIPE>
+__device__ __forceinline__ bool chain_step(const Params& p, ChainShared& sh, int64_t b, int64_t h, int64_t step,
+                                           ChainK<P>& cur, ChainK<P>& nxt, f32x4 (&Sg)[8], int w, int lane, int n,
+                                           unsigned& sink) {
+  using frag = typename P::frag;
+  const int vc = 16 * n + (lane & 15);
+  const int64_t c = REV ? p.nch - 1 - step : step;
+  const bool more = step + 1 < p.nch;
+  const int64_t cn = REV ? c - 1 : c + 1;
+  float* rec = record(p, b, h, c);
+  if constexpr (!PIPE) chain_load_kx<P>(cur, rec, w, lane);
+  // operands used later in this iteration
+  const f32x8 tp0 = frag_rows(rec + (REV ? Rec::TPT : Rec::TP), C, 16 * w, 0, lane);
+  const f32x8 tp1 = frag_rows(rec + (REV ? Rec::TPT : Rec::TP), C, 16 * w, 32, lane);
+  const f32x4 ur = reinterpret_cast<const f32x4*>(rec + (REV ? Rec::R : Rec::U))[(w * 4 + n) * 64 + lane];
+  const f32x4 lr = *reinterpret_cast<const f32x4*>(rec + Rec::VEC + 16 * w + 4 * (lane >> 4));
+  const float l63 = rec[Rec::VEC + 63];
+  unsigned pf = 0;  // L2-prefetch loads, folded into `sink` at the end of the step (no early wait)
+  if (more) {
+    const float* nrec = record(p, b, h, cn);
+    if constexpr (PIPE) chain_load_kx<P>(nxt, nrec, w, lane);
+    // L2 prefetch of the next chunk: one dword per 128-byte line, spread over the head's 4 workgroups
+    const unsigned* nr = reinterpret_cast<const unsigned*>(nrec);
+    const int idx = n * 256 + (int)threadIdx.x;
+    if (idx < 512 * (int)sizeof(frag) / 16) pf += nr[Rec::KTF + 32 * idx];
+    if (idx < 128) pf += nr[(REV ? Rec::TPT : Rec::TP) + 32 * idx];
+    else if (idx < 256) pf += nr[(REV ? Rec::R : Rec::U) + 32 * (idx - 128)];
+    else if (idx < 272) pf += nr[Rec::VEC + 32 * (idx - 256)];
+    if constexpr (!PIPE) pf += nr[Rec::KXF + 32 * idx];
+    if constexpr (REV) pf += nr[Rec::H1 + 32 * idx];
+  }
+
+  float* dst = rec + (REV ? Rec::G : Rec::S);
+#pragma unroll
+  for (int t = 0; t < 8; ++t)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dst[(size_t)(128 * w + 16 * t + 4 * (lane >> 4) + i) * DV + vc] = Sg[t][i];
+
+  // K times the carried slice, partial over this wave's features
+  f32x4 xp[4];
+#pragma unroll
+  for (int m = 0; m < 4; ++m) xp[m] = zero4();
+#pragma unroll
+  for (int jj = 0; jj < 4; ++jj) {
+    const frag sb = P::from_f32(pair_to8(Sg[2 * jj], Sg[2 * jj + 1]));
+#pragma unroll
+    for (int m = 0; m < 4; ++m) xp[m] = P::mma(xp[m], cur.kx[m][jj], sb);
+  }
+#pragma unroll
+  for (int m = 0; m < 4; ++m) sh.xp[w][m][lane] = xp[m];
+  // the old slice is dead past the products above: apply g_C now
+  const float gC = expf(l63);
+#pragma unroll
+  for (int t = 0; t < 8; ++t) Sg[t] = Sg[t] * gC;
+  __syncthreads();
+  f32x4 hh[8];
+  if constexpr (REV) {
+#pragma unroll
+    for (int t = 0; t < 8; ++t) hh[t] = reinterpret_cast<const f32x4*>(rec + Rec::H1)[((8 * w + t) * 4 + n) * 64 + lane];
+  }
+  frag kt[8][2];
+  {
+    const frag* ktf = reinterpret_cast<const frag*>(rec + Rec::KTF);
+#pragma unroll
+    for (int t = 0; t < 8; ++t)
+#pragma unroll
+      for (int jb = 0; jb < 2; ++jb) kt[t][jb] = ktf[((8 * w + t) * 2 + jb) * 64 + lane];
+  }
+  const f32x4 X = sh.xp[0][w][lane] + sh.xp[1][w][lane] + sh.xp[2][w][lane] + sh.xp[3][w][lane];
+  f32x4 kap;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) kap[i] = expf(l63 - lr[i]);
+  if constexpr (!REV) {
+    sh.x[w][lane] = X;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) rec[Rec::XK + (16 * w + 4 * (lane >> 4) + i) * DV + vc] = X[i];
+    __syncthreads();
+    f32x4 tx = mm<PrecF32>(zero4(), tp0, pair_to8(sh.x[0][lane], sh.x[1][lane]));
+    tx = mm<PrecF32>(tx, tp1, pair_to8(sh.x[2][lane], sh.x[3][lane]));
+    const f32x4 Wt = ur - tx;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) rec[Rec::W + (16 * w + 4 * (lane >> 4) + i) * DV + vc] = Wt[i];
+    sh.z[w][lane] = kap * Wt;
+  } else {
+    const f32x4 dW = ur + kap * X;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int ri = 16 * w + 4 * (lane >> 4) + i;
+      rec[Rec::X + ri * DV + vc] = X[i];
+      rec[Rec::DW + ri * DV + vc] = dW[i];
+    }
+    sh.x[w][lane] = dW;
+    __syncthreads();
+    f32x4 zt = mm<PrecF32>(zero4(), tp0, pair_to8(sh.x[0][lane], sh.x[1][lane]));
+    zt = mm<PrecF32>(zt, tp1, pair_to8(sh.x[2][lane], sh.x[3][lane]));
+    sh.z[w][lane] = -zt;
+  }
+  __syncthreads();
+  const frag zb0 = P::from_f32(pair_to8(sh.z[0][lane], sh.z[1][lane]));
+  const frag zb1 = P::from_f32(pair_to8(sh.z[2][lane], sh.z[3][lane]));
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    f32x4 acc = Sg[t];
+    if constexpr (REV) acc += hh[t];
+    Sg[t] = P::mma(P::mma(acc, kt[t][0], zb0), kt[t][1], zb1);
+  }
+  sink += pf;
+  return more;
+}
+
 template <class P, bool REV>
 __global__ void __launch_bounds__(256) bwd_chain_kernel(Params p) {
-  __shared__ f32x4 sh_xp[4][4][64];
-  __shared__ f32x4 sh_x[4][64];
-  __shared__ f32x4 sh_z[4][64];
+  constexpr bool PIPE = std::is_same<P, PrecBF16>::value && !REV;  // two register sets of K fragments fit only as bf16 (forward carry)
+  __shared__ ChainShared sh;
   const int64_t id = blockIdx.x;
   const int64_t xcd = id & 7, jdx = id >> 3;
   const int n = (int)(jdx & 3);
@@ -385,7 +568,7 @@ __global__ void __launch_bounds__(256) bwd_chain_kernel(Params p) {
   const int64_t b = hb / p.H, h = hb % p.H;
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int vc = 16 * n + (lane & 15);  // this lane's value column
+  const int vc = 16 * n + (lane & 15);
 
   f32x4 Sg[8];
   {
@@ -399,81 +582,14 @@ __global__ void __launch_bounds__(256) bwd_chain_kernel(Params p) {
         Sg[t][i] = src ? src[b * s0 + h * s1 + f * s2 + vc * s3] : 0.f;
       }
   }
-  for (int64_t step = 0; step < p.nch; ++step) {
-    const int64_t c = REV ? p.nch - 1 - step : step;
-    float* rec = record(p, b, h, c);
-    float* dst = rec + (REV ? Rec::G : Rec::S);
-#pragma unroll
-    for (int t = 0; t < 8; ++t)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) dst[(size_t)(128 * w + 16 * t + 4 * (lane >> 4) + i) * DV + vc] = Sg[t][i];
-
-    // K times the carried slice, partial over this wave's features.
-    f32x4 xp[4];
-#pragma unroll
-    for (int m = 0; m < 4; ++m) xp[m] = zero4();
-#pragma unroll
-    for (int jj = 0; jj < 4; ++jj) {
-      const f32x8 sb = pair_to8(Sg[2 * jj], Sg[2 * jj + 1]);
-#pragma unroll
-      for (int m = 0; m < 4; ++m) xp[m] = mm<P>(xp[m], frag_rows(rec + Rec::K, D, 16 * m, 128 * w + 32 * jj, lane), sb);
-    }
-#pragma unroll
-    for (int m = 0; m < 4; ++m) sh_xp[w][m][lane] = xp[m];
-    __syncthreads();
-    const f32x4 X = sh_xp[0][w][lane] + sh_xp[1][w][lane] + sh_xp[2][w][lane] + sh_xp[3][w][lane];
-    const float l63 = rec[Rec::VEC + 63];
-    const float gC = expf(l63);
-    f32x4 kap;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) kap[i] = expf(l63 - rec[Rec::VEC + 16 * w + 4 * (lane >> 4) + i]);
-    if constexpr (!REV) {
-      sh_x[w][lane] = X;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) rec[Rec::XK + (16 * w + 4 * (lane >> 4) + i) * DV + vc] = X[i];
-      __syncthreads();
-      f32x4 Wt;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) Wt[i] = rec[Rec::U + (16 * w + 4 * (lane >> 4) + i) * DV + vc];
-      f32x4 tx = zero4();
-#pragma unroll
-      for (int jb = 0; jb < 2; ++jb)
-        tx = mm<P>(tx, frag_rows(rec + Rec::TP, C, 16 * w, 32 * jb, lane), pair_to8(sh_x[2 * jb][lane], sh_x[2 * jb + 1][lane]));
-      Wt = Wt - tx;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) rec[Rec::W + (16 * w + 4 * (lane >> 4) + i) * DV + vc] = Wt[i];
-      sh_z[w][lane] = kap * Wt;
-    } else {
-      f32x4 dW;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int ri = 16 * w + 4 * (lane >> 4) + i;
-        dW[i] = rec[Rec::R + ri * DV + vc] + kap[i] * X[i];
-        rec[Rec::X + ri * DV + vc] = X[i];
-        rec[Rec::DW + ri * DV + vc] = dW[i];
-      }
-      sh_x[w][lane] = dW;
-      __syncthreads();
-      f32x4 zt = zero4();
-#pragma unroll
-      for (int jb = 0; jb < 2; ++jb)
-        zt = mm<P>(zt, frag_rows(rec + Rec::TPT, C, 16 * w, 32 * jb, lane), pair_to8(sh_x[2 * jb][lane], sh_x[2 * jb + 1][lane]));
-      sh_z[w][lane] = -zt;
-    }
-    __syncthreads();
-    const f32x8 zb0 = pair_to8(sh_z[0][lane], sh_z[1][lane]), zb1 = pair_to8(sh_z[2][lane], sh_z[3][lane]);
-#pragma unroll
-    for (int t = 0; t < 8; ++t) {
-      f32x4 acc = Sg[t] * gC;
-      if constexpr (REV) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) acc[i] += rec[Rec::H1 + (size_t)(128 * w + 16 * t + 4 * (lane >> 4) + i) * DV + vc];
-      }
-      acc = mm<P>(acc, frag_cols(rec + Rec::K, D, 128 * w + 16 * t, 0, lane), zb0);
-      acc = mm<P>(acc, frag_cols(rec + Rec::K, D, 128 * w + 16 * t, 32, lane), zb1);
-      Sg[t] = acc;
-    }
+  unsigned sink = 0;  // keeps the L2 prefetch loads alive (never stored: nch is positive)
+  ChainK<P> ka, kb;
+  if constexpr (PIPE) chain_load_kx<P>(ka, record(p, b, h, REV ? p.nch - 1 : 0), w, lane);
+  for (int64_t step = 0;; step += 2) {
+    if (!chain_step<P, REV, PIPE>(p, sh, b, h, step, ka, kb, Sg, w, lane, n, sink)) break;
+    if (!chain_step<P, REV, PIPE>(p, sh, b, h, step + 1, kb, ka, Sg, w, lane, n, sink)) break;
   }
+  if (p.nch < 0) p.ws[0] = (float)sink;
   if constexpr (REV) {
     if (p.dinit) {
 #pragma unroll
@@ -488,34 +604,36 @@ __global__ void __launch_bounds__(256) bwd_chain_kernel(Params p) {
 }
 
 // ---------------------------------------------------------------------------------------------- grad
-// The lift backward of one of q (which = 0) / k (which = 1) for this wave's 128 features, given
-// dPhi^T in acc[ft][m] (rows feature 128w + 16ft + .., column token 16m + ..): ds = -sqrt(2/D) sin(s)
-// (dphi / (n + 1e-8) - phi (phi . dphi) / n), then dx^ = inv_tau ds Omega reduced over the waves into
-// `dx` (LDS [64][LD], zeroed by the caller).  `xh` holds the normalised input rows.
+// The lift backward of one of q / k for this wave's 128 features and the 32 tokens of half hm, given
+// dPhi^T in acc[ft][u] (rows feature 128w + 16ft + .., column token 16(2hm + u) + ..):
+// ds = -sqrt(2/D) sin(s) (dphi / (n + 1e-8) - phi (phi . dphi) / n), then dx^ = ds Omega reduced over
+// the waves into `dx` (LDS [64][LD], zeroed by the caller) with LDS atomics.  `xh` holds the normalised
+// input rows, `s_rd` (zeroed by the caller) collects phi . dphi per token.
 template <class P>
-__device__ __forceinline__ void lift_backward(const Params& p, const float* phi, const float* nrm, float* s_rd,
-                                              const float* xh, float* dx, f32x4 (&acc)[8][4], int w, int lane) {
-  // phi . dphi per token
-  float rd[4] = {0.f, 0.f, 0.f, 0.f};
+__device__ __forceinline__ void lift_backward_half(const Params& p, const float* phi, const float* nrm, float* s_rd,
+                                                   const float* xh, float* dx, f32x4 (&acc)[8][2], int hm, int w,
+                                                   int lane) {
+  float rd[2] = {0.f, 0.f};
 #pragma unroll
   for (int ft = 0; ft < 8; ++ft)
 #pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      const f32x4 ph = *reinterpret_cast<const f32x4*>(phi + (size_t)(16 * m + (lane & 15)) * D + 128 * w + 16 * ft + 4 * (lane >> 4));
-      rd[m] += ph[0] * acc[ft][m][0] + ph[1] * acc[ft][m][1] + ph[2] * acc[ft][m][2] + ph[3] * acc[ft][m][3];
+    for (int u = 0; u < 2; ++u) {
+      const int tok = 16 * (2 * hm + u) + (lane & 15);
+      const f32x4 ph = *reinterpret_cast<const f32x4*>(phi + (size_t)tok * D + 128 * w + 16 * ft + 4 * (lane >> 4));
+      rd[u] += ph[0] * acc[ft][u][0] + ph[1] * acc[ft][u][1] + ph[2] * acc[ft][u][2] + ph[3] * acc[ft][u][3];
     }
 #pragma unroll
-  for (int m = 0; m < 4; ++m) {
-    const float v = sum_col4(rd[m]);
-    if (lane < 16) atomicAdd(&s_rd[16 * m + lane], v);
+  for (int u = 0; u < 2; ++u) {
+    const float v = sum_col4(rd[u]);
+    if (lane < 16) atomicAdd(&s_rd[16 * (2 * hm + u) + lane], v);
   }
   __syncthreads();
   const float amp = sqrtf(2.f / D);
-  f32x8 xb[4][2];
+  f32x8 xb[2][2];
 #pragma unroll
-  for (int m = 0; m < 4; ++m)
+  for (int u = 0; u < 2; ++u)
 #pragma unroll
-    for (int jb = 0; jb < 2; ++jb) xb[m][jb] = frag_rows(xh, LD, 16 * m, 32 * jb, lane);
+    for (int jb = 0; jb < 2; ++jb) xb[u][jb] = frag_rows(xh, LD, 16 * (2 * hm + u), 32 * jb, lane);
 #pragma unroll
   for (int ft = 0; ft < 8; ++ft) {
     const int f0 = 128 * w + 16 * ft;
@@ -524,41 +642,44 @@ __device__ __forceinline__ void lift_backward(const Params& p, const float* phi,
 #pragma unroll
     for (int i = 0; i < 4; ++i) ph4[i] = p.phase[f0 + 4 * (lane >> 4) + i];
 #pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      const f32x4 s = mm<P>(mm<P>(zero4(), o0, xb[m][0]), o1, xb[m][1]);
-      const int tok = 16 * m + (lane & 15);
+    for (int u = 0; u < 2; ++u) {
+      const f32x4 sv = mm<PrecF32>(mm<PrecF32>(zero4(), o0, xb[u][0]), o1, xb[u][1]);
+      const int tok = 16 * (2 * hm + u) + (lane & 15);
       const float n = nrm[tok], rdt = s_rd[tok];
       const f32x4 ph = *reinterpret_cast<const f32x4*>(phi + (size_t)tok * D + f0 + 4 * (lane >> 4));
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float dphit = acc[ft][m][i] / (n + 1e-8f) - ph[i] * rdt / n;
-        acc[ft][m][i] = -amp * sinf(s[i] * p.inv_tau + ph4[i]) * dphit;
+        const float dphit = acc[ft][u][i] / (n + 1e-8f) - ph[i] * rdt / n;
+        acc[ft][u][i] = -amp * sin_rad(sv[i] * p.inv_tau + ph4[i]) * dphit;
       }
     }
+    __builtin_amdgcn_sched_barrier(0);
   }
-  f32x4 d[4][4];
+  f32x4 d[4][2];
 #pragma unroll
   for (int a = 0; a < 4; ++a)
 #pragma unroll
-    for (int m = 0; m < 4; ++m) d[a][m] = zero4();
+    for (int u = 0; u < 2; ++u) d[a][u] = zero4();
 #pragma unroll
   for (int jj = 0; jj < 4; ++jj) {
     f32x8 ob[4];
 #pragma unroll
     for (int a = 0; a < 4; ++a) ob[a] = frag_cols_bf16(p.omega, DK, 16 * a, 128 * w + 32 * jj, lane);
 #pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      const f32x8 bs = pair_to8(acc[2 * jj][m], acc[2 * jj + 1][m]);
+    for (int u = 0; u < 2; ++u) {
+      const f32x8 bs = pair_to8(acc[2 * jj][u], acc[2 * jj + 1][u]);
 #pragma unroll
-      for (int a = 0; a < 4; ++a) d[a][m] = mm<P>(d[a][m], ob[a], bs);
+      for (int a = 0; a < 4; ++a) d[a][u] = mm<P>(d[a][u], ob[a], bs);
     }
+    __builtin_amdgcn_sched_barrier(0);
   }
 #pragma unroll
   for (int a = 0; a < 4; ++a)
 #pragma unroll
-    for (int m = 0; m < 4; ++m)
+    for (int u = 0; u < 2; ++u)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) atomicAdd(&dx[(16 * m + (lane & 15)) * LD + 16 * a + 4 * (lane >> 4) + i], d[a][m][i]);
+      for (int i = 0; i < 4; ++i)
+        atomicAdd(&dx[(16 * (2 * hm + u) + (lane & 15)) * LD + 16 * a + 4 * (lane >> 4) + i], d[a][u][i]);
 }
 
 // Thread (row tid >> 2, features (tid & 3) * 16 ..): dx = inv_tau * dx^ through the input normalisation,
@@ -596,12 +717,13 @@ __device__ __forceinline__ void write_dx(const Params& p, const InT* x, int64_t 
 template <class P, typename InT>
 __global__ void __launch_bounds__(256) bwd_grad_kernel(Params p) {
   __shared__ __attribute__((aligned(16))) float bY[C * LD];   // dY, then a o dY
-  __shared__ __attribute__((aligned(16))) float bW[C * LD];   // W, then kappa o W, then dx^ of k / q
+  __shared__ __attribute__((aligned(16))) float bW[C * LD];   // W, then kappa o W
   __shared__ __attribute__((aligned(16))) float bdW[C * LD];  // dW, then Zn = -Tp^T dW
   __shared__ __attribute__((aligned(16))) float bXK[C * LD];  // X_K, then N
   __shared__ __attribute__((aligned(16))) float bX[C * LD];   // X, then dT, then M + M^T
   __shared__ __attribute__((aligned(16))) float bV[C * LD];   // V, then Y1 = dT T^T
   __shared__ __attribute__((aligned(16))) float bT[C * LD];   // T, then normalised k / q rows
+  __shared__ __attribute__((aligned(16))) float bDX[C * LD];  // dx^ of k / q
   __shared__ float s_ell[C], s_beta[C], s_dl[C], s_db[C], s_ts[C], s_rd[C], s_n[C], s_g[1];
 
   const int64_t c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
@@ -660,12 +782,12 @@ __global__ void __launch_bounds__(256) bwd_grad_kernel(Params p) {
     for (int n = 0; n < 4; ++n) {
       const int cj = 16 * n + (lane & 15);
       // T^T dW
-      const f32x4 td = mm<P>(mm<P>(zero4(), ta0, frag_cols(bdW, LD, 16 * n, 0, lane)), ta1, frag_cols(bdW, LD, 16 * n, 32, lane));
+      const f32x4 td = mm<PrecF32>(mm<PrecF32>(zero4(), ta0, frag_cols(bdW, LD, 16 * n, 0, lane)), ta1, frag_cols(bdW, LD, 16 * n, 32, lane));
       // -dW X_K^T and dW V^T
-      const f32x4 dtp = -mm<P>(mm<P>(zero4(), da0, frag_rows(bXK, LD, 16 * n, 0, lane)), da1, frag_rows(bXK, LD, 16 * n, 32, lane));
-      const f32x4 e1 = mm<P>(mm<P>(zero4(), da0, frag_rows(bV, LD, 16 * n, 0, lane)), da1, frag_rows(bV, LD, 16 * n, 32, lane));
+      const f32x4 dtp = -mm<PrecF32>(mm<PrecF32>(zero4(), da0, frag_rows(bXK, LD, 16 * n, 0, lane)), da1, frag_rows(bXK, LD, 16 * n, 32, lane));
+      const f32x4 e1 = mm<PrecF32>(mm<PrecF32>(zero4(), da0, frag_rows(bV, LD, 16 * n, 0, lane)), da1, frag_rows(bV, LD, 16 * n, 32, lane));
       // dY W^T
-      const f32x4 dp = mm<P>(mm<P>(zero4(), ya0, frag_rows(bW, LD, 16 * n, 0, lane)), ya1, frag_rows(bW, LD, 16 * n, 32, lane));
+      const f32x4 dp = mm<PrecF32>(mm<PrecF32>(zero4(), ya0, frag_rows(bW, LD, 16 * n, 0, lane)), ya1, frag_rows(bW, LD, 16 * n, 32, lane));
       const float bj = s_beta[cj], lj = s_ell[cj], gj = expf(lj);
       float ts = 0.f, colp = 0.f;
 #pragma unroll
@@ -767,8 +889,8 @@ __global__ void __launch_bounds__(256) bwd_grad_kernel(Params p) {
     const f32x8 p0 = frag_rows(rec + Rec::TPT, C, 16 * w, 0, lane), p1 = frag_rows(rec + Rec::TPT, C, 16 * w, 32, lane);
 #pragma unroll
     for (int n = 0; n < 4; ++n) {
-      y1[n] = mm<P>(mm<P>(zero4(), a0, frag_rows(bT, LD, 16 * n, 0, lane)), a1, frag_rows(bT, LD, 16 * n, 32, lane));
-      zn[n] = -mm<P>(mm<P>(zero4(), p0, frag_cols(bdW, LD, 16 * n, 0, lane)), p1, frag_cols(bdW, LD, 16 * n, 32, lane));
+      y1[n] = mm<PrecF32>(mm<PrecF32>(zero4(), a0, frag_rows(bT, LD, 16 * n, 0, lane)), a1, frag_rows(bT, LD, 16 * n, 32, lane));
+      zn[n] = -mm<PrecF32>(mm<PrecF32>(zero4(), p0, frag_cols(bdW, LD, 16 * n, 0, lane)), p1, frag_cols(bdW, LD, 16 * n, 32, lane));
     }
   }
   __syncthreads();
@@ -788,7 +910,7 @@ __global__ void __launch_bounds__(256) bwd_grad_kernel(Params p) {
     float dbr[4] = {0.f, 0.f, 0.f, 0.f}, dlr[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int n = 0; n < 4; ++n) {
-      const f32x4 dA = -mm<P>(mm<P>(zero4(), ta0, frag_cols(bV, LD, 16 * n, 0, lane)), ta1, frag_cols(bV, LD, 16 * n, 32, lane));
+      const f32x4 dA = -mm<PrecF32>(mm<PrecF32>(zero4(), ta0, frag_cols(bV, LD, 16 * n, 0, lane)), ta1, frag_cols(bV, LD, 16 * n, 32, lane));
       const int cj = 16 * n + (lane & 15);
       float dlc = 0.f;
 #pragma unroll
@@ -841,7 +963,7 @@ __global__ void __launch_bounds__(256) bwd_grad_kernel(Params p) {
     }
   }
 
-  // ---- phase 6: dk, then dq
+  // ---- phase 6: dk, then dq, each in two halves of 32 tokens
   for (int which = 1; which >= 0; --which) {
     const InT* x = reinterpret_cast<const InT*>(which == 0 ? p.q : p.k);
     const int64_t xb = which == 0 ? b * p.qs0 + (t0 + r) * p.qs1 + h * p.qs2 + c0 : b * p.ks0 + (t0 + r) * p.ks1 + h * p.ks2 + c0;
@@ -849,61 +971,65 @@ __global__ void __launch_bounds__(256) bwd_grad_kernel(Params p) {
       float part[16];
       load_x_part<InT>(x, xb, rvalid, p.normalize, part);
 #pragma unroll
-      for (int e = 0; e < 16; ++e) bT[r * LD + c0 + e] = part[e];
+      for (int e = 0; e < 16; ++e) {
+        bT[r * LD + c0 + e] = part[e];
+        bDX[r * LD + c0 + e] = 0.f;
+      }
     }
     if (tid < C) {
       s_rd[tid] = 0.f;
       s_n[tid] = rec[Rec::VEC + 128 + 64 * which + tid];
     }
     __syncthreads();
-    f32x4 acc[8][4];
+    for (int hm = 0; hm < 2; ++hm) {
+      f32x4 acc[8][2];
 #pragma unroll
-    for (int ft = 0; ft < 8; ++ft) {
-      const int f0 = 128 * w + 16 * ft;
-      if (which == 1) {
-        // dK^T = Gamma (kappa o W)^T + S^T Zn^T + Q^T N + K^T (M + M^T)
-        const f32x8 g0 = frag_rows(rec + Rec::G, DV, f0, 0, lane), g1 = frag_rows(rec + Rec::G, DV, f0, 32, lane);
-        const f32x8 s0 = frag_rows(rec + Rec::S, DV, f0, 0, lane), s1 = frag_rows(rec + Rec::S, DV, f0, 32, lane);
-        const f32x8 q0 = frag_cols(rec + Rec::Q, D, f0, 0, lane), q1 = frag_cols(rec + Rec::Q, D, f0, 32, lane);
-        const f32x8 k0 = frag_cols(rec + Rec::K, D, f0, 0, lane), k1 = frag_cols(rec + Rec::K, D, f0, 32, lane);
+      for (int ft = 0; ft < 8; ++ft) {
+        const int f0 = 128 * w + 16 * ft;
+        if (which == 1) {
+          // dK^T = Gamma (kappa o W)^T + S^T Zn^T + Q^T N + K^T (M + M^T)
+          const f32x8 g0 = frag_rows(rec + Rec::G, DV, f0, 0, lane), g1 = frag_rows(rec + Rec::G, DV, f0, 32, lane);
+          const f32x8 s0 = frag_rows(rec + Rec::S, DV, f0, 0, lane), s1 = frag_rows(rec + Rec::S, DV, f0, 32, lane);
+          const f32x8 q0 = frag_cols(rec + Rec::Q, D, f0, 0, lane), q1 = frag_cols(rec + Rec::Q, D, f0, 32, lane);
+          const f32x8 k0 = frag_cols(rec + Rec::K, D, f0, 0, lane), k1 = frag_cols(rec + Rec::K, D, f0, 32, lane);
 #pragma unroll
-        for (int m = 0; m < 4; ++m) {
-          f32x4 t = zero4();
-          t = mm<P>(t, g0, frag_rows(bW, LD, 16 * m, 0, lane));
-          t = mm<P>(t, g1, frag_rows(bW, LD, 16 * m, 32, lane));
-          t = mm<P>(t, s0, frag_rows(bdW, LD, 16 * m, 0, lane));
-          t = mm<P>(t, s1, frag_rows(bdW, LD, 16 * m, 32, lane));
-          t = mm<P>(t, q0, frag_cols(bXK, LD, 16 * m, 0, lane));
-          t = mm<P>(t, q1, frag_cols(bXK, LD, 16 * m, 32, lane));
-          t = mm<P>(t, k0, frag_rows(bX, LD, 16 * m, 0, lane));
-          t = mm<P>(t, k1, frag_rows(bX, LD, 16 * m, 32, lane));
-          acc[ft][m] = t;
+          for (int u = 0; u < 2; ++u) {
+            const int m = 2 * hm + u;
+            f32x4 t = zero4();
+            t = mm<P>(t, g0, frag_rows(bW, LD, 16 * m, 0, lane));
+            t = mm<P>(t, g1, frag_rows(bW, LD, 16 * m, 32, lane));
+            t = mm<P>(t, s0, frag_rows(bdW, LD, 16 * m, 0, lane));
+            t = mm<P>(t, s1, frag_rows(bdW, LD, 16 * m, 32, lane));
+            t = mm<P>(t, q0, frag_cols(bXK, LD, 16 * m, 0, lane));
+            t = mm<P>(t, q1, frag_cols(bXK, LD, 16 * m, 32, lane));
+            t = mm<P>(t, k0, frag_rows(bX, LD, 16 * m, 0, lane));
+            t = mm<P>(t, k1, frag_rows(bX, LD, 16 * m, 32, lane));
+            acc[ft][u] = t;
+          }
+        } else {
+          // dQ^T = S^T (a o dY)^T + K^T N^T
+          const f32x8 s0 = frag_rows(rec + Rec::S, DV, f0, 0, lane), s1 = frag_rows(rec + Rec::S, DV, f0, 32, lane);
+          const f32x8 k0 = frag_cols(rec + Rec::K, D, f0, 0, lane), k1 = frag_cols(rec + Rec::K, D, f0, 32, lane);
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            const int m = 2 * hm + u;
+            f32x4 t = zero4();
+            t = mm<P>(t, s0, frag_rows(bY, LD, 16 * m, 0, lane));
+            t = mm<P>(t, s1, frag_rows(bY, LD, 16 * m, 32, lane));
+            t = mm<P>(t, k0, frag_rows(bXK, LD, 16 * m, 0, lane));
+            t = mm<P>(t, k1, frag_rows(bXK, LD, 16 * m, 32, lane));
+            acc[ft][u] = t;
+          }
         }
-      } else {
-        // dQ^T = S^T (a o dY)^T + K^T N^T
-        const f32x8 s0 = frag_rows(rec + Rec::S, DV, f0, 0, lane), s1 = frag_rows(rec + Rec::S, DV, f0, 32, lane);
-        const f32x8 k0 = frag_cols(rec + Rec::K, D, f0, 0, lane), k1 = frag_cols(rec + Rec::K, D, f0, 32, lane);
-#pragma unroll
-        for (int m = 0; m < 4; ++m) {
-          f32x4 t = zero4();
-          t = mm<P>(t, s0, frag_rows(bY, LD, 16 * m, 0, lane));
-          t = mm<P>(t, s1, frag_rows(bY, LD, 16 * m, 32, lane));
-          t = mm<P>(t, k0, frag_rows(bXK, LD, 16 * m, 0, lane));
-          t = mm<P>(t, k1, frag_rows(bXK, LD, 16 * m, 32, lane));
-          acc[ft][m] = t;
-        }
+        __builtin_amdgcn_sched_barrier(0);
       }
+      lift_backward_half<P>(p, rec + (which == 0 ? Rec::Q : Rec::K), s_n, s_rd, bT, bDX, acc, hm, w, lane);
     }
-    __syncthreads();  // every wave has read bW (kappa o W) before it becomes the dx^ accumulator
-#pragma unroll
-    for (int e = 0; e < 16; ++e) bW[r * LD + c0 + e] = 0.f;
-    __syncthreads();
-    lift_backward<P>(p, rec + (which == 0 ? Rec::Q : Rec::K), s_n, s_rd, bT, bW, acc, w, lane);
     __syncthreads();
     if (which == 0) {
-      write_dx<InT>(p, x, xb, p.dq, b * p.dqs0 + (t0 + r) * p.dqs1 + h * p.dqs2 + c0, bW, r, c0, rvalid);
+      write_dx<InT>(p, x, xb, p.dq, b * p.dqs0 + (t0 + r) * p.dqs1 + h * p.dqs2 + c0, bDX, r, c0, rvalid);
     } else {
-      write_dx<InT>(p, x, xb, p.dk, b * p.dks0 + (t0 + r) * p.dks1 + h * p.dks2 + c0, bW, r, c0, rvalid);
+      write_dx<InT>(p, x, xb, p.dk, b * p.dks0 + (t0 + r) * p.dks1 + h * p.dks2 + c0, bDX, r, c0, rvalid);
     }
     __syncthreads();
   }
@@ -982,7 +1108,9 @@ extern "C" int kdn_delta_scan_bwd(const kdn_scan_bwd_args* a, void* stream) {
   p.dis0 = a->dinit_stride[0]; p.dis1 = a->dinit_stride[1]; p.dis2 = a->dinit_stride[2]; p.dis3 = a->dinit_stride[3];
   p.ws = reinterpret_cast<float*>(a->workspace);
   const hipStream_t st = as_stream(stream);
-  if (f->in_dtype == KDN_DTYPE_BF16) return bwd_launch<PrecF32, __bf16>(p, st);
+  // bf16 inputs: the D = 512 contractions take bf16 operands with fp32 accumulation, the forward's
+  // policy for bf16 inputs; the lift and the 64 x 64 chunk algebra stay in fp32 MFMA.
+  if (f->in_dtype == KDN_DTYPE_BF16) return bwd_launch<PrecBF16, __bf16>(p, st);
   return bwd_launch<PrecF32, float>(p, st);
 }
 

@@ -2,8 +2,9 @@
 
 Oracle: torch autograd, in float64 on the CPU, of oracle.scan.delta_rule_torch (the token recurrence over
 the lift, pinned by gradcheck in test_oracle_backward.py) on the same inputs (bf16 inputs rounded
-first), for L = sum(y * dy) + sum(S_T * dS).  The backward computes in fp32 from the inputs, so every
-gradient is held to relative L2 1e-4 (fp32 and bf16 inputs alike).  At sizes the oracle cannot afford:
+first), for L = sum(y * dy) + sum(S_T * dS).  Tolerances (relative L2), as for the forward: 1e-4 for
+fp32 inputs (every product in fp32), 2e-2 for bf16 inputs (the 512-feature contractions take bf16
+operands with fp32 accumulation, the forward's bf16 policy).  At sizes the oracle cannot afford:
 exactness of the gradient of the (bilinear) v-direction against the forward kernel, and linearity of
 the backward in (dy, dS).
 """
@@ -18,7 +19,7 @@ from oracle import scan as osc
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda:0"
-TOL = 1e-4
+TOL = {torch.float32: 1e-4, torch.bfloat16: 2e-2}
 
 
 @pytest.fixture(scope="module")
@@ -95,7 +96,7 @@ def gpu_grads(proj, q, k, v, beta, lam, s0, dy, ds, normalize=False):
     return out
 
 
-def check(got, ref, tol=TOL):
+def check(got, ref, tol=TOL[torch.float32]):
     assert set(got) == set(ref), (sorted(got), sorted(ref))
     errs = {k: rel(got[k].numpy(), ref[k].detach().numpy()) for k in ref}
     assert all(e < tol for e in errs.values()), errs
@@ -105,7 +106,7 @@ def check(got, ref, tol=TOL):
 def test_backward_parity(proj, oproj, dtype):
     # T = 200: three full chunks and a partial one; decay, initial state and dL/dS_T all present
     args = make(1, 200, 2, dtype, seed=11)
-    check(gpu_grads(proj, *args), oracle_grads(*args, oproj))
+    check(gpu_grads(proj, *args), oracle_grads(*args, oproj), TOL[dtype])
 
 
 def test_backward_normalised_inputs(proj, oproj):
@@ -125,7 +126,7 @@ def test_backward_single_partial_chunk(proj, oproj):
 
 def test_backward_is_linear_in_the_output_gradients(proj):
     # large enough for many chunks and a 32-workgroup chain grid: bwd(a dy1 + b dy2) = a bwd(dy1) + b bwd(dy2)
-    q, k, v, beta, lam, s0, dy1, ds1 = make(2, 1500, 4, torch.bfloat16, seed=15)
+    q, k, v, beta, lam, s0, dy1, ds1 = make(2, 1500, 4, torch.float32, seed=15)
     g = torch.Generator().manual_seed(16)
     dy2, ds2 = torch.randn(dy1.shape, generator=g), torch.randn(ds1.shape, generator=g)
     g1 = gpu_grads(proj, q, k, v, beta, lam, s0, dy1, ds1)
