@@ -118,6 +118,9 @@ def main():
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain device copy of known size (for PMC byte-counter calibration)")
     ap.add_argument("--pmc", default=None)
+    ap.add_argument("--backward", action="store_true",
+                    help="time the backward pass (kdn_delta_scan_bwd: gradients of q, k, v, beta) on the config "
+                         "3 shape instead of the forward")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -135,6 +138,8 @@ def main():
         torch.cuda.synchronize()
         print(json.dumps({"copy_calibration_bytes_per_dispatch_each_way": n}), flush=True)
         return
+    if args.backward:
+        return bench_backward(args, dev)
     if args.config == 2:
         return bench_lift(args, dev)
     if args.config == 5:
@@ -269,6 +274,112 @@ def bench_scan(args, dev):
         Bs = 1 if cfg == 4 else B
         out["cpu_baseline"] = cpu_baseline(q[:Bs, :Ts].cpu(), k[:Bs, :Ts].cpu(), v[:Bs, :Ts].cpu(),
                                            beta[:Bs, :Ts].cpu(), Ts)
+    else:
+        out["cpu_baseline"] = None
+    print(json.dumps(out), flush=True)
+
+
+def bwd_flops_per_chunk(D: int, dv: int, dk: int = 64) -> dict:
+    """Algorithmic FLOPs per (head, 64-token chunk) of the closed-form chunk backward, split by launch:
+    the matrix products the gradient needs (2 m n k each), as the kernels form them.
+      prep   lift of q and k (2 C D dk each), K K^T and Q K^T (2 C^2 D each), H = Q^T (a o dY) (2 D C dv),
+             U~ and R (2 C^2 dv each), the triangular inverse (2/3 C^3)
+      carry  K Sigma and K^T Z (2 C D dv each), W or Tp^T dW (2 C^2 dv)   -- forward and reverse alike
+      grad   Q S^T (2 C D dv); dQ^T: S^T (a o dY)^T, K^T N^T; dK^T: Gamma (kappa o W)^T, S^T Zn^T, Q^T N,
+             K^T (M + M^T) (2 D C dv or 2 D C^2 each); lift recompute and dx^ for q and k (2 C D dk each);
+             the 64 x 64 algebra T^T dW, dW X_K^T, dW V^T, dY W^T, dT T^T, Tp^T dW, T^T Y1 (2 C^2 dv or 2 C^3)"""
+    prep = 4 * C * D * dk + 4 * C * C * D + 2 * D * C * dv + 4 * C * C * dv + (2.0 / 3.0) * C ** 3
+    carry = 4 * C * D * dv + 2 * C * C * dv
+    grad = (2 * C * D * dv + (2 * D * dv * C + 2 * D * C * C) + (4 * D * dv * C + 4 * D * C * C)
+            + 8 * C * D * dk + (5 * 2 * C * C * dv + 2 * 2 * C ** 3))
+    return {"prep": prep, "carry_fwd": carry, "carry_rev": carry, "grad": grad,
+            "total": prep + 2 * carry + grad}
+
+
+def cpu_backward_baseline(q, k, v, beta, dy, T_sample: int, H: int) -> dict:
+    """Float64 autograd of the oracle's token recurrence over the lift (one head, first T_sample tokens)."""
+    from oracle import lift as ol
+    from oracle import scan as osc
+
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    proj = ol.make_projection(64, 512, 42)
+    qf = q[:1, :T_sample, 0].double().clone().requires_grad_(True)
+    kf = k[:1, :T_sample, 0].double().clone().requires_grad_(True)
+    vf = v[:1, :T_sample, 0].double().clone().requires_grad_(True)
+    bf = beta[:1, :T_sample, 0].double().clone().requires_grad_(True)
+    t0 = time.perf_counter()
+    Y, S = osc.delta_rule_torch(qf, kf, vf, bf, None, proj)
+    (Y * dy[:1, :T_sample, 0].double()).sum().backward()
+    sec = time.perf_counter() - t0
+    return {"value": T_sample / (sec * H), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"float64 torch autograd of the oracle token recurrence (forward + backward) over one "
+                      f"head's first {T_sample} tokens; value scaled to all {H} heads ({sec:.2f} s measured)"}
+
+
+def bench_backward(args, dev):
+    """The backward pass on the config 3 shape (B=1, H=16, T=65536, bf16 q/k/v, fp32 beta, lambda = 1,
+    dL/dy ~ N(0,1)): kdn_delta_scan_bwd computing dq, dk, dv, dbeta.  A step = one whole backward."""
+    from kdn import ops
+    from kernels import FastWalshHadamardProjection
+
+    B = args.B if args.B is not None else 1
+    T = args.T if args.T is not None else 65536
+    H, dv, D = args.H, args.dv, 512
+    q, k, v, beta = synthetic_inputs(B, T, H, dv, dev)
+    qd, kd, vd, bd = q.to(dev), k.to(dev), v.to(dev), beta.to(dev)
+    gd = torch.Generator(device=dev).manual_seed(4321)
+    dy = torch.randn(B, T, H, dv, generator=gd, device=dev)
+    proj = FastWalshHadamardProjection(64, D, 42)
+    plan = ops.ScanBackwardPlan(qd, kd, vd, bd, None, proj.device_omega(dev), proj.device_phase(dev),
+                                proj.tau_star_inv, dy, need_dinit=False)
+    stream = torch.cuda.current_stream(dev)
+    for _ in range(args.warmup):
+        plan.run()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(args.steps):
+        plan.run()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / args.steps
+    names = ("prep", "carry_fwd", "carry_rev", "grad")
+    timed = {n: [] for n in names}
+    for _ in range(args.steps):
+        for i, n in enumerate(names):
+            a0, a1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a0.record(stream)
+            plan.phase(i)
+            a1.record(stream)
+            timed[n].append((a0, a1))
+    torch.cuda.synchronize()
+    fl = bwd_flops_per_chunk(D, dv)
+    nch = (T + C - 1) // C
+    units = B * H * nch
+    phases = {}
+    for n in names:
+        pm = sum(x.elapsed_time(y) for x, y in timed[n]) / args.steps
+        phases[n] = {"ms": pm, "launches": 1, "avg_launch_ms": pm, "alg_flops": fl[n] * units,
+                     "tflops": fl[n] * units / pm / 1e9}
+    dom = max(phases, key=lambda x: phases[x]["ms"])
+    achieved = phases[dom]["tflops"]
+    out = {
+        "metric": "backward (gradients of q, k, v, beta) tokens/s at T=64k, D=512 on 1 GPU; % of MFMA roofline",
+        "value": B * T / (ms / 1e3), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) q/k/v, sigmoid(N(0,1)) beta, N(0,1) dL/dy; projection seed 42)",
+        "config": {"workload": f"backward of config3 (one layer, B={B}, H={H}, T={T}, d_k=64->D={D}, d_v={dv}, "
+                               f"bf16 q/k/v, fp32 beta, lambda=1)", "B": B, "H": H, "T": T, "D": D, "d_v": dv,
+                   "workspace_bytes": plan.workspace.numel(), "parallelism": "single GPU"},
+        "roofline": {"bound": "mfma", "achieved": achieved, "peak": MFMA_BF16_PEAK / 1e12, "unit": "TFLOP/s",
+                     "frac": achieved / (MFMA_BF16_PEAK / 1e12), "traffic": None, "kernel": dom},
+        "phases": phases,
+        "path": {"alg_flops": fl["total"] * units, "tflops": fl["total"] * units / ms / 1e9},
+    }
+    if args.cpu_tokens > 0:
+        out["cpu_baseline"] = cpu_backward_baseline(q.cpu(), k.cpu(), v.cpu(), beta.cpu(), dy.cpu(),
+                                                    min(args.cpu_tokens, 4096), H)
     else:
         out["cpu_baseline"] = None
     print(json.dumps(out), flush=True)

@@ -81,6 +81,16 @@ int kdn_fwht_lift(const void* x, int64_t rows, int64_t x_row_stride, int x_dtype
                   const void* omega_bf16, const float* phase, int d_k, int D, float inv_tau,
                   void* out, int64_t out_row_stride, int out_dtype, void* stream);
 
+/* Factored lift for d_k = 128 -> D = 1024 (ABI 1.4): out[r][0:512] = lift(x[r][0:64]; omega1, phase1),
+ * out[r][512:1024] = lift(x[r][64:128]; omega2, phase2) (each as kdn_fwht_lift without input
+ * normalisation, the two projections of seeds s and s + 1000), then out[r] <- out[r] / (||out[r]|| + 1e-7).
+ * Replaces FactoredFastWalshHadamardProjection.forward, kernels/factored_kernel_deltanet.py:42-74.
+ * Alignment as kdn_fwht_lift; x_row_stride >= 128, out_row_stride >= 1024. */
+int kdn_fwht_lift_factored(const void* x, int64_t rows, int64_t x_row_stride, int x_dtype,
+                           const void* omega1_bf16, const float* phase1, const void* omega2_bf16,
+                           const float* phase2, float inv_tau, void* out, int64_t out_row_stride, int out_dtype,
+                           void* stream);
+
 /* Arguments of the chunked delta-rule prefill scan.  Tensors are addressed as
  *   q[b][t][h][0:d_k], k[b][t][h][0:d_k], v[b][t][h][0:d_v], beta[b][t][h], decay[b][t][h],
  *   y[b][t][h][0:d_v], state[b][h][0:D][0:d_v]   (state element (d, j) = S[j][d] of the recurrence)
@@ -89,7 +99,9 @@ int kdn_fwht_lift(const void* x, int64_t rows, int64_t x_row_stride, int x_dtype
  * state stride {d_v*D, 0, 1, D}. */
 typedef struct kdn_scan_args {
   int64_t B, T, H;
-  int d_k, D, d_v;             /* d_k = 64, D = 512, d_v a multiple of 16 up to 128 */
+  int d_k, D, d_v;             /* d_k = 64, D = 512, d_v a multiple of 16 up to 128; or (ABI 1.4) pre-lifted
+                                * features with d_k = D = 1024, d_v 64 or 128, the delta rule, uniform batches
+                                * (the factored d_k = 128 path; full-scan entry points only) */
   int in_dtype;                /* dtype of q, k, v */
   int out_dtype;               /* dtype of y */
   int normalize_input;         /* L2-normalise q, k rows (F.normalize, eps 1e-6) before the lift */
@@ -216,6 +228,11 @@ size_t kdn_scan_bwd_workspace_bytes(const kdn_scan_bwd_args* a);
  * forward state carry (state at every chunk start), the reverse carry of dL/dS, and the per-chunk
  * gradients with the lift's backward. */
 int kdn_delta_scan_bwd(const kdn_scan_bwd_args* a, void* stream);
+
+/* One of the four launches of kdn_delta_scan_bwd (phase 0: per-chunk recompute, 1: forward carry,
+ * 2: reverse carry, 3: gradients), for callers that time or schedule them; on one workspace they must
+ * run in the order 0, 1, 2, 3 (stream order or events).  Same arguments and checks. */
+int kdn_scan_bwd_phase(const kdn_scan_bwd_args* a, int phase, void* stream);
 
 /* ---- Serving: ragged mixed prefill + decode step over resident states -------------------------
  * One step of a batch of sequences that continue from states resident in a slab (the reference's

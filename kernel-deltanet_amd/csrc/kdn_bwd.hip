@@ -30,6 +30,7 @@
 #include <type_traits>
 #include "kdn_frag.hpp"
 #include "kdn_internal.hpp"
+#include "kdn_tile.hpp"
 
 namespace kdn {
 namespace bwd {
@@ -90,68 +91,6 @@ __device__ __forceinline__ float* record(const Params& p, int64_t b, int64_t h, 
   return p.ws + ((b * p.H + h) * p.nch + c) * (int64_t)Rec::floats;
 }
 
-template <typename T>
-__device__ __forceinline__ float ldx(const T* p) { return (float)*p; }
-
-// Fragment loads (kappa order, see kdn_frag.hpp).  rows: element (r0 + l%16, k0 + kappa) = base[row * ld + depth]
-// (two 16-byte loads); cols: element (c0 + l%16, k0 + kappa) = base[depth * ld + c0 + l%16] (eight loads).
-__device__ __forceinline__ f32x8 frag_rows(const float* base, int ld, int r0, int k0, int lane) {
-  const float* p = base + (size_t)(r0 + (lane & 15)) * ld + k0 + 4 * (lane >> 4);
-  const f32x4 lo = *reinterpret_cast<const f32x4*>(p);
-  const f32x4 hi = *reinterpret_cast<const f32x4*>(p + 16);
-  return pair_to8(lo, hi);
-}
-__device__ __forceinline__ f32x8 frag_cols(const float* base, int ld, int c0, int k0, int lane) {
-  f32x8 r;
-#pragma unroll
-  for (int s = 0; s < 8; ++s) r[s] = base[(size_t)(k0 + kappa(lane, s)) * ld + c0 + (lane & 15)];
-  return r;
-}
-__device__ __forceinline__ f32x8 frag_rows_bf16(const __bf16* base, int ld, int r0, int k0, int lane) {
-  typedef __attribute__((ext_vector_type(4))) __bf16 bf16x4;
-  const __bf16* p = base + (size_t)(r0 + (lane & 15)) * ld + k0 + 4 * (lane >> 4);
-  const bf16x4 lo = *reinterpret_cast<const bf16x4*>(p);
-  const bf16x4 hi = *reinterpret_cast<const bf16x4*>(p + 16);
-  f32x8 r;
-#pragma unroll
-  for (int s = 0; s < 4; ++s) { r[s] = (float)lo[s]; r[4 + s] = (float)hi[s]; }
-  return r;
-}
-__device__ __forceinline__ f32x8 frag_cols_bf16(const __bf16* base, int ld, int c0, int k0, int lane) {
-  f32x8 r;
-#pragma unroll
-  for (int s = 0; s < 8; ++s) r[s] = (float)base[(size_t)(k0 + kappa(lane, s)) * ld + c0 + (lane & 15)];
-  return r;
-}
-
-// cos / sin of an angle in radians, branch-free: the angle in revolutions reduced to [0, 1) (v_fract),
-// then the hardware v_cos_f32 / v_sin_f32 (which take revolutions).  Absolute error ~1e-6 at the
-// angles of the lift (|s| up to ~100 rad).
-__device__ __forceinline__ float cos_rad(float s) {
-  return __builtin_amdgcn_cosf(__builtin_amdgcn_fractf(s * 0.15915494309189535f));
-}
-__device__ __forceinline__ float sin_rad(float s) {
-  return __builtin_amdgcn_sinf(__builtin_amdgcn_fractf(s * 0.15915494309189535f));
-}
-
-template <class P>
-__device__ __forceinline__ f32x4 mm(f32x4 acc, const f32x8& a, const f32x8& b) {
-  return P::mma(acc, P::from_f32(a), P::from_f32(b));
-}
-
-// Sum over the 16 lanes sharing (lane >> 4) (one tile row) / over the 4 lane groups (one tile column).
-__device__ __forceinline__ float sum_row16(float v) {
-  v += __shfl_xor(v, 1);
-  v += __shfl_xor(v, 2);
-  v += __shfl_xor(v, 4);
-  v += __shfl_xor(v, 8);
-  return v;
-}
-__device__ __forceinline__ float sum_col4(float v) {
-  v += __shfl_xor(v, 16);
-  v += __shfl_xor(v, 32);
-  return v;
-}
 
 // Thread `tid` of 256 holds 16 consecutive features (tid & 3) * 16 .. of token row tid >> 2: loads the
 // raw row part of x (zero past T), its L2 norm over the 64 features (shared by the four threads of the
@@ -1066,18 +1005,21 @@ extern "C" size_t kdn_scan_bwd_workspace_bytes(const kdn_scan_bwd_args* a) {
   return (size_t)(f->B * f->H * bwd_chunks(f)) * Rec::floats * sizeof(float);
 }
 
+// Launches phases [first, last] (0 prep, 1 forward carry, 2 reverse carry, 3 gradients) in order.
 template <class P, typename InT>
-static int bwd_launch(const Params& p, hipStream_t st) {
+static int bwd_launch(const Params& p, int first, int last, hipStream_t st) {
   const dim3 chunk_grid((unsigned)p.nch, (unsigned)p.H, (unsigned)p.B);
   const unsigned chain_wgs = (unsigned)(((p.B * p.H + 7) / 8) * 8 * 4);
-  hipLaunchKernelGGL((bwd_prep_kernel<P, InT>), chunk_grid, dim3(256), 0, st, p);
-  hipLaunchKernelGGL((bwd_chain_kernel<P, false>), dim3(chain_wgs), dim3(256), 0, st, p);
-  hipLaunchKernelGGL((bwd_chain_kernel<P, true>), dim3(chain_wgs), dim3(256), 0, st, p);
-  hipLaunchKernelGGL((bwd_grad_kernel<P, InT>), chunk_grid, dim3(256), 0, st, p);
+  for (int ph = first; ph <= last; ++ph) {
+    if (ph == 0) hipLaunchKernelGGL((bwd_prep_kernel<P, InT>), chunk_grid, dim3(256), 0, st, p);
+    if (ph == 1) hipLaunchKernelGGL((bwd_chain_kernel<P, false>), dim3(chain_wgs), dim3(256), 0, st, p);
+    if (ph == 2) hipLaunchKernelGGL((bwd_chain_kernel<P, true>), dim3(chain_wgs), dim3(256), 0, st, p);
+    if (ph == 3) hipLaunchKernelGGL((bwd_grad_kernel<P, InT>), chunk_grid, dim3(256), 0, st, p);
+  }
   return launch_status();
 }
 
-extern "C" int kdn_delta_scan_bwd(const kdn_scan_bwd_args* a, void* stream) {
+static int bwd_run(const kdn_scan_bwd_args* a, int first, int last, void* stream) {
   const int rc = bwd_check(a);
   if (rc != KDN_OK) return rc;
   const kdn_scan_args* f = a->fwd;
@@ -1110,8 +1052,15 @@ extern "C" int kdn_delta_scan_bwd(const kdn_scan_bwd_args* a, void* stream) {
   const hipStream_t st = as_stream(stream);
   // bf16 inputs: the D = 512 contractions take bf16 operands with fp32 accumulation, the forward's
   // policy for bf16 inputs; the lift and the 64 x 64 chunk algebra stay in fp32 MFMA.
-  if (f->in_dtype == KDN_DTYPE_BF16) return bwd_launch<PrecBF16, __bf16>(p, st);
-  return bwd_launch<PrecF32, float>(p, st);
+  if (f->in_dtype == KDN_DTYPE_BF16) return bwd_launch<PrecBF16, __bf16>(p, first, last, st);
+  return bwd_launch<PrecF32, float>(p, first, last, st);
+}
+
+extern "C" int kdn_delta_scan_bwd(const kdn_scan_bwd_args* a, void* stream) { return bwd_run(a, 0, 3, stream); }
+
+extern "C" int kdn_scan_bwd_phase(const kdn_scan_bwd_args* a, int phase, void* stream) {
+  if (phase < 0 || phase > 3) return KDN_ERR_INVALID_ARGUMENT;
+  return bwd_run(a, phase, phase, stream);
 }
 
 }  // namespace kdn

@@ -37,4 +37,12 @@ int scan_pipelined(const kdn_scan_args* a, const int64_t* seq_lo, const int64_t*
                    void* aux_stream, void* out_stream);
 size_t scan_workspace_bytes_pipelined(const kdn_scan_args* a);
 
+// The general-D scan (kdn_general.hip): D = 1024 over pre-lifted features, d_v 64 or 128, the delta rule,
+// uniform batches.  general_scan_applies selects it; the other functions assume it applies and that the
+// common argument checks have passed.
+bool general_scan_applies(const kdn_scan_args* a);
+int general_scan_validate(const kdn_scan_args* a);
+size_t general_scan_workspace_bytes(const kdn_scan_args* a);
+int general_scan(const kdn_scan_args* a, void* stream);
+
 }  // namespace kdn

@@ -309,3 +309,49 @@ extern "C" int kdn_fwht_lift(const void* x, int64_t rows, int64_t x_row_stride, 
     return dispatch_lift_D<float, __bf16>(D, x, rows, x_row_stride, nz, omega_bf16, phase, inv_tau, out, out_row_stride, st);
   return dispatch_lift_D<float, float>(D, x, rows, x_row_stride, nz, omega_bf16, phase, inv_tau, out, out_row_stride, st);
 }
+
+namespace kdn {
+// Row renormalisation in place: x[r] <- x[r] / (||x[r]||_2 + eps), one wave per row of n elements.
+template <typename T>
+__global__ void __launch_bounds__(256) renorm_rows_kernel(T* x, int64_t rows, int64_t stride, int n, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  T* p = x + row * stride;
+  float ss = 0.f;
+  for (int e = lane; e < n; e += 64) {
+    const float v = (float)p[e];
+    ss += v * v;
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
+  const float inv = 1.f / (sqrtf(ss) + eps);
+  for (int e = lane; e < n; e += 64) p[e] = (T)((float)p[e] * inv);
+}
+}  // namespace kdn
+
+extern "C" int kdn_fwht_lift_factored(const void* x, int64_t rows, int64_t x_row_stride, int x_dtype,
+                                      const void* omega1_bf16, const float* phase1, const void* omega2_bf16,
+                                      const float* phase2, float inv_tau, void* out, int64_t out_row_stride,
+                                      int out_dtype, void* stream) {
+  if (!x || !omega1_bf16 || !phase1 || !omega2_bf16 || !phase2 || !out || rows < 0) return KDN_ERR_INVALID_ARGUMENT;
+  if (!valid_dtype(x_dtype) || !valid_dtype(out_dtype)) return KDN_ERR_INVALID_ARGUMENT;
+  if (x_row_stride < 128 || out_row_stride < 1024) return KDN_ERR_INVALID_ARGUMENT;
+  const size_t isz = dtype_size(x_dtype), osz = dtype_size(out_dtype);
+  // each half: the structured lift of 64 features into 512 (rows of x and out stay 16-byte aligned)
+  int rc = kdn_fwht_lift(x, rows, x_row_stride, x_dtype, 0, omega1_bf16, phase1, 64, 512, inv_tau, out,
+                         out_row_stride, out_dtype, stream);
+  if (rc != KDN_OK) return rc;
+  rc = kdn_fwht_lift(static_cast<const unsigned char*>(x) + 64 * isz, rows, x_row_stride, x_dtype, 0, omega2_bf16,
+                     phase2, 64, 512, inv_tau, static_cast<unsigned char*>(out) + 512 * osz, out_row_stride, out_dtype,
+                     stream);
+  if (rc != KDN_OK || rows == 0) return rc;
+  const dim3 grid((unsigned)((rows + 3) / 4));
+  if (out_dtype == KDN_DTYPE_BF16)
+    hipLaunchKernelGGL(renorm_rows_kernel<__bf16>, grid, dim3(256), 0, as_stream(stream), static_cast<__bf16*>(out),
+                       rows, out_row_stride, 1024, 1e-7f);
+  else
+    hipLaunchKernelGGL(renorm_rows_kernel<float>, grid, dim3(256), 0, as_stream(stream), static_cast<float*>(out), rows,
+                       out_row_stride, 1024, 1e-7f);
+  return launch_status();
+}

@@ -1236,7 +1236,12 @@ static int validate(const kdn_scan_args* a) {
   if (!valid_dtype(a->in_dtype) || !valid_dtype(a->out_dtype)) return KDN_ERR_INVALID_ARGUMENT;
   if (a->feature_mode != 0 && a->feature_mode != 1) return KDN_ERR_INVALID_ARGUMENT;
   if (a->rule != 0 && a->rule != 1) return KDN_ERR_INVALID_ARGUMENT;
-  if (a->D != 512) return KDN_ERR_UNSUPPORTED;
+  if (general_scan_applies(a)) {
+    const int rc = general_scan_validate(a);  // D = 1024: pre-lifted features, kdn_general.hip
+    if (rc != KDN_OK) return rc;
+  } else if (a->D != 512) {
+    return KDN_ERR_UNSUPPORTED;
+  }
   if (a->feature_mode == 0 ? a->d_k != 64 : a->d_k != a->D) return KDN_ERR_UNSUPPORTED;
   if (a->omega_head_stride < 0 || a->phase_head_stride < 0) return KDN_ERR_INVALID_ARGUMENT;
   if (a->d_v != 16 && a->d_v != 32 && a->d_v != 64 && a->d_v != 128) return KDN_ERR_UNSUPPORTED;
@@ -1272,6 +1277,7 @@ static int validate_launch(const kdn_scan_args* a) {
 static int run_phase(const kdn_scan_args* a, int64_t chunk0, int64_t nchunks, int phase, void* stream) {
   int rc = validate_launch(a);
   if (rc != KDN_OK) return rc;
+  if (general_scan_applies(a)) return KDN_ERR_UNSUPPORTED;  // the general-D scan has no phase entry points
   const int64_t total = (a->T + CH - 1) / CH;
   if (chunk0 < 0 || nchunks < 1 || chunk0 + nchunks > total) return KDN_ERR_INVALID_ARGUMENT;
   const size_t need = chunk_bytes(a) * (size_t)a->B * (size_t)a->H * (size_t)(nchunks + 1);
@@ -1285,6 +1291,7 @@ using namespace kdn;
 
 extern "C" size_t kdn_scan_workspace_bytes(const kdn_scan_args* a) {
   if (validate(a) != KDN_OK) return 0;
+  if (general_scan_applies(a)) return general_scan_workspace_bytes(a);
   const int64_t seg = choose_segment(a);
   return chunk_bytes(a) * (size_t)a->B * (size_t)a->H * (size_t)(seg + 1);
 }
@@ -1292,6 +1299,7 @@ extern "C" size_t kdn_scan_workspace_bytes(const kdn_scan_args* a) {
 extern "C" int kdn_delta_scan_fwd(const kdn_scan_args* a, void* stream) {
   int rc = validate_launch(a);
   if (rc != KDN_OK) return rc;
+  if (general_scan_applies(a)) return general_scan(a, stream);
   const int64_t seg = choose_segment(a);
   const size_t need = chunk_bytes(a) * (size_t)a->B * (size_t)a->H * (size_t)(seg + 1);
   if (a->workspace_bytes < need) return KDN_ERR_WORKSPACE_TOO_SMALL;
@@ -1317,6 +1325,7 @@ int scan_pipelined(const kdn_scan_args* a, const int64_t* seq_lo, const int64_t*
                    void* aux_stream, void* out_stream) {
   int rc = validate_launch(a);
   if (rc != KDN_OK) return rc;
+  if (general_scan_applies(a)) return seq_lo ? KDN_ERR_UNSUPPORTED : general_scan(a, stream);
   const int64_t seg = pipeline_segment(a);
   const size_t buf = chunk_bytes(a) * (size_t)a->B * (size_t)a->H * (size_t)(seg + 1);
   if (a->workspace_bytes < buf) return KDN_ERR_WORKSPACE_TOO_SMALL;
@@ -1337,6 +1346,7 @@ int scan_pipelined(const kdn_scan_args* a, const int64_t* seq_lo, const int64_t*
 
 size_t scan_workspace_bytes_pipelined(const kdn_scan_args* a) {
   if (validate(a) != KDN_OK) return 0;
+  if (general_scan_applies(a)) return general_scan_workspace_bytes(a);
   const int64_t seg = pipeline_segment(a);
   const int64_t nsegs = ((a->T + CH - 1) / CH + seg - 1) / seg;
   const int64_t nbuf = nsegs < 3 ? nsegs : 3;

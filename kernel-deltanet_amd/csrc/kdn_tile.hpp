@@ -1,0 +1,70 @@
+// Row-major fp32 tiles <-> MFMA fragments, and small wave reductions (gfx950), shared by the kernels
+// that keep their per-chunk matrices as plain fp32 rows (the backward pass and the general-D scan).
+#pragma once
+#include <hip/hip_runtime.h>
+#include "kdn_frag.hpp"
+
+namespace kdn {
+
+template <typename T>
+__device__ __forceinline__ float ldx(const T* p) { return (float)*p; }
+
+// Fragment loads (kappa order, see kdn_frag.hpp).  rows: element (r0 + l%16, k0 + kappa) = base[row * ld + depth]
+// (two 16-byte loads); cols: element (c0 + l%16, k0 + kappa) = base[depth * ld + c0 + l%16] (eight loads).
+__device__ __forceinline__ f32x8 frag_rows(const float* base, int ld, int r0, int k0, int lane) {
+  const float* p = base + (size_t)(r0 + (lane & 15)) * ld + k0 + 4 * (lane >> 4);
+  const f32x4 lo = *reinterpret_cast<const f32x4*>(p);
+  const f32x4 hi = *reinterpret_cast<const f32x4*>(p + 16);
+  return pair_to8(lo, hi);
+}
+__device__ __forceinline__ f32x8 frag_cols(const float* base, int ld, int c0, int k0, int lane) {
+  f32x8 r;
+#pragma unroll
+  for (int s = 0; s < 8; ++s) r[s] = base[(size_t)(k0 + kappa(lane, s)) * ld + c0 + (lane & 15)];
+  return r;
+}
+__device__ __forceinline__ f32x8 frag_rows_bf16(const __bf16* base, int ld, int r0, int k0, int lane) {
+  typedef __attribute__((ext_vector_type(4))) __bf16 bf16x4;
+  const __bf16* p = base + (size_t)(r0 + (lane & 15)) * ld + k0 + 4 * (lane >> 4);
+  const bf16x4 lo = *reinterpret_cast<const bf16x4*>(p);
+  const bf16x4 hi = *reinterpret_cast<const bf16x4*>(p + 16);
+  f32x8 r;
+#pragma unroll
+  for (int s = 0; s < 4; ++s) { r[s] = (float)lo[s]; r[4 + s] = (float)hi[s]; }
+  return r;
+}
+__device__ __forceinline__ f32x8 frag_cols_bf16(const __bf16* base, int ld, int c0, int k0, int lane) {
+  f32x8 r;
+#pragma unroll
+  for (int s = 0; s < 8; ++s) r[s] = (float)base[(size_t)(k0 + kappa(lane, s)) * ld + c0 + (lane & 15)];
+  return r;
+}
+
+// sin of an angle in radians via v_sin_f32 (revolutions), reduced to [-0.5, 0.5] revolutions as
+// cos_rad (kdn_frag.hpp) does.
+__device__ __forceinline__ float sin_rad(float angle) {
+  float r = angle * 0.15915494309189535f;  // 1 / (2 pi)
+  r = r - __builtin_rintf(r);
+  return __builtin_amdgcn_sinf(r);
+}
+
+template <class P>
+__device__ __forceinline__ f32x4 mm(f32x4 acc, const f32x8& a, const f32x8& b) {
+  return P::mma(acc, P::from_f32(a), P::from_f32(b));
+}
+
+// Sum over the 16 lanes sharing (lane >> 4) (one tile row) / over the 4 lane groups (one tile column).
+__device__ __forceinline__ float sum_row16(float v) {
+  v += __shfl_xor(v, 1);
+  v += __shfl_xor(v, 2);
+  v += __shfl_xor(v, 4);
+  v += __shfl_xor(v, 8);
+  return v;
+}
+__device__ __forceinline__ float sum_col4(float v) {
+  v += __shfl_xor(v, 16);
+  v += __shfl_xor(v, 32);
+  return v;
+}
+
+}  // namespace kdn

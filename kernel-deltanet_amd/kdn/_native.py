@@ -23,6 +23,7 @@ EXPORTED = (
     "kdn_build_omega",
     "kdn_fwht",
     "kdn_fwht_lift",
+    "kdn_fwht_lift_factored",
     "kdn_scan_workspace_bytes",
     "kdn_delta_scan_fwd",
     "kdn_scan_prep",
@@ -43,6 +44,7 @@ EXPORTED = (
     "kdn_pool_free_bytes",
     "kdn_scan_bwd_workspace_bytes",
     "kdn_delta_scan_bwd",
+    "kdn_scan_bwd_phase",
 )
 
 KDN_ERR_CAPACITY = -6
@@ -195,6 +197,10 @@ def lib() -> ctypes.CDLL:
             L.kdn_scan_bwd_workspace_bytes.restype = sz
             L.kdn_delta_scan_bwd.argtypes = [ctypes.POINTER(ScanBwdArgs), vp]
             L.kdn_delta_scan_bwd.restype = ci
+            L.kdn_fwht_lift_factored.argtypes = [vp, i64, i64, ci, vp, vp, vp, vp, cf, vp, i64, ci, vp]
+            L.kdn_fwht_lift_factored.restype = ci
+            L.kdn_scan_bwd_phase.argtypes = [ctypes.POINTER(ScanBwdArgs), ci, vp]
+            L.kdn_scan_bwd_phase.restype = ci
             _lib = L
     return _lib
 

@@ -92,6 +92,31 @@ def lift(x: torch.Tensor, omega_bf16: torch.Tensor, phase: torch.Tensor, inv_tau
     return out.view(*x.shape[:-1], D)
 
 
+def lift_factored(x: torch.Tensor, omega1: torch.Tensor, phase1: torch.Tensor, omega2: torch.Tensor,
+                  phase2: torch.Tensor, inv_tau: float, out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+    """(..., 128) -> (..., 1024) factored lift (kdn_fwht_lift_factored): the two halves of x lifted by the
+    two 64 -> 512 projections, concatenated and renormalised (eps 1e-7)."""
+    require_device(x, "lift_factored")
+    if x.shape[-1] != 128 or tuple(omega1.shape) != (512, 64) or tuple(omega2.shape) != (512, 64):
+        raise ValueError(f"lift_factored: expects x (..., 128) and two (512, 64) projections; got {tuple(x.shape)}")
+    out_dtype = x.dtype if out_dtype is None else out_dtype
+    x2 = _rows(x, 128)
+    if (x2.stride(0) * x2.element_size()) % 16 or x2.data_ptr() % 16:
+        x2 = x2.contiguous()
+    dev = x.device
+    o1, o2 = omega1.to(device=dev).contiguous(), omega2.to(device=dev).contiguous()
+    p1 = phase1.to(device=dev, dtype=torch.float32).contiguous()
+    p2 = phase2.to(device=dev, dtype=torch.float32).contiguous()
+    out = torch.empty(x2.shape[0], 1024, dtype=out_dtype, device=dev)
+    with torch.cuda.device(dev):
+        N.check(N.lib().kdn_fwht_lift_factored(
+            ctypes.c_void_p(x2.data_ptr()), x2.shape[0], x2.stride(0), _tag(x.dtype, "lift_factored"),
+            ctypes.c_void_p(o1.data_ptr()), ctypes.c_void_p(p1.data_ptr()), ctypes.c_void_p(o2.data_ptr()),
+            ctypes.c_void_p(p2.data_ptr()), float(inv_tau), ctypes.c_void_p(out.data_ptr()), out.stride(0),
+            _tag(out_dtype, "lift_factored output"), ctypes.c_void_p(_stream(dev))), "kdn_fwht_lift_factored")
+    return out.view(*x.shape[:-1], 1024)
+
+
 def _last_contig(t: torch.Tensor) -> torch.Tensor:
     return t if t.stride(-1) == 1 else t.contiguous()
 
@@ -282,70 +307,103 @@ def scan(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, beta: torch.Tensor, 
     return y, final_state
 
 
+class ScanBackwardPlan:
+    """One backward call of the scan (kdn_delta_scan_bwd) with its arguments, outputs and workspace
+    prepared once: run() issues the whole backward, phase(i) one of its four launches (0 per-chunk
+    recompute, 1 forward carry, 2 reverse carry, 3 gradients; in that order), e.g. for timing.
+
+    Same layouts as `scan`: q, k (B, T, H, 64), v and dy (B, T, H, 64), beta and decay (B, T, H), states
+    (B, H, 512, 64); dL/dy = dy, dL/d(final state) = d_final_state (None: zero).  `outputs` holds the
+    float32 gradients (dq, dk, dv, dbeta, ddecay or None, d_initial_state or None).  The structured lift
+    with one shared Omega and the delta rule only."""
+
+    def __init__(self, q, k, v, beta, decay, omega_bf16, phase, inv_tau, dy, d_final_state=None,
+                 normalize: bool = False, initial_state=None, need_ddecay: bool = True, need_dinit: bool = True,
+                 workspace: Optional[torch.Tensor] = None):
+        for t, nm in ((q, "q"), (k, "k"), (v, "v"), (beta, "beta"), (dy, "dy")):
+            require_device(t, f"scan_backward: {nm}")
+        dev = q.device
+        if q.dim() != 4 or k.shape != q.shape or v.shape[:3] != q.shape[:3] or beta.shape != q.shape[:3] \
+                or dy.shape != v.shape:
+            raise ValueError(f"scan_backward: shapes q{tuple(q.shape)} k{tuple(k.shape)} v{tuple(v.shape)} "
+                             f"beta{tuple(beta.shape)} dy{tuple(dy.shape)}")
+        if k.dtype != q.dtype or v.dtype != q.dtype:
+            raise TypeError("scan_backward: q, k and v must share a dtype")
+        q, k, v = _last_contig(q), _last_contig(k), _last_contig(v)
+        beta = beta.to(torch.float32)
+        if decay is not None:
+            decay = decay.to(device=dev, dtype=torch.float32)
+        dy = _last_contig(dy.to(torch.float32))
+        B, T, H, d_k = q.shape
+        d_v = v.shape[-1]
+        fm = _features_on(FeatureMap(omega_bf16, phase), dev, H)
+        D = fm.dim(q)
+        if initial_state is not None:
+            initial_state = initial_state.to(device=dev, dtype=torch.float32)
+        if d_final_state is not None:
+            d_final_state = d_final_state.to(device=dev, dtype=torch.float32)
+            if tuple(d_final_state.shape) != (B, H, D, d_v):
+                raise ValueError(f"scan_backward: d_final_state must be (B, H, D, d_v) = {(B, H, D, d_v)}")
+        unused = torch.empty(1, device=dev, dtype=torch.float32).expand(B, H, D, d_v)  # fwd.final_state (ignored)
+        self._fa = scan_args(q, k, v, beta, decay, None, None, inv_tau, normalize, initial_state, unused, dy, None,
+                             0, fm)
+        f32 = dict(device=dev, dtype=torch.float32)
+        dq, dk = torch.empty(B, T, H, d_k, **f32), torch.empty(B, T, H, d_k, **f32)
+        dv, dbeta = torch.empty(B, T, H, d_v, **f32), torch.empty(B, T, H, **f32)
+        ddecay = torch.empty(B, T, H, **f32) if (decay is not None and need_ddecay) else None
+        dinit = torch.empty(B, H, D, d_v, **f32) if need_dinit else None
+        a = N.ScanBwdArgs()
+        a.fwd = ctypes.addressof(self._fa)
+        a.dy, a.dy_stride = dy.data_ptr(), N._i64x3(*dy.stride()[:3])
+        if d_final_state is not None:
+            a.d_final_state, a.dfinal_stride = d_final_state.data_ptr(), N._i64x4(*d_final_state.stride())
+        for nm, t in (("dq", dq), ("dk", dk), ("dv", dv)):
+            setattr(a, nm, t.data_ptr())
+            setattr(a, nm + "_stride", N._i64x3(*t.stride()[:3]))
+        a.dbeta, a.dbeta_stride = dbeta.data_ptr(), N._i64x3(*dbeta.stride())
+        if ddecay is not None:
+            a.ddecay, a.ddecay_stride = ddecay.data_ptr(), N._i64x3(*ddecay.stride())
+        if dinit is not None:
+            a.d_initial_state, a.dinit_stride = dinit.data_ptr(), N._i64x4(*dinit.stride())
+        nbytes = N.lib().kdn_scan_bwd_workspace_bytes(ctypes.byref(a))
+        if nbytes == 0:
+            raise ValueError("scan_backward: unsupported request (kdn_scan_bwd_workspace_bytes returned 0; the "
+                             "backward covers d_k = 64, D = 512, d_v = 64 with the shared structured lift)")
+        if workspace is None or workspace.numel() * workspace.element_size() < nbytes:
+            workspace = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+        a.workspace, a.workspace_bytes = workspace.data_ptr(), workspace.numel() * workspace.element_size()
+        self.args, self.device, self.workspace = a, dev, workspace
+        self.outputs = (dq, dk, dv, dbeta, ddecay, dinit)
+        self.shape = (B, T, H)
+        self._keep = (q, k, v, beta, decay, dy, d_final_state, initial_state, unused, fm.keep())
+
+    def _st(self, stream):
+        return stream if stream is not None else torch.cuda.current_stream(self.device)
+
+    def run(self, stream=None):
+        st = self._st(stream)
+        with torch.cuda.device(self.device):
+            N.check(N.lib().kdn_delta_scan_bwd(ctypes.byref(self.args), ctypes.c_void_p(st.cuda_stream)),
+                    "kdn_delta_scan_bwd")
+        return self.outputs
+
+    def phase(self, i: int, stream=None):
+        st = self._st(stream)
+        with torch.cuda.device(self.device):
+            N.check(N.lib().kdn_scan_bwd_phase(ctypes.byref(self.args), int(i), ctypes.c_void_p(st.cuda_stream)),
+                    "kdn_scan_bwd_phase")
+
+
 def scan_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, beta: torch.Tensor,
                   decay: Optional[torch.Tensor], omega_bf16: torch.Tensor, phase: torch.Tensor, inv_tau: float,
                   dy: torch.Tensor, d_final_state: Optional[torch.Tensor] = None, normalize: bool = False,
                   initial_state: Optional[torch.Tensor] = None, need_ddecay: bool = True,
                   need_dinit: bool = True, workspace: Optional[torch.Tensor] = None):
     """Gradients of `scan` (kdn_delta_scan_bwd) for the loss with dL/dy = dy and dL/d(final state) =
-    d_final_state (None: zero).  Same layouts as `scan`: q, k (B, T, H, 64), v and dy (B, T, H, 64),
-    beta and decay (B, T, H), states (B, H, 512, 64).  Returns float32
-    (dq, dk, dv, dbeta, ddecay or None, d_initial_state or None).  The structured lift with one shared
-    Omega and the delta rule only (the C entry point returns KDN_ERR_UNSUPPORTED otherwise)."""
-    for t, nm in ((q, "q"), (k, "k"), (v, "v"), (beta, "beta"), (dy, "dy")):
-        require_device(t, f"scan_backward: {nm}")
-    dev = q.device
-    if q.dim() != 4 or k.shape != q.shape or v.shape[:3] != q.shape[:3] or beta.shape != q.shape[:3] \
-            or dy.shape != v.shape:
-        raise ValueError(f"scan_backward: shapes q{tuple(q.shape)} k{tuple(k.shape)} v{tuple(v.shape)} "
-                         f"beta{tuple(beta.shape)} dy{tuple(dy.shape)}")
-    if k.dtype != q.dtype or v.dtype != q.dtype:
-        raise TypeError("scan_backward: q, k and v must share a dtype")
-    q, k, v = _last_contig(q), _last_contig(k), _last_contig(v)
-    beta = beta.to(torch.float32)
-    if decay is not None:
-        decay = decay.to(device=dev, dtype=torch.float32)
-    dy = _last_contig(dy.to(torch.float32))
-    B, T, H, d_k = q.shape
-    d_v = v.shape[-1]
-    fm = _features_on(FeatureMap(omega_bf16, phase), dev, H)
-    D = fm.dim(q)
-    if initial_state is not None:
-        initial_state = initial_state.to(device=dev, dtype=torch.float32)
-    if d_final_state is not None:
-        d_final_state = d_final_state.to(device=dev, dtype=torch.float32)
-        if tuple(d_final_state.shape) != (B, H, D, d_v):
-            raise ValueError(f"scan_backward: d_final_state must be (B, H, D, d_v) = {(B, H, D, d_v)}")
-    unused = torch.empty(1, device=dev, dtype=torch.float32).expand(B, H, D, d_v)  # fwd.final_state (ignored)
-    fa = scan_args(q, k, v, beta, decay, None, None, inv_tau, normalize, initial_state, unused, dy, None, 0, fm)
-    f32 = dict(device=dev, dtype=torch.float32)
-    dq, dk = torch.empty(B, T, H, d_k, **f32), torch.empty(B, T, H, d_k, **f32)
-    dv, dbeta = torch.empty(B, T, H, d_v, **f32), torch.empty(B, T, H, **f32)
-    ddecay = torch.empty(B, T, H, **f32) if (decay is not None and need_ddecay) else None
-    dinit = torch.empty(B, H, D, d_v, **f32) if need_dinit else None
-    a = N.ScanBwdArgs()
-    a.fwd = ctypes.addressof(fa)
-    a.dy, a.dy_stride = dy.data_ptr(), N._i64x3(*dy.stride()[:3])
-    if d_final_state is not None:
-        a.d_final_state, a.dfinal_stride = d_final_state.data_ptr(), N._i64x4(*d_final_state.stride())
-    for nm, t in (("dq", dq), ("dk", dk), ("dv", dv)):
-        setattr(a, nm, t.data_ptr())
-        setattr(a, nm + "_stride", N._i64x3(*t.stride()[:3]))
-    a.dbeta, a.dbeta_stride = dbeta.data_ptr(), N._i64x3(*dbeta.stride())
-    if ddecay is not None:
-        a.ddecay, a.ddecay_stride = ddecay.data_ptr(), N._i64x3(*ddecay.stride())
-    if dinit is not None:
-        a.d_initial_state, a.dinit_stride = dinit.data_ptr(), N._i64x4(*dinit.stride())
-    nbytes = N.lib().kdn_scan_bwd_workspace_bytes(ctypes.byref(a))
-    if nbytes == 0:
-        raise ValueError("scan_backward: unsupported request (kdn_scan_bwd_workspace_bytes returned 0; the "
-                         "backward covers d_k = 64, D = 512, d_v = 64 with the shared structured lift)")
-    if workspace is None or workspace.numel() * workspace.element_size() < nbytes:
-        workspace = torch.empty(nbytes, dtype=torch.uint8, device=dev)
-    a.workspace, a.workspace_bytes = workspace.data_ptr(), workspace.numel() * workspace.element_size()
-    with torch.cuda.device(dev):
-        N.check(N.lib().kdn_delta_scan_bwd(ctypes.byref(a), ctypes.c_void_p(_stream(dev))), "kdn_delta_scan_bwd")
-    return dq, dk, dv, dbeta, ddecay, dinit
+    d_final_state (None: zero); see ScanBackwardPlan for layouts.  Returns float32
+    (dq, dk, dv, dbeta, ddecay or None, d_initial_state or None)."""
+    return ScanBackwardPlan(q, k, v, beta, decay, omega_bf16, phase, inv_tau, dy, d_final_state, normalize,
+                            initial_state, need_ddecay, need_dinit, workspace).run()
 
 
 class _Scan(torch.autograd.Function):

@@ -23,6 +23,9 @@ How each function is pinned (see tests/test_oracle_*.py):
                     overwrite closed forms, contractivity.
   chunked_forward   equals token_recurrence to 1e-12 in float64 for every chunk size, with and without
                     decay and initial state; reference carry-algebra pin (tests/test_inter_woodbury.py:14-84).
+  factored_lift     ||phi|| = 1; closed form at x = 0 (cos(b1), cos(b2) halves); with both halves of x and
+                    both projections equal it is the single lift divided by sqrt(2) (to the 1e-7 and 1e-8
+                    epsilons); the seed-42 and seed-1042 tables are make_projection's (pinned above).
   rff_features      with renorm and the seed-42 projection equals lift (pinned above); closed form at x = 0.
   rkhs_features     ||phi|| = 1 exactly; phi(x).phi(y) = mean cos(sqrt(2 gamma) Omega (x - y)) (the
                     cos/sin pairing); gamma scaling at x and sqrt(gamma) x.

@@ -132,6 +132,16 @@ def lift(x: np.ndarray, proj: dict, normalize: bool = False) -> np.ndarray:
     return phi / (np.linalg.norm(phi, axis=-1, keepdims=True) + 1e-8)
 
 
+def factored_lift(x: np.ndarray, proj1: dict, proj2: dict) -> np.ndarray:
+    """FactoredFastWalshHadamardProjection.forward (kernels/factored_kernel_deltanet.py:62-74), float64:
+    the two halves of x lifted by `lift` with the projections of seeds s and s + 1000
+    (:57-58), concatenated and divided by (norm + 1e-7)."""
+    xx = np.asarray(x, dtype=np.float64)
+    d0 = xx.shape[-1] // 2
+    phi = np.concatenate([lift(xx[..., :d0], proj1), lift(xx[..., d0:], proj2)], axis=-1)
+    return phi / (np.linalg.norm(phi, axis=-1, keepdims=True) + 1e-7)
+
+
 def rff_features(x: np.ndarray, omega: np.ndarray, phase: np.ndarray, tau, normalize: bool = True,
                  renorm: bool = False) -> np.ndarray:
     """phi = sqrt(2/D) cos(x_hat Omega_h^T / tau_h + b_h), per head; float64.

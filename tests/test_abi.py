@@ -40,7 +40,8 @@ def test_library_exports_every_declared_symbol(lib):
         assert hasattr(lib, name)
 
 
-@pytest.mark.parametrize("cname,pystruct", [("kdn_scan_args", N.ScanArgs), ("kdn_ragged_args", N.RaggedArgs)])
+@pytest.mark.parametrize("cname,pystruct", [("kdn_scan_args", N.ScanArgs), ("kdn_ragged_args", N.RaggedArgs),
+                                            ("kdn_scan_bwd_args", N.ScanBwdArgs)])
 def test_args_layout_matches_c(cname, pystruct):
     fields = [f[0] for f in pystruct._fields_]
     src = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', "int main(void){",
@@ -61,7 +62,7 @@ def test_args_layout_matches_c(cname, pystruct):
 def test_strerror_and_version(lib):
     for code in (0, -1, -2, -3, -4, -5, -99):
         assert len(lib.kdn_strerror(code)) > 0
-    assert lib.kdn_abi_version() == (1 << 16) | 3
+    assert lib.kdn_abi_version() == (1 << 16) | 4
 
 
 def _args(**kw):
@@ -128,3 +129,42 @@ def test_lift_fwht_omega_argument_errors_need_no_device(lib):
     assert lib.kdn_fwht(p, 0, 64, 64, 0, p, 64, None) == 0
     assert lib.kdn_build_omega(p, 32, 512, p, 1, None) == -2
     assert lib.kdn_build_omega(None, 64, 512, p, 1, None) == -1
+
+
+def test_general_width_requests_need_no_device(lib):
+    # D = 1024 (the factored d_k = 128 path): pre-lifted features only, d_v 64 or 128, the delta rule; one
+    # fp32 record per (batch, head, chunk): 417,920 floats at d_v = 128, 344,192 at d_v = 64
+    a = _args(T=256, H=2, d_k=1024, D=1024, d_v=128, feature_mode=1)
+    assert lib.kdn_scan_workspace_bytes(ctypes.byref(a)) == 2 * 4 * 417920 * 4
+    assert lib.kdn_scan_workspace_bytes_pipelined(ctypes.byref(a)) == 2 * 4 * 417920 * 4
+    assert lib.kdn_scan_workspace_bytes(ctypes.byref(_args(T=256, d_k=1024, D=1024, d_v=64, feature_mode=1))) \
+        == 16 * 4 * 344192 * 4
+    assert lib.kdn_scan_workspace_bytes(ctypes.byref(_args(d_k=64, D=1024, feature_mode=0))) == 0
+    assert lib.kdn_scan_workspace_bytes(ctypes.byref(_args(d_k=1024, D=1024, d_v=32, feature_mode=1))) == 0
+    assert lib.kdn_scan_workspace_bytes(ctypes.byref(_args(d_k=1024, D=1024, feature_mode=1, rule=1))) == 0
+    # the general-width scan has no phase entry points: rejected on the host before anything is enqueued
+    a = _fake_ptrs(_args(T=256, H=2, d_k=1024, D=1024, d_v=128, feature_mode=1))
+    a.workspace_bytes = 1 << 40
+    assert lib.kdn_scan_prep(ctypes.byref(a), 0, 1, None) == -2
+    assert lib.kdn_scan_state(ctypes.byref(a), 0, 1, None) == -2
+    a.workspace_bytes = 1024
+    assert lib.kdn_delta_scan_fwd(ctypes.byref(a), None) == -3
+
+
+def test_backward_workspace_and_errors_need_no_device(lib):
+    f = _fake_ptrs(_args(T=256, H=2))
+    g = N.ScanBwdArgs()
+    g.fwd = ctypes.addressof(f)
+    for i, nm in enumerate(("dy", "dq", "dk", "dv", "dbeta", "workspace")):
+        setattr(g, nm, 0x7E0000000000 + 0x100000 * i)
+    assert lib.kdn_scan_bwd_workspace_bytes(ctypes.byref(g)) == 2 * 4 * 1116160
+    g.workspace_bytes = 1024
+    assert lib.kdn_delta_scan_bwd(ctypes.byref(g), None) == -3
+    assert lib.kdn_scan_bwd_phase(ctypes.byref(g), 4, None) == -1
+    f2 = _fake_ptrs(_args(T=256, H=2, d_v=32))
+    g.fwd = ctypes.addressof(f2)
+    assert lib.kdn_scan_bwd_workspace_bytes(ctypes.byref(g)) == 0
+    assert lib.kdn_delta_scan_bwd(ctypes.byref(g), None) == -2
+    g.fwd = ctypes.addressof(f)
+    g.dy = None
+    assert lib.kdn_delta_scan_bwd(ctypes.byref(g), None) == -1
