@@ -118,6 +118,9 @@ def main():
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain device copy of known size (for PMC byte-counter calibration)")
     ap.add_argument("--pmc", default=None)
+    ap.add_argument("--factored", action="store_true",
+                    help="time the factored d_k = 128 path (two 64 -> 512 lifts, D = 1024 scan, d_v = 128) on a "
+                         "B=1, H=32, T=16384 layer instead of config 3")
     ap.add_argument("--backward", action="store_true",
                     help="time the backward pass (kdn_delta_scan_bwd: gradients of q, k, v, beta) on the config "
                          "3 shape instead of the forward")
@@ -140,6 +143,8 @@ def main():
         return
     if args.backward:
         return bench_backward(args, dev)
+    if args.factored:
+        return bench_factored(args, dev)
     if args.config == 2:
         return bench_lift(args, dev)
     if args.config == 5:
@@ -382,6 +387,84 @@ def bench_backward(args, dev):
                                                     min(args.cpu_tokens, 4096), H)
     else:
         out["cpu_baseline"] = None
+    print(json.dumps(out), flush=True)
+
+
+def bench_factored(args, dev):
+    """The factored d_k = 128 path (reference kernels/factored_kernel_deltanet.py): q, k (B, T, H, 128) bf16
+    lifted to D = 1024 by kdn_fwht_lift_factored, then the D = 1024 delta-rule scan (d_v = 128, fp32 state,
+    lambda = 1).  A step = both lifts and the scan."""
+    from kdn import ops
+    from kernels import FactoredFastWalshHadamardProjection
+
+    B = args.B if args.B is not None else 1
+    T = args.T if args.T is not None else 16384
+    H = 32 if args.H == 16 else args.H
+    D, dv, dk = 1024, 128, 128
+    g = torch.Generator(device=dev).manual_seed(1234)
+    q = torch.randn(B, T, H, dk, generator=g, device=dev).to(torch.bfloat16)
+    k = torch.randn(B, T, H, dk, generator=g, device=dev).to(torch.bfloat16)
+    v = torch.randn(B, T, H, dv, generator=g, device=dev).to(torch.bfloat16)
+    beta = torch.sigmoid(torch.randn(B, T, H, generator=g, device=dev))
+    fp = FactoredFastWalshHadamardProjection(dk, D, 42)
+    o1, p1 = fp.proj1.device_omega(dev), fp.proj1.device_phase(dev)
+    o2, p2 = fp.proj2.device_omega(dev), fp.proj2.device_phase(dev)
+    inv_tau = fp.proj1.tau_star_inv
+    fm = ops.FeatureMap(lifted=True)
+    final = torch.empty(B, H, D, dv, device=dev)
+    y = torch.empty(B, T, H, dv, device=dev, dtype=torch.bfloat16)
+    pq = ops.lift_factored(q, o1, p1, o2, p2, inv_tau)
+    ws = torch.empty(ops.scan_workspace_bytes(pq, v, None, 0, True, fm), dtype=torch.uint8, device=dev)
+    stream = torch.cuda.current_stream(dev)
+
+    def step(times=None):
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)] if times is not None else None
+        if ev:
+            ev[0].record(stream)
+        fq = ops.lift_factored(q, o1, p1, o2, p2, inv_tau)
+        fk = ops.lift_factored(k, o1, p1, o2, p2, inv_tau)
+        if ev:
+            ev[1].record(stream)
+        ops.scan(fq, fk, v, beta, None, None, None, 1.0, final_state=final, y=y, workspace=ws, features=fm)
+        if ev:
+            ev[2].record(stream)
+            times.append(ev)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(args.steps):
+        step()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / args.steps
+    times = []
+    for _ in range(args.steps):
+        step(times)
+    torch.cuda.synchronize()
+    lift_ms = sum(a.elapsed_time(b) for a, b, _ in times) / args.steps
+    scan_ms = sum(b.elapsed_time(c) for _, b, c in times) / args.steps
+    nch = (T + C - 1) // C
+    units = B * H * nch
+    f_chunk = 4 * C * C * D + 6 * C * D * dv + 9 * C * C * dv + (2.0 / 3.0) * C ** 3
+    achieved = f_chunk * units / scan_ms / 1e9
+    lift_bytes = 2 * B * T * H * (dk + D) * 2  # q and k: bf16 rows in, bf16 features out
+    out = {
+        "metric": "factored d_k=128 prefill tokens/s (lift + D=1024 scan) on 1 GPU; % of MFMA roofline",
+        "value": B * T / (ms / 1e3), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) q/k/v, sigmoid(N(0,1)) beta; projection seeds 42 and 1042)",
+        "config": {"workload": f"factored d_k=128 layer, B={B}, H={H}, T={T}, d_k=128->D={D} (2 x 64->512), "
+                               f"d_v={dv}, bf16 q/k/v, fp32 beta and state, lambda=1",
+                   "B": B, "H": H, "T": T, "D": D, "d_v": dv, "parallelism": "single GPU"},
+        "roofline": {"bound": "mfma", "achieved": achieved, "peak": MFMA_BF16_PEAK / 1e12, "unit": "TFLOP/s",
+                     "frac": achieved / (MFMA_BF16_PEAK / 1e12), "traffic": None, "kernel": "scan (3 launches)"},
+        "phases": {"lift": {"ms": lift_ms, "alg_bytes": lift_bytes, "gbps": lift_bytes / lift_ms / 1e6},
+                   "scan": {"ms": scan_ms, "alg_flops": f_chunk * units, "tflops": achieved}},
+        "cpu_baseline": None,
+    }
     print(json.dumps(out), flush=True)
 
 

@@ -6,7 +6,7 @@
 // D = 512 scan: y_t = S_{t-1} phi_q(t), S_t = lambda_t S_{t-1} (I - beta_t phi_k phi_k^T) + beta_t v_t phi_k^T.
 //
 // Three launches per call, with one fp32 record per (batch, head, 64-token chunk):
-//   prep   (parallel)   features to fp32 rows, Grams K K^T and Q K^T, A, T = (I + A)^-1 (lane-quad
+//   prep   (parallel)   Grams K K^T and Q K^T from the feature rows in place, A, T = (I + A)^-1 (lane-quad
 //                       substitution), Tp = T diag(beta g), P, U~ = T (beta o V); K packed in MFMA
 //                       fragment order (rows and transposed)
 //   carry  (sequential) S^T at every chunk start; X_K = K S^T, W = U~ - Tp X_K,
@@ -19,6 +19,7 @@
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdint.h>
+#include <type_traits>
 #include "kdn_frag.hpp"
 #include "kdn_internal.hpp"
 #include "kdn_io.hpp"
@@ -33,11 +34,9 @@ constexpr int LD = 68;
 template <int D, int DV>
 struct Rec {
   static constexpr int NV = DV / 16;
-  static constexpr size_t K = 0;              // [64][D] phi_k rows (0 past T)
-  static constexpr size_t Q = K + C * D;      // [64][D] phi_q rows
-  static constexpr size_t KXF = Q + C * D;    // K-row fragments [m 4][jb D/32][lane], sized for f32x8
+  static constexpr size_t KXF = 0;            // K-row fragments [m 4][jb D/32][lane], sized for f32x8
   static constexpr size_t KTF = KXF + C * D;  // K^T-row fragments [ft D/16][jb 2][lane]
-  static constexpr size_t S = KTF + C * D;    // [D][DV] S^T at the chunk start
+  static constexpr size_t S = KTF + C * D;    // S^T at the chunk start as output B fragments [jb D/32][n NV][lane]
   static constexpr size_t TP = S + D * DV;    // [64][64] T diag(beta g)
   static constexpr size_t P = TP + C * C;     // [64][64]
   static constexpr size_t U = P + C * C;      // U~ as tiles [m 4][n NV][lane] f32x4
@@ -62,6 +61,37 @@ struct Params {
 template <int D, int DV>
 __device__ __forceinline__ float* record(const Params& p, int64_t b, int64_t h, int64_t c) {
   return p.ws + ((b * p.H + h) * p.nch + c) * (int64_t)Rec<D, DV>::floats;
+}
+
+// Fragments read straight from the input feature rows of one chunk (row i = token t0 + i, stride rs
+// elements; rows at or past `nrows` read as zero).  rows: element (r0 + l%16, k0 + kappa);
+// cols: element (c0 + l%16, k0 + kappa) = row k0 + kappa, column c0 + l%16.
+template <typename InT>
+__device__ __forceinline__ f32x8 frag_rows_in(const InT* base, int64_t rs, int r0, int k0, int lane, int nrows) {
+  const int row = r0 + (lane & 15);
+  f32x8 r;
+  if (row < nrows) {
+    const InT* q = base + row * rs + k0 + 4 * (lane >> 4);
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      r[s] = ldx(q + s);
+      r[4 + s] = ldx(q + 16 + s);
+    }
+  } else {
+#pragma unroll
+    for (int s = 0; s < 8; ++s) r[s] = 0.f;
+  }
+  return r;
+}
+template <typename InT>
+__device__ __forceinline__ f32x8 frag_cols_in(const InT* base, int64_t rs, int c0, int k0, int lane, int nrows) {
+  f32x8 r;
+#pragma unroll
+  for (int s = 0; s < 8; ++s) {
+    const int row = k0 + kappa(lane, s);
+    r[s] = row < nrows ? ldx(base + row * rs + c0 + (lane & 15)) : 0.f;
+  }
+  return r;
 }
 
 // ---------------------------------------------------------------------------------------------- prep
@@ -98,28 +128,10 @@ __global__ void __launch_bounds__(256) gen_prep_kernel(Params p) {
     rec[R::VEC + lane] = l;
     rec[R::VEC + 64 + lane] = be;
   }
-  // feature rows (fp32, zero past T): thread (row r, quarter part) copies D / 4 features of q and k
-  {
-    const InT* qi = reinterpret_cast<const InT*>(p.q) + b * p.qs0 + (t0 + r) * p.qs1 + h * p.qs2 + part * (D / 4);
-    const InT* ki = reinterpret_cast<const InT*>(p.k) + b * p.ks0 + (t0 + r) * p.ks1 + h * p.ks2 + part * (D / 4);
-    float* qo = rec + R::Q + (size_t)r * D + part * (D / 4);
-    float* ko = rec + R::K + (size_t)r * D + part * (D / 4);
-    for (int e = 0; e < D / 4; e += 8) {
-      float a8[8], b8[8];
-      if (rvalid) {
-        load8<InT>(qi + e, a8);
-        load8<InT>(ki + e, b8);
-      } else {
-#pragma unroll
-        for (int s = 0; s < 8; ++s) a8[s] = b8[s] = 0.f;
-      }
-      *reinterpret_cast<f32x4*>(qo + e) = f32x4{a8[0], a8[1], a8[2], a8[3]};
-      *reinterpret_cast<f32x4*>(qo + e + 4) = f32x4{a8[4], a8[5], a8[6], a8[7]};
-      *reinterpret_cast<f32x4*>(ko + e) = f32x4{b8[0], b8[1], b8[2], b8[3]};
-      *reinterpret_cast<f32x4*>(ko + e + 4) = f32x4{b8[4], b8[5], b8[6], b8[7]};
-    }
-  }
-  __threadfence();
+  // the chunk's feature rows, read in place (rows past T read as zero)
+  const int nrows = (int)(p.T - t0 < C ? p.T - t0 : C);
+  const InT* Kin = reinterpret_cast<const InT*>(p.k) + b * p.ks0 + t0 * p.ks1 + h * p.ks2;
+  const InT* Qin = reinterpret_cast<const InT*>(p.q) + b * p.qs0 + t0 * p.qs1 + h * p.qs2;
   __syncthreads();
   // beta o V in LDS
   {
@@ -130,17 +142,15 @@ __global__ void __launch_bounds__(256) gen_prep_kernel(Params p) {
   }
   // Grams (row tile w) -> A and P
   {
-    const float* K = rec + R::K;
-    const float* Q = rec + R::Q;
     f32x4 gkk[4], gqk[4];
 #pragma unroll
     for (int n = 0; n < 4; ++n) gkk[n] = gqk[n] = zero4();
     for (int jb = 0; jb < D / 32; ++jb) {
-      const f32x8 kw = frag_rows(K, D, 16 * w, 32 * jb, lane);
-      const f32x8 qw = frag_rows(Q, D, 16 * w, 32 * jb, lane);
+      const f32x8 kw = frag_rows_in(Kin, p.ks1, 16 * w, 32 * jb, lane, nrows);
+      const f32x8 qw = frag_rows_in(Qin, p.qs1, 16 * w, 32 * jb, lane, nrows);
 #pragma unroll
       for (int n = 0; n < 4; ++n) {
-        const f32x8 kn = frag_rows(K, D, 16 * n, 32 * jb, lane);
+        const f32x8 kn = frag_rows_in(Kin, p.ks1, 16 * n, 32 * jb, lane, nrows);
         gkk[n] = mm<PB>(gkk[n], kw, kn);
         gqk[n] = mm<PB>(gqk[n], qw, kn);
       }
@@ -159,18 +169,19 @@ __global__ void __launch_bounds__(256) gen_prep_kernel(Params p) {
   // the transposed fragments of feature tiles [w D/64, (w+1) D/64)
   {
     using frag = typename PB::frag;
-    const float* K = rec + R::K;
     frag* kxf = reinterpret_cast<frag*>(rec + R::KXF);
     frag* ktf = reinterpret_cast<frag*>(rec + R::KTF);
     for (int jj = 0; jj < D / 128; ++jj) {
       const int jb = w * (D / 128) + jj;
 #pragma unroll
-      for (int m = 0; m < 4; ++m) kxf[(m * (D / 32) + jb) * 64 + lane] = PB::from_f32(frag_rows(K, D, 16 * m, 32 * jb, lane));
+      for (int m = 0; m < 4; ++m)
+        kxf[(m * (D / 32) + jb) * 64 + lane] = PB::from_f32(frag_rows_in(Kin, p.ks1, 16 * m, 32 * jb, lane, nrows));
     }
     for (int tt = 0; tt < D / 64; ++tt) {
       const int ft = w * (D / 64) + tt;
 #pragma unroll
-      for (int jb = 0; jb < 2; ++jb) ktf[(ft * 2 + jb) * 64 + lane] = PB::from_f32(frag_cols(K, D, 16 * ft, 32 * jb, lane));
+      for (int jb = 0; jb < 2; ++jb)
+        ktf[(ft * 2 + jb) * 64 + lane] = PB::from_f32(frag_cols_in(Kin, p.ks1, 16 * ft, 32 * jb, lane, nrows));
     }
   }
   __syncthreads();
@@ -213,18 +224,125 @@ __global__ void __launch_bounds__(256) gen_prep_kernel(Params p) {
 // --------------------------------------------------------------------------------------------- carry
 // grid: 8 * ceil(B*H / 8) * NV workgroups of 256 threads; workgroup (head-batch hb, value tile n), the
 // NV value tiles of a head on one XCD.  Wave w keeps features [w D/4, (w+1) D/4) of its D x 16 slice of
-// S^T in registers.
+// S^T in registers.  The chunk-start slice is stored as the B fragments of the output's Q S^T product
+// (the pairs of 16-feature tiles, kdn_frag.hpp) in the policy's fragment type.  With bf16 fragments the
+// next chunk's K-row fragments are loaded one iteration ahead (two register sets).
 struct CarryShared {
   f32x4 xp[4][4][64];
   f32x4 x[4][64];
   f32x4 z[4][64];
 };
 
+template <class PB, int D>
+struct CarryK {
+  typename PB::frag kx[4][D / 128];
+};
+
+template <class PB, int D, int DV>
+__device__ __forceinline__ void carry_load_kx(CarryK<PB, D>& o, const float* rec, int w, int lane) {
+  using R = Rec<D, DV>;
+  constexpr int JPW = D / 128;
+  const typename PB::frag* kxf = reinterpret_cast<const typename PB::frag*>(rec + R::KXF);
+#pragma unroll
+  for (int m = 0; m < 4; ++m)
+#pragma unroll
+    for (int jj = 0; jj < JPW; ++jj) o.kx[m][jj] = kxf[(m * (D / 32) + w * JPW + jj) * 64 + lane];
+}
+
+template <class PB, int D, int DV, bool PIPE>
+__device__ __forceinline__ bool carry_step(const Params& p, CarryShared& sh, int64_t b, int64_t h, int64_t c,
+                                           CarryK<PB, D>& cur, CarryK<PB, D>& nxt, f32x4 (&Sg)[D / 64], int w,
+                                           int lane, int n, unsigned& sink) {
+  using R = Rec<D, DV>;
+  using frag = typename PB::frag;
+  constexpr int NV = R::NV, TPW = D / 64, JPW = D / 128;
+  const bool more = c + 1 < p.nch;
+  float* rec = record<D, DV>(p, b, h, c);
+  const frag* kxf = reinterpret_cast<const frag*>(rec + R::KXF);
+  const f32x8 tp0 = frag_rows(rec + R::TP, C, 16 * w, 0, lane), tp1 = frag_rows(rec + R::TP, C, 16 * w, 32, lane);
+  const f32x4 ur = reinterpret_cast<const f32x4*>(rec + R::U)[(w * NV + n) * 64 + lane];
+  const f32x4 lr = *reinterpret_cast<const f32x4*>(rec + R::VEC + 16 * w + 4 * (lane >> 4));
+  const float l63 = rec[R::VEC + 63];
+  unsigned pf = 0;  // L2-prefetch loads, folded into `sink` at the end of the step
+  if (more) {
+    const float* nrec = record<D, DV>(p, b, h, c + 1);
+    if constexpr (PIPE) carry_load_kx<PB, D, DV>(nxt, nrec, w, lane);
+    const unsigned* nr = reinterpret_cast<const unsigned*>(nrec);
+    const int idx = n * 256 + (int)threadIdx.x;  // 0 .. 256 NV - 1
+    constexpr int KLINES = D * (int)sizeof(frag) / 16;  // 128-byte lines of one packed K (D/8 fragments)
+    for (int l = idx; l < KLINES; l += 256 * NV) {
+      pf += nr[R::KTF + 32 * l];
+      if constexpr (!PIPE) pf += nr[R::KXF + 32 * l];
+    }
+    if (idx < 128) pf += nr[R::TP + 32 * idx];                       // 128 lines of Tp
+    else if (idx < 128 + 2 * DV) pf += nr[R::U + 32 * (idx - 128)];  // 2 DV lines of U~
+  }
+
+  // store the chunk-start slice (as output fragments) and form K times it, partial over this wave's features
+  frag* sf = reinterpret_cast<frag*>(rec + R::S);
+  f32x4 xp[4];
+#pragma unroll
+  for (int m = 0; m < 4; ++m) xp[m] = zero4();
+#pragma unroll
+  for (int jj = 0; jj < JPW; ++jj) {
+    const frag sb = PB::from_f32(pair_to8(Sg[2 * jj], Sg[2 * jj + 1]));
+    sf[((w * JPW + jj) * NV + n) * 64 + lane] = sb;
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+      xp[m] = PB::mma(xp[m], PIPE ? cur.kx[m][jj] : kxf[(m * (D / 32) + w * JPW + jj) * 64 + lane], sb);
+  }
+#pragma unroll
+  for (int m = 0; m < 4; ++m) sh.xp[w][m][lane] = xp[m];
+  const float gC = expf(l63);
+#pragma unroll
+  for (int t = 0; t < TPW; ++t) Sg[t] = Sg[t] * gC;
+  __syncthreads();
+  // K^T fragments for the update, issued now (bf16: 128 registers) so that they arrive during the W / Z
+  // phase; fp32 fragments are read where the update consumes them
+  constexpr bool EARLY = std::is_same<PB, PrecBF16>::value;
+  const frag* ktf = reinterpret_cast<const frag*>(rec + R::KTF);
+  frag kt[EARLY ? TPW : 1][2];
+  if constexpr (EARLY) {
+#pragma unroll
+    for (int t = 0; t < TPW; ++t)
+#pragma unroll
+      for (int jb = 0; jb < 2; ++jb) kt[t][jb] = ktf[((w * TPW + t) * 2 + jb) * 64 + lane];
+  }
+  const f32x4 X = sh.xp[0][w][lane] + sh.xp[1][w][lane] + sh.xp[2][w][lane] + sh.xp[3][w][lane];
+  sh.x[w][lane] = X;
+  __syncthreads();
+  f32x4 tx = mm<PrecF32>(zero4(), tp0, pair_to8(sh.x[0][lane], sh.x[1][lane]));
+  tx = mm<PrecF32>(tx, tp1, pair_to8(sh.x[2][lane], sh.x[3][lane]));
+  const f32x4 Wt = ur - tx;
+  const int vc = 16 * n + (lane & 15);
+  f32x4 kap;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    rec[R::W + (16 * w + 4 * (lane >> 4) + i) * DV + vc] = Wt[i];
+    kap[i] = expf(l63 - lr[i]);
+  }
+  sh.z[w][lane] = kap * Wt;
+  __syncthreads();
+  const frag zb0 = PB::from_f32(pair_to8(sh.z[0][lane], sh.z[1][lane]));
+  const frag zb1 = PB::from_f32(pair_to8(sh.z[2][lane], sh.z[3][lane]));
+#pragma unroll
+  for (int t = 0; t < TPW; ++t) {
+    if constexpr (EARLY) {
+      Sg[t] = PB::mma(PB::mma(Sg[t], kt[t][0], zb0), kt[t][1], zb1);
+    } else {
+      Sg[t] = PB::mma(PB::mma(Sg[t], ktf[((w * TPW + t) * 2) * 64 + lane], zb0), ktf[((w * TPW + t) * 2 + 1) * 64 + lane],
+                      zb1);
+    }
+  }
+  sink += pf;
+  return more;
+}
+
 template <class PB, int D, int DV>
 __global__ void __launch_bounds__(256) gen_carry_kernel(Params p) {
   using R = Rec<D, DV>;
-  using frag = typename PB::frag;
-  constexpr int NV = R::NV, FPW = D / 4, TPW = FPW / 16, JPW = FPW / 32;
+  constexpr int NV = R::NV, FPW = D / 4, TPW = FPW / 16;
+  constexpr bool PIPE = false;  // two register sets of 32 K fragments do not fit beside the D = 1024 slice
   __shared__ CarryShared sh;
   const int64_t id = blockIdx.x;
   const int64_t xcd = id & 7, jdx = id >> 3;
@@ -245,66 +363,11 @@ __global__ void __launch_bounds__(256) gen_carry_kernel(Params p) {
       Sg[t][i] = p.init ? p.init[b * p.is0 + h * p.is1 + f * p.is2 + vc * p.is3] : 0.f;
     }
   unsigned sink = 0;  // keeps the L2 prefetch loads alive (never stored: nch is positive)
-  for (int64_t c = 0; c < p.nch; ++c) {
-    float* rec = record<D, DV>(p, b, h, c);
-    const frag* kxf = reinterpret_cast<const frag*>(rec + R::KXF);
-    const frag* ktf = reinterpret_cast<const frag*>(rec + R::KTF);
-    const f32x8 tp0 = frag_rows(rec + R::TP, C, 16 * w, 0, lane), tp1 = frag_rows(rec + R::TP, C, 16 * w, 32, lane);
-    const f32x4 ur = reinterpret_cast<const f32x4*>(rec + R::U)[(w * NV + n) * 64 + lane];
-    const f32x4 lr = *reinterpret_cast<const f32x4*>(rec + R::VEC + 16 * w + 4 * (lane >> 4));
-    const float l63 = rec[R::VEC + 63];
-    unsigned pf = 0;
-    if (c + 1 < p.nch) {
-      // L2 prefetch of the next chunk's K fragments (both orders), Tp, U~ and vectors
-      const unsigned* nr = reinterpret_cast<const unsigned*>(record<D, DV>(p, b, h, c + 1));
-      const int idx = n * 256 + (int)threadIdx.x;  // 0 .. 256 NV - 1
-      constexpr int KLINES = D * (int)sizeof(frag) / 16;  // 128-byte lines of one packed K (D/8 fragments)
-      for (int l = idx; l < KLINES; l += 256 * NV) pf += nr[R::KXF + 32 * l] + nr[R::KTF + 32 * l];
-      if (idx < 128) pf += nr[R::TP + 32 * idx];                                // 128 lines of Tp
-      else if (idx < 128 + 2 * DV) pf += nr[R::U + 32 * (idx - 128)];           // 2 DV lines of U~
-    }
-
-    float* dst = rec + R::S;
-#pragma unroll
-    for (int t = 0; t < TPW; ++t)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) dst[(size_t)(FPW * w + 16 * t + 4 * (lane >> 4) + i) * DV + vc] = Sg[t][i];
-
-    f32x4 xp[4];
-#pragma unroll
-    for (int m = 0; m < 4; ++m) xp[m] = zero4();
-#pragma unroll
-    for (int jj = 0; jj < JPW; ++jj) {
-      const frag sb = PB::from_f32(pair_to8(Sg[2 * jj], Sg[2 * jj + 1]));
-#pragma unroll
-      for (int m = 0; m < 4; ++m) xp[m] = PB::mma(xp[m], kxf[(m * (D / 32) + w * JPW + jj) * 64 + lane], sb);
-    }
-#pragma unroll
-    for (int m = 0; m < 4; ++m) sh.xp[w][m][lane] = xp[m];
-    const float gC = expf(l63);
-#pragma unroll
-    for (int t = 0; t < TPW; ++t) Sg[t] = Sg[t] * gC;
-    __syncthreads();
-    const f32x4 X = sh.xp[0][w][lane] + sh.xp[1][w][lane] + sh.xp[2][w][lane] + sh.xp[3][w][lane];
-    sh.x[w][lane] = X;
-    __syncthreads();
-    f32x4 tx = mm<PrecF32>(zero4(), tp0, pair_to8(sh.x[0][lane], sh.x[1][lane]));
-    tx = mm<PrecF32>(tx, tp1, pair_to8(sh.x[2][lane], sh.x[3][lane]));
-    const f32x4 Wt = ur - tx;
-    f32x4 kap;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      rec[R::W + (16 * w + 4 * (lane >> 4) + i) * DV + vc] = Wt[i];
-      kap[i] = expf(l63 - lr[i]);
-    }
-    sh.z[w][lane] = kap * Wt;
-    __syncthreads();
-    const frag zb0 = PB::from_f32(pair_to8(sh.z[0][lane], sh.z[1][lane]));
-    const frag zb1 = PB::from_f32(pair_to8(sh.z[2][lane], sh.z[3][lane]));
-#pragma unroll
-    for (int t = 0; t < TPW; ++t)
-      Sg[t] = PB::mma(PB::mma(Sg[t], ktf[((w * TPW + t) * 2) * 64 + lane], zb0), ktf[((w * TPW + t) * 2 + 1) * 64 + lane], zb1);
-    sink += pf;
+  CarryK<PB, D> ka, kb;
+  if constexpr (PIPE) carry_load_kx<PB, D, DV>(ka, record<D, DV>(p, b, h, 0), w, lane);
+  for (int64_t c = 0;; c += 2) {
+    if (!carry_step<PB, D, DV, PIPE>(p, sh, b, h, c, ka, kb, Sg, w, lane, n, sink)) break;
+    if (!carry_step<PB, D, DV, PIPE>(p, sh, b, h, c + 1, kb, ka, Sg, w, lane, n, sink)) break;
   }
   if (p.nch < 0) p.ws[0] = (float)sink;
 #pragma unroll
@@ -325,7 +388,7 @@ __device__ __forceinline__ void store_el<float>(float* p, float v) { *p = v; }
 template <>
 __device__ __forceinline__ void store_el<__bf16>(__bf16* p, float v) { *p = (__bf16)v; }
 
-template <class PB, typename OutT, int D, int DV>
+template <class PB, typename InT, typename OutT, int D, int DV>
 __global__ void __launch_bounds__(256) gen_output_kernel(Params p) {
   using R = Rec<D, DV>;
   constexpr int NV = R::NV;
@@ -334,13 +397,16 @@ __global__ void __launch_bounds__(256) gen_output_kernel(Params p) {
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int64_t t0 = c * C;
   const float* rec = record<D, DV>(p, b, h, c);
+  const int nrows = (int)(p.T - t0 < C ? p.T - t0 : C);
+  const InT* Qin = reinterpret_cast<const InT*>(p.q) + b * p.qs0 + t0 * p.qs1 + h * p.qs2;
   f32x4 qs[NV];
 #pragma unroll
   for (int n = 0; n < NV; ++n) qs[n] = zero4();
+  const typename PB::frag* sf = reinterpret_cast<const typename PB::frag*>(rec + R::S);
   for (int jb = 0; jb < D / 32; ++jb) {
-    const f32x8 qa = frag_rows(rec + R::Q, D, 16 * w, 32 * jb, lane);
+    const typename PB::frag qa = PB::from_f32(frag_rows_in(Qin, p.qs1, 16 * w, 32 * jb, lane, nrows));
 #pragma unroll
-    for (int n = 0; n < NV; ++n) qs[n] = mm<PB>(qs[n], qa, frag_cols(rec + R::S, DV, 16 * n, 32 * jb, lane));
+    for (int n = 0; n < NV; ++n) qs[n] = PB::mma(qs[n], qa, sf[(jb * NV + n) * 64 + lane]);
   }
   const f32x8 p0 = frag_rows(rec + R::P, C, 16 * w, 0, lane), p1 = frag_rows(rec + R::P, C, 16 * w, 32, lane);
   f32x4 a;
@@ -368,7 +434,7 @@ static int launch(const Params& p, hipStream_t st) {
   const unsigned carry_wgs = (unsigned)(((p.B * p.H + 7) / 8) * 8 * (DV / 16));
   hipLaunchKernelGGL((gen_prep_kernel<PB, InT, D, DV>), chunk_grid, dim3(256), 0, st, p);
   hipLaunchKernelGGL((gen_carry_kernel<PB, D, DV>), dim3(carry_wgs), dim3(256), 0, st, p);
-  hipLaunchKernelGGL((gen_output_kernel<PB, OutT, D, DV>), chunk_grid, dim3(256), 0, st, p);
+  hipLaunchKernelGGL((gen_output_kernel<PB, InT, OutT, D, DV>), chunk_grid, dim3(256), 0, st, p);
   return launch_status();
 }
 

@@ -31,6 +31,23 @@ __device__ __forceinline__ void load8<float>(const float* p, float* o) {
   o[4] = b[0]; o[5] = b[1]; o[6] = b[2]; o[7] = b[3];
 }
 
+// Eight consecutive elements from fp32 values (one 16-byte store for bf16, two for fp32).
+template <typename T>
+__device__ __forceinline__ void store_row8(T* p, const float* v);
+template <>
+__device__ __forceinline__ void store_row8<__bf16>(__bf16* p, const float* v) {
+  bf16x8 r;
+#pragma unroll
+  for (int s = 0; s < 8; ++s) r[s] = (__bf16)v[s];
+  *reinterpret_cast<bf16x8*>(p) = r;
+}
+template <>
+__device__ __forceinline__ void store_row8<float>(float* p, const float* v) {
+  f32x4 a = {v[0], v[1], v[2], v[3]}, c = {v[4], v[5], v[6], v[7]};
+  reinterpret_cast<f32x4*>(p)[0] = a;
+  reinterpret_cast<f32x4*>(p)[1] = c;
+}
+
 template <typename T>
 __device__ __forceinline__ void store4(T* p, const float* v);
 template <>

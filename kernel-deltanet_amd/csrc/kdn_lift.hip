@@ -311,22 +311,27 @@ extern "C" int kdn_fwht_lift(const void* x, int64_t rows, int64_t x_row_stride, 
 }
 
 namespace kdn {
-// Row renormalisation in place: x[r] <- x[r] / (||x[r]||_2 + eps), one wave per row of n elements.
+// Row renormalisation in place of rows of 1024 elements: x[r] <- x[r] / (||x[r]||_2 + eps).  One wave per
+// row; lane l holds the 16 contiguous elements 16l .. 16l+15 (16- or 32-byte vector accesses).
 template <typename T>
-__global__ void __launch_bounds__(256) renorm_rows_kernel(T* x, int64_t rows, int64_t stride, int n, float eps) {
+__global__ void __launch_bounds__(256) renorm_rows_kernel(T* x, int64_t rows, int64_t stride, float eps) {
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= rows) return;
-  T* p = x + row * stride;
+  T* p = x + row * stride + 16 * lane;
+  float v[16];
+  load8<T>(p, v);
+  load8<T>(p + 8, v + 8);
   float ss = 0.f;
-  for (int e = lane; e < n; e += 64) {
-    const float v = (float)p[e];
-    ss += v * v;
-  }
+#pragma unroll
+  for (int e = 0; e < 16; ++e) ss += v[e] * v[e];
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
   const float inv = 1.f / (sqrtf(ss) + eps);
-  for (int e = lane; e < n; e += 64) p[e] = (T)((float)p[e] * inv);
+#pragma unroll
+  for (int e = 0; e < 16; ++e) v[e] *= inv;
+  store_row8<T>(p, v);
+  store_row8<T>(p + 8, v + 8);
 }
 }  // namespace kdn
 
@@ -349,9 +354,9 @@ extern "C" int kdn_fwht_lift_factored(const void* x, int64_t rows, int64_t x_row
   const dim3 grid((unsigned)((rows + 3) / 4));
   if (out_dtype == KDN_DTYPE_BF16)
     hipLaunchKernelGGL(renorm_rows_kernel<__bf16>, grid, dim3(256), 0, as_stream(stream), static_cast<__bf16*>(out),
-                       rows, out_row_stride, 1024, 1e-7f);
+                       rows, out_row_stride, 1e-7f);
   else
     hipLaunchKernelGGL(renorm_rows_kernel<float>, grid, dim3(256), 0, as_stream(stream), static_cast<float*>(out), rows,
-                       out_row_stride, 1024, 1e-7f);
+                       out_row_stride, 1e-7f);
   return launch_status();
 }

@@ -877,22 +877,6 @@ __global__ void __launch_bounds__(256) state_kernel(ScanParams p) {
 // chunk-start S^T fragments are staged in LDS, NG value tiles per pass, and read by all four waves.
 // Each wave assembles its 16 x d_v block of Y in a wave-private LDS tile and writes whole rows with
 // 16-byte stores.
-template <typename T>
-__device__ __forceinline__ void store_row8(T* p, const float* v);
-template <>
-__device__ __forceinline__ void store_row8<__bf16>(__bf16* p, const float* v) {
-  bf16x8 r;
-#pragma unroll
-  for (int s = 0; s < 8; ++s) r[s] = (__bf16)v[s];
-  *reinterpret_cast<bf16x8*>(p) = r;
-}
-template <>
-__device__ __forceinline__ void store_row8<float>(float* p, const float* v) {
-  f32x4 a = {v[0], v[1], v[2], v[3]}, c = {v[4], v[5], v[6], v[7]};
-  reinterpret_cast<f32x4*>(p)[0] = a;
-  reinterpret_cast<f32x4*>(p)[1] = c;
-}
-
 template <class P, typename OutT, int D, int DV>
 __global__ void __launch_bounds__(256) output_kernel(ScanParams p) {
   using L = WsLayout<P, D, DV>;

@@ -133,12 +133,12 @@ def test_lift_fwht_omega_argument_errors_need_no_device(lib):
 
 def test_general_width_requests_need_no_device(lib):
     # D = 1024 (the factored d_k = 128 path): pre-lifted features only, d_v 64 or 128, the delta rule; one
-    # fp32 record per (batch, head, chunk): 417,920 floats at d_v = 128, 344,192 at d_v = 64
+    # fp32 record per (batch, head, chunk): 286,848 floats at d_v = 128, 213,120 at d_v = 64
     a = _args(T=256, H=2, d_k=1024, D=1024, d_v=128, feature_mode=1)
-    assert lib.kdn_scan_workspace_bytes(ctypes.byref(a)) == 2 * 4 * 417920 * 4
-    assert lib.kdn_scan_workspace_bytes_pipelined(ctypes.byref(a)) == 2 * 4 * 417920 * 4
+    assert lib.kdn_scan_workspace_bytes(ctypes.byref(a)) == 2 * 4 * 286848 * 4
+    assert lib.kdn_scan_workspace_bytes_pipelined(ctypes.byref(a)) == 2 * 4 * 286848 * 4
     assert lib.kdn_scan_workspace_bytes(ctypes.byref(_args(T=256, d_k=1024, D=1024, d_v=64, feature_mode=1))) \
-        == 16 * 4 * 344192 * 4
+        == 16 * 4 * 213120 * 4
     assert lib.kdn_scan_workspace_bytes(ctypes.byref(_args(d_k=64, D=1024, feature_mode=0))) == 0
     assert lib.kdn_scan_workspace_bytes(ctypes.byref(_args(d_k=1024, D=1024, d_v=32, feature_mode=1))) == 0
     assert lib.kdn_scan_workspace_bytes(ctypes.byref(_args(d_k=1024, D=1024, feature_mode=1, rule=1))) == 0
