@@ -103,3 +103,16 @@ def test_factored_scan_continues_across_calls(fproj):
     torch.cuda.synchronize()
     assert rel(torch.cat([Y1, Y2], 1).cpu().numpy(), Y.cpu().numpy()) < 1e-5
     assert rel(S2.cpu().numpy(), S.cpu().numpy()) < 1e-5
+
+
+def test_factored_scan_single_partial_chunk(fproj, oprojs):
+    g = torch.Generator().manual_seed(9)
+    q, k = torch.randn(1, 5, 128, generator=g), torch.randn(1, 5, 128, generator=g)
+    v = torch.randn(1, 5, 128, generator=g)
+    beta = torch.sigmoid(torch.randn(1, 5, generator=g))
+    dec = 0.9 + 0.1 * torch.rand(1, 5, generator=g)
+    Y, S = factored_chunked_deltanet_forward(q.to(DEV), k.to(DEV), v.to(DEV), beta.to(DEV), dec.to(DEV), fproj)
+    torch.cuda.synchronize()
+    Yr, Sr = oracle_scan(q, k, v, beta, dec, oprojs)
+    assert rel(Y.cpu().numpy(), Yr) < 1e-4
+    assert rel(S.cpu().numpy(), Sr) < 1e-4
