@@ -111,6 +111,13 @@ __device__ __forceinline__ float xor_shuffle(float v) {
 }
 
 // Sum over the lanes that share (lane & 15): lanes l, l^16, l^32, l^48.
+// The value of lane 4 (l >> 2) + P of each lane's quad (DPP quad_perm [P, P, P, P]).
+template <int P>
+__device__ __forceinline__ float quad_bcast(float v) {
+  static_assert(P >= 0 && P < 4, "quad_bcast: P must be a lane of the quad");
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), P * 0x55, 0xF, 0xF, true));
+}
+
 __device__ __forceinline__ float sum_over_lane_groups(float v) {
   v += xor_shuffle<16>(v);
   v += xor_shuffle<32>(v);

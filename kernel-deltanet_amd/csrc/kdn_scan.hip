@@ -321,7 +321,7 @@ __global__ void __launch_bounds__(256) prep_kernel(ScanParams p) {
 
   bf16x8* s_omega = reinterpret_cast<bf16x8*>(smem);
   frag* s_phik = reinterpret_cast<frag*>(smem + OMEGA_BYTES);
-  float* s_A = reinterpret_cast<float*>(smem + OMEGA_BYTES);          // [t][p][k'] = A[t][4k'+p]
+  float* s_A = reinterpret_cast<float*>(smem + OMEGA_BYTES);          // [j][p][s] = A[4s+p][j]
   float* s_T = s_A + 64 * 64;                                          // [t][68]
   InT* s_V = reinterpret_cast<InT*>(s_T + 64 * 68);                    // [t][DV]
 
@@ -443,7 +443,7 @@ __global__ void __launch_bounds__(256) prep_kernel(ScanParams p) {
           const int j = 16 * m + 4 * (lane >> 4) + i;
           const float gj = s_g[j], skj = s_sk[j];
           const float a = (j < t) ? bt * __expf(fminf(gt - gj, 0.f)) * gkk[m][i] * skt * skj : 0.f;
-          s_A[(t * 4 + i) * 16 + 4 * m + (lane >> 4)] = a;  // j = 4(4m + (l>>4)) + i
+          s_A[(j * 4 + (t & 3)) * 16 + (t >> 2)] = a;
           pt[m][i] = (j < t) ? __expf(fminf(gtm1 - gj, 0.f)) * gqk[m][i] * sqt * skj : 0.f;
         }
       }
@@ -467,27 +467,45 @@ __global__ void __launch_bounds__(256) prep_kernel(ScanParams p) {
     }
     __syncthreads();
 
-    // ---- T = (I + A)^{-1}: column col = 16w + (l>>2) per lane quad; lane p = l&3 keeps rows 4k'+p.
-    // Forward substitution; each row's dot product is summed as four independent partial sums.
+    // ---- T = (I + A)^{-1}: column col = 16w + (l>>2) per lane quad; lane p = l&3 keeps rows 4s+p.
+    // Column-oriented forward substitution: once row i of the column is final (lane i & 3, slot i >> 2)
+    // it is broadcast over the quad and every later row takes its term A[r][i] T[i][col] at once, so
+    // the sequential chain per row is one broadcast and one FMA.  acc[s] = -(partial T[4s+p][col]);
+    // the entries of A on and above the diagonal are zero, so updating every slot from i >> 2 on leaves
+    // rows r <= i unchanged.
     {
       const int col = 16 * w + (lane >> 2), pq = lane & 3;
-      float Tr[16];
+      float acc[16];
 #pragma unroll
-      for (int k = 0; k < 16; ++k) Tr[k] = 0.f;
+      for (int s2 = 0; s2 < 16; ++s2) acc[s2] = (4 * s2 + pq == col) ? -1.f : 0.f;
+      // Column i of A for the lane's rows, in 16-byte pieces from piece i >> 4 on (the earlier rows of
+      // the column are zero), loaded AHEAD steps before it is used so that no step waits for LDS.
+      constexpr int AHEAD = 3;
+      f32x4 acol[AHEAD][4];
+      auto load_col = [&](int i, f32x4 (&dst)[4]) {
+        const f32x4* src = reinterpret_cast<const f32x4*>(s_A + (i * 4 + pq) * 16);
 #pragma unroll
-      for (int i = 0; i < 64; ++i) {
-        const float* arow = s_A + (i * 4 + pq) * 16;
-        float part4[4] = {0.f, 0.f, 0.f, 0.f};
+        for (int q = 0; q < 4; ++q)
+          if (q >= (i >> 4)) dst[q] = src[q];
+      };
 #pragma unroll
-        for (int k = 0; k < (i + 3) / 4; ++k) part4[k & 3] += arow[k] * Tr[k];
-        float part = (part4[0] + part4[1]) + (part4[2] + part4[3]);
-        part += xor_shuffle<1>(part);
-        part += xor_shuffle<2>(part);
-        const float val = (i == col ? 1.f : 0.f) - part;
-        if (pq == (i & 3)) Tr[i >> 2] = val;
+      for (int i = 0; i < AHEAD; ++i) load_col(i, acol[i]);
+#pragma unroll
+      for (int i = 0; i < 63; ++i) {
+        float bc;  // -T[i][col]
+        switch (i & 3) {
+          case 0: bc = quad_bcast<0>(acc[i >> 2]); break;
+          case 1: bc = quad_bcast<1>(acc[i >> 2]); break;
+          case 2: bc = quad_bcast<2>(acc[i >> 2]); break;
+          default: bc = quad_bcast<3>(acc[i >> 2]); break;
+        }
+        const f32x4 (&a)[4] = acol[i % AHEAD];
+#pragma unroll
+        for (int s2 = i >> 2; s2 < 16; ++s2) acc[s2] = fmaf(-a[s2 >> 2][s2 & 3], bc, acc[s2]);
+        if (i + AHEAD < 63) load_col(i + AHEAD, acol[i % AHEAD]);
       }
 #pragma unroll
-      for (int k = 0; k < 16; ++k) s_T[(4 * k + pq) * 68 + col] = Tr[k];
+      for (int s2 = 0; s2 < 16; ++s2) s_T[(4 * s2 + pq) * 68 + col] = -acc[s2];
     }
     __syncthreads();
 

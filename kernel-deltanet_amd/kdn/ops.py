@@ -559,20 +559,9 @@ def forward_only(what: str, outputs, inputs):
 # ------------------------------------------------------------------------------------------------ serving
 
 
-def ragged_step(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, beta: torch.Tensor, decay: Optional[torch.Tensor],
-                cu_seqlens, slots: torch.Tensor, states: torch.Tensor, omega_bf16: torch.Tensor, phase: torch.Tensor,
-                inv_tau: float, normalize: bool = False, rule: int = RULE_DELTA, y: Optional[torch.Tensor] = None,
-                out_dtype: Optional[torch.dtype] = None, workspace: Optional[torch.Tensor] = None,
-                pipelined: bool = True, cu_seqlens_device: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """One ragged mixed prefill + decode step (kdn_ragged_step).
-
-    q, k (tokens, H, d_k) and v (tokens, H, d_v) share a dtype; beta, decay (tokens, H) float32 (decay may
-    be None); cu_seqlens: num_seqs + 1 token offsets (host list/array or tensor); slots (num_seqs,) the
-    distinct state slots; states (slots_total, H, D, d_v) float32, any strides, updated in place.
-    A serving loop that keeps its batch metadata on the device passes slots as a device int32 tensor and
-    cu_seqlens_device (the same offsets, device int64); nothing is then copied to the device per call.
-    Returns y (tokens, H, d_v).
-    """
+def _ragged_args(q, k, v, beta, decay, cu_seqlens, slots, states, omega_bf16, phase, inv_tau, normalize, rule, y,
+                 out_dtype, cu_seqlens_device):
+    """Checks the arguments of a ragged step and fills kdn_ragged_args; returns (args, tensors it points to)."""
     for t, nm in ((q, "q"), (k, "k"), (v, "v"), (beta, "beta"), (states, "states")):
         require_device(t, f"ragged_step: {nm}")
     dev = q.device
@@ -620,6 +609,46 @@ def ragged_step(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, beta: torch.T
     a.omega_bf16, a.phase = om.data_ptr(), ph.data_ptr()
     a.states, a.state_stride = states.data_ptr(), N._i64x4(*states.stride())
     a.y, a.y_stride = y.data_ptr(), N._i64x2(*y.stride()[:2])
+    return a, (q, k, v, beta, decay, om, ph, states, y, cu_d, slots_d, cu_host)
+
+
+def ragged_workspace_bytes(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, beta: torch.Tensor,
+                           decay: Optional[torch.Tensor], cu_seqlens, slots: torch.Tensor, states: torch.Tensor,
+                           omega_bf16: torch.Tensor, phase: torch.Tensor, inv_tau: float, normalize: bool = False,
+                           rule: int = RULE_DELTA, y: Optional[torch.Tensor] = None,
+                           out_dtype: Optional[torch.dtype] = None,
+                           cu_seqlens_device: Optional[torch.Tensor] = None) -> int:
+    """Bytes of workspace that ragged_step needs for these arguments (kdn_ragged_workspace_bytes).  A serving
+    loop allocates it once for its largest step and passes it as ragged_step(workspace=...), so that no
+    call allocates device memory."""
+    a, _ = _ragged_args(q, k, v, beta, decay, cu_seqlens, slots, states, omega_bf16, phase, inv_tau, normalize, rule,
+                        y, out_dtype, cu_seqlens_device)
+    need = int(N.lib().kdn_ragged_workspace_bytes(ctypes.byref(a)))
+    if need == 0:
+        raise ValueError("ragged_step: unsupported shape (kdn_ragged_workspace_bytes returned 0)")
+    return need
+
+
+def ragged_step(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, beta: torch.Tensor, decay: Optional[torch.Tensor],
+                cu_seqlens, slots: torch.Tensor, states: torch.Tensor, omega_bf16: torch.Tensor, phase: torch.Tensor,
+                inv_tau: float, normalize: bool = False, rule: int = RULE_DELTA, y: Optional[torch.Tensor] = None,
+                out_dtype: Optional[torch.dtype] = None, workspace: Optional[torch.Tensor] = None,
+                pipelined: bool = True, cu_seqlens_device: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """One ragged mixed prefill + decode step (kdn_ragged_step).
+
+    q, k (tokens, H, d_k) and v (tokens, H, d_v) share a dtype; beta, decay (tokens, H) float32 (decay may
+    be None); cu_seqlens: num_seqs + 1 token offsets (host list/array or tensor); slots (num_seqs,) the
+    distinct state slots; states (slots_total, H, D, d_v) float32, any strides, updated in place.
+    A serving loop that keeps its batch metadata on the device passes slots as a device int32 tensor and
+    cu_seqlens_device (the same offsets, device int64); nothing is then copied to the device per call.
+    Without `workspace` each call allocates one (ragged_workspace_bytes; several GB for long prefills)
+    from torch's caching allocator; a loop passes one buffer instead.
+    Returns y (tokens, H, d_v).
+    """
+    a, keep = _ragged_args(q, k, v, beta, decay, cu_seqlens, slots, states, omega_bf16, phase, inv_tau, normalize,
+                           rule, y, out_dtype, cu_seqlens_device)
+    dev = q.device
+    y = keep[8]
     need = int(N.lib().kdn_ragged_workspace_bytes(ctypes.byref(a)))
     if need == 0:
         raise ValueError("ragged_step: unsupported shape (kdn_ragged_workspace_bytes returned 0)")
@@ -631,7 +660,7 @@ def ragged_step(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, beta: torch.T
         aux = None
         if pipelined:
             aux = aux_stream(dev)
-            for t in (q, k, v, beta, decay, om, ph, states, y, workspace, cu_d, slots_d):
+            for t in keep[:11] + (workspace,):
                 if t is not None:
                     t.record_stream(aux)
         N.check(N.lib().kdn_ragged_step(ctypes.byref(a), ctypes.c_void_p(st.cuda_stream),

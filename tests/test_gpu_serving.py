@@ -195,3 +195,22 @@ def test_pool_zeroes_and_forks_on_device(proj):
     torch.cuda.synchronize()
     changed = (pool.slab != before).reshape(6, 2, -1).any(-1)
     assert changed[b, 1] and int(changed.sum()) == 1
+
+
+def test_caller_workspace_reused_across_steps(proj):
+    # a serving loop sizes one workspace with ragged_workspace_bytes and passes it to every step: the same
+    # results, bit for bit, as steps that allocate their own
+    q, k, v, beta, lam, cu, slots, states = make_step(LENS, 2, 64, torch.bfloat16, 20, seed=5, decay=True)
+    dq, dk, dv, db, dl = (t.to(DEV) for t in (q, k, v, beta, lam))
+    om, ph = proj.device_omega(DEV), proj.device_phase(DEV)
+    need = ops.ragged_workspace_bytes(dq, dk, dv, db, dl, cu, slots, states.to(DEV), om, ph, proj.tau_star_inv)
+    ws = torch.empty(need, dtype=torch.uint8, device=DEV)
+    s_own, s_ws = states.to(DEV), states.to(DEV)
+    for _ in range(2):
+        y_own = ops.ragged_step(dq, dk, dv, db, dl, cu, slots, s_own, om, ph, proj.tau_star_inv)
+        y_ws = ops.ragged_step(dq, dk, dv, db, dl, cu, slots, s_ws, om, ph, proj.tau_star_inv, workspace=ws)
+        torch.cuda.synchronize()
+        assert torch.equal(y_own, y_ws)
+        assert torch.equal(s_own, s_ws)
+    with pytest.raises(ValueError):
+        ops.ragged_workspace_bytes(dq, dk, dv, db, dl, [0, 1], slots, s_ws, om, ph, proj.tau_star_inv)
