@@ -236,7 +236,15 @@ def bench_scan(args, dev):
     phases = {k: {"ms": ms_kernel[k], "launches": launches[k], "avg_launch_ms": ms_kernel[k] / launches[k],
                   "alg_flops": fl[k] * units, "tflops": fl[k] * units / ms_kernel[k] / 1e9}
               for k in ("prep", "state", "output")}
-    dom = max(phases, key=lambda p: phases[p]["ms"])
+    # The dominant kernel: with fewer state workgroups than CUs (one sequence per head, config 3) the
+    # state kernel is the sequential chain that prep and output run beside, so it bounds the step even
+    # when concurrency stretches the others' launches; otherwise the kernels compete for CUs and the one
+    # with the most launch time dominates.
+    n_cu = torch.cuda.get_device_properties(dev).multi_processor_count
+    if plan.pipelined and B * H * (dv // 16) < n_cu:
+        dom = "state"
+    else:
+        dom = max(phases, key=lambda p: phases[p]["ms"])
     achieved = phases[dom]["tflops"]
     pmc_path = args.pmc or os.path.join(REPO, "profiles", f"pmc_config{cfg}.txt")
     pmc = read_pmc(pmc_path) if (cfg == 3 and B == 1 and T == 65536 and H == 16 and dv == 64) or args.pmc else {}

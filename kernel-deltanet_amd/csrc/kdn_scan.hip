@@ -15,9 +15,9 @@
 //
 // Three kernels per segment of chunks, so that the only sequential kernel streams as few bytes per
 // chunk as possible (64 KB of K per chunk and head):
-//   prep   (one workgroup per chunk and head): lift q and k on MFMA, Gram matrices, the triangular
-//          inverse and every S-independent factor; writes K, Tp = T diag(beta e^g |phi_k|), P, U~ and
-//          per-token scale vectors to the workspace in MFMA-fragment order.
+//   prep   (one workgroup per chunk and head; kdn_prep.hip): lift q and k on MFMA, Gram matrices, the
+//          triangular inverse and every S-independent factor; writes K, Tp = T diag(beta e^g |phi_k|),
+//          P, U~ and per-token scale vectors to the workspace in MFMA-fragment order.
 //   state  (one workgroup per head and 16 value components, sequential over chunks): X_K = K S^T,
 //          E = U~ - Tp X_K and the state update; checkpoints each chunk's starting S^T and E.
 //   output (one workgroup per chunk and head): re-lifts q, Y = diag(qscale) Q S^T + P E.
@@ -27,537 +27,9 @@
 #include "kdn_frag.hpp"
 #include "kdn_internal.hpp"
 #include "kdn_io.hpp"
+#include "kdn_scan_common.hpp"
 
 namespace kdn {
-
-constexpr int CH = 64;  // tokens per chunk (internal; the WY form is exact for any chunk length)
-
-// Per (chunk, head) workspace record.  A segment of nseg chunks uses nseg + 1 records per head: the
-// last one is scratch for the state kernel's writes past the final chunk.
-template <class P, int D, int DV>
-struct WsLayout {
-  static constexpr size_t FB = P::frag_bytes;
-  static constexpr int NJ = D / 32;   // 32-deep blocks over features
-  static constexpr int NV = DV / 16;  // 16-wide value tiles
-  static constexpr size_t phiK = 0;                                 // [m 4][j NJ][lane] K row frags (cos)
-  static constexpr size_t Tp = phiK + (size_t)4 * NJ * 64 * FB;     // [m 4][jb 2][lane]  T diag(beta e^g s_k)
-  static constexpr size_t Pm = Tp + (size_t)4 * 2 * 64 * FB;        // [m 4][jb 2][lane]  P
-  static constexpr size_t U = Pm + (size_t)4 * 2 * 64 * FB;         // [m 4][n NV][lane] f32x4  U~
-  static constexpr size_t VEC = U + (size_t)4 * NV * 64 * 16;       // qscale[64] kscale[64] gammaC
-  static constexpr size_t Sfr = VEC + 1024;                         // [j NJ][n NV][lane] chunk-start S^T frags
-  static constexpr size_t Eck = Sfr + (size_t)NJ * NV * 64 * FB;    // [m 4][n NV][lane] f32x4  E
-  static constexpr size_t phiQ = Eck + (size_t)4 * NV * 64 * 16;    // [m 4][j NJ][lane] Q row frags (cos)
-  static constexpr size_t bytes = (phiQ + (size_t)4 * NJ * 64 * FB + 255) / 256 * 256;
-};
-
-struct ScanParams {
-  int64_t B, T, H;
-  const void* q; int64_t qs0, qs1, qs2;
-  const void* k; int64_t ks0, ks1, ks2;
-  const void* v; int64_t vs0, vs1, vs2;
-  const float* beta; int64_t bs0, bs1, bs2;
-  const float* decay; int64_t ds0, ds1, ds2;
-  const __bf16* omega; const float* phase;
-  float inv_tau; int normalize;
-  const float* state_in; int64_t is0, is1, is2, is3;
-  float* state_out; int64_t os0, os1, os2, os3;
-  void* y; int64_t ys0, ys1, ys2;
-  unsigned char* ws;
-  int64_t chunk0, nseg;  // first global chunk of the segment, chunks in the segment
-  int prep_run;          // chunks per prep workgroup (bf16)
-  // feature map: per-head Omega (hi [+ lo]) / phases / 1/tau, renormalisation, pre-lifted inputs
-  const __bf16* omega_lo; int64_t oms, phs;
-  const float* inv_tau_head;
-  int no_renorm, prelifted;
-  int linear;  // update rule without the erasure term: T = I, Tp = 0
-  // ragged batches: sequence b is token rows seq_lo[b] .. seq_hi[b] (stride 1 of each token tensor; for
-  // cu_seqlens, seq_hi = cu_seqlens + 1); its state is slot slots[b] (stride 0 of the state tensors)
-  const int64_t* seq_lo;
-  const int64_t* seq_hi;
-  const int* slots;
-};
-
-// Sequence b of the batch: element offsets of its first token in each token-indexed tensor, and its
-// length.  A uniform batch addresses b * stride0 and has T tokens per sequence; a ragged batch
-// addresses rows seq_lo[b] .. seq_hi[b] of one packed token dimension.
-struct Seq {
-  int64_t q, k, v, be, de, y, len;
-};
-__device__ __forceinline__ Seq seq_of(const ScanParams& p, int64_t b) {
-  Seq s;
-  if (p.seq_lo) {
-    const int64_t r0 = p.seq_lo[b];
-    s.q = r0 * p.qs1; s.k = r0 * p.ks1; s.v = r0 * p.vs1;
-    s.be = r0 * p.bs1; s.de = r0 * p.ds1; s.y = r0 * p.ys1;
-    s.len = p.seq_hi[b] - r0;
-  } else {
-    s.q = b * p.qs0; s.k = b * p.ks0; s.v = b * p.vs0;
-    s.be = b * p.bs0; s.de = b * p.ds0; s.y = b * p.ys0;
-    s.len = p.T;
-  }
-  return s;
-}
-// Chunks of the current segment that hold tokens of the sequence (0 once it has ended).
-__device__ __forceinline__ int64_t seg_chunks(const ScanParams& p, const Seq& s) {
-  const int64_t n = (s.len + CH - 1) / CH - p.chunk0;
-  return n <= 0 ? 0 : (n < p.nseg ? n : p.nseg);
-}
-
-// Feature modes of the prep kernel: Omega exact in bf16 (the structured projection), Omega as hi + lo
-// bf16 parts (general projections), or q / k already lifted (d_k = D).
-enum FeatureMode { FM_EXACT = 0, FM_HILO = 1, FM_PRELIFTED = 2 };
-
-template <class P>
-struct IsBF16 : std::integral_constant<bool, std::is_same<P, PrecBF16>::value> {};
-
-// ------------------------------------------------------------------------------------------------
-// Raw 16-byte pieces of one lane's part of an input row (8 elements per 32-deep block kb): 1 piece per
-// block for bf16, 2 for fp32.
-template <typename InT>
-struct RawRow {
-  static constexpr int R = (int)(8 * sizeof(InT) / 16);
-  u32x4 piece[2 * R];
-  __device__ __forceinline__ void load(const InT* row, bool valid, int lane) {
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int r = 0; r < R; ++r) {
-        u32x4 z = {0u, 0u, 0u, 0u};
-        piece[kb * R + r] = valid ? reinterpret_cast<const u32x4*>(row + 32 * kb + 8 * (lane >> 4))[r] : z;
-      }
-  }
-  __device__ __forceinline__ void to_f32(int kb, float* o) const {
-    if constexpr (R == 1) {
-      const bf16x8 v = __builtin_bit_cast(bf16x8, piece[kb]);
-#pragma unroll
-      for (int s = 0; s < 8; ++s) o[s] = (float)v[s];
-    } else {
-      const f32x4 a = __builtin_bit_cast(f32x4, piece[kb * 2]), c = __builtin_bit_cast(f32x4, piece[kb * 2 + 1]);
-      o[0] = a[0]; o[1] = a[1]; o[2] = a[2]; o[3] = a[3];
-      o[4] = c[0]; o[5] = c[1]; o[6] = c[2]; o[7] = c[3];
-    }
-  }
-};
-
-// Lift of one 16-row tile per wave, for NX inputs at once (each Omega fragment feeds NX MFMAs).
-// Projection in the transposed orientation Phi^T = Omega X^T: accumulator tile t holds, in lane l,
-// feature 16t + 4(l>>4) + i of row (l & 15), which is slot (t & 1) * 4 + i of X fragment t / 2.
-// The angle in revolutions is reduced with v_fract before v_cos (which takes revolutions), so any
-// finite angle stays inside the instruction's domain.
-// Output: unnormalised cos values as X fragments, and each row's sum of squares (all lanes).
-template <class P, typename InT, int D, bool OMEGA_LDS, int NX, bool LO = false>
-__device__ __forceinline__ void lift_tile(const RawRow<InT> (&raw)[NX], int normalize,
-                                          const bf16x8* s_omega, const __bf16* omega, const float* s_phrev,
-                                          float ang, int lane, typename P::frag (&out)[NX][D / 32],
-                                          float (&ss)[NX], const __bf16* omega_lo = nullptr) {
-  constexpr int NT = D / 16;
-  constexpr int NSPLIT = XFrag<InT>::NSPLIT;
-  float xv[NX][2][8];
-#pragma unroll
-  for (int x = 0; x < NX; ++x)
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) raw[x].to_f32(kb, xv[x][kb]);
-  if (normalize) {
-#pragma unroll
-    for (int x = 0; x < NX; ++x) {
-      float sq = 0.f;
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int s = 0; s < 8; ++s) sq += xv[x][kb][s] * xv[x][kb][s];
-      sq = sum_over_lane_groups(sq);
-      const float inv = 1.0f / fmaxf(sqrtf(sq), 1e-6f);
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int s = 0; s < 8; ++s) {
-          const float a = xv[x][kb][s] * inv;
-          xv[x][kb][s] = (NSPLIT == 1) ? (float)(__bf16)a : a;  // F.normalize output keeps x's dtype
-        }
-    }
-  }
-  bf16x8 xb[NX][2][NSPLIT];
-#pragma unroll
-  for (int x = 0; x < NX; ++x) {
-    split_frag<NSPLIT>(xv[x][0], xb[x][0]);
-    split_frag<NSPLIT>(xv[x][1], xb[x][1]);
-    ss[x] = 0.f;
-  }
-  // Feature tile t: acc[x] = x . Omega[16t .. 16t+16)^T.  Software-pipelined: the MFMAs of tile t+1 are
-  // issued in the scheduling region of the cosines of tile t.
-  auto project = [&](int t, f32x4 (&acc)[NX]) {
-#pragma unroll
-    for (int x = 0; x < NX; ++x) acc[x] = zero4();
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      bf16x8 a;
-      if constexpr (OMEGA_LDS) a = s_omega[(t * 2 + kb) * 64 + lane];
-      else a = *reinterpret_cast<const bf16x8*>(omega + (int64_t)(16 * t + (lane & 15)) * 64 + 32 * kb + 8 * (lane >> 4));
-#pragma unroll
-      for (int s = 0; s < NSPLIT; ++s)
-#pragma unroll
-        for (int x = 0; x < NX; ++x) acc[x] = PrecBF16::mma(acc[x], a, xb[x][kb][s]);
-      if constexpr (LO) {
-        const bf16x8 alo = *reinterpret_cast<const bf16x8*>(omega_lo + (int64_t)(16 * t + (lane & 15)) * 64 + 32 * kb + 8 * (lane >> 4));
-#pragma unroll
-        for (int s = 0; s < NSPLIT; ++s)
-#pragma unroll
-          for (int x = 0; x < NX; ++x) acc[x] = PrecBF16::mma(acc[x], alo, xb[x][kb][s]);
-      }
-    }
-  };
-  f32x4 acc[NX];
-  project(0, acc);
-#pragma unroll
-  for (int t = 0; t < NT; ++t) {
-    // one feature tile per scheduling region: hoisting the Omega reads of every tile to the top
-    // would hold them all in registers at once
-    __builtin_amdgcn_sched_barrier(0);
-    f32x4 next[NX];
-    if (t + 1 < NT) project(t + 1, next);
-    const f32x4 ph = *reinterpret_cast<const f32x4*>(&s_phrev[16 * t + 4 * (lane >> 4)]);
-#pragma unroll
-    for (int x = 0; x < NX; ++x)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float c = __builtin_amdgcn_cosf(__builtin_amdgcn_fractf(acc[x][i] * ang + ph[i]));
-        ss[x] += c * c;
-        P::set(out[x][t >> 1], (t & 1) * 4 + i, c);
-      }
-    if (t + 1 < NT) {
-#pragma unroll
-      for (int x = 0; x < NX; ++x) acc[x] = next[x];
-    }
-  }
-#pragma unroll
-  for (int x = 0; x < NX; ++x) ss[x] = sum_over_lane_groups(ss[x]);
-}
-
-// Omega as A fragments in LDS (lane l of fragment (t, kb): Omega[16t + (l&15)][32kb + 8(l>>4) .. +8])
-// and phase / (2 pi).
-template <int D, bool OMEGA_LDS>
-__device__ __forceinline__ void stage_omega(const __bf16* omega, const float* phase, bf16x8* s_omega, float* s_phrev) {
-  if constexpr (OMEGA_LDS) {
-    for (int idx = threadIdx.x; idx < (D / 16) * 2 * 64; idx += blockDim.x) {
-      const int l = idx & 63, tk = idx >> 6, t = tk >> 1, kb = tk & 1;
-      s_omega[idx] = *reinterpret_cast<const bf16x8*>(omega + (int64_t)(16 * t + (l & 15)) * 64 + 32 * kb + 8 * (l >> 4));
-    }
-  }
-  for (int f = threadIdx.x; f < D; f += blockDim.x) s_phrev[f] = phase[f] * 0.15915494309189535f;
-}
-
-// ------------------------------------------------------------------------------------------------
-// prep: grid (ceil(nseg / run), H, B), 256 threads.  A workgroup prepares `run` consecutive chunks
-// of one head: Omega and the phases are staged in LDS once, and the raw q / k / v / beta / decay of the
-// next chunk are loaded into registers while the current chunk is processed.  Wave w owns token rows
-// [16w, 16w+16) of a chunk.
-// Chunks per prep workgroup: chosen at launch for bf16 with the exact or given features
-// (ScanParams::prep_run); 1 for fp32, whose fragments (twice as wide) leave no registers for the
-// prefetch, and for the hi + lo projection, whose second operand stream does the same.
-template <class P, int FM>
-struct PrepRun : std::integral_constant<int, (IsBF16<P>::value && FM != FM_HILO) ? 0 : 1> {};
-
-// Raw inputs of one chunk for one thread of the prep workgroup: the q / k row pieces of the lane's row
-// and beta / decay of token `lane` (prefetched one chunk ahead), and the V pieces of the thread
-// (loaded at the start of the chunk; they are first needed after the Gram).
-template <typename InT, int DV>
-struct PrepInputs {
-  static constexpr int VPR = DV * (int)sizeof(InT) / 16;        // 16-byte pieces per V row
-  static constexpr int VPT = (64 * VPR + 255) / 256;             // pieces per thread
-  RawRow<InT> qk[2];
-  float be, la;
-  __device__ __forceinline__ void load_qk(const ScanParams& p, const Seq& sq, int64_t h, int64_t t0, int w, int lane) {
-    const int64_t trow = t0 + 16 * w + (lane & 15);
-    const bool rvalid = trow < sq.len;
-    qk[0].load((const InT*)p.q + sq.q + trow * p.qs1 + h * p.qs2, rvalid, lane);
-    qk[1].load((const InT*)p.k + sq.k + trow * p.ks1 + h * p.ks2, rvalid, lane);
-    const int64_t t = t0 + lane;
-    const bool valid = t < sq.len;
-    be = valid ? p.beta[sq.be + t * p.bs1 + h * p.bs2] : 0.f;
-    la = (valid && p.decay) ? p.decay[sq.de + t * p.ds1 + h * p.ds2] : 1.f;
-  }
-  __device__ __forceinline__ static void load_v(const ScanParams& p, const Seq& sq, int64_t h, int64_t t0, u32x4 (&v)[VPT]) {
-#pragma unroll
-    for (int i = 0; i < VPT; ++i) {
-      const int idx = (int)threadIdx.x + 256 * i;
-      const int r = idx / VPR, pc = idx % VPR;
-      const int64_t t = t0 + r;
-      u32x4 val = {0u, 0u, 0u, 0u};
-      if (idx < 64 * VPR && t < sq.len)
-        val = *reinterpret_cast<const u32x4*>((const InT*)p.v + sq.v + t * p.vs1 + h * p.vs2 + pc * (16 / (int)sizeof(InT)));
-      v[i] = val;
-    }
-  }
-};
-
-// Lifted features given as input (FM_PRELIFTED): X fragment j of the lane's row, features 32j + kappa(l, s)
-// (two runs of four: 32j + 4(l>>4) .. +3 and 32j + 16 + 4(l>>4) .. +3).
-template <class P, typename InT, int D>
-__device__ __forceinline__ void load_lifted(const InT* row, bool valid, int lane, typename P::frag (&out)[D / 32]) {
-#pragma unroll
-  for (int j = 0; j < D / 32; ++j) {
-#pragma unroll
-    for (int half = 0; half < 2; ++half) {
-      const InT* src = row + 32 * j + 16 * half + 4 * (lane >> 4);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) P::set(out[j], 4 * half + i, valid ? (float)src[i] : 0.f);
-    }
-  }
-}
-
-template <class P, typename InT, int D, int DV, int FM>
-__global__ void __launch_bounds__(256) prep_kernel(ScanParams p) {
-  using L = WsLayout<P, D, DV>;
-  using frag = typename P::frag;
-  using In = PrepInputs<InT, DV>;
-  constexpr int NT = D / 16, NJ = D / 32, NV = DV / 16;
-  constexpr bool OMEGA_LDS = IsBF16<P>::value && FM != FM_PRELIFTED;
-  constexpr size_t OMEGA_BYTES = OMEGA_LDS ? (size_t)NT * 2 * 64 * 16 : 0;
-  constexpr size_t PHIK_BYTES = (size_t)4 * NJ * 64 * sizeof(frag);
-  // After the Gram the K-fragment area is reused for A (16 KB), T (17 KB) and V.
-  static_assert(64 * 64 * 4 + 64 * 68 * 4 + 64 * DV * sizeof(InT) <= PHIK_BYTES, "LDS reuse does not fit");
-  __shared__ __attribute__((aligned(16))) unsigned char smem[OMEGA_BYTES + PHIK_BYTES];
-  __shared__ __attribute__((aligned(16))) float s_beta[64], s_g[64], s_sq[64], s_sk[64], s_phrev[D];
-
-  bf16x8* s_omega = reinterpret_cast<bf16x8*>(smem);
-  frag* s_phik = reinterpret_cast<frag*>(smem + OMEGA_BYTES);
-  float* s_A = reinterpret_cast<float*>(smem + OMEGA_BYTES);          // [j][p][s] = A[4s+p][j]
-  float* s_T = s_A + 64 * 64;                                          // [t][68]
-  InT* s_V = reinterpret_cast<InT*>(s_T + 64 * 68);                    // [t][DV]
-
-  const int lane = threadIdx.x & 63;
-  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int64_t h = blockIdx.y, b = blockIdx.z;
-  constexpr int RUN = PrepRun<P, FM>::value;  // 0: runtime run length with prefetch
-  const int run = RUN ? RUN : p.prep_run;
-  const int64_t cl0 = (int64_t)blockIdx.x * run;
-  const Seq sq = seq_of(p, b);
-  const int64_t nloc = seg_chunks(p, sq);
-  if (cl0 >= nloc) return;  // past the end of this sequence (ragged batches): nothing to prepare
-  const int64_t cl_end = (cl0 + run < nloc) ? cl0 + run : nloc;
-
-  const __bf16* omega_h = p.omega + h * p.oms;
-  const __bf16* omega_lo_h = (FM == FM_HILO) ? p.omega_lo + h * p.oms : nullptr;
-  const float ang = (p.inv_tau_head ? p.inv_tau_head[h] : p.inv_tau) * 0.15915494309189535f;
-  In in;
-  if constexpr (FM != FM_PRELIFTED) {
-    stage_omega<D, OMEGA_LDS>(omega_h, p.phase + h * p.phs, s_omega, s_phrev);
-    in.load_qk(p, sq, h, (p.chunk0 + cl0) * CH, w, lane);
-  } else {
-    // no lift: only beta / decay come through the prefetch
-    const int64_t t = (p.chunk0 + cl0) * CH + lane;
-    const bool valid = t < sq.len;
-    in.be = valid ? p.beta[sq.be + t * p.bs1 + h * p.bs2] : 0.f;
-    in.la = (valid && p.decay) ? p.decay[sq.de + t * p.ds1 + h * p.ds2] : 1.f;
-  }
-
-  auto process = [&](int64_t cl) {
-    const int64_t t0 = (p.chunk0 + cl) * CH;
-    unsigned char* ws = p.ws + ((b * p.H + h) * (p.nseg + 1) + cl) * L::bytes;
-    u32x4 vraw[In::VPT];
-    if constexpr (RUN != 1) In::load_v(p, sq, h, t0, vraw);  // early: first needed after the Gram
-    __syncthreads();  // Omega staged (first chunk); the previous chunk's LDS reads are done
-
-    // ---- beta and the in-chunk log-decay prefix (wave 0)
-    if (w == 0) {
-      float g = logf(fminf(fmaxf(in.la, 1e-5f), 1.f));
-#pragma unroll
-      for (int off = 1; off < 64; off <<= 1) {
-        const float o = __shfl_up(g, off);
-        if (lane >= off) g += o;
-      }
-      s_beta[lane] = in.be;
-      s_g[lane] = g;
-    }
-
-    // ---- lift q and k rows of this wave (or load the given features)
-    frag cqk[2][NJ];  // [0] = q, [1] = k; X fragments (m = w, j): row 16w + (l&15), feature 32j + kappa(l, s)
-    float ss[2] = {0.f, 0.f};
-    if constexpr (FM == FM_PRELIFTED) {
-      const int64_t trow = t0 + 16 * w + (lane & 15);
-      load_lifted<P, InT, D>((const InT*)p.q + sq.q + trow * p.qs1 + h * p.qs2, trow < sq.len, lane, cqk[0]);
-      load_lifted<P, InT, D>((const InT*)p.k + sq.k + trow * p.ks1 + h * p.ks2, trow < sq.len, lane, cqk[1]);
-      const int64_t tn = (p.chunk0 + ((cl + 1 < cl_end) ? cl + 1 : cl)) * CH + lane;
-      in.be = (tn < sq.len) ? p.beta[sq.be + tn * p.bs1 + h * p.bs2] : 0.f;
-      in.la = (tn < sq.len && p.decay) ? p.decay[sq.de + tn * p.ds1 + h * p.ds2] : 1.f;
-    } else {
-      lift_tile<P, InT, D, OMEGA_LDS, 2, FM == FM_HILO>(in.qk, p.normalize, s_omega, omega_h, s_phrev, ang, lane,
-                                                         cqk, ss, omega_lo_h);
-      // the next chunk's rows travel while this one is processed (clamped: the last chunk reloads itself)
-      if constexpr (RUN != 1) in.load_qk(p, sq, h, (p.chunk0 + ((cl + 1 < cl_end) ? cl + 1 : cl)) * CH, w, lane);
-    }
-    {
-      // per-row scale of the stored (unnormalised) features: 1 for given features, sqrt(2/D) without
-      // renormalisation, sqrt(2/D) / (||sqrt(2/D) c|| + 1e-8) with it
-      const float amp = sqrtf(2.0f / (float)D);
-      if (lane < 16) {
-        float sq_, sk_;
-        if constexpr (FM == FM_PRELIFTED) {
-          sq_ = 1.f; sk_ = 1.f;
-        } else if (p.no_renorm) {
-          sq_ = amp; sk_ = amp;
-        } else {
-          sq_ = amp / (amp * sqrtf(ss[0]) + 1e-8f);
-          sk_ = amp / (amp * sqrtf(ss[1]) + 1e-8f);
-        }
-        s_sq[16 * w + lane] = sq_;
-        s_sk[16 * w + lane] = sk_;
-      }
-    }
-#pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-      // The records are read back by the state and output kernels a segment or more later, long after
-      // they could still sit in L2: streaming stores keep them from evicting the state kernel's lines.
-      store_frag_nt<P>(ws + L::phiK + (size_t)(w * NJ + j) * 64 * L::FB, lane, cqk[1][j]);
-      store_frag_nt<P>(ws + L::phiQ + (size_t)(w * NJ + j) * 64 * L::FB, lane, cqk[0][j]);
-      s_phik[(w * NJ + j) * 64 + lane] = cqk[1][j];
-    }
-    __syncthreads();
-
-    // ---- Gram tiles (m, n = w):  Gkk[m][w] = K_m K_w^T,  GqkT[m][w] = K_m Q_w^T  (unnormalised)
-    f32x4 gkk[4], gqk[4];
-#pragma unroll
-    for (int m = 0; m < 4; ++m) { gkk[m] = zero4(); gqk[m] = zero4(); }
-#pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-#pragma unroll
-      for (int m = 0; m < 4; ++m) {
-        const frag a = s_phik[(m * NJ + j) * 64 + lane];
-        gkk[m] = P::mma(gkk[m], a, cqk[1][j]);
-        gqk[m] = P::mma(gqk[m], a, cqk[0][j]);
-      }
-    }
-    __syncthreads();  // K fragments in LDS are dead from here on
-
-    // ---- A (for the inverse), P fragments, V staging, scale vectors
-    {
-      const int t = 16 * w + (lane & 15);
-      // the linear rule has no erasure coupling: A = 0, so T = I below
-      const float bt = p.linear ? 0.f : s_beta[t], gt = s_g[t], gtm1 = t > 0 ? s_g[t - 1] : 0.f;
-      const float skt = s_sk[t], sqt = s_sq[t];
-      f32x4 pt[4];
-#pragma unroll
-      for (int m = 0; m < 4; ++m) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int j = 16 * m + 4 * (lane >> 4) + i;
-          const float gj = s_g[j], skj = s_sk[j];
-          const float a = (j < t) ? bt * __expf(fminf(gt - gj, 0.f)) * gkk[m][i] * skt * skj : 0.f;
-          s_A[(j * 4 + (t & 3)) * 16 + (t >> 2)] = a;
-          pt[m][i] = (j < t) ? __expf(fminf(gtm1 - gj, 0.f)) * gqk[m][i] * sqt * skj : 0.f;
-        }
-      }
-#pragma unroll
-      for (int jb = 0; jb < 2; ++jb)
-        store_frag_nt<P>(ws + L::Pm + (size_t)(w * 2 + jb) * 64 * L::FB, lane, P::from_f32(pair_to8(pt[2 * jb], pt[2 * jb + 1])));
-    }
-    if constexpr (RUN == 1) In::load_v(p, sq, h, t0, vraw);
-#pragma unroll
-    for (int i = 0; i < In::VPT; ++i) {
-      const int idx = (int)threadIdx.x + 256 * i;
-      if (idx < 64 * In::VPR) *reinterpret_cast<u32x4*>(s_V + (idx / In::VPR) * DV + (idx % In::VPR) * (16 / (int)sizeof(InT))) = vraw[i];
-    }
-    if (w == 1) {
-      float* vec = reinterpret_cast<float*>(ws + L::VEC);
-      const float g63 = s_g[63];
-      const float gtm1 = lane > 0 ? s_g[lane - 1] : 0.f;
-      vec[lane] = __expf(fminf(gtm1, 0.f)) * s_sq[lane];                 // e^{g_{t-1}} * |phi_q| scale
-      vec[64 + lane] = __expf(fminf(g63 - s_g[lane], 0.f)) * s_sk[lane]; // e^{g_63 - g_t} * |phi_k| scale
-      if (lane == 0) vec[128] = __expf(fminf(g63, 0.f));
-    }
-    __syncthreads();
-
-    // ---- T = (I + A)^{-1}: column col = 16w + (l>>2) per lane quad; lane p = l&3 keeps rows 4s+p.
-    // Column-oriented forward substitution: once row i of the column is final (lane i & 3, slot i >> 2)
-    // it is broadcast over the quad and every later row takes its term A[r][i] T[i][col] at once, so
-    // the sequential chain per row is one broadcast and one FMA.  acc[s] = -(partial T[4s+p][col]);
-    // the entries of A on and above the diagonal are zero, so updating every slot from i >> 2 on leaves
-    // rows r <= i unchanged.
-    {
-      const int col = 16 * w + (lane >> 2), pq = lane & 3;
-      float acc[16];
-#pragma unroll
-      for (int s2 = 0; s2 < 16; ++s2) acc[s2] = (4 * s2 + pq == col) ? -1.f : 0.f;
-      // Column i of A for the lane's rows, in 16-byte pieces from piece i >> 4 on (the earlier rows of
-      // the column are zero), loaded AHEAD steps before it is used so that no step waits for LDS.
-      constexpr int AHEAD = 3;
-      f32x4 acol[AHEAD][4];
-      auto load_col = [&](int i, f32x4 (&dst)[4]) {
-        const f32x4* src = reinterpret_cast<const f32x4*>(s_A + (i * 4 + pq) * 16);
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-          if (q >= (i >> 4)) dst[q] = src[q];
-      };
-#pragma unroll
-      for (int i = 0; i < AHEAD; ++i) load_col(i, acol[i]);
-#pragma unroll
-      for (int i = 0; i < 63; ++i) {
-        float bc;  // -T[i][col]
-        switch (i & 3) {
-          case 0: bc = quad_bcast<0>(acc[i >> 2]); break;
-          case 1: bc = quad_bcast<1>(acc[i >> 2]); break;
-          case 2: bc = quad_bcast<2>(acc[i >> 2]); break;
-          default: bc = quad_bcast<3>(acc[i >> 2]); break;
-        }
-        const f32x4 (&a)[4] = acol[i % AHEAD];
-#pragma unroll
-        for (int s2 = i >> 2; s2 < 16; ++s2) acc[s2] = fmaf(-a[s2 >> 2][s2 & 3], bc, acc[s2]);
-        if (i + AHEAD < 63) load_col(i + AHEAD, acol[i % AHEAD]);
-      }
-#pragma unroll
-      for (int s2 = 0; s2 < 16; ++s2) s_T[(4 * s2 + pq) * 68 + col] = -acc[s2];
-    }
-    __syncthreads();
-
-    // ---- W~ factor T diag(beta e^g |phi_k|) fragments, and U~ = T diag(beta) V   (wave w: rows m = w)
-    {
-      const int t = 16 * w + (lane & 15);
-      f32x8 tb[2];
-#pragma unroll
-      for (int jb = 0; jb < 2; ++jb) {
-        f32x8 tw;
-#pragma unroll
-        for (int s = 0; s < 8; ++s) {
-          const int j = 32 * jb + kappa(lane, s);
-          const float tv = s_T[t * 68 + j];
-          tw[s] = p.linear ? 0.f : tv * s_beta[j] * __expf(s_g[j]) * s_sk[j];  // linear: E = U~
-          tb[jb][s] = tv * s_beta[j];
-        }
-        store_frag_nt<P>(ws + L::Tp + (size_t)(w * 2 + jb) * 64 * L::FB, lane, P::from_f32(tw));
-      }
-#pragma unroll
-      for (int n = 0; n < NV; ++n) {
-        f32x4 acc = zero4();
-#pragma unroll
-        for (int jb = 0; jb < 2; ++jb) {
-          f32x8 vv;
-#pragma unroll
-          for (int s = 0; s < 8; ++s) vv[s] = (float)s_V[(32 * jb + kappa(lane, s)) * DV + 16 * n + (lane & 15)];
-          if constexpr (IsBF16<P>::value) {
-            // hi + lo split of T diag(beta): V is exact in bf16, so U~ keeps ~16 bits.
-            bf16x8 hi, lo, vb;
-#pragma unroll
-            for (int s = 0; s < 8; ++s) {
-              hi[s] = (__bf16)tb[jb][s];
-              lo[s] = (__bf16)(tb[jb][s] - (float)hi[s]);
-              vb[s] = (__bf16)vv[s];
-            }
-            acc = PrecBF16::mma(acc, hi, vb);
-            acc = PrecBF16::mma(acc, lo, vb);
-          } else {
-            acc = P::mma(acc, P::from_f32(tb[jb]), P::from_f32(vv));
-          }
-        }
-        __builtin_nontemporal_store(acc, reinterpret_cast<f32x4*>(ws + L::U + ((size_t)(w * NV + n) * 64 + lane) * 16));
-      }
-    }
-  };
-  if constexpr (RUN == 1) {
-    process(cl0);
-  } else {
-    for (int64_t cl = cl0; cl < cl_end; ++cl) process(cl);
-  }
-}
 
 // ------------------------------------------------------------------------------------------------
 // state: one workgroup of 4 waves per (head, 16 value components = 16 state rows), sequential over the
@@ -1065,14 +537,7 @@ template <class P, typename InT, typename OutT, int D, int DV>
 static int launch_phase(const ScanParams& p, int phase, hipStream_t st) {
   const dim3 chunk_grid((unsigned)p.nseg, (unsigned)p.H, (unsigned)p.B);
   if (phase == PHASE_PREP) {
-    const int fm = p.prelifted ? FM_PRELIFTED : (p.omega_lo ? FM_HILO : FM_EXACT);
-    const int run_t = fm == FM_PRELIFTED ? PrepRun<P, FM_PRELIFTED>::value
-                    : fm == FM_HILO ? PrepRun<P, FM_HILO>::value : PrepRun<P, FM_EXACT>::value;
-    const int run = run_t ? run_t : p.prep_run;
-    const dim3 prep_grid((unsigned)((p.nseg + run - 1) / run), (unsigned)p.H, (unsigned)p.B);
-    if (fm == FM_PRELIFTED) hipLaunchKernelGGL((prep_kernel<P, InT, D, DV, FM_PRELIFTED>), prep_grid, dim3(256), 0, st, p);
-    else if (fm == FM_HILO) hipLaunchKernelGGL((prep_kernel<P, InT, D, DV, FM_HILO>), prep_grid, dim3(256), 0, st, p);
-    else hipLaunchKernelGGL((prep_kernel<P, InT, D, DV, FM_EXACT>), prep_grid, dim3(256), 0, st, p);
+    return launch_prep<P, InT, D, DV>(p, st);
   } else if (phase == PHASE_STATE) {
     // The state workgroups are the sequential critical path: reserve enough LDS that no prep or output
     // workgroup can share their CU (a CU has 160 KB; the bf16 state kernel uses 88 KB statically).

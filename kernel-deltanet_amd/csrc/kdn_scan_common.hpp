@@ -1,0 +1,96 @@
+// Definitions shared by the prep kernel (kdn_prep.hip) and the state / output kernels and the launch
+// code (kdn_scan.hip) of the D = 512 prefill scan: the per-chunk workspace record, the kernel parameter
+// block and ragged-sequence addressing.
+#pragma once
+#include <type_traits>
+#include "kdn_frag.hpp"
+#include "kdn_internal.hpp"
+
+namespace kdn {
+
+constexpr int CH = 64;  // tokens per chunk (internal; the WY form is exact for any chunk length)
+
+// Per (chunk, head) workspace record.  A segment of nseg chunks uses nseg + 1 records per head: the
+// last one is scratch for the state kernel's writes past the final chunk.
+template <class P, int D, int DV>
+struct WsLayout {
+  static constexpr size_t FB = P::frag_bytes;
+  static constexpr int NJ = D / 32;   // 32-deep blocks over features
+  static constexpr int NV = DV / 16;  // 16-wide value tiles
+  static constexpr size_t phiK = 0;                                 // [m 4][j NJ][lane] K row frags (cos)
+  static constexpr size_t Tp = phiK + (size_t)4 * NJ * 64 * FB;     // [m 4][jb 2][lane]  T diag(beta e^g s_k)
+  static constexpr size_t Pm = Tp + (size_t)4 * 2 * 64 * FB;        // [m 4][jb 2][lane]  P
+  static constexpr size_t U = Pm + (size_t)4 * 2 * 64 * FB;         // [m 4][n NV][lane] f32x4  U~
+  static constexpr size_t VEC = U + (size_t)4 * NV * 64 * 16;       // qscale[64] kscale[64] gammaC
+  static constexpr size_t Sfr = VEC + 1024;                         // [j NJ][n NV][lane] chunk-start S^T frags
+  static constexpr size_t Eck = Sfr + (size_t)NJ * NV * 64 * FB;    // [m 4][n NV][lane] f32x4  E
+  static constexpr size_t phiQ = Eck + (size_t)4 * NV * 64 * 16;    // [m 4][j NJ][lane] Q row frags (cos)
+  static constexpr size_t bytes = (phiQ + (size_t)4 * NJ * 64 * FB + 255) / 256 * 256;
+};
+
+struct ScanParams {
+  int64_t B, T, H;
+  const void* q; int64_t qs0, qs1, qs2;
+  const void* k; int64_t ks0, ks1, ks2;
+  const void* v; int64_t vs0, vs1, vs2;
+  const float* beta; int64_t bs0, bs1, bs2;
+  const float* decay; int64_t ds0, ds1, ds2;
+  const __bf16* omega; const float* phase;
+  float inv_tau; int normalize;
+  const float* state_in; int64_t is0, is1, is2, is3;
+  float* state_out; int64_t os0, os1, os2, os3;
+  void* y; int64_t ys0, ys1, ys2;
+  unsigned char* ws;
+  int64_t chunk0, nseg;  // first global chunk of the segment, chunks in the segment
+  int prep_run;          // chunks per prep workgroup (bf16)
+  // feature map: per-head Omega (hi [+ lo]) / phases / 1/tau, renormalisation, pre-lifted inputs
+  const __bf16* omega_lo; int64_t oms, phs;
+  const float* inv_tau_head;
+  int no_renorm, prelifted;
+  int linear;  // update rule without the erasure term: T = I, Tp = 0
+  // ragged batches: sequence b is token rows seq_lo[b] .. seq_hi[b] (stride 1 of each token tensor; for
+  // cu_seqlens, seq_hi = cu_seqlens + 1); its state is slot slots[b] (stride 0 of the state tensors)
+  const int64_t* seq_lo;
+  const int64_t* seq_hi;
+  const int* slots;
+};
+
+// Sequence b of the batch: element offsets of its first token in each token-indexed tensor, and its
+// length.  A uniform batch addresses b * stride0 and has T tokens per sequence; a ragged batch
+// addresses rows seq_lo[b] .. seq_hi[b] of one packed token dimension.
+struct Seq {
+  int64_t q, k, v, be, de, y, len;
+};
+__device__ __forceinline__ Seq seq_of(const ScanParams& p, int64_t b) {
+  Seq s;
+  if (p.seq_lo) {
+    const int64_t r0 = p.seq_lo[b];
+    s.q = r0 * p.qs1; s.k = r0 * p.ks1; s.v = r0 * p.vs1;
+    s.be = r0 * p.bs1; s.de = r0 * p.ds1; s.y = r0 * p.ys1;
+    s.len = p.seq_hi[b] - r0;
+  } else {
+    s.q = b * p.qs0; s.k = b * p.ks0; s.v = b * p.vs0;
+    s.be = b * p.bs0; s.de = b * p.ds0; s.y = b * p.ys0;
+    s.len = p.T;
+  }
+  return s;
+}
+// Chunks of the current segment that hold tokens of the sequence (0 once it has ended).
+__device__ __forceinline__ int64_t seg_chunks(const ScanParams& p, const Seq& s) {
+  const int64_t n = (s.len + CH - 1) / CH - p.chunk0;
+  return n <= 0 ? 0 : (n < p.nseg ? n : p.nseg);
+}
+
+// Feature modes of the prep kernel: Omega exact in bf16 (the structured projection), Omega as hi + lo
+// bf16 parts (general projections), or q / k already lifted (d_k = D).
+enum FeatureMode { FM_EXACT = 0, FM_HILO = 1, FM_PRELIFTED = 2 };
+
+template <class P>
+struct IsBF16 : std::integral_constant<bool, std::is_same<P, PrecBF16>::value> {};
+
+// Launches the prep kernel of one segment (kdn_prep.hip; compiled on its own so that its MFMA results
+// can be kept in VGPRs: it post-processes nearly all of them on the VALU).
+template <class P, typename InT, int D, int DV>
+int launch_prep(const ScanParams& p, hipStream_t st);
+
+}  // namespace kdn

@@ -14,13 +14,18 @@ from concurrent.futures import ThreadPoolExecutor
 _HERE = os.path.dirname(os.path.abspath(__file__))
 PKG_ROOT = os.path.dirname(_HERE)
 CSRC = os.path.join(PKG_ROOT, "csrc")
-SOURCES = ["kdn_api.hip", "kdn_lift.hip", "kdn_scan.hip", "kdn_serve.hip", "kdn_pool.hip", "kdn_bwd.hip",
-           "kdn_general.hip"]
+SOURCES = ["kdn_api.hip", "kdn_lift.hip", "kdn_prep.hip", "kdn_scan.hip", "kdn_serve.hip", "kdn_pool.hip",
+           "kdn_bwd.hip", "kdn_general.hip"]
 OUT = os.path.join(_HERE, "libkdn.so")
 OBJDIR = os.path.join(_HERE, "_build")
 ARCH = "gfx950"
 HIP_FLAGS = [f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
              "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+# Per-source extra flags.  -amdgpu-mfma-vgpr-form puts MFMA results in VGPRs rather than AGPRs, so that
+# VALU work on them needs no v_accvgpr_read copies: faster for the prep and backward kernels, which
+# post-process nearly every MFMA result (measured); slower for the state kernel, so not global.
+SOURCE_FLAGS = {"kdn_prep.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+                "kdn_bwd.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 
 
 def hipcc() -> str:
@@ -43,7 +48,8 @@ def build_native(verbose: bool = False) -> str:
     """Compile every source into kdn/libkdn.so; returns the library path.  Always recompiles."""
     os.makedirs(OBJDIR, exist_ok=True)
     objs = [os.path.join(OBJDIR, os.path.splitext(s)[0] + ".o") for s in SOURCES]
-    cmds = [[hipcc()] + HIP_FLAGS + ["-c", "-o", o, os.path.join(CSRC, s)] for s, o in zip(SOURCES, objs)]
+    cmds = [[hipcc()] + HIP_FLAGS + SOURCE_FLAGS.get(s, []) + ["-c", "-o", o, os.path.join(CSRC, s)]
+            for s, o in zip(SOURCES, objs)]
     with ThreadPoolExecutor(max_workers=len(cmds)) as ex:
         list(ex.map(lambda c: _run(c, verbose), cmds))
     tmp = OUT + ".tmp"
