@@ -87,6 +87,13 @@ __device__ __forceinline__ void store_frag_nt(void* base, int lane, const typena
   __builtin_nontemporal_store(f, reinterpret_cast<typename P::frag*>(base) + lane);
 }
 
+// Streaming load (nt): for data read once by the last kernel that uses it, so that it does not evict
+// lines other kernels running at the same time are about to read.
+template <class P>
+__device__ __forceinline__ typename P::frag load_frag_nt(const void* base, int lane) {
+  return __builtin_nontemporal_load(reinterpret_cast<const typename P::frag*>(base) + lane);
+}
+
 // Read-only streaming loads that bypass nothing: plain global loads (the workspace is re-read once).
 __device__ __forceinline__ f32x4 ld4(const float* p) { return *reinterpret_cast<const f32x4*>(p); }
 

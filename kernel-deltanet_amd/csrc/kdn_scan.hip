@@ -27,6 +27,7 @@
 #include "kdn_frag.hpp"
 #include "kdn_internal.hpp"
 #include "kdn_io.hpp"
+#include "kdn_lift_tile.hpp"
 #include "kdn_scan_common.hpp"
 
 namespace kdn {
@@ -363,11 +364,12 @@ __global__ void __launch_bounds__(256) state_kernel(ScanParams p) {
 
 // ------------------------------------------------------------------------------------------------
 // output: grid (nseg, H, B), 256 threads.  Y = diag(qscale) Q S_c^T + P E for one (chunk, head).
-// Wave w keeps the lifted query fragments of token tile w (written by prep) in registers; the
-// chunk-start S^T fragments are staged in LDS, NG value tiles per pass, and read by all four waves.
-// Each wave assembles its 16 x d_v block of Y in a wave-private LDS tile and writes whole rows with
-// 16-byte stores.
-template <class P, typename OutT, int D, int DV>
+// Wave w keeps the lifted query fragments of token tile w in registers: read back from the record, or
+// (RELIFT, bf16 with the exact projection) lifted again from q here exactly as prep lifted them, Omega
+// read from L2.  The chunk-start S^T fragments are staged in LDS, NG value tiles per pass, and read by
+// all four waves.  Each wave assembles its 16 x d_v block of Y in a wave-private LDS tile and writes
+// whole rows with 16-byte stores.  Every operand is read once: streaming loads.
+template <class P, typename OutT, int D, int DV, bool RELIFT>
 __global__ void __launch_bounds__(256) output_kernel(ScanParams p) {
   using L = WsLayout<P, D, DV>;
   using frag = typename P::frag;
@@ -377,6 +379,7 @@ __global__ void __launch_bounds__(256) output_kernel(ScanParams p) {
   constexpr int YS = DV + 4;                     // padded row of the Y tile
   __shared__ frag s_s[NJ * NG * 64];
   __shared__ __attribute__((aligned(16))) float s_y[4][16 * YS];
+  __shared__ __attribute__((aligned(16))) float s_phrev[RELIFT ? D : 4];
 
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -388,11 +391,25 @@ __global__ void __launch_bounds__(256) output_kernel(ScanParams p) {
   const float* vec = reinterpret_cast<const float*>(ws + L::VEC);
 
   frag aq[NJ];
+  if constexpr (RELIFT) {
+    for (int f = threadIdx.x; f < D; f += 256) s_phrev[f] = p.phase[h * p.phs + f] * 0.15915494309189535f;
+    RawRow<__bf16> raw[1];
+    const int64_t trow = t0 + 16 * w + (lane & 15);
+    raw[0].load((const __bf16*)p.q + sq.q + trow * p.qs1 + h * p.qs2, trow < sq.len, lane);
+    const float ang = (p.inv_tau_head ? p.inv_tau_head[h] : p.inv_tau) * 0.15915494309189535f;
+    __syncthreads();
+    frag lifted[1][NJ];
+    float ss[1];
+    lift_tile<P, __bf16, D, false, 1>(raw, p.normalize, nullptr, p.omega + h * p.oms, s_phrev, ang, lane, lifted, ss);
 #pragma unroll
-  for (int j = 0; j < NJ; ++j) aq[j] = load_frag<P>(ws + L::phiQ + (size_t)(w * NJ + j) * 64 * L::FB, lane);
+    for (int j = 0; j < NJ; ++j) aq[j] = lifted[0][j];
+  } else {
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) aq[j] = load_frag_nt<P>(ws + L::phiQ + (size_t)(w * NJ + j) * 64 * L::FB, lane);
+  }
   frag pf[2];
 #pragma unroll
-  for (int jb = 0; jb < 2; ++jb) pf[jb] = load_frag<P>(ws + L::Pm + (size_t)(w * 2 + jb) * 64 * L::FB, lane);
+  for (int jb = 0; jb < 2; ++jb) pf[jb] = load_frag_nt<P>(ws + L::Pm + (size_t)(w * 2 + jb) * 64 * L::FB, lane);
   const f32x4 qs = *reinterpret_cast<const f32x4*>(vec + 16 * w + 4 * (lane >> 4));
   float* yt = s_y[w];
 
@@ -400,7 +417,7 @@ __global__ void __launch_bounds__(256) output_kernel(ScanParams p) {
     if (n0 > 0) __syncthreads();  // the previous pass's fragments have been read
     for (int idx = threadIdx.x; idx < NJ * NG * 64; idx += 256) {
       const int l = idx & 63, g = (idx >> 6) % NG, j = idx / (64 * NG);
-      s_s[idx] = load_frag<P>(ws + L::Sfr + (size_t)(j * NV + n0 + g) * 64 * L::FB, l);
+      s_s[idx] = load_frag_nt<P>(ws + L::Sfr + (size_t)(j * NV + n0 + g) * 64 * L::FB, l);
     }
     __syncthreads();
 #pragma unroll
@@ -412,8 +429,8 @@ __global__ void __launch_bounds__(256) output_kernel(ScanParams p) {
       frag eb[2];
 #pragma unroll
       for (int jb = 0; jb < 2; ++jb) {
-        const f32x4 e0 = *reinterpret_cast<const f32x4*>(ws + L::Eck + ((size_t)((2 * jb) * NV + n) * 64 + lane) * 16);
-        const f32x4 e1 = *reinterpret_cast<const f32x4*>(ws + L::Eck + ((size_t)((2 * jb + 1) * NV + n) * 64 + lane) * 16);
+        const f32x4 e0 = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(ws + L::Eck + ((size_t)((2 * jb) * NV + n) * 64 + lane) * 16));
+        const f32x4 e1 = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(ws + L::Eck + ((size_t)((2 * jb + 1) * NV + n) * 64 + lane) * 16));
         eb[jb] = P::from_f32(pair_to8(e0, e1));
       }
       f32x4 y = zero4();
@@ -471,6 +488,7 @@ static ScanParams fill_params(const kdn_scan_args* a) {
   p.seq_lo = a->cu_seqlens;
   p.seq_hi = a->cu_seqlens ? a->cu_seqlens + 1 : nullptr;
   p.slots = a->state_slots;
+  p.relift_q = 0;
   return p;
 }
 
@@ -544,8 +562,10 @@ static int launch_phase(const ScanParams& p, int phase, hipStream_t st) {
     const size_t excl = IsBF16<P>::value ? (size_t)STATE_EXCLUSIVE_LDS : 0;
     if (p.decay) hipLaunchKernelGGL((state_kernel<P, D, DV, true>), dim3(state_grid(p.B, p.H, DV / 16)), dim3(256), excl, st, p);
     else hipLaunchKernelGGL((state_kernel<P, D, DV, false>), dim3(state_grid(p.B, p.H, DV / 16)), dim3(256), excl, st, p);
+  } else if (IsBF16<P>::value && p.relift_q) {
+    hipLaunchKernelGGL((output_kernel<P, OutT, D, DV, IsBF16<P>::value>), chunk_grid, dim3(256), 0, st, p);
   } else {
-    hipLaunchKernelGGL((output_kernel<P, OutT, D, DV>), chunk_grid, dim3(256), 0, st, p);
+    hipLaunchKernelGGL((output_kernel<P, OutT, D, DV, false>), chunk_grid, dim3(256), 0, st, p);
   }
   return hipGetLastError() == hipSuccess ? KDN_OK : KDN_ERR_DEVICE;
 }
@@ -610,10 +630,16 @@ static int run_pipelined(const kdn_scan_args* a, const RunSpec& r) {
   hipEvent_t evIn = evs.ev[3 * nbuf], evOut = evs.ev[3 * nbuf + 1];
   // prep shares the device with the state kernel's workgroups (one per CU)
   const int prep_cus = device_cus() - (int)state_grid(a->B, a->H, DV / 16);
+  // With CUs to spare beside the state chain, the output kernel lifts q again rather than reading the
+  // features back: the chain is slowed by the HBM traffic of the kernels beside it, not by their work.
+  const bool relift = IsBF16<P>::value && a->feature_mode == 0 && !a->omega_lo && !r.seq_lo && !a->cu_seqlens &&
+                      prep_cus > 0;
   auto seg_p = [&](int64_t s) {
     const int64_t c0 = s * seg;
-    return segment_params(a, r, c0, (nchunks - c0 < seg) ? (nchunks - c0) : seg,
-                          (unsigned char*)a->workspace + (size_t)(s % nbuf) * buf_bytes, prep_cus);
+    ScanParams p = segment_params(a, r, c0, (nchunks - c0 < seg) ? (nchunks - c0) : seg,
+                                  (unsigned char*)a->workspace + (size_t)(s % nbuf) * buf_bytes, prep_cus);
+    p.relift_q = relift ? 1 : 0;
+    return p;
   };
 #define KDN_TRY(x) do { if ((x) != hipSuccess) return KDN_ERR_DEVICE; } while (0)
 #define KDN_TRYK(x) do { const int _rc = (x); if (_rc != KDN_OK) return _rc; } while (0)
