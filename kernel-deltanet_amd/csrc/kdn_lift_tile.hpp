@@ -107,9 +107,10 @@ __device__ __forceinline__ void lift_tile(const RawRow<InT> (&raw)[NX], int norm
   project(0, acc);
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
-    // one feature tile per scheduling region: hoisting the Omega reads of every tile to the top
-    // would hold them all in registers at once
-    __builtin_amdgcn_sched_barrier(0);
+    // two feature tiles per scheduling region (16 independent cosine chains to interleave; measured
+    // ~3 % faster than one tile and than four): hoisting the Omega reads of every tile to the top would
+    // hold them all in registers at once
+    if (t % 2 == 0) __builtin_amdgcn_sched_barrier(0);
     f32x4 next[NX];
     if (t + 1 < NT) project(t + 1, next);
     const f32x4 ph = *reinterpret_cast<const f32x4*>(&s_phrev[16 * t + 4 * (lane >> 4)]);

@@ -11,14 +11,17 @@ namespace kdn {
 
 // ------------------------------------------------------------------------------------------------
 // prep: grid (ceil(nseg / run), H, B), 256 threads.  A workgroup prepares `run` consecutive chunks
-// of one head: Omega and the phases are staged in LDS once, and the raw q / k / v / beta / decay of the
-// next chunk are loaded into registers while the current chunk is processed.  Wave w owns token rows
-// [16w, 16w+16) of a chunk.
-// Chunks per prep workgroup: chosen at launch for bf16 with the exact or given features
-// (ScanParams::prep_run); 1 for fp32, whose fragments (twice as wide) leave no registers for the
-// prefetch, and for the hi + lo projection, whose second operand stream does the same.
+// of one head.  Wave w owns token rows [16w, 16w+16) of a chunk.
+// bf16 lifts (exact or hi + lo projection): one chunk per workgroup, Omega read from L2 (it is shared
+// by every workgroup) rather than staged in LDS, so that the kernel fits 67 KB of LDS and 256 registers
+// per wave and two workgroups share a CU, each hiding the other's latencies: 1.22 -> 0.99 ms for config
+// 3's prep, measured against one workgroup per CU with Omega in LDS and the next chunk prefetched.
+// Given features (bf16): runs of `run` chunks chosen at launch (ScanParams::prep_run), the next chunk's
+// beta / decay prefetched.  fp32: one chunk, one workgroup per CU (its fragments are twice as wide).
 template <class P, int FM>
-struct PrepRun : std::integral_constant<int, (IsBF16<P>::value && FM != FM_HILO) ? 0 : 1> {};
+struct PrepRun : std::integral_constant<int, (IsBF16<P>::value && FM == FM_PRELIFTED) ? 0 : 1> {};
+template <class P, int FM>
+struct PrepWaves : std::integral_constant<int, (IsBF16<P>::value && FM != FM_PRELIFTED) ? 2 : 1> {};
 
 // Raw inputs of one chunk for one thread of the prep workgroup: the q / k row pieces of the lane's row
 // and beta / decay of token `lane` (prefetched one chunk ahead), and the V pieces of the thread
@@ -69,12 +72,12 @@ __device__ __forceinline__ void load_lifted(const InT* row, bool valid, int lane
 }
 
 template <class P, typename InT, int D, int DV, int FM>
-__global__ void __launch_bounds__(256) prep_kernel(ScanParams p) {
+__global__ void __launch_bounds__(256, (PrepWaves<P, FM>::value)) prep_kernel(ScanParams p) {
   using L = WsLayout<P, D, DV>;
   using frag = typename P::frag;
   using In = PrepInputs<InT, DV>;
   constexpr int NT = D / 16, NJ = D / 32, NV = DV / 16;
-  constexpr bool OMEGA_LDS = IsBF16<P>::value && FM != FM_PRELIFTED;
+  constexpr bool OMEGA_LDS = false;  // Omega from L2 (see above)
   constexpr size_t OMEGA_BYTES = OMEGA_LDS ? (size_t)NT * 2 * 64 * 16 : 0;
   constexpr size_t PHIK_BYTES = (size_t)4 * NJ * 64 * sizeof(frag);
   // After the Gram the K-fragment area is reused for A (16 KB), T (17 KB) and V.

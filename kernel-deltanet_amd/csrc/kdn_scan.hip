@@ -492,10 +492,11 @@ static ScanParams fill_params(const kdn_scan_args* a) {
   return p;
 }
 
-// Chunks per prep workgroup: each workgroup of the prep kernel holds a CU alone (its LDS), so the
-// kernel runs in ceil(workgroups / CUs) rounds, each costing the staging of Omega (about 0.3 of a
-// chunk, measured) plus `run` chunks.  Pick the run length (1..8) with the least total for the CUs
-// left free (all of them, or those the concurrent state kernel does not occupy).
+// Chunks per prep workgroup for given (pre-lifted) features, whose prep workgroup holds a CU alone, so
+// that the kernel runs in ceil(workgroups / CUs) rounds, each costing a fixed start-up (about 0.3 of a
+// chunk) plus `run` chunks.  Pick the run length (1..8) with the least total for the CUs left free (all
+// of them, or those the concurrent state kernel does not occupy).  The lifting prep kernels take one
+// chunk per workgroup.
 static int choose_prep_run(int64_t nseg, int64_t heads, int cus) {
   if (cus <= 0) return 4;
   int best = 1;
