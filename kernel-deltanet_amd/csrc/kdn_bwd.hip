@@ -564,7 +564,7 @@ __global__ void __launch_bounds__(256) bwd_chain_kernel(Params p) {
 // The lift backward of one of q / k for this wave's 128 features and the 32 tokens of half hm, given
 // dPhi^T in acc[ft][u] (rows feature 128w + 16ft + .., column token 16(2hm + u) + ..):
 // ds = -sqrt(2/D) sin(s) (dphi / (n + 1e-8) - phi (phi . dphi) / n), then dx^ = ds Omega reduced over
-// the waves into `dx` (LDS [64][LD], zeroed by the caller) with LDS atomics.  `xh` holds the normalised
+// the waves into `dx` (LDS [64][LD], zeroed by the caller).  `xh` holds the normalised
 // input rows, `s_rd` (zeroed by the caller) collects phi . dphi per token.
 template <class P>
 __device__ __forceinline__ void lift_backward_half(const Params& p, const float* phi, const float* nrm, float* s_rd,
@@ -586,6 +586,14 @@ __device__ __forceinline__ void lift_backward_half(const Params& p, const float*
   }
   __syncthreads();
   const float amp = sqrtf(2.f / D);
+  // per token of the half: 1 / (n + 1e-8) and (phi . dphi) / n
+  float inv_n[2], rd_n[2];
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int tok = 16 * (2 * hm + u) + (lane & 15);
+    inv_n[u] = 1.f / (nrm[tok] + 1e-8f);
+    rd_n[u] = s_rd[tok] / nrm[tok];
+  }
   f32x8 xb[2][2];
 #pragma unroll
   for (int u = 0; u < 2; ++u)
@@ -595,18 +603,15 @@ __device__ __forceinline__ void lift_backward_half(const Params& p, const float*
   for (int ft = 0; ft < 8; ++ft) {
     const int f0 = 128 * w + 16 * ft;
     const f32x8 o0 = frag_rows_bf16(p.omega, DK, f0, 0, lane), o1 = frag_rows_bf16(p.omega, DK, f0, 32, lane);
-    f32x4 ph4;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) ph4[i] = p.phase[f0 + 4 * (lane >> 4) + i];
+    const f32x4 ph4 = *reinterpret_cast<const f32x4*>(p.phase + f0 + 4 * (lane >> 4));
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       const f32x4 sv = mm<PrecF32>(mm<PrecF32>(zero4(), o0, xb[u][0]), o1, xb[u][1]);
-      const int tok = 16 * (2 * hm + u) + (lane & 15);
-      const float n = nrm[tok], rdt = s_rd[tok];
-      const f32x4 ph = *reinterpret_cast<const f32x4*>(phi + (size_t)tok * D + f0 + 4 * (lane >> 4));
+      const f32x4 ph = *reinterpret_cast<const f32x4*>(phi + (size_t)(16 * (2 * hm + u) + (lane & 15)) * D + f0 +
+                                                         4 * (lane >> 4));
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float dphit = acc[ft][u][i] / (n + 1e-8f) - ph[i] * rdt / n;
+        const float dphit = acc[ft][u][i] * inv_n[u] - ph[i] * rd_n[u];
         acc[ft][u][i] = -amp * sin_rad(sv[i] * p.inv_tau + ph4[i]) * dphit;
       }
     }
@@ -630,13 +635,24 @@ __device__ __forceinline__ void lift_backward_half(const Params& p, const float*
     }
     __builtin_amdgcn_sched_barrier(0);
   }
+  // Reduce over the four waves into dx: in turn t wave w adds its partial of input columns 16a .. 16a+15,
+  // a = (w + t) & 3, with 16-byte read-modify-writes; within a turn the waves touch disjoint columns.
+  // (Per-element LDS atomics here cost ~15 % of the kernel: four waves adding to the same addresses.)
 #pragma unroll
-  for (int a = 0; a < 4; ++a)
+  for (int t = 0; t < 4; ++t) {
+    const int a = (w + t) & 3;  // uniform over the wave
 #pragma unroll
-    for (int u = 0; u < 2; ++u)
+    for (int aa = 0; aa < 4; ++aa) {
+      if (aa == a) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        atomicAdd(&dx[(16 * (2 * hm + u) + (lane & 15)) * LD + 16 * a + 4 * (lane >> 4) + i], d[a][u][i]);
+        for (int u = 0; u < 2; ++u) {
+          f32x4* px = reinterpret_cast<f32x4*>(&dx[(16 * (2 * hm + u) + (lane & 15)) * LD + 16 * aa + 4 * (lane >> 4)]);
+          *px = *px + d[aa][u];
+        }
+      }
+    }
+    __syncthreads();
+  }
 }
 
 // Thread (row tid >> 2, features (tid & 3) * 16 ..): dx = inv_tau * dx^ through the input normalisation,
@@ -940,6 +956,25 @@ __global__ void __launch_bounds__(256) bwd_grad_kernel(Params p) {
     __syncthreads();
     for (int hm = 0; hm < 2; ++hm) {
       f32x4 acc[8][2];
+      // B operands of the half's two token tiles (LDS), the same for every feature tile: converted once
+      // dk: [(kappa o W), Zn, N (transposed), M + M^T]; dq: [(a o dY), N]
+      typename P::frag bo[2][4][2];
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int m = 2 * hm + u;
+#pragma unroll
+        for (int jb = 0; jb < 2; ++jb) {
+          if (which == 1) {
+            bo[u][0][jb] = P::from_f32(frag_rows(bW, LD, 16 * m, 32 * jb, lane));
+            bo[u][1][jb] = P::from_f32(frag_rows(bdW, LD, 16 * m, 32 * jb, lane));
+            bo[u][2][jb] = P::from_f32(frag_cols(bXK, LD, 16 * m, 32 * jb, lane));
+            bo[u][3][jb] = P::from_f32(frag_rows(bX, LD, 16 * m, 32 * jb, lane));
+          } else {
+            bo[u][0][jb] = P::from_f32(frag_rows(bY, LD, 16 * m, 32 * jb, lane));
+            bo[u][1][jb] = P::from_f32(frag_rows(bXK, LD, 16 * m, 32 * jb, lane));
+          }
+        }
+      }
 #pragma unroll
       for (int ft = 0; ft < 8; ++ft) {
         const int f0 = 128 * w + 16 * ft;
@@ -949,32 +984,29 @@ __global__ void __launch_bounds__(256) bwd_grad_kernel(Params p) {
           const f32x8 s0 = frag_rows(rec + Rec::S, DV, f0, 0, lane), s1 = frag_rows(rec + Rec::S, DV, f0, 32, lane);
           const f32x8 q0 = frag_cols(rec + Rec::Q, D, f0, 0, lane), q1 = frag_cols(rec + Rec::Q, D, f0, 32, lane);
           const f32x8 k0 = frag_cols(rec + Rec::K, D, f0, 0, lane), k1 = frag_cols(rec + Rec::K, D, f0, 32, lane);
+          const typename P::frag a[4][2] = {{P::from_f32(g0), P::from_f32(g1)}, {P::from_f32(s0), P::from_f32(s1)},
+                                            {P::from_f32(q0), P::from_f32(q1)}, {P::from_f32(k0), P::from_f32(k1)}};
 #pragma unroll
           for (int u = 0; u < 2; ++u) {
-            const int m = 2 * hm + u;
             f32x4 t = zero4();
-            t = mm<P>(t, g0, frag_rows(bW, LD, 16 * m, 0, lane));
-            t = mm<P>(t, g1, frag_rows(bW, LD, 16 * m, 32, lane));
-            t = mm<P>(t, s0, frag_rows(bdW, LD, 16 * m, 0, lane));
-            t = mm<P>(t, s1, frag_rows(bdW, LD, 16 * m, 32, lane));
-            t = mm<P>(t, q0, frag_cols(bXK, LD, 16 * m, 0, lane));
-            t = mm<P>(t, q1, frag_cols(bXK, LD, 16 * m, 32, lane));
-            t = mm<P>(t, k0, frag_rows(bX, LD, 16 * m, 0, lane));
-            t = mm<P>(t, k1, frag_rows(bX, LD, 16 * m, 32, lane));
+#pragma unroll
+            for (int o = 0; o < 4; ++o)
+#pragma unroll
+              for (int jb = 0; jb < 2; ++jb) t = P::mma(t, a[o][jb], bo[u][o][jb]);
             acc[ft][u] = t;
           }
         } else {
           // dQ^T = S^T (a o dY)^T + K^T N^T
           const f32x8 s0 = frag_rows(rec + Rec::S, DV, f0, 0, lane), s1 = frag_rows(rec + Rec::S, DV, f0, 32, lane);
           const f32x8 k0 = frag_cols(rec + Rec::K, D, f0, 0, lane), k1 = frag_cols(rec + Rec::K, D, f0, 32, lane);
+          const typename P::frag a[2][2] = {{P::from_f32(s0), P::from_f32(s1)}, {P::from_f32(k0), P::from_f32(k1)}};
 #pragma unroll
           for (int u = 0; u < 2; ++u) {
-            const int m = 2 * hm + u;
             f32x4 t = zero4();
-            t = mm<P>(t, s0, frag_rows(bY, LD, 16 * m, 0, lane));
-            t = mm<P>(t, s1, frag_rows(bY, LD, 16 * m, 32, lane));
-            t = mm<P>(t, k0, frag_rows(bXK, LD, 16 * m, 0, lane));
-            t = mm<P>(t, k1, frag_rows(bXK, LD, 16 * m, 32, lane));
+#pragma unroll
+            for (int o = 0; o < 2; ++o)
+#pragma unroll
+              for (int jb = 0; jb < 2; ++jb) t = P::mma(t, a[o][jb], bo[u][o][jb]);
             acc[ft][u] = t;
           }
         }

@@ -212,6 +212,18 @@ def test_pipelined_equals_serial(proj, seg, decay_kind):
     assert torch.equal(S1, S2)
 
 
+def test_pipelined_without_spare_cus_equals_serial(proj):
+    # 4 sequences x 16 heads x 4 value tiles fill every CU with state workgroups: the pipelined schedule
+    # then keeps q's lifted features in the workspace (prep stores them, the output kernel reads them);
+    # with one sequence (above) the output kernel lifts q again.  Both equal the serial schedule bit for bit.
+    q, k, v, beta, decay = make_inputs(4, 64 * 6 + 9, 16, 64, torch.bfloat16, "sigmoid", seed=3)
+    y1, S1 = run(proj, q, k, v, beta, decay, segment_chunks=2, pipelined=True)
+    y2, S2 = run(proj, q, k, v, beta, decay, segment_chunks=2, pipelined=False)
+    torch.cuda.synchronize()
+    assert torch.equal(y1, y2)
+    assert torch.equal(S1, S2)
+
+
 def test_two_stream_pipeline_equals_serial(proj):
     """kdn_delta_scan_fwd_pipelined (prep and output sharing one auxiliary stream) is bit-identical too."""
     import ctypes
