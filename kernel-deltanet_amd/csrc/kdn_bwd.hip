@@ -37,6 +37,7 @@ namespace bwd {
 
 constexpr int C = 64, D = 512, DK = 64, DV = 64;
 constexpr int LD = 68;  // LDS row stride (floats) of a 64-wide tile: rows stay 16-byte aligned
+constexpr size_t OMT_BYTES = (size_t)4 * 16 * 64 * 16;  // the Omega^T fragment table after the records
 
 // Per (head, chunk) record, offsets in floats.
 struct Rec {
@@ -85,6 +86,7 @@ struct Params {
   float* ddecay; int64_t dds0, dds1, dds2;
   float* dinit; int64_t dis0, dis1, dis2, dis3;
   float* ws;
+  const bf16x8* omt;  // Omega^T fragments [a 4][jb 16][lane] (workspace tail, written before the gradients)
 };
 
 __device__ __forceinline__ float* record(const Params& p, int64_t b, int64_t h, int64_t c) {
@@ -178,7 +180,7 @@ __global__ void __launch_bounds__(256) bwd_prep_kernel(Params p) {
 #pragma unroll
       for (int u = 0; u < 2; ++u)
 #pragma unroll
-        for (int jb = 0; jb < 2; ++jb) xa[u][jb] = frag_rows(xs, LD, 16 * (2 * hm + u), 32 * jb, lane);
+        for (int jb = 0; jb < 2; ++jb) xa[u][jb] = frag_rows_plain(xs, LD, 16 * (2 * hm + u), 32 * jb, lane);
       float ss[2][4];
 #pragma unroll
       for (int u = 0; u < 2; ++u)
@@ -187,7 +189,7 @@ __global__ void __launch_bounds__(256) bwd_prep_kernel(Params p) {
 #pragma unroll
       for (int ft = 0; ft < 8; ++ft) {
         const int f0 = 128 * w + 16 * ft;
-        const f32x8 o0 = frag_rows_bf16(p.omega, DK, f0, 0, lane), o1 = frag_rows_bf16(p.omega, DK, f0, 32, lane);
+        const f32x8 o0 = frag_rows_plain_bf16(p.omega, DK, f0, 0, lane), o1 = frag_rows_plain_bf16(p.omega, DK, f0, 32, lane);
         const float ph = p.phase[f0 + (lane & 15)];
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
@@ -598,11 +600,11 @@ __device__ __forceinline__ void lift_backward_half(const Params& p, const float*
 #pragma unroll
   for (int u = 0; u < 2; ++u)
 #pragma unroll
-    for (int jb = 0; jb < 2; ++jb) xb[u][jb] = frag_rows(xh, LD, 16 * (2 * hm + u), 32 * jb, lane);
+    for (int jb = 0; jb < 2; ++jb) xb[u][jb] = frag_rows_plain(xh, LD, 16 * (2 * hm + u), 32 * jb, lane);
 #pragma unroll
   for (int ft = 0; ft < 8; ++ft) {
     const int f0 = 128 * w + 16 * ft;
-    const f32x8 o0 = frag_rows_bf16(p.omega, DK, f0, 0, lane), o1 = frag_rows_bf16(p.omega, DK, f0, 32, lane);
+    const f32x8 o0 = frag_rows_plain_bf16(p.omega, DK, f0, 0, lane), o1 = frag_rows_plain_bf16(p.omega, DK, f0, 32, lane);
     const f32x4 ph4 = *reinterpret_cast<const f32x4*>(p.phase + f0 + 4 * (lane >> 4));
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
@@ -626,7 +628,11 @@ __device__ __forceinline__ void lift_backward_half(const Params& p, const float*
   for (int jj = 0; jj < 4; ++jj) {
     f32x8 ob[4];
 #pragma unroll
-    for (int a = 0; a < 4; ++a) ob[a] = frag_cols_bf16(p.omega, DK, 16 * a, 128 * w + 32 * jj, lane);
+    for (int a = 0; a < 4; ++a) {
+      const bf16x8 t = p.omt[(a * 16 + 4 * w + jj) * 64 + lane];
+#pragma unroll
+      for (int s = 0; s < 8; ++s) ob[a][s] = (float)t[s];
+    }
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       const f32x8 bs = pair_to8(acc[2 * jj][u], acc[2 * jj + 1][u]);
@@ -1052,7 +1058,18 @@ static int64_t bwd_chunks(const kdn_scan_args* f) { return (f->T + C - 1) / C; }
 extern "C" size_t kdn_scan_bwd_workspace_bytes(const kdn_scan_bwd_args* a) {
   if (bwd_check(a) != KDN_OK) return 0;
   const kdn_scan_args* f = a->fwd;
-  return (size_t)(f->B * f->H * bwd_chunks(f)) * Rec::floats * sizeof(float);
+  return (size_t)(f->B * f->H * bwd_chunks(f)) * Rec::floats * sizeof(float) + OMT_BYTES;
+}
+
+// Omega^T as A fragments for the gradient kernel's dx^ = ds Omega: fragment (a, jb) lane l slot s holds
+// Omega[32jb + kappa(l, s)][16a + (l & 15)] (a column gather done once per call instead of per chunk).
+__global__ void __launch_bounds__(256) bwd_omega_t_kernel(const __bf16* omega, bf16x8* table) {
+  const int idx = blockIdx.x * 256 + threadIdx.x;  // 16 blocks of 256 cover [a 4][jb 16][lane 64]
+  const int lane = idx & 63, jb = (idx >> 6) & 15, a = idx >> 10;
+  bf16x8 v;
+#pragma unroll
+  for (int s = 0; s < 8; ++s) v[s] = omega[(size_t)(32 * jb + kappa(lane, s)) * DK + 16 * a + (lane & 15)];
+  table[idx] = v;
 }
 
 // Launches phases [first, last] (0 prep, 1 forward carry, 2 reverse carry, 3 gradients) in order.
@@ -1064,7 +1081,10 @@ static int bwd_launch(const Params& p, int first, int last, hipStream_t st) {
     if (ph == 0) hipLaunchKernelGGL((bwd_prep_kernel<P, InT>), chunk_grid, dim3(256), 0, st, p);
     if (ph == 1) hipLaunchKernelGGL((bwd_chain_kernel<P, false>), dim3(chain_wgs), dim3(256), 0, st, p);
     if (ph == 2) hipLaunchKernelGGL((bwd_chain_kernel<P, true>), dim3(chain_wgs), dim3(256), 0, st, p);
-    if (ph == 3) hipLaunchKernelGGL((bwd_grad_kernel<P, InT>), chunk_grid, dim3(256), 0, st, p);
+    if (ph == 3) {
+      hipLaunchKernelGGL(bwd_omega_t_kernel, dim3(16), dim3(256), 0, st, p.omega, const_cast<bf16x8*>(p.omt));
+      hipLaunchKernelGGL((bwd_grad_kernel<P, InT>), chunk_grid, dim3(256), 0, st, p);
+    }
   }
   return launch_status();
 }
@@ -1099,6 +1119,8 @@ static int bwd_run(const kdn_scan_bwd_args* a, int first, int last, void* stream
   p.dinit = a->d_initial_state;
   p.dis0 = a->dinit_stride[0]; p.dis1 = a->dinit_stride[1]; p.dis2 = a->dinit_stride[2]; p.dis3 = a->dinit_stride[3];
   p.ws = reinterpret_cast<float*>(a->workspace);
+  p.omt = reinterpret_cast<const bf16x8*>(static_cast<unsigned char*>(a->workspace) +
+                                          (size_t)(f->B * f->H * p.nch) * Rec::floats * sizeof(float));
   const hipStream_t st = as_stream(stream);
   // bf16 inputs: the D = 512 contractions take bf16 operands with fp32 accumulation, the forward's
   // policy for bf16 inputs; the lift and the 64 x 64 chunk algebra stay in fp32 MFMA.

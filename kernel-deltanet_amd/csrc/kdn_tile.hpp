@@ -40,6 +40,20 @@ __device__ __forceinline__ f32x8 frag_cols_bf16(const __bf16* base, int ld, int 
   return r;
 }
 
+// Fragments in plain depth order (slot s of lane l at depth k0 + 8(l>>4) + s, one 16- or 32-byte run
+// per lane): a product is exact in any depth order as long as both operands use the same one.
+__device__ __forceinline__ f32x8 frag_rows_plain(const float* base, int ld, int r0, int k0, int lane) {
+  const float* p = base + (size_t)(r0 + (lane & 15)) * ld + k0 + 8 * (lane >> 4);
+  return pair_to8(*reinterpret_cast<const f32x4*>(p), *reinterpret_cast<const f32x4*>(p + 4));
+}
+__device__ __forceinline__ f32x8 frag_rows_plain_bf16(const __bf16* base, int ld, int r0, int k0, int lane) {
+  const bf16x8 v = *reinterpret_cast<const bf16x8*>(base + (size_t)(r0 + (lane & 15)) * ld + k0 + 8 * (lane >> 4));
+  f32x8 r;
+#pragma unroll
+  for (int s = 0; s < 8; ++s) r[s] = (float)v[s];
+  return r;
+}
+
 // sin of an angle in radians via v_sin_f32 (revolutions), reduced to [-0.5, 0.5] revolutions as
 // cos_rad (kdn_frag.hpp) does.
 __device__ __forceinline__ float sin_rad(float angle) {
