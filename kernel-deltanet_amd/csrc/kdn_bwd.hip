@@ -116,6 +116,19 @@ __device__ __forceinline__ float load_x_part(const InT* x, int64_t base, bool va
   return nrm;
 }
 
+// The normalised rows the lift consumes, as the forward lifts them: for bf16 inputs F.normalize keeps the
+// dtype, so x^ is rounded to bf16; its products with the bf16-exact Omega are then exact on the bf16
+// MFMA, and the pre-activations s equal the forward's.
+template <typename InT>
+__device__ __forceinline__ void round_like_input(int normalize, float* part) {
+  if constexpr (std::is_same<InT, __bf16>::value) {
+    if (normalize) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) part[e] = (float)(__bf16)part[e];
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------------------------- prep
 // grid (nch, H, B), 256 threads.
 template <class P, typename InT>
@@ -167,6 +180,7 @@ __global__ void __launch_bounds__(256) bwd_prep_kernel(Params p) {
     const int64_t xb = which == 0 ? b * p.qs0 + (t0 + r) * p.qs1 + h * p.qs2 : b * p.ks0 + (t0 + r) * p.ks1 + h * p.ks2;
     float part[16];
     load_x_part<InT>(x, xb + c0, rvalid, p.normalize, part);
+    round_like_input<InT>(p.normalize, part);
 #pragma unroll
     for (int e = 0; e < 16; ++e) xs[r * LD + c0 + e] = part[e];
     __syncthreads();
@@ -193,7 +207,7 @@ __global__ void __launch_bounds__(256) bwd_prep_kernel(Params p) {
         const float ph = p.phase[f0 + (lane & 15)];
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
-          f32x4 sv = mm<PrecF32>(mm<PrecF32>(zero4(), xa[u][0], o0), xa[u][1], o1);
+          f32x4 sv = mm<P>(mm<P>(zero4(), xa[u][0], o0), xa[u][1], o1);
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const float v = amp * cos_rad(sv[i] * p.inv_tau + ph);
@@ -608,7 +622,7 @@ __device__ __forceinline__ void lift_backward_half(const Params& p, const float*
     const f32x4 ph4 = *reinterpret_cast<const f32x4*>(p.phase + f0 + 4 * (lane >> 4));
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
-      const f32x4 sv = mm<PrecF32>(mm<PrecF32>(zero4(), o0, xb[u][0]), o1, xb[u][1]);
+      const f32x4 sv = mm<P>(mm<P>(zero4(), o0, xb[u][0]), o1, xb[u][1]);
       const f32x4 ph = *reinterpret_cast<const f32x4*>(phi + (size_t)(16 * (2 * hm + u) + (lane & 15)) * D + f0 +
                                                          4 * (lane >> 4));
 #pragma unroll
@@ -949,6 +963,7 @@ __global__ void __launch_bounds__(256) bwd_grad_kernel(Params p) {
     {
       float part[16];
       load_x_part<InT>(x, xb, rvalid, p.normalize, part);
+      round_like_input<InT>(p.normalize, part);
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         bT[r * LD + c0 + e] = part[e];
