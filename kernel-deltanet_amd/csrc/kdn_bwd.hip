@@ -737,16 +737,21 @@ __global__ void __launch_bounds__(256) bwd_grad_kernel(Params p) {
     const InT* v = reinterpret_cast<const InT*>(p.v);
     const int64_t vb = b * p.vs0 + (t0 + r) * p.vs1 + h * p.vs2 + c0;
     const int64_t yb = b * p.ys0 + (t0 + r) * p.ys1 + h * p.ys2 + c0;
+    // the record's rows as 16-byte pieces (16 contiguous floats per thread, 64-byte aligned)
+#pragma unroll
+    for (int e4 = 0; e4 < 4; ++e4) {
+      const int o = r * LD + c0 + 4 * e4, q = r * DV + c0 + 4 * e4;
+      *reinterpret_cast<f32x4*>(&bW[o]) = *reinterpret_cast<const f32x4*>(rec + Rec::W + q);
+      *reinterpret_cast<f32x4*>(&bdW[o]) = rvalid ? *reinterpret_cast<const f32x4*>(rec + Rec::DW + q) : zero4();
+      *reinterpret_cast<f32x4*>(&bXK[o]) = *reinterpret_cast<const f32x4*>(rec + Rec::XK + q);
+      *reinterpret_cast<f32x4*>(&bX[o]) = *reinterpret_cast<const f32x4*>(rec + Rec::X + q);
+      *reinterpret_cast<f32x4*>(&bT[o]) = *reinterpret_cast<const f32x4*>(rec + Rec::T + r * C + c0 + 4 * e4);
+    }
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
-      const int o = r * LD + c0 + e, q = r * DV + c0 + e;
+      const int o = r * LD + c0 + e;
       bY[o] = rvalid ? p.dy[yb + e] : 0.f;
-      bW[o] = rec[Rec::W + q];
-      bdW[o] = rvalid ? rec[Rec::DW + q] : 0.f;
-      bXK[o] = rec[Rec::XK + q];
-      bX[o] = rec[Rec::X + q];
       bV[o] = rvalid ? ldx(v + vb + e) : 0.f;
-      bT[o] = rec[Rec::T + r * C + c0 + e];
     }
   }
   __syncthreads();
@@ -838,6 +843,7 @@ __global__ void __launch_bounds__(256) bwd_grad_kernel(Params p) {
     f32x4 qs[4];
 #pragma unroll
     for (int n = 0; n < 4; ++n) qs[n] = zero4();
+#pragma unroll 4
     for (int jb = 0; jb < D / 32; ++jb) {
       const f32x8 qa = frag_rows(rec + Rec::Q, D, 16 * w, 32 * jb, lane);
 #pragma unroll
@@ -865,6 +871,8 @@ __global__ void __launch_bounds__(256) bwd_grad_kernel(Params p) {
     float gs = 0.f;
     const f32x4* G4 = reinterpret_cast<const f32x4*>(rec + Rec::G);
     const f32x4* S4 = reinterpret_cast<const f32x4*>(rec + Rec::S);
+    // 32 iterations per thread, unrolled so that their loads are in flight together
+#pragma unroll 8
     for (int e = tid; e < D * DV / 4; e += 256) {
       const f32x4 g = G4[e], s = S4[e];
       gs += g[0] * s[0] + g[1] * s[1] + g[2] * s[2] + g[3] * s[3];
