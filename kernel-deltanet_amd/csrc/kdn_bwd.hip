@@ -320,43 +320,8 @@ __global__ void __launch_bounds__(256) bwd_prep_kernel(Params p) {
       }
   }
   __syncthreads();
-  // T = (I + A)^-1 by column-oriented forward substitution: column 16w + (lane >> 2) per lane quad, lane
-  // pq = lane & 3 keeping rows 4s + pq in registers.  Once row i of the column is final (lane i & 3, slot
-  // i >> 2) it is broadcast over the quad and every later row takes its term at once: one broadcast and
-  // one FMA per row on the sequential chain.  acc[s] = -(partial T[4s+pq][col]); A is zero on and above
-  // its diagonal, so updating every slot from i >> 2 on leaves rows r <= i unchanged.
-  {
-    const int col = 16 * w + (lane >> 2), pq = lane & 3;
-    float acc[16];
-#pragma unroll
-    for (int s2 = 0; s2 < 16; ++s2) acc[s2] = (4 * s2 + pq == col) ? -1.f : 0.f;
-    constexpr int AHEAD = 3;  // columns of A in flight (LDS latency off the chain)
-    f32x4 acol[AHEAD][4];
-    auto load_col = [&](int i, f32x4 (&dst)[4]) {
-      const f32x4* src = reinterpret_cast<const f32x4*>(bA + (i * 4 + pq) * 16);
-#pragma unroll
-      for (int q = 0; q < 4; ++q)
-        if (q >= (i >> 4)) dst[q] = src[q];
-    };
-#pragma unroll
-    for (int i = 0; i < AHEAD; ++i) load_col(i, acol[i]);
-#pragma unroll
-    for (int i = 0; i < C - 1; ++i) {
-      float bc;  // -T[i][col]
-      switch (i & 3) {
-        case 0: bc = quad_bcast<0>(acc[i >> 2]); break;
-        case 1: bc = quad_bcast<1>(acc[i >> 2]); break;
-        case 2: bc = quad_bcast<2>(acc[i >> 2]); break;
-        default: bc = quad_bcast<3>(acc[i >> 2]); break;
-      }
-      const f32x4 (&a)[4] = acol[i % AHEAD];
-#pragma unroll
-      for (int s2 = i >> 2; s2 < 16; ++s2) acc[s2] = fmaf(-a[s2 >> 2][s2 & 3], bc, acc[s2]);
-      if (i + AHEAD < C - 1) load_col(i + AHEAD, acol[i % AHEAD]);
-    }
-#pragma unroll
-    for (int s2 = 0; s2 < 16; ++s2) bT[(4 * s2 + pq) * LD + col] = -acc[s2];
-  }
+  // T = (I + A)^-1 (column-oriented substitution over lane quads)
+  unit_lower_inverse(bA, bT, LD, w, lane);
   __syncthreads();
   for (int idx = tid; idx < C * C; idx += 256) {
     const int i = idx >> 6, j = idx & 63;

@@ -6,8 +6,8 @@
 // D = 512 scan: y_t = S_{t-1} phi_q(t), S_t = lambda_t S_{t-1} (I - beta_t phi_k phi_k^T) + beta_t v_t phi_k^T.
 //
 // Three launches per call, with one fp32 record per (batch, head, 64-token chunk):
-//   prep   (parallel)   Grams K K^T and Q K^T from the feature rows in place, A, T = (I + A)^-1 (lane-quad
-//                       substitution), Tp = T diag(beta g), P, U~ = T (beta o V); K packed in MFMA
+//   prep   (parallel)   Grams K K^T and Q K^T from the feature rows in place, A, T = (I + A)^-1 (column-
+//                       oriented substitution), Tp = T diag(beta g), P, U~ = T (beta o V); K packed in MFMA
 //                       fragment order (rows and transposed)
 //   carry  (sequential) S^T at every chunk start; X_K = K S^T, W = U~ - Tp X_K,
 //                       S^T <- g_C S^T + K^T (kappa o W); the final state
@@ -161,7 +161,8 @@ __global__ void __launch_bounds__(256) gen_prep_kernel(Params p) {
       for (int i = 0; i < 4; ++i) {
         const int ri = 16 * w + 4 * (lane >> 4) + i, cj = 16 * n + (lane & 15);
         const float li = s_ell[ri], lj = s_ell[cj], lim1 = ri > 0 ? s_ell[ri - 1] : 0.f;
-        bA[ri * LD + cj] = cj < ri ? s_beta[ri] * expf(fminf(li - lj, 0.f)) * gkk[n][i] : 0.f;
+        // A transposed for the column-oriented inverse: [j][p][s] = A[4s+p][j]
+        bA[(cj * 4 + (ri & 3)) * 16 + (ri >> 2)] = cj < ri ? s_beta[ri] * expf(fminf(li - lj, 0.f)) * gkk[n][i] : 0.f;
         rec[R::P + ri * C + cj] = cj < ri ? expf(fminf(lim1 - lj, 0.f)) * gqk[n][i] : 0.f;
       }
   }
@@ -185,25 +186,8 @@ __global__ void __launch_bounds__(256) gen_prep_kernel(Params p) {
     }
   }
   __syncthreads();
-  // T = (I + A)^-1: column 16w + (lane >> 2) per lane quad, lane pq keeping rows 4k + pq in registers
-  {
-    const int col = 16 * w + (lane >> 2), pq = lane & 3;
-    float Tr[16];
-#pragma unroll
-    for (int k = 0; k < 16; ++k) Tr[k] = 0.f;
-#pragma unroll
-    for (int i = 0; i < C; ++i) {
-      float acc = 0.f;
-#pragma unroll
-      for (int k = 0; k < (i + 3) / 4; ++k) acc += bA[i * LD + 4 * k + pq] * Tr[k];
-      acc += __shfl_xor(acc, 1);
-      acc += __shfl_xor(acc, 2);
-      const float val = (i == col ? 1.f : 0.f) - acc;
-      if (pq == (i & 3)) Tr[i >> 2] = val;
-    }
-#pragma unroll
-    for (int k = 0; k < 16; ++k) bT[(4 * k + pq) * LD + col] = Tr[k];
-  }
+  // T = (I + A)^-1 (column-oriented substitution over lane quads)
+  unit_lower_inverse(bA, bT, LD, w, lane);
   __syncthreads();
   for (int idx = tid; idx < C * C; idx += 256) {
     const int i = idx >> 6, j = idx & 63;

@@ -5,6 +5,7 @@
 #include "kdn_internal.hpp"
 #include "kdn_io.hpp"
 #include "kdn_lift_tile.hpp"
+#include "kdn_tile.hpp"
 #include "kdn_scan_common.hpp"
 
 namespace kdn {
@@ -233,46 +234,8 @@ __global__ void __launch_bounds__(256, (PrepWaves<P, FM>::value)) prep_kernel(Sc
     }
     __syncthreads();
 
-    // ---- T = (I + A)^{-1}: column col = 16w + (l>>2) per lane quad; lane p = l&3 keeps rows 4s+p.
-    // Column-oriented forward substitution: once row i of the column is final (lane i & 3, slot i >> 2)
-    // it is broadcast over the quad and every later row takes its term A[r][i] T[i][col] at once, so
-    // the sequential chain per row is one broadcast and one FMA.  acc[s] = -(partial T[4s+p][col]);
-    // the entries of A on and above the diagonal are zero, so updating every slot from i >> 2 on leaves
-    // rows r <= i unchanged.
-    {
-      const int col = 16 * w + (lane >> 2), pq = lane & 3;
-      float acc[16];
-#pragma unroll
-      for (int s2 = 0; s2 < 16; ++s2) acc[s2] = (4 * s2 + pq == col) ? -1.f : 0.f;
-      // Column i of A for the lane's rows, in 16-byte pieces from piece i >> 4 on (the earlier rows of
-      // the column are zero), loaded AHEAD steps before it is used so that no step waits for LDS.
-      constexpr int AHEAD = 3;
-      f32x4 acol[AHEAD][4];
-      auto load_col = [&](int i, f32x4 (&dst)[4]) {
-        const f32x4* src = reinterpret_cast<const f32x4*>(s_A + (i * 4 + pq) * 16);
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-          if (q >= (i >> 4)) dst[q] = src[q];
-      };
-#pragma unroll
-      for (int i = 0; i < AHEAD; ++i) load_col(i, acol[i]);
-#pragma unroll
-      for (int i = 0; i < 63; ++i) {
-        float bc;  // -T[i][col]
-        switch (i & 3) {
-          case 0: bc = quad_bcast<0>(acc[i >> 2]); break;
-          case 1: bc = quad_bcast<1>(acc[i >> 2]); break;
-          case 2: bc = quad_bcast<2>(acc[i >> 2]); break;
-          default: bc = quad_bcast<3>(acc[i >> 2]); break;
-        }
-        const f32x4 (&a)[4] = acol[i % AHEAD];
-#pragma unroll
-        for (int s2 = i >> 2; s2 < 16; ++s2) acc[s2] = fmaf(-a[s2 >> 2][s2 & 3], bc, acc[s2]);
-        if (i + AHEAD < 63) load_col(i + AHEAD, acol[i % AHEAD]);
-      }
-#pragma unroll
-      for (int s2 = 0; s2 < 16; ++s2) s_T[(4 * s2 + pq) * 68 + col] = -acc[s2];
-    }
+    // ---- T = (I + A)^{-1} (column-oriented substitution over lane quads)
+    unit_lower_inverse(s_A, s_T, 68, w, lane);
     __syncthreads();
 
     // ---- W~ factor T diag(beta e^g |phi_k|) fragments, and U~ = T diag(beta) V   (wave w: rows m = w)

@@ -67,6 +67,48 @@ __device__ __forceinline__ f32x4 mm(f32x4 acc, const f32x8& a, const f32x8& b) {
   return P::mma(acc, P::from_f32(a), P::from_f32(b));
 }
 
+// T = (I + A)^{-1} of a strictly lower triangular 64 x 64 A, by column-oriented forward substitution:
+// wave w (0..3) computes columns 16w .. 16w+15, one per lane quad (col = 16w + (lane >> 2)); lane
+// pq = lane & 3 keeps rows 4s + pq.  Once row i of the column is final (lane i & 3, slot i >> 2) it is
+// broadcast over the quad and every later row takes its term at once: one broadcast and one FMA per row
+// on the sequential chain.  acc[s] = -(partial T[4s+pq][col]); A is zero on and above its diagonal, so
+// updating every slot from i >> 2 on leaves rows r <= i unchanged.  The columns of A are loaded three
+// rows ahead.
+//   At: A transposed in LDS, At[(j * 4 + p) * 16 + s] = A[4s + p][j] (16-byte aligned)
+//   T:  output rows, T[r * ldt + c] (LDS)
+__device__ __forceinline__ void unit_lower_inverse(const float* At, float* T, int ldt, int w, int lane) {
+  const int col = 16 * w + (lane >> 2), pq = lane & 3;
+  float acc[16];
+#pragma unroll
+  for (int s2 = 0; s2 < 16; ++s2) acc[s2] = (4 * s2 + pq == col) ? -1.f : 0.f;
+  constexpr int AHEAD = 3;
+  f32x4 acol[AHEAD][4];
+  auto load_col = [&](int i, f32x4 (&dst)[4]) {
+    const f32x4* src = reinterpret_cast<const f32x4*>(At + (i * 4 + pq) * 16);
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      if (q >= (i >> 4)) dst[q] = src[q];
+  };
+#pragma unroll
+  for (int i = 0; i < AHEAD; ++i) load_col(i, acol[i]);
+#pragma unroll
+  for (int i = 0; i < 63; ++i) {
+    float bc;  // -T[i][col]
+    switch (i & 3) {
+      case 0: bc = quad_bcast<0>(acc[i >> 2]); break;
+      case 1: bc = quad_bcast<1>(acc[i >> 2]); break;
+      case 2: bc = quad_bcast<2>(acc[i >> 2]); break;
+      default: bc = quad_bcast<3>(acc[i >> 2]); break;
+    }
+    const f32x4 (&a)[4] = acol[i % AHEAD];
+#pragma unroll
+    for (int s2 = i >> 2; s2 < 16; ++s2) acc[s2] = fmaf(-a[s2 >> 2][s2 & 3], bc, acc[s2]);
+    if (i + AHEAD < 63) load_col(i + AHEAD, acol[i % AHEAD]);
+  }
+#pragma unroll
+  for (int s2 = 0; s2 < 16; ++s2) T[(4 * s2 + pq) * ldt + col] = -acc[s2];
+}
+
 // Sum over the 16 lanes sharing (lane >> 4) (one tile row) / over the 4 lane groups (one tile column).
 __device__ __forceinline__ float sum_row16(float v) {
   v += __shfl_xor(v, 1);
