@@ -200,11 +200,19 @@ __global__ void __launch_bounds__(256) bwd_prep_kernel(Params p) {
       for (int u = 0; u < 2; ++u)
 #pragma unroll
         for (int i = 0; i < 4; ++i) ss[u][i] = 0.f;
+      // Omega rows and phases of feature tile ft + 1 are issued in the region of tile ft
+      f32x8 on0 = frag_rows_plain_bf16(p.omega, DK, 128 * w, 0, lane), on1 = frag_rows_plain_bf16(p.omega, DK, 128 * w, 32, lane);
+      float phn = p.phase[128 * w + (lane & 15)];
 #pragma unroll
       for (int ft = 0; ft < 8; ++ft) {
         const int f0 = 128 * w + 16 * ft;
-        const f32x8 o0 = frag_rows_plain_bf16(p.omega, DK, f0, 0, lane), o1 = frag_rows_plain_bf16(p.omega, DK, f0, 32, lane);
-        const float ph = p.phase[f0 + (lane & 15)];
+        const f32x8 o0 = on0, o1 = on1;
+        const float ph = phn;
+        if (ft + 1 < 8) {
+          on0 = frag_rows_plain_bf16(p.omega, DK, f0 + 16, 0, lane);
+          on1 = frag_rows_plain_bf16(p.omega, DK, f0 + 16, 32, lane);
+          phn = p.phase[f0 + 16 + (lane & 15)];
+        }
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
           f32x4 sv = mm<P>(mm<P>(zero4(), xa[u][0], o0), xa[u][1], o1);
@@ -275,10 +283,15 @@ __global__ void __launch_bounds__(256) bwd_prep_kernel(Params p) {
     for (int n = 0; n < 4; ++n)
 #pragma unroll
       for (int jb = 0; jb < 2; ++jb) yb[n][jb] = frag_cols(bA, LD, 16 * n, 32 * jb, lane);
+    f32x8 qn0 = frag_cols(Q, D, 128 * w, 0, lane), qn1 = frag_cols(Q, D, 128 * w, 32, lane);
 #pragma unroll
     for (int ft = 0; ft < 8; ++ft) {
       const int f0 = 128 * w + 16 * ft;
-      const f32x8 qa0 = frag_cols(Q, D, f0, 0, lane), qa1 = frag_cols(Q, D, f0, 32, lane);
+      const f32x8 qa0 = qn0, qa1 = qn1;
+      if (ft + 1 < 8) {
+        qn0 = frag_cols(Q, D, f0 + 16, 0, lane);
+        qn1 = frag_cols(Q, D, f0 + 16, 32, lane);
+      }
 #pragma unroll
       for (int n = 0; n < 4; ++n) {
         const f32x4 hv = mm<P>(mm<P>(zero4(), qa0, yb[n][0]), qa1, yb[n][1]);
@@ -296,6 +309,7 @@ __global__ void __launch_bounds__(256) bwd_prep_kernel(Params p) {
     f32x4 gkk[4], gqk[4];
 #pragma unroll
     for (int n = 0; n < 4; ++n) gkk[n] = gqk[n] = zero4();
+#pragma unroll 4
     for (int jb = 0; jb < D / 32; ++jb) {
       const f32x8 kw = frag_rows(K, D, 16 * w, 32 * jb, lane);
       const f32x8 qw = frag_rows(Q, D, 16 * w, 32 * jb, lane);
@@ -580,11 +594,18 @@ __device__ __forceinline__ void lift_backward_half(const Params& p, const float*
   for (int u = 0; u < 2; ++u)
 #pragma unroll
     for (int jb = 0; jb < 2; ++jb) xb[u][jb] = frag_rows_plain(xh, LD, 16 * (2 * hm + u), 32 * jb, lane);
+  f32x8 on0 = frag_rows_plain_bf16(p.omega, DK, 128 * w, 0, lane), on1 = frag_rows_plain_bf16(p.omega, DK, 128 * w, 32, lane);
+  f32x4 phn = *reinterpret_cast<const f32x4*>(p.phase + 128 * w + 4 * (lane >> 4));
 #pragma unroll
   for (int ft = 0; ft < 8; ++ft) {
     const int f0 = 128 * w + 16 * ft;
-    const f32x8 o0 = frag_rows_plain_bf16(p.omega, DK, f0, 0, lane), o1 = frag_rows_plain_bf16(p.omega, DK, f0, 32, lane);
-    const f32x4 ph4 = *reinterpret_cast<const f32x4*>(p.phase + f0 + 4 * (lane >> 4));
+    const f32x8 o0 = on0, o1 = on1;
+    const f32x4 ph4 = phn;
+    if (ft + 1 < 8) {  // the next feature tile's Omega rows and phases, issued one region ahead
+      on0 = frag_rows_plain_bf16(p.omega, DK, f0 + 16, 0, lane);
+      on1 = frag_rows_plain_bf16(p.omega, DK, f0 + 16, 32, lane);
+      phn = *reinterpret_cast<const f32x4*>(p.phase + f0 + 16 + 4 * (lane >> 4));
+    }
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       const f32x4 sv = mm<P>(mm<P>(zero4(), o0, xb[u][0]), o1, xb[u][1]);
