@@ -207,7 +207,7 @@ int kdn_scan_output(const kdn_scan_args* a, int64_t chunk0, int64_t nchunks, voi
  * d_final_state NULL means dL/dS_T = 0; ddecay (allowed only with decay) and d_initial_state may be
  * NULL.  The gradient of lambda is zero where the forward's clamp to [1e-5, 1] is active.  The
  * workspace holds one fp32 record per (batch, head, 64-token chunk) (1,116,160 bytes each; 256-byte
- * aligned). */
+ * aligned) followed by a 64 KB table of Omega^T fragments that the gradient launch writes. */
 typedef struct kdn_scan_bwd_args {
   const kdn_scan_args* fwd;
   const float* dy;            int64_t dy_stride[3];
