@@ -10,6 +10,7 @@
 //                      A dense 64 x D MFMA projection costs ~4 MFMA issues per row versus ~430 VALU
 //                      issues for the 8-block x 3-stage butterfly, so the lift's hot path uses MFMA and
 //                      the butterfly builds Omega once.
+#include <type_traits>
 #include "kdn_frag.hpp"
 #include "kdn_internal.hpp"
 #include "kdn_io.hpp"
@@ -72,33 +73,43 @@ __global__ void __launch_bounds__(256) fwht_rows_kernel(const T* __restrict__ x,
 }
 
 // ------------------------------------------------------------------------------------------------
-// Lift: one wave per 16-row tile, four tiles per workgroup, persistent over tiles.
+// Waves (16-row tiles) per lift workgroup.  The bf16 -> bf16 D = 512 lift fits 168 registers, three
+// waves per SIMD: twelve waves share one LDS copy of Omega (measured 2-3 % faster than two 4-wave
+// workgroups per CU, with two spilled registers); the other variants would spill more and keep four.
+template <typename InT, typename OutT, int D>
+struct LiftWaves {
+  static constexpr int value =
+      (std::is_same<InT, __bf16>::value && std::is_same<OutT, __bf16>::value && D == 512) ? 12 : 4;
+};
+
+// Lift: one wave per 16-row tile, LiftWaves tiles per workgroup, persistent over tiles.
 // Projection in the transposed orientation  Phi^T[f][r] = sum_k Omega[f][k] x[r][k]:
 //   A = Omega fragments (f rows, k depth)   read from LDS (staged once per workgroup)
 //   B = x fragments      (k depth, r column) read from global, 16/32 bytes per lane
 // Accumulator tile (f-tile t): lane l holds Phi^T[16t + 4(l>>4) + i][row (l & 15)].
 template <typename InT, typename OutT, int D>
-__global__ void __launch_bounds__(256) lift_kernel(const InT* __restrict__ x, int64_t rows, int64_t xs, int normalize,
+__global__ void __launch_bounds__((64 * LiftWaves<InT, OutT, D>::value)) lift_kernel(const InT* __restrict__ x, int64_t rows, int64_t xs, int normalize,
                                                    const __bf16* __restrict__ omega, const float* __restrict__ phase,
                                                    float inv_tau, OutT* __restrict__ out, int64_t os) {
   constexpr int NT = D / 16;                 // feature tiles
+  constexpr int NW = LiftWaves<InT, OutT, D>::value;
   constexpr int NSPLIT = XFrag<InT>::NSPLIT;
   __shared__ bf16x8 s_omega[NT * 2 * 64];    // [t][kb][lane] A fragments, D*64*2 bytes
   __shared__ __attribute__((aligned(16))) float s_phase_rev[D];           // phase / (2 pi)
   // Per-wave staging of 16 rows x 64 features of output, rows padded by 16 bytes.
   constexpr int SRS = 64 * (int)sizeof(OutT) + 16;  // row stride in bytes
   constexpr int SCPR = 64 * (int)sizeof(OutT) / 16;  // 16-byte chunks per staged row
-  __shared__ __attribute__((aligned(16))) unsigned char s_stage[4][16 * SRS];
+  __shared__ __attribute__((aligned(16))) unsigned char s_stage[NW][16 * SRS];
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
 
   // Stage Omega as A fragments: lane l of fragment (t, kb) holds Omega[16t + (l&15)][32kb + 8(l>>4) .. +8].
-  for (int idx = threadIdx.x; idx < NT * 2 * 64; idx += 256) {
+  for (int idx = threadIdx.x; idx < NT * 2 * 64; idx += 64 * NW) {
     const int l = idx & 63, tk = idx >> 6, t = tk >> 1, kb = tk & 1;
     s_omega[idx] = *reinterpret_cast<const bf16x8*>(omega + (int64_t)(16 * t + (l & 15)) * 64 + 32 * kb + 8 * (l >> 4));
   }
-  for (int f = threadIdx.x; f < D; f += 256) s_phase_rev[f] = phase[f] * 0.15915494309189535f;
+  for (int f = threadIdx.x; f < D; f += 64 * NW) s_phase_rev[f] = phase[f] * 0.15915494309189535f;
   __syncthreads();
 
   const float ang_scale = inv_tau * 0.15915494309189535f;  // radians -> revolutions folded in
@@ -109,7 +120,7 @@ __global__ void __launch_bounds__(256) lift_kernel(const InT* __restrict__ x, in
   // index is clamped to the last row, so every load is unconditional and in bounds; rows past the end
   // are zeroed after the load and never stored.
   constexpr int PIECES = 2 * (int)sizeof(InT) / 2;  // 16-byte pieces per lane: 8 elements per depth block
-  const int64_t stride = (int64_t)gridDim.x * 4;
+  const int64_t stride = (int64_t)gridDim.x * NW;
   auto load_tile = [&](int64_t t, u32x4 (&raw)[PIECES]) {
     int64_t row = t * 16 + (lane & 15);
     row = row < rows ? row : rows - 1;
@@ -121,7 +132,7 @@ __global__ void __launch_bounds__(256) lift_kernel(const InT* __restrict__ x, in
         raw[kb * (PIECES / 2) + pc] = *reinterpret_cast<const u32x4*>(src + 32 * kb * sizeof(InT) + 16 * pc);
   };
   u32x4 nraw[PIECES];
-  int64_t tile = (int64_t)blockIdx.x * 4 + wave;
+  int64_t tile = (int64_t)blockIdx.x * NW + wave;
   if (tile < ntiles) load_tile(tile, nraw);
   for (; tile < ntiles; tile += stride) {
     const int64_t row = tile * 16 + (lane & 15);
@@ -217,14 +228,15 @@ template <typename InT, typename OutT, int D>
 static void launch_lift(const void* x, int64_t rows, int64_t xs, int normalize, const void* omega, const float* phase,
                         float inv_tau, void* out, int64_t os, hipStream_t st) {
   const int64_t ntiles = (rows + 15) / 16;
-  int64_t wgs = (ntiles + 3) / 4;
+  constexpr int NW = LiftWaves<InT, OutT, D>::value;
+  int64_t wgs = (ntiles + NW - 1) / NW;
   // one round of resident workgroups (as many per CU as the LDS allows); the kernel loops over tiles
-  constexpr size_t lds = (size_t)D * 64 * 2 + (size_t)D * 4 + 4 * 16 * (64 * sizeof(OutT) + 16);
+  constexpr size_t lds = (size_t)D * 64 * 2 + (size_t)D * 4 + NW * 16 * (64 * sizeof(OutT) + 16);
   const int per_cu = (int)(CU_LDS_BYTES / lds) > 0 ? (int)(CU_LDS_BYTES / lds) : 1;
   const int cus = device_cus() > 0 ? device_cus() : 256;
   const int64_t cap = (int64_t)cus * per_cu;
   if (wgs > cap) wgs = cap;
-  hipLaunchKernelGGL((lift_kernel<InT, OutT, D>), dim3((unsigned)wgs), dim3(256), 0, st, (const InT*)x, rows, xs, normalize,
+  hipLaunchKernelGGL((lift_kernel<InT, OutT, D>), dim3((unsigned)wgs), dim3(64 * NW), 0, st, (const InT*)x, rows, xs, normalize,
                      (const __bf16*)omega, phase, inv_tau, (OutT*)out, os);
 }
 
