@@ -229,6 +229,13 @@ size_t kdn_scan_bwd_workspace_bytes(const kdn_scan_bwd_args* a);
  * gradients with the lift's backward. */
 int kdn_delta_scan_bwd(const kdn_scan_bwd_args* a, void* stream);
 
+/* kdn_delta_scan_bwd with the reverse carry on aux_stream, beside the forward carry on `stream` (the two
+ * carries are independent given the per-chunk recompute); the gradients wait for both.  Same workspace;
+ * results equal kdn_delta_scan_bwd's up to the summation order of its LDS reductions.  aux_stream NULL
+ * (or equal to `stream`) is kdn_delta_scan_bwd.  Both streams should have default priority.  Replaces
+ * kernels/fused_kernel_deltanet.py:168-179, like kdn_delta_scan_bwd. */
+int kdn_delta_scan_bwd_streams(const kdn_scan_bwd_args* a, void* stream, void* aux_stream);
+
 /* One of the four launches of kdn_delta_scan_bwd (phase 0: per-chunk recompute, 1: forward carry,
  * 2: reverse carry, 3: gradients), for callers that time or schedule them; on one workspace they must
  * run in the order 0, 1, 2, 3 (stream order or events).  Same arguments and checks. */

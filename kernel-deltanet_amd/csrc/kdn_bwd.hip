@@ -1082,12 +1082,28 @@ __global__ void __launch_bounds__(256) bwd_omega_t_kernel(const __bf16* omega, b
 }
 
 // Launches phases [first, last] (0 prep, 1 forward carry, 2 reverse carry, 3 gradients) in order.
+// The two carries read only what prep wrote and write disjoint record fields (S, XK, W forward; G, X,
+// DW reverse), so given an auxiliary stream the reverse carry runs there beside the forward carry: each
+// chain occupies B*H*4 workgroups, a quarter of the GPU at B*H = 16.
 template <class P, typename InT>
-static int bwd_launch(const Params& p, int first, int last, hipStream_t st) {
+static int bwd_launch(const Params& p, int first, int last, hipStream_t st, hipStream_t aux) {
   const dim3 chunk_grid((unsigned)p.nch, (unsigned)p.H, (unsigned)p.B);
   const unsigned chain_wgs = (unsigned)(((p.B * p.H + 7) / 8) * 8 * 4);
+  const bool side = aux && aux != st && first <= 1 && last >= 2;
+  EventSet evs;
+  if (side && evs.create(2) != KDN_OK) return KDN_ERR_DEVICE;
   for (int ph = first; ph <= last; ++ph) {
     if (ph == 0) hipLaunchKernelGGL((bwd_prep_kernel<P, InT>), chunk_grid, dim3(256), 0, st, p);
+    if (ph == 1 && side) {
+      if (hipEventRecord(evs.ev[0], st) != hipSuccess || hipStreamWaitEvent(aux, evs.ev[0], 0) != hipSuccess)
+        return KDN_ERR_DEVICE;
+      hipLaunchKernelGGL((bwd_chain_kernel<P, true>), dim3(chain_wgs), dim3(256), 0, aux, p);
+      hipLaunchKernelGGL((bwd_chain_kernel<P, false>), dim3(chain_wgs), dim3(256), 0, st, p);
+      if (hipEventRecord(evs.ev[1], aux) != hipSuccess || hipStreamWaitEvent(st, evs.ev[1], 0) != hipSuccess)
+        return KDN_ERR_DEVICE;
+      ph = 2;
+      continue;
+    }
     if (ph == 1) hipLaunchKernelGGL((bwd_chain_kernel<P, false>), dim3(chain_wgs), dim3(256), 0, st, p);
     if (ph == 2) hipLaunchKernelGGL((bwd_chain_kernel<P, true>), dim3(chain_wgs), dim3(256), 0, st, p);
     if (ph == 3) {
@@ -1098,7 +1114,7 @@ static int bwd_launch(const Params& p, int first, int last, hipStream_t st) {
   return launch_status();
 }
 
-static int bwd_run(const kdn_scan_bwd_args* a, int first, int last, void* stream) {
+static int bwd_run(const kdn_scan_bwd_args* a, int first, int last, void* stream, void* aux_stream) {
   const int rc = bwd_check(a);
   if (rc != KDN_OK) return rc;
   const kdn_scan_args* f = a->fwd;
@@ -1130,18 +1146,24 @@ static int bwd_run(const kdn_scan_bwd_args* a, int first, int last, void* stream
   p.ws = reinterpret_cast<float*>(a->workspace);
   p.omt = reinterpret_cast<const bf16x8*>(static_cast<unsigned char*>(a->workspace) +
                                           (size_t)(f->B * f->H * p.nch) * Rec::floats * sizeof(float));
-  const hipStream_t st = as_stream(stream);
+  const hipStream_t st = as_stream(stream), aux = aux_stream ? as_stream(aux_stream) : nullptr;
   // bf16 inputs: the D = 512 contractions take bf16 operands with fp32 accumulation, the forward's
   // policy for bf16 inputs; the lift and the 64 x 64 chunk algebra stay in fp32 MFMA.
-  if (f->in_dtype == KDN_DTYPE_BF16) return bwd_launch<PrecBF16, __bf16>(p, first, last, st);
-  return bwd_launch<PrecF32, float>(p, first, last, st);
+  if (f->in_dtype == KDN_DTYPE_BF16) return bwd_launch<PrecBF16, __bf16>(p, first, last, st, aux);
+  return bwd_launch<PrecF32, float>(p, first, last, st, aux);
 }
 
-extern "C" int kdn_delta_scan_bwd(const kdn_scan_bwd_args* a, void* stream) { return bwd_run(a, 0, 3, stream); }
+extern "C" int kdn_delta_scan_bwd(const kdn_scan_bwd_args* a, void* stream) {
+  return bwd_run(a, 0, 3, stream, nullptr);
+}
+
+extern "C" int kdn_delta_scan_bwd_streams(const kdn_scan_bwd_args* a, void* stream, void* aux_stream) {
+  return bwd_run(a, 0, 3, stream, aux_stream);
+}
 
 extern "C" int kdn_scan_bwd_phase(const kdn_scan_bwd_args* a, int phase, void* stream) {
   if (phase < 0 || phase > 3) return KDN_ERR_INVALID_ARGUMENT;
-  return bwd_run(a, phase, phase, stream);
+  return bwd_run(a, phase, phase, stream, nullptr);
 }
 
 }  // namespace kdn

@@ -45,4 +45,19 @@ int general_scan_validate(const kdn_scan_args* a);
 size_t general_scan_workspace_bytes(const kdn_scan_args* a);
 int general_scan(const kdn_scan_args* a, void* stream);
 
+// Events of a multi-stream launch sequence, released when the call returns (destroying an event whose
+// record is still pending is allowed; its resources are freed once it completes).
+struct EventSet {
+  hipEvent_t ev[16];
+  int n = 0;
+  int create(int count) {
+    for (; n < count; ++n)
+      if (hipEventCreateWithFlags(&ev[n], hipEventDisableTiming) != hipSuccess) return KDN_ERR_DEVICE;
+    return KDN_OK;
+  }
+  ~EventSet() {
+    for (int i = 0; i < n; ++i) (void)hipEventDestroy(ev[i]);
+  }
+};
+
 }  // namespace kdn

@@ -587,21 +587,6 @@ static int run_scan(const kdn_scan_args* a, const RunSpec& r) {
   return KDN_OK;
 }
 
-// Events of the pipelined scan, released when the call returns (destroying an event whose record is
-// still pending is allowed; its resources are freed once it completes).
-struct EventSet {
-  hipEvent_t ev[16];
-  int n = 0;
-  int create(int count) {
-    for (; n < count; ++n)
-      if (hipEventCreateWithFlags(&ev[n], hipEventDisableTiming) != hipSuccess) return KDN_ERR_DEVICE;
-    return KDN_OK;
-  }
-  ~EventSet() {
-    for (int i = 0; i < n; ++i) (void)hipEventDestroy(ev[i]);
-  }
-};
-
 // Segments rotate through `nbuf` workspace buffers.  The state chain runs on `st` (the caller's stream);
 // prep runs on `aux` and output on `aux_out` (the same stream as prep when only one auxiliary stream is
 // given, in the order prep(s+1), output(s)), so that while state(s) occupies its B*H*d_v/16 workgroups the

@@ -44,6 +44,7 @@ EXPORTED = (
     "kdn_pool_free_bytes",
     "kdn_scan_bwd_workspace_bytes",
     "kdn_delta_scan_bwd",
+    "kdn_delta_scan_bwd_streams",
     "kdn_scan_bwd_phase",
 )
 
@@ -197,6 +198,8 @@ def lib() -> ctypes.CDLL:
             L.kdn_scan_bwd_workspace_bytes.restype = sz
             L.kdn_delta_scan_bwd.argtypes = [ctypes.POINTER(ScanBwdArgs), vp]
             L.kdn_delta_scan_bwd.restype = ci
+            L.kdn_delta_scan_bwd_streams.argtypes = [ctypes.POINTER(ScanBwdArgs), vp, vp]
+            L.kdn_delta_scan_bwd_streams.restype = ci
             L.kdn_fwht_lift_factored.argtypes = [vp, i64, i64, ci, vp, vp, vp, vp, cf, vp, i64, ci, vp]
             L.kdn_fwht_lift_factored.restype = ci
             L.kdn_scan_bwd_phase.argtypes = [ctypes.POINTER(ScanBwdArgs), ci, vp]

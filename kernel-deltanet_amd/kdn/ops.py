@@ -380,11 +380,33 @@ class ScanBackwardPlan:
     def _st(self, stream):
         return stream if stream is not None else torch.cuda.current_stream(self.device)
 
-    def run(self, stream=None):
+    def _tensors(self):
+        out, todo = [], [self._keep, self.outputs, self.workspace]
+        while todo:
+            t = todo.pop()
+            if isinstance(t, torch.Tensor):
+                out.append(t)
+            elif isinstance(t, (tuple, list)):
+                todo.extend(t)
+        return out
+
+    def run(self, stream=None, concurrent_carries: bool = True):
+        """Issues the whole backward on `stream` (default: the current stream).  With
+        concurrent_carries the reverse carry runs on the device's auxiliary stream 0 beside the forward
+        carry (kdn_delta_scan_bwd_streams), else all four launches run in order on `stream`
+        (kdn_delta_scan_bwd)."""
         st = self._st(stream)
         with torch.cuda.device(self.device):
-            N.check(N.lib().kdn_delta_scan_bwd(ctypes.byref(self.args), ctypes.c_void_p(st.cuda_stream)),
-                    "kdn_delta_scan_bwd")
+            if concurrent_carries:
+                aux = aux_stream(self.device, 0)
+                for t in self._tensors():
+                    t.record_stream(aux)
+                N.check(N.lib().kdn_delta_scan_bwd_streams(ctypes.byref(self.args), ctypes.c_void_p(st.cuda_stream),
+                                                           ctypes.c_void_p(aux.cuda_stream)),
+                        "kdn_delta_scan_bwd_streams")
+            else:
+                N.check(N.lib().kdn_delta_scan_bwd(ctypes.byref(self.args), ctypes.c_void_p(st.cuda_stream)),
+                        "kdn_delta_scan_bwd")
         return self.outputs
 
     def phase(self, i: int, stream=None):

@@ -189,3 +189,22 @@ def test_backward_rejects_unsupported_shapes(proj):
     with pytest.raises(ValueError, match="unsupported"):
         ops.scan_backward(q, q, v, beta, None, proj.device_omega(DEV), proj.device_phase(DEV), proj.tau_star_inv,
                           torch.randn(1, 64, 1, 32, device=DEV))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_carries_on_two_streams_equal_one_stream(proj, dtype):
+    # kdn_delta_scan_bwd_streams runs the reverse carry on an auxiliary stream beside the forward carry;
+    # its results equal kdn_delta_scan_bwd's up to the summation order of the gradient kernel's LDS
+    # float atomics (which already varies between two runs on one stream).  Issued twice back to back
+    # so that the second call's prep overwrites records only after the first call's carries have read them.
+    q, k, v, beta, lam, s0, dy, ds = make(2, 1500, 4, dtype, seed=21)
+    plan = ops.ScanBackwardPlan(q.to(DEV), k.to(DEV), v.to(DEV), beta.to(DEV), lam.to(DEV), proj.device_omega(DEV),
+                                proj.device_phase(DEV), proj.tau_star_inv, dy.to(DEV), ds.to(DEV),
+                                initial_state=s0.to(DEV))
+    ref = [t.clone() for t in plan.run(concurrent_carries=False)]
+    for _ in range(2):
+        got = plan.run(concurrent_carries=True)
+    torch.cuda.synchronize()
+    names = ("dq", "dk", "dv", "dbeta", "ddecay", "dinit")
+    errs = {n: rel(g.cpu().numpy(), r.cpu().numpy()) for n, g, r in zip(names, got, ref)}
+    assert all(e < 1e-4 for e in errs.values()), errs
