@@ -97,8 +97,9 @@ __global__ void __launch_bounds__((64 * LiftWaves<InT, OutT, D>::value)) lift_ke
   __shared__ bf16x8 s_omega[NT * 2 * 64];    // [t][kb][lane] A fragments, D*64*2 bytes
   __shared__ __attribute__((aligned(16))) float s_phase_rev[D];           // phase / (2 pi)
   // Per-wave staging of 16 rows x 64 features of output, rows padded by 16 bytes.
-  constexpr int SRS = 64 * (int)sizeof(OutT) + 16;  // row stride in bytes
-  constexpr int SCPR = 64 * (int)sizeof(OutT) / 16;  // 16-byte chunks per staged row
+  constexpr int TG = 128 / (16 * (int)sizeof(OutT));  // feature tiles per staged group: 128 bytes of a row
+  constexpr int SRS = 16 * TG * (int)sizeof(OutT) + 16;  // row stride in bytes
+  constexpr int SCPR = 16 * TG * (int)sizeof(OutT) / 16;  // 16-byte chunks per staged row
   __shared__ __attribute__((aligned(16))) unsigned char s_stage[NW][16 * SRS];
 
   const int lane = threadIdx.x & 63;
@@ -202,14 +203,15 @@ __global__ void __launch_bounds__((64 * LiftWaves<InT, OutT, D>::value)) lift_ke
     ss = sum_over_lane_groups(ss);
     // phi = amp * c ; out = phi / (||phi|| + 1e-8)
     const float scale = amp / (amp * sqrtf(ss) + 1e-8f);
-    // Store 64 features of the 16 rows at a time through the wave's staging tile, so that every lane
-    // writes 16 contiguous bytes and each store instruction covers whole 128-byte lines of rows.
+    // Store 128 bytes of each of the 16 rows at a time (64 bf16 or 32 fp32 features) through the wave's
+    // staging tile, so that every lane writes 16 contiguous bytes and each store instruction covers
+    // whole 128-byte lines of rows.
     unsigned char* stg = s_stage[wave];
 #pragma unroll
-    for (int g = 0; g < NT / 4; ++g) {
+    for (int g = 0; g < NT / TG; ++g) {
 #pragma unroll
-      for (int tp = 0; tp < 4; ++tp) {
-        const int t = 4 * g + tp;
+      for (int tp = 0; tp < TG; ++tp) {
+        const int t = TG * g + tp;
         float v[4] = {c[t][0] * scale, c[t][1] * scale, c[t][2] * scale, c[t][3] * scale};
         store4<OutT>(reinterpret_cast<OutT*>(stg + (lane & 15) * SRS) + 16 * tp + 4 * (lane >> 4), v);
       }
@@ -218,7 +220,7 @@ __global__ void __launch_bounds__((64 * LiftWaves<InT, OutT, D>::value)) lift_ke
         const int q = 64 * j + lane, r = q / SCPR, ch = q % SCPR;
         const u32x4 val = *reinterpret_cast<const u32x4*>(stg + r * SRS + 16 * ch);
         const int64_t grow = tile * 16 + r;
-        if (grow < rows) *reinterpret_cast<u32x4*>(reinterpret_cast<unsigned char*>(out + grow * os + 64 * g) + 16 * ch) = val;
+        if (grow < rows) *reinterpret_cast<u32x4*>(reinterpret_cast<unsigned char*>(out + grow * os + 16 * TG * g) + 16 * ch) = val;
       }
     }
   }
@@ -231,7 +233,7 @@ static void launch_lift(const void* x, int64_t rows, int64_t xs, int normalize, 
   constexpr int NW = LiftWaves<InT, OutT, D>::value;
   int64_t wgs = (ntiles + NW - 1) / NW;
   // one round of resident workgroups (as many per CU as the LDS allows); the kernel loops over tiles
-  constexpr size_t lds = (size_t)D * 64 * 2 + (size_t)D * 4 + NW * 16 * (64 * sizeof(OutT) + 16);
+  constexpr size_t lds = (size_t)D * 64 * 2 + (size_t)D * 4 + NW * 16 * (128 + 16);
   const int per_cu = (int)(CU_LDS_BYTES / lds) > 0 ? (int)(CU_LDS_BYTES / lds) : 1;
   const int cus = device_cus() > 0 ? device_cus() : 256;
   const int64_t cap = (int64_t)cus * per_cu;
