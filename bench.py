@@ -384,7 +384,10 @@ def bench_backward(args, dev):
         "data": "synthetic (seeded N(0,1) q/k/v, sigmoid(N(0,1)) beta, N(0,1) dL/dy; projection seed 42)",
         "config": {"workload": f"backward of config3 (one layer, B={B}, H={H}, T={T}, d_k=64->D={D}, d_v={dv}, "
                                f"bf16 q/k/v, fp32 beta, lambda=1)", "B": B, "H": H, "T": T, "D": D, "d_v": dv,
-                   "workspace_bytes": plan.workspace.numel(), "parallelism": "single GPU"},
+                   "workspace_bytes": plan.workspace.numel(), "parallelism": "single GPU",
+                   "schedule": "recompute, then the forward carry on the launch stream beside the reverse carry "
+                               "on an auxiliary stream, then gradients (kdn_delta_scan_bwd_streams); the "
+                               "per-phase times below are measured one phase at a time"},
         "roofline": {"bound": "mfma", "achieved": achieved, "peak": MFMA_BF16_PEAK / 1e12, "unit": "TFLOP/s",
                      "frac": achieved / (MFMA_BF16_PEAK / 1e12), "traffic": None, "kernel": dom},
         "phases": phases,
