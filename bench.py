@@ -64,29 +64,46 @@ def read_pmc(path: str) -> dict:
     return out
 
 
-def cpu_baseline(q, k, v, beta, T_sample: int) -> dict:
-    """Oracle fp32 chunked restatement (heads folded into batch) on the first T_sample tokens."""
+def cpu_model() -> str:
+    """The host CPU's model name (what lscpu prints as "Model name"), from /proc/cpuinfo."""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.lower().startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(q, k, v, beta, T_sample: int, decay=None, runs: int = 3) -> dict:
+    """Oracle fp32 chunked restatement (heads folded into batch) on the first T_sample tokens; the median
+    of `runs` timed runs after a one-chunk warm-up."""
     from oracle import lift as ol
     from oracle import scan as osc
 
     torch.set_num_threads(len(os.sched_getaffinity(0)))
     B, T, H, _ = q.shape
     f = lambda t: t[:, :T_sample].float().permute(0, 2, 1, 3).reshape(B * H, T_sample, -1).contiguous()
-    fb = lambda t: t[:, :T_sample].float().permute(0, 2, 1).reshape(B * H, T_sample).contiguous()
+    fb = lambda t: None if t is None else t[:, :T_sample].float().permute(0, 2, 1).reshape(B * H, T_sample).contiguous()
     proj = ol.make_projection(64, 512, 42)
-    args = (f(q), f(k), f(v), fb(beta), None, proj, C, None, torch.float32)
+    args = (f(q), f(k), f(v), fb(beta), fb(decay), proj, C, None, torch.float32)
     osc.chunked_forward(*[a[:, :C] if isinstance(a, torch.Tensor) else a for a in args])  # warm-up
-    t0 = time.perf_counter()
-    osc.chunked_forward(*args)
-    dt = time.perf_counter() - t0
+    times = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        osc.chunked_forward(*args)
+        times.append(time.perf_counter() - t0)
+    dt = sorted(times)[len(times) // 2]
     return {"value": B * T_sample / dt, "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
+            "cpu_model": cpu_model(), "runs_s": [round(t, 3) for t in times],
             "sample": f"oracle fp32 chunked restatement (torch CPU, heads folded into batch) on the first "
-                      f"{T_sample} tokens of the same B={B}, H={H} inputs; {dt:.2f} s"}
+                      f"{T_sample} tokens of the same B={B}, H={H} inputs; median of {runs} runs, {dt:.2f} s"}
 
 
-def synthetic_inputs(B: int, T: int, H: int, dv: int, dev) -> tuple:
-    """q, k, v ~ N(0,1) (bf16) and beta = sigmoid(N(0,1)) (fp32) from one generator seeded 1234, drawn in
-    that order; on the host for up to 2^24 head-tokens, on the device beyond (config 4)."""
+def synthetic_inputs(B: int, T: int, H: int, dv: int, dev, decay: str = "none") -> tuple:
+    """q, k, v ~ N(0,1) (bf16), beta = sigmoid(N(0,1)) (fp32) and, with decay "sigmoid", lambda =
+    sigmoid(N(0,1)) (fp32) from one generator seeded 1234, drawn in that order; on the host for up to 2^24
+    head-tokens, on the device beyond (config 4).  decay "none" is lambda = 1 (returned as None)."""
     big = B * T * H > (1 << 24)
     where = dev if big else "cpu"
     g = torch.Generator(device=where).manual_seed(1234)
@@ -94,7 +111,8 @@ def synthetic_inputs(B: int, T: int, H: int, dv: int, dev) -> tuple:
     k = torch.randn(B, T, H, 64, generator=g, device=where).to(torch.bfloat16)
     v = torch.randn(B, T, H, dv, generator=g, device=where).to(torch.bfloat16)
     beta = torch.sigmoid(torch.randn(B, T, H, generator=g, device=where))
-    return q, k, v, beta
+    lam = torch.sigmoid(torch.randn(B, T, H, generator=g, device=where)) if decay == "sigmoid" else None
+    return q, k, v, beta, lam
 
 
 def main():
@@ -114,6 +132,9 @@ def main():
                     help="chunks per segment (0 = the library default)")
     ap.add_argument("--serial", action="store_true",
                     help="serial schedule (kdn_delta_scan_fwd) instead of the pipelined one")
+    ap.add_argument("--decay", default="none", choices=("none", "sigmoid"),
+                    help="decay lambda: none (lambda = 1, the headline) or sigmoid(N(0,1)) per head-token "
+                         "(the decay variant reported separately; configs 3 and 4)")
     ap.add_argument("--cpu-tokens", type=int, default=65536, help="tokens in the CPU-baseline sample (0 = skip)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain device copy of known size (for PMC byte-counter calibration)")
@@ -160,10 +181,11 @@ def bench_scan(args, dev):
     B = args.B if args.B is not None else (32 if cfg == 4 else 1)
     T = args.T if args.T is not None else 65536
     H, dv, D = args.H, args.dv, 512
-    q, k, v, beta = synthetic_inputs(B, T, H, dv, dev)
+    q, k, v, beta, lam = synthetic_inputs(B, T, H, dv, dev, args.decay)
     proj = FastWalshHadamardProjection(64, D, 42)
     qd, kd, vd, bd = q.to(dev), k.to(dev), v.to(dev), beta.to(dev)
-    plan = ops.ScanPlan(qd, kd, vd, bd, None, proj.device_omega(dev), proj.device_phase(dev), proj.tau_star_inv,
+    ld = None if lam is None else lam.to(dev)
+    plan = ops.ScanPlan(qd, kd, vd, bd, ld, proj.device_omega(dev), proj.device_phase(dev), proj.tau_star_inv,
                         segment_chunks=args.segment_chunks, pipelined=not args.serial)
     nchunks, seg = plan.nchunks, plan.segment_chunks
     stream = torch.cuda.current_stream(dev)
@@ -247,7 +269,8 @@ def bench_scan(args, dev):
         dom = max(phases, key=lambda p: phases[p]["ms"])
     achieved = phases[dom]["tflops"]
     pmc_path = args.pmc or os.path.join(REPO, "profiles", f"pmc_config{cfg}.txt")
-    pmc = read_pmc(pmc_path) if (cfg == 3 and B == 1 and T == 65536 and H == 16 and dv == 64) or args.pmc else {}
+    pmc = read_pmc(pmc_path) if (cfg == 3 and B == 1 and T == 65536 and H == 16 and dv == 64 and args.decay == "none") \
+        or args.pmc else {}
     traffic = None
     if f"{dom}_fetch_kib" in pmc and f"{dom}_write_kib" in pmc and "copy_fetch_kib" in pmc and "copy_write_kib" in pmc:
         copy_bytes = pmc.get("copy_bytes", 256 << 20)
@@ -271,7 +294,9 @@ def bench_scan(args, dev):
         "dtype": "bf16",
         "data": "synthetic (seeded N(0,1) q/k/v, sigmoid(N(0,1)) beta; projection seed 42)",
         "config": {"workload": f"{name}, B={B}, H={H}, T={T}, d_k=64->D={D}, "
-                               f"d_v={dv}, chunk 64, bf16 q/k/v, fp32 beta and state, lambda=1",
+                               f"d_v={dv}, chunk 64, bf16 q/k/v, fp32 beta and state, "
+                               + ("lambda=1" if lam is None else "lambda=sigmoid(N(0,1)) fp32 (decay variant)"),
+                   "decay": args.decay,
                    "B": B, "H": H, "T": T, "D": D, "d_v": dv, "chunk": C, "segment_chunks": seg,
                    "schedule": "pipelined (state chain on the launch stream, prep and output on two auxiliary "
                                "streams)" if plan.pipelined else "serial", "parallelism": "single GPU"},
@@ -286,7 +311,7 @@ def bench_scan(args, dev):
         Ts = min(args.cpu_tokens, T)
         Bs = 1 if cfg == 4 else B
         out["cpu_baseline"] = cpu_baseline(q[:Bs, :Ts].cpu(), k[:Bs, :Ts].cpu(), v[:Bs, :Ts].cpu(),
-                                           beta[:Bs, :Ts].cpu(), Ts)
+                                           beta[:Bs, :Ts].cpu(), Ts, None if lam is None else lam[:Bs, :Ts].cpu())
     else:
         out["cpu_baseline"] = None
     print(json.dumps(out), flush=True)
@@ -339,7 +364,7 @@ def bench_backward(args, dev):
     B = args.B if args.B is not None else 1
     T = args.T if args.T is not None else 65536
     H, dv, D = args.H, args.dv, 512
-    q, k, v, beta = synthetic_inputs(B, T, H, dv, dev)
+    q, k, v, beta, _ = synthetic_inputs(B, T, H, dv, dev)
     qd, kd, vd, bd = q.to(dev), k.to(dev), v.to(dev), beta.to(dev)
     gd = torch.Generator(device=dev).manual_seed(4321)
     dy = torch.randn(B, T, H, dv, generator=gd, device=dev)

@@ -17,9 +17,10 @@
  * Reference interfaces replaced (paths relative to jatin-yadav-acad/kernel-deltanet):
  *   kdn_build_omega     <- FastWalshHadamardProjection.__init__ Omega build, kernels/fwht.py:94-111
  *   kdn_fwht            <- fast_walsh_hadamard_transform, kernels/fwht.py:25-45
- *   kdn_fwht_lift       <- pybind fwht_forward(input, rademacher_bits, D_lifted, tau_star_inv),
+ *   kdn_fwht_lift_bits  <- pybind fwht_forward(input, rademacher_bits, D_lifted, tau_star_inv),
  *                          kernels/fwht_cuda.cpp:29-32, with the semantics of the torch branch of
  *                          FastWalshHadamardProjection.forward, kernels/fwht.py:122-131
+ *   kdn_fwht_lift       <- the same forward with Omega passed as its bf16 table (kernels/fwht.py:122-131)
  *   kdn_delta_scan_fwd  <- fused_chunked_deltanet_forward, kernels/fused_kernel_deltanet.py:31-155
  *   kdn_scan_prep       <- the S-independent part of its chunk loop, kernels/fused_kernel_deltanet.py:95-122
  *   kdn_scan_state      <- the state carry, kernels/fused_kernel_deltanet.py:128-129,144-149
@@ -74,12 +75,28 @@ int kdn_fwht(const void* x, int64_t rows, int64_t x_row_stride, int n, int dtype
  *   phi = sqrt(2/D) cos(xh Omega^T * inv_tau + phase),   out = phi / (||phi||_2 + 1e-8)
  * omega is the bf16 [D][d_k] table from kdn_build_omega (exact in bf16); phase is fp32 [D].
  * Products are exact (bf16 operands; fp32 inputs are split into three bf16 parts), sums in fp32.
- * Replaces kernels/fwht_cuda.cpp:29-32 with the semantics of kernels/fwht.py:122-131.
+ * The torch branch of FastWalshHadamardProjection.forward, kernels/fwht.py:122-131, with Omega given as
+ * its bf16 table (the scan and callers that keep Omega resident); kdn_fwht_lift_bits below is the same
+ * lift at the reference's native boundary, kernels/fwht_cuda.cpp:29-32.
  * d_k must be 64; D in {128, 256, 512}.  x, out, omega and phase 16-byte aligned; row strides in bytes
  * multiples of 16. */
 int kdn_fwht_lift(const void* x, int64_t rows, int64_t x_row_stride, int x_dtype, int normalize_input,
                   const void* omega_bf16, const float* phase, int d_k, int D, float inv_tau,
                   void* out, int64_t out_row_stride, int out_dtype, void* stream);
+
+/* The same lift at the reference's native boundary (ABI 1.5): pybind fwht_forward(input, rademacher_bits,
+ * D_lifted, tau_star_inv) of kernels/fwht_cuda.cpp:11-32 takes the packed sign table, not Omega.  Here
+ * rademacher_bits is that table, device int64 [D_lifted / 64][3] (column s = stage d1, d2, d3; bit i set
+ * <=> entry i is -1; the module buffer of kernels/fwht.py:74-83); every workgroup builds Omega from it in
+ * LDS with wave64 butterflies (the sign flips fused into the transform), then lifts as kdn_fwht_lift.
+ * The torch-branch semantics this lift implements (kernels/fwht.py:122-131) also need the module's phases
+ * b, passed as `phase` (device fp32 [D_lifted]); the reference's CUDA function has no phase argument.
+ * normalize_input as kdn_fwht_lift (0 in the reference's call).  d_k must be 64; D_lifted in
+ * {128, 256, 512}; x, out and phase 16-byte aligned, rademacher_bits 8-byte aligned; row strides in bytes
+ * multiples of 16. */
+int kdn_fwht_lift_bits(const void* x, int64_t rows, int64_t x_row_stride, int x_dtype, int d_k,
+                       const int64_t* rademacher_bits, int D_lifted, float tau_star_inv, const float* phase,
+                       int normalize_input, void* out, int64_t out_row_stride, int out_dtype, void* stream);
 
 /* Factored lift for d_k = 128 -> D = 1024 (ABI 1.4): out[r][0:512] = lift(x[r][0:64]; omega1, phase1),
  * out[r][512:1024] = lift(x[r][64:128]; omega2, phase2) (each as kdn_fwht_lift without input
@@ -257,8 +274,10 @@ typedef struct kdn_ragged_args {
   int in_dtype, out_dtype, normalize_input, rule;
   float inv_tau;
   const int64_t* cu_seqlens;       /* device [num_seqs + 1] */
-  const int64_t* cu_seqlens_host;  /* the same offsets in host memory (scheduling: counts, longest) */
-  const int32_t* slots;            /* device [num_seqs]: distinct state slots */
+  const int64_t* cu_seqlens_host;  /* the same offsets in host memory (scheduling: counts, longest); they
+                                    * must equal the device copy (entries the two disagree on are
+                                    * skipped, never read unwritten) */
+  const int32_t* slots;            /* device [num_seqs]: distinct state slots (see num_slots) */
   const void* q;   int64_t q_stride[2];   /* [token][head] element strides; innermost contiguous */
   const void* k;   int64_t k_stride[2];
   const void* v;   int64_t v_stride[2];
@@ -268,6 +287,9 @@ typedef struct kdn_ragged_args {
   float* states;   int64_t state_stride[4];       /* [slot][head][feature][value] */
   void* y;         int64_t y_stride[2];
   void* workspace; size_t workspace_bytes;
+  int64_t num_slots;   /* (ABI 1.5) slots in `states`; required.  A sequence whose slot lies outside
+                        * [0, num_slots) -- a negative slot is the padding convention -- is skipped on the
+                        * device: its state is not touched and its y rows are not written. */
 } kdn_ragged_args;
 
 /* Workspace bytes kdn_ragged_step needs (0 if the arguments are invalid); reads the shape fields and

@@ -1057,8 +1057,22 @@ static int bwd_check(const kdn_scan_bwd_args* a) {
   if (!f->q || !f->k || !f->v || !f->beta || !f->omega_bf16 || !f->phase) return KDN_ERR_INVALID_ARGUMENT;
   if (!a->dy || !a->dq || !a->dk || !a->dv || !a->dbeta) return KDN_ERR_INVALID_ARGUMENT;
   if (a->ddecay && !f->decay) return KDN_ERR_INVALID_ARGUMENT;
-  if (f->q_stride[2] < 0 || f->k_stride[2] < 0 || f->v_stride[2] < 0) return KDN_ERR_INVALID_ARGUMENT;
-  if (!aligned(f->omega_bf16, 8)) return KDN_ERR_MISALIGNED;
+  for (int i = 0; i < 3; ++i)
+    if (f->q_stride[i] < 0 || f->k_stride[i] < 0 || f->v_stride[i] < 0 || f->beta_stride[i] < 0 ||
+        a->dy_stride[i] < 0)
+      return KDN_ERR_INVALID_ARGUMENT;
+  // the forward's pointer rules: 16-byte rows of q, k, v (element loads here, but the same buffers feed
+  // the forward's vector loads), 16-byte phase (read four at a time) and Omega rows; fp32 gradients and
+  // dL/dy at least 4-byte aligned
+  const size_t isz = dtype_size(f->in_dtype);
+  if (!aligned(f->q, 16) || !aligned(f->k, 16) || !aligned(f->v, 16)) return KDN_ERR_MISALIGNED;
+  for (int i = 0; i < 3; ++i)
+    if (((f->q_stride[i] * (int64_t)isz) % 16) != 0 || ((f->k_stride[i] * (int64_t)isz) % 16) != 0 ||
+        ((f->v_stride[i] * (int64_t)isz) % 16) != 0)
+      return KDN_ERR_MISALIGNED;
+  if (!aligned(f->omega_bf16, 16) || !aligned(f->phase, 16)) return KDN_ERR_MISALIGNED;
+  if (!aligned(a->dy, 4) || !aligned(a->dq, 4) || !aligned(a->dk, 4) || !aligned(a->dv, 4) || !aligned(a->dbeta, 4))
+    return KDN_ERR_MISALIGNED;
   return KDN_OK;
 }
 

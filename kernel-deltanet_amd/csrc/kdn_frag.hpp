@@ -97,6 +97,15 @@ __device__ __forceinline__ typename P::frag load_frag_nt(const void* base, int l
 // Read-only streaming loads that bypass nothing: plain global loads (the workspace is re-read once).
 __device__ __forceinline__ f32x4 ld4(const float* p) { return *reinterpret_cast<const f32x4*>(p); }
 
+// Orders one wave's LDS accesses at this point for exchanges between its lanes (a lane reading what
+// another lane of the same wave stored): the hardware performs a wave's LDS operations in order, so no
+// instruction is emitted at wavefront scope, but the compiler may no longer move loads or stores across
+// it (it could otherwise reorder accesses that look disjoint from one lane's point of view).
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+}
+
 // 64-lane butterfly partner exchange: value held by lane (lane ^ H).
 template <int H>
 __device__ __forceinline__ float xor_shuffle(float v) {

@@ -87,9 +87,16 @@ struct LiftWaves {
 //   A = Omega fragments (f rows, k depth)   read from LDS (staged once per workgroup)
 //   B = x fragments      (k depth, r column) read from global, 16/32 bytes per lane
 // Accumulator tile (f-tile t): lane l holds Phi^T[16t + 4(l>>4) + i][row (l & 15)].
-template <typename InT, typename OutT, int D>
+//
+// FROM_BITS: Omega is not read from memory; each workgroup builds it in LDS from the packed Rademacher
+// table bits[D/64][3] (the reference's native boundary, kernels/fwht_cuda.cpp:29-32): wave w takes
+// columns j of block m in turn, column j of H d1 is (-1)^popcount(lane & j) d1_j in lane `lane`, then the
+// d2 / d3 sign flips and two wave64 butterflies (fwht_wave) give Omega[64m + lane][j] * 8 exactly, and
+// each lane writes its element into the A fragment that the staged copy would hold.
+template <typename InT, typename OutT, int D, bool FROM_BITS>
 __global__ void __launch_bounds__((64 * LiftWaves<InT, OutT, D>::value)) lift_kernel(const InT* __restrict__ x, int64_t rows, int64_t xs, int normalize,
-                                                   const __bf16* __restrict__ omega, const float* __restrict__ phase,
+                                                   const __bf16* __restrict__ omega, const int64_t* __restrict__ bits,
+                                                   const float* __restrict__ phase,
                                                    float inv_tau, OutT* __restrict__ out, int64_t os) {
   constexpr int NT = D / 16;                 // feature tiles
   constexpr int NW = LiftWaves<InT, OutT, D>::value;
@@ -106,9 +113,24 @@ __global__ void __launch_bounds__((64 * LiftWaves<InT, OutT, D>::value)) lift_ke
   const int wave = threadIdx.x >> 6;
 
   // Stage Omega as A fragments: lane l of fragment (t, kb) holds Omega[16t + (l&15)][32kb + 8(l>>4) .. +8].
-  for (int idx = threadIdx.x; idx < NT * 2 * 64; idx += 64 * NW) {
-    const int l = idx & 63, tk = idx >> 6, t = tk >> 1, kb = tk & 1;
-    s_omega[idx] = *reinterpret_cast<const bf16x8*>(omega + (int64_t)(16 * t + (l & 15)) * 64 + 32 * kb + 8 * (l >> 4));
+  if constexpr (FROM_BITS) {
+    __bf16* so = reinterpret_cast<__bf16*>(s_omega);
+    for (int cj = wave; cj < D; cj += NW) {
+      const int m = cj >> 6, j = cj & 63;
+      const int64_t b1 = bits[3 * m + 0], b2 = bits[3 * m + 1], b3 = bits[3 * m + 2];
+      float v = (__builtin_popcount(lane & j) & 1) ? -sign_of(b1, j) : sign_of(b1, j);
+      v *= sign_of(b2, lane);
+      v = fwht_wave<64>(v, lane);
+      v *= sign_of(b3, lane);
+      v = fwht_wave<64>(v, lane);
+      const int f = 64 * m + lane;  // feature row of this lane's element
+      so[(((f >> 4) * 2 + (j >> 5)) * 64 + (f & 15) + 16 * ((j & 31) >> 3)) * 8 + (j & 7)] = (__bf16)(v * 0.125f);
+    }
+  } else {
+    for (int idx = threadIdx.x; idx < NT * 2 * 64; idx += 64 * NW) {
+      const int l = idx & 63, tk = idx >> 6, t = tk >> 1, kb = tk & 1;
+      s_omega[idx] = *reinterpret_cast<const bf16x8*>(omega + (int64_t)(16 * t + (l & 15)) * 64 + 32 * kb + 8 * (l >> 4));
+    }
   }
   for (int f = threadIdx.x; f < D; f += 64 * NW) s_phase_rev[f] = phase[f] * 0.15915494309189535f;
   __syncthreads();
@@ -215,6 +237,9 @@ __global__ void __launch_bounds__((64 * LiftWaves<InT, OutT, D>::value)) lift_ke
         float v[4] = {c[t][0] * scale, c[t][1] * scale, c[t][2] * scale, c[t][3] * scale};
         store4<OutT>(reinterpret_cast<OutT*>(stg + (lane & 15) * SRS) + 16 * tp + 4 * (lane >> 4), v);
       }
+      // The read-back below takes rows other lanes wrote, and the next group's stores overwrite rows
+      // other lanes read.
+      wave_lds_sync();
 #pragma unroll
       for (int j = 0; j < 16 * SCPR / 64; ++j) {
         const int q = 64 * j + lane, r = q / SCPR, ch = q % SCPR;
@@ -222,13 +247,14 @@ __global__ void __launch_bounds__((64 * LiftWaves<InT, OutT, D>::value)) lift_ke
         const int64_t grow = tile * 16 + r;
         if (grow < rows) *reinterpret_cast<u32x4*>(reinterpret_cast<unsigned char*>(out + grow * os + 16 * TG * g) + 16 * ch) = val;
       }
+      wave_lds_sync();
     }
   }
 }
 
 template <typename InT, typename OutT, int D>
-static void launch_lift(const void* x, int64_t rows, int64_t xs, int normalize, const void* omega, const float* phase,
-                        float inv_tau, void* out, int64_t os, hipStream_t st) {
+static void launch_lift(const void* x, int64_t rows, int64_t xs, int normalize, const void* omega, const int64_t* bits,
+                        const float* phase, float inv_tau, void* out, int64_t os, hipStream_t st) {
   const int64_t ntiles = (rows + 15) / 16;
   constexpr int NW = LiftWaves<InT, OutT, D>::value;
   int64_t wgs = (ntiles + NW - 1) / NW;
@@ -238,20 +264,53 @@ static void launch_lift(const void* x, int64_t rows, int64_t xs, int normalize, 
   const int cus = device_cus() > 0 ? device_cus() : 256;
   const int64_t cap = (int64_t)cus * per_cu;
   if (wgs > cap) wgs = cap;
-  hipLaunchKernelGGL((lift_kernel<InT, OutT, D>), dim3((unsigned)wgs), dim3(64 * NW), 0, st, (const InT*)x, rows, xs, normalize,
-                     (const __bf16*)omega, phase, inv_tau, (OutT*)out, os);
+  if (bits)
+    hipLaunchKernelGGL((lift_kernel<InT, OutT, D, true>), dim3((unsigned)wgs), dim3(64 * NW), 0, st, (const InT*)x, rows, xs,
+                       normalize, nullptr, bits, phase, inv_tau, (OutT*)out, os);
+  else
+    hipLaunchKernelGGL((lift_kernel<InT, OutT, D, false>), dim3((unsigned)wgs), dim3(64 * NW), 0, st, (const InT*)x, rows, xs,
+                       normalize, (const __bf16*)omega, nullptr, phase, inv_tau, (OutT*)out, os);
 }
 
 template <typename InT, typename OutT>
 static int dispatch_lift_D(int D, const void* x, int64_t rows, int64_t xs, int normalize, const void* omega,
-                           const float* phase, float inv_tau, void* out, int64_t os, hipStream_t st) {
+                           const int64_t* bits, const float* phase, float inv_tau, void* out, int64_t os, hipStream_t st) {
   switch (D) {
-    case 128: launch_lift<InT, OutT, 128>(x, rows, xs, normalize, omega, phase, inv_tau, out, os, st); break;
-    case 256: launch_lift<InT, OutT, 256>(x, rows, xs, normalize, omega, phase, inv_tau, out, os, st); break;
-    case 512: launch_lift<InT, OutT, 512>(x, rows, xs, normalize, omega, phase, inv_tau, out, os, st); break;
+    case 128: launch_lift<InT, OutT, 128>(x, rows, xs, normalize, omega, bits, phase, inv_tau, out, os, st); break;
+    case 256: launch_lift<InT, OutT, 256>(x, rows, xs, normalize, omega, bits, phase, inv_tau, out, os, st); break;
+    case 512: launch_lift<InT, OutT, 512>(x, rows, xs, normalize, omega, bits, phase, inv_tau, out, os, st); break;
     default: return KDN_ERR_UNSUPPORTED;
   }
   return launch_status();
+}
+
+// The lift with Omega given as the bf16 table (omega) or as the packed sign table (bits); exactly one is
+// non-null.  Argument checks of kdn_fwht_lift / kdn_fwht_lift_bits.
+static int fwht_lift_impl(const void* x, int64_t rows, int64_t x_row_stride, int x_dtype, int normalize_input,
+                          const void* omega_bf16, const int64_t* bits, const float* phase, int d_k, int D,
+                          float inv_tau, void* out, int64_t out_row_stride, int out_dtype, void* stream) {
+  if (!x || !(omega_bf16 || bits) || !phase || !out || rows < 0) return KDN_ERR_INVALID_ARGUMENT;
+  if (!valid_dtype(x_dtype) || !valid_dtype(out_dtype)) return KDN_ERR_INVALID_ARGUMENT;
+  if (d_k != 64) return KDN_ERR_UNSUPPORTED;
+  if (D != 128 && D != 256 && D != 512) return KDN_ERR_UNSUPPORTED;
+  if (x_row_stride < d_k || out_row_stride < D) return KDN_ERR_INVALID_ARGUMENT;
+  if (!(inv_tau == inv_tau)) return KDN_ERR_INVALID_ARGUMENT;
+  // 16-byte vector accesses: row starts of x and out, omega rows, phase; 8-byte words of the sign table.
+  if (!aligned(x, 16) || !aligned(out, 16) || !aligned(phase, 16)) return KDN_ERR_MISALIGNED;
+  if ((omega_bf16 && !aligned(omega_bf16, 16)) || (bits && !aligned(bits, 8))) return KDN_ERR_MISALIGNED;
+  if ((x_row_stride * (int64_t)dtype_size(x_dtype)) % 16 != 0) return KDN_ERR_MISALIGNED;
+  if ((out_row_stride * (int64_t)dtype_size(out_dtype)) % 16 != 0) return KDN_ERR_MISALIGNED;
+  if (rows == 0) return KDN_OK;
+  hipStream_t st = as_stream(stream);
+  const int nz = normalize_input ? 1 : 0;
+  if (x_dtype == KDN_DTYPE_BF16) {
+    if (out_dtype == KDN_DTYPE_BF16)
+      return dispatch_lift_D<__bf16, __bf16>(D, x, rows, x_row_stride, nz, omega_bf16, bits, phase, inv_tau, out, out_row_stride, st);
+    return dispatch_lift_D<__bf16, float>(D, x, rows, x_row_stride, nz, omega_bf16, bits, phase, inv_tau, out, out_row_stride, st);
+  }
+  if (out_dtype == KDN_DTYPE_BF16)
+    return dispatch_lift_D<float, __bf16>(D, x, rows, x_row_stride, nz, omega_bf16, bits, phase, inv_tau, out, out_row_stride, st);
+  return dispatch_lift_D<float, float>(D, x, rows, x_row_stride, nz, omega_bf16, bits, phase, inv_tau, out, out_row_stride, st);
 }
 
 }  // namespace kdn
@@ -301,27 +360,17 @@ extern "C" int kdn_fwht(const void* x, int64_t rows, int64_t x_row_stride, int n
 extern "C" int kdn_fwht_lift(const void* x, int64_t rows, int64_t x_row_stride, int x_dtype, int normalize_input,
                              const void* omega_bf16, const float* phase, int d_k, int D, float inv_tau, void* out,
                              int64_t out_row_stride, int out_dtype, void* stream) {
-  if (!x || !omega_bf16 || !phase || !out || rows < 0) return KDN_ERR_INVALID_ARGUMENT;
-  if (!valid_dtype(x_dtype) || !valid_dtype(out_dtype)) return KDN_ERR_INVALID_ARGUMENT;
-  if (d_k != 64) return KDN_ERR_UNSUPPORTED;
-  if (D != 128 && D != 256 && D != 512) return KDN_ERR_UNSUPPORTED;
-  if (x_row_stride < d_k || out_row_stride < D) return KDN_ERR_INVALID_ARGUMENT;
-  if (!(inv_tau == inv_tau)) return KDN_ERR_INVALID_ARGUMENT;
-  // 16-byte vector accesses: row starts of x and out, omega rows, phase.
-  if (!aligned(x, 16) || !aligned(out, 16) || !aligned(omega_bf16, 16) || !aligned(phase, 16)) return KDN_ERR_MISALIGNED;
-  if ((x_row_stride * (int64_t)dtype_size(x_dtype)) % 16 != 0) return KDN_ERR_MISALIGNED;
-  if ((out_row_stride * (int64_t)dtype_size(out_dtype)) % 16 != 0) return KDN_ERR_MISALIGNED;
-  if (rows == 0) return KDN_OK;
-  hipStream_t st = as_stream(stream);
-  const int nz = normalize_input ? 1 : 0;
-  if (x_dtype == KDN_DTYPE_BF16) {
-    if (out_dtype == KDN_DTYPE_BF16)
-      return dispatch_lift_D<__bf16, __bf16>(D, x, rows, x_row_stride, nz, omega_bf16, phase, inv_tau, out, out_row_stride, st);
-    return dispatch_lift_D<__bf16, float>(D, x, rows, x_row_stride, nz, omega_bf16, phase, inv_tau, out, out_row_stride, st);
-  }
-  if (out_dtype == KDN_DTYPE_BF16)
-    return dispatch_lift_D<float, __bf16>(D, x, rows, x_row_stride, nz, omega_bf16, phase, inv_tau, out, out_row_stride, st);
-  return dispatch_lift_D<float, float>(D, x, rows, x_row_stride, nz, omega_bf16, phase, inv_tau, out, out_row_stride, st);
+  if (!omega_bf16) return KDN_ERR_INVALID_ARGUMENT;
+  return fwht_lift_impl(x, rows, x_row_stride, x_dtype, normalize_input, omega_bf16, nullptr, phase, d_k, D, inv_tau,
+                        out, out_row_stride, out_dtype, stream);
+}
+
+extern "C" int kdn_fwht_lift_bits(const void* x, int64_t rows, int64_t x_row_stride, int x_dtype, int d_k,
+                                  const int64_t* rademacher_bits, int D_lifted, float tau_star_inv, const float* phase,
+                                  int normalize_input, void* out, int64_t out_row_stride, int out_dtype, void* stream) {
+  if (!rademacher_bits) return KDN_ERR_INVALID_ARGUMENT;
+  return fwht_lift_impl(x, rows, x_row_stride, x_dtype, normalize_input, nullptr, rademacher_bits, phase, d_k,
+                        D_lifted, tau_star_inv, out, out_row_stride, out_dtype, stream);
 }
 
 namespace kdn {

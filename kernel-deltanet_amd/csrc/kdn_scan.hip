@@ -316,6 +316,7 @@ __global__ void __launch_bounds__(256) state_kernel(ScanParams p) {
   // its initial state copied through (below, no chunk is run).
   if (nloc == 0 && !(sq.len <= 0 && p.chunk0 == 0)) return;
   const int64_t sl = p.slots ? (int64_t)p.slots[b] : b;
+  if (sl < 0) return;  // a skipped sequence of a ragged step (its state is not touched)
 
   const int lane = threadIdx.x & 63;
   // The wave index is uniform across the wave; reading it into a scalar register lets every
@@ -441,7 +442,8 @@ __global__ void __launch_bounds__(256) output_kernel(ScanParams p) {
     }
   }
   // Rows of the wave's tile: (16 rows) x (DV / 8 pieces of 8 elements); the tile was written by this
-  // wave only, and a wave's LDS accesses are performed in order.
+  // wave only.
+  wave_lds_sync();
   constexpr int PIECES = 16 * (DV / 8);
 #pragma unroll
   for (int base = 0; base < PIECES; base += 64) {
@@ -852,3 +854,4 @@ extern "C" int kdn_scan_state(const kdn_scan_args* a, int64_t chunk0, int64_t nc
 extern "C" int kdn_scan_output(const kdn_scan_args* a, int64_t chunk0, int64_t nchunks, void* stream) {
   return run_phase(a, chunk0, nchunks, PHASE_OUTPUT, stream);
 }
+

@@ -23,13 +23,25 @@ constexpr int SRV_DK = 64;   // input features
 // ---- split ----------------------------------------------------------------------------------------
 // One workgroup: thread t counts the decode / prefill sequences of its contiguous range, an inclusive
 // Hillis-Steele scan over the 1024 counts gives each range its output offsets, and the ranges are then
-// written in sequence order.
+// written in sequence order.  The lists are first filled with skip entries (slot -1, no tokens), so
+// that a launch sized from host counts that differ from the device offsets reads no unwritten entry.
+// A sequence whose slot lies outside [0, num_slots) (a negative slot is the padding convention) keeps
+// its place in its list with slot -1 and no tokens: the decode and scan kernels skip it, its state is
+// not touched and its y rows are not written.
 __global__ void __launch_bounds__(1024) ragged_split_kernel(const int64_t* __restrict__ cu, const int32_t* __restrict__ slots,
-                                                            int64_t n, int64_t* __restrict__ dec_row,
+                                                            int64_t n, int64_t num_slots, int64_t* __restrict__ dec_row,
                                                             int32_t* __restrict__ dec_slot, int64_t* __restrict__ pre_lo,
                                                             int64_t* __restrict__ pre_hi, int32_t* __restrict__ pre_slot) {
   __shared__ int64_t s_d[1024], s_p[1024];
   const int t = threadIdx.x;
+  for (int64_t i = t; i < n; i += 1024) {
+    dec_row[i] = 0;
+    dec_slot[i] = -1;
+    pre_lo[i] = 0;
+    pre_hi[i] = 0;
+    pre_slot[i] = -1;
+  }
+  __syncthreads();
   const int64_t per = (n + 1023) / 1024;
   const int64_t i0 = t * per, i1 = (i0 + per < n) ? i0 + per : n;
   int64_t nd = 0, np = 0;
@@ -51,14 +63,16 @@ __global__ void __launch_bounds__(1024) ragged_split_kernel(const int64_t* __res
   int64_t od = s_d[t] - nd, op = s_p[t] - np;
   for (int64_t i = i0; i < i1; ++i) {
     const int64_t lo = cu[i], hi = cu[i + 1];
+    const int32_t sl = slots[i];
+    const bool ok = sl >= 0 && (int64_t)sl < num_slots;
     if (hi - lo == 1) {
       dec_row[od] = lo;
-      dec_slot[od] = slots[i];
+      dec_slot[od] = ok ? sl : -1;
       ++od;
     } else if (hi - lo >= 2) {
-      pre_lo[op] = lo;
-      pre_hi[op] = hi;
-      pre_slot[op] = slots[i];
+      pre_lo[op] = ok ? lo : 0;
+      pre_hi[op] = ok ? hi : 0;
+      pre_slot[op] = ok ? sl : -1;
       ++op;
     }
   }
@@ -119,8 +133,9 @@ __global__ void __launch_bounds__(DecodeThreads<DV>::value) decode_kernel(Decode
 
   const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
   const int64_t i = blockIdx.x, h = blockIdx.y, c0 = (int64_t)blockIdx.z * DV;
-  const int64_t row = p.rows[i];
   const int64_t sl = p.slots[i];
+  if (sl < 0) return;  // padding, an out-of-range slot or an entry the split did not fill (uniform)
+  const int64_t row = p.rows[i];
 
   // The state elements of thread (g, j) and its scalar inputs are loaded first: they do not depend on
   // the lift, so their memory latency overlaps it.
@@ -242,7 +257,7 @@ static int ragged_plan(const kdn_ragged_args* a, RaggedPlan& pl) {
   if (a->d_k != SRV_DK || a->D != SRV_D) return KDN_ERR_UNSUPPORTED;
   if (a->d_v != 16 && a->d_v != 32 && a->d_v != 64 && a->d_v != 128) return KDN_ERR_UNSUPPORTED;
   if (!(a->inv_tau == a->inv_tau)) return KDN_ERR_INVALID_ARGUMENT;
-  if (a->num_seqs > 0 && !a->cu_seqlens_host) return KDN_ERR_INVALID_ARGUMENT;
+  if (a->num_seqs > 0 && (!a->cu_seqlens_host || a->num_slots <= 0)) return KDN_ERR_INVALID_ARGUMENT;
   for (int64_t i = 0; i < a->num_seqs; ++i) {
     const int64_t lo = a->cu_seqlens_host[i], hi = a->cu_seqlens_host[i + 1];
     if (lo < 0 || hi < lo) return KDN_ERR_INVALID_ARGUMENT;
@@ -314,8 +329,8 @@ extern "C" int kdn_ragged_step(const kdn_ragged_args* a, void* stream, void* aux
   int32_t* dec_slot = (int32_t*)w;           w += round256(n * 8);
   int32_t* pre_slot = (int32_t*)w;           w += round256(n * 8);
   w += round256(n * 4);
-  hipLaunchKernelGGL(ragged_split_kernel, dim3(1), dim3(1024), 0, st, a->cu_seqlens, a->slots, a->num_seqs, dec_row,
-                     dec_slot, pre_lo, pre_hi, pre_slot);
+  hipLaunchKernelGGL(ragged_split_kernel, dim3(1), dim3(1024), 0, st, a->cu_seqlens, a->slots, a->num_seqs,
+                     a->num_slots, dec_row, dec_slot, pre_lo, pre_hi, pre_slot);
   rc = launch_status();
   if (rc != KDN_OK) return rc;
   if (pl.n_dec > 0) {

@@ -23,6 +23,7 @@ EXPORTED = (
     "kdn_build_omega",
     "kdn_fwht",
     "kdn_fwht_lift",
+    "kdn_fwht_lift_bits",
     "kdn_fwht_lift_factored",
     "kdn_scan_workspace_bytes",
     "kdn_delta_scan_fwd",
@@ -111,6 +112,7 @@ class RaggedArgs(ctypes.Structure):
         ("states", ctypes.c_void_p), ("state_stride", _i64x4),
         ("y", ctypes.c_void_p), ("y_stride", _i64x2),
         ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_size_t),
+        ("num_slots", _i64),
     ]
 
 
@@ -162,6 +164,8 @@ def lib() -> ctypes.CDLL:
             L.kdn_fwht.restype = ci
             L.kdn_fwht_lift.argtypes = [vp, i64, i64, ci, ci, vp, vp, ci, ci, cf, vp, i64, ci, vp]
             L.kdn_fwht_lift.restype = ci
+            L.kdn_fwht_lift_bits.argtypes = [vp, i64, i64, ci, ci, vp, ci, cf, vp, ci, vp, i64, ci, vp]
+            L.kdn_fwht_lift_bits.restype = ci
             L.kdn_scan_workspace_bytes.argtypes = [ctypes.POINTER(ScanArgs)]
             L.kdn_scan_workspace_bytes.restype = sz
             L.kdn_delta_scan_fwd.argtypes = [ctypes.POINTER(ScanArgs), vp]

@@ -92,6 +92,34 @@ def lift(x: torch.Tensor, omega_bf16: torch.Tensor, phase: torch.Tensor, inv_tau
     return out.view(*x.shape[:-1], D)
 
 
+def lift_bits(x: torch.Tensor, rademacher_bits: torch.Tensor, phase: torch.Tensor, inv_tau: float,
+              normalize: bool = False, out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+    """(..., 64) -> (..., D) feature lift from the packed [D/64, 3] sign table (kdn_fwht_lift_bits): each
+    workgroup builds Omega in LDS with wave64 butterflies, then lifts as `lift`.  D = 64 * rows of the
+    table; phase is the (D,) phase vector b."""
+    require_device(x, "lift_bits")
+    d_k = x.shape[-1]
+    D = 64 * rademacher_bits.shape[0]
+    if rademacher_bits.dim() != 2 or rademacher_bits.shape[1] != 3 or phase.numel() != D:
+        raise ValueError(f"lift_bits: expects rademacher_bits (D/64, 3) and phase (D,); got "
+                         f"{tuple(rademacher_bits.shape)}, {tuple(phase.shape)}")
+    out_dtype = x.dtype if out_dtype is None else out_dtype
+    x2 = _rows(x, d_k)
+    if (x2.stride(0) * x2.element_size()) % 16 or x2.data_ptr() % 16:
+        x2 = x2.contiguous()
+    bits = rademacher_bits.to(device=x.device, dtype=torch.int64).contiguous()
+    ph = phase.to(device=x.device, dtype=torch.float32).contiguous()
+    out = torch.empty(x2.shape[0], D, dtype=out_dtype, device=x.device)
+    with torch.cuda.device(x.device):
+        N.check(N.lib().kdn_fwht_lift_bits(ctypes.c_void_p(x2.data_ptr()), x2.shape[0], x2.stride(0),
+                                           _tag(x.dtype, "lift_bits"), d_k, ctypes.c_void_p(bits.data_ptr()), D,
+                                           float(inv_tau), ctypes.c_void_p(ph.data_ptr()), 1 if normalize else 0,
+                                           ctypes.c_void_p(out.data_ptr()), out.stride(0),
+                                           _tag(out_dtype, "lift_bits output"), ctypes.c_void_p(_stream(x.device))),
+                "kdn_fwht_lift_bits")
+    return out.view(*x.shape[:-1], D)
+
+
 def lift_factored(x: torch.Tensor, omega1: torch.Tensor, phase1: torch.Tensor, omega2: torch.Tensor,
                   phase2: torch.Tensor, inv_tau: float, out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
     """(..., 128) -> (..., 1024) factored lift (kdn_fwht_lift_factored): the two halves of x lifted by the
@@ -339,6 +367,8 @@ class ScanBackwardPlan:
         fm = _features_on(FeatureMap(omega_bf16, phase), dev, H)
         D = fm.dim(q)
         if initial_state is not None:
+            if tuple(initial_state.shape) != (B, H, D, d_v):
+                raise ValueError(f"scan_backward: initial_state must be (B, H, D, d_v) = {(B, H, D, d_v)}")
             initial_state = initial_state.to(device=dev, dtype=torch.float32)
         if d_final_state is not None:
             d_final_state = d_final_state.to(device=dev, dtype=torch.float32)
@@ -454,7 +484,13 @@ class _Scan(torch.autograd.Function):
 def scan_autograd(q, k, v, beta, decay, omega_bf16, phase, inv_tau, normalize: bool = False,
                   initial_state: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor]:
     """`scan` (default schedule) recorded for autograd: gradients flow to q, k, v, beta, decay and
-    initial_state through kdn_delta_scan_bwd.  Returns (y (B, T, H, d_v), final_state (B, H, D, d_v))."""
+    initial_state through kdn_delta_scan_bwd.  Returns (y (B, T, H, d_v), final_state (B, H, D, d_v)).
+    The backward covers d_k = 64, D = 512, d_v = 64; other shapes are rejected here, before the forward
+    runs, rather than inside .backward()."""
+    d_k, D, d_v = q.shape[-1], omega_bf16.shape[-2], v.shape[-1]
+    if (d_k, D, d_v) != (64, 512, 64):
+        raise ValueError(f"scan with gradients: the backward supports d_k = 64, D = 512, d_v = 64 (got d_k = {d_k}, "
+                         f"D = {D}, d_v = {d_v}); run the forward under torch.no_grad() or detach the inputs")
     return _Scan.apply(q, k, v, beta, decay, initial_state, omega_bf16, phase, inv_tau, normalize)
 
 
@@ -581,6 +617,18 @@ def forward_only(what: str, outputs, inputs):
 # ------------------------------------------------------------------------------------------------ serving
 
 
+def check_host_slots(slots, n_slots: int) -> None:
+    """Rejects per-sequence state slots given on the host that the step must not run with: a slot at or
+    above n_slots, or a slot shared by two sequences (they would race).  Negative slots are padding.
+    (Device slots are not checked here, which would synchronise; the kernels skip out-of-range ones.)"""
+    sl = torch.as_tensor(slots, dtype=torch.int64).reshape(-1)
+    if sl.numel() and int(sl.max()) >= n_slots:
+        raise ValueError(f"ragged_step: slot {int(sl.max())} is outside the {n_slots} state slots")
+    live = sl[sl >= 0]
+    if torch.unique(live).numel() != live.numel():
+        raise ValueError("ragged_step: two sequences of one step share a state slot")
+
+
 def _ragged_args(q, k, v, beta, decay, cu_seqlens, slots, states, omega_bf16, phase, inv_tau, normalize, rule, y,
                  out_dtype, cu_seqlens_device):
     """Checks the arguments of a ragged step and fills kdn_ragged_args; returns (args, tensors it points to)."""
@@ -597,6 +645,9 @@ def _ragged_args(q, k, v, beta, decay, cu_seqlens, slots, states, omega_bf16, ph
     n = cu_host.numel() - 1
     if n < 0 or int(cu_host[-1]) > q.shape[0]:
         raise ValueError("ragged_step: cu_seqlens must hold num_seqs + 1 offsets within the token count")
+    n_slots = states.shape[0]
+    if not (isinstance(slots, torch.Tensor) and slots.is_cuda):
+        check_host_slots(slots, n_slots)
     slots_d = torch.as_tensor(slots).to(device=dev, dtype=torch.int32).contiguous()
     if slots_d.numel() != n:
         raise ValueError("ragged_step: one slot per sequence")
@@ -631,6 +682,7 @@ def _ragged_args(q, k, v, beta, decay, cu_seqlens, slots, states, omega_bf16, ph
     a.omega_bf16, a.phase = om.data_ptr(), ph.data_ptr()
     a.states, a.state_stride = states.data_ptr(), N._i64x4(*states.stride())
     a.y, a.y_stride = y.data_ptr(), N._i64x2(*y.stride()[:2])
+    a.num_slots = n_slots
     return a, (q, k, v, beta, decay, om, ph, states, y, cu_d, slots_d, cu_host)
 
 
@@ -661,8 +713,12 @@ def ragged_step(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, beta: torch.T
     q, k (tokens, H, d_k) and v (tokens, H, d_v) share a dtype; beta, decay (tokens, H) float32 (decay may
     be None); cu_seqlens: num_seqs + 1 token offsets (host list/array or tensor); slots (num_seqs,) the
     distinct state slots; states (slots_total, H, D, d_v) float32, any strides, updated in place.
+    A negative slot marks a padding sequence: it is skipped (no state touched, its y rows left as they
+    are).  Slots given on the host are checked (range, distinctness) before anything is launched.
     A serving loop that keeps its batch metadata on the device passes slots as a device int32 tensor and
-    cu_seqlens_device (the same offsets, device int64); nothing is then copied to the device per call.
+    cu_seqlens_device (the same offsets as cu_seqlens, device int64); nothing is then copied to the device
+    per call, and the kernels skip any sequence whose slot is outside the slab instead of checking on the
+    host (which would synchronise).
     Without `workspace` each call allocates one (ragged_workspace_bytes; several GB for long prefills)
     from torch's caching allocator; a loop passes one buffer instead.
     Returns y (tokens, H, d_v).

@@ -5,8 +5,10 @@ Same public names, constructor arguments, buffers and forward semantics as the r
 rademacher_bits (non-persistent), b and Omega, and forward(x) = phi / (||phi|| + 1e-8) with
 phi = sqrt(2/D) cos(x Omega^T / tau* + b), tau* = d_k^(1/4).
 
-The forward runs the gfx950 MFMA lift kernel (kdn_fwht_lift); the device copy of Omega is built from
-the packed sign table by the wave64 butterfly kernel (kdn_build_omega).  Device tensors only.
+The forward runs the gfx950 lift kernel at the reference's native boundary (kdn_fwht_lift_bits, the
+replacement of kernel_deltanet_cuda.fwht_forward): every workgroup builds Omega in LDS from the packed
+sign table with wave64 butterflies, then projects on MFMA.  The scan's kernels read a resident bf16 copy
+of Omega instead, built once per device by the same butterflies (kdn_build_omega).  Device tensors only.
 """
 from __future__ import annotations
 
@@ -76,6 +78,7 @@ class FastWalshHadamardProjection(nn.Module):
         if not bool((Omega.to(torch.bfloat16).to(torch.float32) == Omega).all()):
             raise ValueError(f"seed {seed}: Omega is not exactly representable in bf16; unsupported")
         self._dev_omega = {}
+        self._dev_tables = {}
 
     def device_omega(self, device) -> torch.Tensor:
         """bf16 Omega on `device`, built once per device from the sign table by kdn_build_omega."""
@@ -89,11 +92,33 @@ class FastWalshHadamardProjection(nn.Module):
             self._dev_omega[key] = om
         return om
 
+    def _device_table(self, name: str, device, dtype) -> torch.Tensor:
+        """Buffer `name` on `device` in `dtype`: the buffer itself when it is already there (the module was
+        moved), else a copy kept per device and refreshed only when the buffer changes (load_state_dict
+        writes buffers in place, which bumps their version), so that a forward issues no host-to-device
+        copy."""
+        buf = getattr(self, name)
+        device = torch.device(device)
+        if buf.device == device or (device.index is None and buf.is_cuda):
+            return buf if buf.dtype == dtype else buf.to(dtype)
+        key = (name, device.index if device.index is not None else torch.cuda.current_device())
+        stamp = (buf.data_ptr(), buf._version)
+        hit = self._dev_tables.get(key)
+        if hit is None or hit[0] != stamp:
+            hit = (stamp, buf.to(device=device, dtype=dtype))
+            self._dev_tables[key] = hit
+        return hit[1]
+
     def device_phase(self, device) -> torch.Tensor:
-        return self.b.to(device=device, dtype=torch.float32)
+        """The phases b as float32 on `device`."""
+        return self._device_table("b", device, torch.float32)
+
+    def device_bits(self, device) -> torch.Tensor:
+        """The packed [M, 3] sign table on `device` (the argument of kdn_fwht_lift_bits)."""
+        return self._device_table("rademacher_bits", device, torch.int64)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         """(..., d_k) -> (..., D) in x's dtype (bfloat16 or float32); fp32 arithmetic inside."""
         ops.require_device(x, "FastWalshHadamardProjection")
-        return ops.lift(x, self.device_omega(x.device), self.device_phase(x.device), self.tau_star_inv,
-                        normalize=False, out_dtype=x.dtype)
+        return ops.lift_bits(x, self.device_bits(x.device), self.device_phase(x.device), self.tau_star_inv,
+                             normalize=False, out_dtype=x.dtype)

@@ -62,7 +62,7 @@ def test_args_layout_matches_c(cname, pystruct):
 def test_strerror_and_version(lib):
     for code in (0, -1, -2, -3, -4, -5, -99):
         assert len(lib.kdn_strerror(code)) > 0
-    assert lib.kdn_abi_version() == (1 << 16) | 4
+    assert lib.kdn_abi_version() == (1 << 16) | 5
 
 
 def _args(**kw):
@@ -129,6 +129,17 @@ def test_lift_fwht_omega_argument_errors_need_no_device(lib):
     assert lib.kdn_fwht(p, 0, 64, 64, 0, p, 64, None) == 0
     assert lib.kdn_build_omega(p, 32, 512, p, 1, None) == -2
     assert lib.kdn_build_omega(None, 64, 512, p, 1, None) == -1
+    # the sign-table lift (the reference's fwht_forward boundary): (x, rows, stride, dtype, d_k, bits, D, 1/tau,
+    # phase, normalize, out, out stride, out dtype, stream)
+    lb = lib.kdn_fwht_lift_bits
+    assert lb(p, 10, 64, 0, 64, None, 512, 0.35, p, 0, p, 512, 0, None) == -1     # no table
+    assert lb(p, 10, 64, 0, 64, p, 512, 0.35, None, 0, p, 512, 0, None) == -1     # no phase
+    assert lb(p, 10, 64, 0, 128, p, 512, 0.35, p, 0, p, 512, 0, None) == -2      # d_k 128
+    assert lb(p, 10, 64, 0, 64, p, 1024, 0.35, p, 0, p, 1024, 0, None) == -2     # D 1024
+    assert lb(p, 10, 64, 0, 64, p + 4, 512, 0.35, p, 0, p, 512, 0, None) == -4   # table not 8-byte aligned
+    assert lb(p, 10, 64, 0, 64, p, 512, 0.35, p + 8, 0, p, 512, 0, None) == -4   # phase not 16-byte aligned
+    assert lb(p, 10, 64, 0, 64, p, 512, float("nan"), p, 0, p, 512, 0, None) == -1
+    assert lb(p, 0, 64, 0, 64, p, 512, 0.35, p, 0, p, 512, 0, None) == 0         # no rows: nothing launched
 
 
 def test_general_width_requests_need_no_device(lib):

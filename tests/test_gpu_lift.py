@@ -130,3 +130,60 @@ def test_lift_config2_properties(proj, oproj):
     xs = torch.nn.functional.normalize(x[idx].float(), dim=-1, eps=1e-6).to(torch.bfloat16).float().numpy()
     ref = ol.lift(xs, oproj)
     assert rel_l2(out[idx.to(DEV)].float().cpu().numpy(), ref) < 1e-2
+
+
+@pytest.mark.parametrize("D", [128, 256, 512])
+@pytest.mark.parametrize("seed", [42, 7])
+@pytest.mark.parametrize("dtype,normalize", [(torch.float32, False), (torch.bfloat16, False), (torch.bfloat16, True)])
+def test_lift_bits_equals_table_lift(D, seed, dtype, normalize):
+    """kdn_fwht_lift_bits builds Omega in LDS from the sign table; with the same Omega values the lift does
+    the same arithmetic as kdn_fwht_lift, so the outputs are equal bit for bit (this pins the in-kernel
+    build, element by element, to kdn_build_omega, which is bit-exact against the oracle), and both match
+    the oracle."""
+    p = FastWalshHadamardProjection(64, D, seed)
+    op = ol.make_projection(64, D, seed)
+    g = torch.Generator().manual_seed(seed + D)
+    x = (torch.randn(1037, 64, generator=g) * 1.3).to(dtype)
+    xd = x.to(DEV)
+    a = ops.lift_bits(xd, p.device_bits(DEV), p.device_phase(DEV), p.tau_star_inv, normalize)
+    b = ops.lift(xd, p.device_omega(DEV), p.device_phase(DEV), p.tau_star_inv, normalize)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
+    xr = x.float()
+    if normalize:
+        xr = torch.nn.functional.normalize(xr, dim=-1, eps=1e-6).to(dtype).float()
+    tol = 1e-5 if dtype == torch.float32 else 1e-2
+    assert rel_l2(a.float().cpu().numpy(), ol.lift(xr.numpy(), op)) < tol
+
+
+def test_reference_call_site_shim(proj, oproj):
+    """The drop-in for the reference's extension module: kernel_deltanet_cuda.fwht_forward called with the
+    reference's argument list (kernels/fwht.py:120) plus phase=self.b, no Omega."""
+    import kernel_deltanet_cuda
+
+    p = FastWalshHadamardProjection(64, 512, 42).to(DEV)   # the reference moves the module to the GPU
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(2, 300, 64, generator=g)
+    xd = x.to(DEV)
+    out = kernel_deltanet_cuda.fwht_forward(xd.contiguous(), p.rademacher_bits, p.D, p.tau_star_inv, phase=p.b)
+    assert out.shape == (2, 300, 512) and out.dtype == torch.float32
+    ref = ol.lift(x.reshape(-1, 64).numpy(), oproj).reshape(2, 300, 512)
+    assert rel_l2(out.cpu().numpy(), ref) < 1e-5
+    # host-side tables (a module left on the CPU) are copied to the input's device
+    cpu_p = FastWalshHadamardProjection(64, 512, 42)
+    out2 = kernel_deltanet_cuda.fwht_forward(xd, cpu_p.rademacher_bits, 512, cpu_p.tau_star_inv, phase=cpu_p.b)
+    assert torch.equal(out, out2)
+    with pytest.raises(ValueError, match="phase=self.b"):
+        kernel_deltanet_cuda.fwht_forward(xd.contiguous(), p.rademacher_bits, p.D, p.tau_star_inv)
+
+
+def test_lift_bits_config2_equals_table_lift(proj):
+    """At config 2's full size (2,097,152 bf16 rows, normalised inputs) the sign-table lift equals the
+    table lift bit for bit (the latter is checked against the oracle above)."""
+    rows = 8 * 16384 * 16
+    g = torch.Generator(device=DEV).manual_seed(99)
+    x = torch.randn(rows, 64, generator=g, device=DEV).to(torch.bfloat16)
+    a = ops.lift_bits(x, proj.device_bits(DEV), proj.device_phase(DEV), proj.tau_star_inv, normalize=True)
+    b = ops.lift(x, proj.device_omega(DEV), proj.device_phase(DEV), proj.tau_star_inv, normalize=True)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)

@@ -214,3 +214,78 @@ def test_caller_workspace_reused_across_steps(proj):
         assert torch.equal(s_own, s_ws)
     with pytest.raises(ValueError):
         ops.ragged_workspace_bytes(dq, dk, dv, db, dl, [0, 1], slots, s_ws, om, ph, proj.tau_star_inv)
+
+
+def test_padding_and_out_of_range_device_slots_are_skipped(proj, oproj):
+    """Device slots are not checked on the host (that would synchronise): a negative slot (padding) and a
+    slot past the slab are skipped on the device -- their states untouched, their y rows left as they
+    were -- while the other sequences match the oracle."""
+    lens = [1, 1, 45, 1, 70, 1, 9]
+    n_slots = 10
+    q, k, v, beta, lam, cu, slots, states = make_step(lens, 2, 64, torch.float32, n_slots, seed=8)
+    bad = {1: -1, 4: n_slots + 3, 6: -7}          # decode padding, prefill past the slab, prefill padding
+    for i, s in bad.items():
+        slots[i] = s
+    sd = states.to(DEV)
+    y = torch.full((q.shape[0], 2, 64), 123.0, device=DEV)
+    ops.ragged_step(q.to(DEV), k.to(DEV), v.to(DEV), beta.to(DEV), lam.to(DEV), cu, slots.to(DEV), sd,
+                    proj.device_omega(DEV), proj.device_phase(DEV), proj.tau_star_inv, y=y,
+                    cu_seqlens_device=cu.to(DEV))
+    torch.cuda.synchronize()
+    # the oracle over the other sequences only
+    good = [i for i in range(len(lens)) if i not in bad]
+    keep = torch.tensor(good)
+    sub_cu, rows = [0], []
+    for i in good:
+        rows += list(range(int(cu[i]), int(cu[i + 1])))
+        sub_cu.append(sub_cu[-1] + lens[i])
+    rows_t = torch.tensor(rows)
+    Yr, Sr = oracle_step(q[rows_t], k[rows_t], v[rows_t], beta[rows_t], lam[rows_t], torch.tensor(sub_cu),
+                         slots[keep], states, oproj)
+    yc = y.cpu()
+    assert rel_l2(yc[rows_t].numpy(), Yr) < 1e-4
+    for i in bad:
+        assert bool((yc[int(cu[i]):int(cu[i + 1])] == 123.0).all()), i
+    used = set(int(slots[i]) for i in good)
+    S = sd.cpu()
+    for s in range(n_slots):
+        if s in used:
+            assert rel_l2(S[s].numpy(), Sr[s]) < 1e-4, s
+        else:
+            assert torch.equal(S[s], states[s]), s
+    with pytest.raises(ValueError, match="outside"):   # the same slots from the host are rejected
+        ops.ragged_step(q.to(DEV), k.to(DEV), v.to(DEV), beta.to(DEV), lam.to(DEV), cu, slots, sd,
+                        proj.device_omega(DEV), proj.device_phase(DEV), proj.tau_star_inv)
+
+
+@pytest.mark.parametrize("gather_slots", [False, True])
+def test_serving_op_without_host_sync(proj, oproj, gather_slots):
+    """hybrid_recurrent_forward with the scheduler's host offsets, their device copy and device slots (or
+    slots gathered from slot_mapping on the device): one step under torch's sync debug mode "error" (any
+    synchronising call or blocking copy raises), with results equal to the oracle's."""
+    lens = [1, 40, 1, 1, 25, 0]
+    q, k, v, beta, lam, cu, slots, states = make_step(lens, 2, 64, torch.float32, 9, seed=12)
+    slot_mapping = torch.repeat_interleave(slots.to(torch.int64), torch.tensor(lens)).to(DEV)
+    rs = states.transpose(2, 3).contiguous().to(DEV)
+    qd, kd, vd, bd, ld = (t.to(DEV) for t in (q, k, v, beta, lam))
+    cu_d, slots_d = cu.to(DEV), slots.to(DEV)
+    out = torch.empty(q.shape[0], 2, 64, device=DEV)
+    ws = torch.empty(ops.ragged_workspace_bytes(qd, kd, vd, bd, ld, cu, slots_d, rs.transpose(2, 3),
+                                                proj.device_omega(DEV), proj.device_phase(DEV), proj.tau_star_inv),
+                     dtype=torch.uint8, device=DEV)
+    kw = dict(cu_seqlens=cu, cu_seqlens_device=cu_d, seq_slots=None if gather_slots else slots_d, fwht_proj=proj,
+              workspace=ws)
+    scratch = rs.clone()
+    hybrid_recurrent_forward(qd, kd, vd, bd, ld, scratch, slot_mapping, out, **kw)   # first call: streams, tables
+    torch.cuda.synchronize()
+    torch.cuda.set_sync_debug_mode("error")
+    try:
+        hybrid_recurrent_forward(qd, kd, vd, bd, ld, rs, slot_mapping, out, **kw)
+    finally:
+        torch.cuda.set_sync_debug_mode("default")
+    torch.cuda.synchronize()
+    Yr, Sr = oracle_step(q, k, v, beta, lam, cu, slots, states, oproj)
+    assert rel_l2(out.cpu().numpy(), Yr) < 1e-4
+    for i, s in enumerate(slots.tolist()):
+        if lens[i]:
+            assert rel_l2(rs[s].transpose(1, 2).cpu().numpy(), Sr[s]) < 1e-4

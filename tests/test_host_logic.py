@@ -55,6 +55,25 @@ def test_scan_argument_checks():
         fused_chunked_deltanet_forward(q, q, torch.randn(1, 8, 64), torch.rand(1, 9), torch.rand(1, 8), p)
 
 
+def test_host_slot_checks():
+    """Slots known on the host are checked before anything is launched: in range of the slab, one
+    sequence per slot; negative slots are padding (skipped on the device)."""
+    from kdn import ops
+    from serving.vllm_kernel_deltanet_op import sequences_from_slot_mapping
+
+    ops.check_host_slots([0, 3, -1, 5, -1], 6)
+    with pytest.raises(ValueError, match="outside"):
+        ops.check_host_slots([0, 6], 6)
+    with pytest.raises(ValueError, match="share"):
+        ops.check_host_slots(torch.tensor([2, 1, 2], dtype=torch.int32), 6)
+    cu, slots = sequences_from_slot_mapping(torch.tensor([4, 4, 4, 1, -1, -1, 0, 0]), 5)
+    assert cu.tolist() == [0, 3, 4, 6, 8] and slots.tolist() == [4, 1, -1, 0]
+    with pytest.raises(ValueError, match="two separate runs"):
+        sequences_from_slot_mapping(torch.tensor([1, 1, 2, 1]), 5)
+    with pytest.raises(ValueError, match="outside"):
+        sequences_from_slot_mapping(torch.tensor([1, 1, 7]), 5)
+
+
 def test_module_surface():
     m = FusedKernelDeltaNet(d_model=64, d_kernel=512, chunk_size=64)
     assert m.fwht_proj.D == 512 and m.chunk_size == 64

@@ -25,6 +25,26 @@ def test_seeded_uniform_stream_known_values():
     np.testing.assert_allclose(u, known, atol=6e-5)
 
 
+def test_draw_order_stream_positions(proj):
+    """d1, d2, d3 and b take consecutive blocks of the seed-42 stream in that order (kernels/fwht.py:66-86:
+    three rand(M, d_k) draws, then rand(D)): with M * d_k = 512, d1 = u[0:512], d2 = u[512:1024],
+    d3 = u[1024:1536] (+1 iff u > 0.5) and b = 2 pi u[1536:2048] of one rand(2048) draw.  Known values of
+    the stream at each block start pin the positions themselves; a swap of d2 / d3 (equal in only about
+    half of their entries) or of the signs and b fails here."""
+    g = torch.Generator().manual_seed(42)
+    u = torch.rand(2048, generator=g)
+    starts = {0: [0.882269, 0.915004, 0.382864, 0.959306], 512: [0.655622, 0.118564, 0.183628, 0.084309],
+              1024: [0.778491, 0.42534, 0.712356, 0.206497], 1536: [0.572927, 0.346504, 0.241869, 0.339226]}
+    for s, vals in starts.items():
+        np.testing.assert_allclose(u[s:s + 4].numpy(), vals, atol=1e-6)
+    signs = lambda a: np.where(a.numpy() > 0.5, 1.0, -1.0).reshape(8, 64)
+    np.testing.assert_array_equal(proj["d1"], signs(u[0:512]))
+    np.testing.assert_array_equal(proj["d2"], signs(u[512:1024]))
+    np.testing.assert_array_equal(proj["d3"], signs(u[1024:1536]))
+    np.testing.assert_array_equal(np.asarray(proj["b"], np.float32), (u[1536:] * (2 * math.pi)).numpy())
+    assert 0.3 < (proj["d2"] == proj["d3"]).mean() < 0.7
+
+
 def test_first_signs_follow_rand_gt_half(proj):
     # d1 row 0 comes from the first 64 uniforms: +1 iff u > 0.5 (kernels/fwht.py:69).
     assert list(proj["d1"][0, :10]) == [1, 1, -1, 1, -1, 1, -1, 1, 1, -1]
