@@ -207,6 +207,20 @@ size_t kdn_scan_workspace_bytes_pipelined(const kdn_scan_args* a);
  * output_stream NULL (or equal to another stream) falls back to kdn_delta_scan_fwd_pipelined. */
 int kdn_delta_scan_fwd_streams(const kdn_scan_args* a, void* stream, void* prep_stream, void* output_stream);
 
+/* kdn_delta_scan_fwd without a caller workspace (ABI 1.5).  No counterpart in the reference: it is for
+ * callers that cannot allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  The workspace of one segment of chunks lives in a fixed device array
+ * of KDN_NOALLOC_SCRATCH_BYTES that the library holds on each GPU it runs on until the process ends; the
+ * call allocates nothing.  a->workspace and a->workspace_bytes are ignored; segments are as long as the
+ * array allows (at most a->segment_chunks when that is positive), so the results equal
+ * kdn_delta_scan_fwd's bit for bit.  A request whose heads need more than the array for one chunk
+ * (B * H * 2 records, 246,784 bytes each at D = 512, d_v = 64, bf16: up to B * H = 543) returns
+ * KDN_ERR_WORKSPACE_TOO_SMALL; the pre-lifted D = 1024 path returns KDN_ERR_UNSUPPORTED.  All calls on one
+ * GPU share its array: calls that overlap in time on one GPU (two streams, two host threads) race and must
+ * be serialised by the caller. */
+#define KDN_NOALLOC_SCRATCH_BYTES ((size_t)256 << 20)
+int kdn_delta_scan_fwd_noalloc(const kdn_scan_args* a, void* stream);
+
 int kdn_scan_prep(const kdn_scan_args* a, int64_t chunk0, int64_t nchunks, void* stream);
 int kdn_scan_state(const kdn_scan_args* a, int64_t chunk0, int64_t nchunks, void* stream);
 int kdn_scan_output(const kdn_scan_args* a, int64_t chunk0, int64_t nchunks, void* stream);

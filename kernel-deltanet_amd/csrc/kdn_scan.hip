@@ -23,6 +23,7 @@
 //   output (one workgroup per chunk and head): re-lifts q, Y = diag(qscale) Q S^T + P E.
 // The lifted features are stored unnormalised (cos values); per-row norms are folded into the small
 // per-token scale vectors, so a lift never has to hold a whole row before using it.
+#include <mutex>
 #include <type_traits>
 #include "kdn_frag.hpp"
 #include "kdn_internal.hpp"
@@ -855,3 +856,57 @@ extern "C" int kdn_scan_output(const kdn_scan_args* a, int64_t chunk0, int64_t n
   return run_phase(a, chunk0, nchunks, PHASE_OUTPUT, stream);
 }
 
+// ------------------------------------------------------------------------------------------------
+// Allocation-free scan (kdn_delta_scan_fwd_noalloc): the workspace of one segment lives in `scratch`, a
+// file-scope device array, instead of a caller buffer, for callers that cannot allocate.  In host code
+// the name `scratch` is only a host-side stand-in: its device address (one copy per GPU) is looked up
+// with hipGetSymbolAddress on the first call on each device, with that device current, and every use
+// below goes through that address.  The array keeps its contents between calls and nothing reads a
+// record before the segment's prep has written it, so no clearing is needed; calls that overlap on one
+// GPU share the array and race.
+namespace kdn {
+
+static __device__ __align__(256) unsigned char scratch[KDN_NOALLOC_SCRATCH_BYTES];
+
+constexpr int MAX_DEVICES = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[MAX_DEVICES] = {};
+
+// Device address of the current device's copy of `scratch`.
+static int scratch_address(void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEVICES) return KDN_ERR_DEVICE;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return KDN_ERR_DEVICE;
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return KDN_OK;
+}
+
+}  // namespace kdn
+
+extern "C" int kdn_delta_scan_fwd_noalloc(const kdn_scan_args* a, void* stream) {
+  int rc = validate(a);
+  if (rc != KDN_OK) return rc;
+  if (general_scan_applies(a)) return KDN_ERR_UNSUPPORTED;  // its workspace spans the whole sequence
+  // Segments of as many chunks as the scratch holds: one record per (head, chunk) plus a spare per head.
+  const size_t per_chunk = chunk_bytes(a) * (size_t)a->B * (size_t)a->H;
+  const int64_t fit = (int64_t)(KDN_NOALLOC_SCRATCH_BYTES / per_chunk) - 1;
+  if (fit < 1) return KDN_ERR_WORKSPACE_TOO_SMALL;  // more heads than one segment of scratch can hold
+  const int64_t nchunks = (a->T + CH - 1) / CH;
+  int64_t seg = fit < nchunks ? fit : nchunks;
+  if (a->segment_chunks > 0 && a->segment_chunks < seg) seg = a->segment_chunks;
+  void* ws = nullptr;
+  rc = scratch_address(&ws);
+  if (rc != KDN_OK) return rc;
+  kdn_scan_args b = *a;
+  b.workspace = ws;
+  b.workspace_bytes = KDN_NOALLOC_SCRATCH_BYTES;
+  b.segment_chunks = seg;
+  rc = validate_launch(&b);
+  if (rc != KDN_OK) return rc;
+  return dispatch(&b, 0, nchunks, seg, PHASE_ALL, as_stream(stream));
+}

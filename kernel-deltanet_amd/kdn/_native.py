@@ -27,6 +27,7 @@ EXPORTED = (
     "kdn_fwht_lift_factored",
     "kdn_scan_workspace_bytes",
     "kdn_delta_scan_fwd",
+    "kdn_delta_scan_fwd_noalloc",
     "kdn_scan_prep",
     "kdn_scan_state",
     "kdn_scan_output",
@@ -50,6 +51,8 @@ EXPORTED = (
 )
 
 KDN_ERR_CAPACITY = -6
+KDN_ERR_WORKSPACE_TOO_SMALL = -3
+NOALLOC_SCRATCH_BYTES = 256 << 20   # KDN_NOALLOC_SCRATCH_BYTES of include/kdn.h
 
 _i64 = ctypes.c_int64
 _i64x3 = ctypes.c_int64 * 3
@@ -170,6 +173,8 @@ def lib() -> ctypes.CDLL:
             L.kdn_scan_workspace_bytes.restype = sz
             L.kdn_delta_scan_fwd.argtypes = [ctypes.POINTER(ScanArgs), vp]
             L.kdn_delta_scan_fwd.restype = ci
+            L.kdn_delta_scan_fwd_noalloc.argtypes = [ctypes.POINTER(ScanArgs), vp]
+            L.kdn_delta_scan_fwd_noalloc.restype = ci
             L.kdn_scan_workspace_bytes_pipelined.argtypes = [ctypes.POINTER(ScanArgs)]
             L.kdn_scan_workspace_bytes_pipelined.restype = sz
             L.kdn_delta_scan_fwd_pipelined.argtypes = [ctypes.POINTER(ScanArgs), vp, vp]
