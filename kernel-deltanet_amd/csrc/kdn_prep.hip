@@ -175,7 +175,10 @@ __global__ void __launch_bounds__(256, (PrepWaves<P, FM>::value)) prep_kernel(Sc
     for (int j = 0; j < NJ; ++j) {
       // The records are read back by the state and output kernels a segment or more later, long after
       // they could still sit in L2: streaming stores keep them from evicting the state kernel's lines.
-      store_frag_nt<P>(ws + L::phiK + (size_t)(w * NJ + j) * 64 * L::FB, lane, cqk[1][j]);
+      if constexpr (IsBF16<P>::value && D == 512)
+        store_k_image(ws + L::phiK, w, j, lane, cqk[1][j]);
+      else
+        store_frag_nt<P>(ws + L::phiK + (size_t)(w * NJ + j) * 64 * L::FB, lane, cqk[1][j]);
       if (!p.relift_q) store_frag_nt<P>(ws + L::phiQ + (size_t)(w * NJ + j) * 64 * L::FB, lane, cqk[0][j]);
       s_phik[(w * NJ + j) * 64 + lane] = cqk[1][j];
     }

@@ -365,6 +365,206 @@ __global__ void __launch_bounds__(256) state_kernel(ScanParams p) {
 }
 
 // ------------------------------------------------------------------------------------------------
+// state (bf16, D = 512): the carry of state_kernel with each chunk's lifted keys streamed by a fifth
+// wave.  Waves 0-3 carry the state as state_kernel does (wave w owns features [128w, 128w + 128) of the
+// workgroup's 16 state rows; the same products in the same order, so the results are identical).  Wave 4
+// copies each chunk's K image (64 KB, written by prep in the LDS layout, store_k_image) into a two-slot
+// LDS ring with global_load_lds_dwordx4 one chunk ahead, and touches the records L2_AHEAD chunks ahead
+// so that the copies hit L2.  The carry waves issue no load of K (a burst of 24 such loads per wave and
+// chunk stalled their in-order issue): their vector-memory traffic is the small per-chunk operands (a
+// register ring two chunks ahead) and the checkpoint stores.  Four barriers per chunk:
+//   phase 1: checkpoint S^T, X_K partial from the ring        | A
+//   reduce X_K token tile w                                   | B
+//   E tile w = U~ - Tp X_K (checkpointed), refill small ops   | C
+//   S^T <- gammaC S^T + K^T (kscale o E), K^T from the ring   | D
+// Slot c % 2 is read from phase 1 to the update of chunk c; the copy of chunk c+1 into the other slot is
+// issued after barrier D of chunk c-1, and the loader waits for it before barrier D of chunk c.
+__device__ __forceinline__ PrecBF16::frag kimg_frag(const unsigned char* kw, int lane, int m, int jj) {
+  typedef __attribute__((ext_vector_type(4))) __bf16 bf16x4;
+  const unsigned char* a = kw + (size_t)((m * 4 + jj) * 64 + lane) * 8;
+  const bf16x4 lo = *reinterpret_cast<const bf16x4*>(a);
+  const bf16x4 hi = *reinterpret_cast<const bf16x4*>(a + KIMG_PLANE);
+  return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+// s_waitcnt for at most n outstanding vector-memory operations (other counters left alone).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+template <int DV>
+struct DmaState {
+  using O = StateOps<PrecBF16, 512, DV>;
+  using L = typename O::L;
+  static constexpr int NV = DV / 16;
+  static constexpr int KIMG = 4 * KIMG_SLICE;  // bytes of a chunk's K image
+  // dword loads of the L2 prefetch per loader wave: one per 128-byte line of the operand area [0, Sfr),
+  // shared by the NV workgroups of a head
+  static constexpr int L2_LOADS = (int)((L::Sfr / 128 + 64 * NV - 1) / (64 * NV));
+  __device__ static void load_small(const unsigned char* ws, int w, int lane, int n, typename O::Small& sm) {
+#pragma unroll
+    for (int jb = 0; jb < 2; ++jb) sm.tp[jb] = load_frag<PrecBF16>(ws + L::Tp + (size_t)(w * 2 + jb) * 64 * L::FB, lane);
+    sm.u = *reinterpret_cast<const f32x4*>(ws + L::U + ((size_t)(w * NV + n) * 64 + lane) * 16);
+    sm.ks = *reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(ws + L::VEC) + 64 + 16 * w + 4 * (lane >> 4));
+    sm.gC = reinterpret_cast<const float*>(ws + L::VEC)[128];
+  }
+  // The loader wave's copy of one chunk's K image into a ring slot: 64 instructions of 1 KB.
+  __device__ static void copy_k(const unsigned char* src, unsigned char* slot, int lane) {
+#pragma unroll
+    for (int i = 0; i < KIMG / 1024; ++i)
+      __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(src + (size_t)i * 1024 + lane * 16),
+                                       (__attribute__((address_space(3))) void*)(slot + i * 1024), 16, 0, 0);
+  }
+};
+
+// One chunk of a carry wave (four barriers); kw is the wave's slice of the ring slot holding the chunk,
+// sm its small operands, refilled here with those of chunk min(cl + 2, last).
+template <int DV, bool DECAY>
+__device__ __forceinline__ void dma_step(StateShared& sh, const unsigned char* kw, unsigned char* wsh, int64_t cl,
+                                         int w, int lane, int n, f32x4 (&S)[8], typename StateOps<PrecBF16, 512, DV>::Small& sm,
+                                         int64_t nloc) {
+  using P = PrecBF16;
+  using Dm = DmaState<DV>;
+  using L = typename Dm::L;
+  using frag = P::frag;
+  constexpr int NV = Dm::NV;
+  unsigned char* cur = wsh + cl * L::bytes;
+  // phase 1: checkpoint of the chunk-start S^T, X_K partial over the wave's 128 features
+  frag sf[4];
+#pragma unroll
+  for (int jj = 0; jj < 4; ++jj) {
+    sf[jj] = P::from_f32(pair_to8(S[2 * jj], S[2 * jj + 1]));
+    store_frag<P>(cur + L::Sfr + (size_t)((4 * w + jj) * NV + n) * 64 * L::FB, lane, sf[jj]);
+  }
+  f32x4 xp[4];
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    xp[m] = zero4();
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) xp[m] = P::mma(xp[m], kimg_frag(kw, lane, m, jj), sf[jj]);
+  }
+#pragma unroll
+  for (int m = 0; m < 4; ++m) sh.xp[w][m][lane] = xp[m];
+  __syncthreads();  // A
+  sh.x[w][lane] = sh.xp[0][w][lane] + sh.xp[1][w][lane] + sh.xp[2][w][lane] + sh.xp[3][w][lane];
+  __syncthreads();  // B
+  f32x4 ek = zero4();
+#pragma unroll
+  for (int jb = 0; jb < 2; ++jb) ek = P::mma(ek, sm.tp[jb], P::from_f32(pair_to8(sh.x[2 * jb][lane], sh.x[2 * jb + 1][lane])));
+  const f32x4 e = sm.u - ek;
+  sh.e[w][lane] = e * sm.ks;
+  *reinterpret_cast<f32x4*>(cur + L::Eck + ((size_t)(w * NV + n) * 64 + lane) * 16) = e;
+  const float gC = sm.gC;
+  Dm::load_small(wsh + ((cl + 2 < nloc) ? cl + 2 : nloc - 1) * L::bytes, w, lane, n, sm);
+  __syncthreads();  // C
+  frag eb[2];
+#pragma unroll
+  for (int jb = 0; jb < 2; ++jb) eb[jb] = P::from_f32(pair_to8(sh.e[2 * jb][lane], sh.e[2 * jb + 1][lane]));
+  const frag* kl = reinterpret_cast<const frag*>(kw);
+#pragma unroll
+  for (int tl = 0; tl < 8; ++tl) {
+    f32x4 acc = S[tl];
+    if constexpr (DECAY) acc = acc * gC;  // without decay gammaC is exactly 1
+#pragma unroll
+    for (int jb = 0; jb < 2; ++jb) acc = P::mma(acc, kt_frag<P>(kl, lane, tl, jb), eb[jb]);
+    S[tl] = acc;
+  }
+  __syncthreads();  // D
+}
+
+template <int DV, bool DECAY>
+__global__ void __launch_bounds__(320) state_kernel_dma(ScanParams p) {
+  using P = PrecBF16;
+  using Dm = DmaState<DV>;
+  using O = typename Dm::O;
+  using L = typename Dm::L;
+  constexpr int NV = Dm::NV;
+  __shared__ StateShared sh;
+  __shared__ __attribute__((aligned(16))) unsigned char s_ring0[Dm::KIMG];
+  __shared__ __attribute__((aligned(16))) unsigned char s_ring1[Dm::KIMG];
+  __shared__ __attribute__((aligned(16))) unsigned s_sink[64];  // target of the loader's L2-prefetch copies
+
+  // the XCD-aware grid decomposition and early exits of state_kernel (uniform per workgroup)
+  const int64_t id = blockIdx.x;
+  const int64_t xcd = id & 7, jdx = id >> 3;
+  const int n = (int)(jdx % NV);
+  const int64_t hb = (jdx / NV) * 8 + xcd;
+  if (hb >= p.B * p.H) return;
+  const int64_t b = hb / p.H, h = hb % p.H;
+  const Seq sq = seq_of(p, b);
+  const int64_t nloc = seg_chunks(p, sq);
+  if (nloc == 0 && !(sq.len <= 0 && p.chunk0 == 0)) return;
+  const int64_t sl = p.slots ? (int64_t)p.slots[b] : b;
+  if (sl < 0) return;
+
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  unsigned char* wsh = p.ws + hb * (p.nseg + 1) * L::bytes;
+
+  if (w == 4) {
+    // loader: barrier P after chunk 0 has landed, then per chunk A, B, C, (copy of the next chunk
+    // complete) D -- the carry waves' barriers, one for one
+    if (nloc == 0) return;
+    Dm::copy_k(wsh, s_ring0, lane);
+    // The loader's barriers are bare s_barrier: __syncthreads() adds a workgroup release fence, for which
+    // the compiler drains every outstanding copy into LDS; the loader orders its copies itself instead
+    // (vmcnt waits before P and D), and it touches no LDS that another wave writes.
+    wait_vmcnt<0>();
+    __builtin_amdgcn_s_barrier();  // P
+    for (int64_t cl = 0; cl < nloc; ++cl) {
+      if (cl + 1 < nloc) Dm::copy_k(wsh + (cl + 1) * L::bytes, ((cl + 1) & 1) ? s_ring1 : s_ring0, lane);
+      // L2 prefetch: one dword per 128-byte line of the operand area of chunk cl + 1 + L2_AHEAD, each lane
+      // its own line, copied into a scratch LDS word (no register result, so nothing waits for it)
+      const int64_t cp = (cl + 1 + O::L2_AHEAD < nloc) ? cl + 1 + O::L2_AHEAD : nloc - 1;
+      const unsigned char* pb = wsh + cp * L::bytes;
+#pragma unroll
+      for (int i = 0; i < Dm::L2_LOADS; ++i) {
+        const size_t off = ((size_t)((i * NV + n) * 64 + lane)) * 128;
+        __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(pb + (off < L::Sfr ? off : 0)),
+                                         (__attribute__((address_space(3))) void*)s_sink, 4, 0, 0);
+      }
+      __builtin_amdgcn_s_barrier();  // A
+      __builtin_amdgcn_s_barrier();  // B
+      __builtin_amdgcn_s_barrier();  // C
+      wait_vmcnt<Dm::L2_LOADS>();    // the copy has landed (only the prefetches issued after it may be pending)
+      __builtin_amdgcn_s_barrier();  // D
+    }
+    return;
+  }
+
+  const int r = 16 * n + (lane & 15);
+  f32x4 S[8];
+  if (p.state_in) {
+    const float* si = p.state_in + sl * p.is0 + h * p.is1 + r * p.is3;
+#pragma unroll
+    for (int tl = 0; tl < 8; ++tl)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) S[tl][i] = si[(int64_t)(16 * (8 * w + tl) + 4 * (lane >> 4) + i) * p.is2];
+  } else {
+#pragma unroll
+    for (int tl = 0; tl < 8; ++tl) S[tl] = zero4();
+  }
+  if (nloc > 0) {
+    typename O::Small sm0, sm1;
+    Dm::load_small(wsh, w, lane, n, sm0);
+    Dm::load_small(wsh + (nloc > 1 ? L::bytes : 0), w, lane, n, sm1);
+    __syncthreads();  // P: slot 0 holds chunk 0
+    for (int64_t cl = 0; cl < nloc; cl += 2) {
+      dma_step<DV, DECAY>(sh, s_ring0 + w * KIMG_SLICE, wsh, cl, w, lane, n, S, sm0, nloc);
+      if (cl + 1 >= nloc) break;
+      dma_step<DV, DECAY>(sh, s_ring1 + w * KIMG_SLICE, wsh, cl + 1, w, lane, n, S, sm1, nloc);
+    }
+  }
+  float* so = p.state_out + sl * p.os0 + h * p.os1 + r * p.os3;
+#pragma unroll
+  for (int tl = 0; tl < 8; ++tl)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) so[(int64_t)(16 * (8 * w + tl) + 4 * (lane >> 4) + i) * p.os2] = S[tl][i];
+}
+
+// ------------------------------------------------------------------------------------------------
 // output: grid (nseg, H, B), 256 threads.  Y = diag(qscale) Q S_c^T + P E for one (chunk, head).
 // Wave w keeps the lifted query fragments of token tile w in registers: read back from the record, or
 // (RELIFT, bf16 with the exact projection) lifted again from q here exactly as prep lifted them, Omega
@@ -563,9 +763,15 @@ static int launch_phase(const ScanParams& p, int phase, hipStream_t st) {
   } else if (phase == PHASE_STATE) {
     // The state workgroups are the sequential critical path: reserve enough LDS that no prep or output
     // workgroup can share their CU (a CU has 160 KB; the bf16 state kernel uses 88 KB statically).
-    const size_t excl = IsBF16<P>::value ? (size_t)STATE_EXCLUSIVE_LDS : 0;
-    if (p.decay) hipLaunchKernelGGL((state_kernel<P, D, DV, true>), dim3(state_grid(p.B, p.H, DV / 16)), dim3(256), excl, st, p);
-    else hipLaunchKernelGGL((state_kernel<P, D, DV, false>), dim3(state_grid(p.B, p.H, DV / 16)), dim3(256), excl, st, p);
+    // (bf16: the streaming kernel's 152 KB of LDS keep its CU exclusive by themselves.)
+    if constexpr (IsBF16<P>::value && D == 512) {
+      if (p.decay) hipLaunchKernelGGL((state_kernel_dma<DV, true>), dim3(state_grid(p.B, p.H, DV / 16)), dim3(320), 0, st, p);
+      else hipLaunchKernelGGL((state_kernel_dma<DV, false>), dim3(state_grid(p.B, p.H, DV / 16)), dim3(320), 0, st, p);
+    } else {
+      const size_t excl = IsBF16<P>::value ? (size_t)STATE_EXCLUSIVE_LDS : 0;
+      if (p.decay) hipLaunchKernelGGL((state_kernel<P, D, DV, true>), dim3(state_grid(p.B, p.H, DV / 16)), dim3(256), excl, st, p);
+      else hipLaunchKernelGGL((state_kernel<P, D, DV, false>), dim3(state_grid(p.B, p.H, DV / 16)), dim3(256), excl, st, p);
+    }
   } else if (IsBF16<P>::value && p.relift_q) {
     hipLaunchKernelGGL((output_kernel<P, OutT, D, DV, IsBF16<P>::value>), chunk_grid, dim3(256), 0, st, p);
   } else {
