@@ -214,7 +214,7 @@ int kdn_delta_scan_fwd_streams(const kdn_scan_args* a, void* stream, void* prep_
  * call allocates nothing.  a->workspace and a->workspace_bytes are ignored; segments are as long as the
  * array allows (at most a->segment_chunks when that is positive), so the results equal
  * kdn_delta_scan_fwd's bit for bit.  A request whose heads need more than the array for one chunk
- * (B * H * 2 records, 246,784 bytes each at D = 512, d_v = 64, bf16: up to B * H = 543) returns
+ * (B * H * 2 records, 238,592 bytes each at D = 512, d_v = 64, bf16: up to B * H = 562) returns
  * KDN_ERR_WORKSPACE_TOO_SMALL; the pre-lifted D = 1024 path returns KDN_ERR_UNSUPPORTED.  All calls on one
  * GPU share its array: calls that overlap in time on one GPU (two streams, two host threads) race and must
  * be serialised by the caller. */

@@ -220,7 +220,7 @@ __device__ __forceinline__ void state_phase2(StateShared& sh, unsigned char* cur
   for (int jb = 0; jb < 2; ++jb) ek = P::mma(ek, sm.tp[jb], P::from_f32(pair_to8(sh.x[2 * jb][lane], sh.x[2 * jb + 1][lane])));
   const f32x4 e = sm.u - ek;
   sh.e[w][lane] = e * sm.ks;
-  *reinterpret_cast<f32x4*>(cur + L::Eck + ((size_t)(w * NV + n) * 64 + lane) * 16) = e;
+  store_e_tile<P>(cur + L::Eck, (size_t)(w * NV + n), lane, e);
   __syncthreads();
 }
 
@@ -455,7 +455,7 @@ __device__ __forceinline__ void dma_step(StateShared& sh, const unsigned char* k
   for (int jb = 0; jb < 2; ++jb) ek = P::mma(ek, sm.tp[jb], P::from_f32(pair_to8(sh.x[2 * jb][lane], sh.x[2 * jb + 1][lane])));
   const f32x4 e = sm.u - ek;
   sh.e[w][lane] = e * sm.ks;
-  *reinterpret_cast<f32x4*>(cur + L::Eck + ((size_t)(w * NV + n) * 64 + lane) * 16) = e;
+  store_e_tile<P>(cur + L::Eck, (size_t)(w * NV + n), lane, e);
   const float gC = sm.gC;
   Dm::load_small(wsh + ((cl + 2 < nloc) ? cl + 2 : nloc - 1) * L::bytes, w, lane, n, sm);
   __syncthreads();  // C
@@ -630,11 +630,8 @@ __global__ void __launch_bounds__(256) output_kernel(ScanParams p) {
       for (int j = 0; j < NJ; ++j) xq = P::mma(xq, aq[j], s_s[(j * NG + g) * 64 + lane]);
       frag eb[2];
 #pragma unroll
-      for (int jb = 0; jb < 2; ++jb) {
-        const f32x4 e0 = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(ws + L::Eck + ((size_t)((2 * jb) * NV + n) * 64 + lane) * 16));
-        const f32x4 e1 = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(ws + L::Eck + ((size_t)((2 * jb + 1) * NV + n) * 64 + lane) * 16));
-        eb[jb] = P::from_f32(pair_to8(e0, e1));
-      }
+      for (int jb = 0; jb < 2; ++jb)
+        eb[jb] = load_e_frag<P>(ws + L::Eck, (size_t)((2 * jb) * NV + n), (size_t)((2 * jb + 1) * NV + n), lane);
       f32x4 y = zero4();
 #pragma unroll
       for (int jb = 0; jb < 2; ++jb) y = P::mma(y, pf[jb], eb[jb]);

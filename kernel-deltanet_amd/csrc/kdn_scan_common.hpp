@@ -23,8 +23,9 @@ struct WsLayout {
   static constexpr size_t U = Pm + (size_t)4 * 2 * 64 * FB;         // [m 4][n NV][lane] f32x4  U~
   static constexpr size_t VEC = U + (size_t)4 * NV * 64 * 16;       // qscale[64] kscale[64] gammaC
   static constexpr size_t Sfr = VEC + 1024;                         // [j NJ][n NV][lane] chunk-start S^T frags
-  static constexpr size_t Eck = Sfr + (size_t)NJ * NV * 64 * FB;    // [m 4][n NV][lane] f32x4  E
-  static constexpr size_t phiQ = Eck + (size_t)4 * NV * 64 * 16;    // [m 4][j NJ][lane] Q row frags (cos)
+  static constexpr size_t EB = FB / 2;                              // bytes of a lane's E tile (bf16x4 / f32x4)
+  static constexpr size_t Eck = Sfr + (size_t)NJ * NV * 64 * FB;    // [m 4][n NV][lane] E tiles
+  static constexpr size_t phiQ = Eck + (size_t)4 * NV * 64 * EB;    // [m 4][j NJ][lane] Q row frags (cos)
   static constexpr size_t bytes = (phiQ + (size_t)4 * NJ * 64 * FB + 255) / 256 * 256;
 };
 
@@ -42,6 +43,35 @@ __device__ __forceinline__ void store_k_image(unsigned char* kimg, int m, int j,
   unsigned char* base = kimg + (size_t)(j >> 2) * KIMG_SLICE + (size_t)((m * 4 + (j & 3)) * 64 + lane) * 8;
   __builtin_nontemporal_store(__builtin_shufflevector(f, f, 0, 1, 2, 3), reinterpret_cast<bf16x4*>(base));
   __builtin_nontemporal_store(__builtin_shufflevector(f, f, 4, 5, 6, 7), reinterpret_cast<bf16x4*>(base + KIMG_PLANE));
+}
+
+// E tiles in the record, lane l holding rows 4(l>>4) .. +3 of column (l & 15) of tile `tile`: bf16 for
+// bf16 inputs (the output kernel's product P E takes bf16 operands, so storing the rounded values
+// changes no result and halves the bytes), fp32 otherwise.
+template <class P>
+__device__ __forceinline__ void store_e_tile(unsigned char* eck, size_t tile, int lane, const f32x4& e) {
+  if constexpr (P::frag_bytes == 16) {
+    typedef __attribute__((ext_vector_type(4))) __bf16 bf16x4;
+    const bf16x4 b = {(__bf16)e[0], (__bf16)e[1], (__bf16)e[2], (__bf16)e[3]};
+    *reinterpret_cast<bf16x4*>(eck + (tile * 64 + lane) * 8) = b;
+  } else {
+    *reinterpret_cast<f32x4*>(eck + (tile * 64 + lane) * 16) = e;
+  }
+}
+// The B fragment (32 token rows in kappa order, 16 columns) made of E tiles t0 (rows 0-15) and t1 (rows
+// 16-31), read with streaming loads (the output kernel is the last reader).
+template <class P>
+__device__ __forceinline__ typename P::frag load_e_frag(const unsigned char* eck, size_t t0, size_t t1, int lane) {
+  if constexpr (P::frag_bytes == 16) {
+    typedef __attribute__((ext_vector_type(4))) __bf16 bf16x4;
+    const bf16x4 lo = __builtin_nontemporal_load(reinterpret_cast<const bf16x4*>(eck + (t0 * 64 + lane) * 8));
+    const bf16x4 hi = __builtin_nontemporal_load(reinterpret_cast<const bf16x4*>(eck + (t1 * 64 + lane) * 8));
+    return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+  } else {
+    const f32x4 e0 = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(eck + (t0 * 64 + lane) * 16));
+    const f32x4 e1 = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(eck + (t1 * 64 + lane) * 16));
+    return P::from_f32(pair_to8(e0, e1));
+  }
 }
 
 struct ScanParams {

@@ -76,14 +76,14 @@ def _args(**kw):
 
 
 def test_workspace_bytes(lib):
-    # one 64-token chunk record of one head = 246784 bytes for bf16 inputs, D = 512, d_v = 64; a segment
+    # one 64-token chunk record of one head = 238592 bytes for bf16 inputs, D = 512, d_v = 64; a segment
     # of n chunks uses n + 1 records per head (the last is the state kernel's scratch record)
     a = _args(segment_chunks=1)
-    assert lib.kdn_scan_workspace_bytes(ctypes.byref(a)) == 16 * 2 * 246784
+    assert lib.kdn_scan_workspace_bytes(ctypes.byref(a)) == 16 * 2 * 238592
     assert lib.kdn_scan_workspace_bytes(ctypes.byref(_args(d_k=32))) == 0
     assert lib.kdn_scan_workspace_bytes(ctypes.byref(_args(d_v=48))) == 0
     a = _args(segment_chunks=100000)  # clamped to the number of chunks
-    assert lib.kdn_scan_workspace_bytes(ctypes.byref(a)) == 16 * 1025 * 246784
+    assert lib.kdn_scan_workspace_bytes(ctypes.byref(a)) == 16 * 1025 * 238592
 
 
 def _fake_ptrs(a, base=0x7F0000000000):

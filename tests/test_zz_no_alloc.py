@@ -55,12 +55,12 @@ def test_noalloc_equals_workspace_entry_point():
 
 
 def test_noalloc_refuses_requests_beyond_the_array():
-    # 600 heads need 600 * 2 records of 246,784 bytes (bf16, d_v = 64) > 256 MiB: refused on the host
+    # 600 heads need 600 * 2 records of 238,592 bytes (bf16, d_v = 64) > 256 MiB: refused on the host
     a = N.ScanArgs()
     a.B, a.T, a.H, a.d_k, a.D, a.d_v = 1, 4096, 600, 64, 512, 64
     a.in_dtype = a.out_dtype = N.KDN_DTYPE_BF16
     a.inv_tau = 0.35355339
-    assert 600 * 2 * 246784 > N.NOALLOC_SCRATCH_BYTES
+    assert 600 * 2 * 238592 > N.NOALLOC_SCRATCH_BYTES
     assert N.lib().kdn_delta_scan_fwd_noalloc(ctypes.byref(a), None) == N.KDN_ERR_WORKSPACE_TOO_SMALL
     a.d_k, a.D, a.feature_mode = 1024, 1024, 1     # the pre-lifted D = 1024 path has no segment form
     assert N.lib().kdn_delta_scan_fwd_noalloc(ctypes.byref(a), None) == -2
