@@ -225,20 +225,29 @@ int kdn_scan_prep(const kdn_scan_args* a, int64_t chunk0, int64_t nchunks, void*
 int kdn_scan_state(const kdn_scan_args* a, int64_t chunk0, int64_t nchunks, void* stream);
 int kdn_scan_output(const kdn_scan_args* a, int64_t chunk0, int64_t nchunks, void* stream);
 
-/* ---- Backward of the scan (ABI 1.3) -------------------------------------------------------------
+/* ---- Backward of the scan (ABI 1.3; segmented and deterministic since ABI 1.6) ----------------------
  * Gradients of a loss L through kdn_delta_scan_fwd, given dL/dy and optionally dL/d(final state).
  * Replaces the autograd recompute of FusedKernelDeltaNetFunction.backward,
  * kernels/fused_kernel_deltanet.py:168-179.  `fwd` holds the forward's arguments (shapes, q, k, v, beta,
- * decay, omega_bf16, phase, inv_tau, normalize_input, initial_state; its y, final_state, workspace and
- * segment_chunks are ignored).  Supported: d_k = 64, D = 512, d_v = 64, the delta rule (rule 0) with the
+ * decay, omega_bf16, phase, inv_tau, normalize_input, initial_state, segment_chunks; its y, final_state
+ * and workspace are ignored).  Supported: d_k = 64, D = 512, d_v = 64, the delta rule (rule 0) with the
  * structured lift of one shared Omega (no hi + lo, per-head or pre-lifted features, no_renorm 0), uniform
  * batches (no cu_seqlens / state_slots); other requests return KDN_ERR_UNSUPPORTED.  dy and
  * d_final_state are fp32; every gradient is written in fp32 with the layout of its input: dq, dk
  * (B, T, H, d_k), dv (B, T, H, d_v), dbeta, ddecay (B, T, H), d_initial_state (B, H, D, d_v).
  * d_final_state NULL means dL/dS_T = 0; ddecay (allowed only with decay) and d_initial_state may be
- * NULL.  The gradient of lambda is zero where the forward's clamp to [1e-5, 1] is active.  The
- * workspace holds one fp32 record per (batch, head, 64-token chunk) (1,116,160 bytes each; 256-byte
- * aligned) followed by a 64 KB table of Omega^T fragments that the gradient launch writes. */
+ * NULL.  The gradient of lambda is zero where the forward's clamp to [1e-5, 1] is active.
+ *
+ * The backward runs in segments of fwd->segment_chunks 64-token chunks (0: the largest power of two
+ * from 4 to 64 whose per-chunk records fit 1.25 GiB), last segment first: a checkpoint pass of the
+ * forward scan's prep and state kernels stores the state at each segment start, then each segment
+ * recomputes its chunks, carries the state forward from its checkpoint and dL/dS backward from the
+ * next segment, and writes its gradients.  The workspace (256-byte aligned) holds up to three segments'
+ * fp32 records (1,116,160 bytes per (batch, head, chunk)), one fp32 [B][H][512][64] state per segment
+ * boundary plus one more, up to two buffers of the forward scan's records and a 64 KB table: it grows
+ * with the segment, not with T, apart from the 128 KB per head per segment boundary.  Every reduction
+ * runs in a fixed order: the results are identical bit for bit from run to run and between
+ * kdn_delta_scan_bwd and kdn_delta_scan_bwd_streams. */
 typedef struct kdn_scan_bwd_args {
   const kdn_scan_args* fwd;
   const float* dy;            int64_t dy_stride[3];
@@ -255,22 +264,30 @@ typedef struct kdn_scan_bwd_args {
 /* Workspace bytes kdn_delta_scan_bwd needs (0 if the arguments are invalid or unsupported). */
 size_t kdn_scan_bwd_workspace_bytes(const kdn_scan_bwd_args* a);
 
-/* Enqueues the backward on `stream`: per-chunk recompute of the lift and the chunk matrices, the
- * forward state carry (state at every chunk start), the reverse carry of dL/dS, and the per-chunk
- * gradients with the lift's backward. */
+/* Segments of the backward (ABI 1.6): returns their number (0 if the arguments are invalid or
+ * unsupported) and, when segment_chunks is not NULL, their length in 64-token chunks. */
+int64_t kdn_scan_bwd_segments(const kdn_scan_bwd_args* a, int64_t* segment_chunks);
+
+/* Enqueues the backward on `stream`: the checkpoint pass, then per segment (last first) the per-chunk
+ * recompute of the lift and the chunk matrices, the forward state carry (state at every chunk start),
+ * the reverse carry of dL/dS, and the per-chunk gradients with the lift's backward. */
 int kdn_delta_scan_bwd(const kdn_scan_bwd_args* a, void* stream);
 
-/* kdn_delta_scan_bwd with the reverse carry on aux_stream, beside the forward carry on `stream` (the two
- * carries are independent given the per-chunk recompute); the gradients wait for both.  Same workspace;
- * results equal kdn_delta_scan_bwd's up to the summation order of its LDS reductions.  aux_stream NULL
- * (or equal to `stream`) is kdn_delta_scan_bwd.  Both streams should have default priority.  Replaces
- * kernels/fused_kernel_deltanet.py:168-179, like kdn_delta_scan_bwd. */
+/* kdn_delta_scan_bwd over two streams: the reverse carries (the sequential critical path) run back to
+ * back on `stream` while aux_stream runs the recompute, forward carry and gradients of the segments
+ * around them (and the checkpoint pass's prep kernels beside its state kernels).  Same workspace, same
+ * results bit for bit.  aux_stream NULL (or equal to `stream`) is kdn_delta_scan_bwd.  Both streams
+ * should have default priority.  Replaces kernels/fused_kernel_deltanet.py:168-179, like
+ * kdn_delta_scan_bwd. */
 int kdn_delta_scan_bwd_streams(const kdn_scan_bwd_args* a, void* stream, void* aux_stream);
 
-/* One of the four launches of kdn_delta_scan_bwd (phase 0: per-chunk recompute, 1: forward carry,
- * 2: reverse carry, 3: gradients), for callers that time or schedule them; on one workspace they must
- * run in the order 0, 1, 2, 3 (stream order or events).  Same arguments and checks. */
-int kdn_scan_bwd_phase(const kdn_scan_bwd_args* a, int phase, void* stream);
+/* One launch group of kdn_delta_scan_bwd (ABI 1.6 signature), for callers that time or schedule them:
+ * phase 0 is the start of a call (the Omega^T table and the checkpoint pass; `segment` ignored); phases
+ * 1 (per-chunk recompute), 2 (forward carry), 3 (reverse carry) and 4 (gradients) are those of segment
+ * `segment` (0 .. kdn_scan_bwd_segments - 1).  On one workspace they must run in the order of
+ * kdn_delta_scan_bwd: 0, then for segments from the last to the first 1, 2, 3, 4 (stream order or
+ * events).  Same arguments and checks. */
+int kdn_scan_bwd_phase(const kdn_scan_bwd_args* a, int phase, int64_t segment, void* stream);
 
 /* ---- Serving: ragged mixed prefill + decode step over resident states -------------------------
  * One step of a batch of sequences that continue from states resident in a slab (the reference's

@@ -37,7 +37,13 @@ namespace bwd {
 
 constexpr int C = 64, D = 512, DK = 64, DV = 64;
 constexpr int LD = 68;  // LDS row stride (floats) of a 64-wide tile: rows stay 16-byte aligned
-constexpr size_t OMT_BYTES = (size_t)4 * 16 * 64 * 16;  // the Omega^T fragment table after the records
+constexpr size_t OMT_BYTES = (size_t)4 * 16 * 64 * 16;  // the Omega^T fragment table
+
+// Rows of the gradient kernel's dl_i contribution table, one per source term: the dkappa term (-t_i),
+// the per-wave column sums of P o dP (4 rows), the row sums of P o dP (at i - 1), beta g (T o dTp)
+// column sums, the a o dY . Q S^T term (at i - 1), the per-wave column sums of A o dA (4 rows) and the
+// row sums of A o dA.
+constexpr int DL_KAPPA = 0, DL_COLP = 1, DL_RP = 5, DL_TS = 6, DL_DA = 7, DL_DLC = 8, DL_A = 12, NDL = 13;
 
 // Per (head, chunk) record, offsets in floats.
 struct Rec {
@@ -69,6 +75,7 @@ static_assert((Rec::floats * 4) % 256 == 0, "records stay 256-byte aligned");
 
 struct Params {
   int64_t B, T, H, nch;
+  int64_t c0, nseg, cap;  // this segment: first global chunk, chunks in it, records per head in its buffer
   const void* q; int64_t qs0, qs1, qs2;
   const void* k; int64_t ks0, ks1, ks2;
   const void* v; int64_t vs0, vs1, vs2;
@@ -76,21 +83,22 @@ struct Params {
   const float* decay; int64_t ds0, ds1, ds2;
   const __bf16* omega; const float* phase;
   float inv_tau; int normalize;
-  const float* init; int64_t is0, is1, is2, is3;
+  const float* init; int64_t is0, is1, is2, is3;  // S^T at the segment start (NULL: zero)
   const float* dy; int64_t ys0, ys1, ys2;
-  const float* dfin; int64_t fs0, fs1, fs2, fs3;
+  const float* dfin; int64_t fs0, fs1, fs2, fs3;  // dL/dS^T at the segment end (NULL: zero)
   float* dq; int64_t dqs0, dqs1, dqs2;
   float* dk; int64_t dks0, dks1, dks2;
   float* dv; int64_t dvs0, dvs1, dvs2;
   float* dbeta; int64_t dbs0, dbs1, dbs2;
   float* ddecay; int64_t dds0, dds1, dds2;
-  float* dinit; int64_t dis0, dis1, dis2, dis3;
-  float* ws;
+  float* gout; int64_t gos0, gos1, gos2, gos3;    // dL/dS^T at the segment start (NULL: not kept)
+  float* ws;                                       // this segment's buffer of records
   const bf16x8* omt;  // Omega^T fragments [a 4][jb 16][lane] (workspace tail, written before the gradients)
 };
 
+// Record of local chunk c (0 .. nseg - 1) of the segment.
 __device__ __forceinline__ float* record(const Params& p, int64_t b, int64_t h, int64_t c) {
-  return p.ws + ((b * p.H + h) * p.nch + c) * (int64_t)Rec::floats;
+  return p.ws + ((b * p.H + h) * p.cap + c) * (int64_t)Rec::floats;
 }
 
 
@@ -140,11 +148,11 @@ __global__ void __launch_bounds__(256) bwd_prep_kernel(Params p) {
   __shared__ __attribute__((aligned(16))) float bY[C * LD];   // dY
   __shared__ float s_ell[C], s_beta[C], s_n[C], s_red[4][C];
 
-  const int64_t c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int64_t h = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int64_t t0 = c * C;
-  float* rec = record(p, b, h, c);
+  const int64_t t0 = (p.c0 + blockIdx.x) * C;
+  float* rec = record(p, b, h, blockIdx.x);
   const int r = tid >> 2, c0 = (tid & 3) * 16;
   const bool rvalid = t0 + r < p.T;
 
@@ -404,8 +412,8 @@ __device__ __forceinline__ bool chain_step(const Params& p, ChainShared& sh, int
                                            unsigned& sink) {
   using frag = typename P::frag;
   const int vc = 16 * n + (lane & 15);
-  const int64_t c = REV ? p.nch - 1 - step : step;
-  const bool more = step + 1 < p.nch;
+  const int64_t c = REV ? p.nseg - 1 - step : step;
+  const bool more = step + 1 < p.nseg;
   const int64_t cn = REV ? c - 1 : c + 1;
   float* rec = record(p, b, h, c);
   if constexpr (!PIPE) chain_load_kx<P>(cur, rec, w, lane);
@@ -534,22 +542,24 @@ __global__ void __launch_bounds__(256) bwd_chain_kernel(Params p) {
         Sg[t][i] = src ? src[b * s0 + h * s1 + f * s2 + vc * s3] : 0.f;
       }
   }
-  unsigned sink = 0;  // keeps the L2 prefetch loads alive (never stored: nch is positive)
+  unsigned sink = 0;  // keeps the L2 prefetch loads alive (never stored: nseg is positive)
   ChainK<P> ka, kb;
-  if constexpr (PIPE) chain_load_kx<P>(ka, record(p, b, h, REV ? p.nch - 1 : 0), w, lane);
+  if constexpr (PIPE) chain_load_kx<P>(ka, record(p, b, h, REV ? p.nseg - 1 : 0), w, lane);
   for (int64_t step = 0;; step += 2) {
     if (!chain_step<P, REV, PIPE>(p, sh, b, h, step, ka, kb, Sg, w, lane, n, sink)) break;
     if (!chain_step<P, REV, PIPE>(p, sh, b, h, step + 1, kb, ka, Sg, w, lane, n, sink)) break;
   }
-  if (p.nch < 0) p.ws[0] = (float)sink;
+  if (p.nseg < 0) p.ws[0] = (float)sink;
   if constexpr (REV) {
-    if (p.dinit) {
+    // dL/dS^T at the segment start: the next (earlier) segment's reverse carry starts from it; this
+    // thread rewrites exactly the elements it read at the top when both are the segment carry
+    if (p.gout) {
 #pragma unroll
       for (int t = 0; t < 8; ++t)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int f = 128 * w + 16 * t + 4 * (lane >> 4) + i;
-          p.dinit[b * p.dis0 + h * p.dis1 + f * p.dis2 + vc * p.dis3] = Sg[t][i];
+          p.gout[b * p.gos0 + h * p.gos1 + f * p.gos2 + vc * p.gos3] = Sg[t][i];
         }
     }
   }
@@ -560,11 +570,11 @@ __global__ void __launch_bounds__(256) bwd_chain_kernel(Params p) {
 // dPhi^T in acc[ft][u] (rows feature 128w + 16ft + .., column token 16(2hm + u) + ..):
 // ds = -sqrt(2/D) sin(s) (dphi / (n + 1e-8) - phi (phi . dphi) / n), then dx^ = ds Omega reduced over
 // the waves into `dx` (LDS [64][LD], zeroed by the caller).  `xh` holds the normalised
-// input rows, `s_rd` (zeroed by the caller) collects phi . dphi per token.
+// input rows; s_rd[w] receives wave w's part of phi . dphi per token (summed in wave order).
 template <class P>
-__device__ __forceinline__ void lift_backward_half(const Params& p, const float* phi, const float* nrm, float* s_rd,
-                                                   const float* xh, float* dx, f32x4 (&acc)[8][2], int hm, int w,
-                                                   int lane) {
+__device__ __forceinline__ void lift_backward_half(const Params& p, const float* phi, const float* nrm,
+                                                   float (*s_rd)[C], const float* xh, float* dx,
+                                                   f32x4 (&acc)[8][2], int hm, int w, int lane) {
   float rd[2] = {0.f, 0.f};
 #pragma unroll
   for (int ft = 0; ft < 8; ++ft)
@@ -577,7 +587,7 @@ __device__ __forceinline__ void lift_backward_half(const Params& p, const float*
 #pragma unroll
   for (int u = 0; u < 2; ++u) {
     const float v = sum_col4(rd[u]);
-    if (lane < 16) atomicAdd(&s_rd[16 * (2 * hm + u) + lane], v);
+    if (lane < 16) s_rd[w][16 * (2 * hm + u) + lane] = v;
   }
   __syncthreads();
   const float amp = sqrtf(2.f / D);
@@ -587,7 +597,7 @@ __device__ __forceinline__ void lift_backward_half(const Params& p, const float*
   for (int u = 0; u < 2; ++u) {
     const int tok = 16 * (2 * hm + u) + (lane & 15);
     inv_n[u] = 1.f / (nrm[tok] + 1e-8f);
-    rd_n[u] = s_rd[tok] / nrm[tok];
+    rd_n[u] = (((s_rd[0][tok] + s_rd[1][tok]) + s_rd[2][tok]) + s_rd[3][tok]) / nrm[tok];
   }
   f32x8 xb[2][2];
 #pragma unroll
@@ -703,22 +713,27 @@ __global__ void __launch_bounds__(256) bwd_grad_kernel(Params p) {
   __shared__ __attribute__((aligned(16))) float bV[C * LD];   // V, then Y1 = dT T^T
   __shared__ __attribute__((aligned(16))) float bT[C * LD];   // T, then normalised k / q rows
   __shared__ __attribute__((aligned(16))) float bDX[C * LD];  // dx^ of k / q
-  __shared__ float s_ell[C], s_beta[C], s_dl[C], s_db[C], s_ts[C], s_rd[C], s_n[C], s_g[1];
+  __shared__ float s_ell[C], s_beta[C], s_n[C];
+  // Fixed-order reductions (the gradients do not depend on the order the waves run in): every partial
+  // sum has a slot of its own, written once, and the slots are added in a fixed order; no atomics.
+  //   s_dlp: contributions to dl_i = dL/dl_i, one row per source (see NDL); s_dbp: to dbeta_i;
+  //   s_tsp: per-wave column sums of T o dTp; s_rdp: per-wave phi . dphi (lift backward);
+  //   s_w63: per-wave sums that land on dl_63 (the dkappa term [0..3] and <Gamma, S> [4..7])
+  __shared__ float s_dlp[NDL][C], s_dbp[3][C], s_tsp[4][C], s_rdp[4][C], s_w63[8];
 
-  const int64_t c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int64_t h = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int64_t t0 = c * C;
-  const float* rec = record(p, b, h, c);
+  const int64_t t0 = (p.c0 + blockIdx.x) * C;
+  const float* rec = record(p, b, h, blockIdx.x);
   const int r = tid >> 2, c0 = (tid & 3) * 16;
   const bool rvalid = t0 + r < p.T;
 
   if (tid < C) {
     s_ell[tid] = rec[Rec::VEC + tid];
     s_beta[tid] = rec[Rec::VEC + 64 + tid];
-    s_dl[tid] = s_db[tid] = s_ts[tid] = s_rd[tid] = 0.f;
   }
-  if (tid == 0) s_g[0] = 0.f;
+  if (tid == 0) s_dlp[DL_RP][63] = s_dlp[DL_DA][63] = 0.f;  // the only slots no source writes
   {
     const InT* v = reinterpret_cast<const InT*>(p.v);
     const int64_t vb = b * p.vs0 + (t0 + r) * p.vs1 + h * p.vs2 + c0;
@@ -750,11 +765,10 @@ __global__ void __launch_bounds__(256) bwd_grad_kernel(Params p) {
     for (int e = 0; e < 16; ++e) dkp += bW[r * LD + c0 + e] * bX[r * LD + c0 + e];
     dkp += __shfl_xor(dkp, 1);
     dkp += __shfl_xor(dkp, 2);
-    if ((tid & 3) == 0) {
-      const float t = dkp * expf(l63 - s_ell[r]);
-      atomicAdd(&s_dl[63], t);
-      atomicAdd(&s_dl[r], -t);
-    }
+    const float t = dkp * expf(l63 - s_ell[r]);  // the same in the four threads of row r
+    if ((tid & 3) == 0) s_dlp[DL_KAPPA][r] = -t;
+    const float tw = sum_col4(sum_row16((tid & 3) == 0 ? t : 0.f));
+    if (lane == 0) s_w63[w] = tw;
   }
   f32x4 dT[4], nN[4];
   {
@@ -795,8 +809,8 @@ __global__ void __launch_bounds__(256) bwd_grad_kernel(Params p) {
       ts = sum_col4(ts);
       colp = sum_col4(colp);
       if (lane < 16) {
-        atomicAdd(&s_ts[cj], ts);
-        atomicAdd(&s_dl[cj], -colp);
+        s_tsp[w][cj] = ts;
+        s_dlp[DL_COLP + w][cj] = -colp;
       }
     }
 #pragma unroll
@@ -804,8 +818,8 @@ __global__ void __launch_bounds__(256) bwd_grad_kernel(Params p) {
       const int ri = 16 * w + 4 * (lane >> 4) + i;
       const float db = sum_row16(dbp[i]), rp = sum_row16(rowp[i]);
       if ((lane & 15) == 0) {
-        atomicAdd(&s_db[ri], db);
-        if (ri > 0) atomicAdd(&s_dl[ri - 1], rp);
+        s_dbp[0][ri] = db;
+        if (ri > 0) s_dlp[DL_RP][ri - 1] = rp;
       }
     }
   }
@@ -821,9 +835,9 @@ __global__ void __launch_bounds__(256) bwd_grad_kernel(Params p) {
       bXK[ri * LD + cj] = nN[n][i];
     }
   if (tid < C) {
-    const float g = expf(s_ell[tid]), ts = s_ts[tid];
-    atomicAdd(&s_db[tid], g * ts);
-    atomicAdd(&s_dl[tid], s_beta[tid] * g * ts);
+    const float g = expf(s_ell[tid]), ts = ((s_tsp[0][tid] + s_tsp[1][tid]) + s_tsp[2][tid]) + s_tsp[3][tid];
+    s_dbp[1][tid] = g * ts;
+    s_dlp[DL_TS][tid] = s_beta[tid] * g * ts;
   }
   {
     f32x4 qs[4];
@@ -844,7 +858,7 @@ __global__ void __launch_bounds__(256) bwd_grad_kernel(Params p) {
     for (int i = 0; i < 4; ++i) {
       const int ri = 16 * w + 4 * (lane >> 4) + i;
       const float da = sum_row16(dap[i]);
-      if ((lane & 15) == 0 && ri > 0) atomicAdd(&s_dl[ri - 1], da * expf(s_ell[ri - 1]));
+      if ((lane & 15) == 0 && ri > 0) s_dlp[DL_DA][ri - 1] = da * expf(s_ell[ri - 1]);
     }
     // scale this wave's rows only (no other wave reads them in this phase)
     for (int e = lane; e < 16 * DV; e += 64) {
@@ -864,10 +878,9 @@ __global__ void __launch_bounds__(256) bwd_grad_kernel(Params p) {
       gs += g[0] * s[0] + g[1] * s[1] + g[2] * s[2] + g[3] * s[3];
     }
     gs = sum_col4(sum_row16(gs));
-    if (lane == 0) atomicAdd(&s_g[0], gs);
+    if (lane == 0) s_w63[4 + w] = gs;
   }
   __syncthreads();
-  if (tid == 0) atomicAdd(&s_dl[63], s_g[0] * gC);
 
   // ---- phase 3: Y1 = dT T^T; Zn = -Tp^T dW
   f32x4 y1[4], zn[4];
@@ -918,15 +931,15 @@ __global__ void __launch_bounds__(256) bwd_grad_kernel(Params p) {
         }
       }
       dlc = sum_col4(dlc);
-      if (lane < 16) atomicAdd(&s_dl[cj], -dlc);
+      if (lane < 16) s_dlp[DL_DLC + w][cj] = -dlc;
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int ri = 16 * w + 4 * (lane >> 4) + i;
       const float a = sum_row16(dbr[i]), d = sum_row16(dlr[i]);
       if ((lane & 15) == 0) {
-        atomicAdd(&s_db[ri], a);
-        atomicAdd(&s_dl[ri], d);
+        s_dbp[2][ri] = a;
+        s_dlp[DL_A][ri] = d;
       }
     }
   }
@@ -934,7 +947,12 @@ __global__ void __launch_bounds__(256) bwd_grad_kernel(Params p) {
 
   // ---- phase 5: dbeta and dlambda (dlog lambda_t = sum_{i >= t} dl_i)
   if (w == 0) {
-    float dl = s_dl[lane];
+    float dl = 0.f;
+#pragma unroll
+    for (int k = 0; k < NDL; ++k) dl += s_dlp[k][lane];
+    if (lane == 63)
+      dl += (((s_w63[0] + s_w63[1]) + s_w63[2]) + s_w63[3]) + (((s_w63[4] + s_w63[5]) + s_w63[6]) + s_w63[7]) * gC;
+    const float dbeta = (s_dbp[0][lane] + s_dbp[1][lane]) + s_dbp[2][lane];
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) {
       const float u = __shfl_down(dl, o);
@@ -942,7 +960,7 @@ __global__ void __launch_bounds__(256) bwd_grad_kernel(Params p) {
     }
     const int64_t t = t0 + lane;
     if (t < p.T) {
-      p.dbeta[b * p.dbs0 + t * p.dbs1 + h * p.dbs2] = s_db[lane];
+      p.dbeta[b * p.dbs0 + t * p.dbs1 + h * p.dbs2] = dbeta;
       if (p.ddecay) {
         const float la = p.decay ? p.decay[b * p.ds0 + t * p.ds1 + h * p.ds2] : 1.f;
         p.ddecay[b * p.dds0 + t * p.dds1 + h * p.dds2] = (la >= 1e-5f && la <= 1.f) ? dl / la : 0.f;
@@ -964,10 +982,7 @@ __global__ void __launch_bounds__(256) bwd_grad_kernel(Params p) {
         bDX[r * LD + c0 + e] = 0.f;
       }
     }
-    if (tid < C) {
-      s_rd[tid] = 0.f;
-      s_n[tid] = rec[Rec::VEC + 128 + 64 * which + tid];
-    }
+    if (tid < C) s_n[tid] = rec[Rec::VEC + 128 + 64 * which + tid];
     __syncthreads();
     for (int hm = 0; hm < 2; ++hm) {
       f32x4 acc[8][2];
@@ -1027,7 +1042,7 @@ __global__ void __launch_bounds__(256) bwd_grad_kernel(Params p) {
         }
         __builtin_amdgcn_sched_barrier(0);
       }
-      lift_backward_half<P>(p, rec + (which == 0 ? Rec::Q : Rec::K), s_n, s_rd, bT, bDX, acc, hm, w, lane);
+      lift_backward_half<P>(p, rec + (which == 0 ? Rec::Q : Rec::K), s_n, s_rdp, bT, bDX, acc, hm, w, lane);
     }
     __syncthreads();
     if (which == 0) {
@@ -1078,10 +1093,63 @@ static int bwd_check(const kdn_scan_bwd_args* a) {
 
 static int64_t bwd_chunks(const kdn_scan_args* f) { return (f->T + C - 1) / C; }
 
+// The backward runs in segments of `seg` chunks (the last may be shorter), last segment first, so that
+// its workspace grows with the segment, not with T:
+//   nbuf record buffers (seg records per head each)   the per-chunk recompute and both carries of one
+//                                                     segment, rotating so that up to three segments
+//                                                     are in flight
+//   nsegs - 1 states, fp32 [B][H][512][64] each       S^T at the start of segments 1 .. nsegs-1 (the
+//                                                     checkpoint pass: the forward scan's prep and
+//                                                     state kernels, kdn_scan.hip)
+//   one such array                                    dL/dS^T carried from one segment to the previous
+//   nfb buffers of the forward scan's records         for the checkpoint pass
+//   the Omega^T fragment table
+struct BwdLayout {
+  int64_t seg, nsegs;
+  int nbuf, nfb;
+  size_t rec_buf, state_bytes, ckpt_off, carry_off, fwd_off, fwd_buf, omt_off, total;
+};
+
+// Default segment: the largest power of two from 4 to 64 chunks whose records fit 1.25 GiB.
+constexpr size_t BWD_SEGMENT_BUDGET = (size_t)1280 << 20;
+
+static BwdLayout bwd_layout(const kdn_scan_args* f) {
+  BwdLayout L;
+  const int64_t nch = bwd_chunks(f), heads = f->B * f->H;
+  const size_t per_chunk = (size_t)heads * Rec::floats * sizeof(float);
+  int64_t seg = 4;
+  if (f->segment_chunks > 0) {
+    seg = f->segment_chunks;
+  } else {
+    const size_t fit = BWD_SEGMENT_BUDGET / per_chunk;
+    while (seg < 64 && (size_t)(2 * seg) <= fit) seg *= 2;
+  }
+  if (seg > nch) seg = nch;
+  L.seg = seg;
+  L.nsegs = (nch + seg - 1) / seg;
+  L.nbuf = (int)(L.nsegs < 3 ? L.nsegs : 3);
+  L.nfb = (int)(L.nsegs - 1 < 2 ? L.nsegs - 1 : 2);
+  L.rec_buf = (size_t)seg * per_chunk;
+  L.state_bytes = (size_t)heads * D * DV * sizeof(float);
+  L.ckpt_off = (size_t)L.nbuf * L.rec_buf;
+  L.carry_off = L.ckpt_off + (size_t)(L.nsegs - 1) * L.state_bytes;
+  L.fwd_off = L.carry_off + (L.nsegs > 1 ? L.state_bytes : 0);
+  L.fwd_buf = L.nfb > 0 ? (scan_checkpoint_buffer_bytes(f, seg) + 255) / 256 * 256 : 0;
+  L.omt_off = L.fwd_off + (size_t)L.nfb * L.fwd_buf;
+  L.total = L.omt_off + OMT_BYTES;
+  return L;
+}
+
 extern "C" size_t kdn_scan_bwd_workspace_bytes(const kdn_scan_bwd_args* a) {
   if (bwd_check(a) != KDN_OK) return 0;
-  const kdn_scan_args* f = a->fwd;
-  return (size_t)(f->B * f->H * bwd_chunks(f)) * Rec::floats * sizeof(float) + OMT_BYTES;
+  return bwd_layout(a->fwd).total;
+}
+
+extern "C" int64_t kdn_scan_bwd_segments(const kdn_scan_bwd_args* a, int64_t* segment_chunks) {
+  if (bwd_check(a) != KDN_OK) return 0;
+  const BwdLayout L = bwd_layout(a->fwd);
+  if (segment_chunks) *segment_chunks = L.seg;
+  return L.nsegs;
 }
 
 // Omega^T as A fragments for the gradient kernel's dx^ = ds Omega: fragment (a, jb) lane l slot s holds
@@ -1095,48 +1163,122 @@ __global__ void __launch_bounds__(256) bwd_omega_t_kernel(const __bf16* omega, b
   table[idx] = v;
 }
 
-// Launches phases [first, last] (0 prep, 1 forward carry, 2 reverse carry, 3 gradients) in order.
-// The two carries read only what prep wrote and write disjoint record fields (S, XK, W forward; G, X,
-// DW reverse), so given an auxiliary stream the reverse carry runs there beside the forward carry: each
-// chain occupies B*H*4 workgroups, a quarter of the GPU at B*H = 16.
-template <class P, typename InT>
-static int bwd_launch(const Params& p, int first, int last, hipStream_t st, hipStream_t aux) {
-  const dim3 chunk_grid((unsigned)p.nch, (unsigned)p.H, (unsigned)p.B);
-  const unsigned chain_wgs = (unsigned)(((p.B * p.H + 7) / 8) * 8 * 4);
-  const bool side = aux && aux != st && first <= 1 && last >= 2;
-  EventSet evs;
-  if (side && evs.create(2) != KDN_OK) return KDN_ERR_DEVICE;
-  for (int ph = first; ph <= last; ++ph) {
-    if (ph == 0) hipLaunchKernelGGL((bwd_prep_kernel<P, InT>), chunk_grid, dim3(256), 0, st, p);
-    if (ph == 1 && side) {
-      if (hipEventRecord(evs.ev[0], st) != hipSuccess || hipStreamWaitEvent(aux, evs.ev[0], 0) != hipSuccess)
-        return KDN_ERR_DEVICE;
-      hipLaunchKernelGGL((bwd_chain_kernel<P, true>), dim3(chain_wgs), dim3(256), 0, aux, p);
-      hipLaunchKernelGGL((bwd_chain_kernel<P, false>), dim3(chain_wgs), dim3(256), 0, st, p);
-      if (hipEventRecord(evs.ev[1], aux) != hipSuccess || hipStreamWaitEvent(st, evs.ev[1], 0) != hipSuccess)
-        return KDN_ERR_DEVICE;
-      ph = 2;
-      continue;
-    }
-    if (ph == 1) hipLaunchKernelGGL((bwd_chain_kernel<P, false>), dim3(chain_wgs), dim3(256), 0, st, p);
-    if (ph == 2) hipLaunchKernelGGL((bwd_chain_kernel<P, true>), dim3(chain_wgs), dim3(256), 0, st, p);
-    if (ph == 3) {
-      hipLaunchKernelGGL(bwd_omega_t_kernel, dim3(16), dim3(256), 0, st, p.omega, const_cast<bf16x8*>(p.omt));
-      hipLaunchKernelGGL((bwd_grad_kernel<P, InT>), chunk_grid, dim3(256), 0, st, p);
-    }
+// The parameters of segment s: its chunks, its record buffer (rotating in processing order, last segment
+// first), the state it starts from (initial_state or its checkpoint), the dL/dS^T it ends with
+// (d_final_state or the carry) and where its reverse carry leaves dL/dS^T (the carry, or
+// d_initial_state for segment 0).
+static Params segment_params(const Params& base, const kdn_scan_bwd_args* a, const BwdLayout& L, int64_t s) {
+  Params p = base;
+  unsigned char* ws = static_cast<unsigned char*>(a->workspace);
+  p.c0 = s * L.seg;
+  p.nseg = (p.nch - p.c0 < L.seg) ? p.nch - p.c0 : L.seg;
+  p.cap = L.seg;
+  p.ws = reinterpret_cast<float*>(ws + (size_t)((L.nsegs - 1 - s) % L.nbuf) * L.rec_buf);
+  const int64_t c0s = base.H * D * DV, c1s = D * DV, c2s = DV, c3s = 1;  // a contiguous [B][H][D][DV] state
+  float* carry = reinterpret_cast<float*>(ws + L.carry_off);
+  if (s > 0) {
+    p.init = reinterpret_cast<const float*>(ws + L.ckpt_off + (size_t)(s - 1) * L.state_bytes);
+    p.is0 = c0s; p.is1 = c1s; p.is2 = c2s; p.is3 = c3s;
+    p.gout = carry;
+    p.gos0 = c0s; p.gos1 = c1s; p.gos2 = c2s; p.gos3 = c3s;
   }
+  if (s < L.nsegs - 1) {
+    p.dfin = carry;
+    p.fs0 = c0s; p.fs1 = c1s; p.fs2 = c2s; p.fs3 = c3s;
+  }
+  return p;
+}
+
+// One launch of segment p: 1 per-chunk recompute, 2 forward carry, 3 reverse carry, 4 gradients.
+template <class P, typename InT>
+static int segment_phase(const Params& p, int phase, hipStream_t st) {
+  const dim3 chunk_grid((unsigned)p.nseg, (unsigned)p.H, (unsigned)p.B);
+  const unsigned chain_wgs = (unsigned)(((p.B * p.H + 7) / 8) * 8 * 4);
+  if (phase == 1) hipLaunchKernelGGL((bwd_prep_kernel<P, InT>), chunk_grid, dim3(256), 0, st, p);
+  if (phase == 2) hipLaunchKernelGGL((bwd_chain_kernel<P, false>), dim3(chain_wgs), dim3(256), 0, st, p);
+  if (phase == 3) hipLaunchKernelGGL((bwd_chain_kernel<P, true>), dim3(chain_wgs), dim3(256), 0, st, p);
+  if (phase == 4) hipLaunchKernelGGL((bwd_grad_kernel<P, InT>), chunk_grid, dim3(256), 0, st, p);
   return launch_status();
 }
 
-static int bwd_run(const kdn_scan_bwd_args* a, int first, int last, void* stream, void* aux_stream) {
+// The start of a call: the Omega^T table, then the checkpoint pass (its prep kernels on aux if given).
+static int bwd_start(const kdn_scan_bwd_args* a, const Params& base, const BwdLayout& L, hipStream_t st,
+                     hipStream_t aux) {
+  hipLaunchKernelGGL(bwd_omega_t_kernel, dim3(16), dim3(256), 0, st, base.omega, const_cast<bf16x8*>(base.omt));
+  const int rc = launch_status();
+  if (rc != KDN_OK) return rc;
+  unsigned char* ws = static_cast<unsigned char*>(a->workspace);
+  return scan_checkpoints(a->fwd, L.seg, L.nsegs - 1, reinterpret_cast<float*>(ws + L.ckpt_off), ws + L.fwd_off,
+                          L.fwd_buf, L.nfb, st, aux);
+}
+
+// Serial: the start, then per segment (last first) recompute, forward carry, reverse carry, gradients.
+// With aux: the checkpoint pass's prep kernels run on aux beside its state kernels; then per segment
+// (processing step i, segment s = nsegs - 1 - i, buffer i % nbuf)
+//   aux: recompute(s) -> event R[i % nbuf]; forward carry(s) (the first waits for the checkpoints);
+//        gradients(s + 1) after its reverse carry (event V[(i - 1) % nbuf])
+//   st:  reverse carry(s) after R[i % nbuf] -> event V[i % nbuf]
+// so that the reverse carries, the sequential critical path, run back to back on st while aux recomputes
+// and finishes the segments around them.  The recompute of step i reuses the buffer of step i - nbuf,
+// whose gradients precede it on aux.  Every kernel reads and writes the same data in either schedule, so
+// the results are identical bit for bit.
+template <class P, typename InT>
+static int bwd_schedule(const kdn_scan_bwd_args* a, const Params& base, const BwdLayout& L, hipStream_t st,
+                        hipStream_t aux) {
+#define KDN_TRY(x) do { if ((x) != hipSuccess) return KDN_ERR_DEVICE; } while (0)
+#define KDN_TRYK(x) do { const int _rc = (x); if (_rc != KDN_OK) return _rc; } while (0)
+  if (!aux || aux == st) {
+    KDN_TRYK(bwd_start(a, base, L, st, nullptr));
+    for (int64_t s = L.nsegs - 1; s >= 0; --s) {
+      const Params p = segment_params(base, a, L, s);
+      for (int ph = 1; ph <= 4; ++ph) KDN_TRYK((segment_phase<P, InT>(p, ph, st)));
+    }
+    return KDN_OK;
+  }
+  EventSet evs;
+  KDN_TRYK(evs.create(2 * L.nbuf + 3));
+  hipEvent_t* evR = evs.ev;
+  hipEvent_t* evV = evs.ev + L.nbuf;
+  hipEvent_t evIn = evs.ev[2 * L.nbuf], evCk = evs.ev[2 * L.nbuf + 1], evDone = evs.ev[2 * L.nbuf + 2];
+  KDN_TRY(hipEventRecord(evIn, st));
+  KDN_TRY(hipStreamWaitEvent(aux, evIn, 0));
+  KDN_TRYK(bwd_start(a, base, L, st, aux));
+  KDN_TRY(hipEventRecord(evCk, st));
+  for (int64_t i = 0; i < L.nsegs; ++i) {
+    const int64_t s = L.nsegs - 1 - i;
+    const int bb = (int)(i % L.nbuf);
+    const Params p = segment_params(base, a, L, s);
+    KDN_TRYK((segment_phase<P, InT>(p, 1, aux)));
+    KDN_TRY(hipEventRecord(evR[bb], aux));
+    if (i == 0) KDN_TRY(hipStreamWaitEvent(aux, evCk, 0));
+    KDN_TRYK((segment_phase<P, InT>(p, 2, aux)));
+    KDN_TRY(hipStreamWaitEvent(st, evR[bb], 0));
+    KDN_TRYK((segment_phase<P, InT>(p, 3, st)));
+    KDN_TRY(hipEventRecord(evV[bb], st));
+    if (i > 0) {
+      KDN_TRY(hipStreamWaitEvent(aux, evV[(i - 1) % L.nbuf], 0));
+      KDN_TRYK((segment_phase<P, InT>(segment_params(base, a, L, s + 1), 4, aux)));
+    }
+  }
+  KDN_TRY(hipStreamWaitEvent(aux, evV[(L.nsegs - 1) % L.nbuf], 0));
+  KDN_TRYK((segment_phase<P, InT>(segment_params(base, a, L, 0), 4, aux)));
+  KDN_TRY(hipEventRecord(evDone, aux));
+  KDN_TRY(hipStreamWaitEvent(st, evDone, 0));
+#undef KDN_TRY
+#undef KDN_TRYK
+  return KDN_OK;
+}
+
+// Checks the call and fills the parameters shared by every segment.
+static int bwd_params(const kdn_scan_bwd_args* a, Params& p, BwdLayout& L) {
   const int rc = bwd_check(a);
   if (rc != KDN_OK) return rc;
   const kdn_scan_args* f = a->fwd;
-  const size_t need = kdn_scan_bwd_workspace_bytes(a);
-  if (!a->workspace || a->workspace_bytes < need) return KDN_ERR_WORKSPACE_TOO_SMALL;
+  L = bwd_layout(f);
+  if (!a->workspace || a->workspace_bytes < L.total) return KDN_ERR_WORKSPACE_TOO_SMALL;
   if (!aligned(a->workspace, 256)) return KDN_ERR_MISALIGNED;
-  if (f->B > 65535 || f->H > 65535 || bwd_chunks(f) > 0x7fffffff) return KDN_ERR_UNSUPPORTED;
-  Params p = {};
+  if (f->B > 65535 || f->H > 65535 || L.seg > 0x7fffffff) return KDN_ERR_UNSUPPORTED;
+  p = Params{};
   p.B = f->B; p.T = f->T; p.H = f->H; p.nch = bwd_chunks(f);
   p.q = f->q; p.qs0 = f->q_stride[0]; p.qs1 = f->q_stride[1]; p.qs2 = f->q_stride[2];
   p.k = f->k; p.ks0 = f->k_stride[0]; p.ks1 = f->k_stride[1]; p.ks2 = f->k_stride[2];
@@ -1155,29 +1297,42 @@ static int bwd_run(const kdn_scan_bwd_args* a, int first, int last, void* stream
   p.dv = a->dv; p.dvs0 = a->dv_stride[0]; p.dvs1 = a->dv_stride[1]; p.dvs2 = a->dv_stride[2];
   p.dbeta = a->dbeta; p.dbs0 = a->dbeta_stride[0]; p.dbs1 = a->dbeta_stride[1]; p.dbs2 = a->dbeta_stride[2];
   p.ddecay = a->ddecay; p.dds0 = a->ddecay_stride[0]; p.dds1 = a->ddecay_stride[1]; p.dds2 = a->ddecay_stride[2];
-  p.dinit = a->d_initial_state;
-  p.dis0 = a->dinit_stride[0]; p.dis1 = a->dinit_stride[1]; p.dis2 = a->dinit_stride[2]; p.dis3 = a->dinit_stride[3];
-  p.ws = reinterpret_cast<float*>(a->workspace);
-  p.omt = reinterpret_cast<const bf16x8*>(static_cast<unsigned char*>(a->workspace) +
-                                          (size_t)(f->B * f->H * p.nch) * Rec::floats * sizeof(float));
-  const hipStream_t st = as_stream(stream), aux = aux_stream ? as_stream(aux_stream) : nullptr;
-  // bf16 inputs: the D = 512 contractions take bf16 operands with fp32 accumulation, the forward's
-  // policy for bf16 inputs; the lift and the 64 x 64 chunk algebra stay in fp32 MFMA.
-  if (f->in_dtype == KDN_DTYPE_BF16) return bwd_launch<PrecBF16, __bf16>(p, first, last, st, aux);
-  return bwd_launch<PrecF32, float>(p, first, last, st, aux);
+  p.gout = a->d_initial_state;
+  p.gos0 = a->dinit_stride[0]; p.gos1 = a->dinit_stride[1]; p.gos2 = a->dinit_stride[2]; p.gos3 = a->dinit_stride[3];
+  p.omt = reinterpret_cast<const bf16x8*>(static_cast<unsigned char*>(a->workspace) + L.omt_off);
+  return KDN_OK;
 }
 
-extern "C" int kdn_delta_scan_bwd(const kdn_scan_bwd_args* a, void* stream) {
-  return bwd_run(a, 0, 3, stream, nullptr);
+// bf16 inputs: the D = 512 contractions take bf16 operands with fp32 accumulation, the forward's policy
+// for bf16 inputs; the lift and the 64 x 64 chunk algebra stay in fp32 MFMA.
+static int bwd_run(const kdn_scan_bwd_args* a, void* stream, void* aux_stream) {
+  Params p;
+  BwdLayout L;
+  const int rc = bwd_params(a, p, L);
+  if (rc != KDN_OK) return rc;
+  const hipStream_t st = as_stream(stream), aux = aux_stream ? as_stream(aux_stream) : nullptr;
+  if (a->fwd->in_dtype == KDN_DTYPE_BF16) return bwd_schedule<PrecBF16, __bf16>(a, p, L, st, aux);
+  return bwd_schedule<PrecF32, float>(a, p, L, st, aux);
 }
+
+extern "C" int kdn_delta_scan_bwd(const kdn_scan_bwd_args* a, void* stream) { return bwd_run(a, stream, nullptr); }
 
 extern "C" int kdn_delta_scan_bwd_streams(const kdn_scan_bwd_args* a, void* stream, void* aux_stream) {
-  return bwd_run(a, 0, 3, stream, aux_stream);
+  return bwd_run(a, stream, aux_stream);
 }
 
-extern "C" int kdn_scan_bwd_phase(const kdn_scan_bwd_args* a, int phase, void* stream) {
-  if (phase < 0 || phase > 3) return KDN_ERR_INVALID_ARGUMENT;
-  return bwd_run(a, phase, phase, stream, nullptr);
+extern "C" int kdn_scan_bwd_phase(const kdn_scan_bwd_args* a, int phase, int64_t segment, void* stream) {
+  if (phase < 0 || phase > 4) return KDN_ERR_INVALID_ARGUMENT;
+  Params p;
+  BwdLayout L;
+  const int rc = bwd_params(a, p, L);
+  if (rc != KDN_OK) return rc;
+  const hipStream_t st = as_stream(stream);
+  if (phase == 0) return bwd_start(a, p, L, st, nullptr);
+  if (segment < 0 || segment >= L.nsegs) return KDN_ERR_INVALID_ARGUMENT;
+  const Params ps = segment_params(p, a, L, segment);
+  if (a->fwd->in_dtype == KDN_DTYPE_BF16) return segment_phase<PrecBF16, __bf16>(ps, phase, st);
+  return segment_phase<PrecF32, float>(ps, phase, st);
 }
 
 }  // namespace kdn

@@ -37,6 +37,17 @@ int scan_pipelined(const kdn_scan_args* a, const int64_t* seq_lo, const int64_t*
                    void* aux_stream, void* out_stream);
 size_t scan_workspace_bytes_pipelined(const kdn_scan_args* a);
 
+// Segment checkpoints of the D = 512, d_v = 64 scan (the backward's first pass): the states at the starts
+// of segments 1 .. n of `seg` chunks each, written as fp32 [B][H][512][64] arrays one after another from
+// `ckpt` (segment s's at ckpt + (s - 1) * B*H*512*64), by the scan's prep and state kernels alone (no
+// output kernel); segment 0 starts from a->initial_state (zeros if NULL).  Each equals, bit for bit, the
+// state that kdn_delta_scan_fwd with segment_chunks = seg carries across that boundary.  `ws` holds `nbuf`
+// buffers of `buf_bytes` >= scan_checkpoint_buffer_bytes(a, seg); with aux (not st) and two buffers, prep
+// of segment s + 1 runs on aux beside the state kernel of segment s.  The last launch is on st.
+size_t scan_checkpoint_buffer_bytes(const kdn_scan_args* a, int64_t seg);
+int scan_checkpoints(const kdn_scan_args* a, int64_t seg, int64_t n, float* ckpt, void* ws, size_t buf_bytes,
+                     int nbuf, hipStream_t st, hipStream_t aux);
+
 // The general-D scan (kdn_general.hip): D = 1024 over pre-lifted features, d_v 64 or 128, the delta rule,
 // uniform batches.  general_scan_applies selects it; the other functions assume it applies and that the
 // common argument checks have passed.
@@ -51,6 +62,7 @@ struct EventSet {
   hipEvent_t ev[16];
   int n = 0;
   int create(int count) {
+    if (count > 16) return KDN_ERR_INVALID_ARGUMENT;
     for (; n < count; ++n)
       if (hipEventCreateWithFlags(&ev[n], hipEventDisableTiming) != hipSuccess) return KDN_ERR_DEVICE;
     return KDN_OK;

@@ -970,6 +970,84 @@ static int run_phase(const kdn_scan_args* a, int64_t chunk0, int64_t nchunks, in
   return dispatch(a, chunk0, chunk0 + nchunks, nchunks, phase, as_stream(stream));
 }
 
+size_t scan_checkpoint_buffer_bytes(const kdn_scan_args* a, int64_t seg) {
+  return chunk_bytes(a) * (size_t)a->B * (size_t)a->H * (size_t)(seg + 1);
+}
+
+// The states at the starts of segments 1 .. n (of `seg` chunks) by the prep and state kernels alone; see
+// kdn_internal.hpp.
+template <class P, typename InT>
+static int checkpoints_t(const kdn_scan_args* a, int64_t seg, int64_t n, float* ckpt, unsigned char* ws,
+                         size_t buf_bytes, int nbuf, hipStream_t st, hipStream_t aux) {
+  const int64_t nchunks = (a->T + CH - 1) / CH;
+  const int64_t heads = a->B * a->H;
+  const size_t state_floats = (size_t)heads * 512 * 64;
+  const bool side = aux && aux != st && nbuf >= 2 && n >= 2;
+  const RunSpec r = {0, nchunks, seg, PHASE_PREP | PHASE_STATE, st, nullptr, 0, 0};
+  const int prep_cus = side ? device_cus() - (int)state_grid(a->B, a->H, 4) : device_cus();
+  auto seg_p = [&](int64_t s) {
+    const int64_t c0 = s * seg;
+    ScanParams p = segment_params(a, r, c0, (nchunks - c0 < seg) ? (nchunks - c0) : seg,
+                                  ws + (size_t)(side ? s % nbuf : 0) * buf_bytes, prep_cus);
+    p.relift_q = 1;  // no output kernel reads the lifted queries
+    p.y = nullptr;
+    if (s > 0) {
+      p.state_in = ckpt + (size_t)(s - 1) * state_floats;
+      p.is0 = a->H * 512 * 64; p.is1 = 512 * 64; p.is2 = 64; p.is3 = 1;
+    }
+    p.state_out = ckpt + (size_t)s * state_floats;
+    p.os0 = a->H * 512 * 64; p.os1 = 512 * 64; p.os2 = 64; p.os3 = 1;
+    return p;
+  };
+  if (!side) {
+    for (int64_t s = 0; s < n; ++s) {
+      const ScanParams p = seg_p(s);
+      int rc = launch_phase<P, InT, float, 512, 64>(p, PHASE_PREP, st);
+      if (rc == KDN_OK) rc = launch_phase<P, InT, float, 512, 64>(p, PHASE_STATE, st);
+      if (rc != KDN_OK) return rc;
+    }
+    return KDN_OK;
+  }
+  // prep(s + 1) on aux beside state(s) on st, over two buffers:
+  //   state(s) waits for prep(s) (event P[s % 2]); prep(s) waits for state(s - 2), the last reader of
+  //   its buffer (event S[s % 2]); st finally waits for nothing more (the last state kernel is on it)
+  EventSet evs;
+  int rc = evs.create(5);
+  if (rc != KDN_OK) return rc;
+  hipEvent_t* evP = evs.ev;
+  hipEvent_t* evS = evs.ev + 2;
+  hipEvent_t evIn = evs.ev[4];
+#define KDN_TRY(x) do { if ((x) != hipSuccess) return KDN_ERR_DEVICE; } while (0)
+#define KDN_TRYK(x) do { const int _rc = (x); if (_rc != KDN_OK) return _rc; } while (0)
+  KDN_TRY(hipEventRecord(evIn, st));
+  KDN_TRY(hipStreamWaitEvent(aux, evIn, 0));
+  KDN_TRYK((launch_phase<P, InT, float, 512, 64>(seg_p(0), PHASE_PREP, aux)));
+  KDN_TRY(hipEventRecord(evP[0], aux));
+  for (int64_t s = 0; s < n; ++s) {
+    KDN_TRY(hipStreamWaitEvent(st, evP[s % 2], 0));
+    KDN_TRYK((launch_phase<P, InT, float, 512, 64>(seg_p(s), PHASE_STATE, st)));
+    KDN_TRY(hipEventRecord(evS[s % 2], st));
+    if (s + 1 < n) {
+      if (s >= 1) KDN_TRY(hipStreamWaitEvent(aux, evS[(s + 1) % 2], 0));
+      KDN_TRYK((launch_phase<P, InT, float, 512, 64>(seg_p(s + 1), PHASE_PREP, aux)));
+      KDN_TRY(hipEventRecord(evP[(s + 1) % 2], aux));
+    }
+  }
+#undef KDN_TRY
+#undef KDN_TRYK
+  return KDN_OK;
+}
+
+int scan_checkpoints(const kdn_scan_args* a, int64_t seg, int64_t n, float* ckpt, void* ws, size_t buf_bytes,
+                     int nbuf, hipStream_t st, hipStream_t aux) {
+  if (n <= 0) return KDN_OK;
+  if (a->D != 512 || a->d_v != 64 || a->feature_mode != 0 || a->cu_seqlens || a->state_slots)
+    return KDN_ERR_UNSUPPORTED;
+  unsigned char* w = static_cast<unsigned char*>(ws);
+  if (a->in_dtype == KDN_DTYPE_BF16) return checkpoints_t<PrecBF16, __bf16>(a, seg, n, ckpt, w, buf_bytes, nbuf, st, aux);
+  return checkpoints_t<PrecF32, float>(a, seg, n, ckpt, w, buf_bytes, nbuf, st, aux);
+}
+
 }  // namespace kdn
 
 using namespace kdn;

@@ -48,6 +48,7 @@ EXPORTED = (
     "kdn_delta_scan_bwd",
     "kdn_delta_scan_bwd_streams",
     "kdn_scan_bwd_phase",
+    "kdn_scan_bwd_segments",
 )
 
 KDN_ERR_CAPACITY = -6
@@ -211,8 +212,10 @@ def lib() -> ctypes.CDLL:
             L.kdn_delta_scan_bwd_streams.restype = ci
             L.kdn_fwht_lift_factored.argtypes = [vp, i64, i64, ci, vp, vp, vp, vp, cf, vp, i64, ci, vp]
             L.kdn_fwht_lift_factored.restype = ci
-            L.kdn_scan_bwd_phase.argtypes = [ctypes.POINTER(ScanBwdArgs), ci, vp]
+            L.kdn_scan_bwd_phase.argtypes = [ctypes.POINTER(ScanBwdArgs), ci, i64, vp]
             L.kdn_scan_bwd_phase.restype = ci
+            L.kdn_scan_bwd_segments.argtypes = [ctypes.POINTER(ScanBwdArgs), ctypes.POINTER(ctypes.c_int64)]
+            L.kdn_scan_bwd_segments.restype = i64
             _lib = L
     return _lib
 

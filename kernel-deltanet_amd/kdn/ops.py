@@ -337,17 +337,20 @@ def scan(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, beta: torch.Tensor, 
 
 class ScanBackwardPlan:
     """One backward call of the scan (kdn_delta_scan_bwd) with its arguments, outputs and workspace
-    prepared once: run() issues the whole backward, phase(i) one of its four launches (0 per-chunk
-    recompute, 1 forward carry, 2 reverse carry, 3 gradients; in that order), e.g. for timing.
+    prepared once: run() issues the whole backward; phase(0) the start of a call (the checkpoint pass)
+    and phase(i, s) for i = 1 .. 4 one launch of segment s (1 per-chunk recompute, 2 forward carry,
+    3 reverse carry, 4 gradients), e.g. for timing: phase 0, then for s from segments - 1 down to 0
+    phases 1, 2, 3, 4.
 
     Same layouts as `scan`: q, k (B, T, H, 64), v and dy (B, T, H, 64), beta and decay (B, T, H), states
     (B, H, 512, 64); dL/dy = dy, dL/d(final state) = d_final_state (None: zero).  `outputs` holds the
     float32 gradients (dq, dk, dv, dbeta, ddecay or None, d_initial_state or None).  The structured lift
-    with one shared Omega and the delta rule only."""
+    with one shared Omega and the delta rule only.  segment_chunks (0: the library's default) sets the
+    backward's segment length in 64-token chunks; `segments` and `segment_chunks` hold the schedule."""
 
     def __init__(self, q, k, v, beta, decay, omega_bf16, phase, inv_tau, dy, d_final_state=None,
                  normalize: bool = False, initial_state=None, need_ddecay: bool = True, need_dinit: bool = True,
-                 workspace: Optional[torch.Tensor] = None):
+                 workspace: Optional[torch.Tensor] = None, segment_chunks: int = 0):
         for t, nm in ((q, "q"), (k, "k"), (v, "v"), (beta, "beta"), (dy, "dy")):
             require_device(t, f"scan_backward: {nm}")
         dev = q.device
@@ -375,8 +378,10 @@ class ScanBackwardPlan:
             if tuple(d_final_state.shape) != (B, H, D, d_v):
                 raise ValueError(f"scan_backward: d_final_state must be (B, H, D, d_v) = {(B, H, D, d_v)}")
         unused = torch.empty(1, device=dev, dtype=torch.float32).expand(B, H, D, d_v)  # fwd.final_state (ignored)
+        if segment_chunks < 0:
+            raise ValueError("scan_backward: segment_chunks must be >= 0")
         self._fa = scan_args(q, k, v, beta, decay, None, None, inv_tau, normalize, initial_state, unused, dy, None,
-                             0, fm)
+                             segment_chunks, fm)
         f32 = dict(device=dev, dtype=torch.float32)
         dq, dk = torch.empty(B, T, H, d_k, **f32), torch.empty(B, T, H, d_k, **f32)
         dv, dbeta = torch.empty(B, T, H, d_v, **f32), torch.empty(B, T, H, **f32)
@@ -402,6 +407,9 @@ class ScanBackwardPlan:
         if workspace is None or workspace.numel() * workspace.element_size() < nbytes:
             workspace = torch.empty(nbytes, dtype=torch.uint8, device=dev)
         a.workspace, a.workspace_bytes = workspace.data_ptr(), workspace.numel() * workspace.element_size()
+        seg = ctypes.c_int64(0)
+        self.segments = int(N.lib().kdn_scan_bwd_segments(ctypes.byref(a), ctypes.byref(seg)))
+        self.segment_chunks = int(seg.value)
         self.args, self.device, self.workspace = a, dev, workspace
         self.outputs = (dq, dk, dv, dbeta, ddecay, dinit)
         self.shape = (B, T, H)
@@ -422,9 +430,9 @@ class ScanBackwardPlan:
 
     def run(self, stream=None, concurrent_carries: bool = True):
         """Issues the whole backward on `stream` (default: the current stream).  With
-        concurrent_carries the reverse carry runs on the device's auxiliary stream 0 beside the forward
-        carry (kdn_delta_scan_bwd_streams), else all four launches run in order on `stream`
-        (kdn_delta_scan_bwd)."""
+        concurrent_carries the reverse carries run back to back on `stream` while the device's auxiliary
+        stream 0 runs the other launches around them (kdn_delta_scan_bwd_streams), else every launch runs
+        in order on `stream` (kdn_delta_scan_bwd).  The results are the same bit for bit."""
         st = self._st(stream)
         with torch.cuda.device(self.device):
             if concurrent_carries:
@@ -439,23 +447,25 @@ class ScanBackwardPlan:
                         "kdn_delta_scan_bwd")
         return self.outputs
 
-    def phase(self, i: int, stream=None):
+    def phase(self, i: int, segment: int = 0, stream=None):
         st = self._st(stream)
         with torch.cuda.device(self.device):
-            N.check(N.lib().kdn_scan_bwd_phase(ctypes.byref(self.args), int(i), ctypes.c_void_p(st.cuda_stream)),
-                    "kdn_scan_bwd_phase")
+            N.check(N.lib().kdn_scan_bwd_phase(ctypes.byref(self.args), int(i), int(segment),
+                                               ctypes.c_void_p(st.cuda_stream)), "kdn_scan_bwd_phase")
 
 
 def scan_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, beta: torch.Tensor,
                   decay: Optional[torch.Tensor], omega_bf16: torch.Tensor, phase: torch.Tensor, inv_tau: float,
                   dy: torch.Tensor, d_final_state: Optional[torch.Tensor] = None, normalize: bool = False,
                   initial_state: Optional[torch.Tensor] = None, need_ddecay: bool = True,
-                  need_dinit: bool = True, workspace: Optional[torch.Tensor] = None):
+                  need_dinit: bool = True, workspace: Optional[torch.Tensor] = None, segment_chunks: int = 0,
+                  concurrent_carries: bool = True):
     """Gradients of `scan` (kdn_delta_scan_bwd) for the loss with dL/dy = dy and dL/d(final state) =
-    d_final_state (None: zero); see ScanBackwardPlan for layouts.  Returns float32
+    d_final_state (None: zero); see ScanBackwardPlan for layouts and segment_chunks.  Returns float32
     (dq, dk, dv, dbeta, ddecay or None, d_initial_state or None)."""
     return ScanBackwardPlan(q, k, v, beta, decay, omega_bf16, phase, inv_tau, dy, d_final_state, normalize,
-                            initial_state, need_ddecay, need_dinit, workspace).run()
+                            initial_state, need_ddecay, need_dinit, workspace,
+                            segment_chunks).run(concurrent_carries=concurrent_carries)
 
 
 class _Scan(torch.autograd.Function):

@@ -62,7 +62,7 @@ def test_args_layout_matches_c(cname, pystruct):
 def test_strerror_and_version(lib):
     for code in (0, -1, -2, -3, -4, -5, -99):
         assert len(lib.kdn_strerror(code)) > 0
-    assert lib.kdn_abi_version() == (1 << 16) | 5
+    assert lib.kdn_abi_version() == (1 << 16) | 6
 
 
 def _args(**kw):
@@ -168,10 +168,25 @@ def test_backward_workspace_and_errors_need_no_device(lib):
     g.fwd = ctypes.addressof(f)
     for i, nm in enumerate(("dy", "dq", "dk", "dv", "dbeta", "workspace")):
         setattr(g, nm, 0x7E0000000000 + 0x100000 * i)
+    # one segment (the default at this size): its 4 chunk records per head and the Omega^T table
     assert lib.kdn_scan_bwd_workspace_bytes(ctypes.byref(g)) == 2 * 4 * 1116160 + 65536
+    seg = ctypes.c_int64(0)
+    assert lib.kdn_scan_bwd_segments(ctypes.byref(g), ctypes.byref(seg)) == 1 and seg.value == 4
+    # segments of one chunk: three rotating record buffers, three segment-start states and the carried
+    # dL/dS (2 heads x 512 x 64 fp32 each), two buffers of the forward scan's records for the checkpoint
+    # pass (2 records of 238,592 bytes per head), the table
+    f.segment_chunks = 1
+    assert lib.kdn_scan_bwd_segments(ctypes.byref(g), ctypes.byref(seg)) == 4 and seg.value == 1
+    assert lib.kdn_scan_bwd_workspace_bytes(ctypes.byref(g)) == \
+        3 * 2 * 1116160 + 4 * 2 * 512 * 64 * 4 + 2 * 2 * 2 * 238592 + 65536
+    g.workspace_bytes = 1 << 40
+    assert lib.kdn_scan_bwd_phase(ctypes.byref(g), 5, 0, None) == -1
+    assert lib.kdn_scan_bwd_phase(ctypes.byref(g), 1, 4, None) == -1   # segments 0 .. 3
+    assert lib.kdn_scan_bwd_phase(ctypes.byref(g), 2, -1, None) == -1
+    f.segment_chunks = 0
     g.workspace_bytes = 1024
     assert lib.kdn_delta_scan_bwd(ctypes.byref(g), None) == -3
-    assert lib.kdn_scan_bwd_phase(ctypes.byref(g), 4, None) == -1
+    assert lib.kdn_scan_bwd_phase(ctypes.byref(g), 1, 0, None) == -3
     f2 = _fake_ptrs(_args(T=256, H=2, d_v=32))
     g.fwd = ctypes.addressof(f2)
     assert lib.kdn_scan_bwd_workspace_bytes(ctypes.byref(g)) == 0

@@ -192,19 +192,87 @@ def test_backward_rejects_unsupported_shapes(proj):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_carries_on_two_streams_equal_one_stream(proj, dtype):
-    # kdn_delta_scan_bwd_streams runs the reverse carry on an auxiliary stream beside the forward carry;
-    # its results equal kdn_delta_scan_bwd's up to the summation order of the gradient kernel's LDS
-    # float atomics (which already varies between two runs on one stream).  Issued twice back to back
-    # so that the second call's prep overwrites records only after the first call's carries have read them.
+def test_two_streams_equal_one_stream_bit_for_bit(proj, dtype):
+    # kdn_delta_scan_bwd_streams runs the reverse carries on the launch stream and everything else on an
+    # auxiliary stream; every reduction has a fixed order, so its results equal kdn_delta_scan_bwd's bit
+    # for bit, and two runs on one stream agree bit for bit.  Segments of 4 chunks (6 segments over three
+    # rotating record buffers); issued twice back to back so that the second call's recompute overwrites
+    # records only after the first call's readers are done.
     q, k, v, beta, lam, s0, dy, ds = make(2, 1500, 4, dtype, seed=21)
     plan = ops.ScanBackwardPlan(q.to(DEV), k.to(DEV), v.to(DEV), beta.to(DEV), lam.to(DEV), proj.device_omega(DEV),
                                 proj.device_phase(DEV), proj.tau_star_inv, dy.to(DEV), ds.to(DEV),
-                                initial_state=s0.to(DEV))
+                                initial_state=s0.to(DEV), segment_chunks=4)
+    assert plan.segments == 6 and plan.segment_chunks == 4
     ref = [t.clone() for t in plan.run(concurrent_carries=False)]
+    again = [t.clone() for t in plan.run(concurrent_carries=False)]
     for _ in range(2):
         got = plan.run(concurrent_carries=True)
     torch.cuda.synchronize()
     names = ("dq", "dk", "dv", "dbeta", "ddecay", "dinit")
-    errs = {n: rel(g.cpu().numpy(), r.cpu().numpy()) for n, g, r in zip(names, got, ref)}
-    assert all(e < 1e-4 for e in errs.values()), errs
+    for n, g, a, r in zip(names, got, again, ref):
+        assert torch.equal(a, r), n
+        assert torch.equal(g, r), n
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_backward_parity_segmented(proj, oproj, dtype):
+    # one (batch, head) at T = 1500 (24 chunks, the last partial) in segments of 5 chunks (4 full segments
+    # and one of 4): the checkpoint pass, the carried dL/dS and the segment-local chunk indexing all count
+    args = make(1, 1500, 1, dtype, seed=22)
+    q, k, v, beta, lam, s0, dy, ds = args
+    dq, dk, dv, db, dd, di = ops.scan_backward(
+        q.to(DEV), k.to(DEV), v.to(DEV), beta.to(DEV), lam.to(DEV), proj.device_omega(DEV), proj.device_phase(DEV),
+        proj.tau_star_inv, dy.to(DEV), ds.to(DEV), initial_state=s0.to(DEV), segment_chunks=5)
+    got = {"dq": dq.cpu(), "dk": dk.cpu(), "dv": dv.cpu(), "dbeta": db.cpu(), "ddecay": dd.cpu(), "dinit": di.cpu()}
+    check(got, oracle_grads(*args, oproj), TOL[dtype])
+
+
+def test_segment_length_changes_only_rounding(proj):
+    # the same gradients in one segment and in segments of 3 chunks (fp32: rounding only)
+    q, k, v, beta, lam, s0, dy, ds = make(2, 1500, 2, torch.float32, seed=23)
+    runs = []
+    for seg in (0, 3):
+        dq, dk, dv, db, dd, di = ops.scan_backward(
+            q.to(DEV), k.to(DEV), v.to(DEV), beta.to(DEV), lam.to(DEV), proj.device_omega(DEV),
+            proj.device_phase(DEV), proj.tau_star_inv, dy.to(DEV), ds.to(DEV), initial_state=s0.to(DEV),
+            segment_chunks=seg)
+        runs.append([t.cpu() for t in (dq, dk, dv, db, dd, di)])
+    for n, a, b in zip(("dq", "dk", "dv", "dbeta", "ddecay", "dinit"), *runs):
+        assert rel(a.numpy(), b.numpy()) < 1e-5, n
+
+
+def test_backward_config4_shape(proj):
+    # B = 32, H = 16, T = 16384 (bf16, decay, initial state, dL/dS_T): the workspace is bounded by the
+    # segment (default 4 chunks at B*H = 512), every gradient is finite, and one (batch, head) equals bit
+    # for bit the backward of that head alone with the same segments (no kernel mixes heads), which the
+    # segmented parity test above pins to the float64 oracle
+    B, T, H = 32, 16384, 16
+    g = torch.Generator(device=DEV).manual_seed(24)
+    q = torch.randn(B, T, H, 64, generator=g, device=DEV).to(torch.bfloat16)
+    k = torch.randn(B, T, H, 64, generator=g, device=DEV).to(torch.bfloat16)
+    v = torch.randn(B, T, H, 64, generator=g, device=DEV).to(torch.bfloat16)
+    beta = torch.sigmoid(torch.randn(B, T, H, generator=g, device=DEV))
+    lam = 0.95 + 0.05 * torch.rand(B, T, H, generator=g, device=DEV)
+    s0 = 0.1 * torch.randn(B, H, 512, 64, generator=g, device=DEV)
+    dy = torch.randn(B, T, H, 64, generator=g, device=DEV)
+    ds = 0.5 * torch.randn(B, H, 512, 64, generator=g, device=DEV)
+    omega, phase = proj.device_omega(DEV), proj.device_phase(DEV)
+    plan = ops.ScanBackwardPlan(q, k, v, beta, lam, omega, phase, proj.tau_star_inv, dy, ds, initial_state=s0)
+    assert plan.segment_chunks == 4 and plan.segments == 64
+    # the records of three 4-chunk segments, 63 segment-start states and the carry, the checkpoint
+    # pass's two buffers and the table: about 12 GB, against 150 GB for records of every chunk
+    assert plan.workspace.numel() < 13 * 10**9
+    full = [t.clone() for t in plan.run()]
+    torch.cuda.synchronize()
+    for n, t in zip(("dq", "dk", "dv", "dbeta", "ddecay", "dinit"), full):
+        assert bool(torch.isfinite(t).all()), n
+    del plan
+    b, h = 5, 7
+    one = ops.scan_backward(q[b:b + 1, :, h:h + 1], k[b:b + 1, :, h:h + 1], v[b:b + 1, :, h:h + 1],
+                            beta[b:b + 1, :, h:h + 1], lam[b:b + 1, :, h:h + 1], omega, phase, proj.tau_star_inv,
+                            dy[b:b + 1, :, h:h + 1], ds[b:b + 1, h:h + 1].contiguous(),
+                            initial_state=s0[b:b + 1, h:h + 1].contiguous(), segment_chunks=4)
+    torch.cuda.synchronize()
+    for n, f, o in zip(("dq", "dk", "dv", "dbeta", "ddecay"), full, one):
+        assert torch.equal(f[b:b + 1, :, h:h + 1], o), n
+    assert torch.equal(full[5][b:b + 1, h:h + 1], one[5]), "dinit"

@@ -59,6 +59,7 @@ def test_ragged_workspace_query_needs_no_device():
     a = N.RaggedArgs()
     cu = np.array([0, 1, 2, 70, 70, 200], dtype=np.int64)
     a.num_seqs, a.H, a.d_k, a.D, a.d_v = 5, 16, 64, 512, 64
+    a.num_slots = 8
     a.in_dtype = a.out_dtype = 1
     a.inv_tau = 0.35
     a.cu_seqlens_host = cu.ctypes.data
