@@ -268,15 +268,22 @@ def bench_scan(args, dev):
     else:
         dom = max(phases, key=lambda p: phases[p]["ms"])
     achieved = phases[dom]["tflops"]
-    pmc_path = args.pmc or os.path.join(REPO, "profiles", f"pmc_config{cfg}.txt")
-    pmc = read_pmc(pmc_path) if (cfg == 3 and B == 1 and T == 65536 and H == 16 and dv == 64 and args.decay == "none") \
-        or args.pmc else {}
+    # Counter summaries committed under profiles/ for the measured shapes (rocprofv3 --pmc runs of this
+    # script): HBM bytes (FETCH_SIZE / WRITE_SIZE) and MFMA busy % (MfmaUtil) of the dominant kernel.
+    # The pipelined schedule runs the output kernel that lifts q again ("output_relift").
+    std = dv == 64 and H == 16 and args.decay == "none" and ((cfg == 3 and B == 1 and T == 65536) or
+                                                            (cfg == 4 and B == 32))
+    stem = f"pmc_config3" if cfg == 3 else f"pmc_config4_T{T}"
+    pmc = read_pmc(args.pmc) if args.pmc else (read_pmc(os.path.join(REPO, "profiles", stem + ".txt")) if std else {})
+    pmc_mfma = read_pmc(os.path.join(REPO, "profiles", stem + "_mfma.txt")) if std else {}
+    key = "output_relift" if (dom == "output" and plan.pipelined) else dom
     traffic = None
-    if f"{dom}_fetch_kib" in pmc and f"{dom}_write_kib" in pmc and "copy_fetch_kib" in pmc and "copy_write_kib" in pmc:
+    if f"{key}_fetch_kib" in pmc and f"{key}_write_kib" in pmc and "copy_fetch_kib" in pmc and "copy_write_kib" in pmc:
         copy_bytes = pmc.get("copy_bytes", 256 << 20)
         f_fac = copy_bytes / (pmc["copy_fetch_kib"] * 1024.0)
         w_fac = copy_bytes / (pmc["copy_write_kib"] * 1024.0)
-        traffic = pmc[f"{dom}_fetch_kib"] * 1024.0 * f_fac + pmc[f"{dom}_write_kib"] * 1024.0 * w_fac
+        traffic = pmc[f"{key}_fetch_kib"] * 1024.0 * f_fac + pmc[f"{key}_write_kib"] * 1024.0 * w_fac
+    mfma_util = pmc_mfma.get(f"{key}_mfma_util_pct")
     path_flops = fl["total"] * units
     name = ("config3: one Kernel-DeltaNet layer prefill" if cfg == 3 else
             "config4: batched long-context prefill (concurrent streams)")
@@ -301,7 +308,11 @@ def bench_scan(args, dev):
                    "schedule": "pipelined (state chain on the launch stream, prep and output on two auxiliary "
                                "streams)" if plan.pipelined else "serial", "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "achieved": achieved, "peak": MFMA_BF16_PEAK / 1e12, "unit": "TFLOP/s",
-                     "frac": achieved / (MFMA_BF16_PEAK / 1e12), "traffic": traffic, "kernel": dom},
+                     "frac": achieved / (MFMA_BF16_PEAK / 1e12), "traffic": traffic, "kernel": dom,
+                     "mfma_util": mfma_util,
+                     "mfma_util_source": (f"profiles/{stem}_mfma.txt ({key}_mfma_util_pct: rocprofv3 MfmaUtil, % "
+                                          "of the GPU's MFMA cycles over the dispatch run alone)")
+                     if mfma_util is not None else None},
         "phases": phases,
         "path": {"alg_flops": path_flops, "alg_bytes": path_bytes(B, T, H, D, dv),
                  "tflops": path_flops / ms_per_step / 1e9,
@@ -325,13 +336,18 @@ def bwd_flops_per_chunk(D: int, dv: int, dk: int = 64) -> dict:
       carry  K Sigma and K^T Z (2 C D dv each), W or Tp^T dW (2 C^2 dv)   -- forward and reverse alike
       grad   Q S^T (2 C D dv); dQ^T: S^T (a o dY)^T, K^T N^T; dK^T: Gamma (kappa o W)^T, S^T Zn^T, Q^T N,
              K^T (M + M^T) (2 D C dv or 2 D C^2 each); lift recompute and dx^ for q and k (2 C D dk each);
-             the 64 x 64 algebra T^T dW, dW X_K^T, dW V^T, dY W^T, dT T^T, Tp^T dW, T^T Y1 (2 C^2 dv or 2 C^3)"""
+             the 64 x 64 algebra T^T dW, dW X_K^T, dW V^T, dY W^T, dT T^T, Tp^T dW, T^T Y1 (2 C^2 dv or 2 C^3)
+    The checkpoint pass (the forward scan's prep and state kernels, once per chunk) counts as the forward
+    scan's prep (lift of q and k, K K^T and Q K^T, the inverse, U~ = T (beta o V)) and state (K S^T,
+    K^T E, Tp X_K) products.
+    """
     prep = 4 * C * D * dk + 4 * C * C * D + 2 * D * C * dv + 4 * C * C * dv + (2.0 / 3.0) * C ** 3
     carry = 4 * C * D * dv + 2 * C * C * dv
     grad = (2 * C * D * dv + (2 * D * dv * C + 2 * D * C * C) + (4 * D * dv * C + 4 * D * C * C)
             + 8 * C * D * dk + (5 * 2 * C * C * dv + 2 * 2 * C ** 3))
-    return {"prep": prep, "carry_fwd": carry, "carry_rev": carry, "grad": grad,
-            "total": prep + 2 * carry + grad}
+    ckpt = (4 * C * D * dk + 4 * C * C * D + (2.0 / 3.0) * C ** 3 + 2 * C * C * dv) + carry
+    return {"checkpoint": ckpt, "prep": prep, "carry_fwd": carry, "carry_rev": carry, "grad": grad,
+            "total": ckpt + prep + 2 * carry + grad}
 
 
 def cpu_backward_baseline(q, k, v, beta, dy, T_sample: int, H: int) -> dict:
@@ -370,27 +386,35 @@ def bench_backward(args, dev):
     dy = torch.randn(B, T, H, dv, generator=gd, device=dev)
     proj = FastWalshHadamardProjection(64, D, 42)
     plan = ops.ScanBackwardPlan(qd, kd, vd, bd, None, proj.device_omega(dev), proj.device_phase(dev),
-                                proj.tau_star_inv, dy, need_dinit=False)
+                                proj.tau_star_inv, dy, need_dinit=False, segment_chunks=args.segment_chunks)
     stream = torch.cuda.current_stream(dev)
     for _ in range(args.warmup):
-        plan.run()
+        plan.run(concurrent_carries=not args.serial)
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record(stream)
     for _ in range(args.steps):
-        plan.run()
+        plan.run(concurrent_carries=not args.serial)
     e1.record(stream)
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / args.steps
-    names = ("prep", "carry_fwd", "carry_rev", "grad")
+    # one phase at a time, on one stream: the checkpoint pass, then per segment (last first) the four
+    # launches of the segment
+    names = ("checkpoint", "prep", "carry_fwd", "carry_rev", "grad")
     timed = {n: [] for n in names}
+
+    def timed_phase(n, i, s):
+        a0, a1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a0.record(stream)
+        plan.phase(i, s)
+        a1.record(stream)
+        timed[n].append((a0, a1))
+
     for _ in range(args.steps):
-        for i, n in enumerate(names):
-            a0, a1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            a0.record(stream)
-            plan.phase(i)
-            a1.record(stream)
-            timed[n].append((a0, a1))
+        timed_phase("checkpoint", 0, 0)
+        for s in reversed(range(plan.segments)):
+            for i in range(1, 5):
+                timed_phase(names[i], i, s)
     torch.cuda.synchronize()
     fl = bwd_flops_per_chunk(D, dv)
     nch = (T + C - 1) // C
@@ -398,7 +422,8 @@ def bench_backward(args, dev):
     phases = {}
     for n in names:
         pm = sum(x.elapsed_time(y) for x, y in timed[n]) / args.steps
-        phases[n] = {"ms": pm, "launches": 1, "avg_launch_ms": pm, "alg_flops": fl[n] * units,
+        launches = 1 if n == "checkpoint" else plan.segments
+        phases[n] = {"ms": pm, "launches": launches, "avg_launch_ms": pm / launches, "alg_flops": fl[n] * units,
                      "tflops": fl[n] * units / pm / 1e9}
     dom = max(phases, key=lambda x: phases[x]["ms"])
     achieved = phases[dom]["tflops"]
@@ -410,9 +435,12 @@ def bench_backward(args, dev):
         "config": {"workload": f"backward of config3 (one layer, B={B}, H={H}, T={T}, d_k=64->D={D}, d_v={dv}, "
                                f"bf16 q/k/v, fp32 beta, lambda=1)", "B": B, "H": H, "T": T, "D": D, "d_v": dv,
                    "workspace_bytes": plan.workspace.numel(), "parallelism": "single GPU",
-                   "schedule": "recompute, then the forward carry on the launch stream beside the reverse carry "
-                               "on an auxiliary stream, then gradients (kdn_delta_scan_bwd_streams); the "
-                               "per-phase times below are measured one phase at a time"},
+                   "segments": plan.segments, "segment_chunks": plan.segment_chunks,
+                   "schedule": "checkpoint pass (forward prep + state kernels, prep on an auxiliary stream), "
+                               "then per segment, last first, the reverse carries back to back on the launch "
+                               "stream while the auxiliary stream recomputes, carries forward and writes the "
+                               "gradients of the segments around them (kdn_delta_scan_bwd_streams); the "
+                               "per-phase times below are measured one phase at a time on one stream"},
         "roofline": {"bound": "mfma", "achieved": achieved, "peak": MFMA_BF16_PEAK / 1e12, "unit": "TFLOP/s",
                      "frac": achieved / (MFMA_BF16_PEAK / 1e12), "traffic": None, "kernel": dom},
         "phases": phases,
