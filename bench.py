@@ -139,6 +139,9 @@ def main():
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain device copy of known size (for PMC byte-counter calibration)")
     ap.add_argument("--pmc", default=None)
+    ap.add_argument("--lift-variant", default="table", choices=("table", "bits", "butterfly"),
+                    help="config 2: kdn_fwht_lift (resident Omega table), kdn_fwht_lift_bits (Omega built from the "
+                         "sign table per workgroup) or kdn_fwht_lift_bits_butterfly (in-register butterflies)")
     ap.add_argument("--factored", action="store_true",
                     help="time the factored d_k = 128 path (two 64 -> 512 lifts, D = 1024 scan, d_v = 128) on a "
                          "B=1, H=32, T=16384 layer instead of config 3")
@@ -623,23 +626,34 @@ def bench_lift(args, dev):
     g = torch.Generator(device=dev).manual_seed(1234)
     x = torch.randn(rows, 64, generator=g, device=dev).to(torch.bfloat16)
     proj = FastWalshHadamardProjection(64, D, 42)
-    om, ph = proj.device_omega(dev), proj.device_phase(dev)
+    om, ph, bits = proj.device_omega(dev), proj.device_phase(dev), proj.device_bits(dev)
     stream = torch.cuda.current_stream(dev)
+    variant = args.lift_variant
+
+    def lift_once():
+        if variant == "table":     # kdn_fwht_lift: Omega from the resident bf16 table, MFMA projection
+            return ops.lift(x, om, ph, proj.tau_star_inv, normalize=True)
+        # kdn_fwht_lift_bits (Omega built in LDS per workgroup, MFMA projection) or
+        # kdn_fwht_lift_bits_butterfly (in-register wave64 butterflies, no Omega)
+        return ops.lift_bits(x, bits, ph, proj.tau_star_inv, normalize=True, butterfly=variant == "butterfly")
+
     for _ in range(args.warmup):
-        y = ops.lift(x, om, ph, proj.tau_star_inv, normalize=True)
+        y = lift_once()
     torch.cuda.synchronize()
     evs = []
     for _ in range(args.steps):
         a0, a1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         a0.record(stream)
-        y = ops.lift(x, om, ph, proj.tau_star_inv, normalize=True)
+        y = lift_once()
         a1.record(stream)
         evs.append((a0, a1))
     torch.cuda.synchronize()
     ms = sorted(a.elapsed_time(b) for a, b in evs)[len(evs) // 2]
     alg_bytes = rows * (64 + D) * 2
     achieved = alg_bytes / (ms / 1e3) / 1e9
-    pmc = read_pmc(args.pmc or os.path.join(REPO, "profiles", "pmc_config2.txt")) if rows == 2097152 else {}
+    std = rows == 2097152 and variant == "table"
+    pmc = read_pmc(args.pmc) if args.pmc else (read_pmc(os.path.join(REPO, "profiles", "pmc_config2.txt")) if std else {})
+    pmc_mfma = read_pmc(os.path.join(REPO, "profiles", "pmc_config2_mfma.txt")) if std else {}
     traffic = None
     if all(k in pmc for k in ("lift_fetch_kib", "lift_write_kib", "copy_fetch_kib", "copy_write_kib")):
         copy_bytes = pmc.get("copy_bytes", 256 << 20)
@@ -651,9 +665,13 @@ def bench_lift(args, dev):
         "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic (seeded N(0,1) x; projection seed 42)",
         "config": {"workload": f"config2: standalone lift, x [{rows}, 64] bf16 L2-normalised -> [{rows}, 512] bf16 "
-                               f"(B={B}, T={T}, H={args.H})", "rows": rows, "D": D, "parallelism": "single GPU"},
+                               f"(B={B}, T={T}, H={args.H})", "rows": rows, "D": D, "parallelism": "single GPU",
+                   "lift_variant": variant},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK / 1e9, "unit": "GB/s",
-                     "frac": achieved * 1e9 / HBM_PEAK, "traffic": traffic, "kernel": "lift"},
+                     "frac": achieved * 1e9 / HBM_PEAK, "traffic": traffic,
+                     "kernel": "lift" if variant != "butterfly" else "lift_butterfly",
+                     "mfma_util": pmc_mfma.get("lift_mfma_util_pct"),
+                     "mfma_util_source": "profiles/pmc_config2_mfma.txt (lift_mfma_util_pct)" if pmc_mfma else None},
     }
     if args.cpu_tokens > 0:
         from oracle import lift as ol

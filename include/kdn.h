@@ -98,6 +98,16 @@ int kdn_fwht_lift_bits(const void* x, int64_t rows, int64_t x_row_stride, int x_
                        const int64_t* rademacher_bits, int D_lifted, float tau_star_inv, const float* phase,
                        int normalize_input, void* out, int64_t out_row_stride, int out_dtype, void* stream);
 
+/* kdn_fwht_lift_bits with the projection by in-register wave64 butterflies (ABI 1.6): the design of the
+ * reference's CUDA lift, kernels/in_register_fwht.cu:10-93 (one wave per row, the sign flips and three
+ * Walsh-Hadamard transforms per 64-feature block, no Omega table), with the semantics of
+ * kernels/fwht.py:122-131.  Same arguments, checks and results up to fp32 summation order; kept as the
+ * measured alternative to the MFMA projection of kdn_fwht_lift_bits, which is faster on gfx950. */
+int kdn_fwht_lift_bits_butterfly(const void* x, int64_t rows, int64_t x_row_stride, int x_dtype, int d_k,
+                                 const int64_t* rademacher_bits, int D_lifted, float tau_star_inv,
+                                 const float* phase, int normalize_input, void* out, int64_t out_row_stride,
+                                 int out_dtype, void* stream);
+
 /* Factored lift for d_k = 128 -> D = 1024 (ABI 1.4): out[r][0:512] = lift(x[r][0:64]; omega1, phase1),
  * out[r][512:1024] = lift(x[r][64:128]; omega2, phase2) (each as kdn_fwht_lift without input
  * normalisation, the two projections of seeds s and s + 1000), then out[r] <- out[r] / (||out[r]|| + 1e-7).
@@ -239,11 +249,11 @@ int kdn_scan_output(const kdn_scan_args* a, int64_t chunk0, int64_t nchunks, voi
  * NULL.  The gradient of lambda is zero where the forward's clamp to [1e-5, 1] is active.
  *
  * The backward runs in segments of fwd->segment_chunks 64-token chunks (0: the largest power of two
- * from 4 to 64 whose per-chunk records fit 1.25 GiB), last segment first: a checkpoint pass of the
+ * from 4 to 64 whose per-chunk records fit 1.5 GiB), last segment first: a checkpoint pass of the
  * forward scan's prep and state kernels stores the state at each segment start, then each segment
  * recomputes its chunks, carries the state forward from its checkpoint and dL/dS backward from the
  * next segment, and writes its gradients.  The workspace (256-byte aligned) holds up to three segments'
- * fp32 records (1,116,160 bytes per (batch, head, chunk)), one fp32 [B][H][512][64] state per segment
+ * records (1,247,232 bytes per (batch, head, chunk)), one fp32 [B][H][512][64] state per segment
  * boundary plus one more, up to two buffers of the forward scan's records and a 64 KB table: it grows
  * with the segment, not with T, apart from the 128 KB per head per segment boundary.  Every reduction
  * runs in a fixed order: the results are identical bit for bit from run to run and between

@@ -45,6 +45,11 @@ constexpr size_t OMT_BYTES = (size_t)4 * 16 * 64 * 16;  // the Omega^T fragment 
 // row sums of A o dA.
 constexpr int DL_KAPPA = 0, DL_COLP = 1, DL_RP = 5, DL_TS = 6, DL_DA = 7, DL_DLC = 8, DL_A = 12, NDL = 13;
 
+// Fragment slots of the dx kernel's B operands in the record's K-fragment area: token tile m (0..3),
+// operand o, 32-token depth block jb; 32 slots for dK^T (4 operands) then 16 for dQ^T (2 operands).
+__host__ __device__ constexpr int bop_dk(int m, int o, int jb) { return (m * 4 + o) * 2 + jb; }
+__host__ __device__ constexpr int bop_dq(int m, int o, int jb) { return 32 + (m * 2 + o) * 2 + jb; }
+
 // Per (head, chunk) record, offsets in floats.
 struct Rec {
   static constexpr size_t Q = 0;                // [64][512] lifted, normalised q rows (0 past T)
@@ -69,9 +74,11 @@ struct Rec {
   // precision policy's fragment type (bf16x8 or f32x8; the area is sized for f32x8):
   static constexpr size_t KXF = VEC + 512;      // [m 4][jb 16][lane]: rows 16m.., features 32jb..
   static constexpr size_t KTF = KXF + C * D;    // [ft 32][jb 2][lane]: K^T rows 16ft.., tokens 32jb..
-  static constexpr size_t floats = KTF + C * D;
+  static constexpr size_t QTF = KTF + C * D;    // [ft 32][jb 2][lane]: Q^T rows 16ft.., tokens 32jb..
+  static constexpr size_t floats = QTF + C * D;
 };
 static_assert((Rec::floats * 4) % 256 == 0, "records stay 256-byte aligned");
+static_assert(48 * 64 * sizeof(f32x8) <= (Rec::KTF - Rec::KXF) * sizeof(float), "the dx operands fit the K-fragment area");
 
 struct Params {
   int64_t B, T, H, nch;
@@ -99,6 +106,67 @@ struct Params {
 // Record of local chunk c (0 .. nseg - 1) of the segment.
 __device__ __forceinline__ float* record(const Params& p, int64_t b, int64_t h, int64_t c) {
   return p.ws + ((b * p.H + h) * p.cap + c) * (int64_t)Rec::floats;
+}
+
+// The lifted rows Q, K and the carried S^T, Gamma are stored in their record areas as bf16 under the bf16
+// policy (every product that reads them rounds its operands to bf16 anyway; the lift backward's
+// phi . dphi and <Gamma, S> read the rounded values) and as fp32 under the fp32 policy.
+template <class P> struct Feat { typedef float T; };
+template <> struct Feat<PrecBF16> { typedef __bf16 T; };
+template <class P> struct IsBf16Policy : std::integral_constant<bool, std::is_same<P, PrecBF16>::value> {};
+template <class P>
+__device__ __forceinline__ typename Feat<P>::T* feat(float* rec, size_t off) {
+  return reinterpret_cast<typename Feat<P>::T*>(rec + off);
+}
+template <class P>
+__device__ __forceinline__ const typename Feat<P>::T* feat(const float* rec, size_t off) {
+  return reinterpret_cast<const typename Feat<P>::T*>(rec + off);
+}
+__device__ __forceinline__ f32x8 frag_rows_t(const float* b, int ld, int r0, int k0, int lane) { return frag_rows(b, ld, r0, k0, lane); }
+__device__ __forceinline__ f32x8 frag_rows_t(const __bf16* b, int ld, int r0, int k0, int lane) { return frag_rows_bf16(b, ld, r0, k0, lane); }
+__device__ __forceinline__ f32x8 frag_cols_t(const float* b, int ld, int c0, int k0, int lane) { return frag_cols(b, ld, c0, k0, lane); }
+__device__ __forceinline__ f32x8 frag_cols_t(const __bf16* b, int ld, int c0, int k0, int lane) { return frag_cols_bf16(b, ld, c0, k0, lane); }
+__device__ __forceinline__ f32x4 ld4_t(const float* p) { return *reinterpret_cast<const f32x4*>(p); }
+__device__ __forceinline__ f32x4 ld4_t(const __bf16* p) {
+  typedef __attribute__((ext_vector_type(4))) __bf16 bf16x4;
+  const bf16x4 v = *reinterpret_cast<const bf16x4*>(p);
+  const f32x4 r = {(float)v[0], (float)v[1], (float)v[2], (float)v[3]};
+  return r;
+}
+
+// Operand fragments straight in the policy's type (no fp32 round trip for bf16 data):
+//   frag_rows_p: kappa-ordered rows of a record matrix in its storage type (as frag_rows)
+//   omega_frag:  rows r0.. of the bf16 Omega [D][64], plain depth order (as frag_rows_plain_bf16)
+//   bf16_frag:   a bf16x8 fragment
+template <class P>
+__device__ __forceinline__ typename P::frag frag_rows_p(const typename Feat<P>::T* b, int ld, int r0, int k0, int lane) {
+  if constexpr (IsBf16Policy<P>::value) {
+    typedef __attribute__((ext_vector_type(4))) __bf16 bf16x4;
+    const __bf16* q = b + (size_t)(r0 + (lane & 15)) * ld + k0 + 4 * (lane >> 4);
+    const bf16x4 lo = *reinterpret_cast<const bf16x4*>(q);
+    const bf16x4 hi = *reinterpret_cast<const bf16x4*>(q + 16);
+    return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+  } else {
+    return frag_rows(b, ld, r0, k0, lane);
+  }
+}
+template <class P>
+__device__ __forceinline__ typename P::frag omega_frag(const __bf16* omega, int r0, int k0, int lane) {
+  if constexpr (IsBf16Policy<P>::value)
+    return *reinterpret_cast<const bf16x8*>(omega + (size_t)(r0 + (lane & 15)) * DK + k0 + 8 * (lane >> 4));
+  else
+    return frag_rows_plain_bf16(omega, DK, r0, k0, lane);
+}
+template <class P>
+__device__ __forceinline__ typename P::frag bf16_frag(const bf16x8& t) {
+  if constexpr (IsBf16Policy<P>::value) {
+    return t;
+  } else {
+    f32x8 r;
+#pragma unroll
+    for (int s = 0; s < 8; ++s) r[s] = (float)t[s];
+    return r;
+  }
 }
 
 
@@ -140,12 +208,17 @@ __device__ __forceinline__ void round_like_input(int normalize, float* part) {
 // ---------------------------------------------------------------------------------------------- prep
 // grid (nch, H, B), 256 threads.
 template <class P, typename InT>
-__global__ void __launch_bounds__(256) bwd_prep_kernel(Params p) {
-  __shared__ __attribute__((aligned(16))) float xs[C * LD];   // normalised x rows; later beta o V
-  __shared__ __attribute__((aligned(16))) float bA[C * LD];   // a o dY; later A
-  __shared__ __attribute__((aligned(16))) float bT[C * LD];   // T
-  __shared__ __attribute__((aligned(16))) float bP[C * LD];   // P
-  __shared__ __attribute__((aligned(16))) float bY[C * LD];   // dY
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) bwd_prep_kernel(Params p) {
+  // Four 64 x 64 tiles (71 KB with the vectors), so that two workgroups share a CU.
+  __shared__ __attribute__((aligned(16))) float smem[4 * C * LD];
+  float* xs = smem;               // normalised x rows; then beta o V; then dY
+  float* bA = smem + C * LD;      // a o dY; later A
+  float* bT = smem + 2 * C * LD;  // T
+  float* bP = smem + 3 * C * LD;  // P
+  // bT and bP are free during the lift: there each wave stages its 128 features of 32 token rows (bf16,
+  // rows padded to 272 bytes against bank conflicts) to write the record's rows 16 bytes per lane
+  constexpr int STG_ROW = 272, STG_WAVE = 32 * STG_ROW;
+  static_assert(4 * STG_WAVE <= 2 * C * LD * (int)sizeof(float), "the lift's staging fits bT and bP");
   __shared__ float s_ell[C], s_beta[C], s_n[C], s_red[4][C];
 
   const int64_t h = blockIdx.y, b = blockIdx.z;
@@ -172,14 +245,14 @@ __global__ void __launch_bounds__(256) bwd_prep_kernel(Params p) {
     rec[Rec::VEC + lane] = l;
     rec[Rec::VEC + 64 + lane] = be;
   }
-#pragma unroll
-  for (int e = 0; e < 16; ++e)
-    bY[r * LD + c0 + e] = rvalid ? p.dy[b * p.ys0 + (t0 + r) * p.ys1 + h * p.ys2 + c0 + e] : 0.f;
-  __syncthreads();
   {
+    float dyp[16];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) dyp[e] = rvalid ? p.dy[b * p.ys0 + (t0 + r) * p.ys1 + h * p.ys2 + c0 + e] : 0.f;
+    __syncthreads();
     const float a = r == 0 ? 1.f : expf(s_ell[r - 1]);
 #pragma unroll
-    for (int e = 0; e < 16; ++e) bA[r * LD + c0 + e] = a * bY[r * LD + c0 + e];
+    for (int e = 0; e < 16; ++e) bA[r * LD + c0 + e] = a * dyp[e];
   }
 
   const float amp = sqrtf(2.f / D);
@@ -195,7 +268,7 @@ __global__ void __launch_bounds__(256) bwd_prep_kernel(Params p) {
 
     // phi~ (tokens x this wave's 128 features), in two halves of 32 tokens: tile [ft][u] holds rows
     // token 16 (2 hm + u) + .., column feature.  Normalised rows go straight to the record.
-    float* phi = rec + (which == 0 ? Rec::Q : Rec::K);
+    typename Feat<P>::T* phi = feat<P>(rec, which == 0 ? Rec::Q : Rec::K);
     for (int hm = 0; hm < 2; ++hm) {
       f32x4 acc[8][2];
       f32x8 xa[2][2];
@@ -249,15 +322,56 @@ __global__ void __launch_bounds__(256) bwd_prep_kernel(Params p) {
         rec[Rec::VEC + 128 + 64 * which + row] = n;
       }
       __syncthreads();
+      // The normalised tiles: the q^T / k^T fragments of depth block hm straight from the registers (an
+      // accumulator tile pair [ft][0..1] is the fragment of feature tile ft, tokens 32 hm + kappa), and
+      // the record's rows.
+      {
+        using frag = typename P::frag;
+        frag* tf = reinterpret_cast<frag*>(rec + (which == 0 ? Rec::QTF : Rec::KTF));
+        f32x4 sc[2];
 #pragma unroll
-      for (int u = 0; u < 2; ++u)
+        for (int u = 0; u < 2; ++u)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int row = 32 * hm + 16 * u + 4 * (lane >> 4) + i;
-          const float sc = (t0 + row < p.T) ? 1.f / (s_n[row] + 1e-8f) : 0.f;
+          for (int i = 0; i < 4; ++i) {
+            const int row = 32 * hm + 16 * u + 4 * (lane >> 4) + i;
+            sc[u][i] = (t0 + row < p.T) ? 1.f / (s_n[row] + 1e-8f) : 0.f;
+          }
 #pragma unroll
-          for (int ft = 0; ft < 8; ++ft) phi[(size_t)row * D + 128 * w + 16 * ft + (lane & 15)] = acc[ft][u][i] * sc;
+        for (int ft = 0; ft < 8; ++ft) {
+          acc[ft][0] = acc[ft][0] * sc[0];
+          acc[ft][1] = acc[ft][1] * sc[1];
+          tf[((8 * w + ft) * 2 + hm) * 64 + lane] = P::from_f32(pair_to8(acc[ft][0], acc[ft][1]));
         }
+        if constexpr (IsBf16Policy<P>::value) {
+          // rows through this wave's staging area: 2-byte LDS writes, then 16-byte global stores
+          unsigned char* stg = reinterpret_cast<unsigned char*>(bT) + w * STG_WAVE;
+#pragma unroll
+          for (int ft = 0; ft < 8; ++ft)
+#pragma unroll
+            for (int u = 0; u < 2; ++u)
+#pragma unroll
+              for (int i = 0; i < 4; ++i)
+                *reinterpret_cast<__bf16*>(stg + (16 * u + 4 * (lane >> 4) + i) * STG_ROW + 2 * (16 * ft + (lane & 15))) =
+                    (__bf16)acc[ft][u][i];
+          wave_lds_sync();
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {  // 32 rows x 16 pieces of 16 bytes
+            const int q = 64 * j + lane, row = q >> 4, pc = q & 15;
+            *reinterpret_cast<bf16x8*>(phi + (size_t)(32 * hm + row) * D + 128 * w + 8 * pc) =
+                *reinterpret_cast<const bf16x8*>(stg + row * STG_ROW + 16 * pc);
+          }
+          wave_lds_sync();
+        } else {
+#pragma unroll
+          for (int u = 0; u < 2; ++u)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const int row = 32 * hm + 16 * u + 4 * (lane >> 4) + i;
+#pragma unroll
+              for (int ft = 0; ft < 8; ++ft) phi[(size_t)row * D + 128 * w + 16 * ft + (lane & 15)] = acc[ft][u][i];
+            }
+        }
+      }
     }
     __syncthreads();
   }
@@ -265,44 +379,37 @@ __global__ void __launch_bounds__(256) bwd_prep_kernel(Params p) {
   __syncthreads();
 
   // K packed in fragment order for the chains: wave w the K-row fragments of feature blocks 4w .. 4w+3
-  // and the K^T-row fragments of feature tiles 8w .. 8w+7.
+  // (the K^T fragments went to the record during the lift).
   {
     using frag = typename P::frag;
-    const float* K = rec + Rec::K;
+    const typename Feat<P>::T* K = feat<P>(rec, Rec::K);
     frag* kxf = reinterpret_cast<frag*>(rec + Rec::KXF);
-    frag* ktf = reinterpret_cast<frag*>(rec + Rec::KTF);
 #pragma unroll
     for (int m = 0; m < 4; ++m)
 #pragma unroll
-      for (int jj = 0; jj < 4; ++jj)
-        kxf[(m * 16 + 4 * w + jj) * 64 + lane] = P::from_f32(frag_rows(K, D, 16 * m, 32 * (4 * w + jj), lane));
-#pragma unroll
-    for (int t = 0; t < 8; ++t)
-#pragma unroll
-      for (int jb = 0; jb < 2; ++jb)
-        ktf[((8 * w + t) * 2 + jb) * 64 + lane] = P::from_f32(frag_cols(K, D, 16 * (8 * w + t), 32 * jb, lane));
+      for (int jj = 0; jj < 4; ++jj) kxf[(m * 16 + 4 * w + jj) * 64 + lane] = frag_rows_p<P>(K, D, 16 * m, 32 * (4 * w + jj), lane);
   }
 
-  // H = Q^T (a o dY) from the Q rows just written (A = Q^T fragments, B = a o dY from LDS).
+  // H = Q^T (a o dY) (A = the Q^T fragments this wave stored during the lift, B = a o dY from LDS).
   {
-    const float* Q = rec + Rec::Q;
-    f32x8 yb[4][2];
+    using frag = typename P::frag;
+    const frag* qtf = reinterpret_cast<const frag*>(rec + Rec::QTF);
+    frag yb[4][2];
 #pragma unroll
     for (int n = 0; n < 4; ++n)
 #pragma unroll
-      for (int jb = 0; jb < 2; ++jb) yb[n][jb] = frag_cols(bA, LD, 16 * n, 32 * jb, lane);
-    f32x8 qn0 = frag_cols(Q, D, 128 * w, 0, lane), qn1 = frag_cols(Q, D, 128 * w, 32, lane);
+      for (int jb = 0; jb < 2; ++jb) yb[n][jb] = P::from_f32(frag_cols(bA, LD, 16 * n, 32 * jb, lane));
+    frag qn0 = qtf[((8 * w) * 2 + 0) * 64 + lane], qn1 = qtf[((8 * w) * 2 + 1) * 64 + lane];
 #pragma unroll
     for (int ft = 0; ft < 8; ++ft) {
-      const int f0 = 128 * w + 16 * ft;
-      const f32x8 qa0 = qn0, qa1 = qn1;
+      const frag qa0 = qn0, qa1 = qn1;
       if (ft + 1 < 8) {
-        qn0 = frag_cols(Q, D, f0 + 16, 0, lane);
-        qn1 = frag_cols(Q, D, f0 + 16, 32, lane);
+        qn0 = qtf[((8 * w + ft + 1) * 2 + 0) * 64 + lane];
+        qn1 = qtf[((8 * w + ft + 1) * 2 + 1) * 64 + lane];
       }
 #pragma unroll
       for (int n = 0; n < 4; ++n) {
-        const f32x4 hv = mm<P>(mm<P>(zero4(), qa0, yb[n][0]), qa1, yb[n][1]);
+        const f32x4 hv = P::mma(P::mma(zero4(), qa0, yb[n][0]), qa1, yb[n][1]);
         reinterpret_cast<f32x4*>(rec + Rec::H1)[((8 * w + ft) * 4 + n) * 64 + lane] = hv;
       }
       __builtin_amdgcn_sched_barrier(0);
@@ -312,20 +419,20 @@ __global__ void __launch_bounds__(256) bwd_prep_kernel(Params p) {
 
   // Gram matrices (row tile w) from the rows just written; A and P into LDS.
   {
-    const float* K = rec + Rec::K;
-    const float* Q = rec + Rec::Q;
+    const typename Feat<P>::T* K = feat<P>(rec, Rec::K);
+    const typename Feat<P>::T* Q = feat<P>(rec, Rec::Q);
     f32x4 gkk[4], gqk[4];
 #pragma unroll
     for (int n = 0; n < 4; ++n) gkk[n] = gqk[n] = zero4();
 #pragma unroll 4
     for (int jb = 0; jb < D / 32; ++jb) {
-      const f32x8 kw = frag_rows(K, D, 16 * w, 32 * jb, lane);
-      const f32x8 qw = frag_rows(Q, D, 16 * w, 32 * jb, lane);
+      const typename P::frag kw = frag_rows_p<P>(K, D, 16 * w, 32 * jb, lane);
+      const typename P::frag qw = frag_rows_p<P>(Q, D, 16 * w, 32 * jb, lane);
 #pragma unroll
       for (int n = 0; n < 4; ++n) {
-        const f32x8 kn = frag_rows(K, D, 16 * n, 32 * jb, lane);
-        gkk[n] = mm<P>(gkk[n], kw, kn);
-        gqk[n] = mm<P>(gqk[n], qw, kn);
+        const typename P::frag kn = frag_rows_p<P>(K, D, 16 * n, 32 * jb, lane);
+        gkk[n] = P::mma(gkk[n], kw, kn);
+        gqk[n] = P::mma(gqk[n], qw, kn);
       }
     }
 #pragma unroll
@@ -362,15 +469,26 @@ __global__ void __launch_bounds__(256) bwd_prep_kernel(Params p) {
     for (int e = 0; e < 16; ++e) xs[r * LD + c0 + e] = rvalid ? be * ldx(v + vb + e) : 0.f;
   }
   __syncthreads();
-  // U~ = T (beta o V), R = P^T dY (row tile w).
+  // U~ = T (beta o V) (row tile w)
   {
     const f32x8 ta0 = frag_rows(bT, LD, 16 * w, 0, lane), ta1 = frag_rows(bT, LD, 16 * w, 32, lane);
-    const f32x8 pa0 = frag_cols(bP, LD, 16 * w, 0, lane), pa1 = frag_cols(bP, LD, 16 * w, 32, lane);
 #pragma unroll
     for (int n = 0; n < 4; ++n) {
       const f32x4 u = mm<PrecF32>(mm<PrecF32>(zero4(), ta0, frag_cols(xs, LD, 16 * n, 0, lane)), ta1, frag_cols(xs, LD, 16 * n, 32, lane));
-      const f32x4 rr = mm<PrecF32>(mm<PrecF32>(zero4(), pa0, frag_cols(bY, LD, 16 * n, 0, lane)), pa1, frag_cols(bY, LD, 16 * n, 32, lane));
       reinterpret_cast<f32x4*>(rec + Rec::U)[(w * 4 + n) * 64 + lane] = u;
+    }
+  }
+  __syncthreads();  // beta o V is dead: dY again (the same fp32 values) in its place
+#pragma unroll
+  for (int e = 0; e < 16; ++e)
+    xs[r * LD + c0 + e] = rvalid ? p.dy[b * p.ys0 + (t0 + r) * p.ys1 + h * p.ys2 + c0 + e] : 0.f;
+  __syncthreads();
+  // R = P^T dY (row tile w)
+  {
+    const f32x8 pa0 = frag_cols(bP, LD, 16 * w, 0, lane), pa1 = frag_cols(bP, LD, 16 * w, 32, lane);
+#pragma unroll
+    for (int n = 0; n < 4; ++n) {
+      const f32x4 rr = mm<PrecF32>(mm<PrecF32>(zero4(), pa0, frag_cols(xs, LD, 16 * n, 0, lane)), pa1, frag_cols(xs, LD, 16 * n, 32, lane));
       reinterpret_cast<f32x4*>(rec + Rec::R)[(w * 4 + n) * 64 + lane] = rr;
     }
   }
@@ -438,7 +556,7 @@ __device__ __forceinline__ bool chain_step(const Params& p, ChainShared& sh, int
     if constexpr (REV) pf += nr[Rec::H1 + 32 * idx];
   }
 
-  float* dst = rec + (REV ? Rec::G : Rec::S);
+  typename Feat<P>::T* dst = feat<P>(rec, REV ? Rec::G : Rec::S);
 #pragma unroll
   for (int t = 0; t < 8; ++t)
 #pragma unroll
@@ -516,11 +634,10 @@ __device__ __forceinline__ bool chain_step(const Params& p, ChainShared& sh, int
   return more;
 }
 
+// The carry of workgroup `id` of a chain grid.
 template <class P, bool REV>
-__global__ void __launch_bounds__(256) bwd_chain_kernel(Params p) {
+__device__ __forceinline__ void chain_body(const Params& p, ChainShared& sh, int64_t id) {
   constexpr bool PIPE = std::is_same<P, PrecBF16>::value && !REV;  // two register sets of K fragments fit only as bf16 (forward carry)
-  __shared__ ChainShared sh;
-  const int64_t id = blockIdx.x;
   const int64_t xcd = id & 7, jdx = id >> 3;
   const int n = (int)(jdx & 3);
   const int64_t hb = (jdx >> 2) * 8 + xcd;
@@ -565,6 +682,22 @@ __global__ void __launch_bounds__(256) bwd_chain_kernel(Params p) {
   }
 }
 
+template <class P, bool REV>
+__global__ void __launch_bounds__(256) bwd_chain_kernel(Params p) {
+  __shared__ ChainShared sh;
+  chain_body<P, REV>(p, sh, blockIdx.x);
+}
+
+// Both carries of a segment in one launch: workgroups below `half` carry S^T forward, the others dL/dS^T
+// backward (each reads only what the recompute wrote and they write disjoint fields).  `half` is a
+// multiple of 8, so both halves keep the XCD mapping of a single carry.
+template <class P>
+__global__ void __launch_bounds__(256) bwd_chains_kernel(Params p, unsigned half) {
+  __shared__ ChainShared sh;
+  if (blockIdx.x < half) chain_body<P, false>(p, sh, blockIdx.x);
+  else chain_body<P, true>(p, sh, blockIdx.x - half);
+}
+
 // ---------------------------------------------------------------------------------------------- grad
 // The lift backward of one of q / k for this wave's 128 features and the 32 tokens of half hm, given
 // dPhi^T in acc[ft][u] (rows feature 128w + 16ft + .., column token 16(2hm + u) + ..):
@@ -572,16 +705,22 @@ __global__ void __launch_bounds__(256) bwd_chain_kernel(Params p) {
 // the waves into `dx` (LDS [64][LD], zeroed by the caller).  `xh` holds the normalised
 // input rows; s_rd[w] receives wave w's part of phi . dphi per token (summed in wave order).
 template <class P>
-__device__ __forceinline__ void lift_backward_half(const Params& p, const float* phi, const float* nrm,
+__device__ __forceinline__ void lift_backward_half(const Params& p, const typename Feat<P>::T* phi, const float* nrm,
                                                    float (*s_rd)[C], const float* xh, float* dx,
                                                    f32x4 (&acc)[8][2], int hm, int w, int lane) {
+  // Omega, its phases and the Omega^T table, opaque per call: their load addresses do not depend on the
+  // half, and hoisted out of the caller's loop they would hold registers through it.
+  const __bf16* omega = p.omega;
+  const float* phase = p.phase;
+  const bf16x8* omt = p.omt;
+  asm volatile("" : "+s"(omega), "+s"(phase), "+s"(omt));
   float rd[2] = {0.f, 0.f};
 #pragma unroll
   for (int ft = 0; ft < 8; ++ft)
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       const int tok = 16 * (2 * hm + u) + (lane & 15);
-      const f32x4 ph = *reinterpret_cast<const f32x4*>(phi + (size_t)tok * D + 128 * w + 16 * ft + 4 * (lane >> 4));
+      const f32x4 ph = ld4_t(phi + (size_t)tok * D + 128 * w + 16 * ft + 4 * (lane >> 4));
       rd[u] += ph[0] * acc[ft][u][0] + ph[1] * acc[ft][u][1] + ph[2] * acc[ft][u][2] + ph[3] * acc[ft][u][3];
     }
 #pragma unroll
@@ -599,28 +738,27 @@ __device__ __forceinline__ void lift_backward_half(const Params& p, const float*
     inv_n[u] = 1.f / (nrm[tok] + 1e-8f);
     rd_n[u] = (((s_rd[0][tok] + s_rd[1][tok]) + s_rd[2][tok]) + s_rd[3][tok]) / nrm[tok];
   }
-  f32x8 xb[2][2];
+  typename P::frag xb[2][2];
 #pragma unroll
   for (int u = 0; u < 2; ++u)
 #pragma unroll
-    for (int jb = 0; jb < 2; ++jb) xb[u][jb] = frag_rows_plain(xh, LD, 16 * (2 * hm + u), 32 * jb, lane);
-  f32x8 on0 = frag_rows_plain_bf16(p.omega, DK, 128 * w, 0, lane), on1 = frag_rows_plain_bf16(p.omega, DK, 128 * w, 32, lane);
-  f32x4 phn = *reinterpret_cast<const f32x4*>(p.phase + 128 * w + 4 * (lane >> 4));
+    for (int jb = 0; jb < 2; ++jb) xb[u][jb] = P::from_f32(frag_rows_plain(xh, LD, 16 * (2 * hm + u), 32 * jb, lane));
+  typename P::frag on0 = omega_frag<P>(omega, 128 * w, 0, lane), on1 = omega_frag<P>(omega, 128 * w, 32, lane);
+  f32x4 phn = *reinterpret_cast<const f32x4*>(phase + 128 * w + 4 * (lane >> 4));
 #pragma unroll
   for (int ft = 0; ft < 8; ++ft) {
     const int f0 = 128 * w + 16 * ft;
-    const f32x8 o0 = on0, o1 = on1;
+    const typename P::frag o0 = on0, o1 = on1;
     const f32x4 ph4 = phn;
     if (ft + 1 < 8) {  // the next feature tile's Omega rows and phases, issued one region ahead
-      on0 = frag_rows_plain_bf16(p.omega, DK, f0 + 16, 0, lane);
-      on1 = frag_rows_plain_bf16(p.omega, DK, f0 + 16, 32, lane);
-      phn = *reinterpret_cast<const f32x4*>(p.phase + f0 + 16 + 4 * (lane >> 4));
+      on0 = omega_frag<P>(omega, f0 + 16, 0, lane);
+      on1 = omega_frag<P>(omega, f0 + 16, 32, lane);
+      phn = *reinterpret_cast<const f32x4*>(phase + f0 + 16 + 4 * (lane >> 4));
     }
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
-      const f32x4 sv = mm<P>(mm<P>(zero4(), o0, xb[u][0]), o1, xb[u][1]);
-      const f32x4 ph = *reinterpret_cast<const f32x4*>(phi + (size_t)(16 * (2 * hm + u) + (lane & 15)) * D + f0 +
-                                                         4 * (lane >> 4));
+      const f32x4 sv = P::mma(P::mma(zero4(), o0, xb[u][0]), o1, xb[u][1]);
+      const f32x4 ph = ld4_t(phi + (size_t)(16 * (2 * hm + u) + (lane & 15)) * D + f0 + 4 * (lane >> 4));
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const float dphit = acc[ft][u][i] * inv_n[u] - ph[i] * rd_n[u];
@@ -636,18 +774,14 @@ __device__ __forceinline__ void lift_backward_half(const Params& p, const float*
     for (int u = 0; u < 2; ++u) d[a][u] = zero4();
 #pragma unroll
   for (int jj = 0; jj < 4; ++jj) {
-    f32x8 ob[4];
+    typename P::frag ob[4];
 #pragma unroll
-    for (int a = 0; a < 4; ++a) {
-      const bf16x8 t = p.omt[(a * 16 + 4 * w + jj) * 64 + lane];
-#pragma unroll
-      for (int s = 0; s < 8; ++s) ob[a][s] = (float)t[s];
-    }
+    for (int a = 0; a < 4; ++a) ob[a] = bf16_frag<P>(omt[(a * 16 + 4 * w + jj) * 64 + lane]);
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
-      const f32x8 bs = pair_to8(acc[2 * jj][u], acc[2 * jj + 1][u]);
+      const typename P::frag bs = P::from_f32(pair_to8(acc[2 * jj][u], acc[2 * jj + 1][u]));
 #pragma unroll
-      for (int a = 0; a < 4; ++a) d[a][u] = mm<P>(d[a][u], ob[a], bs);
+      for (int a = 0; a < 4; ++a) d[a][u] = P::mma(d[a][u], ob[a], bs);
     }
     __builtin_amdgcn_sched_barrier(0);
   }
@@ -711,21 +845,20 @@ __global__ void __launch_bounds__(256) bwd_grad_kernel(Params p) {
   __shared__ __attribute__((aligned(16))) float bXK[C * LD];  // X_K, then N
   __shared__ __attribute__((aligned(16))) float bX[C * LD];   // X, then dT, then M + M^T
   __shared__ __attribute__((aligned(16))) float bV[C * LD];   // V, then Y1 = dT T^T
-  __shared__ __attribute__((aligned(16))) float bT[C * LD];   // T, then normalised k / q rows
-  __shared__ __attribute__((aligned(16))) float bDX[C * LD];  // dx^ of k / q
-  __shared__ float s_ell[C], s_beta[C], s_n[C];
+  __shared__ __attribute__((aligned(16))) float bT[C * LD];   // T
+  __shared__ float s_ell[C], s_beta[C];
   // Fixed-order reductions (the gradients do not depend on the order the waves run in): every partial
   // sum has a slot of its own, written once, and the slots are added in a fixed order; no atomics.
   //   s_dlp: contributions to dl_i = dL/dl_i, one row per source (see NDL); s_dbp: to dbeta_i;
-  //   s_tsp: per-wave column sums of T o dTp; s_rdp: per-wave phi . dphi (lift backward);
+  //   s_tsp: per-wave column sums of T o dTp;
   //   s_w63: per-wave sums that land on dl_63 (the dkappa term [0..3] and <Gamma, S> [4..7])
-  __shared__ float s_dlp[NDL][C], s_dbp[3][C], s_tsp[4][C], s_rdp[4][C], s_w63[8];
+  __shared__ float s_dlp[NDL][C], s_dbp[3][C], s_tsp[4][C], s_w63[8];
 
   const int64_t h = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int64_t t0 = (p.c0 + blockIdx.x) * C;
-  const float* rec = record(p, b, h, blockIdx.x);
+  float* rec = record(p, b, h, blockIdx.x);
   const int r = tid >> 2, c0 = (tid & 3) * 16;
   const bool rvalid = t0 + r < p.T;
 
@@ -845,9 +978,10 @@ __global__ void __launch_bounds__(256) bwd_grad_kernel(Params p) {
     for (int n = 0; n < 4; ++n) qs[n] = zero4();
 #pragma unroll 4
     for (int jb = 0; jb < D / 32; ++jb) {
-      const f32x8 qa = frag_rows(rec + Rec::Q, D, 16 * w, 32 * jb, lane);
+      const typename P::frag qa = frag_rows_p<P>(feat<P>(rec, Rec::Q), D, 16 * w, 32 * jb, lane);
 #pragma unroll
-      for (int n = 0; n < 4; ++n) qs[n] = mm<P>(qs[n], qa, frag_cols(rec + Rec::S, DV, 16 * n, 32 * jb, lane));
+      for (int n = 0; n < 4; ++n)
+        qs[n] = P::mma(qs[n], qa, P::from_f32(frag_cols_t(feat<P>(rec, Rec::S), DV, 16 * n, 32 * jb, lane)));
     }
     float dap[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -869,12 +1003,12 @@ __global__ void __launch_bounds__(256) bwd_grad_kernel(Params p) {
   }
   {
     float gs = 0.f;
-    const f32x4* G4 = reinterpret_cast<const f32x4*>(rec + Rec::G);
-    const f32x4* S4 = reinterpret_cast<const f32x4*>(rec + Rec::S);
+    const typename Feat<P>::T* G4 = feat<P>(rec, Rec::G);
+    const typename Feat<P>::T* S4 = feat<P>(rec, Rec::S);
     // 32 iterations per thread, unrolled so that their loads are in flight together
 #pragma unroll 8
     for (int e = tid; e < D * DV / 4; e += 256) {
-      const f32x4 g = G4[e], s = S4[e];
+      const f32x4 g = ld4_t(G4 + 4 * e), s = ld4_t(S4 + 4 * e);
       gs += g[0] * s[0] + g[1] * s[1] + g[2] * s[2] + g[3] * s[3];
     }
     gs = sum_col4(sum_row16(gs));
@@ -968,90 +1102,137 @@ __global__ void __launch_bounds__(256) bwd_grad_kernel(Params p) {
     }
   }
 
-  // ---- phase 6: dk, then dq, each in two halves of 32 tokens
-  for (int which = 1; which >= 0; --which) {
-    const InT* x = reinterpret_cast<const InT*>(which == 0 ? p.q : p.k);
-    const int64_t xb = which == 0 ? b * p.qs0 + (t0 + r) * p.qs1 + h * p.qs2 + c0 : b * p.ks0 + (t0 + r) * p.ks1 + h * p.ks2 + c0;
-    {
-      float part[16];
-      load_x_part<InT>(x, xb, rvalid, p.normalize, part);
-      round_like_input<InT>(p.normalize, part);
+  // ---- the B operands of the dx kernel, as P fragments in the record's K-fragment area (dead once both
+  // carries are done): token tile m = w, dK^T [kappa o W, Zn, N^T, M + M^T], dQ^T [a o dY, N]
+  {
+    using frag = typename P::frag;
+    frag* bop = reinterpret_cast<frag*>(rec + Rec::KXF);
+    const int m = w;
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        bT[r * LD + c0 + e] = part[e];
-        bDX[r * LD + c0 + e] = 0.f;
-      }
+    for (int jb = 0; jb < 2; ++jb) {
+      bop[bop_dk(m, 0, jb) * 64 + lane] = P::from_f32(frag_rows(bW, LD, 16 * m, 32 * jb, lane));
+      bop[bop_dk(m, 1, jb) * 64 + lane] = P::from_f32(frag_rows(bdW, LD, 16 * m, 32 * jb, lane));
+      bop[bop_dk(m, 2, jb) * 64 + lane] = P::from_f32(frag_cols(bXK, LD, 16 * m, 32 * jb, lane));
+      bop[bop_dk(m, 3, jb) * 64 + lane] = P::from_f32(frag_rows(bX, LD, 16 * m, 32 * jb, lane));
+      bop[bop_dq(m, 0, jb) * 64 + lane] = P::from_f32(frag_rows(bY, LD, 16 * m, 32 * jb, lane));
+      bop[bop_dq(m, 1, jb) * 64 + lane] = P::from_f32(frag_rows(bXK, LD, 16 * m, 32 * jb, lane));
     }
-    if (tid < C) s_n[tid] = rec[Rec::VEC + 128 + 64 * which + tid];
-    __syncthreads();
-    for (int hm = 0; hm < 2; ++hm) {
-      f32x4 acc[8][2];
-      // B operands of the half's two token tiles (LDS), the same for every feature tile: converted once
-      // dk: [(kappa o W), Zn, N (transposed), M + M^T]; dq: [(a o dY), N]
-      typename P::frag bo[2][4][2];
+  }
+}
+
+// ---------------------------------------------------------------------------------------------- dx
+// One of the two passes of the dx kernel: WHICH 1 (k: dK^T and the lift backward of k) or 0 (q).
+template <class P, typename InT, int WHICH>
+__device__ __forceinline__ void dx_pass(const Params& p, const float* rec, const typename P::frag* bop, float* bT,
+                                        float* bDX, float* s_n, float (*s_rdp)[C], int64_t b, int64_t h, int64_t t0,
+                                        int tid, int w, int lane, int r, int c0, bool rvalid) {
+  constexpr int which = WHICH;
+  const InT* x = reinterpret_cast<const InT*>(which == 0 ? p.q : p.k);
+  const int64_t xb = which == 0 ? b * p.qs0 + (t0 + r) * p.qs1 + h * p.qs2 + c0 : b * p.ks0 + (t0 + r) * p.ks1 + h * p.ks2 + c0;
+  {
+    float part[16];
+    load_x_part<InT>(x, xb, rvalid, p.normalize, part);
+    round_like_input<InT>(p.normalize, part);
 #pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        const int m = 2 * hm + u;
+    for (int e = 0; e < 16; ++e) {
+      bT[r * LD + c0 + e] = part[e];
+      bDX[r * LD + c0 + e] = 0.f;
+    }
+  }
+  if (tid < C) s_n[tid] = rec[Rec::VEC + 128 + 64 * which + tid];
+  __syncthreads();
+#pragma nounroll
+  for (int hm = 0; hm < 2; ++hm) {
+    // The record pointer, opaque to the compiler in each half: the addresses of the A-operand loads below
+    // (a few hundred, 64-bit) do not depend on hm, and hoisted out of the loop they would hold more
+    // registers than the wave has.
+    const float* rec_h = rec;
+    asm volatile("" : "+s"(rec_h));
+    f32x4 acc[8][2];
+    // dPhi^T of the half's two token tiles as sums of products of A operands over this wave's features
+    // and B operands from the record (the same for every feature tile):
+    //   dK^T = Gamma (kappa o W)^T + S^T Zn^T + Q^T N + K^T (M + M^T)    (in two passes of two products,
+    //          the accumulators carried, so that only four B fragments per token tile are live)
+    //   dQ^T = S^T (a o dY)^T + K^T N^T
+    constexpr int NPASS = which == 1 ? 2 : 1;
 #pragma unroll
-        for (int jb = 0; jb < 2; ++jb) {
-          if (which == 1) {
-            bo[u][0][jb] = P::from_f32(frag_rows(bW, LD, 16 * m, 32 * jb, lane));
-            bo[u][1][jb] = P::from_f32(frag_rows(bdW, LD, 16 * m, 32 * jb, lane));
-            bo[u][2][jb] = P::from_f32(frag_cols(bXK, LD, 16 * m, 32 * jb, lane));
-            bo[u][3][jb] = P::from_f32(frag_rows(bX, LD, 16 * m, 32 * jb, lane));
-          } else {
-            bo[u][0][jb] = P::from_f32(frag_rows(bY, LD, 16 * m, 32 * jb, lane));
-            bo[u][1][jb] = P::from_f32(frag_rows(bXK, LD, 16 * m, 32 * jb, lane));
-          }
-        }
-      }
+    for (int ps = 0; ps < NPASS; ++ps) {
+      typename P::frag bo[2][2][2];  // [token tile u][product][depth block jb]
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int oo = 0; oo < 2; ++oo)
+#pragma unroll
+          for (int jb = 0; jb < 2; ++jb)
+            bo[u][oo][jb] = bop[(which == 1 ? bop_dk(2 * hm + u, 2 * ps + oo, jb) : bop_dq(2 * hm + u, oo, jb)) * 64 + lane];
 #pragma unroll
       for (int ft = 0; ft < 8; ++ft) {
         const int f0 = 128 * w + 16 * ft;
-        if (which == 1) {
-          // dK^T = Gamma (kappa o W)^T + S^T Zn^T + Q^T N + K^T (M + M^T)
-          const f32x8 g0 = frag_rows(rec + Rec::G, DV, f0, 0, lane), g1 = frag_rows(rec + Rec::G, DV, f0, 32, lane);
-          const f32x8 s0 = frag_rows(rec + Rec::S, DV, f0, 0, lane), s1 = frag_rows(rec + Rec::S, DV, f0, 32, lane);
-          const f32x8 q0 = frag_cols(rec + Rec::Q, D, f0, 0, lane), q1 = frag_cols(rec + Rec::Q, D, f0, 32, lane);
-          const f32x8 k0 = frag_cols(rec + Rec::K, D, f0, 0, lane), k1 = frag_cols(rec + Rec::K, D, f0, 32, lane);
-          const typename P::frag a[4][2] = {{P::from_f32(g0), P::from_f32(g1)}, {P::from_f32(s0), P::from_f32(s1)},
-                                            {P::from_f32(q0), P::from_f32(q1)}, {P::from_f32(k0), P::from_f32(k1)}};
-#pragma unroll
-          for (int u = 0; u < 2; ++u) {
-            f32x4 t = zero4();
-#pragma unroll
-            for (int o = 0; o < 4; ++o)
-#pragma unroll
-              for (int jb = 0; jb < 2; ++jb) t = P::mma(t, a[o][jb], bo[u][o][jb]);
-            acc[ft][u] = t;
-          }
+        // the pass's two A operands (depth blocks 0, 1): Gamma and S^T rows from the record, Q^T and K^T as
+        // the fragments prep stored (one 16- or 32-byte load each)
+        using frag = typename P::frag;
+        const frag* qtf = reinterpret_cast<const frag*>(rec_h + Rec::QTF);
+        const frag* ktf = reinterpret_cast<const frag*>(rec_h + Rec::KTF);
+        const int fi = (f0 >> 4) * 2;  // fragment index of feature tile f0 / 16, depth block 0
+        frag a[2][2];
+        if (which == 1 && ps == 0) {
+          const auto* fG = feat<P>(rec_h, Rec::G);
+          const auto* fS = feat<P>(rec_h, Rec::S);
+          a[0][0] = frag_rows_p<P>(fG, DV, f0, 0, lane); a[0][1] = frag_rows_p<P>(fG, DV, f0, 32, lane);
+          a[1][0] = frag_rows_p<P>(fS, DV, f0, 0, lane); a[1][1] = frag_rows_p<P>(fS, DV, f0, 32, lane);
+        } else if (which == 1) {
+          a[0][0] = qtf[fi * 64 + lane]; a[0][1] = qtf[(fi + 1) * 64 + lane];
+          a[1][0] = ktf[fi * 64 + lane]; a[1][1] = ktf[(fi + 1) * 64 + lane];
         } else {
-          // dQ^T = S^T (a o dY)^T + K^T N^T
-          const f32x8 s0 = frag_rows(rec + Rec::S, DV, f0, 0, lane), s1 = frag_rows(rec + Rec::S, DV, f0, 32, lane);
-          const f32x8 k0 = frag_cols(rec + Rec::K, D, f0, 0, lane), k1 = frag_cols(rec + Rec::K, D, f0, 32, lane);
-          const typename P::frag a[2][2] = {{P::from_f32(s0), P::from_f32(s1)}, {P::from_f32(k0), P::from_f32(k1)}};
+          const auto* fS = feat<P>(rec_h, Rec::S);
+          a[0][0] = frag_rows_p<P>(fS, DV, f0, 0, lane); a[0][1] = frag_rows_p<P>(fS, DV, f0, 32, lane);
+          a[1][0] = ktf[fi * 64 + lane]; a[1][1] = ktf[(fi + 1) * 64 + lane];
+        }
 #pragma unroll
-          for (int u = 0; u < 2; ++u) {
-            f32x4 t = zero4();
+        for (int u = 0; u < 2; ++u) {
+          f32x4 t = ps == 0 ? zero4() : acc[ft][u];
 #pragma unroll
-            for (int o = 0; o < 2; ++o)
+          for (int oo = 0; oo < 2; ++oo)
 #pragma unroll
-              for (int jb = 0; jb < 2; ++jb) t = P::mma(t, a[o][jb], bo[u][o][jb]);
-            acc[ft][u] = t;
-          }
+            for (int jb = 0; jb < 2; ++jb) t = P::mma(t, a[oo][jb], bo[u][oo][jb]);
+          acc[ft][u] = t;
         }
         __builtin_amdgcn_sched_barrier(0);
       }
-      lift_backward_half<P>(p, rec + (which == 0 ? Rec::Q : Rec::K), s_n, s_rdp, bT, bDX, acc, hm, w, lane);
     }
-    __syncthreads();
-    if (which == 0) {
-      write_dx<InT>(p, x, xb, p.dq, b * p.dqs0 + (t0 + r) * p.dqs1 + h * p.dqs2 + c0, bDX, r, c0, rvalid);
-    } else {
-      write_dx<InT>(p, x, xb, p.dk, b * p.dks0 + (t0 + r) * p.dks1 + h * p.dks2 + c0, bDX, r, c0, rvalid);
-    }
-    __syncthreads();
+    lift_backward_half<P>(p, feat<P>(rec_h, which == 0 ? Rec::Q : Rec::K), s_n, s_rdp, bT, bDX, acc, hm, w, lane);
   }
+  __syncthreads();
+  if (which == 0) {
+    write_dx<InT>(p, x, xb, p.dq, b * p.dqs0 + (t0 + r) * p.dqs1 + h * p.dqs2 + c0, bDX, r, c0, rvalid);
+  } else {
+    write_dx<InT>(p, x, xb, p.dk, b * p.dks0 + (t0 + r) * p.dks1 + h * p.dks2 + c0, bDX, r, c0, rvalid);
+  }
+  __syncthreads();
+}
+
+// grid (nseg, H, B), 256 threads.  dK^T = Gamma (kappa o W)^T + S^T Zn^T + Q^T N + K^T (M + M^T) and
+// dQ^T = S^T (a o dY)^T + K^T N^T over this wave's 128 features, then the lift backward of k and q to
+// dk, dq, each in two halves of 32 tokens.  The small B operands come from the gradient kernel through
+// the record; LDS holds only the input rows and dx^ (35 KB), so that the workgroups of this (long)
+// launch share CUs.
+template <class P, typename InT>
+__global__ void __launch_bounds__(256) bwd_dx_kernel(Params p) {
+  __shared__ __attribute__((aligned(16))) float bT[C * LD];   // normalised k / q rows
+  __shared__ __attribute__((aligned(16))) float bDX[C * LD];  // dx^ of k / q
+  __shared__ float s_n[C], s_rdp[4][C];
+
+  const int64_t h = blockIdx.y, b = blockIdx.z;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int64_t t0 = (p.c0 + blockIdx.x) * C;
+  const float* rec = record(p, b, h, blockIdx.x);
+  const int r = tid >> 2, c0 = (tid & 3) * 16;
+  const bool rvalid = t0 + r < p.T;
+  const typename P::frag* bop = reinterpret_cast<const typename P::frag*>(rec + Rec::KXF);
+
+  dx_pass<P, InT, 1>(p, rec, bop, bT, bDX, s_n, s_rdp, b, h, t0, tid, w, lane, r, c0, rvalid);
+  dx_pass<P, InT, 0>(p, rec, bop, bT, bDX, s_n, s_rdp, b, h, t0, tid, w, lane, r, c0, rvalid);
 }
 
 }  // namespace bwd
@@ -1110,8 +1291,8 @@ struct BwdLayout {
   size_t rec_buf, state_bytes, ckpt_off, carry_off, fwd_off, fwd_buf, omt_off, total;
 };
 
-// Default segment: the largest power of two from 4 to 64 chunks whose records fit 1.25 GiB.
-constexpr size_t BWD_SEGMENT_BUDGET = (size_t)1280 << 20;
+// Default segment: the largest power of two from 4 to 64 chunks whose records fit 1.5 GiB.
+constexpr size_t BWD_SEGMENT_BUDGET = (size_t)1536 << 20;
 
 static BwdLayout bwd_layout(const kdn_scan_args* f) {
   BwdLayout L;
@@ -1189,7 +1370,9 @@ static Params segment_params(const Params& base, const kdn_scan_bwd_args* a, con
   return p;
 }
 
-// One launch of segment p: 1 per-chunk recompute, 2 forward carry, 3 reverse carry, 4 gradients.
+// One launch of segment p: 1 per-chunk recompute, 2 forward carry, 3 reverse carry, 4 gradients, or
+// PH_CARRIES: both carries in one launch.
+constexpr int PH_CARRIES = 5;
 template <class P, typename InT>
 static int segment_phase(const Params& p, int phase, hipStream_t st) {
   const dim3 chunk_grid((unsigned)p.nseg, (unsigned)p.H, (unsigned)p.B);
@@ -1197,7 +1380,11 @@ static int segment_phase(const Params& p, int phase, hipStream_t st) {
   if (phase == 1) hipLaunchKernelGGL((bwd_prep_kernel<P, InT>), chunk_grid, dim3(256), 0, st, p);
   if (phase == 2) hipLaunchKernelGGL((bwd_chain_kernel<P, false>), dim3(chain_wgs), dim3(256), 0, st, p);
   if (phase == 3) hipLaunchKernelGGL((bwd_chain_kernel<P, true>), dim3(chain_wgs), dim3(256), 0, st, p);
-  if (phase == 4) hipLaunchKernelGGL((bwd_grad_kernel<P, InT>), chunk_grid, dim3(256), 0, st, p);
+  if (phase == 4) {
+    hipLaunchKernelGGL((bwd_grad_kernel<P, InT>), chunk_grid, dim3(256), 0, st, p);
+    hipLaunchKernelGGL((bwd_dx_kernel<P, InT>), chunk_grid, dim3(256), 0, st, p);
+  }
+  if (phase == PH_CARRIES) hipLaunchKernelGGL((bwd_chains_kernel<P>), dim3(2 * chain_wgs), dim3(256), 0, st, p, chain_wgs);
   return launch_status();
 }
 
@@ -1212,16 +1399,16 @@ static int bwd_start(const kdn_scan_bwd_args* a, const Params& base, const BwdLa
                           L.fwd_buf, L.nfb, st, aux);
 }
 
-// Serial: the start, then per segment (last first) recompute, forward carry, reverse carry, gradients.
+// Serial: the start, then per segment (last first) recompute, both carries (one launch), gradients.
 // With aux: the checkpoint pass's prep kernels run on aux beside its state kernels; then per segment
 // (processing step i, segment s = nsegs - 1 - i, buffer i % nbuf)
-//   aux: recompute(s) -> event R[i % nbuf]; forward carry(s) (the first waits for the checkpoints);
-//        gradients(s + 1) after its reverse carry (event V[(i - 1) % nbuf])
-//   st:  reverse carry(s) after R[i % nbuf] -> event V[i % nbuf]
-// so that the reverse carries, the sequential critical path, run back to back on st while aux recomputes
-// and finishes the segments around them.  The recompute of step i reuses the buffer of step i - nbuf,
-// whose gradients precede it on aux.  Every kernel reads and writes the same data in either schedule, so
-// the results are identical bit for bit.
+//   aux: recompute(s) -> event R[i % nbuf]; gradients(s + 1) after its carries (event V[(i - 1) % nbuf])
+//   st:  both carries of s after R[i % nbuf] (the forward one after the checkpoint pass, which ends on
+//        st) -> event V[i % nbuf]
+// so that the carries, the sequential critical path (two chain grids of B*H*4 workgroups), run back to
+// back on st while aux recomputes and finishes the segments around them.  The recompute of step i
+// reuses the buffer of step i - nbuf, whose gradients precede it on aux.  Every kernel reads and writes
+// the same data in either schedule, so the results are identical bit for bit.
 template <class P, typename InT>
 static int bwd_schedule(const kdn_scan_bwd_args* a, const Params& base, const BwdLayout& L, hipStream_t st,
                         hipStream_t aux) {
@@ -1231,29 +1418,26 @@ static int bwd_schedule(const kdn_scan_bwd_args* a, const Params& base, const Bw
     KDN_TRYK(bwd_start(a, base, L, st, nullptr));
     for (int64_t s = L.nsegs - 1; s >= 0; --s) {
       const Params p = segment_params(base, a, L, s);
-      for (int ph = 1; ph <= 4; ++ph) KDN_TRYK((segment_phase<P, InT>(p, ph, st)));
+      for (int ph : {1, PH_CARRIES, 4}) KDN_TRYK((segment_phase<P, InT>(p, ph, st)));
     }
     return KDN_OK;
   }
   EventSet evs;
-  KDN_TRYK(evs.create(2 * L.nbuf + 3));
+  KDN_TRYK(evs.create(2 * L.nbuf + 2));
   hipEvent_t* evR = evs.ev;
   hipEvent_t* evV = evs.ev + L.nbuf;
-  hipEvent_t evIn = evs.ev[2 * L.nbuf], evCk = evs.ev[2 * L.nbuf + 1], evDone = evs.ev[2 * L.nbuf + 2];
+  hipEvent_t evIn = evs.ev[2 * L.nbuf], evDone = evs.ev[2 * L.nbuf + 1];
   KDN_TRY(hipEventRecord(evIn, st));
   KDN_TRY(hipStreamWaitEvent(aux, evIn, 0));
   KDN_TRYK(bwd_start(a, base, L, st, aux));
-  KDN_TRY(hipEventRecord(evCk, st));
   for (int64_t i = 0; i < L.nsegs; ++i) {
     const int64_t s = L.nsegs - 1 - i;
     const int bb = (int)(i % L.nbuf);
     const Params p = segment_params(base, a, L, s);
     KDN_TRYK((segment_phase<P, InT>(p, 1, aux)));
     KDN_TRY(hipEventRecord(evR[bb], aux));
-    if (i == 0) KDN_TRY(hipStreamWaitEvent(aux, evCk, 0));
-    KDN_TRYK((segment_phase<P, InT>(p, 2, aux)));
     KDN_TRY(hipStreamWaitEvent(st, evR[bb], 0));
-    KDN_TRYK((segment_phase<P, InT>(p, 3, st)));
+    KDN_TRYK((segment_phase<P, InT>(p, PH_CARRIES, st)));
     KDN_TRY(hipEventRecord(evV[bb], st));
     if (i > 0) {
       KDN_TRY(hipStreamWaitEvent(aux, evV[(i - 1) % L.nbuf], 0));

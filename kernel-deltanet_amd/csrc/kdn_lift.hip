@@ -73,13 +73,13 @@ __global__ void __launch_bounds__(256) fwht_rows_kernel(const T* __restrict__ x,
 }
 
 // ------------------------------------------------------------------------------------------------
-// Waves (16-row tiles) per lift workgroup.  The bf16 -> bf16 D = 512 lift fits 168 registers, three
-// waves per SIMD: twelve waves share one LDS copy of Omega (measured 2-3 % faster than two 4-wave
-// workgroups per CU, with two spilled registers); the other variants would spill more and keep four.
+// Waves (16-row tiles) per lift workgroup.  The bf16 -> bf16 D = 512 lift takes 180 registers: eight
+// waves (two per SIMD) share one LDS copy of Omega with nothing spilled, measured 8 % faster at config 2
+// than twelve waves squeezed into 168 registers (three spilled to scratch); the other variants keep four.
 template <typename InT, typename OutT, int D>
 struct LiftWaves {
   static constexpr int value =
-      (std::is_same<InT, __bf16>::value && std::is_same<OutT, __bf16>::value && D == 512) ? 12 : 4;
+      (std::is_same<InT, __bf16>::value && std::is_same<OutT, __bf16>::value && D == 512) ? 8 : 4;
 };
 
 // Lift: one wave per 16-row tile, LiftWaves tiles per workgroup, persistent over tiles.
@@ -252,6 +252,80 @@ __global__ void __launch_bounds__((64 * LiftWaves<InT, OutT, D>::value)) lift_ke
   }
 }
 
+// ------------------------------------------------------------------------------------------------
+// The same lift with the projection by in-register butterflies instead of the MFMA product (the design
+// of the reference's CUDA P3 kernel, kernels/in_register_fwht.cu:10-93 / .cuh, with the semantics of
+// kernels/fwht.py:122-131): one wave per row, lane i holding x_i; for each 64-feature block m the sign
+// flips d1, d2, d3 and three wave64 Walsh-Hadamard transforms give 8 (Omega x)[64m + lane] with no
+// Omega table (Omega_m = H D3 H D2 H D1 / 8).  Kept as the measured alternative to lift_kernel: each
+// wave64 transform is six stages of a lane exchange (DPP, ds_swizzle or ds_bpermute), a select and an
+// add, and a 512-feature row takes 24 transforms, where the MFMA form needs 4 MFMA issues per row.
+template <int H>
+__device__ __forceinline__ float wave_sum_step(float v) { return v + xor_shuffle<H>(v); }
+__device__ __forceinline__ float wave_sum64(float v) {
+  v = wave_sum_step<1>(v);
+  v = wave_sum_step<2>(v);
+  v = wave_sum_step<4>(v);
+  v = wave_sum_step<8>(v);
+  v = wave_sum_step<16>(v);
+  return wave_sum_step<32>(v);
+}
+
+template <typename InT, typename OutT, int D>
+__global__ void __launch_bounds__(256) lift_butterfly_kernel(const InT* __restrict__ x, int64_t rows, int64_t xs,
+                                                            int normalize, const int64_t* __restrict__ bits,
+                                                            const float* __restrict__ phase, float inv_tau,
+                                                            OutT* __restrict__ out, int64_t os) {
+  constexpr int M = D / 64;
+  const int lane = threadIdx.x & 63;
+  // this lane's signs (d1, d2, d3 of each block) and phases (in revolutions)
+  float s1[M], s2[M], s3[M], ph[M];
+#pragma unroll
+  for (int m = 0; m < M; ++m) {
+    s1[m] = sign_of(bits[3 * m + 0], lane);
+    s2[m] = sign_of(bits[3 * m + 1], lane);
+    s3[m] = sign_of(bits[3 * m + 2], lane);
+    ph[m] = phase[64 * m + lane] * 0.15915494309189535f;
+  }
+  const float ang_scale = inv_tau * 0.15915494309189535f;
+  const float amp = sqrtf(2.0f / (float)D);
+  const int64_t stride = (int64_t)gridDim.x * 4;
+  int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  float xn = row < rows ? (float)x[row * xs + lane] : 0.f;
+  for (; row < rows; row += stride) {
+    float xv = xn;
+    if (row + stride < rows) xn = (float)x[(row + stride) * xs + lane];
+    if (normalize) {
+      const float inv = 1.0f / fmaxf(sqrtf(wave_sum64(xv * xv)), 1e-6f);
+      xv *= inv;
+      if constexpr (std::is_same<InT, __bf16>::value) xv = (float)(__bf16)xv;  // F.normalize keeps x's dtype
+    }
+    float c[M];
+    float ss = 0.f;
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      float v = fwht_wave<64>(xv * s1[m], lane);
+      v = fwht_wave<64>(v * s2[m], lane);
+      v = fwht_wave<64>(v * s3[m], lane);
+      c[m] = __builtin_amdgcn_cosf(__builtin_amdgcn_fractf(v * 0.125f * ang_scale + ph[m]));
+      ss += c[m] * c[m];
+    }
+    const float scale = amp / (amp * sqrtf(wave_sum64(ss)) + 1e-8f);
+#pragma unroll
+    for (int m = 0; m < M; ++m) out[row * os + 64 * m + lane] = (OutT)(c[m] * scale);
+  }
+}
+
+template <typename InT, typename OutT, int D>
+static void launch_lift_butterfly(const void* x, int64_t rows, int64_t xs, int normalize, const int64_t* bits,
+                                  const float* phase, float inv_tau, void* out, int64_t os, hipStream_t st) {
+  int64_t wgs = (rows + 3) / 4;
+  const int cus = device_cus() > 0 ? device_cus() : 256;
+  if (wgs > (int64_t)cus * 8) wgs = (int64_t)cus * 8;  // persistent: eight 4-wave workgroups per CU
+  hipLaunchKernelGGL((lift_butterfly_kernel<InT, OutT, D>), dim3((unsigned)wgs), dim3(256), 0, st, (const InT*)x, rows,
+                     xs, normalize, bits, phase, inv_tau, (OutT*)out, os);
+}
+
 template <typename InT, typename OutT, int D>
 static void launch_lift(const void* x, int64_t rows, int64_t xs, int normalize, const void* omega, const int64_t* bits,
                         const float* phase, float inv_tau, void* out, int64_t os, hipStream_t st) {
@@ -274,7 +348,17 @@ static void launch_lift(const void* x, int64_t rows, int64_t xs, int normalize, 
 
 template <typename InT, typename OutT>
 static int dispatch_lift_D(int D, const void* x, int64_t rows, int64_t xs, int normalize, const void* omega,
-                           const int64_t* bits, const float* phase, float inv_tau, void* out, int64_t os, hipStream_t st) {
+                           const int64_t* bits, const float* phase, float inv_tau, void* out, int64_t os, hipStream_t st,
+                           bool butterfly) {
+  if (butterfly) {
+    switch (D) {
+      case 128: launch_lift_butterfly<InT, OutT, 128>(x, rows, xs, normalize, bits, phase, inv_tau, out, os, st); break;
+      case 256: launch_lift_butterfly<InT, OutT, 256>(x, rows, xs, normalize, bits, phase, inv_tau, out, os, st); break;
+      case 512: launch_lift_butterfly<InT, OutT, 512>(x, rows, xs, normalize, bits, phase, inv_tau, out, os, st); break;
+      default: return KDN_ERR_UNSUPPORTED;
+    }
+    return launch_status();
+  }
   switch (D) {
     case 128: launch_lift<InT, OutT, 128>(x, rows, xs, normalize, omega, bits, phase, inv_tau, out, os, st); break;
     case 256: launch_lift<InT, OutT, 256>(x, rows, xs, normalize, omega, bits, phase, inv_tau, out, os, st); break;
@@ -285,10 +369,12 @@ static int dispatch_lift_D(int D, const void* x, int64_t rows, int64_t xs, int n
 }
 
 // The lift with Omega given as the bf16 table (omega) or as the packed sign table (bits); exactly one is
-// non-null.  Argument checks of kdn_fwht_lift / kdn_fwht_lift_bits.
+// non-null (butterfly: bits, projected by lift_butterfly_kernel).  Argument checks of kdn_fwht_lift /
+// kdn_fwht_lift_bits / kdn_fwht_lift_bits_butterfly.
 static int fwht_lift_impl(const void* x, int64_t rows, int64_t x_row_stride, int x_dtype, int normalize_input,
                           const void* omega_bf16, const int64_t* bits, const float* phase, int d_k, int D,
-                          float inv_tau, void* out, int64_t out_row_stride, int out_dtype, void* stream) {
+                          float inv_tau, void* out, int64_t out_row_stride, int out_dtype, void* stream,
+                          bool butterfly = false) {
   if (!x || !(omega_bf16 || bits) || !phase || !out || rows < 0) return KDN_ERR_INVALID_ARGUMENT;
   if (!valid_dtype(x_dtype) || !valid_dtype(out_dtype)) return KDN_ERR_INVALID_ARGUMENT;
   if (d_k != 64) return KDN_ERR_UNSUPPORTED;
@@ -305,12 +391,12 @@ static int fwht_lift_impl(const void* x, int64_t rows, int64_t x_row_stride, int
   const int nz = normalize_input ? 1 : 0;
   if (x_dtype == KDN_DTYPE_BF16) {
     if (out_dtype == KDN_DTYPE_BF16)
-      return dispatch_lift_D<__bf16, __bf16>(D, x, rows, x_row_stride, nz, omega_bf16, bits, phase, inv_tau, out, out_row_stride, st);
-    return dispatch_lift_D<__bf16, float>(D, x, rows, x_row_stride, nz, omega_bf16, bits, phase, inv_tau, out, out_row_stride, st);
+      return dispatch_lift_D<__bf16, __bf16>(D, x, rows, x_row_stride, nz, omega_bf16, bits, phase, inv_tau, out, out_row_stride, st, butterfly);
+    return dispatch_lift_D<__bf16, float>(D, x, rows, x_row_stride, nz, omega_bf16, bits, phase, inv_tau, out, out_row_stride, st, butterfly);
   }
   if (out_dtype == KDN_DTYPE_BF16)
-    return dispatch_lift_D<float, __bf16>(D, x, rows, x_row_stride, nz, omega_bf16, bits, phase, inv_tau, out, out_row_stride, st);
-  return dispatch_lift_D<float, float>(D, x, rows, x_row_stride, nz, omega_bf16, bits, phase, inv_tau, out, out_row_stride, st);
+    return dispatch_lift_D<float, __bf16>(D, x, rows, x_row_stride, nz, omega_bf16, bits, phase, inv_tau, out, out_row_stride, st, butterfly);
+  return dispatch_lift_D<float, float>(D, x, rows, x_row_stride, nz, omega_bf16, bits, phase, inv_tau, out, out_row_stride, st, butterfly);
 }
 
 }  // namespace kdn
@@ -371,6 +457,15 @@ extern "C" int kdn_fwht_lift_bits(const void* x, int64_t rows, int64_t x_row_str
   if (!rademacher_bits) return KDN_ERR_INVALID_ARGUMENT;
   return fwht_lift_impl(x, rows, x_row_stride, x_dtype, normalize_input, nullptr, rademacher_bits, phase, d_k,
                         D_lifted, tau_star_inv, out, out_row_stride, out_dtype, stream);
+}
+
+extern "C" int kdn_fwht_lift_bits_butterfly(const void* x, int64_t rows, int64_t x_row_stride, int x_dtype, int d_k,
+                                            const int64_t* rademacher_bits, int D_lifted, float tau_star_inv,
+                                            const float* phase, int normalize_input, void* out, int64_t out_row_stride,
+                                            int out_dtype, void* stream) {
+  if (!rademacher_bits) return KDN_ERR_INVALID_ARGUMENT;
+  return fwht_lift_impl(x, rows, x_row_stride, x_dtype, normalize_input, nullptr, rademacher_bits, phase, d_k,
+                        D_lifted, tau_star_inv, out, out_row_stride, out_dtype, stream, true);
 }
 
 namespace kdn {

@@ -49,6 +49,7 @@ EXPORTED = (
     "kdn_delta_scan_bwd_streams",
     "kdn_scan_bwd_phase",
     "kdn_scan_bwd_segments",
+    "kdn_fwht_lift_bits_butterfly",
 )
 
 KDN_ERR_CAPACITY = -6
@@ -169,7 +170,9 @@ def lib() -> ctypes.CDLL:
             L.kdn_fwht_lift.argtypes = [vp, i64, i64, ci, ci, vp, vp, ci, ci, cf, vp, i64, ci, vp]
             L.kdn_fwht_lift.restype = ci
             L.kdn_fwht_lift_bits.argtypes = [vp, i64, i64, ci, ci, vp, ci, cf, vp, ci, vp, i64, ci, vp]
+            L.kdn_fwht_lift_bits_butterfly.argtypes = L.kdn_fwht_lift_bits.argtypes
             L.kdn_fwht_lift_bits.restype = ci
+            L.kdn_fwht_lift_bits_butterfly.restype = ci
             L.kdn_scan_workspace_bytes.argtypes = [ctypes.POINTER(ScanArgs)]
             L.kdn_scan_workspace_bytes.restype = sz
             L.kdn_delta_scan_fwd.argtypes = [ctypes.POINTER(ScanArgs), vp]

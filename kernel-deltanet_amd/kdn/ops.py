@@ -93,10 +93,12 @@ def lift(x: torch.Tensor, omega_bf16: torch.Tensor, phase: torch.Tensor, inv_tau
 
 
 def lift_bits(x: torch.Tensor, rademacher_bits: torch.Tensor, phase: torch.Tensor, inv_tau: float,
-              normalize: bool = False, out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+              normalize: bool = False, out_dtype: Optional[torch.dtype] = None,
+              butterfly: bool = False) -> torch.Tensor:
     """(..., 64) -> (..., D) feature lift from the packed [D/64, 3] sign table (kdn_fwht_lift_bits): each
     workgroup builds Omega in LDS with wave64 butterflies, then lifts as `lift`.  D = 64 * rows of the
-    table; phase is the (D,) phase vector b."""
+    table; phase is the (D,) phase vector b.  butterfly=True projects every row by in-register wave64
+    butterflies instead (kdn_fwht_lift_bits_butterfly, the reference's P3 design; slower)."""
     require_device(x, "lift_bits")
     d_k = x.shape[-1]
     D = 64 * rademacher_bits.shape[0]
@@ -110,13 +112,14 @@ def lift_bits(x: torch.Tensor, rademacher_bits: torch.Tensor, phase: torch.Tenso
     bits = rademacher_bits.to(device=x.device, dtype=torch.int64).contiguous()
     ph = phase.to(device=x.device, dtype=torch.float32).contiguous()
     out = torch.empty(x2.shape[0], D, dtype=out_dtype, device=x.device)
+    name = "kdn_fwht_lift_bits_butterfly" if butterfly else "kdn_fwht_lift_bits"
     with torch.cuda.device(x.device):
-        N.check(N.lib().kdn_fwht_lift_bits(ctypes.c_void_p(x2.data_ptr()), x2.shape[0], x2.stride(0),
-                                           _tag(x.dtype, "lift_bits"), d_k, ctypes.c_void_p(bits.data_ptr()), D,
-                                           float(inv_tau), ctypes.c_void_p(ph.data_ptr()), 1 if normalize else 0,
-                                           ctypes.c_void_p(out.data_ptr()), out.stride(0),
-                                           _tag(out_dtype, "lift_bits output"), ctypes.c_void_p(_stream(x.device))),
-                "kdn_fwht_lift_bits")
+        N.check(getattr(N.lib(), name)(ctypes.c_void_p(x2.data_ptr()), x2.shape[0], x2.stride(0),
+                                       _tag(x.dtype, "lift_bits"), d_k, ctypes.c_void_p(bits.data_ptr()), D,
+                                       float(inv_tau), ctypes.c_void_p(ph.data_ptr()), 1 if normalize else 0,
+                                       ctypes.c_void_p(out.data_ptr()), out.stride(0),
+                                       _tag(out_dtype, "lift_bits output"), ctypes.c_void_p(_stream(x.device))),
+                name)
     return out.view(*x.shape[:-1], D)
 
 

@@ -131,7 +131,11 @@ def test_lift_fwht_omega_argument_errors_need_no_device(lib):
     assert lib.kdn_build_omega(None, 64, 512, p, 1, None) == -1
     # the sign-table lift (the reference's fwht_forward boundary): (x, rows, stride, dtype, d_k, bits, D, 1/tau,
     # phase, normalize, out, out stride, out dtype, stream)
-    lb = lib.kdn_fwht_lift_bits
+    for lb in (lib.kdn_fwht_lift_bits, lib.kdn_fwht_lift_bits_butterfly):
+        _lift_bits_errors(lb, p)
+
+
+def _lift_bits_errors(lb, p):
     assert lb(p, 10, 64, 0, 64, None, 512, 0.35, p, 0, p, 512, 0, None) == -1     # no table
     assert lb(p, 10, 64, 0, 64, p, 512, 0.35, None, 0, p, 512, 0, None) == -1     # no phase
     assert lb(p, 10, 64, 0, 128, p, 512, 0.35, p, 0, p, 512, 0, None) == -2      # d_k 128
@@ -169,7 +173,7 @@ def test_backward_workspace_and_errors_need_no_device(lib):
     for i, nm in enumerate(("dy", "dq", "dk", "dv", "dbeta", "workspace")):
         setattr(g, nm, 0x7E0000000000 + 0x100000 * i)
     # one segment (the default at this size): its 4 chunk records per head and the Omega^T table
-    assert lib.kdn_scan_bwd_workspace_bytes(ctypes.byref(g)) == 2 * 4 * 1116160 + 65536
+    assert lib.kdn_scan_bwd_workspace_bytes(ctypes.byref(g)) == 2 * 4 * 1247232 + 65536
     seg = ctypes.c_int64(0)
     assert lib.kdn_scan_bwd_segments(ctypes.byref(g), ctypes.byref(seg)) == 1 and seg.value == 4
     # segments of one chunk: three rotating record buffers, three segment-start states and the carried
@@ -178,7 +182,7 @@ def test_backward_workspace_and_errors_need_no_device(lib):
     f.segment_chunks = 1
     assert lib.kdn_scan_bwd_segments(ctypes.byref(g), ctypes.byref(seg)) == 4 and seg.value == 1
     assert lib.kdn_scan_bwd_workspace_bytes(ctypes.byref(g)) == \
-        3 * 2 * 1116160 + 4 * 2 * 512 * 64 * 4 + 2 * 2 * 2 * 238592 + 65536
+        3 * 2 * 1247232 + 4 * 2 * 512 * 64 * 4 + 2 * 2 * 2 * 238592 + 65536
     g.workspace_bytes = 1 << 40
     assert lib.kdn_scan_bwd_phase(ctypes.byref(g), 5, 0, None) == -1
     assert lib.kdn_scan_bwd_phase(ctypes.byref(g), 1, 4, None) == -1   # segments 0 .. 3

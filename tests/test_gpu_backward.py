@@ -260,8 +260,8 @@ def test_backward_config4_shape(proj):
     plan = ops.ScanBackwardPlan(q, k, v, beta, lam, omega, phase, proj.tau_star_inv, dy, ds, initial_state=s0)
     assert plan.segment_chunks == 4 and plan.segments == 64
     # the records of three 4-chunk segments, 63 segment-start states and the carry, the checkpoint
-    # pass's two buffers and the table: about 12 GB, against 150 GB for records of every chunk
-    assert plan.workspace.numel() < 13 * 10**9
+    # pass's two buffers and the table: about 13 GB, against 163 GB for records of every chunk
+    assert plan.workspace.numel() < 14 * 10**9
     full = [t.clone() for t in plan.run()]
     torch.cuda.synchronize()
     for n, t in zip(("dq", "dk", "dv", "dbeta", "ddecay", "dinit"), full):

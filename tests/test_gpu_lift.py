@@ -187,3 +187,28 @@ def test_lift_bits_config2_equals_table_lift(proj):
     b = ops.lift(x, proj.device_omega(DEV), proj.device_phase(DEV), proj.tau_star_inv, normalize=True)
     torch.cuda.synchronize()
     assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("D", [128, 256, 512])
+@pytest.mark.parametrize("dtype,normalize", [(torch.float32, False), (torch.float32, True), (torch.bfloat16, False),
+                                             (torch.bfloat16, True)])
+def test_lift_bits_butterfly_matches_oracle(D, dtype, normalize):
+    """kdn_fwht_lift_bits_butterfly (in-register wave64 butterflies, no Omega table) against the oracle, and
+    against the MFMA-projection lift: the same function up to fp32 summation order (bf16 outputs may
+    differ by one rounding step)."""
+    p = FastWalshHadamardProjection(64, D, 11)
+    op = ol.make_projection(64, D, 11)
+    g = torch.Generator().manual_seed(D + 1)
+    x = (torch.randn(2051, 64, generator=g) * 1.3).to(dtype)
+    xd = x.to(DEV)
+    a = ops.lift_bits(xd, p.device_bits(DEV), p.device_phase(DEV), p.tau_star_inv, normalize, butterfly=True)
+    b = ops.lift_bits(xd, p.device_bits(DEV), p.device_phase(DEV), p.tau_star_inv, normalize)
+    torch.cuda.synchronize()
+    assert a.dtype == dtype and a.shape == (2051, D)
+    xr = x.float()
+    if normalize:
+        xr = torch.nn.functional.normalize(xr, dim=-1, eps=1e-6).to(dtype).float()
+    tol = 1e-5 if dtype == torch.float32 else 1e-2
+    ref = ol.lift(xr.numpy(), op)
+    assert rel_l2(a.float().cpu().numpy(), ref) < tol
+    assert rel_l2(a.float().cpu().numpy(), b.float().cpu().numpy()) < tol
