@@ -699,15 +699,18 @@ __global__ void __launch_bounds__(256) bwd_chains_kernel(Params p, unsigned half
 }
 
 // ---------------------------------------------------------------------------------------------- grad
-// The lift backward of one of q / k for this wave's 128 features and the 32 tokens of half hm, given
-// dPhi^T in acc[ft][u] (rows feature 128w + 16ft + .., column token 16(2hm + u) + ..):
+// The lift backward of one of q / k for this wave's NFT = 32 / NW feature tiles (16 features each,
+// features [16 NFT w, 16 NFT (w + 1))) and the 32 tokens of half hm, given dPhi^T in acc[ft][u] (rows
+// feature 16 NFT w + 16 ft + .., column token 16(2hm + u) + ..):
 // ds = -sqrt(2/D) sin(s) (dphi / (n + 1e-8) - phi (phi . dphi) / n), then dx^ = ds Omega reduced over
 // the waves into `dx` (LDS [64][LD], zeroed by the caller).  `xh` holds the normalised
 // input rows; s_rd[w] receives wave w's part of phi . dphi per token (summed in wave order).
-template <class P>
+template <class P, int NW>
 __device__ __forceinline__ void lift_backward_half(const Params& p, const typename Feat<P>::T* phi, const float* nrm,
                                                    float (*s_rd)[C], const float* xh, float* dx,
-                                                   f32x4 (&acc)[8][2], int hm, int w, int lane) {
+                                                   f32x4 (&acc)[32 / NW][2], int hm, int w, int lane) {
+  constexpr int NFT = 32 / NW;
+  const int fb = 16 * NFT * w;  // the wave's first feature
   // Omega, its phases and the Omega^T table, opaque per call: their load addresses do not depend on the
   // half, and hoisted out of the caller's loop they would hold registers through it.
   const __bf16* omega = p.omega;
@@ -716,11 +719,11 @@ __device__ __forceinline__ void lift_backward_half(const Params& p, const typena
   asm volatile("" : "+s"(omega), "+s"(phase), "+s"(omt));
   float rd[2] = {0.f, 0.f};
 #pragma unroll
-  for (int ft = 0; ft < 8; ++ft)
+  for (int ft = 0; ft < NFT; ++ft)
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       const int tok = 16 * (2 * hm + u) + (lane & 15);
-      const f32x4 ph = ld4_t(phi + (size_t)tok * D + 128 * w + 16 * ft + 4 * (lane >> 4));
+      const f32x4 ph = ld4_t(phi + (size_t)tok * D + fb + 16 * ft + 4 * (lane >> 4));
       rd[u] += ph[0] * acc[ft][u][0] + ph[1] * acc[ft][u][1] + ph[2] * acc[ft][u][2] + ph[3] * acc[ft][u][3];
     }
 #pragma unroll
@@ -736,21 +739,24 @@ __device__ __forceinline__ void lift_backward_half(const Params& p, const typena
   for (int u = 0; u < 2; ++u) {
     const int tok = 16 * (2 * hm + u) + (lane & 15);
     inv_n[u] = 1.f / (nrm[tok] + 1e-8f);
-    rd_n[u] = (((s_rd[0][tok] + s_rd[1][tok]) + s_rd[2][tok]) + s_rd[3][tok]) / nrm[tok];
+    float rs = s_rd[0][tok];
+#pragma unroll
+    for (int v = 1; v < NW; ++v) rs += s_rd[v][tok];
+    rd_n[u] = rs / nrm[tok];
   }
   typename P::frag xb[2][2];
 #pragma unroll
   for (int u = 0; u < 2; ++u)
 #pragma unroll
     for (int jb = 0; jb < 2; ++jb) xb[u][jb] = P::from_f32(frag_rows_plain(xh, LD, 16 * (2 * hm + u), 32 * jb, lane));
-  typename P::frag on0 = omega_frag<P>(omega, 128 * w, 0, lane), on1 = omega_frag<P>(omega, 128 * w, 32, lane);
-  f32x4 phn = *reinterpret_cast<const f32x4*>(phase + 128 * w + 4 * (lane >> 4));
+  typename P::frag on0 = omega_frag<P>(omega, fb, 0, lane), on1 = omega_frag<P>(omega, fb, 32, lane);
+  f32x4 phn = *reinterpret_cast<const f32x4*>(phase + fb + 4 * (lane >> 4));
 #pragma unroll
-  for (int ft = 0; ft < 8; ++ft) {
-    const int f0 = 128 * w + 16 * ft;
+  for (int ft = 0; ft < NFT; ++ft) {
+    const int f0 = fb + 16 * ft;
     const typename P::frag o0 = on0, o1 = on1;
     const f32x4 ph4 = phn;
-    if (ft + 1 < 8) {  // the next feature tile's Omega rows and phases, issued one region ahead
+    if (ft + 1 < NFT) {  // the next feature tile's Omega rows and phases, issued one region ahead
       on0 = omega_frag<P>(omega, f0 + 16, 0, lane);
       on1 = omega_frag<P>(omega, f0 + 16, 32, lane);
       phn = *reinterpret_cast<const f32x4*>(phase + f0 + 16 + 4 * (lane >> 4));
@@ -773,10 +779,10 @@ __device__ __forceinline__ void lift_backward_half(const Params& p, const typena
 #pragma unroll
     for (int u = 0; u < 2; ++u) d[a][u] = zero4();
 #pragma unroll
-  for (int jj = 0; jj < 4; ++jj) {
+  for (int jj = 0; jj < NFT / 2; ++jj) {
     typename P::frag ob[4];
 #pragma unroll
-    for (int a = 0; a < 4; ++a) ob[a] = bf16_frag<P>(omt[(a * 16 + 4 * w + jj) * 64 + lane]);
+    for (int a = 0; a < 4; ++a) ob[a] = bf16_frag<P>(omt[(a * 16 + fb / 32 + jj) * 64 + lane]);
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       const typename P::frag bs = P::from_f32(pair_to8(acc[2 * jj][u], acc[2 * jj + 1][u]));
@@ -785,15 +791,17 @@ __device__ __forceinline__ void lift_backward_half(const Params& p, const typena
     }
     __builtin_amdgcn_sched_barrier(0);
   }
-  // Reduce over the four waves into dx: in turn t wave w adds its partial of input columns 16a .. 16a+15,
-  // a = (w + t) & 3, with 16-byte read-modify-writes; within a turn the waves touch disjoint columns.
-  // (Per-element LDS atomics here cost ~15 % of the kernel: four waves adding to the same addresses.)
+  // Reduce over the waves into dx: groups of four waves in turn, and in turn t of a group wave w adds its
+  // partial of input columns 16a .. 16a+15, a = (w + t) & 3, with 16-byte read-modify-writes; within a
+  // turn the active waves touch disjoint columns.  (Per-element LDS atomics here cost ~15 % of the
+  // kernel: four waves adding to the same addresses.)
 #pragma unroll
-  for (int t = 0; t < 4; ++t) {
-    const int a = (w + t) & 3;  // uniform over the wave
+  for (int t = 0; t < NW; ++t) {
+    const bool mine = (w >> 2) == (t >> 2);  // uniform over the wave
+    const int a = (w + t) & 3;
 #pragma unroll
     for (int aa = 0; aa < 4; ++aa) {
-      if (aa == a) {
+      if (mine && aa == a) {
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
           f32x4* px = reinterpret_cast<f32x4*>(&dx[(16 * (2 * hm + u) + (lane & 15)) * LD + 16 * aa + 4 * (lane >> 4)]);
@@ -1121,15 +1129,17 @@ __global__ void __launch_bounds__(256) bwd_grad_kernel(Params p) {
 }
 
 // ---------------------------------------------------------------------------------------------- dx
-// One of the two passes of the dx kernel: WHICH 1 (k: dK^T and the lift backward of k) or 0 (q).
-template <class P, typename InT, int WHICH>
+// One of the two passes of the dx kernel (NW waves, each 512 / NW features): WHICH 1 (k: dK^T and the
+// lift backward of k) or 0 (q).  The first four waves load the input rows and write dx.
+template <class P, typename InT, int WHICH, int NW>
 __device__ __forceinline__ void dx_pass(const Params& p, const float* rec, const typename P::frag* bop, float* bT,
                                         float* bDX, float* s_n, float (*s_rdp)[C], int64_t b, int64_t h, int64_t t0,
                                         int tid, int w, int lane, int r, int c0, bool rvalid) {
   constexpr int which = WHICH;
+  constexpr int NFT = 32 / NW;  // 16-feature tiles per wave
   const InT* x = reinterpret_cast<const InT*>(which == 0 ? p.q : p.k);
   const int64_t xb = which == 0 ? b * p.qs0 + (t0 + r) * p.qs1 + h * p.qs2 + c0 : b * p.ks0 + (t0 + r) * p.ks1 + h * p.ks2 + c0;
-  {
+  if (tid < 256) {
     float part[16];
     load_x_part<InT>(x, xb, rvalid, p.normalize, part);
     round_like_input<InT>(p.normalize, part);
@@ -1148,7 +1158,7 @@ __device__ __forceinline__ void dx_pass(const Params& p, const float* rec, const
     // registers than the wave has.
     const float* rec_h = rec;
     asm volatile("" : "+s"(rec_h));
-    f32x4 acc[8][2];
+    f32x4 acc[NFT][2];
     // dPhi^T of the half's two token tiles as sums of products of A operands over this wave's features
     // and B operands from the record (the same for every feature tile):
     //   dK^T = Gamma (kappa o W)^T + S^T Zn^T + Q^T N + K^T (M + M^T)    (in two passes of two products,
@@ -1166,8 +1176,8 @@ __device__ __forceinline__ void dx_pass(const Params& p, const float* rec, const
           for (int jb = 0; jb < 2; ++jb)
             bo[u][oo][jb] = bop[(which == 1 ? bop_dk(2 * hm + u, 2 * ps + oo, jb) : bop_dq(2 * hm + u, oo, jb)) * 64 + lane];
 #pragma unroll
-      for (int ft = 0; ft < 8; ++ft) {
-        const int f0 = 128 * w + 16 * ft;
+      for (int ft = 0; ft < NFT; ++ft) {
+        const int f0 = 16 * NFT * w + 16 * ft;
         // the pass's two A operands (depth blocks 0, 1): Gamma and S^T rows from the record, Q^T and K^T as
         // the fragments prep stored (one 16- or 32-byte load each)
         using frag = typename P::frag;
@@ -1200,27 +1210,30 @@ __device__ __forceinline__ void dx_pass(const Params& p, const float* rec, const
         __builtin_amdgcn_sched_barrier(0);
       }
     }
-    lift_backward_half<P>(p, feat<P>(rec_h, which == 0 ? Rec::Q : Rec::K), s_n, s_rdp, bT, bDX, acc, hm, w, lane);
+    lift_backward_half<P, NW>(p, feat<P>(rec_h, which == 0 ? Rec::Q : Rec::K), s_n, s_rdp, bT, bDX, acc, hm, w, lane);
   }
   __syncthreads();
-  if (which == 0) {
-    write_dx<InT>(p, x, xb, p.dq, b * p.dqs0 + (t0 + r) * p.dqs1 + h * p.dqs2 + c0, bDX, r, c0, rvalid);
-  } else {
-    write_dx<InT>(p, x, xb, p.dk, b * p.dks0 + (t0 + r) * p.dks1 + h * p.dks2 + c0, bDX, r, c0, rvalid);
+  if (tid < 256) {
+    if (which == 0) {
+      write_dx<InT>(p, x, xb, p.dq, b * p.dqs0 + (t0 + r) * p.dqs1 + h * p.dqs2 + c0, bDX, r, c0, rvalid);
+    } else {
+      write_dx<InT>(p, x, xb, p.dk, b * p.dks0 + (t0 + r) * p.dks1 + h * p.dks2 + c0, bDX, r, c0, rvalid);
+    }
   }
   __syncthreads();
 }
 
-// grid (nseg, H, B), 256 threads.  dK^T = Gamma (kappa o W)^T + S^T Zn^T + Q^T N + K^T (M + M^T) and
-// dQ^T = S^T (a o dY)^T + K^T N^T over this wave's 128 features, then the lift backward of k and q to
-// dk, dq, each in two halves of 32 tokens.  The small B operands come from the gradient kernel through
-// the record; LDS holds only the input rows and dx^ (35 KB), so that the workgroups of this (long)
-// launch share CUs.
+// grid (nseg, H, B), DX_WAVES waves.  dK^T = Gamma (kappa o W)^T + S^T Zn^T + Q^T N + K^T (M + M^T) and
+// dQ^T = S^T (a o dY)^T + K^T N^T over each wave's 512 / DX_WAVES features, then the lift backward of k
+// and q to dk, dq, each in two halves of 32 tokens.  The small B operands come from the gradient kernel
+// through the record; LDS holds only the input rows and dx^ (36 KB).  Eight waves (64 features each)
+// halve each wave's accumulators and loops, so that two waves share each SIMD.
+constexpr int DX_WAVES = 8;
 template <class P, typename InT>
-__global__ void __launch_bounds__(256) bwd_dx_kernel(Params p) {
+__global__ void __launch_bounds__(64 * DX_WAVES) bwd_dx_kernel(Params p) {
   __shared__ __attribute__((aligned(16))) float bT[C * LD];   // normalised k / q rows
   __shared__ __attribute__((aligned(16))) float bDX[C * LD];  // dx^ of k / q
-  __shared__ float s_n[C], s_rdp[4][C];
+  __shared__ float s_n[C], s_rdp[DX_WAVES][C];
 
   const int64_t h = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x, lane = tid & 63;
@@ -1231,8 +1244,8 @@ __global__ void __launch_bounds__(256) bwd_dx_kernel(Params p) {
   const bool rvalid = t0 + r < p.T;
   const typename P::frag* bop = reinterpret_cast<const typename P::frag*>(rec + Rec::KXF);
 
-  dx_pass<P, InT, 1>(p, rec, bop, bT, bDX, s_n, s_rdp, b, h, t0, tid, w, lane, r, c0, rvalid);
-  dx_pass<P, InT, 0>(p, rec, bop, bT, bDX, s_n, s_rdp, b, h, t0, tid, w, lane, r, c0, rvalid);
+  dx_pass<P, InT, 1, DX_WAVES>(p, rec, bop, bT, bDX, s_n, s_rdp, b, h, t0, tid, w, lane, r, c0, rvalid);
+  dx_pass<P, InT, 0, DX_WAVES>(p, rec, bop, bT, bDX, s_n, s_rdp, b, h, t0, tid, w, lane, r, c0, rvalid);
 }
 
 }  // namespace bwd
@@ -1382,7 +1395,7 @@ static int segment_phase(const Params& p, int phase, hipStream_t st) {
   if (phase == 3) hipLaunchKernelGGL((bwd_chain_kernel<P, true>), dim3(chain_wgs), dim3(256), 0, st, p);
   if (phase == 4) {
     hipLaunchKernelGGL((bwd_grad_kernel<P, InT>), chunk_grid, dim3(256), 0, st, p);
-    hipLaunchKernelGGL((bwd_dx_kernel<P, InT>), chunk_grid, dim3(256), 0, st, p);
+    hipLaunchKernelGGL((bwd_dx_kernel<P, InT>), chunk_grid, dim3(64 * DX_WAVES), 0, st, p);
   }
   if (phase == PH_CARRIES) hipLaunchKernelGGL((bwd_chains_kernel<P>), dim3(2 * chain_wgs), dim3(256), 0, st, p, chain_wgs);
   return launch_status();
