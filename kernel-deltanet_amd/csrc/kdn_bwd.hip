@@ -39,11 +39,16 @@ constexpr int C = 64, D = 512, DK = 64, DV = 64;
 constexpr int LD = 68;  // LDS row stride (floats) of a 64-wide tile: rows stay 16-byte aligned
 constexpr size_t OMT_BYTES = (size_t)4 * 16 * 64 * 16;  // the Omega^T fragment table
 
-// Rows of the gradient kernel's dl_i contribution table, one per source term: the dkappa term (-t_i),
-// the per-wave column sums of P o dP (4 rows), the row sums of P o dP (at i - 1), beta g (T o dTp)
-// column sums, the a o dY . Q S^T term (at i - 1), the per-wave column sums of A o dA (4 rows) and the
-// row sums of A o dA.
-constexpr int DL_KAPPA = 0, DL_COLP = 1, DL_RP = 5, DL_TS = 6, DL_DA = 7, DL_DLC = 8, DL_A = 12, NDL = 13;
+// The gradient kernel runs eight waves: wave w owns row tile w & 3 and column tiles 2 (w >> 2) .. +1 of
+// the 64 x 64 chunk algebra.  Rows of its dl_i contribution table, one per source term: the dkappa term
+// (-t_i), the column sums of P o dP per row tile (4 rows), the row sums of P o dP per column half (at
+// i - 1; 2 rows), beta g (T o dTp) column sums, the a o dY . Q S^T term per column half (at i - 1; 2
+// rows), the column sums of A o dA per row tile (4 rows) and the row sums of A o dA per column half (2).
+constexpr int GRAD_WAVES = 8;
+constexpr int DL_KAPPA = 0, DL_COLP = 1, DL_RP = 5, DL_TS = 7, DL_DA = 8, DL_DLC = 10, DL_A = 14, NDL = 16;
+// Rows of its dbeta table: the T^T dW . V row sums per column half (2), the Tp column sums, the A o dA
+// row sums per column half (2).
+constexpr int DB_V = 0, DB_TS = 2, DB_A = 3, NDB = 5;
 
 // Fragment slots of the dx kernel's B operands in the record's K-fragment area: token tile m (0..3),
 // operand o, 32-token depth block jb; 32 slots for dK^T (4 operands) then 16 for dQ^T (2 operands).
@@ -844,9 +849,10 @@ __device__ __forceinline__ void write_dx(const Params& p, const InT* x, int64_t 
   }
 }
 
-// grid (nch, H, B), 256 threads.
+// grid (nseg, H, B), GRAD_WAVES waves.  Wave w: row tile rt = w & 3, column tiles 2 ch .. 2 ch + 1 with
+// ch = w >> 2 (the first four waves also load the tiles and the per-row terms).
 template <class P, typename InT>
-__global__ void __launch_bounds__(256) bwd_grad_kernel(Params p) {
+__global__ void __launch_bounds__(64 * GRAD_WAVES) bwd_grad_kernel(Params p) {
   __shared__ __attribute__((aligned(16))) float bY[C * LD];   // dY, then a o dY
   __shared__ __attribute__((aligned(16))) float bW[C * LD];   // W, then kappa o W
   __shared__ __attribute__((aligned(16))) float bdW[C * LD];  // dW, then Zn = -Tp^T dW
@@ -857,25 +863,27 @@ __global__ void __launch_bounds__(256) bwd_grad_kernel(Params p) {
   __shared__ float s_ell[C], s_beta[C];
   // Fixed-order reductions (the gradients do not depend on the order the waves run in): every partial
   // sum has a slot of its own, written once, and the slots are added in a fixed order; no atomics.
-  //   s_dlp: contributions to dl_i = dL/dl_i, one row per source (see NDL); s_dbp: to dbeta_i;
-  //   s_tsp: per-wave column sums of T o dTp;
-  //   s_w63: per-wave sums that land on dl_63 (the dkappa term [0..3] and <Gamma, S> [4..7])
-  __shared__ float s_dlp[NDL][C], s_dbp[3][C], s_tsp[4][C], s_w63[8];
+  //   s_dlp: contributions to dl_i = dL/dl_i (rows DL_*); s_dbp: to dbeta_i (rows DB_*);
+  //   s_tsp: column sums of T o dTp per row tile;
+  //   s_w63: sums that land on dl_63: the dkappa term per row tile [0..3], <Gamma, S> per wave [4..11]
+  __shared__ float s_dlp[NDL][C], s_dbp[NDB][C], s_tsp[4][C], s_w63[4 + GRAD_WAVES];
 
   const int64_t h = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int rt = w & 3, ch = w >> 2;
   const int64_t t0 = (p.c0 + blockIdx.x) * C;
   float* rec = record(p, b, h, blockIdx.x);
-  const int r = tid >> 2, c0 = (tid & 3) * 16;
+  const int r = (tid >> 2) & 63, c0 = (tid & 3) * 16;  // loaders (tid < 256): row r, columns c0 .. c0 + 15
   const bool rvalid = t0 + r < p.T;
 
   if (tid < C) {
     s_ell[tid] = rec[Rec::VEC + tid];
     s_beta[tid] = rec[Rec::VEC + 64 + tid];
   }
-  if (tid == 0) s_dlp[DL_RP][63] = s_dlp[DL_DA][63] = 0.f;  // the only slots no source writes
-  {
+  if (tid == 0)  // the only slots no source writes
+    s_dlp[DL_RP][63] = s_dlp[DL_RP + 1][63] = s_dlp[DL_DA][63] = s_dlp[DL_DA + 1][63] = 0.f;
+  if (tid < 256) {
     const InT* v = reinterpret_cast<const InT*>(p.v);
     const int64_t vb = b * p.vs0 + (t0 + r) * p.vs1 + h * p.vs2 + c0;
     const int64_t yb = b * p.ys0 + (t0 + r) * p.ys1 + h * p.ys2 + c0;
@@ -900,7 +908,7 @@ __global__ void __launch_bounds__(256) bwd_grad_kernel(Params p) {
   const float l63 = s_ell[63], gC = expf(l63);
 
   // ---- phase 1: dkappa; T^T dW -> dv, dbeta; dTp, dT; dP -> N
-  {
+  if (tid < 256) {
     float dkp = 0.f;
 #pragma unroll
     for (int e = 0; e < 16; ++e) dkp += bW[r * LD + c0 + e] * bX[r * LD + c0 + e];
@@ -911,14 +919,15 @@ __global__ void __launch_bounds__(256) bwd_grad_kernel(Params p) {
     const float tw = sum_col4(sum_row16((tid & 3) == 0 ? t : 0.f));
     if (lane == 0) s_w63[w] = tw;
   }
-  f32x4 dT[4], nN[4];
+  f32x4 dT[2], nN[2];
   {
-    const f32x8 ta0 = frag_cols(bT, LD, 16 * w, 0, lane), ta1 = frag_cols(bT, LD, 16 * w, 32, lane);
-    const f32x8 da0 = frag_rows(bdW, LD, 16 * w, 0, lane), da1 = frag_rows(bdW, LD, 16 * w, 32, lane);
-    const f32x8 ya0 = frag_rows(bY, LD, 16 * w, 0, lane), ya1 = frag_rows(bY, LD, 16 * w, 32, lane);
+    const f32x8 ta0 = frag_cols(bT, LD, 16 * rt, 0, lane), ta1 = frag_cols(bT, LD, 16 * rt, 32, lane);
+    const f32x8 da0 = frag_rows(bdW, LD, 16 * rt, 0, lane), da1 = frag_rows(bdW, LD, 16 * rt, 32, lane);
+    const f32x8 ya0 = frag_rows(bY, LD, 16 * rt, 0, lane), ya1 = frag_rows(bY, LD, 16 * rt, 32, lane);
     float dbp[4] = {0.f, 0.f, 0.f, 0.f}, rowp[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int n = 0; n < 4; ++n) {
+    for (int nn = 0; nn < 2; ++nn) {
+      const int n = 2 * ch + nn;
       const int cj = 16 * n + (lane & 15);
       // T^T dW
       const f32x4 td = mm<PrecF32>(mm<PrecF32>(zero4(), ta0, frag_cols(bdW, LD, 16 * n, 0, lane)), ta1, frag_cols(bdW, LD, 16 * n, 32, lane));
@@ -931,36 +940,36 @@ __global__ void __launch_bounds__(256) bwd_grad_kernel(Params p) {
       float ts = 0.f, colp = 0.f;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int ri = 16 * w + 4 * (lane >> 4) + i;
+        const int ri = 16 * rt + 4 * (lane >> 4) + i;
         const bool valid = t0 + ri < p.T;
         if (valid) p.dv[b * p.dvs0 + (t0 + ri) * p.dvs1 + h * p.dvs2 + cj] = s_beta[ri] * td[i];
         dbp[i] += bV[ri * LD + cj] * td[i];
         ts += bT[ri * LD + cj] * dtp[i];
-        dT[n][i] = bj * (e1[i] + gj * dtp[i]);
+        dT[nn][i] = bj * (e1[i] + gj * dtp[i]);
         if (cj < ri) {
           const float pb = dp[i] * rec[Rec::P + ri * C + cj];
           rowp[i] += pb;
           colp += pb;
           const float lim1 = s_ell[ri - 1];
-          nN[n][i] = dp[i] * expf(fminf(lim1 - lj, 0.f));
+          nN[nn][i] = dp[i] * expf(fminf(lim1 - lj, 0.f));
         } else {
-          nN[n][i] = 0.f;
+          nN[nn][i] = 0.f;
         }
       }
       ts = sum_col4(ts);
       colp = sum_col4(colp);
       if (lane < 16) {
-        s_tsp[w][cj] = ts;
-        s_dlp[DL_COLP + w][cj] = -colp;
+        s_tsp[rt][cj] = ts;
+        s_dlp[DL_COLP + rt][cj] = -colp;
       }
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int ri = 16 * w + 4 * (lane >> 4) + i;
+      const int ri = 16 * rt + 4 * (lane >> 4) + i;
       const float db = sum_row16(dbp[i]), rp = sum_row16(rowp[i]);
       if ((lane & 15) == 0) {
-        s_dbp[0][ri] = db;
-        if (ri > 0) s_dlp[DL_RP][ri - 1] = rp;
+        s_dbp[DB_V + ch][ri] = db;
+        if (ri > 0) s_dlp[DL_RP + ch][ri - 1] = rp;
       }
     }
   }
@@ -968,43 +977,44 @@ __global__ void __launch_bounds__(256) bwd_grad_kernel(Params p) {
 
   // ---- phase 2: dT and N to LDS; Tp sums; Q S^T -> da; a o dY, kappa o W; <Gamma, S>
 #pragma unroll
-  for (int n = 0; n < 4; ++n)
+  for (int nn = 0; nn < 2; ++nn)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int ri = 16 * w + 4 * (lane >> 4) + i, cj = 16 * n + (lane & 15);
-      bX[ri * LD + cj] = dT[n][i];
-      bXK[ri * LD + cj] = nN[n][i];
+      const int ri = 16 * rt + 4 * (lane >> 4) + i, cj = 16 * (2 * ch + nn) + (lane & 15);
+      bX[ri * LD + cj] = dT[nn][i];
+      bXK[ri * LD + cj] = nN[nn][i];
     }
   if (tid < C) {
     const float g = expf(s_ell[tid]), ts = ((s_tsp[0][tid] + s_tsp[1][tid]) + s_tsp[2][tid]) + s_tsp[3][tid];
-    s_dbp[1][tid] = g * ts;
+    s_dbp[DB_TS][tid] = g * ts;
     s_dlp[DL_TS][tid] = s_beta[tid] * g * ts;
   }
   {
-    f32x4 qs[4];
+    f32x4 qs[2];
 #pragma unroll
-    for (int n = 0; n < 4; ++n) qs[n] = zero4();
+    for (int nn = 0; nn < 2; ++nn) qs[nn] = zero4();
 #pragma unroll 4
     for (int jb = 0; jb < D / 32; ++jb) {
-      const typename P::frag qa = frag_rows_p<P>(feat<P>(rec, Rec::Q), D, 16 * w, 32 * jb, lane);
+      const typename P::frag qa = frag_rows_p<P>(feat<P>(rec, Rec::Q), D, 16 * rt, 32 * jb, lane);
 #pragma unroll
-      for (int n = 0; n < 4; ++n)
-        qs[n] = P::mma(qs[n], qa, P::from_f32(frag_cols_t(feat<P>(rec, Rec::S), DV, 16 * n, 32 * jb, lane)));
+      for (int nn = 0; nn < 2; ++nn)
+        qs[nn] = P::mma(qs[nn], qa, P::from_f32(frag_cols_t(feat<P>(rec, Rec::S), DV, 16 * (2 * ch + nn), 32 * jb, lane)));
     }
     float dap[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int n = 0; n < 4; ++n)
+    for (int nn = 0; nn < 2; ++nn)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) dap[i] += bY[(16 * w + 4 * (lane >> 4) + i) * LD + 16 * n + (lane & 15)] * qs[n][i];
+      for (int i = 0; i < 4; ++i)
+        dap[i] += bY[(16 * rt + 4 * (lane >> 4) + i) * LD + 16 * (2 * ch + nn) + (lane & 15)] * qs[nn][i];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int ri = 16 * w + 4 * (lane >> 4) + i;
+      const int ri = 16 * rt + 4 * (lane >> 4) + i;
       const float da = sum_row16(dap[i]);
-      if ((lane & 15) == 0 && ri > 0) s_dlp[DL_DA][ri - 1] = da * expf(s_ell[ri - 1]);
+      if ((lane & 15) == 0 && ri > 0) s_dlp[DL_DA + ch][ri - 1] = da * expf(s_ell[ri - 1]);
     }
-    // scale this wave's rows only (no other wave reads them in this phase)
-    for (int e = lane; e < 16 * DV; e += 64) {
-      const int ri = 16 * w + (e >> 6), cv = e & 63;
+    // scale this wave's block only (no other wave reads it in this phase)
+    for (int e = lane; e < 16 * 32; e += 64) {
+      const int ri = 16 * rt + (e >> 5), cv = 32 * ch + (e & 31);
       bY[ri * LD + cv] *= ri > 0 ? expf(s_ell[ri - 1]) : 1.f;
       bW[ri * LD + cv] *= expf(l63 - s_ell[ri]);
     }
@@ -1013,9 +1023,9 @@ __global__ void __launch_bounds__(256) bwd_grad_kernel(Params p) {
     float gs = 0.f;
     const typename Feat<P>::T* G4 = feat<P>(rec, Rec::G);
     const typename Feat<P>::T* S4 = feat<P>(rec, Rec::S);
-    // 32 iterations per thread, unrolled so that their loads are in flight together
+    // 16 iterations per thread, unrolled so that their loads are in flight together
 #pragma unroll 8
-    for (int e = tid; e < D * DV / 4; e += 256) {
+    for (int e = tid; e < D * DV / 4; e += 64 * GRAD_WAVES) {
       const f32x4 g = ld4_t(G4 + 4 * e), s = ld4_t(S4 + 4 * e);
       gs += g[0] * s[0] + g[1] * s[1] + g[2] * s[2] + g[3] * s[3];
     }
@@ -1025,39 +1035,41 @@ __global__ void __launch_bounds__(256) bwd_grad_kernel(Params p) {
   __syncthreads();
 
   // ---- phase 3: Y1 = dT T^T; Zn = -Tp^T dW
-  f32x4 y1[4], zn[4];
+  f32x4 y1[2], zn[2];
   {
-    const f32x8 a0 = frag_rows(bX, LD, 16 * w, 0, lane), a1 = frag_rows(bX, LD, 16 * w, 32, lane);
-    const f32x8 p0 = frag_rows(rec + Rec::TPT, C, 16 * w, 0, lane), p1 = frag_rows(rec + Rec::TPT, C, 16 * w, 32, lane);
+    const f32x8 a0 = frag_rows(bX, LD, 16 * rt, 0, lane), a1 = frag_rows(bX, LD, 16 * rt, 32, lane);
+    const f32x8 p0 = frag_rows(rec + Rec::TPT, C, 16 * rt, 0, lane), p1 = frag_rows(rec + Rec::TPT, C, 16 * rt, 32, lane);
 #pragma unroll
-    for (int n = 0; n < 4; ++n) {
-      y1[n] = mm<PrecF32>(mm<PrecF32>(zero4(), a0, frag_rows(bT, LD, 16 * n, 0, lane)), a1, frag_rows(bT, LD, 16 * n, 32, lane));
-      zn[n] = -mm<PrecF32>(mm<PrecF32>(zero4(), p0, frag_cols(bdW, LD, 16 * n, 0, lane)), p1, frag_cols(bdW, LD, 16 * n, 32, lane));
+    for (int nn = 0; nn < 2; ++nn) {
+      const int n = 2 * ch + nn;
+      y1[nn] = mm<PrecF32>(mm<PrecF32>(zero4(), a0, frag_rows(bT, LD, 16 * n, 0, lane)), a1, frag_rows(bT, LD, 16 * n, 32, lane));
+      zn[nn] = -mm<PrecF32>(mm<PrecF32>(zero4(), p0, frag_cols(bdW, LD, 16 * n, 0, lane)), p1, frag_cols(bdW, LD, 16 * n, 32, lane));
     }
   }
   __syncthreads();
 #pragma unroll
-  for (int n = 0; n < 4; ++n)
+  for (int nn = 0; nn < 2; ++nn)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int ri = 16 * w + 4 * (lane >> 4) + i, cj = 16 * n + (lane & 15);
-      bV[ri * LD + cj] = y1[n][i];
-      bdW[ri * LD + cj] = zn[n][i];
+      const int ri = 16 * rt + 4 * (lane >> 4) + i, cj = 16 * (2 * ch + nn) + (lane & 15);
+      bV[ri * LD + cj] = y1[nn][i];
+      bdW[ri * LD + cj] = zn[nn][i];
     }
   __syncthreads();
 
   // ---- phase 4: dA = -T^T Y1 (strictly lower); M + M^T into bX; dbeta, dl from A
   {
-    const f32x8 ta0 = frag_cols(bT, LD, 16 * w, 0, lane), ta1 = frag_cols(bT, LD, 16 * w, 32, lane);
+    const f32x8 ta0 = frag_cols(bT, LD, 16 * rt, 0, lane), ta1 = frag_cols(bT, LD, 16 * rt, 32, lane);
     float dbr[4] = {0.f, 0.f, 0.f, 0.f}, dlr[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int n = 0; n < 4; ++n) {
+    for (int nn = 0; nn < 2; ++nn) {
+      const int n = 2 * ch + nn;
       const f32x4 dA = -mm<PrecF32>(mm<PrecF32>(zero4(), ta0, frag_cols(bV, LD, 16 * n, 0, lane)), ta1, frag_cols(bV, LD, 16 * n, 32, lane));
       const int cj = 16 * n + (lane & 15);
       float dlc = 0.f;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int ri = 16 * w + 4 * (lane >> 4) + i;
+        const int ri = 16 * rt + 4 * (lane >> 4) + i;
         if (cj < ri) {
           const float ex = expf(fminf(s_ell[ri] - s_ell[cj], 0.f));
           const float e = dA[i] * ex * rec[Rec::GKK + ri * C + cj];
@@ -1073,15 +1085,15 @@ __global__ void __launch_bounds__(256) bwd_grad_kernel(Params p) {
         }
       }
       dlc = sum_col4(dlc);
-      if (lane < 16) s_dlp[DL_DLC + w][cj] = -dlc;
+      if (lane < 16) s_dlp[DL_DLC + rt][cj] = -dlc;
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int ri = 16 * w + 4 * (lane >> 4) + i;
+      const int ri = 16 * rt + 4 * (lane >> 4) + i;
       const float a = sum_row16(dbr[i]), d = sum_row16(dlr[i]);
       if ((lane & 15) == 0) {
-        s_dbp[2][ri] = a;
-        s_dlp[DL_A][ri] = d;
+        s_dbp[DB_A + ch][ri] = a;
+        s_dlp[DL_A + ch][ri] = d;
       }
     }
   }
@@ -1092,9 +1104,17 @@ __global__ void __launch_bounds__(256) bwd_grad_kernel(Params p) {
     float dl = 0.f;
 #pragma unroll
     for (int k = 0; k < NDL; ++k) dl += s_dlp[k][lane];
-    if (lane == 63)
-      dl += (((s_w63[0] + s_w63[1]) + s_w63[2]) + s_w63[3]) + (((s_w63[4] + s_w63[5]) + s_w63[6]) + s_w63[7]) * gC;
-    const float dbeta = (s_dbp[0][lane] + s_dbp[1][lane]) + s_dbp[2][lane];
+    if (lane == 63) {
+      float kap = 0.f, gs = 0.f;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) kap += s_w63[v];
+#pragma unroll
+      for (int v = 0; v < GRAD_WAVES; ++v) gs += s_w63[4 + v];
+      dl += kap + gs * gC;
+    }
+    float dbeta = 0.f;
+#pragma unroll
+    for (int k = 0; k < NDB; ++k) dbeta += s_dbp[k][lane];
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) {
       const float u = __shfl_down(dl, o);
@@ -1111,20 +1131,18 @@ __global__ void __launch_bounds__(256) bwd_grad_kernel(Params p) {
   }
 
   // ---- the B operands of the dx kernel, as P fragments in the record's K-fragment area (dead once both
-  // carries are done): token tile m = w, dK^T [kappa o W, Zn, N^T, M + M^T], dQ^T [a o dY, N]
+  // carries are done): token tile m = w & 3, depth block jb = w >> 2, dK^T [kappa o W, Zn, N^T, M + M^T],
+  // dQ^T [a o dY, N]
   {
     using frag = typename P::frag;
     frag* bop = reinterpret_cast<frag*>(rec + Rec::KXF);
-    const int m = w;
-#pragma unroll
-    for (int jb = 0; jb < 2; ++jb) {
-      bop[bop_dk(m, 0, jb) * 64 + lane] = P::from_f32(frag_rows(bW, LD, 16 * m, 32 * jb, lane));
-      bop[bop_dk(m, 1, jb) * 64 + lane] = P::from_f32(frag_rows(bdW, LD, 16 * m, 32 * jb, lane));
-      bop[bop_dk(m, 2, jb) * 64 + lane] = P::from_f32(frag_cols(bXK, LD, 16 * m, 32 * jb, lane));
-      bop[bop_dk(m, 3, jb) * 64 + lane] = P::from_f32(frag_rows(bX, LD, 16 * m, 32 * jb, lane));
-      bop[bop_dq(m, 0, jb) * 64 + lane] = P::from_f32(frag_rows(bY, LD, 16 * m, 32 * jb, lane));
-      bop[bop_dq(m, 1, jb) * 64 + lane] = P::from_f32(frag_rows(bXK, LD, 16 * m, 32 * jb, lane));
-    }
+    const int m = rt, jb = ch;
+    bop[bop_dk(m, 0, jb) * 64 + lane] = P::from_f32(frag_rows(bW, LD, 16 * m, 32 * jb, lane));
+    bop[bop_dk(m, 1, jb) * 64 + lane] = P::from_f32(frag_rows(bdW, LD, 16 * m, 32 * jb, lane));
+    bop[bop_dk(m, 2, jb) * 64 + lane] = P::from_f32(frag_cols(bXK, LD, 16 * m, 32 * jb, lane));
+    bop[bop_dk(m, 3, jb) * 64 + lane] = P::from_f32(frag_rows(bX, LD, 16 * m, 32 * jb, lane));
+    bop[bop_dq(m, 0, jb) * 64 + lane] = P::from_f32(frag_rows(bY, LD, 16 * m, 32 * jb, lane));
+    bop[bop_dq(m, 1, jb) * 64 + lane] = P::from_f32(frag_rows(bXK, LD, 16 * m, 32 * jb, lane));
   }
 }
 
@@ -1394,7 +1412,7 @@ static int segment_phase(const Params& p, int phase, hipStream_t st) {
   if (phase == 2) hipLaunchKernelGGL((bwd_chain_kernel<P, false>), dim3(chain_wgs), dim3(256), 0, st, p);
   if (phase == 3) hipLaunchKernelGGL((bwd_chain_kernel<P, true>), dim3(chain_wgs), dim3(256), 0, st, p);
   if (phase == 4) {
-    hipLaunchKernelGGL((bwd_grad_kernel<P, InT>), chunk_grid, dim3(256), 0, st, p);
+    hipLaunchKernelGGL((bwd_grad_kernel<P, InT>), chunk_grid, dim3(64 * GRAD_WAVES), 0, st, p);
     hipLaunchKernelGGL((bwd_dx_kernel<P, InT>), chunk_grid, dim3(64 * DX_WAVES), 0, st, p);
   }
   if (phase == PH_CARRIES) hipLaunchKernelGGL((bwd_chains_kernel<P>), dim3(2 * chain_wgs), dim3(256), 0, st, p, chain_wgs);
