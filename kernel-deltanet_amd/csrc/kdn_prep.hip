@@ -33,10 +33,11 @@ struct PrepInputs {
   static constexpr int VPT = (64 * VPR + 255) / 256;             // pieces per thread
   RawRow<InT> qk[2];
   float be, la;
+  template <bool NOQ = false>
   __device__ __forceinline__ void load_qk(const ScanParams& p, const Seq& sq, int64_t h, int64_t t0, int w, int lane) {
     const int64_t trow = t0 + 16 * w + (lane & 15);
     const bool rvalid = trow < sq.len;
-    qk[0].load((const InT*)p.q + sq.q + trow * p.qs1 + h * p.qs2, rvalid, lane);
+    if constexpr (!NOQ) qk[0].load((const InT*)p.q + sq.q + trow * p.qs1 + h * p.qs2, rvalid, lane);
     qk[1].load((const InT*)p.k + sq.k + trow * p.ks1 + h * p.ks2, rvalid, lane);
     const int64_t t = t0 + lane;
     const bool valid = t < sq.len;
@@ -72,8 +73,12 @@ __device__ __forceinline__ void load_lifted(const InT* row, bool valid, int lane
   }
 }
 
-template <class P, typename InT, int D, int DV, int FM>
+// NOQ (exact projection only, ScanParams::prep_no_q): no output kernel reads this segment's records (the
+// backward's checkpoint pass runs prep and state only), so the queries are not lifted and neither P nor
+// the query scales are formed.
+template <class P, typename InT, int D, int DV, int FM, bool NOQ = false>
 __global__ void __launch_bounds__(256, (PrepWaves<P, FM>::value)) prep_kernel(ScanParams p) {
+  static_assert(!NOQ || FM == FM_EXACT, "only the exact projection is lifted again by the output kernel");
   using L = WsLayout<P, D, DV>;
   using frag = typename P::frag;
   using In = PrepInputs<InT, DV>;
@@ -109,7 +114,7 @@ __global__ void __launch_bounds__(256, (PrepWaves<P, FM>::value)) prep_kernel(Sc
   In in;
   if constexpr (FM != FM_PRELIFTED) {
     stage_omega<D, OMEGA_LDS>(omega_h, p.phase + h * p.phs, s_omega, s_phrev);
-    in.load_qk(p, sq, h, (p.chunk0 + cl0) * CH, w, lane);
+    in.template load_qk<NOQ>(p, sq, h, (p.chunk0 + cl0) * CH, w, lane);
   } else {
     // no lift: only beta / decay come through the prefetch
     const int64_t t = (p.chunk0 + cl0) * CH + lane;
@@ -138,8 +143,10 @@ __global__ void __launch_bounds__(256, (PrepWaves<P, FM>::value)) prep_kernel(Sc
     }
 
     // ---- lift q and k rows of this wave (or load the given features)
-    frag cqk[2][NJ];  // [0] = q, [1] = k; X fragments (m = w, j): row 16w + (l&15), feature 32j + kappa(l, s)
-    float ss[2] = {0.f, 0.f};
+    // X fragments (m = w, j): row 16w + (l&15), feature 32j + kappa(l, s); [QI] = q, [KI] = k
+    constexpr int NX = NOQ ? 1 : 2, QI = 0, KI = NX - 1;
+    frag cqk[NX][NJ];
+    float ss[NX];
     if constexpr (FM == FM_PRELIFTED) {
       const int64_t trow = t0 + 16 * w + (lane & 15);
       load_lifted<P, InT, D>((const InT*)p.q + sq.q + trow * p.qs1 + h * p.qs2, trow < sq.len, lane, cqk[0]);
@@ -148,10 +155,15 @@ __global__ void __launch_bounds__(256, (PrepWaves<P, FM>::value)) prep_kernel(Sc
       in.be = (tn < sq.len) ? p.beta[sq.be + tn * p.bs1 + h * p.bs2] : 0.f;
       in.la = (tn < sq.len && p.decay) ? p.decay[sq.de + tn * p.ds1 + h * p.ds2] : 1.f;
     } else {
-      lift_tile<P, InT, D, OMEGA_LDS, 2, FM == FM_HILO>(in.qk, p.normalize, s_omega, omega_h, s_phrev, ang, lane,
-                                                         cqk, ss, omega_lo_h);
+      if constexpr (NOQ) {
+        const RawRow<InT> kraw[1] = {in.qk[1]};
+        lift_tile<P, InT, D, OMEGA_LDS, 1>(kraw, p.normalize, s_omega, omega_h, s_phrev, ang, lane, cqk, ss);
+      } else {
+        lift_tile<P, InT, D, OMEGA_LDS, 2, FM == FM_HILO>(in.qk, p.normalize, s_omega, omega_h, s_phrev, ang, lane,
+                                                           cqk, ss, omega_lo_h);
+      }
       // the next chunk's rows travel while this one is processed (clamped: the last chunk reloads itself)
-      if constexpr (RUN != 1) in.load_qk(p, sq, h, (p.chunk0 + ((cl + 1 < cl_end) ? cl + 1 : cl)) * CH, w, lane);
+      if constexpr (RUN != 1) in.template load_qk<NOQ>(p, sq, h, (p.chunk0 + ((cl + 1 < cl_end) ? cl + 1 : cl)) * CH, w, lane);
     }
     {
       // per-row scale of the stored (unnormalised) features: 1 for given features, sqrt(2/D) without
@@ -164,10 +176,10 @@ __global__ void __launch_bounds__(256, (PrepWaves<P, FM>::value)) prep_kernel(Sc
         } else if (p.no_renorm) {
           sq_ = amp; sk_ = amp;
         } else {
-          sq_ = amp / (amp * sqrtf(ss[0]) + 1e-8f);
-          sk_ = amp / (amp * sqrtf(ss[1]) + 1e-8f);
+          sq_ = NOQ ? 0.f : amp / (amp * sqrtf(ss[QI]) + 1e-8f);
+          sk_ = amp / (amp * sqrtf(ss[KI]) + 1e-8f);
         }
-        s_sq[16 * w + lane] = sq_;
+        if constexpr (!NOQ) s_sq[16 * w + lane] = sq_;
         s_sk[16 * w + lane] = sk_;
       }
     }
@@ -176,11 +188,13 @@ __global__ void __launch_bounds__(256, (PrepWaves<P, FM>::value)) prep_kernel(Sc
       // The records are read back by the state and output kernels a segment or more later, long after
       // they could still sit in L2: streaming stores keep them from evicting the state kernel's lines.
       if constexpr (IsBF16<P>::value && D == 512)
-        store_k_image(ws + L::phiK, w, j, lane, cqk[1][j]);
+        store_k_image(ws + L::phiK, w, j, lane, cqk[KI][j]);
       else
-        store_frag_nt<P>(ws + L::phiK + (size_t)(w * NJ + j) * 64 * L::FB, lane, cqk[1][j]);
-      if (!p.relift_q) store_frag_nt<P>(ws + L::phiQ + (size_t)(w * NJ + j) * 64 * L::FB, lane, cqk[0][j]);
-      s_phik[(w * NJ + j) * 64 + lane] = cqk[1][j];
+        store_frag_nt<P>(ws + L::phiK + (size_t)(w * NJ + j) * 64 * L::FB, lane, cqk[KI][j]);
+      if constexpr (!NOQ) {
+        if (!p.relift_q) store_frag_nt<P>(ws + L::phiQ + (size_t)(w * NJ + j) * 64 * L::FB, lane, cqk[QI][j]);
+      }
+      s_phik[(w * NJ + j) * 64 + lane] = cqk[KI][j];
     }
     __syncthreads();
 
@@ -193,8 +207,8 @@ __global__ void __launch_bounds__(256, (PrepWaves<P, FM>::value)) prep_kernel(Sc
 #pragma unroll
       for (int m = 0; m < 4; ++m) {
         const frag a = s_phik[(m * NJ + j) * 64 + lane];
-        gkk[m] = P::mma(gkk[m], a, cqk[1][j]);
-        gqk[m] = P::mma(gqk[m], a, cqk[0][j]);
+        gkk[m] = P::mma(gkk[m], a, cqk[KI][j]);
+        if constexpr (!NOQ) gqk[m] = P::mma(gqk[m], a, cqk[QI][j]);
       }
     }
     __syncthreads();  // K fragments in LDS are dead from here on
@@ -204,7 +218,7 @@ __global__ void __launch_bounds__(256, (PrepWaves<P, FM>::value)) prep_kernel(Sc
       const int t = 16 * w + (lane & 15);
       // the linear rule has no erasure coupling: A = 0, so T = I below
       const float bt = p.linear ? 0.f : s_beta[t], gt = s_g[t], gtm1 = t > 0 ? s_g[t - 1] : 0.f;
-      const float skt = s_sk[t], sqt = s_sq[t];
+      const float skt = s_sk[t], sqt = NOQ ? 0.f : s_sq[t];
       f32x4 pt[4];
 #pragma unroll
       for (int m = 0; m < 4; ++m) {
@@ -214,12 +228,14 @@ __global__ void __launch_bounds__(256, (PrepWaves<P, FM>::value)) prep_kernel(Sc
           const float gj = s_g[j], skj = s_sk[j];
           const float a = (j < t) ? bt * __expf(fminf(gt - gj, 0.f)) * gkk[m][i] * skt * skj : 0.f;
           s_A[(j * 4 + (t & 3)) * 16 + (t >> 2)] = a;
-          pt[m][i] = (j < t) ? __expf(fminf(gtm1 - gj, 0.f)) * gqk[m][i] * sqt * skj : 0.f;
+          if constexpr (!NOQ) pt[m][i] = (j < t) ? __expf(fminf(gtm1 - gj, 0.f)) * gqk[m][i] * sqt * skj : 0.f;
         }
       }
+      if constexpr (!NOQ) {
 #pragma unroll
-      for (int jb = 0; jb < 2; ++jb)
-        store_frag_nt<P>(ws + L::Pm + (size_t)(w * 2 + jb) * 64 * L::FB, lane, P::from_f32(pair_to8(pt[2 * jb], pt[2 * jb + 1])));
+        for (int jb = 0; jb < 2; ++jb)
+          store_frag_nt<P>(ws + L::Pm + (size_t)(w * 2 + jb) * 64 * L::FB, lane, P::from_f32(pair_to8(pt[2 * jb], pt[2 * jb + 1])));
+      }
     }
     if constexpr (RUN == 1) In::load_v(p, sq, h, t0, vraw);
 #pragma unroll
@@ -231,7 +247,7 @@ __global__ void __launch_bounds__(256, (PrepWaves<P, FM>::value)) prep_kernel(Sc
       float* vec = reinterpret_cast<float*>(ws + L::VEC);
       const float g63 = s_g[63];
       const float gtm1 = lane > 0 ? s_g[lane - 1] : 0.f;
-      vec[lane] = __expf(fminf(gtm1, 0.f)) * s_sq[lane];                 // e^{g_{t-1}} * |phi_q| scale
+      if constexpr (!NOQ) vec[lane] = __expf(fminf(gtm1, 0.f)) * s_sq[lane];  // e^{g_{t-1}} * |phi_q| scale
       vec[64 + lane] = __expf(fminf(g63 - s_g[lane], 0.f)) * s_sk[lane]; // e^{g_63 - g_t} * |phi_k| scale
       if (lane == 0) vec[128] = __expf(fminf(g63, 0.f));
     }
@@ -300,6 +316,7 @@ int launch_prep(const ScanParams& p, hipStream_t st) {
   const dim3 prep_grid((unsigned)((p.nseg + run - 1) / run), (unsigned)p.H, (unsigned)p.B);
   if (fm == FM_PRELIFTED) hipLaunchKernelGGL((prep_kernel<P, InT, D, DV, FM_PRELIFTED>), prep_grid, dim3(256), 0, st, p);
   else if (fm == FM_HILO) hipLaunchKernelGGL((prep_kernel<P, InT, D, DV, FM_HILO>), prep_grid, dim3(256), 0, st, p);
+  else if (p.prep_no_q) hipLaunchKernelGGL((prep_kernel<P, InT, D, DV, FM_EXACT, true>), prep_grid, dim3(256), 0, st, p);
   else hipLaunchKernelGGL((prep_kernel<P, InT, D, DV, FM_EXACT>), prep_grid, dim3(256), 0, st, p);
   return hipGetLastError() == hipSuccess ? KDN_OK : KDN_ERR_DEVICE;
 }

@@ -689,6 +689,7 @@ static ScanParams fill_params(const kdn_scan_args* a) {
   p.seq_hi = a->cu_seqlens ? a->cu_seqlens + 1 : nullptr;
   p.slots = a->state_slots;
   p.relift_q = 0;
+  p.prep_no_q = 0;
   return p;
 }
 
@@ -990,6 +991,7 @@ static int checkpoints_t(const kdn_scan_args* a, int64_t seg, int64_t n, float* 
     ScanParams p = segment_params(a, r, c0, (nchunks - c0 < seg) ? (nchunks - c0) : seg,
                                   ws + (size_t)(side ? s % nbuf : 0) * buf_bytes, prep_cus);
     p.relift_q = 1;  // no output kernel reads the lifted queries
+    p.prep_no_q = 1;
     p.y = nullptr;
     if (s > 0) {
       p.state_in = ckpt + (size_t)(s - 1) * state_floats;

@@ -97,6 +97,8 @@ struct ScanParams {
   // the output kernel lifts q itself and prep does not store phiQ (bf16, exact projection, pipelined
   // with CUs to spare: recomputing q's features on those CUs is cheaper than streaming them through HBM)
   int relift_q;
+  // no output kernel reads the segment (the backward's checkpoint pass): prep lifts only the keys
+  int prep_no_q;
   // ragged batches: sequence b is token rows seq_lo[b] .. seq_hi[b] (stride 1 of each token tensor; for
   // cu_seqlens, seq_hi = cu_seqlens + 1); its state is slot slots[b] (stride 0 of the state tensors)
   const int64_t* seq_lo;
