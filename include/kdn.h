@@ -240,9 +240,11 @@ int kdn_scan_output(const kdn_scan_args* a, int64_t chunk0, int64_t nchunks, voi
  * Replaces the autograd recompute of FusedKernelDeltaNetFunction.backward,
  * kernels/fused_kernel_deltanet.py:168-179.  `fwd` holds the forward's arguments (shapes, q, k, v, beta,
  * decay, omega_bf16, phase, inv_tau, normalize_input, initial_state, segment_chunks; its y, final_state
- * and workspace are ignored).  Supported: d_k = 64, D = 512, d_v = 64, the delta rule (rule 0) with the
- * structured lift of one shared Omega (no hi + lo, per-head or pre-lifted features, no_renorm 0), uniform
- * batches (no cu_seqlens / state_slots); other requests return KDN_ERR_UNSUPPORTED.  dy and
+ * and workspace are ignored).  Supported: d_k = 64, D = 512, d_v = 64, the delta rule (rule 0) or the
+ * linear rule (rule 1), the lifted features of feature mode 0 with every feature-map field (one shared or
+ * per-head Omega, with or without low parts, shared or per-head phases and 1/tau, with or without
+ * renormalisation; ABI 1.7, before which only one shared structured Omega), uniform batches (no
+ * cu_seqlens / state_slots); pre-lifted features and other requests return KDN_ERR_UNSUPPORTED.  dy and
  * d_final_state are fp32; every gradient is written in fp32 with the layout of its input: dq, dk
  * (B, T, H, d_k), dv (B, T, H, d_v), dbeta, ddecay (B, T, H), d_initial_state (B, H, D, d_v).
  * d_final_state NULL means dL/dS_T = 0; ddecay (allowed only with decay) and d_initial_state may be
@@ -254,7 +256,9 @@ int kdn_scan_output(const kdn_scan_args* a, int64_t chunk0, int64_t nchunks, voi
  * recomputes its chunks, carries the state forward from its checkpoint and dL/dS backward from the
  * next segment, and writes its gradients.  The workspace (256-byte aligned) holds up to three segments'
  * records (1,247,232 bytes per (batch, head, chunk)), one fp32 [B][H][512][64] state per segment
- * boundary plus one more, up to two buffers of the forward scan's records and a 64 KB table: it grows
+ * boundary plus one more, up to two buffers of the forward scan's records and a 64 KB table of Omega^T
+ * fragments (one per head with per-head Omega, twice that with low parts; with dinv_tau, 4 bytes per
+ * (batch, head, chunk) more): it grows
  * with the segment, not with T, apart from the 128 KB per head per segment boundary.  Every reduction
  * runs in a fixed order: the results are identical bit for bit from run to run and between
  * kdn_delta_scan_bwd and kdn_delta_scan_bwd_streams. */
@@ -269,6 +273,10 @@ typedef struct kdn_scan_bwd_args {
   float* ddecay;              int64_t ddecay_stride[3];
   float* d_initial_state;     int64_t dinit_stride[4];
   void* workspace;            size_t workspace_bytes;
+  /* ABI 1.7: dL/d(1/tau) per head, float32 [H] (NULL: not computed).  With per-head 1/tau
+   * (fwd->inv_tau_head) it is that head's gradient; with the shared fwd->inv_tau the H values sum to its
+   * gradient.  Reduced in a fixed order over batches and chunks (deterministic). */
+  float* dinv_tau;
 } kdn_scan_bwd_args;
 
 /* Workspace bytes kdn_delta_scan_bwd needs (0 if the arguments are invalid or unsupported). */

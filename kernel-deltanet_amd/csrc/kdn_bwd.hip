@@ -95,6 +95,14 @@ struct Params {
   const float* decay; int64_t ds0, ds1, ds2;
   const __bf16* omega; const float* phase;
   float inv_tau; int normalize;
+  // the feature map beyond one shared structured Omega: low parts of Omega (Omega = hi + lo; NULL when
+  // hi is exact), head strides of Omega and the phases in elements (0: shared), per-head 1/tau (NULL:
+  // inv_tau), phi = sqrt(2/D) cos(.) without renormalisation; the linear update rule
+  const __bf16* omega_lo; int64_t oms, phs;
+  const float* inv_tau_head;
+  int no_renorm, linear;
+  float* dit;       // dL/d(1/tau) of each (batch, head, chunk) [B][H][nch] (NULL: not wanted)
+  float* dinv_tau;  // dL/d(1/tau) per head [H], the sum of dit over batches and chunks
   const float* init; int64_t is0, is1, is2, is3;  // S^T at the segment start (NULL: zero)
   const float* dy; int64_t ys0, ys1, ys2;
   const float* dfin; int64_t fs0, fs1, fs2, fs3;  // dL/dS^T at the segment end (NULL: zero)
@@ -105,8 +113,14 @@ struct Params {
   float* ddecay; int64_t dds0, dds1, dds2;
   float* gout; int64_t gos0, gos1, gos2, gos3;    // dL/dS^T at the segment start (NULL: not kept)
   float* ws;                                       // this segment's buffer of records
-  const bf16x8* omt;  // Omega^T fragments [a 4][jb 16][lane] (workspace tail, written before the gradients)
+  const bf16x8* omt;  // Omega^T fragments [part][a 4][jb 16][lane] (workspace tail, written before the gradients)
+  int64_t omt_hs;     // entries between heads' tables (0: one table); part 1 (the lo parts) at +OMT_ENTRIES
 };
+constexpr int OMT_ENTRIES = 4 * 16 * 64;
+
+__device__ __forceinline__ float head_inv_tau(const Params& p, int64_t h) {
+  return p.inv_tau_head ? p.inv_tau_head[h] : p.inv_tau;
+}
 
 // Record of local chunk c (0 .. nseg - 1) of the segment.
 __device__ __forceinline__ float* record(const Params& p, int64_t b, int64_t h, int64_t c) {
@@ -212,7 +226,8 @@ __device__ __forceinline__ void round_like_input(int normalize, float* part) {
 
 // ---------------------------------------------------------------------------------------------- prep
 // grid (nch, H, B), 256 threads.
-template <class P, typename InT>
+// LO: Omega has low parts (their products are added in the lift).
+template <class P, typename InT, bool LO>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) bwd_prep_kernel(Params p) {
   // Four 64 x 64 tiles (71 KB with the vectors), so that two workgroups share a CU.
   __shared__ __attribute__((aligned(16))) float smem[4 * C * LD];
@@ -261,6 +276,10 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
   }
 
   const float amp = sqrtf(2.f / D);
+  const __bf16* om = p.omega + h * p.oms;
+  const __bf16* oml = LO ? p.omega_lo + h * p.oms : nullptr;
+  const float* phs = p.phase + h * p.phs;
+  const float itau = head_inv_tau(p, h);
   for (int which = 0; which < 2; ++which) {  // 0: q, 1: k
     const InT* x = reinterpret_cast<const InT*>(which == 0 ? p.q : p.k);
     const int64_t xb = which == 0 ? b * p.qs0 + (t0 + r) * p.qs1 + h * p.qs2 : b * p.ks0 + (t0 + r) * p.ks1 + h * p.ks2;
@@ -287,24 +306,30 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
 #pragma unroll
         for (int i = 0; i < 4; ++i) ss[u][i] = 0.f;
       // Omega rows and phases of feature tile ft + 1 are issued in the region of tile ft
-      f32x8 on0 = frag_rows_plain_bf16(p.omega, DK, 128 * w, 0, lane), on1 = frag_rows_plain_bf16(p.omega, DK, 128 * w, 32, lane);
-      float phn = p.phase[128 * w + (lane & 15)];
+      f32x8 on0 = frag_rows_plain_bf16(om, DK, 128 * w, 0, lane), on1 = frag_rows_plain_bf16(om, DK, 128 * w, 32, lane);
+      float phn = phs[128 * w + (lane & 15)];
 #pragma unroll
       for (int ft = 0; ft < 8; ++ft) {
         const int f0 = 128 * w + 16 * ft;
         const f32x8 o0 = on0, o1 = on1;
         const float ph = phn;
         if (ft + 1 < 8) {
-          on0 = frag_rows_plain_bf16(p.omega, DK, f0 + 16, 0, lane);
-          on1 = frag_rows_plain_bf16(p.omega, DK, f0 + 16, 32, lane);
-          phn = p.phase[f0 + 16 + (lane & 15)];
+          on0 = frag_rows_plain_bf16(om, DK, f0 + 16, 0, lane);
+          on1 = frag_rows_plain_bf16(om, DK, f0 + 16, 32, lane);
+          phn = phs[f0 + 16 + (lane & 15)];
+        }
+        f32x8 l0 = {}, l1 = {};
+        if constexpr (LO) {  // the low parts: their products are added like the forward's
+          l0 = frag_rows_plain_bf16(oml, DK, f0, 0, lane);
+          l1 = frag_rows_plain_bf16(oml, DK, f0, 32, lane);
         }
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
           f32x4 sv = mm<P>(mm<P>(zero4(), xa[u][0], o0), xa[u][1], o1);
+          if constexpr (LO) sv = mm<P>(mm<P>(sv, xa[u][0], l0), xa[u][1], l1);
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            const float v = amp * cos_rad(sv[i] * p.inv_tau + ph);
+            const float v = amp * cos_rad(sv[i] * itau + ph);
             sv[i] = v;
             ss[u][i] += v * v;
           }
@@ -339,7 +364,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int row = 32 * hm + 16 * u + 4 * (lane >> 4) + i;
-            sc[u][i] = (t0 + row < p.T) ? 1.f / (s_n[row] + 1e-8f) : 0.f;
+            sc[u][i] = (t0 + row < p.T) ? (p.no_renorm ? 1.f : 1.f / (s_n[row] + 1e-8f)) : 0.f;
           }
 #pragma unroll
         for (int ft = 0; ft < 8; ++ft) {
@@ -449,7 +474,9 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
         rec[Rec::GQK + ri * C + cj] = gqk[n][i];
         const float li = s_ell[ri], lj = s_ell[cj], lim1 = ri > 0 ? s_ell[ri - 1] : 0.f;
         // A transposed for the column-oriented inverse below: [j][p][s] = A[4s+p][j]
-        bA[(cj * 4 + (ri & 3)) * 16 + (ri >> 2)] = cj < ri ? s_beta[ri] * expf(fminf(li - lj, 0.f)) * gkk[n][i] : 0.f;
+        // (the linear rule has no erasure coupling: A = 0, so T = I and Tp = 0 below)
+        bA[(cj * 4 + (ri & 3)) * 16 + (ri >> 2)] =
+            (cj < ri && !p.linear) ? s_beta[ri] * expf(fminf(li - lj, 0.f)) * gkk[n][i] : 0.f;
         bP[ri * LD + cj] = cj < ri ? expf(fminf(lim1 - lj, 0.f)) * gqk[n][i] : 0.f;
       }
   }
@@ -460,7 +487,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
   for (int idx = tid; idx < C * C; idx += 256) {
     const int i = idx >> 6, j = idx & 63;
     const float tij = bT[i * LD + j];
-    const float tp = tij * s_beta[j] * expf(s_ell[j]);
+    const float tp = p.linear ? 0.f : tij * s_beta[j] * expf(s_ell[j]);
     rec[Rec::T + idx] = tij;
     rec[Rec::TP + idx] = tp;
     rec[Rec::TPT + j * C + i] = tp;
@@ -710,45 +737,55 @@ __global__ void __launch_bounds__(256) bwd_chains_kernel(Params p, unsigned half
 // ds = -sqrt(2/D) sin(s) (dphi / (n + 1e-8) - phi (phi . dphi) / n), then dx^ = ds Omega reduced over
 // the waves into `dx` (LDS [64][LD], zeroed by the caller).  `xh` holds the normalised
 // input rows; s_rd[w] receives wave w's part of phi . dphi per token (summed in wave order).
-template <class P, int NW>
+// GEN: the general feature map (per-head or hi + lo Omega, per-head phases and 1/tau, optional
+// renormalisation, dL/d(1/tau)); without it the one shared structured Omega, renormalised, in the
+// registers the path needs alone.  LO (with GEN): Omega has low parts.
+template <class P, int NW, bool LO, bool GEN>
 __device__ __forceinline__ void lift_backward_half(const Params& p, const typename Feat<P>::T* phi, const float* nrm,
                                                    float (*s_rd)[C], const float* xh, float* dx,
-                                                   f32x4 (&acc)[32 / NW][2], int hm, int w, int lane) {
+                                                   f32x4 (&acc)[32 / NW][2], int hm, int w, int lane, int64_t h,
+                                                   float& dit) {
   constexpr int NFT = 32 / NW;
   const int fb = 16 * NFT * w;  // the wave's first feature
-  // Omega, its phases and the Omega^T table, opaque per call: their load addresses do not depend on the
-  // half, and hoisted out of the caller's loop they would hold registers through it.
-  const __bf16* omega = p.omega;
-  const float* phase = p.phase;
-  const bf16x8* omt = p.omt;
-  asm volatile("" : "+s"(omega), "+s"(phase), "+s"(omt));
-  float rd[2] = {0.f, 0.f};
+  // Omega (and its low parts), the phases and the Omega^T tables of head h, opaque per call: their load
+  // addresses do not depend on the half, and hoisted out of the caller's loop they would hold registers
+  // through it.
+  const __bf16* omega = GEN ? p.omega + h * p.oms : p.omega;
+  const __bf16* omega_lo = LO ? p.omega_lo + h * p.oms : nullptr;
+  const float* phase = GEN ? p.phase + h * p.phs : p.phase;
+  const bf16x8* omt = GEN ? p.omt + h * p.omt_hs : p.omt;
+  asm volatile("" : "+s"(omega), "+s"(omega_lo), "+s"(phase), "+s"(omt));
+  const float itau = GEN ? head_inv_tau(p, h) : p.inv_tau;
+  const bool renorm = GEN ? !p.no_renorm : true;
+  // per token of the half: 1 / (n + 1e-8) and (phi . dphi) / n (without renormalisation dphi~ = dphi)
+  float inv_n[2] = {1.f, 1.f}, rd_n[2] = {0.f, 0.f};
+  if (renorm) {  // uniform over the workgroup
+    float rd[2] = {0.f, 0.f};
 #pragma unroll
-  for (int ft = 0; ft < NFT; ++ft)
+    for (int ft = 0; ft < NFT; ++ft)
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int tok = 16 * (2 * hm + u) + (lane & 15);
+        const f32x4 ph = ld4_t(phi + (size_t)tok * D + fb + 16 * ft + 4 * (lane >> 4));
+        rd[u] += ph[0] * acc[ft][u][0] + ph[1] * acc[ft][u][1] + ph[2] * acc[ft][u][2] + ph[3] * acc[ft][u][3];
+      }
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const float v = sum_col4(rd[u]);
+      if (lane < 16) s_rd[w][16 * (2 * hm + u) + lane] = v;
+    }
+    __syncthreads();
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       const int tok = 16 * (2 * hm + u) + (lane & 15);
-      const f32x4 ph = ld4_t(phi + (size_t)tok * D + fb + 16 * ft + 4 * (lane >> 4));
-      rd[u] += ph[0] * acc[ft][u][0] + ph[1] * acc[ft][u][1] + ph[2] * acc[ft][u][2] + ph[3] * acc[ft][u][3];
+      inv_n[u] = 1.f / (nrm[tok] + 1e-8f);
+      float rs = s_rd[0][tok];
+#pragma unroll
+      for (int v = 1; v < NW; ++v) rs += s_rd[v][tok];
+      rd_n[u] = rs / nrm[tok];
     }
-#pragma unroll
-  for (int u = 0; u < 2; ++u) {
-    const float v = sum_col4(rd[u]);
-    if (lane < 16) s_rd[w][16 * (2 * hm + u) + lane] = v;
   }
-  __syncthreads();
   const float amp = sqrtf(2.f / D);
-  // per token of the half: 1 / (n + 1e-8) and (phi . dphi) / n
-  float inv_n[2], rd_n[2];
-#pragma unroll
-  for (int u = 0; u < 2; ++u) {
-    const int tok = 16 * (2 * hm + u) + (lane & 15);
-    inv_n[u] = 1.f / (nrm[tok] + 1e-8f);
-    float rs = s_rd[0][tok];
-#pragma unroll
-    for (int v = 1; v < NW; ++v) rs += s_rd[v][tok];
-    rd_n[u] = rs / nrm[tok];
-  }
   typename P::frag xb[2][2];
 #pragma unroll
   for (int u = 0; u < 2; ++u)
@@ -756,6 +793,7 @@ __device__ __forceinline__ void lift_backward_half(const Params& p, const typena
     for (int jb = 0; jb < 2; ++jb) xb[u][jb] = P::from_f32(frag_rows_plain(xh, LD, 16 * (2 * hm + u), 32 * jb, lane));
   typename P::frag on0 = omega_frag<P>(omega, fb, 0, lane), on1 = omega_frag<P>(omega, fb, 32, lane);
   f32x4 phn = *reinterpret_cast<const f32x4*>(phase + fb + 4 * (lane >> 4));
+  float dsv = 0.f;  // sum of dL/d(angle) * (Omega x^) over this lane's elements: dL/d(1/tau)
 #pragma unroll
   for (int ft = 0; ft < NFT; ++ft) {
     const int f0 = fb + 16 * ft;
@@ -766,18 +804,28 @@ __device__ __forceinline__ void lift_backward_half(const Params& p, const typena
       on1 = omega_frag<P>(omega, f0 + 16, 32, lane);
       phn = *reinterpret_cast<const f32x4*>(phase + f0 + 16 + 4 * (lane >> 4));
     }
+    typename P::frag l0{}, l1{};
+    if constexpr (LO) {
+      l0 = omega_frag<P>(omega_lo, f0, 0, lane);
+      l1 = omega_frag<P>(omega_lo, f0, 32, lane);
+    }
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
-      const f32x4 sv = P::mma(P::mma(zero4(), o0, xb[u][0]), o1, xb[u][1]);
-      const f32x4 ph = ld4_t(phi + (size_t)(16 * (2 * hm + u) + (lane & 15)) * D + f0 + 4 * (lane >> 4));
+      f32x4 sv = P::mma(P::mma(zero4(), o0, xb[u][0]), o1, xb[u][1]);
+      if constexpr (LO) sv = P::mma(P::mma(sv, l0, xb[u][0]), l1, xb[u][1]);
+      f32x4 ph = zero4();
+      if (renorm) ph = ld4_t(phi + (size_t)(16 * (2 * hm + u) + (lane & 15)) * D + f0 + 4 * (lane >> 4));
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const float dphit = acc[ft][u][i] * inv_n[u] - ph[i] * rd_n[u];
-        acc[ft][u][i] = -amp * sin_rad(sv[i] * p.inv_tau + ph4[i]) * dphit;
+        const float da = -amp * sin_rad(sv[i] * itau + ph4[i]) * dphit;
+        acc[ft][u][i] = da;
+        if constexpr (GEN) dsv += da * sv[i];
       }
     }
     __builtin_amdgcn_sched_barrier(0);
   }
+  dit += dsv;
   f32x4 d[4][2];
 #pragma unroll
   for (int a = 0; a < 4; ++a)
@@ -788,11 +836,20 @@ __device__ __forceinline__ void lift_backward_half(const Params& p, const typena
     typename P::frag ob[4];
 #pragma unroll
     for (int a = 0; a < 4; ++a) ob[a] = bf16_frag<P>(omt[(a * 16 + fb / 32 + jj) * 64 + lane]);
+    typename P::frag bs[2];
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
-      const typename P::frag bs = P::from_f32(pair_to8(acc[2 * jj][u], acc[2 * jj + 1][u]));
+      bs[u] = P::from_f32(pair_to8(acc[2 * jj][u], acc[2 * jj + 1][u]));
 #pragma unroll
-      for (int a = 0; a < 4; ++a) d[a][u] = P::mma(d[a][u], ob[a], bs);
+      for (int a = 0; a < 4; ++a) d[a][u] = P::mma(d[a][u], ob[a], bs[u]);
+    }
+    if constexpr (LO) {  // dx^ through the low parts of Omega (their table follows the head's)
+#pragma unroll
+      for (int a = 0; a < 4; ++a) ob[a] = bf16_frag<P>(omt[OMT_ENTRIES + (a * 16 + fb / 32 + jj) * 64 + lane]);
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int a = 0; a < 4; ++a) d[a][u] = P::mma(d[a][u], ob[a], bs[u]);
     }
     __builtin_amdgcn_sched_barrier(0);
   }
@@ -822,12 +879,12 @@ __device__ __forceinline__ void lift_backward_half(const Params& p, const typena
 // written for tokens before T.
 template <typename InT>
 __device__ __forceinline__ void write_dx(const Params& p, const InT* x, int64_t xbase, float* out, int64_t obase,
-                                         const float* dx, int r, int c0, bool valid) {
+                                         const float* dx, int r, int c0, bool valid, float itau) {
   float part[16];
   const float nrm = load_x_part<InT>(x, xbase, valid, p.normalize, part);
   float g[16];
 #pragma unroll
-  for (int e = 0; e < 16; ++e) g[e] = p.inv_tau * dx[r * LD + c0 + e];
+  for (int e = 0; e < 16; ++e) g[e] = itau * dx[r * LD + c0 + e];
   if (p.normalize) {
     float dot = 0.f;
 #pragma unroll
@@ -944,8 +1001,9 @@ __global__ void __launch_bounds__(64 * GRAD_WAVES) bwd_grad_kernel(Params p) {
         const bool valid = t0 + ri < p.T;
         if (valid) p.dv[b * p.dvs0 + (t0 + ri) * p.dvs1 + h * p.dvs2 + cj] = s_beta[ri] * td[i];
         dbp[i] += bV[ri * LD + cj] * td[i];
-        ts += bT[ri * LD + cj] * dtp[i];
-        dT[nn][i] = bj * (e1[i] + gj * dtp[i]);
+        // the linear rule's T = I and Tp = 0 are constants: no gradient flows through them
+        ts += p.linear ? 0.f : bT[ri * LD + cj] * dtp[i];
+        dT[nn][i] = p.linear ? 0.f : bj * (e1[i] + gj * dtp[i]);
         if (cj < ri) {
           const float pb = dp[i] * rec[Rec::P + ri * C + cj];
           rowp[i] += pb;
@@ -1149,10 +1207,10 @@ __global__ void __launch_bounds__(64 * GRAD_WAVES) bwd_grad_kernel(Params p) {
 // ---------------------------------------------------------------------------------------------- dx
 // One of the two passes of the dx kernel (NW waves, each 512 / NW features): WHICH 1 (k: dK^T and the
 // lift backward of k) or 0 (q).  The first four waves load the input rows and write dx.
-template <class P, typename InT, int WHICH, int NW>
+template <class P, typename InT, int WHICH, int NW, bool LO, bool GEN>
 __device__ __forceinline__ void dx_pass(const Params& p, const float* rec, const typename P::frag* bop, float* bT,
                                         float* bDX, float* s_n, float (*s_rdp)[C], int64_t b, int64_t h, int64_t t0,
-                                        int tid, int w, int lane, int r, int c0, bool rvalid) {
+                                        int tid, int w, int lane, int r, int c0, bool rvalid, float& dit) {
   constexpr int which = WHICH;
   constexpr int NFT = 32 / NW;  // 16-feature tiles per wave
   const InT* x = reinterpret_cast<const InT*>(which == 0 ? p.q : p.k);
@@ -1228,14 +1286,16 @@ __device__ __forceinline__ void dx_pass(const Params& p, const float* rec, const
         __builtin_amdgcn_sched_barrier(0);
       }
     }
-    lift_backward_half<P, NW>(p, feat<P>(rec_h, which == 0 ? Rec::Q : Rec::K), s_n, s_rdp, bT, bDX, acc, hm, w, lane);
+    lift_backward_half<P, NW, LO, GEN>(p, feat<P>(rec_h, which == 0 ? Rec::Q : Rec::K), s_n, s_rdp, bT, bDX, acc,
+                                       hm, w, lane, h, dit);
   }
   __syncthreads();
   if (tid < 256) {
+    const float itau = GEN ? head_inv_tau(p, h) : p.inv_tau;
     if (which == 0) {
-      write_dx<InT>(p, x, xb, p.dq, b * p.dqs0 + (t0 + r) * p.dqs1 + h * p.dqs2 + c0, bDX, r, c0, rvalid);
+      write_dx<InT>(p, x, xb, p.dq, b * p.dqs0 + (t0 + r) * p.dqs1 + h * p.dqs2 + c0, bDX, r, c0, rvalid, itau);
     } else {
-      write_dx<InT>(p, x, xb, p.dk, b * p.dks0 + (t0 + r) * p.dks1 + h * p.dks2 + c0, bDX, r, c0, rvalid);
+      write_dx<InT>(p, x, xb, p.dk, b * p.dks0 + (t0 + r) * p.dks1 + h * p.dks2 + c0, bDX, r, c0, rvalid, itau);
     }
   }
   __syncthreads();
@@ -1247,11 +1307,11 @@ __device__ __forceinline__ void dx_pass(const Params& p, const float* rec, const
 // through the record; LDS holds only the input rows and dx^ (36 KB).  Eight waves (64 features each)
 // halve each wave's accumulators and loops, so that two waves share each SIMD.
 constexpr int DX_WAVES = 8;
-template <class P, typename InT>
+template <class P, typename InT, bool LO, bool GEN>
 __global__ void __launch_bounds__(64 * DX_WAVES) bwd_dx_kernel(Params p) {
   __shared__ __attribute__((aligned(16))) float bT[C * LD];   // normalised k / q rows
   __shared__ __attribute__((aligned(16))) float bDX[C * LD];  // dx^ of k / q
-  __shared__ float s_n[C], s_rdp[DX_WAVES][C];
+  __shared__ float s_n[C], s_rdp[DX_WAVES][C], s_dit[DX_WAVES];
 
   const int64_t h = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x, lane = tid & 63;
@@ -1262,8 +1322,21 @@ __global__ void __launch_bounds__(64 * DX_WAVES) bwd_dx_kernel(Params p) {
   const bool rvalid = t0 + r < p.T;
   const typename P::frag* bop = reinterpret_cast<const typename P::frag*>(rec + Rec::KXF);
 
-  dx_pass<P, InT, 1, DX_WAVES>(p, rec, bop, bT, bDX, s_n, s_rdp, b, h, t0, tid, w, lane, r, c0, rvalid);
-  dx_pass<P, InT, 0, DX_WAVES>(p, rec, bop, bT, bDX, s_n, s_rdp, b, h, t0, tid, w, lane, r, c0, rvalid);
+  float dit = 0.f;  // this lane's share of dL/d(1/tau) over k, then q
+  dx_pass<P, InT, 1, DX_WAVES, LO, GEN>(p, rec, bop, bT, bDX, s_n, s_rdp, b, h, t0, tid, w, lane, r, c0, rvalid, dit);
+  dx_pass<P, InT, 0, DX_WAVES, LO, GEN>(p, rec, bop, bT, bDX, s_n, s_rdp, b, h, t0, tid, w, lane, r, c0, rvalid, dit);
+  if (GEN && p.dit) {  // fixed order: lanes by a shuffle tree, then the waves in order
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) dit += __shfl_xor(dit, o);
+    if (lane == 0) s_dit[w] = dit;
+    __syncthreads();
+    if (tid == 0) {
+      float t = s_dit[0];
+#pragma unroll
+      for (int v = 1; v < DX_WAVES; ++v) t += s_dit[v];
+      p.dit[(b * p.H + h) * p.nch + p.c0 + blockIdx.x] = t;
+    }
+  }
 }
 
 }  // namespace bwd
@@ -1271,9 +1344,8 @@ __global__ void __launch_bounds__(64 * DX_WAVES) bwd_dx_kernel(Params p) {
 using namespace bwd;
 
 static bool bwd_supported(const kdn_scan_args* f) {
-  return f->d_k == DK && f->D == D && f->d_v == DV && f->rule == 0 && f->feature_mode == 0 && !f->omega_lo &&
-         f->omega_head_stride == 0 && f->phase_head_stride == 0 && !f->inv_tau_head && !f->no_renorm &&
-         !f->cu_seqlens && !f->state_slots;
+  return f->d_k == DK && f->D == D && f->d_v == DV && (f->rule == 0 || f->rule == 1) && f->feature_mode == 0 &&
+         f->omega_head_stride >= 0 && f->phase_head_stride >= 0 && !f->cu_seqlens && !f->state_slots;
 }
 
 static int bwd_check(const kdn_scan_bwd_args* a) {
@@ -1298,6 +1370,10 @@ static int bwd_check(const kdn_scan_bwd_args* a) {
         ((f->v_stride[i] * (int64_t)isz) % 16) != 0)
       return KDN_ERR_MISALIGNED;
   if (!aligned(f->omega_bf16, 16) || !aligned(f->phase, 16)) return KDN_ERR_MISALIGNED;
+  // per-head Omega rows and phases stay 16-byte aligned (Omega fragments and phases are vector loads)
+  if ((f->omega_lo && !aligned(f->omega_lo, 16)) || (f->omega_head_stride * 2) % 16 != 0 ||
+      (f->phase_head_stride * 4) % 16 != 0 || (a->dinv_tau && !aligned(a->dinv_tau, 4)))
+    return KDN_ERR_MISALIGNED;
   if (!aligned(a->dy, 4) || !aligned(a->dq, 4) || !aligned(a->dk, 4) || !aligned(a->dv, 4) || !aligned(a->dbeta, 4))
     return KDN_ERR_MISALIGNED;
   return KDN_OK;
@@ -1319,13 +1395,13 @@ static int64_t bwd_chunks(const kdn_scan_args* f) { return (f->T + C - 1) / C; }
 struct BwdLayout {
   int64_t seg, nsegs;
   int nbuf, nfb;
-  size_t rec_buf, state_bytes, ckpt_off, carry_off, fwd_off, fwd_buf, omt_off, total;
+  size_t rec_buf, state_bytes, ckpt_off, carry_off, fwd_off, fwd_buf, omt_off, dit_off, total;
 };
 
 // Default segment: the largest power of two from 4 to 64 chunks whose records fit 1.5 GiB.
 constexpr size_t BWD_SEGMENT_BUDGET = (size_t)1536 << 20;
 
-static BwdLayout bwd_layout(const kdn_scan_args* f) {
+static BwdLayout bwd_layout(const kdn_scan_args* f, bool want_dit) {
   BwdLayout L;
   const int64_t nch = bwd_chunks(f), heads = f->B * f->H;
   const size_t per_chunk = (size_t)heads * Rec::floats * sizeof(float);
@@ -1348,31 +1424,40 @@ static BwdLayout bwd_layout(const kdn_scan_args* f) {
   L.fwd_off = L.carry_off + (L.nsegs > 1 ? L.state_bytes : 0);
   L.fwd_buf = L.nfb > 0 ? (scan_checkpoint_buffer_bytes(f, seg) + 255) / 256 * 256 : 0;
   L.omt_off = L.fwd_off + (size_t)L.nfb * L.fwd_buf;
-  L.total = L.omt_off + OMT_BYTES;
+  // one Omega^T table, or one per head; twice with low parts
+  const size_t tables = (f->omega_head_stride ? (size_t)f->H : 1) * (f->omega_lo ? 2 : 1);
+  L.dit_off = L.omt_off + tables * OMT_BYTES;
+  L.total = L.dit_off + (want_dit ? ((size_t)heads * nch * sizeof(float) + 255) / 256 * 256 : 0);
   return L;
 }
 
 extern "C" size_t kdn_scan_bwd_workspace_bytes(const kdn_scan_bwd_args* a) {
   if (bwd_check(a) != KDN_OK) return 0;
-  return bwd_layout(a->fwd).total;
+  return bwd_layout(a->fwd, a->dinv_tau != nullptr).total;
 }
 
 extern "C" int64_t kdn_scan_bwd_segments(const kdn_scan_bwd_args* a, int64_t* segment_chunks) {
   if (bwd_check(a) != KDN_OK) return 0;
-  const BwdLayout L = bwd_layout(a->fwd);
+  const BwdLayout L = bwd_layout(a->fwd, a->dinv_tau != nullptr);
   if (segment_chunks) *segment_chunks = L.seg;
   return L.nsegs;
 }
 
 // Omega^T as A fragments for the gradient kernel's dx^ = ds Omega: fragment (a, jb) lane l slot s holds
 // Omega[32jb + kappa(l, s)][16a + (l & 15)] (a column gather done once per call instead of per chunk).
-__global__ void __launch_bounds__(256) bwd_omega_t_kernel(const __bf16* omega, bf16x8* table) {
+// grid (16, tables' heads, parts): part 0 from Omega (hi), part 1 from its low parts; head y's Omega at
+// y * oms elements, its tables at y * parts * OMT_ENTRIES.
+__global__ void __launch_bounds__(256) bwd_omega_t_kernel(const __bf16* omega, const __bf16* omega_lo, int64_t oms,
+                                                          bf16x8* table) {
   const int idx = blockIdx.x * 256 + threadIdx.x;  // 16 blocks of 256 cover [a 4][jb 16][lane 64]
   const int lane = idx & 63, jb = (idx >> 6) & 15, a = idx >> 10;
+  const int64_t hy = blockIdx.y;
+  const int part = blockIdx.z;
+  const __bf16* src = (part ? omega_lo : omega) + hy * oms;
   bf16x8 v;
 #pragma unroll
-  for (int s = 0; s < 8; ++s) v[s] = omega[(size_t)(32 * jb + kappa(lane, s)) * DK + 16 * a + (lane & 15)];
-  table[idx] = v;
+  for (int s = 0; s < 8; ++s) v[s] = src[(size_t)(32 * jb + kappa(lane, s)) * DK + 16 * a + (lane & 15)];
+  table[(hy * gridDim.z + part) * OMT_ENTRIES + idx] = v;
 }
 
 // The parameters of segment s: its chunks, its record buffer (rotating in processing order, last segment
@@ -1403,17 +1488,40 @@ static Params segment_params(const Params& base, const kdn_scan_bwd_args* a, con
 
 // One launch of segment p: 1 per-chunk recompute, 2 forward carry, 3 reverse carry, 4 gradients, or
 // PH_CARRIES: both carries in one launch.
+// dL/d(1/tau) of head blockIdx.x: the per-(batch, chunk) partials summed in a fixed order (lane-strided
+// sums, then a shuffle tree), so that the result does not depend on the schedule.
+__global__ void __launch_bounds__(64) bwd_dit_reduce_kernel(const float* dit, int64_t B, int64_t H, int64_t nch,
+                                                            float* out) {
+  const int64_t h = blockIdx.x;
+  const int lane = threadIdx.x;
+  float t = 0.f;
+  for (int64_t b = 0; b < B; ++b)
+    for (int64_t c = lane; c < nch; c += 64) t += dit[(b * H + h) * nch + c];
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) t += __shfl_xor(t, o);
+  if (lane == 0) out[h] = t;
+}
+
 constexpr int PH_CARRIES = 5;
 template <class P, typename InT>
 static int segment_phase(const Params& p, int phase, hipStream_t st) {
   const dim3 chunk_grid((unsigned)p.nseg, (unsigned)p.H, (unsigned)p.B);
   const unsigned chain_wgs = (unsigned)(((p.B * p.H + 7) / 8) * 8 * 4);
-  if (phase == 1) hipLaunchKernelGGL((bwd_prep_kernel<P, InT>), chunk_grid, dim3(256), 0, st, p);
+  if (phase == 1) {
+    if (p.omega_lo) hipLaunchKernelGGL((bwd_prep_kernel<P, InT, true>), chunk_grid, dim3(256), 0, st, p);
+    else hipLaunchKernelGGL((bwd_prep_kernel<P, InT, false>), chunk_grid, dim3(256), 0, st, p);
+  }
   if (phase == 2) hipLaunchKernelGGL((bwd_chain_kernel<P, false>), dim3(chain_wgs), dim3(256), 0, st, p);
   if (phase == 3) hipLaunchKernelGGL((bwd_chain_kernel<P, true>), dim3(chain_wgs), dim3(256), 0, st, p);
   if (phase == 4) {
     hipLaunchKernelGGL((bwd_grad_kernel<P, InT>), chunk_grid, dim3(64 * GRAD_WAVES), 0, st, p);
-    hipLaunchKernelGGL((bwd_dx_kernel<P, InT>), chunk_grid, dim3(64 * DX_WAVES), 0, st, p);
+    const bool gen = p.omega_lo || p.oms || p.phs || p.inv_tau_head || p.no_renorm || p.dit;
+    if (p.omega_lo) hipLaunchKernelGGL((bwd_dx_kernel<P, InT, true, true>), chunk_grid, dim3(64 * DX_WAVES), 0, st, p);
+    else if (gen) hipLaunchKernelGGL((bwd_dx_kernel<P, InT, false, true>), chunk_grid, dim3(64 * DX_WAVES), 0, st, p);
+    else hipLaunchKernelGGL((bwd_dx_kernel<P, InT, false, false>), chunk_grid, dim3(64 * DX_WAVES), 0, st, p);
+    // segment 0 is the last one processed: every partial of dL/d(1/tau) is written
+    if (p.dit && p.c0 == 0)
+      hipLaunchKernelGGL(bwd_dit_reduce_kernel, dim3((unsigned)p.H), dim3(64), 0, st, p.dit, p.B, p.H, p.nch, p.dinv_tau);
   }
   if (phase == PH_CARRIES) hipLaunchKernelGGL((bwd_chains_kernel<P>), dim3(2 * chain_wgs), dim3(256), 0, st, p, chain_wgs);
   return launch_status();
@@ -1422,7 +1530,9 @@ static int segment_phase(const Params& p, int phase, hipStream_t st) {
 // The start of a call: the Omega^T table, then the checkpoint pass (its prep kernels on aux if given).
 static int bwd_start(const kdn_scan_bwd_args* a, const Params& base, const BwdLayout& L, hipStream_t st,
                      hipStream_t aux) {
-  hipLaunchKernelGGL(bwd_omega_t_kernel, dim3(16), dim3(256), 0, st, base.omega, const_cast<bf16x8*>(base.omt));
+  const unsigned heads = base.oms ? (unsigned)base.H : 1u, parts = base.omega_lo ? 2u : 1u;
+  hipLaunchKernelGGL(bwd_omega_t_kernel, dim3(16, heads, parts), dim3(256), 0, st, base.omega, base.omega_lo, base.oms,
+                     const_cast<bf16x8*>(base.omt));
   const int rc = launch_status();
   if (rc != KDN_OK) return rc;
   unsigned char* ws = static_cast<unsigned char*>(a->workspace);
@@ -1489,7 +1599,7 @@ static int bwd_params(const kdn_scan_bwd_args* a, Params& p, BwdLayout& L) {
   const int rc = bwd_check(a);
   if (rc != KDN_OK) return rc;
   const kdn_scan_args* f = a->fwd;
-  L = bwd_layout(f);
+  L = bwd_layout(f, a->dinv_tau != nullptr);
   if (!a->workspace || a->workspace_bytes < L.total) return KDN_ERR_WORKSPACE_TOO_SMALL;
   if (!aligned(a->workspace, 256)) return KDN_ERR_MISALIGNED;
   if (f->B > 65535 || f->H > 65535 || L.seg > 0x7fffffff) return KDN_ERR_UNSUPPORTED;
@@ -1515,6 +1625,14 @@ static int bwd_params(const kdn_scan_bwd_args* a, Params& p, BwdLayout& L) {
   p.gout = a->d_initial_state;
   p.gos0 = a->dinit_stride[0]; p.gos1 = a->dinit_stride[1]; p.gos2 = a->dinit_stride[2]; p.gos3 = a->dinit_stride[3];
   p.omt = reinterpret_cast<const bf16x8*>(static_cast<unsigned char*>(a->workspace) + L.omt_off);
+  p.omega_lo = reinterpret_cast<const __bf16*>(f->omega_lo);
+  p.oms = f->omega_head_stride; p.phs = f->phase_head_stride;
+  p.inv_tau_head = f->inv_tau_head;
+  p.no_renorm = f->no_renorm ? 1 : 0;
+  p.linear = f->rule == 1 ? 1 : 0;
+  p.omt_hs = f->omega_head_stride ? (f->omega_lo ? 2 : 1) * OMT_ENTRIES : 0;
+  p.dinv_tau = a->dinv_tau;
+  p.dit = a->dinv_tau ? reinterpret_cast<float*>(static_cast<unsigned char*>(a->workspace) + L.dit_off) : nullptr;
   return KDN_OK;
 }
 

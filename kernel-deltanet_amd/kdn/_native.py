@@ -135,6 +135,7 @@ class ScanBwdArgs(ctypes.Structure):
         ("ddecay", ctypes.c_void_p), ("ddecay_stride", _i64x3),
         ("d_initial_state", ctypes.c_void_p), ("dinit_stride", _i64x4),
         ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_size_t),
+        ("dinv_tau", ctypes.c_void_p),
     ]
 
 

@@ -347,13 +347,17 @@ class ScanBackwardPlan:
 
     Same layouts as `scan`: q, k (B, T, H, 64), v and dy (B, T, H, 64), beta and decay (B, T, H), states
     (B, H, 512, 64); dL/dy = dy, dL/d(final state) = d_final_state (None: zero).  `outputs` holds the
-    float32 gradients (dq, dk, dv, dbeta, ddecay or None, d_initial_state or None).  The structured lift
-    with one shared Omega and the delta rule only.  segment_chunks (0: the library's default) sets the
-    backward's segment length in 64-token chunks; `segments` and `segment_chunks` hold the schedule."""
+    float32 gradients (dq, dk, dv, dbeta, ddecay or None, d_initial_state or None).  The feature map is
+    one shared Omega (omega_bf16, phase, inv_tau) or `features` (per-head Omega with low parts, phases and
+    1/tau, no renormalisation; not pre-lifted features); `rule` is RULE_DELTA or RULE_LINEAR.  With
+    need_dinv_tau, `dinv_tau` holds dL/d(1/tau) per head (H,) in float32.  segment_chunks (0: the
+    library's default) sets the backward's segment length in 64-token chunks; `segments` and
+    `segment_chunks` hold the schedule."""
 
     def __init__(self, q, k, v, beta, decay, omega_bf16, phase, inv_tau, dy, d_final_state=None,
                  normalize: bool = False, initial_state=None, need_ddecay: bool = True, need_dinit: bool = True,
-                 workspace: Optional[torch.Tensor] = None, segment_chunks: int = 0):
+                 workspace: Optional[torch.Tensor] = None, segment_chunks: int = 0,
+                 features: Optional[FeatureMap] = None, rule: int = RULE_DELTA, need_dinv_tau: bool = False):
         for t, nm in ((q, "q"), (k, "k"), (v, "v"), (beta, "beta"), (dy, "dy")):
             require_device(t, f"scan_backward: {nm}")
         dev = q.device
@@ -370,7 +374,9 @@ class ScanBackwardPlan:
         dy = _last_contig(dy.to(torch.float32))
         B, T, H, d_k = q.shape
         d_v = v.shape[-1]
-        fm = _features_on(FeatureMap(omega_bf16, phase), dev, H)
+        fm = _features_on(features if features is not None else FeatureMap(omega_bf16, phase), dev, H)
+        if fm.lifted:
+            raise ValueError("scan_backward: pre-lifted features have no backward here")
         D = fm.dim(q)
         if initial_state is not None:
             if tuple(initial_state.shape) != (B, H, D, d_v):
@@ -384,7 +390,7 @@ class ScanBackwardPlan:
         if segment_chunks < 0:
             raise ValueError("scan_backward: segment_chunks must be >= 0")
         self._fa = scan_args(q, k, v, beta, decay, None, None, inv_tau, normalize, initial_state, unused, dy, None,
-                             segment_chunks, fm)
+                             segment_chunks, fm, rule)
         f32 = dict(device=dev, dtype=torch.float32)
         dq, dk = torch.empty(B, T, H, d_k, **f32), torch.empty(B, T, H, d_k, **f32)
         dv, dbeta = torch.empty(B, T, H, d_v, **f32), torch.empty(B, T, H, **f32)
@@ -403,10 +409,13 @@ class ScanBackwardPlan:
             a.ddecay, a.ddecay_stride = ddecay.data_ptr(), N._i64x3(*ddecay.stride())
         if dinit is not None:
             a.d_initial_state, a.dinit_stride = dinit.data_ptr(), N._i64x4(*dinit.stride())
+        self.dinv_tau = torch.empty(H, **f32) if need_dinv_tau else None
+        if self.dinv_tau is not None:
+            a.dinv_tau = self.dinv_tau.data_ptr()
         nbytes = N.lib().kdn_scan_bwd_workspace_bytes(ctypes.byref(a))
         if nbytes == 0:
             raise ValueError("scan_backward: unsupported request (kdn_scan_bwd_workspace_bytes returned 0; the "
-                             "backward covers d_k = 64, D = 512, d_v = 64 with the shared structured lift)")
+                             "backward covers d_k = 64, D = 512, d_v = 64 with lifted features)")
         if workspace is None or workspace.numel() * workspace.element_size() < nbytes:
             workspace = torch.empty(nbytes, dtype=torch.uint8, device=dev)
         a.workspace, a.workspace_bytes = workspace.data_ptr(), workspace.numel() * workspace.element_size()
@@ -416,7 +425,7 @@ class ScanBackwardPlan:
         self.args, self.device, self.workspace = a, dev, workspace
         self.outputs = (dq, dk, dv, dbeta, ddecay, dinit)
         self.shape = (B, T, H)
-        self._keep = (q, k, v, beta, decay, dy, d_final_state, initial_state, unused, fm.keep())
+        self._keep = (q, k, v, beta, decay, dy, d_final_state, initial_state, unused, fm.keep(), self.dinv_tau)
 
     def _st(self, stream):
         return stream if stream is not None else torch.cuda.current_stream(self.device)
@@ -505,6 +514,54 @@ def scan_autograd(q, k, v, beta, decay, omega_bf16, phase, inv_tau, normalize: b
         raise ValueError(f"scan with gradients: the backward supports d_k = 64, D = 512, d_v = 64 (got d_k = {d_k}, "
                          f"D = {D}, d_v = {d_v}); run the forward under torch.no_grad() or detach the inputs")
     return _Scan.apply(q, k, v, beta, decay, initial_state, omega_bf16, phase, inv_tau, normalize)
+
+
+class _FeatureScan(torch.autograd.Function):
+    """`scan` with a per-head feature map and its backward (kdn_delta_scan_bwd): gradients flow to q, k,
+    v, beta, decay, initial_state and the per-head 1/tau; Omega, its low parts and the phases are
+    constants (buffers on the reference's surfaces)."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, beta, decay, initial_state, inv_tau_head, omega, omega_lo, phase, no_renorm,
+                normalize, rule):
+        fm = FeatureMap(omega=omega, phase=phase, omega_lo=omega_lo, inv_tau_head=inv_tau_head.detach(),
+                        no_renorm=no_renorm)
+        y, final = scan(q, k, v, beta, decay, None, None, 1.0, normalize=normalize, initial_state=initial_state,
+                        features=fm, rule=rule)
+        ctx.save_for_backward(q, k, v, beta, decay, initial_state, inv_tau_head, omega, omega_lo, phase)
+        ctx.flags = (no_renorm, normalize, rule)
+        return y, final
+
+    @staticmethod
+    def backward(ctx, dy, dfinal):
+        q, k, v, beta, decay, init, itau, omega, omega_lo, phase = ctx.saved_tensors
+        no_renorm, normalize, rule = ctx.flags
+        need = ctx.needs_input_grad
+        fm = FeatureMap(omega=omega, phase=phase, omega_lo=omega_lo, inv_tau_head=itau.detach(), no_renorm=no_renorm)
+        plan = ScanBackwardPlan(q, k, v, beta, decay, None, None, 1.0, dy, dfinal, normalize=normalize,
+                                initial_state=init, need_ddecay=decay is not None and bool(need[4]),
+                                need_dinit=init is not None and bool(need[5]), features=fm, rule=rule,
+                                need_dinv_tau=bool(need[6]))
+        dq, dk, dv, dbeta, ddecay, dinit = plan.run()
+        ditau = None if plan.dinv_tau is None else plan.dinv_tau.to(itau.dtype)
+        return (dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), dbeta.to(beta.dtype),
+                None if ddecay is None else ddecay.to(decay.dtype),
+                None if dinit is None else dinit.to(init.dtype), ditau, None, None, None, None, None, None)
+
+
+def feature_scan_autograd(q, k, v, beta, decay, omega, phase, inv_tau_head, omega_lo=None, no_renorm: bool = False,
+                          normalize: bool = False, initial_state=None, rule: int = RULE_DELTA
+                          ) -> Tuple[torch.Tensor, torch.Tensor]:
+    """`scan` over (B, T, H, .) views with a per-head feature map, recorded for autograd (gradients through
+    kdn_delta_scan_bwd to q, k, v, beta, decay, initial_state and inv_tau_head (H,)).  omega (H, 512, 64)
+    bf16 with optional bf16 low parts, phase (H, 512), the delta or the linear rule; d_k = 64, D = 512,
+    d_v = 64.  Returns (y (B, T, H, d_v), final_state (B, H, D, d_v))."""
+    d_k, D, d_v = q.shape[-1], omega.shape[-2], v.shape[-1]
+    if (d_k, D, d_v) != (64, 512, 64):
+        raise ValueError(f"scan with gradients: the backward supports d_k = 64, D = 512, d_v = 64 (got d_k = {d_k}, "
+                         f"D = {D}, d_v = {d_v}); run the forward under torch.no_grad() or detach the inputs")
+    return _FeatureScan.apply(q, k, v, beta, decay, initial_state, inv_tau_head, omega, omega_lo, phase,
+                              bool(no_renorm), bool(normalize), int(rule))
 
 
 def _features_on(fm: FeatureMap, dev: torch.device, H: int) -> FeatureMap:

@@ -85,8 +85,16 @@ def kernel_deltanet_scan(q, k, v, omega, b_rff, tau, beta, decay, initial_state=
     return y, final
 
 
+def _feature_map(omega, b_rff, inv_tau_head, dev) -> ops.FeatureMap:
+    hi, lo = split_bf16(omega.detach().to(dev))
+    return ops.FeatureMap(omega=hi, phase=b_rff.detach().to(device=dev, dtype=torch.float32), omega_lo=lo,
+                          inv_tau_head=inv_tau_head, no_renorm=True)
+
+
 class FusedKernelDeltaNetFunction(torch.autograd.Function):
-    """Reference: kernels/kernel_deltanet_fused.py:36-178.  Forward returns (Y, S_final)."""
+    """Reference: kernels/kernel_deltanet_fused.py:36-178.  Forward returns (Y, S_final).  Backward:
+    kdn_delta_scan_bwd with this surface's feature map, gradients for q, k, v, tau, beta and decay
+    (omega and b_rff are buffers of the reference module: no gradient)."""
 
     @staticmethod
     def forward(ctx, q, k, v, omega, b_rff, tau, beta, decay, chunk_size: int = 64):
@@ -94,12 +102,35 @@ class FusedKernelDeltaNetFunction(torch.autograd.Function):
             raise ValueError(f"chunk_size must be positive, got {chunk_size}")
         with torch.no_grad():
             y, final = kernel_deltanet_scan(q, k, v, omega, b_rff, tau, beta, decay)
+        ctx.save_for_backward(q, k, v, omega, b_rff, tau if isinstance(tau, torch.Tensor) else None, beta, decay)
+        ctx.tau = tau
         return y, final.to(k.dtype)
 
     @staticmethod
-    def backward(ctx, *grads):
-        raise NotImplementedError("the backward pass of the delta-rule scan is not implemented on MI355X "
-                                  "(forward/prefill only)")
+    def backward(ctx, dy, dfinal):
+        q, k, v, omega, b_rff, tau_t, beta, decay = ctx.saved_tensors
+        tau = tau_t if tau_t is not None else ctx.tau
+        need = ctx.needs_input_grad
+        B, H, T, _ = q.shape
+        dev = q.device
+        tau_h = _head_vector(tau.detach() if isinstance(tau, torch.Tensor) else tau, H, dev, "tau")
+        fm = _feature_map(omega, b_rff, (1.0 / tau_h).contiguous(), dev)
+        dt = q.dtype
+        plan = ops.ScanBackwardPlan(
+            q.transpose(1, 2), k.to(dt).transpose(1, 2), v.to(dt).transpose(1, 2),
+            beta.to(torch.float32).transpose(1, 2),
+            None if decay is None else decay.to(torch.float32).transpose(1, 2), None, None, 1.0,
+            dy.transpose(1, 2), None if dfinal is None else dfinal.to(torch.float32).transpose(2, 3),
+            normalize=True, need_ddecay=decay is not None and bool(need[7]), need_dinit=False, features=fm,
+            need_dinv_tau=tau_t is not None and bool(need[5]))
+        dq, dk, dv, dbeta, ddecay, _ = plan.run()
+        dtau = None
+        if plan.dinv_tau is not None:
+            g = -plan.dinv_tau / (tau_h * tau_h)  # d(1/tau)/dtau = -1/tau^2
+            dtau = (g.sum() if tau_t.numel() == 1 else g).reshape(tau_t.shape).to(tau_t.dtype)
+        return (dq.transpose(1, 2).to(q.dtype), dk.transpose(1, 2).to(k.dtype), dv.transpose(1, 2).to(v.dtype),
+                None, None, dtau, dbeta.transpose(1, 2).to(beta.dtype),
+                None if ddecay is None else ddecay.transpose(1, 2).to(decay.dtype), None)
 
 
 class FusedKernelDeltaNet(nn.Module):
@@ -154,11 +185,18 @@ class FusedKernelDeltaNet(nn.Module):
         beta = torch.sigmoid(self.w_beta(x))
         decay = torch.sigmoid(self.w_decay(x))
         tau = self.get_tau()
+        if torch.is_grad_enabled():
+            # differentiable end to end: the scan's backward (kdn_delta_scan_bwd) gives q, k, v, beta, decay,
+            # the state and 1/tau their gradients, autograd the rest (projections, softplus of raw_tau)
+            fm = _feature_map(self.omega, self.b_rff, None, x.device)
+            inv_tau = 1.0 / tau.reshape(H).to(torch.float32)
+            init = None if state is None else state.to(device=x.device, dtype=torch.float32).transpose(2, 3)
+            y, final = ops.feature_scan_autograd(q, k, v, beta.to(torch.float32), decay.to(torch.float32), fm.omega,
+                                                 fm.phase, inv_tau, omega_lo=fm.omega_lo, no_renorm=True,
+                                                 normalize=True, initial_state=init)
+            return self.w_out(y.reshape(B, T, self.d_model)), final.transpose(2, 3).to(x.dtype)
         y = torch.empty(B, T, H, dh, device=x.device, dtype=q.dtype)
-        with torch.no_grad():
-            _, final = kernel_deltanet_scan(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2), self.omega,
-                                            self.b_rff, tau, beta.transpose(1, 2), decay.transpose(1, 2),
-                                            initial_state=state, y=y.transpose(1, 2))
-        y, final = ops.forward_only("FusedKernelDeltaNet", (y, final.to(x.dtype)),
-                                    (q, k, v, beta, decay, tau, state))
-        return self.w_out(y.view(B, T, self.d_model)), final
+        _, final = kernel_deltanet_scan(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2), self.omega,
+                                        self.b_rff, tau, beta.transpose(1, 2), decay.transpose(1, 2),
+                                        initial_state=state, y=y.transpose(1, 2))
+        return self.w_out(y.view(B, T, self.d_model)), final.to(x.dtype)

@@ -144,23 +144,32 @@ class KernelDeltaNetLayer(nn.Module):
         v = self.w_v(x).view(B, T, H, dh)
         lam = self.get_decay().reshape(H)
         eta = self.get_eta().reshape(H)
-        y = torch.empty(B, T, H, dh, device=x.device, dtype=q.dtype)
-        final = torch.empty(B, H, dh, D, device=x.device, dtype=torch.float32)
-        with torch.no_grad():
-            init = None
-            if state is not None:
-                if tuple(state.shape) != (B, H, dh, D):
-                    raise ValueError(f"state must be (B, H, d_head, rkhs_dim) = {(B, H, dh, D)}")
-                init = state.to(device=x.device, dtype=torch.float32).transpose(2, 3)
+        if state is not None and tuple(state.shape) != (B, H, dh, D):
+            raise ValueError(f"state must be (B, H, d_head, rkhs_dim) = {(B, H, dh, D)}")
+        if torch.is_grad_enabled():
+            # differentiable end to end: the scan's backward (kdn_delta_scan_bwd, linear rule) gives q, k, v,
+            # the per-token eta and lambda (summed over the stride-0 views by autograd), the state and
+            # 1/tau_h = sqrt(2 gamma_h) their gradients; autograd the rest (projections, log_gamma, logits)
+            fm = self.kernel.feature_map(x.device)
+            inv_tau = torch.sqrt(2.0 * torch.exp(self.kernel.log_gamma.to(device=x.device, dtype=torch.float32)))
             beta = eta.to(torch.float32).view(1, 1, H).expand(B, T, H)
             decay = lam.to(torch.float32).view(1, 1, H).expand(B, T, H)
-            ops.scan(q, k, v, beta, decay, None, None, 1.0, normalize=True, initial_state=init,
-                     final_state=final.transpose(2, 3), y=y, features=self.kernel.feature_map(x.device),
-                     rule=ops.RULE_LINEAR)
-        y, final = ops.forward_only("KernelDeltaNetLayer", (y, final.to(x.dtype)),
-                                    (q, k, v, lam, eta, self.kernel.log_gamma, state))
+            init = None if state is None else state.to(device=x.device, dtype=torch.float32).transpose(2, 3)
+            y, final = ops.feature_scan_autograd(q, k, v, beta, decay, fm.omega, fm.phase, inv_tau,
+                                                 omega_lo=fm.omega_lo, no_renorm=True, normalize=True,
+                                                 initial_state=init, rule=ops.RULE_LINEAR)
+            out = self.w_out(y.reshape(B, T, d_in))
+            return out, (final.transpose(2, 3).to(x.dtype) if step_mode else None)
+        y = torch.empty(B, T, H, dh, device=x.device, dtype=q.dtype)
+        final = torch.empty(B, H, dh, D, device=x.device, dtype=torch.float32)
+        init = None if state is None else state.to(device=x.device, dtype=torch.float32).transpose(2, 3)
+        beta = eta.to(torch.float32).view(1, 1, H).expand(B, T, H)
+        decay = lam.to(torch.float32).view(1, 1, H).expand(B, T, H)
+        ops.scan(q, k, v, beta, decay, None, None, 1.0, normalize=True, initial_state=init,
+                 final_state=final.transpose(2, 3), y=y, features=self.kernel.feature_map(x.device),
+                 rule=ops.RULE_LINEAR)
         out = self.w_out(y.view(B, T, d_in))
-        return out, (final if step_mode else None)
+        return out, (final.to(x.dtype) if step_mode else None)
 
 
 # the reference's backwards-compatibility alias (:147)

@@ -8,6 +8,11 @@
   linear_recurrence <- recurrent_step of the P4 layer, core/chunked_scan.py:145-186 (no erasure term):
                        y_t = S_{t-1} phi_q(t);  S_t = lambda_t S_{t-1} + beta_t v_t phi_k(t)^T
   linear_chunked    <- chunked_affine_scan, core/chunked_scan.py:48-143 (per-head constant lambda, eta)
+  *_torch           <- the same definitions on torch tensors, for autograd (the gradient oracle):
+                       token_recurrence_torch, delta_rule_torch (lift of kernels/fwht.py:122-131),
+                       linear_recurrence_torch, rff_features_torch (the per-head feature map of the P2
+                       module, kernels/kernel_deltanet_fused.py:238-251, and of the P4 layer's shifted
+                       [cos, sin] form, core/rkhs_features.py:107-131)
 """
 from __future__ import annotations
 
@@ -63,6 +68,39 @@ def token_recurrence_torch(phi_q: torch.Tensor, phi_k: torch.Tensor, v: torch.Te
         b = beta[:, t, None, None]
         S = lam * (S - b * s_phi[:, :, None] * phi_k[:, t, None, :]) + b * v[:, t, :, None] * phi_k[:, t, None, :]
     return torch.stack(ys, 1), S
+
+
+def linear_recurrence_torch(phi_q: torch.Tensor, phi_k: torch.Tensor, v: torch.Tensor, beta: torch.Tensor,
+                            decay: Optional[torch.Tensor] = None, S0: Optional[torch.Tensor] = None
+                            ) -> Tuple[torch.Tensor, torch.Tensor]:
+    """linear_recurrence on torch tensors (core/chunked_scan.py:145-186 with eta -> beta_t, decay ->
+    lambda_t, lambda clamped to [1e-5, 1] as the scan clamps log lambda), for autograd.  Shapes as
+    token_recurrence; returns (Y (B, T, d_v), S (B, d_v, D))."""
+    B, T, D = phi_k.shape
+    dv = v.shape[-1]
+    S = torch.zeros(B, dv, D, dtype=phi_k.dtype) if S0 is None else S0
+    ys = []
+    for t in range(T):
+        ys.append(torch.einsum("bvd,bd->bv", S, phi_q[:, t]))
+        lam = 1.0 if decay is None else decay[:, t].clamp(1e-5, 1.0)[:, None, None]
+        S = lam * S + beta[:, t, None, None] * v[:, t, :, None] * phi_k[:, t, None, :]
+    return torch.stack(ys, 1), S
+
+
+def rff_features_torch(x: torch.Tensor, omega: torch.Tensor, phase: torch.Tensor, inv_tau: torch.Tensor,
+                       normalize: bool = True, renorm: bool = False) -> torch.Tensor:
+    """oracle.lift.rff_features on torch tensors, with 1/tau as the (differentiable) per-head input:
+    phi = sqrt(2/D) cos(x_hat Omega_h^T inv_tau_h + phase_h), optionally renormalised.
+
+    x (B, H, T, d_k); omega (H, D, d_k); phase (H, D); inv_tau (H,).  Returns (B, H, T, D)."""
+    if normalize:
+        x = F.normalize(x, p=2, dim=-1, eps=1e-6)
+    D = omega.shape[1]
+    ang = torch.einsum("bhtd,hfd->bhtf", x, omega) * inv_tau[None, :, None, None] + phase[None, :, None, :]
+    phi = math.sqrt(2.0 / D) * torch.cos(ang)
+    if renorm:
+        phi = phi / (torch.norm(phi, dim=-1, keepdim=True) + 1e-8)
+    return phi
 
 
 def delta_rule_torch(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, beta: torch.Tensor,

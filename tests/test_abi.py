@@ -62,7 +62,7 @@ def test_args_layout_matches_c(cname, pystruct):
 def test_strerror_and_version(lib):
     for code in (0, -1, -2, -3, -4, -5, -99):
         assert len(lib.kdn_strerror(code)) > 0
-    assert lib.kdn_abi_version() == (1 << 16) | 6
+    assert lib.kdn_abi_version() == (1 << 16) | 7
 
 
 def _args(**kw):
@@ -195,6 +195,20 @@ def test_backward_workspace_and_errors_need_no_device(lib):
     g.fwd = ctypes.addressof(f2)
     assert lib.kdn_scan_bwd_workspace_bytes(ctypes.byref(g)) == 0
     assert lib.kdn_delta_scan_bwd(ctypes.byref(g), None) == -2
+    g.fwd = ctypes.addressof(f)
+    # per-head Omega with low parts (the P2 / P4 feature maps, ABI 1.7): one Omega^T table per head and
+    # part; dL/d(1/tau) adds one fp32 partial per (batch, head, chunk), rounded up to 256 bytes
+    f3 = _fake_ptrs(_args(T=256, H=2, rule=1, no_renorm=1))
+    f3.omega_lo, f3.omega_head_stride, f3.phase_head_stride = 0x7D0000000000, 512 * 64, 512
+    g.fwd = ctypes.addressof(f3)
+    assert lib.kdn_scan_bwd_workspace_bytes(ctypes.byref(g)) == 2 * 4 * 1247232 + 2 * 2 * 65536
+    g.dinv_tau = 0x7C0000000000
+    assert lib.kdn_scan_bwd_workspace_bytes(ctypes.byref(g)) == 2 * 4 * 1247232 + 2 * 2 * 65536 + 256
+    f3.phase_head_stride = 510                                          # per-head phases must stay 16-byte aligned
+    assert lib.kdn_delta_scan_bwd(ctypes.byref(g), None) == -4
+    f3.feature_mode, f3.d_k = 1, 512                                    # pre-lifted features: no backward
+    assert lib.kdn_scan_bwd_workspace_bytes(ctypes.byref(g)) == 0
+    g.dinv_tau = None
     g.fwd = ctypes.addressof(f)
     g.dy = None
     assert lib.kdn_delta_scan_bwd(ctypes.byref(g), None) == -1

@@ -224,10 +224,15 @@ def test_layer_bf16():
 
 
 def test_forward_only_surfaces_raise_on_backward():
-    layer = KernelDeltaNetLayer(128, 2, rkhs_factor=8).to(DEV)
-    out, _ = layer(torch.randn(1, 64, 128, device=DEV))
+    # the pre-lifted (Triton-named) surfaces have no backward: a training step fails loudly instead of
+    # skipping the scan's gradient (the layer and the P2 surfaces differentiate: test_gpu_feature_backward)
+    g = torch.Generator().manual_seed(9)
+    phi = F.normalize(torch.randn(1, 2, 64, 512, generator=g), dim=-1).to(DEV).requires_grad_(True)
+    v = torch.randn(1, 2, 64, 64, generator=g).to(DEV)
+    beta, decay = torch.full((1, 2, 64), 0.5, device=DEV), torch.full((1, 2, 64), 0.99, device=DEV)
+    y = fused_triton_chunk_scan(phi, phi, v, beta, decay)
     with pytest.raises(NotImplementedError):
-        out.sum().backward()
+        y.float().sum().backward()
 
 
 # ------------------------------------------------------------------------------------------------ linear rule
