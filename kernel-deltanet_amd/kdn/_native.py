@@ -10,7 +10,8 @@ import os
 import threading
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "libkdn.so")
+# KDN_LIBRARY selects another build of the same library (the host-sanitized one of the host-path tests)
+LIB_PATH = os.environ.get("KDN_LIBRARY") or os.path.join(_HERE, "libkdn.so")
 
 KDN_OK = 0
 KDN_DTYPE_F32 = 0

@@ -58,5 +58,36 @@ def build_native(verbose: bool = False) -> str:
     return OUT
 
 
+# AddressSanitizer + UndefinedBehaviorSanitizer on the host code only (the C ABI, argument checks,
+# workspace layouts, the slab pool, the schedules); the device code is built as usual.  Every sanitizer
+# flag is behind -Xarch_host: this pool runs no GPU code built with a sanitizer.
+SANITIZE_FLAGS = ["-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fsanitize=undefined",
+                  "-Xarch_host", "-fno-sanitize-recover=undefined", "-Xarch_host", "-fno-omit-frame-pointer"]
+
+
+def asan_runtime() -> str:
+    """The shared ASan runtime of hipcc's clang, which a process must preload to load the sanitized
+    library (empty if it is not installed)."""
+    import glob
+    hits = sorted(glob.glob("/opt/rocm/llvm/lib/clang/*/lib/linux/libclang_rt.asan-x86_64.so"))
+    return hits[-1] if hits else ""
+
+
+def build_host_sanitized(out_dir: str, verbose: bool = False) -> str:
+    """Compile every source with the host code under ASan + UBSan into out_dir/libkdn_hostsan.so (for the
+    host-path tests; not shipped).  Returns the library path."""
+    os.makedirs(out_dir, exist_ok=True)
+    objs = [os.path.join(out_dir, os.path.splitext(s)[0] + ".o") for s in SOURCES]
+    flags = [f"--offload-arch={ARCH}", "-O1", "-std=c++17", "-fPIC", "-Xclang", "-target-feature", "-Xclang",
+             "-packed-fp32-ops"] + SANITIZE_FLAGS
+    cmds = [[hipcc()] + flags + ["-c", "-o", o, os.path.join(CSRC, s)] for s, o in zip(SOURCES, objs)]
+    with ThreadPoolExecutor(max_workers=len(cmds)) as ex:
+        list(ex.map(lambda c: _run(c, verbose), cmds))
+    out = os.path.join(out_dir, "libkdn_hostsan.so")
+    _run([hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-Xarch_host", "-fsanitize=address",
+          "-Xarch_host", "-fsanitize=undefined", "-Xarch_host", "-shared-libasan", "-o", out] + objs, verbose)
+    return out
+
+
 if __name__ == "__main__":
     print(build_native(verbose=True))
