@@ -118,6 +118,16 @@ int kdn_fwht_lift_factored(const void* x, int64_t rows, int64_t x_row_stride, in
                            const float* phase2, float inv_tau, void* out, int64_t out_row_stride, int out_dtype,
                            void* stream);
 
+/* Backward of kdn_fwht_lift_factored (ABI 1.8): dx[r] = (d out[r] / d x[r])^T dout[r] for the same x, Omega
+ * and phase arguments, with dout fp32 rows of 1024 (dout_row_stride) and dx fp32 rows of 128
+ * (dx_row_stride).  The lift is recomputed in fp32 from x (the forward's bf16 rounding of its output is
+ * not differentiated).  Replaces autograd through FactoredFastWalshHadamardProjection.forward,
+ * kernels/factored_kernel_deltanet.py:60-74.  Omega 16-byte aligned; x, phases, dout, dx element-aligned. */
+int kdn_fwht_lift_factored_bwd(const void* x, int64_t rows, int64_t x_row_stride, int x_dtype,
+                               const void* omega1_bf16, const float* phase1, const void* omega2_bf16,
+                               const float* phase2, float inv_tau, const float* dout, int64_t dout_row_stride,
+                               float* dx, int64_t dx_row_stride, void* stream);
+
 /* Arguments of the chunked delta-rule prefill scan.  Tensors are addressed as
  *   q[b][t][h][0:d_k], k[b][t][h][0:d_k], v[b][t][h][0:d_v], beta[b][t][h], decay[b][t][h],
  *   y[b][t][h][0:d_v], state[b][h][0:D][0:d_v]   (state element (d, j) = S[j][d] of the recurrence)
@@ -244,7 +254,10 @@ int kdn_scan_output(const kdn_scan_args* a, int64_t chunk0, int64_t nchunks, voi
  * linear rule (rule 1), the lifted features of feature mode 0 with every feature-map field (one shared or
  * per-head Omega, with or without low parts, shared or per-head phases and 1/tau, with or without
  * renormalisation; ABI 1.7, before which only one shared structured Omega), uniform batches (no
- * cu_seqlens / state_slots); pre-lifted features and other requests return KDN_ERR_UNSUPPORTED.  dy and
+ * cu_seqlens / state_slots); and (ABI 1.8) D = 1024 over pre-lifted features (feature mode 1, d_k = D,
+ * d_v 64 or 128, the delta rule: the scan of the factored d_k = 128 path, whose reference trains through
+ * autograd of kernels/factored_kernel_deltanet.py:77-183), where dq and dk are dL/dphi_q and dL/dphi_k.
+ * Other requests return KDN_ERR_UNSUPPORTED.  dy and
  * d_final_state are fp32; every gradient is written in fp32 with the layout of its input: dq, dk
  * (B, T, H, d_k), dv (B, T, H, d_v), dbeta, ddecay (B, T, H), d_initial_state (B, H, D, d_v).
  * d_final_state NULL means dL/dS_T = 0; ddecay (allowed only with decay) and d_initial_state may be
@@ -261,7 +274,14 @@ int kdn_scan_output(const kdn_scan_args* a, int64_t chunk0, int64_t nchunks, voi
  * (batch, head, chunk) more): it grows
  * with the segment, not with T, apart from the 128 KB per head per segment boundary.  Every reduction
  * runs in a fixed order: the results are identical bit for bit from run to run and between
- * kdn_delta_scan_bwd and kdn_delta_scan_bwd_streams. */
+ * kdn_delta_scan_bwd and kdn_delta_scan_bwd_streams.
+ *
+ * At D = 1024 (ABI 1.8) the backward is one segment on one stream (the auxiliary stream is not used, and
+ * kdn_scan_bwd_phase returns KDN_ERR_UNSUPPORTED): the forward's prep and carry kernels recompute every
+ * chunk, a reverse carry takes dL/dS from the last chunk to the first, and two parallel launches write
+ * the gradients.  Its workspace is one record per (batch, head, chunk) for the whole sequence
+ * (3,015,168 bytes at d_v = 128, 1,819,136 at d_v = 64) plus one fp32 [B][H][1024][d_v] state; it grows
+ * with T.  Its reductions also run in a fixed order. */
 typedef struct kdn_scan_bwd_args {
   const kdn_scan_args* fwd;
   const float* dy;            int64_t dy_stride[3];

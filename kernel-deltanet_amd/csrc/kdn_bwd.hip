@@ -1432,11 +1432,17 @@ static BwdLayout bwd_layout(const kdn_scan_args* f, bool want_dit) {
 }
 
 extern "C" size_t kdn_scan_bwd_workspace_bytes(const kdn_scan_bwd_args* a) {
+  if (a && general_bwd_applies(a->fwd)) return general_bwd_workspace_bytes(a);
   if (bwd_check(a) != KDN_OK) return 0;
   return bwd_layout(a->fwd, a->dinv_tau != nullptr).total;
 }
 
 extern "C" int64_t kdn_scan_bwd_segments(const kdn_scan_bwd_args* a, int64_t* segment_chunks) {
+  if (a && general_bwd_applies(a->fwd)) {  // one segment: every chunk
+    if (general_bwd_workspace_bytes(a) == 0) return 0;
+    if (segment_chunks) *segment_chunks = bwd_chunks(a->fwd);
+    return 1;
+  }
   if (bwd_check(a) != KDN_OK) return 0;
   const BwdLayout L = bwd_layout(a->fwd, a->dinv_tau != nullptr);
   if (segment_chunks) *segment_chunks = L.seg;
@@ -1639,6 +1645,7 @@ static int bwd_params(const kdn_scan_bwd_args* a, Params& p, BwdLayout& L) {
 // bf16 inputs: the D = 512 contractions take bf16 operands with fp32 accumulation, the forward's policy
 // for bf16 inputs; the lift and the 64 x 64 chunk algebra stay in fp32 MFMA.
 static int bwd_run(const kdn_scan_bwd_args* a, void* stream, void* aux_stream) {
+  if (a && general_bwd_applies(a->fwd)) return general_bwd(a, stream);  // one stream
   Params p;
   BwdLayout L;
   const int rc = bwd_params(a, p, L);
@@ -1656,6 +1663,7 @@ extern "C" int kdn_delta_scan_bwd_streams(const kdn_scan_bwd_args* a, void* stre
 
 extern "C" int kdn_scan_bwd_phase(const kdn_scan_bwd_args* a, int phase, int64_t segment, void* stream) {
   if (phase < 0 || phase > 4) return KDN_ERR_INVALID_ARGUMENT;
+  if (a && general_bwd_applies(a->fwd)) return KDN_ERR_UNSUPPORTED;  // no phase entry points at D = 1024
   Params p;
   BwdLayout L;
   const int rc = bwd_params(a, p, L);

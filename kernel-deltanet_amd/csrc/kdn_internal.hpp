@@ -55,6 +55,11 @@ bool general_scan_applies(const kdn_scan_args* a);
 int general_scan_validate(const kdn_scan_args* a);
 size_t general_scan_workspace_bytes(const kdn_scan_args* a);
 int general_scan(const kdn_scan_args* a, void* stream);
+// Its backward (kdn_delta_scan_bwd for D = 1024 over pre-lifted features: dq, dk are dL/dphi_q, dL/dphi_k):
+// one workspace record per (batch, head, chunk) for the whole sequence, one launch sequence on one stream.
+bool general_bwd_applies(const kdn_scan_args* f);
+size_t general_bwd_workspace_bytes(const kdn_scan_bwd_args* a);
+int general_bwd(const kdn_scan_bwd_args* a, void* stream);
 
 // Events of a multi-stream launch sequence, released when the call returns (destroying an event whose
 // record is still pending is allowed; its resources are freed once it completes).

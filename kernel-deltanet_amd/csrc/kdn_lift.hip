@@ -14,6 +14,7 @@
 #include "kdn_frag.hpp"
 #include "kdn_internal.hpp"
 #include "kdn_io.hpp"
+#include "kdn_tile.hpp"
 
 namespace kdn {
 
@@ -516,5 +517,138 @@ extern "C" int kdn_fwht_lift_factored(const void* x, int64_t rows, int64_t x_row
   else
     hipLaunchKernelGGL(renorm_rows_kernel<float>, grid, dim3(256), 0, as_stream(stream), static_cast<float*>(out), rows,
                        out_row_stride, 1e-7f);
+  return launch_status();
+}
+
+namespace kdn {
+// Backward of the factored lift: dx = d out / d x applied to dout, eight rows per workgroup.  The angles
+// theta = inv_tau (Omega_h x_h) + b_h of both halves are recomputed in fp32 (a thread per feature, its
+// Omega row in registers, all eight rows); per row (wave w: rows w and w + 4) the outer renormalisation,
+// the halves' renormalisations and the cosine are differentiated in place of the angles (dL/dtheta);
+// then dx_h = inv_tau Omega_h^T dL/dtheta_h (a thread per input column, Omega read row by row, so that a
+// wave's 64 reads of a row are one 128-byte line).  Per-row sums are wave reductions in a fixed order.
+constexpr int FLB_ROWS = 8;
+
+template <typename InT>
+__global__ void __launch_bounds__(256) lift_factored_bwd_kernel(const InT* x, int64_t rows, int64_t xs,
+                                                                const __bf16* om1, const float* ph1,
+                                                                const __bf16* om2, const float* ph2, float inv_tau,
+                                                                const float* dout, int64_t ds, float* dx,
+                                                                int64_t dxs) {
+  __shared__ float s_x[FLB_ROWS][128];
+  __shared__ float s_th[FLB_ROWS][1024];  // theta, then dL/dtheta
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int64_t r0 = (int64_t)blockIdx.x * FLB_ROWS;
+  for (int idx = tid; idx < FLB_ROWS * 128; idx += 256) {
+    const int r = idx >> 7, j = idx & 127;
+    s_x[r][j] = (r0 + r < rows) ? (float)x[(r0 + r) * xs + j] : 0.f;
+  }
+  __syncthreads();
+  for (int u = 0; u < 4; ++u) {
+    const int f = tid + 256 * u, hf = f >> 9, fl = f & 511;
+    const __bf16* om = (hf ? om2 : om1) + fl * 64;
+    float wv[64];
+#pragma unroll
+    for (int j8 = 0; j8 < 8; ++j8) load8<__bf16>(om + 8 * j8, wv + 8 * j8);
+    const float ph = (hf ? ph2 : ph1)[fl];
+#pragma unroll
+    for (int r = 0; r < FLB_ROWS; ++r) {
+      float acc = 0.f;
+#pragma unroll
+      for (int j = 0; j < 64; ++j) acc += wv[j] * s_x[r][64 * hf + j];
+      s_th[r][f] = acc * inv_tau + ph;
+    }
+  }
+  __syncthreads();
+  const float amp = sqrtf(2.f / 512.f);
+  for (int rr = 0; rr < 2; ++rr) {
+    const int r = w + 4 * rr;
+    const bool valid = r0 + r < rows;
+    // feature f = lane + 64 k of the row; k < 8 the first half
+    float cs[16], sn[16], g[16];
+    float n1 = 0.f, n2 = 0.f;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      const float th = s_th[r][lane + 64 * k];
+      cs[k] = amp * cos_rad(th);
+      sn[k] = amp * sin_rad(th);
+      g[k] = valid ? dout[(r0 + r) * ds + lane + 64 * k] : 0.f;
+      if (k < 8) n1 += cs[k] * cs[k];
+      else n2 += cs[k] * cs[k];
+    }
+    n1 = sqrtf(wave_sum64(n1));
+    n2 = sqrtf(wave_sum64(n2));
+    const float e1 = n1 + 1e-8f, e2 = n2 + 1e-8f;
+    float c[16], nn = 0.f, sc = 0.f;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      c[k] = cs[k] / (k < 8 ? e1 : e2);
+      nn += c[k] * c[k];
+      sc += c[k] * g[k];
+    }
+    const float N = sqrtf(wave_sum64(nn));
+    sc = wave_sum64(sc);
+    const float E = N + 1e-7f;
+    const float corr = N > 0.f ? sc / (E * E * N) : 0.f;
+    float s1 = 0.f, s2 = 0.f;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      g[k] = g[k] / E - c[k] * corr;  // dL/d(concatenated halves)
+      if (k < 8) s1 += cs[k] * g[k];
+      else s2 += cs[k] * g[k];
+    }
+    s1 = wave_sum64(s1);
+    s2 = wave_sum64(s2);
+    const float k1 = n1 > 0.f ? s1 / (e1 * e1 * n1) : 0.f, k2 = n2 > 0.f ? s2 / (e2 * e2 * n2) : 0.f;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      const float dphit = k < 8 ? g[k] / e1 - cs[k] * k1 : g[k] / e2 - cs[k] * k2;
+      s_th[r][lane + 64 * k] = -sn[k] * dphit;
+    }
+  }
+  __syncthreads();
+  const int j = tid & 63, rg = tid >> 6;
+  for (int hf = 0; hf < 2; ++hf) {
+    const __bf16* om = hf ? om2 : om1;
+    float a0 = 0.f, a1 = 0.f;
+    for (int fl = 0; fl < 512; ++fl) {
+      const float wv = (float)om[fl * 64 + j];
+      a0 += wv * s_th[rg][512 * hf + fl];
+      a1 += wv * s_th[rg + 4][512 * hf + fl];
+    }
+    if (r0 + rg < rows) dx[(r0 + rg) * dxs + 64 * hf + j] = inv_tau * a0;
+    if (r0 + rg + 4 < rows) dx[(r0 + rg + 4) * dxs + 64 * hf + j] = inv_tau * a1;
+  }
+}
+}  // namespace kdn
+
+extern "C" int kdn_fwht_lift_factored_bwd(const void* x, int64_t rows, int64_t x_row_stride, int x_dtype,
+                                          const void* omega1_bf16, const float* phase1, const void* omega2_bf16,
+                                          const float* phase2, float inv_tau, const float* dout,
+                                          int64_t dout_row_stride, float* dx, int64_t dx_row_stride, void* stream) {
+  if (!x || !omega1_bf16 || !phase1 || !omega2_bf16 || !phase2 || !dout || !dx || rows < 0)
+    return KDN_ERR_INVALID_ARGUMENT;
+  if (!valid_dtype(x_dtype)) return KDN_ERR_INVALID_ARGUMENT;
+  if (x_row_stride < 128 || dout_row_stride < 1024 || dx_row_stride < 128) return KDN_ERR_INVALID_ARGUMENT;
+  if (!(inv_tau == inv_tau)) return KDN_ERR_INVALID_ARGUMENT;
+  // Omega rows are read 16 bytes at a time; everything else element by element
+  if (!aligned(omega1_bf16, 16) || !aligned(omega2_bf16, 16)) return KDN_ERR_MISALIGNED;
+  if (!aligned(x, dtype_size(x_dtype)) || !aligned(phase1, 4) || !aligned(phase2, 4) || !aligned(dout, 4) ||
+      !aligned(dx, 4))
+    return KDN_ERR_MISALIGNED;
+  if (rows == 0) return KDN_OK;
+  const int64_t wgs = (rows + FLB_ROWS - 1) / FLB_ROWS;
+  if (wgs > 0x7fffffff) return KDN_ERR_UNSUPPORTED;
+  const hipStream_t st = as_stream(stream);
+  const __bf16* o1 = static_cast<const __bf16*>(omega1_bf16);
+  const __bf16* o2 = static_cast<const __bf16*>(omega2_bf16);
+  if (x_dtype == KDN_DTYPE_BF16)
+    hipLaunchKernelGGL(lift_factored_bwd_kernel<__bf16>, dim3((unsigned)wgs), dim3(256), 0, st,
+                       static_cast<const __bf16*>(x), rows, x_row_stride, o1, phase1, o2, phase2, inv_tau, dout,
+                       dout_row_stride, dx, dx_row_stride);
+  else
+    hipLaunchKernelGGL(lift_factored_bwd_kernel<float>, dim3((unsigned)wgs), dim3(256), 0, st,
+                       static_cast<const float*>(x), rows, x_row_stride, o1, phase1, o2, phase2, inv_tau, dout,
+                       dout_row_stride, dx, dx_row_stride);
   return launch_status();
 }

@@ -51,6 +51,7 @@ EXPORTED = (
     "kdn_scan_bwd_phase",
     "kdn_scan_bwd_segments",
     "kdn_fwht_lift_bits_butterfly",
+    "kdn_fwht_lift_factored_bwd",
 )
 
 KDN_ERR_CAPACITY = -6
@@ -217,6 +218,8 @@ def lib() -> ctypes.CDLL:
             L.kdn_delta_scan_bwd_streams.restype = ci
             L.kdn_fwht_lift_factored.argtypes = [vp, i64, i64, ci, vp, vp, vp, vp, cf, vp, i64, ci, vp]
             L.kdn_fwht_lift_factored.restype = ci
+            L.kdn_fwht_lift_factored_bwd.argtypes = [vp, i64, i64, ci, vp, vp, vp, vp, cf, vp, i64, vp, i64, vp]
+            L.kdn_fwht_lift_factored_bwd.restype = ci
             L.kdn_scan_bwd_phase.argtypes = [ctypes.POINTER(ScanBwdArgs), ci, i64, vp]
             L.kdn_scan_bwd_phase.restype = ci
             L.kdn_scan_bwd_segments.argtypes = [ctypes.POINTER(ScanBwdArgs), ctypes.POINTER(ctypes.c_int64)]

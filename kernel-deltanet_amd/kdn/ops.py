@@ -148,6 +148,30 @@ def lift_factored(x: torch.Tensor, omega1: torch.Tensor, phase1: torch.Tensor, o
     return out.view(*x.shape[:-1], 1024)
 
 
+def lift_factored_backward(x: torch.Tensor, dphi: torch.Tensor, omega1: torch.Tensor, phase1: torch.Tensor,
+                           omega2: torch.Tensor, phase2: torch.Tensor, inv_tau: float) -> torch.Tensor:
+    """dL/dx (float32, x's shape) of lift_factored(x, ...) for dL/d(out) = dphi (..., 1024)
+    (kdn_fwht_lift_factored_bwd; the lift is recomputed in fp32 from x)."""
+    require_device(x, "lift_factored_backward")
+    if x.shape[-1] != 128 or dphi.shape != (*x.shape[:-1], 1024):
+        raise ValueError(f"lift_factored_backward: expects x (..., 128) and dphi (..., 1024); got {tuple(x.shape)}, "
+                         f"{tuple(dphi.shape)}")
+    dev = x.device
+    x2 = _rows(x, 128)
+    g2 = _rows(dphi.to(device=dev, dtype=torch.float32), 1024)
+    o1, o2 = omega1.to(device=dev).contiguous(), omega2.to(device=dev).contiguous()
+    p1 = phase1.to(device=dev, dtype=torch.float32).contiguous()
+    p2 = phase2.to(device=dev, dtype=torch.float32).contiguous()
+    dx = torch.empty(x2.shape[0], 128, dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        N.check(N.lib().kdn_fwht_lift_factored_bwd(
+            ctypes.c_void_p(x2.data_ptr()), x2.shape[0], x2.stride(0), _tag(x.dtype, "lift_factored_backward"),
+            ctypes.c_void_p(o1.data_ptr()), ctypes.c_void_p(p1.data_ptr()), ctypes.c_void_p(o2.data_ptr()),
+            ctypes.c_void_p(p2.data_ptr()), float(inv_tau), ctypes.c_void_p(g2.data_ptr()), g2.stride(0),
+            ctypes.c_void_p(dx.data_ptr()), dx.stride(0), ctypes.c_void_p(_stream(dev))), "kdn_fwht_lift_factored_bwd")
+    return dx.view(*x.shape)
+
+
 def _last_contig(t: torch.Tensor) -> torch.Tensor:
     return t if t.stride(-1) == 1 else t.contiguous()
 
@@ -375,8 +399,8 @@ class ScanBackwardPlan:
         B, T, H, d_k = q.shape
         d_v = v.shape[-1]
         fm = _features_on(features if features is not None else FeatureMap(omega_bf16, phase), dev, H)
-        if fm.lifted:
-            raise ValueError("scan_backward: pre-lifted features have no backward here")
+        if fm.lifted and d_k != 1024:
+            raise ValueError("scan_backward: pre-lifted features have a backward at D = 1024 only (the factored path)")
         D = fm.dim(q)
         if initial_state is not None:
             if tuple(initial_state.shape) != (B, H, D, d_v):
@@ -415,7 +439,8 @@ class ScanBackwardPlan:
         nbytes = N.lib().kdn_scan_bwd_workspace_bytes(ctypes.byref(a))
         if nbytes == 0:
             raise ValueError("scan_backward: unsupported request (kdn_scan_bwd_workspace_bytes returned 0; the "
-                             "backward covers d_k = 64, D = 512, d_v = 64 with lifted features)")
+                             "backward covers d_k = 64, D = 512, d_v = 64 with lifted features and D = 1024 "
+                             "pre-lifted features with d_v 64 or 128)")
         if workspace is None or workspace.numel() * workspace.element_size() < nbytes:
             workspace = torch.empty(nbytes, dtype=torch.uint8, device=dev)
         a.workspace, a.workspace_bytes = workspace.data_ptr(), workspace.numel() * workspace.element_size()

@@ -12,7 +12,8 @@
                        token_recurrence_torch, delta_rule_torch (lift of kernels/fwht.py:122-131),
                        linear_recurrence_torch, rff_features_torch (the per-head feature map of the P2
                        module, kernels/kernel_deltanet_fused.py:238-251, and of the P4 layer's shifted
-                       [cos, sin] form, core/rkhs_features.py:107-131)
+                       [cos, sin] form, core/rkhs_features.py:107-131), factored_lift_torch (the d_k = 128
+                       factored lift, kernels/factored_kernel_deltanet.py:60-74)
 """
 from __future__ import annotations
 
@@ -110,6 +111,15 @@ def delta_rule_torch(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, beta: to
     end to end, in the inputs' dtype (float64 for the gradient oracle)."""
     return token_recurrence_torch(_torch_lift(q, proj, normalize), _torch_lift(k, proj, normalize), v, beta, decay,
                                   initial_state)
+
+
+def factored_lift_torch(x: torch.Tensor, proj1: dict, proj2: dict) -> torch.Tensor:
+    """oracle.lift.factored_lift on torch tensors (FactoredFastWalshHadamardProjection.forward,
+    kernels/factored_kernel_deltanet.py:60-74): the halves of x lifted by _torch_lift with the projections
+    of seeds s and s + 1000, concatenated and divided by (norm + 1e-7); differentiable."""
+    d0 = x.shape[-1] // 2
+    phi = torch.cat([_torch_lift(x[..., :d0], proj1, False), _torch_lift(x[..., d0:], proj2, False)], dim=-1)
+    return phi / (torch.norm(phi, dim=-1, keepdim=True) + 1e-7)
 
 
 def delta_rule(q, k, v, beta, decay, proj: dict, initial_state=None, normalize: bool = False):

@@ -62,7 +62,7 @@ def test_args_layout_matches_c(cname, pystruct):
 def test_strerror_and_version(lib):
     for code in (0, -1, -2, -3, -4, -5, -99):
         assert len(lib.kdn_strerror(code)) > 0
-    assert lib.kdn_abi_version() == (1 << 16) | 7
+    assert lib.kdn_abi_version() == (1 << 16) | 8
 
 
 def _args(**kw):
@@ -212,3 +212,51 @@ def test_backward_workspace_and_errors_need_no_device(lib):
     g.fwd = ctypes.addressof(f)
     g.dy = None
     assert lib.kdn_delta_scan_bwd(ctypes.byref(g), None) == -1
+
+
+def test_general_width_backward_needs_no_device(lib):
+    # D = 1024 over pre-lifted features (ABI 1.8): one record per (batch, head, chunk) for the whole
+    # sequence (753,792 floats at d_v = 128, 454,784 at d_v = 64) plus the forward carry's final state
+    f = _fake_ptrs(_args(T=256, H=2, d_k=1024, D=1024, d_v=128, feature_mode=1))
+    g = N.ScanBwdArgs()
+    g.fwd = ctypes.addressof(f)
+    for i, nm in enumerate(("dy", "dq", "dk", "dv", "dbeta", "workspace")):
+        setattr(g, nm, 0x7E0000000000 + 0x100000 * i)
+    rec128, rec64 = 753792 * 4, 454784 * 4
+    assert lib.kdn_scan_bwd_workspace_bytes(ctypes.byref(g)) == 2 * 4 * rec128 + 2 * 1024 * 128 * 4
+    seg = ctypes.c_int64(0)
+    assert lib.kdn_scan_bwd_segments(ctypes.byref(g), ctypes.byref(seg)) == 1 and seg.value == 4
+    f.d_v = 64
+    assert lib.kdn_scan_bwd_workspace_bytes(ctypes.byref(g)) == 2 * 4 * rec64 + 2 * 1024 * 64 * 4
+    g.workspace_bytes = 1 << 40
+    assert lib.kdn_scan_bwd_phase(ctypes.byref(g), 1, 0, None) == -2   # no phase entry points at D = 1024
+    g.workspace_bytes = 1024
+    assert lib.kdn_delta_scan_bwd(ctypes.byref(g), None) == -3
+    g.dinv_tau = 0x7C0000000000                                        # no temperature to differentiate
+    assert lib.kdn_scan_bwd_workspace_bytes(ctypes.byref(g)) == 0
+    g.dinv_tau = None
+    f.d_v = 32
+    assert lib.kdn_scan_bwd_workspace_bytes(ctypes.byref(g)) == 0
+    f.d_v, f.rule = 64, 1
+    assert lib.kdn_scan_bwd_workspace_bytes(ctypes.byref(g)) == 0
+    f.rule = 0
+    g.ddecay = 0x7B0000000000                                          # ddecay without a forward decay
+    assert lib.kdn_delta_scan_bwd(ctypes.byref(g), None) == -1
+    g.ddecay = None
+    g.dk = None
+    assert lib.kdn_delta_scan_bwd(ctypes.byref(g), None) == -1
+
+
+def test_factored_lift_backward_errors_need_no_device(lib):
+    fb = lib.kdn_fwht_lift_factored_bwd
+    p = 0x7F0000000000
+    ok = (p, 10, 128, 1, p, p, p, p, 0.35, p, 1024, p, 128, None)
+    assert fb(*ok[:1], 0, *ok[2:]) == 0                                  # no rows: nothing launched
+    assert fb(None, *ok[1:]) == -1
+    assert fb(*ok[:1], -1, *ok[2:]) == -1
+    assert fb(*ok[:2], 64, *ok[3:]) == -1                                # x rows of 128
+    assert fb(*ok[:3], 7, *ok[4:]) == -1                                 # dtype
+    assert fb(*ok[:4], p + 8, *ok[5:]) == -4                             # Omega 16-byte aligned
+    assert fb(*ok[:8], float("nan"), *ok[9:]) == -1
+    assert fb(*ok[:10], 512, *ok[11:]) == -1                             # dout rows of 1024
+    assert fb(*ok[:9], p + 2, *ok[10:]) == -4                            # fp32 dout

@@ -116,3 +116,111 @@ def test_factored_scan_single_partial_chunk(fproj, oprojs):
     Yr, Sr = oracle_scan(q, k, v, beta, dec, oprojs)
     assert rel(Y.cpu().numpy(), Yr) < 1e-4
     assert rel(S.cpu().numpy(), Sr) < 1e-4
+
+
+# ------------------------------------------------------------------------------------------------ backward
+# Gradient oracle: torch autograd in float64 of oracle.scan.factored_lift_torch (equal to the numpy
+# factored-lift oracle, gradcheck-pinned in test_oracle_factored.py) and oracle.scan.token_recurrence_torch
+# (gradcheck-pinned in test_oracle_backward.py) -- the role the reference gives torch autograd over its
+# chunked forward.  Tolerances (relative L2): 1e-4 for fp32 inputs, 2e-2 for bf16 inputs; the lift's
+# backward alone 1e-5 (it recomputes the lift in fp32 from bf16-exact inputs).
+
+def _t64(x):
+    return torch.as_tensor(np.asarray(x, dtype=np.float64))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_factored_lift_backward(fproj, oprojs, dtype):
+    g = torch.Generator().manual_seed(11)
+    x = torch.randn(3, 20, 128, generator=g).to(dtype)
+    dphi = torch.randn(3, 20, 1024, generator=g)
+    p1, p2 = fproj.proj1, fproj.proj2
+    dx = ops.lift_factored_backward(x.to(DEV), dphi.to(DEV), p1.device_omega(DEV), p1.device_phase(DEV),
+                                    p2.device_omega(DEV), p2.device_phase(DEV), p1.tau_star_inv)
+    torch.cuda.synchronize()
+    xr = x.double().requires_grad_(True)
+    (osc.factored_lift_torch(xr, *oprojs) * dphi.double()).sum().backward()
+    assert dx.shape == x.shape and dx.dtype == torch.float32
+    assert rel(dx.cpu().numpy(), xr.grad.numpy()) < 1e-5
+
+
+def _prelifted_case(B, T, dv, dtype, oprojs, seed):
+    g = torch.Generator().manual_seed(seed)
+    pq = torch.from_numpy(ol.factored_lift(torch.randn(B, T, 128, generator=g).numpy(), *oprojs)).to(dtype)
+    pk = torch.from_numpy(ol.factored_lift(torch.randn(B, T, 128, generator=g).numpy(), *oprojs)).to(dtype)
+    v = torch.randn(B, T, dv, generator=g).to(dtype)
+    beta = torch.sigmoid(torch.randn(B, T, generator=g))
+    decay = 0.9 + 0.1 * torch.rand(B, T, generator=g)
+    s0 = 0.1 * torch.randn(B, dv, 1024, generator=g)
+    dy = torch.randn(B, T, dv, generator=g)
+    ds = torch.randn(B, dv, 1024, generator=g)
+    return pq, pk, v, beta, decay, s0, dy, ds
+
+
+def _oracle_scan_grads(pq, pk, v, beta, decay, s0, dy, ds):
+    leaves = [t.double().requires_grad_(True) for t in (pq, pk, v, beta, decay, s0)]
+    Y, S = osc.token_recurrence_torch(*leaves)
+    ((Y * dy.double()).sum() + (S * ds.double()).sum()).backward()
+    return [t.grad.numpy() for t in leaves]
+
+
+@pytest.mark.parametrize("dtype,dv,T", [(torch.float32, 128, 200), (torch.bfloat16, 128, 200),
+                                        (torch.float32, 64, 700)])
+def test_d1024_scan_backward(oprojs, dtype, dv, T):
+    # kdn_delta_scan_bwd at D = 1024 over pre-lifted features: every gradient, with decay, an initial
+    # state, dL/dS_T and a partial last chunk
+    B = 2
+    pq, pk, v, beta, decay, s0, dy, ds = _prelifted_case(B, T, dv, dtype, oprojs, 5)
+    d = lambda t: t.to(DEV)
+    plan = ops.ScanBackwardPlan(d(pq).unsqueeze(2), d(pk).unsqueeze(2), d(v).unsqueeze(2), d(beta).unsqueeze(-1),
+                                d(decay).unsqueeze(-1), None, None, 1.0, d(dy).unsqueeze(2),
+                                d(ds).unsqueeze(1).transpose(2, 3), initial_state=d(s0).unsqueeze(1).transpose(2, 3),
+                                features=ops.FeatureMap(lifted=True))
+    assert plan.segments == 1
+    dq, dk, dvv, dbeta, ddecay, dinit = plan.run(concurrent_carries=False)
+    torch.cuda.synchronize()
+    ref = _oracle_scan_grads(pq, pk, v, beta, decay, s0, dy, ds)
+    tol = 1e-4 if dtype == torch.float32 else 2e-2
+    got = [dq[:, :, 0], dk[:, :, 0], dvv[:, :, 0], dbeta[:, :, 0], ddecay[:, :, 0], dinit[:, 0].transpose(1, 2)]
+    for name, a, r in zip(("dphi_q", "dphi_k", "dv", "dbeta", "ddecay", "dS0"), got, ref):
+        assert rel(a.cpu().numpy(), r) < tol, name
+
+
+def test_d1024_scan_backward_is_deterministic(oprojs):
+    pq, pk, v, beta, decay, s0, dy, ds = _prelifted_case(1, 300, 128, torch.bfloat16, oprojs, 6)
+    d = lambda t: t.to(DEV)
+    outs = []
+    for _ in range(2):
+        plan = ops.ScanBackwardPlan(d(pq).unsqueeze(2), d(pk).unsqueeze(2), d(v).unsqueeze(2),
+                                    d(beta).unsqueeze(-1), d(decay).unsqueeze(-1), None, None, 1.0,
+                                    d(dy).unsqueeze(2), None, features=ops.FeatureMap(lifted=True))
+        outs.append([t.clone() for t in plan.run() if t is not None])
+    torch.cuda.synchronize()
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_factored_module_gradients(fproj, oprojs, dtype):
+    # autograd through factored_chunked_deltanet_forward (the reference's training path for d_k = 128):
+    # gradients of q, k, v, beta, decay and the initial state
+    g = torch.Generator().manual_seed(12)
+    B, T, dv = 2, 150, 128
+    q, k = torch.randn(B, T, 128, generator=g).to(dtype), torch.randn(B, T, 128, generator=g).to(dtype)
+    v = torch.randn(B, T, dv, generator=g).to(dtype)
+    beta = torch.sigmoid(torch.randn(B, T, generator=g))
+    decay = 0.9 + 0.1 * torch.rand(B, T, generator=g)
+    s0 = 0.1 * torch.randn(B, dv, 1024, generator=g)
+    dy, ds = torch.randn(B, T, dv, generator=g), torch.randn(B, dv, 1024, generator=g)
+    leaves = [t.to(DEV).requires_grad_(True) for t in (q, k, v, beta, decay, s0)]
+    Y, S = factored_chunked_deltanet_forward(*leaves[:5], fproj, initial_state=leaves[5])
+    ((Y.float() * dy.to(DEV)).sum() + (S.float() * ds.to(DEV)).sum()).backward()
+    torch.cuda.synchronize()
+    refs = [t.double().requires_grad_(True) for t in (q, k, v, beta, decay, s0)]
+    Yr, Sr = osc.token_recurrence_torch(osc.factored_lift_torch(refs[0], *oprojs),
+                                        osc.factored_lift_torch(refs[1], *oprojs), *refs[2:])
+    ((Yr * dy.double()).sum() + (Sr * ds.double()).sum()).backward()
+    tol = 1e-4 if dtype == torch.float32 else 2e-2
+    for name, a, r in zip(("dq", "dk", "dv", "dbeta", "ddecay", "dS0"), leaves, refs):
+        assert a.grad is not None and a.grad.dtype == a.dtype, name
+        assert rel(a.grad.float().cpu().numpy(), r.grad.numpy()) < tol, name

@@ -49,3 +49,17 @@ def test_second_projection_uses_seed_plus_1000():
     h2 = ol.lift(x[:, 64:], p2)
     ratio = phi[:, 512:] / h2
     assert np.abs(ratio - ratio[:, :1]).max() < 1e-9
+
+
+def test_torch_factored_lift_equals_the_numpy_oracle_and_passes_gradcheck():
+    # oracle.scan.factored_lift_torch (the gradient oracle of the factored backward) restates
+    # oracle.lift.factored_lift on torch tensors: equal in float64, and its autograd gradient agrees with
+    # central differences (torch.autograd.gradcheck)
+    import torch
+    from oracle import scan as osc
+    p1, p2 = ol.make_projection(64, 512, 42), ol.make_projection(64, 512, 1042)
+    x = np.random.default_rng(3).standard_normal((3, 128))
+    got = osc.factored_lift_torch(torch.from_numpy(x), p1, p2).numpy()
+    assert np.abs(got - ol.factored_lift(x, p1, p2)).max() < 1e-13
+    xt = torch.from_numpy(x[:2]).requires_grad_(True)
+    assert torch.autograd.gradcheck(lambda t: osc.factored_lift_torch(t, p1, p2), (xt,), eps=1e-6, atol=1e-7)
