@@ -144,7 +144,7 @@ def main():
                          "sign table per workgroup) or kdn_fwht_lift_bits_butterfly (in-register butterflies)")
     ap.add_argument("--factored", action="store_true",
                     help="time the factored d_k = 128 path (two 64 -> 512 lifts, D = 1024 scan, d_v = 128) on a "
-                         "B=1, H=32, T=16384 layer instead of config 3")
+                         "B=1, H=32, T=16384 layer instead of config 3 (with --backward: its backward)")
     ap.add_argument("--backward", action="store_true",
                     help="time the backward pass (kdn_delta_scan_bwd: gradients of q, k, v, beta) on the config "
                          "3 shape instead of the forward")
@@ -165,6 +165,8 @@ def main():
         torch.cuda.synchronize()
         print(json.dumps({"copy_calibration_bytes_per_dispatch_each_way": n}), flush=True)
         return
+    if args.backward and args.factored:
+        return bench_factored_backward(args, dev)
     if args.backward:
         return bench_backward(args, dev)
     if args.factored:
@@ -530,6 +532,86 @@ def bench_factored(args, dev):
                      "frac": achieved / (MFMA_BF16_PEAK / 1e12), "traffic": None, "kernel": "scan (3 launches)"},
         "phases": {"lift": {"ms": lift_ms, "alg_bytes": lift_bytes, "gbps": lift_bytes / lift_ms / 1e6},
                    "scan": {"ms": scan_ms, "alg_flops": f_chunk * units, "tflops": achieved}},
+        "cpu_baseline": None,
+    }
+    print(json.dumps(out), flush=True)
+
+
+def bench_factored_backward(args, dev):
+    """The backward of the factored d_k = 128 layer of bench_factored (B=1, H=32, T=16384, bf16, d_v = 128,
+    lambda = 1, dL/dy ~ N(0,1)): kdn_delta_scan_bwd at D = 1024 over the lifted features (dL/dphi_q,
+    dL/dphi_k, dv, dbeta), then kdn_fwht_lift_factored_bwd for q and k.  A step = the whole backward."""
+    from kdn import ops
+    from kernels import FactoredFastWalshHadamardProjection
+
+    B = args.B if args.B is not None else 1
+    T = args.T if args.T is not None else 16384
+    H = 32 if args.H == 16 else args.H
+    D, dv, dk = 1024, 128, 128
+    g = torch.Generator(device=dev).manual_seed(1234)
+    q = torch.randn(B, T, H, dk, generator=g, device=dev).to(torch.bfloat16)
+    k = torch.randn(B, T, H, dk, generator=g, device=dev).to(torch.bfloat16)
+    v = torch.randn(B, T, H, dv, generator=g, device=dev).to(torch.bfloat16)
+    beta = torch.sigmoid(torch.randn(B, T, H, generator=g, device=dev))
+    dy = torch.randn(B, T, H, dv, generator=g, device=dev)
+    fp = FactoredFastWalshHadamardProjection(dk, D, 42)
+    lift_args = (fp.proj1.device_omega(dev), fp.proj1.device_phase(dev), fp.proj2.device_omega(dev),
+                 fp.proj2.device_phase(dev), fp.proj1.tau_star_inv)
+    fq, fk = ops.lift_factored(q, *lift_args), ops.lift_factored(k, *lift_args)
+    plan = ops.ScanBackwardPlan(fq, fk, v, beta, None, None, None, 1.0, dy, need_dinit=False,
+                                features=ops.FeatureMap(lifted=True))
+    stream = torch.cuda.current_stream(dev)
+
+    def step(times=None):
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)] if times is not None else None
+        if ev:
+            ev[0].record(stream)
+        dpq, dpk = plan.run(concurrent_carries=False)[:2]
+        if ev:
+            ev[1].record(stream)
+        ops.lift_factored_backward(q, dpq, *lift_args)
+        ops.lift_factored_backward(k, dpk, *lift_args)
+        if ev:
+            ev[2].record(stream)
+            times.append(ev)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(args.steps):
+        step()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / args.steps
+    times = []
+    for _ in range(args.steps):
+        step(times)
+    torch.cuda.synchronize()
+    scan_ms = sum(a.elapsed_time(b) for a, b, _ in times) / args.steps
+    lift_ms = sum(b.elapsed_time(c) for _, b, c in times) / args.steps
+    nch = (T + C - 1) // C
+    units = B * H * nch
+    # per chunk: the recompute's Grams and carry (4 C^2 D + 4 C D d_v), R and H (2 C D d_v), the reverse
+    # carry (4 C D d_v), Q S^T (2 C D d_v) and the feature gradients (6 C D d_v + 6 C^2 D), plus the
+    # 64 x 64 algebra (~16 C^2 d_v + 6 C^3)
+    f_chunk = 10 * C * C * D + 18 * C * D * dv + 16 * C * C * dv + 6 * C ** 3
+    achieved = f_chunk * units / scan_ms / 1e9
+    out = {
+        "metric": "factored d_k=128 backward tokens/s (D=1024 scan backward + lift backward) on 1 GPU; "
+                  "% of MFMA roofline",
+        "value": B * T / (ms / 1e3), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) q/k/v, sigmoid(N(0,1)) beta, N(0,1) dL/dy; projection seeds 42, 1042)",
+        "config": {"workload": f"backward of the factored d_k=128 layer, B={B}, H={H}, T={T}, d_k=128->D={D}, "
+                               f"d_v={dv}, bf16 q/k/v, fp32 beta, lambda=1",
+                   "B": B, "H": H, "T": T, "D": D, "d_v": dv, "workspace_bytes": plan.workspace.numel(),
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "mfma", "achieved": achieved, "peak": MFMA_BF16_PEAK / 1e12, "unit": "TFLOP/s",
+                     "frac": achieved / (MFMA_BF16_PEAK / 1e12), "traffic": None, "kernel": "scan backward (6 launches)"},
+        "phases": {"scan_backward": {"ms": scan_ms, "alg_flops": f_chunk * units, "tflops": achieved},
+                   "lift_backward": {"ms": lift_ms}},
         "cpu_baseline": None,
     }
     print(json.dumps(out), flush=True)

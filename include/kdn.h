@@ -122,7 +122,8 @@ int kdn_fwht_lift_factored(const void* x, int64_t rows, int64_t x_row_stride, in
  * and phase arguments, with dout fp32 rows of 1024 (dout_row_stride) and dx fp32 rows of 128
  * (dx_row_stride).  The lift is recomputed in fp32 from x (the forward's bf16 rounding of its output is
  * not differentiated).  Replaces autograd through FactoredFastWalshHadamardProjection.forward,
- * kernels/factored_kernel_deltanet.py:60-74.  Omega 16-byte aligned; x, phases, dout, dx element-aligned. */
+ * kernels/factored_kernel_deltanet.py:60-74.  Omega 8-byte aligned; phases, dout and dx 16-byte aligned
+ * with row strides that are multiples of 4; x element-aligned. */
 int kdn_fwht_lift_factored_bwd(const void* x, int64_t rows, int64_t x_row_stride, int x_dtype,
                                const void* omega1_bf16, const float* phase1, const void* omega2_bf16,
                                const float* phase2, float inv_tau, const float* dout, int64_t dout_row_stride,

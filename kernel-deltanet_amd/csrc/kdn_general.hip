@@ -52,10 +52,10 @@ struct BRec {
   static constexpr size_t T = Rec<D, DV>::floats;  // [64][64] (I + A)^-1
   static constexpr size_t G = T + C * C;            // [64][64] K K^T
   static constexpr size_t XK = G + C * C;           // [64][DV] K S^T
-  static constexpr size_t SR = XK + C * DV;         // [D][DV] S^T at the chunk start, fp32
-  static constexpr size_t H1 = SR + D * DV;         // [D][DV] Q^T (a o dY)
+  static constexpr size_t SR = XK + C * DV;         // [DV][D] the chunk-start state (S, not S^T), fp32
+  static constexpr size_t H1 = SR + D * DV;         // [DV][D] (Q^T (a o dY))^T
   static constexpr size_t RR = H1 + D * DV;         // [64][DV] P^T dY
-  static constexpr size_t GR = RR + C * DV;         // [D][DV] dL/dS^T at the chunk end
+  static constexpr size_t GR = RR + C * DV;         // [DV][D] (dL/dS^T)^T at the chunk end
   static constexpr size_t X = GR + D * DV;          // [64][DV] K Gamma
   static constexpr size_t DW = X + C * DV;          // [64][DV] dL/dW
   static constexpr size_t ZN = DW + C * DV;         // [64][DV] -Tp^T dW (= dL/dX_K)
@@ -289,11 +289,10 @@ __device__ __forceinline__ bool carry_step(const Params& p, CarryShared& sh, int
 
   // store the chunk-start slice (as output fragments) and form K times it, partial over this wave's features
   // (the backward's recompute keeps the slice in fp32 rows instead: no output kernel reads the fragments)
-  if constexpr (BWD) {
+  if constexpr (BWD) {  // value-major rows: a lane's four features are one 16-byte store
+    float* srow = rec + BRec<D, DV>::SR + (int64_t)(16 * n + (lane & 15)) * D + (D / 4) * w + 4 * (lane >> 4);
 #pragma unroll
-    for (int t = 0; t < TPW; ++t)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) rec[BRec<D, DV>::SR + (int64_t)((D / 4) * w + 16 * t + 4 * (lane >> 4) + i) * DV + 16 * n + (lane & 15)] = Sg[t][i];
+    for (int t = 0; t < TPW; ++t) *reinterpret_cast<f32x4*>(srow + 16 * t) = Sg[t];
   }
   frag* sf = reinterpret_cast<frag*>(rec + R::S);
   f32x4 xp[4];
@@ -489,8 +488,10 @@ static size_t record_floats(int D, int DV) {
 //                                        dphi_k = (kappa o W) Gamma^T - Z S + (M + M^T) K + N^T Q
 // with S the chunk-start state (D x d_v transposed: the d_v x D matrix of the recurrence), N_ij =
 // dP_ij g_{i-1}/g_j and M_ij = dA_ij beta_i g_i/g_j below the diagonal, dP = dY W^T, dA = -T^T dT T^T.
-// The carries and H take the forward's precision policy (bf16 operands for bf16 inputs); the per-chunk
-// gradient products run on fp32 MFMA.  Every reduction has a fixed order (no atomics).
+// The contractions that involve the features (the carries, H, Q S^T and the feature gradients) take the
+// forward's precision policy (bf16 operands with fp32 accumulation for bf16 inputs, as the D = 512
+// backward); the 64 x 64 chunk algebra runs on fp32 MFMA.  Every reduction has a fixed order (no
+// atomics).
 
 struct BwdP {
   const float* dy; int64_t ys0, ys1, ys2;
@@ -544,9 +545,7 @@ __global__ void __launch_bounds__(256) gbwd_rh_kernel(Params p, BwdP g) {
     for (int n = 0; n < NV; ++n) {
       const f32x4 hv = PB::mma(PB::mma(zero4(), q0, PB::from_f32(frag_cols(bAY, LDV, 16 * n, 0, lane))), q1,
                                PB::from_f32(frag_cols(bAY, LDV, 16 * n, 32, lane)));
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        rec[R::H1 + (int64_t)(16 * ft + 4 * (lane >> 4) + i) * DV + 16 * n + (lane & 15)] = hv[i];
+      *reinterpret_cast<f32x4*>(rec + R::H1 + (int64_t)(16 * n + (lane & 15)) * D + 16 * ft + 4 * (lane >> 4)) = hv;
     }
   }
 }
@@ -579,23 +578,35 @@ __global__ void __launch_bounds__(256) gbwd_rchain_kernel(Params p, BwdP g) {
       const int f = FPW * w + 16 * t + 4 * (lane >> 4) + i;
       Gg[t][i] = g.dfin ? g.dfin[b * g.fs0 + h * g.fs1 + f * g.fs2 + vc * g.fs3] : 0.f;
     }
+  unsigned sink = 0;  // keeps the L2-prefetch loads alive (never stored: nch is positive)
   for (int64_t c = p.nch - 1; c >= 0; --c) {
     float* rec = record<D, DV, true>(p, b, h, c);
     const frag* kxf = reinterpret_cast<const frag*>(rec + F::KXF);
     const frag* ktf = reinterpret_cast<const frag*>(rec + F::KTF);
     const float l63 = rec[F::VEC + 63];
+    if (c > 0) {
+      // touch the previous chunk's operands so that its loads hit L2: the packed K (lines shared by the
+      // head's NV workgroups), Tp, P^T dY and this workgroup's 16 rows of H (one dword per 128-byte line)
+      const unsigned* pr = reinterpret_cast<const unsigned*>(record<D, DV, true>(p, b, h, c - 1));
+      const int idx = n * 256 + (int)threadIdx.x;
+      constexpr int KLINES = D * (int)sizeof(frag) / 16;
+      for (int l = idx; l < KLINES; l += 256 * NV) sink += pr[F::KXF + 32 * l] + pr[F::KTF + 32 * l];
+      if (idx < 128) sink += pr[F::TP + 32 * idx];
+      else if (idx < 128 + 2 * DV) sink += pr[R::RR + 32 * (idx - 128)];
+      for (int l = (int)threadIdx.x; l < 16 * D / 32; l += 256)
+        sink += pr[R::H1 + (int64_t)(16 * n + l / (D / 32)) * D + 32 * (l % (D / 32))];
+    }
     const f32x4 lr = *reinterpret_cast<const f32x4*>(rec + F::VEC + 16 * w + 4 * (lane >> 4));
     // Gamma at the chunk end; K Gamma, partial over this wave's features
     f32x4 xp[4];
 #pragma unroll
     for (int m = 0; m < 4; ++m) xp[m] = zero4();
+    float* grow = rec + R::GR + (int64_t)vc * D + FPW * w + 4 * (lane >> 4);
+    const float* hrow = rec + R::H1 + (int64_t)vc * D + FPW * w + 4 * (lane >> 4);
 #pragma unroll
     for (int jj = 0; jj < JPW; ++jj) {
 #pragma unroll
-      for (int u = 0; u < 2; ++u)
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          rec[R::GR + (int64_t)(FPW * w + 16 * (2 * jj + u) + 4 * (lane >> 4) + i) * DV + vc] = Gg[2 * jj + u][i];
+      for (int u = 0; u < 2; ++u) *reinterpret_cast<f32x4*>(grow + 16 * (2 * jj + u)) = Gg[2 * jj + u];
       const frag gb = PB::from_f32(pair_to8(Gg[2 * jj], Gg[2 * jj + 1]));
 #pragma unroll
       for (int m = 0; m < 4; ++m) xp[m] = PB::mma(xp[m], kxf[(m * (D / 32) + w * JPW + jj) * 64 + lane], gb);
@@ -630,14 +641,12 @@ __global__ void __launch_bounds__(256) gbwd_rchain_kernel(Params p, BwdP g) {
     const float gC = expf(l63);
 #pragma unroll
     for (int t = 0; t < TPW; ++t) {
-      f32x4 acc;
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        acc[i] = gC * Gg[t][i] + rec[R::H1 + (int64_t)(FPW * w + 16 * t + 4 * (lane >> 4) + i) * DV + vc];
+      const f32x4 acc = gC * Gg[t] + *reinterpret_cast<const f32x4*>(hrow + 16 * t);
       Gg[t] = PB::mma(PB::mma(acc, ktf[((w * TPW + t) * 2) * 64 + lane], zb0), ktf[((w * TPW + t) * 2 + 1) * 64 + lane],
                       zb1);
     }
   }
+  if (p.nch < 0) p.ws[0] = (float)sink;
   if (g.dinit) {
 #pragma unroll
     for (int t = 0; t < TPW; ++t)
@@ -665,7 +674,7 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
-template <typename InT, int D, int DV>
+template <class PB, typename InT, int D, int DV>
 __global__ void __launch_bounds__(256) gbwd_grad_kernel(Params p, BwdP g) {
   using F = Rec<D, DV>;
   using R = BRec<D, DV>;
@@ -797,16 +806,21 @@ __global__ void __launch_bounds__(256) gbwd_grad_kernel(Params p, BwdP g) {
   }
   {
     float dap[4] = {0.f, 0.f, 0.f, 0.f};
+    f32x4 qs[NV];
+#pragma unroll
+    for (int nv = 0; nv < NV; ++nv) qs[nv] = zero4();
+    for (int jb = 0; jb < D / 32; ++jb) {
+      const typename PB::frag qa = PB::from_f32(frag_rows_in(Qin, p.qs1, 16 * rt, 32 * jb, lane, nrows));
+#pragma unroll
+      for (int nv = 0; nv < NV; ++nv)
+        qs[nv] = PB::mma(qs[nv], qa, PB::from_f32(frag_rows(rec + R::SR, D, 16 * nv, 32 * jb, lane)));
+    }
 #pragma unroll
     for (int nv = 0; nv < NV; ++nv) {
-      f32x4 qs = zero4();
-      for (int jb = 0; jb < D / 32; ++jb)
-        qs = mm<PrecF32>(qs, frag_rows_in(Qin, p.qs1, 16 * rt, 32 * jb, lane, nrows),
-                         frag_cols(rec + R::SR, DV, 16 * nv, 32 * jb, lane));
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int ri = 16 * rt + 4 * (lane >> 4) + i;
-        if (ri < nrows) dap[i] += Yin[ri * g.ys1 + 16 * nv + (lane & 15)] * qs[i];
+        if (ri < nrows) dap[i] += Yin[ri * g.ys1 + 16 * nv + (lane & 15)] * qs[nv][i];
       }
     }
 #pragma unroll
@@ -910,11 +924,12 @@ __global__ void __launch_bounds__(256) gbwd_grad_kernel(Params p, BwdP g) {
 }
 
 // ---------------------------------------------------------------------------------------------- dphi
-// grid (nch * D / 256, H, B), 256 threads; workgroup (chunk, block of 256 features), wave w token tile w.
-template <typename InT, int D, int DV>
+// grid (nch * D / 256, H, B), 256 threads; workgroup (chunk, block of 256 features), wave w features
+// [64 w, 64 w + 64) of the block for all 64 tokens (each wave loads only its own features' operands).
+template <class PB, typename InT, int D, int DV>
 __global__ void __launch_bounds__(256) gbwd_dphi_kernel(Params p, BwdP g) {
   using R = BRec<D, DV>;
-  constexpr int FB = 256, NFT = FB / 16;
+  constexpr int FB = 256;
   const int64_t c = blockIdx.x / (D / FB), h = blockIdx.y, b = blockIdx.z;
   const int fb = (int)(blockIdx.x % (D / FB));
   const int lane = threadIdx.x & 63;
@@ -924,49 +939,66 @@ __global__ void __launch_bounds__(256) gbwd_dphi_kernel(Params p, BwdP g) {
   const int nrows = (int)(p.T - t0 < C ? p.T - t0 : C);
   const InT* Qin = reinterpret_cast<const InT*>(p.q) + b * p.qs0 + t0 * p.qs1 + h * p.qs2;
   const InT* Kin = reinterpret_cast<const InT*>(p.k) + b * p.ks0 + t0 * p.ks1 + h * p.ks2;
-  f32x4 aq[NFT], ak[NFT];
+  const int f0 = fb * FB + 64 * w;
+  f32x4 aq[4][4], ak[4][4];  // [token tile][feature tile]
 #pragma unroll
-  for (int ft = 0; ft < NFT; ++ft) aq[ft] = ak[ft] = zero4();
+  for (int m = 0; m < 4; ++m)
+#pragma unroll
+    for (int ft = 0; ft < 4; ++ft) aq[m][ft] = ak[m][ft] = zero4();
   // contractions over the value columns: (a o dY) S, (kappa o W) Gamma^T, -Z S
   for (int kb = 0; kb < DV / 32; ++kb) {
-    const f32x8 ay = frag_rows(rec + R::AY, DV, 16 * w, 32 * kb, lane);
-    const f32x8 kw = frag_rows(rec + R::KW, DV, 16 * w, 32 * kb, lane);
-    const f32x8 zn = frag_rows(rec + R::ZN, DV, 16 * w, 32 * kb, lane);
+    f32x8 sb[4], gb[4];
 #pragma unroll
-    for (int ft = 0; ft < NFT; ++ft) {
-      const int f0 = fb * FB + 16 * ft;
-      const f32x8 s = frag_rows(rec + R::SR, DV, f0, 32 * kb, lane);
-      const f32x8 gm = frag_rows(rec + R::GR, DV, f0, 32 * kb, lane);
-      aq[ft] = mm<PrecF32>(aq[ft], ay, s);
-      ak[ft] = mm<PrecF32>(mm<PrecF32>(ak[ft], kw, gm), zn, s);
+    for (int ft = 0; ft < 4; ++ft) {
+      sb[ft] = frag_cols(rec + R::SR, D, f0 + 16 * ft, 32 * kb, lane);
+      gb[ft] = frag_cols(rec + R::GR, D, f0 + 16 * ft, 32 * kb, lane);
+    }
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      const f32x8 ay = frag_rows(rec + R::AY, DV, 16 * m, 32 * kb, lane);
+      const f32x8 kw = frag_rows(rec + R::KW, DV, 16 * m, 32 * kb, lane);
+      const f32x8 zn = frag_rows(rec + R::ZN, DV, 16 * m, 32 * kb, lane);
+#pragma unroll
+      for (int ft = 0; ft < 4; ++ft) {
+        aq[m][ft] = mm<PB>(aq[m][ft], ay, sb[ft]);
+        ak[m][ft] = mm<PB>(mm<PB>(ak[m][ft], kw, gb[ft]), zn, sb[ft]);
+      }
     }
   }
   // contractions over the chunk's tokens: N K, (M + M^T) K, N^T Q
   for (int kb = 0; kb < 2; ++kb) {
-    const f32x8 nr = frag_rows(rec + R::NN, C, 16 * w, 32 * kb, lane);
-    const f32x8 mr = frag_rows(rec + R::MM, C, 16 * w, 32 * kb, lane);
-    const f32x8 nt = frag_cols(rec + R::NN, C, 16 * w, 32 * kb, lane);
+    f32x8 kf[4], qf[4];
 #pragma unroll
-    for (int ft = 0; ft < NFT; ++ft) {
-      const int f0 = fb * FB + 16 * ft;
-      const f32x8 kf = frag_cols_in(Kin, p.ks1, f0, 32 * kb, lane, nrows);
-      const f32x8 qf = frag_cols_in(Qin, p.qs1, f0, 32 * kb, lane, nrows);
-      aq[ft] = mm<PrecF32>(aq[ft], nr, kf);
-      ak[ft] = mm<PrecF32>(mm<PrecF32>(ak[ft], mr, kf), nt, qf);
+    for (int ft = 0; ft < 4; ++ft) {
+      kf[ft] = frag_cols_in(Kin, p.ks1, f0 + 16 * ft, 32 * kb, lane, nrows);
+      qf[ft] = frag_cols_in(Qin, p.qs1, f0 + 16 * ft, 32 * kb, lane, nrows);
+    }
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      const f32x8 nr = frag_rows(rec + R::NN, C, 16 * m, 32 * kb, lane);
+      const f32x8 mr = frag_rows(rec + R::MM, C, 16 * m, 32 * kb, lane);
+      const f32x8 nt = frag_cols(rec + R::NN, C, 16 * m, 32 * kb, lane);
+#pragma unroll
+      for (int ft = 0; ft < 4; ++ft) {
+        aq[m][ft] = mm<PB>(aq[m][ft], nr, kf[ft]);
+        ak[m][ft] = mm<PB>(mm<PB>(ak[m][ft], mr, kf[ft]), nt, qf[ft]);
+      }
     }
   }
 #pragma unroll
-  for (int ft = 0; ft < NFT; ++ft)
+  for (int m = 0; m < 4; ++m)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int ri = 16 * w + 4 * (lane >> 4) + i;
-      if (ri < nrows) {
-        const int64_t t = t0 + ri;
-        const int f = fb * FB + 16 * ft + (lane & 15);
-        g.dq[b * g.dqs0 + t * g.dqs1 + h * g.dqs2 + f] = aq[ft][i];
-        g.dk[b * g.dks0 + t * g.dks1 + h * g.dks2 + f] = ak[ft][i];
+    for (int ft = 0; ft < 4; ++ft)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int ri = 16 * m + 4 * (lane >> 4) + i;
+        if (ri < nrows) {
+          const int64_t t = t0 + ri;
+          const int f = f0 + 16 * ft + (lane & 15);
+          g.dq[b * g.dqs0 + t * g.dqs1 + h * g.dqs2 + f] = aq[m][ft][i];
+          g.dk[b * g.dks0 + t * g.dks1 + h * g.dks2 + f] = ak[m][ft][i];
+        }
       }
-    }
 }
 
 template <class PB, typename InT, int D, int DV>
@@ -977,8 +1009,8 @@ static int launch_bwd(const Params& p, const BwdP& g, hipStream_t st) {
   hipLaunchKernelGGL((gen_carry_kernel<PB, D, DV, true>), dim3(carry_wgs), dim3(256), 0, st, p);
   hipLaunchKernelGGL((gbwd_rh_kernel<PB, InT, D, DV>), chunk_grid, dim3(256), 0, st, p, g);
   hipLaunchKernelGGL((gbwd_rchain_kernel<PB, D, DV>), dim3(carry_wgs), dim3(256), 0, st, p, g);
-  hipLaunchKernelGGL((gbwd_grad_kernel<InT, D, DV>), chunk_grid, dim3(256), 0, st, p, g);
-  hipLaunchKernelGGL((gbwd_dphi_kernel<InT, D, DV>), dim3((unsigned)(p.nch * (D / 256)), (unsigned)p.H, (unsigned)p.B),
+  hipLaunchKernelGGL((gbwd_grad_kernel<PB, InT, D, DV>), chunk_grid, dim3(256), 0, st, p, g);
+  hipLaunchKernelGGL((gbwd_dphi_kernel<PB, InT, D, DV>), dim3((unsigned)(p.nch * (D / 256)), (unsigned)p.H, (unsigned)p.B),
                      dim3(256), 0, st, p, g);
   return launch_status();
 }

@@ -521,103 +521,152 @@ extern "C" int kdn_fwht_lift_factored(const void* x, int64_t rows, int64_t x_row
 }
 
 namespace kdn {
-// Backward of the factored lift: dx = d out / d x applied to dout, eight rows per workgroup.  The angles
-// theta = inv_tau (Omega_h x_h) + b_h of both halves are recomputed in fp32 (a thread per feature, its
-// Omega row in registers, all eight rows); per row (wave w: rows w and w + 4) the outer renormalisation,
-// the halves' renormalisations and the cosine are differentiated in place of the angles (dL/dtheta);
-// then dx_h = inv_tau Omega_h^T dL/dtheta_h (a thread per input column, Omega read row by row, so that a
-// wave's 64 reads of a row are one 128-byte line).  Per-row sums are wave reductions in a fixed order.
-constexpr int FLB_ROWS = 8;
-
-template <typename InT>
+constexpr int FLB_TILES = 2;
+// Backward of the factored lift: dx = (d out / d x)^T dout, one wave per 16 x FLB_TILES rows.  Each wave forms the
+// transposed angles theta^T = Omega_h x_h^T (features x rows) on MFMA, feature tile by feature tile, so
+// that a lane holds four consecutive features of one row (16-byte loads of the phases and of dout), and
+// needs two passes over them:
+//   1. per half h and row: n_h^2 = sum cs^2 and t_h = sum cs g (cs = sqrt(2/512) cos theta, g = dout);
+//      the renormalisations' backward needs only these four sums per row:
+//        E = |c| + 1e-7 with |c|^2 = sum_h n_h^2 / e_h^2, e_h = n_h + 1e-8, c = cs / e_h;
+//        dc = g / E - c (c . g) / (E^2 |c|);  s_h = cs . dc = t_h / E - (c . g) / (E^2 |c|) n_h^2 / e_h;
+//        dphi~ = dc / e_h - cs s_h / (e_h^2 n_h)
+//   2. dL/dtheta = -sqrt(2/512) sin(theta) dphi~, and dx_h^T += Omega_h^T dtheta^T: the accumulator
+//      tiles of two feature tiles are the B operand of that product as they stand (kappa order).
+// A wave takes FLB_TILES row tiles, so that each Omega fragment it loads feeds that many products.
+// Per-row sums run over the four lane groups in a fixed order.  Products take the precision policy P
+// (bf16 operands for bf16 inputs: x and Omega are exact in bf16, so the angles equal the forward's).
+template <class P, typename InT>
 __global__ void __launch_bounds__(256) lift_factored_bwd_kernel(const InT* x, int64_t rows, int64_t xs,
                                                                 const __bf16* om1, const float* ph1,
                                                                 const __bf16* om2, const float* ph2, float inv_tau,
                                                                 const float* dout, int64_t ds, float* dx,
                                                                 int64_t dxs) {
-  __shared__ float s_x[FLB_ROWS][128];
-  __shared__ float s_th[FLB_ROWS][1024];  // theta, then dL/dtheta
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int64_t r0 = (int64_t)blockIdx.x * FLB_ROWS;
-  for (int idx = tid; idx < FLB_ROWS * 128; idx += 256) {
-    const int r = idx >> 7, j = idx & 127;
-    s_x[r][j] = (r0 + r < rows) ? (float)x[(r0 + r) * xs + j] : 0.f;
+  using frag = typename P::frag;
+  constexpr int RT = FLB_TILES;  // 16-row tiles per wave: each Omega fragment feeds RT products
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int64_t r0 = ((int64_t)blockIdx.x * 4 + w) * 16 * RT;
+  if (r0 >= rows) return;  // wave-uniform; the kernel has no barriers
+  const int fq = 4 * (lane >> 4);  // this lane's first feature inside a 16-feature tile
+  int64_t row[RT];
+  bool valid[RT];
+  frag xb[RT][2][2];  // x^T as B fragments: row tile, half h, 32-deep block kb
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) {
+    row[rt] = r0 + 16 * rt + (lane & 15);
+    valid[rt] = row[rt] < rows;
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        f32x8 v;
+#pragma unroll
+        for (int s = 0; s < 8; ++s)
+          v[s] = valid[rt] ? (float)x[row[rt] * xs + 64 * h + 32 * kb + kappa(lane, s)] : 0.f;
+        xb[rt][h][kb] = P::from_f32(v);
+      }
   }
-  __syncthreads();
-  for (int u = 0; u < 4; ++u) {
-    const int f = tid + 256 * u, hf = f >> 9, fl = f & 511;
-    const __bf16* om = (hf ? om2 : om1) + fl * 64;
-    float wv[64];
-#pragma unroll
-    for (int j8 = 0; j8 < 8; ++j8) load8<__bf16>(om + 8 * j8, wv + 8 * j8);
-    const float ph = (hf ? ph2 : ph1)[fl];
-#pragma unroll
-    for (int r = 0; r < FLB_ROWS; ++r) {
-      float acc = 0.f;
-#pragma unroll
-      for (int j = 0; j < 64; ++j) acc += wv[j] * s_x[r][64 * hf + j];
-      s_th[r][f] = acc * inv_tau + ph;
-    }
-  }
-  __syncthreads();
   const float amp = sqrtf(2.f / 512.f);
-  for (int rr = 0; rr < 2; ++rr) {
-    const int r = w + 4 * rr;
-    const bool valid = r0 + r < rows;
-    // feature f = lane + 64 k of the row; k < 8 the first half
-    float cs[16], sn[16], g[16];
-    float n1 = 0.f, n2 = 0.f;
+  // pass 1
+  float n2[RT][2], tg[RT][2];
 #pragma unroll
-    for (int k = 0; k < 16; ++k) {
-      const float th = s_th[r][lane + 64 * k];
-      cs[k] = amp * cos_rad(th);
-      sn[k] = amp * sin_rad(th);
-      g[k] = valid ? dout[(r0 + r) * ds + lane + 64 * k] : 0.f;
-      if (k < 8) n1 += cs[k] * cs[k];
-      else n2 += cs[k] * cs[k];
-    }
-    n1 = sqrtf(wave_sum64(n1));
-    n2 = sqrtf(wave_sum64(n2));
-    const float e1 = n1 + 1e-8f, e2 = n2 + 1e-8f;
-    float c[16], nn = 0.f, sc = 0.f;
+  for (int rt = 0; rt < RT; ++rt) n2[rt][0] = n2[rt][1] = tg[rt][0] = tg[rt][1] = 0.f;
 #pragma unroll
-    for (int k = 0; k < 16; ++k) {
-      c[k] = cs[k] / (k < 8 ? e1 : e2);
-      nn += c[k] * c[k];
-      sc += c[k] * g[k];
-    }
-    const float N = sqrtf(wave_sum64(nn));
-    sc = wave_sum64(sc);
-    const float E = N + 1e-7f;
-    const float corr = N > 0.f ? sc / (E * E * N) : 0.f;
-    float s1 = 0.f, s2 = 0.f;
+  for (int h = 0; h < 2; ++h) {
+    const __bf16* om = h ? om2 : om1;
+    const float* ph = h ? ph2 : ph1;
+    for (int ft = 0; ft < 32; ++ft) {
+      const int f0 = 16 * ft;
+      const frag oa0 = P::from_f32(frag_rows_bf16(om, 64, f0, 0, lane));
+      const frag oa1 = P::from_f32(frag_rows_bf16(om, 64, f0, 32, lane));
+      const f32x4 b4 = *reinterpret_cast<const f32x4*>(ph + f0 + fq);
 #pragma unroll
-    for (int k = 0; k < 16; ++k) {
-      g[k] = g[k] / E - c[k] * corr;  // dL/d(concatenated halves)
-      if (k < 8) s1 += cs[k] * g[k];
-      else s2 += cs[k] * g[k];
-    }
-    s1 = wave_sum64(s1);
-    s2 = wave_sum64(s2);
-    const float k1 = n1 > 0.f ? s1 / (e1 * e1 * n1) : 0.f, k2 = n2 > 0.f ? s2 / (e2 * e2 * n2) : 0.f;
+      for (int rt = 0; rt < RT; ++rt) {
+        const f32x4 acc = P::mma(P::mma(zero4(), oa0, xb[rt][h][0]), oa1, xb[rt][h][1]);
+        const f32x4 g4 =
+            valid[rt] ? *reinterpret_cast<const f32x4*>(dout + row[rt] * ds + 512 * h + f0 + fq) : zero4();
 #pragma unroll
-    for (int k = 0; k < 16; ++k) {
-      const float dphit = k < 8 ? g[k] / e1 - cs[k] * k1 : g[k] / e2 - cs[k] * k2;
-      s_th[r][lane + 64 * k] = -sn[k] * dphit;
+        for (int i = 0; i < 4; ++i) {
+          const float cs = amp * cos_rad(acc[i] * inv_tau + b4[i]);
+          n2[rt][h] += cs * cs;
+          tg[rt][h] += cs * g4[i];
+        }
+      }
     }
   }
-  __syncthreads();
-  const int j = tid & 63, rg = tid >> 6;
-  for (int hf = 0; hf < 2; ++hf) {
-    const __bf16* om = hf ? om2 : om1;
-    float a0 = 0.f, a1 = 0.f;
-    for (int fl = 0; fl < 512; ++fl) {
-      const float wv = (float)om[fl * 64 + j];
-      a0 += wv * s_th[rg][512 * hf + fl];
-      a1 += wv * s_th[rg + 4][512 * hf + fl];
+  // per row: 1/e_h, 1/E, and the coefficients of dphi~ = g / (E e_h) - cs (corr / e_h^2 + k_h)
+  float ie[RT][2], ca[RT][2], cb[RT][2];
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) {
+    float nn[2], e[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      n2[rt][h] = sum_over_lane_groups(n2[rt][h]);
+      tg[rt][h] = sum_over_lane_groups(tg[rt][h]);
+      nn[h] = sqrtf(n2[rt][h]);
+      e[h] = nn[h] + 1e-8f;
+      ie[rt][h] = 1.f / e[h];
     }
-    if (r0 + rg < rows) dx[(r0 + rg) * dxs + 64 * hf + j] = inv_tau * a0;
-    if (r0 + rg + 4 < rows) dx[(r0 + rg + 4) * dxs + 64 * hf + j] = inv_tau * a1;
+    const float cn = sqrtf(n2[rt][0] * ie[rt][0] * ie[rt][0] + n2[rt][1] * ie[rt][1] * ie[rt][1]);
+    const float iE = 1.f / (cn + 1e-7f);
+    const float sc = tg[rt][0] * ie[rt][0] + tg[rt][1] * ie[rt][1];
+    const float corr = cn > 0.f ? sc * iE * iE / cn : 0.f;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const float sh = tg[rt][h] * iE - corr * n2[rt][h] * ie[rt][h];
+      const float kh = nn[h] > 0.f ? sh * ie[rt][h] * ie[rt][h] / nn[h] : 0.f;
+      ca[rt][h] = iE * ie[rt][h];                   // times g
+      cb[rt][h] = corr * ie[rt][h] * ie[rt][h] + kh;  // times cs
+    }
+  }
+  // pass 2
+  f32x4 dxt[RT][2][4];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const __bf16* om = h ? om2 : om1;
+    const float* ph = h ? ph2 : ph1;
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+      for (int jt = 0; jt < 4; ++jt) dxt[rt][h][jt] = zero4();
+    for (int fb = 0; fb < 16; ++fb) {
+      f32x4 dth[RT][2];
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int f0 = 32 * fb + 16 * u;
+        const frag oa0 = P::from_f32(frag_rows_bf16(om, 64, f0, 0, lane));
+        const frag oa1 = P::from_f32(frag_rows_bf16(om, 64, f0, 32, lane));
+        const f32x4 b4 = *reinterpret_cast<const f32x4*>(ph + f0 + fq);
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) {
+          const f32x4 acc = P::mma(P::mma(zero4(), oa0, xb[rt][h][0]), oa1, xb[rt][h][1]);
+          const f32x4 g4 =
+              valid[rt] ? *reinterpret_cast<const f32x4*>(dout + row[rt] * ds + 512 * h + f0 + fq) : zero4();
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float th = acc[i] * inv_tau + b4[i];
+            const float cs = amp * cos_rad(th), sn = amp * sin_rad(th);
+            dth[rt][u][i] = -sn * (g4[i] * ca[rt][h] - cs * cb[rt][h]);
+          }
+        }
+      }
+#pragma unroll
+      for (int jt = 0; jt < 4; ++jt) {
+        const frag ot = P::from_f32(frag_cols_bf16(om, 64, 16 * jt, 32 * fb, lane));
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) dxt[rt][h][jt] = P::mma(dxt[rt][h][jt], ot, P::from_f32(pair_to8(dth[rt][0], dth[rt][1])));
+      }
+    }
+  }
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) {
+    if (valid[rt]) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int jt = 0; jt < 4; ++jt)
+          *reinterpret_cast<f32x4*>(dx + row[rt] * dxs + 64 * h + 16 * jt + fq) = inv_tau * dxt[rt][h][jt];
+    }
   }
 }
 }  // namespace kdn
@@ -631,23 +680,23 @@ extern "C" int kdn_fwht_lift_factored_bwd(const void* x, int64_t rows, int64_t x
   if (!valid_dtype(x_dtype)) return KDN_ERR_INVALID_ARGUMENT;
   if (x_row_stride < 128 || dout_row_stride < 1024 || dx_row_stride < 128) return KDN_ERR_INVALID_ARGUMENT;
   if (!(inv_tau == inv_tau)) return KDN_ERR_INVALID_ARGUMENT;
-  // Omega rows are read 16 bytes at a time; everything else element by element
-  if (!aligned(omega1_bf16, 16) || !aligned(omega2_bf16, 16)) return KDN_ERR_MISALIGNED;
-  if (!aligned(x, dtype_size(x_dtype)) || !aligned(phase1, 4) || !aligned(phase2, 4) || !aligned(dout, 4) ||
-      !aligned(dx, 4))
+  // phases, dout and dx rows are read and written 16 bytes at a time, Omega rows 8 bytes at a time
+  if (!aligned(omega1_bf16, 8) || !aligned(omega2_bf16, 8) || !aligned(x, dtype_size(x_dtype))) return KDN_ERR_MISALIGNED;
+  if (!aligned(phase1, 16) || !aligned(phase2, 16) || !aligned(dout, 16) || !aligned(dx, 16) || dout_row_stride % 4 ||
+      dx_row_stride % 4)
     return KDN_ERR_MISALIGNED;
   if (rows == 0) return KDN_OK;
-  const int64_t wgs = (rows + FLB_ROWS - 1) / FLB_ROWS;
+  const int64_t wgs = (rows + 64 * FLB_TILES - 1) / (64 * FLB_TILES);
   if (wgs > 0x7fffffff) return KDN_ERR_UNSUPPORTED;
   const hipStream_t st = as_stream(stream);
   const __bf16* o1 = static_cast<const __bf16*>(omega1_bf16);
   const __bf16* o2 = static_cast<const __bf16*>(omega2_bf16);
   if (x_dtype == KDN_DTYPE_BF16)
-    hipLaunchKernelGGL(lift_factored_bwd_kernel<__bf16>, dim3((unsigned)wgs), dim3(256), 0, st,
+    hipLaunchKernelGGL((lift_factored_bwd_kernel<PrecBF16, __bf16>), dim3((unsigned)wgs), dim3(256), 0, st,
                        static_cast<const __bf16*>(x), rows, x_row_stride, o1, phase1, o2, phase2, inv_tau, dout,
                        dout_row_stride, dx, dx_row_stride);
   else
-    hipLaunchKernelGGL(lift_factored_bwd_kernel<float>, dim3((unsigned)wgs), dim3(256), 0, st,
+    hipLaunchKernelGGL((lift_factored_bwd_kernel<PrecF32, float>), dim3((unsigned)wgs), dim3(256), 0, st,
                        static_cast<const float*>(x), rows, x_row_stride, o1, phase1, o2, phase2, inv_tau, dout,
                        dout_row_stride, dx, dx_row_stride);
   return launch_status();

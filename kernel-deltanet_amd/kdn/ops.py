@@ -159,6 +159,8 @@ def lift_factored_backward(x: torch.Tensor, dphi: torch.Tensor, omega1: torch.Te
     dev = x.device
     x2 = _rows(x, 128)
     g2 = _rows(dphi.to(device=dev, dtype=torch.float32), 1024)
+    if g2.data_ptr() % 16 or g2.stride(0) % 4:
+        g2 = g2.contiguous()
     o1, o2 = omega1.to(device=dev).contiguous(), omega2.to(device=dev).contiguous()
     p1 = phase1.to(device=dev, dtype=torch.float32).contiguous()
     p2 = phase2.to(device=dev, dtype=torch.float32).contiguous()

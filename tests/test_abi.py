@@ -256,7 +256,9 @@ def test_factored_lift_backward_errors_need_no_device(lib):
     assert fb(*ok[:1], -1, *ok[2:]) == -1
     assert fb(*ok[:2], 64, *ok[3:]) == -1                                # x rows of 128
     assert fb(*ok[:3], 7, *ok[4:]) == -1                                 # dtype
-    assert fb(*ok[:4], p + 8, *ok[5:]) == -4                             # Omega 16-byte aligned
+    assert fb(*ok[:4], p + 4, *ok[5:]) == -4                             # Omega 8-byte aligned
+    assert fb(*ok[:5], p + 8, *ok[6:]) == -4                             # phases 16-byte aligned
+    assert fb(*ok[:10], 1026, *ok[11:]) == -4                            # dout rows of 16-byte multiples
     assert fb(*ok[:8], float("nan"), *ok[9:]) == -1
     assert fb(*ok[:10], 512, *ok[11:]) == -1                             # dout rows of 1024
     assert fb(*ok[:9], p + 2, *ok[10:]) == -4                            # fp32 dout

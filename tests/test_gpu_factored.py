@@ -123,14 +123,15 @@ def test_factored_scan_single_partial_chunk(fproj, oprojs):
 # factored-lift oracle, gradcheck-pinned in test_oracle_factored.py) and oracle.scan.token_recurrence_torch
 # (gradcheck-pinned in test_oracle_backward.py) -- the role the reference gives torch autograd over its
 # chunked forward.  Tolerances (relative L2): 1e-4 for fp32 inputs, 2e-2 for bf16 inputs; the lift's
-# backward alone 1e-5 (it recomputes the lift in fp32 from bf16-exact inputs).
+# backward alone 1e-5 for fp32 inputs and 5e-3 for bf16 inputs (whose dL/dtheta is rounded to bf16 for
+# the product with Omega, the bf16 policy of every feature contraction of the backward).
 
 def _t64(x):
     return torch.as_tensor(np.asarray(x, dtype=np.float64))
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_factored_lift_backward(fproj, oprojs, dtype):
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-5), (torch.bfloat16, 5e-3)])
+def test_factored_lift_backward(fproj, oprojs, dtype, tol):
     g = torch.Generator().manual_seed(11)
     x = torch.randn(3, 20, 128, generator=g).to(dtype)
     dphi = torch.randn(3, 20, 1024, generator=g)
@@ -141,7 +142,7 @@ def test_factored_lift_backward(fproj, oprojs, dtype):
     xr = x.double().requires_grad_(True)
     (osc.factored_lift_torch(xr, *oprojs) * dphi.double()).sum().backward()
     assert dx.shape == x.shape and dx.dtype == torch.float32
-    assert rel(dx.cpu().numpy(), xr.grad.numpy()) < 1e-5
+    assert rel(dx.cpu().numpy(), xr.grad.numpy()) < tol
 
 
 def _prelifted_case(B, T, dv, dtype, oprojs, seed):
