@@ -67,8 +67,7 @@ struct Rec {
   static constexpr size_t TPT = TP + C * C;     // [64][64] Tp^T
   static constexpr size_t P = TPT + C * C;      // [64][64]
   static constexpr size_t GKK = P + C * C;      // [64][64] K K^T
-  static constexpr size_t GQK = GKK + C * C;    // [64][64] Q K^T
-  static constexpr size_t U = GQK + C * C;      // U~ = T (beta o V) as tiles [m 4][n 4][lane] f32x4
+  static constexpr size_t U = GKK + C * C;      // U~ = T (beta o V) as tiles [m 4][n 4][lane] f32x4
   static constexpr size_t R = U + C * DV;       // P^T dY, tiles as U~
   static constexpr size_t W = R + C * DV;       // [64][64] W = U~ - Tp X_K
   static constexpr size_t XK = W + C * DV;      // [64][64] K S^T
@@ -471,7 +470,6 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
       for (int i = 0; i < 4; ++i) {
         const int ri = 16 * w + 4 * (lane >> 4) + i, cj = 16 * n + (lane & 15);
         rec[Rec::GKK + ri * C + cj] = gkk[n][i];
-        rec[Rec::GQK + ri * C + cj] = gqk[n][i];
         const float li = s_ell[ri], lj = s_ell[cj], lim1 = ri > 0 ? s_ell[ri - 1] : 0.f;
         // A transposed for the column-oriented inverse below: [j][p][s] = A[4s+p][j]
         // (the linear rule has no erasure coupling: A = 0, so T = I and Tp = 0 below)
