@@ -225,3 +225,26 @@ def test_factored_module_gradients(fproj, oprojs, dtype):
     for name, a, r in zip(("dq", "dk", "dv", "dbeta", "ddecay", "dS0"), leaves, refs):
         assert a.grad is not None and a.grad.dtype == a.dtype, name
         assert rel(a.grad.float().cpu().numpy(), r.grad.numpy()) < tol, name
+
+
+def test_d1024_scan_backward_two_heads_without_decay(oprojs):
+    # head indexing of every record and gradient (H = 2 in the (B, T, H, .) layout), no decay, no initial
+    # state and no dL/dS_T (their NULL paths), a partial last chunk
+    g = torch.Generator().manual_seed(21)
+    B, T, H, dv = 1, 130, 2, 64
+    pq = torch.from_numpy(ol.factored_lift(torch.randn(B, T, H, 128, generator=g).numpy(), *oprojs)).float()
+    pk = torch.from_numpy(ol.factored_lift(torch.randn(B, T, H, 128, generator=g).numpy(), *oprojs)).float()
+    v = torch.randn(B, T, H, dv, generator=g)
+    beta = torch.sigmoid(torch.randn(B, T, H, generator=g))
+    dy = torch.randn(B, T, H, dv, generator=g)
+    plan = ops.ScanBackwardPlan(pq.to(DEV), pk.to(DEV), v.to(DEV), beta.to(DEV), None, None, None, 1.0, dy.to(DEV),
+                                need_dinit=False, features=ops.FeatureMap(lifted=True))
+    dq, dk, dvv, dbeta, ddecay, dinit = plan.run()
+    torch.cuda.synchronize()
+    assert ddecay is None and dinit is None
+    for h in range(H):
+        leaves = [t[:, :, h].double().requires_grad_(True) for t in (pq, pk, v, beta)]
+        Y, _ = osc.token_recurrence_torch(*leaves)
+        (Y * dy[:, :, h].double()).sum().backward()
+        for name, a, r in zip(("dphi_q", "dphi_k", "dv", "dbeta"), (dq, dk, dvv, dbeta), leaves):
+            assert rel(a[:, :, h].cpu().numpy(), r.grad.numpy()) < 1e-4, (h, name)
