@@ -486,8 +486,9 @@ static size_t record_floats(int D, int DV) {
 //   dphi    (parallel, 256 features per workgroup)
 //                                        dphi_q = (a o dY) S + N K
 //                                        dphi_k = (kappa o W) Gamma^T - Z S + (M + M^T) K + N^T Q
-// with S the chunk-start state (D x d_v transposed: the d_v x D matrix of the recurrence), N_ij =
-// dP_ij g_{i-1}/g_j and M_ij = dA_ij beta_i g_i/g_j below the diagonal, dP = dY W^T, dA = -T^T dT T^T.
+// with S the chunk-start state as the recurrence's d_v x D matrix (the carries hold S^T, D x d_v),
+// N_ij = dP_ij g_{i-1}/g_j and M_ij = dA_ij beta_i g_i/g_j below the diagonal, dP = dY W^T and
+// dA = -T^T dT T^T.
 // The contractions that involve the features (the carries, H, Q S^T and the feature gradients) take the
 // forward's precision policy (bf16 operands with fp32 accumulation for bf16 inputs, as the D = 512
 // backward); the 64 x 64 chunk algebra runs on fp32 MFMA.  Every reduction has a fixed order (no
