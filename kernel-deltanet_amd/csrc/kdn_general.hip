@@ -598,12 +598,21 @@ __global__ void __launch_bounds__(256) gbwd_rchain_kernel(Params p, BwdP g) {
         sink += pr[R::H1 + (int64_t)(16 * n + l / (D / 32)) * D + 32 * (l % (D / 32))];
     }
     const f32x4 lr = *reinterpret_cast<const f32x4*>(rec + F::VEC + 16 * w + 4 * (lane >> 4));
+    // the step's small operands and this wave's rows of H, issued first so that their latency overlaps
+    // the K Gamma products instead of following the last barrier
+    float* grow = rec + R::GR + (int64_t)vc * D + FPW * w + 4 * (lane >> 4);
+    const float* hrow = rec + R::H1 + (int64_t)vc * D + FPW * w + 4 * (lane >> 4);
+    f32x4 hv[TPW];
+#pragma unroll
+    for (int t = 0; t < TPW; ++t) hv[t] = *reinterpret_cast<const f32x4*>(hrow + 16 * t);
+    const f32x8 ta0 = frag_cols(rec + F::TP, C, 16 * w, 0, lane), ta1 = frag_cols(rec + F::TP, C, 16 * w, 32, lane);
+    f32x4 rr;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) rr[i] = rec[R::RR + (16 * w + 4 * (lane >> 4) + i) * DV + vc];
     // Gamma at the chunk end; K Gamma, partial over this wave's features
     f32x4 xp[4];
 #pragma unroll
     for (int m = 0; m < 4; ++m) xp[m] = zero4();
-    float* grow = rec + R::GR + (int64_t)vc * D + FPW * w + 4 * (lane >> 4);
-    const float* hrow = rec + R::H1 + (int64_t)vc * D + FPW * w + 4 * (lane >> 4);
 #pragma unroll
     for (int jj = 0; jj < JPW; ++jj) {
 #pragma unroll
@@ -621,14 +630,13 @@ __global__ void __launch_bounds__(256) gbwd_rchain_kernel(Params p, BwdP g) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int ri = 16 * w + 4 * (lane >> 4) + i;
-      dw[i] = rec[R::RR + ri * DV + vc] + expf(l63 - lr[i]) * X[i];
+      dw[i] = rr[i] + expf(l63 - lr[i]) * X[i];
       rec[R::X + ri * DV + vc] = X[i];
       rec[R::DW + ri * DV + vc] = dw[i];
     }
     sh.z[w][lane] = dw;
     __syncthreads();
     // token tile w of Z = Tp^T dW (stored negated: dL/dX_K)
-    const f32x8 ta0 = frag_cols(rec + F::TP, C, 16 * w, 0, lane), ta1 = frag_cols(rec + F::TP, C, 16 * w, 32, lane);
     const f32x4 Z = mm<PrecF32>(mm<PrecF32>(zero4(), ta0, pair_to8(sh.z[0][lane], sh.z[1][lane])), ta1,
                                 pair_to8(sh.z[2][lane], sh.z[3][lane]));
     const f32x4 zn = -Z;
@@ -642,7 +650,7 @@ __global__ void __launch_bounds__(256) gbwd_rchain_kernel(Params p, BwdP g) {
     const float gC = expf(l63);
 #pragma unroll
     for (int t = 0; t < TPW; ++t) {
-      const f32x4 acc = gC * Gg[t] + *reinterpret_cast<const f32x4*>(hrow + 16 * t);
+      const f32x4 acc = gC * Gg[t] + hv[t];
       Gg[t] = PB::mma(PB::mma(acc, ktf[((w * TPW + t) * 2) * 64 + lane], zb0), ktf[((w * TPW + t) * 2 + 1) * 64 + lane],
                       zb1);
     }
@@ -684,7 +692,7 @@ __global__ void __launch_bounds__(256) gbwd_grad_kernel(Params p, BwdP g) {
   __shared__ __attribute__((aligned(16))) float bD[C * LD];   // dT
   __shared__ __attribute__((aligned(16))) float bY1[C * LD];  // dT T^T
   __shared__ float s_ell[C], s_beta[C];
-  __shared__ float s_dl[GNDL][C], s_db[GNDB][C], s_ts[4][C], s_63[5];
+  __shared__ float s_dl[GNDL][C], s_db[GNDB][C], s_ts[4][C], s_kt[C], s_63[5];
 
   const int64_t c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x, lane = tid & 63;
@@ -782,22 +790,31 @@ __global__ void __launch_bounds__(256) gbwd_grad_kernel(Params p, BwdP g) {
       if ((lane & 15) == 0) s_db[GDB_V][ri] = s;
     }
   }
-  if (w == 0) {
-    // the kappa term (row `lane`): dkappa_i = W_i . X_i; and kappa o W for the feature gradients
-    const int r = lane;
+  {
+    // the kappa term: dkappa_i = W_i . X_i (row tid / 4, a quarter of the columns per thread, the quad's
+    // four partials added in a fixed order); and kappa o W for the feature gradients
+    const int r = tid >> 2, q0 = (tid & 3) * (DV / 4);
     const float kap = expf(l63 - s_ell[r]);
     float dk = 0.f;
-    for (int v = 0; v < DV; ++v) {
-      const float wv = rec[F::W + r * DV + v];
-      dk += wv * rec[R::X + r * DV + v];
-      rec[R::KW + r * DV + v] = kap * wv;
+#pragma unroll 4
+    for (int v = q0; v < q0 + DV / 4; v += 4) {
+      const f32x4 wv = *reinterpret_cast<const f32x4*>(rec + F::W + r * DV + v);
+      const f32x4 xv = *reinterpret_cast<const f32x4*>(rec + R::X + r * DV + v);
+      dk += wv[0] * xv[0] + wv[1] * xv[1] + wv[2] * xv[2] + wv[3] * xv[3];
+      *reinterpret_cast<f32x4*>(rec + R::KW + r * DV + v) = kap * wv;
     }
-    const float t = dk * kap;
-    s_dl[GDL_K][r] = -t;
-    const float tot = wave_sum(t);
-    if (lane == 0) s_63[0] = tot;
+    dk += __shfl_xor(dk, 1);
+    dk += __shfl_xor(dk, 2);
+    if ((tid & 3) == 0) {
+      s_dl[GDL_K][r] = -dk * kap;
+      s_kt[r] = dk * kap;
+    }
   }
   __syncthreads();
+  if (w == 0) {
+    const float tot = wave_sum(s_kt[lane]);
+    if (lane == 0) s_63[0] = tot;
+  }
 
   // ---- phase 2: the Tp sums; Q S^T -> da; <Gamma, S>
   if (tid < C) {
