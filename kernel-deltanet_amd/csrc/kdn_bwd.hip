@@ -7,11 +7,11 @@
 //
 //   prep  (parallel over chunks x heads)  lift q, k; Gram matrices K K^T, Q K^T; A, T = (I + A)^-1,
 //                                         Tp = T diag(beta g), U~ = T (beta o V), P; R = P^T dY and
-//                                         H = Q^T (a o dY) (a_i = g_{i-1})
+//                                         a o dY (a_i = g_{i-1})
 //   chain (sequential over chunks)        forward:  S_c^T at every chunk start, X_K = K S_c^T,
 //                                                   W = U~ - Tp X_K, S_{c+1}^T = g_C S_c^T + K^T (kappa o W)
 //         (same kernel, reversed)         backward: Gamma = dL/dS^T at every chunk end, X = K Gamma,
-//                                                   dW = R + kappa o X,
+//                                                   dW = R + kappa o X, H = Q^T (a o dY),
 //                                                   Gamma <- g_C Gamma + H - K^T Tp^T dW
 //   grad  (parallel over chunks x heads)  dv, dbeta, dlambda and dphi_q, dphi_k in closed form, then
 //                                         the lift backward (cos -> -sin, renormalisation, input
@@ -59,8 +59,8 @@ __host__ __device__ constexpr int bop_dq(int m, int o, int jb) { return 32 + (m 
 struct Rec {
   static constexpr size_t Q = 0;                // [64][512] lifted, normalised q rows (0 past T)
   static constexpr size_t K = Q + C * D;        // [64][512] lifted, normalised k rows (0 past T)
-  static constexpr size_t H1 = K + C * D;       // Q^T (a o dY) as 16x16 tiles [ft 32][n 4][lane] f32x4
-  static constexpr size_t S = H1 + D * DV;      // [512][64] S^T at the chunk start
+  static constexpr size_t AYF = K + C * D;      // a o dY as B fragments [n 4][jb 2][lane] (sized for f32x8)
+  static constexpr size_t S = AYF + 4 * 2 * 64 * 8;  // [512][64] S^T at the chunk start
   static constexpr size_t G = S + D * DV;       // [512][64] dL/dS^T at the chunk end
   static constexpr size_t T = G + D * DV;       // [64][64] (I + A)^-1
   static constexpr size_t TP = T + C * C;       // [64][64] T diag(beta g)
@@ -419,30 +419,13 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
       for (int jj = 0; jj < 4; ++jj) kxf[(m * 16 + 4 * w + jj) * 64 + lane] = frag_rows_p<P>(K, D, 16 * m, 32 * (4 * w + jj), lane);
   }
 
-  // H = Q^T (a o dY) (A = the Q^T fragments this wave stored during the lift, B = a o dY from LDS).
+  // a o dY as the B fragments of H = Q^T (a o dY), which the reverse carry forms per chunk from these and
+  // the Q^T fragments (wave w: value tile w)
   {
     using frag = typename P::frag;
-    const frag* qtf = reinterpret_cast<const frag*>(rec + Rec::QTF);
-    frag yb[4][2];
+    frag* ayf = reinterpret_cast<frag*>(rec + Rec::AYF);
 #pragma unroll
-    for (int n = 0; n < 4; ++n)
-#pragma unroll
-      for (int jb = 0; jb < 2; ++jb) yb[n][jb] = P::from_f32(frag_cols(bA, LD, 16 * n, 32 * jb, lane));
-    frag qn0 = qtf[((8 * w) * 2 + 0) * 64 + lane], qn1 = qtf[((8 * w) * 2 + 1) * 64 + lane];
-#pragma unroll
-    for (int ft = 0; ft < 8; ++ft) {
-      const frag qa0 = qn0, qa1 = qn1;
-      if (ft + 1 < 8) {
-        qn0 = qtf[((8 * w + ft + 1) * 2 + 0) * 64 + lane];
-        qn1 = qtf[((8 * w + ft + 1) * 2 + 1) * 64 + lane];
-      }
-#pragma unroll
-      for (int n = 0; n < 4; ++n) {
-        const f32x4 hv = P::mma(P::mma(zero4(), qa0, yb[n][0]), qa1, yb[n][1]);
-        reinterpret_cast<f32x4*>(rec + Rec::H1)[((8 * w + ft) * 4 + n) * 64 + lane] = hv;
-      }
-      __builtin_amdgcn_sched_barrier(0);
-    }
+    for (int jb = 0; jb < 2; ++jb) ayf[(w * 2 + jb) * 64 + lane] = P::from_f32(frag_cols(bA, LD, 16 * w, 32 * jb, lane));
   }
   __syncthreads();  // a o dY in bA is dead from here on (bA becomes A below)
 
@@ -583,7 +566,10 @@ __device__ __forceinline__ bool chain_step(const Params& p, ChainShared& sh, int
     else if (idx < 256) pf += nr[(REV ? Rec::R : Rec::U) + 32 * (idx - 128)];
     else if (idx < 272) pf += nr[Rec::VEC + 32 * (idx - 256)];
     if constexpr (!PIPE) pf += nr[Rec::KXF + 32 * idx];
-    if constexpr (REV) pf += nr[Rec::H1 + 32 * idx];
+    if constexpr (REV) {
+      if (idx < 512 * (int)sizeof(frag) / 16) pf += nr[Rec::QTF + 32 * idx];
+      if (idx < 8 * (int)sizeof(frag) / 2) pf += nr[Rec::AYF + 32 * idx];
+    }
   }
 
   typename Feat<P>::T* dst = feat<P>(rec, REV ? Rec::G : Rec::S);
@@ -611,8 +597,13 @@ __device__ __forceinline__ bool chain_step(const Params& p, ChainShared& sh, int
   __syncthreads();
   f32x4 hh[8];
   if constexpr (REV) {
+    // this wave's rows of H = Q^T (a o dY) for value tile n
+    const frag* qtf = reinterpret_cast<const frag*>(rec + Rec::QTF);
+    const frag* ayf = reinterpret_cast<const frag*>(rec + Rec::AYF);
+    const frag y0 = ayf[(n * 2) * 64 + lane], y1 = ayf[(n * 2 + 1) * 64 + lane];
 #pragma unroll
-    for (int t = 0; t < 8; ++t) hh[t] = reinterpret_cast<const f32x4*>(rec + Rec::H1)[((8 * w + t) * 4 + n) * 64 + lane];
+    for (int t = 0; t < 8; ++t)
+      hh[t] = P::mma(P::mma(zero4(), qtf[((8 * w + t) * 2) * 64 + lane], y0), qtf[((8 * w + t) * 2 + 1) * 64 + lane], y1);
   }
   frag kt[8][2];
   {
