@@ -494,6 +494,139 @@ __global__ void __launch_bounds__(256) renorm_rows_kernel(T* x, int64_t rows, in
 }
 }  // namespace kdn
 
+namespace kdn {
+// The factored lift d_k = 128 -> D = 1024 in one pass (bf16 inputs): a workgroup of 8 waves, wave w lifting
+// half h = w >> 2 of row tile base + (w & 3) with that half's Omega (both staged in LDS) exactly as
+// lift_kernel lifts one half: phi_h = amp cos / (amp |cos| + 1e-8), rounded to the output type.  The
+// halves' sums of squares of those rounded values meet in LDS, and each wave scales its half by
+// 1 / (sqrt(n_0^2 + n_1^2) + 1e-7) before its only store: the concatenation renormalised onto S^1023
+// (kernels/factored_kernel_deltanet.py:60-74) without a second pass over the output.
+template <typename OutT>
+__device__ __forceinline__ float round_to(float v) {
+  if constexpr (std::is_same<OutT, __bf16>::value) return (float)(__bf16)v;
+  else return v;
+}
+
+template <typename OutT>
+__global__ void __launch_bounds__(512) lift_factored_kernel(const __bf16* __restrict__ x, int64_t rows, int64_t xs,
+                                                            const __bf16* __restrict__ om1, const float* __restrict__ ph1,
+                                                            const __bf16* __restrict__ om2, const float* __restrict__ ph2,
+                                                            float inv_tau, OutT* __restrict__ out, int64_t os) {
+  constexpr int D = 512, NT = D / 16;
+  constexpr int TG = 128 / (16 * (int)sizeof(OutT));
+  constexpr int SRS = 16 * TG * (int)sizeof(OutT) + 16;
+  constexpr int SCPR = 16 * TG * (int)sizeof(OutT) / 16;
+  __shared__ bf16x8 s_omega[2][NT * 2 * 64];
+  __shared__ __attribute__((aligned(16))) float s_phase_rev[2][D];
+  __shared__ __attribute__((aligned(16))) unsigned char s_stage[8][16 * SRS];
+  __shared__ float s_n2[2][2][4][16];  // [iteration parity][half][row tile][row]
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int h = wave >> 2, slot = wave & 3;
+  for (int idx = threadIdx.x; idx < 2 * NT * 2 * 64; idx += 512) {
+    const int hh = idx / (NT * 2 * 64), i = idx % (NT * 2 * 64);
+    const int l = i & 63, t = i >> 7, kb = (i >> 6) & 1;
+    const __bf16* om = hh ? om2 : om1;
+    s_omega[hh][i] = *reinterpret_cast<const bf16x8*>(om + (int64_t)(16 * t + (l & 15)) * 64 + 32 * kb + 8 * (l >> 4));
+  }
+  for (int f = threadIdx.x; f < 2 * D; f += 512) s_phase_rev[f / D][f % D] = (f < D ? ph1[f] : ph2[f - D]) * 0.15915494309189535f;
+  __syncthreads();
+
+  const float ang_scale = inv_tau * 0.15915494309189535f;
+  const float amp = sqrtf(2.0f / (float)D);
+  const int64_t ntiles = (rows + 15) / 16;
+  const int64_t stride = (int64_t)gridDim.x * 4;
+  const __bf16* xh = x + 64 * h;
+  // rows clamped to the last one: every load is in bounds (rows > 0); rows past the end are never stored
+  auto load_tile = [&](int64_t t, u32x4 (&raw)[2]) {
+    int64_t row = t * 16 + (lane & 15);
+    row = row < rows ? row : rows - 1;
+    const __bf16* src = xh + row * xs + 8 * (lane >> 4);
+    raw[0] = *reinterpret_cast<const u32x4*>(src);
+    raw[1] = *reinterpret_cast<const u32x4*>(src + 32);
+  };
+  u32x4 nraw[2];
+  load_tile((int64_t)blockIdx.x * 4 + slot, nraw);
+  int par = 0;
+  for (int64_t base = (int64_t)blockIdx.x * 4; base < ntiles; base += stride, par ^= 1) {
+    const int64_t tile = base + slot;
+    const u32x4 raw[2] = {nraw[0], nraw[1]};
+    load_tile(tile + stride, nraw);
+    const bool valid = tile * 16 + (lane & 15) < rows;
+    float xv[2][8];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      load8<__bf16>(reinterpret_cast<const __bf16*>(&raw[kb]), xv[kb]);
+#pragma unroll
+      for (int s = 0; s < 8; ++s) xv[kb][s] = valid ? xv[kb][s] : 0.f;
+    }
+    bf16x8 xb[2][1];
+    split_frag<1>(xv[0], xb[0]);
+    split_frag<1>(xv[1], xb[1]);
+    auto project = [&](int t) {
+      f32x4 acc = zero4();
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) acc = PrecBF16::mma(acc, s_omega[h][(t * 2 + kb) * 64 + lane], xb[kb][0]);
+      return acc;
+    };
+    float c[NT][4];
+    float ss = 0.f;
+    f32x4 acc = project(0);
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      __builtin_amdgcn_sched_barrier(0);
+      const f32x4 next = (t + 1 < NT) ? project(t + 1) : zero4();
+      const f32x4 ph = *reinterpret_cast<const f32x4*>(&s_phase_rev[h][16 * t + 4 * (lane >> 4)]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float cv = __builtin_amdgcn_cosf(__builtin_amdgcn_fractf(acc[i] * ang_scale + ph[i]));
+        c[t][i] = cv;
+        ss += cv * cv;
+      }
+      acc = next;
+    }
+    ss = sum_over_lane_groups(ss);
+    const float scale = amp / (amp * sqrtf(ss) + 1e-8f);
+    // this half's values as the single lift stores them, and their sum of squares per row
+    float n2 = 0.f;
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        c[t][i] = round_to<OutT>(c[t][i] * scale);
+        n2 += c[t][i] * c[t][i];
+      }
+    n2 = sum_over_lane_groups(n2);
+    if (lane < 16) s_n2[par][h][slot][lane] = n2;
+    // One barrier per tile: a wave writes the other parity's slots next, and cannot pass the next
+    // barrier before every wave has read these.
+    __syncthreads();
+    const float inv = 1.f / (sqrtf(s_n2[par][0][slot][lane & 15] + s_n2[par][1][slot][lane & 15]) + 1e-7f);
+    unsigned char* stg = s_stage[wave];
+#pragma unroll
+    for (int g = 0; g < NT / TG; ++g) {
+#pragma unroll
+      for (int tp = 0; tp < TG; ++tp) {
+        const int t = TG * g + tp;
+        float v[4] = {c[t][0] * inv, c[t][1] * inv, c[t][2] * inv, c[t][3] * inv};
+        store4<OutT>(reinterpret_cast<OutT*>(stg + (lane & 15) * SRS) + 16 * tp + 4 * (lane >> 4), v);
+      }
+      wave_lds_sync();
+#pragma unroll
+      for (int j = 0; j < 16 * SCPR / 64; ++j) {
+        const int q = 64 * j + lane, r = q / SCPR, ch = q % SCPR;
+        const u32x4 val = *reinterpret_cast<const u32x4*>(stg + r * SRS + 16 * ch);
+        const int64_t grow = tile * 16 + r;
+        if (grow < rows)
+          *reinterpret_cast<u32x4*>(reinterpret_cast<unsigned char*>(out + grow * os + D * h + 16 * TG * g) + 16 * ch) = val;
+      }
+      wave_lds_sync();
+    }
+  }
+}
+}  // namespace kdn
+
 extern "C" int kdn_fwht_lift_factored(const void* x, int64_t rows, int64_t x_row_stride, int x_dtype,
                                       const void* omega1_bf16, const float* phase1, const void* omega2_bf16,
                                       const float* phase2, float inv_tau, void* out, int64_t out_row_stride,
@@ -502,6 +635,27 @@ extern "C" int kdn_fwht_lift_factored(const void* x, int64_t rows, int64_t x_row
   if (!valid_dtype(x_dtype) || !valid_dtype(out_dtype)) return KDN_ERR_INVALID_ARGUMENT;
   if (x_row_stride < 128 || out_row_stride < 1024) return KDN_ERR_INVALID_ARGUMENT;
   const size_t isz = dtype_size(x_dtype), osz = dtype_size(out_dtype);
+  if (x_dtype == KDN_DTYPE_BF16 && rows > 0) {
+    // bf16 inputs: both halves and the renormalisation in one pass, one 8-wave workgroup per CU (151 KB
+    // of LDS), persistent over 4-tile groups (x and out rows 16-byte aligned, as below)
+    if (!aligned(x, 16) || !aligned(out, 16) || !aligned(omega1_bf16, 16) || !aligned(omega2_bf16, 16) ||
+        (x_row_stride * (int64_t)isz) % 16 != 0 || (out_row_stride * (int64_t)osz) % 16 != 0)
+      return KDN_ERR_MISALIGNED;
+    int64_t wgs = ((rows + 15) / 16 + 3) / 4;
+    const int cus = device_cus() > 0 ? device_cus() : 256;
+    if (wgs > cus) wgs = cus;
+    if (out_dtype == KDN_DTYPE_BF16)
+      hipLaunchKernelGGL(lift_factored_kernel<__bf16>, dim3((unsigned)wgs), dim3(512), 0, as_stream(stream),
+                         static_cast<const __bf16*>(x), rows, x_row_stride, static_cast<const __bf16*>(omega1_bf16),
+                         phase1, static_cast<const __bf16*>(omega2_bf16), phase2, inv_tau, static_cast<__bf16*>(out),
+                         out_row_stride);
+    else
+      hipLaunchKernelGGL(lift_factored_kernel<float>, dim3((unsigned)wgs), dim3(512), 0, as_stream(stream),
+                         static_cast<const __bf16*>(x), rows, x_row_stride, static_cast<const __bf16*>(omega1_bf16),
+                         phase1, static_cast<const __bf16*>(omega2_bf16), phase2, inv_tau, static_cast<float*>(out),
+                         out_row_stride);
+    return launch_status();
+  }
   // each half: the structured lift of 64 features into 512 (rows of x and out stay 16-byte aligned)
   int rc = kdn_fwht_lift(x, rows, x_row_stride, x_dtype, 0, omega1_bf16, phase1, 64, 512, inv_tau, out,
                          out_row_stride, out_dtype, stream);
