@@ -639,6 +639,7 @@ extern "C" int kdn_fwht_lift_factored(const void* x, int64_t rows, int64_t x_row
     // bf16 inputs: both halves and the renormalisation in one pass, one 8-wave workgroup per CU (151 KB
     // of LDS), persistent over 4-tile groups (x and out rows 16-byte aligned, as below)
     if (!aligned(x, 16) || !aligned(out, 16) || !aligned(omega1_bf16, 16) || !aligned(omega2_bf16, 16) ||
+        !aligned(phase1, 16) || !aligned(phase2, 16) ||
         (x_row_stride * (int64_t)isz) % 16 != 0 || (out_row_stride * (int64_t)osz) % 16 != 0)
       return KDN_ERR_MISALIGNED;
     int64_t wgs = ((rows + 15) / 16 + 3) / 4;
