@@ -48,6 +48,29 @@ def test_factored_lift(fproj, oprojs, dtype, tol):
     assert torch.allclose(norms, torch.ones_like(norms), atol=1e-5 if dtype == torch.float32 else 1e-2)
 
 
+@pytest.mark.parametrize("rows", [1, 37, 70001])
+def test_factored_lift_one_pass_bf16_inputs(fproj, oprojs, rows):
+    """bf16 inputs take the one-pass kernel (both halves and the renormalisation per workgroup, persistent
+    over 4-tile groups): fp32 outputs against the oracle at the fp32 tolerance (x is exact in bf16 and
+    nothing is rounded to bf16 on the way), bf16 outputs equal to those rounded within one bf16 step, at
+    row counts that leave partial tiles, idle waves in the last group and several groups per workgroup."""
+    x = torch.randn(rows, 128, generator=torch.Generator().manual_seed(rows)).to(torch.bfloat16)
+    p1, p2 = fproj.proj1, fproj.proj2
+    args = (p1.device_omega(DEV), p1.device_phase(DEV), p2.device_omega(DEV), p2.device_phase(DEV), p1.tau_star_inv)
+    xd = x.to(DEV)
+    y32 = ops.lift_factored(xd, *args, out_dtype=torch.float32)
+    y16 = ops.lift_factored(xd, *args)
+    torch.cuda.synchronize()
+    assert y32.dtype == torch.float32 and y16.dtype == torch.bfloat16 and y32.shape == (rows, 1024)
+    idx = np.unique(np.linspace(0, rows - 1, min(rows, 512)).astype(np.int64))
+    ref = ol.factored_lift(x.float().numpy()[idx], *oprojs)
+    assert rel(y32.cpu().numpy()[idx], ref) < 1e-5
+    norms = torch.linalg.vector_norm(y32, dim=-1).cpu()
+    assert torch.allclose(norms, torch.ones_like(norms), atol=1e-5)
+    # the bf16 path rounds each half and then the renormalised value: within 2^-7 relative of fp32
+    assert torch.allclose(y16.float(), y32, rtol=2 ** -7, atol=1e-6)
+
+
 def oracle_scan(q, k, v, beta, decay, oprojs, s0=None):
     pq = ol.factored_lift(q.float().numpy(), *oprojs)
     pk = ol.factored_lift(k.float().numpy(), *oprojs)
