@@ -269,7 +269,7 @@ int kdn_scan_output(const kdn_scan_args* a, int64_t chunk0, int64_t nchunks, voi
  * forward scan's prep and state kernels stores the state at each segment start, then each segment
  * recomputes its chunks, carries the state forward from its checkpoint and dL/dS backward from the
  * next segment, and writes its gradients.  The workspace (256-byte aligned) holds up to three segments'
- * records (1,116,160 bytes per (batch, head, chunk)), one fp32 [B][H][512][64] state per segment
+ * records (1,099,776 bytes per (batch, head, chunk)), one fp32 [B][H][512][64] state per segment
  * boundary plus one more, up to two buffers of the forward scan's records and a 64 KB table of Omega^T
  * fragments (one per head with per-head Omega, twice that with low parts; with dinv_tau, 4 bytes per
  * (batch, head, chunk) more): it grows

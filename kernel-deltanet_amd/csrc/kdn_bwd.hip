@@ -64,8 +64,7 @@ struct Rec {
   static constexpr size_t G = S + D * DV;       // [512][64] dL/dS^T at the chunk end
   static constexpr size_t T = G + D * DV;       // [64][64] (I + A)^-1
   static constexpr size_t TP = T + C * C;       // [64][64] T diag(beta g)
-  static constexpr size_t TPT = TP + C * C;     // [64][64] Tp^T
-  static constexpr size_t P = TPT + C * C;      // [64][64]
+  static constexpr size_t P = TP + C * C;       // [64][64]
   static constexpr size_t GKK = P + C * C;      // [64][64] K K^T
   static constexpr size_t U = GKK + C * C;      // U~ = T (beta o V) as tiles [m 4][n 4][lane] f32x4
   static constexpr size_t R = U + C * DV;       // P^T dY, tiles as U~
@@ -471,7 +470,6 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
     const float tp = p.linear ? 0.f : tij * s_beta[j] * expf(s_ell[j]);
     rec[Rec::T + idx] = tij;
     rec[Rec::TP + idx] = tp;
-    rec[Rec::TPT + j * C + i] = tp;
     rec[Rec::P + idx] = bP[i * LD + j];
   }
   {
@@ -549,8 +547,9 @@ __device__ __forceinline__ bool chain_step(const Params& p, ChainShared& sh, int
   float* rec = record(p, b, h, c);
   if constexpr (!PIPE) chain_load_kx<P>(cur, rec, w, lane);
   // operands used later in this iteration
-  const f32x8 tp0 = frag_rows(rec + (REV ? Rec::TPT : Rec::TP), C, 16 * w, 0, lane);
-  const f32x8 tp1 = frag_rows(rec + (REV ? Rec::TPT : Rec::TP), C, 16 * w, 32, lane);
+  // Tp rows (forward) or Tp^T rows, i.e. Tp columns (reverse)
+  const f32x8 tp0 = REV ? frag_cols(rec + Rec::TP, C, 16 * w, 0, lane) : frag_rows(rec + Rec::TP, C, 16 * w, 0, lane);
+  const f32x8 tp1 = REV ? frag_cols(rec + Rec::TP, C, 16 * w, 32, lane) : frag_rows(rec + Rec::TP, C, 16 * w, 32, lane);
   const f32x4 ur = reinterpret_cast<const f32x4*>(rec + (REV ? Rec::R : Rec::U))[(w * 4 + n) * 64 + lane];
   const f32x4 lr = *reinterpret_cast<const f32x4*>(rec + Rec::VEC + 16 * w + 4 * (lane >> 4));
   const float l63 = rec[Rec::VEC + 63];
@@ -562,7 +561,7 @@ __device__ __forceinline__ bool chain_step(const Params& p, ChainShared& sh, int
     const unsigned* nr = reinterpret_cast<const unsigned*>(nrec);
     const int idx = n * 256 + (int)threadIdx.x;
     if (idx < 512 * (int)sizeof(frag) / 16) pf += nr[Rec::KTF + 32 * idx];
-    if (idx < 128) pf += nr[(REV ? Rec::TPT : Rec::TP) + 32 * idx];
+    if (idx < 128) pf += nr[Rec::TP + 32 * idx];
     else if (idx < 256) pf += nr[(REV ? Rec::R : Rec::U) + 32 * (idx - 128)];
     else if (idx < 272) pf += nr[Rec::VEC + 32 * (idx - 256)];
     if constexpr (!PIPE) pf += nr[Rec::KXF + 32 * idx];
@@ -1085,7 +1084,7 @@ __global__ void __launch_bounds__(64 * GRAD_WAVES) bwd_grad_kernel(Params p) {
   f32x4 y1[2], zn[2];
   {
     const f32x8 a0 = frag_rows(bX, LD, 16 * rt, 0, lane), a1 = frag_rows(bX, LD, 16 * rt, 32, lane);
-    const f32x8 p0 = frag_rows(rec + Rec::TPT, C, 16 * rt, 0, lane), p1 = frag_rows(rec + Rec::TPT, C, 16 * rt, 32, lane);
+    const f32x8 p0 = frag_cols(rec + Rec::TP, C, 16 * rt, 0, lane), p1 = frag_cols(rec + Rec::TP, C, 16 * rt, 32, lane);
 #pragma unroll
     for (int nn = 0; nn < 2; ++nn) {
       const int n = 2 * ch + nn;

@@ -173,7 +173,7 @@ def test_backward_workspace_and_errors_need_no_device(lib):
     for i, nm in enumerate(("dy", "dq", "dk", "dv", "dbeta", "workspace")):
         setattr(g, nm, 0x7E0000000000 + 0x100000 * i)
     # one segment (the default at this size): its 4 chunk records per head and the Omega^T table
-    assert lib.kdn_scan_bwd_workspace_bytes(ctypes.byref(g)) == 2 * 4 * 1116160 + 65536
+    assert lib.kdn_scan_bwd_workspace_bytes(ctypes.byref(g)) == 2 * 4 * 1099776 + 65536
     seg = ctypes.c_int64(0)
     assert lib.kdn_scan_bwd_segments(ctypes.byref(g), ctypes.byref(seg)) == 1 and seg.value == 4
     # segments of one chunk: three rotating record buffers, three segment-start states and the carried
@@ -182,7 +182,7 @@ def test_backward_workspace_and_errors_need_no_device(lib):
     f.segment_chunks = 1
     assert lib.kdn_scan_bwd_segments(ctypes.byref(g), ctypes.byref(seg)) == 4 and seg.value == 1
     assert lib.kdn_scan_bwd_workspace_bytes(ctypes.byref(g)) == \
-        3 * 2 * 1116160 + 4 * 2 * 512 * 64 * 4 + 2 * 2 * 2 * 238592 + 65536
+        3 * 2 * 1099776 + 4 * 2 * 512 * 64 * 4 + 2 * 2 * 2 * 238592 + 65536
     g.workspace_bytes = 1 << 40
     assert lib.kdn_scan_bwd_phase(ctypes.byref(g), 5, 0, None) == -1
     assert lib.kdn_scan_bwd_phase(ctypes.byref(g), 1, 4, None) == -1   # segments 0 .. 3
@@ -201,9 +201,9 @@ def test_backward_workspace_and_errors_need_no_device(lib):
     f3 = _fake_ptrs(_args(T=256, H=2, rule=1, no_renorm=1))
     f3.omega_lo, f3.omega_head_stride, f3.phase_head_stride = 0x7D0000000000, 512 * 64, 512
     g.fwd = ctypes.addressof(f3)
-    assert lib.kdn_scan_bwd_workspace_bytes(ctypes.byref(g)) == 2 * 4 * 1116160 + 2 * 2 * 65536
+    assert lib.kdn_scan_bwd_workspace_bytes(ctypes.byref(g)) == 2 * 4 * 1099776 + 2 * 2 * 65536
     g.dinv_tau = 0x7C0000000000
-    assert lib.kdn_scan_bwd_workspace_bytes(ctypes.byref(g)) == 2 * 4 * 1116160 + 2 * 2 * 65536 + 256
+    assert lib.kdn_scan_bwd_workspace_bytes(ctypes.byref(g)) == 2 * 4 * 1099776 + 2 * 2 * 65536 + 256
     f3.phase_head_stride = 510                                          # per-head phases must stay 16-byte aligned
     assert lib.kdn_delta_scan_bwd(ctypes.byref(g), None) == -4
     f3.feature_mode, f3.d_k = 1, 512                                    # pre-lifted features: no backward
