@@ -112,6 +112,14 @@ __global__ void __launch_bounds__(256, (PrepWaves<P, FM>::value)) prep_kernel(Sc
   const __bf16* omega_lo_h = (FM == FM_HILO) ? p.omega_lo + h * p.oms : nullptr;
   const float ang = (p.inv_tau_head ? p.inv_tau_head[h] : p.inv_tau) * 0.15915494309189535f;
   In in;
+  // Record stores: streaming for the state / output kernels, which read a record a segment or more later
+  // (so that it does not evict the lines the concurrent kernels are about to read); cacheable for the
+  // fused chain, so that its records stay in the last-level cache until the chain reads them.
+  const bool cached = p.k_plain != 0;
+  auto put = [&](void* base, const frag& f) {
+    if (cached) store_frag<P>(base, lane, f);
+    else store_frag_nt<P>(base, lane, f);
+  };
   if constexpr (FM != FM_PRELIFTED) {
     stage_omega<D, OMEGA_LDS>(omega_h, p.phase + h * p.phs, s_omega, s_phrev);
     in.template load_qk<NOQ>(p, sq, h, (p.chunk0 + cl0) * CH, w, lane);
@@ -187,12 +195,14 @@ __global__ void __launch_bounds__(256, (PrepWaves<P, FM>::value)) prep_kernel(Sc
     for (int j = 0; j < NJ; ++j) {
       // The records are read back by the state and output kernels a segment or more later, long after
       // they could still sit in L2: streaming stores keep them from evicting the state kernel's lines.
-      if constexpr (IsBF16<P>::value && D == 512)
-        store_k_image(ws + L::phiK, w, j, lane, cqk[KI][j]);
-      else
+      if constexpr (IsBF16<P>::value && D == 512) {
+        if (p.k_plain) put(ws + L::phiK + (size_t)(w * NJ + j) * 64 * L::FB, cqk[KI][j]);
+        else store_k_image(ws + L::phiK, w, j, lane, cqk[KI][j]);
+      } else {
         store_frag_nt<P>(ws + L::phiK + (size_t)(w * NJ + j) * 64 * L::FB, lane, cqk[KI][j]);
+      }
       if constexpr (!NOQ) {
-        if (!p.relift_q) store_frag_nt<P>(ws + L::phiQ + (size_t)(w * NJ + j) * 64 * L::FB, lane, cqk[QI][j]);
+        if (!p.relift_q) put(ws + L::phiQ + (size_t)(w * NJ + j) * 64 * L::FB, cqk[QI][j]);
       }
       s_phik[(w * NJ + j) * 64 + lane] = cqk[KI][j];
     }
@@ -234,7 +244,7 @@ __global__ void __launch_bounds__(256, (PrepWaves<P, FM>::value)) prep_kernel(Sc
       if constexpr (!NOQ) {
 #pragma unroll
         for (int jb = 0; jb < 2; ++jb)
-          store_frag_nt<P>(ws + L::Pm + (size_t)(w * 2 + jb) * 64 * L::FB, lane, P::from_f32(pair_to8(pt[2 * jb], pt[2 * jb + 1])));
+          put(ws + L::Pm + (size_t)(w * 2 + jb) * 64 * L::FB, P::from_f32(pair_to8(pt[2 * jb], pt[2 * jb + 1])));
       }
     }
     if constexpr (RUN == 1) In::load_v(p, sq, h, t0, vraw);
@@ -271,7 +281,7 @@ __global__ void __launch_bounds__(256, (PrepWaves<P, FM>::value)) prep_kernel(Sc
           tw[s] = p.linear ? 0.f : tv * s_beta[j] * __expf(s_g[j]) * s_sk[j];  // linear: E = U~
           tb[jb][s] = tv * s_beta[j];
         }
-        store_frag_nt<P>(ws + L::Tp + (size_t)(w * 2 + jb) * 64 * L::FB, lane, P::from_f32(tw));
+        put(ws + L::Tp + (size_t)(w * 2 + jb) * 64 * L::FB, P::from_f32(tw));
       }
 #pragma unroll
       for (int n = 0; n < NV; ++n) {
@@ -296,7 +306,9 @@ __global__ void __launch_bounds__(256, (PrepWaves<P, FM>::value)) prep_kernel(Sc
             acc = P::mma(acc, P::from_f32(tb[jb]), P::from_f32(vv));
           }
         }
-        __builtin_nontemporal_store(acc, reinterpret_cast<f32x4*>(ws + L::U + ((size_t)(w * NV + n) * 64 + lane) * 16));
+        f32x4* ud = reinterpret_cast<f32x4*>(ws + L::U + ((size_t)(w * NV + n) * 64 + lane) * 16);
+        if (cached) *ud = acc;
+        else __builtin_nontemporal_store(acc, ud);
       }
     }
   };

@@ -23,6 +23,8 @@
 //   output (one workgroup per chunk and head): re-lifts q, Y = diag(qscale) Q S^T + P E.
 // The lifted features are stored unnormalised (cos values); per-row norms are folded into the small
 // per-token scale vectors, so a lift never has to hold a whole row before using it.
+#include <cstdlib>
+#include <cstring>
 #include <mutex>
 #include <type_traits>
 #include "kdn_frag.hpp"
@@ -662,7 +664,28 @@ __global__ void __launch_bounds__(256) output_kernel(ScanParams p) {
 static inline unsigned state_grid(int64_t B, int64_t H, int nv) { return (unsigned)(8 * ((B * H + 7) / 8) * nv); }
 
 // ------------------------------------------------------------------------------------------------
-enum Phase { PHASE_PREP = 1, PHASE_STATE = 2, PHASE_OUTPUT = 4, PHASE_ALL = 7 };
+enum Phase { PHASE_PREP = 1, PHASE_STATE = 2, PHASE_OUTPUT = 4, PHASE_ALL = 7, PHASE_CHAIN = 8 };
+
+// Two schedules for a whole-scan call with bf16 inputs:
+//  - split: prep / state / output (the state kernel streams only K, 64 KB per chunk, through its LDS ring;
+//    the output kernel reads the state checkpoints);
+//  - fused: prep + the fused chain (kdn_chain.hip: state update and readout in one sequential kernel, no
+//    output kernel and no checkpoints; each chain workgroup streams K and Q, 128 KB per chunk).
+// With few heads the chain is a latency-bound sequence of steps, and the split schedule's shorter step
+// wins (config 3, 16 heads: 2.7 against 5.3 ms); once the split schedule's state workgroups (4 per head at
+// d_v = 64) fill the GPU the layer is throughput-bound and the fused one wins (B = 32, H = 16, T = 16384:
+// 13.0 against 16.1 ms).  KDN_SCAN_SCHEDULE=split / fused overrides the choice (tuning and tests).
+// fp32 inputs and the phase entry points always run the split kernels.
+template <class P, int D>
+struct Fused : std::integral_constant<bool, IsBF16<P>::value && D == 512> {};
+
+static bool use_fused(const kdn_scan_args* a) {
+  const char* e = getenv("KDN_SCAN_SCHEDULE");  // read per call, so that a process can switch it
+  if (e && !strcmp(e, "fused")) return true;
+  if (e && !strcmp(e, "split")) return false;
+  const int cus = device_cus();
+  return cus > 0 && (int64_t)state_grid(a->B, a->H, a->d_v / 16) >= cus;
+}
 
 static ScanParams fill_params(const kdn_scan_args* a) {
   ScanParams p;
@@ -690,6 +713,7 @@ static ScanParams fill_params(const kdn_scan_args* a) {
   p.slots = a->state_slots;
   p.relift_q = 0;
   p.prep_no_q = 0;
+  p.k_plain = 0;
   return p;
 }
 
@@ -758,6 +782,9 @@ static int launch_phase(const ScanParams& p, int phase, hipStream_t st) {
   const dim3 chunk_grid((unsigned)p.nseg, (unsigned)p.H, (unsigned)p.B);
   if (phase == PHASE_PREP) {
     return launch_prep<P, InT, D, DV>(p, st);
+  } else if (phase == PHASE_CHAIN) {
+    if constexpr (Fused<P, D>::value) return launch_chain<OutT, DV>(p, st);
+    return KDN_ERR_UNSUPPORTED;
   } else if (phase == PHASE_STATE) {
     // The state workgroups are the sequential critical path: reserve enough LDS that no prep or output
     // workgroup can share their CU (a CU has 160 KB; the bf16 state kernel uses 88 KB statically).
@@ -783,8 +810,17 @@ static int launch_phase(const ScanParams& p, int phase, hipStream_t st) {
 template <class P, typename InT, typename OutT, int D, int DV>
 static int run_scan(const kdn_scan_args* a, const RunSpec& r) {
   const int cus = device_cus();
+  const bool fused = Fused<P, D>::value && r.phases == PHASE_ALL && use_fused(a);
   for (int64_t c0 = r.c_begin; c0 < r.c_end; c0 += r.seg) {
-    const ScanParams p = segment_params(a, r, c0, (r.c_end - c0 < r.seg) ? (r.c_end - c0) : r.seg, a->workspace, cus);
+    ScanParams p = segment_params(a, r, c0, (r.c_end - c0 < r.seg) ? (r.c_end - c0) : r.seg, a->workspace, cus);
+    if (fused) {
+      p.k_plain = 1;
+      for (int ph : {PHASE_PREP, PHASE_CHAIN}) {
+        const int rc = launch_phase<P, InT, OutT, D, DV>(p, ph, r.st);
+        if (rc != KDN_OK) return rc;
+      }
+      continue;
+    }
     for (int ph : {PHASE_PREP, PHASE_STATE, PHASE_OUTPUT}) {
       if (!(r.phases & ph)) continue;
       const int rc = launch_phase<P, InT, OutT, D, DV>(p, ph, r.st);
@@ -862,8 +898,56 @@ static int run_pipelined(const kdn_scan_args* a, const RunSpec& r) {
   return KDN_OK;
 }
 
+// The fused schedule: the chain of segment s runs on `st` while prep of segment s + 1 runs on `aux`;
+// segments rotate through `nbuf` >= 2 workspace buffers.
+//   chain(s) waits for prep(s)                 (event P[s % nbuf])
+//   prep(s)  waits for chain(s - nbuf), the last reader of its buffer (event C[s % nbuf])
+// aux first waits for the work already queued on st; the last chain, on st, ends the call.
+template <class P, typename InT, typename OutT, int D, int DV>
+static int run_pipelined_fused(const kdn_scan_args* a, const RunSpec& r) {
+  const int64_t seg = r.seg;
+  const int nbuf = r.nbuf;
+  const hipStream_t st = r.st, aux = r.aux;
+  const int64_t nchunks = (a->T + CH - 1) / CH;
+  const int64_t nsegs = (nchunks + seg - 1) / seg;
+  EventSet evs;
+  int rc = evs.create(2 * nbuf + 1);
+  if (rc != KDN_OK) return rc;
+  hipEvent_t* evP = evs.ev;
+  hipEvent_t* evC = evs.ev + nbuf;
+  hipEvent_t evIn = evs.ev[2 * nbuf];
+  const int prep_cus = device_cus() - (int)(a->B * a->H * (DV / (DV >= 32 ? 32 : 16)));
+  auto seg_p = [&](int64_t s) {
+    const int64_t c0 = s * seg;
+    ScanParams p = segment_params(a, r, c0, (nchunks - c0 < seg) ? (nchunks - c0) : seg,
+                                  (unsigned char*)a->workspace + (size_t)(s % nbuf) * r.buf_bytes, prep_cus);
+    p.k_plain = 1;
+    return p;
+  };
+#define KDN_TRY(x) do { if ((x) != hipSuccess) return KDN_ERR_DEVICE; } while (0)
+#define KDN_TRYK(x) do { const int _rc = (x); if (_rc != KDN_OK) return _rc; } while (0)
+  KDN_TRY(hipEventRecord(evIn, st));
+  KDN_TRY(hipStreamWaitEvent(aux, evIn, 0));
+  KDN_TRYK((launch_phase<P, InT, OutT, D, DV>(seg_p(0), PHASE_PREP, aux)));
+  KDN_TRY(hipEventRecord(evP[0], aux));
+  for (int64_t s = 0; s < nsegs; ++s) {
+    KDN_TRY(hipStreamWaitEvent(st, evP[s % nbuf], 0));
+    KDN_TRYK((launch_phase<P, InT, OutT, D, DV>(seg_p(s), PHASE_CHAIN, st)));
+    KDN_TRY(hipEventRecord(evC[s % nbuf], st));
+    if (s + 1 < nsegs) {
+      if (s + 1 >= nbuf) KDN_TRY(hipStreamWaitEvent(aux, evC[(s + 1) % nbuf], 0));
+      KDN_TRYK((launch_phase<P, InT, OutT, D, DV>(seg_p(s + 1), PHASE_PREP, aux)));
+      KDN_TRY(hipEventRecord(evP[(s + 1) % nbuf], aux));
+    }
+  }
+#undef KDN_TRY
+#undef KDN_TRYK
+  return KDN_OK;
+}
+
 template <class P, typename InT, typename OutT, int D, int DV>
 static int run(const kdn_scan_args* a, const RunSpec& r) {
+  if (r.aux && Fused<P, D>::value && r.phases == PHASE_ALL && use_fused(a)) return run_pipelined_fused<P, InT, OutT, D, DV>(a, r);
   if (r.aux) return run_pipelined<P, InT, OutT, D, DV>(a, r);
   return run_scan<P, InT, OutT, D, DV>(a, r);
 }

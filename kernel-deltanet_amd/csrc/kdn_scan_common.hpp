@@ -99,6 +99,9 @@ struct ScanParams {
   int relift_q;
   // no output kernel reads the segment (the backward's checkpoint pass): prep lifts only the keys
   int prep_no_q;
+  // the fused chain reads the segment (kdn_chain.hip): prep stores K as plain fragments (each lane's 16
+  // bytes contiguous) instead of the state kernel's LDS image
+  int k_plain;
   // ragged batches: sequence b is token rows seq_lo[b] .. seq_hi[b] (stride 1 of each token tensor; for
   // cu_seqlens, seq_hi = cu_seqlens + 1); its state is slot slots[b] (stride 0 of the state tensors)
   const int64_t* seq_lo;
@@ -143,5 +146,15 @@ struct IsBF16 : std::integral_constant<bool, std::is_same<P, PrecBF16>::value> {
 // can be kept in VGPRs: it post-processes nearly all of them on the VALU).
 template <class P, typename InT, int D, int DV>
 int launch_prep(const ScanParams& p, hipStream_t st);
+
+// The fused chain (kdn_chain.hip, bf16 inputs, D = 512): the state update and the readout of one segment
+// in one sequential kernel.  16 * min(2, d_v / 16) value columns per workgroup, the workgroups of a head
+// on one XCD (ids xcd + 8 (rank * per_head + part)).
+inline unsigned chain_grid(int64_t B, int64_t H, int dv) {
+  const int nwg = dv / (dv >= 32 ? 32 : 16);
+  return (unsigned)(8 * ((B * H + 7) / 8) * nwg);
+}
+template <typename OutT, int DV>
+int launch_chain(const ScanParams& p, hipStream_t st);
 
 }  // namespace kdn
