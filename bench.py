@@ -35,11 +35,13 @@ MFMA_BF16_PEAK = 2.5e15    # FLOP/s, MI355X dense bf16
 
 def flops_per_chunk(D: int, dv: int) -> dict:
     """Algorithmic FLOPs per (head, 64-token chunk), split by kernel (terms of the reference algebra,
-    kernels/fused_kernel_deltanet.py:99-149; total 4C^2D + 6CDdv + 9C^2dv + (2/3)C^3)."""
+    kernels/fused_kernel_deltanet.py:99-149; total 4C^2D + 6CDdv + 9C^2dv + (2/3)C^3).  The fused
+    schedule's chain forms the state kernel's and the output kernel's products."""
     prep = 4 * C * C * D + 5 * C * C * dv + (2.0 / 3.0) * C ** 3     # Grams, resolvents, U~, W~ factor
     state = 4 * C * D * dv + 2 * C * C * dv                           # K S^T, the update; E
     output = 2 * C * D * dv + 2 * C * C * dv                          # Q S^T; P E
-    return {"prep": prep, "state": state, "output": output, "total": prep + state + output}
+    return {"prep": prep, "state": state, "output": output, "chain": state + output,
+            "total": prep + state + output}
 
 
 def path_bytes(B: int, T: int, H: int, D: int, dv: int, in_bytes: int = 2, out_bytes: int = 2) -> float:
@@ -207,9 +209,12 @@ def bench_scan(args, dev):
     ms_per_step = e0.elapsed_time(e1) / args.steps
 
     # Per-kernel durations: the same step issued phase by phase from here, in the order of the library's
-    # schedule, with HIP events around each launch on the stream it is launched on.
+    # schedule (split: prep, state, output; fused: prep, chain), with HIP events around each launch on the
+    # stream it is launched on.
+    fused = plan.schedule == ops.SCHEDULE_FUSED
+    kinds = ("prep_fused", "chain") if fused else ("prep", "state", "output")
     segs = [(c0, min(seg, nchunks - c0)) for c0 in range(0, nchunks, seg)]
-    timed = {"prep": [], "state": [], "output": []}
+    timed = {kd: [] for kd in kinds}
 
     def launch(kind, s, st):
         c0, nc = segs[s]
@@ -221,9 +226,29 @@ def bench_scan(args, dev):
 
     nbuf = max(1, plan.workspace.numel() // plan.seg_bytes)
     for _ in range(args.steps):
-        if plan.pipelined:
-            # the library's three-stream schedule: state on the launch stream, prep and output on two
-            # auxiliary streams; prep into a reused buffer waits for that buffer's last output
+        if plan.pipelined and fused:
+            # the library's fused schedule: the chain on the launch stream, prep on an auxiliary stream;
+            # prep into a reused buffer waits for that buffer's last chain
+            aux = ops.aux_stream(dev, 0)
+            ev_in = torch.cuda.Event()
+            ev_in.record(stream)
+            aux.wait_event(ev_in)
+            ev_p = [torch.cuda.Event() for _ in segs]
+            ev_c = [torch.cuda.Event() for _ in segs]
+            launch("prep_fused", 0, aux)
+            ev_p[0].record(aux)
+            for s_ in range(len(segs)):
+                stream.wait_event(ev_p[s_])
+                launch("chain", s_, stream)
+                ev_c[s_].record(stream)
+                if s_ + 1 < len(segs):
+                    if s_ + 1 >= nbuf:
+                        aux.wait_event(ev_c[s_ + 1 - nbuf])
+                    launch("prep_fused", s_ + 1, aux)
+                    ev_p[s_ + 1].record(aux)
+        elif plan.pipelined:
+            # the library's split schedule: state on the launch stream, prep and output on two auxiliary
+            # streams; prep into a reused buffer waits for that buffer's last output
             aux, aux_o = ops.aux_stream(dev, 0), ops.aux_stream(dev, 1)
             ev_in = torch.cuda.Event()
             ev_in.record(stream)
@@ -251,37 +276,36 @@ def bench_scan(args, dev):
             stream.wait_event(ev_out)
         else:
             for s_ in range(len(segs)):
-                for kind in ("prep", "state", "output"):
+                for kind in kinds:
                     launch(kind, s_, stream)
     torch.cuda.synchronize()
-    ms_kernel = {k: sum(x.elapsed_time(y) for x, y in v) / args.steps for k, v in timed.items()}
-    launches = {k: len(v) / args.steps for k, v in timed.items()}
+    ms_kernel = {(k if k != "prep_fused" else "prep"): sum(x.elapsed_time(y) for x, y in v) / args.steps
+                 for k, v in timed.items()}
+    launches = {(k if k != "prep_fused" else "prep"): len(v) / args.steps for k, v in timed.items()}
 
     fl = flops_per_chunk(D, dv)
     units = B * H * nchunks
     tokens = B * T
     phases = {k: {"ms": ms_kernel[k], "launches": launches[k], "avg_launch_ms": ms_kernel[k] / launches[k],
                   "alg_flops": fl[k] * units, "tflops": fl[k] * units / ms_kernel[k] / 1e9}
-              for k in ("prep", "state", "output")}
-    # The dominant kernel: with fewer state workgroups than CUs (one sequence per head, config 3) the
-    # state kernel is the sequential chain that prep and output run beside, so it bounds the step even
-    # when concurrency stretches the others' launches; otherwise the kernels compete for CUs and the one
-    # with the most launch time dominates.
-    n_cu = torch.cuda.get_device_properties(dev).multi_processor_count
-    if plan.pipelined and B * H * (dv // 16) < n_cu:
+              for k in ms_kernel}
+    # The dominant kernel: in the split schedule with fewer state workgroups than CUs (config 3) the state
+    # kernel is the sequential chain that prep and output run beside, so it bounds the step even when
+    # concurrency stretches the others' launches; otherwise the kernels compete for CUs and the one with
+    # the most launch time dominates.
+    if plan.pipelined and not fused:
         dom = "state"
     else:
         dom = max(phases, key=lambda p: phases[p]["ms"])
     achieved = phases[dom]["tflops"]
     # Counter summaries committed under profiles/ for the measured shapes (rocprofv3 --pmc runs of this
     # script): HBM bytes (FETCH_SIZE / WRITE_SIZE) and MFMA busy % (MfmaUtil) of the dominant kernel.
-    # The pipelined schedule runs the output kernel that lifts q again ("output_relift").
     std = dv == 64 and H == 16 and args.decay == "none" and ((cfg == 3 and B == 1 and T == 65536) or
                                                             (cfg == 4 and B == 32))
     stem = f"pmc_config3" if cfg == 3 else f"pmc_config4_T{T}"
     pmc = read_pmc(args.pmc) if args.pmc else (read_pmc(os.path.join(REPO, "profiles", stem + ".txt")) if std else {})
     pmc_mfma = read_pmc(os.path.join(REPO, "profiles", stem + "_mfma.txt")) if std else {}
-    key = "output_relift" if (dom == "output" and plan.pipelined) else dom
+    key = dom
     traffic = None
     if f"{key}_fetch_kib" in pmc and f"{key}_write_kib" in pmc and "copy_fetch_kib" in pmc and "copy_write_kib" in pmc:
         copy_bytes = pmc.get("copy_bytes", 256 << 20)
@@ -310,8 +334,10 @@ def bench_scan(args, dev):
                                + ("lambda=1" if lam is None else "lambda=sigmoid(N(0,1)) fp32 (decay variant)"),
                    "decay": args.decay,
                    "B": B, "H": H, "T": T, "D": D, "d_v": dv, "chunk": C, "segment_chunks": seg,
-                   "schedule": "pipelined (state chain on the launch stream, prep and output on two auxiliary "
-                               "streams)" if plan.pipelined else "serial", "parallelism": "single GPU"},
+                   "schedule": ("fused (prep on an auxiliary stream beside the fused chain, which writes y)"
+                                if fused else "split (state chain on the launch stream, prep and output on two "
+                                              "auxiliary streams)") + ("" if plan.pipelined else ", serial"),
+                   "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "achieved": achieved, "peak": MFMA_BF16_PEAK / 1e12, "unit": "TFLOP/s",
                      "frac": achieved / (MFMA_BF16_PEAK / 1e12), "traffic": traffic, "kernel": dom,
                      "mfma_util": mfma_util,

@@ -6,12 +6,17 @@
  *
  * Conventions (every entry point):
  *   - All tensor pointers are device pointers; the caller allocates every buffer (inputs, outputs,
- *     workspace).  Nothing in the library allocates device memory.
+ *     workspace).  The library allocates no device memory at run time.  The one exception is
+ *     kdn_delta_scan_fwd_noalloc's fixed scratch array (KDN_NOALLOC_SCRATCH_BYTES per GPU), a device
+ *     global of its own code object that is reserved on a GPU from the first call of that entry point
+ *     there until the process ends.
  *   - Work is enqueued on `stream` (a hipStream_t passed as void*; NULL = the null stream) and is
  *     stream-ordered; entry points return without synchronising.
  *   - Return 0 (KDN_OK) or a negative kdn_status.  No exception or abort crosses the ABI.  Argument
  *     errors are detected on the host before anything is enqueued.
- *   - Stateless and reentrant: no global caches, safe to call from several host threads.
+ *   - Reentrant and safe to call from several host threads.  The only process-wide state is the
+ *     per-device address of the noalloc scratch array (looked up once per device, under a lock) and
+ *     the state pool handles (single-threaded each).
  *   - Strides are in elements; the innermost (feature) dimension of every tensor must be contiguous.
  *
  * Reference interfaces replaced (paths relative to jatin-yadav-acad/kernel-deltanet):
@@ -25,6 +30,13 @@
  *   kdn_scan_prep       <- the S-independent part of its chunk loop, kernels/fused_kernel_deltanet.py:95-122
  *   kdn_scan_state      <- the state carry, kernels/fused_kernel_deltanet.py:128-129,144-149
  *   kdn_scan_output     <- the chunk readout, kernels/fused_kernel_deltanet.py:118-141
+ *   kdn_scan_prep_fused, kdn_scan_chain <- the same chunk loop as prep + one sequential kernel that carries
+ *                          the state and reads out y (kernels/fused_kernel_deltanet.py:95-149)
+ *
+ * ABI 2.0 (breaking): kdn_scan_bwd_args and kdn_ragged_args gained trailing fields that the library reads
+ * on every call (dinv_tau, num_slots) and kdn_scan_bwd_phase gained its `segment` argument in 1.6-1.8;
+ * callers built against a header older than 1.8 must be recompiled.  2.0 adds kdn_scan_schedule,
+ * kdn_scan_prep_fused and kdn_scan_chain.
  */
 #ifndef KDN_H
 #define KDN_H
@@ -204,8 +216,9 @@ int kdn_delta_scan_fwd(const kdn_scan_args* a, void* stream);
  *                     chunk's starting state and its error terms E into the slot, reads initial_state
  *                     when chunk0 == 0 (zeros if NULL) and final_state otherwise, writes final_state.
  *                     Replaces kernels/fused_kernel_deltanet.py:128-129,144-149.
- *   kdn_scan_output : y of each chunk from its slot (re-lifting q).  Replaces
- *                     kernels/fused_kernel_deltanet.py:118-141. */
+ *   kdn_scan_output : y of each chunk from its slot.  Replaces kernels/fused_kernel_deltanet.py:118-141.
+ * These are the split schedule's phases; kdn_scan_schedule says which schedule the whole-scan entry
+ * points run, and kdn_scan_prep_fused / kdn_scan_chain below are the fused schedule's. */
 /* kdn_delta_scan_fwd scheduled over two streams.  The sequence is cut into segments of
  * a->segment_chunks chunks (0 = 64).  The segments rotate through as many workspace buffers of
  * kdn_scan_workspace_bytes() (for that segment size) as a->workspace_bytes holds, up to three.
@@ -245,6 +258,38 @@ int kdn_delta_scan_fwd_noalloc(const kdn_scan_args* a, void* stream);
 int kdn_scan_prep(const kdn_scan_args* a, int64_t chunk0, int64_t nchunks, void* stream);
 int kdn_scan_state(const kdn_scan_args* a, int64_t chunk0, int64_t nchunks, void* stream);
 int kdn_scan_output(const kdn_scan_args* a, int64_t chunk0, int64_t nchunks, void* stream);
+
+/* The schedule that kdn_delta_scan_fwd, _pipelined, _streams and _noalloc run for these arguments on the
+ * current device (ABI 2.0), or a negative kdn_status for invalid arguments:
+ *   KDN_SCHEDULE_SPLIT   per segment the prep, state and output kernels above: the state kernel carries only
+ *                        the state and checkpoints it per chunk, the output kernel reads y out;
+ *   KDN_SCHEDULE_FUSED   per segment the prep kernel and the fused chain, which carries the state and writes y
+ *                        itself (no checkpoints, no output kernel).  bf16 inputs at D = 512, chosen when the
+ *                        split schedule's state workgroups (B * H * d_v / 16, heads rounded up to 8) fill the
+ *                        GPU: a few heads are a latency-bound sequence whose shortest step is the split
+ *                        state kernel's, many heads are throughput-bound and the fused chain does less work;
+ *   KDN_SCHEDULE_GENERAL the pre-lifted D = 1024 scan.
+ * The environment variable KDN_SCAN_SCHEDULE=split or =fused, read at every call, overrides the choice
+ * between the first two.  Both give the same final state bit for bit; y differs by the order of one fp32
+ * sum (Q S^T over four feature quarters). */
+#define KDN_SCHEDULE_SPLIT 0
+#define KDN_SCHEDULE_FUSED 1
+#define KDN_SCHEDULE_GENERAL 2
+int kdn_scan_schedule(const kdn_scan_args* a);
+
+/* The fused schedule's two phases (ABI 2.0), used like kdn_scan_prep / kdn_scan_state: on chunks
+ * [chunk0, chunk0 + nchunks) with workspace slots 0 .. nchunks-1, in the order prep, chain.
+ *   kdn_scan_prep_fused : kdn_scan_prep writing the chain's slot layout (the lifted keys as plain MFMA
+ *                         fragments and the lifted queries stored).
+ *   kdn_scan_chain      : the sequential carry as kdn_scan_state (initial_state when chunk0 == 0, zeros if
+ *                         NULL, final_state otherwise; writes final_state) that also writes y of each chunk.
+ * bf16 inputs at D = 512 only (KDN_ERR_UNSUPPORTED otherwise).  Replace kernels/fused_kernel_deltanet.py:95-149. */
+int kdn_scan_prep_fused(const kdn_scan_args* a, int64_t chunk0, int64_t nchunks, void* stream);
+/* The segment length (chunks) that kdn_delta_scan_fwd (pipelined = 0) or the pipelined entry points
+ * (pipelined != 0) use for these arguments on the current device: a->segment_chunks when positive, else the
+ * default, at most the sequence's chunks.  0 for invalid arguments or the D = 1024 scan (ABI 2.0). */
+int64_t kdn_scan_segment_chunks(const kdn_scan_args* a, int pipelined);
+int kdn_scan_chain(const kdn_scan_args* a, int64_t chunk0, int64_t nchunks, void* stream);
 
 /* ---- Backward of the scan (ABI 1.3; segmented and deterministic since ABI 1.6) ----------------------
  * Gradients of a loss L through kdn_delta_scan_fwd, given dL/dy and optionally dL/d(final state).

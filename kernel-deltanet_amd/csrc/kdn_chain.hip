@@ -49,10 +49,6 @@ namespace kdn {
 
 namespace {
 
-// Workgroup barrier that orders LDS only: this wave's LDS operations are complete, then s_barrier.  The
-// memory clobber keeps the compiler from moving memory operations across it.
-__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
-
 __device__ __forceinline__ bf16x8 identity_slab(int lane, int hsel) {
   bf16x8 r;
 #pragma unroll

@@ -106,6 +106,13 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_wave_barrier();
 }
 
+// Workgroup barrier that orders LDS only: this wave's LDS operations are complete, then s_barrier.  Unlike
+// __syncthreads() it does not drain the wave's outstanding global loads and stores (whose release fence the
+// compiler implements as s_waitcnt vmcnt(0)), so loads issued early keep travelling across it.  For
+// kernels whose waves exchange data through LDS only.  The memory clobber keeps the compiler from moving
+// memory operations across it.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 // 64-lane butterfly partner exchange: value held by lane (lane ^ H).
 template <int H>
 __device__ __forceinline__ float xor_shuffle(float v) {

@@ -1,5 +1,4 @@
-// Lift of 16-row tiles of q / k on MFMA plus v_cos, shared by the prep kernel (kdn_prep.hip) and the
-// output kernel (kdn_scan.hip, which re-lifts q instead of reading it back when that pays).
+// Lift of 16-row tiles of q / k on MFMA plus v_cos, for the prep kernel of the D = 512 scan (kdn_prep.hip).
 #pragma once
 #include <type_traits>
 #include "kdn_frag.hpp"
@@ -140,16 +139,30 @@ __device__ __forceinline__ void lift_tile(const RawRow<InT> (&raw)[NX], int norm
 }
 
 // Omega as A fragments in LDS (lane l of fragment (t, kb): Omega[16t + (l&15)][32kb + 8(l>>4) .. +8])
-// and phase / (2 pi).
-template <int D, bool OMEGA_LDS>
+// and phase / (2 pi), by a workgroup of NTHREADS threads.  The fragment loop has a fixed trip count, so
+// that every load is issued before the first LDS store waits for one (a loop bounded by blockDim is not
+// unrolled and pays one L2 round trip per iteration).
+template <int D, bool OMEGA_LDS, int NTHREADS = 256>
 __device__ __forceinline__ void stage_omega(const __bf16* omega, const float* phase, bf16x8* s_omega, float* s_phrev) {
   if constexpr (OMEGA_LDS) {
-    for (int idx = threadIdx.x; idx < (D / 16) * 2 * 64; idx += blockDim.x) {
+    constexpr int NF = (D / 16) * 2 * 64;
+    static_assert(NF % NTHREADS == 0, "fragment slots per thread");
+    bf16x8 v[NF / NTHREADS];
+#pragma unroll
+    for (int i = 0; i < NF / NTHREADS; ++i) {
+      const int idx = (int)threadIdx.x + NTHREADS * i;
       const int l = idx & 63, tk = idx >> 6, t = tk >> 1, kb = tk & 1;
-      s_omega[idx] = *reinterpret_cast<const bf16x8*>(omega + (int64_t)(16 * t + (l & 15)) * 64 + 32 * kb + 8 * (l >> 4));
+      v[i] = *reinterpret_cast<const bf16x8*>(omega + (int64_t)(16 * t + (l & 15)) * 64 + 32 * kb + 8 * (l >> 4));
     }
+#pragma unroll
+    for (int i = 0; i < NF / NTHREADS; ++i) s_omega[(int)threadIdx.x + NTHREADS * i] = v[i];
   }
-  for (int f = threadIdx.x; f < D; f += blockDim.x) s_phrev[f] = phase[f] * 0.15915494309189535f;
+  static_assert(D % NTHREADS == 0, "phases per thread");
+  float ph[D / NTHREADS];
+#pragma unroll
+  for (int i = 0; i < D / NTHREADS; ++i) ph[i] = phase[(int)threadIdx.x + NTHREADS * i];
+#pragma unroll
+  for (int i = 0; i < D / NTHREADS; ++i) s_phrev[(int)threadIdx.x + NTHREADS * i] = ph[i] * 0.15915494309189535f;
 }
 
 }  // namespace kdn

@@ -11,12 +11,13 @@
 namespace kdn {
 
 // ------------------------------------------------------------------------------------------------
-// prep: grid (ceil(nseg / run), H, B), 256 threads.  A workgroup prepares `run` consecutive chunks
-// of one head.  Wave w owns token rows [16w, 16w+16) of a chunk.
-// bf16 lifts (exact or hi + lo projection): one chunk per workgroup, Omega read from L2 (it is shared
-// by every workgroup) rather than staged in LDS, so that the kernel fits 67 KB of LDS and 256 registers
-// per wave and two workgroups share a CU, each hiding the other's latencies: 1.22 -> 0.99 ms for config
-// 3's prep, measured against one workgroup per CU with Omega in LDS and the next chunk prefetched.
+// prep: grid (ceil(nseg / run), H, B), 256 threads.  A workgroup prepares `run` consecutive chunks of one
+// head.  Wave w owns token rows [16w, 16w+16) of a chunk.  The waves exchange data through LDS only, so
+// the barriers order LDS only (lds_barrier): the global loads issued early (q, k, V rows) travel across
+// them instead of being drained at every barrier.
+// bf16 lifts (exact or hi + lo projection): one chunk per workgroup, two workgroups per CU (67 KB of LDS,
+// at most 256 registers per wave), each hiding the other's latencies.  The exact projection's Omega is
+// staged in LDS in the area the K fragments take later; the hi + lo parts are read from L2.
 // Given features (bf16): runs of `run` chunks chosen at launch (ScanParams::prep_run), the next chunk's
 // beta / decay prefetched.  fp32: one chunk, one workgroup per CU (its fragments are twice as wide).
 template <class P, int FM>
@@ -78,22 +79,26 @@ __device__ __forceinline__ void load_lifted(const InT* row, bool valid, int lane
 // the query scales are formed.
 template <class P, typename InT, int D, int DV, int FM, bool NOQ = false>
 __global__ void __launch_bounds__(256, (PrepWaves<P, FM>::value)) prep_kernel(ScanParams p) {
-  static_assert(!NOQ || FM == FM_EXACT, "only the exact projection is lifted again by the output kernel");
+  static_assert(!NOQ || FM == FM_EXACT, "the key-only prep is the exact projection's");
   using L = WsLayout<P, D, DV>;
   using frag = typename P::frag;
   using In = PrepInputs<InT, DV>;
   constexpr int NT = D / 16, NJ = D / 32, NV = DV / 16;
-  constexpr bool OMEGA_LDS = false;  // Omega from L2 (see above)
-  constexpr size_t OMEGA_BYTES = OMEGA_LDS ? (size_t)NT * 2 * 64 * 16 : 0;
+  // The exact projection's Omega (64 KB of bf16 A fragments) is staged in the LDS area that holds the K
+  // fragments for the Gram later: the lift reads it from LDS (from L2 it waited on every feature tile's
+  // fragments), and the kernel still fits two workgroups per CU.  The hi + lo projection reads its two
+  // parts from L2.
+  constexpr bool OMEGA_LDS = FM == FM_EXACT;
   constexpr size_t PHIK_BYTES = (size_t)4 * NJ * 64 * sizeof(frag);
+  static_assert(!OMEGA_LDS || (size_t)NT * 2 * 64 * 16 <= PHIK_BYTES, "Omega does not fit the K-fragment area");
   // After the Gram the K-fragment area is reused for A (16 KB), T (17 KB) and V.
   static_assert(64 * 64 * 4 + 64 * 68 * 4 + 64 * DV * sizeof(InT) <= PHIK_BYTES, "LDS reuse does not fit");
-  __shared__ __attribute__((aligned(16))) unsigned char smem[OMEGA_BYTES + PHIK_BYTES];
+  __shared__ __attribute__((aligned(16))) unsigned char smem[PHIK_BYTES];
   __shared__ __attribute__((aligned(16))) float s_beta[64], s_g[64], s_sq[64], s_sk[64], s_phrev[D];
 
-  bf16x8* s_omega = reinterpret_cast<bf16x8*>(smem);
-  frag* s_phik = reinterpret_cast<frag*>(smem + OMEGA_BYTES);
-  float* s_A = reinterpret_cast<float*>(smem + OMEGA_BYTES);          // [j][p][s] = A[4s+p][j]
+  bf16x8* s_omega = reinterpret_cast<bf16x8*>(smem);                 // during the lift (OMEGA_LDS)
+  frag* s_phik = reinterpret_cast<frag*>(smem);                       // from the lift to the Gram
+  float* s_A = reinterpret_cast<float*>(smem);                        // [j][p][s] = A[4s+p][j]
   float* s_T = s_A + 64 * 64;                                          // [t][68]
   InT* s_V = reinterpret_cast<InT*>(s_T + 64 * 68);                    // [t][DV]
 
@@ -135,8 +140,8 @@ __global__ void __launch_bounds__(256, (PrepWaves<P, FM>::value)) prep_kernel(Sc
     const int64_t t0 = (p.chunk0 + cl) * CH;
     unsigned char* ws = p.ws + ((b * p.H + h) * (p.nseg + 1) + cl) * L::bytes;
     u32x4 vraw[In::VPT];
-    if constexpr (RUN != 1) In::load_v(p, sq, h, t0, vraw);  // early: first needed after the Gram
-    __syncthreads();  // Omega staged (first chunk); the previous chunk's LDS reads are done
+    In::load_v(p, sq, h, t0, vraw);  // early: first needed after the Gram, its latency hides behind the lift
+    lds_barrier();  // Omega staged (first chunk); the previous chunk's LDS reads are done
 
     // ---- beta and the in-chunk log-decay prefix (wave 0)
     if (w == 0) {
@@ -202,11 +207,13 @@ __global__ void __launch_bounds__(256, (PrepWaves<P, FM>::value)) prep_kernel(Sc
         store_frag_nt<P>(ws + L::phiK + (size_t)(w * NJ + j) * 64 * L::FB, lane, cqk[KI][j]);
       }
       if constexpr (!NOQ) {
-        if (!p.relift_q) put(ws + L::phiQ + (size_t)(w * NJ + j) * 64 * L::FB, cqk[QI][j]);
+        put(ws + L::phiQ + (size_t)(w * NJ + j) * 64 * L::FB, cqk[QI][j]);
       }
-      s_phik[(w * NJ + j) * 64 + lane] = cqk[KI][j];
     }
-    __syncthreads();
+    if constexpr (OMEGA_LDS) lds_barrier();  // every wave's lift has read Omega from the area
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) s_phik[(w * NJ + j) * 64 + lane] = cqk[KI][j];
+    lds_barrier();
 
     // ---- Gram tiles (m, n = w):  Gkk[m][w] = K_m K_w^T,  GqkT[m][w] = K_m Q_w^T  (unnormalised)
     f32x4 gkk[4], gqk[4];
@@ -221,7 +228,7 @@ __global__ void __launch_bounds__(256, (PrepWaves<P, FM>::value)) prep_kernel(Sc
         if constexpr (!NOQ) gqk[m] = P::mma(gqk[m], a, cqk[QI][j]);
       }
     }
-    __syncthreads();  // K fragments in LDS are dead from here on
+    lds_barrier();  // K fragments in LDS are dead from here on
 
     // ---- A (for the inverse), P fragments, V staging, scale vectors
     {
@@ -247,7 +254,6 @@ __global__ void __launch_bounds__(256, (PrepWaves<P, FM>::value)) prep_kernel(Sc
           put(ws + L::Pm + (size_t)(w * 2 + jb) * 64 * L::FB, P::from_f32(pair_to8(pt[2 * jb], pt[2 * jb + 1])));
       }
     }
-    if constexpr (RUN == 1) In::load_v(p, sq, h, t0, vraw);
 #pragma unroll
     for (int i = 0; i < In::VPT; ++i) {
       const int idx = (int)threadIdx.x + 256 * i;
@@ -261,11 +267,11 @@ __global__ void __launch_bounds__(256, (PrepWaves<P, FM>::value)) prep_kernel(Sc
       vec[64 + lane] = __expf(fminf(g63 - s_g[lane], 0.f)) * s_sk[lane]; // e^{g_63 - g_t} * |phi_k| scale
       if (lane == 0) vec[128] = __expf(fminf(g63, 0.f));
     }
-    __syncthreads();
+    lds_barrier();
 
     // ---- T = (I + A)^{-1} (column-oriented substitution over lane quads)
     unit_lower_inverse(s_A, s_T, 68, w, lane);
-    __syncthreads();
+    lds_barrier();
 
     // ---- W~ factor T diag(beta e^g |phi_k|) fragments, and U~ = T diag(beta) V   (wave w: rows m = w)
     {

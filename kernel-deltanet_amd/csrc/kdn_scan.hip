@@ -13,14 +13,15 @@
 // which is algebraically the scan of kernels/fused_kernel_deltanet.py:93-149 (that code factors the
 // decay-free homogeneous part through an upper-triangular resolvent; both equal the token recurrence).
 //
-// Three kernels per segment of chunks, so that the only sequential kernel streams as few bytes per
-// chunk as possible (64 KB of K per chunk and head):
+// Three kernels per segment of chunks (the split schedule), so that the only sequential kernel streams as
+// few bytes per chunk as possible (64 KB of K per chunk and head):
 //   prep   (one workgroup per chunk and head; kdn_prep.hip): lift q and k on MFMA, Gram matrices, the
 //          triangular inverse and every S-independent factor; writes K, Tp = T diag(beta e^g |phi_k|),
 //          P, U~ and per-token scale vectors to the workspace in MFMA-fragment order.
 //   state  (one workgroup per head and 16 value components, sequential over chunks): X_K = K S^T,
 //          E = U~ - Tp X_K and the state update; checkpoints each chunk's starting S^T and E.
-//   output (one workgroup per chunk and head): re-lifts q, Y = diag(qscale) Q S^T + P E.
+//   output (one workgroup per chunk and head): Y = diag(qscale) Q S^T + P E.
+// The fused schedule (kdn_chain.hip) runs prep and one sequential kernel that forms Y as well.
 // The lifted features are stored unnormalised (cos values); per-row norms are folded into the small
 // per-token scale vectors, so a lift never has to hold a whole row before using it.
 #include <cstdlib>
@@ -30,7 +31,6 @@
 #include "kdn_frag.hpp"
 #include "kdn_internal.hpp"
 #include "kdn_io.hpp"
-#include "kdn_lift_tile.hpp"
 #include "kdn_scan_common.hpp"
 
 namespace kdn {
@@ -568,12 +568,10 @@ __global__ void __launch_bounds__(320) state_kernel_dma(ScanParams p) {
 
 // ------------------------------------------------------------------------------------------------
 // output: grid (nseg, H, B), 256 threads.  Y = diag(qscale) Q S_c^T + P E for one (chunk, head).
-// Wave w keeps the lifted query fragments of token tile w in registers: read back from the record, or
-// (RELIFT, bf16 with the exact projection) lifted again from q here exactly as prep lifted them, Omega
-// read from L2.  The chunk-start S^T fragments are staged in LDS, NG value tiles per pass, and read by
-// all four waves.  Each wave assembles its 16 x d_v block of Y in a wave-private LDS tile and writes
+// Wave w keeps the lifted query fragments of token tile w (read back from the record) in registers.
+// The chunk-start S^T fragments are staged in LDS, NG value tiles per pass, and read by all four waves.  Each wave assembles its 16 x d_v block of Y in a wave-private LDS tile and writes
 // whole rows with 16-byte stores.  Every operand is read once: streaming loads.
-template <class P, typename OutT, int D, int DV, bool RELIFT>
+template <class P, typename OutT, int D, int DV>
 __global__ void __launch_bounds__(256) output_kernel(ScanParams p) {
   using L = WsLayout<P, D, DV>;
   using frag = typename P::frag;
@@ -583,7 +581,6 @@ __global__ void __launch_bounds__(256) output_kernel(ScanParams p) {
   constexpr int YS = DV + 4;                     // padded row of the Y tile
   __shared__ frag s_s[NJ * NG * 64];
   __shared__ __attribute__((aligned(16))) float s_y[4][16 * YS];
-  __shared__ __attribute__((aligned(16))) float s_phrev[RELIFT ? D : 4];
 
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -595,22 +592,8 @@ __global__ void __launch_bounds__(256) output_kernel(ScanParams p) {
   const float* vec = reinterpret_cast<const float*>(ws + L::VEC);
 
   frag aq[NJ];
-  if constexpr (RELIFT) {
-    for (int f = threadIdx.x; f < D; f += 256) s_phrev[f] = p.phase[h * p.phs + f] * 0.15915494309189535f;
-    RawRow<__bf16> raw[1];
-    const int64_t trow = t0 + 16 * w + (lane & 15);
-    raw[0].load((const __bf16*)p.q + sq.q + trow * p.qs1 + h * p.qs2, trow < sq.len, lane);
-    const float ang = (p.inv_tau_head ? p.inv_tau_head[h] : p.inv_tau) * 0.15915494309189535f;
-    __syncthreads();
-    frag lifted[1][NJ];
-    float ss[1];
-    lift_tile<P, __bf16, D, false, 1>(raw, p.normalize, nullptr, p.omega + h * p.oms, s_phrev, ang, lane, lifted, ss);
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) aq[j] = lifted[0][j];
-  } else {
-#pragma unroll
-    for (int j = 0; j < NJ; ++j) aq[j] = load_frag_nt<P>(ws + L::phiQ + (size_t)(w * NJ + j) * 64 * L::FB, lane);
-  }
+  for (int j = 0; j < NJ; ++j) aq[j] = load_frag_nt<P>(ws + L::phiQ + (size_t)(w * NJ + j) * 64 * L::FB, lane);
   frag pf[2];
 #pragma unroll
   for (int jb = 0; jb < 2; ++jb) pf[jb] = load_frag_nt<P>(ws + L::Pm + (size_t)(w * 2 + jb) * 64 * L::FB, lane);
@@ -664,7 +647,8 @@ __global__ void __launch_bounds__(256) output_kernel(ScanParams p) {
 static inline unsigned state_grid(int64_t B, int64_t H, int nv) { return (unsigned)(8 * ((B * H + 7) / 8) * nv); }
 
 // ------------------------------------------------------------------------------------------------
-enum Phase { PHASE_PREP = 1, PHASE_STATE = 2, PHASE_OUTPUT = 4, PHASE_ALL = 7, PHASE_CHAIN = 8 };
+// PHASE_PREP_FUSED is prep writing the fused chain's record layout (K as plain fragments, Q stored).
+enum Phase { PHASE_PREP = 1, PHASE_STATE = 2, PHASE_OUTPUT = 4, PHASE_ALL = 7, PHASE_CHAIN = 8, PHASE_PREP_FUSED = 16 };
 
 // Two schedules for a whole-scan call with bf16 inputs:
 //  - split: prep / state / output (the state kernel streams only K, 64 KB per chunk, through its LDS ring;
@@ -711,7 +695,6 @@ static ScanParams fill_params(const kdn_scan_args* a) {
   p.seq_lo = a->cu_seqlens;
   p.seq_hi = a->cu_seqlens ? a->cu_seqlens + 1 : nullptr;
   p.slots = a->state_slots;
-  p.relift_q = 0;
   p.prep_no_q = 0;
   p.k_plain = 0;
   return p;
@@ -797,33 +780,26 @@ static int launch_phase(const ScanParams& p, int phase, hipStream_t st) {
       if (p.decay) hipLaunchKernelGGL((state_kernel<P, D, DV, true>), dim3(state_grid(p.B, p.H, DV / 16)), dim3(256), excl, st, p);
       else hipLaunchKernelGGL((state_kernel<P, D, DV, false>), dim3(state_grid(p.B, p.H, DV / 16)), dim3(256), excl, st, p);
     }
-  } else if (IsBF16<P>::value && p.relift_q) {
-    hipLaunchKernelGGL((output_kernel<P, OutT, D, DV, IsBF16<P>::value>), chunk_grid, dim3(256), 0, st, p);
   } else {
-    hipLaunchKernelGGL((output_kernel<P, OutT, D, DV, false>), chunk_grid, dim3(256), 0, st, p);
+    hipLaunchKernelGGL((output_kernel<P, OutT, D, DV>), chunk_grid, dim3(256), 0, st, p);
   }
   return hipGetLastError() == hipSuccess ? KDN_OK : KDN_ERR_DEVICE;
 }
 
 // Runs chunks [c_begin, c_end) in segments of `seg` chunks, all in one workspace buffer: per segment the
-// selected kernels, in the order prep, state, output.
+// selected kernels, in the order prep, state, output (split) or prep, chain (fused).  A whole-scan call
+// (PHASE_ALL) takes the schedule use_fused() picks.
 template <class P, typename InT, typename OutT, int D, int DV>
 static int run_scan(const kdn_scan_args* a, const RunSpec& r) {
   const int cus = device_cus();
-  const bool fused = Fused<P, D>::value && r.phases == PHASE_ALL && use_fused(a);
+  int phases = r.phases;
+  if (phases == PHASE_ALL && Fused<P, D>::value && use_fused(a)) phases = PHASE_PREP_FUSED | PHASE_CHAIN;
   for (int64_t c0 = r.c_begin; c0 < r.c_end; c0 += r.seg) {
     ScanParams p = segment_params(a, r, c0, (r.c_end - c0 < r.seg) ? (r.c_end - c0) : r.seg, a->workspace, cus);
-    if (fused) {
-      p.k_plain = 1;
-      for (int ph : {PHASE_PREP, PHASE_CHAIN}) {
-        const int rc = launch_phase<P, InT, OutT, D, DV>(p, ph, r.st);
-        if (rc != KDN_OK) return rc;
-      }
-      continue;
-    }
-    for (int ph : {PHASE_PREP, PHASE_STATE, PHASE_OUTPUT}) {
-      if (!(r.phases & ph)) continue;
-      const int rc = launch_phase<P, InT, OutT, D, DV>(p, ph, r.st);
+    if (phases & (PHASE_PREP_FUSED | PHASE_CHAIN)) p.k_plain = 1;
+    for (int ph : {PHASE_PREP, PHASE_PREP_FUSED, PHASE_STATE, PHASE_CHAIN, PHASE_OUTPUT}) {
+      if (!(phases & ph)) continue;
+      const int rc = launch_phase<P, InT, OutT, D, DV>(p, ph == PHASE_PREP_FUSED ? PHASE_PREP : ph, r.st);
       if (rc != KDN_OK) return rc;
     }
   }
@@ -859,16 +835,10 @@ static int run_pipelined(const kdn_scan_args* a, const RunSpec& r) {
   hipEvent_t evIn = evs.ev[3 * nbuf], evOut = evs.ev[3 * nbuf + 1];
   // prep shares the device with the state kernel's workgroups (one per CU)
   const int prep_cus = device_cus() - (int)state_grid(a->B, a->H, DV / 16);
-  // With CUs to spare beside the state chain, the output kernel lifts q again rather than reading the
-  // features back: the chain is slowed by the HBM traffic of the kernels beside it, not by their work.
-  const bool relift = IsBF16<P>::value && a->feature_mode == 0 && !a->omega_lo && !r.seq_lo && !a->cu_seqlens &&
-                      prep_cus > 0;
   auto seg_p = [&](int64_t s) {
     const int64_t c0 = s * seg;
-    ScanParams p = segment_params(a, r, c0, (nchunks - c0 < seg) ? (nchunks - c0) : seg,
-                                  (unsigned char*)a->workspace + (size_t)(s % nbuf) * buf_bytes, prep_cus);
-    p.relift_q = relift ? 1 : 0;
-    return p;
+    return segment_params(a, r, c0, (nchunks - c0 < seg) ? (nchunks - c0) : seg,
+                          (unsigned char*)a->workspace + (size_t)(s % nbuf) * buf_bytes, prep_cus);
   };
 #define KDN_TRY(x) do { if ((x) != hipSuccess) return KDN_ERR_DEVICE; } while (0)
 #define KDN_TRYK(x) do { const int _rc = (x); if (_rc != KDN_OK) return _rc; } while (0)
@@ -1048,6 +1018,8 @@ static int run_phase(const kdn_scan_args* a, int64_t chunk0, int64_t nchunks, in
   int rc = validate_launch(a);
   if (rc != KDN_OK) return rc;
   if (general_scan_applies(a)) return KDN_ERR_UNSUPPORTED;  // the general-D scan has no phase entry points
+  // the fused schedule's phases exist for bf16 inputs at D = 512
+  if ((phase & (PHASE_PREP_FUSED | PHASE_CHAIN)) && a->in_dtype != KDN_DTYPE_BF16) return KDN_ERR_UNSUPPORTED;
   const int64_t total = (a->T + CH - 1) / CH;
   if (chunk0 < 0 || nchunks < 1 || chunk0 + nchunks > total) return KDN_ERR_INVALID_ARGUMENT;
   const size_t need = chunk_bytes(a) * (size_t)a->B * (size_t)a->H * (size_t)(nchunks + 1);
@@ -1074,8 +1046,7 @@ static int checkpoints_t(const kdn_scan_args* a, int64_t seg, int64_t n, float* 
     const int64_t c0 = s * seg;
     ScanParams p = segment_params(a, r, c0, (nchunks - c0 < seg) ? (nchunks - c0) : seg,
                                   ws + (size_t)(side ? s % nbuf : 0) * buf_bytes, prep_cus);
-    p.relift_q = 1;  // no output kernel reads the lifted queries
-    p.prep_no_q = 1;
+    p.prep_no_q = 1;  // no output kernel reads the lifted queries
     p.y = nullptr;
     if (s > 0) {
       p.state_in = ckpt + (size_t)(s - 1) * state_floats;
@@ -1156,11 +1127,22 @@ extern "C" int kdn_delta_scan_fwd(const kdn_scan_args* a, void* stream) {
   return dispatch(a, 0, nchunks, seg, PHASE_ALL, as_stream(stream));
 }
 
-// Default segment of the pipelined scan: 64 chunks (4096 tokens), fewer for short sequences.
+// Default segment of the pipelined scan: 64 or 128 chunks, fewer for short sequences
+// (128 while the split schedule's state workgroups leave CUs idle, where the chain is a latency-bound
+// sequence and longer segments mean fewer launch gaps on it: config 3 2.565 against 2.598 ms for 64.)
 static int64_t pipeline_segment(const kdn_scan_args* a) {
   const int64_t nchunks = (a->T + CH - 1) / CH;
-  const int64_t seg = a->segment_chunks > 0 ? a->segment_chunks : 64;
+  int64_t seg = a->segment_chunks;
+  if (seg <= 0) {
+    const int cus = device_cus();
+    seg = (cus > 0 && (int64_t)state_grid(a->B, a->H, a->d_v / 16) < cus) ? 128 : 64;
+  }
   return seg < nchunks ? seg : nchunks;
+}
+
+extern "C" int64_t kdn_scan_segment_chunks(const kdn_scan_args* a, int pipelined) {
+  if (validate(a) != KDN_OK || general_scan_applies(a)) return 0;
+  return pipelined ? pipeline_segment(a) : choose_segment(a);
 }
 
 extern "C" size_t kdn_scan_workspace_bytes_pipelined(const kdn_scan_args* a) {
@@ -1221,6 +1203,21 @@ extern "C" int kdn_scan_state(const kdn_scan_args* a, int64_t chunk0, int64_t nc
 
 extern "C" int kdn_scan_output(const kdn_scan_args* a, int64_t chunk0, int64_t nchunks, void* stream) {
   return run_phase(a, chunk0, nchunks, PHASE_OUTPUT, stream);
+}
+
+extern "C" int kdn_scan_prep_fused(const kdn_scan_args* a, int64_t chunk0, int64_t nchunks, void* stream) {
+  return run_phase(a, chunk0, nchunks, PHASE_PREP_FUSED, stream);
+}
+
+extern "C" int kdn_scan_chain(const kdn_scan_args* a, int64_t chunk0, int64_t nchunks, void* stream) {
+  return run_phase(a, chunk0, nchunks, PHASE_CHAIN, stream);
+}
+
+extern "C" int kdn_scan_schedule(const kdn_scan_args* a) {
+  const int rc = validate(a);
+  if (rc != KDN_OK) return rc;
+  if (general_scan_applies(a)) return KDN_SCHEDULE_GENERAL;
+  return (a->in_dtype == KDN_DTYPE_BF16 && use_fused(a)) ? KDN_SCHEDULE_FUSED : KDN_SCHEDULE_SPLIT;
 }
 
 // ------------------------------------------------------------------------------------------------

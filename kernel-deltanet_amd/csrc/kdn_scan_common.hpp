@@ -94,9 +94,6 @@ struct ScanParams {
   const float* inv_tau_head;
   int no_renorm, prelifted;
   int linear;  // update rule without the erasure term: T = I, Tp = 0
-  // the output kernel lifts q itself and prep does not store phiQ (bf16, exact projection, pipelined
-  // with CUs to spare: recomputing q's features on those CUs is cheaper than streaming them through HBM)
-  int relift_q;
   // no output kernel reads the segment (the backward's checkpoint pass): prep lifts only the keys
   int prep_no_q;
   // the fused chain reads the segment (kdn_chain.hip): prep stores K as plain fragments (each lane's 16

@@ -32,6 +32,10 @@ EXPORTED = (
     "kdn_scan_prep",
     "kdn_scan_state",
     "kdn_scan_output",
+    "kdn_scan_prep_fused",
+    "kdn_scan_chain",
+    "kdn_scan_schedule",
+    "kdn_scan_segment_chunks",
     "kdn_scan_workspace_bytes_pipelined",
     "kdn_delta_scan_fwd_pipelined",
     "kdn_delta_scan_fwd_streams",
@@ -188,7 +192,11 @@ def lib() -> ctypes.CDLL:
             L.kdn_delta_scan_fwd_pipelined.restype = ci
             L.kdn_delta_scan_fwd_streams.argtypes = [ctypes.POINTER(ScanArgs), vp, vp, vp]
             L.kdn_delta_scan_fwd_streams.restype = ci
-            for nm in ("kdn_scan_prep", "kdn_scan_state", "kdn_scan_output"):
+            L.kdn_scan_schedule.argtypes = [ctypes.POINTER(ScanArgs)]
+            L.kdn_scan_schedule.restype = ci
+            L.kdn_scan_segment_chunks.argtypes = [ctypes.POINTER(ScanArgs), ci]
+            L.kdn_scan_segment_chunks.restype = i64
+            for nm in ("kdn_scan_prep", "kdn_scan_state", "kdn_scan_output", "kdn_scan_prep_fused", "kdn_scan_chain"):
                 fn = getattr(L, nm)
                 fn.argtypes = [ctypes.POINTER(ScanArgs), i64, i64, vp]
                 fn.restype = ci

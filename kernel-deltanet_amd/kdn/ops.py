@@ -620,12 +620,17 @@ def _features_on(fm: FeatureMap, dev: torch.device, H: int) -> FeatureMap:
                       fm.no_renorm, False)
 
 
+SCHEDULE_SPLIT, SCHEDULE_FUSED, SCHEDULE_GENERAL = 0, 1, 2  # kdn_scan_schedule (include/kdn.h)
+
+
 class ScanPlan:
     """Reusable launch description for repeated prefills of one shape (benchmarks, serving loops).
 
     Holds the filled kdn_scan_args, the workspace for one segment of `segment_chunks` chunks and the
     tensors the arguments point into, so each run is only the native calls.  `run()` is
-    kdn_delta_scan_fwd; `prep()` / `state()` launch the two phases of one segment.
+    kdn_delta_scan_fwd (or the pipelined variant); `schedule` is the schedule it runs (kdn_scan_schedule:
+    SCHEDULE_SPLIT or SCHEDULE_FUSED) and `prep()` / `state()` / `output()` (split) or `prep_fused()` /
+    `chain()` (fused) launch that schedule's phases of one segment.
     """
 
     def __init__(self, q, k, v, beta, decay, omega_bf16, phase, inv_tau, normalize=False, initial_state=None,
@@ -635,10 +640,6 @@ class ScanPlan:
         D, d_v = omega_bf16.shape[0], v.shape[-1]
         self.nchunks = (T + 63) // 64
         self.pipelined = pipelined
-        if pipelined:
-            self.segment_chunks = min(segment_chunks if segment_chunks > 0 else 64, self.nchunks)
-        else:
-            self.segment_chunks = self.nchunks if segment_chunks <= 0 else min(segment_chunks, self.nchunks)
         self.q, self.k, self.v = _last_contig(q), _last_contig(k), _last_contig(v)
         self.beta = beta.to(torch.float32)
         self.decay = None if decay is None else decay.to(torch.float32)
@@ -647,6 +648,14 @@ class ScanPlan:
         self.initial_state = initial_state
         self.final_state = torch.empty(B, H, D, d_v, device=dev, dtype=torch.float32)
         self.y = torch.empty(B, T, H, d_v, device=dev, dtype=q.dtype if out_dtype is None else out_dtype)
+        # the library's segment length for this shape (its default when segment_chunks is 0)
+        probe = scan_args(self.q, self.k, self.v, self.beta, self.decay, self.omega, self.phase, inv_tau, normalize,
+                          initial_state, self.final_state, self.y, None, segment_chunks)
+        with torch.cuda.device(dev):
+            self.segment_chunks = int(N.lib().kdn_scan_segment_chunks(ctypes.byref(probe), 1 if pipelined else 0))
+            self.schedule = int(N.lib().kdn_scan_schedule(ctypes.byref(probe)))
+        if self.segment_chunks <= 0 or self.schedule < 0:
+            raise ValueError("ScanPlan: unsupported shape")
         nbytes = scan_workspace_bytes(self.q, self.v, self.omega, self.segment_chunks, pipelined)
         if nbytes == 0:
             raise ValueError("ScanPlan: unsupported shape")
@@ -680,6 +689,12 @@ class ScanPlan:
 
     def output(self, chunk0: int, nchunks: int, args: Optional[N.ScanArgs] = None, stream=None):
         self._phase("kdn_scan_output", chunk0, nchunks, args, stream)
+
+    def prep_fused(self, chunk0: int, nchunks: int, args: Optional[N.ScanArgs] = None, stream=None):
+        self._phase("kdn_scan_prep_fused", chunk0, nchunks, args, stream)
+
+    def chain(self, chunk0: int, nchunks: int, args: Optional[N.ScanArgs] = None, stream=None):
+        self._phase("kdn_scan_chain", chunk0, nchunks, args, stream)
 
     def _phase(self, name, chunk0, nchunks, args, stream):
         a = self.args if args is None else args

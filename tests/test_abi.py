@@ -62,7 +62,7 @@ def test_args_layout_matches_c(cname, pystruct):
 def test_strerror_and_version(lib):
     for code in (0, -1, -2, -3, -4, -5, -99):
         assert len(lib.kdn_strerror(code)) > 0
-    assert lib.kdn_abi_version() == (1 << 16) | 8
+    assert lib.kdn_abi_version() == (2 << 16) | 0
 
 
 def _args(**kw):
@@ -164,6 +164,32 @@ def test_general_width_requests_need_no_device(lib):
     assert lib.kdn_scan_state(ctypes.byref(a), 0, 1, None) == -2
     a.workspace_bytes = 1024
     assert lib.kdn_delta_scan_fwd(ctypes.byref(a), None) == -3
+
+
+def test_schedule_query_and_fused_phases_need_no_device(lib, monkeypatch):
+    """kdn_scan_schedule: the pre-lifted D = 1024 scan is its own schedule, fp32 inputs always run the split
+    kernels, and KDN_SCAN_SCHEDULE (read per call) forces the bf16 choice; the fused schedule's phase entry
+    points reject what the fused chain does not implement before anything is enqueued."""
+    monkeypatch.delenv("KDN_SCAN_SCHEDULE", raising=False)
+    assert lib.kdn_scan_schedule(ctypes.byref(_args(d_k=1024, D=1024, d_v=64, feature_mode=1))) == 2
+    f32 = _args(in_dtype=N.KDN_DTYPE_F32, out_dtype=N.KDN_DTYPE_F32)
+    assert lib.kdn_scan_schedule(ctypes.byref(f32)) == 0
+    monkeypatch.setenv("KDN_SCAN_SCHEDULE", "fused")
+    assert lib.kdn_scan_schedule(ctypes.byref(_args())) == 1
+    assert lib.kdn_scan_schedule(ctypes.byref(f32)) == 0
+    monkeypatch.setenv("KDN_SCAN_SCHEDULE", "split")
+    assert lib.kdn_scan_schedule(ctypes.byref(_args())) == 0
+    assert lib.kdn_scan_schedule(ctypes.byref(_args(d_v=48))) == -2
+    a = _fake_ptrs(_args(T=256, H=2, in_dtype=N.KDN_DTYPE_F32, out_dtype=N.KDN_DTYPE_F32))
+    a.workspace_bytes = 1 << 40
+    assert lib.kdn_scan_prep_fused(ctypes.byref(a), 0, 1, None) == -2
+    assert lib.kdn_scan_chain(ctypes.byref(a), 0, 1, None) == -2
+    g = _fake_ptrs(_args(T=256, H=2, d_k=1024, D=1024, d_v=128, feature_mode=1))
+    g.workspace_bytes = 1 << 40
+    assert lib.kdn_scan_chain(ctypes.byref(g), 0, 1, None) == -2
+    b = _fake_ptrs(_args(T=256, H=2))
+    b.workspace_bytes = 1024
+    assert lib.kdn_scan_chain(ctypes.byref(b), 0, 1, None) == -3
 
 
 def test_backward_workspace_and_errors_need_no_device(lib):
