@@ -1419,8 +1419,15 @@ static BwdLayout bwd_layout(const kdn_scan_args* f, bool want_dit) {
   return L;
 }
 
+namespace vsplit {
+static bool applies(const kdn_scan_args* f);
+static size_t workspace_bytes(const kdn_scan_bwd_args* a);
+static int64_t segments(const kdn_scan_bwd_args* a, int64_t* segment_chunks);
+}  // namespace vsplit
+
 extern "C" size_t kdn_scan_bwd_workspace_bytes(const kdn_scan_bwd_args* a) {
   if (a && general_bwd_applies(a->fwd)) return general_bwd_workspace_bytes(a);
+  if (a && vsplit::applies(a->fwd)) return vsplit::workspace_bytes(a);
   if (bwd_check(a) != KDN_OK) return 0;
   return bwd_layout(a->fwd, a->dinv_tau != nullptr).total;
 }
@@ -1431,6 +1438,7 @@ extern "C" int64_t kdn_scan_bwd_segments(const kdn_scan_bwd_args* a, int64_t* se
     if (segment_chunks) *segment_chunks = bwd_chunks(a->fwd);
     return 1;
   }
+  if (a && vsplit::applies(a->fwd)) return vsplit::segments(a, segment_chunks);
   if (bwd_check(a) != KDN_OK) return 0;
   const BwdLayout L = bwd_layout(a->fwd, a->dinv_tau != nullptr);
   if (segment_chunks) *segment_chunks = L.seg;
@@ -1632,15 +1640,282 @@ static int bwd_params(const kdn_scan_bwd_args* a, Params& p, BwdLayout& L) {
 
 // bf16 inputs: the D = 512 contractions take bf16 operands with fp32 accumulation, the forward's policy
 // for bf16 inputs; the lift and the 64 x 64 chunk algebra stay in fp32 MFMA.
-static int bwd_run(const kdn_scan_bwd_args* a, void* stream, void* aux_stream) {
-  if (a && general_bwd_applies(a->fwd)) return general_bwd(a, stream);  // one stream
+static int bwd_run64(const kdn_scan_bwd_args* a, hipStream_t st, hipStream_t aux) {
   Params p;
   BwdLayout L;
   const int rc = bwd_params(a, p, L);
   if (rc != KDN_OK) return rc;
-  const hipStream_t st = as_stream(stream), aux = aux_stream ? as_stream(aux_stream) : nullptr;
   if (a->fwd->in_dtype == KDN_DTYPE_BF16) return bwd_schedule<PrecBF16, __bf16>(a, p, L, st, aux);
   return bwd_schedule<PrecF32, float>(a, p, L, st, aux);
+}
+
+// ------------------------------------------------------------------------------------------------
+// d_v = 16, 32 or 128 at D = 512: the kernels above are built for 64 value columns.  The value columns of
+// the rule are independent given the keys, beta and lambda: row j of S evolves from column j of v alone
+// (S_t[j] = lambda_t S_{t-1}[j] (I - beta_t k k^T) + beta_t v_t[j] k^T), and y[:, j] reads row j only.
+// So the backward of d_v = 128 is the 64-wide backward of each column half, whose gradients of q, k,
+// beta, lambda and 1/tau add up (the second half's go to workspace buffers, then are added in a fixed
+// order); the backward of d_v = 16 or 32 is the 64-wide backward of v, dL/dy, the initial state and
+// dL/dS_T padded with zero columns (zero columns of S and of dL/dS stay zero and add exact zeros to every
+// shared gradient), with dv and dL/dS_0 cut back to d_v columns.
+namespace vsplit {
+
+static bool applies(const kdn_scan_args* f) {
+  return f && f->D == D && f->feature_mode == 0 && (f->d_v == 16 || f->d_v == 32 || f->d_v == 128);
+}
+
+// The 64-wide request's arguments and the buffers after its workspace.
+struct Plan {
+  kdn_scan_args f64;
+  size_t base, total;
+  // d_v = 128: the second half's shared gradients (contiguous [B][T][H][64] / [B][T][H] / [H])
+  size_t dq, dk, dbeta, ddecay, dit;
+  // d_v < 64: padded copies (contiguous [B][T][H][64] rows, [B][H][512][64] states)
+  size_t v, dy, s0, dfin, dv, gout;
+};
+
+static size_t up(size_t x) { return (x + 255) / 256 * 256; }
+
+static Plan plan(const kdn_scan_bwd_args* a) {
+  Plan P;
+  P.f64 = *a->fwd;
+  P.f64.d_v = DV;
+  const kdn_scan_args* f = a->fwd;
+  const size_t rows = (size_t)f->B * f->T * f->H, states = (size_t)f->B * f->H * D * DV;
+  P.base = up(bwd_layout(&P.f64, a->dinv_tau != nullptr).total);
+  size_t o = P.base;
+  P.dq = P.dk = P.dbeta = P.ddecay = P.dit = P.v = P.dy = P.s0 = P.dfin = P.dv = P.gout = 0;
+  if (f->d_v > DV) {
+    P.dq = o; o += up(rows * DV * 4);
+    P.dk = o; o += up(rows * DV * 4);
+    P.dbeta = o; o += up(rows * 4);
+    if (a->ddecay) { P.ddecay = o; o += up(rows * 4); }
+    if (a->dinv_tau) { P.dit = o; o += up((size_t)f->H * 4); }
+  } else {
+    P.v = o; o += up(rows * DV * dtype_size(f->in_dtype));
+    P.dy = o; o += up(rows * DV * 4);
+    P.dv = o; o += up(rows * DV * 4);
+    if (f->initial_state) { P.s0 = o; o += up(states * 4); }
+    if (a->d_final_state) { P.dfin = o; o += up(states * 4); }
+    if (a->d_initial_state) { P.gout = o; o += up(states * 4); }
+  }
+  P.total = o;
+  return P;
+}
+
+// rows r = (b, t, h) of a (B, T, H, width) tensor given by three strides, and of a contiguous copy
+struct Rows {
+  int64_t T, H;
+  __device__ __forceinline__ int64_t off(int64_t r, int64_t s0, int64_t s1, int64_t s2) const {
+    const int64_t h = r % H, bt = r / H;
+    return (bt / T) * s0 + (bt % T) * s1 + h * s2;
+  }
+};
+
+// dst[r][c] = c < w ? src(r, c) : 0 for c < 64 (zero-padded contiguous copy)
+template <typename T>
+__global__ void __launch_bounds__(256) pad_rows(const T* src, int64_t s0, int64_t s1, int64_t s2, Rows R, int w,
+                                                T* dst, int64_t n) {
+  for (int64_t i = blockIdx.x * 256ll + threadIdx.x; i < n * DV; i += (int64_t)gridDim.x * 256) {
+    const int64_t r = i / DV;
+    const int c = (int)(i % DV);
+    dst[i] = c < w ? src[R.off(r, s0, s1, s2) + c] : (T)0.f;
+  }
+}
+
+// dst(r, c) = src[r][c] for c < w
+__global__ void __launch_bounds__(256) unpad_rows(const float* src, float* dst, int64_t s0, int64_t s1, int64_t s2,
+                                                  Rows R, int w, int64_t n) {
+  for (int64_t i = blockIdx.x * 256ll + threadIdx.x; i < n * w; i += (int64_t)gridDim.x * 256) {
+    const int64_t r = i / w;
+    const int c = (int)(i % w);
+    dst[R.off(r, s0, s1, s2) + c] = src[r * DV + c];
+  }
+}
+
+// dst(r, c) += src[r][c] for c < w (src rows of w contiguous values)
+__global__ void __launch_bounds__(256) add_rows(const float* src, float* dst, int64_t s0, int64_t s1, int64_t s2,
+                                                Rows R, int w, int64_t n) {
+  for (int64_t i = blockIdx.x * 256ll + threadIdx.x; i < n * w; i += (int64_t)gridDim.x * 256) {
+    const int64_t r = i / w;
+    const int c = (int)(i % w);
+    dst[R.off(r, s0, s1, s2) + c] += src[i];
+  }
+}
+
+// states [b][h][d][c] (four strides) <-> contiguous [B][H][512][64], zero-padded / cut to w columns
+__global__ void __launch_bounds__(256) pad_state(const float* src, int64_t s0, int64_t s1, int64_t s2, int64_t s3,
+                                                 int64_t H, int w, float* dst, int64_t n) {
+  for (int64_t i = blockIdx.x * 256ll + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+    const int c = (int)(i % DV);
+    const int64_t d = (i / DV) % D, bh = i / ((int64_t)DV * D);
+    dst[i] = c < w ? src[(bh / H) * s0 + (bh % H) * s1 + d * s2 + c * s3] : 0.f;
+  }
+}
+__global__ void __launch_bounds__(256) unpad_state(const float* src, float* dst, int64_t s0, int64_t s1, int64_t s2,
+                                                   int64_t s3, int64_t H, int w, int64_t n) {
+  for (int64_t i = blockIdx.x * 256ll + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+    const int c = (int)(i % DV);
+    if (c >= w) continue;
+    const int64_t d = (i / DV) % D, bh = i / ((int64_t)DV * D);
+    dst[(bh / H) * s0 + (bh % H) * s1 + d * s2 + c * s3] = src[i];
+  }
+}
+
+static unsigned grid_for(int64_t n) {
+  const int64_t g = (n + 255) / 256;
+  return (unsigned)(g < 8192 ? (g > 0 ? g : 1) : 8192);
+}
+
+// the request's checks as the 64-wide one's (the pointers and strides of the d_v-wide tensors are what
+// that one reads or writes, with the layouts above)
+static int check(const kdn_scan_bwd_args* a, Plan& P) {
+  if (!a || !a->fwd) return KDN_ERR_INVALID_ARGUMENT;
+  P = plan(a);
+  kdn_scan_bwd_args b = *a;
+  b.fwd = &P.f64;
+  return bwd_check(&b);
+}
+
+static size_t workspace_bytes(const kdn_scan_bwd_args* a) {
+  Plan P;
+  return check(a, P) == KDN_OK ? P.total : 0;
+}
+
+// the 64-wide backward's segments (each of its runs has the same ones)
+static int64_t segments(const kdn_scan_bwd_args* a, int64_t* segment_chunks) {
+  Plan P;
+  if (check(a, P) != KDN_OK) return 0;
+  const BwdLayout L = bwd_layout(&P.f64, a->dinv_tau != nullptr);
+  if (segment_chunks) *segment_chunks = L.seg;
+  return L.nsegs;
+}
+
+static int run(const kdn_scan_bwd_args* a, hipStream_t st, hipStream_t aux) {
+  const kdn_scan_args* f = a->fwd;
+  Plan P;
+  const int rc0 = check(a, P);
+  if (rc0 != KDN_OK) return rc0;
+  kdn_scan_bwd_args b = *a;
+  b.fwd = &P.f64;
+  if (!a->workspace || a->workspace_bytes < P.total) return KDN_ERR_WORKSPACE_TOO_SMALL;
+  if (!aligned(a->workspace, 256)) return KDN_ERR_MISALIGNED;
+  if (f->B > 65535 || f->H > 65535) return KDN_ERR_UNSUPPORTED;
+  unsigned char* ws = static_cast<unsigned char*>(a->workspace);
+  const Rows R = {f->T, f->H};
+  const int64_t rows = f->B * f->T * f->H, states = f->B * f->H * (int64_t)D * DV;
+  b.workspace_bytes = P.base;
+  if (f->d_v > DV) {
+    // first half: the caller's tensors as they are (64-column views)
+    int rc = bwd_run64(&b, st, aux);
+    if (rc != KDN_OK) return rc;
+    // second half: columns 64 .. 127 of v, dL/dy, the states and dv; its shared gradients to the workspace
+    kdn_scan_args g = P.f64;
+    g.v = static_cast<const unsigned char*>(f->v) + DV * dtype_size(f->in_dtype);
+    if (f->initial_state) g.initial_state = f->initial_state + DV * f->init_stride[3];
+    kdn_scan_bwd_args c = *a;
+    c.fwd = &g;
+    c.workspace_bytes = P.base;
+    c.dy = a->dy + DV;
+    if (a->d_final_state) c.d_final_state = a->d_final_state + DV * a->dfinal_stride[3];
+    c.dv = a->dv + DV;
+    if (a->d_initial_state) c.d_initial_state = a->d_initial_state + DV * a->dinit_stride[3];
+    const int64_t rs[3] = {f->T * f->H * DV, f->H * DV, DV}, ss[3] = {f->T * f->H, f->H, 1};
+    c.dq = reinterpret_cast<float*>(ws + P.dq);
+    c.dk = reinterpret_cast<float*>(ws + P.dk);
+    c.dbeta = reinterpret_cast<float*>(ws + P.dbeta);
+    c.ddecay = a->ddecay ? reinterpret_cast<float*>(ws + P.ddecay) : nullptr;
+    c.dinv_tau = a->dinv_tau ? reinterpret_cast<float*>(ws + P.dit) : nullptr;
+    for (int i = 0; i < 3; ++i) {
+      c.dq_stride[i] = rs[i]; c.dk_stride[i] = rs[i];
+      c.dbeta_stride[i] = ss[i]; c.ddecay_stride[i] = ss[i];
+    }
+    rc = bwd_run64(&c, st, aux);
+    if (rc != KDN_OK) return rc;
+    // first half + second half, element by element
+    hipLaunchKernelGGL(add_rows, dim3(grid_for(rows * DV)), dim3(256), 0, st, c.dq, a->dq, a->dq_stride[0],
+                       a->dq_stride[1], a->dq_stride[2], R, DV, rows);
+    hipLaunchKernelGGL(add_rows, dim3(grid_for(rows * DV)), dim3(256), 0, st, c.dk, a->dk, a->dk_stride[0],
+                       a->dk_stride[1], a->dk_stride[2], R, DV, rows);
+    hipLaunchKernelGGL(add_rows, dim3(grid_for(rows)), dim3(256), 0, st, c.dbeta, a->dbeta, a->dbeta_stride[0],
+                       a->dbeta_stride[1], a->dbeta_stride[2], R, 1, rows);
+    if (a->ddecay)
+      hipLaunchKernelGGL(add_rows, dim3(grid_for(rows)), dim3(256), 0, st, c.ddecay, a->ddecay, a->ddecay_stride[0],
+                         a->ddecay_stride[1], a->ddecay_stride[2], R, 1, rows);
+    if (a->dinv_tau) {
+      const Rows Rh = {1, f->H};  // H rows of one value: offset h
+      hipLaunchKernelGGL(add_rows, dim3(1), dim3(256), 0, st, c.dinv_tau, a->dinv_tau, (int64_t)0, (int64_t)0,
+                         (int64_t)1, Rh, 1, f->H);
+    }
+    return launch_status();
+  }
+  // d_v < 64: zero-padded copies in, the 64-wide backward, d_v columns out
+  kdn_scan_args g = P.f64;
+  const int w = (int)f->d_v;
+  const size_t isz = dtype_size(f->in_dtype);
+  void* v64 = ws + P.v;
+  if (isz == 2)
+    hipLaunchKernelGGL(pad_rows<__bf16>, dim3(grid_for(rows * DV)), dim3(256), 0, st,
+                       static_cast<const __bf16*>(f->v), f->v_stride[0], f->v_stride[1], f->v_stride[2], R, w,
+                       static_cast<__bf16*>(v64), rows);
+  else
+    hipLaunchKernelGGL(pad_rows<float>, dim3(grid_for(rows * DV)), dim3(256), 0, st,
+                       static_cast<const float*>(f->v), f->v_stride[0], f->v_stride[1], f->v_stride[2], R, w,
+                       static_cast<float*>(v64), rows);
+  g.v = v64;
+  g.v_stride[0] = f->T * f->H * DV; g.v_stride[1] = f->H * DV; g.v_stride[2] = DV;
+  if (f->initial_state) {
+    float* s0 = reinterpret_cast<float*>(ws + P.s0);
+    hipLaunchKernelGGL(pad_state, dim3(grid_for(states)), dim3(256), 0, st, f->initial_state, f->init_stride[0],
+                       f->init_stride[1], f->init_stride[2], f->init_stride[3], f->H, w, s0, states);
+    g.initial_state = s0;
+    g.init_stride[0] = f->H * (int64_t)D * DV; g.init_stride[1] = (int64_t)D * DV; g.init_stride[2] = DV;
+    g.init_stride[3] = 1;
+  }
+  kdn_scan_bwd_args c = *a;
+  c.fwd = &g;
+  c.workspace_bytes = P.base;
+  float* dy64 = reinterpret_cast<float*>(ws + P.dy);
+  hipLaunchKernelGGL(pad_rows<float>, dim3(grid_for(rows * DV)), dim3(256), 0, st, a->dy, a->dy_stride[0],
+                     a->dy_stride[1], a->dy_stride[2], R, w, dy64, rows);
+  c.dy = dy64;
+  c.dy_stride[0] = f->T * f->H * DV; c.dy_stride[1] = f->H * DV; c.dy_stride[2] = DV;
+  if (a->d_final_state) {
+    float* df = reinterpret_cast<float*>(ws + P.dfin);
+    hipLaunchKernelGGL(pad_state, dim3(grid_for(states)), dim3(256), 0, st, a->d_final_state, a->dfinal_stride[0],
+                       a->dfinal_stride[1], a->dfinal_stride[2], a->dfinal_stride[3], f->H, w, df, states);
+    c.d_final_state = df;
+    c.dfinal_stride[0] = f->H * (int64_t)D * DV; c.dfinal_stride[1] = (int64_t)D * DV; c.dfinal_stride[2] = DV;
+    c.dfinal_stride[3] = 1;
+  }
+  float* dv64 = reinterpret_cast<float*>(ws + P.dv);
+  c.dv = dv64;
+  c.dv_stride[0] = f->T * f->H * DV; c.dv_stride[1] = f->H * DV; c.dv_stride[2] = DV;
+  float* go = a->d_initial_state ? reinterpret_cast<float*>(ws + P.gout) : nullptr;
+  if (go) {
+    c.d_initial_state = go;
+    c.dinit_stride[0] = f->H * (int64_t)D * DV; c.dinit_stride[1] = (int64_t)D * DV; c.dinit_stride[2] = DV;
+    c.dinit_stride[3] = 1;
+  }
+  int rc = launch_status();
+  if (rc != KDN_OK) return rc;
+  rc = bwd_run64(&c, st, aux);
+  if (rc != KDN_OK) return rc;
+  hipLaunchKernelGGL(unpad_rows, dim3(grid_for(rows * w)), dim3(256), 0, st, dv64, a->dv, a->dv_stride[0],
+                     a->dv_stride[1], a->dv_stride[2], R, w, rows);
+  if (go)
+    hipLaunchKernelGGL(unpad_state, dim3(grid_for(states)), dim3(256), 0, st, go, a->d_initial_state,
+                       a->dinit_stride[0], a->dinit_stride[1], a->dinit_stride[2], a->dinit_stride[3], f->H, w, states);
+  return launch_status();
+}
+
+}  // namespace vsplit
+
+static int bwd_run(const kdn_scan_bwd_args* a, void* stream, void* aux_stream) {
+  if (a && general_bwd_applies(a->fwd)) return general_bwd(a, stream);  // one stream
+  const hipStream_t st = as_stream(stream), aux = aux_stream ? as_stream(aux_stream) : nullptr;
+  if (a && vsplit::applies(a->fwd)) return vsplit::run(a, st, aux);
+  return bwd_run64(a, st, aux);
 }
 
 extern "C" int kdn_delta_scan_bwd(const kdn_scan_bwd_args* a, void* stream) { return bwd_run(a, stream, nullptr); }
@@ -1652,6 +1927,7 @@ extern "C" int kdn_delta_scan_bwd_streams(const kdn_scan_bwd_args* a, void* stre
 extern "C" int kdn_scan_bwd_phase(const kdn_scan_bwd_args* a, int phase, int64_t segment, void* stream) {
   if (phase < 0 || phase > 4) return KDN_ERR_INVALID_ARGUMENT;
   if (a && general_bwd_applies(a->fwd)) return KDN_ERR_UNSUPPORTED;  // no phase entry points at D = 1024
+  if (a && vsplit::applies(a->fwd)) return KDN_ERR_UNSUPPORTED;        // nor for d_v other than 64
   Params p;
   BwdLayout L;
   const int rc = bwd_params(a, p, L);

@@ -441,7 +441,7 @@ class ScanBackwardPlan:
         nbytes = N.lib().kdn_scan_bwd_workspace_bytes(ctypes.byref(a))
         if nbytes == 0:
             raise ValueError("scan_backward: unsupported request (kdn_scan_bwd_workspace_bytes returned 0; the "
-                             "backward covers d_k = 64, D = 512, d_v = 64 with lifted features and D = 1024 "
+                             "backward covers d_k = 64, D = 512, d_v 16, 32, 64 or 128 with lifted features and D = 1024 "
                              "pre-lifted features with d_v 64 or 128)")
         if workspace is None or workspace.numel() * workspace.element_size() < nbytes:
             workspace = torch.empty(nbytes, dtype=torch.uint8, device=dev)
@@ -534,12 +534,13 @@ def scan_autograd(q, k, v, beta, decay, omega_bf16, phase, inv_tau, normalize: b
                   initial_state: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor]:
     """`scan` (default schedule) recorded for autograd: gradients flow to q, k, v, beta, decay and
     initial_state through kdn_delta_scan_bwd.  Returns (y (B, T, H, d_v), final_state (B, H, D, d_v)).
-    The backward covers d_k = 64, D = 512, d_v = 64; other shapes are rejected here, before the forward
-    runs, rather than inside .backward()."""
+    The backward covers d_k = 64, D = 512, d_v in {16, 32, 64, 128}; other shapes are rejected here,
+    before the forward runs, rather than inside .backward()."""
     d_k, D, d_v = q.shape[-1], omega_bf16.shape[-2], v.shape[-1]
-    if (d_k, D, d_v) != (64, 512, 64):
-        raise ValueError(f"scan with gradients: the backward supports d_k = 64, D = 512, d_v = 64 (got d_k = {d_k}, "
-                         f"D = {D}, d_v = {d_v}); run the forward under torch.no_grad() or detach the inputs")
+    if d_k != 64 or D != 512 or d_v not in (16, 32, 64, 128):
+        raise ValueError(f"scan with gradients: the backward supports d_k = 64, D = 512, d_v in 16, 32, 64, 128 "
+                         f"(got d_k = {d_k}, D = {D}, d_v = {d_v}); run the forward under torch.no_grad() or detach "
+                         f"the inputs")
     return _Scan.apply(q, k, v, beta, decay, initial_state, omega_bf16, phase, inv_tau, normalize)
 
 
@@ -582,11 +583,12 @@ def feature_scan_autograd(q, k, v, beta, decay, omega, phase, inv_tau_head, omeg
     """`scan` over (B, T, H, .) views with a per-head feature map, recorded for autograd (gradients through
     kdn_delta_scan_bwd to q, k, v, beta, decay, initial_state and inv_tau_head (H,)).  omega (H, 512, 64)
     bf16 with optional bf16 low parts, phase (H, 512), the delta or the linear rule; d_k = 64, D = 512,
-    d_v = 64.  Returns (y (B, T, H, d_v), final_state (B, H, D, d_v))."""
+    d_v in {16, 32, 64, 128}.  Returns (y (B, T, H, d_v), final_state (B, H, D, d_v))."""
     d_k, D, d_v = q.shape[-1], omega.shape[-2], v.shape[-1]
-    if (d_k, D, d_v) != (64, 512, 64):
-        raise ValueError(f"scan with gradients: the backward supports d_k = 64, D = 512, d_v = 64 (got d_k = {d_k}, "
-                         f"D = {D}, d_v = {d_v}); run the forward under torch.no_grad() or detach the inputs")
+    if d_k != 64 or D != 512 or d_v not in (16, 32, 64, 128):
+        raise ValueError(f"scan with gradients: the backward supports d_k = 64, D = 512, d_v in 16, 32, 64, 128 "
+                         f"(got d_k = {d_k}, D = {D}, d_v = {d_v}); run the forward under torch.no_grad() or detach "
+                         f"the inputs")
     return _FeatureScan.apply(q, k, v, beta, decay, initial_state, inv_tau_head, omega, omega_lo, phase,
                               bool(no_renorm), bool(normalize), int(rule))
 

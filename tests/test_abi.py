@@ -217,10 +217,24 @@ def test_backward_workspace_and_errors_need_no_device(lib):
     g.workspace_bytes = 1024
     assert lib.kdn_delta_scan_bwd(ctypes.byref(g), None) == -3
     assert lib.kdn_scan_bwd_phase(ctypes.byref(g), 1, 0, None) == -3
-    f2 = _fake_ptrs(_args(T=256, H=2, d_v=32))
+    f2 = _fake_ptrs(_args(T=256, H=2, d_v=48))                         # d_v outside {16, 32, 64, 128}
     g.fwd = ctypes.addressof(f2)
     assert lib.kdn_scan_bwd_workspace_bytes(ctypes.byref(g)) == 0
     assert lib.kdn_delta_scan_bwd(ctypes.byref(g), None) == -2
+    # d_v = 32 runs the 64-wide backward on zero-padded copies: its workspace, then (256-byte aligned) the
+    # padded v (512 rows x 64 bf16), dy and dv (512 x 64 fp32 each); no phase entry points
+    f2.d_v = 32
+    assert lib.kdn_scan_bwd_workspace_bytes(ctypes.byref(g)) == 2 * 4 * 1099776 + 65536 + 512 * 64 * (2 + 4 + 4)
+    seg = ctypes.c_int64(0)
+    assert lib.kdn_scan_bwd_segments(ctypes.byref(g), ctypes.byref(seg)) == 1 and seg.value == 4
+    g.workspace_bytes = 1 << 40
+    assert lib.kdn_scan_bwd_phase(ctypes.byref(g), 1, 0, None) == -2
+    g.workspace_bytes = 1024
+    assert lib.kdn_delta_scan_bwd(ctypes.byref(g), None) == -3
+    # d_v = 128: two 64-wide passes; the second pass's dq, dk (512 x 64 fp32) and dbeta (512 fp32) go to
+    # the workspace before they are added into the outputs
+    f2.d_v = 128
+    assert lib.kdn_scan_bwd_workspace_bytes(ctypes.byref(g)) == 2 * 4 * 1099776 + 65536 + 2 * 512 * 64 * 4 + 2048
     g.fwd = ctypes.addressof(f)
     # per-head Omega with low parts (the P2 / P4 feature maps, ABI 1.7): one Omega^T table per head and
     # part; dL/d(1/tau) adds one fp32 partial per (batch, head, chunk), rounded up to 256 bytes

@@ -184,11 +184,11 @@ def test_function_apply_backward(proj, oproj):
 
 def test_backward_rejects_unsupported_shapes(proj):
     q = torch.randn(1, 64, 1, 64, device=DEV)
-    v = torch.randn(1, 64, 1, 32, device=DEV)
+    v = torch.randn(1, 64, 1, 48, device=DEV)   # d_v outside {16, 32, 64, 128}
     beta = torch.rand(1, 64, 1, device=DEV)
     with pytest.raises(ValueError, match="unsupported"):
         ops.scan_backward(q, q, v, beta, None, proj.device_omega(DEV), proj.device_phase(DEV), proj.tau_star_inv,
-                          torch.randn(1, 64, 1, 32, device=DEV))
+                          torch.randn(1, 64, 1, 48, device=DEV))
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
