@@ -1086,6 +1086,7 @@ static int general_bwd_check(const kdn_scan_bwd_args* a) {
   if (!a || !a->fwd) return KDN_ERR_INVALID_ARGUMENT;
   const kdn_scan_args* f = a->fwd;
   if (f->B <= 0 || f->T <= 0 || f->H <= 0 || !valid_dtype(f->in_dtype)) return KDN_ERR_INVALID_ARGUMENT;
+  if (f->B > 65535 || f->H > 65535) return KDN_ERR_UNSUPPORTED;  // grid y / z limits of the chunk launches
   const int rc = general_scan_validate(f);
   if (rc != KDN_OK) return rc;
   if (a->dinv_tau) return KDN_ERR_UNSUPPORTED;  // pre-lifted features have no temperature

@@ -60,6 +60,8 @@ int general_scan(const kdn_scan_args* a, void* stream);
 bool general_bwd_applies(const kdn_scan_args* f);
 size_t general_bwd_workspace_bytes(const kdn_scan_bwd_args* a);
 int general_bwd(const kdn_scan_bwd_args* a, void* stream);
+// Device address of the current device's copy of kdn_delta_scan_fwd_noalloc's scratch array (kdn_noalloc.hip).
+int noalloc_scratch_address(void** out);
 
 // Events of a multi-stream launch sequence, released when the call returns (destroying an event whose
 // record is still pending is allowed; its resources are freed once it completes).

@@ -26,7 +26,6 @@
 // per-token scale vectors, so a lift never has to hold a whole row before using it.
 #include <cstdlib>
 #include <cstring>
-#include <mutex>
 #include <type_traits>
 #include "kdn_frag.hpp"
 #include "kdn_internal.hpp"
@@ -1221,37 +1220,10 @@ extern "C" int kdn_scan_schedule(const kdn_scan_args* a) {
 }
 
 // ------------------------------------------------------------------------------------------------
-// Allocation-free scan (kdn_delta_scan_fwd_noalloc): the workspace of one segment lives in `scratch`, a
-// file-scope device array, instead of a caller buffer, for callers that cannot allocate.  In host code
-// the name `scratch` is only a host-side stand-in: its device address (one copy per GPU) is looked up
-// with hipGetSymbolAddress on the first call on each device, with that device current, and every use
-// below goes through that address.  The array keeps its contents between calls and nothing reads a
-// record before the segment's prep has written it, so no clearing is needed; calls that overlap on one
-// GPU share the array and race.
-namespace kdn {
-
-static __device__ __align__(256) unsigned char scratch[KDN_NOALLOC_SCRATCH_BYTES];
-
-constexpr int MAX_DEVICES = 64;
-static std::mutex g_scratch_mu;
-static void* g_scratch_ptr[MAX_DEVICES] = {};
-
-// Device address of the current device's copy of `scratch`.
-static int scratch_address(void** out) {
-  int dev = -1;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEVICES) return KDN_ERR_DEVICE;
-  std::lock_guard<std::mutex> lock(g_scratch_mu);
-  if (!g_scratch_ptr[dev]) {
-    void* p = nullptr;
-    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return KDN_ERR_DEVICE;
-    g_scratch_ptr[dev] = p;
-  }
-  *out = g_scratch_ptr[dev];
-  return KDN_OK;
-}
-
-}  // namespace kdn
-
+// Allocation-free scan: the workspace of one segment lives in the fixed scratch array of kdn_noalloc.hip
+// instead of a caller buffer.  The array keeps its contents between calls and nothing reads a record
+// before the segment's prep has written it, so no clearing is needed; calls that overlap on one GPU share
+// the array and race.
 extern "C" int kdn_delta_scan_fwd_noalloc(const kdn_scan_args* a, void* stream) {
   int rc = validate(a);
   if (rc != KDN_OK) return rc;
@@ -1264,7 +1236,7 @@ extern "C" int kdn_delta_scan_fwd_noalloc(const kdn_scan_args* a, void* stream) 
   int64_t seg = fit < nchunks ? fit : nchunks;
   if (a->segment_chunks > 0 && a->segment_chunks < seg) seg = a->segment_chunks;
   void* ws = nullptr;
-  rc = scratch_address(&ws);
+  rc = noalloc_scratch_address(&ws);
   if (rc != KDN_OK) return rc;
   kdn_scan_args b = *a;
   b.workspace = ws;

@@ -26,7 +26,9 @@ import os
 
 import torch
 
-_LIB_PATH = os.environ.get("KDN_LIB") or os.path.join(os.path.dirname(os.path.abspath(__file__)), "kdn", "libkdn.so")
+# KDN_LIBRARY names another build of libkdn.so, as for the kdn package (kdn/_native.py), so both load the same
+# copy
+_LIB_PATH = os.environ.get("KDN_LIBRARY") or os.path.join(os.path.dirname(os.path.abspath(__file__)), "kdn", "libkdn.so")
 _L = None
 _TAG = {torch.float32: 0, torch.bfloat16: 1}
 

@@ -272,6 +272,10 @@ def test_general_width_backward_needs_no_device(lib):
     assert lib.kdn_scan_bwd_phase(ctypes.byref(g), 1, 0, None) == -2   # no phase entry points at D = 1024
     g.workspace_bytes = 1024
     assert lib.kdn_delta_scan_bwd(ctypes.byref(g), None) == -3
+    f.H = 70000                                                        # beyond the chunk launches' grid limit
+    assert lib.kdn_scan_bwd_workspace_bytes(ctypes.byref(g)) == 0
+    assert lib.kdn_delta_scan_bwd(ctypes.byref(g), None) == -2
+    f.H = 2
     g.dinv_tau = 0x7C0000000000                                        # no temperature to differentiate
     assert lib.kdn_scan_bwd_workspace_bytes(ctypes.byref(g)) == 0
     g.dinv_tau = None
