@@ -36,7 +36,8 @@
  * ABI 2.0 (breaking): kdn_scan_bwd_args and kdn_ragged_args gained trailing fields that the library reads
  * on every call (dinv_tau, num_slots) and kdn_scan_bwd_phase gained its `segment` argument in 1.6-1.8;
  * callers built against a header older than 1.8 must be recompiled.  2.0 adds kdn_scan_schedule,
- * kdn_scan_prep_fused and kdn_scan_chain.
+ * kdn_scan_prep_fused and kdn_scan_chain.  2.1 accepts D = 128 and 256 (scan and backward) and d_v 16,
+ * 32 and 128 in the D = 512 backward.
  */
 #ifndef KDN_H
 #define KDN_H
@@ -149,9 +150,13 @@ int kdn_fwht_lift_factored_bwd(const void* x, int64_t rows, int64_t x_row_stride
  * state stride {d_v*D, 0, 1, D}. */
 typedef struct kdn_scan_args {
   int64_t B, T, H;
-  int d_k, D, d_v;             /* d_k = 64, D = 512, d_v a multiple of 16 up to 128; or (ABI 1.4) pre-lifted
-                                * features with d_k = D = 1024, d_v 64 or 128, the delta rule, uniform batches
-                                * (the factored d_k = 128 path; full-scan entry points only) */
+  int d_k, D, d_v;             /* d_k = 64, D = 512, d_v 16, 32, 64 or 128; or (ABI 2.1) D = 128 or 256, run
+                                * on the D = 512 kernels with Omega and the phases replicated 512 / D times
+                                * (exact: the replicated features have the D-wide inner products; the state
+                                * is folded back to D columns), uniform batches, full-scan entry points only;
+                                * or (ABI 1.4) pre-lifted features with d_k = D = 1024, d_v 64 or 128, the
+                                * delta rule, uniform batches (the factored d_k = 128 path; full-scan entry
+                                * points only) */
   int in_dtype;                /* dtype of q, k, v */
   int out_dtype;               /* dtype of y */
   int normalize_input;         /* L2-normalise q, k rows (F.normalize, eps 1e-6) before the lift */
@@ -193,7 +198,8 @@ typedef struct kdn_scan_args {
 } kdn_scan_args;
 
 /* Workspace bytes kdn_delta_scan_fwd needs for these arguments (0 if the arguments are invalid).
- * Only the shape, dtype and segment_chunks fields are read. */
+ * Only the shape, dtype and segment_chunks fields are read, and at D = 128 or 256 also omega_lo (NULL or
+ * not), omega_head_stride and phase_head_stride (zero or not), which size the replicated tables. */
 size_t kdn_scan_workspace_bytes(const kdn_scan_args* a);
 
 /* The exact chunked gated delta rule with readout before update (see top of file), carried in fp32,

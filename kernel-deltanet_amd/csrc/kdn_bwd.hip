@@ -1425,8 +1425,14 @@ static size_t workspace_bytes(const kdn_scan_bwd_args* a);
 static int64_t segments(const kdn_scan_bwd_args* a, int64_t* segment_chunks);
 }  // namespace vsplit
 
+namespace frep {
+static size_t workspace_bytes(const kdn_scan_bwd_args* a);
+static int64_t segments(const kdn_scan_bwd_args* a, int64_t* segment_chunks);
+}  // namespace frep
+
 extern "C" size_t kdn_scan_bwd_workspace_bytes(const kdn_scan_bwd_args* a) {
   if (a && general_bwd_applies(a->fwd)) return general_bwd_workspace_bytes(a);
+  if (a && a->fwd && frep_applies(a->fwd)) return frep::workspace_bytes(a);
   if (a && vsplit::applies(a->fwd)) return vsplit::workspace_bytes(a);
   if (bwd_check(a) != KDN_OK) return 0;
   return bwd_layout(a->fwd, a->dinv_tau != nullptr).total;
@@ -1438,6 +1444,7 @@ extern "C" int64_t kdn_scan_bwd_segments(const kdn_scan_bwd_args* a, int64_t* se
     if (segment_chunks) *segment_chunks = bwd_chunks(a->fwd);
     return 1;
   }
+  if (a && a->fwd && frep_applies(a->fwd)) return frep::segments(a, segment_chunks);
   if (a && vsplit::applies(a->fwd)) return vsplit::segments(a, segment_chunks);
   if (bwd_check(a) != KDN_OK) return 0;
   const BwdLayout L = bwd_layout(a->fwd, a->dinv_tau != nullptr);
@@ -1911,8 +1918,91 @@ static int run(const kdn_scan_bwd_args* a, hipStream_t st, hipStream_t aux) {
 
 }  // namespace vsplit
 
+static int bwd_run(const kdn_scan_bwd_args* a, void* stream, void* aux_stream);
+
+// ------------------------------------------------------------------------------------------------
+// D = 128 and 256 (feature replication, kdn_frep.hip): the 512-wide backward on replicated Omega and
+// phases, from L(S_0) with dL/dS'_T = L(dL/dS_T); dL/dS_0 = P(dL/dS'_0).  Its workspace: the 512-wide
+// request's, then the tables and three 512-wide states (S'_0, dL/dS'_T, dL/dS'_0).
+namespace frep {
+
+// The 512-wide request with the caller's pointers (for sizing and checks) and its workspace bytes.
+static size_t base_bytes(const kdn_scan_bwd_args* a, kdn_scan_args* w) {
+  *w = frep_wide(a->fwd, nullptr, nullptr);
+  kdn_scan_bwd_args g = *a;
+  g.fwd = w;
+  return kdn_scan_bwd_workspace_bytes(&g);
+}
+
+static size_t workspace_bytes(const kdn_scan_bwd_args* a) {
+  if (a->fwd->cu_seqlens || a->fwd->state_slots) return 0;
+  kdn_scan_args w;
+  const size_t base = base_bytes(a, &w);
+  return base ? frep_layout(a->fwd, base, 3).total : 0;
+}
+
+static int64_t segments(const kdn_scan_bwd_args* a, int64_t* segment_chunks) {
+  if (workspace_bytes(a) == 0) return 0;
+  kdn_scan_args w = frep_wide(a->fwd, nullptr, nullptr);
+  kdn_scan_bwd_args g = *a;
+  g.fwd = &w;
+  return kdn_scan_bwd_segments(&g, segment_chunks);
+}
+
+static int run(const kdn_scan_bwd_args* a, void* stream, void* aux) {
+  const kdn_scan_args* f = a->fwd;
+  const size_t need = workspace_bytes(a);
+  if (!need) {  // the 512-wide request's own argument error (its checks at d_v = 64), else unsupported
+    kdn_scan_args wc = frep_wide(f, nullptr, nullptr);
+    wc.d_v = 64;
+    kdn_scan_bwd_args gc = *a;
+    gc.fwd = &wc;
+    const int rc = bwd_check(&gc);
+    return rc != KDN_OK ? rc : KDN_ERR_UNSUPPORTED;
+  }
+  if (!a->workspace || a->workspace_bytes < need) return KDN_ERR_WORKSPACE_TOO_SMALL;
+  if (!aligned(a->workspace, 256)) return KDN_ERR_MISALIGNED;
+  kdn_scan_args w0;
+  const FrepLayout L = frep_layout(f, base_bytes(a, &w0), 3);
+  kdn_scan_args w = frep_wide(f, &L, a->workspace);
+  w.workspace = f->workspace;
+  w.workspace_bytes = f->workspace_bytes;
+  unsigned char* ws = static_cast<unsigned char*>(a->workspace);
+  float* s0 = reinterpret_cast<float*>(ws + L.state[0]);
+  float* dsT = reinterpret_cast<float*>(ws + L.state[1]);
+  float* ds0 = reinterpret_cast<float*>(ws + L.state[2]);
+  int64_t cs[4];
+  frep_contiguous_strides(f, cs);
+  kdn_scan_bwd_args g = *a;
+  g.fwd = &w;
+  g.workspace_bytes = L.base;
+  if (f->initial_state) {
+    w.initial_state = s0;
+    for (int i = 0; i < 4; ++i) w.init_stride[i] = cs[i];
+  }
+  if (a->d_final_state) {
+    g.d_final_state = dsT;
+    for (int i = 0; i < 4; ++i) g.dfinal_stride[i] = cs[i];
+  }
+  if (a->d_initial_state) {
+    g.d_initial_state = ds0;
+    for (int i = 0; i < 4; ++i) g.dinit_stride[i] = cs[i];
+  }
+  const hipStream_t st = as_stream(stream);
+  int rc = frep_tables(f, &L, a->workspace, st);
+  if (rc == KDN_OK && f->initial_state) rc = frep_state_lift(f, f->initial_state, f->init_stride, s0, st);
+  if (rc == KDN_OK && a->d_final_state) rc = frep_state_lift(f, a->d_final_state, a->dfinal_stride, dsT, st);
+  if (rc != KDN_OK) return rc;
+  rc = bwd_run(&g, stream, aux);
+  if (rc != KDN_OK || !a->d_initial_state) return rc;
+  return frep_state_fold(f, ds0, a->d_initial_state, a->dinit_stride, st);
+}
+
+}  // namespace frep
+
 static int bwd_run(const kdn_scan_bwd_args* a, void* stream, void* aux_stream) {
   if (a && general_bwd_applies(a->fwd)) return general_bwd(a, stream);  // one stream
+  if (a && a->fwd && frep_applies(a->fwd)) return frep::run(a, stream, aux_stream);
   const hipStream_t st = as_stream(stream), aux = aux_stream ? as_stream(aux_stream) : nullptr;
   if (a && vsplit::applies(a->fwd)) return vsplit::run(a, st, aux);
   return bwd_run64(a, st, aux);
@@ -1928,6 +2018,7 @@ extern "C" int kdn_scan_bwd_phase(const kdn_scan_bwd_args* a, int phase, int64_t
   if (phase < 0 || phase > 4) return KDN_ERR_INVALID_ARGUMENT;
   if (a && general_bwd_applies(a->fwd)) return KDN_ERR_UNSUPPORTED;  // no phase entry points at D = 1024
   if (a && vsplit::applies(a->fwd)) return KDN_ERR_UNSUPPORTED;        // nor for d_v other than 64
+  if (a && a->fwd && frep_applies(a->fwd)) return KDN_ERR_UNSUPPORTED;  // nor for D = 128, 256
   Params p;
   BwdLayout L;
   const int rc = bwd_params(a, p, L);

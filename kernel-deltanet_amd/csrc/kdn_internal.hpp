@@ -63,6 +63,24 @@ int general_bwd(const kdn_scan_bwd_args* a, void* stream);
 // Device address of the current device's copy of kdn_delta_scan_fwd_noalloc's scratch array (kdn_noalloc.hip).
 int noalloc_scratch_address(void** out);
 
+// D = 128 and 256 lifts on the D = 512 kernels by feature replication (kdn_frep.hip).  Workspace of such a
+// request: [0, base) the 512-wide request's own workspace, then the replicated Omega (and low parts) and
+// phases, then up to three 512-wide fp32 states [B][H][512][d_v] (offsets from the workspace start).
+bool frep_applies(const kdn_scan_args* a);
+struct FrepLayout {
+  size_t base, omega, omega_lo, phase, state[3], total;
+};
+FrepLayout frep_layout(const kdn_scan_args* a, size_t base, int nstates);
+size_t frep_state_bytes(const kdn_scan_args* a);
+// *a at D = 512: per-head strides of the replicated tables; with L and ws, tables and workspace in ws
+// (workspace_bytes = L->base); the state pointers are left as in *a
+kdn_scan_args frep_wide(const kdn_scan_args* a, const FrepLayout* L, void* ws);
+void frep_contiguous_strides(const kdn_scan_args* a, int64_t s[4]);
+int frep_tables(const kdn_scan_args* a, const FrepLayout* L, void* ws, hipStream_t st);
+// L(S) = S J^T into a contiguous 512-wide state, and P(S') = S' J from one (s4: the D-wide state's strides)
+int frep_state_lift(const kdn_scan_args* a, const float* s, const int64_t* s4, float* dst, hipStream_t st);
+int frep_state_fold(const kdn_scan_args* a, const float* src, float* s, const int64_t* s4, hipStream_t st);
+
 // Events of a multi-stream launch sequence, released when the call returns (destroying an event whose
 // record is still pending is allowed; its resources are freed once it completes).
 struct EventSet {

@@ -933,6 +933,7 @@ static int dispatch_dv(const kdn_scan_args* a, const RunSpec& r) {
 }
 
 static int dispatch(const kdn_scan_args* a, const RunSpec& r) {
+  if (a->D != 512) return KDN_ERR_UNSUPPORTED;  // narrower lifts arrive here replicated to 512 (kdn_frep.hip)
   if (a->in_dtype == KDN_DTYPE_BF16) {
     if (a->out_dtype == KDN_DTYPE_BF16) return dispatch_dv<PrecBF16, __bf16, __bf16, 512>(a, r);
     return dispatch_dv<PrecBF16, __bf16, float, 512>(a, r);
@@ -978,7 +979,7 @@ static int validate(const kdn_scan_args* a) {
   if (general_scan_applies(a)) {
     const int rc = general_scan_validate(a);  // D = 1024: pre-lifted features, kdn_general.hip
     if (rc != KDN_OK) return rc;
-  } else if (a->D != 512) {
+  } else if (a->D != 512 && !frep_applies(a)) {  // D = 128, 256: lifted, then replicated to 512
     return KDN_ERR_UNSUPPORTED;
   }
   if (a->feature_mode == 0 ? a->d_k != 64 : a->d_k != a->D) return KDN_ERR_UNSUPPORTED;
@@ -1016,7 +1017,8 @@ static int validate_launch(const kdn_scan_args* a) {
 static int run_phase(const kdn_scan_args* a, int64_t chunk0, int64_t nchunks, int phase, void* stream) {
   int rc = validate_launch(a);
   if (rc != KDN_OK) return rc;
-  if (general_scan_applies(a)) return KDN_ERR_UNSUPPORTED;  // the general-D scan has no phase entry points
+  // neither the general-D scan nor the replicated narrower lifts have phase entry points
+  if (general_scan_applies(a) || frep_applies(a)) return KDN_ERR_UNSUPPORTED;
   // the fused schedule's phases exist for bf16 inputs at D = 512
   if ((phase & (PHASE_PREP_FUSED | PHASE_CHAIN)) && a->in_dtype != KDN_DTYPE_BF16) return KDN_ERR_UNSUPPORTED;
   const int64_t total = (a->T + CH - 1) / CH;
@@ -1108,9 +1110,49 @@ int scan_checkpoints(const kdn_scan_args* a, int64_t seg, int64_t n, float* ckpt
 
 using namespace kdn;
 
+// D = 128 / 256 (feature replication, kdn_frep.hip): the 512-wide request's workspace, then the replicated
+// tables and two 512-wide states (initial, final).
+static size_t frep_workspace(const kdn_scan_args* a, bool pipelined) {
+  if (a->cu_seqlens || a->state_slots) return 0;  // uniform batches only
+  const kdn_scan_args w = frep_wide(a, nullptr, nullptr);
+  const size_t base = pipelined ? scan_workspace_bytes_pipelined(&w) : kdn_scan_workspace_bytes(&w);
+  return base ? frep_layout(a, base, 2).total : 0;
+}
+
+// The D-wide scan as the 512-wide one: replicate the tables and the initial state into the workspace, run,
+// fold the 512-wide final state into final_state.  All on `stream` (the pipelined form joins its auxiliary
+// streams back into it).
+static int frep_scan(const kdn_scan_args* a, bool pipelined, void* stream, void* aux, void* out) {
+  int rc = validate_launch(a);
+  if (rc != KDN_OK) return rc;
+  const size_t need = frep_workspace(a, pipelined);
+  if (!need) return KDN_ERR_UNSUPPORTED;
+  if (a->workspace_bytes < need) return KDN_ERR_WORKSPACE_TOO_SMALL;
+  const kdn_scan_args w0 = frep_wide(a, nullptr, nullptr);
+  const size_t base = pipelined ? scan_workspace_bytes_pipelined(&w0) : kdn_scan_workspace_bytes(&w0);
+  const FrepLayout L = frep_layout(a, base, 2);
+  kdn_scan_args w = frep_wide(a, &L, a->workspace);
+  unsigned char* ws = static_cast<unsigned char*>(a->workspace);
+  float* s_in = reinterpret_cast<float*>(ws + L.state[0]);
+  float* s_out = reinterpret_cast<float*>(ws + L.state[1]);
+  int64_t cs[4];
+  frep_contiguous_strides(a, cs);
+  w.initial_state = a->initial_state ? s_in : nullptr;
+  w.final_state = s_out;
+  for (int i = 0; i < 4; ++i) w.init_stride[i] = w.final_stride[i] = cs[i];
+  const hipStream_t st = as_stream(stream);
+  rc = frep_tables(a, &L, a->workspace, st);
+  if (rc == KDN_OK && a->initial_state) rc = frep_state_lift(a, a->initial_state, a->init_stride, s_in, st);
+  if (rc != KDN_OK) return rc;
+  rc = pipelined ? scan_pipelined(&w, nullptr, nullptr, stream, aux, out) : kdn_delta_scan_fwd(&w, stream);
+  if (rc != KDN_OK) return rc;
+  return frep_state_fold(a, s_out, a->final_state, a->final_stride, st);
+}
+
 extern "C" size_t kdn_scan_workspace_bytes(const kdn_scan_args* a) {
   if (validate(a) != KDN_OK) return 0;
   if (general_scan_applies(a)) return general_scan_workspace_bytes(a);
+  if (frep_applies(a)) return frep_workspace(a, false);
   const int64_t seg = choose_segment(a);
   return chunk_bytes(a) * (size_t)a->B * (size_t)a->H * (size_t)(seg + 1);
 }
@@ -1119,6 +1161,7 @@ extern "C" int kdn_delta_scan_fwd(const kdn_scan_args* a, void* stream) {
   int rc = validate_launch(a);
   if (rc != KDN_OK) return rc;
   if (general_scan_applies(a)) return general_scan(a, stream);
+  if (frep_applies(a)) return frep_scan(a, false, stream, nullptr, nullptr);
   const int64_t seg = choose_segment(a);
   const size_t need = chunk_bytes(a) * (size_t)a->B * (size_t)a->H * (size_t)(seg + 1);
   if (a->workspace_bytes < need) return KDN_ERR_WORKSPACE_TOO_SMALL;
@@ -1141,6 +1184,10 @@ static int64_t pipeline_segment(const kdn_scan_args* a) {
 
 extern "C" int64_t kdn_scan_segment_chunks(const kdn_scan_args* a, int pipelined) {
   if (validate(a) != KDN_OK || general_scan_applies(a)) return 0;
+  if (frep_applies(a)) {
+    const kdn_scan_args w = frep_wide(a, nullptr, nullptr);
+    return pipelined ? pipeline_segment(&w) : choose_segment(&w);
+  }
   return pipelined ? pipeline_segment(a) : choose_segment(a);
 }
 
@@ -1156,6 +1203,7 @@ int scan_pipelined(const kdn_scan_args* a, const int64_t* seq_lo, const int64_t*
   int rc = validate_launch(a);
   if (rc != KDN_OK) return rc;
   if (general_scan_applies(a)) return seq_lo ? KDN_ERR_UNSUPPORTED : general_scan(a, stream);
+  if (frep_applies(a)) return seq_lo ? KDN_ERR_UNSUPPORTED : frep_scan(a, true, stream, aux_stream, out_stream);
   const int64_t seg = pipeline_segment(a);
   const size_t buf = chunk_bytes(a) * (size_t)a->B * (size_t)a->H * (size_t)(seg + 1);
   if (a->workspace_bytes < buf) return KDN_ERR_WORKSPACE_TOO_SMALL;
@@ -1177,6 +1225,7 @@ int scan_pipelined(const kdn_scan_args* a, const int64_t* seq_lo, const int64_t*
 size_t scan_workspace_bytes_pipelined(const kdn_scan_args* a) {
   if (validate(a) != KDN_OK) return 0;
   if (general_scan_applies(a)) return general_scan_workspace_bytes(a);
+  if (frep_applies(a)) return frep_workspace(a, true);
   const int64_t seg = pipeline_segment(a);
   const int64_t nsegs = ((a->T + CH - 1) / CH + seg - 1) / seg;
   const int64_t nbuf = nsegs < 3 ? nsegs : 3;
@@ -1216,7 +1265,7 @@ extern "C" int kdn_scan_schedule(const kdn_scan_args* a) {
   const int rc = validate(a);
   if (rc != KDN_OK) return rc;
   if (general_scan_applies(a)) return KDN_SCHEDULE_GENERAL;
-  return (a->in_dtype == KDN_DTYPE_BF16 && use_fused(a)) ? KDN_SCHEDULE_FUSED : KDN_SCHEDULE_SPLIT;
+  return (a->in_dtype == KDN_DTYPE_BF16 && use_fused(a)) ? KDN_SCHEDULE_FUSED : KDN_SCHEDULE_SPLIT;  // same at D < 512
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -1228,6 +1277,7 @@ extern "C" int kdn_delta_scan_fwd_noalloc(const kdn_scan_args* a, void* stream) 
   int rc = validate(a);
   if (rc != KDN_OK) return rc;
   if (general_scan_applies(a)) return KDN_ERR_UNSUPPORTED;  // its workspace spans the whole sequence
+  if (frep_applies(a)) return KDN_ERR_UNSUPPORTED;          // nor for the replicated narrower lifts
   // Segments of as many chunks as the scratch holds: one record per (head, chunk) plus a spare per head.
   const size_t per_chunk = chunk_bytes(a) * (size_t)a->B * (size_t)a->H;
   const int64_t fit = (int64_t)(KDN_NOALLOC_SCRATCH_BYTES / per_chunk) - 1;

@@ -15,7 +15,7 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 PKG_ROOT = os.path.dirname(_HERE)
 CSRC = os.path.join(PKG_ROOT, "csrc")
 SOURCES = ["kdn_api.hip", "kdn_lift.hip", "kdn_prep.hip", "kdn_scan.hip", "kdn_chain.hip", "kdn_serve.hip", "kdn_pool.hip",
-           "kdn_bwd.hip", "kdn_general.hip", "kdn_noalloc.hip"]
+           "kdn_bwd.hip", "kdn_general.hip", "kdn_noalloc.hip", "kdn_frep.hip"]
 OUT = os.path.join(_HERE, "libkdn.so")
 OBJDIR = os.path.join(_HERE, "_build")
 ARCH = "gfx950"

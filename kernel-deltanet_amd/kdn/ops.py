@@ -268,6 +268,8 @@ def scan_workspace_bytes(q, v, omega_bf16, segment_chunks: int = 0, pipelined: b
     D = features.dim(q) if features is not None else omega_bf16.shape[-2]
     a.B, a.T, a.H, a.d_k, a.D, a.d_v = B, T, H, d_k, D, v.shape[-1]
     a.feature_mode = 1 if (features is not None and features.lifted) else 0
+    if features is not None:
+        _fill_features(a, features)  # D < 512: the replicated tables' size follows the heads and low parts
     a.in_dtype = _tag(q.dtype, "scan inputs")
     a.out_dtype = a.in_dtype
     a.inv_tau = 1.0
@@ -534,11 +536,12 @@ def scan_autograd(q, k, v, beta, decay, omega_bf16, phase, inv_tau, normalize: b
                   initial_state: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor]:
     """`scan` (default schedule) recorded for autograd: gradients flow to q, k, v, beta, decay and
     initial_state through kdn_delta_scan_bwd.  Returns (y (B, T, H, d_v), final_state (B, H, D, d_v)).
-    The backward covers d_k = 64, D = 512, d_v in {16, 32, 64, 128}; other shapes are rejected here,
-    before the forward runs, rather than inside .backward()."""
+    The backward covers d_k = 64, D in {128, 256, 512}, d_v in {16, 32, 64, 128}; other shapes are rejected
+    here, before the forward runs, rather than inside .backward()."""
     d_k, D, d_v = q.shape[-1], omega_bf16.shape[-2], v.shape[-1]
-    if d_k != 64 or D != 512 or d_v not in (16, 32, 64, 128):
-        raise ValueError(f"scan with gradients: the backward supports d_k = 64, D = 512, d_v in 16, 32, 64, 128 "
+    if d_k != 64 or D not in (128, 256, 512) or d_v not in (16, 32, 64, 128):
+        raise ValueError(f"scan with gradients: the backward supports d_k = 64, D in 128, 256, 512, d_v in 16, 32, "
+                         f"64, 128 "
                          f"(got d_k = {d_k}, D = {D}, d_v = {d_v}); run the forward under torch.no_grad() or detach "
                          f"the inputs")
     return _Scan.apply(q, k, v, beta, decay, initial_state, omega_bf16, phase, inv_tau, normalize)
@@ -581,12 +584,13 @@ def feature_scan_autograd(q, k, v, beta, decay, omega, phase, inv_tau_head, omeg
                           normalize: bool = False, initial_state=None, rule: int = RULE_DELTA
                           ) -> Tuple[torch.Tensor, torch.Tensor]:
     """`scan` over (B, T, H, .) views with a per-head feature map, recorded for autograd (gradients through
-    kdn_delta_scan_bwd to q, k, v, beta, decay, initial_state and inv_tau_head (H,)).  omega (H, 512, 64)
-    bf16 with optional bf16 low parts, phase (H, 512), the delta or the linear rule; d_k = 64, D = 512,
-    d_v in {16, 32, 64, 128}.  Returns (y (B, T, H, d_v), final_state (B, H, D, d_v))."""
+    kdn_delta_scan_bwd to q, k, v, beta, decay, initial_state and inv_tau_head (H,)).  omega (H, D, 64)
+    bf16 with optional bf16 low parts, phase (H, D), the delta or the linear rule; d_k = 64, D in {128, 256,
+    512}, d_v in {16, 32, 64, 128}.  Returns (y (B, T, H, d_v), final_state (B, H, D, d_v))."""
     d_k, D, d_v = q.shape[-1], omega.shape[-2], v.shape[-1]
-    if d_k != 64 or D != 512 or d_v not in (16, 32, 64, 128):
-        raise ValueError(f"scan with gradients: the backward supports d_k = 64, D = 512, d_v in 16, 32, 64, 128 "
+    if d_k != 64 or D not in (128, 256, 512) or d_v not in (16, 32, 64, 128):
+        raise ValueError(f"scan with gradients: the backward supports d_k = 64, D in 128, 256, 512, d_v in 16, 32, "
+                         f"64, 128 "
                          f"(got d_k = {d_k}, D = {D}, d_v = {d_v}); run the forward under torch.no_grad() or detach "
                          f"the inputs")
     return _FeatureScan.apply(q, k, v, beta, decay, initial_state, inv_tau_head, omega, omega_lo, phase,

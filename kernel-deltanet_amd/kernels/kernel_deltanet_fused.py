@@ -136,7 +136,7 @@ class FusedKernelDeltaNetFunction(torch.autograd.Function):
 class FusedKernelDeltaNet(nn.Module):
     """Reference: kernels/kernel_deltanet_fused.py:181-303.  Parameters and buffers carry the reference's
     names and shapes (w_q, w_k, w_v, w_out, w_beta, w_decay, raw_tau, omega, b_rff), so state dicts load
-    either way.  The device path needs d_model / num_heads = 64 and rkhs_dim = 512."""
+    either way.  The device path needs d_model / num_heads = 64 and rkhs_dim 128, 256 or 512."""
 
     def __init__(self, d_model: int, num_heads: int, rkhs_dim: int = 512, chunk_size: int = 64,
                  tau_init: float = 1.0):

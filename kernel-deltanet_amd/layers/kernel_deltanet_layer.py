@@ -20,8 +20,8 @@ lambda = lambda_h reach the kernels as stride-0 (B, T, H) views, and the update 
 
 Differences from the reference, all outside the ranges the layer produces: F.normalize's eps is 1e-6
 here (1e-12 there), and lambda is clamped below at 1e-5 (lambda_h < 1e-5 needs logit_decay < -11.5).
-The device path needs d_model / num_heads = 64 and rkhs_dim = d_head * rkhs_factor = 512
-(rkhs_factor = 8); other sizes raise.
+The device path needs d_model / num_heads = 64 and rkhs_dim = d_head * rkhs_factor in {128, 256, 512}
+(rkhs_factor 2, 4 (the default) or 8); other sizes raise.
 """
 from __future__ import annotations
 
@@ -135,9 +135,9 @@ class KernelDeltaNetLayer(nn.Module):
         (out, new state (B, H, d_head, rkhs_dim)) -- reference :76-143."""
         B, T, d_in = x.shape
         H, dh, D = self.num_heads, self.d_head, self.rkhs_dim
-        if dh != 64 or D != 512:
-            raise ValueError(f"KernelDeltaNetLayer on MI355X needs d_head = 64 and rkhs_dim = 512 "
-                             f"(rkhs_factor = 8); got d_head = {dh}, rkhs_dim = {D}")
+        if dh != 64 or D not in (128, 256, 512):
+            raise ValueError(f"KernelDeltaNetLayer on MI355X needs d_head = 64 and rkhs_dim 128, 256 or 512 "
+                             f"(rkhs_factor 2, 4 or 8); got d_head = {dh}, rkhs_dim = {D}")
         step_mode = state is not None or T == 1
         q = self.w_q(x).view(B, T, H, dh)
         k = self.w_k(x).view(B, T, H, dh)

@@ -62,7 +62,7 @@ def test_args_layout_matches_c(cname, pystruct):
 def test_strerror_and_version(lib):
     for code in (0, -1, -2, -3, -4, -5, -99):
         assert len(lib.kdn_strerror(code)) > 0
-    assert lib.kdn_abi_version() == (2 << 16) | 0
+    assert lib.kdn_abi_version() == (2 << 16) | 1
 
 
 def _args(**kw):
@@ -84,6 +84,18 @@ def test_workspace_bytes(lib):
     assert lib.kdn_scan_workspace_bytes(ctypes.byref(_args(d_v=48))) == 0
     a = _args(segment_chunks=100000)  # clamped to the number of chunks
     assert lib.kdn_scan_workspace_bytes(ctypes.byref(a)) == 16 * 1025 * 238592
+    # D = 256 runs the 512-wide scan on replicated tables: its workspace (4 + 1 records of 2 heads), then
+    # the replicated Omega (512 x 64 bf16) and phases (512 fp32) and two 512-wide fp32 states; per-head
+    # Omega with low parts: 2 x 2 tables
+    a = _args(T=256, H=2, D=256)
+    assert lib.kdn_scan_workspace_bytes(ctypes.byref(a)) == 5 * 2 * 238592 + 65536 + 2048 + 2 * 2 * 512 * 64 * 4
+    assert lib.kdn_scan_segment_chunks(ctypes.byref(a), 0) == 4
+    a.omega_lo, a.omega_head_stride, a.phase_head_stride = 0x7D0000000000, 256 * 64, 256
+    assert lib.kdn_scan_workspace_bytes(ctypes.byref(a)) == \
+        5 * 2 * 238592 + 2 * 2 * 65536 + 2 * 2048 + 2 * 2 * 512 * 64 * 4
+    assert lib.kdn_scan_workspace_bytes(ctypes.byref(_args(T=256, H=2, D=128))) == \
+        5 * 2 * 238592 + 65536 + 2048 + 2 * 2 * 512 * 64 * 4
+    assert lib.kdn_scan_workspace_bytes(ctypes.byref(_args(T=256, H=2, D=384))) == 0
 
 
 def _fake_ptrs(a, base=0x7F0000000000):
@@ -99,7 +111,14 @@ def test_scan_argument_errors_need_no_device(lib):
     run = lambda a: lib.kdn_delta_scan_fwd(ctypes.byref(a), None)
     assert lib.kdn_delta_scan_fwd(None, None) == -1
     assert run(_fake_ptrs(_args(d_k=32))) == -2
-    assert run(_fake_ptrs(_args(D=256))) == -2
+    assert run(_fake_ptrs(_args(D=384))) == -2
+    assert run(_fake_ptrs(_args(D=256))) == -3                            # supported; workspace too small
+    a = _fake_ptrs(_args(D=256))
+    a.workspace_bytes = 1 << 40
+    assert lib.kdn_scan_prep(ctypes.byref(a), 0, 1, None) == -2           # no phase entry points below 512
+    assert lib.kdn_delta_scan_fwd_noalloc(ctypes.byref(a), None) == -2
+    a.state_slots = 0x7A0000000000                                       # uniform batches only
+    assert run(a) == -2
     assert run(_fake_ptrs(_args(T=0))) == -1
     assert run(_fake_ptrs(_args(in_dtype=7))) == -1
     a = _fake_ptrs(_args())
@@ -235,6 +254,14 @@ def test_backward_workspace_and_errors_need_no_device(lib):
     # the workspace before they are added into the outputs
     f2.d_v = 128
     assert lib.kdn_scan_bwd_workspace_bytes(ctypes.byref(g)) == 2 * 4 * 1099776 + 65536 + 2 * 512 * 64 * 4 + 2048
+    # D = 256: the 512-wide backward's workspace, the replicated tables, three 512-wide fp32 states
+    f2.d_v, f2.D = 64, 256
+    assert lib.kdn_scan_bwd_workspace_bytes(ctypes.byref(g)) == \
+        2 * 4 * 1099776 + 65536 + 65536 + 2048 + 3 * 2 * 512 * 64 * 4
+    assert lib.kdn_scan_bwd_segments(ctypes.byref(g), ctypes.byref(seg)) == 1 and seg.value == 4
+    assert lib.kdn_scan_bwd_phase(ctypes.byref(g), 1, 0, None) == -2
+    assert lib.kdn_delta_scan_bwd(ctypes.byref(g), None) == -3
+    f2.D = 512
     g.fwd = ctypes.addressof(f)
     # per-head Omega with low parts (the P2 / P4 feature maps, ABI 1.7): one Omega^T table per head and
     # part; dL/d(1/tau) adds one fp32 partial per (batch, head, chunk), rounded up to 256 bytes

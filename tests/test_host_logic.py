@@ -115,7 +115,7 @@ def test_surface_argument_checks_on_host():
         tiled_triton_chunk_scan(x, x, torch.zeros(1, 2, 100, 64), torch.zeros(1, 2, 100), torch.zeros(1, 2, 100),
                                 block_d=48)
     layer = KernelDeltaNetLayer(64, 4)  # reference default rkhs_factor = 4: d_head 16, rkhs_dim 64
-    with pytest.raises(ValueError, match="d_head = 64 and rkhs_dim = 512"):
+    with pytest.raises(ValueError, match="d_head = 64 and rkhs_dim 128, 256 or 512"):
         layer(torch.zeros(1, 8, 64))
     sd = KernelDeltaNetLayer(128, 2, rkhs_factor=8).state_dict()
     assert set(sd) == {"w_q.weight", "w_k.weight", "w_v.weight", "w_out.weight", "kernel.log_gamma",
