@@ -566,26 +566,37 @@ __global__ void __launch_bounds__(320) state_kernel_dma(ScanParams p) {
 }
 
 // ------------------------------------------------------------------------------------------------
-// output: grid (nseg, H, B), 256 threads.  Y = diag(qscale) Q S_c^T + P E for one (chunk, head).
+// output: 256 threads per workgroup, workgroup i taking (chunk, head, sequence) items i, i + grid, ...
+// (one item each with a grid of nseg * H * B).  Y = diag(qscale) Q S_c^T + P E for one (chunk, head).
 // Wave w keeps the lifted query fragments of token tile w (read back from the record) in registers.
 // The chunk-start S^T fragments are staged in LDS, NG value tiles per pass, and read by all four waves.  Each wave assembles its 16 x d_v block of Y in a wave-private LDS tile and writes
 // whole rows with 16-byte stores.  Every operand is read once: streaming loads.
+template <class P, int D, int DV>
+struct OutputLds {
+  static constexpr int NJ = D / 32, NV = DV / 16;
+  static constexpr int NG0 = IsBF16<P>::value ? 2 : 1;  // value tiles per LDS pass (32 KB of S fragments)
+  static constexpr int NG = NV < NG0 ? NV : NG0;
+  static constexpr int YS = DV + 4;                     // padded row of the Y tile
+  static constexpr size_t bytes = (size_t)NJ * NG * 64 * P::frag_bytes + (size_t)4 * 16 * YS * 4;
+};
+
 template <class P, typename OutT, int D, int DV>
 __global__ void __launch_bounds__(256) output_kernel(ScanParams p) {
   using L = WsLayout<P, D, DV>;
   using frag = typename P::frag;
-  constexpr int NJ = D / 32, NV = DV / 16;
-  constexpr int NG0 = IsBF16<P>::value ? 2 : 1;  // value tiles per LDS pass (32 KB of S fragments)
-  constexpr int NG = NV < NG0 ? NV : NG0;
-  constexpr int YS = DV + 4;                     // padded row of the Y tile
+  using O = OutputLds<P, D, DV>;
+  constexpr int NJ = O::NJ, NV = O::NV, NG = O::NG, YS = O::YS;
   __shared__ frag s_s[NJ * NG * 64];
   __shared__ __attribute__((aligned(16))) float s_y[4][16 * YS];
 
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int64_t cl = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int64_t items = p.nseg * p.H * p.B;
+  for (int64_t it = blockIdx.x; it < items; it += gridDim.x) {
+  if (it != (int64_t)blockIdx.x) __syncthreads();  // the previous item's LDS tiles have been read
+  const int64_t cl = it % p.nseg, h = (it / p.nseg) % p.H, b = it / (p.nseg * p.H);
   const Seq sq = seq_of(p, b);
-  if (cl >= seg_chunks(p, sq)) return;  // past the end of this sequence (ragged batches)
+  if (cl >= seg_chunks(p, sq)) continue;  // past the end of this sequence (ragged batches)
   const int64_t t0 = (p.chunk0 + cl) * CH;
   const unsigned char* ws = p.ws + ((b * p.H + h) * (p.nseg + 1) + cl) * L::bytes;
   const float* vec = reinterpret_cast<const float*>(ws + L::VEC);
@@ -640,6 +651,7 @@ __global__ void __launch_bounds__(256) output_kernel(ScanParams p) {
         store_row8<OutT>((OutT*)p.y + sq.y + t * p.ys1 + h * p.ys2 + 8 * pc, v);
       }
     }
+  }
   }
 }
 
@@ -696,6 +708,8 @@ static ScanParams fill_params(const kdn_scan_args* a) {
   p.slots = a->state_slots;
   p.prep_no_q = 0;
   p.k_plain = 0;
+  p.prep_run = 0;
+  p.out_wgs = 0;
   return p;
 }
 
@@ -744,6 +758,7 @@ static ScanParams segment_params(const kdn_scan_args* a, const RunSpec& r, int64
   p.nseg = nseg;
   p.ws = (unsigned char*)ws;
   p.prep_run = choose_prep_run(nseg, a->B * a->H, prep_cus);
+  p.out_wgs = 0;
   if (c0 == 0) {
     p.state_in = a->initial_state;
     p.is0 = a->init_stride[0]; p.is1 = a->init_stride[1]; p.is2 = a->init_stride[2]; p.is3 = a->init_stride[3];
@@ -761,7 +776,6 @@ constexpr int STATE_EXCLUSIVE_LDS = 40 * 1024;
 
 template <class P, typename InT, typename OutT, int D, int DV>
 static int launch_phase(const ScanParams& p, int phase, hipStream_t st) {
-  const dim3 chunk_grid((unsigned)p.nseg, (unsigned)p.H, (unsigned)p.B);
   if (phase == PHASE_PREP) {
     return launch_prep<P, InT, D, DV>(p, st);
   } else if (phase == PHASE_CHAIN) {
@@ -780,7 +794,19 @@ static int launch_phase(const ScanParams& p, int phase, hipStream_t st) {
       else hipLaunchKernelGGL((state_kernel<P, D, DV, false>), dim3(state_grid(p.B, p.H, DV / 16)), dim3(256), excl, st, p);
     }
   } else {
-    hipLaunchKernelGGL((output_kernel<P, OutT, D, DV>), chunk_grid, dim3(256), 0, st, p);
+    // Beside the state kernel (p.out_wgs > 0): at most one workgroup per CU it leaves free, each CU held
+    // alone (LDS padded past half a CU), all resident from the start.  The state kernel of the next
+    // segment becomes ready together with this one, and needs whole CUs: a grid of one workgroup per
+    // (chunk, head) took every free CU and held up a quarter of its workgroups by ~55 us per segment
+    // (config 3: 2.59 against 2.41 ms per layer, measured with clock stamps).
+    const int64_t items = (int64_t)p.nseg * p.H * p.B;
+    if (p.out_wgs > 0 && p.out_wgs < items) {
+      constexpr size_t excl = CU_LDS_BYTES / 2 + 1024;
+      const size_t pad = OutputLds<P, D, DV>::bytes < excl ? excl - OutputLds<P, D, DV>::bytes : 0;
+      hipLaunchKernelGGL((output_kernel<P, OutT, D, DV>), dim3((unsigned)p.out_wgs), dim3(256), pad, st, p);
+    } else {
+      hipLaunchKernelGGL((output_kernel<P, OutT, D, DV>), dim3((unsigned)items), dim3(256), 0, st, p);
+    }
   }
   return hipGetLastError() == hipSuccess ? KDN_OK : KDN_ERR_DEVICE;
 }
@@ -832,12 +858,14 @@ static int run_pipelined(const kdn_scan_args* a, const RunSpec& r) {
   hipEvent_t* evS = evs.ev + nbuf;
   hipEvent_t* evO = evs.ev + 2 * nbuf;
   hipEvent_t evIn = evs.ev[3 * nbuf], evOut = evs.ev[3 * nbuf + 1];
-  // prep shares the device with the state kernel's workgroups (one per CU)
+  // prep and output share the device with the state kernel's workgroups (one per CU)
   const int prep_cus = device_cus() - (int)state_grid(a->B, a->H, DV / 16);
   auto seg_p = [&](int64_t s) {
     const int64_t c0 = s * seg;
-    return segment_params(a, r, c0, (nchunks - c0 < seg) ? (nchunks - c0) : seg,
-                          (unsigned char*)a->workspace + (size_t)(s % nbuf) * buf_bytes, prep_cus);
+    ScanParams p = segment_params(a, r, c0, (nchunks - c0 < seg) ? (nchunks - c0) : seg,
+                                  (unsigned char*)a->workspace + (size_t)(s % nbuf) * buf_bytes, prep_cus);
+    p.out_wgs = prep_cus > 0 ? prep_cus : 0;
+    return p;
   };
 #define KDN_TRY(x) do { if ((x) != hipSuccess) return KDN_ERR_DEVICE; } while (0)
 #define KDN_TRYK(x) do { const int _rc = (x); if (_rc != KDN_OK) return _rc; } while (0)

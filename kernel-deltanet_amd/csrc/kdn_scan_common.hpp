@@ -89,6 +89,7 @@ struct ScanParams {
   unsigned char* ws;
   int64_t chunk0, nseg;  // first global chunk of the segment, chunks in the segment
   int prep_run;          // chunks per prep workgroup (bf16)
+  int64_t out_wgs;       // output workgroups beside the state kernel (0: one per chunk and head)
   // feature map: per-head Omega (hi [+ lo]) / phases / 1/tau, renormalisation, pre-lifted inputs
   const __bf16* omega_lo; int64_t oms, phs;
   const float* inv_tau_head;
