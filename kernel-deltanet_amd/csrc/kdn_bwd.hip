@@ -1293,13 +1293,17 @@ __device__ __forceinline__ void dx_pass(const Params& p, const float* rec, const
 // dQ^T = S^T (a o dY)^T + K^T N^T over each wave's 512 / DX_WAVES features, then the lift backward of k
 // and q to dk, dq, each in two halves of 32 tokens.  The small B operands come from the gradient kernel
 // through the record; LDS holds only the input rows and dx^ (36 KB).  Eight waves (64 features each)
-// halve each wave's accumulators and loops, so that two waves share each SIMD.
+// halve each wave's accumulators and loops, so that two waves share each SIMD.  With Omega's low parts the
+// lift backward reads twice the Omega fragments, which two waves per SIMD (256 registers each) cannot
+// hold without spilling: that variant runs four waves of 128 features.
 constexpr int DX_WAVES = 8;
-template <class P, typename InT, bool LO, bool GEN>
-__global__ void __launch_bounds__(64 * DX_WAVES) bwd_dx_kernel(Params p) {
+template <bool LO>
+struct DxWaves : std::integral_constant<int, LO ? 4 : DX_WAVES> {};
+template <class P, typename InT, bool LO, bool GEN, int NW = DxWaves<LO>::value>
+__global__ void __launch_bounds__(64 * NW) bwd_dx_kernel(Params p) {
   __shared__ __attribute__((aligned(16))) float bT[C * LD];   // normalised k / q rows
   __shared__ __attribute__((aligned(16))) float bDX[C * LD];  // dx^ of k / q
-  __shared__ float s_n[C], s_rdp[DX_WAVES][C], s_dit[DX_WAVES];
+  __shared__ float s_n[C], s_rdp[NW][C], s_dit[NW];
 
   const int64_t h = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x, lane = tid & 63;
@@ -1311,8 +1315,8 @@ __global__ void __launch_bounds__(64 * DX_WAVES) bwd_dx_kernel(Params p) {
   const typename P::frag* bop = reinterpret_cast<const typename P::frag*>(rec + Rec::KXF);
 
   float dit = 0.f;  // this lane's share of dL/d(1/tau) over k, then q
-  dx_pass<P, InT, 1, DX_WAVES, LO, GEN>(p, rec, bop, bT, bDX, s_n, s_rdp, b, h, t0, tid, w, lane, r, c0, rvalid, dit);
-  dx_pass<P, InT, 0, DX_WAVES, LO, GEN>(p, rec, bop, bT, bDX, s_n, s_rdp, b, h, t0, tid, w, lane, r, c0, rvalid, dit);
+  dx_pass<P, InT, 1, NW, LO, GEN>(p, rec, bop, bT, bDX, s_n, s_rdp, b, h, t0, tid, w, lane, r, c0, rvalid, dit);
+  dx_pass<P, InT, 0, NW, LO, GEN>(p, rec, bop, bT, bDX, s_n, s_rdp, b, h, t0, tid, w, lane, r, c0, rvalid, dit);
   if (GEN && p.dit) {  // fixed order: lanes by a shuffle tree, then the waves in order
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) dit += __shfl_xor(dit, o);
@@ -1321,7 +1325,7 @@ __global__ void __launch_bounds__(64 * DX_WAVES) bwd_dx_kernel(Params p) {
     if (tid == 0) {
       float t = s_dit[0];
 #pragma unroll
-      for (int v = 1; v < DX_WAVES; ++v) t += s_dit[v];
+      for (int v = 1; v < NW; ++v) t += s_dit[v];
       p.dit[(b * p.H + h) * p.nch + p.c0 + blockIdx.x] = t;
     }
   }
@@ -1525,7 +1529,7 @@ static int segment_phase(const Params& p, int phase, hipStream_t st) {
   if (phase == 4) {
     hipLaunchKernelGGL((bwd_grad_kernel<P, InT>), chunk_grid, dim3(64 * GRAD_WAVES), 0, st, p);
     const bool gen = p.omega_lo || p.oms || p.phs || p.inv_tau_head || p.no_renorm || p.dit;
-    if (p.omega_lo) hipLaunchKernelGGL((bwd_dx_kernel<P, InT, true, true>), chunk_grid, dim3(64 * DX_WAVES), 0, st, p);
+    if (p.omega_lo) hipLaunchKernelGGL((bwd_dx_kernel<P, InT, true, true>), chunk_grid, dim3(64 * DxWaves<true>::value), 0, st, p);
     else if (gen) hipLaunchKernelGGL((bwd_dx_kernel<P, InT, false, true>), chunk_grid, dim3(64 * DX_WAVES), 0, st, p);
     else hipLaunchKernelGGL((bwd_dx_kernel<P, InT, false, false>), chunk_grid, dim3(64 * DX_WAVES), 0, st, p);
     // segment 0 is the last one processed: every partial of dL/d(1/tau) is written
