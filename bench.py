@@ -643,6 +643,16 @@ def bench_factored_backward(args, dev):
     print(json.dumps(out), flush=True)
 
 
+def _slot_args_probe(T, H, dv, n_slots):
+    """kdn_slot_step_args with the shape fields the workspace size reads (bf16, D = 512)."""
+    from kdn import _native as N
+    a = N.SlotStepArgs()
+    a.num_tokens, a.H, a.d_k, a.D, a.d_v = T, H, 64, 512, dv
+    a.in_dtype = a.out_dtype = N.KDN_DTYPE_BF16
+    a.inv_tau, a.slot_bytes, a.num_slots = 1.0, 8, n_slots
+    return a
+
+
 def bench_serving(args, dev):
     """Config 5: one ragged mixed step over 256 sequences, 224 single-token decodes (rank-1 update of a
     resident [16, 512, 64] fp32 state in a slab pool) and 32 prefills with lengths uniform in
@@ -690,6 +700,23 @@ def bench_serving(args, dev):
         return e0.elapsed_time(e1) / steps
 
     ms = timed(cu, slots, q, k, v, beta, y, args.steps)
+    # the same step described by the token -> slot map alone (kdn_slot_step: no host offsets, launches sized
+    # from the token and slot counts), workspace allocated once
+    import ctypes
+    from kdn import _native as N
+    slot_map = torch.repeat_interleave(slots.to(torch.int64), lens).to(dev)
+    ws_slot = torch.empty(int(N.lib().kdn_slot_step_workspace_bytes(ctypes.byref(_slot_args_probe(
+        T, H, dv, states.shape[0])))), dtype=torch.uint8, device=dev)
+    for _ in range(args.warmup):
+        ops.slot_step(q, k, v, beta, None, slot_map, states, om, ph, proj.tau_star_inv, y=y, workspace=ws_slot)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(args.steps):
+        ops.slot_step(q, k, v, beta, None, slot_map, states, om, ph, proj.tau_star_inv, y=y, workspace=ws_slot)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms_slot = e0.elapsed_time(e1) / args.steps
     # the two parts alone: the decode tokens (rows 0..223) and the prefill tokens (rows 224..)
     ms_dec = timed(cu[: n_dec + 1], slots[:n_dec], q, k, v, beta, y, args.steps)
     cu_pre = cu[n_dec:] - n_dec
@@ -716,7 +743,9 @@ def bench_serving(args, dev):
         "parts": {"decode": {"ms": ms_dec, "sequences": n_dec, "alg_bytes": dec_bytes, "GBps": dec_gbs,
                              "hbm_frac": dec_gbs * 1e9 / HBM_PEAK},
                   "prefill": {"ms": ms_pre, "sequences": n_pre, "tokens": pre_tokens, "alg_flops": pre_flops,
-                              "tflops": pre_tflops, "mfma_frac": pre_tflops * 1e12 / MFMA_BF16_PEAK}},
+                              "tflops": pre_tflops, "mfma_frac": pre_tflops * 1e12 / MFMA_BF16_PEAK},
+                  "slot_map_step": {"ms": ms_slot, "note": "the whole step from slot_mapping alone (kdn_slot_step, "
+                                                           "no host offsets)"}},
         "cpu_baseline": None,
     }
     print(json.dumps(out), flush=True)

@@ -32,12 +32,14 @@
  *   kdn_scan_output     <- the chunk readout, kernels/fused_kernel_deltanet.py:118-141
  *   kdn_scan_prep_fused, kdn_scan_chain <- the same chunk loop as prep + one sequential kernel that carries
  *                          the state and reads out y (kernels/fused_kernel_deltanet.py:95-149)
+ *   kdn_slot_step       <- vllm_hybrid_recurrent_forward(query, ..., recurrent_states, slot_mapping, output),
+ *                          serving/vllm_kernel_deltanet_op.cpp:11-34 (declared there with an empty body)
  *
  * ABI 2.0 (breaking): kdn_scan_bwd_args and kdn_ragged_args gained trailing fields that the library reads
  * on every call (dinv_tau, num_slots) and kdn_scan_bwd_phase gained its `segment` argument in 1.6-1.8;
  * callers built against a header older than 1.8 must be recompiled.  2.0 adds kdn_scan_schedule,
  * kdn_scan_prep_fused and kdn_scan_chain.  2.1 accepts D = 128 and 256 (scan and backward) and d_v 16,
- * 32 and 128 in the D = 512 backward.
+ * 32 and 128 in the D = 512 backward.  2.2 adds kdn_slot_step (the serving step from a slot map).
  */
 #ifndef KDN_H
 #define KDN_H
@@ -419,6 +421,40 @@ size_t kdn_ragged_workspace_bytes(const kdn_ragged_args* a);
 
 /* Runs the step on `stream`; the prefill part uses the pipelined scan when aux_stream is not NULL. */
 int kdn_ragged_step(const kdn_ragged_args* a, void* stream, void* aux_stream);
+
+/* The same step described by a token -> slot map alone, with nothing read back to the host (ABI 2.2):
+ * the reference op's own arguments, vllm_hybrid_recurrent_forward(query, key, value, beta, decay,
+ * recurrent_states, slot_mapping, output), serving/vllm_kernel_deltanet_op.cpp:11-34.  A sequence is a
+ * run of consecutive tokens with one slot; a negative slot, or one at or above num_slots, marks padding
+ * (skipped: no state touched, no y row written).  The runs, the decode / prefill split and the prefill's
+ * packed layout are all formed on the device and every launch is sized from num_tokens and num_slots, so
+ * distinct runs must have distinct slots (not checked); a map with more than 2 * num_slots + 1 runs is
+ * invalid, and then nothing runs and *status (device int32, if not NULL) is set to 1 (else 0).  The
+ * prefill runs the split scan over windows of 128 packed chunk slots (each sequence's chunks plus one spare
+ * slot), pipelined over aux_stream when it is not NULL. */
+typedef struct kdn_slot_step_args {
+  int64_t num_tokens, H;
+  int d_k, D, d_v;             /* d_k = 64, D = 512, d_v in {16, 32, 64, 128} */
+  int in_dtype, out_dtype, normalize_input, rule;
+  float inv_tau;
+  const void* slot_mapping;    /* device [num_tokens] */
+  int slot_bytes;              /* 4 (int32) or 8 (int64) bytes per slot_mapping entry */
+  const void* q;   int64_t q_stride[2];   /* [token][head] element strides; innermost contiguous */
+  const void* k;   int64_t k_stride[2];
+  const void* v;   int64_t v_stride[2];
+  const float* beta;  int64_t beta_stride[2];
+  const float* decay; int64_t decay_stride[2];   /* NULL means lambda = 1 */
+  const void* omega_bf16; const float* phase;
+  float* states;   int64_t state_stride[4];       /* [slot][head][feature][value] */
+  int64_t num_slots;
+  void* y;         int64_t y_stride[2];
+  void* workspace; size_t workspace_bytes;
+  int32_t* status;
+} kdn_slot_step_args;
+
+/* Workspace bytes kdn_slot_step needs (0 if the arguments are invalid); reads the shape fields only. */
+size_t kdn_slot_step_workspace_bytes(const kdn_slot_step_args* a);
+int kdn_slot_step(const kdn_slot_step_args* a, void* stream, void* aux_stream);
 
 /* ---- Slab state pool --------------------------------------------------------------------------
  * Slot bookkeeping over a caller-allocated slab of `max_slots` equal fp32 state slots of slot_bytes

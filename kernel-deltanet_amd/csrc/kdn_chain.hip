@@ -94,19 +94,17 @@ __global__ void __launch_bounds__(256) chain_kernel(ScanParams p) {
   const int vh = (int)(jdx % NWG);
   const int64_t hb = (jdx / NWG) * 8 + xcd;
   if (hb >= p.B * p.H) return;
-  const int64_t b = hb / p.H, h = hb % p.H;
+  int64_t b, h, nloc, cfirst;
+  size_t woff;
+  if (!state_item<L::bytes>(p, hb, b, h, nloc, woff, cfirst)) return;
   const Seq sq = seq_of(p, b);
-  const int64_t nloc = seg_chunks(p, sq);
-  // A sequence that ended in an earlier segment has its final state already; one without tokens gets its
-  // initial state copied through (no chunk is run).
-  if (nloc == 0 && !(sq.len <= 0 && p.chunk0 == 0)) return;
   const int64_t sl = p.slots ? (int64_t)p.slots[b] : b;
   if (sl < 0) return;  // a skipped sequence of a ragged step
 
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int col0 = 16 * NVW * vh;
-  const unsigned char* wsh = p.ws + hb * (p.nseg + 1) * L::bytes;
+  const unsigned char* wsh = p.ws + woff;
 
   f32x4 S[8][NVW];
   if (p.state_in) {
@@ -190,7 +188,7 @@ __global__ void __launch_bounds__(256) chain_kernel(ScanParams p) {
       touch_off[k] = li < C::LINES_K ? (size_t)li * 128 : L::phiQ + (size_t)(li - C::LINES_K) * 128;
     }
     float* yt = s_y[w];
-    const int64_t t0_seq = p.chunk0 * CH;
+    const int64_t t0_seq = cfirst * CH;
 
     for (int64_t c = 0; c < nloc; ++c) {
       // the next chunk's record (the last chunk reloads its own, so that the loads stay unconditional)

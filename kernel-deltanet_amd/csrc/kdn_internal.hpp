@@ -37,6 +37,23 @@ int scan_pipelined(const kdn_scan_args* a, const int64_t* seq_lo, const int64_t*
                    void* aux_stream, void* out_stream);
 size_t scan_workspace_bytes_pipelined(const kdn_scan_args* a);
 
+// Packed windows of a ragged prefill whose layout is planned on the device (the serving step from a slot
+// map, kdn_serve.hip): `off` (nseq + 1 slot offsets), `first` (per window) and `total` as ScanParams
+// describes them; windows of `win` slots, `nwin` of them (a bound: windows past *total do nothing).
+struct FlatPlan {
+  const int64_t* off;
+  const int64_t* first;
+  const int64_t* total;
+  int64_t nseq, win, nwin;
+};
+// The split schedule over packed windows: a->B bounds the sequences that meet one window and a->T the
+// longest; sequence b is token rows seq_lo[b] .. seq_hi[b]-1 with state slot a->state_slots[b], read and
+// written in place (a->initial_state is a->final_state).  The workspace holds one to three window buffers
+// of scan_flat_buffer_bytes each (pipelined over aux_stream when two or more fit).
+int scan_flat(const kdn_scan_args* a, const int64_t* seq_lo, const int64_t* seq_hi, const FlatPlan& fp, void* stream,
+              void* aux_stream);
+size_t scan_flat_buffer_bytes(const kdn_scan_args* a, int64_t win);
+
 // Segment checkpoints of the D = 512, d_v = 64 scan (the backward's first pass): the states at the starts
 // of segments 1 .. n of `seg` chunks each, written as fp32 [B][H][512][64] arrays one after another from
 // `ckpt` (segment s's at ckpt + (s - 1) * B*H*512*64), by the scan's prep and state kernels alone (no

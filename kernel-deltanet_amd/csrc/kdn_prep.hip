@@ -104,13 +104,28 @@ __global__ void __launch_bounds__(256, (PrepWaves<P, FM>::value)) prep_kernel(Sc
 
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int64_t h = blockIdx.y, b = blockIdx.z;
   constexpr int RUN = PrepRun<P, FM>::value;  // 0: runtime run length with prefetch
   const int run = RUN ? RUN : p.prep_run;
-  const int64_t cl0 = (int64_t)blockIdx.x * run;
+  // chunks [cl0, cl_end) of sequence b (chunk indices of the segment, chunk0 + cl in the sequence) with
+  // their records from rec0; a packed window gives each workgroup the one chunk of its slot
+  const int64_t h = blockIdx.y;
+  int64_t b, cl0, nloc;
+  unsigned char* rec0;
+  if (p.fl_off) {
+    const FlatChunk fc = flat_chunk(p, blockIdx.x);
+    if (!fc.ok) return;  // a spare slot, or past the last
+    b = fc.b;
+    cl0 = fc.c;
+    nloc = fc.c + 1;
+    rec0 = p.ws + (h * (p.nseg + 1) + blockIdx.x) * L::bytes;
+  } else {
+    b = blockIdx.z;
+    cl0 = (int64_t)blockIdx.x * run;
+    nloc = seg_chunks(p, seq_of(p, b));
+    if (cl0 >= nloc) return;  // past the end of this sequence (ragged batches): nothing to prepare
+    rec0 = p.ws + ((b * p.H + h) * (p.nseg + 1) + cl0) * L::bytes;
+  }
   const Seq sq = seq_of(p, b);
-  const int64_t nloc = seg_chunks(p, sq);
-  if (cl0 >= nloc) return;  // past the end of this sequence (ragged batches): nothing to prepare
   const int64_t cl_end = (cl0 + run < nloc) ? cl0 + run : nloc;
 
   const __bf16* omega_h = p.omega + h * p.oms;
@@ -138,7 +153,7 @@ __global__ void __launch_bounds__(256, (PrepWaves<P, FM>::value)) prep_kernel(Sc
 
   auto process = [&](int64_t cl) {
     const int64_t t0 = (p.chunk0 + cl) * CH;
-    unsigned char* ws = p.ws + ((b * p.H + h) * (p.nseg + 1) + cl) * L::bytes;
+    unsigned char* ws = rec0 + (cl - cl0) * L::bytes;
     u32x4 vraw[In::VPT];
     In::load_v(p, sq, h, t0, vraw);  // early: first needed after the Gram, its latency hides behind the lift
     lds_barrier();  // Omega staged (first chunk); the previous chunk's LDS reads are done
@@ -331,7 +346,8 @@ int launch_prep(const ScanParams& p, hipStream_t st) {
   const int run_t = fm == FM_PRELIFTED ? PrepRun<P, FM_PRELIFTED>::value
                   : fm == FM_HILO ? PrepRun<P, FM_HILO>::value : PrepRun<P, FM_EXACT>::value;
   const int run = run_t ? run_t : p.prep_run;
-  const dim3 prep_grid((unsigned)((p.nseg + run - 1) / run), (unsigned)p.H, (unsigned)p.B);
+  const dim3 prep_grid = p.fl_off ? dim3((unsigned)p.nseg, (unsigned)p.H, 1u)
+                                  : dim3((unsigned)((p.nseg + run - 1) / run), (unsigned)p.H, (unsigned)p.B);
   if (fm == FM_PRELIFTED) hipLaunchKernelGGL((prep_kernel<P, InT, D, DV, FM_PRELIFTED>), prep_grid, dim3(256), 0, st, p);
   else if (fm == FM_HILO) hipLaunchKernelGGL((prep_kernel<P, InT, D, DV, FM_HILO>), prep_grid, dim3(256), 0, st, p);
   else if (p.prep_no_q) hipLaunchKernelGGL((prep_kernel<P, InT, D, DV, FM_EXACT, true>), prep_grid, dim3(256), 0, st, p);

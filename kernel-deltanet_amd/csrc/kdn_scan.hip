@@ -311,12 +311,9 @@ __global__ void __launch_bounds__(256) state_kernel(ScanParams p) {
   const int n = (int)(jdx % NV);
   const int64_t hb = (jdx / NV) * 8 + xcd;
   if (hb >= p.B * p.H) return;
-  const int64_t b = hb / p.H, h = hb % p.H;
-  const Seq sq = seq_of(p, b);
-  const int64_t nloc = seg_chunks(p, sq);
-  // A sequence that ended in an earlier segment has its final state already; one without tokens gets
-  // its initial state copied through (below, no chunk is run).
-  if (nloc == 0 && !(sq.len <= 0 && p.chunk0 == 0)) return;
+  int64_t b, h, nloc, cfirst;
+  size_t woff;
+  if (!state_item<L::bytes>(p, hb, b, h, nloc, woff, cfirst)) return;
   const int64_t sl = p.slots ? (int64_t)p.slots[b] : b;
   if (sl < 0) return;  // a skipped sequence of a ragged step (its state is not touched)
 
@@ -339,7 +336,7 @@ __global__ void __launch_bounds__(256) state_kernel(ScanParams p) {
     for (int tl = 0; tl < TPW; ++tl) S[tl] = zero4();
   }
 
-  unsigned char* wsh = p.ws + hb * (p.nseg + 1) * L::bytes;
+  unsigned char* wsh = p.ws + woff;
   frag k0[4][JPW], k1[4][JPW];
   typename O::Small s0, s1;
   unsigned l2acc = 0, l2s0 = 0, l2s1 = 0;  // sink of the L2-prefetch loads (never stored; see below)
@@ -493,16 +490,15 @@ __global__ void __launch_bounds__(320) state_kernel_dma(ScanParams p) {
   const int n = (int)(jdx % NV);
   const int64_t hb = (jdx / NV) * 8 + xcd;
   if (hb >= p.B * p.H) return;
-  const int64_t b = hb / p.H, h = hb % p.H;
-  const Seq sq = seq_of(p, b);
-  const int64_t nloc = seg_chunks(p, sq);
-  if (nloc == 0 && !(sq.len <= 0 && p.chunk0 == 0)) return;
+  int64_t b, h, nloc, cfirst;
+  size_t woff;
+  if (!state_item<L::bytes>(p, hb, b, h, nloc, woff, cfirst)) return;
   const int64_t sl = p.slots ? (int64_t)p.slots[b] : b;
   if (sl < 0) return;
 
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  unsigned char* wsh = p.ws + hb * (p.nseg + 1) * L::bytes;
+  unsigned char* wsh = p.ws + woff;
 
   if (w == 4) {
     // loader: barrier P after chunk 0 has landed, then per chunk A, B, C, (copy of the next chunk
@@ -591,14 +587,27 @@ __global__ void __launch_bounds__(256) output_kernel(ScanParams p) {
 
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int64_t items = p.nseg * p.H * p.B;
+  const int64_t items = p.nseg * p.H * (p.fl_off ? 1 : p.B);
   for (int64_t it = blockIdx.x; it < items; it += gridDim.x) {
   if (it != (int64_t)blockIdx.x) __syncthreads();  // the previous item's LDS tiles have been read
-  const int64_t cl = it % p.nseg, h = (it / p.nseg) % p.H, b = it / (p.nseg * p.H);
+  const int64_t x = it % p.nseg, h = (it / p.nseg) % p.H;
+  // chunk cl (chunk0 + cl in the sequence) of sequence b, its record at ws
+  int64_t b, cl;
+  const unsigned char* ws;
+  if (p.fl_off) {
+    const FlatChunk fc = flat_chunk(p, x);
+    if (!fc.ok) continue;  // a spare slot, or past the last
+    b = fc.b;
+    cl = fc.c;
+    ws = p.ws + (h * (p.nseg + 1) + x) * L::bytes;
+  } else {
+    b = it / (p.nseg * p.H);
+    cl = x;
+    if (cl >= seg_chunks(p, seq_of(p, b))) continue;  // past the end of this sequence (ragged batches)
+    ws = p.ws + ((b * p.H + h) * (p.nseg + 1) + cl) * L::bytes;
+  }
   const Seq sq = seq_of(p, b);
-  if (cl >= seg_chunks(p, sq)) continue;  // past the end of this sequence (ragged batches)
   const int64_t t0 = (p.chunk0 + cl) * CH;
-  const unsigned char* ws = p.ws + ((b * p.H + h) * (p.nseg + 1) + cl) * L::bytes;
   const float* vec = reinterpret_cast<const float*>(ws + L::VEC);
 
   frag aq[NJ];
@@ -706,6 +715,11 @@ static ScanParams fill_params(const kdn_scan_args* a) {
   p.seq_lo = a->cu_seqlens;
   p.seq_hi = a->cu_seqlens ? a->cu_seqlens + 1 : nullptr;
   p.slots = a->state_slots;
+  p.fl_off = nullptr;
+  p.fl_first = nullptr;
+  p.fl_total = nullptr;
+  p.fl_lo = 0;
+  p.fl_nseq = 0;
   p.prep_no_q = 0;
   p.k_plain = 0;
   p.prep_run = 0;
@@ -742,6 +756,8 @@ struct RunSpec {
   // ragged sequences given as separate start / end arrays (device), overriding cu_seqlens
   const int64_t* seq_lo = nullptr;
   const int64_t* seq_hi = nullptr;
+  // packed windows instead of segments (the sequences' layout planned on the device)
+  const FlatPlan* flat = nullptr;
 };
 
 // Parameters of one segment: chunks [c0, c0 + nseg) with its records at `ws`.  The state kernel of the
@@ -766,6 +782,27 @@ static ScanParams segment_params(const kdn_scan_args* a, const RunSpec& r, int64
     p.state_in = a->final_state;
     p.is0 = p.os0; p.is1 = p.os1; p.is2 = p.os2; p.is3 = p.os3;
   }
+  return p;
+}
+
+// Parameters of packed window s (slots [s * win, (s + 1) * win)) with its records at `ws`: the states
+// are read and written in place (initial_state is final_state).
+static ScanParams flat_params(const kdn_scan_args* a, const RunSpec& r, int64_t s, void* ws) {
+  ScanParams p = fill_params(a);
+  p.seq_lo = r.seq_lo;
+  p.seq_hi = r.seq_hi;
+  p.chunk0 = 0;
+  p.nseg = r.flat->win;
+  p.ws = (unsigned char*)ws;
+  p.prep_run = 1;
+  p.out_wgs = 0;
+  p.state_in = a->final_state;
+  p.is0 = p.os0; p.is1 = p.os1; p.is2 = p.os2; p.is3 = p.os3;
+  p.fl_off = r.flat->off;
+  p.fl_first = r.flat->first;
+  p.fl_total = r.flat->total;
+  p.fl_lo = s * r.flat->win;
+  p.fl_nseq = r.flat->nseq;
   return p;
 }
 
@@ -799,7 +836,7 @@ static int launch_phase(const ScanParams& p, int phase, hipStream_t st) {
     // segment becomes ready together with this one, and needs whole CUs: a grid of one workgroup per
     // (chunk, head) took every free CU and held up a quarter of its workgroups by ~55 us per segment
     // (config 3: 2.59 against 2.41 ms per layer, measured with clock stamps).
-    const int64_t items = (int64_t)p.nseg * p.H * p.B;
+    const int64_t items = (int64_t)p.nseg * p.H * (p.fl_off ? 1 : p.B);
     if (p.out_wgs > 0 && p.out_wgs < items) {
       constexpr size_t excl = CU_LDS_BYTES / 2 + 1024;
       const size_t pad = OutputLds<P, D, DV>::bytes < excl ? excl - OutputLds<P, D, DV>::bytes : 0;
@@ -817,6 +854,19 @@ static int launch_phase(const ScanParams& p, int phase, hipStream_t st) {
 template <class P, typename InT, typename OutT, int D, int DV>
 static int run_scan(const kdn_scan_args* a, const RunSpec& r) {
   const int cus = device_cus();
+  if (r.flat) {  // packed windows, one after another
+    const bool fused = Fused<P, D>::value && r.phases == PHASE_ALL && use_fused(a);
+    for (int64_t s = 0; s < r.flat->nwin; ++s) {
+      ScanParams p = flat_params(a, r, s, a->workspace);
+      p.k_plain = fused ? 1 : 0;
+      for (int ph : {PHASE_PREP, PHASE_STATE, PHASE_CHAIN, PHASE_OUTPUT}) {
+        if ((ph == PHASE_CHAIN) != fused && ph != PHASE_PREP) continue;
+        const int rc = launch_phase<P, InT, OutT, D, DV>(p, ph, r.st);
+        if (rc != KDN_OK) return rc;
+      }
+    }
+    return KDN_OK;
+  }
   int phases = r.phases;
   if (phases == PHASE_ALL && Fused<P, D>::value && use_fused(a)) phases = PHASE_PREP_FUSED | PHASE_CHAIN;
   for (int64_t c0 = r.c_begin; c0 < r.c_end; c0 += r.seg) {
@@ -850,7 +900,7 @@ static int run_pipelined(const kdn_scan_args* a, const RunSpec& r) {
   const hipStream_t aux_out = r.aux_out ? r.aux_out : r.aux;
   const bool split = aux_out != aux;
   const int64_t nchunks = (a->T + CH - 1) / CH;
-  const int64_t nsegs = (nchunks + seg - 1) / seg;
+  const int64_t nsegs = r.flat ? r.flat->nwin : (nchunks + seg - 1) / seg;
   EventSet evs;
   int rc = evs.create(3 * nbuf + 2);
   if (rc != KDN_OK) return rc;
@@ -862,8 +912,9 @@ static int run_pipelined(const kdn_scan_args* a, const RunSpec& r) {
   const int prep_cus = device_cus() - (int)state_grid(a->B, a->H, DV / 16);
   auto seg_p = [&](int64_t s) {
     const int64_t c0 = s * seg;
-    ScanParams p = segment_params(a, r, c0, (nchunks - c0 < seg) ? (nchunks - c0) : seg,
-                                  (unsigned char*)a->workspace + (size_t)(s % nbuf) * buf_bytes, prep_cus);
+    void* buf = (unsigned char*)a->workspace + (size_t)(s % nbuf) * buf_bytes;
+    ScanParams p = r.flat ? flat_params(a, r, s, buf)
+                          : segment_params(a, r, c0, (nchunks - c0 < seg) ? (nchunks - c0) : seg, buf, prep_cus);
     p.out_wgs = prep_cus > 0 ? prep_cus : 0;
     return p;
   };
@@ -906,7 +957,7 @@ static int run_pipelined_fused(const kdn_scan_args* a, const RunSpec& r) {
   const int nbuf = r.nbuf;
   const hipStream_t st = r.st, aux = r.aux;
   const int64_t nchunks = (a->T + CH - 1) / CH;
-  const int64_t nsegs = (nchunks + seg - 1) / seg;
+  const int64_t nsegs = r.flat ? r.flat->nwin : (nchunks + seg - 1) / seg;
   EventSet evs;
   int rc = evs.create(2 * nbuf + 1);
   if (rc != KDN_OK) return rc;
@@ -916,8 +967,9 @@ static int run_pipelined_fused(const kdn_scan_args* a, const RunSpec& r) {
   const int prep_cus = device_cus() - (int)(a->B * a->H * (DV / (DV >= 32 ? 32 : 16)));
   auto seg_p = [&](int64_t s) {
     const int64_t c0 = s * seg;
-    ScanParams p = segment_params(a, r, c0, (nchunks - c0 < seg) ? (nchunks - c0) : seg,
-                                  (unsigned char*)a->workspace + (size_t)(s % nbuf) * r.buf_bytes, prep_cus);
+    void* buf = (unsigned char*)a->workspace + (size_t)(s % nbuf) * r.buf_bytes;
+    ScanParams p = r.flat ? flat_params(a, r, s, buf)
+                          : segment_params(a, r, c0, (nchunks - c0 < seg) ? (nchunks - c0) : seg, buf, prep_cus);
     p.k_plain = 1;
     return p;
   };
@@ -944,7 +996,8 @@ static int run_pipelined_fused(const kdn_scan_args* a, const RunSpec& r) {
 
 template <class P, typename InT, typename OutT, int D, int DV>
 static int run(const kdn_scan_args* a, const RunSpec& r) {
-  if (r.aux && Fused<P, D>::value && r.phases == PHASE_ALL && use_fused(a)) return run_pipelined_fused<P, InT, OutT, D, DV>(a, r);
+  if (r.aux && Fused<P, D>::value && r.phases == PHASE_ALL && use_fused(a))
+    return run_pipelined_fused<P, InT, OutT, D, DV>(a, r);
   if (r.aux) return run_pipelined<P, InT, OutT, D, DV>(a, r);
   return run_scan<P, InT, OutT, D, DV>(a, r);
 }
@@ -1247,6 +1300,30 @@ int scan_pipelined(const kdn_scan_args* a, const int64_t* seq_lo, const int64_t*
     r.aux = nullptr;
     r.aux_out = nullptr;
   }
+  return dispatch(a, r);
+}
+
+size_t scan_flat_buffer_bytes(const kdn_scan_args* a, int64_t win) {
+  return chunk_bytes(a) * (size_t)a->H * (size_t)(win + 1);
+}
+
+int scan_flat(const kdn_scan_args* a, const int64_t* seq_lo, const int64_t* seq_hi, const FlatPlan& fp, void* stream,
+              void* aux_stream) {
+  int rc = validate_launch(a);
+  if (rc != KDN_OK) return rc;
+  if (general_scan_applies(a) || frep_applies(a) || a->D != 512) return KDN_ERR_UNSUPPORTED;
+  if (a->initial_state != a->final_state || !a->state_slots || !seq_lo || !seq_hi || fp.win < 1 || fp.nwin < 0)
+    return KDN_ERR_INVALID_ARGUMENT;
+  const size_t buf = scan_flat_buffer_bytes(a, fp.win);
+  if (a->workspace_bytes < buf) return KDN_ERR_WORKSPACE_TOO_SMALL;
+  if (fp.nwin == 0) return KDN_OK;
+  const size_t fit = a->workspace_bytes / buf;
+  const int nbuf = (int)(fit < 3 ? fit : 3);
+  RunSpec r = {0, 0, fp.win, PHASE_ALL, as_stream(stream), as_stream(aux_stream), nbuf, buf};
+  r.seq_lo = seq_lo;
+  r.seq_hi = seq_hi;
+  r.flat = &fp;
+  if (!aux_stream || aux_stream == stream || nbuf < 2 || fp.nwin < 2) r.aux = nullptr;
   return dispatch(a, r);
 }
 

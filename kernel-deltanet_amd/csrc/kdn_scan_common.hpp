@@ -105,7 +105,54 @@ struct ScanParams {
   const int64_t* seq_lo;
   const int64_t* seq_hi;
   const int* slots;
+  // Packed windows (ragged batches sized on the device, the serving step from a slot map): sequence b's
+  // chunks and one spare slot take the consecutive slots fl_off[b] .. fl_off[b+1]-1 of a packed slot
+  // space (the spare last; a sequence without tokens takes none), *fl_total slots in all.  A call covers
+  // the window of slots [fl_lo, fl_lo + nseg): its records are [head][slot - fl_lo], nseg + 1 per head
+  // (the last is the spare of a sequence that the window's end cuts), chunk0 is 0 and B bounds the
+  // sequences that meet one window.  fl_first[w] is the sequence holding slot w * nseg; fl_nseq the
+  // entries of fl_off less one.  fl_off NULL: the layouts above.
+  const int64_t* fl_off;
+  const int64_t* fl_first;
+  const int64_t* fl_total;
+  int64_t fl_lo, fl_nseq;
 };
+
+// Slot x of the current packed window: its sequence, its chunk index in that sequence, and whether it
+// holds one (a spare slot or a slot past the last holds none).
+struct FlatChunk {
+  int64_t b, c;
+  bool ok;
+};
+__device__ __forceinline__ FlatChunk flat_chunk(const ScanParams& p, int64_t x) {
+  FlatChunk r = {0, 0, false};
+  const int64_t g = p.fl_lo + x;
+  if (g >= *p.fl_total) return r;
+  // the last sequence whose first slot is at or before g (fl_off is nondecreasing from 0)
+  int64_t lo = p.fl_first[p.fl_lo / p.nseg], hi = p.fl_nseq;
+  while (hi - lo > 1) {
+    const int64_t mid = (lo + hi) >> 1;
+    if (p.fl_off[mid] <= g) lo = mid;
+    else hi = mid;
+  }
+  r.b = lo;
+  r.c = g - p.fl_off[lo];
+  r.ok = r.c < p.fl_off[lo + 1] - p.fl_off[lo] - 1;
+  return r;
+}
+
+// The real chunks of sequence fl_first[window] + i inside the current packed window: first slot (window-
+// relative) and count (0: none).
+__device__ __forceinline__ int64_t flat_run(const ScanParams& p, int64_t b, int64_t* first) {
+  if (b >= p.fl_nseq) return 0;
+  const int64_t a0 = p.fl_off[b], a1 = p.fl_off[b + 1] - 1;  // real chunks [a0, a1)
+  const int64_t lo = a0 > p.fl_lo ? a0 : p.fl_lo;
+  int64_t hi = a1 < p.fl_lo + p.nseg ? a1 : p.fl_lo + p.nseg;
+  const int64_t tot = *p.fl_total;
+  if (hi > tot) hi = tot;
+  *first = lo - p.fl_lo;
+  return hi > lo ? hi - lo : 0;
+}
 
 // Sequence b of the batch: element offsets of its first token in each token-indexed tensor, and its
 // length.  A uniform batch addresses b * stride0 and has T tokens per sequence; a ragged batch
@@ -131,6 +178,31 @@ __device__ __forceinline__ Seq seq_of(const ScanParams& p, int64_t b) {
 __device__ __forceinline__ int64_t seg_chunks(const ScanParams& p, const Seq& s) {
   const int64_t n = (s.len + CH - 1) / CH - p.chunk0;
   return n <= 0 ? 0 : (n < p.nseg ? n : p.nseg);
+}
+
+// The work of state workgroup row hb (b_local * H + h): sequence b and head h, the chunks it carries
+// (nloc) and the byte offset of its first record in the segment's buffer; false: nothing to do (a
+// sequence that ended in an earlier segment has its final state already; one without tokens gets its
+// initial state copied through, with no chunk run).
+// cfirst: the chunk index in the sequence of its first chunk here.
+template <size_t BYTES>
+__device__ __forceinline__ bool state_item(const ScanParams& p, int64_t hb, int64_t& b, int64_t& h, int64_t& nloc,
+                                           size_t& off, int64_t& cfirst) {
+  h = hb % p.H;
+  if (p.fl_off) {
+    b = p.fl_first[p.fl_lo / p.nseg] + hb / p.H;
+    int64_t first = 0;
+    nloc = flat_run(p, b, &first);
+    off = (size_t)(h * (p.nseg + 1) + first) * BYTES;
+    cfirst = nloc > 0 ? p.fl_lo + first - p.fl_off[b] : 0;
+    return nloc > 0;
+  }
+  b = hb / p.H;
+  const Seq sq = seq_of(p, b);
+  nloc = seg_chunks(p, sq);
+  off = (size_t)hb * (p.nseg + 1) * BYTES;
+  cfirst = p.chunk0;
+  return !(nloc == 0 && !(sq.len <= 0 && p.chunk0 == 0));
 }
 
 // Feature modes of the prep kernel: Omega exact in bf16 (the structured projection), Omega as hi + lo

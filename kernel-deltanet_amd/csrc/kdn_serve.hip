@@ -78,6 +78,106 @@ __global__ void __launch_bounds__(1024) ragged_split_kernel(const int64_t* __res
   }
 }
 
+// ---- runs of a slot map (kdn_slot_step) -------------------------------------------------------------
+// One workgroup: thread t counts the run starts (token 0, or a slot other than the previous token's) in its
+// contiguous range of tokens, an inclusive scan over the 1024 counts gives each range its first run
+// index, and the starts are written in token order: cu[r] = first token of run r, slot[r] = its slot.
+// Entries from the number of runs to `cap` get cu = n (no tokens) and slot -1.  More runs than `cap` (a
+// map whose distinct runs do not have distinct slots) mark every run skipped and set *status to 1.
+__global__ void __launch_bounds__(1024) slot_runs_kernel(const void* __restrict__ sm, int slot_bytes, int64_t n,
+                                                         int64_t cap, int64_t* __restrict__ cu, int32_t* __restrict__ slot,
+                                                         int32_t* __restrict__ status) {
+  __shared__ int64_t s_c[1024];
+  __shared__ int64_t s_total;
+  const int t = threadIdx.x;
+  auto at = [&](int64_t i) -> int64_t {
+    return slot_bytes == 8 ? reinterpret_cast<const int64_t*>(sm)[i] : (int64_t)reinterpret_cast<const int32_t*>(sm)[i];
+  };
+  const int64_t per = (n + 1023) / 1024;
+  const int64_t i0 = t * per < n ? t * per : n, i1 = (i0 + per < n) ? i0 + per : n;
+  int64_t cnt = 0;
+  for (int64_t i = i0; i < i1; ++i) cnt += (i == 0 || at(i) != at(i - 1));
+  s_c[t] = cnt;
+  __syncthreads();
+  for (int off = 1; off < 1024; off <<= 1) {
+    const int64_t a = t >= off ? s_c[t - off] : 0;
+    __syncthreads();
+    s_c[t] += a;
+    __syncthreads();
+  }
+  if (t == 1023) s_total = s_c[1023];
+  __syncthreads();
+  const int64_t total = s_total;
+  const bool over = total > cap;
+  int64_t r = s_c[t] - cnt;
+  for (int64_t i = i0; i < i1; ++i) {
+    if (i == 0 || at(i) != at(i - 1)) {
+      if (r < cap) {
+        cu[r] = i;
+        const int64_t sv = at(i);
+        slot[r] = (over || sv < 0 || sv > 0x7fffffff) ? -1 : (int32_t)sv;
+      }
+      ++r;
+    }
+  }
+  const int64_t used = over ? cap : total;
+  for (int64_t k = used + t; k < cap; k += 1024) {
+    cu[k] = n;
+    slot[k] = -1;
+  }
+  if (t == 0) {
+    cu[cap] = n;
+    if (status) *status = over ? 1 : 0;
+  }
+}
+
+// The packed slot layout of the prefill list (ragged_split_kernel's pre_lo / pre_hi, `cap` entries):
+// entry i takes ceil(len / 64) chunk slots and one spare when it has tokens, none otherwise; off[i] is the
+// exclusive prefix of those counts (off[cap] = *total) and first[w] the entry holding slot w * win (for
+// windows past the total, the last entry).  One workgroup, the scan as in slot_runs_kernel.
+__global__ void __launch_bounds__(1024) flat_plan_kernel(const int64_t* __restrict__ lo, const int64_t* __restrict__ hi,
+                                                         int64_t cap, int64_t win, int64_t nwin, int64_t* __restrict__ off,
+                                                         int64_t* __restrict__ first, int64_t* __restrict__ total) {
+  __shared__ int64_t s_c[1024];
+  const int t = threadIdx.x;
+  const int64_t per = (cap + 1023) / 1024;
+  const int64_t i0 = t * per < cap ? t * per : cap, i1 = (i0 + per < cap) ? i0 + per : cap;
+  auto slots_of = [&](int64_t i) -> int64_t {
+    const int64_t len = hi[i] - lo[i];
+    return len >= 2 ? (len + 63) / 64 + 1 : 0;
+  };
+  int64_t cnt = 0;
+  for (int64_t i = i0; i < i1; ++i) cnt += slots_of(i);
+  s_c[t] = cnt;
+  __syncthreads();
+  for (int o = 1; o < 1024; o <<= 1) {
+    const int64_t a = t >= o ? s_c[t - o] : 0;
+    __syncthreads();
+    s_c[t] += a;
+    __syncthreads();
+  }
+  int64_t acc = s_c[t] - cnt;
+  for (int64_t i = i0; i < i1; ++i) {
+    off[i] = acc;
+    acc += slots_of(i);
+  }
+  if (t == 1023) {
+    off[cap] = s_c[1023];
+    *total = s_c[1023];
+  }
+  __syncthreads();  // off[] complete (the block's global writes are visible to its own threads after the barrier)
+  for (int64_t w = t; w < nwin; w += 1024) {
+    const int64_t g = w * win;
+    int64_t a = 0, b = cap;  // the last i in [0, cap) with off[i] <= g
+    while (b - a > 1) {
+      const int64_t m = (a + b) >> 1;
+      if (off[m] <= g) a = m;
+      else b = m;
+    }
+    first[w] = a;
+  }
+}
+
 // ---- decode -----------------------------------------------------------------------------------------
 struct DecodeParams {
   const int64_t* rows;   // token row of decode sequence i
@@ -363,4 +463,142 @@ extern "C" int kdn_ragged_step(const kdn_ragged_args* a, void* stream, void* aux
     if (rc != KDN_OK) return rc;
   }
   return KDN_OK;
+}
+
+// ---- the step from a slot map ----------------------------------------------------------------------
+namespace kdn {
+
+// Packed chunk slots per prefill window: at most SLOT_WIN_MAX (the sequences of one window carry their
+// states side by side, so a window must hold many of them: 128 slots, about two config-5 prefills per
+// window, took 5.8 ms for the config-5 step against 3.7 with host offsets), fewer when all fit.
+constexpr int64_t SLOT_WIN_MAX = 1024;
+
+// Sizes of kdn_slot_step's workspace, all bounds from num_tokens and num_slots: `cap` runs at most (one
+// per slot, and the padding runs between them), n_pre prefills (two tokens or more each), G packed slots
+// (each prefill's chunks and its spare), `nwin` windows of SLOT_WIN slots.
+struct SlotPlan {
+  int64_t cap, n_pre, win, nwin, seq_bound;
+  size_t small_bytes, buf_bytes, total;
+};
+
+static kdn_scan_args slot_scan_args(const kdn_slot_step_args* a, int64_t seq_bound) {
+  kdn_scan_args s = {};
+  s.B = seq_bound; s.T = a->num_tokens; s.H = a->H;
+  s.d_k = a->d_k; s.D = a->D; s.d_v = a->d_v;
+  s.in_dtype = a->in_dtype; s.out_dtype = a->out_dtype;
+  s.normalize_input = a->normalize_input; s.inv_tau = a->inv_tau; s.rule = a->rule;
+  s.q = a->q; s.q_stride[0] = 0; s.q_stride[1] = a->q_stride[0]; s.q_stride[2] = a->q_stride[1];
+  s.k = a->k; s.k_stride[0] = 0; s.k_stride[1] = a->k_stride[0]; s.k_stride[2] = a->k_stride[1];
+  s.v = a->v; s.v_stride[0] = 0; s.v_stride[1] = a->v_stride[0]; s.v_stride[2] = a->v_stride[1];
+  s.beta = a->beta; s.beta_stride[0] = 0; s.beta_stride[1] = a->beta_stride[0]; s.beta_stride[2] = a->beta_stride[1];
+  s.decay = a->decay; s.decay_stride[0] = 0; s.decay_stride[1] = a->decay_stride[0]; s.decay_stride[2] = a->decay_stride[1];
+  s.omega_bf16 = a->omega_bf16; s.phase = a->phase;
+  s.initial_state = a->states; s.final_state = a->states;
+  for (int d = 0; d < 4; ++d) s.init_stride[d] = s.final_stride[d] = a->state_stride[d];
+  s.y = a->y; s.y_stride[0] = 0; s.y_stride[1] = a->y_stride[0]; s.y_stride[2] = a->y_stride[1];
+  return s;
+}
+
+static int slot_plan(const kdn_slot_step_args* a, SlotPlan& pl) {
+  if (!a || a->num_tokens < 0 || a->H <= 0 || a->H > 65535) return KDN_ERR_INVALID_ARGUMENT;
+  if (!valid_dtype(a->in_dtype) || !valid_dtype(a->out_dtype) || (a->rule != 0 && a->rule != 1))
+    return KDN_ERR_INVALID_ARGUMENT;
+  if (a->slot_bytes != 4 && a->slot_bytes != 8) return KDN_ERR_INVALID_ARGUMENT;
+  if (a->d_k != SRV_DK || a->D != SRV_D) return KDN_ERR_UNSUPPORTED;
+  if (a->d_v != 16 && a->d_v != 32 && a->d_v != 64 && a->d_v != 128) return KDN_ERR_UNSUPPORTED;
+  if (!(a->inv_tau == a->inv_tau) || a->num_slots <= 0) return KDN_ERR_INVALID_ARGUMENT;
+  const int64_t n = a->num_tokens;
+  pl.cap = 2 * a->num_slots + 1 < n ? 2 * a->num_slots + 1 : n;
+  if (pl.cap < 1) pl.cap = 1;
+  pl.n_pre = pl.cap < n / 2 ? pl.cap : n / 2;
+  const int64_t g = (n + 63) / 64 + 2 * pl.n_pre;
+  pl.win = (g + 63) / 64 * 64 < SLOT_WIN_MAX ? (g + 63) / 64 * 64 : SLOT_WIN_MAX;
+  pl.nwin = pl.n_pre > 0 ? (g + pl.win - 1) / pl.win : 0;
+  pl.seq_bound = pl.win / 2 + 1 < pl.cap ? pl.win / 2 + 1 : pl.cap;
+  const size_t c = (size_t)pl.cap;
+  pl.small_bytes = round256((c + 1) * 8) + round256(c * 4)                       // runs
+                 + 3 * round256(c * 8) + 2 * round256(c * 4)                      // decode / prefill lists
+                 + round256((c + 1) * 8) + round256(8) + round256((size_t)(pl.nwin > 0 ? pl.nwin : 1) * 8);  // layout
+  pl.buf_bytes = 0;
+  if (pl.nwin > 0) {
+    const kdn_scan_args s = slot_scan_args(a, pl.seq_bound);
+    pl.buf_bytes = round256(scan_flat_buffer_bytes(&s, pl.win));
+  }
+  const size_t nbuf = pl.nwin >= 3 ? 3 : (size_t)pl.nwin;
+  pl.total = pl.small_bytes + nbuf * pl.buf_bytes;
+  return KDN_OK;
+}
+
+}  // namespace kdn
+
+extern "C" size_t kdn_slot_step_workspace_bytes(const kdn_slot_step_args* a) {
+  SlotPlan pl;
+  if (slot_plan(a, pl) != KDN_OK) return 0;
+  return pl.total;
+}
+
+extern "C" int kdn_slot_step(const kdn_slot_step_args* a, void* stream, void* aux_stream) {
+  SlotPlan pl;
+  int rc = slot_plan(a, pl);
+  if (rc != KDN_OK) return rc;
+  if (a->num_tokens == 0) return KDN_OK;
+  if (!a->slot_mapping || !a->q || !a->k || !a->v || !a->beta || !a->omega_bf16 || !a->phase || !a->states || !a->y ||
+      !a->workspace)
+    return KDN_ERR_INVALID_ARGUMENT;
+  if (!aligned(a->workspace, 256) || !aligned(a->omega_bf16, 16) || !aligned(a->slot_mapping, (size_t)a->slot_bytes))
+    return KDN_ERR_MISALIGNED;
+  if (a->workspace_bytes < pl.total) return KDN_ERR_WORKSPACE_TOO_SMALL;
+  const hipStream_t st = as_stream(stream);
+  const size_t c = (size_t)pl.cap;
+  unsigned char* w = (unsigned char*)a->workspace;
+  int64_t* cu = (int64_t*)w;        w += round256((c + 1) * 8);
+  int32_t* rslot = (int32_t*)w;     w += round256(c * 4);
+  int64_t* dec_row = (int64_t*)w;   w += round256(c * 8);
+  int64_t* pre_lo = (int64_t*)w;    w += round256(c * 8);
+  int64_t* pre_hi = (int64_t*)w;    w += round256(c * 8);
+  int32_t* dec_slot = (int32_t*)w;  w += round256(c * 4);
+  int32_t* pre_slot = (int32_t*)w;  w += round256(c * 4);
+  int64_t* fl_off = (int64_t*)w;    w += round256((c + 1) * 8);
+  int64_t* fl_total = (int64_t*)w;  w += round256(8);
+  int64_t* fl_first = (int64_t*)w;  w += round256((size_t)(pl.nwin > 0 ? pl.nwin : 1) * 8);
+  hipLaunchKernelGGL(slot_runs_kernel, dim3(1), dim3(1024), 0, st, a->slot_mapping, a->slot_bytes, a->num_tokens,
+                     pl.cap, cu, rslot, a->status);
+  hipLaunchKernelGGL(ragged_split_kernel, dim3(1), dim3(1024), 0, st, (const int64_t*)cu, (const int32_t*)rslot,
+                     pl.cap, a->num_slots, dec_row, dec_slot, pre_lo, pre_hi, pre_slot);
+  rc = launch_status();
+  if (rc != KDN_OK) return rc;
+  // decode: one entry per possible run; entries the split did not fill have slot -1 and exit at once
+  DecodeParams dp;
+  dp.rows = dec_row; dp.slots = dec_slot;
+  dp.q = a->q; dp.qs0 = a->q_stride[0]; dp.qs1 = a->q_stride[1];
+  dp.k = a->k; dp.ks0 = a->k_stride[0]; dp.ks1 = a->k_stride[1];
+  dp.v = a->v; dp.vs0 = a->v_stride[0]; dp.vs1 = a->v_stride[1];
+  dp.beta = a->beta; dp.bs0 = a->beta_stride[0]; dp.bs1 = a->beta_stride[1];
+  dp.decay = a->decay; dp.ds0 = a->decay_stride[0]; dp.ds1 = a->decay_stride[1];
+  dp.omega = (const __bf16*)a->omega_bf16; dp.phase = a->phase;
+  dp.inv_tau = a->inv_tau; dp.normalize = a->normalize_input ? 1 : 0; dp.linear = a->rule == 1 ? 1 : 0;
+  dp.states = a->states;
+  dp.ss0 = a->state_stride[0]; dp.ss1 = a->state_stride[1]; dp.ss2 = a->state_stride[2]; dp.ss3 = a->state_stride[3];
+  dp.y = a->y; dp.ys0 = a->y_stride[0]; dp.ys1 = a->y_stride[1];
+  if (a->in_dtype == KDN_DTYPE_BF16)
+    rc = a->out_dtype == KDN_DTYPE_BF16 ? launch_decode<__bf16, __bf16>(dp, pl.cap, a->H, a->d_v, st)
+                                        : launch_decode<__bf16, float>(dp, pl.cap, a->H, a->d_v, st);
+  else
+    rc = a->out_dtype == KDN_DTYPE_BF16 ? launch_decode<float, __bf16>(dp, pl.cap, a->H, a->d_v, st)
+                                        : launch_decode<float, float>(dp, pl.cap, a->H, a->d_v, st);
+  if (rc != KDN_OK) return rc;
+  if (pl.nwin == 0) return KDN_OK;
+  // prefill: the packed layout, then the split scan over its windows
+  hipLaunchKernelGGL(flat_plan_kernel, dim3(1), dim3(1024), 0, st, (const int64_t*)pre_lo, (const int64_t*)pre_hi,
+                     pl.cap, pl.win, pl.nwin, fl_off, fl_first, fl_total);
+  rc = launch_status();
+  if (rc != KDN_OK) return rc;
+  kdn_scan_args s = slot_scan_args(a, pl.seq_bound);
+  s.state_slots = pre_slot;
+  s.workspace = w;
+  s.workspace_bytes = a->workspace_bytes - (size_t)(w - (unsigned char*)a->workspace);
+  FlatPlan fp;
+  fp.off = fl_off; fp.first = fl_first; fp.total = fl_total;
+  fp.nseq = pl.cap; fp.win = pl.win; fp.nwin = pl.nwin;
+  return scan_flat(&s, pre_lo, pre_hi, fp, stream, aux_stream);
 }

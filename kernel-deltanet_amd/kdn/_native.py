@@ -41,6 +41,8 @@ EXPORTED = (
     "kdn_delta_scan_fwd_streams",
     "kdn_ragged_workspace_bytes",
     "kdn_ragged_step",
+    "kdn_slot_step_workspace_bytes",
+    "kdn_slot_step",
     "kdn_pool_create",
     "kdn_pool_destroy",
     "kdn_pool_allocate",
@@ -127,6 +129,31 @@ class RaggedArgs(ctypes.Structure):
     ]
 
 
+class SlotStepArgs(ctypes.Structure):
+    """Mirror of struct kdn_slot_step_args (include/kdn.h)."""
+
+    _fields_ = [
+        ("num_tokens", _i64), ("H", _i64),
+        ("d_k", ctypes.c_int), ("D", ctypes.c_int), ("d_v", ctypes.c_int),
+        ("in_dtype", ctypes.c_int), ("out_dtype", ctypes.c_int), ("normalize_input", ctypes.c_int),
+        ("rule", ctypes.c_int),
+        ("inv_tau", ctypes.c_float),
+        ("slot_mapping", ctypes.c_void_p),
+        ("slot_bytes", ctypes.c_int),
+        ("q", ctypes.c_void_p), ("q_stride", _i64x2),
+        ("k", ctypes.c_void_p), ("k_stride", _i64x2),
+        ("v", ctypes.c_void_p), ("v_stride", _i64x2),
+        ("beta", ctypes.c_void_p), ("beta_stride", _i64x2),
+        ("decay", ctypes.c_void_p), ("decay_stride", _i64x2),
+        ("omega_bf16", ctypes.c_void_p), ("phase", ctypes.c_void_p),
+        ("states", ctypes.c_void_p), ("state_stride", _i64x4),
+        ("num_slots", _i64),
+        ("y", ctypes.c_void_p), ("y_stride", _i64x2),
+        ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_size_t),
+        ("status", ctypes.c_void_p),
+    ]
+
+
 class ScanBwdArgs(ctypes.Structure):
     """Mirror of struct kdn_scan_bwd_args (include/kdn.h)."""
 
@@ -204,6 +231,10 @@ def lib() -> ctypes.CDLL:
             L.kdn_ragged_workspace_bytes.restype = sz
             L.kdn_ragged_step.argtypes = [ctypes.POINTER(RaggedArgs), vp, vp]
             L.kdn_ragged_step.restype = ci
+            L.kdn_slot_step_workspace_bytes.argtypes = [ctypes.POINTER(SlotStepArgs)]
+            L.kdn_slot_step_workspace_bytes.restype = sz
+            L.kdn_slot_step.argtypes = [ctypes.POINTER(SlotStepArgs), vp, vp]
+            L.kdn_slot_step.restype = ci
             L.kdn_pool_create.argtypes = [i64, i64, ctypes.POINTER(vp)]
             L.kdn_pool_create.restype = ci
             L.kdn_pool_destroy.argtypes = [vp]

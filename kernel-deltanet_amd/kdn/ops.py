@@ -865,6 +865,76 @@ def ragged_step(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, beta: torch.T
     return y
 
 
+def slot_step(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, beta: torch.Tensor, decay: Optional[torch.Tensor],
+              slot_mapping: torch.Tensor, states: torch.Tensor, omega_bf16: torch.Tensor, phase: torch.Tensor,
+              inv_tau: float, normalize: bool = False, rule: int = RULE_DELTA, y: Optional[torch.Tensor] = None,
+              out_dtype: Optional[torch.dtype] = None, workspace: Optional[torch.Tensor] = None,
+              pipelined: bool = True, status: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """The ragged step described by a token -> slot map alone (kdn_slot_step): nothing is read back to the
+    host.  q, k (tokens, H, d_k), v (tokens, H, d_v), beta, decay (tokens, H); slot_mapping (tokens,) int32
+    or int64 on the device, a sequence being a run of equal consecutive slots (negative: padding);
+    states (slots, H, D, d_v) float32 updated in place.  Distinct runs must have distinct slots (not
+    checked); `status` (device int32 (1,), optional) is set to 1 when the map has more runs than
+    2 * slots + 1 (then nothing runs).  Returns y (tokens, H, d_v)."""
+    for t, nm in ((q, "q"), (k, "k"), (v, "v"), (beta, "beta"), (states, "states"), (slot_mapping, "slot_mapping")):
+        require_device(t, f"slot_step: {nm}")
+    dev = q.device
+    if q.dim() != 3 or k.shape != q.shape or v.dim() != 3 or v.shape[:2] != q.shape[:2] or beta.shape != q.shape[:2]:
+        raise ValueError(f"slot_step: shapes q{tuple(q.shape)} k{tuple(k.shape)} v{tuple(v.shape)} beta{tuple(beta.shape)}")
+    if k.dtype != q.dtype or v.dtype != q.dtype:
+        raise TypeError("slot_step: q, k and v must share a dtype")
+    if states.dtype != torch.float32 or states.dim() != 4:
+        raise TypeError("slot_step: states must be a float32 (slots, H, D, d_v) tensor")
+    if slot_mapping.dim() != 1 or slot_mapping.shape[0] != q.shape[0] or slot_mapping.dtype not in (torch.int32, torch.int64):
+        raise ValueError("slot_step: slot_mapping must be an int32 or int64 (tokens,) tensor")
+    sm = slot_mapping.contiguous()
+    q, k, v = _last_contig(q), _last_contig(k), _last_contig(v)
+    beta = beta.to(torch.float32)
+    if decay is not None:
+        decay = decay.to(device=dev, dtype=torch.float32)
+    T, H = q.shape[:2]
+    d_v = v.shape[-1]
+    if y is None:
+        y = torch.empty(T, H, d_v, device=dev, dtype=q.dtype if out_dtype is None else out_dtype)
+    om = omega_bf16.to(dev).contiguous()
+    ph = phase.to(device=dev, dtype=torch.float32).contiguous()
+    a = N.SlotStepArgs()
+    a.num_tokens, a.H = T, H
+    a.d_k, a.D, a.d_v = q.shape[-1], om.shape[0], d_v
+    a.in_dtype, a.out_dtype = _tag(q.dtype, "slot step inputs"), _tag(y.dtype, "slot step output")
+    a.normalize_input, a.rule, a.inv_tau = 1 if normalize else 0, int(rule), float(inv_tau)
+    a.slot_mapping, a.slot_bytes = sm.data_ptr(), sm.element_size()
+    a.q, a.q_stride = q.data_ptr(), N._i64x2(*q.stride()[:2])
+    a.k, a.k_stride = k.data_ptr(), N._i64x2(*k.stride()[:2])
+    a.v, a.v_stride = v.data_ptr(), N._i64x2(*v.stride()[:2])
+    a.beta, a.beta_stride = beta.data_ptr(), N._i64x2(*beta.stride())
+    if decay is not None:
+        a.decay, a.decay_stride = decay.data_ptr(), N._i64x2(*decay.stride())
+    a.omega_bf16, a.phase = om.data_ptr(), ph.data_ptr()
+    a.states, a.state_stride = states.data_ptr(), N._i64x4(*states.stride())
+    a.num_slots = states.shape[0]
+    a.y, a.y_stride = y.data_ptr(), N._i64x2(*y.stride()[:2])
+    a.status = status.data_ptr() if status is not None else None
+    need = int(N.lib().kdn_slot_step_workspace_bytes(ctypes.byref(a)))
+    if need == 0:
+        raise ValueError("slot_step: unsupported shape (kdn_slot_step_workspace_bytes returned 0)")
+    if workspace is None or workspace.numel() * workspace.element_size() < need:
+        workspace = torch.empty(need, dtype=torch.uint8, device=dev)
+    a.workspace, a.workspace_bytes = workspace.data_ptr(), workspace.numel() * workspace.element_size()
+    st = torch.cuda.current_stream(dev)
+    with torch.cuda.device(dev):
+        aux = None
+        if pipelined:
+            aux = aux_stream(dev)
+            for t in (q, k, v, beta, decay, om, ph, states, y, sm, workspace, status):
+                if t is not None:
+                    t.record_stream(aux)
+        N.check(N.lib().kdn_slot_step(ctypes.byref(a), ctypes.c_void_p(st.cuda_stream),
+                                      ctypes.c_void_p(aux.cuda_stream) if aux is not None else None),
+                "kdn_slot_step")
+    return y
+
+
 class StatePool:
     """Slab state pool (kdn_pool_*): `max_slots` fp32 slots of shape (layers, H, D, d_v) in one device
     tensor, with slot bookkeeping in the native library.  New slots are zeroed; fork copies a slot."""

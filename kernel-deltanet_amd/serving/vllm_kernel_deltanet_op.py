@@ -10,14 +10,18 @@ hybrid_recurrent_forward(query, key, value, beta, decay, recurrent_states, slot_
   update) and the structured lift (kernels/fwht.py:122-131), one-token sequences on the decode kernel and
   longer ones on the chunked scan, and the slots are updated in place.
 
-  Two ways to describe the batch:
-  - slot_mapping alone: the runs of equal slots are found on the host (one device-to-host copy of
-    slot_mapping per call, a synchronisation), and their slots checked (in range, one run per slot).
+  Two ways to describe the batch, neither of which synchronises with the host:
+  - slot_mapping alone (the reference's eight arguments): kdn_slot_step finds the runs of equal slots,
+    splits them into decode and prefill sequences and packs the prefills on the device, with every launch
+    sized from num_tokens and the number of slots.  Distinct runs must have distinct slots (not checked);
+    a slot outside recurrent_states marks padding.
   - cu_seqlens (host offsets, as a scheduler keeps them) with cu_seqlens_device (the same offsets on the
     device) and optionally seq_slots (device, one slot per sequence; default: slot_mapping at each
-    sequence's first token, gathered on the device): no synchronisation and no host-to-device copy per
-    call.  Device slots are not checked on the host; the kernels skip sequences whose slot is outside
+    sequence's first token, gathered on the device): launches sized from the actual sequence lengths.
+    Device slots are not checked on the host; the kernels skip sequences whose slot is outside
     recurrent_states.
+  sequences_from_slot_mapping() gives a host caller the runs and checks them (it copies slot_mapping to
+  the host).
 fork_recurrent_state(recurrent_states, parent_slot, child_slot)
   Copies one slot's state into another on the current stream (reference :41-58).
 """
@@ -75,8 +79,11 @@ def hybrid_recurrent_forward(query: torch.Tensor, key: torch.Tensor, value: torc
     if query.shape[0] == 0:
         return output
     if cu_seqlens is None:
-        cu, slots = sequences_from_slot_mapping(slot_mapping, recurrent_states.shape[0])
-        cu_dev = None
+        sm = slot_mapping if slot_mapping.device == dev else slot_mapping.to(dev)
+        ops.slot_step(query, key, value, beta, decay, sm, recurrent_states.transpose(2, 3), proj.device_omega(dev),
+                      proj.device_phase(dev), proj.tau_star_inv, normalize=normalize_input, y=output,
+                      workspace=workspace)
+        return output
     else:
         cu = torch.as_tensor(cu_seqlens, dtype=torch.int64)
         if cu.is_cuda:

@@ -62,7 +62,7 @@ def test_args_layout_matches_c(cname, pystruct):
 def test_strerror_and_version(lib):
     for code in (0, -1, -2, -3, -4, -5, -99):
         assert len(lib.kdn_strerror(code)) > 0
-    assert lib.kdn_abi_version() == (2 << 16) | 1
+    assert lib.kdn_abi_version() == (2 << 16) | 2
 
 
 def _args(**kw):
@@ -333,3 +333,27 @@ def test_factored_lift_backward_errors_need_no_device(lib):
     assert fb(*ok[:8], float("nan"), *ok[9:]) == -1
     assert fb(*ok[:10], 512, *ok[11:]) == -1                             # dout rows of 1024
     assert fb(*ok[:9], p + 2, *ok[10:]) == -4                            # fp32 dout
+
+
+def test_slot_step_workspace_and_errors_need_no_device(lib):
+    # the serving step from a slot map: every size from num_tokens and num_slots.  1000 tokens, 10 slots:
+    # at most 21 runs (and prefills), 16 + 2 * 21 packed slots = one 128-slot window; the small arrays
+    # (runs, lists, layout: 2560 bytes) and one window buffer of 2 heads x 129 records of 238,592 bytes
+    a = N.SlotStepArgs()
+    a.num_tokens, a.H, a.d_k, a.D, a.d_v = 1000, 2, 64, 512, 64
+    a.in_dtype = a.out_dtype = N.KDN_DTYPE_BF16
+    a.inv_tau, a.slot_bytes, a.num_slots = 0.35355339, 8, 10
+    assert lib.kdn_slot_step_workspace_bytes(ctypes.byref(a)) == 2560 + 2 * 129 * 238592
+    a.num_tokens = 1                          # one token: a decode at most, no prefill window
+    assert lib.kdn_slot_step_workspace_bytes(ctypes.byref(a)) == 10 * 256
+    a.num_tokens = 1000
+    a.slot_bytes = 2
+    assert lib.kdn_slot_step_workspace_bytes(ctypes.byref(a)) == 0
+    a.slot_bytes, a.D = 4, 256
+    assert lib.kdn_slot_step_workspace_bytes(ctypes.byref(a)) == 0   # D = 512 only
+    a.D = 512
+    assert lib.kdn_slot_step(ctypes.byref(a), None, None) == -1       # no pointers
+    for i, f in enumerate(("slot_mapping", "q", "k", "v", "beta", "omega_bf16", "phase", "states", "y", "workspace")):
+        setattr(a, f, 0x7F0000000000 + 0x100000 * i)
+    a.workspace_bytes = 1024
+    assert lib.kdn_slot_step(ctypes.byref(a), None, None) == -3

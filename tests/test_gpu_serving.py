@@ -289,3 +289,96 @@ def test_serving_op_without_host_sync(proj, oproj, gather_slots):
     for i, s in enumerate(slots.tolist()):
         if lens[i]:
             assert rel_l2(rs[s].transpose(1, 2).cpu().numpy(), Sr[s]) < 1e-4
+
+
+def _slot_map(lens, slots):
+    return torch.repeat_interleave(torch.as_tensor(slots, dtype=torch.int64), torch.tensor(lens))
+
+
+def test_reference_signature_without_host_sync(proj, oproj):
+    """hybrid_recurrent_forward with the reference op's eight arguments only (kdn_slot_step: runs, split and
+    packed prefill layout on the device) under torch's sync debug mode "error": decodes, prefills of 2, 64,
+    300 and 64 * 140 + 17 tokens (the last spans two 128-slot windows), padding runs; results against the
+    float64 oracle, slots no run uses bit-identical."""
+    lens = [1, 2, 1, 300, 5, 1, 64 * 140 + 17, 64, 1]
+    run_slots = [3, 7, -1, 0, -1, 11, 5, 2, 9]          # -1: padding runs
+    H, n_slots = 2, 12
+    g = torch.Generator().manual_seed(21)
+    T = int(sum(lens))
+    q = torch.randn(T, H, 64, generator=g).to(torch.bfloat16)
+    k = torch.randn(T, H, 64, generator=g).to(torch.bfloat16)
+    v = torch.randn(T, H, 64, generator=g).to(torch.bfloat16)
+    beta = torch.sigmoid(torch.randn(T, H, generator=g))
+    lam = 0.95 + 0.05 * torch.rand(T, H, generator=g)
+    states = 0.05 * torch.randn(n_slots, H, 512, 64, generator=g)
+    slot_mapping = _slot_map(lens, run_slots).to(DEV)
+    qd, kd, vd, bd, ld = (t.to(DEV) for t in (q, k, v, beta, lam))
+    out = torch.full((T, H, 64), 7.0, device=DEV, dtype=torch.bfloat16)
+    scratch = states.transpose(2, 3).contiguous().to(DEV)
+    hybrid_recurrent_forward(qd, kd, vd, bd, ld, scratch, slot_mapping, out)   # first call: tables, streams
+    torch.cuda.synchronize()
+    rs = states.transpose(2, 3).contiguous().to(DEV)
+    out.fill_(7.0)
+    torch.cuda.set_sync_debug_mode("error")
+    try:
+        hybrid_recurrent_forward(qd, kd, vd, bd, ld, rs, slot_mapping, out)
+    finally:
+        torch.cuda.set_sync_debug_mode("default")
+    torch.cuda.synchronize()
+    cu = torch.tensor([0] + list(np.cumsum(lens)), dtype=torch.int64)
+    live = [i for i, s in enumerate(run_slots) if s >= 0]
+    y = out.float().cpu().numpy()
+    S = rs.transpose(2, 3).cpu()
+    for i in live:
+        lo, hi, s = int(cu[i]), int(cu[i + 1]), run_slots[i]
+        for h in range(H):
+            pq = ol.lift(q[lo:hi, h].float().numpy(), oproj)
+            pk = ol.lift(k[lo:hi, h].float().numpy(), oproj)
+            yr, Sr = osc.token_recurrence(pq[None], pk[None], v[lo:hi, h].double().numpy()[None],
+                                          beta[lo:hi, h].double().numpy()[None], lam[lo:hi, h].double().numpy()[None],
+                                          states[s, h].double().numpy().T[None])
+            assert rel_l2(y[lo:hi, h], yr[0]) < TOL[torch.bfloat16], (i, h)
+            assert rel_l2(S[s, h].numpy(), Sr[0].T) < TOL[torch.bfloat16], (i, h)
+    for i, s in enumerate(run_slots):   # padding rows keep what the caller had
+        if s < 0:
+            assert (out[int(cu[i]):int(cu[i + 1])].float() == 7.0).all()
+    used = {s for s in run_slots if s >= 0}
+    for s in range(n_slots):
+        if s not in used:
+            assert torch.equal(S[s], states[s]), s
+
+
+@pytest.mark.parametrize("dtype,schedule", [(torch.float32, "split"), (torch.bfloat16, "split"),
+                                            (torch.bfloat16, "fused")])
+def test_slot_step_equals_ragged_step(proj, monkeypatch, dtype, schedule):
+    """kdn_slot_step (layout from the slot map on the device, packed windows) against kdn_ragged_step (host
+    offsets, segments) on the same step, both on one schedule: the same kernels and products, so y and the
+    states agree bit for bit."""
+    monkeypatch.setenv("KDN_SCAN_SCHEDULE", schedule)
+    lens = [1, 37, 1, 200, 1, 64, 130, 1, 2, 64 * 130 + 5]
+    q, k, v, beta, lam, cu, slots, states = make_step(lens, 2, 64, dtype, 16, seed=23)
+    d = lambda t: t.to(DEV)
+    s1, s2 = d(states), d(states)
+    y1 = ops.ragged_step(d(q), d(k), d(v), d(beta), d(lam), cu, slots, s1, proj.device_omega(DEV),
+                         proj.device_phase(DEV), proj.tau_star_inv)
+    y2 = ops.slot_step(d(q), d(k), d(v), d(beta), d(lam), d(_slot_map(lens, slots)), s2, proj.device_omega(DEV),
+                       proj.device_phase(DEV), proj.tau_star_inv)
+    torch.cuda.synchronize()
+    assert torch.equal(y1, y2)
+    assert torch.equal(s1, s2)
+
+
+def test_slot_step_rejects_maps_with_too_many_runs(proj):
+    """2 slots allow at most 5 runs: a map of 7 alternating runs is invalid, status is set to 1 and nothing
+    runs (states and y untouched)."""
+    lens = [3, 1, 4, 1, 5, 1, 2]
+    q, k, v, beta, lam, _, _, states = make_step(lens, 2, 64, torch.float32, 2, seed=5)
+    sm = _slot_map(lens, [0, 1, 0, 1, 0, 1, 0]).to(torch.int32).to(DEV)
+    sd = states.to(DEV)
+    y = torch.full((q.shape[0], 2, 64), 3.0, device=DEV)
+    status = torch.zeros(1, dtype=torch.int32, device=DEV)
+    ops.slot_step(q.to(DEV), k.to(DEV), v.to(DEV), beta.to(DEV), lam.to(DEV), sm, sd, proj.device_omega(DEV),
+                  proj.device_phase(DEV), proj.tau_star_inv, y=y, status=status)
+    torch.cuda.synchronize()
+    assert int(status[0]) == 1
+    assert torch.equal(sd.cpu(), states) and (y == 3.0).all()
