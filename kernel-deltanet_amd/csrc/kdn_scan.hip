@@ -102,8 +102,8 @@ struct StateShared {
 // Wave-private LDS copy of the wave's 16 K fragments (token tile m, local 32-feature block jj), from
 // which the K^T operand of the state update is read back transposed.
 //   bf16: two planes of 8 KB; plane h holds bytes [8h, 8h+8) of every lane's 16-byte fragment slot
-//         (features 16h .. 16h+15 of the 32-block) at (fragment * 64 + lane) * 8, so that each
-//         transposed read below covers 512 contiguous bytes (no bank conflicts).
+//         (features 16h .. 16h+15 of the 32-block) at (fragment * 64 + kimg_swizzle(lane)) * 8, the
+//         layout of the record's K image (bank-conflict-free for the plain and the transposed read).
 //   fp32: fragments in lane order, 32 bytes per lane.
 template <class P>
 __device__ __forceinline__ void stage_k(typename P::frag* kl, int lane, const typename P::frag (&ak)[4][4]);
@@ -117,8 +117,9 @@ __device__ __forceinline__ void stage_k<PrecBF16>(PrecBF16::frag* kl, int lane, 
 #pragma unroll
     for (int jj = 0; jj < 4; ++jj) {
       const int fi = m * 4 + jj;
-      *reinterpret_cast<bf16x4*>(base + (size_t)(fi * 64 + lane) * 8) = __builtin_shufflevector(ak[m][jj], ak[m][jj], 0, 1, 2, 3);
-      *reinterpret_cast<bf16x4*>(base + 8192 + (size_t)(fi * 64 + lane) * 8) =
+      *reinterpret_cast<bf16x4*>(base + (size_t)(fi * 64 + kimg_swizzle(lane)) * 8) =
+          __builtin_shufflevector(ak[m][jj], ak[m][jj], 0, 1, 2, 3);
+      *reinterpret_cast<bf16x4*>(base + 8192 + (size_t)(fi * 64 + kimg_swizzle(lane)) * 8) =
           __builtin_shufflevector(ak[m][jj], ak[m][jj], 4, 5, 6, 7);
     }
 }
@@ -141,7 +142,8 @@ __device__ __forceinline__ PrecBF16::frag kt_frag<PrecBF16>(const PrecBF16::frag
   // ds_read_b64_tr_b16: in each 16-lane group, output lane i slot v = element (i & 3) of the 8-byte run
   // addressed by lane 4v + (i >> 2).  Source lane (group g, j = l & 15) addresses the 4 features
   // 16tl + 4(j & 3) .. +3 of chunk row c = 32jb + 16 half + 4g + (j >> 2); in X-fragment order that run
-  // is half (tl & 1) of fragment (c >> 4, tl >> 1), lane (c & 15) + 16 (j & 3), i.e. plane (tl & 1).
+  // is half (tl & 1) of fragment (c >> 4, tl >> 1), lane (c & 15) + 16 (j & 3), i.e. plane (tl & 1), at
+  // that lane's swizzled slot.
   // The two 4-element halves are combined as whole vectors: building the fragment element by element
   // through scalar bf16 bit casts was miscompiled (every slot took element 0).
   typedef __attribute__((ext_vector_type(4))) short s16x4;
@@ -152,7 +154,7 @@ __device__ __forceinline__ PrecBF16::frag kt_frag<PrecBF16>(const PrecBF16::frag
 #pragma unroll
   for (int half = 0; half < 2; ++half) {
     const int c = 32 * jb + 16 * half + 4 * g + (j >> 2);
-    const unsigned char* a = plane + (size_t)(((c >> 4) * 4 + (tl >> 1)) * 64 + (c & 15) + 16 * (j & 3)) * 8;
+    const unsigned char* a = plane + (size_t)(((c >> 4) * 4 + (tl >> 1)) * 64 + kimg_swizzle((c & 15) + 16 * (j & 3))) * 8;
     part[half] = __builtin_bit_cast(bf16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(a)));
   }
   return __builtin_shufflevector(part[0], part[1], 0, 1, 2, 3, 4, 5, 6, 7);
@@ -379,7 +381,7 @@ __global__ void __launch_bounds__(256) state_kernel(ScanParams p) {
 // issued after barrier D of chunk c-1, and the loader waits for it before barrier D of chunk c.
 __device__ __forceinline__ PrecBF16::frag kimg_frag(const unsigned char* kw, int lane, int m, int jj) {
   typedef __attribute__((ext_vector_type(4))) __bf16 bf16x4;
-  const unsigned char* a = kw + (size_t)((m * 4 + jj) * 64 + lane) * 8;
+  const unsigned char* a = kw + (size_t)((m * 4 + jj) * 64 + kimg_swizzle(lane)) * 8;
   const bf16x4 lo = *reinterpret_cast<const bf16x4*>(a);
   const bf16x4 hi = *reinterpret_cast<const bf16x4*>(a + KIMG_PLANE);
   return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);

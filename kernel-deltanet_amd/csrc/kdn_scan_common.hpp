@@ -32,15 +32,20 @@ struct WsLayout {
 // bf16, D = 512: the K area of a record holds the chunk's lifted keys as the exact LDS image that the
 // state kernel streams into its ring with global_load_lds (1 KB per instruction, copied verbatim): four
 // slices of 16 KB, slice s for the state wave that owns features [128s, 128s + 128); inside a slice,
-// plane h (8 KB) holds bytes [8h, 8h + 8) of each lane's 16-byte fragment slot at (fi * 64 + lane) * 8,
-// fi = 4 m + jj for token tile m and the slice's 32-feature block jj.  The state kernel reads a fragment
-// back with one ds_read2st64_b64 and K^T from the same planes with ds_read_b64_tr_b16; each half-fragment
-// is 512 contiguous bytes (no bank conflicts).
+// plane h (8 KB) holds bytes [8h, 8h + 8) of each lane's 16-byte fragment slot at
+// (fi * 64 + kimg_swizzle(lane)) * 8, fi = 4 m + jj for token tile m and the slice's 32-feature block jj.
+// The state kernel reads a fragment back with one ds_read2st64_b64 and K^T from the same planes with
+// ds_read_b64_tr_b16.  The swizzle (bits 2-3 of the 8-byte slot index XORed with bits 4-5) makes both
+// conflict-free: a 16-lane group of the plain read covers slots 16k .. 16k + 15 and one of the
+// transposed read slots {4g + q + 16r}; after the swizzle each group's 16 slots differ modulo 16, i.e.
+// fall on distinct bank pairs.  Without it the transposed read conflicts two ways (measured with
+// SQ_LDS_BANK_CONFLICT on a probe of both layouts: half its busy LDS cycles, none after the swizzle).
+__device__ __forceinline__ constexpr int kimg_swizzle(int s) { return s ^ (((s >> 4) & 3) << 2); }
 constexpr int KIMG_SLICE = 16384;
 constexpr int KIMG_PLANE = 8192;
 __device__ __forceinline__ void store_k_image(unsigned char* kimg, int m, int j, int lane, const bf16x8& f) {
   typedef __attribute__((ext_vector_type(4))) __bf16 bf16x4;
-  unsigned char* base = kimg + (size_t)(j >> 2) * KIMG_SLICE + (size_t)((m * 4 + (j & 3)) * 64 + lane) * 8;
+  unsigned char* base = kimg + (size_t)(j >> 2) * KIMG_SLICE + (size_t)((m * 4 + (j & 3)) * 64 + kimg_swizzle(lane)) * 8;
   __builtin_nontemporal_store(__builtin_shufflevector(f, f, 0, 1, 2, 3), reinterpret_cast<bf16x4*>(base));
   __builtin_nontemporal_store(__builtin_shufflevector(f, f, 4, 5, 6, 7), reinterpret_cast<bf16x4*>(base + KIMG_PLANE));
 }

@@ -79,53 +79,120 @@ __global__ void __launch_bounds__(1024) ragged_split_kernel(const int64_t* __res
 }
 
 // ---- runs of a slot map (kdn_slot_step) -------------------------------------------------------------
-// One workgroup: thread t counts the run starts (token 0, or a slot other than the previous token's) in its
-// contiguous range of tokens, an inclusive scan over the 1024 counts gives each range its first run
-// index, and the starts are written in token order: cu[r] = first token of run r, slot[r] = its slot.
+// Two passes over blocks of `span` tokens (a multiple of RUN_TILE; at most RUN_BLOCKS_MAX blocks): a run
+// starts at token 0 and wherever a token's slot differs from the previous token's.
+//   slot_count_kernel: block b counts the run starts among its tokens (coalesced loads) -> cnt[b];
+//   slot_runs_kernel:  block b takes its first run index from the counts of the blocks before it, then
+//     writes its runs in token order, RUN_TILE tokens per pass (thread t owns 8 consecutive tokens, an
+//     exclusive scan over the workgroup orders them): cu[r] = first token of run r, slot[r] = its slot.
 // Entries from the number of runs to `cap` get cu = n (no tokens) and slot -1.  More runs than `cap` (a
 // map whose distinct runs do not have distinct slots) mark every run skipped and set *status to 1.
-__global__ void __launch_bounds__(1024) slot_runs_kernel(const void* __restrict__ sm, int slot_bytes, int64_t n,
-                                                         int64_t cap, int64_t* __restrict__ cu, int32_t* __restrict__ slot,
-                                                         int32_t* __restrict__ status) {
-  __shared__ int64_t s_c[1024];
-  __shared__ int64_t s_total;
+constexpr int RUN_THREADS = 256, RUN_PER_THREAD = 8, RUN_TILE = RUN_THREADS * RUN_PER_THREAD;
+constexpr int64_t RUN_BLOCKS_MAX = 1024;
+
+struct RunGrid {
+  int64_t span, blocks;
+};
+static RunGrid run_grid(int64_t n) {
+  const int64_t tiles = (n + RUN_TILE - 1) / RUN_TILE;
+  const int64_t per = (tiles + RUN_BLOCKS_MAX - 1) / RUN_BLOCKS_MAX;
+  RunGrid g;
+  g.span = (per > 0 ? per : 1) * RUN_TILE;
+  g.blocks = n > 0 ? (n + g.span - 1) / g.span : 1;
+  return g;
+}
+
+__device__ __forceinline__ int64_t slot_at(const void* sm, int slot_bytes, int64_t i) {
+  return slot_bytes == 8 ? reinterpret_cast<const int64_t*>(sm)[i] : (int64_t)reinterpret_cast<const int32_t*>(sm)[i];
+}
+
+// Sum over the workgroup (256 threads); every thread gets the result.
+__device__ __forceinline__ int64_t run_block_sum(int64_t v, int64_t* s_w) {
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
   const int t = threadIdx.x;
-  auto at = [&](int64_t i) -> int64_t {
-    return slot_bytes == 8 ? reinterpret_cast<const int64_t*>(sm)[i] : (int64_t)reinterpret_cast<const int32_t*>(sm)[i];
-  };
-  const int64_t per = (n + 1023) / 1024;
-  const int64_t i0 = t * per < n ? t * per : n, i1 = (i0 + per < n) ? i0 + per : n;
-  int64_t cnt = 0;
-  for (int64_t i = i0; i < i1; ++i) cnt += (i == 0 || at(i) != at(i - 1));
-  s_c[t] = cnt;
   __syncthreads();
-  for (int off = 1; off < 1024; off <<= 1) {
-    const int64_t a = t >= off ? s_c[t - off] : 0;
-    __syncthreads();
-    s_c[t] += a;
-    __syncthreads();
+  if ((t & 63) == 0) s_w[t >> 6] = v;
+  __syncthreads();
+  return s_w[0] + s_w[1] + s_w[2] + s_w[3];
+}
+
+__global__ void __launch_bounds__(RUN_THREADS) slot_count_kernel(const void* __restrict__ sm, int slot_bytes, int64_t n,
+                                                                 int64_t span, int64_t* __restrict__ cnt) {
+  __shared__ int64_t s_w[4];
+  const int64_t lo = (int64_t)blockIdx.x * span, hi = lo + span < n ? lo + span : n;
+  int64_t c = 0;
+  for (int64_t i = lo + threadIdx.x; i < hi; i += RUN_THREADS)
+    c += (i == 0 || slot_at(sm, slot_bytes, i) != slot_at(sm, slot_bytes, i - 1));
+  c = run_block_sum(c, s_w);
+  if (threadIdx.x == 0) cnt[blockIdx.x] = c;
+}
+
+__global__ void __launch_bounds__(RUN_THREADS) slot_runs_kernel(const void* __restrict__ sm, int slot_bytes, int64_t n,
+                                                                int64_t span, int64_t nblocks,
+                                                                const int64_t* __restrict__ cnt, int64_t cap,
+                                                                int64_t* __restrict__ cu, int32_t* __restrict__ slot,
+                                                                int32_t* __restrict__ status) {
+  __shared__ int64_t s_w[4];
+  __shared__ int s_scan[4];
+  const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
+  int64_t pre = 0, tot = 0;
+  for (int64_t g = t; g < nblocks; g += RUN_THREADS) {
+    const int64_t v = cnt[g];
+    tot += v;
+    pre += g < (int64_t)blockIdx.x ? v : 0;
   }
-  if (t == 1023) s_total = s_c[1023];
-  __syncthreads();
-  const int64_t total = s_total;
-  const bool over = total > cap;
-  int64_t r = s_c[t] - cnt;
-  for (int64_t i = i0; i < i1; ++i) {
-    if (i == 0 || at(i) != at(i - 1)) {
-      if (r < cap) {
-        cu[r] = i;
-        const int64_t sv = at(i);
-        slot[r] = (over || sv < 0 || sv > 0x7fffffff) ? -1 : (int32_t)sv;
-      }
-      ++r;
+  pre = run_block_sum(pre, s_w);
+  tot = run_block_sum(tot, s_w);
+  const bool over = tot > cap;
+  const int64_t lo = (int64_t)blockIdx.x * span, hi = lo + span < n ? lo + span : n;
+  int64_t r0 = pre;
+  for (int64_t base = lo; base < hi; base += RUN_TILE) {
+    const int64_t i0 = base + (int64_t)RUN_PER_THREAD * t;
+    int64_t v[RUN_PER_THREAD + 1];
+#pragma unroll
+    for (int k = 0; k <= RUN_PER_THREAD; ++k) {
+      const int64_t i = i0 - 1 + k;
+      v[k] = (i >= 0 && i < hi) ? slot_at(sm, slot_bytes, i) : 0;
     }
+    int c = 0;
+#pragma unroll
+    for (int k = 1; k <= RUN_PER_THREAD; ++k) {
+      const int64_t i = i0 - 1 + k;
+      c += (i < hi && (i == 0 || v[k] != v[k - 1])) ? 1 : 0;
+    }
+    // exclusive scan of c over the workgroup
+    int inc = c;
+    for (int o = 1; o < 64; o <<= 1) {
+      const int u = __shfl_up(inc, o);
+      if (lane >= o) inc += u;
+    }
+    __syncthreads();
+    if (lane == 63) s_scan[wv] = inc;
+    __syncthreads();
+    int wbase = 0;
+    for (int q = 0; q < wv; ++q) wbase += s_scan[q];
+    const int tile_total = s_scan[0] + s_scan[1] + s_scan[2] + s_scan[3];
+    int64_t r = r0 + wbase + inc - c;
+#pragma unroll
+    for (int k = 1; k <= RUN_PER_THREAD; ++k) {
+      const int64_t i = i0 - 1 + k;
+      if (i < hi && (i == 0 || v[k] != v[k - 1])) {
+        if (r < cap) {
+          cu[r] = i;
+          const int64_t sv = v[k];
+          slot[r] = (over || sv < 0 || sv > 0x7fffffff) ? -1 : (int32_t)sv;
+        }
+        ++r;
+      }
+    }
+    r0 += tile_total;
   }
-  const int64_t used = over ? cap : total;
-  for (int64_t k = used + t; k < cap; k += 1024) {
+  const int64_t used = over ? cap : tot;
+  for (int64_t k = used + (int64_t)blockIdx.x * RUN_THREADS + t; k < cap; k += nblocks * RUN_THREADS) {
     cu[k] = n;
     slot[k] = -1;
   }
-  if (t == 0) {
+  if (blockIdx.x == 0 && t == 0) {
     cu[cap] = n;
     if (status) *status = over ? 1 : 0;
   }
@@ -134,7 +201,8 @@ __global__ void __launch_bounds__(1024) slot_runs_kernel(const void* __restrict_
 // The packed slot layout of the prefill list (ragged_split_kernel's pre_lo / pre_hi, `cap` entries):
 // entry i takes ceil(len / 64) chunk slots and one spare when it has tokens, none otherwise; off[i] is the
 // exclusive prefix of those counts (off[cap] = *total) and first[w] the entry holding slot w * win (for
-// windows past the total, the last entry).  One workgroup, the scan as in slot_runs_kernel.
+// windows past the total, the last entry).  One workgroup: thread t sums a contiguous range of entries and
+// an inclusive scan over the 1024 sums gives each range its offset.
 __global__ void __launch_bounds__(1024) flat_plan_kernel(const int64_t* __restrict__ lo, const int64_t* __restrict__ hi,
                                                          int64_t cap, int64_t win, int64_t nwin, int64_t* __restrict__ off,
                                                          int64_t* __restrict__ first, int64_t* __restrict__ total) {
@@ -516,7 +584,8 @@ static int slot_plan(const kdn_slot_step_args* a, SlotPlan& pl) {
   pl.nwin = pl.n_pre > 0 ? (g + pl.win - 1) / pl.win : 0;
   pl.seq_bound = pl.win / 2 + 1 < pl.cap ? pl.win / 2 + 1 : pl.cap;
   const size_t c = (size_t)pl.cap;
-  pl.small_bytes = round256((c + 1) * 8) + round256(c * 4)                       // runs
+  pl.small_bytes = round256((size_t)run_grid(n).blocks * 8)                      // run counts per block
+                 + round256((c + 1) * 8) + round256(c * 4)                       // runs
                  + 3 * round256(c * 8) + 2 * round256(c * 4)                      // decode / prefill lists
                  + round256((c + 1) * 8) + round256(8) + round256((size_t)(pl.nwin > 0 ? pl.nwin : 1) * 8);  // layout
   pl.buf_bytes = 0;
@@ -550,7 +619,9 @@ extern "C" int kdn_slot_step(const kdn_slot_step_args* a, void* stream, void* au
   if (a->workspace_bytes < pl.total) return KDN_ERR_WORKSPACE_TOO_SMALL;
   const hipStream_t st = as_stream(stream);
   const size_t c = (size_t)pl.cap;
+  const RunGrid rg = run_grid(a->num_tokens);
   unsigned char* w = (unsigned char*)a->workspace;
+  int64_t* rcnt = (int64_t*)w;      w += round256((size_t)rg.blocks * 8);
   int64_t* cu = (int64_t*)w;        w += round256((c + 1) * 8);
   int32_t* rslot = (int32_t*)w;     w += round256(c * 4);
   int64_t* dec_row = (int64_t*)w;   w += round256(c * 8);
@@ -561,8 +632,10 @@ extern "C" int kdn_slot_step(const kdn_slot_step_args* a, void* stream, void* au
   int64_t* fl_off = (int64_t*)w;    w += round256((c + 1) * 8);
   int64_t* fl_total = (int64_t*)w;  w += round256(8);
   int64_t* fl_first = (int64_t*)w;  w += round256((size_t)(pl.nwin > 0 ? pl.nwin : 1) * 8);
-  hipLaunchKernelGGL(slot_runs_kernel, dim3(1), dim3(1024), 0, st, a->slot_mapping, a->slot_bytes, a->num_tokens,
-                     pl.cap, cu, rslot, a->status);
+  hipLaunchKernelGGL(slot_count_kernel, dim3((unsigned)rg.blocks), dim3(RUN_THREADS), 0, st, a->slot_mapping,
+                     a->slot_bytes, a->num_tokens, rg.span, rcnt);
+  hipLaunchKernelGGL(slot_runs_kernel, dim3((unsigned)rg.blocks), dim3(RUN_THREADS), 0, st, a->slot_mapping,
+                     a->slot_bytes, a->num_tokens, rg.span, rg.blocks, (const int64_t*)rcnt, pl.cap, cu, rslot, a->status);
   hipLaunchKernelGGL(ragged_split_kernel, dim3(1), dim3(1024), 0, st, (const int64_t*)cu, (const int32_t*)rslot,
                      pl.cap, a->num_slots, dec_row, dec_slot, pre_lo, pre_hi, pre_slot);
   rc = launch_status();

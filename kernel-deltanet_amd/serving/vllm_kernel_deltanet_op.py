@@ -1,5 +1,6 @@
 """Serving operators -- the reference's op names (serving/vllm_kernel_deltanet_op.cpp:11-58, pybind names
-hybrid_recurrent_forward / fork_recurrent_state), implemented on kdn_ragged_step.
+hybrid_recurrent_forward / fork_recurrent_state), implemented on kdn_slot_step (slot map alone) and
+kdn_ragged_step (host offsets).
 
 hybrid_recurrent_forward(query, key, value, beta, decay, recurrent_states, slot_mapping, output)
   query, key [num_tokens, H, d_k], value [num_tokens, H, d_v], beta, decay [num_tokens, H],

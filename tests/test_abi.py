@@ -338,16 +338,18 @@ def test_factored_lift_backward_errors_need_no_device(lib):
 def test_slot_step_workspace_and_errors_need_no_device(lib):
     # the serving step from a slot map: every size from num_tokens and num_slots.  1000 tokens, 10 slots:
     # at most 21 runs (and prefills), 16 + 2 * 21 = 58 packed slots: one window of 64; the small arrays
-    # (runs, lists, layout: 2560 bytes) and one window buffer of 2 heads x 65 records of 238,592 bytes
+    # (run counts of one 2048-token block, runs, lists, layout: 2816 bytes) and one window buffer of
+    # 2 heads x 65 records of 238,592 bytes
     a = N.SlotStepArgs()
     a.num_tokens, a.H, a.d_k, a.D, a.d_v = 1000, 2, 64, 512, 64
     a.in_dtype = a.out_dtype = N.KDN_DTYPE_BF16
     a.inv_tau, a.slot_bytes, a.num_slots = 0.35355339, 8, 10
-    assert lib.kdn_slot_step_workspace_bytes(ctypes.byref(a)) == 2560 + 2 * 65 * 238592
-    a.num_tokens = 1 << 20    # 16384 + 2 * 21 slots: windows of 1024 (the most), three buffers of 1025 records
-    assert lib.kdn_slot_step_workspace_bytes(ctypes.byref(a)) == 2560 + 3 * 2 * 1025 * 238592
+    assert lib.kdn_slot_step_workspace_bytes(ctypes.byref(a)) == 2816 + 2 * 65 * 238592
+    a.num_tokens = 1 << 20    # 16384 + 2 * 21 slots: windows of 1024 (the most), three buffers of 1025 records;
+    # 512 run-count blocks of 2048 tokens
+    assert lib.kdn_slot_step_workspace_bytes(ctypes.byref(a)) == 2560 + 512 * 8 + 3 * 2 * 1025 * 238592
     a.num_tokens = 1                          # one token: a decode at most, no prefill window
-    assert lib.kdn_slot_step_workspace_bytes(ctypes.byref(a)) == 10 * 256
+    assert lib.kdn_slot_step_workspace_bytes(ctypes.byref(a)) == 11 * 256
     a.num_tokens = 1000
     a.slot_bytes = 2
     assert lib.kdn_slot_step_workspace_bytes(ctypes.byref(a)) == 0
