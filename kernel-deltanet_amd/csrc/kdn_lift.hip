@@ -103,11 +103,19 @@ __global__ void __launch_bounds__((64 * LiftWaves<InT, OutT, D>::value)) lift_ke
   constexpr int NW = LiftWaves<InT, OutT, D>::value;
   constexpr int NSPLIT = XFrag<InT>::NSPLIT;
   __shared__ bf16x8 s_omega[NT * 2 * 64];    // [t][kb][lane] A fragments, D*64*2 bytes
-  __shared__ __attribute__((aligned(16))) float s_phase_rev[D];           // phase / (2 pi)
-  // Per-wave staging of 16 rows x 64 features of output, rows padded by 16 bytes.
+  // phase / (2 pi) per tile and lane: entry (t, l) holds the phases of the features 16t + 4(l >> 4) + 0..3
+  // that lane l's accumulator rows take, so that each tile's read is one 16-byte load per lane at its own
+  // address (reads of one shared 2 KB table, sixteen lanes to an address, were counted as bank conflicts:
+  // 128 cycles per 16-row tile)
+  __shared__ f32x4 s_phr[NT * 64];
+  // Per-wave staging of 16 rows x 128 bytes of output.  Chunk c (16 bytes) of row r sits at chunk position
+  // c ^ ((r >> 1) & 7) of the row: the accumulator stores (16 rows x 8 or 16 bytes per instruction) and
+  // the 16-byte row read-back (two whole rows per 16 lanes) both fall on distinct banks.  (Rows padded
+  // by 16 bytes instead: the read-back's two rows overlapped on one bank.)
   constexpr int TG = 128 / (16 * (int)sizeof(OutT));  // feature tiles per staged group: 128 bytes of a row
-  constexpr int SRS = 16 * TG * (int)sizeof(OutT) + 16;  // row stride in bytes
-  constexpr int SCPR = 16 * TG * (int)sizeof(OutT) / 16;  // 16-byte chunks per staged row
+  constexpr int SRS = 16 * TG * (int)sizeof(OutT);   // row stride in bytes (128)
+  constexpr int SCPR = 16 * TG * (int)sizeof(OutT) / 16;  // 16-byte chunks per staged row (8)
+  static_assert(SCPR == 8, "the staging swizzle assumes 8 chunks per row");
   __shared__ __attribute__((aligned(16))) unsigned char s_stage[NW][16 * SRS];
 
   const int lane = threadIdx.x & 63;
@@ -133,7 +141,13 @@ __global__ void __launch_bounds__((64 * LiftWaves<InT, OutT, D>::value)) lift_ke
       s_omega[idx] = *reinterpret_cast<const bf16x8*>(omega + (int64_t)(16 * t + (l & 15)) * 64 + 32 * kb + 8 * (l >> 4));
     }
   }
-  for (int f = threadIdx.x; f < D; f += 64 * NW) s_phase_rev[f] = phase[f] * 0.15915494309189535f;
+  for (int idx = threadIdx.x; idx < NT * 64; idx += 64 * NW) {
+    const int f0 = 16 * (idx >> 6) + 4 * ((idx & 63) >> 4);
+    f32x4 v;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = phase[f0 + i] * 0.15915494309189535f;
+    s_phr[idx] = v;
+  }
   __syncthreads();
 
   const float ang_scale = inv_tau * 0.15915494309189535f;  // radians -> revolutions folded in
@@ -194,19 +208,27 @@ __global__ void __launch_bounds__((64 * LiftWaves<InT, OutT, D>::value)) lift_ke
     split_frag<NSPLIT>(xv[1], xb[1]);
 
     // Feature tile t: acc = x . Omega[16t .. 16t+16)^T.  Software-pipelined: the MFMAs of tile t+1 are
-    // issued in the same scheduling region as the cosines of tile t.
+    // issued in the same scheduling region as the cosines of tile t, with their Omega fragments read one
+    // tile earlier still (the LDS read's latency covered by a tile's cosines).
+    bf16x8 om_next[2];
+    auto fetch = [&](int t) {
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) om_next[kb] = s_omega[(t * 2 + kb) * 64 + lane];
+    };
     auto project = [&](int t) {
+      const bf16x8 om_t[2] = {om_next[0], om_next[1]};
+      if (t + 1 < NT) fetch(t + 1);
       f32x4 acc = zero4();
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
-        const bf16x8 a = s_omega[(t * 2 + kb) * 64 + lane];
 #pragma unroll
-        for (int p = 0; p < NSPLIT; ++p) acc = PrecBF16::mma(acc, a, xb[kb][p]);
+        for (int p = 0; p < NSPLIT; ++p) acc = PrecBF16::mma(acc, om_t[kb], xb[kb][p]);
       }
       return acc;
     };
     float c[NT][4];
     float ss = 0.f;
+    fetch(0);
     f32x4 acc = project(0);
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
@@ -214,7 +236,7 @@ __global__ void __launch_bounds__((64 * LiftWaves<InT, OutT, D>::value)) lift_ke
       // would need 256 registers for them alone
       __builtin_amdgcn_sched_barrier(0);
       const f32x4 next = (t + 1 < NT) ? project(t + 1) : zero4();
-      const f32x4 ph = *reinterpret_cast<const f32x4*>(&s_phase_rev[16 * t + 4 * (lane >> 4)]);
+      const f32x4 ph = s_phr[t * 64 + lane];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const float cv = __builtin_amdgcn_cosf(__builtin_amdgcn_fractf(acc[i] * ang_scale + ph[i]));
@@ -236,15 +258,16 @@ __global__ void __launch_bounds__((64 * LiftWaves<InT, OutT, D>::value)) lift_ke
       for (int tp = 0; tp < TG; ++tp) {
         const int t = TG * g + tp;
         float v[4] = {c[t][0] * scale, c[t][1] * scale, c[t][2] * scale, c[t][3] * scale};
-        store4<OutT>(reinterpret_cast<OutT*>(stg + (lane & 15) * SRS) + 16 * tp + 4 * (lane >> 4), v);
+        const int r = lane & 15, byte = (int)sizeof(OutT) * (16 * tp + 4 * (lane >> 4));
+        store4<OutT>(reinterpret_cast<OutT*>(stg + r * SRS + 16 * ((byte >> 4) ^ ((r >> 1) & 7)) + (byte & 15)), v);
       }
       // The read-back below takes rows other lanes wrote, and the next group's stores overwrite rows
       // other lanes read.
       wave_lds_sync();
 #pragma unroll
       for (int j = 0; j < 16 * SCPR / 64; ++j) {
-        const int q = 64 * j + lane, r = q / SCPR, ch = q % SCPR;
-        const u32x4 val = *reinterpret_cast<const u32x4*>(stg + r * SRS + 16 * ch);
+        const int q = 64 * j + lane, r = q / SCPR, pos = q % SCPR, ch = pos ^ ((r >> 1) & 7);
+        const u32x4 val = *reinterpret_cast<const u32x4*>(stg + r * SRS + 16 * pos);
         const int64_t grow = tile * 16 + r;
         // streaming stores: the features are far larger than the caches, and their readers come later
         // (13 back-to-back config-2 lifts: 0.46 against 0.50 ms per launch once the clocks have settled)
@@ -515,9 +538,11 @@ __global__ void __launch_bounds__(512) lift_factored_kernel(const __bf16* __rest
                                                             const __bf16* __restrict__ om2, const float* __restrict__ ph2,
                                                             float inv_tau, OutT* __restrict__ out, int64_t os) {
   constexpr int D = 512, NT = D / 16;
+  // output staging as in lift_kernel (128-byte rows, chunk c of row r at position c ^ ((r >> 1) & 7))
   constexpr int TG = 128 / (16 * (int)sizeof(OutT));
-  constexpr int SRS = 16 * TG * (int)sizeof(OutT) + 16;
+  constexpr int SRS = 16 * TG * (int)sizeof(OutT);
   constexpr int SCPR = 16 * TG * (int)sizeof(OutT) / 16;
+  static_assert(SCPR == 8, "the staging swizzle assumes 8 chunks per row");
   __shared__ bf16x8 s_omega[2][NT * 2 * 64];
   __shared__ __attribute__((aligned(16))) float s_phase_rev[2][D];
   __shared__ __attribute__((aligned(16))) unsigned char s_stage[8][16 * SRS];
@@ -612,13 +637,14 @@ __global__ void __launch_bounds__(512) lift_factored_kernel(const __bf16* __rest
       for (int tp = 0; tp < TG; ++tp) {
         const int t = TG * g + tp;
         float v[4] = {c[t][0] * inv, c[t][1] * inv, c[t][2] * inv, c[t][3] * inv};
-        store4<OutT>(reinterpret_cast<OutT*>(stg + (lane & 15) * SRS) + 16 * tp + 4 * (lane >> 4), v);
+        const int r = lane & 15, byte = (int)sizeof(OutT) * (16 * tp + 4 * (lane >> 4));
+        store4<OutT>(reinterpret_cast<OutT*>(stg + r * SRS + 16 * ((byte >> 4) ^ ((r >> 1) & 7)) + (byte & 15)), v);
       }
       wave_lds_sync();
 #pragma unroll
       for (int j = 0; j < 16 * SCPR / 64; ++j) {
-        const int q = 64 * j + lane, r = q / SCPR, ch = q % SCPR;
-        const u32x4 val = *reinterpret_cast<const u32x4*>(stg + r * SRS + 16 * ch);
+        const int q = 64 * j + lane, r = q / SCPR, pos = q % SCPR, ch = pos ^ ((r >> 1) & 7);
+        const u32x4 val = *reinterpret_cast<const u32x4*>(stg + r * SRS + 16 * pos);
         const int64_t grow = tile * 16 + r;
         if (grow < rows)
           *reinterpret_cast<u32x4*>(reinterpret_cast<unsigned char*>(out + grow * os + D * h + 16 * TG * g) + 16 * ch) = val;

@@ -80,15 +80,30 @@ __device__ __forceinline__ void lift_tile(const RawRow<InT> (&raw)[NX], int norm
     ss[x] = 0.f;
   }
   // Feature tile t: acc[x] = x . Omega[16t .. 16t+16)^T.  Software-pipelined: the MFMAs of tile t+1 are
-  // issued in the scheduling region of the cosines of tile t.
+  // issued in the scheduling region of the cosines of tile t, with Omega's fragments for them read one
+  // tile earlier still (so that the read's latency is covered by a tile's cosines, not waited on by the
+  // MFMAs that follow it).
+  auto fetch = [&](int t, bf16x8 (&a)[2]) {
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      if constexpr (OMEGA_LDS) a[kb] = s_omega[(t * 2 + kb) * 64 + lane];
+      else a[kb] = *reinterpret_cast<const bf16x8*>(omega + (int64_t)(16 * t + (lane & 15)) * 64 + 32 * kb + 8 * (lane >> 4));
+    }
+  };
+  // tiles of Omega in flight ahead of the one projected (one; the exact projection reading Omega from L2
+  // three tiles ahead instead of staging it in LDS measured slower: config-3 prep 139 -> 150 us)
+  constexpr int PF = 1;
+  bf16x8 om_ring[PF][2];
   auto project = [&](int t, f32x4 (&acc)[NX]) {
+    bf16x8 om_t[2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) om_t[kb] = om_ring[t % PF][kb];
+    if (t + PF < NT) fetch(t + PF, om_ring[t % PF]);
 #pragma unroll
     for (int x = 0; x < NX; ++x) acc[x] = zero4();
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
-      bf16x8 a;
-      if constexpr (OMEGA_LDS) a = s_omega[(t * 2 + kb) * 64 + lane];
-      else a = *reinterpret_cast<const bf16x8*>(omega + (int64_t)(16 * t + (lane & 15)) * 64 + 32 * kb + 8 * (lane >> 4));
+      const bf16x8 a = om_t[kb];
 #pragma unroll
       for (int s = 0; s < NSPLIT; ++s)
 #pragma unroll
@@ -103,6 +118,8 @@ __device__ __forceinline__ void lift_tile(const RawRow<InT> (&raw)[NX], int norm
     }
   };
   f32x4 acc[NX];
+#pragma unroll
+  for (int t = 0; t < PF; ++t) fetch(t, om_ring[t]);
   project(0, acc);
 #pragma unroll
   for (int t = 0; t < NT; ++t) {

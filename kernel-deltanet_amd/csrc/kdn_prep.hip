@@ -91,16 +91,19 @@ __global__ void __launch_bounds__(256, (PrepWaves<P, FM>::value)) prep_kernel(Sc
   constexpr bool OMEGA_LDS = FM == FM_EXACT;
   constexpr size_t PHIK_BYTES = (size_t)4 * NJ * 64 * sizeof(frag);
   static_assert(!OMEGA_LDS || (size_t)NT * 2 * 64 * 16 <= PHIK_BYTES, "Omega does not fit the K-fragment area");
-  // After the Gram the K-fragment area is reused for A (16 KB), T (17 KB) and V.
-  static_assert(64 * 64 * 4 + 64 * 68 * 4 + 64 * DV * sizeof(InT) <= PHIK_BYTES, "LDS reuse does not fit");
+  // After the Gram the K-fragment area is reused for A (16 KB), T (16 KB) and V.  V rows are padded by
+  // four elements: the fragment reads below take rows 4 apart in the four lane groups, which then fall
+  // on disjoint banks (unpadded they hit the same banks, a four-way conflict on every read).
+  constexpr int DVP = DV + 4;
+  static_assert(64 * 64 * 4 + 64 * 64 * 4 + 64 * DVP * sizeof(InT) <= PHIK_BYTES, "LDS reuse does not fit");
   __shared__ __attribute__((aligned(16))) unsigned char smem[PHIK_BYTES];
   __shared__ __attribute__((aligned(16))) float s_beta[64], s_g[64], s_sq[64], s_sk[64], s_phrev[D];
 
   bf16x8* s_omega = reinterpret_cast<bf16x8*>(smem);                 // during the lift (OMEGA_LDS)
   frag* s_phik = reinterpret_cast<frag*>(smem);                       // from the lift to the Gram
-  float* s_A = reinterpret_cast<float*>(smem);                        // [j][p][s] = A[4s+p][j]
-  float* s_T = s_A + 64 * 64;                                          // [t][68]
-  InT* s_V = reinterpret_cast<InT*>(s_T + 64 * 68);                    // [t][DV]
+  float* s_A = reinterpret_cast<float*>(smem);                        // [j][p][s'] = A[4s+p][j] (s swizzled, a_swizzle)
+  float* s_T = s_A + 64 * 64;                                          // [t][64] (columns swizzled, t_swizzle)
+  InT* s_V = reinterpret_cast<InT*>(s_T + 64 * 64);                    // [t][DVP]
 
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -259,7 +262,7 @@ __global__ void __launch_bounds__(256, (PrepWaves<P, FM>::value)) prep_kernel(Sc
           const int j = 16 * m + 4 * (lane >> 4) + i;
           const float gj = s_g[j], skj = s_sk[j];
           const float a = (j < t) ? bt * __expf(fminf(gt - gj, 0.f)) * gkk[m][i] * skt * skj : 0.f;
-          s_A[(j * 4 + (t & 3)) * 16 + (t >> 2)] = a;
+          s_A[(j * 4 + (t & 3)) * 16 + a_swizzle(j, t >> 2)] = a;
           if constexpr (!NOQ) pt[m][i] = (j < t) ? __expf(fminf(gtm1 - gj, 0.f)) * gqk[m][i] * sqt * skj : 0.f;
         }
       }
@@ -272,7 +275,12 @@ __global__ void __launch_bounds__(256, (PrepWaves<P, FM>::value)) prep_kernel(Sc
 #pragma unroll
     for (int i = 0; i < In::VPT; ++i) {
       const int idx = (int)threadIdx.x + 256 * i;
-      if (idx < 64 * In::VPR) *reinterpret_cast<u32x4*>(s_V + (idx / In::VPR) * DV + (idx % In::VPR) * (16 / (int)sizeof(InT))) = vraw[i];
+      if (idx < 64 * In::VPR) {
+        // padded rows are 8-byte aligned: two 8-byte stores per 16-byte piece
+        u32x2* d = reinterpret_cast<u32x2*>(s_V + (idx / In::VPR) * DVP + (idx % In::VPR) * (16 / (int)sizeof(InT)));
+        d[0] = __builtin_shufflevector(vraw[i], vraw[i], 0, 1);
+        d[1] = __builtin_shufflevector(vraw[i], vraw[i], 2, 3);
+      }
     }
     if (w == 1) {
       float* vec = reinterpret_cast<float*>(ws + L::VEC);
@@ -285,7 +293,7 @@ __global__ void __launch_bounds__(256, (PrepWaves<P, FM>::value)) prep_kernel(Sc
     lds_barrier();
 
     // ---- T = (I + A)^{-1} (column-oriented substitution over lane quads)
-    unit_lower_inverse(s_A, s_T, 68, w, lane);
+    unit_lower_inverse<true>(s_A, s_T, 64, w, lane);
     lds_barrier();
 
     // ---- W~ factor T diag(beta e^g |phi_k|) fragments, and U~ = T diag(beta) V   (wave w: rows m = w)
@@ -295,12 +303,21 @@ __global__ void __launch_bounds__(256, (PrepWaves<P, FM>::value)) prep_kernel(Sc
 #pragma unroll
       for (int jb = 0; jb < 2; ++jb) {
         f32x8 tw;
+        // slots 4h .. 4h + 3 are the four consecutive columns j = 32jb + 16h + 4(lane >> 4) + 0..3
+        // (kappa), read as one 16-byte vector from each array (T's rows swizzled by t_swizzle: the 16
+        // rows of a lane group fall on distinct banks)
 #pragma unroll
-        for (int s = 0; s < 8; ++s) {
-          const int j = 32 * jb + kappa(lane, s);
-          const float tv = s_T[t * 68 + j];
-          tw[s] = p.linear ? 0.f : tv * s_beta[j] * __expf(s_g[j]) * s_sk[j];  // linear: E = U~
-          tb[jb][s] = tv * s_beta[j];
+        for (int hh = 0; hh < 2; ++hh) {
+          const int j0 = 32 * jb + 16 * hh + 4 * (lane >> 4);
+          const f32x4 tv = *reinterpret_cast<const f32x4*>(s_T + t * 64 + t_swizzle(t, j0));
+          const f32x4 be = *reinterpret_cast<const f32x4*>(s_beta + j0);
+          const f32x4 gj = *reinterpret_cast<const f32x4*>(s_g + j0);
+          const f32x4 sk = *reinterpret_cast<const f32x4*>(s_sk + j0);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            tw[4 * hh + i] = p.linear ? 0.f : tv[i] * be[i] * __expf(gj[i]) * sk[i];  // linear: E = U~
+            tb[jb][4 * hh + i] = tv[i] * be[i];
+          }
         }
         put(ws + L::Tp + (size_t)(w * 2 + jb) * 64 * L::FB, P::from_f32(tw));
       }
@@ -311,7 +328,7 @@ __global__ void __launch_bounds__(256, (PrepWaves<P, FM>::value)) prep_kernel(Sc
         for (int jb = 0; jb < 2; ++jb) {
           f32x8 vv;
 #pragma unroll
-          for (int s = 0; s < 8; ++s) vv[s] = (float)s_V[(32 * jb + kappa(lane, s)) * DV + 16 * n + (lane & 15)];
+          for (int s = 0; s < 8; ++s) vv[s] = (float)s_V[(32 * jb + kappa(lane, s)) * DVP + 16 * n + (lane & 15)];
           if constexpr (IsBF16<P>::value) {
             // hi + lo split of T diag(beta): V is exact in bf16, so U~ keeps ~16 bits.
             bf16x8 hi, lo, vb;

@@ -74,8 +74,19 @@ __device__ __forceinline__ f32x4 mm(f32x4 acc, const f32x8& a, const f32x8& b) {
 // on the sequential chain.  acc[s] = -(partial T[4s+pq][col]); A is zero on and above its diagonal, so
 // updating every slot from i >> 2 on leaves rows r <= i unchanged.  The columns of A are loaded three
 // rows ahead.
-//   At: A transposed in LDS, At[(j * 4 + p) * 16 + s] = A[4s + p][j] (16-byte aligned)
-//   T:  output rows, T[r * ldt + c] (LDS)
+//   At: A transposed in LDS, At[(j * 4 + p) * 16 + s] = A[4s + p][j] (16-byte aligned); with SWZ the
+//       16-byte groups of a row are permuted, At[(j * 4 + p) * 16 + a_swizzle(j, s)] = A[4s + p][j]
+//   T:  output rows, T[r * ldt + c] (LDS); with SWZ T[r * ldt + t_swizzle(r, c)] and ldt = 64
+// a_swizzle lets a writer that stores one element per lane, lane groups g = 0..3 taking columns
+// j = 4g + const and the lanes of a group s = 4w + 0..3 (p = 0..3), hit 64 distinct banks (unswizzled,
+// the four groups' stores collide on the same 16 banks).
+__device__ __forceinline__ int a_swizzle(int j, int s) { return 4 * ((s >> 2) ^ ((j >> 2) & 3)) + (s & 3); }
+// t_swizzle permutes the 16-byte groups of a row of T (ldt = 64) so that both the substitution's stores
+// (rows 4s + 0..3, columns 16w + 0..15 per instruction) and 16-byte reads of four consecutive columns
+// of rows r0 .. r0 + 15 fall on distinct banks.
+__device__ __forceinline__ int t_swizzle(int r, int c) { return c ^ (16 * (r & 3)) ^ (4 * ((r >> 2) & 3)); }
+
+template <bool SWZ = false>
 __device__ __forceinline__ void unit_lower_inverse(const float* At, float* T, int ldt, int w, int lane) {
   const int col = 16 * w + (lane >> 2), pq = lane & 3;
   float acc[16];
@@ -87,7 +98,7 @@ __device__ __forceinline__ void unit_lower_inverse(const float* At, float* T, in
     const f32x4* src = reinterpret_cast<const f32x4*>(At + (i * 4 + pq) * 16);
 #pragma unroll
     for (int q = 0; q < 4; ++q)
-      if (q >= (i >> 4)) dst[q] = src[q];
+      if (q >= (i >> 4)) dst[q] = src[SWZ ? (q ^ ((i >> 2) & 3)) : q];
   };
 #pragma unroll
   for (int i = 0; i < AHEAD; ++i) load_col(i, acol[i]);
@@ -106,7 +117,7 @@ __device__ __forceinline__ void unit_lower_inverse(const float* At, float* T, in
     if (i + AHEAD < 63) load_col(i + AHEAD, acol[i % AHEAD]);
   }
 #pragma unroll
-  for (int s2 = 0; s2 < 16; ++s2) T[(4 * s2 + pq) * ldt + col] = -acc[s2];
+  for (int s2 = 0; s2 < 16; ++s2) T[(4 * s2 + pq) * ldt + (SWZ ? t_swizzle(4 * s2 + pq, col) : col)] = -acc[s2];
 }
 
 // Sum over the 16 lanes sharing (lane >> 4) (one tile row) / over the 4 lane groups (one tile column).
