@@ -1443,11 +1443,7 @@ extern "C" size_t kdn_scan_bwd_workspace_bytes(const kdn_scan_bwd_args* a) {
 }
 
 extern "C" int64_t kdn_scan_bwd_segments(const kdn_scan_bwd_args* a, int64_t* segment_chunks) {
-  if (a && general_bwd_applies(a->fwd)) {  // one segment: every chunk
-    if (general_bwd_workspace_bytes(a) == 0) return 0;
-    if (segment_chunks) *segment_chunks = bwd_chunks(a->fwd);
-    return 1;
-  }
+  if (a && general_bwd_applies(a->fwd)) return general_bwd_segments(a, segment_chunks);
   if (a && a->fwd && frep_applies(a->fwd)) return frep::segments(a, segment_chunks);
   if (a && vsplit::applies(a->fwd)) return vsplit::segments(a, segment_chunks);
   if (bwd_check(a) != KDN_OK) return 0;

@@ -1033,10 +1033,54 @@ static int launch_bwd(const Params& p, const BwdP& g, hipStream_t st) {
   return launch_status();
 }
 
+// The checkpoint pass of a segmented backward: the recompute and the forward carry of one segment, which
+// writes the state at the segment's end to p.fin.
+template <class PB, typename InT, int D, int DV>
+static int launch_ckpt(const Params& p, hipStream_t st) {
+  const dim3 chunk_grid((unsigned)p.nch, (unsigned)p.H, (unsigned)p.B);
+  const unsigned carry_wgs = (unsigned)(((p.B * p.H + 7) / 8) * 8 * (DV / 16));
+  hipLaunchKernelGGL((gen_prep_kernel<PB, InT, D, DV, true>), chunk_grid, dim3(256), 0, st, p);
+  hipLaunchKernelGGL((gen_carry_kernel<PB, D, DV, true>), dim3(carry_wgs), dim3(256), 0, st, p);
+  return launch_status();
+}
+
 static size_t bwd_record_floats(int D, int DV) {
   if (D == 1024 && DV == 64) return BRec<1024, 64>::floats;
   if (D == 1024 && DV == 128) return BRec<1024, 128>::floats;
   return 0;
+}
+
+// Segments of the backward: fwd->segment_chunks when positive, else the largest power of two from 4 to 256
+// chunks whose records fit 12 GiB; at most the sequence's chunks.  Workspace: one segment's records, one
+// fp32 [B][H][1024][d_v] state per segment boundary (the checkpoints), the carried dL/dS (with more than
+// one segment) and the forward carry's final state (scratch).
+constexpr size_t BWD_SEGMENT_BUDGET = (size_t)12 << 30;
+struct BwdPlan {
+  int64_t nch, seg, nsegs;
+  size_t rec_bytes, state_bytes, ckpt_off, carry_off, fin_off, total;
+};
+static BwdPlan bwd_plan(const kdn_scan_args* f) {
+  BwdPlan L;
+  L.nch = (f->T + C - 1) / C;
+  const int64_t heads = f->B * f->H;
+  const size_t per_chunk = (size_t)heads * bwd_record_floats((int)f->D, (int)f->d_v) * sizeof(float);
+  int64_t seg = 4;
+  if (f->segment_chunks > 0) {
+    seg = f->segment_chunks;
+  } else {
+    const size_t fit = BWD_SEGMENT_BUDGET / per_chunk;
+    while (seg < 256 && (size_t)(2 * seg) <= fit) seg *= 2;
+  }
+  if (seg > L.nch) seg = L.nch;
+  L.seg = seg;
+  L.nsegs = (L.nch + seg - 1) / seg;
+  L.rec_bytes = (size_t)seg * per_chunk;
+  L.state_bytes = (size_t)heads * (size_t)f->D * (size_t)f->d_v * sizeof(float);
+  L.ckpt_off = L.rec_bytes;
+  L.carry_off = L.ckpt_off + (size_t)(L.nsegs - 1) * L.state_bytes;
+  L.fin_off = L.carry_off + (L.nsegs > 1 ? L.state_bytes : 0);
+  L.total = L.fin_off + L.state_bytes;
+  return L;
 }
 
 }  // namespace gen
@@ -1112,14 +1156,80 @@ static int general_bwd_check(const kdn_scan_bwd_args* a) {
   return KDN_OK;
 }
 
-// One record per (batch, head, chunk) for the whole sequence, then the forward carry's final state
-// (scratch: the backward does not return it).
 size_t general_bwd_workspace_bytes(const kdn_scan_bwd_args* a) {
   if (general_bwd_check(a) != KDN_OK) return 0;
-  const kdn_scan_args* f = a->fwd;
-  const int64_t nch = (f->T + gen::C - 1) / gen::C;
-  return ((size_t)(f->B * f->H * nch) * gen::bwd_record_floats((int)f->D, (int)f->d_v) +
-          (size_t)(f->B * f->H) * (size_t)f->D * (size_t)f->d_v) * sizeof(float);
+  return gen::bwd_plan(a->fwd).total;
+}
+
+int64_t general_bwd_segments(const kdn_scan_bwd_args* a, int64_t* segment_chunks) {
+  if (general_bwd_check(a) != KDN_OK) return 0;
+  const gen::BwdPlan L = gen::bwd_plan(a->fwd);
+  if (segment_chunks) *segment_chunks = L.seg;
+  return L.nsegs;
+}
+
+// Segmented like the D = 512 backward: a checkpoint pass runs the recompute and the forward carry over
+// segments 0 .. n-2 and keeps the state at each segment start; then each segment, last first, recomputes
+// its chunks from its checkpoint, carries dL/dS back from the next segment (in place in one buffer: every
+// workgroup of the reverse carry reads its slice before it writes it) and writes its gradients.  A segment
+// is the chunk range [c0, c0 + n) as a sequence of its own (input and gradient pointers advanced by 64 c0
+// tokens); the kernels carry the same sums in the same order as over the whole sequence, so the results
+// do not depend on the segment length.
+template <class PB, typename InT, int D, int DV>
+static int general_bwd_run(const gen::Params& p, const gen::BwdP& g, const gen::BwdPlan& L, size_t isz,
+                           hipStream_t st) {
+  unsigned char* ws = reinterpret_cast<unsigned char*>(p.ws);
+  const int64_t ss0 = p.H * D * DV, ss1 = (int64_t)D * DV, ss2 = DV, ss3 = 1;  // checkpoint / carry layout
+  auto state_at = [&](size_t off) { return reinterpret_cast<float*>(ws + off); };
+  auto segment = [&](int64_t s, gen::Params& ps, gen::BwdP& gs) {
+    const int64_t c0 = s * L.seg, n = (L.nch - c0 < L.seg) ? L.nch - c0 : L.seg, t0 = c0 * gen::C;
+    ps = p;
+    gs = g;
+    ps.nch = n;
+    ps.T = (p.T - t0 < n * gen::C) ? p.T - t0 : n * gen::C;
+    ps.q = static_cast<const unsigned char*>(p.q) + (size_t)(t0 * p.qs1) * isz;
+    ps.k = static_cast<const unsigned char*>(p.k) + (size_t)(t0 * p.ks1) * isz;
+    ps.v = static_cast<const unsigned char*>(p.v) + (size_t)(t0 * p.vs1) * isz;
+    ps.beta = p.beta + t0 * p.bs1;
+    if (p.decay) ps.decay = p.decay + t0 * p.ds1;
+    gs.dy = g.dy + t0 * g.ys1;
+    gs.dq = g.dq + t0 * g.dqs1;
+    gs.dk = g.dk + t0 * g.dks1;
+    gs.dv = g.dv + t0 * g.dvs1;
+    gs.dbeta = g.dbeta + t0 * g.dbs1;
+    if (g.ddecay) gs.ddecay = g.ddecay + t0 * g.dds1;
+    if (s > 0) {  // the state at the segment start: the checkpoint of segment s - 1's end
+      ps.init = state_at(L.ckpt_off + (size_t)(s - 1) * L.state_bytes);
+      ps.is0 = ss0; ps.is1 = ss1; ps.is2 = ss2; ps.is3 = ss3;
+    }
+  };
+  for (int64_t s = 0; s + 1 < L.nsegs; ++s) {
+    gen::Params ps;
+    gen::BwdP gs;
+    segment(s, ps, gs);
+    ps.fin = state_at(L.ckpt_off + (size_t)s * L.state_bytes);
+    ps.fs0 = ss0; ps.fs1 = ss1; ps.fs2 = ss2; ps.fs3 = ss3;
+    const int rc = gen::launch_ckpt<PB, InT, D, DV>(ps, st);
+    if (rc != KDN_OK) return rc;
+  }
+  for (int64_t s = L.nsegs - 1; s >= 0; --s) {
+    gen::Params ps;
+    gen::BwdP gs;
+    segment(s, ps, gs);
+    ps.fin = state_at(L.fin_off);
+    ps.fs0 = ss0; ps.fs1 = ss1; ps.fs2 = ss2; ps.fs3 = ss3;
+    if (s + 1 < L.nsegs) {  // dL/dS at the segment end, left by the next segment's reverse carry
+      gs.dfin = state_at(L.carry_off);
+      gs.fs0 = ss0; gs.fs1 = ss1; gs.fs2 = ss2; gs.fs3 = ss3;
+    }
+    if (s > 0) {  // dL/dS at the segment start, for the previous segment
+      gs.dinit = state_at(L.carry_off);
+      gs.gis0 = ss0; gs.gis1 = ss1; gs.gis2 = ss2; gs.gis3 = ss3;
+    }
+    const int rc = gen::launch_bwd<PB, InT, D, DV>(ps, gs, st);
+    if (rc != KDN_OK) return rc;
+  }
+  return KDN_OK;
 }
 
 int general_bwd(const kdn_scan_bwd_args* a, void* stream) {
@@ -1127,9 +1237,11 @@ int general_bwd(const kdn_scan_bwd_args* a, void* stream) {
   if (rc != KDN_OK) return rc;
   if (a->workspace_bytes < general_bwd_workspace_bytes(a)) return KDN_ERR_WORKSPACE_TOO_SMALL;
   if (!a->workspace) return KDN_ERR_INVALID_ARGUMENT;
+  if (!aligned(a->workspace, 256)) return KDN_ERR_MISALIGNED;
   const kdn_scan_args* f = a->fwd;
+  const gen::BwdPlan L = gen::bwd_plan(f);
   gen::Params p = {};
-  p.B = f->B; p.T = f->T; p.H = f->H; p.nch = (f->T + gen::C - 1) / gen::C;
+  p.B = f->B; p.T = f->T; p.H = f->H; p.nch = L.nch;
   if (p.nch > 0x7fffffff) return KDN_ERR_UNSUPPORTED;
   p.q = f->q; p.qs0 = f->q_stride[0]; p.qs1 = f->q_stride[1]; p.qs2 = f->q_stride[2];
   p.k = f->k; p.ks0 = f->k_stride[0]; p.ks1 = f->k_stride[1]; p.ks2 = f->k_stride[2];
@@ -1139,9 +1251,7 @@ int general_bwd(const kdn_scan_bwd_args* a, void* stream) {
   p.init = f->initial_state;
   p.is0 = f->init_stride[0]; p.is1 = f->init_stride[1]; p.is2 = f->init_stride[2]; p.is3 = f->init_stride[3];
   p.ws = reinterpret_cast<float*>(a->workspace);
-  const int D = (int)f->D, DV = (int)f->d_v;
-  p.fin = p.ws + p.B * p.H * p.nch * (int64_t)gen::bwd_record_floats(D, DV);
-  p.fs0 = p.H * D * DV; p.fs1 = (int64_t)D * DV; p.fs2 = DV; p.fs3 = 1;
+  const int DV = (int)f->d_v;
   gen::BwdP g = {};
   g.dy = a->dy; g.ys0 = a->dy_stride[0]; g.ys1 = a->dy_stride[1]; g.ys2 = a->dy_stride[2];
   g.dfin = a->d_final_state;
@@ -1154,12 +1264,13 @@ int general_bwd(const kdn_scan_bwd_args* a, void* stream) {
   g.dinit = a->d_initial_state;
   g.gis0 = a->dinit_stride[0]; g.gis1 = a->dinit_stride[1]; g.gis2 = a->dinit_stride[2]; g.gis3 = a->dinit_stride[3];
   const hipStream_t st = as_stream(stream);
+  const size_t isz = dtype_size(f->in_dtype);
   if (DV == 64) {
-    if (f->in_dtype == KDN_DTYPE_BF16) return gen::launch_bwd<PrecBF16, __bf16, 1024, 64>(p, g, st);
-    return gen::launch_bwd<PrecF32, float, 1024, 64>(p, g, st);
+    if (f->in_dtype == KDN_DTYPE_BF16) return general_bwd_run<PrecBF16, __bf16, 1024, 64>(p, g, L, isz, st);
+    return general_bwd_run<PrecF32, float, 1024, 64>(p, g, L, isz, st);
   }
-  if (f->in_dtype == KDN_DTYPE_BF16) return gen::launch_bwd<PrecBF16, __bf16, 1024, 128>(p, g, st);
-  return gen::launch_bwd<PrecF32, float, 1024, 128>(p, g, st);
+  if (f->in_dtype == KDN_DTYPE_BF16) return general_bwd_run<PrecBF16, __bf16, 1024, 128>(p, g, L, isz, st);
+  return general_bwd_run<PrecF32, float, 1024, 128>(p, g, L, isz, st);
 }
 
 }  // namespace kdn

@@ -76,6 +76,7 @@ int general_scan(const kdn_scan_args* a, void* stream);
 // one workspace record per (batch, head, chunk) for the whole sequence, one launch sequence on one stream.
 bool general_bwd_applies(const kdn_scan_args* f);
 size_t general_bwd_workspace_bytes(const kdn_scan_bwd_args* a);
+int64_t general_bwd_segments(const kdn_scan_bwd_args* a, int64_t* segment_chunks);
 int general_bwd(const kdn_scan_bwd_args* a, void* stream);
 // Device address of the current device's copy of kdn_delta_scan_fwd_noalloc's scratch array (kdn_noalloc.hip).
 int noalloc_scratch_address(void** out);

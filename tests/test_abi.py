@@ -282,8 +282,8 @@ def test_backward_workspace_and_errors_need_no_device(lib):
 
 
 def test_general_width_backward_needs_no_device(lib):
-    # D = 1024 over pre-lifted features (ABI 1.8): one record per (batch, head, chunk) for the whole
-    # sequence (753,792 floats at d_v = 128, 454,784 at d_v = 64) plus the forward carry's final state
+    # D = 1024 over pre-lifted features (ABI 1.8): one record per (batch, head, chunk) of a segment
+    # (753,792 floats at d_v = 128, 454,784 at d_v = 64) plus the forward carry's final state
     f = _fake_ptrs(_args(T=256, H=2, d_k=1024, D=1024, d_v=128, feature_mode=1))
     g = N.ScanBwdArgs()
     g.fwd = ctypes.addressof(f)
@@ -303,6 +303,20 @@ def test_general_width_backward_needs_no_device(lib):
     assert lib.kdn_scan_bwd_workspace_bytes(ctypes.byref(g)) == 0
     assert lib.kdn_delta_scan_bwd(ctypes.byref(g), None) == -2
     f.H = 2
+    # segments: the records of one segment plus a state per segment boundary, the carried dL/dS and the
+    # forward carry's final state; the default segment is the largest power of two up to 256 chunks whose
+    # records fit 12 GiB (2 heads x 3,015,168 bytes per chunk: 256), so the workspace stops growing with T
+    f.d_v = 128
+    st = 2 * 1024 * 128 * 4
+    f.segment_chunks = 3                                               # 4 chunks in segments of 3 and 1
+    assert lib.kdn_scan_bwd_segments(ctypes.byref(g), ctypes.byref(seg)) == 2 and seg.value == 3
+    assert lib.kdn_scan_bwd_workspace_bytes(ctypes.byref(g)) == 2 * 3 * rec128 + 3 * st
+    f.segment_chunks, f.T = 0, 64 * 1000                               # 1000 chunks: 4 segments of 256
+    assert lib.kdn_scan_bwd_segments(ctypes.byref(g), ctypes.byref(seg)) == 4 and seg.value == 256
+    assert lib.kdn_scan_bwd_workspace_bytes(ctypes.byref(g)) == 2 * 256 * rec128 + (3 + 1 + 1) * st
+    f.T = 64 * 100000                                                  # 100,000 chunks: the same records
+    assert lib.kdn_scan_bwd_workspace_bytes(ctypes.byref(g)) == 2 * 256 * rec128 + (391 + 1) * st
+    f.T = 256
     g.dinv_tau = 0x7C0000000000                                        # no temperature to differentiate
     assert lib.kdn_scan_bwd_workspace_bytes(ctypes.byref(g)) == 0
     g.dinv_tau = None

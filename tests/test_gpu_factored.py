@@ -210,6 +210,33 @@ def test_d1024_scan_backward(oprojs, dtype, dv, T):
         assert rel(a.cpu().numpy(), r) < tol, name
 
 
+@pytest.mark.parametrize("dtype,dv", [(torch.float32, 64), (torch.bfloat16, 128)])
+def test_d1024_scan_backward_segments(oprojs, dtype, dv):
+    # the segmented backward (checkpoint pass, then segments last first with dL/dS carried between them):
+    # 11 chunks in segments of 3 give every gradient bit for bit as one segment does, and match the oracle
+    B, T = 2, 700
+    pq, pk, v, beta, decay, s0, dy, ds = _prelifted_case(B, T, dv, dtype, oprojs, 8)
+    d = lambda t: t.to(DEV)
+    outs = []
+    for seg in (0, 3):
+        plan = ops.ScanBackwardPlan(d(pq).unsqueeze(2), d(pk).unsqueeze(2), d(v).unsqueeze(2),
+                                    d(beta).unsqueeze(-1), d(decay).unsqueeze(-1), None, None, 1.0,
+                                    d(dy).unsqueeze(2), d(ds).unsqueeze(1).transpose(2, 3),
+                                    initial_state=d(s0).unsqueeze(1).transpose(2, 3), segment_chunks=seg,
+                                    features=ops.FeatureMap(lifted=True))
+        assert plan.segments == (1 if seg == 0 else 4)
+        outs.append([t.clone() for t in plan.run()])
+    torch.cuda.synchronize()
+    for name, a, b in zip(("dphi_q", "dphi_k", "dv", "dbeta", "ddecay", "dS0"), *outs):
+        assert torch.equal(a, b), name
+    ref = _oracle_scan_grads(pq, pk, v, beta, decay, s0, dy, ds)
+    dq, dk, dvv, dbeta, ddecay, dinit = outs[1]
+    tol = 1e-4 if dtype == torch.float32 else 2e-2
+    got = [dq[:, :, 0], dk[:, :, 0], dvv[:, :, 0], dbeta[:, :, 0], ddecay[:, :, 0], dinit[:, 0].transpose(1, 2)]
+    for name, a, r in zip(("dphi_q", "dphi_k", "dv", "dbeta", "ddecay", "dS0"), got, ref):
+        assert rel(a.cpu().numpy(), r) < tol, name
+
+
 def test_d1024_scan_backward_is_deterministic(oprojs):
     pq, pk, v, beta, decay, s0, dy, ds = _prelifted_case(1, 300, 128, torch.bfloat16, oprojs, 6)
     d = lambda t: t.to(DEV)
