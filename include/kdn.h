@@ -330,12 +330,16 @@ int kdn_scan_chain(const kdn_scan_args* a, int64_t chunk0, int64_t nchunks, void
  * runs in a fixed order: the results are identical bit for bit from run to run and between
  * kdn_delta_scan_bwd and kdn_delta_scan_bwd_streams.
  *
- * At D = 1024 (ABI 1.8) the backward is one segment on one stream (the auxiliary stream is not used, and
- * kdn_scan_bwd_phase returns KDN_ERR_UNSUPPORTED): the forward's prep and carry kernels recompute every
- * chunk, a reverse carry takes dL/dS from the last chunk to the first, and two parallel launches write
- * the gradients.  Its workspace is one record per (batch, head, chunk) for the whole sequence
- * (3,015,168 bytes at d_v = 128, 1,819,136 at d_v = 64) plus one fp32 [B][H][1024][d_v] state; it grows
- * with T.  Its reductions also run in a fixed order. */
+ * At D = 1024 (ABI 1.8) the backward runs on one stream (the auxiliary stream is not used, and
+ * kdn_scan_bwd_phase returns KDN_ERR_UNSUPPORTED), in segments of fwd->segment_chunks chunks (0: the
+ * largest power of two from 4 to 256 whose records fit 12 GiB; ABI 2.3): a checkpoint pass of the
+ * recompute and the forward carry stores the state at each segment start, then each segment, last first,
+ * recomputes its chunks, carries the state forward from its checkpoint and dL/dS backward from the next
+ * segment (a reverse carry from its last chunk to its first), and two parallel launches write its
+ * gradients.  Its workspace is one record per (batch, head, chunk) of a segment (3,015,168 bytes at
+ * d_v = 128, 1,819,136 at d_v = 64), one fp32 [B][H][1024][d_v] state per segment boundary, one more for
+ * the carried dL/dS with more than one segment and one for the forward carry's final state.  The results
+ * do not depend on the segment length (bit for bit), and its reductions run in a fixed order. */
 typedef struct kdn_scan_bwd_args {
   const kdn_scan_args* fwd;
   const float* dy;            int64_t dy_stride[3];

@@ -14,4 +14,4 @@ extern "C" const char* kdn_strerror(int status) {
   }
 }
 
-extern "C" int kdn_abi_version(void) { return (2 << 16) | 2; }
+extern "C" int kdn_abi_version(void) { return (2 << 16) | 3; }
