@@ -292,8 +292,8 @@ __global__ void __launch_bounds__(256, (PrepWaves<P, FM>::value)) prep_kernel(Sc
     }
     lds_barrier();
 
-    // ---- T = (I + A)^{-1} (column-oriented substitution over lane quads)
-    unit_lower_inverse<true>(s_A, s_T, 64, w, lane);
+    // ---- T = (I + A)^{-1} (16 x 16 blocks: substitution on the diagonal, MFMA products below it)
+    unit_lower_inverse_blocked(s_A, s_T, w, lane);
     lds_barrier();
 
     // ---- W~ factor T diag(beta e^g |phi_k|) fragments, and U~ = T diag(beta) V   (wave w: rows m = w)

@@ -74,19 +74,8 @@ __device__ __forceinline__ f32x4 mm(f32x4 acc, const f32x8& a, const f32x8& b) {
 // on the sequential chain.  acc[s] = -(partial T[4s+pq][col]); A is zero on and above its diagonal, so
 // updating every slot from i >> 2 on leaves rows r <= i unchanged.  The columns of A are loaded three
 // rows ahead.
-//   At: A transposed in LDS, At[(j * 4 + p) * 16 + s] = A[4s + p][j] (16-byte aligned); with SWZ the
-//       16-byte groups of a row are permuted, At[(j * 4 + p) * 16 + a_swizzle(j, s)] = A[4s + p][j]
-//   T:  output rows, T[r * ldt + c] (LDS); with SWZ T[r * ldt + t_swizzle(r, c)] and ldt = 64
-// a_swizzle lets a writer that stores one element per lane, lane groups g = 0..3 taking columns
-// j = 4g + const and the lanes of a group s = 4w + 0..3 (p = 0..3), hit 64 distinct banks (unswizzled,
-// the four groups' stores collide on the same 16 banks).
-__device__ __forceinline__ int a_swizzle(int j, int s) { return 4 * ((s >> 2) ^ ((j >> 2) & 3)) + (s & 3); }
-// t_swizzle permutes the 16-byte groups of a row of T (ldt = 64) so that both the substitution's stores
-// (rows 4s + 0..3, columns 16w + 0..15 per instruction) and 16-byte reads of four consecutive columns
-// of rows r0 .. r0 + 15 fall on distinct banks.
-__device__ __forceinline__ int t_swizzle(int r, int c) { return c ^ (16 * (r & 3)) ^ (4 * ((r >> 2) & 3)); }
-
-template <bool SWZ = false>
+//   At: A transposed in LDS, At[(j * 4 + p) * 16 + s] = A[4s + p][j] (16-byte aligned)
+//   T:  output rows, T[r * ldt + c] (LDS)
 __device__ __forceinline__ void unit_lower_inverse(const float* At, float* T, int ldt, int w, int lane) {
   const int col = 16 * w + (lane >> 2), pq = lane & 3;
   float acc[16];
@@ -98,7 +87,7 @@ __device__ __forceinline__ void unit_lower_inverse(const float* At, float* T, in
     const f32x4* src = reinterpret_cast<const f32x4*>(At + (i * 4 + pq) * 16);
 #pragma unroll
     for (int q = 0; q < 4; ++q)
-      if (q >= (i >> 4)) dst[q] = src[SWZ ? (q ^ ((i >> 2) & 3)) : q];
+      if (q >= (i >> 4)) dst[q] = src[q];
   };
 #pragma unroll
   for (int i = 0; i < AHEAD; ++i) load_col(i, acol[i]);
@@ -117,7 +106,115 @@ __device__ __forceinline__ void unit_lower_inverse(const float* At, float* T, in
     if (i + AHEAD < 63) load_col(i + AHEAD, acol[i % AHEAD]);
   }
 #pragma unroll
-  for (int s2 = 0; s2 < 16; ++s2) T[(4 * s2 + pq) * ldt + (SWZ ? t_swizzle(4 * s2 + pq, col) : col)] = -acc[s2];
+  for (int s2 = 0; s2 < 16; ++s2) T[(4 * s2 + pq) * ldt + col] = -acc[s2];
+}
+
+// Swizzled layouts of A and T for unit_lower_inverse_blocked: At[(j * 4 + p) * 16 + a_swizzle(j, s)] =
+// A[4s + p][j] and T[r * 64 + t_swizzle(r, c)] = T[r][c].
+// a_swizzle lets a writer that stores one element per lane, lane groups g = 0..3 taking columns
+// j = 4g + const and the lanes of a group s = 4w + 0..3 (p = 0..3), hit 64 distinct banks (unswizzled,
+// the four groups' stores collide on the same 16 banks).
+__device__ __forceinline__ int a_swizzle(int j, int s) { return 4 * ((s >> 2) ^ ((j >> 2) & 3)) + (s & 3); }
+// t_swizzle permutes the 16-byte groups of a row of T (ldt = 64) so that both stores of rows 4s + 0..3,
+// columns 16w + 0..15 per instruction and 16-byte reads of four consecutive columns
+// of rows r0 .. r0 + 15 fall on distinct banks.
+__device__ __forceinline__ int t_swizzle(int r, int c) { return c ^ (16 * (r & 3)) ^ (4 * ((r >> 2) & 3)); }
+
+// Block column J of T below the diagonal (step 2 of unit_lower_inverse_blocked): T_iJ for i = J+1 .. 3.
+template <int J>
+__device__ __forceinline__ void inverse_block_column(const float* At, float* T, int lane) {
+  auto at_idx = [](int r, int c) { return (c * 4 + (r & 3)) * 16 + a_swizzle(c, r >> 2); };
+  auto t_idx = [](int r, int c) { return r * 64 + t_swizzle(r, c); };
+  const int g = lane >> 4, m = lane & 15;
+  // operands read first: L_ik as A operands (depth 4g + kb) and T_ii rows, for every i > J and k in [J, i)
+  float la[4][4][4];  // la[i][k][kb] = A[16i + m][16k + 4g + kb]
+#pragma unroll
+  for (int i = J + 1; i < 4; ++i)
+#pragma unroll
+    for (int k = J; k < i; ++k)
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) la[i][k][kb] = At[at_idx(16 * i + m, 16 * k + 4 * g + kb)];
+  f32x4 tii[4];  // T_ii[m][4g .. 4g + 3]
+#pragma unroll
+  for (int i = J + 1; i < 4; ++i) tii[i] = *reinterpret_cast<const f32x4*>(T + t_idx(16 * i + m, 16 * i + 4 * g));
+  f32x4 tcol[4];  // T_kJ in accumulator layout: tcol[k][e] = T[16k + 4g + e][16J + m]
+#pragma unroll
+  for (int e = 0; e < 4; ++e) tcol[J][e] = T[t_idx(16 * J + 4 * g + e, 16 * J + m)];
+#pragma unroll
+  for (int i = J + 1; i < 4; ++i) {
+    f32x4 S = zero4();
+#pragma unroll
+    for (int k = J; k < i; ++k)
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) S = __builtin_amdgcn_mfma_f32_16x16x4f32(la[i][k][kb], tcol[k][kb], S, 0, 0, 0);
+    f32x4 tn = zero4();
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) tn = __builtin_amdgcn_mfma_f32_16x16x4f32(tii[i][kb], S[kb], tn, 0, 0, 0);
+    tcol[i] = -tn;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) T[t_idx(16 * i + 4 * g + e, 16 * J + m)] = tcol[i][e];
+  }
+}
+
+// The same inverse in 16 x 16 blocks, for the swizzled layouts above (At by a_swizzle, T by t_swizzle with
+// ldt = 64).  L = I + A with blocks L_ik; T_ii = L_ii^{-1} and T_ij = -T_ii sum_{k=j}^{i-1} L_ik T_kj (i > j).
+//   1. wave b inverts diagonal block b by the column substitution above restricted to 16 rows (15 steps of
+//      one quad broadcast and at most four FMAs), writes T_bb and the zero blocks to its right;
+//   2. after a barrier, wave j (0..2) walks down block column j: S = sum_k L_ik T_kj, T_ij = -T_ii S, as
+//      fp32 16x16x4 MFMAs.  Lane group g supplies depth 4g + kb to MFMA kb for both operands, so a product
+//      in accumulator layout (lane l: rows 4(l >> 4) + e of column l & 15) is the B operand of the next
+//      one as it stands (element kb), and L_ik and T_ii enter as A operands read from LDS.
+// The sequential chain is 15 substitution steps plus three dependent block products (wave 0), against
+// 63 substitution steps column by column.  Ends with the stores of T issued: the caller's barrier orders
+// them for its readers.
+__device__ __forceinline__ void unit_lower_inverse_blocked(const float* At, float* T, int w, int lane) {
+  auto t_idx = [](int r, int c) { return r * 64 + t_swizzle(r, c); };
+  {
+    // 1. diagonal block b = w: lane quad c = lane >> 2 holds column c, lane pq = lane & 3 rows 4s + pq
+    const int b = w, c = lane >> 2, pq = lane & 3;
+    float acc[4];  // -(partial T_bb[4s + pq][c])
+#pragma unroll
+    for (int s = 0; s < 4; ++s) acc[s] = (4 * s + pq == c) ? -1.f : 0.f;
+    // column i of L_bb's strict lower part, rows 16b + 4s + pq (s = 0..3): one 16-byte group of At
+    auto col = [&](int i) {
+      const int C = 16 * b + i;
+      return *reinterpret_cast<const f32x4*>(At + (C * 4 + pq) * 16 + 4 * (b ^ ((C >> 2) & 3)));
+    };
+    // every column's read issued before the chain starts (nothing else is live here)
+    f32x4 acol[15];
+#pragma unroll
+    for (int i = 0; i < 15; ++i) acol[i] = col(i);
+#pragma unroll
+    for (int i = 0; i < 15; ++i) {
+      const f32x4 a = acol[i];
+      float bc;  // -T[i][c], held by lane pq = i & 3, slot i >> 2 of the quad
+      switch (i & 3) {
+        case 0: bc = quad_bcast<0>(acc[i >> 2]); break;
+        case 1: bc = quad_bcast<1>(acc[i >> 2]); break;
+        case 2: bc = quad_bcast<2>(acc[i >> 2]); break;
+        default: bc = quad_bcast<3>(acc[i >> 2]); break;
+      }
+#pragma unroll
+      for (int s = i >> 2; s < 4; ++s) acc[s] = fmaf(-a[s], bc, acc[s]);
+    }
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const int r = 16 * b + 4 * s + pq;
+      T[t_idx(r, 16 * b + c)] = -acc[s];
+#pragma unroll
+      for (int blk = 0; blk < 4; ++blk)
+        if (blk > b) T[t_idx(r, 16 * blk + c)] = 0.f;
+    }
+  }
+  lds_barrier();
+  // 2. block column j = w below the diagonal, one code path per wave so that every LDS read of the walk
+  //    can be issued ahead of the products
+  switch (w) {
+    case 0: inverse_block_column<0>(At, T, lane); break;
+    case 1: inverse_block_column<1>(At, T, lane); break;
+    case 2: inverse_block_column<2>(At, T, lane); break;
+    default: break;
+  }
 }
 
 // Sum over the 16 lanes sharing (lane >> 4) (one tile row) / over the 4 lane groups (one tile column).
