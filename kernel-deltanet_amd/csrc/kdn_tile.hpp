@@ -115,10 +115,15 @@ __device__ __forceinline__ void unit_lower_inverse(const float* At, float* T, in
 // j = 4g + const and the lanes of a group s = 4w + 0..3 (p = 0..3), hit 64 distinct banks (unswizzled,
 // the four groups' stores collide on the same 16 banks).
 __device__ __forceinline__ int a_swizzle(int j, int s) { return 4 * ((s >> 2) ^ ((j >> 2) & 3)) + (s & 3); }
-// t_swizzle permutes the 16-byte groups of a row of T (ldt = 64) so that both stores of rows 4s + 0..3,
-// columns 16w + 0..15 per instruction and 16-byte reads of four consecutive columns
-// of rows r0 .. r0 + 15 fall on distinct banks.
-__device__ __forceinline__ int t_swizzle(int r, int c) { return c ^ (16 * (r & 3)) ^ (4 * ((r >> 2) & 3)); }
+// t_swizzle XORs the 16-byte group index of column c in row r (ldt = 64) with h(r) = 4 (a ^ p) + a,
+// a = (r >> 2) & 3, p = r & 3, so that each of these falls on distinct banks: 4-byte accesses of rows
+// 4a + 0..3 (a fixed) or of rows 4·0..3 + p (p fixed) at 16 consecutive columns of one 16-column block per
+// instruction (h >> 2 differs over p for fixed a and over a for fixed p), and 16-byte reads of four
+// consecutive columns of 16 consecutive rows (h is a bijection on a 16-row block).
+__device__ __forceinline__ int t_swizzle(int r, int c) {
+  const int a = (r >> 2) & 3, p = r & 3;
+  return c ^ (16 * (a ^ p)) ^ (4 * a);
+}
 
 // Block column J of T below the diagonal (step 2 of unit_lower_inverse_blocked): T_iJ for i = J+1 .. 3.
 template <int J>
