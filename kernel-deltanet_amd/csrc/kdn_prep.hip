@@ -225,7 +225,7 @@ __global__ void __launch_bounds__(256, (PrepWaves<P, FM>::value)) prep_kernel(Sc
         store_frag_nt<P>(ws + L::phiK + (size_t)(w * NJ + j) * 64 * L::FB, lane, cqk[KI][j]);
       }
       if constexpr (!NOQ) {
-        put(ws + L::phiQ + (size_t)(w * NJ + j) * 64 * L::FB, cqk[QI][j]);
+        if (!p.q_relift) put(ws + L::phiQ + (size_t)(w * NJ + j) * 64 * L::FB, cqk[QI][j]);
       }
     }
     if constexpr (OMEGA_LDS) lds_barrier();  // every wave's lift has read Omega from the area

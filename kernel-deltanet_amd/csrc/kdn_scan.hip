@@ -31,6 +31,7 @@
 #include "kdn_internal.hpp"
 #include "kdn_io.hpp"
 #include "kdn_scan_common.hpp"
+#include "kdn_lift_tile.hpp"
 
 namespace kdn {
 
@@ -578,17 +579,29 @@ struct OutputLds {
   static constexpr size_t bytes = (size_t)NJ * NG * 64 * P::frag_bytes + (size_t)4 * 16 * YS * 4;
 };
 
-template <class P, typename OutT, int D, int DV>
+//
+// RELIFT (the resident form beside the state chain, bf16, one shared exact Omega): instead of reading the
+// record's Q fragments (64 KB per item, written by prep), the workgroup stages Omega and the phases in LDS
+// once and lifts its q rows again per item, with the code and inputs that prep's lift uses, so the
+// fragments are the same bits; 120 KB less HBM traffic per (head, chunk) beside the chain.
+template <class P, typename OutT, int D, int DV, bool RELIFT = false>
 __global__ void __launch_bounds__(256) output_kernel(ScanParams p) {
   using L = WsLayout<P, D, DV>;
   using frag = typename P::frag;
   using O = OutputLds<P, D, DV>;
   constexpr int NJ = O::NJ, NV = O::NV, NG = O::NG, YS = O::YS;
+  static_assert(!RELIFT || (IsBF16<P>::value && D == 512), "the q re-lift is the bf16 D = 512 path's");
   __shared__ frag s_s[NJ * NG * 64];
   __shared__ __attribute__((aligned(16))) float s_y[4][16 * YS];
+  __shared__ bf16x8 s_om[RELIFT ? (D / 16) * 2 * 64 : 1];
+  __shared__ __attribute__((aligned(16))) float s_phr[RELIFT ? D : 1];
 
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  if constexpr (RELIFT) {
+    stage_omega<D, true>(p.omega, p.phase, s_om, s_phr);
+    __syncthreads();
+  }
   const int64_t items = p.nseg * p.H * (p.fl_off ? 1 : p.B);
   for (int64_t it = blockIdx.x; it < items; it += gridDim.x) {
   if (it != (int64_t)blockIdx.x) __syncthreads();  // the previous item's LDS tiles have been read
@@ -613,8 +626,22 @@ __global__ void __launch_bounds__(256) output_kernel(ScanParams p) {
   const float* vec = reinterpret_cast<const float*>(ws + L::VEC);
 
   frag aq[NJ];
+  if constexpr (RELIFT) {
+    // the lifted queries of token tile w, as prep lifts them (unnormalised cos values; the per-row
+    // scale comes from the record)
+    const int64_t trow = t0 + 16 * w + (lane & 15);
+    RawRow<__bf16> raw[1];
+    raw[0].load((const __bf16*)p.q + sq.q + trow * p.qs1 + h * p.qs2, trow < sq.len, lane);
+    const float ang = (p.inv_tau_head ? p.inv_tau_head[h] : p.inv_tau) * 0.15915494309189535f;
+    frag cq[1][NJ];
+    float ssq[1];
+    lift_tile<P, __bf16, D, true, 1>(raw, p.normalize, s_om, p.omega, s_phr, ang, lane, cq, ssq);
 #pragma unroll
-  for (int j = 0; j < NJ; ++j) aq[j] = load_frag_nt<P>(ws + L::phiQ + (size_t)(w * NJ + j) * 64 * L::FB, lane);
+    for (int j = 0; j < NJ; ++j) aq[j] = cq[0][j];
+  } else {
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) aq[j] = load_frag_nt<P>(ws + L::phiQ + (size_t)(w * NJ + j) * 64 * L::FB, lane);
+  }
   frag pf[2];
 #pragma unroll
   for (int jb = 0; jb < 2; ++jb) pf[jb] = load_frag_nt<P>(ws + L::Pm + (size_t)(w * 2 + jb) * 64 * L::FB, lane);
@@ -724,6 +751,7 @@ static ScanParams fill_params(const kdn_scan_args* a) {
   p.fl_nseq = 0;
   p.prep_no_q = 0;
   p.k_plain = 0;
+  p.q_relift = 0;
   p.prep_run = 0;
   p.out_wgs = 0;
   return p;
@@ -839,6 +867,15 @@ static int launch_phase(const ScanParams& p, int phase, hipStream_t st) {
     // (chunk, head) took every free CU and held up a quarter of its workgroups by ~55 us per segment
     // (config 3: 2.59 against 2.41 ms per layer, measured with clock stamps).
     const int64_t items = (int64_t)p.nseg * p.H * (p.fl_off ? 1 : p.B);
+    if constexpr (IsBF16<P>::value && D == 512) {
+      if (p.q_relift) {
+        // prep stored no Q for this segment: the re-lifting form, whatever the item count (Omega and the
+        // phases in LDS make the workgroup more than half a CU: no pad needed)
+        const int64_t grid = p.out_wgs < items ? p.out_wgs : items;
+        hipLaunchKernelGGL((output_kernel<P, OutT, D, DV, true>), dim3((unsigned)grid), dim3(256), 0, st, p);
+        return hipGetLastError() == hipSuccess ? KDN_OK : KDN_ERR_DEVICE;
+      }
+    }
     if (p.out_wgs > 0 && p.out_wgs < items) {
       constexpr size_t excl = CU_LDS_BYTES / 2 + 1024;
       const size_t pad = OutputLds<P, D, DV>::bytes < excl ? excl - OutputLds<P, D, DV>::bytes : 0;
@@ -918,6 +955,10 @@ static int run_pipelined(const kdn_scan_args* a, const RunSpec& r) {
     ScanParams p = r.flat ? flat_params(a, r, s, buf)
                           : segment_params(a, r, c0, (nchunks - c0 < seg) ? (nchunks - c0) : seg, buf, prep_cus);
     p.out_wgs = prep_cus > 0 ? prep_cus : 0;
+    // the resident output workgroups lift q again (one shared exact bf16 Omega and phases): prep stores
+    // no Q fragments
+    p.q_relift = (IsBF16<P>::value && D == 512 && p.out_wgs > 0 && !p.prelifted && !p.omega_lo && p.oms == 0 &&
+                  p.phs == 0) ? 1 : 0;
     return p;
   };
 #define KDN_TRY(x) do { if ((x) != hipSuccess) return KDN_ERR_DEVICE; } while (0)

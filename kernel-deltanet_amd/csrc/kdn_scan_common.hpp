@@ -105,6 +105,8 @@ struct ScanParams {
   // the fused chain reads the segment (kdn_chain.hip): prep stores K as plain fragments (each lane's 16
   // bytes contiguous) instead of the state kernel's LDS image
   int k_plain;
+  // the resident output kernel lifts q again (bf16, one shared exact Omega): prep stores no Q fragments
+  int q_relift;
   // ragged batches: sequence b is token rows seq_lo[b] .. seq_hi[b] (stride 1 of each token tensor; for
   // cu_seqlens, seq_hi = cu_seqlens + 1); its state is slot slots[b] (stride 0 of the state tensors)
   const int64_t* seq_lo;
