@@ -40,13 +40,15 @@ struct RawRow {
 // feature 16t + 4(l>>4) + i of row (l & 15), which is slot (t & 1) * 4 + i of X fragment t / 2.
 // The angle in revolutions is reduced with v_fract before v_cos (which takes revolutions), so any
 // finite angle stays inside the instruction's domain.
-// Output: unnormalised cos values as X fragments, and each row's sum of squares (all lanes).
-template <class P, typename InT, int D, bool OMEGA_LDS, int NX, bool LO = false>
+// Output: unnormalised cos values as X fragments, and each row's sum of squares (all lanes).  NTL tiles
+// from tile0 (default: all D / 16): fragment j of `out` holds features 32 (tile0 / 2 + j) .. + 31, and ss
+// the sum over those features.
+template <class P, typename InT, int D, bool OMEGA_LDS, int NX, bool LO = false, int NTL = D / 16>
 __device__ __forceinline__ void lift_tile(const RawRow<InT> (&raw)[NX], int normalize,
                                           const bf16x8* s_omega, const __bf16* omega, const float* s_phrev,
-                                          float ang, int lane, typename P::frag (&out)[NX][D / 32],
-                                          float (&ss)[NX], const __bf16* omega_lo = nullptr) {
-  constexpr int NT = D / 16;
+                                          float ang, int lane, typename P::frag (&out)[NX][NTL / 2],
+                                          float (&ss)[NX], const __bf16* omega_lo = nullptr, int tile0 = 0) {
+  constexpr int NT = NTL;
   constexpr int NSPLIT = XFrag<InT>::NSPLIT;
   float xv[NX][2][8];
 #pragma unroll
@@ -84,10 +86,11 @@ __device__ __forceinline__ void lift_tile(const RawRow<InT> (&raw)[NX], int norm
   // tile earlier still (so that the read's latency is covered by a tile's cosines, not waited on by the
   // MFMAs that follow it).
   auto fetch = [&](int t, bf16x8 (&a)[2]) {
+    const int tg = tile0 + t;
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
-      if constexpr (OMEGA_LDS) a[kb] = s_omega[(t * 2 + kb) * 64 + lane];
-      else a[kb] = *reinterpret_cast<const bf16x8*>(omega + (int64_t)(16 * t + (lane & 15)) * 64 + 32 * kb + 8 * (lane >> 4));
+      if constexpr (OMEGA_LDS) a[kb] = s_omega[(tg * 2 + kb) * 64 + lane];
+      else a[kb] = *reinterpret_cast<const bf16x8*>(omega + (int64_t)(16 * tg + (lane & 15)) * 64 + 32 * kb + 8 * (lane >> 4));
     }
   };
   // tiles of Omega in flight ahead of the one projected (one; the exact projection reading Omega from L2
@@ -109,7 +112,7 @@ __device__ __forceinline__ void lift_tile(const RawRow<InT> (&raw)[NX], int norm
 #pragma unroll
         for (int x = 0; x < NX; ++x) acc[x] = PrecBF16::mma(acc[x], a, xb[x][kb][s]);
       if constexpr (LO) {
-        const bf16x8 alo = *reinterpret_cast<const bf16x8*>(omega_lo + (int64_t)(16 * t + (lane & 15)) * 64 + 32 * kb + 8 * (lane >> 4));
+        const bf16x8 alo = *reinterpret_cast<const bf16x8*>(omega_lo + (int64_t)(16 * (tile0 + t) + (lane & 15)) * 64 + 32 * kb + 8 * (lane >> 4));
 #pragma unroll
         for (int s = 0; s < NSPLIT; ++s)
 #pragma unroll
@@ -129,7 +132,7 @@ __device__ __forceinline__ void lift_tile(const RawRow<InT> (&raw)[NX], int norm
     if (t % 2 == 0) __builtin_amdgcn_sched_barrier(0);
     f32x4 next[NX];
     if (t + 1 < NT) project(t + 1, next);
-    const f32x4 ph = *reinterpret_cast<const f32x4*>(&s_phrev[16 * t + 4 * (lane >> 4)]);
+    const f32x4 ph = *reinterpret_cast<const f32x4*>(&s_phrev[16 * (tile0 + t) + 4 * (lane >> 4)]);
 #pragma unroll
     for (int x = 0; x < NX; ++x)
 #pragma unroll

@@ -172,11 +172,12 @@ __device__ __forceinline__ void inverse_block_column(const float* At, float* T, 
 // The sequential chain is 15 substitution steps plus three dependent block products (wave 0), against
 // 63 substitution steps column by column.  Ends with the stores of T issued: the caller's barrier orders
 // them for its readers.
-__device__ __forceinline__ void unit_lower_inverse_blocked(const float* At, float* T, int w, int lane) {
+// Step 1 for diagonal block b (one wave).
+__device__ __forceinline__ void inverse_diag_block(const float* At, float* T, int b, int lane) {
   auto t_idx = [](int r, int c) { return r * 64 + t_swizzle(r, c); };
   {
-    // 1. diagonal block b = w: lane quad c = lane >> 2 holds column c, lane pq = lane & 3 rows 4s + pq
-    const int b = w, c = lane >> 2, pq = lane & 3;
+    // diagonal block b: lane quad c = lane >> 2 holds column c, lane pq = lane & 3 rows 4s + pq
+    const int c = lane >> 2, pq = lane & 3;
     float acc[4];  // -(partial T_bb[4s + pq][c])
 #pragma unroll
     for (int s = 0; s < 4; ++s) acc[s] = (4 * s + pq == c) ? -1.f : 0.f;
@@ -211,15 +212,23 @@ __device__ __forceinline__ void unit_lower_inverse_blocked(const float* At, floa
         if (blk > b) T[t_idx(r, 16 * blk + c)] = 0.f;
     }
   }
-  lds_barrier();
-  // 2. block column j = w below the diagonal, one code path per wave so that every LDS read of the walk
-  //    can be issued ahead of the products
+}
+
+// Step 2 for block column j = w (waves 0..2; others return), one code path per wave so that every LDS
+// read of the walk can be issued ahead of the products.
+__device__ __forceinline__ void inverse_block_columns(const float* At, float* T, int w, int lane) {
   switch (w) {
     case 0: inverse_block_column<0>(At, T, lane); break;
     case 1: inverse_block_column<1>(At, T, lane); break;
     case 2: inverse_block_column<2>(At, T, lane); break;
     default: break;
   }
+}
+
+__device__ __forceinline__ void unit_lower_inverse_blocked(const float* At, float* T, int w, int lane) {
+  inverse_diag_block(At, T, w, lane);
+  lds_barrier();
+  inverse_block_columns(At, T, w, lane);
 }
 
 // Sum over the 16 lanes sharing (lane >> 4) (one tile row) / over the 4 lane groups (one tile column).
