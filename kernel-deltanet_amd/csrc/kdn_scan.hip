@@ -27,6 +27,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <type_traits>
+#include <vector>
 #include "kdn_frag.hpp"
 #include "kdn_internal.hpp"
 #include "kdn_io.hpp"
@@ -920,6 +921,30 @@ static int run_scan(const kdn_scan_args* a, const RunSpec& r) {
   return KDN_OK;
 }
 
+// Segment starts of the pipelined split schedule (nsegs + 1 entries).  With at least three segments'
+// worth of chunks the first two segments take seg / 4 and seg / 2 chunks and the last two seg / 2 and
+// seg / 4: the first prep and the last output run alone, and short segments there shorten the layer's
+// head and tail; each prep still fits beside the state launch before it (prep takes about half a state
+// launch's time per chunk).  The chunks and the state carried between segments are the same for any
+// boundaries, so the results do not depend on them.
+static std::vector<int64_t> split_bounds(int64_t nchunks, int64_t seg) {
+  std::vector<int64_t> b{0};
+  auto add = [&](int64_t n) { if (n > 0) b.push_back(b.back() + n); };
+  if (seg >= 4 && nchunks >= 3 * seg) {
+    const int64_t q = seg / 4, hh = seg / 2;
+    add(q);
+    add(hh);
+    const int64_t rest = nchunks - 2 * (q + hh);
+    for (int64_t i = 0; i < rest / seg; ++i) add(seg);
+    add(rest % seg);
+    add(hh);
+    add(q);
+  } else {
+    for (int64_t c = 0; c < nchunks; c += seg) add(nchunks - c < seg ? nchunks - c : seg);
+  }
+  return b;
+}
+
 // Segments rotate through `nbuf` workspace buffers.  The state chain runs on `st` (the caller's stream);
 // prep runs on `aux` and output on `aux_out` (the same stream as prep when only one auxiliary stream is
 // given, in the order prep(s+1), output(s)), so that while state(s) occupies its B*H*d_v/16 workgroups the
@@ -939,7 +964,8 @@ static int run_pipelined(const kdn_scan_args* a, const RunSpec& r) {
   const hipStream_t aux_out = r.aux_out ? r.aux_out : r.aux;
   const bool split = aux_out != aux;
   const int64_t nchunks = (a->T + CH - 1) / CH;
-  const int64_t nsegs = r.flat ? r.flat->nwin : (nchunks + seg - 1) / seg;
+  const std::vector<int64_t> bounds = r.flat ? std::vector<int64_t>{} : split_bounds(nchunks, seg);
+  const int64_t nsegs = r.flat ? r.flat->nwin : (int64_t)bounds.size() - 1;
   EventSet evs;
   int rc = evs.create(3 * nbuf + 2);
   if (rc != KDN_OK) return rc;
@@ -950,10 +976,9 @@ static int run_pipelined(const kdn_scan_args* a, const RunSpec& r) {
   // prep and output share the device with the state kernel's workgroups (one per CU)
   const int prep_cus = device_cus() - (int)state_grid(a->B, a->H, DV / 16);
   auto seg_p = [&](int64_t s) {
-    const int64_t c0 = s * seg;
     void* buf = (unsigned char*)a->workspace + (size_t)(s % nbuf) * buf_bytes;
     ScanParams p = r.flat ? flat_params(a, r, s, buf)
-                          : segment_params(a, r, c0, (nchunks - c0 < seg) ? (nchunks - c0) : seg, buf, prep_cus);
+                          : segment_params(a, r, bounds[s], bounds[s + 1] - bounds[s], buf, prep_cus);
     p.out_wgs = prep_cus > 0 ? prep_cus : 0;
     // the resident output workgroups lift q again (one shared exact bf16 Omega and phases): prep stores
     // no Q fragments
