@@ -100,14 +100,20 @@ int frep_state_lift(const kdn_scan_args* a, const float* s, const int64_t* s4, f
 int frep_state_fold(const kdn_scan_args* a, const float* src, float* s, const int64_t* s4, hipStream_t st);
 
 // Events of a multi-stream launch sequence, released when the call returns (destroying an event whose
-// record is still pending is allowed; its resources are freed once it completes).
+// record is still pending is allowed; its resources are freed once it completes).  They only order
+// kernels of one device against each other (hipStreamWaitEvent; the host never waits on them), so they
+// carry no system-scope fence: the kernels' own end-of-kernel release makes their writes visible to the
+// device's later kernels, and the caller's synchronisation makes the results visible to the host.
+// Without the fence every record wrote back the caches at each segment boundary: config 3's layer
+// 2.09 -> 2.05 ms.
 struct EventSet {
   hipEvent_t ev[16];
   int n = 0;
   int create(int count) {
     if (count > 16) return KDN_ERR_INVALID_ARGUMENT;
     for (; n < count; ++n)
-      if (hipEventCreateWithFlags(&ev[n], hipEventDisableTiming) != hipSuccess) return KDN_ERR_DEVICE;
+      if (hipEventCreateWithFlags(&ev[n], hipEventDisableTiming | hipEventDisableSystemFence) != hipSuccess)
+        return KDN_ERR_DEVICE;
     return KDN_OK;
   }
   ~EventSet() {
