@@ -286,7 +286,9 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
     round_like_input<InT>(p.normalize, part);
 #pragma unroll
     for (int e = 0; e < 16; ++e) xs[r * LD + c0 + e] = part[e];
-    __syncthreads();
+    // The barriers of the lift order LDS only: the record stores issued in it drain in the background
+    // (once, at the fence after the lift) instead of at every barrier.
+    lds_barrier();
 
     // phi~ (tokens x this wave's 128 features), in two halves of 32 tokens: tile [ft][u] holds rows
     // token 16 (2 hm + u) + .., column feature.  Normalised rows go straight to the record.
@@ -342,14 +344,14 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
           const float v = sum_row16(ss[u][i]);
           if ((lane & 15) == 0) s_red[w][32 * hm + 16 * u + 4 * (lane >> 4) + i] = v;
         }
-      __syncthreads();
+      lds_barrier();
       if (tid < 32) {
         const int row = 32 * hm + tid;
         const float n = sqrtf(s_red[0][row] + s_red[1][row] + s_red[2][row] + s_red[3][row]);
         s_n[row] = n;
         rec[Rec::VEC + 128 + 64 * which + row] = n;
       }
-      __syncthreads();
+      lds_barrier();
       // The normalised tiles: the q^T / k^T fragments of depth block hm straight from the registers (an
       // accumulator tile pair [ft][0..1] is the fragment of feature tile ft, tokens 32 hm + kappa), and
       // the record's rows.
@@ -388,6 +390,21 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
             *reinterpret_cast<bf16x8*>(phi + (size_t)(32 * hm + row) * D + 128 * w + 8 * pc) =
                 *reinterpret_cast<const bf16x8*>(stg + row * STG_ROW + 16 * pc);
           }
+          if (which == 1) {
+            // K packed in fragment order for the chains, from the same staging rows: token tiles
+            // 2 hm, 2 hm + 1, feature blocks 4w .. 4w + 3 (lane: row l & 15, features kappa(l, 0..7))
+            typedef __attribute__((ext_vector_type(4))) __bf16 bf16x4;
+            frag* kxf = reinterpret_cast<frag*>(rec + Rec::KXF);
+#pragma unroll
+            for (int mu = 0; mu < 2; ++mu)
+#pragma unroll
+              for (int jj = 0; jj < 4; ++jj) {
+                const unsigned char* q = stg + (16 * mu + (lane & 15)) * STG_ROW + 2 * (32 * jj + 4 * (lane >> 4));
+                const bf16x4 lo = *reinterpret_cast<const bf16x4*>(q);
+                const bf16x4 hi = *reinterpret_cast<const bf16x4*>(q + 32);
+                kxf[((2 * hm + mu) * 16 + 4 * w + jj) * 64 + lane] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+              }
+          }
           wave_lds_sync();
         } else {
 #pragma unroll
@@ -401,14 +418,17 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
         }
       }
     }
-    __syncthreads();
+    lds_barrier();
   }
-  __threadfence();
+  // The Grams below read the rows this workgroup just wrote to the record: a workgroup-scope release /
+  // acquire (__syncthreads) orders them.  A device-scope fence here wrote back and invalidated the whole
+  // L2 in every workgroup (recompute 365 -> 2xx us per segment launch without it).
   __syncthreads();
 
   // K packed in fragment order for the chains: wave w the K-row fragments of feature blocks 4w .. 4w+3
-  // (the K^T fragments went to the record during the lift).
-  {
+  // (the K^T fragments went to the record during the lift; with bf16 features these too, from the
+  // lift's staging rows).
+  if constexpr (!IsBf16Policy<P>::value) {
     using frag = typename P::frag;
     const typename Feat<P>::T* K = feat<P>(rec, Rec::K);
     frag* kxf = reinterpret_cast<frag*>(rec + Rec::KXF);
@@ -1496,7 +1516,8 @@ static Params segment_params(const Params& base, const kdn_scan_bwd_args* a, con
 }
 
 // One launch of segment p: 1 per-chunk recompute, 2 forward carry, 3 reverse carry, 4 gradients, or
-// PH_CARRIES: both carries in one launch.
+// PH_CARRIES: both carries in one launch; PH_GRAD and PH_DX: the two launches of phase 4 (the gradient
+// algebra, then dx) on their own.
 // dL/d(1/tau) of head blockIdx.x: the per-(batch, chunk) partials summed in a fixed order (lane-strided
 // sums, then a shuffle tree), so that the result does not depend on the schedule.
 __global__ void __launch_bounds__(64) bwd_dit_reduce_kernel(const float* dit, int64_t B, int64_t H, int64_t nch,
@@ -1511,7 +1532,7 @@ __global__ void __launch_bounds__(64) bwd_dit_reduce_kernel(const float* dit, in
   if (lane == 0) out[h] = t;
 }
 
-constexpr int PH_CARRIES = 5;
+constexpr int PH_CARRIES = 5, PH_GRAD = 6, PH_DX = 7;
 template <class P, typename InT>
 static int segment_phase(const Params& p, int phase, hipStream_t st) {
   const dim3 chunk_grid((unsigned)p.nseg, (unsigned)p.H, (unsigned)p.B);
@@ -1522,8 +1543,9 @@ static int segment_phase(const Params& p, int phase, hipStream_t st) {
   }
   if (phase == 2) hipLaunchKernelGGL((bwd_chain_kernel<P, false>), dim3(chain_wgs), dim3(256), 0, st, p);
   if (phase == 3) hipLaunchKernelGGL((bwd_chain_kernel<P, true>), dim3(chain_wgs), dim3(256), 0, st, p);
-  if (phase == 4) {
+  if (phase == 4 || phase == PH_GRAD)
     hipLaunchKernelGGL((bwd_grad_kernel<P, InT>), chunk_grid, dim3(64 * GRAD_WAVES), 0, st, p);
+  if (phase == 4 || phase == PH_DX) {
     const bool gen = p.omega_lo || p.oms || p.phs || p.inv_tau_head || p.no_renorm || p.dit;
     if (p.omega_lo) hipLaunchKernelGGL((bwd_dx_kernel<P, InT, true, true>), chunk_grid, dim3(64 * DxWaves<true>::value), 0, st, p);
     else if (gen) hipLaunchKernelGGL((bwd_dx_kernel<P, InT, false, true>), chunk_grid, dim3(64 * DX_WAVES), 0, st, p);
@@ -1552,13 +1574,15 @@ static int bwd_start(const kdn_scan_bwd_args* a, const Params& base, const BwdLa
 // Serial: the start, then per segment (last first) recompute, both carries (one launch), gradients.
 // With aux: the checkpoint pass's prep kernels run on aux beside its state kernels; then per segment
 // (processing step i, segment s = nsegs - 1 - i, buffer i % nbuf)
-//   aux: recompute(s) -> event R[i % nbuf]; gradients(s + 1) after its carries (event V[(i - 1) % nbuf])
+//   aux: recompute(s) -> event R[i % nbuf]; dx(s + 1) after its gradient algebra (event G[(i - 1) % nbuf])
 //   st:  both carries of s after R[i % nbuf] (the forward one after the checkpoint pass, which ends on
-//        st) -> event V[i % nbuf]
-// so that the carries, the sequential critical path (two chain grids of B*H*4 workgroups), run back to
-// back on st while aux recomputes and finishes the segments around them.  The recompute of step i
-// reuses the buffer of step i - nbuf, whose gradients precede it on aux.  Every kernel reads and writes
-// the same data in either schedule, so the results are identical bit for bit.
+//        st), then the gradient algebra of s -> event G[i % nbuf]
+// so that the carries, the sequential chain (two chain grids of B*H*4 workgroups), and the gradient
+// algebra run back to back on st while aux recomputes and runs dx around them: per segment the two
+// streams carry ~0.87 and ~0.75 ms of launches at config 3 (with the algebra on aux, 0.59 and 1.03).
+// The recompute of step i reuses the buffer of step i - nbuf, whose dx precedes it on aux and waited for
+// that step's algebra.  Every kernel reads and writes the same data in either schedule, so the results
+// are identical bit for bit.
 template <class P, typename InT>
 static int bwd_schedule(const kdn_scan_bwd_args* a, const Params& base, const BwdLayout& L, hipStream_t st,
                         hipStream_t aux) {
@@ -1575,7 +1599,7 @@ static int bwd_schedule(const kdn_scan_bwd_args* a, const Params& base, const Bw
   EventSet evs;
   KDN_TRYK(evs.create(2 * L.nbuf + 2));
   hipEvent_t* evR = evs.ev;
-  hipEvent_t* evV = evs.ev + L.nbuf;
+  hipEvent_t* evG = evs.ev + L.nbuf;
   hipEvent_t evIn = evs.ev[2 * L.nbuf], evDone = evs.ev[2 * L.nbuf + 1];
   KDN_TRY(hipEventRecord(evIn, st));
   KDN_TRY(hipStreamWaitEvent(aux, evIn, 0));
@@ -1588,14 +1612,15 @@ static int bwd_schedule(const kdn_scan_bwd_args* a, const Params& base, const Bw
     KDN_TRY(hipEventRecord(evR[bb], aux));
     KDN_TRY(hipStreamWaitEvent(st, evR[bb], 0));
     KDN_TRYK((segment_phase<P, InT>(p, PH_CARRIES, st)));
-    KDN_TRY(hipEventRecord(evV[bb], st));
+    KDN_TRYK((segment_phase<P, InT>(p, PH_GRAD, st)));
+    KDN_TRY(hipEventRecord(evG[bb], st));
     if (i > 0) {
-      KDN_TRY(hipStreamWaitEvent(aux, evV[(i - 1) % L.nbuf], 0));
-      KDN_TRYK((segment_phase<P, InT>(segment_params(base, a, L, s + 1), 4, aux)));
+      KDN_TRY(hipStreamWaitEvent(aux, evG[(i - 1) % L.nbuf], 0));
+      KDN_TRYK((segment_phase<P, InT>(segment_params(base, a, L, s + 1), PH_DX, aux)));
     }
   }
-  KDN_TRY(hipStreamWaitEvent(aux, evV[(L.nsegs - 1) % L.nbuf], 0));
-  KDN_TRYK((segment_phase<P, InT>(segment_params(base, a, L, 0), 4, aux)));
+  KDN_TRY(hipStreamWaitEvent(aux, evG[(L.nsegs - 1) % L.nbuf], 0));
+  KDN_TRYK((segment_phase<P, InT>(segment_params(base, a, L, 0), PH_DX, aux)));
   KDN_TRY(hipEventRecord(evDone, aux));
   KDN_TRY(hipStreamWaitEvent(st, evDone, 0));
 #undef KDN_TRY
