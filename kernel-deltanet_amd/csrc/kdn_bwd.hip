@@ -390,11 +390,13 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
             *reinterpret_cast<bf16x8*>(phi + (size_t)(32 * hm + row) * D + 128 * w + 8 * pc) =
                 *reinterpret_cast<const bf16x8*>(stg + row * STG_ROW + 16 * pc);
           }
-          if (which == 1) {
+          {
             // K packed in fragment order for the chains, from the same staging rows: token tiles
-            // 2 hm, 2 hm + 1, feature blocks 4w .. 4w + 3 (lane: row l & 15, features kappa(l, 0..7))
+            // 2 hm, 2 hm + 1, feature blocks 4w .. 4w + 3 (lane: row l & 15, features kappa(l, 0..7));
+            // Q likewise for the Grams below, in the second half of the area (64 fragments of 1 KB
+            // each, free until the gradient launch writes the dx operands there)
             typedef __attribute__((ext_vector_type(4))) __bf16 bf16x4;
-            frag* kxf = reinterpret_cast<frag*>(rec + Rec::KXF);
+            frag* kxf = reinterpret_cast<frag*>(rec + Rec::KXF) + (which == 0 ? 64 * 64 : 0);
 #pragma unroll
             for (int mu = 0; mu < 2; ++mu)
 #pragma unroll
@@ -422,7 +424,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
   }
   // The Grams below read the rows this workgroup just wrote to the record: a workgroup-scope release /
   // acquire (__syncthreads) orders them.  A device-scope fence here wrote back and invalidated the whole
-  // L2 in every workgroup (recompute 365 -> 2xx us per segment launch without it).
+  // L2 in every workgroup (recompute 365 -> 213 us per segment launch without it).
   __syncthreads();
 
   // K packed in fragment order for the chains: wave w the K-row fragments of feature blocks 4w .. 4w+3
@@ -448,20 +450,23 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
   }
   __syncthreads();  // a o dY in bA is dead from here on (bA becomes A below)
 
-  // Gram matrices (row tile w) from the rows just written; A and P into LDS.
+  // Gram matrices (row tile w) from the features just written, in fragment order (one contiguous 16- or
+  // 32-byte piece per lane; Q from its rows with fp32 features); A and P into LDS.
   {
-    const typename Feat<P>::T* K = feat<P>(rec, Rec::K);
     const typename Feat<P>::T* Q = feat<P>(rec, Rec::Q);
+    const typename P::frag* kxf = reinterpret_cast<const typename P::frag*>(rec + Rec::KXF);
     f32x4 gkk[4], gqk[4];
 #pragma unroll
     for (int n = 0; n < 4; ++n) gkk[n] = gqk[n] = zero4();
 #pragma unroll 4
     for (int jb = 0; jb < D / 32; ++jb) {
-      const typename P::frag kw = frag_rows_p<P>(K, D, 16 * w, 32 * jb, lane);
-      const typename P::frag qw = frag_rows_p<P>(Q, D, 16 * w, 32 * jb, lane);
+      const typename P::frag kw = kxf[(w * 16 + jb) * 64 + lane];
+      typename P::frag qw;
+      if constexpr (IsBf16Policy<P>::value) qw = kxf[(64 + w * 16 + jb) * 64 + lane];
+      else qw = frag_rows_p<P>(Q, D, 16 * w, 32 * jb, lane);
 #pragma unroll
       for (int n = 0; n < 4; ++n) {
-        const typename P::frag kn = frag_rows_p<P>(K, D, 16 * n, 32 * jb, lane);
+        const typename P::frag kn = kxf[(n * 16 + jb) * 64 + lane];
         gkk[n] = P::mma(gkk[n], kw, kn);
         gqk[n] = P::mma(gqk[n], qw, kn);
       }
