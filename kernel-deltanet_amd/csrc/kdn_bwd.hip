@@ -540,6 +540,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
 // and Z = -Tp^T dW; Sigma <- g_C Sigma (+ H) + K^T Z.  With bf16 fragments the K-row fragments of the
 // next chunk are loaded one iteration ahead (two register sets); every other operand is issued at the
 // top of its own iteration, ahead of the first barrier, and the next chunk's lines are prefetched to L2.
+// The barriers order the LDS exchange only (no wave reads another's global writes within a step), so
+// the loads issued ahead and the stores of the step stay in flight across them.
 template <class P>
 struct ChainK {
   typename P::frag kx[4][4];  // K rows 16m .., features 128w + 32jj ..
@@ -596,6 +598,30 @@ __device__ __forceinline__ bool chain_step(const Params& p, ChainShared& sh, int
     }
   }
 
+  // K^T fragments (the update) and, in reverse, Q^T and a o dY fragments (H): with bf16 fragments
+  // issued here and used after the first barrier, so that their latency hides behind the products of the
+  // carried slice (fp32 fragments, twice the registers, are loaded after the barrier)
+  constexpr bool HOIST = IsBf16Policy<P>::value;
+  frag kt[8][2], qt[REV ? 8 : 1][2], y0, y1;
+  auto load_kq = [&]() {
+    const frag* ktf = reinterpret_cast<const frag*>(rec + Rec::KTF);
+#pragma unroll
+    for (int t = 0; t < 8; ++t)
+#pragma unroll
+      for (int jb = 0; jb < 2; ++jb) kt[t][jb] = ktf[((8 * w + t) * 2 + jb) * 64 + lane];
+    if constexpr (REV) {
+      const frag* qtf = reinterpret_cast<const frag*>(rec + Rec::QTF);
+      const frag* ayf = reinterpret_cast<const frag*>(rec + Rec::AYF);
+      y0 = ayf[(n * 2) * 64 + lane];
+      y1 = ayf[(n * 2 + 1) * 64 + lane];
+#pragma unroll
+      for (int t = 0; t < 8; ++t)
+#pragma unroll
+        for (int jb = 0; jb < 2; ++jb) qt[t][jb] = qtf[((8 * w + t) * 2 + jb) * 64 + lane];
+    }
+  };
+  if constexpr (HOIST) load_kq();
+
   typename Feat<P>::T* dst = feat<P>(rec, REV ? Rec::G : Rec::S);
 #pragma unroll
   for (int t = 0; t < 8; ++t)
@@ -618,24 +644,13 @@ __device__ __forceinline__ bool chain_step(const Params& p, ChainShared& sh, int
   const float gC = expf(l63);
 #pragma unroll
   for (int t = 0; t < 8; ++t) Sg[t] = Sg[t] * gC;
-  __syncthreads();
+  lds_barrier();
+  if constexpr (!HOIST) load_kq();
   f32x4 hh[8];
   if constexpr (REV) {
     // this wave's rows of H = Q^T (a o dY) for value tile n
-    const frag* qtf = reinterpret_cast<const frag*>(rec + Rec::QTF);
-    const frag* ayf = reinterpret_cast<const frag*>(rec + Rec::AYF);
-    const frag y0 = ayf[(n * 2) * 64 + lane], y1 = ayf[(n * 2 + 1) * 64 + lane];
 #pragma unroll
-    for (int t = 0; t < 8; ++t)
-      hh[t] = P::mma(P::mma(zero4(), qtf[((8 * w + t) * 2) * 64 + lane], y0), qtf[((8 * w + t) * 2 + 1) * 64 + lane], y1);
-  }
-  frag kt[8][2];
-  {
-    const frag* ktf = reinterpret_cast<const frag*>(rec + Rec::KTF);
-#pragma unroll
-    for (int t = 0; t < 8; ++t)
-#pragma unroll
-      for (int jb = 0; jb < 2; ++jb) kt[t][jb] = ktf[((8 * w + t) * 2 + jb) * 64 + lane];
+    for (int t = 0; t < 8; ++t) hh[t] = P::mma(P::mma(zero4(), qt[t][0], y0), qt[t][1], y1);
   }
   const f32x4 X = sh.xp[0][w][lane] + sh.xp[1][w][lane] + sh.xp[2][w][lane] + sh.xp[3][w][lane];
   f32x4 kap;
@@ -645,7 +660,7 @@ __device__ __forceinline__ bool chain_step(const Params& p, ChainShared& sh, int
     sh.x[w][lane] = X;
 #pragma unroll
     for (int i = 0; i < 4; ++i) rec[Rec::XK + (16 * w + 4 * (lane >> 4) + i) * DV + vc] = X[i];
-    __syncthreads();
+    lds_barrier();
     f32x4 tx = mm<PrecF32>(zero4(), tp0, pair_to8(sh.x[0][lane], sh.x[1][lane]));
     tx = mm<PrecF32>(tx, tp1, pair_to8(sh.x[2][lane], sh.x[3][lane]));
     const f32x4 Wt = ur - tx;
@@ -661,12 +676,12 @@ __device__ __forceinline__ bool chain_step(const Params& p, ChainShared& sh, int
       rec[Rec::DW + ri * DV + vc] = dW[i];
     }
     sh.x[w][lane] = dW;
-    __syncthreads();
+    lds_barrier();
     f32x4 zt = mm<PrecF32>(zero4(), tp0, pair_to8(sh.x[0][lane], sh.x[1][lane]));
     zt = mm<PrecF32>(zt, tp1, pair_to8(sh.x[2][lane], sh.x[3][lane]));
     sh.z[w][lane] = -zt;
   }
-  __syncthreads();
+  lds_barrier();
   const frag zb0 = P::from_f32(pair_to8(sh.z[0][lane], sh.z[1][lane]));
   const frag zb1 = P::from_f32(pair_to8(sh.z[2][lane], sh.z[3][lane]));
 #pragma unroll
