@@ -369,9 +369,9 @@ int64_t kdn_scan_bwd_segments(const kdn_scan_bwd_args* a, int64_t* segment_chunk
  * the reverse carry of dL/dS, and the per-chunk gradients with the lift's backward. */
 int kdn_delta_scan_bwd(const kdn_scan_bwd_args* a, void* stream);
 
-/* kdn_delta_scan_bwd over two streams: the reverse carries (the sequential critical path) run back to
- * back on `stream` while aux_stream runs the recompute, forward carry and gradients of the segments
- * around them (and the checkpoint pass's prep kernels beside its state kernels).  Same workspace, same
+/* kdn_delta_scan_bwd over two streams: both carries of each segment (one launch) and its gradient
+ * algebra run back to back on `stream` while aux_stream runs the recompute and dx launches of the
+ * segments around them (and the checkpoint pass's prep kernels beside its state kernels).  Same workspace, same
  * results bit for bit.  aux_stream NULL (or equal to `stream`) is kdn_delta_scan_bwd.  Both streams
  * should have default priority.  Replaces kernels/fused_kernel_deltanet.py:168-179, like
  * kdn_delta_scan_bwd. */
