@@ -423,7 +423,9 @@ typedef struct kdn_ragged_args {
  * cu_seqlens_host. */
 size_t kdn_ragged_workspace_bytes(const kdn_ragged_args* a);
 
-/* Runs the step on `stream`; the prefill part uses the pipelined scan when aux_stream is not NULL. */
+/* Runs the step on `stream`.  With aux_stream (not NULL, not `stream`) the prefill part uses the
+ * pipelined scan and the decode part runs on aux_stream after the prefill's prep launches; aux_stream
+ * first waits for the work queued on `stream`, and `stream` finally waits for aux_stream. */
 int kdn_ragged_step(const kdn_ragged_args* a, void* stream, void* aux_stream);
 
 /* The same step described by a token -> slot map alone, with nothing read back to the host (ABI 2.2):
@@ -458,6 +460,7 @@ typedef struct kdn_slot_step_args {
 
 /* Workspace bytes kdn_slot_step needs (0 if the arguments are invalid); reads the shape fields only. */
 size_t kdn_slot_step_workspace_bytes(const kdn_slot_step_args* a);
+/* Streams as kdn_ragged_step. */
 int kdn_slot_step(const kdn_slot_step_args* a, void* stream, void* aux_stream);
 
 /* ---- Slab state pool --------------------------------------------------------------------------

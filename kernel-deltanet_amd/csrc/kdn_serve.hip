@@ -501,7 +501,19 @@ extern "C" int kdn_ragged_step(const kdn_ragged_args* a, void* stream, void* aux
                      a->num_slots, dec_row, dec_slot, pre_lo, pre_hi, pre_slot);
   rc = launch_status();
   if (rc != KDN_OK) return rc;
-  if (pl.n_dec > 0) {
+  // With an auxiliary stream and both kinds of sequences, the decode runs on it after the prefill's prep
+  // launches (which fill the GPU), beside the prefill's last chain launches (which do not): the two share
+  // no state slot and no row of y.  Events order it after the split and `stream` after it.
+  const hipStream_t aux = aux_stream ? as_stream(aux_stream) : nullptr;
+  const bool dec_aux = pl.n_dec > 0 && pl.n_pre > 0 && aux && aux != st;
+  EventSet evs;
+  if (dec_aux) {
+    rc = evs.create(2);
+    if (rc != KDN_OK) return rc;
+    if (hipEventRecord(evs.ev[0], st) != hipSuccess || hipStreamWaitEvent(aux, evs.ev[0], 0) != hipSuccess)
+      return KDN_ERR_DEVICE;
+  }
+  auto run_decode = [&](hipStream_t ds) -> int {
     DecodeParams dp;
     dp.rows = dec_row; dp.slots = dec_slot;
     dp.q = a->q; dp.qs0 = a->q_stride[0]; dp.qs1 = a->q_stride[1];
@@ -515,11 +527,13 @@ extern "C" int kdn_ragged_step(const kdn_ragged_args* a, void* stream, void* aux
     dp.ss0 = a->state_stride[0]; dp.ss1 = a->state_stride[1]; dp.ss2 = a->state_stride[2]; dp.ss3 = a->state_stride[3];
     dp.y = a->y; dp.ys0 = a->y_stride[0]; dp.ys1 = a->y_stride[1];
     if (a->in_dtype == KDN_DTYPE_BF16)
-      rc = a->out_dtype == KDN_DTYPE_BF16 ? launch_decode<__bf16, __bf16>(dp, pl.n_dec, a->H, a->d_v, st)
-                                          : launch_decode<__bf16, float>(dp, pl.n_dec, a->H, a->d_v, st);
-    else
-      rc = a->out_dtype == KDN_DTYPE_BF16 ? launch_decode<float, __bf16>(dp, pl.n_dec, a->H, a->d_v, st)
-                                          : launch_decode<float, float>(dp, pl.n_dec, a->H, a->d_v, st);
+      return a->out_dtype == KDN_DTYPE_BF16 ? launch_decode<__bf16, __bf16>(dp, pl.n_dec, a->H, a->d_v, ds)
+                                            : launch_decode<__bf16, float>(dp, pl.n_dec, a->H, a->d_v, ds);
+    return a->out_dtype == KDN_DTYPE_BF16 ? launch_decode<float, __bf16>(dp, pl.n_dec, a->H, a->d_v, ds)
+                                          : launch_decode<float, float>(dp, pl.n_dec, a->H, a->d_v, ds);
+  };
+  if (pl.n_dec > 0 && !dec_aux) {
+    rc = run_decode(st);
     if (rc != KDN_OK) return rc;
   }
   if (pl.n_pre > 0) {
@@ -529,6 +543,12 @@ extern "C" int kdn_ragged_step(const kdn_ragged_args* a, void* stream, void* aux
     s.workspace_bytes = a->workspace_bytes - (size_t)(w - (unsigned char*)a->workspace);
     rc = scan_pipelined(&s, pre_lo, pre_hi, stream, aux_stream, nullptr);
     if (rc != KDN_OK) return rc;
+  }
+  if (dec_aux) {
+    rc = run_decode(aux);
+    if (rc != KDN_OK) return rc;
+    if (hipEventRecord(evs.ev[1], aux) != hipSuccess || hipStreamWaitEvent(st, evs.ev[1], 0) != hipSuccess)
+      return KDN_ERR_DEVICE;
   }
   return KDN_OK;
 }
@@ -640,6 +660,17 @@ extern "C" int kdn_slot_step(const kdn_slot_step_args* a, void* stream, void* au
                      pl.cap, a->num_slots, dec_row, dec_slot, pre_lo, pre_hi, pre_slot);
   rc = launch_status();
   if (rc != KDN_OK) return rc;
+  // with an auxiliary stream the decode runs on it after the prefill's prep launches, as in
+  // kdn_ragged_step
+  const hipStream_t aux = aux_stream ? as_stream(aux_stream) : nullptr;
+  const bool dec_aux = pl.nwin > 0 && aux && aux != st;
+  EventSet evs;
+  if (dec_aux) {
+    rc = evs.create(2);
+    if (rc != KDN_OK) return rc;
+    if (hipEventRecord(evs.ev[0], st) != hipSuccess || hipStreamWaitEvent(aux, evs.ev[0], 0) != hipSuccess)
+      return KDN_ERR_DEVICE;
+  }
   // decode: one entry per possible run; entries the split did not fill have slot -1 and exit at once
   DecodeParams dp;
   dp.rows = dec_row; dp.slots = dec_slot;
@@ -653,13 +684,17 @@ extern "C" int kdn_slot_step(const kdn_slot_step_args* a, void* stream, void* au
   dp.states = a->states;
   dp.ss0 = a->state_stride[0]; dp.ss1 = a->state_stride[1]; dp.ss2 = a->state_stride[2]; dp.ss3 = a->state_stride[3];
   dp.y = a->y; dp.ys0 = a->y_stride[0]; dp.ys1 = a->y_stride[1];
-  if (a->in_dtype == KDN_DTYPE_BF16)
-    rc = a->out_dtype == KDN_DTYPE_BF16 ? launch_decode<__bf16, __bf16>(dp, pl.cap, a->H, a->d_v, st)
-                                        : launch_decode<__bf16, float>(dp, pl.cap, a->H, a->d_v, st);
-  else
-    rc = a->out_dtype == KDN_DTYPE_BF16 ? launch_decode<float, __bf16>(dp, pl.cap, a->H, a->d_v, st)
-                                        : launch_decode<float, float>(dp, pl.cap, a->H, a->d_v, st);
-  if (rc != KDN_OK) return rc;
+  auto run_decode = [&](hipStream_t ds) -> int {
+    if (a->in_dtype == KDN_DTYPE_BF16)
+      return a->out_dtype == KDN_DTYPE_BF16 ? launch_decode<__bf16, __bf16>(dp, pl.cap, a->H, a->d_v, ds)
+                                            : launch_decode<__bf16, float>(dp, pl.cap, a->H, a->d_v, ds);
+    return a->out_dtype == KDN_DTYPE_BF16 ? launch_decode<float, __bf16>(dp, pl.cap, a->H, a->d_v, ds)
+                                          : launch_decode<float, float>(dp, pl.cap, a->H, a->d_v, ds);
+  };
+  if (!dec_aux) {
+    rc = run_decode(st);
+    if (rc != KDN_OK) return rc;
+  }
   if (pl.nwin == 0) return KDN_OK;
   // prefill: the packed layout, then the split scan over its windows
   hipLaunchKernelGGL(flat_plan_kernel, dim3(1), dim3(1024), 0, st, (const int64_t*)pre_lo, (const int64_t*)pre_hi,
@@ -673,5 +708,13 @@ extern "C" int kdn_slot_step(const kdn_slot_step_args* a, void* stream, void* au
   FlatPlan fp;
   fp.off = fl_off; fp.first = fl_first; fp.total = fl_total;
   fp.nseq = pl.cap; fp.win = pl.win; fp.nwin = pl.nwin;
-  return scan_flat(&s, pre_lo, pre_hi, fp, stream, aux_stream);
+  rc = scan_flat(&s, pre_lo, pre_hi, fp, stream, aux_stream);
+  if (rc != KDN_OK) return rc;
+  if (dec_aux) {
+    rc = run_decode(aux);
+    if (rc != KDN_OK) return rc;
+    if (hipEventRecord(evs.ev[1], aux) != hipSuccess || hipStreamWaitEvent(st, evs.ev[1], 0) != hipSuccess)
+      return KDN_ERR_DEVICE;
+  }
+  return KDN_OK;
 }
