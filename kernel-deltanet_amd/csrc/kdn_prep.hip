@@ -263,7 +263,7 @@ __global__ void __launch_bounds__(256, (PrepWaves<P, FM>::value)) prep_kernel(Sc
           const int j = 16 * m + 4 * (lane >> 4) + i;
           const float gj = s_g[j], skj = s_sk[j];
           const float a = (j < t) ? bt * __expf(fminf(gt - gj, 0.f)) * gkk[m][i] * skt * skj : 0.f;
-          s_A[(j * 4 + (t & 3)) * 16 + a_swizzle(j, t >> 2)] = a;
+          s_A[(j * 4 + (t & 3)) * 16 + a_swizzle(j, t >> 2, t & 3)] = a;
           if constexpr (!NOQ) pt[m][i] = (j < t) ? __expf(fminf(gtm1 - gj, 0.f)) * gqk[m][i] * sqt * skj : 0.f;
         }
       }
@@ -535,7 +535,7 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))
         for (int i = 0; i < 4; ++i) {
           const int j = 16 * mm + 4 * (lane >> 4) + i;
           const float a = (j < t) ? bt * __expf(fminf(gt - s_g[j], 0.f)) * gk[i] * skt * s_sk[j] : 0.f;
-          s_A[(j * 4 + (t & 3)) * 16 + a_swizzle(j, t >> 2)] = a;
+          s_A[(j * 4 + (t & 3)) * 16 + a_swizzle(j, t >> 2, t & 3)] = a;
         }
       }
     } else {

@@ -109,12 +109,18 @@ __device__ __forceinline__ void unit_lower_inverse(const float* At, float* T, in
   for (int s2 = 0; s2 < 16; ++s2) T[(4 * s2 + pq) * ldt + col] = -acc[s2];
 }
 
-// Swizzled layouts of A and T for unit_lower_inverse_blocked: At[(j * 4 + p) * 16 + a_swizzle(j, s)] =
+// Swizzled layouts of A and T for unit_lower_inverse_blocked: At[(j * 4 + p) * 16 + a_swizzle(j, s, p)] =
 // A[4s + p][j] and T[r * 64 + t_swizzle(r, c)] = T[r][c].
-// a_swizzle lets a writer that stores one element per lane, lane groups g = 0..3 taking columns
-// j = 4g + const and the lanes of a group s = 4w + 0..3 (p = 0..3), hit 64 distinct banks (unswizzled,
-// the four groups' stores collide on the same 16 banks).
-__device__ __forceinline__ int a_swizzle(int j, int s) { return 4 * ((s >> 2) ^ ((j >> 2) & 3)) + (s & 3); }
+// 4-byte LDS accesses are served per half-wave over 32 banks (16-byte reads per 16 lanes over 64; measured
+// with SQ_LDS_BANK_CONFLICT on a probe of both).  a_swizzle keeps each group of four s (one 16-byte read)
+// contiguous and spreads a half-wave's 4-byte accesses of A over 32 banks: the writer storing one element
+// per lane (p = lane & 3, s & 3 = (lane >> 2) & 3, column group g = lane >> 4) and the column walk reading
+// A[16i + m][16k + 4g + kb] (p = m & 3, s & 3 = m >> 2).  Row j * 4 + p puts p & 1 on bank bit 4; XORing
+// the group index with (j >> 2) & 3 and with 2 (p >> 1) separates the two lane groups of a half-wave and
+// p from p ^ 2.
+__device__ __forceinline__ int a_swizzle(int j, int s, int p) {
+  return 4 * ((s >> 2) ^ ((j >> 2) & 3) ^ (2 * (p >> 1))) + (s & 3);
+}
 // t_swizzle XORs the 16-byte group index of column c in row r (ldt = 64) with h(r) = 4 (a ^ p) + a,
 // a = (r >> 2) & 3, p = r & 3, so that each of these falls on distinct banks: 4-byte accesses of rows
 // 4a + 0..3 (a fixed) or of rows 4·0..3 + p (p fixed) at 16 consecutive columns of one 16-column block per
@@ -128,7 +134,7 @@ __device__ __forceinline__ int t_swizzle(int r, int c) {
 // Block column J of T below the diagonal (step 2 of unit_lower_inverse_blocked): T_iJ for i = J+1 .. 3.
 template <int J>
 __device__ __forceinline__ void inverse_block_column(const float* At, float* T, int lane) {
-  auto at_idx = [](int r, int c) { return (c * 4 + (r & 3)) * 16 + a_swizzle(c, r >> 2); };
+  auto at_idx = [](int r, int c) { return (c * 4 + (r & 3)) * 16 + a_swizzle(c, r >> 2, r & 3); };
   auto t_idx = [](int r, int c) { return r * 64 + t_swizzle(r, c); };
   const int g = lane >> 4, m = lane & 15;
   // operands read first: L_ik as A operands (depth 4g + kb) and T_ii rows, for every i > J and k in [J, i)
@@ -184,7 +190,7 @@ __device__ __forceinline__ void inverse_diag_block(const float* At, float* T, in
     // column i of L_bb's strict lower part, rows 16b + 4s + pq (s = 0..3): one 16-byte group of At
     auto col = [&](int i) {
       const int C = 16 * b + i;
-      return *reinterpret_cast<const f32x4*>(At + (C * 4 + pq) * 16 + 4 * (b ^ ((C >> 2) & 3)));
+      return *reinterpret_cast<const f32x4*>(At + (C * 4 + pq) * 16 + 4 * (b ^ ((C >> 2) & 3) ^ (2 * (pq >> 1))));
     };
     // every column's read issued before the chain starts (nothing else is live here)
     f32x4 acol[15];
@@ -203,10 +209,13 @@ __device__ __forceinline__ void inverse_diag_block(const float* At, float* T, in
 #pragma unroll
       for (int s = i >> 2; s < 4; ++s) acc[s] = fmaf(-a[s], bc, acc[s]);
     }
+    // store k writes row 4s + pq with s = k ^ 2 (pq >> 1): a half-wave (columns c = 0..7) then spans bank
+    // bit 3 through s as well as bit 4 through pq, 32 distinct banks (s = k for every lane: 16)
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
+    for (int k = 0; k < 4; ++k) {
+      const int s = k ^ (2 * (pq >> 1));
       const int r = 16 * b + 4 * s + pq;
-      T[t_idx(r, 16 * b + c)] = -acc[s];
+      T[t_idx(r, 16 * b + c)] = (pq & 2) ? -acc[k ^ 2] : -acc[k];
 #pragma unroll
       for (int blk = 0; blk < 4; ++blk)
         if (blk > b) T[t_idx(r, 16 * blk + c)] = 0.f;
