@@ -94,6 +94,31 @@ struct LiftWaves {
 // columns j of block m in turn, column j of H d1 is (-1)^popcount(lane & j) d1_j in lane `lane`, then the
 // d2 / d3 sign flips and two wave64 butterflies (fwht_wave) give Omega[64m + lane][j] * 8 exactly, and
 // each lane writes its element into the A fragment that the staged copy would hold.
+// Output staging tile (16 rows of 128 bytes per wave): chunk c (16 bytes) of row r sits at chunk
+// position c ^ ((r >> 1) & 7).  With bf16 output each lane stores 8 bytes (one half of a chunk) of its row,
+// and the halves of a chunk are swapped in rows with h(r) = (r ^ (r >> 1)) & 1 = 1.  8-byte stores are
+// served 16 lanes per cycle from a 128-byte bank window: the 16 rows of a store take 16 distinct 8-byte
+// slots (h separates rows 2k and 2k + 1, whose chunk positions agree).  The read-back takes each chunk as
+// its two halves in row order; 8-byte reads are served 32 lanes (4 rows) per cycle from 256 bytes, where
+// h separates rows 4k and 4k + 2 (and 4k + 1, 4k + 3).  Both measured on probes of the access widths.
+__device__ __forceinline__ int stage_h(int r) { return (r ^ (r >> 1)) & 1; }
+template <typename OutT>
+__device__ __forceinline__ int stage_off(int r, int byte) {
+  const int half = sizeof(OutT) == 2 ? ((byte & 15) ^ (8 * stage_h(r))) : (byte & 15);
+  return r * 128 + 16 * ((byte >> 4) ^ ((r >> 1) & 7)) + half;
+}
+template <typename OutT>
+__device__ __forceinline__ u32x4 stage_read(const unsigned char* stg, int r, int pos) {
+  const unsigned char* c = stg + r * 128 + 16 * pos;
+  if constexpr (sizeof(OutT) == 2) {
+    const int lo = 8 * stage_h(r);
+    const u32x2 a = *reinterpret_cast<const u32x2*>(c + lo), b = *reinterpret_cast<const u32x2*>(c + (8 ^ lo));
+    return __builtin_shufflevector(a, b, 0, 1, 2, 3);
+  } else {
+    return *reinterpret_cast<const u32x4*>(c);
+  }
+}
+
 template <typename InT, typename OutT, int D, bool FROM_BITS>
 __global__ void __launch_bounds__((64 * LiftWaves<InT, OutT, D>::value)) lift_kernel(const InT* __restrict__ x, int64_t rows, int64_t xs, int normalize,
                                                    const __bf16* __restrict__ omega, const int64_t* __restrict__ bits,
@@ -108,10 +133,9 @@ __global__ void __launch_bounds__((64 * LiftWaves<InT, OutT, D>::value)) lift_ke
   // address (reads of one shared 2 KB table, sixteen lanes to an address, were counted as bank conflicts:
   // 128 cycles per 16-row tile)
   __shared__ f32x4 s_phr[NT * 64];
-  // Per-wave staging of 16 rows x 128 bytes of output.  Chunk c (16 bytes) of row r sits at chunk position
-  // c ^ ((r >> 1) & 7) of the row: the accumulator stores (16 rows x 8 or 16 bytes per instruction) and
-  // the 16-byte row read-back (two whole rows per 16 lanes) both fall on distinct banks.  (Rows padded
-  // by 16 bytes instead: the read-back's two rows overlapped on one bank.)
+  // Per-wave staging of 16 rows x 128 bytes of output (stage_off, stage_read): the accumulator stores
+  // (16 rows x 8 or 16 bytes per instruction) and the row read-back (two whole rows per 16 lanes) fall on
+  // distinct banks.  (Rows padded by 16 bytes instead: the read-back's two rows overlapped on one bank.)
   constexpr int TG = 128 / (16 * (int)sizeof(OutT));  // feature tiles per staged group: 128 bytes of a row
   constexpr int SRS = 16 * TG * (int)sizeof(OutT);   // row stride in bytes (128)
   constexpr int SCPR = 16 * TG * (int)sizeof(OutT) / 16;  // 16-byte chunks per staged row (8)
@@ -259,7 +283,7 @@ __global__ void __launch_bounds__((64 * LiftWaves<InT, OutT, D>::value)) lift_ke
         const int t = TG * g + tp;
         float v[4] = {c[t][0] * scale, c[t][1] * scale, c[t][2] * scale, c[t][3] * scale};
         const int r = lane & 15, byte = (int)sizeof(OutT) * (16 * tp + 4 * (lane >> 4));
-        store4<OutT>(reinterpret_cast<OutT*>(stg + r * SRS + 16 * ((byte >> 4) ^ ((r >> 1) & 7)) + (byte & 15)), v);
+        store4<OutT>(reinterpret_cast<OutT*>(stg + stage_off<OutT>(r, byte)), v);
       }
       // The read-back below takes rows other lanes wrote, and the next group's stores overwrite rows
       // other lanes read.
@@ -267,7 +291,7 @@ __global__ void __launch_bounds__((64 * LiftWaves<InT, OutT, D>::value)) lift_ke
 #pragma unroll
       for (int j = 0; j < 16 * SCPR / 64; ++j) {
         const int q = 64 * j + lane, r = q / SCPR, pos = q % SCPR, ch = pos ^ ((r >> 1) & 7);
-        const u32x4 val = *reinterpret_cast<const u32x4*>(stg + r * SRS + 16 * pos);
+        const u32x4 val = stage_read<OutT>(stg, r, pos);
         const int64_t grow = tile * 16 + r;
         // streaming stores: the features are far larger than the caches, and their readers come later
         // (13 back-to-back config-2 lifts: 0.46 against 0.50 ms per launch once the clocks have settled)
@@ -538,7 +562,7 @@ __global__ void __launch_bounds__(512) lift_factored_kernel(const __bf16* __rest
                                                             const __bf16* __restrict__ om2, const float* __restrict__ ph2,
                                                             float inv_tau, OutT* __restrict__ out, int64_t os) {
   constexpr int D = 512, NT = D / 16;
-  // output staging as in lift_kernel (128-byte rows, chunk c of row r at position c ^ ((r >> 1) & 7))
+  // output staging as in lift_kernel (stage_off / stage_read)
   constexpr int TG = 128 / (16 * (int)sizeof(OutT));
   constexpr int SRS = 16 * TG * (int)sizeof(OutT);
   constexpr int SCPR = 16 * TG * (int)sizeof(OutT) / 16;
@@ -638,13 +662,13 @@ __global__ void __launch_bounds__(512) lift_factored_kernel(const __bf16* __rest
         const int t = TG * g + tp;
         float v[4] = {c[t][0] * inv, c[t][1] * inv, c[t][2] * inv, c[t][3] * inv};
         const int r = lane & 15, byte = (int)sizeof(OutT) * (16 * tp + 4 * (lane >> 4));
-        store4<OutT>(reinterpret_cast<OutT*>(stg + r * SRS + 16 * ((byte >> 4) ^ ((r >> 1) & 7)) + (byte & 15)), v);
+        store4<OutT>(reinterpret_cast<OutT*>(stg + stage_off<OutT>(r, byte)), v);
       }
       wave_lds_sync();
 #pragma unroll
       for (int j = 0; j < 16 * SCPR / 64; ++j) {
         const int q = 64 * j + lane, r = q / SCPR, pos = q % SCPR, ch = pos ^ ((r >> 1) & 7);
-        const u32x4 val = *reinterpret_cast<const u32x4*>(stg + r * SRS + 16 * pos);
+        const u32x4 val = stage_read<OutT>(stg, r, pos);
         const int64_t grow = tile * 16 + r;
         if (grow < rows)
           *reinterpret_cast<u32x4*>(reinterpret_cast<unsigned char*>(out + grow * os + D * h + 16 * TG * g) + 16 * ch) = val;
