@@ -276,3 +276,39 @@ def test_backward_config4_shape(proj):
     for n, f, o in zip(("dq", "dk", "dv", "dbeta", "ddecay"), full, one):
         assert torch.equal(f[b:b + 1, :, h:h + 1], o), n
     assert torch.equal(full[5][b:b + 1, h:h + 1], one[5]), "dinit"
+
+
+def test_backward_config3_default_segments(proj):
+    # B = 1, H = 16, T = 65536 (bf16, decay, initial state, dL/dS_T): the default segment is 128 chunks,
+    # so each of the three segment buffers of records spans 2.25 GB and the last head's records lie past
+    # 2^31 bytes into its buffer; every gradient is finite and that head equals bit for bit the backward
+    # of the head alone with the same segments
+    B, T, H = 1, 65536, 16
+    g = torch.Generator(device=DEV).manual_seed(25)
+    q = torch.randn(B, T, H, 64, generator=g, device=DEV).to(torch.bfloat16)
+    k = torch.randn(B, T, H, 64, generator=g, device=DEV).to(torch.bfloat16)
+    v = torch.randn(B, T, H, 64, generator=g, device=DEV).to(torch.bfloat16)
+    beta = torch.sigmoid(torch.randn(B, T, H, generator=g, device=DEV))
+    lam = 0.95 + 0.05 * torch.rand(B, T, H, generator=g, device=DEV)
+    s0 = 0.1 * torch.randn(B, H, 512, 64, generator=g, device=DEV)
+    dy = torch.randn(B, T, H, 64, generator=g, device=DEV)
+    ds = 0.5 * torch.randn(B, H, 512, 64, generator=g, device=DEV)
+    omega, phase = proj.device_omega(DEV), proj.device_phase(DEV)
+    plan = ops.ScanBackwardPlan(q, k, v, beta, lam, omega, phase, proj.tau_star_inv, dy, ds, initial_state=s0)
+    assert plan.segment_chunks == 128 and plan.segments == 8
+    print("workspace bytes", plan.workspace.numel(), flush=True)
+    assert plan.workspace.numel() < 8 * 10**9
+    full = [t.clone() for t in plan.run()]
+    torch.cuda.synchronize()
+    for n, t in zip(("dq", "dk", "dv", "dbeta", "ddecay", "dinit"), full):
+        assert bool(torch.isfinite(t).all()), n
+    del plan
+    h = 15
+    one = ops.scan_backward(q[:, :, h:h + 1], k[:, :, h:h + 1], v[:, :, h:h + 1], beta[:, :, h:h + 1],
+                            lam[:, :, h:h + 1], omega, phase, proj.tau_star_inv, dy[:, :, h:h + 1],
+                            ds[:, h:h + 1].contiguous(), initial_state=s0[:, h:h + 1].contiguous(),
+                            segment_chunks=128)
+    torch.cuda.synchronize()
+    for n, f, o in zip(("dq", "dk", "dv", "dbeta", "ddecay"), full, one):
+        assert torch.equal(f[:, :, h:h + 1], o), n
+    assert torch.equal(full[5][:, h:h + 1], one[5]), "dinit"
