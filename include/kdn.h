@@ -318,7 +318,7 @@ int kdn_scan_chain(const kdn_scan_args* a, int64_t chunk0, int64_t nchunks, void
  * NULL.  The gradient of lambda is zero where the forward's clamp to [1e-5, 1] is active.
  *
  * The backward runs in segments of fwd->segment_chunks 64-token chunks (0: the largest power of two
- * from 4 to 128 whose per-chunk records fit 3 GiB), last segment first: a checkpoint pass of the
+ * from 4 to 256 whose per-chunk records fit 4.5 GiB), last segment first: a checkpoint pass of the
  * forward scan's prep and state kernels stores the state at each segment start, then each segment
  * recomputes its chunks, carries the state forward from its checkpoint and dL/dS backward from the
  * next segment, and writes its gradients.  The workspace (256-byte aligned) holds up to three segments'

@@ -1430,10 +1430,11 @@ struct BwdLayout {
   size_t rec_buf, state_bytes, ckpt_off, carry_off, fwd_off, fwd_buf, omt_off, dit_off, total;
 };
 
-// Default segment: the largest power of two from 4 to 128 chunks whose records fit 3 GiB (128 chunks at
-// B*H = 16: 8 segments, 15.95 ms per backward against 16.43 with 16 segments of 64 and 17.77 with 32).
-constexpr size_t BWD_SEGMENT_BUDGET = (size_t)3072 << 20;
-constexpr int64_t BWD_SEGMENT_MAX = 128;
+// Default segment: the largest power of two from 4 to 256 chunks whose records fit 4.5 GiB (256 chunks at
+// B*H = 16: 4 segments, 15.52-15.55 ms per backward against 15.95 with 8 segments of 128, 16.43 with 16
+// of 64, and 15.85-15.93 / 16.56-16.58 with 2 of 512 / 1 of 1024).
+constexpr size_t BWD_SEGMENT_BUDGET = (size_t)4608 << 20;
+constexpr int64_t BWD_SEGMENT_MAX = 256;
 
 static BwdLayout bwd_layout(const kdn_scan_args* f, bool want_dit) {
   BwdLayout L;

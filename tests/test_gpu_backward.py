@@ -243,7 +243,7 @@ def test_segment_length_changes_only_rounding(proj):
 
 def test_backward_config4_shape(proj):
     # B = 32, H = 16, T = 16384 (bf16, decay, initial state, dL/dS_T): the workspace is bounded by the
-    # segment (default 4 chunks at B*H = 512), every gradient is finite, and one (batch, head) equals bit
+    # segment (default 8 chunks at B*H = 512), every gradient is finite, and one (batch, head) equals bit
     # for bit the backward of that head alone with the same segments (no kernel mixes heads), which the
     # segmented parity test above pins to the float64 oracle
     B, T, H = 32, 16384, 16
@@ -258,10 +258,11 @@ def test_backward_config4_shape(proj):
     ds = 0.5 * torch.randn(B, H, 512, 64, generator=g, device=DEV)
     omega, phase = proj.device_omega(DEV), proj.device_phase(DEV)
     plan = ops.ScanBackwardPlan(q, k, v, beta, lam, omega, phase, proj.tau_star_inv, dy, ds, initial_state=s0)
-    assert plan.segment_chunks == 4 and plan.segments == 64
-    # the records of three 4-chunk segments, 63 segment-start states and the carry, the checkpoint
-    # pass's two buffers and the table: about 13 GB, against 163 GB for records of every chunk
-    assert plan.workspace.numel() < 14 * 10**9
+    assert plan.segment_chunks == 8 and plan.segments == 32
+    # the records of three 8-chunk segments, 31 segment-start states and the carry, the checkpoint
+    # pass's two buffers and the table: about 18 GB, against 163 GB for records of every chunk
+    print("workspace bytes", plan.workspace.numel(), flush=True)
+    assert plan.workspace.numel() < 19 * 10**9
     full = [t.clone() for t in plan.run()]
     torch.cuda.synchronize()
     for n, t in zip(("dq", "dk", "dv", "dbeta", "ddecay", "dinit"), full):
@@ -271,7 +272,7 @@ def test_backward_config4_shape(proj):
     one = ops.scan_backward(q[b:b + 1, :, h:h + 1], k[b:b + 1, :, h:h + 1], v[b:b + 1, :, h:h + 1],
                             beta[b:b + 1, :, h:h + 1], lam[b:b + 1, :, h:h + 1], omega, phase, proj.tau_star_inv,
                             dy[b:b + 1, :, h:h + 1], ds[b:b + 1, h:h + 1].contiguous(),
-                            initial_state=s0[b:b + 1, h:h + 1].contiguous(), segment_chunks=4)
+                            initial_state=s0[b:b + 1, h:h + 1].contiguous(), segment_chunks=8)
     torch.cuda.synchronize()
     for n, f, o in zip(("dq", "dk", "dv", "dbeta", "ddecay"), full, one):
         assert torch.equal(f[b:b + 1, :, h:h + 1], o), n
@@ -279,9 +280,9 @@ def test_backward_config4_shape(proj):
 
 
 def test_backward_config3_default_segments(proj):
-    # B = 1, H = 16, T = 65536 (bf16, decay, initial state, dL/dS_T): the default segment is 128 chunks,
-    # so each of the three segment buffers of records spans 2.25 GB and the last head's records lie past
-    # 2^31 bytes into its buffer; every gradient is finite and that head equals bit for bit the backward
+    # B = 1, H = 16, T = 65536 (bf16, decay, initial state, dL/dS_T): the default segment is 256 chunks,
+    # so each of the three segment buffers of records spans 4.5 GB and the last heads' records lie past
+    # 2^31 bytes into their buffer; every gradient is finite and that head equals bit for bit the backward
     # of the head alone with the same segments
     B, T, H = 1, 65536, 16
     g = torch.Generator(device=DEV).manual_seed(25)
@@ -295,9 +296,9 @@ def test_backward_config3_default_segments(proj):
     ds = 0.5 * torch.randn(B, H, 512, 64, generator=g, device=DEV)
     omega, phase = proj.device_omega(DEV), proj.device_phase(DEV)
     plan = ops.ScanBackwardPlan(q, k, v, beta, lam, omega, phase, proj.tau_star_inv, dy, ds, initial_state=s0)
-    assert plan.segment_chunks == 128 and plan.segments == 8
+    assert plan.segment_chunks == 256 and plan.segments == 4
     print("workspace bytes", plan.workspace.numel(), flush=True)
-    assert plan.workspace.numel() < 8 * 10**9
+    assert plan.workspace.numel() < 16 * 10**9
     full = [t.clone() for t in plan.run()]
     torch.cuda.synchronize()
     for n, t in zip(("dq", "dk", "dv", "dbeta", "ddecay", "dinit"), full):
@@ -307,7 +308,7 @@ def test_backward_config3_default_segments(proj):
     one = ops.scan_backward(q[:, :, h:h + 1], k[:, :, h:h + 1], v[:, :, h:h + 1], beta[:, :, h:h + 1],
                             lam[:, :, h:h + 1], omega, phase, proj.tau_star_inv, dy[:, :, h:h + 1],
                             ds[:, h:h + 1].contiguous(), initial_state=s0[:, h:h + 1].contiguous(),
-                            segment_chunks=128)
+                            segment_chunks=256)
     torch.cuda.synchronize()
     for n, f, o in zip(("dq", "dk", "dv", "dbeta", "ddecay"), full, one):
         assert torch.equal(f[:, :, h:h + 1], o), n
