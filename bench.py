@@ -585,7 +585,7 @@ def bench_factored_backward(args, dev):
                  fp.proj2.device_phase(dev), fp.proj1.tau_star_inv)
     fq, fk = ops.lift_factored(q, *lift_args), ops.lift_factored(k, *lift_args)
     plan = ops.ScanBackwardPlan(fq, fk, v, beta, None, None, None, 1.0, dy, need_dinit=False,
-                                features=ops.FeatureMap(lifted=True))
+                                features=ops.FeatureMap(lifted=True), segment_chunks=args.segment_chunks)
     stream = torch.cuda.current_stream(dev)
 
     def step(times=None):

@@ -332,7 +332,7 @@ int kdn_scan_chain(const kdn_scan_args* a, int64_t chunk0, int64_t nchunks, void
  *
  * At D = 1024 (ABI 1.8) the backward runs on one stream (the auxiliary stream is not used, and
  * kdn_scan_bwd_phase returns KDN_ERR_UNSUPPORTED), in segments of fwd->segment_chunks chunks (0: the
- * largest power of two from 4 to 256 whose records fit 12 GiB; ABI 2.3): a checkpoint pass of the
+ * largest power of two from 4 to 256 whose records fit 24 GiB; ABI 2.3): a checkpoint pass of the
  * recompute and the forward carry stores the state at each segment start, then each segment, last first,
  * recomputes its chunks, carries the state forward from its checkpoint and dL/dS backward from the next
  * segment (a reverse carry from its last chunk to its first), and two parallel launches write its
